@@ -1,0 +1,217 @@
+"""Keyswitch/rotation throughput of the gfx950 RNS-CKKS backend.
+
+Workload (one GPU): 64 ciphertexts at N = 2^16 (2^15 slots, values
+uniform[-1, 1] from seed 0), Q = one 60-bit + 35 40-bit primes, dnum 3 hybrid
+key switching with 12 60-bit special primes.  One step = rotations by
+2^0 .. 2^14 of all 64 ciphertexts (chained, 15 x 64 key switches at 36 limbs),
+then HMult + relinearise + rescale at every level 36 -> 2 (34 x 64 key
+switches).  Inputs are resident in HBM before the timed region.
+
+Prints one JSON line: keyswitch/s, the roofline of the dominant kernel (the
+two-pass NTT, timed with events on the library stream) and the CPU oracle's
+keyswitch rate on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "easyfhe-llama3-8b_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PARAMS = dict(log_n=16, depth=35, dnum=3, dcrt_bits=40, first_mod=60, special_bits=60)
+ROTATIONS = tuple(1 << k for k in range(15))
+
+
+def keyswitch_bytes(N: int, limbs: int, alpha: int, digits: int, batch: int, relin: bool) -> float:
+    """Algorithmic HBM bytes per key switch: read c0, c1, write 2 limbs-polys
+    (relinearisation also reads d2), plus the key streamed once per batch."""
+    polys = (5 if relin else 4) * limbs
+    return 8.0 * N * (polys + 2.0 * digits * (limbs + alpha) / batch)
+
+
+def cpu_baseline(seconds_budget: float = 20.0):
+    """Oracle rotations at the full workload size on the host cores."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    L = PARAMS["depth"] + 1
+    ctx = O.OracleContext(log_n=16, limbs=L, alpha=12, dnum=3, first_bits=60, dcrt_bits=40,
+                          special_bits=60, seed=0)
+    g = ctx.galois_elt(1)
+    ctx.gen_rotation_key(g)
+    z = np.random.default_rng(0).uniform(-1, 1, 1 << 15)
+    ct = ctx.encrypt(z, slots=1 << 15, scale=2.0**40, limbs=L, enc_id=1)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        ct = ctx.rotate_g(ct, g)
+        n += 1
+        if time.perf_counter() - t0 > seconds_budget or n >= 64:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
+            "sample": f"{n} chained rotations of one ciphertext at 36 limbs, N=2^16 "
+                      f"(oracle/ckks_oracle.c, OpenMP over limbs)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--cts", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the key-switch "
+              "path shards by ciphertext, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    from easyfhe import _native, fhe
+
+    spec = fhe.CKKSContextSpec(depth=PARAMS["depth"], log_n=PARAMS["log_n"], dnum=PARAMS["dnum"],
+                               dcrt_bits=PARAMS["dcrt_bits"], first_mod=PARAMS["first_mod"],
+                               special_bits=PARAMS["special_bits"], seed=0, rotations=ROTATIONS)
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    ctx.synchronize()
+    keygen_s = time.perf_counter() - t0
+    N, L, alpha = ctx.N, ctx.L, ctx.alpha
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    cts = [client.encrypt(rng.uniform(-1, 1, slots), slots=slots, enc_id=i + 1)
+           for i in range(args.cts)]
+    ctx.synchronize()
+    levels = min(args.levels, L - 2)
+
+    def step():
+        cur = cts
+        for r in ROTATIONS:
+            nxt = fhe.homo_rotate_many(cur, r, ctx)
+            if cur is not cts:
+                for c in cur:
+                    c.release()
+            cur = nxt
+        for _ in range(levels):
+            nxt = fhe.homo_mul_relin_rescale_many(cur, cur, ctx)
+            for c in cur:
+                if c not in cts:
+                    c.release()
+            cur = nxt
+        return cur
+
+    for _ in range(args.warmup):
+        out = step()
+        for c in out:
+            c.release()
+    ctx.synchronize()
+    ev0 = fhe_event(ctx)
+    ev1 = fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+        for c in out:
+            c.release()
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ks_per_step = args.cts * (len(ROTATIONS) + levels)
+    ms_per_step = wall * 1000.0 / args.steps
+    value = ks_per_step * args.steps / wall
+
+    # algorithmic bytes of the key switches of one step
+    digits_at = lambda l: -(-l // ctx.digit_size)  # noqa: E731
+    step_bytes = len(ROTATIONS) * args.cts * keyswitch_bytes(N, L, alpha, digits_at(L), args.cts, False)
+    for lvl in range(levels):
+        l = L - lvl
+        step_bytes += args.cts * keyswitch_bytes(N, l, alpha, digits_at(l), args.cts, True)
+    ks_gbs = step_bytes * args.steps / wall / 1e9
+
+    # dominant kernel: the two-pass NTT over all limb-polynomials of the batch,
+    # timed with events on the library stream (forward then inverse so the
+    # data stays valid)
+    batch = fhe_ptrs(cts)
+    ntt_iters = 5
+    e0, e1 = fhe_event(ctx), fhe_event(ctx)
+    _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 0))
+    _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 1))
+    e0.record()
+    for _ in range(ntt_iters):
+        _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 0))
+        _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 1))
+    e1.record()
+    ctx.synchronize()
+    ntt_ms = e0.elapsed_time(e1) / (2 * ntt_iters)  # one full (2-pass) transform of the batch
+    limb_polys = len(cts) * 2 * L
+    ntt_bytes = limb_polys * 2.0 * 8 * N  # read + write each limb-polynomial once
+    achieved = ntt_bytes / (ntt_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "keyswitch/s @N=2^16",
+        "value": round(value, 2),
+        "unit": "keyswitch/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {
+            "workload": "keyswitch/rotation microbench: 64 ciphertexts, N=2^16, Q=1x60b+35x40b, "
+                        "dnum=3, P=12x60b; rotations 2^0..2^14 then HMult+relin+rescale 36->2",
+            "ciphertexts": args.cts,
+            "keyswitches_per_step": ks_per_step,
+            "levels_per_step": levels,
+        },
+        "keyswitch_hbm_gbs": round(ks_gbs, 1),
+        "gpu_event_ms_per_step": round(gpu_ms / args.steps, 3),
+        "keygen_s": round(keygen_s, 2),
+        "roofline": {
+            "kernel": "ntt (k_ntt_fwd_high + k_ntt_fwd_low / k_ntt_inv_low + k_ntt_inv_high)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_ms": round(ntt_ms, 4),
+            "limb_polys_per_launch": limb_polys,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def fhe_event(ctx):
+    from easyfhe.cuda import Event
+
+    return Event(enable_timing=True, context=ctx)
+
+
+def fhe_ptrs(cts):
+    from easyfhe._native import ptr_array
+
+    return ptr_array([c.handle for c in cts])
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,1588 @@
+// ckks_api.hip -- context set-up, device memory pool, key-switching pipeline
+// and the extern "C" entry points declared in include/ckks_mi355x.h.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <stdexcept>
+#include <thread>
+
+#include "ckks_internal.hpp"
+
+typedef unsigned __int128 u128;
+using namespace ckks;
+
+// ===========================================================================
+// errors
+// ===========================================================================
+
+static thread_local std::string g_err;
+
+const char *ckks_last_error(void) { return g_err.c_str(); }
+
+#define HIPCHECK(x)                                                          \
+  do {                                                                       \
+    hipError_t e_ = (x);                                                     \
+    if (e_ != hipSuccess)                                                    \
+      throw std::runtime_error(std::string(#x ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+struct KeyMissing : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+#define API_BEGIN try {
+#define API_END                                   \
+  return CKKS_OK;                                 \
+  }                                               \
+  catch (const std::invalid_argument &e) {        \
+    g_err = e.what();                             \
+    return CKKS_EINVAL;                           \
+  }                                               \
+  catch (const KeyMissing &e) {                   \
+    g_err = e.what();                             \
+    return CKKS_ENOKEY;                           \
+  }                                               \
+  catch (const std::exception &e) {               \
+    g_err = e.what();                             \
+    return CKKS_ERUNTIME;                         \
+  }
+
+static void require(bool cond, const std::string &msg) {
+  if (!cond) throw std::invalid_argument(msg);
+}
+
+// ===========================================================================
+// device memory pool: exact-size free lists, all use is ordered on the
+// context's single stream, so a buffer released here can be handed to the
+// next kernel on that stream without a synchronisation.
+// ===========================================================================
+
+void *Pool::alloc(size_t bytes) {
+  bytes = (bytes + 255) & ~(size_t)255;
+  auto it = free_.find(bytes);
+  void *p = nullptr;
+  if (it != free_.end() && !it->second.empty()) {
+    p = it->second.back();
+    it->second.pop_back();
+    cached -= bytes;
+  } else if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    trim();
+    HIPCHECK(hipMalloc(&p, bytes));
+  }
+  live += bytes;
+  live_[p] = bytes;
+  return p;
+}
+
+void Pool::release(void *p, size_t bytes) {
+  if (!p) return;
+  bytes = (bytes + 255) & ~(size_t)255;
+  live_.erase(p);
+  free_[bytes].push_back(p);
+  live -= bytes;
+  cached += bytes;
+}
+
+void Pool::release_all() {
+  trim();
+  for (auto &kv : live_) (void)hipFree(kv.first);
+  live_.clear();
+  live = 0;
+}
+
+// Contexts that are alive; a ciphertext released after its context was
+// destroyed only drops its host record (the device memory went with the
+// context).
+static std::unordered_map<ckks_context *, int> g_live_contexts;
+
+void Pool::trim() {
+  (void)hipDeviceSynchronize();
+  for (auto &kv : free_)
+    for (void *p : kv.second) (void)hipFree(p);
+  free_.clear();
+  cached = 0;
+}
+
+// ===========================================================================
+// host number theory (prime rule, roots, constants)
+// ===========================================================================
+
+static u64 mulmod_h(u64 a, u64 b, u64 q) { return (u64)(((u128)a * b) % q); }
+
+static u64 powmod_h(u64 a, u64 e, u64 q) {
+  u64 r = 1 % q;
+  a %= q;
+  while (e) {
+    if (e & 1) r = mulmod_h(r, a, q);
+    a = mulmod_h(a, a, q);
+    e >>= 1;
+  }
+  return r;
+}
+
+static u64 invmod_h(u64 a, u64 q) { return powmod_h(a % q, q - 2, q); }
+
+static bool is_prime_h(u64 n) {
+  static const u64 bases[12] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+  if (n < 2) return false;
+  for (u64 b : bases) {
+    if (n == b) return true;
+    if (n % b == 0) return false;
+  }
+  u64 d = n - 1;
+  int r = 0;
+  while (!(d & 1)) {
+    d >>= 1;
+    r++;
+  }
+  for (u64 b : bases) {
+    u64 x = powmod_h(b, d, n);
+    if (x == 1 || x == n - 1) continue;
+    bool comp = true;
+    for (int k = 1; k < r && comp; k++) {
+      x = mulmod_h(x, x, n);
+      if (x == n - 1) comp = false;
+    }
+    if (comp) return false;
+  }
+  return true;
+}
+
+// Primes q = 1 mod 2N nearest to 2^bits (2^bits + 1 first, then for each
+// distance k*2N the one below before the one above), never >= 2^60.
+static std::vector<u64> prime_chain(int logN, int bits, int count, const std::vector<u64> &used) {
+  const u64 M = (u64)2 << logN, base = (u64)1 << bits, cap = (u64)1 << 60;
+  std::vector<u64> out;
+  for (u64 k = 0; (int)out.size() < count; k++) {
+    if (k * M >= base && base + k * M + 1 >= cap) break;
+    u64 cands[2];
+    int nc = 0;
+    if (k == 0)
+      cands[nc++] = base + 1;
+    else {
+      if (k * M < base) cands[nc++] = base - k * M + 1;
+      cands[nc++] = base + k * M + 1;
+    }
+    for (int i = 0; i < nc && (int)out.size() < count; i++) {
+      u64 cnd = cands[i];
+      if (cnd >= cap || cnd <= M) continue;
+      if (std::find(used.begin(), used.end(), cnd) != used.end()) continue;
+      if (std::find(out.begin(), out.end(), cnd) != out.end()) continue;
+      if (is_prime_h(cnd)) out.push_back(cnd);
+    }
+  }
+  if ((int)out.size() != count) throw std::invalid_argument("prime search exhausted");
+  return out;
+}
+
+// Smallest primitive 2N-th root: psi0 from the first x with psi0^N = -1,
+// then the minimum over its odd powers.
+static u64 min_root_h(u64 q, int logN) {
+  const u64 N = (u64)1 << logN, M = 2 * N;
+  u64 psi0 = 0;
+  for (u64 x = 2;; x++) {
+    psi0 = powmod_h(x, (q - 1) / M, q);
+    if (powmod_h(psi0, N, q) == q - 1) break;
+  }
+  u64 sq = mulmod_h(psi0, psi0, q), cur = psi0, best = psi0;
+  for (u64 k = 1; k < N; k++) {
+    cur = mulmod_h(cur, sq, q);
+    best = std::min(best, cur);
+  }
+  return best;
+}
+
+static u32 bitrev_h(u32 x, int bits) {
+  u32 r = 0;
+  for (int i = 0; i < bits; i++) {
+    r = (r << 1) | (x & 1);
+    x >>= 1;
+  }
+  return r;
+}
+
+static u64 shoup_h(u64 w, u64 q) { return (u64)(((u128)w << 64) / q); }
+
+static ModQ make_modq(u64 q) {
+  ModQ m{};
+  m.q = q;
+  u64 inv = q;  // Newton iteration for q^-1 mod 2^64
+  for (int i = 0; i < 6; i++) inv *= 2 - q * inv;
+  m.qinv = (u64)0 - inv;
+  u64 r1 = (u64)((((u128)1) << 64) % q);
+  m.r2 = mulmod_h(r1, r1, q);
+  int k = 64 - __builtin_clzll(q);
+  m.k = (u32)k;
+  m.mu = (u64)((((u128)1) << (2 * k)) / q);
+  return m;
+}
+
+// ChaCha20 block (RFC 8439) for the host-side secret sampler.
+static inline u32 rotl_h(u32 v, int c) { return (v << c) | (v >> (32 - c)); }
+static void chacha_h(u64 seed, u32 dom, u32 id, u32 sub, u32 counter, u32 out[16]) {
+  u32 s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
+               (u32)seed,   (u32)(seed >> 32), 0u, 0u, 0u, 0u, 0u, 0u,
+               counter,     dom,         id,          sub};
+  u32 x[16];
+  memcpy(x, s, sizeof(s));
+  auto qr = [&](int a, int b, int c, int d) {
+    x[a] += x[b]; x[d] ^= x[a]; x[d] = rotl_h(x[d], 16);
+    x[c] += x[d]; x[b] ^= x[c]; x[b] = rotl_h(x[b], 12);
+    x[a] += x[b]; x[d] ^= x[a]; x[d] = rotl_h(x[d], 8);
+    x[c] += x[d]; x[b] ^= x[c]; x[b] = rotl_h(x[b], 7);
+  };
+  for (int i = 0; i < 10; i++) {
+    qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15);
+    qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14);
+  }
+  for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
+}
+
+// Secret rule: sparse ternary of weight h by a partial Fisher-Yates shuffle
+// (64-bit words t = 0, 1, ... of stream (SECRET, 0, 0): position word, sign
+// word), or uniform ternary (word mod 3 - 1).
+static std::vector<int8_t> sample_secret(u64 seed, int N, int mode, int h) {
+  std::vector<int8_t> s(N, 0);
+  u64 word = 0;
+  auto next = [&]() {
+    u32 blk[16];
+    chacha_h(seed, 1, 0, 0, (u32)(word >> 3), blk);
+    int r = (int)(word & 7);
+    word++;
+    return (u64)blk[2 * r] | ((u64)blk[2 * r + 1] << 32);
+  };
+  if (mode == 0) {
+    std::vector<u32> perm(N);
+    for (int i = 0; i < N; i++) perm[i] = (u32)i;
+    for (int t = 0; t < h; t++) {
+      u64 r = next(), sg = next();
+      u64 j = (u64)t + r % (u64)(N - t);
+      std::swap(perm[t], perm[j]);
+      s[perm[t]] = (sg & 1) ? -1 : 1;
+    }
+  } else {
+    for (int i = 0; i < N; i++) s[i] = (int8_t)((int)(next() % 3) - 1);
+  }
+  return s;
+}
+
+template <class F>
+static void parallel_for(int n, F f) {
+  unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> th;
+  for (unsigned w = 0; w < hw; w++)
+    th.emplace_back([&, w]() {
+      for (int i = (int)w; i < n; i += (int)hw) f(i);
+    });
+  for (auto &t : th) t.join();
+}
+
+// ===========================================================================
+// per-level constant tables (built once, device resident)
+// ===========================================================================
+
+static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::vector<u64> &dst) {
+  const int ns = (int)src.size(), nd = (int)dst.size();
+  std::vector<u64> h(2 * ns + (size_t)ns * nd + nd);
+  for (int t = 0; t < nd; t++) {
+    u64 m = 1;
+    for (int j = 0; j < ns; j++) m = mulmod_h(m, src[j] % dst[t], dst[t]);
+    h[2 * ns + (size_t)ns * nd + t] = m;
+  }
+  for (int i = 0; i < ns; i++) {
+    const u64 qi = src[i];
+    u64 prod = 1;
+    for (int j = 0; j < ns; j++)
+      if (j != i) prod = mulmod_h(prod, src[j] % qi, qi);
+    const u64 inv = invmod_h(prod, qi);
+    h[i] = inv;
+    h[ns + i] = shoup_h(inv, qi);
+    for (int t = 0; t < nd; t++) {
+      const u64 qt = dst[t];
+      u64 pt = 1;
+      for (int j = 0; j < ns; j++)
+        if (j != i) pt = mulmod_h(pt, src[j] % qt, qt);
+      h[2 * ns + (size_t)i * nd + t] = (u64)(((u128)pt << 64) % qt);  // Montgomery form
+    }
+  }
+  BCTable t{ns, nd, nullptr, sizeof(u64) * h.size()};
+  HIPCHECK(hipMalloc(&t.d, t.bytes));
+  HIPCHECK(hipMemcpy(t.d, h.data(), t.bytes, hipMemcpyHostToDevice));
+  return t;
+}
+
+static const BCTable &bc_up(ckks_context *c, int limbs, int j) {
+  auto key = std::make_pair(limbs, j);
+  auto it = c->bc_up.find(key);
+  if (it != c->bc_up.end()) return it->second;
+  const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs);
+  const int E = limbs + c->alpha;
+  std::vector<u64> src, dst;
+  for (int i = lo; i < hi; i++) src.push_back(c->primes[i]);
+  for (int l = 0; l < E; l++) {
+    if (l >= lo && l < hi) continue;
+    dst.push_back(l < limbs ? c->primes[l] : c->primes[c->L + (l - limbs)]);
+  }
+  return c->bc_up[key] = make_bc(c, src, dst);
+}
+
+static const BCTable &bc_down(ckks_context *c, int limbs) {
+  auto it = c->bc_down.find(limbs);
+  if (it != c->bc_down.end()) return it->second;
+  std::vector<u64> src, dst;
+  for (int j = 0; j < c->alpha; j++) src.push_back(c->primes[c->L + j]);
+  for (int i = 0; i < limbs; i++) dst.push_back(c->primes[i]);
+  return c->bc_down[limbs] = make_bc(c, src, dst);
+}
+
+static const u64 *pinv_table(ckks_context *c, int limbs) {
+  auto it = c->pinv.find(limbs);
+  if (it != c->pinv.end()) return it->second;
+  std::vector<u64> h(2 * (size_t)limbs);
+  for (int i = 0; i < limbs; i++) {
+    const u64 q = c->primes[i];
+    u64 P = 1;
+    for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
+    const u64 inv = invmod_h(P, q);
+    h[2 * i] = inv;
+    h[2 * i + 1] = shoup_h(inv, q);
+  }
+  u64 *d = nullptr;
+  HIPCHECK(hipMalloc(&d, sizeof(u64) * h.size()));
+  HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
+  return c->pinv[limbs] = d;
+}
+
+static const u64 *rescale_table(ckks_context *c, int limbs) {
+  auto it = c->rescale_c.find(limbs);
+  if (it != c->rescale_c.end()) return it->second;
+  const u64 ql = c->primes[limbs - 1];
+  std::vector<u64> h(4 * (size_t)(limbs - 1), 0);
+  for (int i = 0; i < limbs - 1; i++) {
+    const u64 q = c->primes[i];
+    const u64 m = ql % q, inv = invmod_h(m, q);
+    h[4 * i] = m;
+    h[4 * i + 1] = inv;
+    h[4 * i + 2] = shoup_h(inv, q);
+  }
+  u64 *d = nullptr;
+  HIPCHECK(hipMalloc(&d, sizeof(u64) * std::max<size_t>(4, h.size())));
+  if (!h.empty())
+    HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
+  return c->rescale_c[limbs] = d;
+}
+
+/* cos and sin of 2 pi j / n (n a power of two) from IEEE basic operations
+ * only, so the result does not depend on the compiler or the libm in use
+ * (glibc's sin and sincos differ in the last bit for some arguments):
+ * integer octant reduction of 8 j / n, then Taylor series of degree 22 on
+ * [0, pi/4] by Horner's rule. */
+static void unit_root(long long j, long long n, double *cs, double *sn) {
+  static const double PI_4 = 0.78539816339744830962;
+  j %= n;
+  if (j < 0) j += n;
+  const long long e8 = 8 * j, o = e8 / n, r = e8 - o * n;
+  const long long rr = (o & 1) ? n - r : r;
+  const double x = PI_4 * ((double)rr / (double)n);
+  const double x2 = x * x;
+  double inv_fact[23];
+  inv_fact[0] = 1.0;
+  for (int k = 1; k <= 22; k++) inv_fact[k] = inv_fact[k - 1] / (double)k;
+  double sp = 0.0, cp = 0.0;
+  for (int k = 21; k >= 3; k -= 2) sp = (sp + (((k - 1) / 2) % 2 ? -inv_fact[k] : inv_fact[k])) * x2;
+  const double S = (sp + 1.0) * x;
+  for (int k = 22; k >= 2; k -= 2) cp = (cp + ((k / 2) % 2 ? -inv_fact[k] : inv_fact[k])) * x2;
+  const double C = cp + 1.0;
+  double c, s;
+  switch (o) {
+    case 0: c = C; s = S; break;
+    case 1: c = S; s = C; break;
+    case 2: c = -S; s = C; break;
+    case 3: c = -C; s = S; break;
+    case 4: c = -C; s = -S; break;
+    case 5: c = -S; s = -C; break;
+    case 6: c = S; s = -C; break;
+    default: c = C; s = -S; break;
+  }
+  *cs = c;
+  *sn = s;
+}
+
+static const FFTTable &fft_table(ckks_context *c, int n) {
+  auto it = c->fft.find(n);
+  if (it != c->fft.end()) return it->second;
+  std::vector<double> fw(n > 1 ? n : 2), iv(n > 1 ? n : 2), tw(2 * (size_t)n), utw(2 * (size_t)n);
+  for (int j = 0; j < n / 2; j++) {
+    double cs, sn;
+    unit_root(j, n, &cs, &sn);
+    fw[2 * j] = cs;
+    fw[2 * j + 1] = sn;
+    iv[2 * j] = cs;
+    iv[2 * j + 1] = -sn;
+  }
+  for (int k = 0; k < n; k++) {
+    double cs, sn;
+    unit_root(k, 4 * (long long)n, &cs, &sn);
+    tw[2 * k] = cs;
+    tw[2 * k + 1] = -sn;
+    utw[2 * k] = cs;
+    utw[2 * k + 1] = sn;
+  }
+  std::vector<u32> perm(n);
+  for (int j = 0; j < n; j++) perm[j] = (u32)((powmod_h(5, (u64)j, 4 * (u64)n) - 1) / 4);
+  FFTTable t{};
+  t.n = n;
+  auto up = [&](void **dst, const void *src, size_t bytes) {
+    HIPCHECK(hipMalloc(dst, bytes));
+    HIPCHECK(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+  };
+  up((void **)&t.tw_fwd, fw.data(), sizeof(double) * fw.size());
+  up((void **)&t.tw_inv, iv.data(), sizeof(double) * iv.size());
+  up((void **)&t.twist, tw.data(), sizeof(double) * tw.size());
+  up((void **)&t.untwist, utw.data(), sizeof(double) * utw.size());
+  up((void **)&t.perm, perm.data(), sizeof(u32) * perm.size());
+  return c->fft[n] = t;
+}
+
+// ===========================================================================
+// context
+// ===========================================================================
+
+static u64 galois_of(const ckks_context *c, int64_t rotation) {
+  const u64 M = 2 * (u64)c->N;
+  if ((u64)rotation == M - 1) return M - 1;
+  const int64_t half = c->N / 2;
+  int64_t r = rotation % half;
+  if (r < 0) r += half;
+  return powmod_h(5, (u64)r, M);
+}
+
+static void build_context(ckks_context *c, const ckks_params &p) {
+  require(p.log_n >= 10 && p.log_n <= 17, "log_n must be in [10, 17]");
+  require(p.depth >= 0, "depth must be non-negative");
+  require(p.dnum >= 1, "dnum must be positive");
+  require(p.dcrt_bits >= 33 && p.dcrt_bits <= 60, "dcrt_bits must be in [33, 60]");
+  require(p.first_mod >= 33 && p.first_mod <= 60, "first_mod must be in [33, 60]");
+  require(p.special_bits >= 33 && p.special_bits <= 60, "special_bits must be in [33, 60]");
+  c->params = p;
+  c->logN = p.log_n;
+  c->N = 1 << p.log_n;
+  c->L = p.depth + 1;
+  c->ds = (c->L + p.dnum - 1) / p.dnum;
+  c->alpha = c->ds;
+  c->K = c->L + c->alpha;
+  require(c->ds <= kMaxDigitSize, "digit size ceil((depth+1)/dnum) must be <= 16");
+  require((c->L + c->ds - 1) / c->ds <= kMaxDigits, "at most 8 key-switching digits");
+  require(p.secret_mode == 0 || p.secret_mode == 1, "secret_mode must be 0 or 1");
+  require(p.secret_mode == 1 || (p.hamming_weight > 0 && p.hamming_weight <= c->N),
+          "hamming weight out of range");
+
+  std::vector<u64> used;
+  auto q0 = prime_chain(c->logN, p.first_mod, 1, used);
+  used = q0;
+  auto qs = prime_chain(c->logN, p.dcrt_bits, c->L - 1, used);
+  used.insert(used.end(), qs.begin(), qs.end());
+  auto ps = prime_chain(c->logN, p.special_bits, c->alpha, used);
+  c->primes = used;
+  c->primes.insert(c->primes.end(), ps.begin(), ps.end());
+  // P must exceed every digit's modulus.
+  double logP = 0;
+  for (u64 v : ps) logP += log2((double)v);
+  for (int j = 0; j * c->ds < c->L; j++) {
+    double logD = 0;
+    for (int i = j * c->ds; i < std::min((j + 1) * c->ds, c->L); i++) logD += log2((double)c->primes[i]);
+    require(logP > logD, "special modulus P must exceed every digit modulus");
+  }
+
+  const int K = c->K, N = c->N;
+  c->h_mods.resize(K);
+  for (int i = 0; i < K; i++) c->h_mods[i] = make_modq(c->primes[i]);
+  HIPCHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  HIPCHECK(hipMalloc(&c->d_mods, sizeof(ModQ) * K));
+  HIPCHECK(hipMemcpy(c->d_mods, c->h_mods.data(), sizeof(ModQ) * K, hipMemcpyHostToDevice));
+
+  std::vector<u64> psi((size_t)K * N), psi_sh((size_t)K * N), ipsi((size_t)K * N),
+      ipsi_sh((size_t)K * N), ninv(2 * (size_t)K);
+  parallel_for(K, [&](int pi) {
+    const u64 q = c->primes[pi];
+    const u64 r = min_root_h(q, c->logN), ri = invmod_h(r, q);
+    std::vector<u64> pw(N), ipw(N);
+    pw[0] = ipw[0] = 1;
+    for (int i = 1; i < N; i++) {
+      pw[i] = mulmod_h(pw[i - 1], r, q);
+      ipw[i] = mulmod_h(ipw[i - 1], ri, q);
+    }
+    for (int i = 0; i < N; i++) {
+      const u32 b = bitrev_h((u32)i, c->logN);
+      const size_t o = (size_t)pi * N + i;
+      psi[o] = pw[b];
+      psi_sh[o] = shoup_h(pw[b], q);
+      ipsi[o] = ipw[b];
+      ipsi_sh[o] = shoup_h(ipw[b], q);
+    }
+    ninv[2 * pi] = invmod_h((u64)N, q);
+    ninv[2 * pi + 1] = shoup_h(ninv[2 * pi], q);
+  });
+  auto up = [&](u64 **dst, const std::vector<u64> &v) {
+    HIPCHECK(hipMalloc(dst, sizeof(u64) * v.size()));
+    HIPCHECK(hipMemcpy(*dst, v.data(), sizeof(u64) * v.size(), hipMemcpyHostToDevice));
+  };
+  up(&c->d_psi, psi);
+  up(&c->d_psi_sh, psi_sh);
+  up(&c->d_ipsi, ipsi);
+  up(&c->d_ipsi_sh, ipsi_sh);
+  up(&c->d_ninv, ninv);
+
+  // secret: sampled on the host (client side), moved to every prime's NTT domain
+  c->secret = sample_secret(p.seed, N, p.secret_mode, p.hamming_weight);
+  std::vector<long long> sv(N);
+  for (int i = 0; i < N; i++) sv[i] = c->secret[i];
+  long long *d_sv = nullptr;
+  HIPCHECK(hipMalloc(&d_sv, sizeof(long long) * N));
+  HIPCHECK(hipMemcpy(d_sv, sv.data(), sizeof(long long) * N, hipMemcpyHostToDevice));
+  HIPCHECK(hipMalloc(&c->d_secret, sizeof(u64) * (size_t)K * N));
+  launch_expand_ntt(c, d_sv, c->d_secret, K, c->L);
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  HIPCHECK(hipFree(d_sv));
+}
+
+static void free_context(ckks_context *c) {
+  if (!c) return;
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto &kv : c->keys) (void)hipFree(kv.second.data);
+  for (auto &kv : c->bc_up) (void)hipFree(kv.second.d);
+  for (auto &kv : c->bc_down) (void)hipFree(kv.second.d);
+  for (auto &kv : c->pinv) (void)hipFree(kv.second);
+  for (auto &kv : c->rescale_c) (void)hipFree(kv.second);
+  for (auto &kv : c->garner) (void)hipFree(kv.second);
+  for (auto &kv : c->fft) {
+    (void)hipFree(kv.second.tw_fwd);
+    (void)hipFree(kv.second.tw_inv);
+    (void)hipFree(kv.second.twist);
+    (void)hipFree(kv.second.untwist);
+    (void)hipFree(kv.second.perm);
+  }
+  (void)hipFree(c->d_mods);
+  (void)hipFree(c->d_psi);
+  (void)hipFree(c->d_psi_sh);
+  (void)hipFree(c->d_ipsi);
+  (void)hipFree(c->d_ipsi_sh);
+  (void)hipFree(c->d_ninv);
+  (void)hipFree(c->d_secret);
+  c->pool.trim();
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+// ===========================================================================
+// ciphertext objects
+// ===========================================================================
+
+static ckks_ct *new_ct(ckks_context *c, int polys, int limbs, int is_ext, int slots,
+                       double scale, int scale_degree) {
+  ckks_ct *ct = new ckks_ct();
+  ct->ctx = c;
+  ct->polys = polys;
+  ct->limbs = limbs;
+  ct->is_ext = is_ext;
+  ct->slots = slots;
+  ct->scale = scale;
+  ct->scale_degree = scale_degree;
+  const int rows = polys == 0 ? 1 : polys;
+  const int per = polys == 0 ? limbs : (limbs + (is_ext ? c->alpha : 0)) * c->N;
+  ct->bytes = sizeof(u64) * (size_t)rows * per;
+  ct->d = (u64 *)c->pool.alloc(ct->bytes);
+  return ct;
+}
+
+static void free_ct(ckks_ct *ct) {
+  if (!ct) return;
+  if (g_live_contexts.count(ct->ctx)) ct->ctx->pool.release(ct->d, ct->bytes);
+  delete ct;
+}
+
+static void check_ct(const ckks_context *c, const ckks_ct *ct, const char *what) {
+  require(ct != nullptr, std::string(what) + ": null ciphertext");
+  require(ct->ctx == c, std::string(what) + ": ciphertext belongs to another context");
+}
+
+static int poly_words(const ckks_context *c, const ckks_ct *ct) {
+  return (ct->limbs + (ct->is_ext ? c->alpha : 0)) * c->N;
+}
+
+// scales of two operands that are combined limb-wise must agree to 2^-10
+// relative (fixed-scale bookkeeping); the result takes the left scale.
+static void check_scales(const ckks_ct *a, const ckks_ct *b) {
+  const double r = fabs(a->scale - b->scale) / std::max(a->scale, b->scale);
+  require(r < 1.0 / 1024.0, "operand scales differ");
+}
+
+// ===========================================================================
+// key switching pipeline
+// ===========================================================================
+
+struct Scratch {
+  ckks_context *c;
+  std::vector<std::pair<void *, size_t>> bufs;
+  explicit Scratch(ckks_context *cc) : c(cc) {}
+  u64 *get(size_t words) {
+    void *p = c->pool.alloc(sizeof(u64) * words);
+    bufs.emplace_back(p, sizeof(u64) * words);
+    return (u64 *)p;
+  }
+  ~Scratch() {
+    for (auto &b : bufs) c->pool.release(b.first, b.second);
+  }
+};
+
+static Batch strided(u64 *base, size_t stride) {
+  Batch b{};
+  b.base = base;
+  b.stride = stride;
+  return b;
+}
+
+// ModUp of n polynomials d[i] (NTT domain, `limbs` limbs) into
+// ext = [n][digits][E][N].
+static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
+                     Scratch &s) {
+  const size_t N = c->N;
+  const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  u64 *coeff = s.get((size_t)n * limbs * N);
+  Batch src{};
+  for (int i = 0; i < n; i++) src.p[i] = (u64 *)d[i];
+  launch_ntt(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs, true);
+  for (int j = 0; j < digits; j++) {
+    const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
+    Batch dsrc{};
+    for (int i = 0; i < n; i++) dsrc.p[i] = (u64 *)d[i] + (size_t)lo * N;
+    u64 *ej = ext + (size_t)j * E * N;
+    const size_t est = (size_t)digits * E * N;
+    launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
+    launch_basis_convert(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N), strided(ej, est), n,
+                         bc_up(c, limbs, j), lo, lo, ns, limbs, false);
+    launch_ntt(c, strided(ej, est), strided(ej, est), n, 0, lo, limbs, false);
+    launch_ntt(c, strided(ej, est), strided(ej, est), n, hi, E - hi, limbs, false);
+  }
+}
+
+struct KsJob {
+  int ext_item;
+  const DeviceKey *key;
+  u64 galois;
+  const u64 *add0, *add1;
+  u64 *out0, *out1;
+};
+
+// Key inner product for every job, ModDown, and the combine with addends.
+static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
+                      const std::vector<KsJob> &jobs, Scratch &s) {
+  const size_t N = c->N;
+  const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const int n = (int)jobs.size();
+  const size_t est = (size_t)digits * E * N;
+  u64 *acc = s.get((size_t)n * 2 * E * N);
+  bool shared = true;
+  for (int i = 0; i < n; i++)
+    shared = shared && jobs[i].ext_item == i && jobs[i].key == jobs[0].key &&
+             jobs[i].galois == jobs[0].galois;
+  if (shared) {
+    launch_key_inner(c, strided((u64 *)ext, est), strided(acc, 2 * E * N), n, *jobs[0].key,
+                     digits, E, limbs, jobs[0].galois);
+  } else {
+    for (int i = 0; i < n; i++)
+      launch_key_inner(c, strided((u64 *)ext + (size_t)jobs[i].ext_item * est, 0),
+                       strided(acc + (size_t)i * 2 * E * N, 0), 1, *jobs[i].key, digits, E,
+                       limbs, jobs[i].galois);
+  }
+  (void)n_ext;
+  // ModDown: iNTT of the P limbs of both components
+  u64 *ptmp = s.get((size_t)n * 2 * c->alpha * N);
+  launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N),
+             2 * n, limbs, c->alpha, limbs, true);
+  u64 *conv = s.get((size_t)n * 2 * limbs * N);
+  launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
+                       2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+  launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2 * n, 0,
+             limbs, limbs, false);
+  const u64 *pinv = pinv_table(c, limbs);
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Batch a0{}, a1{}, o0{}, o1{};
+    std::vector<u64> gal(nb);
+    for (int i = 0; i < nb; i++) {
+      const KsJob &jb = jobs[b0 + i];
+      a0.p[i] = (u64 *)jb.add0;
+      a1.p[i] = (u64 *)jb.add1;
+      o0.p[i] = jb.out0;
+      o1.p[i] = jb.out1;
+      gal[i] = jb.galois;
+    }
+    Strided sacc{acc + (size_t)b0 * 2 * E * N, 2 * E * N};
+    Strided sconv{conv + (size_t)b0 * 2 * limbs * N, 2 * limbs * N};
+    launch_moddown_combine(c, sacc, sconv, a0, a1, gal.data(), o0, o1, nb, limbs, E, pinv);
+  }
+}
+
+static const DeviceKey &get_key(ckks_context *c, u64 galois) {
+  auto it = c->keys.find(galois);
+  if (it == c->keys.end()) {
+    if (galois == 0) throw KeyMissing("relinearization key not generated");
+    throw KeyMissing("rotation key for Galois element " + std::to_string(galois) +
+                     " not generated");
+  }
+  return it->second;
+}
+
+static void gen_key(ckks_context *c, u64 id, int relin, u64 galois) {
+  if (c->keys.count(id)) return;
+  DeviceKey k{};
+  k.galois = id;
+  k.digits = (c->L + c->ds - 1) / c->ds;
+  k.bytes = sizeof(u64) * (size_t)k.digits * 2 * c->K * c->N;
+  HIPCHECK(hipMalloc(&k.data, k.bytes));
+  launch_keygen(c, k, id, relin, galois);
+  c->keys[id] = k;
+}
+
+// Rotations of n ciphertexts at one level by the same Galois element.
+static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g, ckks_ct **out) {
+  const int limbs = in[0]->limbs;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Scratch s(c);
+    std::vector<const u64 *> d(nb);
+    for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + P;
+    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+    u64 *ext = s.get((size_t)nb * digits * E * N);
+    ks_modup(c, limbs, nb, d.data(), ext, s);
+    const DeviceKey &key = get_key(c, g);
+    std::vector<KsJob> jobs(nb);
+    for (int i = 0; i < nb; i++)
+      jobs[i] = KsJob{i, &key, g, in[b0 + i]->d, nullptr, out[b0 + i]->d, out[b0 + i]->d + P};
+    ks_finish(c, limbs, ext, nb, jobs, s);
+  }
+}
+
+// Relinearisation of n degree-2 ciphertexts into out.
+static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out) {
+  const int limbs = in[0]->limbs;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  const DeviceKey &key = get_key(c, 0);
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Scratch s(c);
+    std::vector<const u64 *> d(nb);
+    for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
+    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+    u64 *ext = s.get((size_t)nb * digits * E * N);
+    ks_modup(c, limbs, nb, d.data(), ext, s);
+    std::vector<KsJob> jobs(nb);
+    for (int i = 0; i < nb; i++)
+      jobs[i] = KsJob{i, &key, 1, in[b0 + i]->d, in[b0 + i]->d + P, out[b0 + i]->d,
+                      out[b0 + i]->d + P};
+    ks_finish(c, limbs, ext, nb, jobs, s);
+  }
+}
+
+// Rescale n ciphertexts of `polys` polynomials each.
+static void rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out) {
+  const int limbs = in[0]->limbs, polys = in[0]->polys;
+  const size_t N = c->N;
+  const u64 *consts = rescale_table(c, limbs);
+  const int per = kMaxBatch / polys;
+  for (int b0 = 0; b0 < n; b0 += per) {
+    const int nb = std::min(per, n - b0), items = nb * polys;
+    Scratch s(c);
+    u64 *last = s.get((size_t)items * N);
+    u64 *r = s.get((size_t)items * (limbs - 1) * N);
+    Batch src{}, dst{};
+    for (int i = 0; i < nb; i++)
+      for (int p = 0; p < polys; p++) {
+        src.p[i * polys + p] = in[b0 + i]->d + (size_t)p * limbs * N;
+        dst.p[i * polys + p] = out[b0 + i]->d + (size_t)p * (limbs - 1) * N;
+      }
+    launch_ntt(c, src, strided(last - (size_t)(limbs - 1) * N, N), items, limbs - 1, 1, limbs,
+               true);
+    launch_rescale_expand(c, strided(last, N), strided(r, (size_t)(limbs - 1) * N), items, limbs);
+    launch_ntt(c, strided(r, (size_t)(limbs - 1) * N), strided(r, (size_t)(limbs - 1) * N), items,
+               0, limbs - 1, limbs - 1, false);
+    launch_rescale_combine(c, src, strided(r, (size_t)(limbs - 1) * N), dst, items, limbs, consts);
+  }
+}
+
+// ===========================================================================
+// extern "C" API
+// ===========================================================================
+
+extern "C" {
+
+int ckks_context_create(const ckks_params *params, ckks_context **out) {
+  API_BEGIN
+  require(params && out, "null argument");
+  ckks_context *c = new ckks_context();
+  c->stream = nullptr;
+  try {
+    build_context(c, *params);
+  } catch (...) {
+    free_context(c);
+    throw;
+  }
+  g_live_contexts[c] = 1;
+  *out = c;
+  API_END
+}
+
+void ckks_context_destroy(ckks_context *ctx) {
+  if (ctx && g_live_contexts.count(ctx)) free_context(ctx);
+}
+
+int ckks_context_info_get(const ckks_context *c, ckks_context_info *o) {
+  API_BEGIN
+  require(c && o, "null argument");
+  o->N = c->N;
+  o->log_n = c->logN;
+  o->L = c->L;
+  o->alpha = c->alpha;
+  o->digit_size = c->ds;
+  o->dnum = c->params.dnum;
+  o->max_slots = c->N / 2;
+  o->default_scale = ldexp(1.0, c->params.dcrt_bits);
+  API_END
+}
+
+int ckks_context_primes(const ckks_context *c, uint64_t *out) {
+  API_BEGIN
+  require(c && out, "null argument");
+  memcpy(out, c->primes.data(), sizeof(u64) * c->primes.size());
+  API_END
+}
+
+int ckks_context_secret(const ckks_context *c, int8_t *out) {
+  API_BEGIN
+  require(c && out, "null argument");
+  memcpy(out, c->secret.data(), c->secret.size());
+  API_END
+}
+
+double ckks_scale_at(const ckks_context *c, int limbs) {
+  (void)limbs;
+  return ldexp(1.0, c->params.dcrt_bits);
+}
+
+double ckks_rescale_divisor_at(const ckks_context *c, int limbs) {
+  if (limbs < 0 || limbs >= c->L) return 0.0;
+  return (double)c->primes[limbs];
+}
+
+uint64_t ckks_galois_element(const ckks_context *c, int64_t rotation) {
+  return galois_of(c, rotation);
+}
+
+int ckks_keygen_rotations(ckks_context *c, const int64_t *rot, int n) {
+  API_BEGIN
+  require(c && (rot || n == 0), "null argument");
+  for (int i = 0; i < n; i++) {
+    const u64 g = galois_of(c, rot[i]);
+    if (g != 1) gen_key(c, g, 0, g);
+  }
+  API_END
+}
+
+int ckks_keygen_relin(ckks_context *c) {
+  API_BEGIN
+  require(c, "null argument");
+  gen_key(c, 0, 1, 0);
+  API_END
+}
+
+int ckks_has_rotation_key(const ckks_context *c, int64_t rotation) {
+  const u64 g = galois_of(c, rotation);
+  return g == 1 || c->keys.count(g) ? 1 : 0;
+}
+
+__global__ void k_from_mont(u64 *d, size_t words, int K, int logN, const ModQ *mods) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= words) return;
+  const int p = (int)((i >> logN) % K);
+  const ModQ M = mods[p];
+  d[i] = redc(0, d[i], M.q, M.qinv);
+}
+
+int ckks_key_download(ckks_context *c, uint64_t galois, uint64_t *out, int *digits) {
+  API_BEGIN
+  require(c, "null argument");
+  const DeviceKey &k = get_key(c, galois);
+  if (digits) *digits = k.digits;
+  if (out) {
+    const size_t words = k.bytes / sizeof(u64);
+    u64 *tmp = (u64 *)c->pool.alloc(k.bytes);
+    HIPCHECK(hipMemcpyAsync(tmp, k.data, k.bytes, hipMemcpyDeviceToDevice, c->stream));
+    hipLaunchKernelGGL(k_from_mont, dim3((words + 255) / 256), dim3(256), 0, c->stream, tmp,
+                       words, c->K, c->logN, c->d_mods);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipMemcpyAsync(out, tmp, k.bytes, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    c->pool.release(tmp, k.bytes);
+  }
+  API_END
+}
+
+int ckks_clear_rotation_keys(ckks_context *c, const int64_t *keep, int n) {
+  API_BEGIN
+  require(c, "null argument");
+  std::vector<u64> kg;
+  for (int i = 0; i < n; i++) kg.push_back(galois_of(c, keep[i]));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  for (auto it = c->keys.begin(); it != c->keys.end();) {
+    if (it->first != 0 && std::find(kg.begin(), kg.end(), it->first) == kg.end()) {
+      (void)hipFree(it->second.data);
+      it = c->keys.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  API_END
+}
+
+int ckks_synchronize(ckks_context *c) {
+  API_BEGIN
+  require(c, "null argument");
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_memory_info(ckks_context *c, size_t *live, size_t *cached) {
+  API_BEGIN
+  require(c, "null argument");
+  if (live) *live = c->pool.live;
+  if (cached) *cached = c->pool.cached;
+  API_END
+}
+
+int ckks_empty_cache(ckks_context *c) {
+  API_BEGIN
+  require(c, "null argument");
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  c->pool.trim();
+  API_END
+}
+
+static void check_slots(const ckks_context *c, int slots) {
+  require(slots >= 1 && slots <= c->N / 2 && !(slots & (slots - 1)),
+          "slots must be a power of two in [1, N/2]");
+  require(slots >= 2, "at least two slots are required");
+}
+
+static void check_limbs(const ckks_context *c, int limbs) {
+  require(limbs >= 1 && limbs <= c->L, "limb count out of range [1, L]");
+}
+
+int ckks_encrypt(ckks_context *c, const double *re, const double *im, int slots, int limbs,
+                 double scale, uint32_t enc_id, ckks_ct **out) {
+  API_BEGIN
+  require(c && re && out, "null argument");
+  check_slots(c, slots);
+  check_limbs(c, limbs);
+  require(scale > 0, "scale must be positive");
+  fft_table(c, slots);
+  ckks_ct *ct = new_ct(c, 2, limbs, 0, slots, scale, 1);
+  Scratch s(c);
+  double *dre = (double *)s.get(slots), *dim = im ? (double *)s.get(slots) : nullptr;
+  HIPCHECK(hipMemcpyAsync(dre, re, sizeof(double) * slots, hipMemcpyHostToDevice, c->stream));
+  if (im)
+    HIPCHECK(hipMemcpyAsync(dim, im, sizeof(double) * slots, hipMemcpyHostToDevice, c->stream));
+  Batch o{};
+  o.p[0] = ct->d;
+  launch_encode(c, dre, dim, 1, slots, scale, limbs, 0, o);
+  launch_encrypt_finish(c, ct->d, limbs, enc_id);
+  HIPCHECK(hipStreamSynchronize(c->stream));  // host buffers are the caller's
+  *out = ct;
+  API_END
+}
+
+int ckks_decrypt(ckks_context *c, const ckks_ct *ct, double *re, double *im) {
+  API_BEGIN
+  require(c && re, "null argument");
+  check_ct(c, ct, "decrypt");
+  require(ct->polys >= 1 && !ct->is_ext, "decrypt needs a Q-basis ciphertext");
+  fft_table(c, ct->slots);
+  Scratch s(c);
+  double *dre = (double *)s.get(ct->slots), *dim = (double *)s.get(ct->slots);
+  launch_decrypt_decode(c, ct, dre, dim);
+  HIPCHECK(hipMemcpyAsync(re, dre, sizeof(double) * ct->slots, hipMemcpyDeviceToHost, c->stream));
+  if (im)
+    HIPCHECK(hipMemcpyAsync(im, dim, sizeof(double) * ct->slots, hipMemcpyDeviceToHost, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_decode(ckks_context *c, const ckks_ct *pt, double *re, double *im) {
+  return ckks_decrypt(c, pt, re, im);
+}
+
+int ckks_encode_rows(ckks_context *c, const double *re, const double *im, int rows, int slots,
+                     int limbs, double scale, int is_ext, ckks_ct **out) {
+  API_BEGIN
+  require(c && re && out, "null argument");
+  require(rows >= 1, "rows must be positive");
+  check_slots(c, slots);
+  check_limbs(c, limbs);
+  fft_table(c, slots);
+  for (int r = 0; r < rows; r++) out[r] = new_ct(c, 1, limbs, is_ext, slots, scale, 1);
+  for (int r0 = 0; r0 < rows; r0 += kMaxBatch) {
+    const int nr = std::min(kMaxBatch, rows - r0);
+    Scratch s(c);
+    double *dre = (double *)s.get((size_t)nr * slots);
+    double *dim = im ? (double *)s.get((size_t)nr * slots) : nullptr;
+    HIPCHECK(hipMemcpyAsync(dre, re + (size_t)r0 * slots, sizeof(double) * nr * slots,
+                            hipMemcpyHostToDevice, c->stream));
+    if (im)
+      HIPCHECK(hipMemcpyAsync(dim, im + (size_t)r0 * slots, sizeof(double) * nr * slots,
+                              hipMemcpyHostToDevice, c->stream));
+    Batch o{};
+    for (int r = 0; r < nr; r++) o.p[r] = out[r0 + r]->d;
+    launch_encode(c, dre, dim, nr, slots, scale, limbs, is_ext, o);
+    HIPCHECK(hipStreamSynchronize(c->stream));
+  }
+  API_END
+}
+
+int ckks_encode_scalar(ckks_context *c, double value, int limbs, double scale, ckks_ct **out) {
+  API_BEGIN
+  require(c && out, "null argument");
+  check_limbs(c, limbs);
+  ckks_ct *ct = new_ct(c, 0, limbs, 0, 0, scale, 1);
+  launch_scalar_encode(c, value * scale, limbs, ct->d);
+  *out = ct;
+  API_END
+}
+
+int ckks_ct_upload(ckks_context *c, const uint64_t *data, int polys, int limbs, int is_ext,
+                   int slots, double scale, int scale_degree, ckks_ct **out) {
+  API_BEGIN
+  require(c && data && out, "null argument");
+  require(polys >= 1 && polys <= 3, "polys must be 1, 2 or 3");
+  check_limbs(c, limbs);
+  ckks_ct *ct = new_ct(c, polys, limbs, is_ext, slots, scale, scale_degree);
+  HIPCHECK(hipMemcpyAsync(ct->d, data, ct->bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  *out = ct;
+  API_END
+}
+
+int ckks_ct_download(ckks_context *c, const ckks_ct *ct, uint64_t *out) {
+  API_BEGIN
+  require(c && out, "null argument");
+  check_ct(c, ct, "download");
+  HIPCHECK(hipMemcpyAsync(out, ct->d, ct->bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_ct_info_get(const ckks_ct *ct, ckks_ct_info *o) {
+  API_BEGIN
+  require(ct && o, "null argument");
+  o->polys = ct->polys;
+  o->limbs = ct->limbs;
+  o->is_ext = ct->is_ext;
+  o->slots = ct->slots;
+  o->scale = ct->scale;
+  o->scale_degree = ct->scale_degree;
+  API_END
+}
+
+int ckks_ct_set_scale(ckks_ct *ct, double scale, int scale_degree) {
+  API_BEGIN
+  require(ct, "null argument");
+  ct->scale = scale;
+  ct->scale_degree = scale_degree;
+  API_END
+}
+
+int ckks_ct_copy(ckks_context *c, const ckks_ct *ct, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, ct, "copy");
+  ckks_ct *o = new_ct(c, ct->polys, ct->limbs, ct->is_ext, ct->slots, ct->scale, ct->scale_degree);
+  HIPCHECK(hipMemcpyAsync(o->d, ct->d, ct->bytes, hipMemcpyDeviceToDevice, c->stream));
+  *out = o;
+  API_END
+}
+
+void ckks_ct_free(ckks_ct *ct) { free_ct(ct); }
+
+static int binary_limbwise(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out,
+                           int op) {
+  API_BEGIN
+  check_ct(c, a, "add/sub");
+  check_ct(c, b, "add/sub");
+  require(out, "null argument");
+  require(a->limbs == b->limbs, "operands must have the same limb count");
+  require(a->is_ext == b->is_ext, "operands must share the basis");
+  require(a->polys == b->polys, "operands must have the same degree");
+  check_scales(a, b);
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, a->is_ext, a->slots, a->scale, a->scale_degree);
+  const int total = a->limbs + (a->is_ext ? c->alpha : 0);
+  launch_addsub(c, a->d, b->d, o->d, a->polys, total, a->limbs, op);
+  *out = o;
+  API_END
+}
+
+int ckks_add(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out) {
+  return binary_limbwise(c, a, b, out, 0);
+}
+
+int ckks_sub(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out) {
+  return binary_limbwise(c, a, b, out, 1);
+}
+
+int ckks_add_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "add_pt");
+  check_ct(c, pt, "add_pt");
+  require(out, "null argument");
+  require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
+  require(!a->is_ext, "add_pt on a Q-basis ciphertext");
+  check_scales(a, pt);
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, 0, a->slots, a->scale, a->scale_degree);
+  const size_t P = (size_t)a->limbs * c->N;
+  launch_addsub(c, a->d, pt->d, o->d, 1, a->limbs, a->limbs, 0);
+  if (a->polys > 1)
+    HIPCHECK(hipMemcpyAsync(o->d + P, a->d + P, sizeof(u64) * P * (a->polys - 1),
+                            hipMemcpyDeviceToDevice, c->stream));
+  *out = o;
+  API_END
+}
+
+int ckks_mul_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "mul_pt");
+  check_ct(c, pt, "mul_pt");
+  require(out, "null argument");
+  require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
+  require(!a->is_ext && !pt->is_ext, "mul_pt expects Q-basis operands");
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, 0, a->slots, a->scale * pt->scale,
+                      a->scale_degree + pt->scale_degree);
+  launch_mul_pt(c, a->d, pt->d, o->d, a->polys, a->limbs, a->limbs);
+  *out = o;
+  API_END
+}
+
+int ckks_mul_i(ckks_context *c, const ckks_ct *a, int negative, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "mul_i");
+  require(out, "null argument");
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, a->is_ext, a->slots, a->scale, a->scale_degree);
+  const int total = a->limbs + (a->is_ext ? c->alpha : 0);
+  launch_mul_i(c, a->d, o->d, a->polys, total, a->limbs, negative);
+  *out = o;
+  API_END
+}
+
+int ckks_add_scalar(ckks_context *c, const ckks_ct *a, const ckks_ct *s, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "add_scalar");
+  check_ct(c, s, "add_scalar");
+  require(out, "null argument");
+  require(s->polys == 0 && s->limbs >= a->limbs, "scalar limbs below ciphertext limbs");
+  require(!a->is_ext, "add_scalar on a Q-basis ciphertext");
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, 0, a->slots, a->scale, a->scale_degree);
+  launch_scalar(c, a->d, s->d, o->d, a->polys, a->limbs, a->limbs, 0);
+  *out = o;
+  API_END
+}
+
+int ckks_mul_scalar(ckks_context *c, const ckks_ct *a, const ckks_ct *s, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "mul_scalar");
+  check_ct(c, s, "mul_scalar");
+  require(out, "null argument");
+  require(s->polys == 0 && s->limbs >= a->limbs, "scalar limbs below ciphertext limbs");
+  require(!a->is_ext, "mul_scalar on a Q-basis ciphertext");
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, 0, a->slots, a->scale * s->scale,
+                      a->scale_degree + (s->scale == 1.0 ? 0 : 1));
+  launch_scalar(c, a->d, s->d, o->d, a->polys, a->limbs, a->limbs, 1);
+  *out = o;
+  API_END
+}
+
+int ckks_mul_no_relin(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "mul");
+  check_ct(c, b, "mul");
+  require(out, "null argument");
+  require(a->polys == 2 && b->polys == 2, "mul expects degree-1 ciphertexts");
+  require(a->limbs == b->limbs, "operands must have the same limb count");
+  require(!a->is_ext && !b->is_ext, "mul expects Q-basis ciphertexts");
+  ckks_ct *o = new_ct(c, 3, a->limbs, 0, a->slots, a->scale * b->scale,
+                      a->scale_degree + b->scale_degree);
+  Batch ba{}, bb{}, bo{};
+  ba.p[0] = a->d;
+  bb.p[0] = b->d;
+  bo.p[0] = o->d;
+  launch_tensor(c, ba, bb, bo, 1, a->limbs);
+  *out = o;
+  API_END
+}
+
+int ckks_relinearize(ckks_context *c, const ckks_ct *a, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "relinearize");
+  require(out, "null argument");
+  require(a->polys == 3, "relinearize expects a degree-2 ciphertext");
+  ckks_ct *o = new_ct(c, 2, a->limbs, 0, a->slots, a->scale, a->scale_degree);
+  try {
+    relin_batch(c, &a, 1, &o);
+  } catch (...) {
+    free_ct(o);
+    throw;
+  }
+  *out = o;
+  API_END
+}
+
+int ckks_mul_relin(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out) {
+  ckks_ct *t = nullptr;
+  int rc = ckks_mul_no_relin(c, a, b, &t);
+  if (rc) return rc;
+  rc = ckks_relinearize(c, t, out);
+  free_ct(t);
+  return rc;
+}
+
+int ckks_rescale(ckks_context *c, const ckks_ct *a, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "rescale");
+  require(out, "null argument");
+  require(a->limbs >= 2, "rescale needs at least two limbs");
+  require(!a->is_ext, "rescale expects a Q-basis ciphertext");
+  const double div = (double)c->primes[a->limbs - 1];
+  ckks_ct *o = new_ct(c, a->polys, a->limbs - 1, 0, a->slots, a->scale / div,
+                      std::max(1, a->scale_degree - 1));
+  rescale_batch(c, &a, 1, &o);
+  *out = o;
+  API_END
+}
+
+int ckks_drop_limbs(ckks_context *c, const ckks_ct *a, int target, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "drop_limbs");
+  require(out, "null argument");
+  require(!a->is_ext, "drop_limbs expects a Q-basis ciphertext");
+  require(target >= 1 && target <= a->limbs, "target limbs out of range");
+  ckks_ct *o = new_ct(c, a->polys, target, 0, a->slots, a->scale, a->scale_degree);
+  const size_t N = c->N;
+  for (int p = 0; p < std::max(1, a->polys); p++)
+    HIPCHECK(hipMemcpyAsync(o->d + (size_t)p * target * N, a->d + (size_t)p * a->limbs * N,
+                            sizeof(u64) * target * N, hipMemcpyDeviceToDevice, c->stream));
+  *out = o;
+  API_END
+}
+
+int ckks_rotate_many(ckks_context *c, const ckks_ct *const *in, int n, int64_t rotation,
+                     ckks_ct **out) {
+  API_BEGIN
+  require(c && in && out && n >= 1, "null argument");
+  for (int i = 0; i < n; i++) {
+    check_ct(c, in[i], "rotate");
+    require(in[i]->polys == 2 && !in[i]->is_ext, "rotate expects degree-1 Q-basis ciphertexts");
+    require(in[i]->limbs == in[0]->limbs, "batched rotation needs one common level");
+  }
+  const u64 g = galois_of(c, rotation);
+  if (g != 1) get_key(c, g);
+  std::vector<ckks_ct *> o(n, nullptr);
+  for (int i = 0; i < n; i++)
+    o[i] = new_ct(c, 2, in[i]->limbs, 0, in[i]->slots, in[i]->scale, in[i]->scale_degree);
+  if (g == 1) {
+    for (int i = 0; i < n; i++)
+      HIPCHECK(hipMemcpyAsync(o[i]->d, in[i]->d, in[i]->bytes, hipMemcpyDeviceToDevice, c->stream));
+  } else {
+    rotate_batch(c, in, n, g, o.data());
+  }
+  for (int i = 0; i < n; i++) out[i] = o[i];
+  API_END
+}
+
+int ckks_rotate(ckks_context *c, const ckks_ct *a, int64_t rotation, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "rotate");
+  require(out, "null argument");
+  const u64 g = galois_of(c, rotation);
+  if (g == 1) {
+    ckks_ct *o = new_ct(c, a->polys, a->limbs, a->is_ext, a->slots, a->scale, a->scale_degree);
+    HIPCHECK(hipMemcpyAsync(o->d, a->d, a->bytes, hipMemcpyDeviceToDevice, c->stream));
+    *out = o;
+    return CKKS_OK;
+  }
+  require(a->polys == 2 && !a->is_ext, "rotate expects a degree-1 Q-basis ciphertext");
+  get_key(c, g);
+  ckks_ct *o = new_ct(c, 2, a->limbs, 0, a->slots, a->scale, a->scale_degree);
+  rotate_batch(c, &a, 1, g, &o);
+  *out = o;
+  API_END
+}
+
+int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
+                                const ckks_ct *const *b, int n, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && b && out && n >= 1, "null argument");
+  const int limbs = a[0]->limbs;
+  require(limbs >= 2, "rescale needs at least two limbs");
+  for (int i = 0; i < n; i++) {
+    check_ct(c, a[i], "mul");
+    check_ct(c, b[i], "mul");
+    require(a[i]->polys == 2 && b[i]->polys == 2, "mul expects degree-1 ciphertexts");
+    require(a[i]->limbs == limbs && b[i]->limbs == limbs, "one common level required");
+  }
+  get_key(c, 0);
+  const size_t N = c->N;
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Scratch s(c);
+    u64 *t3 = s.get((size_t)nb * 3 * limbs * N);
+    u64 *t2 = s.get((size_t)nb * 2 * limbs * N);
+    Batch ba{}, bb{};
+    for (int i = 0; i < nb; i++) {
+      ba.p[i] = a[b0 + i]->d;
+      bb.p[i] = b[b0 + i]->d;
+    }
+    launch_tensor(c, ba, bb, strided(t3, (size_t)3 * limbs * N), nb, limbs);
+    std::vector<ckks_ct> v3(nb), v2(nb);
+    std::vector<const ckks_ct *> p3(nb);
+    std::vector<ckks_ct *> p2(nb);
+    for (int i = 0; i < nb; i++) {
+      v3[i] = ckks_ct{c, t3 + (size_t)i * 3 * limbs * N, 0, 3, limbs, 0, a[b0 + i]->slots, 2, 0};
+      v2[i] = ckks_ct{c, t2 + (size_t)i * 2 * limbs * N, 0, 2, limbs, 0, a[b0 + i]->slots, 2, 0};
+      p3[i] = &v3[i];
+      p2[i] = &v2[i];
+    }
+    relin_batch(c, p3.data(), nb, p2.data());
+    const double div = (double)c->primes[limbs - 1];
+    std::vector<ckks_ct *> o(nb);
+    for (int i = 0; i < nb; i++)
+      o[i] = out[b0 + i] = new_ct(c, 2, limbs - 1, 0, a[b0 + i]->slots,
+                                  a[b0 + i]->scale * b[b0 + i]->scale / div,
+                                  std::max(1, a[b0 + i]->scale_degree + b[b0 + i]->scale_degree - 1));
+    std::vector<const ckks_ct *> cp2(p2.begin(), p2.end());
+    rescale_batch(c, cp2.data(), nb, o.data());
+  }
+  API_END
+}
+
+int ckks_hoisted_rotate(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,
+                        ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "hoisted_rotate");
+  require(out && rotations && n >= 1, "null argument");
+  require(a->polys == 2 && !a->is_ext, "hoisted rotation expects a degree-1 Q-basis ciphertext");
+  const int limbs = a->limbs;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  std::vector<u64> gs(n);
+  for (int i = 0; i < n; i++) {
+    gs[i] = galois_of(c, rotations[i]);
+    if (gs[i] != 1) get_key(c, gs[i]);
+  }
+  std::vector<ckks_ct *> o(n);
+  for (int i = 0; i < n; i++) o[i] = new_ct(c, 2, limbs, 0, a->slots, a->scale, a->scale_degree);
+  std::vector<KsJob> jobs;
+  for (int i = 0; i < n; i++) {
+    if (gs[i] == 1)
+      HIPCHECK(hipMemcpyAsync(o[i]->d, a->d, a->bytes, hipMemcpyDeviceToDevice, c->stream));
+    else
+      jobs.push_back(KsJob{0, &get_key(c, gs[i]), gs[i], a->d, nullptr, o[i]->d, o[i]->d + P});
+  }
+  if (!jobs.empty()) {
+    Scratch s(c);
+    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+    u64 *ext = s.get((size_t)digits * E * N);
+    const u64 *d = a->d + P;
+    ks_modup(c, limbs, 1, &d, ext, s);
+    for (size_t j0 = 0; j0 < jobs.size(); j0 += kMaxBatch) {
+      std::vector<KsJob> part(jobs.begin() + j0,
+                              jobs.begin() + std::min(jobs.size(), j0 + kMaxBatch));
+      ks_finish(c, limbs, ext, 1, part, s);
+    }
+  }
+  for (int i = 0; i < n; i++) out[i] = o[i];
+  API_END
+}
+
+int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
+                         const ckks_ct *const *pts, int64_t giant_rotation, int giant_count,
+                         ckks_ct **out) {
+  API_BEGIN
+  require(c && babies && pts && out, "null argument");
+  require(B >= 1 && B <= kMaxBatch, "baby count must be in [1, 64]");
+  require(giant_count >= 1, "giant_count must be positive");
+  const int limbs = babies[0]->limbs;
+  for (int b = 0; b < B; b++) {
+    check_ct(c, babies[b], "hoisted_mac_sum");
+    require(babies[b]->limbs == limbs && babies[b]->polys == 2 && !babies[b]->is_ext,
+            "babies must be degree-1 Q-basis ciphertexts at one level");
+  }
+  for (int i = 0; i < B * giant_count; i++) {
+    check_ct(c, pts[i], "hoisted_mac_sum");
+    // an extended plaintext stores its Q limbs first, so its leading
+    // `limbs` limbs are used as they are
+    require(pts[i]->polys == 1 && pts[i]->limbs >= limbs,
+            "plaintexts must be at or above the babies' level");
+  }
+  const u64 gg = galois_of(c, giant_rotation);
+  if (giant_count > 1 && gg != 1) get_key(c, gg);
+  const double scale = babies[0]->scale * pts[0]->scale;
+  const int sdeg = babies[0]->scale_degree + pts[0]->scale_degree;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  Batch bb{};
+  for (int b = 0; b < B; b++) bb.p[b] = babies[b]->d;
+  ckks_ct *acc = nullptr;
+  Scratch s(c);
+  u64 *inner = s.get(2 * P);
+  for (int g = giant_count - 1; g >= 0; g--) {
+    Batch bp{};
+    for (int b = 0; b < B; b++) bp.p[b] = pts[g * B + b]->d;
+    if (!acc) {
+      acc = new_ct(c, 2, limbs, 0, babies[0]->slots, scale, sdeg);
+      launch_mac(c, bb, bp, B, acc->d, limbs);
+      continue;
+    }
+    launch_mac(c, bb, bp, B, inner, limbs);
+    ckks_ct *rot = new_ct(c, 2, limbs, 0, acc->slots, scale, sdeg);
+    if (gg == 1)
+      HIPCHECK(hipMemcpyAsync(rot->d, acc->d, acc->bytes, hipMemcpyDeviceToDevice, c->stream));
+    else {
+      const ckks_ct *ac = acc;
+      rotate_batch(c, &ac, 1, gg, &rot);
+    }
+    launch_addsub(c, rot->d, inner, acc->d, 2, limbs, limbs, 0);
+    free_ct(rot);
+  }
+  *out = acc;
+  API_END
+}
+
+int ckks_poly_ntt(ckks_context *c, const uint64_t *in, uint64_t *out, int n_polys, int limbs,
+                  int q_limbs, int inverse) {
+  API_BEGIN
+  require(c && in && out, "null argument");
+  require(n_polys >= 1 && limbs >= 1 && limbs <= c->K, "bad shape");
+  require(q_limbs >= 0 && q_limbs <= c->L && limbs - q_limbs <= c->alpha, "bad q_limbs");
+  const size_t words = (size_t)n_polys * limbs * c->N;
+  Scratch s(c);
+  u64 *d = s.get(words);
+  HIPCHECK(hipMemcpyAsync(d, in, sizeof(u64) * words, hipMemcpyHostToDevice, c->stream));
+  launch_ntt(c, strided(d, (size_t)limbs * c->N), strided(d, (size_t)limbs * c->N), n_polys, 0,
+             limbs, q_limbs, inverse != 0);
+  HIPCHECK(hipMemcpyAsync(out, d, sizeof(u64) * words, hipMemcpyDeviceToHost, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_poly_modup(ckks_context *c, const uint64_t *dh, int limbs, uint64_t *ext_h) {
+  API_BEGIN
+  require(c && dh && ext_h, "null argument");
+  check_limbs(c, limbs);
+  const size_t N = c->N;
+  const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+  Scratch s(c);
+  u64 *d = s.get((size_t)limbs * N);
+  u64 *ext = s.get((size_t)digits * E * N);
+  HIPCHECK(hipMemcpyAsync(d, dh, sizeof(u64) * limbs * N, hipMemcpyHostToDevice, c->stream));
+  const u64 *dp = d;
+  ks_modup(c, limbs, 1, &dp, ext, s);
+  HIPCHECK(hipMemcpyAsync(ext_h, ext, sizeof(u64) * digits * E * N, hipMemcpyDeviceToHost,
+                          c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_poly_moddown(ckks_context *c, const uint64_t *acc_h, int limbs, uint64_t *out_h) {
+  API_BEGIN
+  require(c && acc_h && out_h, "null argument");
+  check_limbs(c, limbs);
+  const size_t N = c->N;
+  const int E = limbs + c->alpha;
+  Scratch s(c);
+  // run ModDown through the combine path with component 1 = component 0
+  u64 *acc = s.get(2 * (size_t)E * N);
+  u64 *ptmp = s.get(2 * (size_t)c->alpha * N);
+  u64 *conv = s.get(2 * (size_t)limbs * N);
+  u64 *o = s.get(2 * (size_t)limbs * N);
+  HIPCHECK(hipMemcpyAsync(acc, acc_h, sizeof(u64) * E * N, hipMemcpyHostToDevice, c->stream));
+  HIPCHECK(hipMemcpyAsync(acc + (size_t)E * N, acc_h, sizeof(u64) * E * N, hipMemcpyHostToDevice,
+                          c->stream));
+  launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N), 2,
+             limbs, c->alpha, limbs, true);
+  launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N), 2,
+                       bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+  launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2, 0, limbs,
+             limbs, false);
+  Batch a0{}, a1{}, o0{}, o1{};
+  o0.p[0] = o;
+  o1.p[0] = o + (size_t)limbs * N;
+  u64 g = 1;
+  launch_moddown_combine(c, Strided{acc, 2 * (u64)E * N}, Strided{conv, 2 * (u64)limbs * N}, a0,
+                         a1, &g, o0, o1, 1, limbs, E, pinv_table(c, limbs));
+  HIPCHECK(hipMemcpyAsync(out_h, o, sizeof(u64) * limbs * N, hipMemcpyDeviceToHost, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+int ckks_ntt_many(ckks_context *c, ckks_ct *const *cts, int n, int inverse) {
+  API_BEGIN
+  require(c && cts && n >= 1, "null argument");
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    const int limbs = cts[b0]->limbs, polys = cts[b0]->polys;
+    Batch b{};
+    for (int i = 0; i < nb; i++) {
+      check_ct(c, cts[b0 + i], "ntt_many");
+      require(cts[b0 + i]->limbs == limbs && cts[b0 + i]->polys == polys && !cts[b0 + i]->is_ext,
+              "ntt_many needs one shape");
+      b.p[i] = cts[b0 + i]->d;
+    }
+    // polys x limbs limb-polynomials per ciphertext: limb index runs over
+    // [0, polys * limbs) and maps to prime (index mod limbs).
+    for (int p = 0; p < polys; p++) {
+      Batch bp{};
+      for (int i = 0; i < nb; i++) bp.p[i] = b.p[i] + (size_t)p * limbs * c->N;
+      launch_ntt(c, bp, bp, nb, 0, limbs, limbs, inverse != 0);
+    }
+  }
+  API_END
+}
+
+int ckks_event_create(ckks_context *c, ckks_event **out) {
+  API_BEGIN
+  require(c && out, "null argument");
+  ckks_event *e = new ckks_event();
+  e->ctx = c;
+  HIPCHECK(hipEventCreate(&e->ev));
+  *out = e;
+  API_END
+}
+
+int ckks_event_record(ckks_event *e) {
+  API_BEGIN
+  require(e, "null argument");
+  HIPCHECK(hipEventRecord(e->ev, e->ctx->stream));
+  API_END
+}
+
+int ckks_event_elapsed_ms(ckks_event *a, ckks_event *b, float *ms) {
+  API_BEGIN
+  require(a && b && ms, "null argument");
+  HIPCHECK(hipEventSynchronize(b->ev));
+  HIPCHECK(hipEventElapsedTime(ms, a->ev, b->ev));
+  API_END
+}
+
+void ckks_event_destroy(ckks_event *e) {
+  if (!e) return;
+  (void)hipEventDestroy(e->ev);
+  delete e;
+}
+
+}  // extern "C"

@@ -1,0 +1,242 @@
+// ckks_internal.hpp -- shared definitions of the gfx950 RNS-CKKS backend.
+//
+// Word size: every residue is a uint64 in [0, q) with q < 2^60 (the prime
+// rule keeps all primes below 2^60 so that sixteen residues sum below 2^64,
+// which is the bound the lazy Montgomery accumulations below rely on).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ckks_mi355x.h"
+
+typedef uint64_t u64;
+typedef uint32_t u32;
+
+namespace ckks {
+
+constexpr int kMaxBatch = 64;    // explicit pointers per kernel argument block
+constexpr int kMaxDigitSize = 16;  // Montgomery fold bound: 16 * 2^60 <= 2^64
+constexpr int kMaxDigits = 8;
+
+// Per-prime constants, resident in device memory.
+struct ModQ {
+  u64 q;
+  u64 qinv;  // -q^-1 mod 2^64 (Montgomery)
+  u64 r2;    // 2^128 mod q
+  u64 mu;    // floor(2^(2k) / q) (Barrett)
+  u32 k;     // bit length of q
+  u32 pad;
+};
+
+// A set of polynomials addressed either by explicit pointers (p[i]) or by a
+// base and a stride (base + i * stride) when base != nullptr.
+struct Batch {
+  u64 *p[kMaxBatch];
+  u64 *base;
+  u64 stride;
+};
+
+// An internal buffer of equally spaced items.
+struct Strided {
+  u64 *base;
+  u64 stride;
+};
+
+__device__ __forceinline__ u64 *batch_ptr(const Batch &b, int i) {
+  return b.base ? b.base + (u64)i * b.stride : b.p[i];
+}
+
+// ---------------------------------------------------------------------------
+// modular arithmetic (device)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ u64 add_mod(u64 a, u64 b, u64 q) {
+  u64 s = a + b;
+  return s >= q ? s - q : s;
+}
+
+__device__ __forceinline__ u64 sub_mod(u64 a, u64 b, u64 q) {
+  return a >= b ? a - b : a + q - b;
+}
+
+// Shoup: a * w mod q with ws = floor(w 2^64 / q); a < 2^64, result in [0, q).
+__device__ __forceinline__ u64 shoup_mul(u64 a, u64 w, u64 ws, u64 q) {
+  u64 h = __umul64hi(a, ws);
+  u64 r = a * w - h * q;
+  return r >= q ? r - q : r;
+}
+
+// (hi, lo) += a * b
+__device__ __forceinline__ void mac_wide(u64 &hi, u64 &lo, u64 a, u64 b) {
+  u64 l = a * b;
+  u64 h = __umul64hi(a, b);
+  lo += l;
+  hi += h + (lo < l ? 1 : 0);
+}
+
+// Montgomery reduction of x = hi 2^64 + lo < q 2^64: x 2^-64 mod q in [0, q).
+__device__ __forceinline__ u64 redc(u64 hi, u64 lo, u64 q, u64 qinv) {
+  u64 m = lo * qinv;
+  u64 t = hi + __umul64hi(m, q) + (lo != 0 ? 1 : 0);
+  return t >= q ? t - q : t;
+}
+
+// Barrett reduction of x = hi 2^64 + lo < q^2 (HAC 14.42 with radix 2).
+__device__ __forceinline__ u64 barrett(u64 hi, u64 lo, const ModQ &M) {
+  const u32 k = M.k;
+  u64 xs = (hi << (65 - k)) | (lo >> (k - 1));
+  u64 ph = __umul64hi(xs, M.mu), pl = xs * M.mu;
+  u64 qh = (ph << (63 - k)) | (pl >> (k + 1));
+  u64 r = lo - qh * M.q;
+  if (r >= M.q) r -= M.q;
+  if (r >= M.q) r -= M.q;
+  return r;
+}
+
+__device__ __forceinline__ u64 mul_mod(u64 a, u64 b, const ModQ &M) {
+  return barrett(__umul64hi(a, b), a * b, M);
+}
+
+__device__ __forceinline__ u64 to_mont(u64 a, const ModQ &M) {
+  return redc(__umul64hi(a, M.r2), a * M.r2, M.q, M.qinv);
+}
+
+// Index map of the automorphism X -> X^g in the bit-reversed NTT domain:
+// out[i] = in[autom_index(i)].
+__device__ __forceinline__ u32 autom_index(u32 i, u64 g, int logN) {
+  u32 r = __brev(i) >> (32 - logN);
+  u64 e = ((2 * (u64)r + 1) * g) & ((2ull << logN) - 1);
+  return __brev((u32)((e - 1) >> 1)) >> (32 - logN);
+}
+
+__device__ __forceinline__ int prime_of(int limb, int q_limbs, int L) {
+  return limb < q_limbs ? limb : L + (limb - q_limbs);
+}
+
+// ---------------------------------------------------------------------------
+// host-side structures
+// ---------------------------------------------------------------------------
+
+// Device memory of one context: exact-size free lists plus the set of live
+// blocks, so that destroying the context returns everything it allocated.
+struct Pool {
+  std::unordered_map<size_t, std::vector<void *>> free_;
+  std::unordered_map<void *, size_t> live_;
+  size_t live = 0, cached = 0;
+  void *alloc(size_t bytes);
+  void release(void *p, size_t bytes);
+  void trim();
+  void release_all();
+};
+
+struct DeviceKey {
+  u64 galois;
+  int digits;
+  u64 *data;  // [digits][2][K][N], Montgomery form
+  size_t bytes;
+};
+
+struct BCTable {  // fast basis conversion constants, device resident
+  int ns, nd;
+  u64 *d;  // [ns] hinv, [ns] hinv_shoup, [ns*nd] hmod (Montgomery form), [nd] Q mod t
+  size_t bytes;
+};
+
+struct FFTTable {  // encoder tables for one slot count n
+  int n;
+  double *tw_fwd;  // [n/2][2] exp(+2 pi i j / n)
+  double *tw_inv;  // [n/2][2] exp(-2 pi i j / n)
+  double *twist;   // [n][2]   exp(-2 pi i k / 4n)
+  double *untwist; // [n][2]   exp(+2 pi i k / 4n)
+  u32 *perm;       // [n] r_j = (5^j mod 4n - 1) / 4
+};
+
+}  // namespace ckks
+
+struct ckks_context {
+  ckks_params params;
+  int N, logN, L, alpha, ds, K;
+  hipStream_t stream;
+  ckks::Pool pool;
+  std::vector<u64> primes;
+  std::vector<int8_t> secret;
+  ckks::ModQ *d_mods;  // [K]
+  std::vector<ckks::ModQ> h_mods;
+  u64 *d_psi, *d_psi_sh, *d_ipsi, *d_ipsi_sh;  // [K][N] each
+  u64 *d_ninv;                                 // [K][2] value, shoup
+  u64 *d_secret;                               // [K][N] NTT domain
+  std::map<u64, ckks::DeviceKey> keys;          // galois -> key (0 = relin)
+  std::map<std::pair<int, int>, ckks::BCTable> bc_up;  // (limbs, digit)
+  std::map<int, ckks::BCTable> bc_down;                // limbs
+  std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
+  std::map<int, u64 *> rescale_c;  // limbs -> [limbs-1][4] ql mod qi, ql^-1, shoup
+  std::map<int, ckks::FFTTable> fft;
+  std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
+};
+
+struct ckks_ct {
+  ckks_context *ctx;
+  u64 *d;
+  size_t bytes;
+  int polys, limbs, is_ext, slots, scale_degree;
+  double scale;
+};
+
+struct ckks_event {
+  ckks_context *ctx;
+  hipEvent_t ev;
+};
+
+// ---------------------------------------------------------------------------
+// kernel launchers (ckks_kernels.hip)
+// ---------------------------------------------------------------------------
+namespace ckks {
+
+void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                int l_begin, int l_count, int q_limbs, bool inverse);
+// out = a op b over `limbs` limbs of `polys` polynomials (op: 0 add, 1 sub)
+void launch_addsub(ckks_context *c, const u64 *a, const u64 *b, u64 *out, int polys,
+                   int limbs, int q_limbs, int op);
+void launch_mul_pt(ckks_context *c, const u64 *ct, const u64 *pt, u64 *out, int polys,
+                   int limbs, int q_limbs);
+void launch_mul_i(ckks_context *c, const u64 *ct, u64 *out, int polys, int limbs,
+                  int q_limbs, int negative);
+void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int polys,
+                   int limbs, int q_limbs, int op);  // op 0: add to poly 0, 1: mul all
+void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
+                   int n_items, int limbs);
+void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                          const BCTable &t, int src_prime0, int t_split, int t_skip,
+                          int q_limbs, bool centered);
+void launch_copy_limbs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                       int limb_count);
+void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
+                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois);
+void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
+                            const Batch &add0, const Batch &add1, const u64 *galois,
+                            const Batch &out0, const Batch &out1, int n_items, int limbs,
+                            int E, const u64 *pinv);
+void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, int n_items,
+                           int limbs);
+void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
+                            const Batch &out, int n_items, int limbs, const u64 *consts);
+void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
+                int limbs);
+void launch_keygen(ckks_context *c, DeviceKey &key, u64 id, int relin, u64 galois);
+// residues of a signed integer polynomial e[N] over `limbs` limbs, then NTT
+void launch_expand_ntt(ckks_context *c, const long long *e, u64 *out, int limbs, int q_limbs);
+void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int rows,
+                   int slots, double scale, int limbs, int is_ext, const Batch &out);
+void launch_encrypt_finish(ckks_context *c, u64 *ct, int limbs, u32 enc_id);
+void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, double *d_im);
+void launch_scalar_encode(ckks_context *c, double v, int limbs, u64 *out);
+
+}  // namespace ckks

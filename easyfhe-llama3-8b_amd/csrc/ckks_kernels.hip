@@ -1,0 +1,1052 @@
+// ckks_kernels.hip -- gfx950 kernels of the RNS-CKKS backend.
+//
+// All kernels use 256-thread workgroups (four wave64s).  Polynomials are
+// uint64 limb arrays of N residues; the NTT domain is the bit-reversed
+// evaluation order a_hat[i] = a(psi^(2 br(i) + 1)).
+#include <math.h>
+
+#include "ckks_internal.hpp"
+
+namespace ckks {
+
+#define HIP_OK(x)                                                          \
+  do {                                                                     \
+    hipError_t e_ = (x);                                                   \
+    if (e_ != hipSuccess)                                                  \
+      throw std::runtime_error(std::string(#x ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+#define LAUNCH_CHECK()                                                     \
+  do {                                                                     \
+    hipError_t e_ = hipGetLastError();                                     \
+    if (e_ != hipSuccess)                                                  \
+      throw std::runtime_error(std::string("kernel launch: ") +            \
+                               hipGetErrorString(e_));                     \
+  } while (0)
+
+constexpr int TPB = 256;
+
+// ===========================================================================
+// NTT: two passes of LDS-staged radix-2 stages.
+//   high pass: bit positions [logN - S1, logN), a tile is 2^S1 rows (stride
+//              N / 2^S1) by C adjacent columns, so global loads stay
+//              coalesced in C-element runs;
+//   low pass:  bit positions [0, S2), a tile is R contiguous rows of 2^S2.
+// Forward: high then low (Cooley-Tukey, twiddle psi_br[(N + j) >> (b + 1)]).
+// Inverse: low then high (Gentleman-Sande with psi_br^-1), then x N^-1.
+// ===========================================================================
+
+template <int S, int TILE>
+__global__ __launch_bounds__(TPB) void k_ntt_fwd_high(Batch src, Batch dst, int logN,
+                                                      int l_begin, int q_limbs, int L,
+                                                      const ModQ *__restrict__ mods,
+                                                      const u64 *__restrict__ psi,
+                                                      const u64 *__restrict__ psi_sh) {
+  constexpr int ROWS = 1 << S;
+  constexpr int C = TILE / ROWS;
+  constexpr int PER = TILE / TPB;
+  __shared__ u64 s[TILE];
+  const int N = 1 << logN;
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q;
+  const u64 *W = psi + (size_t)p * N;
+  const u64 *Ws = psi_sh + (size_t)p * N;
+  const u64 *in = batch_ptr(src, blockIdx.z) + (size_t)limb * N;
+  u64 *out = batch_ptr(dst, blockIdx.z) + (size_t)limb * N;
+  const int stride = N >> S;
+  const int col0 = blockIdx.x * C;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e = threadIdx.x + TPB * k;
+    s[e] = in[(size_t)(e / C) * stride + col0 + (e % C)];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const int h = ROWS >> (st + 1);
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      int u = threadIdx.x + TPB * k;
+      int cc = u % C, v = u / C;
+      int group = v / h, pos = v % h;
+      int ia = (group * 2 * h + pos) * C + cc, ib = ia + h * C;
+      int ti = (1 << st) + group;
+      u64 a = s[ia];
+      u64 t = shoup_mul(s[ib], W[ti], Ws[ti], q);
+      s[ia] = add_mod(a, t, q);
+      s[ib] = sub_mod(a, t, q);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e = threadIdx.x + TPB * k;
+    out[(size_t)(e / C) * stride + col0 + (e % C)] = s[e];
+  }
+}
+
+template <int S, int TILE>
+__global__ __launch_bounds__(TPB) void k_ntt_fwd_low(Batch dst, int logN, int l_begin,
+                                                     int q_limbs, int L,
+                                                     const ModQ *__restrict__ mods,
+                                                     const u64 *__restrict__ psi,
+                                                     const u64 *__restrict__ psi_sh) {
+  constexpr int COLS = 1 << S;
+  constexpr int PER = TILE / TPB;
+  __shared__ u64 s[TILE];
+  const int N = 1 << logN;
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q;
+  const u64 *W = psi + (size_t)p * N;
+  const u64 *Ws = psi_sh + (size_t)p * N;
+  u64 *base = batch_ptr(dst, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+#pragma unroll
+  for (int k = 0; k < PER; k++) s[threadIdx.x + TPB * k] = base[threadIdx.x + TPB * k];
+  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const int b = S - 1 - st, h = 1 << b;
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      int u = threadIdx.x + TPB * k;
+      int r = u / (COLS / 2), v = u % (COLS / 2);
+      int ca = r * COLS + ((v >> b) << (b + 1)) + (v & (h - 1));
+      int j = blockIdx.x * TILE + ca;
+      int ti = (N + j) >> (b + 1);
+      u64 a = s[ca];
+      u64 t = shoup_mul(s[ca + h], W[ti], Ws[ti], q);
+      s[ca] = add_mod(a, t, q);
+      s[ca + h] = sub_mod(a, t, q);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < PER; k++) base[threadIdx.x + TPB * k] = s[threadIdx.x + TPB * k];
+}
+
+template <int S, int TILE>
+__global__ __launch_bounds__(TPB) void k_ntt_inv_low(Batch src, Batch dst, int logN,
+                                                     int l_begin, int q_limbs, int L,
+                                                     const ModQ *__restrict__ mods,
+                                                     const u64 *__restrict__ ipsi,
+                                                     const u64 *__restrict__ ipsi_sh) {
+  constexpr int COLS = 1 << S;
+  constexpr int PER = TILE / TPB;
+  __shared__ u64 s[TILE];
+  const int N = 1 << logN;
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q;
+  const u64 *W = ipsi + (size_t)p * N;
+  const u64 *Ws = ipsi_sh + (size_t)p * N;
+  const u64 *in = batch_ptr(src, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+  u64 *out = batch_ptr(dst, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+#pragma unroll
+  for (int k = 0; k < PER; k++) s[threadIdx.x + TPB * k] = in[threadIdx.x + TPB * k];
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < S; b++) {
+    const int h = 1 << b;
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      int u = threadIdx.x + TPB * k;
+      int r = u / (COLS / 2), v = u % (COLS / 2);
+      int ca = r * COLS + ((v >> b) << (b + 1)) + (v & (h - 1));
+      int j = blockIdx.x * TILE + ca;
+      int ti = (N + j) >> (b + 1);
+      u64 x = s[ca], y = s[ca + h];
+      s[ca] = add_mod(x, y, q);
+      s[ca + h] = shoup_mul(sub_mod(x, y, q), W[ti], Ws[ti], q);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < PER; k++) out[threadIdx.x + TPB * k] = s[threadIdx.x + TPB * k];
+}
+
+template <int S, int TILE>
+__global__ __launch_bounds__(TPB) void k_ntt_inv_high(Batch dst, int logN, int l_begin,
+                                                      int q_limbs, int L,
+                                                      const ModQ *__restrict__ mods,
+                                                      const u64 *__restrict__ ipsi,
+                                                      const u64 *__restrict__ ipsi_sh,
+                                                      const u64 *__restrict__ ninv) {
+  constexpr int ROWS = 1 << S;
+  constexpr int C = TILE / ROWS;
+  constexpr int PER = TILE / TPB;
+  __shared__ u64 s[TILE];
+  const int N = 1 << logN;
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q;
+  const u64 *W = ipsi + (size_t)p * N;
+  const u64 *Ws = ipsi_sh + (size_t)p * N;
+  u64 *io = batch_ptr(dst, blockIdx.z) + (size_t)limb * N;
+  const int stride = N >> S;
+  const int col0 = blockIdx.x * C;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e = threadIdx.x + TPB * k;
+    s[e] = io[(size_t)(e / C) * stride + col0 + (e % C)];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int st = S - 1; st >= 0; st--) {
+    const int h = ROWS >> (st + 1);
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      int u = threadIdx.x + TPB * k;
+      int cc = u % C, v = u / C;
+      int group = v / h, pos = v % h;
+      int ia = (group * 2 * h + pos) * C + cc, ib = ia + h * C;
+      int ti = (1 << st) + group;
+      u64 x = s[ia], y = s[ib];
+      s[ia] = add_mod(x, y, q);
+      s[ib] = shoup_mul(sub_mod(x, y, q), W[ti], Ws[ti], q);
+    }
+    __syncthreads();
+  }
+  const u64 ni = ninv[2 * p], nis = ninv[2 * p + 1];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    int e = threadIdx.x + TPB * k;
+    io[(size_t)(e / C) * stride + col0 + (e % C)] = shoup_mul(s[e], ni, nis, q);
+  }
+}
+
+template <int S1, int S2, int TILE>
+static void ntt_dispatch(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                         int l_begin, int l_count, int q_limbs, bool inverse) {
+  const int N = c->N;
+  dim3 block(TPB);
+  dim3 g_high((N >> S1) / (TILE >> S1), l_count, n_items);
+  dim3 g_low(N / TILE, l_count, n_items);
+  if (!inverse) {
+    hipLaunchKernelGGL((k_ntt_fwd_high<S1, TILE>), g_high, block, 0, c->stream, src, dst,
+                       c->logN, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL((k_ntt_fwd_low<S2, TILE>), g_low, block, 0, c->stream, dst, c->logN,
+                       l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh);
+    LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL((k_ntt_inv_low<S2, TILE>), g_low, block, 0, c->stream, src, dst,
+                       c->logN, l_begin, q_limbs, c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL((k_ntt_inv_high<S1, TILE>), g_high, block, 0, c->stream, dst,
+                       c->logN, l_begin, q_limbs, c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh,
+                       c->d_ninv);
+    LAUNCH_CHECK();
+  }
+}
+
+void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                int l_begin, int l_count, int q_limbs, bool inverse) {
+  if (n_items <= 0 || l_count <= 0) return;
+  switch (c->logN) {
+    case 10: ntt_dispatch<5, 5, 1024>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 11: ntt_dispatch<5, 6, 2048>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 12: ntt_dispatch<6, 6, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 13: ntt_dispatch<6, 7, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 14: ntt_dispatch<7, 7, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 15: ntt_dispatch<7, 8, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 16: ntt_dispatch<8, 8, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 17: ntt_dispatch<8, 9, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    default: throw std::invalid_argument("log_n must be in [10, 17]");
+  }
+}
+
+// ===========================================================================
+// limb-wise arithmetic; grid (N / 256, limbs, polys)
+// ===========================================================================
+
+__global__ void k_addsub(const u64 *__restrict__ a, const u64 *__restrict__ b,
+                         u64 *__restrict__ out, int logN, int limbs, int q_limbs, int L,
+                         const ModQ *__restrict__ mods, int op) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t off = (((size_t)blockIdx.z * limbs + l) << logN) + k;
+  const u64 q = mods[prime_of(l, q_limbs, L)].q;
+  out[off] = op == 0 ? add_mod(a[off], b[off], q) : sub_mod(a[off], b[off], q);
+}
+
+void launch_addsub(ckks_context *c, const u64 *a, const u64 *b, u64 *out, int polys,
+                   int limbs, int q_limbs, int op) {
+  dim3 grid(c->N / TPB, limbs, polys);
+  hipLaunchKernelGGL(k_addsub, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
+                     q_limbs, c->L, c->d_mods, op);
+  LAUNCH_CHECK();
+}
+
+__global__ void k_mul_pt(const u64 *__restrict__ ct, const u64 *__restrict__ pt,
+                         u64 *__restrict__ out, int logN, int limbs, int q_limbs, int L,
+                         const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t off = (((size_t)blockIdx.z * limbs + l) << logN) + k;
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
+  out[off] = mul_mod(ct[off], pt[((size_t)l << logN) + k], M);
+}
+
+void launch_mul_pt(ckks_context *c, const u64 *ct, const u64 *pt, u64 *out, int polys,
+                   int limbs, int q_limbs) {
+  dim3 grid(c->N / TPB, limbs, polys);
+  hipLaunchKernelGGL(k_mul_pt, grid, dim3(TPB), 0, c->stream, ct, pt, out, c->logN, limbs,
+                     q_limbs, c->L, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// x X^(N/2): evaluation point i gives +I for i < N/2 and -I otherwise, with
+// I = psi^(N/2) = psi_br[1]; negative swaps the signs.
+__global__ void k_mul_i(const u64 *__restrict__ ct, u64 *__restrict__ out, int logN,
+                        int limbs, int q_limbs, int L, const ModQ *__restrict__ mods,
+                        const u64 *__restrict__ psi, int negative) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t off = (((size_t)blockIdx.z * limbs + l) << logN) + k;
+  const int p = prime_of(l, q_limbs, L);
+  const ModQ M = mods[p];
+  const u64 I = psi[((size_t)p << logN) + 1];
+  const bool upper = k >= (1 << (logN - 1));
+  const u64 f = (upper != (negative != 0)) ? M.q - I : I;
+  out[off] = mul_mod(ct[off], f, M);
+}
+
+void launch_mul_i(ckks_context *c, const u64 *ct, u64 *out, int polys, int limbs,
+                  int q_limbs, int negative) {
+  dim3 grid(c->N / TPB, limbs, polys);
+  hipLaunchKernelGGL(k_mul_i, grid, dim3(TPB), 0, c->stream, ct, out, c->logN, limbs,
+                     q_limbs, c->L, c->d_mods, c->d_psi, negative);
+  LAUNCH_CHECK();
+}
+
+// op 0: add the per-limb constant s[l] to polynomial 0; op 1: multiply every
+// polynomial by s[l].  (A constant polynomial is the same value at every NTT
+// evaluation point.)
+__global__ void k_scalar(const u64 *__restrict__ ct, const u64 *__restrict__ sc,
+                         u64 *__restrict__ out, int logN, int limbs, int q_limbs, int L,
+                         const ModQ *__restrict__ mods, int op) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t off = (((size_t)blockIdx.z * limbs + l) << logN) + k;
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
+  u64 v = ct[off];
+  if (op == 0)
+    out[off] = blockIdx.z == 0 ? add_mod(v, sc[l], M.q) : v;
+  else
+    out[off] = mul_mod(v, sc[l], M);
+}
+
+void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int polys,
+                   int limbs, int q_limbs, int op) {
+  dim3 grid(c->N / TPB, limbs, polys);
+  hipLaunchKernelGGL(k_scalar, grid, dim3(TPB), 0, c->stream, ct, s, out, c->logN, limbs,
+                     q_limbs, c->L, c->d_mods, op);
+  LAUNCH_CHECK();
+}
+
+// Tensor product of degree-1 ciphertexts: (a0 b0, a0 b1 + a1 b0, a1 b1).
+// grid (N / 256, limbs, items)
+__global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs,
+                         const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const ModQ M = mods[l];
+  const size_t P = (size_t)limbs << logN;
+  const size_t off = ((size_t)l << logN) + k;
+  const u64 *pa = batch_ptr(a, blockIdx.z), *pb = batch_ptr(b, blockIdx.z);
+  u64 *po = batch_ptr(out, blockIdx.z);
+  const u64 a0 = pa[off], a1 = pa[P + off], b0 = pb[off], b1 = pb[P + off];
+  po[off] = mul_mod(a0, b0, M);
+  // a0 b1 + a1 b0 < 2 q^2 < q 2^64: one Montgomery fold, then x R
+  u64 hi = 0, lo = 0;
+  mac_wide(hi, lo, a0, b1);
+  mac_wide(hi, lo, a1, b0);
+  po[P + off] = to_mont(redc(hi, lo, M.q, M.qinv), M);
+  po[2 * P + off] = mul_mod(a1, b1, M);
+}
+
+void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
+                   int n_items, int limbs) {
+  dim3 grid(c->N / TPB, limbs, n_items);
+  hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
+                     c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// fast basis conversion (ModUp / ModDown); grid (N / 256, items)
+//   v_i = [x_i (Q/q_i)^-1]_{q_i};  y_t = REDC(sum_i v_i [(Q/q_i) R]_t)
+// centered: v_i is taken in (-q_i/2, q_i/2], i.e. y_t -= cnt Q mod t with
+// cnt = #{i : v_i > (q_i - 1)/2}; the conversion error u Q then has zero
+// mean (ModDown uses this; a biased u is amplified at the slot whose
+// evaluation point is nearest 1).
+// Source limbs are contiguous from src; target t is written at limb
+// tl = t < t_split ? t : t + t_skip of dst, in prime prime_of(tl).
+// Table: [ns] hinv, [ns] hinv shoup, [ns][nd] hmod (Montgomery), [nd] Q mod t.
+// ===========================================================================
+
+__global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int logN, int ns,
+                                                       int nd, const u64 *__restrict__ tab,
+                                                       int src_prime0, int t_split, int t_skip,
+                                                       int q_limbs, int L, int centered,
+                                                       const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const u64 *in = batch_ptr(src, blockIdx.y);
+  u64 *out = batch_ptr(dst, blockIdx.y);
+  u64 v[kMaxDigitSize];
+  u64 cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxDigitSize; i++) {
+    if (i < ns) {
+      const u64 qi = mods[src_prime0 + i].q;
+      v[i] = shoup_mul(in[((size_t)i << logN) + k], tab[i], tab[ns + i], qi);
+      cnt += (centered && v[i] > (qi - 1) / 2) ? 1 : 0;
+    }
+  }
+  const u64 *hm = tab + 2 * ns;
+  const u64 *qm = hm + (size_t)ns * nd;
+  for (int t = 0; t < nd; t++) {
+    const int tl = t < t_split ? t : t + t_skip;
+    const ModQ M = mods[prime_of(tl, q_limbs, L)];
+    u64 hi = 0, lo = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i++)
+      if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + t]);
+    u64 y = redc(hi, lo, M.q, M.qinv);
+    if (cnt) y = sub_mod(y, mul_mod(cnt, qm[t], M), M.q);
+    out[((size_t)tl << logN) + k] = y;
+  }
+}
+
+void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                          const BCTable &t, int src_prime0, int t_split, int t_skip,
+                          int q_limbs, bool centered) {
+  dim3 grid(c->N / TPB, n_items);
+  hipLaunchKernelGGL(k_basis_convert, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
+                     t.nd, t.d, src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0,
+                     c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// dst[item][l] = src[item][l] for l < limb_count; grid (N / 256, limbs, items)
+__global__ void k_copy_limbs(Batch src, Batch dst, int logN) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const size_t off = ((size_t)blockIdx.y << logN) + k;
+  batch_ptr(dst, blockIdx.z)[off] = batch_ptr(src, blockIdx.z)[off];
+}
+
+void launch_copy_limbs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                       int limb_count) {
+  if (limb_count <= 0 || n_items <= 0) return;
+  dim3 grid(c->N / TPB, limb_count, n_items);
+  hipLaunchKernelGGL(k_copy_limbs, grid, dim3(TPB), 0, c->stream, src, dst, c->logN);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// key inner product: acc_c[l] = sum_j ext_j[l][sigma(k)] key_j[c][l][k].
+// One thread owns one (limb, coefficient) and keeps the key words in
+// registers while it walks every item, so each key word is read from HBM
+// once per call.  grid (N / 256, E)
+// ===========================================================================
+
+__global__ __launch_bounds__(TPB) void k_key_inner(Batch ext, Batch acc, int n_items,
+                                                   const u64 *__restrict__ key, int digits,
+                                                   int E, int q_limbs, int L, int K, u64 galois,
+                                                   int logN, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const int p = prime_of(l, q_limbs, L);
+  const ModQ M = mods[p];
+  const size_t N = (size_t)1 << logN;
+  u64 kb[kMaxDigits], ka[kMaxDigits];
+#pragma unroll
+  for (int j = 0; j < kMaxDigits; j++) {
+    if (j < digits) {
+      kb[j] = key[((size_t)(2 * j) * K + p) * N + k];
+      ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + k];
+    }
+  }
+  const u32 kk = galois == 1 ? (u32)k : autom_index((u32)k, galois, logN);
+  for (int it = 0; it < n_items; it++) {
+    const u64 *e = batch_ptr(ext, it);
+    u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxDigits; j++) {
+      if (j < digits) {
+        const u64 x = e[((size_t)j * E + l) * N + kk];
+        mac_wide(h0, l0, x, kb[j]);
+        mac_wide(h1, l1, x, ka[j]);
+      }
+    }
+    u64 *o = batch_ptr(acc, it);
+    o[(size_t)l * N + k] = redc(h0, l0, M.q, M.qinv);
+    o[((size_t)E + l) * N + k] = redc(h1, l1, M.q, M.qinv);
+  }
+}
+
+void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
+                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois) {
+  dim3 grid(c->N / TPB, E);
+  hipLaunchKernelGGL(k_key_inner, grid, dim3(TPB), 0, c->stream, ext, acc, n_items, key.data,
+                     digits, E, q_limbs, c->L, c->K, galois, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// ModDown combine: out_c[l] = (acc_c[l] - conv_c[l]) P^-1 + add_c[l][sigma(k)]
+// acc item layout [2][E][N], conv [2][limbs][N] (internal, strided); add_c and
+// out_c are [limbs][N] polynomials per item (a null add pointer adds
+// nothing).  grid (N / 256, limbs, 2 * items)
+// ===========================================================================
+
+struct Galois64 {
+  u64 g[kMaxBatch];
+};
+
+__global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch add1,
+                                  Galois64 gal, Batch out0, Batch out1, int logN, int limbs,
+                                  int E, const u64 *__restrict__ pinv,
+                                  const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const int item = blockIdx.z >> 1, comp = blockIdx.z & 1;
+  const size_t N = (size_t)1 << logN;
+  const u64 q = mods[l].q;
+  const u64 a = acc.base[item * acc.stride + ((size_t)comp * E + l) * N + k];
+  const u64 v = conv.base[item * conv.stride + ((size_t)comp * limbs + l) * N + k];
+  u64 r = shoup_mul(sub_mod(a, v, q), pinv[2 * l], pinv[2 * l + 1], q);
+  const u64 *ad = batch_ptr(comp ? add1 : add0, item);
+  if (ad) {
+    const u64 g = gal.g[item];
+    const u32 kk = g == 1 ? (u32)k : autom_index((u32)k, g, logN);
+    r = add_mod(r, ad[(size_t)l * N + kk], q);
+  }
+  batch_ptr(comp ? out1 : out0, item)[(size_t)l * N + k] = r;
+}
+
+void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
+                            const Batch &add0, const Batch &add1, const u64 *galois,
+                            const Batch &out0, const Batch &out1, int n_items, int limbs,
+                            int E, const u64 *pinv) {
+  if (n_items > kMaxBatch) throw std::invalid_argument("moddown combine: too many items");
+  Galois64 g{};
+  for (int i = 0; i < n_items; i++) g.g[i] = galois[i];
+  dim3 grid(c->N / TPB, limbs, 2 * n_items);
+  hipLaunchKernelGGL(k_moddown_combine, grid, dim3(TPB), 0, c->stream, acc, conv, add0, add1,
+                     g, out0, out1, c->logN, limbs, E, pinv, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// rescale by the last prime q_l (rounded): r = centered(c_last) mod q_i,
+// out_i = (c_i - NTT(r)) q_l^-1.  consts per i: [ql mod qi, ql^-1, shoup, -].
+// ===========================================================================
+
+__global__ void k_rescale_expand(Batch last, Batch r, int logN, int limbs,
+                                 const u64 *__restrict__ consts,
+                                 const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int i = blockIdx.y;  // target limb < limbs - 1
+  const size_t N = (size_t)1 << logN;
+  const ModQ M = mods[i];
+  const u64 ql = mods[limbs - 1].q;
+  const u64 v = batch_ptr(last, blockIdx.z)[k];
+  u64 red = barrett(0, v, M);
+  if (v > (ql - 1) / 2) red = sub_mod(red, consts[4 * i], M.q);
+  batch_ptr(r, blockIdx.z)[(size_t)i * N + k] = red;
+}
+
+void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, int n_items,
+                           int limbs) {
+  dim3 grid(c->N / TPB, limbs - 1, n_items);
+  hipLaunchKernelGGL(k_rescale_expand, grid, dim3(TPB), 0, c->stream, last, r, c->logN, limbs,
+                     c->rescale_c.at(limbs), c->d_mods);
+  LAUNCH_CHECK();
+}
+
+__global__ void k_rescale_combine(Batch src, Batch r, Batch out, int logN, int limbs,
+                                  const u64 *__restrict__ consts,
+                                  const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int i = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  const u64 q = mods[i].q;
+  const u64 a = batch_ptr(src, blockIdx.z)[(size_t)i * N + k];
+  const u64 b = batch_ptr(r, blockIdx.z)[(size_t)i * N + k];
+  batch_ptr(out, blockIdx.z)[(size_t)i * N + k] =
+      shoup_mul(sub_mod(a, b, q), consts[4 * i + 1], consts[4 * i + 2], q);
+}
+
+void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
+                            const Batch &out, int n_items, int limbs, const u64 *consts) {
+  dim3 grid(c->N / TPB, limbs - 1, n_items);
+  hipLaunchKernelGGL(k_rescale_combine, grid, dim3(TPB), 0, c->stream, src, r, out, c->logN,
+                     limbs, consts, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// BSGS inner sum: out[c][l] = sum_b baby_b[c][l] * pt_b[l]
+// Products are folded 16 at a time with REDC (16 q^2 < q 2^64) and the
+// folded sum is multiplied back by R.  grid (N / 256, limbs, 2)
+// ===========================================================================
+
+__global__ void k_mac(Batch babies, Batch pts, int B, u64 *__restrict__ out, int logN,
+                      int limbs, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, comp = blockIdx.z;
+  const size_t N = (size_t)1 << logN;
+  const ModQ M = mods[l];
+  const size_t off = ((size_t)comp * limbs + l) * N + k;
+  u64 acc = 0, hi = 0, lo = 0;
+  for (int b = 0; b < B; b++) {
+    mac_wide(hi, lo, batch_ptr(babies, b)[off], batch_ptr(pts, b)[(size_t)l * N + k]);
+    if ((b & 15) == 15 || b == B - 1) {
+      acc = add_mod(acc, redc(hi, lo, M.q, M.qinv), M.q);
+      hi = lo = 0;
+    }
+  }
+  out[off] = to_mont(acc, M);
+}
+
+void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
+                int limbs) {
+  dim3 grid(c->N / TPB, limbs, 2);
+  hipLaunchKernelGGL(k_mac, grid, dim3(TPB), 0, c->stream, babies, pts, B, out, c->logN,
+                     limbs, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// ChaCha20 (RFC 8439) counter-mode PRNG: key = (seed lo, seed hi, 0, ...),
+// nonce = (domain, id, sub), counter = block index.
+// ===========================================================================
+
+enum { DOM_SECRET = 1, DOM_KEY_A = 2, DOM_KEY_E = 3, DOM_ENC_A = 4, DOM_ENC_E = 5 };
+
+__device__ __forceinline__ u32 rotl32(u32 v, int c) { return (v << c) | (v >> (32 - c)); }
+
+#define DQR(a, b, c, d)                  \
+  a += b; d ^= a; d = rotl32(d, 16);     \
+  c += d; b ^= c; b = rotl32(b, 12);     \
+  a += b; d ^= a; d = rotl32(d, 8);      \
+  c += d; b ^= c; b = rotl32(b, 7);
+
+__device__ void chacha_block(u64 seed, u32 dom, u32 id, u32 sub, u32 counter, u32 out[16]) {
+  u32 s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
+               (u32)seed,   (u32)(seed >> 32), 0u, 0u,
+               0u,          0u,          0u,          0u,
+               counter,     dom,         id,          sub};
+  u32 x[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) x[i] = s[i];
+#pragma unroll 1
+  for (int i = 0; i < 10; i++) {
+    DQR(x[0], x[4], x[8], x[12]);
+    DQR(x[1], x[5], x[9], x[13]);
+    DQR(x[2], x[6], x[10], x[14]);
+    DQR(x[3], x[7], x[11], x[15]);
+    DQR(x[0], x[5], x[10], x[15]);
+    DQR(x[1], x[6], x[11], x[12]);
+    DQR(x[2], x[7], x[8], x[13]);
+    DQR(x[3], x[4], x[9], x[14]);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
+}
+
+// (hi 2^64 + lo) mod q for q >= 2^33: hi is reduced by Barrett (hi < q^2),
+// then REDC(hi' 2^64 + lo) = x 2^-64 and x R restores the factor.
+__device__ __forceinline__ u64 wide_mod(u64 hi, u64 lo, const ModQ &M) {
+  const u64 h = barrett(0, hi, M);
+  return to_mont(redc(h, lo, M.q, M.qinv), M);
+}
+
+// Centered binomial (eta = 21) errors, coefficient k from 64-bit word k of the
+// stream.  grid (N / 8 / 256 rounded up)
+__global__ void k_sample_cbd(u64 seed, u32 dom, u32 id, u32 sub, long long *e, int N) {
+  const int t = blockIdx.x * TPB + threadIdx.x;
+  if (8 * t >= N) return;
+  u32 blk[16];
+  chacha_block(seed, dom, id, sub, (u32)t, blk);
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const u64 w = (u64)blk[2 * r] | ((u64)blk[2 * r + 1] << 32);
+    e[8 * t + r] = (long long)__popcll(w & 0x1FFFFFull) -
+                   (long long)__popcll((w >> 21) & 0x1FFFFFull);
+  }
+}
+
+__device__ __forceinline__ u64 signed_residue(long long x, const ModQ &M) {
+  const u64 a = x < 0 ? (u64)(-x) : (u64)x;
+  const u64 r = barrett(0, a, M);
+  return (x < 0 && r) ? M.q - r : r;
+}
+
+// out[l][k] = e[k] mod q_{prime_of(l)}; grid (N / 256, limbs)
+__global__ void k_expand_int(const long long *__restrict__ e, u64 *__restrict__ out, int logN,
+                             int q_limbs, int L, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
+  out[((size_t)l << logN) + k] = signed_residue(e[k], M);
+}
+
+void launch_expand_ntt(ckks_context *c, const long long *e, u64 *out, int limbs, int q_limbs) {
+  hipLaunchKernelGGL(k_expand_int, dim3(c->N / TPB, limbs), dim3(TPB), 0, c->stream, e, out,
+                     c->logN, q_limbs, c->L, c->d_mods);
+  LAUNCH_CHECK();
+  Batch b{};
+  b.p[0] = out;
+  launch_ntt(c, b, b, 1, 0, limbs, q_limbs, false);
+}
+
+// Switching-key digit j over all K primes (p = blockIdx.y):
+//   a = uniform (KEY_A, id, j << 16 | p), b = e - a s + [p in digit j] [P]_q s'
+// with s' = sigma_g(s) (rotation) or s^2 (relinearisation); both stored in
+// Montgomery form.  Each thread produces 4 coefficients from one block.
+__global__ void k_keygen_digit(u64 seed, u32 id, int j, const u64 *__restrict__ e_ntt,
+                               const u64 *__restrict__ s_ntt, const u64 *__restrict__ pmod,
+                               int relin, u64 galois, int ds, u64 *__restrict__ out_b,
+                               u64 *__restrict__ out_a, int logN, int L,
+                               const ModQ *__restrict__ mods) {
+  const int t = blockIdx.x * TPB + threadIdx.x;
+  const int p = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  if ((size_t)4 * t >= N) return;
+  const ModQ M = mods[p];
+  const bool in_digit = p < L && p / ds == j;
+  u32 blk[16];
+  chacha_block(seed, DOM_KEY_A, id, ((u32)j << 16) | (u32)p, (u32)t, blk);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const u32 k = 4 * t + r;
+    const u64 lo = (u64)blk[4 * r] | ((u64)blk[4 * r + 1] << 32);
+    const u64 hi = (u64)blk[4 * r + 2] | ((u64)blk[4 * r + 3] << 32);
+    const u64 a = wide_mod(hi, lo, M);
+    const u64 s = s_ntt[p * N + k];
+    u64 b = sub_mod(e_ntt[p * N + k], mul_mod(a, s, M), M.q);
+    if (in_digit) {
+      u64 sp;
+      if (relin)
+        sp = mul_mod(s, s, M);
+      else
+        sp = s_ntt[p * N + autom_index(k, galois, logN)];
+      b = add_mod(b, mul_mod(pmod[p], sp, M), M.q);
+    }
+    out_b[p * N + k] = to_mont(b, M);
+    out_a[p * N + k] = to_mont(a, M);
+  }
+}
+
+void launch_keygen(ckks_context *c, DeviceKey &key, u64 id, int relin, u64 galois) {
+  const int N = c->N, K = c->K;
+  long long *e = (long long *)c->pool.alloc(sizeof(long long) * N);
+  u64 *en = (u64 *)c->pool.alloc(sizeof(u64) * (size_t)K * N);
+  u64 *pmod = (u64 *)c->pool.alloc(sizeof(u64) * K);
+  std::vector<u64> hp(K, 0);
+  for (int p = 0; p < c->L; p++) {
+    unsigned __int128 acc = 1;
+    for (int t = 0; t < c->alpha; t++)
+      acc = (acc * (c->primes[c->L + t] % c->primes[p])) % c->primes[p];
+    hp[p] = (u64)acc;
+  }
+  HIP_OK(hipMemcpyAsync(pmod, hp.data(), sizeof(u64) * K, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(hipStreamSynchronize(c->stream));  // hp is a host temporary
+  for (int j = 0; j < key.digits; j++) {
+    hipLaunchKernelGGL(k_sample_cbd, dim3((N / 8 + TPB - 1) / TPB), dim3(TPB), 0, c->stream,
+                       c->params.seed, (u32)DOM_KEY_E, (u32)id, (u32)j, e, N);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_expand_int, dim3(N / TPB, K), dim3(TPB), 0, c->stream, e, en, c->logN,
+                       c->L, c->L, c->d_mods);
+    LAUNCH_CHECK();
+    Batch b{};
+    b.p[0] = en;
+    launch_ntt(c, b, b, 1, 0, K, c->L, false);
+    u64 *ob = key.data + (size_t)(2 * j) * K * N;
+    u64 *oa = key.data + (size_t)(2 * j + 1) * K * N;
+    hipLaunchKernelGGL(k_keygen_digit, dim3((N / 4 + TPB - 1) / TPB, K), dim3(TPB), 0,
+                       c->stream, c->params.seed, (u32)id, j, en, c->d_secret, pmod, relin,
+                       galois, c->ds, ob, oa, c->logN, c->L, c->d_mods);
+    LAUNCH_CHECK();
+  }
+  c->pool.release(e, sizeof(long long) * N);
+  c->pool.release(en, sizeof(u64) * (size_t)K * N);
+  c->pool.release(pmod, sizeof(u64) * K);
+}
+
+// Encryption: c1 = uniform (ENC_A, id, l) in the NTT domain,
+// c0 = e - c1 s + m, with m already encoded in c0.  grid (N / 4 / 256, limbs)
+__global__ void k_encrypt(u64 seed, u32 id, const u64 *__restrict__ e_ntt,
+                          const u64 *__restrict__ s_ntt, u64 *__restrict__ ct, int limbs,
+                          int logN, const ModQ *__restrict__ mods) {
+  const int t = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  if ((size_t)4 * t >= N) return;
+  const ModQ M = mods[l];
+  u32 blk[16];
+  chacha_block(seed, DOM_ENC_A, id, (u32)l, (u32)t, blk);
+  u64 *c0 = ct + (size_t)l * N;
+  u64 *c1 = ct + ((size_t)limbs + l) * N;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const size_t k = 4 * (size_t)t + r;
+    const u64 lo = (u64)blk[4 * r] | ((u64)blk[4 * r + 1] << 32);
+    const u64 hi = (u64)blk[4 * r + 2] | ((u64)blk[4 * r + 3] << 32);
+    const u64 a = wide_mod(hi, lo, M);
+    c1[k] = a;
+    c0[k] = add_mod(sub_mod(e_ntt[l * N + k], mul_mod(a, s_ntt[l * N + k], M), M.q), c0[k], M.q);
+  }
+}
+
+void launch_encrypt_finish(ckks_context *c, u64 *ct, int limbs, u32 enc_id) {
+  const int N = c->N;
+  long long *e = (long long *)c->pool.alloc(sizeof(long long) * N);
+  u64 *en = (u64 *)c->pool.alloc(sizeof(u64) * (size_t)limbs * N);
+  hipLaunchKernelGGL(k_sample_cbd, dim3((N / 8 + TPB - 1) / TPB), dim3(TPB), 0, c->stream,
+                     c->params.seed, (u32)DOM_ENC_E, enc_id, 0u, e, N);
+  LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_expand_int, dim3(N / TPB, limbs), dim3(TPB), 0, c->stream, e, en,
+                     c->logN, limbs, c->L, c->d_mods);
+  LAUNCH_CHECK();
+  Batch b{};
+  b.p[0] = en;
+  launch_ntt(c, b, b, 1, 0, limbs, limbs, false);
+  hipLaunchKernelGGL(k_encrypt, dim3((N / 4 + TPB - 1) / TPB, limbs), dim3(TPB), 0, c->stream,
+                     c->params.seed, enc_id, en, c->d_secret, ct, limbs, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+  c->pool.release(e, sizeof(long long) * N);
+  c->pool.release(en, sizeof(u64) * (size_t)limbs * N);
+}
+
+// ===========================================================================
+// canonical-embedding encoder / decoder (fp64, no contraction: the same
+// operations in the same order as the CPU statement of the algorithm)
+// ===========================================================================
+
+struct cplx {
+  double re, im;
+};
+
+__device__ __forceinline__ cplx cmul(cplx a, cplx b) {
+  const double t1 = __dmul_rn(a.re, b.re);
+  const double t2 = __dmul_rn(a.im, b.im);
+  const double t3 = __dmul_rn(a.re, b.im);
+  const double t4 = __dmul_rn(a.im, b.re);
+  return cplx{__dsub_rn(t1, t2), __dadd_rn(t3, t4)};
+}
+
+// x[row][br(perm[j])] = z[row][j]  (perm, then the FFT's bit-reversal)
+__global__ void k_fft_place(const double *__restrict__ re, const double *__restrict__ im,
+                            cplx *__restrict__ x, const u32 *__restrict__ perm, int n, int logn) {
+  const int j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  const size_t row = blockIdx.y;
+  const u32 r = __brev(perm[j]) >> (32 - logn);
+  x[row * n + r] = cplx{re[row * n + j], im ? im[row * n + j] : 0.0};
+}
+
+// One radix-2 DIT stage of length `len`; grid (n / 2 / 256, rows)
+__global__ void k_fft_stage(cplx *__restrict__ x, int n, int len, const cplx *__restrict__ tw) {
+  const int bidx = blockIdx.x * TPB + threadIdx.x;
+  if (bidx >= n / 2) return;
+  const int half = len >> 1, step = n / len;
+  const int st = (bidx / half) * len, k = bidx % half;
+  cplx *row = x + (size_t)blockIdx.y * n;
+  const cplx u = row[st + k];
+  const cplx v = cmul(row[st + k + half], tw[k * step]);
+  row[st + k] = cplx{__dadd_rn(u.re, v.re), __dadd_rn(u.im, v.im)};
+  row[st + k + half] = cplx{__dsub_rn(u.re, v.re), __dsub_rn(u.im, v.im)};
+}
+
+// Residue of an integer-valued double of any magnitude (exact).
+__device__ u64 dbl_residue(double v, const ModQ &M) {
+  if (fabs(v) < 9.2e18) return signed_residue((long long)v, M);
+  const u64 bits = (u64)__double_as_longlong(v);
+  const int e = (int)((bits >> 52) & 0x7ff) - 1075;
+  const u64 mant = (bits & 0xFFFFFFFFFFFFFull) | (1ull << 52);
+  u64 r = barrett(0, mant, M);
+  for (int i = 0; i < e; i++) r = add_mod(r, r, M.q);
+  return ((long long)bits < 0 && r) ? M.q - r : r;
+}
+
+// Encoder tail: u = (x_k / n) * twist_k, coefficient k gap and (k + n) gap
+// get rint(scale u.re), rint(scale u.im); then residues for every limb.
+// grid (N / 256, total_limbs, rows)
+__global__ void k_encode_finish(const cplx *__restrict__ x, const cplx *__restrict__ twist,
+                                Batch out, int n, int logN, double scale, int q_limbs, int L,
+                                const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;  // coefficient index
+  const int l = blockIdx.y;
+  const int N = 1 << logN, gap = N / (2 * n);
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
+  double v = 0.0;
+  if (k % gap == 0) {
+    const int idx = k / gap;
+    const int kk = idx < n ? idx : idx - n;
+    const cplx w = x[(size_t)blockIdx.z * n + kk];
+    const double inv_n = 1.0 / (double)n;
+    cplx u = cplx{__dmul_rn(w.re, inv_n), __dmul_rn(w.im, inv_n)};
+    u = cmul(u, twist[kk]);
+    v = rint(__dmul_rn(scale, idx < n ? u.re : u.im));
+  }
+  batch_ptr(out, blockIdx.z)[((size_t)l << logN) + k] = dbl_residue(v, M);
+}
+
+void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int rows,
+                   int slots, double scale, int limbs, int is_ext, const Batch &out) {
+  const FFTTable &t = c->fft.at(slots);
+  const int n = slots;
+  int logn = 0;
+  while ((1 << logn) < n) logn++;
+  cplx *x = (cplx *)c->pool.alloc(sizeof(cplx) * (size_t)rows * n);
+  hipLaunchKernelGGL(k_fft_place, dim3((n + TPB - 1) / TPB, rows), dim3(TPB), 0, c->stream,
+                     d_re, d_im, x, t.perm, n, logn);
+  LAUNCH_CHECK();
+  for (int len = 2; len <= n; len <<= 1) {
+    hipLaunchKernelGGL(k_fft_stage, dim3((n / 2 + TPB - 1) / TPB, rows), dim3(TPB), 0,
+                       c->stream, x, n, len, (const cplx *)t.tw_inv);
+    LAUNCH_CHECK();
+  }
+  const int total = limbs + (is_ext ? c->alpha : 0);
+  hipLaunchKernelGGL(k_encode_finish, dim3(c->N / TPB, total, rows), dim3(TPB), 0, c->stream,
+                     x, (const cplx *)t.twist, out, n, c->logN, scale, limbs, c->L, c->d_mods);
+  LAUNCH_CHECK();
+  launch_ntt(c, out, out, rows, 0, total, limbs, false);
+  c->pool.release(x, sizeof(cplx) * (size_t)rows * n);
+}
+
+__global__ void k_scalar_encode(double v, int limbs, u64 *out, const ModQ *__restrict__ mods) {
+  const int l = threadIdx.x;
+  if (l < limbs) out[l] = dbl_residue(v, mods[l]);
+}
+
+void launch_scalar_encode(ckks_context *c, double v, int limbs, u64 *out) {
+  hipLaunchKernelGGL(k_scalar_encode, dim3(1), dim3(TPB), 0, c->stream, rint(v), limbs, out,
+                     c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// m = sum_d c_d s^d on the first K limbs (NTT domain).  grid (N / 256, K)
+__global__ void k_dec_poly(const u64 *__restrict__ ct, int polys, int limbs,
+                           const u64 *__restrict__ s_ntt, u64 *__restrict__ m, int logN,
+                           const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  const ModQ M = mods[l];
+  const u64 s = s_ntt[l * N + k];
+  u64 acc = 0, sp = 1;
+  for (int d = 0; d < polys; d++) {
+    acc = add_mod(acc, mul_mod(ct[((size_t)d * limbs + l) * N + k], sp, M), M.q);
+    sp = mul_mod(sp, s, M);
+  }
+  m[l * N + k] = acc;
+}
+
+// Balanced Garner reconstruction of coefficient (idx gap) over K limbs, then
+// x[br(k)] = (v_k + i v_{k+n}) * untwist_k for the decoding FFT.
+// grid (n / 256 rounded up)
+__global__ void k_dec_garner(const u64 *__restrict__ m, int K, const u64 *__restrict__ inv,
+                             const cplx *__restrict__ untwist, cplx *__restrict__ x, int n,
+                             int logn, int logN, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  if (k >= n) return;
+  const size_t N = (size_t)1 << logN;
+  const int gap = (int)(N / (2 * n));
+  double vv[2];
+  for (int h = 0; h < 2; h++) {
+    const size_t ci = (size_t)(k + h * n) * gap;
+    long long d[64];
+    for (int kk = 0; kk < K; kk++) {
+      const ModQ M = mods[kk];
+      u64 t = m[kk * N + ci];
+      for (int j = 0; j < kk; j++) {
+        t = mul_mod(sub_mod(t, signed_residue(d[j], M), M.q), inv[j * K + kk], M);
+      }
+      d[kk] = t > (M.q - 1) / 2 ? (long long)t - (long long)M.q : (long long)t;
+    }
+    double v = (double)d[K - 1];
+    for (int kk = K - 2; kk >= 0; kk--)
+      v = __dadd_rn(__dmul_rn(v, (double)mods[kk].q), (double)d[kk]);
+    vv[h] = v;
+  }
+  const u32 r = __brev((u32)k) >> (32 - logn);
+  x[r] = cmul(cplx{vv[0], vv[1]}, untwist[k]);
+}
+
+__global__ void k_dec_gather(const cplx *__restrict__ x, const u32 *__restrict__ perm, int n,
+                             double scale, double *__restrict__ re, double *__restrict__ im) {
+  const int j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  const cplx v = x[perm[j]];
+  re[j] = v.re / scale;
+  im[j] = v.im / scale;
+}
+
+void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, double *d_im) {
+  const int N = c->N, n = ct->slots;
+  int logn = 0;
+  while ((1 << logn) < n) logn++;
+  // limbs needed: smallest K with sum log2 q >= log2(scale) + 40
+  double need = log2(ct->scale) + 40.0, have = 0.0;
+  int K = 0;
+  while (K < ct->limbs && K < 64 && have < need) have += log2((double)c->primes[K++]);
+  if (K < 1) K = 1;
+  u64 *m = (u64 *)c->pool.alloc(sizeof(u64) * (size_t)K * N);
+  const bool is_pt = ct->polys == 1;
+  if (is_pt) {
+    HIP_OK(hipMemcpyAsync(m, ct->d, sizeof(u64) * (size_t)K * N, hipMemcpyDeviceToDevice,
+                          c->stream));
+  } else {
+    hipLaunchKernelGGL(k_dec_poly, dim3(N / TPB, K), dim3(TPB), 0, c->stream, ct->d, ct->polys,
+                       ct->limbs + (ct->is_ext ? c->alpha : 0), c->d_secret, m, c->logN,
+                       c->d_mods);
+    LAUNCH_CHECK();
+  }
+  Batch b{};
+  b.p[0] = m;
+  launch_ntt(c, b, b, 1, 0, K, K, true);
+  if (!c->garner.count(K)) {
+    std::vector<u64> inv((size_t)K * K, 0);
+    for (int j = 0; j < K; j++)
+      for (int k = 0; k < K; k++) {
+        if (j == k) continue;
+        const u64 q = c->primes[k];
+        // q_j^-1 mod q_k by Fermat
+        unsigned __int128 base = c->primes[j] % q, r = 1;
+        u64 e = q - 2;
+        while (e) {
+          if (e & 1) r = (r * base) % q;
+          base = (base * base) % q;
+          e >>= 1;
+        }
+        inv[(size_t)j * K + k] = (u64)r;
+      }
+    u64 *d = nullptr;
+    HIP_OK(hipMalloc(&d, sizeof(u64) * (size_t)K * K));
+    HIP_OK(hipMemcpy(d, inv.data(), sizeof(u64) * (size_t)K * K, hipMemcpyHostToDevice));
+    c->garner[K] = d;
+  }
+  const FFTTable &t = c->fft.at(n);
+  cplx *x = (cplx *)c->pool.alloc(sizeof(cplx) * n);
+  hipLaunchKernelGGL(k_dec_garner, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, c->stream, m, K,
+                     c->garner[K], (const cplx *)t.untwist, x, n, logn, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+  for (int len = 2; len <= n; len <<= 1) {
+    hipLaunchKernelGGL(k_fft_stage, dim3((n / 2 + TPB - 1) / TPB, 1), dim3(TPB), 0, c->stream,
+                       x, n, len, (const cplx *)t.tw_fwd);
+    LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(k_dec_gather, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, c->stream, x,
+                     t.perm, n, ct->scale, d_re, d_im);
+  LAUNCH_CHECK();
+  c->pool.release(x, sizeof(cplx) * n);
+  c->pool.release(m, sizeof(u64) * (size_t)K * N);
+}
+
+}  // namespace ckks

@@ -1,0 +1,834 @@
+"""Homomorphic evaluation surface (the ``easyfhe.fhe`` names the reference calls).
+
+Every function here forwards to the gfx950 library through the C ABI in
+include/ckks_mi355x.h; there is no host arithmetic path.  Signatures follow
+the reference's call sites (ciphertext arguments first, the native context
+last before keyword options, a new owned object returned).  Invalid levels,
+slot counts or states raise ``ValueError`` (the reference relies on that,
+operators/nonlinear/bootstrap.py:434); other backend failures raise
+``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import atexit
+import ctypes
+import dataclasses
+import hashlib
+import itertools
+import math
+import weakref
+from dataclasses import dataclass, field
+from typing import Any, Iterable, Sequence
+
+import numpy as np
+
+from . import _native
+from ._native import check, lib, ptr_array
+
+# ---------------------------------------------------------------------------
+# states and specs
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class CipherState:
+    """Level/scale bookkeeping of a ciphertext or plaintext
+    (reference operators/primitives.py:89-93, 140-144)."""
+
+    cur_limbs: int
+    scale_degree: int = 1
+    scaling_factor: float | None = None
+
+    def replace(self, **changes) -> "CipherState":
+        return dataclasses.replace(self, **changes)
+
+
+@dataclass
+class CKKSContextSpec:
+    """Context parameters (reference application/session.py:31-45)."""
+
+    depth: int
+    log_n: int
+    dnum: int = 3
+    dcrt_bits: int = 59
+    first_mod: int = 60
+    secret_key_dist: str = "SPARSE_TERNARY"
+    scale_mode: str = "fixed"
+    rescale_policy: str = "manual"
+    rotations: Sequence[int] = ()
+    auto_load_keys: bool = True
+    seed: int = 0
+    special_bits: int = 60
+    hamming_weight: int = 192
+    relin_key: bool = True
+
+
+_SECRET_MODES = {"SPARSE_TERNARY": 0, "UNIFORM_TERNARY": 1}
+
+# ---------------------------------------------------------------------------
+# native context and objects
+# ---------------------------------------------------------------------------
+
+_live_contexts: "weakref.WeakSet[NativeContext]" = weakref.WeakSet()
+_current: list = []
+
+
+class NativeContext:
+    """The device context: primes, tables, secret and evaluation keys.
+
+    Attributes mirror the reference's native context: ``L`` (Q limbs),
+    ``M`` (= 2N), ``logN``, ``max_slots``, ``device``, ``scale_at(limbs)`` and
+    ``rescale_divisor_at(limbs)`` (reference backend.py:214-228,
+    operators/nonlinear/polynomial.py:59).
+    """
+
+    def __init__(self, spec: CKKSContextSpec, device: str = "cuda"):
+        dist = str(spec.secret_key_dist).upper()
+        if dist not in _SECRET_MODES:
+            raise ValueError(f"unsupported secret_key_dist {spec.secret_key_dist!r}")
+        if str(spec.scale_mode) != "fixed":
+            raise ValueError("only scale_mode='fixed' is supported")
+        params = _native.ckks_params(
+            log_n=int(spec.log_n),
+            depth=int(spec.depth),
+            dnum=int(spec.dnum),
+            dcrt_bits=int(spec.dcrt_bits),
+            first_mod=int(spec.first_mod),
+            special_bits=int(spec.special_bits),
+            secret_mode=_SECRET_MODES[dist],
+            hamming_weight=int(spec.hamming_weight),
+            seed=int(spec.seed) & (2**64 - 1),
+        )
+        handle = ctypes.c_void_p()
+        check(lib.ckks_context_create(ctypes.byref(params), ctypes.byref(handle)))
+        self._h = handle.value
+        info = _native.ckks_context_info()
+        check(lib.ckks_context_info_get(self._h, ctypes.byref(info)))
+        self.N = int(info.N)
+        self.logN = int(info.log_n)
+        self.L = int(info.L)
+        self.alpha = int(info.alpha)
+        self.digit_size = int(info.digit_size)
+        self.max_slots = int(info.max_slots)
+        self.M = 2 * self.N
+        self.device = str(device)
+        self.spec = spec
+        self._enc_ids = itertools.count(1)
+        _live_contexts.add(self)
+        _current.append(weakref.ref(self))
+
+    # -- reference-visible attributes ------------------------------------------
+    def scale_at(self, limbs: int) -> float:
+        return float(lib.ckks_scale_at(self._h, int(limbs)))
+
+    def rescale_divisor_at(self, limbs: int) -> float:
+        return float(lib.ckks_rescale_divisor_at(self._h, int(limbs)))
+
+    def clear_cuda_rotation_cache(self, keep_rotations: Iterable[int] = ()) -> None:
+        keep = np.asarray(list(keep_rotations) or [0], dtype=np.int64)
+        check(lib.ckks_clear_rotation_keys(self._h, keep.ctypes.data_as(_native.I64P),
+                                           len(list(keep_rotations))))
+
+    # -- extras ---------------------------------------------------------------------
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def primes(self) -> np.ndarray:
+        out = np.zeros(self.L + self.alpha, dtype=np.uint64)
+        check(lib.ckks_context_primes(self._h, out.ctypes.data_as(_native.U64P)))
+        return out
+
+    def secret(self) -> np.ndarray:
+        out = np.zeros(self.N, dtype=np.int8)
+        check(lib.ckks_context_secret(self._h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int8))))
+        return out
+
+    def galois_element(self, rotation: int) -> int:
+        return int(lib.ckks_galois_element(self._h, int(rotation)))
+
+    def generate_rotation_keys(self, rotations: Iterable[int]) -> None:
+        rot = np.asarray(sorted({int(r) for r in rotations}), dtype=np.int64)
+        if rot.size:
+            check(lib.ckks_keygen_rotations(self._h, rot.ctypes.data_as(_native.I64P), rot.size))
+
+    def generate_relin_key(self) -> None:
+        check(lib.ckks_keygen_relin(self._h))
+
+    def has_rotation_key(self, rotation: int) -> bool:
+        return bool(lib.ckks_has_rotation_key(self._h, int(rotation)))
+
+    def download_key(self, galois: int) -> np.ndarray:
+        digits = ctypes.c_int()
+        check(lib.ckks_key_download(self._h, int(galois), None, ctypes.byref(digits)))
+        out = np.zeros((digits.value, 2, self.L + self.alpha, self.N), dtype=np.uint64)
+        check(lib.ckks_key_download(self._h, int(galois), out.ctypes.data_as(_native.U64P), None))
+        return out
+
+    def next_encryption_id(self) -> int:
+        return next(self._enc_ids)
+
+    def synchronize(self) -> None:
+        check(lib.ckks_synchronize(self._h))
+
+    def memory_info(self) -> dict[str, int]:
+        live, cached = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib.ckks_memory_info(self._h, ctypes.byref(live), ctypes.byref(cached)))
+        return {"live_bytes": int(live.value), "cached_bytes": int(cached.value)}
+
+    def empty_cache(self) -> None:
+        check(lib.ckks_empty_cache(self._h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib.ckks_context_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _close_all_contexts() -> None:
+    # Destroy device contexts while the HIP runtime is still up; ciphertexts
+    # collected later only drop their host records.
+    for ctx in list(_live_contexts):
+        ctx.close()
+
+
+atexit.register(_close_all_contexts)
+
+
+def current_context() -> NativeContext:
+    while _current:
+        ctx = _current[-1]()
+        if ctx is not None and ctx._h:
+            return ctx
+        _current.pop()
+    raise RuntimeError("no live easyfhe context")
+
+
+class Ciphertext:
+    """Owned device object: a ciphertext (2 or 3 polynomials), a plaintext
+    (1 polynomial) or a scalar constant (per-limb values).
+
+    ``state``, ``slots``, ``is_ext``, ``deep_copy()`` and ``release()`` follow
+    the reference's usage (operators/primitives.py:115-150,
+    backend.py:336-351)."""
+
+    __slots__ = ("context", "_h", "__weakref__")
+
+    def __init__(self, context: NativeContext, handle: int):
+        self.context = context
+        self._h = handle
+
+    @property
+    def handle(self) -> int:
+        if not self._h:
+            raise RuntimeError("ciphertext was released")
+        return self._h
+
+    def _info(self) -> _native.ckks_ct_info:
+        info = _native.ckks_ct_info()
+        check(lib.ckks_ct_info_get(self.handle, ctypes.byref(info)))
+        return info
+
+    @property
+    def state(self) -> CipherState:
+        info = self._info()
+        return CipherState(cur_limbs=int(info.limbs), scale_degree=int(info.scale_degree),
+                           scaling_factor=float(info.scale))
+
+    @property
+    def slots(self) -> int:
+        return int(self._info().slots)
+
+    @property
+    def is_ext(self) -> bool:
+        return bool(self._info().is_ext)
+
+    @property
+    def polys(self) -> int:
+        return int(self._info().polys)
+
+    @property
+    def degree(self) -> int:
+        return self.polys - 1
+
+    def set_scale(self, scale: float, scale_degree: int | None = None) -> None:
+        info = self._info()
+        check(lib.ckks_ct_set_scale(self.handle, float(scale),
+                                    int(info.scale_degree if scale_degree is None else scale_degree)))
+
+    def deep_copy(self) -> "Ciphertext":
+        out = ctypes.c_void_p()
+        check(lib.ckks_ct_copy(self.context.handle, self.handle, ctypes.byref(out)))
+        return Ciphertext(self.context, out.value)
+
+    def download(self) -> np.ndarray:
+        info = self._info()
+        per = int(info.limbs) + (self.context.alpha if info.is_ext else 0)
+        if info.polys == 0:
+            out = np.zeros(int(info.limbs), dtype=np.uint64)
+        else:
+            out = np.zeros((int(info.polys), per, self.context.N), dtype=np.uint64)
+        check(lib.ckks_ct_download(self.context.handle, self.handle,
+                                   out.ctypes.data_as(_native.U64P)))
+        return out
+
+    def release(self) -> None:
+        if self._h:
+            lib.ckks_ct_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+Plaintext = Ciphertext
+
+
+def _wrap(context: NativeContext, handle: ctypes.c_void_p) -> Ciphertext:
+    return Ciphertext(context, handle.value)
+
+
+def _ctx(ct: Ciphertext, context) -> NativeContext:
+    if context is not None and context is not ct.context:
+        raise ValueError("ciphertext belongs to a different context")
+    return ct.context
+
+
+def upload(context: NativeContext, data: np.ndarray, *, slots: int, scale: float,
+           scale_degree: int = 1, is_ext: bool = False) -> Ciphertext:
+    """Raw limbs [polys, limbs(+alpha), N] to a device object (tests, batching)."""
+    data = np.ascontiguousarray(data, dtype=np.uint64)
+    polys, per = int(data.shape[0]), int(data.shape[1])
+    limbs = per - (context.alpha if is_ext else 0)
+    out = ctypes.c_void_p()
+    check(lib.ckks_ct_upload(context.handle, data.ctypes.data_as(_native.U64P), polys, limbs,
+                             int(is_ext), int(slots), float(scale), int(scale_degree),
+                             ctypes.byref(out)))
+    return _wrap(context, out)
+
+
+# ---------------------------------------------------------------------------
+# client (secret-key side)
+# ---------------------------------------------------------------------------
+
+
+class Client:
+    """Encryption and decryption with the context's secret key
+    (reference backend.py:221-229, 305-313; application/session.py:71-77)."""
+
+    def __init__(self, context: NativeContext):
+        self.context = context
+
+    def encrypt(self, values, device: str | None = None, slots: int | None = None,
+                cur_limbs: int | None = None, scaling_factor: float | None = None,
+                enc_id: int | None = None) -> Ciphertext:
+        ctx = self.context
+        slots = ctx.max_slots if slots is None else int(slots)
+        limbs = ctx.L if cur_limbs is None else int(cur_limbs)
+        scale = ctx.scale_at(limbs) if scaling_factor is None else float(scaling_factor)
+        z = np.asarray(values).reshape(-1)
+        if z.size > slots:
+            raise ValueError(f"{z.size} values do not fit {slots} slots")
+        buf = np.zeros(slots, dtype=np.complex128)
+        buf[: z.size] = z
+        re = np.ascontiguousarray(buf.real)
+        im = np.ascontiguousarray(buf.imag)
+        eid = ctx.next_encryption_id() if enc_id is None else int(enc_id)
+        out = ctypes.c_void_p()
+        check(lib.ckks_encrypt(ctx.handle, re.ctypes.data_as(_native.DP),
+                               im.ctypes.data_as(_native.DP), slots, limbs, scale,
+                               eid & 0xFFFFFFFF, ctypes.byref(out)))
+        return _wrap(ctx, out)
+
+    def decrypt_complex(self, ct: Ciphertext) -> np.ndarray:
+        slots = ct.slots
+        re = np.zeros(slots)
+        im = np.zeros(slots)
+        check(lib.ckks_decrypt(self.context.handle, ct.handle, re.ctypes.data_as(_native.DP),
+                               im.ctypes.data_as(_native.DP)))
+        return re + 1j * im
+
+    def decrypt(self, ct: Ciphertext) -> np.ndarray:
+        """Real part of the decrypted slots (reference backend.py:305-313)."""
+        return np.real(self.decrypt_complex(ct)).copy()
+
+
+def generate_client_context(spec: CKKSContextSpec, device: str = "cuda"):
+    """Create the context, the secret key, the relinearisation key and the
+    rotation keys of ``spec.rotations`` (reference application/session.py:31-45)."""
+    ctx = NativeContext(spec, device=device)
+    if spec.relin_key:
+        ctx.generate_relin_key()
+    ctx.generate_rotation_keys(int(r) for r in spec.rotations if int(r))
+    return Client(ctx), ctx
+
+
+# ---------------------------------------------------------------------------
+# encoding
+# ---------------------------------------------------------------------------
+
+
+def encode_rows(context: NativeContext, rows, *, limbs: int, scale: float, slots: int,
+                is_ext: bool = False) -> list[Ciphertext]:
+    z = np.asarray(rows)
+    if z.ndim == 1:
+        z = z[None, :]
+    if z.shape[1] != slots:
+        raise ValueError(f"row length {z.shape[1]} != slots {slots}")
+    z = z.astype(np.complex128)
+    re = np.ascontiguousarray(z.real)
+    im = np.ascontiguousarray(z.imag)
+    n = z.shape[0]
+    handles = (ctypes.c_void_p * n)()
+    check(lib.ckks_encode_rows(context.handle, re.ctypes.data_as(_native.DP),
+                               im.ctypes.data_as(_native.DP), n, int(slots), int(limbs),
+                               float(scale), int(is_ext), handles))
+    return [Ciphertext(context, handles[i]) for i in range(n)]
+
+
+def decode(pt: Ciphertext) -> np.ndarray:
+    slots = pt.slots
+    re = np.zeros(slots)
+    im = np.zeros(slots)
+    check(lib.ckks_decode(pt.context.handle, pt.handle, re.ctypes.data_as(_native.DP),
+                          im.ctypes.data_as(_native.DP)))
+    return re + 1j * im
+
+
+class PackedRaw:
+    """Already packed ``[rows, slots]`` (or ``[slots]``) values
+    (reference backend.py:274-284)."""
+
+    def __init__(self, tensor):
+        self.tensor = tensor
+
+    def values(self, slots: int, context) -> np.ndarray:
+        return np.asarray(self.tensor)
+
+
+class UnpackedRaw:
+    """Raw source plus a packer ``packer(source, slots, context) -> [rows, slots]``
+    (reference operators/linear/weight.py:309-366)."""
+
+    def __init__(self, source, packer):
+        self.source = source
+        self.packer = packer
+
+    def values(self, slots: int, context) -> np.ndarray:
+        return np.asarray(self.packer(self.source, slots, context))
+
+
+class ConstantBundle:
+    """Named constant vectors encoded on demand at a requested state
+    (reference backend.py:260-297, operators/primitives.py:83-97).
+
+    ``plaintext`` returns one plaintext for a 1-D vector and a list of
+    plaintexts (one per row) for a 2-D ``[rows, slots]`` block.
+    Cache modes: ``none`` keeps nothing, ``plain``/``both`` keep encoded
+    plaintexts per (name, limbs, scale, basis, slots), ``middle`` keeps the
+    packed host values."""
+
+    def __init__(self, vectors: dict, cache_mode: str = "none"):
+        if cache_mode not in {"none", "middle", "plain", "both"}:
+            raise ValueError(f"unknown cache_mode {cache_mode!r}")
+        self.vectors = dict(vectors)
+        self.cache_mode = cache_mode
+        self._plain: dict = {}
+        self._middle: dict = {}
+
+    def set_cache_mode(self, mode: str) -> None:
+        if mode not in {"none", "middle", "plain", "both"}:
+            raise ValueError(f"unknown cache_mode {mode!r}")
+        self.cache_mode = mode
+
+    def _values(self, name: str, slots: int, context) -> np.ndarray:
+        if name in self._middle:
+            return self._middle[name]
+        values = self.vectors[name].values(slots, context)
+        if self.cache_mode in ("middle", "both"):
+            self._middle[name] = values
+        return values
+
+    def plaintext(self, name: str, *, state: CipherState, slots: int, context: NativeContext,
+                  is_ext: bool = False, cache: bool = False):
+        limbs = int(state.cur_limbs)
+        scale = float(state.scaling_factor) if state.scaling_factor else context.scale_at(limbs)
+        key = (str(name), limbs, scale, bool(is_ext), int(slots))
+        if key in self._plain:
+            return self._plain[key]
+        values = self._values(str(name), int(slots), context)
+        arr = np.asarray(values)
+        pts = encode_rows(context, arr, limbs=limbs, scale=scale, slots=int(slots),
+                          is_ext=bool(is_ext))
+        result = pts[0] if arr.ndim == 1 else pts
+        if cache or self.cache_mode in ("plain", "both"):
+            self._plain[key] = result
+        return result
+
+    def cache_info(self) -> dict[str, int]:
+        total = 0
+        entries = 0
+        for value in self._plain.values():
+            items = value if isinstance(value, list) else [value]
+            for pt in items:
+                info = pt._info()
+                total += 8 * pt.context.N * (int(info.limbs) +
+                                             (pt.context.alpha if info.is_ext else 0))
+                entries += 1
+        total += sum(int(np.asarray(v).nbytes) for v in self._middle.values())
+        return {"entries": entries, "total_bytes": total}
+
+    def clear_cache(self) -> None:
+        for value in self._plain.values():
+            for pt in (value if isinstance(value, list) else [value]):
+                pt.release()
+        self._plain.clear()
+        self._middle.clear()
+
+
+def encode_scalar(value: float, cur_limbs: int, scale_degree: int = 1,
+                  scaling_factor: float | None = None, mode: str | None = None,
+                  context: NativeContext | None = None) -> Ciphertext:
+    """Per-limb constant round(value * scale); ``mode="integer"`` encodes the
+    value itself (reference operators/nonlinear/polynomial.py:40-67,
+    operators/nonlinear/bootstrap.py:330-349)."""
+    if context is None:
+        context = current_context()
+    if mode == "integer":
+        scale = 1.0
+    else:
+        scale = float(scaling_factor) if scaling_factor else context.scale_at(int(cur_limbs))
+    out = ctypes.c_void_p()
+    check(lib.ckks_encode_scalar(context.handle, float(value), int(cur_limbs), scale,
+                                 ctypes.byref(out)))
+    return _wrap(context, out)
+
+
+# ---------------------------------------------------------------------------
+# arithmetic
+# ---------------------------------------------------------------------------
+
+
+def _binary(fn, a: Ciphertext, b: Ciphertext, context) -> Ciphertext:
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(fn(ctx.handle, a.handle, b.handle, ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def homo_add(a, b, context=None):
+    return _binary(lib.ckks_add, a, b, context)
+
+
+def homo_sub(a, b, context=None):
+    return _binary(lib.ckks_sub, a, b, context)
+
+
+def homo_add_pt(a, pt, context=None):
+    return _binary(lib.ckks_add_pt, a, pt, context)
+
+
+def homo_mul_pt(a, pt, context=None):
+    return _binary(lib.ckks_mul_pt, a, pt, context)
+
+
+def homo_mul_i(a, context=None, negative: bool = False):
+    """Multiply slots by +i (or -i): the monomial X^(N/2), level-free
+    (reference operators/linear/complex.py:21, attention/codec.py:44)."""
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(lib.ckks_mul_i(ctx.handle, a.handle, int(bool(negative)), ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def homo_add_scalar(a, scalar, context=None):
+    return _binary(lib.ckks_add_scalar, a, scalar, context)
+
+
+def homo_mul_scalar(a, scalar, context=None):
+    return _binary(lib.ckks_mul_scalar, a, scalar, context)
+
+
+def homo_mul_scalar_rescale(a, scalar, context=None):
+    prod = homo_mul_scalar(a, scalar, context)
+    try:
+        if float(scalar.state.scaling_factor or 1.0) == 1.0:
+            return prod.deep_copy()
+        return rescale(prod, context)
+    finally:
+        prod.release()
+
+
+def homo_mul_no_relin(a, b, context=None):
+    return _binary(lib.ckks_mul_no_relin, a, b, context)
+
+
+def homo_relinearize(a, context=None):
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(lib.ckks_relinearize(ctx.handle, a.handle, ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def homo_mul_relin(a, b, context=None):
+    return _binary(lib.ckks_mul_relin, a, b, context)
+
+
+def rescale(a, context=None):
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(lib.ckks_rescale(ctx.handle, a.handle, ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def align_to(a, target_state: CipherState, context=None):
+    """Modulus drop to ``target_state.cur_limbs``; returns ``a`` itself when
+    nothing changes (reference operators/primitives.py:145-150).  A target
+    scaling factor must agree with ``a``'s to 2^-10 relative (fixed-scale
+    bookkeeping: primes are within 2^-17 of the nominal scale)."""
+    ctx = _ctx(a, context)
+    target = int(target_state.cur_limbs)
+    info = a._info()
+    if target > int(info.limbs):
+        raise ValueError(
+            f"cannot align {int(info.limbs)} limbs up to {target} limbs")
+    want = target_state.scaling_factor
+    if want is not None and abs(float(want) - info.scale) > float(info.scale) / 1024.0:
+        raise ValueError("align_to cannot change the scaling factor")
+    if target == int(info.limbs):
+        return a
+    out = ctypes.c_void_p()
+    check(lib.ckks_drop_limbs(ctx.handle, a.handle, target, ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def homo_mul_relin_rescale_postop(left, right, context=None, *, apply_double: bool = False,
+                                  sub=None, scalar=None):
+    """rescale(relin(l r)), then x2 when ``apply_double``, then ``- sub`` or
+    ``+ scalar`` at the output state (reference
+    operators/nonlinear/polynomial.py:115-203)."""
+    ctx = _ctx(left, context)
+    limbs = min(left.state.cur_limbs, right.state.cur_limbs)
+    l2 = align_to(left, left.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+    r2 = align_to(right, right.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+    owned = [x for x, y in ((l2, left), (r2, right)) if x is not y]
+    try:
+        prod = homo_mul_relin(l2, r2, ctx)
+        try:
+            value = rescale(prod, ctx)
+        finally:
+            prod.release()
+    finally:
+        for x in owned:
+            x.release()
+    if apply_double:
+        doubled = homo_add(value, value, ctx)
+        value.release()
+        value = doubled
+    if sub is not None:
+        aligned = align_to(sub, value.state.replace(scaling_factor=None), ctx)
+        try:
+            diff = homo_sub(value, aligned, ctx)
+        finally:
+            if aligned is not sub:
+                aligned.release()
+        value.release()
+        value = diff
+    if scalar is not None:
+        added = homo_add_scalar(value, scalar, ctx)
+        value.release()
+        value = added
+    return value
+
+
+def homo_rotate(a, rotation: int, context=None):
+    """Left rotation by ``rotation`` slots (``np.roll(m, -k)``); ``M - 1``
+    conjugates (reference operators/linear/operator.py:333,
+    operators/linear/complex.py:47-51)."""
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(lib.ckks_rotate(ctx.handle, a.handle, int(rotation), ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
+def homo_rotate_many(cts: Sequence[Ciphertext], rotation: int, context=None) -> list:
+    """One rotation of many same-level ciphertexts; the key is streamed once."""
+    cts = list(cts)
+    if not cts:
+        return []
+    ctx = _ctx(cts[0], context)
+    ins = ptr_array([c.handle for c in cts])
+    outs = (ctypes.c_void_p * len(cts))()
+    check(lib.ckks_rotate_many(ctx.handle, ins, len(cts), int(rotation), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(cts))]
+
+
+def homo_mul_relin_rescale_many(left: Sequence[Ciphertext], right: Sequence[Ciphertext],
+                                context=None) -> list:
+    left, right = list(left), list(right)
+    if len(left) != len(right):
+        raise ValueError("operand lists differ in length")
+    if not left:
+        return []
+    ctx = _ctx(left[0], context)
+    outs = (ctypes.c_void_p * len(left))()
+    check(lib.ckks_mul_relin_rescale_many(ctx.handle, ptr_array([c.handle for c in left]),
+                                          ptr_array([c.handle for c in right]), len(left),
+                                          outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(left))]
+
+
+def _hoisted(ct: Ciphertext, offsets: Sequence[int], ctx: NativeContext) -> list:
+    offs = np.asarray([int(o) for o in offsets], dtype=np.int64)
+    outs = (ctypes.c_void_p * len(offs))()
+    check(lib.ckks_hoisted_rotate(ctx.handle, ct.handle, offs.ctypes.data_as(_native.I64P),
+                                  len(offs), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(offs))]
+
+
+def prepare_hoisted_baby_rotations(ct, baby_offsets, context=None, strategy: str = "normal",
+                                   baby_anchor_step: int = -1):
+    """Rotations of ``ct`` by every baby offset from one shared ModUp
+    (reference operators/linear/operator.py:100-117).  With an anchor step
+    A < B the babies come in blocks of A: block k starts from the anchor
+    rot(ct, offsets[kA]) reached by chaining one anchor key, and covers its
+    block with one hoisted call."""
+    ctx = _ctx(ct, context)
+    offsets = [int(o) for o in baby_offsets]
+    if strategy not in {"normal", "ext_normal", "ext_double_hoist"}:
+        raise ValueError(f"unknown strategy {strategy!r}")
+    B = len(offsets)
+    anchor = int(baby_anchor_step)
+    if anchor < 2 or anchor >= B:
+        return tuple(_hoisted(ct, offsets, ctx))
+    result: list = []
+    base = ct
+    for start in range(0, B, anchor):
+        block = offsets[start: start + anchor]
+        if start:
+            nxt = homo_rotate(base, offsets[start] - offsets[start - anchor], ctx)
+            if base is not ct:
+                base.release()
+            base = nxt
+        result.extend(_hoisted(base, [o - offsets[start] for o in block], ctx))
+    if base is not ct:
+        base.release()
+    return tuple(result)
+
+
+def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count: int,
+                    context=None, strategy: str = "normal", baby_anchor_step: int = -1,
+                    baby_rotations=None):
+    """BSGS diagonal MAC
+    ``sum_{g<G} rot_{g giant}( sum_{b<B} pt[g B + b] * rot_{baby_b}(ct) )``
+    with a Horner chain over one giant key; unrescaled
+    (reference operators/linear/operator.py:320-330, operators/transform.py:108).
+    The ext strategies evaluate the same schedule in the Q basis here; the
+    Q limbs of an extended plaintext are used as they are."""
+    ctx = _ctx(ct, context)
+    pts = plaintexts if isinstance(plaintexts, (list, tuple)) else [plaintexts]
+    B = len(list(baby_offsets))
+    if len(pts) < B * int(giant_count):
+        raise ValueError(f"need {B * int(giant_count)} plaintexts, got {len(pts)}")
+    babies = baby_rotations
+    owned = False
+    if babies is None:
+        babies = prepare_hoisted_baby_rotations(ct, baby_offsets, ctx, strategy=strategy,
+                                                baby_anchor_step=baby_anchor_step)
+        owned = True
+    try:
+        out = ctypes.c_void_p()
+        check(lib.ckks_hoisted_mac_sum(ctx.handle, ptr_array([b.handle for b in babies]), B,
+                                       ptr_array([p.handle for p in pts[: B * int(giant_count)]]),
+                                       int(giant_offset), int(giant_count), ctypes.byref(out)))
+        return _wrap(ctx, out)
+    finally:
+        if owned:
+            for b in babies:
+                b.release()
+
+
+# ---------------------------------------------------------------------------
+# batches (reference operators/attention/kernel_helpers.py:83-85,
+# attention/input.py:792-826)
+# ---------------------------------------------------------------------------
+
+
+class CipherBatch:
+    """An ordered group of same-level ciphertexts."""
+
+    def __init__(self, ciphers: Sequence[Ciphertext]):
+        self.cv = list(ciphers)
+
+    @property
+    def batch_size(self) -> int:
+        return len(self.cv)
+
+    def cipher_like(self, cv, batch_size: int | None = None, slots: int | None = None):
+        return CipherBatch(list(cv)[: batch_size] if batch_size else list(cv))
+
+    def __iter__(self):
+        return iter(self.cv)
+
+    def __len__(self):
+        return len(self.cv)
+
+    def release(self) -> None:
+        for c in self.cv:
+            c.release()
+
+
+def pack_cipher_batch(ciphers: Iterable[Ciphertext]) -> CipherBatch:
+    return CipherBatch([c.deep_copy() for c in ciphers])
+
+
+def unpack_cipher_batch(batch: CipherBatch) -> tuple:
+    return tuple(batch.cv)
+
+
+def fast_rotate(ct, offsets, context=None, output_ext: bool = False) -> CipherBatch:
+    """Hoisted rotations of one ciphertext into a batch (outputs in the Q
+    basis; ``moddown_from_ext`` is then the identity)."""
+    ctx = _ctx(ct, context)
+    return CipherBatch(_hoisted(ct, [int(o) for o in offsets], ctx))
+
+
+def moddown_from_ext(ct, context=None):
+    if ct.is_ext:
+        raise ValueError("extended-basis ciphertexts are not produced by this backend")
+    return ct.deep_copy()
+
+
+def grouped_pairwise_mac(batch: CipherBatch, plaintexts, groups, context=None) -> list:
+    """``sum_{i in group} batch[i] * pt[i]`` per group (unrescaled)."""
+    cts = batch.cv if isinstance(batch, CipherBatch) else list(batch)
+    if not cts:
+        return []
+    ctx = _ctx(cts[0], context)
+    results = []
+    for group in groups:
+        acc = None
+        for i in group:
+            term = homo_mul_pt(cts[int(i)], plaintexts[int(i)], ctx)
+            if acc is None:
+                acc = term
+            else:
+                new = homo_add(acc, term, ctx)
+                acc.release()
+                term.release()
+                acc = new
+        results.append(acc)
+    return results
+
+
+__all__ = [name for name in dir() if not name.startswith("_")]

@@ -1,0 +1,190 @@
+/*
+ * ckks_mi355x.h -- C ABI of the MI355X (gfx950) RNS-CKKS evaluation backend.
+ *
+ * This is the drop-in boundary for the reference's backend: every entry point
+ * below replaces one EasyFHE call that the reference's Python makes (cited as
+ * reference file:line).  Handles are opaque; all functions return a status:
+ *   CKKS_OK (0), CKKS_EINVAL (1, maps to Python ValueError),
+ *   CKKS_ERUNTIME (2, RuntimeError), CKKS_ENOKEY (3, missing evaluation key,
+ *   RuntimeError).
+ * ckks_last_error() returns the calling thread's message for the last failure.
+ *
+ * Device work is asynchronous on one HIP stream per context; functions that
+ * return host data (decrypt, decode, download) synchronise that stream.
+ * Ciphertext limbs are uint64 residues in the NTT domain, layout
+ * [polys][limbs][N]; an extended (QP-basis) object carries limbs + alpha
+ * limbs per polynomial.  Ownership: every handle returned is owned by the
+ * caller and released with its *_free function; no callee frees a handle it
+ * was passed (reference llama3fhe/backend.py:336-351 release semantics).
+ */
+#ifndef CKKS_MI355X_H
+#define CKKS_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CKKS_OK 0
+#define CKKS_EINVAL 1
+#define CKKS_ERUNTIME 2
+#define CKKS_ENOKEY 3
+
+typedef struct ckks_context ckks_context;
+typedef struct ckks_ct ckks_ct; /* ciphertext or plaintext polynomial set */
+typedef struct ckks_event ckks_event;
+
+/* Context parameters; fields follow fhe.CKKSContextSpec
+ * (reference llama3fhe/application/session.py:31-45, backend.py:457-471). */
+typedef struct {
+  int log_n;          /* ring degree N = 2^log_n */
+  int depth;          /* multiplicative depth; Q has depth + 1 limbs */
+  int dnum;           /* key-switching digits over the full chain */
+  int dcrt_bits;      /* bit size of q_1 .. q_depth */
+  int first_mod;      /* bit size of q_0 */
+  int special_bits;   /* bit size of the special primes (<= 60) */
+  int secret_mode;    /* 0 sparse ternary (SPARSE_TERNARY), 1 uniform ternary */
+  int hamming_weight; /* sparse secret weight */
+  uint64_t seed;      /* seed of the key / encryption PRNG streams */
+} ckks_params;
+
+typedef struct {
+  int N, log_n, L, alpha, digit_size, dnum, max_slots;
+  double default_scale;
+} ckks_context_info;
+
+typedef struct {
+  int polys, limbs, is_ext, slots, scale_degree;
+  double scale;
+} ckks_ct_info;
+
+const char *ckks_last_error(void);
+
+/* fhe.generate_client_context (reference application/session.py:31-45). */
+int ckks_context_create(const ckks_params *params, ckks_context **out);
+void ckks_context_destroy(ckks_context *ctx);
+int ckks_context_info_get(const ckks_context *ctx, ckks_context_info *out);
+/* Prime chain q_0..q_{L-1}, p_0..p_{alpha-1}. */
+int ckks_context_primes(const ckks_context *ctx, uint64_t *out);
+/* Secret coefficients (client side). */
+int ckks_context_secret(const ckks_context *ctx, int8_t *out);
+/* Native-context scale_at(limbs) / rescale_divisor_at(limbs)
+ * (reference backend.py:228, operators/nonlinear/polynomial.py:59). */
+double ckks_scale_at(const ckks_context *ctx, int limbs);
+double ckks_rescale_divisor_at(const ckks_context *ctx, int limbs);
+/* Galois element for a rotation index (2N-1 requests conjugation). */
+uint64_t ckks_galois_element(const ckks_context *ctx, int64_t rotation);
+
+/* Key generation for the CKKSContextSpec rotation list
+ * (reference application/session.py:41, backend.py:469). */
+int ckks_keygen_rotations(ckks_context *ctx, const int64_t *rotations, int n);
+int ckks_keygen_relin(ckks_context *ctx);
+int ckks_has_rotation_key(const ckks_context *ctx, int64_t rotation);
+/* Evaluation key in normal form, [digits][2][L+alpha][N]; returns digits
+ * through *digits.  Pass out = NULL to query the size. */
+int ckks_key_download(ckks_context *ctx, uint64_t galois, uint64_t *out,
+                      int *digits);
+/* Drop cached keys except the listed rotations (native-context
+ * clear_cuda_rotation_cache, reference operators/nonlinear/bootstrap.py:206). */
+int ckks_clear_rotation_keys(ckks_context *ctx, const int64_t *keep, int n);
+int ckks_synchronize(ckks_context *ctx);
+/* Bytes currently held by the context's device pool (live + cached). */
+int ckks_memory_info(ckks_context *ctx, size_t *live, size_t *cached);
+int ckks_empty_cache(ckks_context *ctx);
+
+/* client.encrypt / client.decrypt (reference backend.py:221-229,305-313,
+ * application/session.py:71-77).  enc_id selects the encryption randomness
+ * stream; im may be NULL. */
+int ckks_encrypt(ckks_context *ctx, const double *re, const double *im,
+                 int slots, int limbs, double scale, uint32_t enc_id,
+                 ckks_ct **out);
+int ckks_decrypt(ckks_context *ctx, const ckks_ct *ct, double *re, double *im);
+/* ConstantBundle.plaintext encode of `rows` vectors of `slots` complex values
+ * (reference operators/linear/weight.py:322-366, backend.py:274-297);
+ * outputs one plaintext per row. */
+int ckks_encode_rows(ckks_context *ctx, const double *re, const double *im,
+                     int rows, int slots, int limbs, double scale, int is_ext,
+                     ckks_ct **out);
+/* fhe.encode_scalar (reference operators/nonlinear/polynomial.py:40-67):
+ * round(value * scale) per limb; integer mode when scale == 1. */
+int ckks_encode_scalar(ckks_context *ctx, double value, int limbs, double scale,
+                       ckks_ct **out);
+int ckks_decode(ckks_context *ctx, const ckks_ct *pt, double *re, double *im);
+
+/* Raw transfer (parity tests and batch plumbing). */
+int ckks_ct_upload(ckks_context *ctx, const uint64_t *data, int polys,
+                   int limbs, int is_ext, int slots, double scale,
+                   int scale_degree, ckks_ct **out);
+int ckks_ct_download(ckks_context *ctx, const ckks_ct *ct, uint64_t *out);
+int ckks_ct_info_get(const ckks_ct *ct, ckks_ct_info *out);
+int ckks_ct_set_scale(ckks_ct *ct, double scale, int scale_degree);
+int ckks_ct_copy(ckks_context *ctx, const ckks_ct *ct, ckks_ct **out);
+void ckks_ct_free(ckks_ct *ct);
+
+/* Limb-wise arithmetic: homo_add / homo_sub / homo_add_pt / homo_mul_pt /
+ * homo_mul_i / homo_add_scalar / homo_mul_scalar (reference
+ * operators/primitives.py:43,56,72; operators/linear/complex.py:21;
+ * operators/nonlinear/polynomial.py:73,82). */
+int ckks_add(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
+int ckks_sub(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
+int ckks_add_pt(ckks_context *ctx, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out);
+int ckks_mul_pt(ckks_context *ctx, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out);
+int ckks_mul_i(ckks_context *ctx, const ckks_ct *a, int negative, ckks_ct **out);
+int ckks_add_scalar(ckks_context *ctx, const ckks_ct *a, const ckks_ct *s, ckks_ct **out);
+int ckks_mul_scalar(ckks_context *ctx, const ckks_ct *a, const ckks_ct *s, ckks_ct **out);
+/* homo_mul_no_relin / homo_relinearize / homo_mul_relin (reference
+ * operators/attention/qk.py:399, kernel_helpers.py:155, primitives.py:25). */
+int ckks_mul_no_relin(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
+int ckks_relinearize(ckks_context *ctx, const ckks_ct *a, ckks_ct **out);
+int ckks_mul_relin(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
+/* fhe.rescale / fhe.align_to as a limb drop (reference
+ * operators/linear/operator.py:386, primitives.py:145). */
+int ckks_rescale(ckks_context *ctx, const ckks_ct *a, ckks_ct **out);
+int ckks_drop_limbs(ckks_context *ctx, const ckks_ct *a, int target_limbs, ckks_ct **out);
+/* fhe.homo_rotate (reference operators/linear/operator.py:333,
+ * operators/linear/complex.py:47). */
+int ckks_rotate(ckks_context *ctx, const ckks_ct *a, int64_t rotation, ckks_ct **out);
+/* Batched key switching: one rotation index applied to n ciphertexts at one
+ * level; the rotation key is streamed from HBM once per call (the keyswitch
+ * hot path under homo_rotate). */
+int ckks_rotate_many(ckks_context *ctx, const ckks_ct *const *in, int n,
+                     int64_t rotation, ckks_ct **out);
+/* homo_mul_relin + rescale for n pairs (config: HMult+relin+rescale). */
+int ckks_mul_relin_rescale_many(ckks_context *ctx, const ckks_ct *const *a,
+                                const ckks_ct *const *b, int n, ckks_ct **out);
+/* fhe.prepare_hoisted_baby_rotations (reference operators/linear/operator.py:105):
+ * one ModUp of c1 shared by all rotations. */
+int ckks_hoisted_rotate(ckks_context *ctx, const ckks_ct *a,
+                        const int64_t *rotations, int n, ckks_ct **out);
+/* fhe.hoisted_mac_sum, strategy "normal" (reference
+ * operators/linear/operator.py:320-330, operators/transform.py:108-116):
+ * sum_g rot(giant)^g (sum_b pt[g B + b] * baby_b); babies as returned by
+ * ckks_hoisted_rotate for the baby offsets; result unrescaled. */
+int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
+                         const ckks_ct *const *pts, int64_t giant_rotation,
+                         int giant_count, ckks_ct **out);
+
+/* Raw polynomial transforms over host buffers [n_polys][limbs][N] with limb i
+ * in prime i (i < q_limbs) or special prime i - q_limbs (parity tests). */
+int ckks_poly_ntt(ckks_context *ctx, const uint64_t *in, uint64_t *out,
+                  int n_polys, int limbs, int q_limbs, int inverse);
+/* ModUp / ModDown of host buffers (parity of the key-switch stages). */
+int ckks_poly_modup(ckks_context *ctx, const uint64_t *d, int limbs, uint64_t *ext);
+int ckks_poly_moddown(ckks_context *ctx, const uint64_t *acc, int limbs, uint64_t *out);
+/* NTT (inverse = 0) or iNTT (inverse = 1) in place over all polynomials of n
+ * resident ciphertexts: the kernel pair that bench.py times. */
+int ckks_ntt_many(ckks_context *ctx, ckks_ct *const *cts, int n, int inverse);
+
+/* Device events on the context stream (reference easyfhe.cuda.Event,
+ * operators/linear/operator.py:273-291). */
+int ckks_event_create(ckks_context *ctx, ckks_event **out);
+int ckks_event_record(ckks_event *ev);
+int ckks_event_elapsed_ms(ckks_event *start, ckks_event *end, float *ms);
+void ckks_event_destroy(ckks_event *ev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

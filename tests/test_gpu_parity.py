@@ -1,0 +1,347 @@
+"""Bit-exact parity of the gfx950 library with the CPU oracle.
+
+Every test drives the library through the C ABI (via the ``easyfhe`` binding)
+and compares ciphertext / key / polynomial limbs with the oracle on the same
+parameters, seeds and inputs.  Integer results must be identical; decrypted
+values are compared with the fp64 expectation at the tolerance stated in
+each test.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import PARAMS, device_context, oracle_context
+
+pytestmark = pytest.mark.gpu
+
+
+def _fhe():
+    from easyfhe import fhe
+
+    return fhe
+
+
+def _rand_poly(rng, primes, shape_limbs, N, q_limbs=None):
+    """Random residues, limb l drawn below the prime of limb l."""
+    out = np.zeros((shape_limbs, N), dtype=np.uint64)
+    for l in range(shape_limbs):
+        out[l] = rng.integers(0, int(primes[l]), N, dtype=np.uint64)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# context: primes, secret, NTT
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", ["small", "matvec", "keyswitch"])
+def test_context_parity(name):
+    client, ctx = device_context(name, relin=False)
+    orc = oracle_context(name)
+    assert np.array_equal(ctx.primes(), orc.primes)
+    assert np.array_equal(ctx.secret(), orc.secret())
+    assert ctx.L == orc.L and ctx.alpha == orc.alpha
+
+
+@pytest.mark.parametrize("log_n", [10, 11, 12, 13, 14, 15, 16])
+def test_ntt_parity(log_n):
+    from easyfhe import _native
+
+    p = dict(log_n=log_n, depth=3, dnum=2, dcrt_bits=40, first_mod=60, special_bits=60)
+    client, ctx = device_context(p, relin=False)
+    orc = oracle_context(p)
+    rng = np.random.default_rng(log_n)
+    primes = orc.primes
+    L, A, N = orc.L, orc.alpha, orc.N
+    # Q limbs then the special limbs (extended basis), 3 polynomials
+    order = [primes[i] for i in range(L)] + [primes[L + j] for j in range(A)]
+    a = np.stack([_rand_poly(rng, order, L + A, N) for _ in range(3)])
+    # edge values: zeros, ones, q - 1
+    a[0, :, :4] = 0
+    a[0, :, 4:8] = 1
+    for l in range(L + A):
+        a[1, l, :8] = order[l] - 1
+    fwd = np.zeros_like(a)
+    _native.check(_native.lib.ckks_poly_ntt(ctx.handle, a.ctypes.data_as(_native.U64P),
+                                            fwd.ctypes.data_as(_native.U64P), 3, L + A, L, 0))
+    exp = np.stack([orc.ntt_limbs(a[i], q_limbs=L) for i in range(3)])
+    assert np.array_equal(fwd, exp)
+    inv = np.zeros_like(a)
+    _native.check(_native.lib.ckks_poly_ntt(ctx.handle, fwd.ctypes.data_as(_native.U64P),
+                                            inv.ctypes.data_as(_native.U64P), 3, L + A, L, 1))
+    assert np.array_equal(inv, a)
+
+
+# ---------------------------------------------------------------------------
+# encryption, keys, key-switch stages
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_encrypt_decrypt_parity(name):
+    fhe = _fhe()
+    client, ctx = device_context(name, relin=False)
+    orc = oracle_context(name)
+    rng = np.random.default_rng(1)
+    slots = ctx.max_slots
+    z = rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots)
+    for limbs in (ctx.L, 2):
+        ct = client.encrypt(z, slots=slots, cur_limbs=limbs, scaling_factor=2.0**40, enc_id=5)
+        ref = orc.encrypt(z, slots=slots, scale=2.0**40, limbs=limbs, enc_id=5)
+        assert np.array_equal(ct.download(), ref)
+        dec = client.decrypt_complex(ct)
+        # fresh-encryption error: sigma ~ 3.2 per coefficient, well below 1e-7
+        assert np.abs(dec - z).max() < 1e-7
+        assert np.abs(dec - orc.decrypt(ref, slots=slots, scale=2.0**40)).max() < 1e-12
+    # sparse slot packing
+    zs = z[:64]
+    ct = client.encrypt(zs, slots=64, cur_limbs=ctx.L, scaling_factor=2.0**40, enc_id=9)
+    ref = orc.encrypt(zs, slots=64, scale=2.0**40, limbs=ctx.L, enc_id=9)
+    assert np.array_equal(ct.download(), ref)
+    assert np.abs(client.decrypt_complex(ct) - zs).max() < 1e-7
+
+
+def test_encode_parity_large_scale():
+    """Encoder integer path for |coefficients| >= 2^63 (scale 2^80)."""
+    fhe = _fhe()
+    client, ctx = device_context("small", relin=False)
+    orc = oracle_context("small")
+    rng = np.random.default_rng(2)
+    z = rng.uniform(-1, 1, (3, ctx.max_slots))
+    pts = fhe.encode_rows(ctx, z, limbs=ctx.L, scale=2.0**80, slots=ctx.max_slots, is_ext=True)
+    for r in range(3):
+        ref = orc.encode(z[r], slots=ctx.max_slots, scale=2.0**80, limbs=ctx.L, is_ext=True)
+        assert np.array_equal(pts[r].download()[0], ref)
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_key_parity(name):
+    client, ctx = device_context(name, rotations=(1, -3))
+    orc = oracle_context(name)
+    orc.gen_relin_key()
+    assert np.array_equal(ctx.download_key(0), orc.get_key(0))
+    for r in (1, -3):
+        g = orc.galois_elt(r)
+        assert g == ctx.galois_element(r)
+        orc.gen_rotation_key(g)
+        assert np.array_equal(ctx.download_key(g), orc.get_key(g))
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_modup_moddown_parity(name):
+    from easyfhe import _native
+
+    client, ctx = device_context(name, relin=False)
+    orc = oracle_context(name)
+    rng = np.random.default_rng(3)
+    for limbs in (ctx.L, ctx.L - 1, 1):
+        d = _rand_poly(rng, orc.primes, limbs, orc.N)
+        digits = -(-limbs // orc.ds)
+        ext = np.zeros((digits, limbs + orc.alpha, orc.N), dtype=np.uint64)
+        _native.check(_native.lib.ckks_poly_modup(ctx.handle, d.ctypes.data_as(_native.U64P),
+                                                  limbs, ext.ctypes.data_as(_native.U64P)))
+        assert np.array_equal(ext, orc.modup(d))
+        order = [orc.primes[i] for i in range(limbs)] + [orc.primes[orc.L + j]
+                                                         for j in range(orc.alpha)]
+        acc = _rand_poly(rng, order, limbs + orc.alpha, orc.N)
+        out = np.zeros((limbs, orc.N), dtype=np.uint64)
+        _native.check(_native.lib.ckks_poly_moddown(ctx.handle, acc.ctypes.data_as(_native.U64P),
+                                                    limbs, out.ctypes.data_as(_native.U64P)))
+        assert np.array_equal(out, orc.moddown(acc))
+
+
+# ---------------------------------------------------------------------------
+# evaluation operations
+# ---------------------------------------------------------------------------
+
+
+def _pair(name, rotations=()):
+    client, ctx = device_context(name, rotations=rotations)
+    orc = oracle_context(name)
+    orc.gen_relin_key()
+    for r in rotations:
+        orc.gen_rotation_key(orc.galois_elt(r))
+    return client, ctx, orc
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_rotation_parity(name):
+    fhe = _fhe()
+    rots = (1, 2, -1, 5)
+    client, ctx, orc = _pair(name, rotations=rots + (2 * (2 ** PARAMS[name]["log_n"]) - 1,))
+    rng = np.random.default_rng(4)
+    slots = ctx.max_slots
+    z = rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots)
+    for limbs in (ctx.L, 2):
+        ct = client.encrypt(z, slots=slots, cur_limbs=limbs, scaling_factor=2.0**40, enc_id=11)
+        ref = orc.encrypt(z, slots=slots, scale=2.0**40, limbs=limbs, enc_id=11)
+        for r in rots:
+            out = fhe.homo_rotate(ct, r, ctx)
+            exp = orc.rotate_g(ref, orc.galois_elt(r))
+            assert np.array_equal(out.download(), exp), (limbs, r)
+            # rotation semantics: np.roll(z, -r); key-switch noise stays below 1e-6
+            assert np.abs(client.decrypt_complex(out) - np.roll(z, -r)).max() < 1e-6
+        conj = fhe.homo_rotate(ct, ctx.M - 1, ctx)
+        assert np.array_equal(conj.download(), orc.rotate_g(ref, ctx.M - 1))
+        assert np.abs(client.decrypt_complex(conj) - np.conj(z)).max() < 1e-6
+        # hoisted: one ModUp, several rotations (0 is the identity)
+        hs = fhe.prepare_hoisted_baby_rotations(ct, [0, 1, 2, 5], ctx)
+        hexp = orc.hoisted_rotate(ref, [orc.galois_elt(r) for r in (0, 1, 2, 5)])
+        for i in range(4):
+            assert np.array_equal(hs[i].download(), hexp[i])
+        # batched rotation of several ciphertexts with one key stream
+        many = fhe.homo_rotate_many([ct, ct, ct], 2, ctx)
+        for m in many:
+            assert np.array_equal(m.download(), orc.rotate_g(ref, orc.galois_elt(2)))
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_mul_relin_rescale_parity(name):
+    fhe = _fhe()
+    client, ctx, orc = _pair(name)
+    rng = np.random.default_rng(5)
+    slots = ctx.max_slots
+    x = rng.uniform(-1, 1, slots)
+    y = rng.uniform(-1, 1, slots)
+    a = client.encrypt(x, slots=slots, enc_id=21)
+    b = client.encrypt(y, slots=slots, enc_id=22)
+    ra = orc.encrypt(x, slots=slots, scale=ctx.scale_at(ctx.L), limbs=ctx.L, enc_id=21)
+    rb = orc.encrypt(y, slots=slots, scale=ctx.scale_at(ctx.L), limbs=ctx.L, enc_id=22)
+    t = fhe.homo_mul_no_relin(a, b, ctx)
+    rt = orc.tensor(ra, rb)
+    assert np.array_equal(t.download(), rt)
+    rl = fhe.homo_relinearize(t, ctx)
+    rrl = orc.relinearize(rt)
+    assert np.array_equal(rl.download(), rrl)
+    rs = fhe.rescale(rl, ctx)
+    rrs = orc.rescale(rrl)
+    assert np.array_equal(rs.download(), rrs)
+    assert rs.state.cur_limbs == ctx.L - 1
+    # x*y after one rescale: error budget 1e-6 (key switch + rescale rounding)
+    assert np.abs(client.decrypt(rs) - x * y).max() < 1e-6
+    # batched form gives identical limbs
+    many = fhe.homo_mul_relin_rescale_many([a, a], [b, b], ctx)
+    for m in many:
+        assert np.array_equal(m.download(), rrs)
+    # rescale of a degree-2 ciphertext (tensor) as well
+    assert np.array_equal(fhe.rescale(t, ctx).download(), orc.rescale(rt))
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_elementwise_parity(name):
+    fhe = _fhe()
+    client, ctx, orc = _pair(name)
+    rng = np.random.default_rng(6)
+    slots = ctx.max_slots
+    x = rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots)
+    y = rng.uniform(-1, 1, slots)
+    a = client.encrypt(x, slots=slots, enc_id=31)
+    b = client.encrypt(y, slots=slots, enc_id=32)
+    sc = ctx.scale_at(ctx.L)
+    ra = orc.encrypt(x, slots=slots, scale=sc, limbs=ctx.L, enc_id=31)
+    rb = orc.encrypt(y, slots=slots, scale=sc, limbs=ctx.L, enc_id=32)
+    assert np.array_equal(fhe.homo_add(a, b, ctx).download(), orc.add(ra, rb))
+    assert np.array_equal(fhe.homo_sub(a, b, ctx).download(), orc.sub(ra, rb))
+    for neg in (False, True):
+        mi = fhe.homo_mul_i(a, ctx, negative=neg)
+        assert np.array_equal(mi.download(), orc.mul_i(ra, negative=neg))
+        want = (-1j if neg else 1j) * x
+        assert np.abs(client.decrypt_complex(mi) - want).max() < 1e-7
+    pt = fhe.encode_rows(ctx, y, limbs=ctx.L, scale=sc, slots=slots)[0]
+    rpt = orc.encode(y, slots=slots, scale=sc, limbs=ctx.L)
+    assert np.array_equal(pt.download()[0], rpt)
+    mp = fhe.homo_mul_pt(a, pt, ctx)
+    assert np.array_equal(mp.download(), orc.mul_pt(ra, rpt))
+    mp_r = fhe.rescale(mp, ctx)
+    assert np.abs(client.decrypt_complex(mp_r) - x * y).max() < 1e-6
+    # scalar constants: add 0.25, multiply by -1.5 (then rescale)
+    s_add = fhe.encode_scalar(0.25, cur_limbs=ctx.L, scaling_factor=sc, context=ctx)
+    s_mul = fhe.encode_scalar(-1.5, cur_limbs=ctx.L, scaling_factor=sc, context=ctx)
+    assert np.abs(client.decrypt_complex(fhe.homo_add_scalar(a, s_add, ctx)) - (x + 0.25)).max() < 1e-7
+    prod = fhe.homo_mul_scalar_rescale(a, s_mul, ctx)
+    assert np.abs(client.decrypt_complex(prod) - (-1.5 * x)).max() < 1e-6
+    dropped = fhe.align_to(a, a.state.replace(cur_limbs=2), ctx)
+    assert np.array_equal(dropped.download(), ra[:, :2])
+
+
+# ---------------------------------------------------------------------------
+# BSGS diagonal matvec (feature-major token-lane packing)
+# ---------------------------------------------------------------------------
+
+
+def _diagonals(W, *, slots, lanes, baby, giant_base, giant_count):
+    """row(g, b)[slot] = W[(slot // lanes - g B) mod D, (slot // lanes + b) mod D]
+    (the diagonal layout of reference operators/linear/weight.py:27-43)."""
+    D = W.shape[0]
+    feat = np.arange(slots) // lanes
+    rows = []
+    for gr in range(giant_count):
+        g = giant_base + gr
+        out_f = (feat - g * baby) % D
+        for b in range(baby):
+            rows.append(W[out_f, (feat + b) % D])
+    return np.stack(rows)
+
+
+def test_bsgs_matvec_parity():
+    """Matvec workload: N = 2^13, 4096 slots, 4 x 40-bit limbs + 1 special,
+    scale 2^40, W and x uniform[-1, 1] from seed 0, B = 16, G = 8, lanes 32."""
+    fhe = _fhe()
+    D, lanes, B, G = 128, 32, 16, 8
+    rots = tuple(lanes * b for b in range(1, B)) + (B * lanes,)
+    client, ctx, orc = _pair("matvec", rotations=rots)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    sc = ctx.scale_at(ctx.L)
+    ct = client.encrypt(packed, slots=slots, enc_id=41)
+    ref = orc.encrypt(packed, slots=slots, scale=sc, limbs=ctx.L, enc_id=41)
+    rows = _diagonals(W, slots=slots, lanes=lanes, baby=B, giant_base=0, giant_count=G)
+    pts = fhe.encode_rows(ctx, rows, limbs=ctx.L, scale=sc, slots=slots)
+    rpts = np.stack([orc.encode(r, slots=slots, scale=sc, limbs=ctx.L) for r in rows])
+    for i in range(len(rows)):
+        assert np.array_equal(pts[i].download()[0], rpts[i])
+    offsets = [lanes * b for b in range(B)]
+    acc = fhe.hoisted_mac_sum(ct, offsets, pts, B * lanes, G, ctx)
+    racc = orc.hoisted_mac_sum(ref, [orc.galois_elt(o) for o in offsets], rpts,
+                               orc.galois_elt(B * lanes), G)
+    assert np.array_equal(acc.download(), racc)
+    out = fhe.rescale(acc, ctx)
+    dec = client.decrypt(out)[np.arange(D) * lanes]
+    # fp64 W @ x; measured error ~1e-7 (128 products at scale 2^40)
+    assert np.abs(dec - W @ x).max() < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# keyswitch workload size (N = 2^16, 36 + 12 limbs, dnum 3)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.slow
+def test_keyswitch_size_parity():
+    fhe = _fhe()
+    rots = (1, 1 << 14)
+    client, ctx, orc = _pair("keyswitch", rotations=rots)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    zs = [rng.uniform(-1, 1, slots) for _ in range(2)]
+    cts = [client.encrypt(z, slots=slots, enc_id=100 + i) for i, z in enumerate(zs)]
+    refs = [orc.encrypt(z, slots=slots, scale=ctx.scale_at(ctx.L), limbs=ctx.L, enc_id=100 + i)
+            for i, z in enumerate(zs)]
+    for i in range(2):
+        assert np.array_equal(cts[i].download(), refs[i])
+    for r in rots:
+        outs = fhe.homo_rotate_many(cts, r, ctx)
+        for i in range(2):
+            assert np.array_equal(outs[i].download(), orc.rotate_g(refs[i], orc.galois_elt(r)))
+            assert np.abs(client.decrypt(outs[i]) - np.roll(zs[i], -r)).max() < 1e-6
+    prods = fhe.homo_mul_relin_rescale_many(cts, cts, ctx)
+    for i in range(2):
+        exp = orc.rescale(orc.relinearize(orc.tensor(refs[i], refs[i])))
+        assert np.array_equal(prods[i].download(), exp)
+        assert np.abs(client.decrypt(prods[i]) - zs[i] ** 2).max() < 1e-6
