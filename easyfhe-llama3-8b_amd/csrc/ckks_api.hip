@@ -529,6 +529,32 @@ static void build_context(ckks_context *c, const ckks_params &p) {
     HIPCHECK(hipMalloc(dst, sizeof(u64) * v.size()));
     HIPCHECK(hipMemcpy(*dst, v.data(), sizeof(u64) * v.size(), hipMemcpyHostToDevice));
   };
+  // fp64 tables for primes below 2^45 (exact doubles; w / q correctly rounded)
+  c->prime_fp.assign(K, 0);
+  for (int pi = 0; pi < K; pi++) c->prime_fp[pi] = c->primes[pi] < ((u64)1 << 45) ? 1 : 0;
+  {
+    std::vector<double> tw(2 * (size_t)K * N, 0.0), itw(2 * (size_t)K * N, 0.0), nv(2 * (size_t)K, 0.0);
+    for (int pi = 0; pi < K; pi++) {
+      if (!c->prime_fp[pi]) continue;
+      const double q = (double)c->primes[pi];
+      for (int i = 0; i < N; i++) {
+        const size_t o = (size_t)pi * N + i;
+        tw[2 * o] = (double)psi[o];
+        tw[2 * o + 1] = (double)psi[o] / q;
+        itw[2 * o] = (double)ipsi[o];
+        itw[2 * o + 1] = (double)ipsi[o] / q;
+      }
+      nv[2 * pi] = (double)ninv[2 * pi];
+      nv[2 * pi + 1] = (double)ninv[2 * pi] / q;
+    }
+    auto upd = [&](double **dst, const std::vector<double> &v) {
+      HIPCHECK(hipMalloc(dst, sizeof(double) * v.size()));
+      HIPCHECK(hipMemcpy(*dst, v.data(), sizeof(double) * v.size(), hipMemcpyHostToDevice));
+    };
+    upd(&c->d_tw_fp, tw);
+    upd(&c->d_itw_fp, itw);
+    upd(&c->d_ninv_fp, nv);
+  }
   up(&c->d_psi, psi);
   up(&c->d_psi_sh, psi_sh);
   up(&c->d_ipsi, ipsi);

@@ -172,6 +172,10 @@ struct ckks_context {
   std::vector<ckks::ModQ> h_mods;
   u64 *d_psi, *d_psi_sh, *d_ipsi, *d_ipsi_sh;  // [K][N] each
   u64 *d_ninv;                                 // [K][2] value, shoup
+  // fp64 path for primes below 2^45 (prime_fp[p] != 0): per prime [N][2]
+  // doubles (w, w / q) of psi_br and psi_br^-1, and [K][2] (N^-1, N^-1 / q)
+  std::vector<int> prime_fp;
+  double *d_tw_fp = nullptr, *d_itw_fp = nullptr, *d_ninv_fp = nullptr;
   u64 *d_secret;                               // [K][N] NTT domain
   std::map<u64, ckks::DeviceKey> keys;          // galois -> key (0 = relin)
   std::map<std::pair<int, int>, ckks::BCTable> bc_up;  // (limbs, digit)

@@ -216,6 +216,550 @@ __global__ __launch_bounds__(TPB) void k_ntt_inv_high(Batch dst, int logN, int l
   }
 }
 
+// ===========================================================================
+// N = 2^16: register-resident radix-16 passes.  Each pass covers 8 bit
+// positions as two rounds of 4 stages held in 16 registers per thread, with
+// one LDS exchange between the rounds.  Butterflies are Harvey's lazy ones
+// (forward values in [0, 4q), inverse values in [0, 2q)); only the last pass
+// reduces to [0, q), so pass-to-pass data in HBM may be lazy.
+// LDS layout: element (r, c) of a 16 x 256 tile at r * 272 + c + (c >> 4):
+// the +1 per 16 keeps 16-apart columns in distinct banks.
+// ===========================================================================
+
+__device__ __forceinline__ u64 shoup_lazy(u64 a, u64 w, u64 ws, u64 q) {
+  return a * w - __umul64hi(a, ws) * q;  // in [0, 2q) for any a < 2^64
+}
+
+// Cooley-Tukey: X, Y in [0, 4q) -> X + wY, X - wY in [0, 4q)
+__device__ __forceinline__ void ct_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u64 q2) {
+  const u64 x = X >= q2 ? X - q2 : X;
+  const u64 t = shoup_lazy(Y, w, ws, q);
+  X = x + t;
+  Y = x - t + q2;
+}
+
+// Gentleman-Sande: X, Y in [0, 2q) -> X + Y, (X - Y) w in [0, 2q)
+__device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u64 q2) {
+  u64 sum = X + Y;
+  sum = sum >= q2 ? sum - q2 : sum;
+  const u64 d = X - Y + q2;
+  X = sum;
+  Y = shoup_lazy(d, w, ws, q);
+}
+
+__device__ __forceinline__ int lds16(int r, int c) { return r * 272 + c + (c >> 4); }
+
+// forward, bit positions 15..8: tile = 256 rows (stride 256) x 16 columns
+__global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, int l_begin,
+                                                        int q_limbs, int L,
+                                                        const ModQ *__restrict__ mods,
+                                                        const u64 *__restrict__ psi,
+                                                        const u64 *__restrict__ psi_sh) {
+  __shared__ u64 sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q, q2 = 2 * q;
+  const u64 *W = psi + ((size_t)p << 16);
+  const u64 *Ws = psi_sh + ((size_t)p << 16);
+  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16);
+  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int col = blockIdx.x * 16 + c;
+  u64 x[16];
+  // round A: row = g + 16 k, stages on row bits 7..4 (k bits 3..0)
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = in[(g + 16 * k) * 256 + col];
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (1 << st) + (k >> (4 - st));
+      ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+  // row = g + 16 k lives at LDS tile row g, "column" 16 k + c
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(g, 16 * k + c)] = x[k];
+  __syncthreads();
+  // round B: row = 16 g + j, stages on row bits 3..0
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(j, 16 * g + c)];
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int half = 8 >> (st - 4);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const int ti = (1 << st) + ((16 * g + j) >> (8 - st));
+      ct_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = x[j];
+}
+
+// forward, bit positions 7..0: tile = 16 contiguous rows of 256; output in [0, q)
+__global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, int q_limbs,
+                                                       int L, const ModQ *__restrict__ mods,
+                                                       const u64 *__restrict__ psi,
+                                                       const u64 *__restrict__ psi_sh) {
+  __shared__ u64 sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q, q2 = 2 * q;
+  const u64 *W = psi + ((size_t)p << 16);
+  const u64 *Ws = psi_sh + ((size_t)p << 16);
+  u64 *base = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = blockIdx.x * 16 + rl;  // global row of 256
+  u64 x[16];
+  // round A: column = c0 + 16 k, stages on column bits 7..4
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = base[rl * 256 + c0 + 16 * k];
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 7 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1));
+      ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
+  __syncthreads();
+  // round B: column = 16 c0 + j, stages on column bits 3..0
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int b = 7 - st, half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1));
+      ct_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+  // store through LDS so that adjacent lanes write adjacent words
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    u64 a = x[j] >= q2 ? x[j] - q2 : x[j];
+    sm[lds16(rl, 16 * c0 + j)] = a >= q ? a - q : a;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
+}
+
+// inverse, bit positions 0..7 (first pass): input in [0, 2q), output lazy
+__global__ __launch_bounds__(TPB) void k_ntt16_inv_low(Batch src, Batch dst, int l_begin,
+                                                       int q_limbs, int L,
+                                                       const ModQ *__restrict__ mods,
+                                                       const u64 *__restrict__ ipsi,
+                                                       const u64 *__restrict__ ipsi_sh) {
+  __shared__ u64 sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q, q2 = 2 * q;
+  const u64 *W = ipsi + ((size_t)p << 16);
+  const u64 *Ws = ipsi_sh + ((size_t)p << 16);
+  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = blockIdx.x * 16 + rl;
+  u64 x[16];
+  // round A: column = 16 c0 + j, stages on column bits 0..3; the load goes
+  // through LDS so that adjacent lanes read adjacent words
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = in[rl * 256 + c0 + 16 * k];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const int half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1));
+      gs_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
+  __syncthreads();
+  // round B: column = c0 + 16 k, stages on column bits 4..7
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
+#pragma unroll
+  for (int b = 4; b < 8; b++) {
+    const int half = 1 << (b - 4);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1));
+      gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = x[k];
+}
+
+// inverse, bit positions 8..15 (second pass), then x N^-1, output in [0, q)
+__global__ __launch_bounds__(TPB) void k_ntt16_inv_high(Batch dst, int l_begin, int q_limbs,
+                                                        int L, const ModQ *__restrict__ mods,
+                                                        const u64 *__restrict__ ipsi,
+                                                        const u64 *__restrict__ ipsi_sh,
+                                                        const u64 *__restrict__ ninv) {
+  __shared__ u64 sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 q = mods[p].q, q2 = 2 * q;
+  const u64 *W = ipsi + ((size_t)p << 16);
+  const u64 *Ws = ipsi_sh + ((size_t)p << 16);
+  u64 *io = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int col = blockIdx.x * 16 + c;
+  u64 x[16];
+  // round A: row = 16 g + j, stages on row bits 0..3 (st = 7..4)
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = io[(16 * g + j) * 256 + col];
+#pragma unroll
+  for (int st = 7; st >= 4; st--) {
+    const int half = 8 >> (st - 4);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const int ti = (1 << st) + ((16 * g + j) >> (8 - st));
+      gs_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) sm[lds16(j, 16 * g + c)] = x[j];
+  __syncthreads();
+  // round B: row = g + 16 k, stages on row bits 4..7 (st = 3..0)
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(g, 16 * k + c)];
+#pragma unroll
+  for (int st = 3; st >= 0; st--) {
+    const int half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (1 << st) + (k >> (4 - st));
+      gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+  const u64 ni = ninv[2 * p], nis = ninv[2 * p + 1];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    u64 v = shoup_lazy(x[k], ni, nis, q);
+    io[(g + 16 * k) * 256 + col] = v >= q ? v - q : v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp64 variant for primes q < 2^45: residues travel as signed doubles (exact
+// integers) and every modular product is
+//   hi = a w, lo = fma(a, w, -hi)             (a w = hi + lo exactly)
+//   t  = round(a (w / q)), r = fma(-t, q, hi) + lo   in [-q, q], exact
+// which needs |a| < 2^50; forward butterflies then need no reduction over
+// all 16 stages (|x| <= 17 q < 2^50), inverse ones reduce every 4 stages.
+// Between the two passes the data is stored as raw double bits.
+// ---------------------------------------------------------------------------
+
+#define FP_ROUND_C 6755399441055744.0  // 1.5 * 2^52: (y + C) - C rounds |y| < 2^51
+
+__device__ __forceinline__ double fp_rint(double y) {
+  return __dsub_rn(__dadd_rn(y, FP_ROUND_C), FP_ROUND_C);
+}
+
+__device__ __forceinline__ double fp_mulmod(double a, double w, double wq, double q) {
+  const double hi = __dmul_rn(a, w);
+  const double lo = __fma_rn(a, w, -hi);
+  const double t = fp_rint(__dmul_rn(a, wq));
+  return __dadd_rn(__fma_rn(-t, q, hi), lo);
+}
+
+// x -> x - round(x / q) q in [-q/2 - 1, q/2 + 1]
+__device__ __forceinline__ double fp_reduce(double x, double qinv, double q) {
+  return __fma_rn(-fp_rint(__dmul_rn(x, qinv)), q, x);
+}
+
+__device__ __forceinline__ u64 fp_canon(double x, double qinv, double q) {
+  double r = fp_reduce(x, qinv, q);
+  r = r < 0.0 ? __dadd_rn(r, q) : r;
+  return (u64)r;
+}
+
+__device__ __forceinline__ void ct_fp(double &X, double &Y, double w, double wq, double q) {
+  const double t = fp_mulmod(Y, w, wq, q);
+  const double x = X;
+  X = __dadd_rn(x, t);
+  Y = __dsub_rn(x, t);
+}
+
+__device__ __forceinline__ void gs_fp(double &X, double &Y, double w, double wq, double q) {
+  const double x = X, y = Y;
+  X = __dadd_rn(x, y);
+  Y = fp_mulmod(__dsub_rn(x, y), w, wq, q);
+}
+
+__device__ __forceinline__ double as_dbl(u64 v) { return __longlong_as_double((long long)v); }
+__device__ __forceinline__ u64 dbl_bits(double v) { return (u64)__double_as_longlong(v); }
+
+// Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
+__global__ __launch_bounds__(TPB) void k_ntt16f_fwd_high(Batch src, Batch dst, int l_begin,
+                                                         int q_limbs, int L,
+                                                         const ModQ *__restrict__ mods,
+                                                         const double2 *__restrict__ tw) {
+  __shared__ double sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const double q = (double)mods[p].q;
+  const double2 *T = tw + ((size_t)p << 16);
+  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16);
+  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int col = blockIdx.x * 16 + c;
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = (double)in[(g + 16 * k) * 256 + col];
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(1 << st) + (k >> (4 - st))];
+      ct_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(g, 16 * k + c)] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(j, 16 * g + c)];
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int half = 8 >> (st - 4);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const double2 w = T[(1 << st) + ((16 * g + j) >> (8 - st))];
+      ct_fp(x[j], x[j + half], w.x, w.y, q);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = dbl_bits(x[j]);
+}
+
+__global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, int q_limbs,
+                                                        int L, const ModQ *__restrict__ mods,
+                                                        const double2 *__restrict__ tw) {
+  __shared__ double sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const double2 *T = tw + ((size_t)p << 16);
+  u64 *base = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = blockIdx.x * 16 + rl;
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = as_dbl(base[rl * 256 + c0 + 16 * k]);
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 7 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1))];
+      ct_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int b = 7 - st, half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1))];
+      ct_fp(x[j], x[j + half], w.x, w.y, q);
+    }
+  }
+  __syncthreads();
+  u64 *smu = reinterpret_cast<u64 *>(sm);
+#pragma unroll
+  for (int j = 0; j < 16; j++) smu[lds16(rl, 16 * c0 + j)] = fp_canon(x[j], qinv, q);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = smu[lds16(rl, c0 + 16 * k)];
+}
+
+__global__ __launch_bounds__(TPB) void k_ntt16f_inv_low(Batch src, Batch dst, int l_begin,
+                                                        int q_limbs, int L,
+                                                        const ModQ *__restrict__ mods,
+                                                        const double2 *__restrict__ itw) {
+  __shared__ double sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const double2 *T = itw + ((size_t)p << 16);
+  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = blockIdx.x * 16 + rl;
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = (double)in[rl * 256 + c0 + 16 * k];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const int half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1))];
+      gs_fp(x[j], x[j + half], w.x, w.y, q);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[lds16(rl, c0 + 16 * k)], qinv, q);
+#pragma unroll
+  for (int b = 4; b < 8; b++) {
+    const int half = 1 << (b - 4);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1))];
+      gs_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = dbl_bits(x[k]);
+}
+
+__global__ __launch_bounds__(TPB) void k_ntt16f_inv_high(Batch dst, int l_begin, int q_limbs,
+                                                         int L, const ModQ *__restrict__ mods,
+                                                         const double2 *__restrict__ itw,
+                                                         const double2 *__restrict__ ninv) {
+  __shared__ double sm[16 * 272];
+  const int limb = l_begin + blockIdx.y;
+  const int p = prime_of(limb, q_limbs, L);
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const double2 *T = itw + ((size_t)p << 16);
+  u64 *io = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int col = blockIdx.x * 16 + c;
+  double x[16];
+#pragma unroll
+  for (int j = 0; j < 16; j++) x[j] = fp_reduce(as_dbl(io[(16 * g + j) * 256 + col]), qinv, q);
+#pragma unroll
+  for (int st = 7; st >= 4; st--) {
+    const int half = 8 >> (st - 4);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const double2 w = T[(1 << st) + ((16 * g + j) >> (8 - st))];
+      gs_fp(x[j], x[j + half], w.x, w.y, q);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) sm[lds16(j, 16 * g + c)] = x[j];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[lds16(g, 16 * k + c)], qinv, q);
+#pragma unroll
+  for (int st = 3; st >= 0; st--) {
+    const int half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(1 << st) + (k >> (4 - st))];
+      gs_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+  const double2 ni = ninv[p];
+#pragma unroll
+  for (int k = 0; k < 16; k++)
+    io[(g + 16 * k) * 256 + col] = fp_canon(fp_mulmod(x[k], ni.x, ni.y, q), qinv, q);
+}
+
+static void ntt16_launch(ckks_context *c, bool fp, const Batch &src, const Batch &dst,
+                         int n_items, int l_begin, int l_count, int q_limbs, bool inverse) {
+  dim3 block(TPB), grid(16, l_count, n_items);
+  if (fp) {
+    const double2 *tw = (const double2 *)(inverse ? c->d_itw_fp : c->d_tw_fp);
+    if (!inverse) {
+      hipLaunchKernelGGL(k_ntt16f_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                         c->L, c->d_mods, tw);
+      LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_ntt16f_fwd_low, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
+                         c->d_mods, tw);
+      LAUNCH_CHECK();
+    } else {
+      hipLaunchKernelGGL(k_ntt16f_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                         c->L, c->d_mods, tw);
+      LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_ntt16f_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs,
+                         c->L, c->d_mods, tw, (const double2 *)c->d_ninv_fp);
+      LAUNCH_CHECK();
+    }
+    return;
+  }
+  if (!inverse) {
+    hipLaunchKernelGGL(k_ntt16_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                       c->L, c->d_mods, c->d_psi, c->d_psi_sh);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_ntt16_fwd_low, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
+                       c->d_mods, c->d_psi, c->d_psi_sh);
+    LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL(k_ntt16_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                       c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_ntt16_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
+                       c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv);
+    LAUNCH_CHECK();
+  }
+}
+
+// Launch over maximal runs of limbs whose primes share one arithmetic path.
+static void ntt16_dispatch(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                           int l_begin, int l_count, int q_limbs, bool inverse) {
+  int start = l_begin;
+  const int end = l_begin + l_count;
+  while (start < end) {
+    auto is_fp = [&](int limb) {
+      const int p = limb < q_limbs ? limb : c->L + (limb - q_limbs);
+      return c->prime_fp[p] != 0;
+    };
+    const bool fp = is_fp(start);
+    int stop = start + 1;
+    while (stop < end && is_fp(stop) == fp) stop++;
+    ntt16_launch(c, fp, src, dst, n_items, start, stop - start, q_limbs, inverse);
+    start = stop;
+  }
+}
+
 template <int S1, int S2, int TILE>
 static void ntt_dispatch(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                          int l_begin, int l_count, int q_limbs, bool inverse) {
@@ -251,7 +795,7 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
     case 13: ntt_dispatch<6, 7, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     case 14: ntt_dispatch<7, 7, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     case 15: ntt_dispatch<7, 8, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
-    case 16: ntt_dispatch<8, 8, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
+    case 16: ntt16_dispatch(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     case 17: ntt_dispatch<8, 9, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     default: throw std::invalid_argument("log_n must be in [10, 17]");
   }
@@ -518,13 +1062,16 @@ __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch a
   const u64 a = acc.base[item * acc.stride + ((size_t)comp * E + l) * N + k];
   const u64 v = conv.base[item * conv.stride + ((size_t)comp * limbs + l) * N + k];
   u64 r = shoup_mul(sub_mod(a, v, q), pinv[2 * l], pinv[2 * l + 1], q);
-  const u64 *ad = batch_ptr(comp ? add1 : add0, item);
+  // select the pointer, not the argument struct: a selected struct is
+  // copied to per-thread scratch memory
+  const u64 *ad = comp ? batch_ptr(add1, item) : batch_ptr(add0, item);
   if (ad) {
     const u64 g = gal.g[item];
     const u32 kk = g == 1 ? (u32)k : autom_index((u32)k, g, logN);
     r = add_mod(r, ad[(size_t)l * N + kk], q);
   }
-  batch_ptr(comp ? out1 : out0, item)[(size_t)l * N + k] = r;
+  u64 *o = comp ? batch_ptr(out1, item) : batch_ptr(out0, item);
+  o[(size_t)l * N + k] = r;
 }
 
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,

@@ -45,11 +45,17 @@ def test_context_parity(name):
     assert ctx.L == orc.L and ctx.alpha == orc.alpha
 
 
-@pytest.mark.parametrize("log_n", [10, 11, 12, 13, 14, 15, 16])
-def test_ntt_parity(log_n):
+@pytest.mark.parametrize("log_n,first_mod,special_bits",
+                         [(10, 60, 60), (11, 60, 60), (12, 60, 60), (13, 60, 60), (14, 60, 60),
+                          (15, 60, 60), (16, 60, 60), (16, 40, 44), (16, 40, 60)])
+def test_ntt_parity(log_n, first_mod, special_bits):
+    """Both arithmetic paths at N = 2^16: 64-bit integer (primes >= 2^45) and
+    fp64 (primes < 2^45), mixed within one call, on Q and special limbs, with
+    edge values."""
     from easyfhe import _native
 
-    p = dict(log_n=log_n, depth=3, dnum=2, dcrt_bits=40, first_mod=60, special_bits=60)
+    p = dict(log_n=log_n, depth=3, dnum=2, dcrt_bits=40, first_mod=first_mod,
+             special_bits=special_bits)
     client, ctx = device_context(p, relin=False)
     orc = oracle_context(p)
     rng = np.random.default_rng(log_n)
