@@ -27,6 +27,10 @@ sys.path.insert(0, str(ROOT / "easyfhe-llama3-8b_amd"))
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes moved by one batch NTT transform per algorithmic byte (read + write
+# of each limb-polynomial once): two passes, FETCH_SIZE/WRITE_SIZE counter
+# runs calibrated against a device copy (profiles/ntt_batch_pmc_traffic.md)
+NTT_TRAFFIC_RATIO = 2.02
 # 12 special primes of 44 bits: P = 2^528 exceeds the largest digit (2^500) and
 # every limb but q_0 takes the fp64 modular-arithmetic path of the NTT
 PARAMS = dict(log_n=16, depth=35, dnum=3, dcrt_bits=40, first_mod=60, special_bits=44)
@@ -75,6 +79,9 @@ def main() -> int:
     ap.add_argument("--cts", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile"], default="keyswitch",
+                    help="ntt-profile: only the batch NTT and a 36 MiB device copy "
+                         "(the calibration kernel), for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the key-switch "
@@ -86,6 +93,8 @@ def main() -> int:
     spec = fhe.CKKSContextSpec(depth=PARAMS["depth"], log_n=PARAMS["log_n"], dnum=PARAMS["dnum"],
                                dcrt_bits=PARAMS["dcrt_bits"], first_mod=PARAMS["first_mod"],
                                special_bits=PARAMS["special_bits"], seed=0, rotations=ROTATIONS)
+    if args.mode == "ntt-profile":
+        return ntt_profile(spec, args.cts)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
     ctx.synchronize()
@@ -186,13 +195,14 @@ def main() -> int:
         "gpu_event_ms_per_step": round(gpu_ms / args.steps, 3),
         "keygen_s": round(keygen_s, 2),
         "roofline": {
-            "kernel": "ntt (k_ntt_fwd_high + k_ntt_fwd_low / k_ntt_inv_low + k_ntt_inv_high)",
+            "kernel": "batch NTT (k_ntt16f_* fp64 passes for 40-bit limbs, k_ntt16_* for the "
+                      "60-bit limb); mean of forward and inverse transform",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": round(ntt_bytes * NTT_TRAFFIC_RATIO),
             "launch_ms": round(ntt_ms, 4),
             "limb_polys_per_launch": limb_polys,
         },
@@ -200,6 +210,29 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def ntt_profile(spec, n_cts: int) -> int:
+    """Three forward+inverse batch NTTs over n_cts ciphertexts at 36 limbs,
+    then three device copies of one 36 MiB ciphertext."""
+    from easyfhe import _native, fhe
+
+    spec.rotations = ()
+    spec.relin_key = False
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    cts = [client.encrypt(rng.uniform(-1, 1, slots), slots=slots, enc_id=i + 1)
+           for i in range(n_cts)]
+    batch = fhe_ptrs(cts)
+    for _ in range(3):
+        _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 0))
+        _native.check(_native.lib.ckks_ntt_many(ctx.handle, batch, len(cts), 1))
+    copies = [cts[0].deep_copy() for _ in range(3)]
+    ctx.synchronize()
+    print(json.dumps({"ntt_limb_polys_per_call": len(cts) * 2 * ctx.L,
+                      "copy_bytes": 2 * ctx.L * ctx.N * 8, "copies": len(copies)}), flush=True)
     return 0
 
 

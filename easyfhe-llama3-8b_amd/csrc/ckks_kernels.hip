@@ -47,13 +47,13 @@ __global__ __launch_bounds__(TPB) void k_ntt_fwd_high(Batch src, Batch dst, int 
   constexpr int PER = TILE / TPB;
   __shared__ u64 s[TILE];
   const int N = 1 << logN;
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q;
   const u64 *W = psi + (size_t)p * N;
   const u64 *Ws = psi_sh + (size_t)p * N;
-  const u64 *in = batch_ptr(src, blockIdx.z) + (size_t)limb * N;
-  u64 *out = batch_ptr(dst, blockIdx.z) + (size_t)limb * N;
+  const u64 *in = batch_ptr(src, blockIdx.y) + (size_t)limb * N;
+  u64 *out = batch_ptr(dst, blockIdx.y) + (size_t)limb * N;
   const int stride = N >> S;
   const int col0 = blockIdx.x * C;
 #pragma unroll
@@ -96,12 +96,12 @@ __global__ __launch_bounds__(TPB) void k_ntt_fwd_low(Batch dst, int logN, int l_
   constexpr int PER = TILE / TPB;
   __shared__ u64 s[TILE];
   const int N = 1 << logN;
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q;
   const u64 *W = psi + (size_t)p * N;
   const u64 *Ws = psi_sh + (size_t)p * N;
-  u64 *base = batch_ptr(dst, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+  u64 *base = batch_ptr(dst, blockIdx.y) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
 #pragma unroll
   for (int k = 0; k < PER; k++) s[threadIdx.x + TPB * k] = base[threadIdx.x + TPB * k];
   __syncthreads();
@@ -136,13 +136,13 @@ __global__ __launch_bounds__(TPB) void k_ntt_inv_low(Batch src, Batch dst, int l
   constexpr int PER = TILE / TPB;
   __shared__ u64 s[TILE];
   const int N = 1 << logN;
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q;
   const u64 *W = ipsi + (size_t)p * N;
   const u64 *Ws = ipsi_sh + (size_t)p * N;
-  const u64 *in = batch_ptr(src, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
-  u64 *out = batch_ptr(dst, blockIdx.z) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+  const u64 *in = batch_ptr(src, blockIdx.y) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
+  u64 *out = batch_ptr(dst, blockIdx.y) + (size_t)limb * N + (size_t)blockIdx.x * TILE;
 #pragma unroll
   for (int k = 0; k < PER; k++) s[threadIdx.x + TPB * k] = in[threadIdx.x + TPB * k];
   __syncthreads();
@@ -178,12 +178,12 @@ __global__ __launch_bounds__(TPB) void k_ntt_inv_high(Batch dst, int logN, int l
   constexpr int PER = TILE / TPB;
   __shared__ u64 s[TILE];
   const int N = 1 << logN;
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q;
   const u64 *W = ipsi + (size_t)p * N;
   const u64 *Ws = ipsi_sh + (size_t)p * N;
-  u64 *io = batch_ptr(dst, blockIdx.z) + (size_t)limb * N;
+  u64 *io = batch_ptr(dst, blockIdx.y) + (size_t)limb * N;
   const int stride = N >> S;
   const int col0 = blockIdx.x * C;
 #pragma unroll
@@ -256,13 +256,13 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, in
                                                         const u64 *__restrict__ psi,
                                                         const u64 *__restrict__ psi_sh) {
   __shared__ u64 sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
   const u64 *W = psi + ((size_t)p << 16);
   const u64 *Ws = psi_sh + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16);
-  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
   const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
   const int col = blockIdx.x * 16 + c;
   u64 x[16];
@@ -306,12 +306,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, i
                                                        const u64 *__restrict__ psi,
                                                        const u64 *__restrict__ psi_sh) {
   __shared__ u64 sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
   const u64 *W = psi + ((size_t)p << 16);
   const u64 *Ws = psi_sh + ((size_t)p << 16);
-  u64 *base = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *base = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;  // global row of 256
   u64 x[16];
@@ -363,13 +363,13 @@ __global__ __launch_bounds__(TPB) void k_ntt16_inv_low(Batch src, Batch dst, int
                                                        const u64 *__restrict__ ipsi,
                                                        const u64 *__restrict__ ipsi_sh) {
   __shared__ u64 sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
   const u64 *W = ipsi + ((size_t)p << 16);
   const u64 *Ws = ipsi_sh + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
-  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
   u64 x[16];
@@ -418,12 +418,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16_inv_high(Batch dst, int l_begin, 
                                                         const u64 *__restrict__ ipsi_sh,
                                                         const u64 *__restrict__ ninv) {
   __shared__ u64 sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
   const u64 *W = ipsi + ((size_t)p << 16);
   const u64 *Ws = ipsi_sh + ((size_t)p << 16);
-  u64 *io = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
   const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
   const int col = blockIdx.x * 16 + c;
   u64 x[16];
@@ -520,12 +520,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_high(Batch src, Batch dst, i
                                                          const ModQ *__restrict__ mods,
                                                          const double2 *__restrict__ tw) {
   __shared__ double sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q;
   const double2 *T = tw + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16);
-  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
   const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
   const int col = blockIdx.x * 16 + c;
   double x[16];
@@ -564,11 +564,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, 
                                                         int L, const ModQ *__restrict__ mods,
                                                         const double2 *__restrict__ tw) {
   __shared__ double sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
   const double2 *T = tw + ((size_t)p << 16);
-  u64 *base = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *base = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
   double x[16];
@@ -613,12 +613,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_inv_low(Batch src, Batch dst, in
                                                         const ModQ *__restrict__ mods,
                                                         const double2 *__restrict__ itw) {
   __shared__ double sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
   const double2 *T = itw + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
-  u64 *out = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
   double x[16];
@@ -662,11 +662,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_inv_high(Batch dst, int l_begin,
                                                          const double2 *__restrict__ itw,
                                                          const double2 *__restrict__ ninv) {
   __shared__ double sm[16 * 272];
-  const int limb = l_begin + blockIdx.y;
+  const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
   const double2 *T = itw + ((size_t)p << 16);
-  u64 *io = batch_ptr(dst, blockIdx.z) + ((size_t)limb << 16);
+  u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
   const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
   const int col = blockIdx.x * 16 + c;
   double x[16];
@@ -705,7 +705,9 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_inv_high(Batch dst, int l_begin,
 
 static void ntt16_launch(ckks_context *c, bool fp, const Batch &src, const Batch &dst,
                          int n_items, int l_begin, int l_count, int q_limbs, bool inverse) {
-  dim3 block(TPB), grid(16, l_count, n_items);
+  // grid (tiles, items, limbs): blocks of one prime run back to back and
+  // share its twiddle table in L2
+  dim3 block(TPB), grid(16, n_items, l_count);
   if (fp) {
     const double2 *tw = (const double2 *)(inverse ? c->d_itw_fp : c->d_tw_fp);
     if (!inverse) {
@@ -765,8 +767,10 @@ static void ntt_dispatch(ckks_context *c, const Batch &src, const Batch &dst, in
                          int l_begin, int l_count, int q_limbs, bool inverse) {
   const int N = c->N;
   dim3 block(TPB);
-  dim3 g_high((N >> S1) / (TILE >> S1), l_count, n_items);
-  dim3 g_low(N / TILE, l_count, n_items);
+  // grid (tiles, items, limbs): blocks of one prime run back to back and
+  // share its twiddle table in L2
+  dim3 g_high((N >> S1) / (TILE >> S1), n_items, l_count);
+  dim3 g_low(N / TILE, n_items, l_count);
   if (!inverse) {
     hipLaunchKernelGGL((k_ntt_fwd_high<S1, TILE>), g_high, block, 0, c->stream, src, dst,
                        c->logN, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh);
