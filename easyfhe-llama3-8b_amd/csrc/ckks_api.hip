@@ -285,6 +285,9 @@ static void parallel_for(int n, F f) {
 
 static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::vector<u64> &dst) {
   const int ns = (int)src.size(), nd = (int)dst.size();
+  // the kernel stages the table in a fixed LDS array
+  require(ns <= kMaxDigitSize && 2 * ns + ns * nd + nd <= 2 * kMaxDigitSize + kMaxDigitSize * 48 + 48,
+          "basis conversion table exceeds the kernel's staging area (16 sources x 48 targets)");
   std::vector<u64> h(2 * ns + (size_t)ns * nd + nd);
   for (int t = 0; t < nd; t++) {
     u64 m = 1;

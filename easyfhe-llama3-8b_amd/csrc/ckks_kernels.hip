@@ -940,6 +940,12 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
                                                        int src_prime0, int t_split, int t_skip,
                                                        int q_limbs, int L, int centered,
                                                        const ModQ *__restrict__ mods) {
+  // the constant table (<= 2*16 + 16*48 + 48 words) is staged in LDS once per
+  // block; every lane then reads the same word (a broadcast)
+  __shared__ u64 st[2 * kMaxDigitSize + kMaxDigitSize * 48 + 48];
+  const int words = 2 * ns + ns * nd + nd;
+  for (int i = threadIdx.x; i < words; i += TPB) st[i] = tab[i];
+  __syncthreads();
   const int k = blockIdx.x * TPB + threadIdx.x;
   const u64 *in = batch_ptr(src, blockIdx.y);
   u64 *out = batch_ptr(dst, blockIdx.y);
@@ -949,13 +955,36 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
   for (int i = 0; i < kMaxDigitSize; i++) {
     if (i < ns) {
       const u64 qi = mods[src_prime0 + i].q;
-      v[i] = shoup_mul(in[((size_t)i << logN) + k], tab[i], tab[ns + i], qi);
+      v[i] = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
       cnt += (centered && v[i] > (qi - 1) / 2) ? 1 : 0;
     }
   }
-  const u64 *hm = tab + 2 * ns;
+  const u64 *hm = st + 2 * ns;
   const u64 *qm = hm + (size_t)ns * nd;
-  for (int t = 0; t < nd; t++) {
+  int t = 0;
+  for (; t + 1 < nd; t += 2) {
+    const int tl0 = t < t_split ? t : t + t_skip;
+    const int tl1 = t + 1 < t_split ? t + 1 : t + 1 + t_skip;
+    const ModQ M0 = mods[prime_of(tl0, q_limbs, L)];
+    const ModQ M1 = mods[prime_of(tl1, q_limbs, L)];
+    u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i++) {
+      if (i < ns) {
+        mac_wide(h0, l0, v[i], hm[i * nd + t]);
+        mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
+      }
+    }
+    u64 y0 = redc(h0, l0, M0.q, M0.qinv);
+    u64 y1 = redc(h1, l1, M1.q, M1.qinv);
+    if (cnt) {
+      y0 = sub_mod(y0, mul_mod(cnt, qm[t], M0), M0.q);
+      y1 = sub_mod(y1, mul_mod(cnt, qm[t + 1], M1), M1.q);
+    }
+    out[((size_t)tl0 << logN) + k] = y0;
+    out[((size_t)tl1 << logN) + k] = y1;
+  }
+  if (t < nd) {
     const int tl = t < t_split ? t : t + t_skip;
     const ModQ M = mods[prime_of(tl, q_limbs, L)];
     u64 hi = 0, lo = 0;
