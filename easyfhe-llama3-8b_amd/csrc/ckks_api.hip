@@ -1311,6 +1311,25 @@ int ckks_drop_limbs(ckks_context *c, const ckks_ct *a, int target, ckks_ct **out
   API_END
 }
 
+int ckks_mod_raise(ckks_context *c, const ckks_ct *a, int target_limbs, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "mod_raise");
+  require(out, "null argument");
+  require(a->limbs == 1 && !a->is_ext, "mod_raise expects a one-limb Q-basis ciphertext");
+  require(a->polys >= 1 && a->polys <= 3, "mod_raise expects 1 to 3 polynomials");
+  check_limbs(c, target_limbs);
+  const size_t N = c->N;
+  ckks_ct *o = new_ct(c, a->polys, target_limbs, 0, a->slots, a->scale, a->scale_degree);
+  Scratch s(c);
+  u64 *coef = s.get((size_t)a->polys * N);
+  launch_ntt(c, strided(a->d, N), strided(coef, N), a->polys, 0, 1, 1, true);
+  launch_mod_raise(c, coef, o->d, a->polys, target_limbs);
+  launch_ntt(c, strided(o->d, (size_t)target_limbs * N), strided(o->d, (size_t)target_limbs * N),
+             a->polys, 0, target_limbs, target_limbs, false);
+  *out = o;
+  API_END
+}
+
 int ckks_rotate_many(ckks_context *c, const ckks_ct *const *in, int n, int64_t rotation,
                      ckks_ct **out) {
   API_BEGIN

@@ -232,6 +232,7 @@ void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, i
                            int limbs);
 void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
                             const Batch &out, int n_items, int limbs, const u64 *consts);
+void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target);
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
                 int limbs);
 void launch_keygen(ckks_context *c, DeviceKey &key, u64 id, int relin, u64 galois);

@@ -1168,6 +1168,28 @@ void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
   LAUNCH_CHECK();
 }
 
+// ModRaise: coefficients of limb 0 (in [0, q_0)) read as integers in
+// (-q_0/2, q_0/2] and reduced into limb i.  grid (N / 256, target, polys)
+__global__ void k_mod_raise(const u64 *__restrict__ coef, u64 *__restrict__ out, int target,
+                            int logN, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int i = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  const ModQ M = mods[i];
+  const u64 q0 = mods[0].q;
+  const u64 v = coef[(size_t)blockIdx.z * N + k];
+  u64 r = barrett(0, v, M);
+  if (v > (q0 - 1) / 2) r = sub_mod(r, barrett(0, q0, M), M.q);
+  out[((size_t)blockIdx.z * target + i) * N + k] = r;
+}
+
+void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target) {
+  dim3 grid(c->N / TPB, target, polys);
+  hipLaunchKernelGGL(k_mod_raise, grid, dim3(TPB), 0, c->stream, coef, out, target, c->logN,
+                     c->d_mods);
+  LAUNCH_CHECK();
+}
+
 // ===========================================================================
 // BSGS inner sum: out[c][l] = sum_b baby_b[c][l] * pt_b[l]
 // Products are folded 16 at a time with REDC (16 q^2 < q 2^64) and the

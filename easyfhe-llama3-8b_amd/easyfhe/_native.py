@@ -105,6 +105,7 @@ SIGNATURES = {
     "ckks_rescale": (I, [VP, VP, VPP]),
     "ckks_drop_limbs": (I, [VP, VP, I, VPP]),
     "ckks_rotate": (I, [VP, VP, ctypes.c_int64, VPP]),
+    "ckks_mod_raise": (I, [VP, VP, I, VPP]),
     "ckks_rotate_many": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
     "ckks_mul_relin_rescale_many": (I, [VP, VPP, VPP, I, VPP]),
     "ckks_hoisted_rotate": (I, [VP, VP, I64P, I, VPP]),

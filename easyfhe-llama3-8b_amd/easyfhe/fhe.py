@@ -661,6 +661,14 @@ def homo_rotate(a, rotation: int, context=None):
     return _wrap(ctx, out)
 
 
+def mod_raise(a, target_limbs: int, context=None):
+    """One-limb ciphertext lifted to ``target_limbs`` limbs (bootstrap ModRaise)."""
+    ctx = _ctx(a, context)
+    out = ctypes.c_void_p()
+    check(lib.ckks_mod_raise(ctx.handle, a.handle, int(target_limbs), ctypes.byref(out)))
+    return _wrap(ctx, out)
+
+
 def homo_rotate_many(cts: Sequence[Ciphertext], rotation: int, context=None) -> list:
     """One rotation of many same-level ciphertexts; the key is streamed once."""
     cts = list(cts)

@@ -143,6 +143,11 @@ int ckks_mul_relin(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_c
  * operators/linear/operator.py:386, primitives.py:145). */
 int ckks_rescale(ckks_context *ctx, const ckks_ct *a, ckks_ct **out);
 int ckks_drop_limbs(ckks_context *ctx, const ckks_ct *a, int target_limbs, ckks_ct **out);
+/* Bootstrap ModRaise: a one-limb ciphertext (mod q_0) lifted with centered
+ * coefficients to target_limbs limbs; the plaintext becomes m + q_0 I
+ * (reference bs.bootstrap, operators/nonlinear/bootstrap.py:370, "modraise_first"
+ * mode, bootstrap.py:29). */
+int ckks_mod_raise(ckks_context *ctx, const ckks_ct *a, int target_limbs, ckks_ct **out);
 /* fhe.homo_rotate (reference operators/linear/operator.py:333,
  * operators/linear/complex.py:47). */
 int ckks_rotate(ckks_context *ctx, const ckks_ct *a, int64_t rotation, ckks_ct **out);

@@ -1238,6 +1238,30 @@ void orc_rescale(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,
   free(last);
 }
 
+/* ModRaise (bootstrap step 1): every polynomial of a one-limb ciphertext is
+ * read as integers in (-q_0/2, q_0/2] and reduced into `target` limbs. */
+void orc_mod_raise(const orc_ctx *c, const uint64_t *ct, int polys, int target,
+                   uint64_t *out) {
+  const int N = c->N;
+  const u64 q0 = c->primes[0];
+  u64 *coef = (u64 *)malloc(sizeof(u64) * N);
+  for (int d = 0; d < polys; d++) {
+    memcpy(coef, ct + (size_t)d * N, sizeof(u64) * N);
+    orc_ntt_inv(c, 0, coef);
+#pragma omp parallel for
+    for (int i = 0; i < target; i++) {
+      const u64 q = c->primes[i];
+      u64 *dst = out + ((size_t)d * target + i) * N;
+      for (int k = 0; k < N; k++) {
+        u64 v = coef[k];
+        dst[k] = v > (q0 - 1) / 2 ? submod(v % q, q0 % q, q) : v % q;
+      }
+      orc_ntt_fwd(c, i, dst);
+    }
+  }
+  free(coef);
+}
+
 void orc_drop_limbs(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,
                     int target, uint64_t *out) {
   const int N = c->N;

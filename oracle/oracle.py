@@ -87,6 +87,7 @@ def lib():
             "orc_hoisted_rotate": (i, [vp, _u64p, i, _u64p, i, _u64p]),
             "orc_rescale": (None, [vp, _u64p, i, i, _u64p]),
             "orc_drop_limbs": (None, [vp, _u64p, i, i, i, _u64p]),
+            "orc_mod_raise": (None, [vp, _u64p, i, i, _u64p]),
             "orc_hoisted_mac_sum": (i, [vp, _u64p, i, _u64p, i, _u64p, u64, i, _u64p]),
         }
         for name, (res, args) in sig.items():
@@ -341,6 +342,13 @@ class OracleContext:
         polys, limbs = ct.shape[0], ct.shape[1]
         out = np.zeros((polys, limbs - 1, self.N), dtype=np.uint64)
         lib().orc_rescale(self._c, _p(ct), polys, limbs, _p(out))
+        return out
+
+    def mod_raise(self, ct, target: int):
+        ct = np.ascontiguousarray(ct, dtype=np.uint64)
+        assert ct.shape[1] == 1
+        out = np.zeros((ct.shape[0], target, self.N), dtype=np.uint64)
+        lib().orc_mod_raise(self._c, _p(ct), ct.shape[0], target, _p(out))
         return out
 
     def drop_limbs(self, ct, target: int):

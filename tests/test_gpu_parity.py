@@ -235,6 +235,22 @@ def test_mul_relin_rescale_parity(name):
     assert np.array_equal(fhe.rescale(t, ctx).download(), orc.rescale(rt))
 
 
+@pytest.mark.parametrize("name", ["small", "keyswitch"])
+def test_mod_raise_parity(name):
+    """ModRaise of a bottom-level ciphertext to every limb, bit-exact."""
+    fhe = _fhe()
+    client, ctx = device_context(name, relin=False)
+    orc = oracle_context(name)
+    slots = orc.N // 2
+    rng = np.random.default_rng(21)
+    z = rng.uniform(-1, 1, slots)
+    ct = orc.encrypt(z, slots=slots, scale=2.0**40, limbs=1, enc_id=5)
+    dev = fhe.upload(ctx, ct, slots=slots, scale=2.0**40)
+    for target in (orc.L, 2):
+        out = fhe.mod_raise(dev, target, ctx).download()
+        assert np.array_equal(out, orc.mod_raise(ct, target)), target
+
+
 @pytest.mark.parametrize("name", ["small", "matvec"])
 def test_elementwise_parity(name):
     fhe = _fhe()

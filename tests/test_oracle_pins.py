@@ -317,6 +317,48 @@ def test_rescale_is_rounded_division():
             assert (V - want) % math.prod(primes[:-1]) == 0
 
 
+def test_mod_raise_is_centered_lift():
+    """Every raised coefficient's CRT value over the target limbs, centered,
+    equals the one-limb coefficient centered mod q_0."""
+    ctx = _small_ctx(log_n=8, limbs=4, dnum=2)
+    rng = np.random.default_rng(10)
+    q0 = int(ctx.primes[0])
+    ct = rng.integers(0, q0, (2, 1, ctx.N), dtype=np.uint64)
+    ct[0, 0, :3] = [0, (q0 - 1) // 2, (q0 + 1) // 2]  # both sides of the centre
+    out = ctx.mod_raise(ct, 4)
+    primes = [int(ctx.primes[l]) for l in range(4)]
+    Q = math.prod(primes)
+    for d in range(2):
+        c = ctx.intt_limbs(ct[d])
+        o = ctx.intt_limbs(out[d])
+        for k in range(0, ctx.N, 3):
+            X = _centered(_crt([o[t, k] for t in range(4)], primes), Q)
+            assert X == _centered(int(c[0, k]), q0), (d, k)
+
+
+def test_mod_raise_plaintext_is_m_plus_q0_multiple():
+    """decrypt(ModRaise(ct)) = m + q_0 I with I small (|I| <= (h + 1) / 2 for
+    a sparse secret of weight h); its q_0 residue is the original plaintext."""
+    ctx = oracle_context("small")
+    slots = ctx.N // 2
+    rng = np.random.default_rng(13)
+    z = rng.uniform(-1, 1, slots)
+    ct = ctx.encrypt(z, slots=slots, scale=2.0**40, limbs=1, enc_id=3)
+    raised = ctx.mod_raise(ct, ctx.L)
+    m0 = ctx.intt_limbs(ctx.decrypt_poly(ct))
+    mr = ctx.intt_limbs(ctx.decrypt_poly(raised))
+    q0 = int(ctx.primes[0])
+    primes = [int(p) for p in ctx.primes[: ctx.L]]
+    Q = math.prod(primes)
+    worst = 0
+    for k in range(0, ctx.N, 11):
+        X = _centered(_crt([mr[t, k] for t in range(ctx.L)], primes), Q)
+        m = _centered(int(m0[0, k]), q0)
+        assert (X - m) % q0 == 0
+        worst = max(worst, abs((X - m) // q0))
+    assert 0 < worst <= (192 + 1) // 2
+
+
 # ---------------------------------------------------------------------------
 # keys, encryption and homomorphic identities (decrypted values)
 # ---------------------------------------------------------------------------
