@@ -1,29 +1,388 @@
-"""CKKS bootstrapping surface (reference operators/nonlinear/bootstrap.py:59-189).
+"""Full-slot CKKS bootstrapping (reference ``easyfhe.bs.openfhe`` as used by
+operators/nonlinear/bootstrap.py:59-189, 352-437).
 
-The bootstrap program (ModRaise, CoeffToSlot, EvalMod, SlotToCoeff) is not
-built in this backend yet; every entry point raises ``NotImplementedError``
-so that a caller never receives a silently wrong refresh.
+Pipeline ("modraise_first", reference bootstrap.py:29):
+
+1. **Pre-scale.**  The input (any level, scale Delta_in) is taken to one limb
+   with its message scaled to Delta' = q_0 2^-ratio_bits, so that
+   t = (m' + q_0 I) / q_0 has a fractional part of at most about 2^-ratio_bits.
+2. **ModRaise** (C entry point ``ckks_mod_raise``) to the limbs the program
+   needs; the raised ciphertext is read at scale 2 K q_0, so its slots are
+   FFT(u) / (2 K) with u_k = t_k + i t_(k+n).
+3. **CoeffToSlot**: the inverse special FFT as ``level_budget[0]`` grouped
+   sparse stages (``lintrans.plan_levels``), each one hoisted BSGS
+   diagonal MAC (``hoisted_mac_sum``) and one rescale.
+4. **EvalMod** on the real and imaginary parts (split with one conjugation):
+   a Chebyshev interpolant of cos(2 pi (K y - 1/4) / 2^r) on [-1, 1] and r
+   double-angle steps give sin(2 pi t), evaluated on an exact-scale ladder
+   (``easyfhe.chebyshev``) at a working scale of at least 2^55 (two primes
+   per level on a 40-bit chain).
+5. **SlotToCoeff**: the special FFT, with q_0 / (2 pi Delta') folded into
+   its first level; the last level lands on the nominal scale 2^dcrt_bits.
+
+The limb cost is fixed by the chain: budget[0] + step (depth + r) + step +
+budget[1] - 1, where step is the primes per EvalMod level; the program raises
+to exactly output_levels + 1 + that many limbs.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .. import chebyshev as cheb
+from .. import fhe
+from .lintrans import LevelPlan, plan_levels
+
+# Encoding scales of the CoeffToSlot diagonals (at least 2^45, and enough to
+# keep the data scale at 2^62 on wide primes) and the scale of the
+# SlotToCoeff levels before the last one.  The CoeffToSlot result is read
+# modulo 1 after a 2^ratio_bits magnification, so its diagonals need
+# relative precision near 2^-40.
+_CTS_MIN_PT = 2.0**45
+_CTS_SCALE = 2.0**62
+_STC_SCALE = 2.0**45
+# EvalMod works at a scale of at least this many bits.
+_EVALMOD_BITS = 55
 
 
 @dataclass(frozen=True)
 class BootstrapSpec:
-    log_slots: int
+    """Program parameters (reference bootstrap.py:59-85)."""
+
+    log_slots: int = 15
     level_budget: tuple = (4, 4)
     output_levels: int = 0
     mode: str = "modraise_first"
 
+    @property
+    def slots(self) -> int:
+        return 1 << int(self.log_slots)
 
-def _missing(*_args, **_kwargs):
-    raise NotImplementedError("bootstrapping is not implemented in this backend yet")
+
+@dataclass(frozen=True)
+class EvalModParams:
+    """K bounds |t| (the integer part I plus the message), r double-angle
+    steps, the interpolant error target, and the headroom 2^ratio_bits of q_0
+    over the pre-scaled message."""
+
+    K: int = 28
+    double_angles: int = 3
+    fit_bits: int = 45
+    ratio_bits: int = 10
 
 
-requirements = _missing
-generate = _missing
-bootstrap = _missing
+@dataclass
+class Requirements:
+    rotations: tuple
 
-__all__ = ["BootstrapSpec", "bootstrap", "generate", "requirements"]
+
+def _check_spec(spec: BootstrapSpec, log_n: int) -> None:
+    if spec.mode != "modraise_first":
+        raise ValueError(f"unsupported bootstrap mode {spec.mode!r}")
+    if int(spec.log_slots) != log_n - 1:
+        raise NotImplementedError(
+            f"only full-slot programs (log_slots = {log_n - 1}) are built; "
+            f"got log_slots = {spec.log_slots}")
+    budget = tuple(int(v) for v in spec.level_budget)
+    if len(budget) != 2 or min(budget) < 1 or max(budget) > int(spec.log_slots):
+        raise ValueError(f"level_budget must be two values in [1, log_slots], got {budget}")
+
+
+def _plans(spec: BootstrapSpec):
+    b0, b1 = (int(v) for v in spec.level_budget)
+    return (plan_levels(int(spec.log_slots), b0, inverse=True),
+            plan_levels(int(spec.log_slots), b1, inverse=False))
+
+
+def _baby_offsets(plan: LevelPlan, n: int) -> list[int]:
+    return [(b * plan.stride - plan.center) % n for b in range(plan.baby)]
+
+
+def _giant_offset(plan: LevelPlan, n: int) -> int:
+    return (plan.baby * plan.stride) % n
+
+
+def _level_rotations(plan: LevelPlan, n: int) -> set[int]:
+    rots = {o for o in _baby_offsets(plan, n) if o}
+    if plan.giant > 1 and _giant_offset(plan, n):
+        rots.add(_giant_offset(plan, n))
+    return rots
+
+
+def requirements(specs, log_n: int) -> Requirements:
+    """Rotation indices every listed program needs, conjugation (2N - 1)
+    included (reference bootstrap.py:154-189)."""
+    if isinstance(specs, BootstrapSpec):
+        specs = (specs,)
+    rots: set[int] = set()
+    for spec in specs:
+        _check_spec(spec, int(log_n))
+        n = spec.slots
+        for plan in (*_plans(spec)[0], *_plans(spec)[1]):
+            rots |= _level_rotations(plan, n)
+        rots.add(2 * (1 << int(log_n)) - 1)
+    return Requirements(rotations=tuple(sorted(rots)))
+
+
+@dataclass
+class _Level:
+    name: str
+    plan: LevelPlan
+    limbs: int          # limbs of the ciphertext entering the level
+    primes: int         # primes dropped after the MAC
+    pt_scale: float     # encoding scale of the diagonals
+    out_scale: float    # exact scale after the rescales
+
+
+@dataclass
+class BootstrapProgram:
+    """Prepared constants and schedule (reference program object:
+    ``.constants.set_cache_mode``, ``.spec.slots``)."""
+
+    spec: BootstrapSpec
+    context: object
+    evalmod: EvalModParams
+    coefficients: np.ndarray
+    cheb_depth: int
+    step: int
+    raise_limbs: int
+    target_ratio: float          # Delta' / q_0
+    cts: list = field(default_factory=list)
+    stc: list = field(default_factory=list)
+    ladder: cheb.Ladder | None = None
+    constants: fhe.ConstantBundle | None = None
+    output_limbs: int = 0
+
+    @property
+    def depth_limbs(self) -> int:
+        return self.raise_limbs - self.output_limbs
+
+    def release(self) -> None:
+        if self.constants is not None:
+            self.constants.clear_cache()
+
+
+def _evalmod_coefficients(p: EvalModParams) -> np.ndarray:
+    period = 2.0 ** p.double_angles
+
+    def f(y):
+        return math.cos(2.0 * math.pi * (p.K * y - 0.25) / period)
+
+    grid = np.cos(np.linspace(0.0, math.pi, 4001))
+    for degree in range(16, 160):
+        c = cheb.chebyshev_coefficients(f, -1.0, 1.0, degree)
+        err = np.abs(cheb.evaluate_direct(grid, c) - np.cos(
+            2.0 * math.pi * (p.K * grid - 0.25) / period)).max()
+        if err < 2.0 ** -p.fit_bits:
+            return c
+    raise ValueError("EvalMod interpolant does not reach the requested precision")
+
+
+def generate(context, spec: BootstrapSpec, evalmod: EvalModParams | None = None
+             ) -> BootstrapProgram:
+    """Plan the program for ``context``'s chain, make sure its rotation keys
+    exist, and register its diagonals (encoded on first use; cached with
+    cache mode "plain") (reference bootstrap.py:113-148)."""
+    ctx = getattr(context, "context", context)
+    _check_spec(spec, ctx.logN)
+    p = evalmod or EvalModParams()
+    primes = [int(q) for q in ctx.primes()[: ctx.L]]
+    n = spec.slots
+    bits = math.log2(primes[1]) if len(primes) > 1 else math.log2(primes[0])
+    step = max(1, math.ceil(_EVALMOD_BITS / bits))
+    coeffs = _evalmod_coefficients(p)
+    depth = cheb.chebyshev_depth(coeffs)
+    cts_plans, stc_plans = _plans(spec)
+    n_cts, n_stc = len(cts_plans), len(stc_plans)
+    ladder_levels = depth + p.double_angles
+    cost = n_cts + step * ladder_levels + step + (n_stc - 1)
+    T = int(spec.output_levels) + 1 + cost
+    if T > ctx.L:
+        raise ValueError(
+            f"output_levels={spec.output_levels} needs {T} limbs (program depth {cost} "
+            f"limbs); the chain has {ctx.L}")
+
+    q0 = float(primes[0])
+    prog = BootstrapProgram(spec=spec, context=ctx, evalmod=p, coefficients=coeffs,
+                            cheb_depth=depth, step=step, raise_limbs=T,
+                            target_ratio=2.0 ** -p.ratio_bits)
+    vectors = {}
+
+    # CoeffToSlot: one prime per level, the last one lands on the ladder top
+    top = T - n_cts
+    ladder = cheb.Ladder(primes, top, math.prod(float(q) for q in primes[top - step: top]),
+                         step, ladder_levels)
+    scale = 2.0 * p.K * q0
+    limbs = T
+    for i, plan in enumerate(cts_plans):
+        q = float(primes[limbs - 1])
+        if i == n_cts - 1:
+            want = ladder.scale[0]
+            w = want * q / scale
+        else:
+            w = max(_CTS_MIN_PT, _CTS_SCALE * q / scale)
+            want = scale * w / q
+        name = f"cts{i}"
+        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n))
+        prog.cts.append(_Level(name, plan, limbs, 1, w, want))
+        scale, limbs = want, limbs - 1
+    prog.ladder = ladder
+
+    # SlotToCoeff: the first level drops `step` primes (back from the
+    # EvalMod scale), the last lands on 2^dcrt_bits
+    limbs = ladder.limbs[-1]
+    scale = ladder.scale[-1]
+    fold = 1.0 / (2.0 * math.pi * prog.target_ratio)
+    for i, plan in enumerate(stc_plans):
+        drop = step if i == 0 else 1
+        div = math.prod(float(q) for q in primes[limbs - drop: limbs])
+        want = ctx.scale_at(limbs - drop) if i == n_stc - 1 else _STC_SCALE
+        w = want * div / scale
+        name = f"stc{i}"
+        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, fold if i == 0 else 1.0))
+        prog.stc.append(_Level(name, plan, limbs, drop, w, want))
+        scale, limbs = want, limbs - drop
+    prog.output_limbs = limbs
+    assert limbs == int(spec.output_levels) + 1, (limbs, spec.output_levels)
+    prog.constants = fhe.ConstantBundle(vectors, cache_mode="plain")
+
+    need = [r for r in requirements(spec, ctx.logN).rotations if not ctx.has_rotation_key(r)]
+    if need:
+        ctx.generate_rotation_keys(need)
+    return prog
+
+
+# ---------------------------------------------------------------------------
+# evaluation
+# ---------------------------------------------------------------------------
+
+
+def _drop(ct, limbs: int, ctx):
+    return fhe.align_to(ct, ct.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+
+
+def _prescale(ct, prog: BootstrapProgram, ctx):
+    """One-limb ciphertext whose message scale is Delta' (close to
+    target_ratio q_0); returns it and Delta' / (target_ratio q_0)."""
+    q0 = float(ctx.primes()[0])
+    want = prog.target_ratio * q0
+    s = float(ct.state.scaling_factor)
+    limbs = int(ct.state.cur_limbs)
+    c = round(want / s)
+    if c >= 1:
+        x = _drop(ct, 1, ctx)
+        if c > 1:
+            enc = fhe.encode_scalar(int(c), 1, scale_degree=0, mode="integer", context=ctx)
+            x = fhe.homo_mul_scalar(x, enc, ctx)
+        return x, s * c / want
+    if limbs < 2:
+        raise ValueError("input scale exceeds q_0 2^-ratio_bits and no limb is left to rescale")
+    q1 = float(ctx.primes()[1])
+    c = round(want * q1 / s)
+    x = _drop(ct, 2, ctx)
+    enc = fhe.encode_scalar(int(c), 2, scale_degree=0, mode="integer", context=ctx)
+    x = fhe.rescale(fhe.homo_mul_scalar(x, enc, ctx), ctx)
+    return x, s * c / q1 / want
+
+
+def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
+    n = prog.spec.slots
+    plan = lv.plan
+    state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
+    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx)
+    acc = fhe.hoisted_mac_sum(x, _baby_offsets(plan, n), pts, _giant_offset(plan, n),
+                              plan.giant, ctx)
+    for _ in range(lv.primes):
+        acc = fhe.rescale(acc, ctx)
+    acc.set_scale(lv.out_scale, 1)
+    return acc
+
+
+def _evalmod(ops: cheb.LadderOps, y: cheb.LCt, prog: BootstrapProgram) -> cheb.LCt:
+    c = cheb.evaluate(ops, y, prog.coefficients)
+    for _ in range(prog.evalmod.double_angles):
+        c = ops.add_const(ops.double(ops.mul(c, c)), -1.0)
+    return c
+
+
+def bootstrap(ct, context, program: BootstrapProgram):
+    """Refreshed copy of ``ct`` with output_levels + 1 limbs; ``ct`` is not
+    consumed (reference bootstrap.py:370)."""
+    prog = program
+    ctx = getattr(context, "context", context)
+    if ct.degree != 1 or ct.is_ext:
+        raise ValueError("bootstrap expects a degree-1 Q-basis ciphertext")
+    if int(ct.slots) != prog.spec.slots:
+        raise ValueError(f"bootstrap input slots={ct.slots} != program slots={prog.spec.slots}")
+    q0 = float(ctx.primes()[0])
+    x, ratio = _prescale(ct, prog, ctx)
+    x = fhe.mod_raise(x, prog.raise_limbs, ctx)
+    x.set_scale(2.0 * prog.evalmod.K * q0, 1)
+    for lv in prog.cts:
+        x = _linear_level(x, lv, prog, ctx)
+
+    ops = cheb.LadderOps(ctx, prog.ladder)
+    y = cheb.LCt(x, 0)
+    yc = cheb.LCt(fhe.homo_rotate(x, 2 * ctx.N - 1, ctx), 0)
+    re = ops.add(y, yc)
+    im = cheb.LCt(fhe.homo_mul_i(ops.add(y, yc, sign=-1.0).ct, ctx, negative=True), 0)
+    del y, yc, x
+    s_re = _evalmod(ops, re, prog)
+    s_im = _evalmod(ops, im, prog)
+    u = fhe.homo_add(s_re.ct, fhe.homo_mul_i(s_im.ct, ctx), ctx)
+    del s_re, s_im
+    for lv in prog.stc:
+        u = _linear_level(u, lv, prog, ctx)
+    u.set_scale(prog.stc[-1].out_scale * ratio, 1)
+    return u
+
+
+def _to_scale(ct, limbs: int, scale: float, value: float, ctx):
+    """value * ct on ``limbs`` limbs at exactly ``scale`` (one rescale; ct
+    needs more than ``limbs`` limbs)."""
+    x = _drop(ct, limbs + 1, ctx)
+    q = float(ctx.primes()[limbs])
+    w = scale * q / float(x.state.scaling_factor)
+    enc = fhe.encode_scalar(float(value), limbs + 1, scaling_factor=w, context=ctx)
+    out = fhe.rescale(fhe.homo_mul_scalar(x, enc, ctx), ctx)
+    out.set_scale(scale, 1)
+    return out
+
+
+def bootstrap_iterated(ct, context, program: BootstrapProgram, iterations: int = 2,
+                       precision_bits: int = 8):
+    """Two-pass (Meta-BTS) refresh: B(ct) - 2^-p B(2^p (B(ct) - ct)), which
+    removes the first pass's error up to p more bits; one more level is
+    consumed (reference operators/nonlinear/bootstrap.py:352-437).  Scales are
+    aligned exactly (not within the fixed-scale tolerance), so the gain is not
+    capped by prime drift."""
+    ctx = getattr(context, "context", context)
+    if int(iterations) not in (1, 2):
+        raise ValueError("bootstrap iterations must be one or two")
+    first = bootstrap(ct, ctx, program)
+    if int(iterations) == 1:
+        return first
+    limbs = int(ct.state.cur_limbs)
+    out_limbs = int(first.state.cur_limbs)
+    if out_limbs <= max(limbs, 1):
+        raise ValueError("the first pass left no level for the correction")
+    s_in = float(ct.state.scaling_factor)
+    down = _to_scale(first, limbs, s_in, 1.0, ctx)
+    diff = fhe.homo_sub(down, ct, ctx)
+    p = int(precision_bits)
+    if p > 0:
+        enc = fhe.encode_scalar(1 << p, limbs, scale_degree=0, mode="integer", context=ctx)
+        diff = fhe.homo_mul_scalar(diff, enc, ctx)
+    err = bootstrap(diff, ctx, program)
+    s1 = float(first.state.scaling_factor)
+    corr = _to_scale(err, out_limbs - 1, s1, 2.0 ** -p, ctx)
+    base = _drop(first, out_limbs - 1, ctx)
+    base.set_scale(s1, 1)
+    return fhe.homo_sub(base, corr, ctx)
+
+
+__all__ = ["BootstrapProgram", "BootstrapSpec", "EvalModParams", "Requirements", "bootstrap",
+           "bootstrap_iterated", "generate", "requirements"]

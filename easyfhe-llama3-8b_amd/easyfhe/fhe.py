@@ -446,9 +446,11 @@ class ConstantBundle:
         self._plain: dict = {}
         self._middle: dict = {}
 
-    def set_cache_mode(self, mode: str) -> None:
+    def set_cache_mode(self, mode: str, clear: bool = False) -> None:
         if mode not in {"none", "middle", "plain", "both"}:
             raise ValueError(f"unknown cache_mode {mode!r}")
+        if clear:
+            self.clear_cache()
         self.cache_mode = mode
 
     def _values(self, name: str, slots: int, context) -> np.ndarray:

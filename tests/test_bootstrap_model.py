@@ -1,0 +1,203 @@
+"""CPU model of the bootstrap program and of the Chebyshev evaluator.
+
+The schedules of ``easyfhe.chebyshev`` and ``easyfhe.bs`` are run on plain
+numpy slot vectors (an ``ops`` object with the ladder interface that acts on
+values instead of ciphertexts), so that the algebra, the BSGS offsets, the
+folded constants and the EvalMod interpolant are checked against the
+mathematics without a GPU:
+
+* Chebyshev division and recursion against numpy.polynomial.chebyshev;
+* the coefficient fit against numpy's chebinterpolate (same nodes);
+* CoeffToSlot -> EvalMod -> SlotToCoeff on t = u 2^-10 + I (I random
+  integers, the ModRaise overflow) returns the message.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+from numpy.polynomial import chebyshev as npcheb
+
+from easyfhe import chebyshev as cheb
+from easyfhe.bs import lintrans
+from easyfhe.bs import openfhe as bs
+
+
+class ValueOps:
+    """Ladder operations on numpy values (optional relative noise)."""
+
+    def __init__(self, noise: float = 0.0, seed: int = 0):
+        self.noise = noise
+        self.rng = np.random.default_rng(seed)
+        self.mults = 0
+
+    def _n(self, v):
+        if not self.noise:
+            return v
+        return v + self.noise * self.rng.standard_normal(np.shape(v))
+
+    def combine(self, terms, const, level):
+        acc = const + sum(w * (x.ct if isinstance(x, cheb.LCt) else x) for x, w in terms)
+        return cheb.LCt(self._n(acc), level)
+
+    def lower(self, x, level):
+        assert level >= x.level
+        return cheb.LCt(x.ct, level)
+
+    def add(self, a, b, sign=1.0):
+        return cheb.LCt(a.ct + sign * b.ct, max(a.level, b.level))
+
+    def add_const(self, a, c):
+        return cheb.LCt(a.ct + c, a.level)
+
+    def double(self, a):
+        return cheb.LCt(2.0 * a.ct, a.level)
+
+    def mul(self, a, b):
+        self.mults += 1
+        return cheb.LCt(self._n(a.ct * b.ct), max(a.level, b.level) + 1)
+
+
+def test_coefficients_match_numpy_interpolation():
+    f = np.exp
+    c = cheb.chebyshev_coefficients(lambda v: math.exp(v), -1.0, 1.0, 20)
+    ref = npcheb.chebinterpolate(f, 20)
+    ref[0] *= 2.0  # reference convention carries 2 c_0
+    assert np.allclose(c, ref, atol=1e-14)
+
+
+def test_division_by_t_d():
+    rng = np.random.default_rng(1)
+    x = np.linspace(-1, 1, 101)
+    for n, d in ((9, 8), (15, 8), (31, 16), (60, 32)):
+        c = rng.standard_normal(n + 1)
+        q, r = cheb.divide_by_t(c, d)
+        td = npcheb.chebval(x, np.eye(d + 1)[d])
+        assert len(r) == d
+        assert np.allclose(npcheb.chebval(x, q) * td + npcheb.chebval(x, r),
+                           npcheb.chebval(x, c), atol=1e-11)
+
+
+@pytest.mark.parametrize("degree", [1, 2, 3, 7, 8, 15, 27, 48, 59, 60, 77, 120])
+def test_series_schedule_values_and_depth(degree):
+    rng = np.random.default_rng(degree)
+    coeffs = rng.uniform(-1, 1, degree + 1) / np.arange(1, degree + 2)
+    y = np.cos(np.linspace(0, math.pi, 257))
+    ops = ValueOps()
+    out = cheb.evaluate(ops, cheb.LCt(y, 0), coeffs)
+    want = cheb.evaluate_direct(y, coeffs)
+    assert np.abs(out.ct - want).max() < 1e-12
+    depth = cheb.chebyshev_depth(coeffs)
+    assert out.level == depth
+    # never more than one level above the information-theoretic minimum
+    assert depth <= math.ceil(math.log2(degree + 1)) + 1
+    if degree in (48, 59, 60):
+        assert depth == 6
+
+
+def test_clenshaw_matches_numpy_chebval():
+    rng = np.random.default_rng(3)
+    c = rng.standard_normal(30)
+    x = np.linspace(-3, 5, 77)
+    ref = c.copy()
+    ref[0] *= 0.5
+    assert np.allclose(cheb.evaluate_direct(x, c, -3, 5),
+                       npcheb.chebval((2 * x - 2) / 8, ref), atol=1e-12)
+
+
+def _special_fft(u: np.ndarray) -> np.ndarray:
+    """z = S_L .. S_1 P u (slots of the coefficient vector u)."""
+    n = len(u)
+    log_n = n.bit_length() - 1
+    idx = np.array([int(format(i, f"0{log_n}b")[::-1], 2) for i in range(n)])
+    x = u[idx]
+    for s in range(1, log_n + 1):
+        x = lintrans.apply_diagonals(lintrans.stage_diagonals(n, s, False), x)
+    return x
+
+
+def _bsgs(x: np.ndarray, plan, rows: np.ndarray) -> np.ndarray:
+    """hoisted_mac_sum on values: sum_g rot_(g giant)(sum_b p[gB+b] rot_(off_b) x)."""
+    n = len(x)
+    offs = bs._baby_offsets(plan, n)
+    giant = bs._giant_offset(plan, n)
+    acc = np.zeros(n, dtype=np.complex128)
+    for g in reversed(range(plan.giant)):
+        inner = sum(rows[g * plan.baby + b] * np.roll(x, -offs[b]) for b in range(plan.baby))
+        acc = np.roll(acc, -giant) + inner if g < plan.giant - 1 else inner
+    return acc
+
+
+def _horner_check(x, plan, rows):
+    """The Horner form used by the device equals the direct BSGS sum."""
+    n = len(x)
+    offs = bs._baby_offsets(plan, n)
+    giant = bs._giant_offset(plan, n)
+    direct = sum(np.roll(sum(rows[g * plan.baby + b] * np.roll(x, -offs[b])
+                             for b in range(plan.baby)), -g * giant) for g in range(plan.giant))
+    return direct
+
+
+@pytest.mark.parametrize("log_n,budget", [(6, (2, 2)), (10, (3, 3)), (10, (4, 4)), (11, (3, 2))])
+def test_bootstrap_model_recovers_message(log_n, budget):
+    n = 1 << log_n
+    rng = np.random.default_rng(log_n)
+    p = bs.EvalModParams()
+    spec = bs.BootstrapSpec(log_slots=log_n, level_budget=budget)
+    cts_plans, stc_plans = bs._plans(spec)
+    z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    # coefficient vector of the message at scale Delta' = 2^-10 q_0, plus the
+    # integer overflow I of ModRaise (|I| well inside K)
+    P = np.array([int(format(i, f"0{log_n}b")[::-1], 2) for i in range(n)])
+    u = z.copy()
+    for s in reversed(range(1, log_n + 1)):
+        u = lintrans.apply_diagonals(lintrans.stage_diagonals(n, s, True), u)
+    u_nat = np.empty_like(u)
+    u_nat[P] = u
+    assert np.abs(_special_fft(u_nat) - z).max() < 1e-9
+    I = rng.integers(-12, 13, n) + 1j * rng.integers(-12, 13, n)
+    t = u_nat * 2.0 ** -p.ratio_bits + I
+    x = _special_fft(t) / (2 * p.K)  # slots of the raised ciphertext at scale 2 K q_0
+    for plan in cts_plans:
+        rows = plan.plaintext_rows(n)
+        y = _bsgs(x, plan, rows)
+        assert np.allclose(y, _horner_check(x, plan, rows), atol=1e-9)
+        x = y
+    assert np.abs(x - t[P] / (2 * p.K)).max() < 1e-9  # bit-reversed t / 2K
+    re = x + np.conj(x)
+    im = -1j * (x - np.conj(x))
+    coeffs = bs._evalmod_coefficients(p)
+    outs = []
+    for v in (re, im):
+        ops = ValueOps()
+        c = cheb.evaluate(ops, cheb.LCt(v.real, 0), coeffs)
+        for _ in range(p.double_angles):
+            c = ops.add_const(ops.double(ops.mul(c, c)), -1.0)
+        outs.append(c.ct)
+    assert np.abs(outs[0] - np.sin(2 * np.pi * t[P].real)).max() < 1e-9
+    u2 = outs[0] + 1j * outs[1]
+    ideal = np.sin(2 * np.pi * t[P].real) + 1j * np.sin(2 * np.pi * t[P].imag)
+    fold = 1.0 / (2 * math.pi * 2.0 ** -p.ratio_bits)
+    for i, plan in enumerate(stc_plans):
+        rows = plan.plaintext_rows(n, fold if i == 0 else 1.0)
+        u2 = _bsgs(u2, plan, rows)
+        ideal = _bsgs(ideal, plan, rows)
+    # the schedule equals SlotToCoeff of the exact sine ...
+    assert np.abs(u2 - ideal).max() < 1e-8
+    # ... whose distance to the message is the sine's curvature on the
+    # coefficients (|u_k| ~ |z| / sqrt(n)): (2 pi)^2 |u|^3 2^-20 / 6 per
+    # coefficient
+    err = np.abs(ideal - z).max()
+    assert 1e-12 < err < 2.0 ** -20, err
+
+
+def test_requirements_and_limb_plan():
+    spec = bs.BootstrapSpec(log_slots=15, level_budget=(3, 3), output_levels=0)
+    req = bs.requirements([spec], log_n=16)
+    assert 2 * 65536 - 1 in req.rotations
+    assert all(0 < r < 2 * 65536 for r in req.rotations)
+    assert len(req.rotations) < 64
+    with pytest.raises(NotImplementedError):
+        bs.requirements([bs.BootstrapSpec(log_slots=7)], log_n=16)

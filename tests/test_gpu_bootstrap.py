@@ -1,0 +1,113 @@
+"""Polynomial evaluation and bootstrapping on the device (decrypted values).
+
+Bootstrapping has no bit-level oracle (the reference's EasyFHE program is
+absent); it is pinned by precision: -log2 max |dec(bts(ct)) - m| against the
+encrypted fp64 message, and by its CPU model (test_bootstrap_model.py).  The
+Chebyshev evaluator is compared with the fp64 series value.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import device_context
+
+pytestmark = pytest.mark.gpu
+
+# N = 2^12, 60-bit q_0 + 30 x 40-bit, dnum 3 (11-limb digits), 11 x 60-bit P
+BOOT = dict(log_n=12, depth=30, dnum=3, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+@pytest.fixture(scope="module")
+def boot_ctx():
+    return device_context(BOOT)
+
+
+def test_chebyshev_series_cipher(boot_ctx):
+    from easyfhe import chebyshev as cheb
+
+    client, ctx = boot_ctx
+    coeffs = cheb.chebyshev_coefficients(math.tanh, -4.0, 4.0, 27)
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-4, 4, ctx.max_slots)
+    ct = client.encrypt(x, cur_limbs=ctx.L, enc_id=71)
+    out = cheb.eval_chebyshev_series_cipher(ct, coeffs, lower_bound=-4.0, upper_bound=4.0,
+                                            crypto_context=ctx)
+    assert out.state.cur_limbs == ctx.L - cheb.series_depth(coeffs)
+    got = client.decrypt(out)
+    want = cheb.evaluate_direct(x, coeffs, -4.0, 4.0)
+    err = np.abs(got - want).max()
+    print(f"tanh deg 27: depth {cheb.series_depth(coeffs)}, max err {err:.3e}")
+    assert err < 1e-6
+
+
+def test_chebyshev_two_prime_ladder(boot_ctx):
+    """A ladder with two primes per level keeps scales exact at ~2^80."""
+    from easyfhe import chebyshev as cheb
+    from easyfhe import fhe
+
+    client, ctx = boot_ctx
+    primes = [int(q) for q in ctx.primes()[: ctx.L]]
+    coeffs = cheb.chebyshev_coefficients(lambda v: math.cos(3.0 * v), -1.0, 1.0, 20)
+    depth = cheb.chebyshev_depth(coeffs)
+    top = ctx.L - 1
+    lad = cheb.Ladder(primes, top - 1, float(primes[top - 3]) * float(primes[top - 2]), 2, depth)
+    ops = cheb.LadderOps(ctx, lad)
+    rng = np.random.default_rng(6)
+    x = rng.uniform(-1, 1, ctx.max_slots)
+    ct = client.encrypt(x, cur_limbs=ctx.L, enc_id=72)
+    y = ops.combine([(ct, 1.0)], 0.0, 0)
+    out = cheb.evaluate(ops, y, coeffs)
+    assert out.ct.state.cur_limbs == lad.limbs[depth]
+    err = np.abs(client.decrypt(out.ct) - cheb.evaluate_direct(x, coeffs)).max()
+    print(f"cos(3x) deg 20 at 2^80: max err {err:.3e}")
+    assert err < 1e-8
+    fhe.homo_add(out.ct, out.ct, ctx)  # scales equal on the ladder
+
+
+@pytest.mark.parametrize("budget", [(3, 3), (2, 2)])
+def test_bootstrap_precision(boot_ctx, budget):
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    spec = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget, output_levels=3)
+    prog = bs.generate(ctx, spec)
+    rng = np.random.default_rng(7)
+    z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    ct = client.encrypt(z, cur_limbs=1, enc_id=73)
+    out = bs.bootstrap(ct, ctx, prog)
+    assert out.state.cur_limbs == spec.output_levels + 1
+    err = np.abs(client.decrypt_complex(out) - z).max()
+    bits = -math.log2(err)
+    print(f"bootstrap {budget}: raise to {prog.raise_limbs} limbs, {bits:.1f} bits")
+    assert bits > 14
+    # the refreshed ciphertext computes: square it and rescale
+    from easyfhe import fhe
+
+    sq = fhe.rescale(fhe.homo_mul_relin(out, out, ctx), ctx)
+    err2 = np.abs(client.decrypt_complex(sq) - z * z).max()
+    assert err2 < 4 * err + 1e-6
+    prog.release()
+
+
+def test_bootstrap_two_pass_gains_precision(boot_ctx):
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    spec = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3), output_levels=3)
+    prog = bs.generate(ctx, spec)
+    rng = np.random.default_rng(8)
+    z = rng.uniform(-1, 1, n)
+    ct = client.encrypt(z, cur_limbs=2, enc_id=74)
+    one = bs.bootstrap(ct, ctx, prog)
+    two = bs.bootstrap_iterated(ct, ctx, prog, iterations=2, precision_bits=8)
+    assert two.state.cur_limbs == one.state.cur_limbs - 1
+    e1 = np.abs(client.decrypt_complex(one) - z).max()
+    e2 = np.abs(client.decrypt_complex(two) - z).max()
+    print(f"one pass {-math.log2(e1):.1f} bits, two passes {-math.log2(e2):.1f} bits")
+    assert e2 < e1 / 4
