@@ -79,9 +79,13 @@ def main() -> int:
     ap.add_argument("--cts", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
-    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile"], default="keyswitch",
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap"],
+                    default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
-                         "(the calibration kernel), for rocprofv3 counter runs")
+                         "(the calibration kernel), for rocprofv3 counter runs; "
+                         "bootstrap: the full-slot bootstrap workload on the same chain")
+    ap.add_argument("--boot-cts", type=int, default=32)
+    ap.add_argument("--budget", type=int, nargs=2, default=(3, 3))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the key-switch "
@@ -95,6 +99,8 @@ def main() -> int:
                                special_bits=PARAMS["special_bits"], seed=0, rotations=ROTATIONS)
     if args.mode == "ntt-profile":
         return ntt_profile(spec, args.cts)
+    if args.mode == "bootstrap":
+        return bootstrap_bench(spec, args)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
     ctx.synchronize()
@@ -209,6 +215,75 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bootstrap_bench(spec, args) -> int:
+    """Full-slot bootstrap of --boot-cts ciphertexts at the bottom level (one
+    limb, values uniform[-1, 1] from seed 0): CoeffToSlot / SlotToCoeff with
+    the given level budget, EvalMod at a 2^80 working scale; output_levels is
+    the most the chain allows.  Reports bootstraps/s and precision bits."""
+    import math
+
+    from easyfhe import fhe
+    from easyfhe.bs import openfhe as bs
+
+    spec.rotations = ()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    budget = tuple(int(v) for v in args.budget)
+    probe = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget, output_levels=0)
+    depth = bs.generate(ctx, probe).depth_limbs
+    bspec = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget,
+                             output_levels=ctx.L - depth - 1)
+    t0 = time.perf_counter()
+    prog = bs.generate(ctx, bspec)
+    ctx.synchronize()
+    setup_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    zs = [rng.uniform(-1, 1, ctx.max_slots) for _ in range(args.boot_cts)]
+    cts = [client.encrypt(z, cur_limbs=1, enc_id=i + 1) for i, z in enumerate(zs)]
+    t0 = time.perf_counter()
+    for _ in range(max(1, args.warmup)):
+        bs.bootstrap(cts[0], ctx, prog).release()
+    ctx.synchronize()
+    first_s = time.perf_counter() - t0
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    outs = [bs.bootstrap(c, ctx, prog) for c in cts]
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    bits = [-math.log2(np.abs(client.decrypt_complex(o) - z).max()) for o, z in zip(outs, zs)]
+    result = {
+        "metric": "bootstrap/s @N=2^16",
+        "value": round(len(cts) / wall, 3),
+        "unit": "bootstrap/s",
+        "n_gpus": 1,
+        "steps": len(cts),
+        "warmup": max(1, args.warmup),
+        "ms_per_step": round(wall * 1000.0 / len(cts), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {
+            "workload": f"full-slot bootstrap, N=2^16, Q=1x60b+35x40b, dnum=3, P=12x44b; "
+                        f"{len(cts)} ciphertexts at one limb; CtS/StC budget {budget}",
+            "raise_limbs": prog.raise_limbs,
+            "output_limbs": prog.output_limbs,
+            "evalmod": {"K": prog.evalmod.K, "double_angles": prog.evalmod.double_angles,
+                        "degree": len(prog.coefficients) - 1, "depth": prog.cheb_depth,
+                        "primes_per_level": prog.step},
+        },
+        "gpu_event_ms_per_step": round(ev0.elapsed_time(ev1) / len(cts), 3),
+        "precision_bits_min": round(min(bits), 2),
+        "precision_bits_mean": round(float(np.mean(bits)), 2),
+        "setup_s": round(setup_s, 2),
+        "first_bootstrap_s": round(first_s, 3),
+    }
     print(json.dumps(result), flush=True)
     return 0
 

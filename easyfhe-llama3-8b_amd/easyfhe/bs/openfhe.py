@@ -11,7 +11,8 @@ Pipeline ("modraise_first", reference bootstrap.py:29):
    FFT(u) / (2 K) with u_k = t_k + i t_(k+n).
 3. **CoeffToSlot**: the inverse special FFT as ``level_budget[0]`` grouped
    sparse stages (``lintrans.plan_levels``), each one hoisted BSGS
-   diagonal MAC (``hoisted_mac_sum``) and one rescale.
+   diagonal MAC (``hoisted_mac_sum``) and the rescales that keep the
+   diagonals at 2^cts_pt_bits (``_plan_cts_drops``).
 4. **EvalMod** on the real and imaginary parts (split with one conjugation):
    a Chebyshev interpolant of cos(2 pi (K y - 1/4) / 2^r) on [-1, 1] and r
    double-angle steps give sin(2 pi t), evaluated on an exact-scale ladder
@@ -20,9 +21,10 @@ Pipeline ("modraise_first", reference bootstrap.py:29):
 5. **SlotToCoeff**: the special FFT, with q_0 / (2 pi Delta') folded into
    its first level; the last level lands on the nominal scale 2^dcrt_bits.
 
-The limb cost is fixed by the chain: budget[0] + step (depth + r) + step +
-budget[1] - 1, where step is the primes per EvalMod level; the program raises
-to exactly output_levels + 1 + that many limbs.
+The limb cost is fixed by the chain: the CoeffToSlot drops (at least
+budget[0]) + step (depth + r) + step + budget[1] - 1, where step is the primes
+per EvalMod level; the program raises to exactly output_levels + 1 + that
+many limbs.
 """
 
 from __future__ import annotations
@@ -36,14 +38,10 @@ from .. import chebyshev as cheb
 from .. import fhe
 from .lintrans import LevelPlan, plan_levels
 
-# Encoding scales of the CoeffToSlot diagonals (at least 2^45, and enough to
-# keep the data scale at 2^62 on wide primes) and the scale of the
-# SlotToCoeff levels before the last one.  The CoeffToSlot result is read
-# modulo 1 after a 2^ratio_bits magnification, so its diagonals need
-# relative precision near 2^-40.
-_CTS_MIN_PT = 2.0**45
-_CTS_SCALE = 2.0**62
+# Scale of the SlotToCoeff levels before the last one, and the data-scale cap
+# of the CoeffToSlot levels (bits).
 _STC_SCALE = 2.0**45
+_CTS_CAP_BITS = 100
 # EvalMod works at a scale of at least this many bits.
 _EVALMOD_BITS = 55
 
@@ -63,15 +61,21 @@ class BootstrapSpec:
 
 
 @dataclass(frozen=True)
-class EvalModParams:
+class BootstrapParams:
     """K bounds |t| (the integer part I plus the message), r double-angle
-    steps, the interpolant error target, and the headroom 2^ratio_bits of q_0
-    over the pre-scaled message."""
+    steps, the interpolant error target, the headroom 2^ratio_bits of q_0
+    over the pre-scaled message, and the encoding precision of the
+    CoeffToSlot diagonals.  The CoeffToSlot output is read modulo 1 after a
+    2^ratio_bits magnification, so its relative error bounds the result:
+    each bit of cts_pt_bits is a bit of precision until the sine's curvature
+    or the input noise dominates; the limbs it costs follow from the chain."""
 
     K: int = 28
     double_angles: int = 3
     fit_bits: int = 45
     ratio_bits: int = 10
+    cts_pt_bits: int = 58
+
 
 
 @dataclass
@@ -144,7 +148,7 @@ class BootstrapProgram:
 
     spec: BootstrapSpec
     context: object
-    evalmod: EvalModParams
+    evalmod: BootstrapParams
     coefficients: np.ndarray
     cheb_depth: int
     step: int
@@ -165,7 +169,7 @@ class BootstrapProgram:
             self.constants.clear_cache()
 
 
-def _evalmod_coefficients(p: EvalModParams) -> np.ndarray:
+def _evalmod_coefficients(p: BootstrapParams) -> np.ndarray:
     period = 2.0 ** p.double_angles
 
     def f(y):
@@ -181,14 +185,35 @@ def _evalmod_coefficients(p: EvalModParams) -> np.ndarray:
     raise ValueError("EvalMod interpolant does not reach the requested precision")
 
 
-def generate(context, spec: BootstrapSpec, evalmod: EvalModParams | None = None
+def _plan_cts_drops(n_levels: int, s_bits: float, prime_bits: float, top_bits: float,
+                    pt_bits: float) -> list[int]:
+    """Primes dropped after each CoeffToSlot level: intermediate levels keep
+    their diagonals at 2^pt_bits and the data scale under the cap; the last
+    drops as many primes as it takes to land on the EvalMod ladder with its
+    own diagonals at 2^pt_bits or finer."""
+    drops = []
+    for i in range(n_levels):
+        if i == n_levels - 1:
+            d = 1
+            while top_bits + d * prime_bits - s_bits < pt_bits - 0.5:
+                d += 1
+        else:
+            d = 1
+            while s_bits + pt_bits - d * prime_bits > _CTS_CAP_BITS:
+                d += 1
+            s_bits += pt_bits - d * prime_bits
+        drops.append(d)
+    return drops
+
+
+def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = None
              ) -> BootstrapProgram:
     """Plan the program for ``context``'s chain, make sure its rotation keys
     exist, and register its diagonals (encoded on first use; cached with
     cache mode "plain") (reference bootstrap.py:113-148)."""
     ctx = getattr(context, "context", context)
     _check_spec(spec, ctx.logN)
-    p = evalmod or EvalModParams()
+    p = evalmod or BootstrapParams()
     primes = [int(q) for q in ctx.primes()[: ctx.L]]
     n = spec.slots
     bits = math.log2(primes[1]) if len(primes) > 1 else math.log2(primes[0])
@@ -198,37 +223,39 @@ def generate(context, spec: BootstrapSpec, evalmod: EvalModParams | None = None
     cts_plans, stc_plans = _plans(spec)
     n_cts, n_stc = len(cts_plans), len(stc_plans)
     ladder_levels = depth + p.double_angles
-    cost = n_cts + step * ladder_levels + step + (n_stc - 1)
+    q0 = float(primes[0])
+    s0 = 2.0 * p.K * q0  # scale the raised ciphertext is read at
+    drops = _plan_cts_drops(n_cts, math.log2(s0), bits, step * bits, p.cts_pt_bits)
+    cost = sum(drops) + step * ladder_levels + step + (n_stc - 1)
     T = int(spec.output_levels) + 1 + cost
     if T > ctx.L:
         raise ValueError(
             f"output_levels={spec.output_levels} needs {T} limbs (program depth {cost} "
             f"limbs); the chain has {ctx.L}")
 
-    q0 = float(primes[0])
     prog = BootstrapProgram(spec=spec, context=ctx, evalmod=p, coefficients=coeffs,
                             cheb_depth=depth, step=step, raise_limbs=T,
                             target_ratio=2.0 ** -p.ratio_bits)
     vectors = {}
 
-    # CoeffToSlot: one prime per level, the last one lands on the ladder top
-    top = T - n_cts
+    # CoeffToSlot: the last level lands on the ladder top
+    top = T - sum(drops)
     ladder = cheb.Ladder(primes, top, math.prod(float(q) for q in primes[top - step: top]),
                          step, ladder_levels)
-    scale = 2.0 * p.K * q0
+    scale = s0
     limbs = T
-    for i, plan in enumerate(cts_plans):
-        q = float(primes[limbs - 1])
+    for i, (plan, d) in enumerate(zip(cts_plans, drops)):
+        div = math.prod(float(q) for q in primes[limbs - d: limbs])
         if i == n_cts - 1:
             want = ladder.scale[0]
-            w = want * q / scale
+            w = want * div / scale
         else:
-            w = max(_CTS_MIN_PT, _CTS_SCALE * q / scale)
-            want = scale * w / q
+            w = 2.0 ** p.cts_pt_bits
+            want = scale * w / div
         name = f"cts{i}"
         vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n))
-        prog.cts.append(_Level(name, plan, limbs, 1, w, want))
-        scale, limbs = want, limbs - 1
+        prog.cts.append(_Level(name, plan, limbs, d, w, want))
+        scale, limbs = want, limbs - d
     prog.ladder = ladder
 
     # SlotToCoeff: the first level drops `step` primes (back from the
@@ -384,5 +411,5 @@ def bootstrap_iterated(ct, context, program: BootstrapProgram, iterations: int =
     return fhe.homo_sub(base, corr, ctx)
 
 
-__all__ = ["BootstrapProgram", "BootstrapSpec", "EvalModParams", "Requirements", "bootstrap",
+__all__ = ["BootstrapParams", "BootstrapProgram", "BootstrapSpec", "Requirements", "bootstrap",
            "bootstrap_iterated", "generate", "requirements"]

@@ -91,10 +91,13 @@ def test_series_schedule_values_and_depth(degree):
     assert np.abs(out.ct - want).max() < 1e-12
     depth = cheb.chebyshev_depth(coeffs)
     assert out.level == depth
-    # never more than one level above the information-theoretic minimum
-    assert depth <= math.ceil(math.log2(degree + 1)) + 1
-    if degree in (48, 59, 60):
-        assert depth == 6
+    # the minimum multiplicative depth of any degree-n evaluation
+    assert depth == math.ceil(math.log2(degree + 1))
+
+
+def test_depth_is_minimal_for_every_degree():
+    for n in range(1, 260):
+        assert cheb.chebyshev_depth(np.ones(n + 1)) == math.ceil(math.log2(n + 1)), n
 
 
 def test_clenshaw_matches_numpy_chebval():
@@ -144,7 +147,7 @@ def _horner_check(x, plan, rows):
 def test_bootstrap_model_recovers_message(log_n, budget):
     n = 1 << log_n
     rng = np.random.default_rng(log_n)
-    p = bs.EvalModParams()
+    p = bs.BootstrapParams()
     spec = bs.BootstrapSpec(log_slots=log_n, level_budget=budget)
     cts_plans, stc_plans = bs._plans(spec)
     z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
