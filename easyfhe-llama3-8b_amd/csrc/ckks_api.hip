@@ -310,9 +310,34 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
       h[2 * ns + (size_t)i * nd + t] = (u64)(((u128)pt << 64) % qt);  // Montgomery form
     }
   }
-  BCTable t{ns, nd, nullptr, sizeof(u64) * h.size()};
+  BCTable t{ns, nd, nullptr, sizeof(u64) * h.size(), nullptr, 0};
   HIPCHECK(hipMalloc(&t.d, t.bytes));
   HIPCHECK(hipMemcpy(t.d, h.data(), t.bytes, hipMemcpyHostToDevice));
+  // the fp64 kernel stages (ns + ns*nd) double pairs in a fixed LDS array
+  bool fp = ns + ns * nd <= kMaxDigitSize + kMaxDigitSize * 48;
+  for (u64 q : src) fp = fp && q < (1ull << 45);
+  if (fp) {
+    // (w, w / q) pairs for the fp64 modular product; hmod in plain form
+    std::vector<double> f(2 * ((size_t)ns + (size_t)ns * nd));
+    for (int i = 0; i < ns; i++) {
+      f[2 * i] = (double)h[i];
+      f[2 * i + 1] = (double)h[i] / (double)src[i];
+    }
+    for (int i = 0; i < ns; i++) {
+      for (int t2 = 0; t2 < nd; t2++) {
+        const u64 qt = dst[t2];
+        u64 pt = 1;
+        for (int j = 0; j < ns; j++)
+          if (j != i) pt = mulmod_h(pt, src[j] % qt, qt);
+        const size_t o = 2 * ((size_t)ns + (size_t)i * nd + t2);
+        f[o] = (double)pt;
+        f[o + 1] = (double)pt / (double)qt;
+      }
+    }
+    t.fbytes = sizeof(double) * f.size();
+    HIPCHECK(hipMalloc(&t.fd, t.fbytes));
+    HIPCHECK(hipMemcpy(t.fd, f.data(), t.fbytes, hipMemcpyHostToDevice));
+  }
   return t;
 }
 
@@ -581,8 +606,14 @@ static void free_context(ckks_context *c) {
   if (!c) return;
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (auto &kv : c->keys) (void)hipFree(kv.second.data);
-  for (auto &kv : c->bc_up) (void)hipFree(kv.second.d);
-  for (auto &kv : c->bc_down) (void)hipFree(kv.second.d);
+  for (auto &kv : c->bc_up) {
+    (void)hipFree(kv.second.d);
+    if (kv.second.fd) (void)hipFree(kv.second.fd);
+  }
+  for (auto &kv : c->bc_down) {
+    (void)hipFree(kv.second.d);
+    if (kv.second.fd) (void)hipFree(kv.second.fd);
+  }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
   for (auto &kv : c->rescale_c) (void)hipFree(kv.second);
   for (auto &kv : c->garner) (void)hipFree(kv.second);
@@ -734,9 +765,24 @@ static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
   u64 *conv = s.get((size_t)n * 2 * limbs * N);
   launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
                        2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+  const u64 *pinv = pinv_table(c, limbs);
+  if (c->logN == 16 && n <= kMaxBatch) {
+    // NTT of the conversion with the combine fused into its last pass
+    Batch a0{}, a1{}, o0{}, o1{};
+    std::vector<u64> gal(n);
+    for (int i = 0; i < n; i++) {
+      a0.p[i] = (u64 *)jobs[i].add0;
+      a1.p[i] = (u64 *)jobs[i].add1;
+      o0.p[i] = jobs[i].out0;
+      o1.p[i] = jobs[i].out1;
+      gal[i] = jobs[i].galois;
+    }
+    launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, Strided{acc, 2 * E * N}, E,
+                       pinv, a0, a1, gal.data(), o0, o1);
+    return;
+  }
   launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2 * n, 0,
              limbs, limbs, false);
-  const u64 *pinv = pinv_table(c, limbs);
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
     Batch a0{}, a1{}, o0{}, o1{};

@@ -148,6 +148,10 @@ struct BCTable {  // fast basis conversion constants, device resident
   int ns, nd;
   u64 *d;  // [ns] hinv, [ns] hinv_shoup, [ns*nd] hmod (Montgomery form), [nd] Q mod t
   size_t bytes;
+  // every source prime below 2^45: fp64 table [ns] (hinv, hinv / q_i),
+  // [ns*nd] (hmod, hmod / t) with hmod in [0, t); null otherwise
+  double *fd;
+  size_t fbytes;
 };
 
 struct FFTTable {  // encoder tables for one slot count n
@@ -232,6 +236,9 @@ void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, i
                            int limbs);
 void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
                             const Batch &out, int n_items, int limbs, const u64 *consts);
+void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
+                        int E, const u64 *pinv, const Batch &add0, const Batch &add1,
+                        const u64 *galois, const Batch &out0, const Batch &out1);
 void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target);
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
                 int limbs);

@@ -249,6 +249,53 @@ __device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u6
 
 __device__ __forceinline__ int lds16(int r, int c) { return r * 272 + c + (c >> 4); }
 
+// ModDown epilogue of the forward low pass (conv items 2 i + c):
+// out_c[l][k] = (acc_c[l][k] - NTT(conv_c)[l][k]) P^-1 + add_c[l][sigma(k)]
+struct Galois64 {
+  u64 g[kMaxBatch];
+};
+
+struct MDCombine {
+  Strided acc;  // item layout [2][E][N]
+  int E;
+  const u64 *pinv;  // per Q limb: P^-1, shoup
+  Batch add0, add1, out0, out1;
+  Galois64 gal;
+};
+
+// Operands of the epilogue for the 16 outputs e(k) = tile + rl 256 + c0 + 16 k
+// of one thread, loaded at kernel entry so that their latency overlaps the
+// butterflies: acc - is kept, add (or 0) is summed in.
+struct MDPrefetch {
+  u64 a[16], d[16];
+};
+
+__device__ __forceinline__ void md_load(const MDCombine &md, int item2, int limb, u32 e0,
+                                        MDPrefetch &pf) {
+  const int item = item2 >> 1, comp = item2 & 1;
+  const size_t N = 65536;
+  const u64 *acc = md.acc.base + item * md.acc.stride + ((size_t)comp * md.E + limb) * N;
+  const u64 *ad = comp ? batch_ptr(md.add1, item) : batch_ptr(md.add0, item);
+  const u64 g = md.gal.g[item];
+#pragma unroll
+  for (int k = 0; k < 16; k++) pf.a[k] = acc[e0 + 16 * k];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const u32 e = e0 + 16 * k;
+    pf.d[k] = ad ? ad[(size_t)limb * N + (g == 1 ? e : autom_index(e, g, 16))] : 0;
+  }
+}
+
+__device__ __forceinline__ void md_store(const MDCombine &md, int item2, int limb, u32 e, u64 y,
+                                         u64 a, u64 d, u64 q) {
+  const int item = item2 >> 1, comp = item2 & 1;
+  const size_t N = 65536;
+  u64 r = shoup_mul(sub_mod(a, y, q), md.pinv[2 * limb], md.pinv[2 * limb + 1], q);
+  r = add_mod(r, d, q);
+  u64 *o = comp ? batch_ptr(md.out1, item) : batch_ptr(md.out0, item);
+  o[(size_t)limb * N + e] = r;
+}
+
 // forward, bit positions 15..8: tile = 256 rows (stride 256) x 16 columns
 __global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
@@ -301,10 +348,13 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, in
 }
 
 // forward, bit positions 7..0: tile = 16 contiguous rows of 256; output in [0, q)
+// (COMBINE: the ModDown epilogue instead of the store)
+template <bool COMBINE>
 __global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, int q_limbs,
                                                        int L, const ModQ *__restrict__ mods,
                                                        const u64 *__restrict__ psi,
-                                                       const u64 *__restrict__ psi_sh) {
+                                                       const u64 *__restrict__ psi_sh,
+                                                       MDCombine md) {
   __shared__ u64 sm[16 * 272];
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
@@ -315,9 +365,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, i
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;  // global row of 256
   u64 x[16];
+  MDPrefetch pf;
   // round A: column = c0 + 16 k, stages on column bits 7..4
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = base[rl * 256 + c0 + 16 * k];
+  if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
 #pragma unroll
   for (int st = 0; st < 4; st++) {
     const int b = 7 - st, half = 8 >> st;
@@ -352,8 +404,15 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, i
     sm[lds16(rl, 16 * c0 + j)] = a >= q ? a - q : a;
   }
   __syncthreads();
+  if constexpr (COMBINE) {
 #pragma unroll
-  for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
+    for (int k = 0; k < 16; k++)
+      md_store(md, blockIdx.y, limb, (u32)(blockIdx.x * 4096 + rl * 256 + c0 + 16 * k),
+               sm[lds16(rl, c0 + 16 * k)], pf.a[k], pf.d[k], q);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
+  }
 }
 
 // inverse, bit positions 0..7 (first pass): input in [0, 2q), output lazy
@@ -560,9 +619,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_high(Batch src, Batch dst, i
   for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = dbl_bits(x[j]);
 }
 
+template <bool COMBINE>
 __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, int q_limbs,
                                                         int L, const ModQ *__restrict__ mods,
-                                                        const double2 *__restrict__ tw) {
+                                                        const double2 *__restrict__ tw,
+                                                        MDCombine md) {
   __shared__ double sm[16 * 272];
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
@@ -572,8 +633,10 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, 
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
   double x[16];
+  MDPrefetch pf;
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = as_dbl(base[rl * 256 + c0 + 16 * k]);
+  if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
 #pragma unroll
   for (int st = 0; st < 4; st++) {
     const int b = 7 - st, half = 8 >> st;
@@ -604,8 +667,16 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, 
 #pragma unroll
   for (int j = 0; j < 16; j++) smu[lds16(rl, 16 * c0 + j)] = fp_canon(x[j], qinv, q);
   __syncthreads();
+  if constexpr (COMBINE) {
+    const u64 qu = mods[p].q;
 #pragma unroll
-  for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = smu[lds16(rl, c0 + 16 * k)];
+    for (int k = 0; k < 16; k++)
+      md_store(md, blockIdx.y, limb, (u32)(blockIdx.x * 4096 + rl * 256 + c0 + 16 * k),
+               smu[lds16(rl, c0 + 16 * k)], pf.a[k], pf.d[k], qu);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = smu[lds16(rl, c0 + 16 * k)];
+  }
 }
 
 __global__ __launch_bounds__(TPB) void k_ntt16f_inv_low(Batch src, Batch dst, int l_begin,
@@ -714,8 +785,8 @@ static void ntt16_launch(ckks_context *c, bool fp, const Batch &src, const Batch
       hipLaunchKernelGGL(k_ntt16f_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
                          c->L, c->d_mods, tw);
       LAUNCH_CHECK();
-      hipLaunchKernelGGL(k_ntt16f_fwd_low, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
-                         c->d_mods, tw);
+      hipLaunchKernelGGL(k_ntt16f_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin,
+                         q_limbs, c->L, c->d_mods, tw, MDCombine{});
       LAUNCH_CHECK();
     } else {
       hipLaunchKernelGGL(k_ntt16f_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
@@ -731,8 +802,8 @@ static void ntt16_launch(ckks_context *c, bool fp, const Batch &src, const Batch
     hipLaunchKernelGGL(k_ntt16_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
                        c->L, c->d_mods, c->d_psi, c->d_psi_sh);
     LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_ntt16_fwd_low, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
-                       c->d_mods, c->d_psi, c->d_psi_sh);
+    hipLaunchKernelGGL(k_ntt16_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin,
+                       q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh, MDCombine{});
     LAUNCH_CHECK();
   } else {
     hipLaunchKernelGGL(k_ntt16_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
@@ -802,6 +873,48 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
     case 16: ntt16_dispatch(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     case 17: ntt_dispatch<8, 9, 4096>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
     default: throw std::invalid_argument("log_n must be in [10, 17]");
+  }
+}
+
+// Forward NTT of the ModDown conversion conv (2 n items, Q limbs) with the
+// combine of k_moddown_combine fused into the low pass: the converted P part
+// is never written back.  N = 2^16 only.
+void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
+                        int E, const u64 *pinv, const Batch &add0, const Batch &add1,
+                        const u64 *galois, const Batch &out0, const Batch &out1) {
+  if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
+  MDCombine md{};
+  md.acc = acc;
+  md.E = E;
+  md.pinv = pinv;
+  md.add0 = add0;
+  md.add1 = add1;
+  md.out0 = out0;
+  md.out1 = out1;
+  for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
+  int start = 0;
+  while (start < limbs) {
+    const bool fp = c->prime_fp[start] != 0;
+    int stop = start + 1;
+    while (stop < limbs && (c->prime_fp[stop] != 0) == fp) stop++;
+    dim3 block(TPB), grid(16, 2 * n, stop - start);
+    if (fp) {
+      const double2 *tw = (const double2 *)c->d_tw_fp;
+      hipLaunchKernelGGL(k_ntt16f_fwd_high, grid, block, 0, c->stream, conv, conv, start, limbs,
+                         c->L, c->d_mods, tw);
+      LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_ntt16f_fwd_low<true>, grid, block, 0, c->stream, conv, start, limbs,
+                         c->L, c->d_mods, tw, md);
+      LAUNCH_CHECK();
+    } else {
+      hipLaunchKernelGGL(k_ntt16_fwd_high, grid, block, 0, c->stream, conv, conv, start, limbs,
+                         c->L, c->d_mods, c->d_psi, c->d_psi_sh);
+      LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_ntt16_fwd_low<true>, grid, block, 0, c->stream, conv, start, limbs,
+                         c->L, c->d_mods, c->d_psi, c->d_psi_sh, md);
+      LAUNCH_CHECK();
+    }
+    start = stop;
   }
 }
 
@@ -946,9 +1059,9 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
   const int words = 2 * ns + ns * nd + nd;
   for (int i = threadIdx.x; i < words; i += TPB) st[i] = tab[i];
   __syncthreads();
-  const int k = blockIdx.x * TPB + threadIdx.x;
   const u64 *in = batch_ptr(src, blockIdx.y);
   u64 *out = batch_ptr(dst, blockIdx.y);
+  const int k = blockIdx.x * TPB + threadIdx.x;
   u64 v[kMaxDigitSize];
   u64 cnt = 0;
 #pragma unroll
@@ -997,13 +1110,127 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
   }
 }
 
+// fp64 variant for source primes below 2^45: v_i = [x_i hinv_i]_{q_i} by the
+// exact fp64 product (centered: v_i in (-q_i/2, q_i/2] directly), and for a
+// target t below 2^45 y_t = sum_i [v_i hmod_i]_t as exact fp64 residues, one
+// final reduction.  The exact integer sum is the same as the 64-bit kernel's,
+// so the output words are identical; a wider target (q_0) keeps the 128-bit
+// Montgomery accumulation of k_basis_convert.
+__global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
+    Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
+    const double2 *__restrict__ ftab, int src_prime0, int t_split, int t_skip, int q_limbs,
+    int L, int centered, const ModQ *__restrict__ mods) {
+  __shared__ u64 st[2 * kMaxDigitSize + kMaxDigitSize * 48 + 48];
+  __shared__ double2 sf[kMaxDigitSize + kMaxDigitSize * 48];
+  const int words = 2 * ns + ns * nd + nd;
+  for (int i = threadIdx.x; i < words; i += TPB) st[i] = tab[i];
+  for (int i = threadIdx.x; i < ns + ns * nd; i += TPB) sf[i] = ftab[i];
+  __syncthreads();
+  const u64 *in = batch_ptr(src, blockIdx.y);
+  u64 *out = batch_ptr(dst, blockIdx.y);
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  // v_i as exact doubles: canonical, or centered when asked (only these stay
+  // live across the target loop, to keep the register count and so the
+  // occupancy of this latency-bound kernel up)
+  double vd[kMaxDigitSize];
+#pragma unroll
+  for (int i = 0; i < kMaxDigitSize; i++) {
+    if (i < ns) {
+      const double q = (double)mods[src_prime0 + i].q;
+      double v = fp_mulmod((double)in[((size_t)i << logN) + k], sf[i].x, sf[i].y, q);
+      v = v < 0.0 ? __dadd_rn(v, q) : v;
+      v = v >= q ? __dsub_rn(v, q) : v;
+      if (centered && v > __dmul_rn(__dsub_rn(q, 1.0), 0.5)) v = __dsub_rn(v, q);
+      vd[i] = v;
+    }
+  }
+  const double2 *hf = sf + ns;
+  const u64 *hm = st + 2 * ns;
+  const u64 *qm = hm + (size_t)ns * nd;
+  // wide target (q_0): 128-bit Montgomery accumulation of the canonical v,
+  // minus cnt Q for the centered ones
+  auto wide = [&](int t) {
+    const int tl = t < t_split ? t : t + t_skip;
+    const ModQ M = mods[prime_of(tl, q_limbs, L)];
+    u64 hi = 0, lo = 0, cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i++) {
+      if (i < ns) {
+        const double v = vd[i];
+        const u64 vu = v < 0.0 ? (u64)__dadd_rn(v, (double)mods[src_prime0 + i].q) : (u64)v;
+        cnt += v < 0.0 ? 1 : 0;
+        mac_wide(hi, lo, vu, hm[i * nd + t]);
+      }
+    }
+    u64 y = redc(hi, lo, M.q, M.qinv);
+    if (cnt) y = sub_mod(y, mul_mod(cnt, qm[t], M), M.q);
+    out[((size_t)tl << logN) + k] = y;
+  };
+  auto narrow = [&](int t) {
+    const int tl = t < t_split ? t : t + t_skip;
+    const double q = (double)mods[prime_of(tl, q_limbs, L)].q;
+    double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i += 2) {
+      if (i < ns) {
+        const double2 h = hf[i * nd + t];
+        a0 = __dadd_rn(a0, fp_mulmod(vd[i], h.x, h.y, q));
+      }
+      if (i + 1 < ns) {
+        const double2 h = hf[(i + 1) * nd + t];
+        a1 = __dadd_rn(a1, fp_mulmod(vd[i + 1], h.x, h.y, q));
+      }
+    }
+    out[((size_t)tl << logN) + k] = fp_canon(__dadd_rn(a0, a1), 1.0 / q, q);
+  };
+  int t = 0;
+  for (; t + 1 < nd; t += 2) {
+    const int tl0 = t < t_split ? t : t + t_skip;
+    const int tl1 = t + 1 < t_split ? t + 1 : t + 1 + t_skip;
+    const u64 q0u = mods[prime_of(tl0, q_limbs, L)].q, q1u = mods[prime_of(tl1, q_limbs, L)].q;
+    if (q0u >= (1ull << 45) || q1u >= (1ull << 45)) {
+      if (q0u >= (1ull << 45)) wide(t); else narrow(t);
+      if (q1u >= (1ull << 45)) wide(t + 1); else narrow(t + 1);
+      continue;
+    }
+    // two fp64 targets: four independent accumulation chains
+    const double q0 = (double)q0u, q1 = (double)q1u;
+    double a0 = 0.0, a1 = 0.0, b0 = 0.0, b1 = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i += 2) {
+      if (i < ns) {
+        const double2 h0 = hf[i * nd + t], h1 = hf[i * nd + t + 1];
+        a0 = __dadd_rn(a0, fp_mulmod(vd[i], h0.x, h0.y, q0));
+        b0 = __dadd_rn(b0, fp_mulmod(vd[i], h1.x, h1.y, q1));
+      }
+      if (i + 1 < ns) {
+        const double2 h0 = hf[(i + 1) * nd + t], h1 = hf[(i + 1) * nd + t + 1];
+        a1 = __dadd_rn(a1, fp_mulmod(vd[i + 1], h0.x, h0.y, q0));
+        b1 = __dadd_rn(b1, fp_mulmod(vd[i + 1], h1.x, h1.y, q1));
+      }
+    }
+    out[((size_t)tl0 << logN) + k] = fp_canon(__dadd_rn(a0, a1), 1.0 / q0, q0);
+    out[((size_t)tl1 << logN) + k] = fp_canon(__dadd_rn(b0, b1), 1.0 / q1, q1);
+  }
+  if (t < nd) {
+    const int tl = t < t_split ? t : t + t_skip;
+    if (mods[prime_of(tl, q_limbs, L)].q >= (1ull << 45)) wide(t); else narrow(t);
+  }
+}
+
 void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered) {
   dim3 grid(c->N / TPB, n_items);
-  hipLaunchKernelGGL(k_basis_convert, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
-                     t.nd, t.d, src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0,
-                     c->d_mods);
+  if (t.fd) {
+    hipLaunchKernelGGL(k_basis_convert_fp, grid, dim3(TPB), 0, c->stream, src, dst, c->logN,
+                       t.ns, t.nd, t.d, (const double2 *)t.fd, src_prime0, t_split, t_skip,
+                       q_limbs, c->L, centered ? 1 : 0, c->d_mods);
+  } else {
+    hipLaunchKernelGGL(k_basis_convert, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
+                       t.nd, t.d, src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0,
+                       c->d_mods);
+  }
   LAUNCH_CHECK();
 }
 
@@ -1078,10 +1305,6 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
 // out_c are [limbs][N] polynomials per item (a null add pointer adds
 // nothing).  grid (N / 256, limbs, 2 * items)
 // ===========================================================================
-
-struct Galois64 {
-  u64 g[kMaxBatch];
-};
 
 __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch add1,
                                   Galois64 gal, Batch out0, Batch out1, int logN, int limbs,
