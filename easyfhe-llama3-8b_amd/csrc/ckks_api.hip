@@ -588,6 +588,18 @@ static void build_context(ckks_context *c, const ckks_params &p) {
   up(&c->d_ipsi, ipsi);
   up(&c->d_ipsi_sh, ipsi_sh);
   up(&c->d_ninv, ninv);
+  {
+    // P mod q_i (and its Shoup companion) for the extended-basis lifts
+    std::vector<u64> pm(2 * (size_t)c->L);
+    for (int i = 0; i < c->L; i++) {
+      const u64 q = c->primes[i];
+      u64 P = 1;
+      for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
+      pm[2 * i] = P;
+      pm[2 * i + 1] = shoup_h(P, q);
+    }
+    up(&c->d_pmod, pm);
+  }
 
   // secret: sampled on the host (client side), moved to every prime's NTT domain
   c->secret = sample_secret(p.seed, N, p.secret_mode, p.hamming_weight);
@@ -630,6 +642,7 @@ static void free_context(ckks_context *c) {
   (void)hipFree(c->d_ipsi);
   (void)hipFree(c->d_ipsi_sh);
   (void)hipFree(c->d_ninv);
+  (void)hipFree(c->d_pmod);
   (void)hipFree(c->d_secret);
   c->pool.trim();
   if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -736,29 +749,14 @@ struct KsJob {
   u64 *out0, *out1;
 };
 
-// Key inner product for every job, ModDown, and the combine with addends.
-static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
-                      const std::vector<KsJob> &jobs, Scratch &s) {
+// ModDown of n accumulators acc = [n][2][E][N] (Q limbs then P limbs) into
+// the jobs' outputs, adding each job's addends (sigma-permuted): the P-part
+// iNTT, the centered conversion, then the forward NTT with the combine.
+static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<KsJob> &jobs,
+                       Scratch &s) {
   const size_t N = c->N;
-  const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const int E = limbs + c->alpha;
   const int n = (int)jobs.size();
-  const size_t est = (size_t)digits * E * N;
-  u64 *acc = s.get((size_t)n * 2 * E * N);
-  bool shared = true;
-  for (int i = 0; i < n; i++)
-    shared = shared && jobs[i].ext_item == i && jobs[i].key == jobs[0].key &&
-             jobs[i].galois == jobs[0].galois;
-  if (shared) {
-    launch_key_inner(c, strided((u64 *)ext, est), strided(acc, 2 * E * N), n, *jobs[0].key,
-                     digits, E, limbs, jobs[0].galois);
-  } else {
-    for (int i = 0; i < n; i++)
-      launch_key_inner(c, strided((u64 *)ext + (size_t)jobs[i].ext_item * est, 0),
-                       strided(acc + (size_t)i * 2 * E * N, 0), 1, *jobs[i].key, digits, E,
-                       limbs, jobs[i].galois);
-  }
-  (void)n_ext;
-  // ModDown: iNTT of the P limbs of both components
   u64 *ptmp = s.get((size_t)n * 2 * c->alpha * N);
   launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N),
              2 * n, limbs, c->alpha, limbs, true);
@@ -799,6 +797,38 @@ static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
     Strided sconv{conv + (size_t)b0 * 2 * limbs * N, 2 * limbs * N};
     launch_moddown_combine(c, sacc, sconv, a0, a1, gal.data(), o0, o1, nb, limbs, E, pinv);
   }
+}
+
+// Key inner product of every job into [n][2][E][N] accumulators.
+static u64 *ks_inner(ckks_context *c, int limbs, const u64 *ext, const std::vector<KsJob> &jobs,
+                     Scratch &s) {
+  const size_t N = c->N;
+  const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const int n = (int)jobs.size();
+  const size_t est = (size_t)digits * E * N;
+  u64 *acc = s.get((size_t)n * 2 * E * N);
+  bool shared = true;
+  for (int i = 0; i < n; i++)
+    shared = shared && jobs[i].ext_item == i && jobs[i].key == jobs[0].key &&
+             jobs[i].galois == jobs[0].galois;
+  if (shared) {
+    launch_key_inner(c, strided((u64 *)ext, est), strided(acc, 2 * E * N), n, *jobs[0].key,
+                     digits, E, limbs, jobs[0].galois);
+  } else {
+    for (int i = 0; i < n; i++)
+      launch_key_inner(c, strided((u64 *)ext + (size_t)jobs[i].ext_item * est, 0),
+                       strided(acc + (size_t)i * 2 * E * N, 0), 1, *jobs[i].key, digits, E,
+                       limbs, jobs[i].galois);
+  }
+  return acc;
+}
+
+// Key inner product for every job, ModDown, and the combine with addends.
+static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
+                      const std::vector<KsJob> &jobs, Scratch &s) {
+  (void)n_ext;
+  u64 *acc = ks_inner(c, limbs, ext, jobs, s);
+  ks_moddown(c, limbs, acc, jobs, s);
 }
 
 static const DeviceKey &get_key(ckks_context *c, u64 galois) {
@@ -1238,10 +1268,14 @@ int ckks_mul_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **
   check_ct(c, pt, "mul_pt");
   require(out, "null argument");
   require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
-  require(!a->is_ext && !pt->is_ext, "mul_pt expects Q-basis operands");
-  ckks_ct *o = new_ct(c, a->polys, a->limbs, 0, a->slots, a->scale * pt->scale,
+  if (a->is_ext)  // Q u P basis: the plaintext's P limbs must follow the same Q limbs
+    require(pt->is_ext && pt->limbs == a->limbs,
+            "an extended ciphertext needs an extended plaintext at its level");
+  ckks_ct *o = new_ct(c, a->polys, a->limbs, a->is_ext, a->slots, a->scale * pt->scale,
                       a->scale_degree + pt->scale_degree);
-  launch_mul_pt(c, a->d, pt->d, o->d, a->polys, a->limbs, a->limbs);
+  // a Q-basis product uses the leading (Q) limbs of an extended plaintext
+  launch_mul_pt(c, a->d, pt->d, o->d, a->polys, a->limbs + (a->is_ext ? c->alpha : 0),
+                a->limbs);
   *out = o;
   API_END
 }
@@ -1539,10 +1573,10 @@ int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
     for (int b = 0; b < B; b++) bp.p[b] = pts[g * B + b]->d;
     if (!acc) {
       acc = new_ct(c, 2, limbs, 0, babies[0]->slots, scale, sdeg);
-      launch_mac(c, bb, bp, B, acc->d, limbs);
+      launch_mac(c, bb, bp, B, acc->d, limbs, limbs);
       continue;
     }
-    launch_mac(c, bb, bp, B, inner, limbs);
+    launch_mac(c, bb, bp, B, inner, limbs, limbs);
     ckks_ct *rot = new_ct(c, 2, limbs, 0, acc->slots, scale, sdeg);
     if (gg == 1)
       HIPCHECK(hipMemcpyAsync(rot->d, acc->d, acc->bytes, hipMemcpyDeviceToDevice, c->stream));
@@ -1554,6 +1588,127 @@ int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
     free_ct(rot);
   }
   *out = acc;
+  API_END
+}
+
+// Extended-basis babies of `a` for the given rotations, each [2][E][N]
+// before its ModDown: (P c0, P c1) for offset 0, (P sigma(c0) + acc_0, acc_1)
+// otherwise; one ModUp is shared by all of them.
+static void ext_babies(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,
+                       u64 *const *dst, Scratch &s) {
+  const int limbs = a->limbs, E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  std::vector<u64> gal(n);
+  bool any = false;
+  for (int b = 0; b < n; b++) {
+    gal[b] = galois_of(c, rotations[b]);
+    if (gal[b] != 1) {
+      get_key(c, gal[b]);
+      any = true;
+    }
+  }
+  u64 *ext = nullptr;
+  if (any) {
+    ext = s.get((size_t)digits * E * N);
+    const u64 *d1 = a->d + P;
+    ks_modup(c, limbs, 1, &d1, ext, s);
+  }
+  for (int b = 0; b < n; b++) {
+    if (gal[b] == 1) {
+      launch_ext_identity(c, a->d, dst[b], limbs);
+      continue;
+    }
+    launch_key_inner(c, strided(ext, 0), strided(dst[b], 0), 1, get_key(c, gal[b]), digits, E,
+                     limbs, gal[b]);
+    launch_ext_add_pc0(c, a->d, dst[b], limbs, gal[b]);
+  }
+}
+
+int ckks_hoisted_mac_sum_ext(ckks_context *c, const ckks_ct *a, const int64_t *baby_rotations,
+                             int B, const ckks_ct *const *pts, int64_t giant_rotation,
+                             int giant_count, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "hoisted_mac_sum_ext");
+  require(baby_rotations && pts && out, "null argument");
+  require(B >= 1 && B <= kMaxBatch, "baby count must be in [1, 64]");
+  require(giant_count >= 1, "giant_count must be positive");
+  require(a->polys == 2 && !a->is_ext, "hoisted_mac_sum_ext expects a degree-1 Q-basis ciphertext");
+  const int limbs = a->limbs, E = limbs + c->alpha;
+  for (int i = 0; i < B * giant_count; i++) {
+    check_ct(c, pts[i], "hoisted_mac_sum_ext");
+    require(pts[i]->polys == 1 && pts[i]->is_ext && pts[i]->limbs == limbs,
+            "plaintexts must be extended (Q u P) at the ciphertext's level");
+  }
+  const u64 gg = galois_of(c, giant_rotation);
+  if (giant_count > 1 && gg != 1) get_key(c, gg);
+  const double scale = a->scale * pts[0]->scale;
+  const int sdeg = a->scale_degree + pts[0]->scale_degree;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  Scratch s(c);
+  u64 *bab = s.get((size_t)B * 2 * E * N);
+  std::vector<u64 *> bp(B);
+  Batch bb{};
+  for (int b = 0; b < B; b++) bb.p[b] = bp[b] = bab + (size_t)b * 2 * E * N;
+  ext_babies(c, a, baby_rotations, B, bp.data(), s);
+  u64 *inner_ext = s.get(2 * (size_t)E * N);
+  u64 *inner = s.get(2 * P);
+  ckks_ct *acc = nullptr;
+  for (int g = giant_count - 1; g >= 0; g--) {
+    Batch ptb{};
+    for (int b = 0; b < B; b++) ptb.p[b] = pts[g * B + b]->d;
+    launch_mac(c, bb, ptb, B, inner_ext, E, limbs);
+    const bool first = acc == nullptr;
+    if (first) acc = new_ct(c, 2, limbs, 0, a->slots, scale, sdeg);
+    u64 *dst = first ? acc->d : inner;
+    {
+      Scratch s2(c);
+      std::vector<KsJob> jobs{KsJob{0, nullptr, 1, nullptr, nullptr, dst, dst + P}};
+      ks_moddown(c, limbs, inner_ext, jobs, s2);
+    }
+    if (first) continue;
+    ckks_ct *rot = new_ct(c, 2, limbs, 0, acc->slots, scale, sdeg);
+    if (gg == 1)
+      HIPCHECK(hipMemcpyAsync(rot->d, acc->d, acc->bytes, hipMemcpyDeviceToDevice, c->stream));
+    else {
+      const ckks_ct *ac = acc;
+      rotate_batch(c, &ac, 1, gg, &rot);
+    }
+    launch_addsub(c, rot->d, inner, acc->d, 2, limbs, limbs, 0);
+    free_ct(rot);
+  }
+  *out = acc;
+  API_END
+}
+
+int ckks_hoisted_rotate_ext(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,
+                            ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "hoisted_rotate_ext");
+  require(rotations && out, "null argument");
+  require(n >= 1, "need at least one rotation");
+  require(a->polys == 2 && !a->is_ext, "hoisted_rotate_ext expects a degree-1 Q-basis ciphertext");
+  for (int r = 0; r < n; r++) out[r] = nullptr;
+  std::vector<u64 *> dst(n);
+  for (int r = 0; r < n; r++) {
+    out[r] = new_ct(c, 2, a->limbs, 1, a->slots, a->scale, a->scale_degree);
+    dst[r] = out[r]->d;
+  }
+  Scratch s(c);
+  ext_babies(c, a, rotations, n, dst.data(), s);
+  API_END
+}
+
+int ckks_moddown_ext(ckks_context *c, const ckks_ct *a, ckks_ct **out) {
+  API_BEGIN
+  check_ct(c, a, "moddown_ext");
+  require(out, "null argument");
+  require(a->polys == 2 && a->is_ext, "moddown_ext expects a degree-1 extended ciphertext");
+  const size_t P = (size_t)a->limbs * c->N;
+  ckks_ct *o = new_ct(c, 2, a->limbs, 0, a->slots, a->scale, a->scale_degree);
+  Scratch s(c);
+  std::vector<KsJob> jobs{KsJob{0, nullptr, 1, nullptr, nullptr, o->d, o->d + P}};
+  ks_moddown(c, a->limbs, a->d, jobs, s);
+  *out = o;
   API_END
 }
 

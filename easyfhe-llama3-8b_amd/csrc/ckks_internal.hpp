@@ -185,6 +185,7 @@ struct ckks_context {
   std::map<std::pair<int, int>, ckks::BCTable> bc_up;  // (limbs, digit)
   std::map<int, ckks::BCTable> bc_down;                // limbs
   std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
+  u64 *d_pmod = nullptr;         // [L][2] P mod q_i, shoup (extended-basis lifts)
   std::map<int, u64 *> rescale_c;  // limbs -> [limbs-1][4] ql mod qi, ql^-1, shoup
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
@@ -240,8 +241,12 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         int E, const u64 *pinv, const Batch &add0, const Batch &add1,
                         const u64 *galois, const Batch &out0, const Batch &out1);
 void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target);
+void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);
+void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64 galois);
+// MAC over limbs_total limbs per component; limbs >= q_limbs are special
+// limbs (an extended object: Q limbs then alpha P limbs)
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
-                int limbs);
+                int limbs_total, int q_limbs);
 void launch_keygen(ckks_context *c, DeviceKey &key, u64 id, int relin, u64 galois);
 // residues of a signed integer polynomial e[N] over `limbs` limbs, then NTT
 void launch_expand_ntt(ckks_context *c, const long long *e, u64 *out, int limbs, int q_limbs);

@@ -1420,11 +1420,11 @@ void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int
 // ===========================================================================
 
 __global__ void k_mac(Batch babies, Batch pts, int B, u64 *__restrict__ out, int logN,
-                      int limbs, const ModQ *__restrict__ mods) {
+                      int limbs, int q_limbs, int L, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = blockIdx.y, comp = blockIdx.z;
   const size_t N = (size_t)1 << logN;
-  const ModQ M = mods[l];
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
   const size_t off = ((size_t)comp * limbs + l) * N + k;
   u64 acc = 0, hi = 0, lo = 0;
   for (int b = 0; b < B; b++) {
@@ -1438,10 +1438,54 @@ __global__ void k_mac(Batch babies, Batch pts, int B, u64 *__restrict__ out, int
 }
 
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
-                int limbs) {
-  dim3 grid(c->N / TPB, limbs, 2);
+                int limbs_total, int q_limbs) {
+  dim3 grid(c->N / TPB, limbs_total, 2);
   hipLaunchKernelGGL(k_mac, grid, dim3(TPB), 0, c->stream, babies, pts, B, out, c->logN,
-                     limbs, c->d_mods);
+                     limbs_total, q_limbs, c->L, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0
+// on the special limbs (layout [2][limbs + alpha][N]); grid (N / 256, E, 2)
+__global__ void k_ext_identity(const u64 *__restrict__ ct, u64 *__restrict__ out, int limbs,
+                               int E, int logN, const u64 *__restrict__ pmod,
+                               const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, comp = blockIdx.z;
+  const size_t N = (size_t)1 << logN;
+  u64 v = 0;
+  if (l < limbs)
+    v = shoup_mul(ct[((size_t)comp * limbs + l) * N + k], pmod[2 * l], pmod[2 * l + 1],
+                  mods[l].q);
+  out[((size_t)comp * E + l) * N + k] = v;
+}
+
+// A rotation baby before its ModDown: out_0 += P sigma(c0) on the Q limbs.
+// grid (N / 256, limbs)
+__global__ void k_ext_add_pc0(const u64 *__restrict__ ct, u64 *__restrict__ out, u64 galois,
+                              int logN, const u64 *__restrict__ pmod,
+                              const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const size_t N = (size_t)1 << logN;
+  const u64 q = mods[l].q;
+  const u32 kk = autom_index((u32)k, galois, logN);
+  const u64 t = shoup_mul(ct[(size_t)l * N + kk], pmod[2 * l], pmod[2 * l + 1], q);
+  u64 *o = out + (size_t)l * N + k;
+  *o = add_mod(*o, t, q);
+}
+
+void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs) {
+  dim3 grid(c->N / TPB, limbs + c->alpha, 2);
+  hipLaunchKernelGGL(k_ext_identity, grid, dim3(TPB), 0, c->stream, ct, out, limbs,
+                     limbs + c->alpha, c->logN, c->d_pmod, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64 galois) {
+  dim3 grid(c->N / TPB, limbs);
+  hipLaunchKernelGGL(k_ext_add_pc0, grid, dim3(TPB), 0, c->stream, ct, out, galois, c->logN,
+                     c->d_pmod, c->d_mods);
   LAUNCH_CHECK();
 }
 

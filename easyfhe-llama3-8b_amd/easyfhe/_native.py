@@ -110,6 +110,9 @@ SIGNATURES = {
     "ckks_mul_relin_rescale_many": (I, [VP, VPP, VPP, I, VPP]),
     "ckks_hoisted_rotate": (I, [VP, VP, I64P, I, VPP]),
     "ckks_hoisted_mac_sum": (I, [VP, VPP, I, VPP, ctypes.c_int64, I, VPP]),
+    "ckks_hoisted_mac_sum_ext": (I, [VP, VP, I64P, I, VPP, ctypes.c_int64, I, VPP]),
+    "ckks_hoisted_rotate_ext": (I, [VP, VP, I64P, I, VPP]),
+    "ckks_moddown_ext": (I, [VP, VP, VPP]),
     "ckks_poly_ntt": (I, [VP, U64P, U64P, I, I, I, I]),
     "ckks_poly_modup": (I, [VP, U64P, I, U64P]),
     "ckks_poly_moddown": (I, [VP, U64P, I, U64P]),

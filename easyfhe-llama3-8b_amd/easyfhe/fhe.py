@@ -743,13 +743,27 @@ def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count
     ``sum_{g<G} rot_{g giant}( sum_{b<B} pt[g B + b] * rot_{baby_b}(ct) )``
     with a Horner chain over one giant key; unrescaled
     (reference operators/linear/operator.py:320-330, operators/transform.py:108).
-    The ext strategies evaluate the same schedule in the Q basis here; the
-    Q limbs of an extended plaintext are used as they are."""
+    Strategies "ext_normal" and "ext_double_hoist" with extended plaintexts
+    keep the babies in the Q u P basis and take one ModDown per giant group
+    instead of one per baby; with Q-basis plaintexts (or precomputed babies
+    or an anchor step) they run the normal schedule."""
     ctx = _ctx(ct, context)
     pts = plaintexts if isinstance(plaintexts, (list, tuple)) else [plaintexts]
     B = len(list(baby_offsets))
     if len(pts) < B * int(giant_count):
         raise ValueError(f"need {B * int(giant_count)} plaintexts, got {len(pts)}")
+    used = pts[: B * int(giant_count)]
+    if (strategy in ("ext_normal", "ext_double_hoist") and baby_rotations is None
+            and int(baby_anchor_step) < 2 and all(p.is_ext for p in used)):
+        # babies kept in Q u P, one ModDown per giant group
+        offs = np.asarray([int(o) for o in baby_offsets], dtype=np.int64)
+        out = ctypes.c_void_p()
+        check(lib.ckks_hoisted_mac_sum_ext(ctx.handle, ct.handle,
+                                           offs.ctypes.data_as(_native.I64P), B,
+                                           ptr_array([p.handle for p in used]),
+                                           int(giant_offset), int(giant_count),
+                                           ctypes.byref(out)))
+        return _wrap(ctx, out)
     babies = baby_rotations
     owned = False
     if babies is None:
@@ -806,17 +820,35 @@ def unpack_cipher_batch(batch: CipherBatch) -> tuple:
     return tuple(batch.cv)
 
 
+def _hoisted_ext(ct: Ciphertext, offsets: Sequence[int], ctx: NativeContext) -> list:
+    offs = np.asarray([int(o) for o in offsets], dtype=np.int64)
+    outs = (ctypes.c_void_p * len(offs))()
+    check(lib.ckks_hoisted_rotate_ext(ctx.handle, ct.handle,
+                                      offs.ctypes.data_as(_native.I64P), len(offs), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(offs))]
+
+
 def fast_rotate(ct, offsets, context=None, output_ext: bool = False) -> CipherBatch:
-    """Hoisted rotations of one ciphertext into a batch (outputs in the Q
-    basis; ``moddown_from_ext`` is then the identity)."""
+    """Hoisted rotations of one ciphertext into a batch; with ``output_ext``
+    the outputs stay in the Q u P basis before their ModDown (P rot_k(ct)),
+    to be multiplied by extended plaintexts, summed and brought back with one
+    ``moddown_from_ext`` (reference operators/attention/input.py:792-826)."""
     ctx = _ctx(ct, context)
-    return CipherBatch(_hoisted(ct, [int(o) for o in offsets], ctx))
+    offs = [int(o) for o in offsets]
+    if output_ext:
+        return CipherBatch(_hoisted_ext(ct, offs, ctx))
+    return CipherBatch(_hoisted(ct, offs, ctx))
 
 
 def moddown_from_ext(ct, context=None):
-    if ct.is_ext:
-        raise ValueError("extended-basis ciphertexts are not produced by this backend")
-    return ct.deep_copy()
+    """Q-basis copy of ``ct``: ModDown (division by P) of an extended
+    ciphertext, a plain copy otherwise."""
+    ctx = _ctx(ct, context)
+    if not ct.is_ext:
+        return ct.deep_copy()
+    out = ctypes.c_void_p()
+    check(lib.ckks_moddown_ext(ctx.handle, ct.handle, ctypes.byref(out)))
+    return _wrap(ctx, out)
 
 
 def grouped_pairwise_mac(batch: CipherBatch, plaintexts, groups, context=None) -> list:

@@ -171,6 +171,24 @@ int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
                          const ckks_ct *const *pts, int64_t giant_rotation,
                          int giant_count, ckks_ct **out);
 
+/* fhe.hoisted_mac_sum, strategies "ext_normal" / "ext_double_hoist" (reference
+ * operators/linear/operator.py:320-330, linear/config.py:296-305): the babies
+ * of `a` for baby_rotations stay in the Q u P basis (no ModDown), the
+ * plaintexts are extended (is_ext, at a's level), and each giant group is
+ * brought back to Q by one ModDown before the Horner chain over the giant key;
+ * result unrescaled. */
+int ckks_hoisted_mac_sum_ext(ckks_context *ctx, const ckks_ct *a, const int64_t *baby_rotations,
+                             int B, const ckks_ct *const *pts, int64_t giant_rotation,
+                             int giant_count, ckks_ct **out);
+/* fhe.fast_rotate(..., output_ext=True) (reference attention/input.py:792-826):
+ * hoisted rotations left in the Q u P basis, i.e. P rot_k(a) before ModDown;
+ * the outputs are extended ciphertexts at a's scale. */
+int ckks_hoisted_rotate_ext(ckks_context *ctx, const ckks_ct *a, const int64_t *rotations, int n,
+                            ckks_ct **out);
+/* fhe.moddown_from_ext (reference attention/input.py:1103-1169): an extended
+ * ciphertext divided by P (centered conversion) back to the Q basis. */
+int ckks_moddown_ext(ckks_context *ctx, const ckks_ct *a, ckks_ct **out);
+
 /* Raw polynomial transforms over host buffers [n_polys][limbs][N] with limb i
  * in prime i (i < q_limbs) or special prime i - q_limbs (parity tests). */
 int ckks_poly_ntt(ckks_context *ctx, const uint64_t *in, uint64_t *out,

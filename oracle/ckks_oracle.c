@@ -1320,3 +1320,87 @@ int orc_hoisted_mac_sum(const orc_ctx *c, const uint64_t *ct, int limbs,
   free(babies);
   return 0;
 }
+
+/* Extended-basis BSGS MAC (hoisted_mac_sum strategies "ext_normal" and
+ * "ext_double_hoist"): every baby stays in the Q u P basis, as
+ * (P sigma(c0) + acc_0, acc_1) for a rotation or (P c0, P c1) for offset 0,
+ * without its ModDown; the plaintexts carry P limbs ([G*B][limbs+alpha][N]);
+ * each giant group sum_b pt_b babies_b is brought back to Q by one ModDown,
+ * then the Horner chain over the giant key runs as in orc_hoisted_mac_sum. */
+int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
+                            const uint64_t *baby_gs, int B, const uint64_t *pts,
+                            uint64_t giant_g, int G, uint64_t *out) {
+  const int N = c->N, A = c->alpha, L = c->L, E = limbs + A;
+  const int digits = (limbs + c->ds - 1) / c->ds;
+  const size_t P = (size_t)limbs * N, EP = (size_t)E * N;
+  for (int b = 0; b < B; b++)
+    if (baby_gs[b] != 1 && !find_key(c, baby_gs[b])) return -1;
+  if (G > 1 && giant_g != 1 && !find_key(c, giant_g)) return -1;
+  u64 *ext = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
+  u64 *extg = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
+  u64 *bab = (u64 *)malloc(sizeof(u64) * (size_t)B * 2 * EP);
+  u64 *sc0 = (u64 *)malloc(sizeof(u64) * P);
+  u64 Pm[64];
+  for (int i = 0; i < limbs; i++) {
+    Pm[i] = 1;
+    for (int j = 0; j < A; j++) Pm[i] = orc_mulmod(Pm[i], c->primes[L + j] % c->primes[i], c->primes[i]);
+  }
+  orc_modup(c, ct + P, limbs, ext);
+  for (int b = 0; b < B; b++) {
+    u64 *b0 = bab + (size_t)b * 2 * EP, *b1 = b0 + EP;
+    if (baby_gs[b] == 1) {
+      memset(b0, 0, sizeof(u64) * 2 * EP);
+      for (int d = 0; d < 2; d++)
+        for (int i = 0; i < limbs; i++)
+          for (int k = 0; k < N; k++)
+            (d ? b1 : b0)[(size_t)i * N + k] =
+                orc_mulmod(ct[(size_t)d * P + (size_t)i * N + k], Pm[i], c->primes[i]);
+      continue;
+    }
+    orc_automorphism_ntt(c, baby_gs[b], ext, extg, digits * E);
+    key_inner(c, find_key(c, baby_gs[b]), extg, limbs, b0, b1);
+    orc_automorphism_ntt(c, baby_gs[b], ct, sc0, limbs);
+    for (int i = 0; i < limbs; i++)
+      for (int k = 0; k < N; k++) {
+        u64 *x = b0 + (size_t)i * N + k;
+        *x = addmod(*x, orc_mulmod(sc0[(size_t)i * N + k], Pm[i], c->primes[i]), c->primes[i]);
+      }
+  }
+  u64 *inner_ext = (u64 *)malloc(sizeof(u64) * 2 * EP);
+  u64 *inner = (u64 *)malloc(sizeof(u64) * 2 * P);
+  u64 *tmp = (u64 *)malloc(sizeof(u64) * 2 * P);
+  for (int g = G - 1; g >= 0; g--) {
+#pragma omp parallel for
+    for (int l = 0; l < E; l++) {
+      const u64 q = c->primes[prime_of(c, l, limbs)];
+      for (int d = 0; d < 2; d++) {
+        u64 *dst = inner_ext + (size_t)d * EP + (size_t)l * N;
+        for (int i = 0; i < N; i++) {
+          u128 s = 0;
+          for (int b = 0; b < B; b++) {
+            s += (u128)bab[(size_t)b * 2 * EP + (size_t)d * EP + (size_t)l * N + i] *
+                 pts[((size_t)(g * B + b) * E + l) * N + i];
+            if ((b & 15) == 15) s %= q;
+          }
+          dst[i] = (u64)(s % q);
+        }
+      }
+    }
+    orc_moddown(c, inner_ext, limbs, inner);
+    orc_moddown(c, inner_ext + EP, limbs, inner + P);
+    if (g == G - 1) {
+      memcpy(out, inner, sizeof(u64) * 2 * P);
+    } else {
+      orc_rotate(c, out, limbs, giant_g, tmp);
+      orc_add(c, tmp, inner, out, 2, limbs);
+    }
+  }
+  free(ext);
+  free(extg);
+  free(bab);
+  free(sc0);
+  free(inner_ext);
+  free(inner);
+  free(tmp);
+  return 0;
+}

@@ -137,6 +137,9 @@ int orc_hoisted_rotate(const orc_ctx *c, const uint64_t *ct, int limbs,
                        const uint64_t *gs, int n, uint64_t *outs);
 void orc_rescale(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,
                  uint64_t *out);
+int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
+                            const uint64_t *baby_gs, int B, const uint64_t *pts,
+                            uint64_t giant_g, int G, uint64_t *out);
 void orc_mod_raise(const orc_ctx *c, const uint64_t *ct, int polys, int target,
                    uint64_t *out);
 void orc_drop_limbs(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,

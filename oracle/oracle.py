@@ -88,6 +88,7 @@ def lib():
             "orc_rescale": (None, [vp, _u64p, i, i, _u64p]),
             "orc_drop_limbs": (None, [vp, _u64p, i, i, i, _u64p]),
             "orc_mod_raise": (None, [vp, _u64p, i, i, _u64p]),
+            "orc_hoisted_mac_sum_ext": (i, [vp, _u64p, i, _u64p, i, _u64p, u64, i, _u64p]),
             "orc_hoisted_mac_sum": (i, [vp, _u64p, i, _u64p, i, _u64p, u64, i, _u64p]),
         }
         for name, (res, args) in sig.items():
@@ -360,6 +361,17 @@ class OracleContext:
         out = np.zeros_like(ct)
         if lib().orc_hoisted_mac_sum(self._c, _p(ct), ct.shape[1], _p(gs), len(gs), _p(pts),
                                      giant_g, giant_count, _p(out)):
+            raise KeyError("missing rotation key")
+        return out
+
+    def hoisted_mac_sum_ext(self, ct, baby_gs, pts_ext, giant_g: int, giant_count: int):
+        """Extended-basis schedule: pts_ext are [G*B][limbs + alpha][N]."""
+        gs = np.asarray(baby_gs, dtype=np.uint64)
+        pts = np.ascontiguousarray(pts_ext, dtype=np.uint64)
+        assert pts.shape[1] == ct.shape[1] + self.alpha
+        out = np.zeros_like(ct)
+        if lib().orc_hoisted_mac_sum_ext(self._c, _p(ct), ct.shape[1], _p(gs), len(gs), _p(pts),
+                                         giant_g, giant_count, _p(out)):
             raise KeyError("missing rotation key")
         return out
 

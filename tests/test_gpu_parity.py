@@ -339,6 +339,63 @@ def test_bsgs_matvec_parity():
     assert np.abs(dec - W @ x).max() < 1e-5
 
 
+def test_bsgs_matvec_ext_parity():
+    """The matvec workload with strategy "ext_normal": babies in Q u P, one
+    ModDown per giant group; bit-exact with the oracle's extended schedule."""
+    fhe = _fhe()
+    D, lanes, B, G = 128, 32, 16, 8
+    rots = tuple(lanes * b for b in range(1, B)) + (B * lanes,)
+    client, ctx, orc = _pair("matvec", rotations=rots)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    sc = ctx.scale_at(ctx.L)
+    ct = client.encrypt(packed, slots=slots, enc_id=41)
+    ref = orc.encrypt(packed, slots=slots, scale=sc, limbs=ctx.L, enc_id=41)
+    rows = _diagonals(W, slots=slots, lanes=lanes, baby=B, giant_base=0, giant_count=G)
+    pts = fhe.encode_rows(ctx, rows, limbs=ctx.L, scale=sc, slots=slots, is_ext=True)
+    rpts = np.stack([orc.encode(r, slots=slots, scale=sc, limbs=ctx.L, is_ext=True)
+                     for r in rows])
+    offsets = [lanes * b for b in range(B)]
+    acc = fhe.hoisted_mac_sum(ct, offsets, pts, B * lanes, G, ctx, strategy="ext_normal")
+    racc = orc.hoisted_mac_sum_ext(ref, [orc.galois_elt(o) for o in offsets], rpts,
+                                   orc.galois_elt(B * lanes), G)
+    assert np.array_equal(acc.download(), racc)
+    dec = client.decrypt(fhe.rescale(acc, ctx))[np.arange(D) * lanes]
+    assert np.abs(dec - W @ x).max() < 1e-5
+
+
+@pytest.mark.parametrize("name", ["small", "matvec"])
+def test_fast_rotate_ext_moddown_is_rotation(name):
+    """ModDown(P sigma(c0) + acc_0, acc_1) is the rotation bit for bit (P
+    sigma(c0) vanishes on the special limbs); offset 0 gives the input back;
+    an extended pairwise MAC brought back by one ModDown decrypts to the sum."""
+    fhe = _fhe()
+    rots = (1, 3)
+    client, ctx, orc = _pair(name, rotations=rots)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(17)
+    z = rng.uniform(-1, 1, slots)
+    ct = client.encrypt(z, slots=slots, enc_id=9)
+    batch = fhe.fast_rotate(ct, [0, 1, 3], ctx, output_ext=True)
+    assert all(b.is_ext for b in batch.cv)
+    plain = [fhe.homo_rotate(ct, r, ctx) for r in (1, 3)]
+    assert np.array_equal(fhe.moddown_from_ext(batch.cv[0], ctx).download(), ct.download())
+    for b, ref in zip(batch.cv[1:], plain):
+        assert np.array_equal(fhe.moddown_from_ext(b, ctx).download(), ref.download())
+    w = [rng.uniform(-1, 1, slots) for _ in range(3)]
+    sc = ctx.scale_at(ctx.L)
+    pts = [fhe.encode_rows(ctx, v, limbs=ctx.L, scale=sc, slots=slots, is_ext=True)[0] for v in w]
+    acc = fhe.grouped_pairwise_mac(batch, pts, [[0, 1, 2]], ctx)[0]
+    assert acc.is_ext
+    out = fhe.rescale(fhe.moddown_from_ext(acc, ctx), ctx)
+    want = w[0] * z + w[1] * np.roll(z, -1) + w[2] * np.roll(z, -3)
+    assert np.abs(client.decrypt(out) - want).max() < 1e-6
+
+
 # ---------------------------------------------------------------------------
 # keyswitch workload size (N = 2^16, 36 + 12 limbs, dnum 3)
 # ---------------------------------------------------------------------------

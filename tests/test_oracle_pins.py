@@ -486,3 +486,33 @@ def test_bsgs_matvec_decrypts_to_wx():
     sc = 2.0**80 / float(ctx.primes[ctx.L - 1])
     dec = ctx.decrypt(out, slots=slots, scale=sc).real[np.arange(D) * lanes]
     assert np.abs(dec - W @ x).max() < 1e-5
+
+
+def test_bsgs_matvec_ext_schedule_decrypts_to_wx():
+    """The extended-basis schedule (one ModDown per giant group) on the
+    oracle: decrypt(rescale(MAC)) = W x, and its limbs differ from the normal
+    schedule's (different rounding, same value)."""
+    ctx = oracle_context("matvec")
+    D, lanes, B, G = 128, 32, 16, 8
+    for o in list(range(lanes, B * lanes, lanes)) + [B * lanes]:
+        ctx.gen_rotation_key(ctx.galois_elt(o))
+    slots = ctx.N // 2
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    ct = ctx.encrypt(packed, slots=slots, scale=2.0**40, limbs=ctx.L, enc_id=41)
+    feat = np.arange(slots) // lanes
+    rows = [W[(feat - g * B) % D, (feat + b) % D] for g in range(G) for b in range(B)]
+    pts = np.stack([ctx.encode(r, slots=slots, scale=2.0**40, limbs=ctx.L, is_ext=True)
+                    for r in rows])
+    gs = [ctx.galois_elt(lanes * b) for b in range(B)]
+    acc = ctx.hoisted_mac_sum_ext(ct, gs, pts, ctx.galois_elt(B * lanes), G)
+    sc = 2.0**80 / float(ctx.primes[ctx.L - 1])
+    dec = ctx.decrypt(ctx.rescale(acc), slots=slots, scale=sc).real[np.arange(D) * lanes]
+    assert np.abs(dec - W @ x).max() < 1e-5
+    normal = ctx.hoisted_mac_sum(ct, gs, np.ascontiguousarray(pts[:, : ctx.L]),
+                                 ctx.galois_elt(B * lanes), G)
+    assert not np.array_equal(acc, normal)
+
