@@ -1712,6 +1712,124 @@ int ckks_moddown_ext(ckks_context *c, const ckks_ct *a, ckks_ct **out) {
   API_END
 }
 
+int ckks_tensor_upload(ckks_context *c, const void *data, size_t bytes, ckks_tensor **out) {
+  API_BEGIN
+  require(c && data && out, "null argument");
+  require(bytes > 0, "empty tensor");
+  ckks_tensor *t = new ckks_tensor{c, nullptr, bytes};
+  if (hipMalloc(&t->d, bytes) != hipSuccess) {
+    delete t;
+    throw std::runtime_error("device allocation failed");
+  }
+  HIPCHECK(hipMemcpyAsync(t->d, data, bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  *out = t;
+  API_END
+}
+
+int ckks_tensor_download(ckks_context *c, const ckks_tensor *t, void *out, size_t bytes) {
+  API_BEGIN
+  require(c && t && out, "null argument");
+  require(t->ctx == c, "tensor belongs to another context");
+  require(bytes <= t->bytes, "download larger than the tensor");
+  HIPCHECK(hipMemcpyAsync(out, t->d, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
+void ckks_tensor_free(ckks_tensor *t) {
+  if (!t) return;
+  if (g_live_contexts.count(t->ctx)) {
+    (void)hipStreamSynchronize(t->ctx->stream);
+    (void)hipFree(t->d);
+  }
+  delete t;
+}
+
+static void check_diag_geom(const ckks_context *c, int D, int lanes, int baby, int giant_base,
+                            int giant_count, int slots) {
+  require(D > 0 && lanes > 0 && baby > 0 && giant_base >= 0 && giant_count > 0,
+          "dimension, token_lanes, baby_steps, giant_count must be positive, giant_base >= 0");
+  require((long long)D * lanes == slots,
+          "token-lane packing needs dimension * token_lanes == slots");
+  check_slots(c, slots);
+}
+
+int ckks_encode_token_lane(ckks_context *c, const ckks_tensor *w, int dtype, int D, int lanes,
+                           int baby, int giant_base, int giant_count, int slots, int limbs,
+                           double scale, int is_ext, ckks_ct **out) {
+  API_BEGIN
+  require(c && w && out, "null argument");
+  require(w->ctx == c, "tensor belongs to another context");
+  require(dtype >= 0 && dtype <= 2, "dtype must be 0 (float64), 1 (float32) or 2 (complex128)");
+  check_diag_geom(c, D, lanes, baby, giant_base, giant_count, slots);
+  check_limbs(c, limbs);
+  const size_t elem = dtype == 0 ? 8 : dtype == 1 ? 4 : 16;
+  require(w->bytes >= elem * (size_t)D * D, "weight tensor is smaller than dimension^2 entries");
+  fft_table(c, slots);
+  const int rows = baby * giant_count;
+  for (int r = 0; r < rows; r++) out[r] = new_ct(c, 1, limbs, is_ext, slots, scale, 1);
+  DiagGeom gm{D, lanes, baby, giant_base};
+  launch_encode_diagonals(c, w->d, dtype, nullptr, nullptr, gm, rows, slots, scale, limbs,
+                          is_ext, out);
+  API_END
+}
+
+int ckks_encode_structured(ckks_context *c, const ckks_tensor *const *sources, int n_sources,
+                           int fp32, const int64_t *shapes, const int64_t *strides,
+                           const int64_t *index_maps, const double *scale_maps, int D,
+                           int lanes, int baby, int giant_base, int giant_count, int slots,
+                           int limbs, double scale, int is_ext, ckks_ct **out) {
+  API_BEGIN
+  require(c && sources && shapes && strides && index_maps && scale_maps && out,
+          "null argument");
+  require(n_sources >= 1 && n_sources <= 3, "one to three sources");
+  check_diag_geom(c, D, lanes, baby, giant_base, giant_count, slots);
+  check_limbs(c, limbs);
+  StructSources src{};
+  src.fp32 = fp32 ? 1 : 0;
+  const size_t elem = fp32 ? 4 : 8;
+  for (int s = 0; s < n_sources; s++) {
+    require(sources[s] && sources[s]->ctx == c, "bad source tensor");
+    const int64_t rows = shapes[2 * s], cols = shapes[2 * s + 1];
+    const int64_t rst = strides[2 * s], cst = strides[2 * s + 1];
+    require(rows > 0 && cols > 0 && rst >= 0 && cst >= 0, "bad source shape or strides");
+    require((size_t)((rows - 1) * rst + (cols - 1) * cst + 1) * elem <= sources[s]->bytes,
+            "source shape and strides exceed the tensor");
+    src.p[s] = sources[s]->d;
+    src.stride[s][0] = (u64)rst;
+    src.stride[s][1] = (u64)cst;
+  }
+  // every index the gather can read is checked here, on the host
+  const int64_t *rsrc = index_maps, *rrow = index_maps + D, *isrc = index_maps + 2 * (size_t)D;
+  const int64_t *irow = index_maps + 3 * (size_t)D, *col = index_maps + 4 * (size_t)D;
+  for (int i = 0; i < D; i++) {
+    for (int part = 0; part < 2; part++) {
+      const int64_t sidx = part ? isrc[i] : rsrc[i], r = part ? irow[i] : rrow[i];
+      require(sidx >= -1 && sidx < n_sources, "source index out of range");
+      if (sidx >= 0) require(r >= 0 && r < shapes[2 * sidx], "row index out of range");
+    }
+    if (col[i] >= 0)
+      for (int s = 0; s < n_sources; s++)
+        require(col[i] < shapes[2 * s + 1], "column index out of range");
+    require(col[i] >= -1, "column index out of range");
+  }
+  std::vector<u64> maps(8 * (size_t)D);
+  memcpy(maps.data(), index_maps, sizeof(int64_t) * 5 * (size_t)D);
+  memcpy(maps.data() + 5 * (size_t)D, scale_maps, sizeof(double) * 3 * (size_t)D);
+  fft_table(c, slots);
+  const int rows = baby * giant_count;
+  for (int r = 0; r < rows; r++) out[r] = new_ct(c, 1, limbs, is_ext, slots, scale, 1);
+  Scratch s(c);
+  u64 *dmaps = s.get(maps.size());
+  HIPCHECK(hipMemcpyAsync(dmaps, maps.data(), sizeof(u64) * maps.size(), hipMemcpyHostToDevice,
+                          c->stream));
+  DiagGeom gm{D, lanes, baby, giant_base};
+  launch_encode_diagonals(c, nullptr, 0, &src, dmaps, gm, rows, slots, scale, limbs, is_ext, out);
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  API_END
+}
+
 int ckks_poly_ntt(ckks_context *c, const uint64_t *in, uint64_t *out, int n_polys, int limbs,
                   int q_limbs, int inverse) {
   API_BEGIN

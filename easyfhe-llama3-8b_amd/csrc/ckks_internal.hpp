@@ -204,6 +204,12 @@ struct ckks_event {
   hipEvent_t ev;
 };
 
+struct ckks_tensor {  // raw device bytes (weights for the diagonal packers)
+  ckks_context *ctx;
+  void *d;
+  size_t bytes;
+};
+
 // ---------------------------------------------------------------------------
 // kernel launchers (ckks_kernels.hip)
 // ---------------------------------------------------------------------------
@@ -240,6 +246,18 @@ void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
                         int E, const u64 *pinv, const Batch &add0, const Batch &add1,
                         const u64 *galois, const Batch &out0, const Batch &out1);
+// Feature-major BSGS diagonal geometry (token-lane packing)
+struct DiagGeom {
+  int D, lanes, baby, giant_base;
+};
+struct StructSources {  // up to three real weight matrices
+  const void *p[3];
+  u64 stride[3][2];  // elements per row, per column
+  int fp32;
+};
+void launch_encode_diagonals(ckks_context *c, const void *w, int dtype, const StructSources *src,
+                             const u64 *maps, const DiagGeom &gm, int rows, int slots,
+                             double scale, int limbs, int is_ext, ckks_ct **out);
 void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target);
 void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);
 void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64 galois);

@@ -1766,16 +1766,12 @@ __global__ void k_encode_finish(const cplx *__restrict__ x, const cplx *__restri
   batch_ptr(out, blockIdx.z)[((size_t)l << logN) + k] = dbl_residue(v, M);
 }
 
-void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int rows,
-                   int slots, double scale, int limbs, int is_ext, const Batch &out) {
+// Encoder tail over rows already placed in x ([rows][n], slot j at
+// bit-reversed perm[j]): inverse FFT, twist, rounding, residues, NTT.
+static void encode_placed(ckks_context *c, cplx *x, int rows, int slots, double scale,
+                          int limbs, int is_ext, const Batch &out) {
   const FFTTable &t = c->fft.at(slots);
   const int n = slots;
-  int logn = 0;
-  while ((1 << logn) < n) logn++;
-  cplx *x = (cplx *)c->pool.alloc(sizeof(cplx) * (size_t)rows * n);
-  hipLaunchKernelGGL(k_fft_place, dim3((n + TPB - 1) / TPB, rows), dim3(TPB), 0, c->stream,
-                     d_re, d_im, x, t.perm, n, logn);
-  LAUNCH_CHECK();
   for (int len = 2; len <= n; len <<= 1) {
     hipLaunchKernelGGL(k_fft_stage, dim3((n / 2 + TPB - 1) / TPB, rows), dim3(TPB), 0,
                        c->stream, x, n, len, (const cplx *)t.tw_inv);
@@ -1786,7 +1782,106 @@ void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int 
                      x, (const cplx *)t.twist, out, n, c->logN, scale, limbs, c->L, c->d_mods);
   LAUNCH_CHECK();
   launch_ntt(c, out, out, rows, 0, total, limbs, false);
+}
+
+void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int rows,
+                   int slots, double scale, int limbs, int is_ext, const Batch &out) {
+  const FFTTable &t = c->fft.at(slots);
+  const int n = slots;
+  int logn = 0;
+  while ((1 << logn) < n) logn++;
+  cplx *x = (cplx *)c->pool.alloc(sizeof(cplx) * (size_t)rows * n);
+  hipLaunchKernelGGL(k_fft_place, dim3((n + TPB - 1) / TPB, rows), dim3(TPB), 0, c->stream,
+                     d_re, d_im, x, t.perm, n, logn);
+  LAUNCH_CHECK();
+  encode_placed(c, x, rows, slots, scale, limbs, is_ext, out);
   c->pool.release(x, sizeof(cplx) * (size_t)rows * n);
+}
+
+// ---------------------------------------------------------------------------
+// BSGS diagonals gathered from a device-resident weight, placed straight into
+// the encoder's FFT input (the [rows, slots] block is never written):
+//   row(g, b)[slot] = W[(f - (giant_base + g) B) mod D, (f + b) mod D],
+//   f = slot / token_lanes, row index g B + b.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void diag_features(int row, int j, const DiagGeom &gm, int &of,
+                                              int &inf) {
+  const int g = gm.giant_base + row / gm.baby, b = row % gm.baby;
+  const int f = j / gm.lanes;
+  of = (int)(((long long)f - (long long)g * gm.baby) % gm.D);
+  if (of < 0) of += gm.D;
+  inf = (f + b) % gm.D;
+}
+
+// dtype 0 float64, 1 float32, 2 complex128 ([D][D] row-major)
+__global__ void k_place_token_lane(const void *__restrict__ w, int dtype, DiagGeom gm,
+                                   cplx *__restrict__ x, const u32 *__restrict__ perm, int n,
+                                   int logn, int row0) {
+  const int j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  const int row = row0 + blockIdx.y;
+  int of, inf;
+  diag_features(row, j, gm, of, inf);
+  const size_t wi = (size_t)of * gm.D + inf;
+  cplx v{0.0, 0.0};
+  if (dtype == 0) v.re = ((const double *)w)[wi];
+  else if (dtype == 1) v.re = (double)((const float *)w)[wi];
+  else v = ((const cplx *)w)[wi];
+  x[(size_t)blockIdx.y * n + (__brev(perm[j]) >> (32 - logn))] = v;
+}
+
+// W_phys[o, i] = column_scale[i] (real_scale[o] src[real_source[o]][real_row[o], column[i]]
+//                + i imag_scale[o] src[imag_source[o]][imag_row[o], column[i]]);
+// an index of -1 (source or column) is zero padding.  maps: [8][D] words:
+// real_source, real_row, imag_source, imag_row, column (int64), real_scale,
+// imag_scale, column_scale (double).
+__global__ void k_place_structured(StructSources src, const u64 *__restrict__ maps, DiagGeom gm,
+                                   cplx *__restrict__ x, const u32 *__restrict__ perm, int n,
+                                   int logn, int row0) {
+  const int j = blockIdx.x * TPB + threadIdx.x;
+  if (j >= n) return;
+  const int row = row0 + blockIdx.y;
+  int of, inf;
+  diag_features(row, j, gm, of, inf);
+  const long long *mi = (const long long *)maps;
+  const double *md = (const double *)maps;
+  const size_t D = gm.D;
+  const long long rs = mi[of], rr = mi[D + of], is = mi[2 * D + of], ir = mi[3 * D + of];
+  const long long col = mi[4 * D + inf];
+  const double rsc = md[5 * D + of], isc = md[6 * D + of], csc = md[7 * D + inf];
+  auto read = [&](long long s, long long r) -> double {
+    if (s < 0 || col < 0) return 0.0;
+    const size_t idx = (size_t)r * src.stride[s][0] + (size_t)col * src.stride[s][1];
+    return src.fp32 ? (double)((const float *)src.p[s])[idx] : ((const double *)src.p[s])[idx];
+  };
+  cplx v{read(rs, rr) * rsc * csc, read(is, ir) * isc * csc};
+  x[(size_t)blockIdx.y * n + (__brev(perm[j]) >> (32 - logn))] = v;
+}
+
+void launch_encode_diagonals(ckks_context *c, const void *w, int dtype, const StructSources *src,
+                             const u64 *maps, const DiagGeom &gm, int rows, int slots,
+                             double scale, int limbs, int is_ext, ckks_ct **out) {
+  const FFTTable &t = c->fft.at(slots);
+  const int n = slots;
+  int logn = 0;
+  while ((1 << logn) < n) logn++;
+  for (int r0 = 0; r0 < rows; r0 += kMaxBatch) {
+    const int nr = std::min(kMaxBatch, rows - r0);
+    cplx *x = (cplx *)c->pool.alloc(sizeof(cplx) * (size_t)nr * n);
+    dim3 grid((n + TPB - 1) / TPB, nr);
+    if (src)
+      hipLaunchKernelGGL(k_place_structured, grid, dim3(TPB), 0, c->stream, *src, maps, gm, x,
+                         t.perm, n, logn, r0);
+    else
+      hipLaunchKernelGGL(k_place_token_lane, grid, dim3(TPB), 0, c->stream, w, dtype, gm, x,
+                         t.perm, n, logn, r0);
+    LAUNCH_CHECK();
+    Batch o{};
+    for (int r = 0; r < nr; r++) o.p[r] = out[r0 + r]->d;
+    encode_placed(c, x, nr, slots, scale, limbs, is_ext, o);
+    c->pool.release(x, sizeof(cplx) * (size_t)nr * n);
+  }
 }
 
 __global__ void k_scalar_encode(double v, int limbs, u64 *out, const ModQ *__restrict__ mods) {

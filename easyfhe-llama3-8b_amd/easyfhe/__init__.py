@@ -13,19 +13,21 @@ from __future__ import annotations
 import numpy as np
 
 from . import _native  # noqa: F401  (loads the library; raises if it is missing)
-from . import bs, cuda, fhe
+from . import bs, cuda, fhe, packing
+from .tensor import DeviceTensor, HostTensor
 
 complex128 = np.complex128
 float64 = np.float64
 float32 = np.float32
 
 
-def from_numpy(array):
-    return np.asarray(array)
+def from_numpy(array) -> HostTensor:
+    """Host tensor; ``.to("cuda")`` moves it to the current context's HBM."""
+    return HostTensor(array)
 
 
 def is_tensor(value) -> bool:
-    return isinstance(value, np.ndarray)
+    return isinstance(value, (np.ndarray, HostTensor, DeviceTensor))
 
 
 def empty(shape, dtype=np.float64, device=None):

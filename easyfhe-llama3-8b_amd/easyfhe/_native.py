@@ -113,6 +113,12 @@ SIGNATURES = {
     "ckks_hoisted_mac_sum_ext": (I, [VP, VP, I64P, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_hoisted_rotate_ext": (I, [VP, VP, I64P, I, VPP]),
     "ckks_moddown_ext": (I, [VP, VP, VPP]),
+    "ckks_tensor_upload": (I, [VP, VP, ctypes.c_size_t, VPP]),
+    "ckks_tensor_download": (I, [VP, VP, VP, ctypes.c_size_t]),
+    "ckks_tensor_free": (None, [VP]),
+    "ckks_encode_token_lane": (I, [VP, VP, I, I, I, I, I, I, I, I, ctypes.c_double, I, VPP]),
+    "ckks_encode_structured": (I, [VP, VPP, I, I, I64P, I64P, I64P, DP, I, I, I, I, I, I, I,
+                                   ctypes.c_double, I, VPP]),
     "ckks_poly_ntt": (I, [VP, U64P, U64P, I, I, I, I]),
     "ckks_poly_modup": (I, [VP, U64P, I, U64P]),
     "ckks_poly_moddown": (I, [VP, U64P, I, U64P]),

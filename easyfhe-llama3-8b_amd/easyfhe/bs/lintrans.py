@@ -123,9 +123,12 @@ class LevelPlan:
         return rows * scale_factor
 
 
-def plan_levels(log_n: int, budget: int, inverse: bool) -> list[LevelPlan]:
+def plan_levels(log_n: int, budget: int, inverse: bool, giants: int = 0) -> list[LevelPlan]:
     """Level plans in evaluation order.  inverse=True is CoeffToSlot
-    (S_L^-1 first), inverse=False is SlotToCoeff (S_1 first)."""
+    (S_L^-1 first), inverse=False is SlotToCoeff (S_1 first).  The baby count
+    is about sqrt(width); with ``giants`` > 0 it is the smallest power of two
+    that needs at most that many giant steps (the extended-basis schedule
+    pays one ModDown per giant group, so it wants few giants)."""
     n = 1 << log_n
     groups = level_groups(log_n, budget)
     order = list(reversed(groups)) if inverse else groups
@@ -145,6 +148,10 @@ def plan_levels(log_n: int, budget: int, inverse: bool) -> list[LevelPlan]:
         else:
             width = 2 * span // stride + 1
         baby = 1 << max(0, math.ceil(math.log2(width)) // 2 + (math.ceil(math.log2(width)) % 2))
+        if giants > 0:
+            baby = 1
+            while -(-width // baby) > giants:
+                baby *= 2
         baby = min(baby, 64)
         giant = -(-width // baby)
         plans.append(LevelPlan(stride=stride, center=span, width=width, baby=baby, giant=giant,

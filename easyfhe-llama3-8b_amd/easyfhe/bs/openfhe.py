@@ -75,6 +75,10 @@ class BootstrapParams:
     fit_bits: int = 45
     ratio_bits: int = 10
     cts_pt_bits: int = 58
+    # linear levels: "ext_normal" keeps the babies in Q u P (one ModDown per
+    # giant group, at most `giants` giants); "normal" ModDowns every baby
+    strategy: str = "ext_normal"
+    giants: int = 2
 
 
 
@@ -95,10 +99,11 @@ def _check_spec(spec: BootstrapSpec, log_n: int) -> None:
         raise ValueError(f"level_budget must be two values in [1, log_slots], got {budget}")
 
 
-def _plans(spec: BootstrapSpec):
+def _plans(spec: BootstrapSpec, params: "BootstrapParams | None" = None):
     b0, b1 = (int(v) for v in spec.level_budget)
-    return (plan_levels(int(spec.log_slots), b0, inverse=True),
-            plan_levels(int(spec.log_slots), b1, inverse=False))
+    giants = params.giants if params is not None and params.strategy != "normal" else 0
+    return (plan_levels(int(spec.log_slots), b0, inverse=True, giants=giants),
+            plan_levels(int(spec.log_slots), b1, inverse=False, giants=giants))
 
 
 def _baby_offsets(plan: LevelPlan, n: int) -> list[int]:
@@ -116,16 +121,18 @@ def _level_rotations(plan: LevelPlan, n: int) -> set[int]:
     return rots
 
 
-def requirements(specs, log_n: int) -> Requirements:
+def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> Requirements:
     """Rotation indices every listed program needs, conjugation (2N - 1)
     included (reference bootstrap.py:154-189)."""
     if isinstance(specs, BootstrapSpec):
         specs = (specs,)
+    p = params or BootstrapParams()
     rots: set[int] = set()
     for spec in specs:
         _check_spec(spec, int(log_n))
         n = spec.slots
-        for plan in (*_plans(spec)[0], *_plans(spec)[1]):
+        cts, stc = _plans(spec, p)
+        for plan in (*cts, *stc):
             rots |= _level_rotations(plan, n)
         rots.add(2 * (1 << int(log_n)) - 1)
     return Requirements(rotations=tuple(sorted(rots)))
@@ -220,7 +227,9 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     step = max(1, math.ceil(_EVALMOD_BITS / bits))
     coeffs = _evalmod_coefficients(p)
     depth = cheb.chebyshev_depth(coeffs)
-    cts_plans, stc_plans = _plans(spec)
+    if p.strategy not in ("normal", "ext_normal"):
+        raise ValueError(f"unknown linear-level strategy {p.strategy!r}")
+    cts_plans, stc_plans = _plans(spec, p)
     n_cts, n_stc = len(cts_plans), len(stc_plans)
     ladder_levels = depth + p.double_angles
     q0 = float(primes[0])
@@ -276,7 +285,7 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     assert limbs == int(spec.output_levels) + 1, (limbs, spec.output_levels)
     prog.constants = fhe.ConstantBundle(vectors, cache_mode="plain")
 
-    need = [r for r in requirements(spec, ctx.logN).rotations if not ctx.has_rotation_key(r)]
+    need = [r for r in requirements(spec, ctx.logN, p).rotations if not ctx.has_rotation_key(r)]
     if need:
         ctx.generate_rotation_keys(need)
     return prog
@@ -318,10 +327,11 @@ def _prescale(ct, prog: BootstrapProgram, ctx):
 def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
     n = prog.spec.slots
     plan = lv.plan
+    ext = prog.evalmod.strategy != "normal"
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
-    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx)
+    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=ext)
     acc = fhe.hoisted_mac_sum(x, _baby_offsets(plan, n), pts, _giant_offset(plan, n),
-                              plan.giant, ctx)
+                              plan.giant, ctx, strategy=prog.evalmod.strategy)
     for _ in range(lv.primes):
         acc = fhe.rescale(acc, ctx)
     acc.set_scale(lv.out_scale, 1)

@@ -412,7 +412,11 @@ class PackedRaw:
     def __init__(self, tensor):
         self.tensor = tensor
 
-    def values(self, slots: int, context) -> np.ndarray:
+    def values(self, slots: int, context):
+        from .packing import DiagonalChunk
+
+        if isinstance(self.tensor, DiagonalChunk):
+            return self.tensor
         return np.asarray(self.tensor)
 
 
@@ -424,8 +428,11 @@ class UnpackedRaw:
         self.source = source
         self.packer = packer
 
-    def values(self, slots: int, context) -> np.ndarray:
-        return np.asarray(self.packer(self.source, slots, context))
+    def values(self, slots: int, context):
+        from .packing import DiagonalChunk
+
+        out = self.packer(self.source, slots, context)
+        return out if isinstance(out, DiagonalChunk) else np.asarray(out)
 
 
 class ConstantBundle:
@@ -469,10 +476,16 @@ class ConstantBundle:
         if key in self._plain:
             return self._plain[key]
         values = self._values(str(name), int(slots), context)
-        arr = np.asarray(values)
-        pts = encode_rows(context, arr, limbs=limbs, scale=scale, slots=int(slots),
-                          is_ext=bool(is_ext))
-        result = pts[0] if arr.ndim == 1 else pts
+        from .packing import DiagonalChunk
+
+        if isinstance(values, DiagonalChunk):
+            # device-resident weight: gather and encode in one device pass
+            result = values.encode(context, limbs=limbs, scale=scale, is_ext=bool(is_ext))
+        else:
+            arr = np.asarray(values)
+            pts = encode_rows(context, arr, limbs=limbs, scale=scale, slots=int(slots),
+                              is_ext=bool(is_ext))
+            result = pts[0] if arr.ndim == 1 else pts
         if cache or self.cache_mode in ("plain", "both"):
             self._plain[key] = result
         return result
@@ -487,7 +500,7 @@ class ConstantBundle:
                 total += 8 * pt.context.N * (int(info.limbs) +
                                              (pt.context.alpha if info.is_ext else 0))
                 entries += 1
-        total += sum(int(np.asarray(v).nbytes) for v in self._middle.values())
+        total += sum(int(v.nbytes) for v in self._middle.values() if isinstance(v, np.ndarray))
         return {"entries": entries, "total_bytes": total}
 
     def clear_cache(self) -> None:

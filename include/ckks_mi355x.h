@@ -35,6 +35,7 @@ extern "C" {
 typedef struct ckks_context ckks_context;
 typedef struct ckks_ct ckks_ct; /* ciphertext or plaintext polynomial set */
 typedef struct ckks_event ckks_event;
+typedef struct ckks_tensor ckks_tensor; /* device-resident raw array (weights) */
 
 /* Context parameters; fields follow fhe.CKKSContextSpec
  * (reference llama3fhe/application/session.py:31-45, backend.py:457-471). */
@@ -188,6 +189,36 @@ int ckks_hoisted_rotate_ext(ckks_context *ctx, const ckks_ct *a, const int64_t *
 /* fhe.moddown_from_ext (reference attention/input.py:1103-1169): an extended
  * ciphertext divided by P (centered conversion) back to the Q basis. */
 int ckks_moddown_ext(ckks_context *ctx, const ckks_ct *a, ckks_ct **out);
+
+/* Device-resident weights for the diagonal packers (the reference keeps them
+ * on the GPU as EasyFHE tensors, operators/linear/gpu_packer.py:79-97). */
+int ckks_tensor_upload(ckks_context *ctx, const void *data, size_t bytes, ckks_tensor **out);
+int ckks_tensor_download(ckks_context *ctx, const ckks_tensor *t, void *out, size_t bytes);
+void ckks_tensor_free(ckks_tensor *t);
+/* Feature-major BSGS diagonals of a device weight W [D][D] (dtype 0 float64,
+ * 1 float32, 2 complex128), encoded at (limbs, scale[, P limbs]):
+ *   row(g, b)[slot] = W[(slot / lanes - (giant_base + g) B) mod D, (slot / lanes + b) mod D]
+ * for g < giant_count, b < B, as giant_count * B plaintexts.  The gather feeds
+ * the encoder directly (reference pack_token_lane_bsgs_weight_chunk_triton_gpu,
+ * operators/linear/gpu_packer.py:49-177, then ConstantBundle.plaintext). */
+int ckks_encode_token_lane(ckks_context *ctx, const ckks_tensor *weight, int dtype, int dimension,
+                           int token_lanes, int baby_steps, int giant_base, int giant_count,
+                           int slots, int limbs, double scale, int is_ext, ckks_ct **out);
+/* The same diagonals of a structured physical matrix
+ *   W[o, i] = column_scale[i] (real_scale[o] src[real_source[o]][real_row[o], column[i]]
+ *             + 1j imag_scale[o] src[imag_source[o]][imag_row[o], column[i]])
+ * (index -1 = zero padding) over 1..3 real sources (fp32 != 0: float32, else
+ * float64) with shapes [n][2] and element strides [n][2]; index_maps holds
+ * real_source, real_row, imag_source, imag_row, column ([5][dimension] host
+ * int64), scale_maps real_scale, imag_scale, column_scale ([3][dimension] host
+ * double).  Every index is checked against the shapes before the device gather
+ * (reference pack_structured_token_lane_bsgs_weight_chunk_triton_gpu,
+ * operators/linear/gpu_packer.py:180-424, structured_weight.py:1-20). */
+int ckks_encode_structured(ckks_context *ctx, const ckks_tensor *const *sources, int n_sources,
+                           int fp32, const int64_t *shapes, const int64_t *strides,
+                           const int64_t *index_maps, const double *scale_maps, int dimension,
+                           int token_lanes, int baby_steps, int giant_base, int giant_count,
+                           int slots, int limbs, double scale, int is_ext, ckks_ct **out);
 
 /* Raw polynomial transforms over host buffers [n_polys][limbs][N] with limb i
  * in prime i (i < q_limbs) or special prime i - q_limbs (parity tests). */

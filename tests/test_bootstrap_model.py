@@ -143,13 +143,17 @@ def _horner_check(x, plan, rows):
     return direct
 
 
-@pytest.mark.parametrize("log_n,budget", [(6, (2, 2)), (10, (3, 3)), (10, (4, 4)), (11, (3, 2))])
-def test_bootstrap_model_recovers_message(log_n, budget):
+@pytest.mark.parametrize("log_n,budget,strategy",
+                         [(6, (2, 2), "normal"), (10, (3, 3), "normal"), (10, (3, 3), "ext_normal"),
+                          (10, (4, 4), "ext_normal"), (11, (3, 2), "normal")])
+def test_bootstrap_model_recovers_message(log_n, budget, strategy):
     n = 1 << log_n
     rng = np.random.default_rng(log_n)
-    p = bs.BootstrapParams()
+    p = bs.BootstrapParams(strategy=strategy)
     spec = bs.BootstrapSpec(log_slots=log_n, level_budget=budget)
-    cts_plans, stc_plans = bs._plans(spec)
+    cts_plans, stc_plans = bs._plans(spec, p)
+    if strategy != "normal":
+        assert all(plan.giant <= p.giants for plan in (*cts_plans, *stc_plans))
     z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
     # coefficient vector of the message at scale Delta' = 2^-10 q_0, plus the
     # integer overflow I of ModRaise (|I| well inside K)
@@ -201,6 +205,7 @@ def test_requirements_and_limb_plan():
     req = bs.requirements([spec], log_n=16)
     assert 2 * 65536 - 1 in req.rotations
     assert all(0 < r < 2 * 65536 for r in req.rotations)
-    assert len(req.rotations) < 64
+    # extended-basis levels (at most 2 giants): up to 32 babies per level
+    assert len(req.rotations) <= 96
     with pytest.raises(NotImplementedError):
         bs.requirements([bs.BootstrapSpec(log_slots=7)], log_n=16)
