@@ -1591,16 +1591,18 @@ int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
   API_END
 }
 
-// Extended-basis babies of `a` for the given rotations, each [2][E][N]
-// before its ModDown: (P c0, P c1) for offset 0, (P sigma(c0) + acc_0, acc_1)
-// otherwise; one ModUp is shared by all of them.
-static void ext_babies(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,
-                       u64 *const *dst, Scratch &s) {
-  const int limbs = a->limbs, E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
-  const size_t N = c->N, P = (size_t)limbs * N;
-  std::vector<u64> gal(n);
+// Extended-basis babies of n ciphertexts for the given rotations, each
+// [2][E][N] before its ModDown: (P c0, P c1) for offset 0,
+// (P sigma(c0) + acc_0, acc_1) otherwise.  One ModUp per ciphertext (batched)
+// is shared by all rotations; each rotation's key is read once for all n.
+// dst[b * n + i] is baby b of ciphertext i.
+static void ext_babies(ckks_context *c, const ckks_ct *const *a, int n, const int64_t *rotations,
+                       int nr, u64 *const *dst, Scratch &s) {
+  const int limbs = a[0]->limbs, E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const size_t N = c->N, P = (size_t)limbs * N, est = (size_t)digits * E * N;
+  std::vector<u64> gal(nr);
   bool any = false;
-  for (int b = 0; b < n; b++) {
+  for (int b = 0; b < nr; b++) {
     gal[b] = galois_of(c, rotations[b]);
     if (gal[b] != 1) {
       get_key(c, gal[b]);
@@ -1609,18 +1611,111 @@ static void ext_babies(ckks_context *c, const ckks_ct *a, const int64_t *rotatio
   }
   u64 *ext = nullptr;
   if (any) {
-    ext = s.get((size_t)digits * E * N);
-    const u64 *d1 = a->d + P;
-    ks_modup(c, limbs, 1, &d1, ext, s);
+    ext = s.get((size_t)n * est);
+    std::vector<const u64 *> d1(n);
+    for (int i = 0; i < n; i++) d1[i] = a[i]->d + P;
+    ks_modup(c, limbs, n, d1.data(), ext, s);
   }
-  for (int b = 0; b < n; b++) {
+  std::vector<int> rb;
+  std::vector<const DeviceKey *> keys;
+  std::vector<u64> ginv;
+  const u64 two_n = 2 * (u64)c->N;
+  for (int b = 0; b < nr; b++) {
     if (gal[b] == 1) {
-      launch_ext_identity(c, a->d, dst[b], limbs);
+      for (int i = 0; i < n; i++) launch_ext_identity(c, a[i]->d, dst[b * n + i], limbs);
       continue;
     }
-    launch_key_inner(c, strided(ext, 0), strided(dst[b], 0), 1, get_key(c, gal[b]), digits, E,
-                     limbs, gal[b]);
-    launch_ext_add_pc0(c, a->d, dst[b], limbs, gal[b]);
+    rb.push_back(b);
+    keys.push_back(&get_key(c, gal[b]));
+    // the units mod 2N have order N, so g^-1 = g^(N-1)
+    u64 inv = 1, base = gal[b] % two_n;
+    for (u64 e = c->N - 1; e; e >>= 1, base = base * base % two_n)
+      if (e & 1) inv = inv * base % two_n;
+    ginv.push_back(inv);
+  }
+  if (rb.empty()) return;
+  // every rotation of a chunk of ciphertexts in one pass over the digits
+  for (int i0 = 0; i0 < n; i0 += kMultiItems) {
+    const int ni = std::min(kMultiItems, n - i0);
+    std::vector<const u64 *> table(rb.size() * ni);
+    for (size_t r = 0; r < rb.size(); r++)
+      for (int it = 0; it < ni; it++) table[r * ni + it] = dst[(size_t)rb[r] * n + i0 + it];
+    u64 *dtab = s.get(table.size());
+    HIPCHECK(hipMemcpyAsync(dtab, table.data(), sizeof(u64) * table.size(),
+                            hipMemcpyHostToDevice, c->stream));
+    Batch c0{};
+    for (int it = 0; it < ni; it++) c0.p[it] = a[i0 + it]->d;
+    launch_key_inner_multi(c, ext + (size_t)i0 * est, est, ni, keys, ginv, c0,
+                           (const u64 *const *)dtab, digits, E, limbs);
+  }
+}
+
+// hoisted_mac_sum_ext for n ciphertexts at one level sharing the plaintexts.
+static void mac_sum_ext(ckks_context *c, const ckks_ct *const *a, int n,
+                        const int64_t *baby_rotations, int B, const ckks_ct *const *pts,
+                        int64_t giant_rotation, int giant_count, ckks_ct **out) {
+  require(n >= 1 && n <= kMaxBatch, "ciphertext count must be in [1, 64]");
+  require(B >= 1 && B <= kMaxBatch, "baby count must be in [1, 64]");
+  require(giant_count >= 1, "giant_count must be positive");
+  const int limbs = a[0]->limbs, E = limbs + c->alpha;
+  for (int i = 0; i < n; i++) {
+    check_ct(c, a[i], "hoisted_mac_sum_ext");
+    require(a[i]->polys == 2 && !a[i]->is_ext && a[i]->limbs == limbs,
+            "hoisted_mac_sum_ext expects degree-1 Q-basis ciphertexts at one level");
+  }
+  for (int i = 0; i < B * giant_count; i++) {
+    check_ct(c, pts[i], "hoisted_mac_sum_ext");
+    require(pts[i]->polys == 1 && pts[i]->is_ext && pts[i]->limbs == limbs,
+            "plaintexts must be extended (Q u P) at the ciphertexts' level");
+  }
+  const u64 gg = galois_of(c, giant_rotation);
+  if (giant_count > 1 && gg != 1) get_key(c, gg);
+  const size_t N = c->N, P = (size_t)limbs * N, EP = 2 * (size_t)E * N;
+  Scratch s(c);
+  u64 *bab = s.get((size_t)B * n * EP);
+  std::vector<u64 *> bp((size_t)B * n);
+  for (size_t k = 0; k < bp.size(); k++) bp[k] = bab + k * EP;
+  ext_babies(c, a, n, baby_rotations, B, bp.data(), s);
+  u64 *inner_ext = s.get((size_t)n * EP);
+  u64 *inner = s.get((size_t)n * 2 * P);
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  for (int g = giant_count - 1; g >= 0; g--) {
+    Batch ptb{};
+    for (int b = 0; b < B; b++) ptb.p[b] = pts[g * B + b]->d;
+    for (int i = 0; i < n; i++) {
+      Batch bb{};
+      for (int b = 0; b < B; b++) bb.p[b] = bp[(size_t)b * n + i];
+      launch_mac(c, bb, ptb, B, inner_ext + (size_t)i * EP, E, limbs);
+    }
+    const bool first = out[0] == nullptr;
+    std::vector<KsJob> jobs(n);
+    for (int i = 0; i < n; i++) {
+      if (first)
+        out[i] = new_ct(c, 2, limbs, 0, a[i]->slots, a[i]->scale * pts[0]->scale,
+                        a[i]->scale_degree + pts[0]->scale_degree);
+      u64 *dst = first ? out[i]->d : inner + (size_t)i * 2 * P;
+      jobs[i] = KsJob{0, nullptr, 1, nullptr, nullptr, dst, dst + P};
+    }
+    {
+      Scratch s2(c);
+      ks_moddown(c, limbs, inner_ext, jobs, s2);
+    }
+    if (first) continue;
+    std::vector<ckks_ct *> rot(n);
+    for (int i = 0; i < n; i++)
+      rot[i] = new_ct(c, 2, limbs, 0, out[i]->slots, out[i]->scale, out[i]->scale_degree);
+    if (gg == 1) {
+      for (int i = 0; i < n; i++)
+        HIPCHECK(hipMemcpyAsync(rot[i]->d, out[i]->d, out[i]->bytes, hipMemcpyDeviceToDevice,
+                                c->stream));
+    } else {
+      std::vector<const ckks_ct *> cur(out, out + n);
+      rotate_batch(c, cur.data(), n, gg, rot.data());
+    }
+    for (int i = 0; i < n; i++) {
+      launch_addsub(c, rot[i]->d, inner + (size_t)i * 2 * P, out[i]->d, 2, limbs, limbs, 0);
+      free_ct(rot[i]);
+    }
   }
 }
 
@@ -1628,55 +1723,38 @@ int ckks_hoisted_mac_sum_ext(ckks_context *c, const ckks_ct *a, const int64_t *b
                              int B, const ckks_ct *const *pts, int64_t giant_rotation,
                              int giant_count, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "hoisted_mac_sum_ext");
-  require(baby_rotations && pts && out, "null argument");
-  require(B >= 1 && B <= kMaxBatch, "baby count must be in [1, 64]");
-  require(giant_count >= 1, "giant_count must be positive");
-  require(a->polys == 2 && !a->is_ext, "hoisted_mac_sum_ext expects a degree-1 Q-basis ciphertext");
-  const int limbs = a->limbs, E = limbs + c->alpha;
-  for (int i = 0; i < B * giant_count; i++) {
-    check_ct(c, pts[i], "hoisted_mac_sum_ext");
-    require(pts[i]->polys == 1 && pts[i]->is_ext && pts[i]->limbs == limbs,
-            "plaintexts must be extended (Q u P) at the ciphertext's level");
+  require(c && a && baby_rotations && pts && out, "null argument");
+  mac_sum_ext(c, &a, 1, baby_rotations, B, pts, giant_rotation, giant_count, out);
+  API_END
+}
+
+int ckks_hoisted_mac_sum_ext_many(ckks_context *c, const ckks_ct *const *a, int n,
+                                  const int64_t *baby_rotations, int B,
+                                  const ckks_ct *const *pts, int64_t giant_rotation,
+                                  int giant_count, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && baby_rotations && pts && out, "null argument");
+  mac_sum_ext(c, a, n, baby_rotations, B, pts, giant_rotation, giant_count, out);
+  API_END
+}
+
+int ckks_rescale_many(ckks_context *c, const ckks_ct *const *a, int n, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && out, "null argument");
+  require(n >= 1, "need at least one ciphertext");
+  for (int i = 0; i < n; i++) {
+    check_ct(c, a[i], "rescale_many");
+    require(!a[i]->is_ext && a[i]->polys >= 1 && a[i]->limbs == a[0]->limbs &&
+                a[i]->polys == a[0]->polys,
+            "rescale_many expects Q-basis ciphertexts of one shape");
   }
-  const u64 gg = galois_of(c, giant_rotation);
-  if (giant_count > 1 && gg != 1) get_key(c, gg);
-  const double scale = a->scale * pts[0]->scale;
-  const int sdeg = a->scale_degree + pts[0]->scale_degree;
-  const size_t N = c->N, P = (size_t)limbs * N;
-  Scratch s(c);
-  u64 *bab = s.get((size_t)B * 2 * E * N);
-  std::vector<u64 *> bp(B);
-  Batch bb{};
-  for (int b = 0; b < B; b++) bb.p[b] = bp[b] = bab + (size_t)b * 2 * E * N;
-  ext_babies(c, a, baby_rotations, B, bp.data(), s);
-  u64 *inner_ext = s.get(2 * (size_t)E * N);
-  u64 *inner = s.get(2 * P);
-  ckks_ct *acc = nullptr;
-  for (int g = giant_count - 1; g >= 0; g--) {
-    Batch ptb{};
-    for (int b = 0; b < B; b++) ptb.p[b] = pts[g * B + b]->d;
-    launch_mac(c, bb, ptb, B, inner_ext, E, limbs);
-    const bool first = acc == nullptr;
-    if (first) acc = new_ct(c, 2, limbs, 0, a->slots, scale, sdeg);
-    u64 *dst = first ? acc->d : inner;
-    {
-      Scratch s2(c);
-      std::vector<KsJob> jobs{KsJob{0, nullptr, 1, nullptr, nullptr, dst, dst + P}};
-      ks_moddown(c, limbs, inner_ext, jobs, s2);
-    }
-    if (first) continue;
-    ckks_ct *rot = new_ct(c, 2, limbs, 0, acc->slots, scale, sdeg);
-    if (gg == 1)
-      HIPCHECK(hipMemcpyAsync(rot->d, acc->d, acc->bytes, hipMemcpyDeviceToDevice, c->stream));
-    else {
-      const ckks_ct *ac = acc;
-      rotate_batch(c, &ac, 1, gg, &rot);
-    }
-    launch_addsub(c, rot->d, inner, acc->d, 2, limbs, limbs, 0);
-    free_ct(rot);
+  require(a[0]->limbs >= 2, "rescale needs at least two limbs");
+  for (int i = 0; i < n; i++) {
+    const double q = (double)c->primes[a[i]->limbs - 1];
+    out[i] = new_ct(c, a[i]->polys, a[i]->limbs - 1, 0, a[i]->slots, a[i]->scale / q,
+                    a[i]->scale_degree > 1 ? a[i]->scale_degree - 1 : 1);
   }
-  *out = acc;
+  rescale_batch(c, a, n, out);
   API_END
 }
 
@@ -1694,7 +1772,7 @@ int ckks_hoisted_rotate_ext(ckks_context *c, const ckks_ct *a, const int64_t *ro
     dst[r] = out[r]->d;
   }
   Scratch s(c);
-  ext_babies(c, a, rotations, n, dst.data(), s);
+  ext_babies(c, &a, 1, rotations, n, dst.data(), s);
   API_END
 }
 

@@ -25,6 +25,7 @@ namespace ckks {
 constexpr int kMaxBatch = 64;    // explicit pointers per kernel argument block
 constexpr int kMaxDigitSize = 16;  // Montgomery fold bound: 16 * 2^60 <= 2^64
 constexpr int kMaxDigits = 8;
+constexpr int kMultiItems = 4;    // items per multi-rotation key inner product launch
 
 // Per-prime constants, resident in device memory.
 struct ModQ {
@@ -259,6 +260,14 @@ void launch_encode_diagonals(ckks_context *c, const void *w, int dtype, const St
                              const u64 *maps, const DiagGeom &gm, int rows, int slots,
                              double scale, int limbs, int is_ext, ckks_ct **out);
 void launch_mod_raise(ckks_context *c, const u64 *coef, u64 *out, int polys, int target);
+struct MultiKeys {  // one key and inverse Galois element per rotation
+  const u64 *key[kMaxBatch];
+  u64 ginv[kMaxBatch];
+};
+void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, int n_items,
+                            const std::vector<const DeviceKey *> &keys,
+                            const std::vector<u64> &galois_inv, const Batch &c0,
+                            const u64 *const *d_outp, int digits, int E, int q_limbs);
 void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);
 void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64 galois);
 // MAC over limbs_total limbs per component; limbs >= q_limbs are special

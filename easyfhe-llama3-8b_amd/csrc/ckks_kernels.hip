@@ -1300,6 +1300,95 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
 }
 
 // ===========================================================================
+// Key inner products of several rotations sharing one ModUp (hoisted babies),
+// written before ModDown in the Q u P basis:
+//   acc_b[t] = sum_j ext_j[s] key_b,j[t],  t = pi_{g_b^-1}(s),
+// i.e. the automorphism is applied on the output side, so each thread reads
+// the extended digits (and c0) at its own index s once for all babies.  With
+// c0 given, acc_b,0[t] += P c0[s] on the Q limbs (the extended lift).
+// grid (N / 256, E); up to kMultiItems items per launch.
+// ===========================================================================
+
+template <int MD>
+__global__ __launch_bounds__(TPB) void k_key_inner_multi(
+    Strided ext, int n_items, MultiKeys mk, int n_babies, Batch c0, const u64 *__restrict__ pmod,
+    const u64 *const *__restrict__ outp, int digits, int E, int q_limbs, int L, int K, int logN,
+    const ModQ *__restrict__ mods) {
+  const int s = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const int p = prime_of(l, q_limbs, L);
+  const ModQ M = mods[p];
+  const size_t N = (size_t)1 << logN;
+  u64 x[kMultiItems][MD];
+  u64 pc[kMultiItems];
+  const bool lift = l < q_limbs;
+#pragma unroll
+  for (int it = 0; it < kMultiItems; it++) {
+    if (it < n_items) {
+      const u64 *e = ext.base + (size_t)it * ext.stride;
+#pragma unroll
+      for (int j = 0; j < MD; j++)
+        if (j < digits) x[it][j] = e[((size_t)j * E + l) * N + s];
+      const u64 *c = batch_ptr(c0, it);
+      pc[it] = (lift && c) ? shoup_mul(c[(size_t)l * N + s], pmod[2 * l], pmod[2 * l + 1], M.q)
+                           : 0;
+    }
+  }
+  for (int b = 0; b < n_babies; b++) {
+    const u32 t = autom_index((u32)s, mk.ginv[b], logN);
+    const u64 *key = mk.key[b];
+    u64 kb[MD], ka[MD];
+#pragma unroll
+    for (int j = 0; j < MD; j++) {
+      if (j < digits) {
+        kb[j] = key[((size_t)(2 * j) * K + p) * N + t];
+        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + t];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kMultiItems; it++) {
+      if (it < n_items) {
+        u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+        for (int j = 0; j < MD; j++) {
+          if (j < digits) {
+            mac_wide(h0, l0, x[it][j], kb[j]);
+            mac_wide(h1, l1, x[it][j], ka[j]);
+          }
+        }
+        u64 *o = (u64 *)outp[(size_t)b * n_items + it];
+        o[(size_t)l * N + t] = add_mod(redc(h0, l0, M.q, M.qinv), pc[it], M.q);
+        o[((size_t)E + l) * N + t] = redc(h1, l1, M.q, M.qinv);
+      }
+    }
+  }
+}
+
+void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, int n_items,
+                            const std::vector<const DeviceKey *> &keys,
+                            const std::vector<u64> &galois_inv, const Batch &c0,
+                            const u64 *const *d_outp, int digits, int E, int q_limbs) {
+  if (n_items < 1 || n_items > kMultiItems) throw std::invalid_argument("key_inner_multi: items");
+  const int nb = (int)keys.size();
+  if (nb < 1 || nb > kMaxBatch) throw std::invalid_argument("key_inner_multi: babies");
+  MultiKeys mk{};
+  for (int b = 0; b < nb; b++) {
+    mk.key[b] = keys[b]->data;
+    mk.ginv[b] = galois_inv[b];
+  }
+  dim3 grid(c->N / TPB, E);
+  if (digits <= 4)
+    hipLaunchKernelGGL(k_key_inner_multi<4>, grid, dim3(TPB), 0, c->stream,
+                       Strided{(u64 *)ext, ext_stride}, n_items, mk, nb, c0, c->d_pmod, d_outp,
+                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods);
+  else
+    hipLaunchKernelGGL(k_key_inner_multi<kMaxDigits>, grid, dim3(TPB), 0, c->stream,
+                       Strided{(u64 *)ext, ext_stride}, n_items, mk, nb, c0, c->d_pmod, d_outp,
+                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
 // ModDown combine: out_c[l] = (acc_c[l] - conv_c[l]) P^-1 + add_c[l][sigma(k)]
 // acc item layout [2][E][N], conv [2][limbs][N] (internal, strided); add_c and
 // out_c are [limbs][N] polynomials per item (a null add pointer adds

@@ -377,6 +377,84 @@ def bootstrap(ct, context, program: BootstrapProgram):
     return u
 
 
+def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> list:
+    n = prog.spec.slots
+    plan = lv.plan
+    if prog.evalmod.strategy == "normal":
+        return [_linear_level(x, lv, prog, ctx) for x in xs]
+    state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
+    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=True)
+    accs = fhe.hoisted_mac_sum_ext_many(xs, _baby_offsets(plan, n), pts,
+                                        _giant_offset(plan, n), plan.giant, ctx)
+    for _ in range(lv.primes):
+        accs = fhe.rescale_many(accs, ctx)
+    for a in accs:
+        a.set_scale(lv.out_scale, 1)
+    return accs
+
+
+def _bootstrap_group(cts: list, ctx, prog: BootstrapProgram) -> list:
+    q0 = float(ctx.primes()[0])
+    xs, ratios = [], []
+    for ct in cts:
+        if ct.degree != 1 or ct.is_ext:
+            raise ValueError("bootstrap expects degree-1 Q-basis ciphertexts")
+        if int(ct.slots) != prog.spec.slots:
+            raise ValueError(f"bootstrap input slots={ct.slots} != program slots={prog.spec.slots}")
+        x, ratio = _prescale(ct, prog, ctx)
+        x = fhe.mod_raise(x, prog.raise_limbs, ctx)
+        x.set_scale(2.0 * prog.evalmod.K * q0, 1)
+        xs.append(x)
+        ratios.append(ratio)
+    for lv in prog.cts:
+        xs = _linear_level_many(xs, lv, prog, ctx)
+    ops = cheb.BatchLadderOps(ctx, prog.ladder)
+    conj = fhe.homo_rotate_many(xs, 2 * ctx.N - 1, ctx)
+    y, yc = cheb.LCt(xs, 0), cheb.LCt(conj, 0)
+    re = ops.add(y, yc)
+    im = [fhe.homo_mul_i(d, ctx, negative=True) for d in ops.add(y, yc, sign=-1.0).ct]
+    del xs, conj, y, yc
+    k = len(cts)
+    # real and imaginary parts of the whole group run through EvalMod together
+    s = _evalmod(ops, cheb.LCt(re.ct + im, 0), prog).ct
+    u = [fhe.homo_add(s[i], fhe.homo_mul_i(s[k + i], ctx), ctx) for i in range(k)]
+    del s
+    for lv in prog.stc:
+        u = _linear_level_many(u, lv, prog, ctx)
+    for x, r in zip(u, ratios):
+        x.set_scale(prog.stc[-1].out_scale * r, 1)
+    return u
+
+
+def bootstrap_many(cts, context, program: BootstrapProgram, group: int = 16) -> list:
+    """Refreshed copies of several ciphertexts, ``group`` at a time: every
+    key switch of a group runs as one batched launch that reads its key once,
+    and EvalMod evaluates the group's real and imaginary parts as one batch.
+    Identical results to ``bootstrap`` per ciphertext."""
+    ctx = getattr(context, "context", context)
+    cts = list(cts)
+    out: list = []
+    for i0 in range(0, len(cts), max(1, int(group))):
+        out.extend(_bootstrap_group(cts[i0: i0 + max(1, int(group))], ctx, program))
+    return out
+
+
+def bootstrap_pair(real_a, real_b, context, program: BootstrapProgram):
+    """Two real-valued ciphertexts refreshed by one bootstrap: a + i b is
+    bootstrapped and split by one conjugation (reference
+    operators/norm/refresh.py:33-67).  The split yields 2a and 2b; the
+    factor 2 is taken out of the recorded scale, so no level is spent."""
+    ctx = getattr(context, "context", context)
+    packed = fhe.homo_add(real_a, fhe.homo_mul_i(real_b, ctx), ctx)
+    value = bootstrap(packed, ctx, program)
+    conj = fhe.homo_rotate(value, 2 * ctx.N - 1, ctx)
+    twice_a = fhe.homo_add(value, conj, ctx)
+    twice_b = fhe.homo_mul_i(fhe.homo_sub(conj, value, ctx), ctx)
+    for t in (twice_a, twice_b):
+        t.set_scale(2.0 * float(t.state.scaling_factor), 1)
+    return twice_a, twice_b
+
+
 def _to_scale(ct, limbs: int, scale: float, value: float, ctx):
     """value * ct on ``limbs`` limbs at exactly ``scale`` (one rescale; ct
     needs more than ``limbs`` limbs)."""
@@ -422,4 +500,4 @@ def bootstrap_iterated(ct, context, program: BootstrapProgram, iterations: int =
 
 
 __all__ = ["BootstrapParams", "BootstrapProgram", "BootstrapSpec", "Requirements", "bootstrap",
-           "bootstrap_iterated", "generate", "requirements"]
+           "bootstrap_iterated", "bootstrap_many", "bootstrap_pair", "generate", "requirements"]

@@ -221,6 +221,78 @@ class LadderOps:
         return self._settle(self._rescale_steps(prod), lev + 1)
 
 
+class BatchLadderOps(LadderOps):
+    """LadderOps over a group of ciphertexts that share every level (an LCt's
+    ``ct`` is a list): products run as one batched relinearise + rescale, so
+    the relinearisation key is read once per group; constants are encoded once
+    and shared."""
+
+    def _rescale_steps(self, cts):
+        for _ in range(self.lad.step):
+            cts = fhe.rescale_many(cts, self.ctx)
+        return cts
+
+    def _settle(self, cts, level: int):
+        for ct in cts:
+            ct.set_scale(self.lad.scale[level], 1)
+        return LCt(cts, level)
+
+    def combine(self, terms, const: float, level: int) -> LCt:
+        lad = self.lad
+        limbs = lad.entry_limbs(level)
+        target = lad.scale[level] * lad.divisor(level)
+        acc = None
+        for x, w in terms:
+            if w == 0.0:
+                continue
+            cts = x.ct if isinstance(x, LCt) else list(x)
+            src = lad.scale[x.level] if isinstance(x, LCt) else float(cts[0].state.scaling_factor)
+            if int(cts[0].state.cur_limbs) < limbs:
+                raise ValueError("operand is below the requested ladder level")
+            enc = fhe.encode_scalar(float(w), limbs, scaling_factor=target / src, context=self.ctx)
+            terms_i = []
+            for ct in cts:
+                t = fhe.homo_mul_scalar(self._drop(ct, limbs), enc, self.ctx)
+                t.set_scale(target, 2)
+                terms_i.append(t)
+            acc = terms_i if acc is None else [fhe.homo_add(a, t, self.ctx)
+                                               for a, t in zip(acc, terms_i)]
+        if acc is None:
+            raise ValueError("linear combination without ciphertext terms")
+        if const != 0.0:
+            enc = fhe.encode_scalar(float(const), limbs, scaling_factor=target, context=self.ctx)
+            acc = [fhe.homo_add_scalar(a, enc, self.ctx) for a in acc]
+        return self._settle(self._rescale_steps(acc), level)
+
+    def add(self, a: LCt, b: LCt, sign: float = 1.0) -> LCt:
+        lev = max(a.level, b.level)
+        a, b = self.lower(a, lev), self.lower(b, lev)
+        fn = fhe.homo_add if sign > 0 else fhe.homo_sub
+        return LCt([fn(x, y, self.ctx) for x, y in zip(a.ct, b.ct)], lev)
+
+    def add_const(self, a: LCt, c: float) -> LCt:
+        if c == 0.0:
+            return a
+        limbs = int(a.ct[0].state.cur_limbs)
+        enc = fhe.encode_scalar(float(c), limbs, scaling_factor=self.lad.scale[a.level],
+                                context=self.ctx)
+        return LCt([fhe.homo_add_scalar(x, enc, self.ctx) for x in a.ct], a.level)
+
+    def double(self, a: LCt) -> LCt:
+        return LCt([fhe.homo_add(x, x, self.ctx) for x in a.ct], a.level)
+
+    def mul(self, a: LCt, b: LCt) -> LCt:
+        lev = max(a.level, b.level)
+        if lev + 1 > self.lad.depth:
+            raise ValueError("ladder depth exhausted")
+        a, b = self.lower(a, lev), self.lower(b, lev)
+        self.mults += len(a.ct)
+        prods = fhe.homo_mul_relin_rescale_many(a.ct, b.ct, self.ctx)
+        for _ in range(self.lad.step - 1):
+            prods = fhe.rescale_many(prods, self.ctx)
+        return self._settle(prods, lev + 1)
+
+
 class _SymbolicOps:
     """Level bookkeeping only: runs the evaluation schedule without data."""
 
@@ -386,7 +458,7 @@ def eval_chebyshev_series_cipher(input_cipher, coefficients, *, lower_bound: flo
 
 
 __all__ = [
-    "Ladder", "LadderOps", "LCt", "chebyshev_coefficients", "chebyshev_degree",
+    "BatchLadderOps", "Ladder", "LadderOps", "LCt", "chebyshev_coefficients", "chebyshev_degree",
     "chebyshev_depth", "divide_by_t", "eval_chebyshev_series_cipher", "evaluate",
     "evaluate_direct", "plan_baby", "series_depth",
 ]

@@ -684,6 +684,41 @@ def mod_raise(a, target_limbs: int, context=None):
     return _wrap(ctx, out)
 
 
+def rescale_many(cts: Sequence[Ciphertext], context=None) -> list:
+    """fhe.rescale of several ciphertexts of one shape in batched launches."""
+    if not cts:
+        return []
+    ctx = _ctx(cts[0], context)
+    outs = (ctypes.c_void_p * len(cts))()
+    check(lib.ckks_rescale_many(ctx.handle, ptr_array([c.handle for c in cts]), len(cts), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(cts))]
+
+
+def hoisted_mac_sum_ext_many(cts: Sequence[Ciphertext], baby_offsets, plaintexts,
+                             giant_offset: int, giant_count: int, context=None) -> list:
+    """The extended-basis hoisted_mac_sum of several ciphertexts at one level
+    with shared (extended) plaintexts; keys and plaintexts are read once per
+    batch of up to 64."""
+    if not cts:
+        return []
+    ctx = _ctx(cts[0], context)
+    offs = np.asarray([int(o) for o in baby_offsets], dtype=np.int64)
+    B = len(offs)
+    pts = list(plaintexts)[: B * int(giant_count)]
+    if len(pts) < B * int(giant_count):
+        raise ValueError(f"need {B * int(giant_count)} plaintexts, got {len(pts)}")
+    results: list = []
+    for i0 in range(0, len(cts), 64):
+        chunk = cts[i0: i0 + 64]
+        outs = (ctypes.c_void_p * len(chunk))()
+        check(lib.ckks_hoisted_mac_sum_ext_many(
+            ctx.handle, ptr_array([c.handle for c in chunk]), len(chunk),
+            offs.ctypes.data_as(_native.I64P), B, ptr_array([p.handle for p in pts]),
+            int(giant_offset), int(giant_count), outs))
+        results.extend(Ciphertext(ctx, outs[i]) for i in range(len(chunk)))
+    return results
+
+
 def homo_rotate_many(cts: Sequence[Ciphertext], rotation: int, context=None) -> list:
     """One rotation of many same-level ciphertexts; the key is streamed once."""
     cts = list(cts)

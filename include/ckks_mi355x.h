@@ -181,6 +181,15 @@ int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
 int ckks_hoisted_mac_sum_ext(ckks_context *ctx, const ckks_ct *a, const int64_t *baby_rotations,
                              int B, const ckks_ct *const *pts, int64_t giant_rotation,
                              int giant_count, ckks_ct **out);
+/* ckks_hoisted_mac_sum_ext for n ciphertexts at one level sharing the
+ * plaintexts (bootstrap linear levels over a batch): one batched ModUp, each
+ * baby key read once for all n, batched ModDowns and giant rotations. */
+int ckks_hoisted_mac_sum_ext_many(ckks_context *ctx, const ckks_ct *const *a, int n,
+                                  const int64_t *baby_rotations, int B,
+                                  const ckks_ct *const *pts, int64_t giant_rotation,
+                                  int giant_count, ckks_ct **out);
+/* fhe.rescale for n ciphertexts of one shape in batched launches. */
+int ckks_rescale_many(ckks_context *ctx, const ckks_ct *const *a, int n, ckks_ct **out);
 /* fhe.fast_rotate(..., output_ext=True) (reference attention/input.py:792-826):
  * hoisted rotations left in the Q u P basis, i.e. P rot_k(a) before ModDown;
  * the outputs are extended ciphertexts at a's scale. */

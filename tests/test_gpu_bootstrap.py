@@ -114,3 +114,38 @@ def test_bootstrap_two_pass_gains_precision(boot_ctx):
     print(f"one pass {-math.log2(e1):.1f} bits, two passes {-math.log2(e2):.1f} bits")
     assert e1 > 2.0**-20
     assert e2 < e1 / 16
+
+
+def test_bootstrap_many_matches_single(boot_ctx):
+    """Batched groups run the same arithmetic per ciphertext: identical limbs."""
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3),
+                                             output_levels=3))
+    rng = np.random.default_rng(9)
+    zs = [rng.uniform(-1, 1, n) for _ in range(3)]
+    cts = [client.encrypt(z, cur_limbs=1, enc_id=80 + i) for i, z in enumerate(zs)]
+    many = bs.bootstrap_many(cts, ctx, prog, group=2)
+    for ct, got in zip(cts, many):
+        assert np.array_equal(got.download(), bs.bootstrap(ct, ctx, prog).download())
+    for z, got in zip(zs, many):
+        assert -math.log2(np.abs(client.decrypt_complex(got) - z).max()) > 14
+
+
+def test_bootstrap_pair_refreshes_two_real_streams(boot_ctx):
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3),
+                                             output_levels=3))
+    rng = np.random.default_rng(10)
+    a, b = rng.uniform(-1, 1, n), rng.uniform(-1, 1, n)
+    ca = client.encrypt(a, cur_limbs=1, enc_id=90)
+    cb = client.encrypt(b, cur_limbs=1, enc_id=91)
+    ra, rb = bs.bootstrap_pair(ca, cb, ctx, prog)
+    for got, want in ((ra, a), (rb, b)):
+        err = np.abs(client.decrypt_complex(got) - want).max()
+        assert -math.log2(err) > 14, err
