@@ -1738,6 +1738,51 @@ int ckks_hoisted_mac_sum_ext_many(ckks_context *c, const ckks_ct *const *a, int 
   API_END
 }
 
+int ckks_linear_combination(ckks_context *c, const ckks_ct *const *terms, int T, int n,
+                            const double *weights, double constant, int limbs, double scale,
+                            int scale_degree, ckks_ct **out) {
+  API_BEGIN
+  require(c && terms && weights && out, "null argument");
+  require(T >= 1 && T <= 256, "term count must be in [1, 256]");
+  require(n >= 1 && n <= 256, "ciphertext count must be in [1, 256]");
+  check_limbs(c, limbs);
+  for (int t = 0; t < T; t++)
+    for (int i = 0; i < n; i++) {
+      const ckks_ct *x = terms[(size_t)t * n + i];
+      check_ct(c, x, "linear_combination");
+      require(x->polys == 2 && !x->is_ext && x->limbs >= limbs,
+              "terms must be degree-1 Q-basis ciphertexts with at least `limbs` limbs");
+    }
+  for (int t = 0; t < T; t++)
+    require(std::isfinite(weights[t]) && fabs(rint(weights[t])) < ldexp(1.0, 1000),
+            "weights must be finite");
+  std::vector<u64> table(2 * (size_t)T * n);
+  for (size_t j = 0; j < (size_t)T * n; j++) {
+    table[2 * j] = (u64)terms[j]->d;
+    table[2 * j + 1] = (u64)terms[j]->limbs;
+  }
+  std::vector<double> w(T);
+  for (int t = 0; t < T; t++) w[t] = rint(weights[t]);
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  std::vector<u64 *> outp(n);
+  for (int i = 0; i < n; i++) {
+    out[i] = new_ct(c, 2, limbs, 0, terms[i]->slots, scale, scale_degree);
+    outp[i] = out[i]->d;
+  }
+  Scratch s(c);
+  u64 *dtab = s.get(table.size());
+  double *dw = (double *)s.get(T);
+  u64 *dout = s.get(n);
+  u64 *wtab = s.get((size_t)T * limbs);
+  u64 *ctab = s.get(limbs);
+  HIPCHECK(hipMemcpyAsync(dtab, table.data(), sizeof(u64) * table.size(), hipMemcpyHostToDevice,
+                          c->stream));
+  HIPCHECK(hipMemcpyAsync(dw, w.data(), sizeof(double) * T, hipMemcpyHostToDevice, c->stream));
+  HIPCHECK(hipMemcpyAsync(dout, outp.data(), sizeof(u64) * n, hipMemcpyHostToDevice, c->stream));
+  launch_lincomb(c, dtab, T, n, dw, rint(constant), (u64 *const *)dout, limbs, wtab, ctab);
+  API_END
+}
+
 int ckks_rescale_many(ckks_context *c, const ckks_ct *const *a, int n, ckks_ct **out) {
   API_BEGIN
   require(c && a && out, "null argument");

@@ -1579,6 +1579,58 @@ void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64
 }
 
 // ===========================================================================
+// Linear combination of n ciphertexts' terms in one launch:
+//   out_i = sum_t W_t x_(t,i) + C   (C on c0 only), on the first `limbs` limbs
+// of every term, W_t = rint(weight_t) and C = rint(constant) as residues.
+// Terms: table of (pointer, limbs) per (t, i), t-major.  grid (N/256, limbs, 2n)
+// ===========================================================================
+
+__device__ u64 dbl_residue(double v, const ModQ &M);
+
+__global__ void k_lincomb_prep(const double *__restrict__ w, int T, double cst, int limbs,
+                               u64 *__restrict__ wtab, u64 *__restrict__ ctab,
+                               const ModQ *__restrict__ mods) {
+  const int l = blockIdx.x, t = threadIdx.x;
+  const ModQ M = mods[l];
+  if (t < T) wtab[(size_t)t * limbs + l] = to_mont(dbl_residue(w[t], M), M);
+  if (t == 0) ctab[l] = dbl_residue(cst, M);
+}
+
+__global__ void k_lincomb(const u64 *__restrict__ table, int T, int n,
+                          const u64 *__restrict__ wtab, const u64 *__restrict__ ctab,
+                          u64 *const *__restrict__ outp, int limbs, int logN,
+                          const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const int i = blockIdx.z >> 1, poly = blockIdx.z & 1;
+  const size_t N = (size_t)1 << logN;
+  const ModQ M = mods[l];
+  u64 acc = 0, hi = 0, lo = 0;
+  for (int t = 0; t < T; t++) {
+    const u64 *x = (const u64 *)table[2 * ((size_t)t * n + i)];
+    const u64 tl = table[2 * ((size_t)t * n + i) + 1];
+    mac_wide(hi, lo, x[((size_t)poly * tl + l) * N + k], wtab[(size_t)t * limbs + l]);
+    if ((t & 15) == 15 || t == T - 1) {
+      acc = add_mod(acc, redc(hi, lo, M.q, M.qinv), M.q);
+      hi = lo = 0;
+    }
+  }
+  if (poly == 0) acc = add_mod(acc, ctab[l], M.q);
+  outp[i][((size_t)poly * limbs + l) * N + k] = acc;
+}
+
+void launch_lincomb(ckks_context *c, const u64 *d_table, int T, int n, const double *d_w,
+                    double cst, u64 *const *d_outp, int limbs, u64 *wtab, u64 *ctab) {
+  hipLaunchKernelGGL(k_lincomb_prep, dim3(limbs), dim3(TPB), 0, c->stream, d_w, T, rint(cst),
+                     limbs, wtab, ctab, c->d_mods);
+  LAUNCH_CHECK();
+  dim3 grid(c->N / TPB, limbs, 2 * n);
+  hipLaunchKernelGGL(k_lincomb, grid, dim3(TPB), 0, c->stream, d_table, T, n, wtab, ctab, d_outp,
+                     limbs, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
 // ChaCha20 (RFC 8439) counter-mode PRNG: key = (seed lo, seed hi, 0, ...),
 // nonce = (domain, id, sub), counter = block index.
 // ===========================================================================

@@ -164,7 +164,7 @@ class LadderOps:
         lad = self.lad
         limbs = lad.entry_limbs(level)
         target = lad.scale[level] * lad.divisor(level)
-        acc = None
+        cts, weights = [], []
         for x, w in terms:
             if w == 0.0:
                 continue
@@ -172,17 +172,13 @@ class LadderOps:
             src = lad.scale[x.level] if isinstance(x, LCt) else float(ct.state.scaling_factor)
             if int(ct.state.cur_limbs) < limbs:
                 raise ValueError("operand is below the requested ladder level")
-            ct = self._drop(ct, limbs)
-            enc = fhe.encode_scalar(float(w), limbs, scaling_factor=target / src, context=self.ctx)
-            term = fhe.homo_mul_scalar(ct, enc, self.ctx)
-            term.set_scale(target, 2)
-            acc = term if acc is None else fhe.homo_add(acc, term, self.ctx)
-        if acc is None:
+            cts.append([ct])
+            weights.append(float(w) * (target / src))
+        if not cts:
             raise ValueError("linear combination without ciphertext terms")
-        if const != 0.0:
-            acc = fhe.homo_add_scalar(
-                acc, fhe.encode_scalar(float(const), limbs, scaling_factor=target,
-                                       context=self.ctx), self.ctx)
+        # one launch: sum_t rint(w_t target / src_t) x_t + rint(const target)
+        acc = fhe.linear_combination(cts, weights, float(const) * target, limbs, target, 2,
+                                     self.ctx)[0]
         return self._settle(self._rescale_steps(acc), level)
 
     def lower(self, x: LCt, level: int) -> LCt:
@@ -241,7 +237,7 @@ class BatchLadderOps(LadderOps):
         lad = self.lad
         limbs = lad.entry_limbs(level)
         target = lad.scale[level] * lad.divisor(level)
-        acc = None
+        rows, weights = [], []
         for x, w in terms:
             if w == 0.0:
                 continue
@@ -249,19 +245,12 @@ class BatchLadderOps(LadderOps):
             src = lad.scale[x.level] if isinstance(x, LCt) else float(cts[0].state.scaling_factor)
             if int(cts[0].state.cur_limbs) < limbs:
                 raise ValueError("operand is below the requested ladder level")
-            enc = fhe.encode_scalar(float(w), limbs, scaling_factor=target / src, context=self.ctx)
-            terms_i = []
-            for ct in cts:
-                t = fhe.homo_mul_scalar(self._drop(ct, limbs), enc, self.ctx)
-                t.set_scale(target, 2)
-                terms_i.append(t)
-            acc = terms_i if acc is None else [fhe.homo_add(a, t, self.ctx)
-                                               for a, t in zip(acc, terms_i)]
-        if acc is None:
+            rows.append(cts)
+            weights.append(float(w) * (target / src))
+        if not rows:
             raise ValueError("linear combination without ciphertext terms")
-        if const != 0.0:
-            enc = fhe.encode_scalar(float(const), limbs, scaling_factor=target, context=self.ctx)
-            acc = [fhe.homo_add_scalar(a, enc, self.ctx) for a in acc]
+        acc = fhe.linear_combination(rows, weights, float(const) * target, limbs, target, 2,
+                                     self.ctx)
         return self._settle(self._rescale_steps(acc), level)
 
     def add(self, a: LCt, b: LCt, sign: float = 1.0) -> LCt:

@@ -684,6 +684,24 @@ def mod_raise(a, target_limbs: int, context=None):
     return _wrap(ctx, out)
 
 
+def linear_combination(terms, weights, constant: float, limbs: int, scale: float,
+                       scale_degree: int = 2, context=None) -> list:
+    """``out_i = sum_t rint(weights[t]) terms[t][i] + rint(constant)`` for every
+    ciphertext i in one launch, on the first ``limbs`` limbs of each term
+    (weights already carry their encoding scales); ``terms`` is [T][n]."""
+    terms = [list(t) for t in terms]
+    T, n = len(terms), len(terms[0])
+    if any(len(t) != n for t in terms):
+        raise ValueError("every term needs one ciphertext per output")
+    ctx = _ctx(terms[0][0], context)
+    w = np.ascontiguousarray(np.asarray(weights, dtype=np.float64))
+    outs = (ctypes.c_void_p * n)()
+    check(lib.ckks_linear_combination(ctx.handle, ptr_array([x.handle for t in terms for x in t]),
+                                      T, n, w.ctypes.data_as(_native.DP), float(constant),
+                                      int(limbs), float(scale), int(scale_degree), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(n)]
+
+
 def rescale_many(cts: Sequence[Ciphertext], context=None) -> list:
     """fhe.rescale of several ciphertexts of one shape in batched launches."""
     if not cts:

@@ -188,6 +188,15 @@ int ckks_hoisted_mac_sum_ext_many(ckks_context *ctx, const ckks_ct *const *a, in
                                   const int64_t *baby_rotations, int B,
                                   const ckks_ct *const *pts, int64_t giant_rotation,
                                   int giant_count, ckks_ct **out);
+/* Linear combination in one launch for n ciphertexts (the many small
+ * homo_mul_scalar / homo_add launches of a polynomial's leaf sums, reference
+ * operators/nonlinear/polynomial.py:182-199):
+ *   out_i = sum_t rint(weights[t]) terms[t*n + i] + rint(constant) (on c0),
+ * over the first `limbs` limbs of every term; weights are already multiplied
+ * by their encoding scales; the outputs carry (scale, scale_degree). */
+int ckks_linear_combination(ckks_context *ctx, const ckks_ct *const *terms, int T, int n,
+                            const double *weights, double constant, int limbs, double scale,
+                            int scale_degree, ckks_ct **out);
 /* fhe.rescale for n ciphertexts of one shape in batched launches. */
 int ckks_rescale_many(ckks_context *ctx, const ckks_ct *const *a, int n, ckks_ct **out);
 /* fhe.fast_rotate(..., output_ext=True) (reference attention/input.py:792-826):

@@ -424,3 +424,29 @@ def test_keyswitch_size_parity():
         exp = orc.rescale(orc.relinearize(orc.tensor(refs[i], refs[i])))
         assert np.array_equal(prods[i].download(), exp)
         assert np.abs(client.decrypt(prods[i]) - zs[i] ** 2).max() < 1e-6
+
+
+def test_linear_combination_matches_composed_ops():
+    """One fused launch = mul_scalar + add + add_scalar on the same words,
+    with terms holding more limbs than the output."""
+    fhe = _fhe()
+    client, ctx, orc = _pair("small")
+    slots = ctx.max_slots
+    rng = np.random.default_rng(23)
+    n, limbs = 3, ctx.L - 2
+    terms = [[client.encrypt(rng.uniform(-1, 1, slots), cur_limbs=ctx.L - t, enc_id=200 + 10 * t + i)
+              for i in range(n)] for t in range(3)]
+    weights = [3.0 * 2**30, -7.5 * 2**30, 2.0**33 + 0.25]
+    const, scale = -0.375 * 2**70, 2.0**70
+    fused = fhe.linear_combination(terms, weights, const, limbs, scale, 2, ctx)
+    for i in range(n):
+        acc = None
+        for t in range(3):
+            x = fhe.align_to(terms[t][i], terms[t][i].state.replace(cur_limbs=limbs,
+                                                                    scaling_factor=None), ctx)
+            enc = fhe.encode_scalar(weights[t], limbs, scaling_factor=1.0, context=ctx)
+            term = fhe.homo_mul_scalar(x, enc, ctx)
+            acc = term if acc is None else fhe.homo_add(acc, term, ctx)
+        acc = fhe.homo_add_scalar(acc, fhe.encode_scalar(const, limbs, scaling_factor=1.0,
+                                                         context=ctx), ctx)
+        assert np.array_equal(fused[i].download(), acc.download()), i
