@@ -1682,11 +1682,7 @@ static void mac_sum_ext(ckks_context *c, const ckks_ct *const *a, int n,
   for (int g = giant_count - 1; g >= 0; g--) {
     Batch ptb{};
     for (int b = 0; b < B; b++) ptb.p[b] = pts[g * B + b]->d;
-    for (int i = 0; i < n; i++) {
-      Batch bb{};
-      for (int b = 0; b < B; b++) bb.p[b] = bp[(size_t)b * n + i];
-      launch_mac(c, bb, ptb, B, inner_ext + (size_t)i * EP, E, limbs);
-    }
+    launch_mac_many(c, bab, n, ptb, B, inner_ext, E, limbs);
     const bool first = out[0] == nullptr;
     std::vector<KsJob> jobs(n);
     for (int i = 0; i < n; i++) {

@@ -1534,6 +1534,39 @@ void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u
   LAUNCH_CHECK();
 }
 
+// Extended-basis MAC of n ciphertexts sharing the plaintexts: babies at
+// bab[(b n + i)][2][E][N], out[i][2][E][N]; the loop over ciphertexts is inside
+// each thread, so every plaintext word is fetched from HBM once (its repeats
+// hit L2).  grid (N / 256, E, 2)
+__global__ void k_mac_many(const u64 *__restrict__ bab, int n, Batch pts, int B,
+                           u64 *__restrict__ out, int E, int q_limbs, int L, int logN,
+                           const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, comp = blockIdx.z;
+  const size_t N = (size_t)1 << logN, EP = 2 * (size_t)E * N;
+  const ModQ M = mods[prime_of(l, q_limbs, L)];
+  const size_t off = ((size_t)comp * E + l) * N + k;
+  for (int i = 0; i < n; i++) {
+    u64 acc = 0, hi = 0, lo = 0;
+    for (int b = 0; b < B; b++) {
+      mac_wide(hi, lo, bab[((size_t)b * n + i) * EP + off], batch_ptr(pts, b)[(size_t)l * N + k]);
+      if ((b & 15) == 15 || b == B - 1) {
+        acc = add_mod(acc, redc(hi, lo, M.q, M.qinv), M.q);
+        hi = lo = 0;
+      }
+    }
+    out[(size_t)i * EP + off] = to_mont(acc, M);
+  }
+}
+
+void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, u64 *out,
+                     int E, int q_limbs) {
+  dim3 grid(c->N / TPB, E, 2);
+  hipLaunchKernelGGL(k_mac_many, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, out, E, q_limbs,
+                     c->L, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
 // Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0
 // on the special limbs (layout [2][limbs + alpha][N]); grid (N / 256, E, 2)
 __global__ void k_ext_identity(const u64 *__restrict__ ct, u64 *__restrict__ out, int limbs,
