@@ -78,6 +78,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--cts", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-bootstrap", action="store_true",
+                    help="skip the bootstrap measurement of the default run")
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap"],
                     default="keyswitch",
@@ -215,25 +217,29 @@ def main() -> int:
             "limb_polys_per_launch": limb_polys,
         },
     }
+    if not args.no_bootstrap:
+        # the bootstrap workload on the same chain (32 ciphertexts at one limb)
+        for c in cts:
+            c.release()
+        result["bootstrap"] = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group,
+                                                args.budget, 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
     return 0
 
 
-def bootstrap_bench(spec, args) -> int:
-    """Full-slot bootstrap of --boot-cts ciphertexts at the bottom level (one
-    limb, values uniform[-1, 1] from seed 0): CoeffToSlot / SlotToCoeff with
-    the given level budget, EvalMod at a 2^80 working scale; output_levels is
-    the most the chain allows.  Reports bootstraps/s and precision bits."""
+def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int) -> dict:
+    """Full-slot bootstrap of n_cts ciphertexts at the bottom level (one limb,
+    values uniform[-1, 1] from seed 0) in batched groups: CoeffToSlot /
+    SlotToCoeff with the given level budget, EvalMod at a 2^80 working scale,
+    output_levels the most the chain allows.  Returns rate, precision and the
+    program's shape."""
     import math
 
-    from easyfhe import fhe
     from easyfhe.bs import openfhe as bs
 
-    spec.rotations = ()
-    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
-    budget = tuple(int(v) for v in args.budget)
+    budget = tuple(int(v) for v in budget)
     probe = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget, output_levels=0)
     depth = bs.generate(ctx, probe).depth_limbs
     bspec = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget,
@@ -243,11 +249,11 @@ def bootstrap_bench(spec, args) -> int:
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
-    zs = [rng.uniform(-1, 1, ctx.max_slots) for _ in range(args.boot_cts)]
-    cts = [client.encrypt(z, cur_limbs=1, enc_id=i + 1) for i, z in enumerate(zs)]
-    group = max(1, min(args.boot_group, len(cts)))
+    zs = [rng.uniform(-1, 1, ctx.max_slots) for _ in range(n_cts)]
+    cts = [client.encrypt(z, cur_limbs=1, enc_id=100000 + i) for i, z in enumerate(zs)]
+    group = max(1, min(group, len(cts)))
     t0 = time.perf_counter()
-    for _ in range(max(1, args.warmup)):
+    for _ in range(max(1, warmup)):
         for o in bs.bootstrap_many(cts[:group], ctx, prog, group=group):
             o.release()
     ctx.synchronize()
@@ -260,14 +266,45 @@ def bootstrap_bench(spec, args) -> int:
     ctx.synchronize()
     wall = time.perf_counter() - t0
     bits = [-math.log2(np.abs(client.decrypt_complex(o) - z).max()) for o, z in zip(outs, zs)]
-    result = {
-        "metric": "bootstrap/s @N=2^16",
+    for o in outs:
+        o.release()
+    prog.release()
+    return {
         "value": round(len(cts) / wall, 3),
         "unit": "bootstrap/s",
+        "ms_per_bootstrap": round(wall * 1000.0 / len(cts), 3),
+        "gpu_event_ms_per_bootstrap": round(ev0.elapsed_time(ev1) / len(cts), 3),
+        "ciphertexts": len(cts),
+        "group": group,
+        "budget": list(budget),
+        "linear_levels": prog.evalmod.strategy,
+        "raise_limbs": prog.raise_limbs,
+        "output_limbs": prog.output_limbs,
+        "evalmod": {"K": prog.evalmod.K, "double_angles": prog.evalmod.double_angles,
+                    "degree": len(prog.coefficients) - 1, "depth": prog.cheb_depth,
+                    "primes_per_level": prog.step},
+        "precision_bits_min": round(min(bits), 2),
+        "precision_bits_mean": round(float(np.mean(bits)), 2),
+        "setup_s": round(setup_s, 2),
+        "first_group_s": round(first_s, 3),
+    }
+
+
+def bootstrap_bench(spec, args) -> int:
+    """The bootstrap workload alone, as its own JSON line."""
+    from easyfhe import fhe
+
+    spec.rotations = ()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    b = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group, args.budget, args.warmup)
+    result = {
+        "metric": "bootstrap/s @N=2^16",
+        "value": b["value"],
+        "unit": "bootstrap/s",
         "n_gpus": 1,
-        "steps": len(cts),
+        "steps": b["ciphertexts"],
         "warmup": max(1, args.warmup),
-        "ms_per_step": round(wall * 1000.0 / len(cts), 3),
+        "ms_per_step": b["ms_per_bootstrap"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -275,20 +312,10 @@ def bootstrap_bench(spec, args) -> int:
         "data": "synthetic",
         "config": {
             "workload": f"full-slot bootstrap, N=2^16, Q=1x60b+35x40b, dnum=3, P=12x44b; "
-                        f"{len(cts)} ciphertexts at one limb; CtS/StC budget {budget}",
-            "group": group,
-            "linear_levels": prog.evalmod.strategy,
-            "raise_limbs": prog.raise_limbs,
-            "output_limbs": prog.output_limbs,
-            "evalmod": {"K": prog.evalmod.K, "double_angles": prog.evalmod.double_angles,
-                        "degree": len(prog.coefficients) - 1, "depth": prog.cheb_depth,
-                        "primes_per_level": prog.step},
+                        f"{b['ciphertexts']} ciphertexts at one limb; CtS/StC budget "
+                        f"{tuple(b['budget'])}",
         },
-        "gpu_event_ms_per_step": round(ev0.elapsed_time(ev1) / len(cts), 3),
-        "precision_bits_min": round(min(bits), 2),
-        "precision_bits_mean": round(float(np.mean(bits)), 2),
-        "setup_s": round(setup_s, 2),
-        "first_group_s": round(first_s, 3),
+        "bootstrap": b,
     }
     print(json.dumps(result), flush=True)
     return 0
