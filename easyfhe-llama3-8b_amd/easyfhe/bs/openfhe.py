@@ -90,20 +90,26 @@ class Requirements:
 def _check_spec(spec: BootstrapSpec, log_n: int) -> None:
     if spec.mode != "modraise_first":
         raise ValueError(f"unsupported bootstrap mode {spec.mode!r}")
-    if int(spec.log_slots) != log_n - 1:
-        raise NotImplementedError(
-            f"only full-slot programs (log_slots = {log_n - 1}) are built; "
-            f"got log_slots = {spec.log_slots}")
+    if not 1 <= int(spec.log_slots) <= log_n - 1:
+        raise ValueError(f"log_slots must be in [1, {log_n - 1}], got {spec.log_slots}")
     budget = tuple(int(v) for v in spec.level_budget)
-    if len(budget) != 2 or min(budget) < 1 or max(budget) > int(spec.log_slots):
-        raise ValueError(f"level_budget must be two values in [1, log_slots], got {budget}")
+    if len(budget) != 2 or min(budget) < 1 or max(budget) > log_n - 1:
+        raise ValueError(f"level_budget must be two values in [1, {log_n - 1}], got {budget}")
 
 
-def _plans(spec: BootstrapSpec, params: "BootstrapParams | None" = None):
+def _transform_log_slots(spec: BootstrapSpec, log_n: int) -> int:
+    """The linear transforms always act on all N/2 slots: a sparse
+    ciphertext's plaintext is a full-slot plaintext whose slots repeat its
+    2^log_slots values, so the full-slot program refreshes it unchanged."""
+    return log_n - 1
+
+
+def _plans(spec: BootstrapSpec, params: "BootstrapParams | None" = None, log_n: int = 0):
     b0, b1 = (int(v) for v in spec.level_budget)
     giants = params.giants if params is not None and params.strategy != "normal" else 0
-    return (plan_levels(int(spec.log_slots), b0, inverse=True, giants=giants),
-            plan_levels(int(spec.log_slots), b1, inverse=False, giants=giants))
+    ls = _transform_log_slots(spec, log_n) if log_n else int(spec.log_slots)
+    return (plan_levels(ls, b0, inverse=True, giants=giants),
+            plan_levels(ls, b1, inverse=False, giants=giants))
 
 
 def _baby_offsets(plan: LevelPlan, n: int) -> list[int]:
@@ -130,8 +136,8 @@ def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> 
     rots: set[int] = set()
     for spec in specs:
         _check_spec(spec, int(log_n))
-        n = spec.slots
-        cts, stc = _plans(spec, p)
+        n = 1 << _transform_log_slots(spec, int(log_n))
+        cts, stc = _plans(spec, p, int(log_n))
         for plan in (*cts, *stc):
             rots |= _level_rotations(plan, n)
         rots.add(2 * (1 << int(log_n)) - 1)
@@ -222,14 +228,14 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     _check_spec(spec, ctx.logN)
     p = evalmod or BootstrapParams()
     primes = [int(q) for q in ctx.primes()[: ctx.L]]
-    n = spec.slots
+    n = 1 << _transform_log_slots(spec, ctx.logN)
     bits = math.log2(primes[1]) if len(primes) > 1 else math.log2(primes[0])
     step = max(1, math.ceil(_EVALMOD_BITS / bits))
     coeffs = _evalmod_coefficients(p)
     depth = cheb.chebyshev_depth(coeffs)
     if p.strategy not in ("normal", "ext_normal"):
         raise ValueError(f"unknown linear-level strategy {p.strategy!r}")
-    cts_plans, stc_plans = _plans(spec, p)
+    cts_plans, stc_plans = _plans(spec, p, ctx.logN)
     n_cts, n_stc = len(cts_plans), len(stc_plans)
     ladder_levels = depth + p.double_angles
     q0 = float(primes[0])
@@ -325,7 +331,7 @@ def _prescale(ct, prog: BootstrapProgram, ctx):
 
 
 def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
-    n = prog.spec.slots
+    n = ctx.N // 2
     plan = lv.plan
     ext = prog.evalmod.strategy != "normal"
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
@@ -378,7 +384,7 @@ def bootstrap(ct, context, program: BootstrapProgram):
 
 
 def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> list:
-    n = prog.spec.slots
+    n = ctx.N // 2
     plan = lv.plan
     if prog.evalmod.strategy == "normal":
         return [_linear_level(x, lv, prog, ctx) for x in xs]

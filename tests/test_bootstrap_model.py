@@ -207,5 +207,8 @@ def test_requirements_and_limb_plan():
     assert all(0 < r < 2 * 65536 for r in req.rotations)
     # extended-basis levels (at most 2 giants): up to 32 babies per level
     assert len(req.rotations) <= 96
-    with pytest.raises(NotImplementedError):
-        bs.requirements([bs.BootstrapSpec(log_slots=7)], log_n=16)
+    # a sparse program runs the full-slot transforms (its slots repeat)
+    sparse = bs.requirements([bs.BootstrapSpec(log_slots=7, level_budget=(3, 3))], log_n=16)
+    assert sparse.rotations == req.rotations
+    with pytest.raises(ValueError):
+        bs.requirements([bs.BootstrapSpec(log_slots=16)], log_n=16)

@@ -149,3 +149,21 @@ def test_bootstrap_pair_refreshes_two_real_streams(boot_ctx):
     for got, want in ((ra, a), (rb, b)):
         err = np.abs(client.decrypt_complex(got) - want).max()
         assert -math.log2(err) > 14, err
+
+
+def test_bootstrap_sparse_slots(boot_ctx):
+    """A 128-slot ciphertext (the reference's slim RMSNorm program shape) is
+    refreshed by the full-slot transform: its plaintext repeats the 128 values."""
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    slots = 128
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=7, level_budget=(3, 3), output_levels=3))
+    assert prog.spec.slots == slots
+    rng = np.random.default_rng(11)
+    z = rng.uniform(-1, 1, slots)
+    ct = client.encrypt(z, slots=slots, cur_limbs=1, enc_id=95)
+    out = bs.bootstrap(ct, ctx, prog)
+    assert out.slots == slots and out.state.cur_limbs == 4
+    err = np.abs(client.decrypt_complex(out) - z).max()
+    assert -math.log2(err) > 14, err
