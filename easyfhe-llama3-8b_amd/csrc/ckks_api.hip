@@ -402,6 +402,49 @@ static const u64 *rescale_table(ckks_context *c, int limbs) {
   return c->rescale_c[limbs] = d;
 }
 
+// Relinearise-rescale constants for a ciphertext of `limbs` limbs (q_l is
+// its last prime, l1 = limbs - 1): [l1][2] (P q_l)^-1 mod q_i + shoup,
+// [l1][2] q_l^-1 mod q_i + shoup, then the conversion's [l1] [P]_t
+// (Montgomery), [l1] [q_l P]_t, P^-1 mod q_l + shoup.
+static const u64 *relin_rs_table(ckks_context *c, int limbs) {
+  auto it = c->relin_rs.find(limbs);
+  if (it != c->relin_rs.end()) return it->second;
+  const int l1 = limbs - 1;
+  const u64 ql = c->primes[l1];
+  std::vector<u64> h(6 * (size_t)l1 + 2);
+  auto pmod = [&](u64 q) {
+    u64 P = 1;
+    for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
+    return P;
+  };
+  for (int i = 0; i < l1; i++) {
+    const u64 q = c->primes[i], P = pmod(q);
+    const u64 inv2 = invmod_h(mulmod_h(P, ql % q, q), q), invq = invmod_h(ql % q, q);
+    h[2 * i] = inv2;
+    h[2 * i + 1] = shoup_h(inv2, q);
+    h[2 * (size_t)l1 + 2 * i] = invq;
+    h[2 * (size_t)l1 + 2 * i + 1] = shoup_h(invq, q);
+    h[4 * (size_t)l1 + i] = (u64)(((u128)P << 64) % q);
+    h[5 * (size_t)l1 + i] = mulmod_h(P, ql % q, q);
+  }
+  const u64 pinv = invmod_h(pmod(ql), ql);
+  h[6 * (size_t)l1] = pinv;
+  h[6 * (size_t)l1 + 1] = shoup_h(pinv, ql);
+  u64 *d = nullptr;
+  HIPCHECK(hipMalloc(&d, sizeof(u64) * h.size()));
+  HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
+  return c->relin_rs[limbs] = d;
+}
+
+// The one-ModDown relinearise-rescale needs the Montgomery sums of its
+// conversion (alpha sources and the lift) below q_t 2^64.
+static bool relin_rs_fits(const ckks_context *c, int limbs) {
+  if (limbs < 2 || limbs > 48 || c->alpha > kMaxDigitSize) return false;
+  u128 s = c->primes[limbs - 1];
+  for (int j = 0; j < c->alpha; j++) s += c->primes[c->L + j];
+  return s < ((u128)1 << 64);
+}
+
 /* cos and sin of 2 pi j / n (n a power of two) from IEEE basic operations
  * only, so the result does not depend on the compiler or the libm in use
  * (glibc's sin and sincos differ in the last bit for some arguments):
@@ -628,6 +671,7 @@ static void free_context(ckks_context *c) {
   }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
   for (auto &kv : c->rescale_c) (void)hipFree(kv.second);
+  for (auto &kv : c->relin_rs) (void)hipFree(kv.second);
   for (auto &kv : c->garner) (void)hipFree(kv.second);
   for (auto &kv : c->fft) {
     (void)hipFree(kv.second.tw_fwd);
@@ -890,6 +934,61 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
       jobs[i] = KsJob{i, &key, 1, in[b0 + i]->d, in[b0 + i]->d + P, out[b0 + i]->d,
                       out[b0 + i]->d + P};
     ks_finish(c, limbs, ext, nb, jobs, s);
+  }
+}
+
+// Relinearisation of n degree-2 ciphertexts followed by the rescale, as one
+// ModDown by P q_l (see k_bc_down_rescale): the same words as relin_batch
+// then rescale_batch, without the relinearised ciphertext's forward NTT, its
+// last-limb inverse NTT and the rescale's lift NTT and combine.
+static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n,
+                                ckks_ct **out) {
+  const int limbs = in[0]->limbs, l1 = limbs - 1, A = c->alpha;
+  const size_t N = c->N, P = (size_t)limbs * N;
+  const DeviceKey &key = get_key(c, 0);
+  const BCTable &bt = bc_down(c, limbs);
+  const u64 *rt = relin_rs_table(c, limbs);
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Scratch s(c);
+    std::vector<const u64 *> d(nb);
+    for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
+    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + A;
+    u64 *ext = s.get((size_t)nb * digits * E * N);
+    ks_modup(c, limbs, nb, d.data(), ext, s);
+    std::vector<KsJob> jobs(nb);
+    for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
+    u64 *acc = ks_inner(c, limbs, ext, jobs, s);
+    // per item: [A] P limbs of X, then its q_l limb, as coefficients
+    const size_t xs = (size_t)(A + 1) * N;
+    u64 *x = s.get((size_t)nb * 2 * xs);
+    launch_ntt(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A, limbs, true);
+    Batch d3{}, a0{}, a1{}, o0{}, o1{};
+    for (int i = 0; i < nb; i++) {
+      d3.p[i] = in[b0 + i]->d;
+      a0.p[i] = in[b0 + i]->d;
+      a1.p[i] = in[b0 + i]->d + P;
+      o0.p[i] = out[b0 + i]->d;
+      o1.p[i] = out[b0 + i]->d + (size_t)l1 * N;
+    }
+    launch_rs_prep(c, Strided{acc, (size_t)E * N}, E, limbs, d3, nb,
+                   Strided{x + (size_t)A * N, xs});
+    launch_ntt(c, strided(x + (size_t)A * N - (size_t)l1 * N, xs),
+               strided(x + (size_t)A * N - (size_t)l1 * N, xs), 2 * nb, l1, 1, limbs, true);
+    u64 *conv = s.get((size_t)nb * 2 * l1 * N);
+    launch_bc_down_rescale(c, strided(x, xs), strided(conv, (size_t)l1 * N), 2 * nb, bt,
+                           rt + 4 * (size_t)l1);
+    std::vector<u64> gal(nb, 1);
+    const u64 *amul = rt + 2 * (size_t)l1;
+    if (c->logN == 16) {
+      launch_ntt_moddown(c, strided(conv, (size_t)l1 * N), nb, l1, Strided{acc, 2 * E * N}, E, rt,
+                         a0, a1, gal.data(), o0, o1, amul);
+    } else {
+      launch_ntt(c, strided(conv, (size_t)l1 * N), strided(conv, (size_t)l1 * N), 2 * nb, 0, l1,
+                 l1, false);
+      launch_moddown_combine(c, Strided{acc, 2 * E * N}, Strided{conv, 2 * l1 * N}, a0, a1,
+                             gal.data(), o0, o1, nb, l1, E, rt, amul);
+    }
   }
 }
 
@@ -1487,13 +1586,17 @@ int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
       p3[i] = &v3[i];
       p2[i] = &v2[i];
     }
-    relin_batch(c, p3.data(), nb, p2.data());
     const double div = (double)c->primes[limbs - 1];
     std::vector<ckks_ct *> o(nb);
     for (int i = 0; i < nb; i++)
       o[i] = out[b0 + i] = new_ct(c, 2, limbs - 1, 0, a[b0 + i]->slots,
                                   a[b0 + i]->scale * b[b0 + i]->scale / div,
                                   std::max(1, a[b0 + i]->scale_degree + b[b0 + i]->scale_degree - 1));
+    if (relin_rs_fits(c, limbs)) {
+      relin_rescale_batch(c, p3.data(), nb, o.data());
+      continue;
+    }
+    relin_batch(c, p3.data(), nb, p2.data());
     std::vector<const ckks_ct *> cp2(p2.begin(), p2.end());
     rescale_batch(c, cp2.data(), nb, o.data());
   }

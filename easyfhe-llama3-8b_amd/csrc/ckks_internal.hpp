@@ -188,6 +188,7 @@ struct ckks_context {
   std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
   u64 *d_pmod = nullptr;         // [L][2] P mod q_i, shoup (extended-basis lifts)
   std::map<int, u64 *> rescale_c;  // limbs -> [limbs-1][4] ql mod qi, ql^-1, shoup
+  std::map<int, u64 *> relin_rs;   // limbs -> relinearise-rescale constants
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
 };
@@ -239,14 +240,19 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
-                            int E, const u64 *pinv);
+                            int E, const u64 *pinv, const u64 *amul = nullptr);
 void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, int n_items,
                            int limbs);
 void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
                             const Batch &out, int n_items, int limbs, const u64 *consts);
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
                         int E, const u64 *pinv, const Batch &add0, const Batch &add1,
-                        const u64 *galois, const Batch &out0, const Batch &out1);
+                        const u64 *galois, const Batch &out0, const Batch &out1,
+                        const u64 *amul = nullptr);
+void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                            const BCTable &t, const u64 *rtab);
+void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, const Batch &d, int n,
+                    const Strided &x);
 // Feature-major BSGS diagonal geometry (token-lane packing)
 struct DiagGeom {
   int D, lanes, baby, giant_base;

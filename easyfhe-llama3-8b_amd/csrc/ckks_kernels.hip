@@ -259,6 +259,7 @@ struct MDCombine {
   Strided acc;  // item layout [2][E][N]
   int E;
   const u64 *pinv;  // per Q limb: P^-1, shoup
+  const u64 *amul;  // per Q limb: multiplier of the addend, shoup (null: 1)
   Batch add0, add1, out0, out1;
   Galois64 gal;
 };
@@ -291,6 +292,7 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
   const int item = item2 >> 1, comp = item2 & 1;
   const size_t N = 65536;
   u64 r = shoup_mul(sub_mod(a, y, q), md.pinv[2 * limb], md.pinv[2 * limb + 1], q);
+  if (md.amul) d = shoup_mul(d, md.amul[2 * limb], md.amul[2 * limb + 1], q);
   r = add_mod(r, d, q);
   u64 *o = comp ? batch_ptr(md.out1, item) : batch_ptr(md.out0, item);
   o[(size_t)limb * N + e] = r;
@@ -881,12 +883,14 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
 // is never written back.  N = 2^16 only.
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
                         int E, const u64 *pinv, const Batch &add0, const Batch &add1,
-                        const u64 *galois, const Batch &out0, const Batch &out1) {
+                        const u64 *galois, const Batch &out0, const Batch &out1,
+                        const u64 *amul) {
   if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
   MDCombine md{};
   md.acc = acc;
   md.E = E;
   md.pinv = pinv;
+  md.amul = amul;
   md.add0 = add0;
   md.add1 = add1;
   md.out0 = out0;
@@ -1234,6 +1238,128 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
   LAUNCH_CHECK();
 }
 
+// ModDown conversion of a relinearisation fused with the rescale that
+// follows it (division by P q_last in one ModDown, bit-identical to the two
+// steps).  Per item (the 2 polynomials of each ciphertext) the source holds
+// the ns = alpha P limbs of X = acc + P d and, at slot ns, its q_last limb,
+// all as coefficients.  y = conv(X_P) in q_last gives the last coefficient of
+// the relinearised ciphertext, rv = [(X_q - y) P^-1]_{q_last}; its centered
+// lift r is what the rescale subtracts.  Written for t < nd - 1:
+//   out_t = conv(X_P)_t + [P]_t r   (mod q_t)
+// so that (acc - NTT(out)) (P q_last)^-1 + d q_last^-1 is the rescaled limb.
+// tab: the ModDown conversion table to the nd = limbs Q primes; rtab:
+// [nd-1] [P]_t (Montgomery), [nd-1] [q_last P]_t, P^-1 mod q_last, shoup.
+// The Montgomery sums stay below q_t 2^64 when sum(p_j) + q_last < 2^64.
+__global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, int logN, int ns,
+                                                         int nd, const u64 *__restrict__ tab,
+                                                         const u64 *__restrict__ rtab, int L,
+                                                         const ModQ *__restrict__ mods) {
+  __shared__ u64 st[2 * kMaxDigitSize + kMaxDigitSize * 48 + 48];
+  __shared__ u64 sr[2 * 48 + 2];
+  const int words = 2 * ns + ns * nd + nd, rwords = 2 * (nd - 1) + 2;
+  for (int i = threadIdx.x; i < words; i += TPB) st[i] = tab[i];
+  for (int i = threadIdx.x; i < rwords; i += TPB) sr[i] = rtab[i];
+  __syncthreads();
+  const u64 *in = batch_ptr(src, blockIdx.y);
+  u64 *out = batch_ptr(dst, blockIdx.y);
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  u64 v[kMaxDigitSize];
+  u64 cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxDigitSize; i++) {
+    if (i < ns) {
+      const u64 qi = mods[L + i].q;
+      v[i] = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
+      cnt += v[i] > (qi - 1) / 2 ? 1 : 0;
+    }
+  }
+  const u64 *hm = st + 2 * ns;
+  const u64 *qm = hm + (size_t)ns * nd;
+  const int n1 = nd - 1;
+  const ModQ Mq = mods[n1];
+  u64 hi = 0, lo = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxDigitSize; i++)
+    if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + n1]);
+  u64 y = redc(hi, lo, Mq.q, Mq.qinv);
+  if (cnt) y = sub_mod(y, mul_mod(cnt, qm[n1], Mq), Mq.q);
+  const u64 xq = in[((size_t)ns << logN) + k];
+  const u64 rv = shoup_mul(sub_mod(xq, y, Mq.q), sr[2 * n1], sr[2 * n1 + 1], Mq.q);
+  const bool neg = rv > (Mq.q - 1) / 2;
+  int t = 0;
+  for (; t + 1 < n1; t += 2) {
+    const ModQ M0 = mods[t], M1 = mods[t + 1];
+    u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i++) {
+      if (i < ns) {
+        mac_wide(h0, l0, v[i], hm[i * nd + t]);
+        mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
+      }
+    }
+    mac_wide(h0, l0, rv, sr[t]);
+    mac_wide(h1, l1, rv, sr[t + 1]);
+    u64 y0 = redc(h0, l0, M0.q, M0.qinv);
+    u64 y1 = redc(h1, l1, M1.q, M1.qinv);
+    if (cnt) {
+      y0 = sub_mod(y0, mul_mod(cnt, qm[t], M0), M0.q);
+      y1 = sub_mod(y1, mul_mod(cnt, qm[t + 1], M1), M1.q);
+    }
+    if (neg) {
+      y0 = sub_mod(y0, sr[n1 + t], M0.q);
+      y1 = sub_mod(y1, sr[n1 + t + 1], M1.q);
+    }
+    out[((size_t)t << logN) + k] = y0;
+    out[((size_t)(t + 1) << logN) + k] = y1;
+  }
+  if (t < n1) {
+    const ModQ M = mods[t];
+    u64 h0 = 0, l0 = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxDigitSize; i++)
+      if (i < ns) mac_wide(h0, l0, v[i], hm[i * nd + t]);
+    mac_wide(h0, l0, rv, sr[t]);
+    u64 y0 = redc(h0, l0, M.q, M.qinv);
+    if (cnt) y0 = sub_mod(y0, mul_mod(cnt, qm[t], M), M.q);
+    if (neg) y0 = sub_mod(y0, sr[n1 + t], M.q);
+    out[((size_t)t << logN) + k] = y0;
+  }
+}
+
+void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                            const BCTable &t, const u64 *rtab) {
+  if (t.nd < 2 || t.nd > 48 || t.ns > kMaxDigitSize)
+    throw std::invalid_argument("relinearise-rescale conversion: 2 <= limbs <= 48");
+  dim3 grid(c->N / TPB, n_items);
+  hipLaunchKernelGGL(k_bc_down_rescale, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
+                     t.nd, t.d, rtab, c->L, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// X_q = acc_q + [P]_q d_q for the q_last limb (limb l1) of every item:
+// acc items [2 n][E][N], d: ciphertext c of item i is batch_ptr(d, i) with
+// polynomials [3][limbs][N]; written to x (strided per item2).
+// grid (N / 256, 2 n)
+__global__ void k_rs_prep(Strided acc, int E, int limbs, Batch d, Strided x, int logN,
+                          const u64 *__restrict__ pm, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int item = blockIdx.y >> 1, comp = blockIdx.y & 1;
+  const size_t N = (size_t)1 << logN;
+  const int l1 = limbs - 1;
+  const u64 q = mods[l1].q;
+  const u64 a = acc.base[blockIdx.y * acc.stride + (size_t)l1 * N + k];
+  const u64 dv = batch_ptr(d, item)[((size_t)comp * limbs + l1) * N + k];
+  x.base[blockIdx.y * x.stride + k] = add_mod(a, shoup_mul(dv, pm[0], pm[1], q), q);
+}
+
+void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, const Batch &d, int n,
+                    const Strided &x) {
+  dim3 grid(c->N / TPB, 2 * n);
+  hipLaunchKernelGGL(k_rs_prep, grid, dim3(TPB), 0, c->stream, acc, E, limbs, d, x, c->logN,
+                     c->d_pmod + 2 * (limbs - 1), c->d_mods);
+  LAUNCH_CHECK();
+}
+
 // dst[item][l] = src[item][l] for l < limb_count; grid (N / 256, limbs, items)
 __global__ void k_copy_limbs(Batch src, Batch dst, int logN) {
   const int k = blockIdx.x * TPB + threadIdx.x;
@@ -1398,7 +1524,7 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
 __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch add1,
                                   Galois64 gal, Batch out0, Batch out1, int logN, int limbs,
                                   int E, const u64 *__restrict__ pinv,
-                                  const ModQ *__restrict__ mods) {
+                                  const u64 *__restrict__ amul, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = blockIdx.y;
   const int item = blockIdx.z >> 1, comp = blockIdx.z & 1;
@@ -1413,7 +1539,9 @@ __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch a
   if (ad) {
     const u64 g = gal.g[item];
     const u32 kk = g == 1 ? (u32)k : autom_index((u32)k, g, logN);
-    r = add_mod(r, ad[(size_t)l * N + kk], q);
+    u64 d = ad[(size_t)l * N + kk];
+    if (amul) d = shoup_mul(d, amul[2 * l], amul[2 * l + 1], q);
+    r = add_mod(r, d, q);
   }
   u64 *o = comp ? batch_ptr(out1, item) : batch_ptr(out0, item);
   o[(size_t)l * N + k] = r;
@@ -1422,13 +1550,13 @@ __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch a
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
-                            int E, const u64 *pinv) {
+                            int E, const u64 *pinv, const u64 *amul) {
   if (n_items > kMaxBatch) throw std::invalid_argument("moddown combine: too many items");
   Galois64 g{};
   for (int i = 0; i < n_items; i++) g.g[i] = galois[i];
   dim3 grid(c->N / TPB, limbs, 2 * n_items);
   hipLaunchKernelGGL(k_moddown_combine, grid, dim3(TPB), 0, c->stream, acc, conv, add0, add1,
-                     g, out0, out1, c->logN, limbs, E, pinv, c->d_mods);
+                     g, out0, out1, c->logN, limbs, E, pinv, amul, c->d_mods);
   LAUNCH_CHECK();
 }
 

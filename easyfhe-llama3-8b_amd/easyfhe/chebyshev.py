@@ -212,9 +212,12 @@ class LadderOps:
             raise ValueError("ladder depth exhausted")
         a, b = self.lower(a, lev), self.lower(b, lev)
         self.mults += 1
-        prod = fhe.homo_mul_relin(a.ct, b.ct, self.ctx) if a is not b else \
-            fhe.homo_mul_relin(a.ct, a.ct, self.ctx)
-        return self._settle(self._rescale_steps(prod), lev + 1)
+        # relinearise and the first rescale as one ModDown (same words as
+        # homo_mul_relin then rescale)
+        prod = fhe.homo_mul_relin_rescale_many([a.ct], [b.ct], self.ctx)[0]
+        for _ in range(self.lad.step - 1):
+            prod = fhe.rescale(prod, self.ctx)
+        return self._settle(prod, lev + 1)
 
 
 class BatchLadderOps(LadderOps):

@@ -233,6 +233,16 @@ def test_mul_relin_rescale_parity(name):
         assert np.array_equal(m.download(), rrs)
     # rescale of a degree-2 ciphertext (tensor) as well
     assert np.array_equal(fhe.rescale(t, ctx).download(), orc.rescale(rt))
+    # one level down (an even number of limbs left after the rescale)
+    lim = ctx.L - 1
+    a2 = client.encrypt(x, slots=slots, cur_limbs=lim, enc_id=23)
+    b2 = client.encrypt(y, slots=slots, cur_limbs=lim, enc_id=24)
+    ra2 = orc.encrypt(x, slots=slots, scale=ctx.scale_at(lim), limbs=lim, enc_id=23)
+    rb2 = orc.encrypt(y, slots=slots, scale=ctx.scale_at(lim), limbs=lim, enc_id=24)
+    assert np.array_equal(a2.download(), ra2)
+    exp2 = orc.rescale(orc.relinearize(orc.tensor(ra2, rb2)))
+    for m in fhe.homo_mul_relin_rescale_many([a2, a2, a2], [b2, b2, b2], ctx):
+        assert np.array_equal(m.download(), exp2)
 
 
 @pytest.mark.parametrize("name", ["small", "keyswitch"])
