@@ -95,7 +95,16 @@ void Pool::release_all() {
 // Contexts that are alive; a ciphertext released after its context was
 // destroyed only drops its host record (the device memory went with the
 // context).
-static std::unordered_map<ckks_context *, int> g_live_contexts;
+// live contexts and their serials: objects freed after their context was
+// destroyed only drop their host record (a later context may reuse the
+// address, the serial tells them apart)
+static std::unordered_map<ckks_context *, u64> g_live_contexts;
+static u64 g_next_serial = 1;
+
+static bool owner_alive(const ckks_context *c, u64 serial) {
+  auto it = g_live_contexts.find(const_cast<ckks_context *>(c));
+  return it != g_live_contexts.end() && it->second == serial;
+}
 
 void Pool::trim() {
   (void)hipDeviceSynchronize();
@@ -659,6 +668,7 @@ static void build_context(ckks_context *c, const ckks_params &p) {
 
 static void free_context(ckks_context *c) {
   if (!c) return;
+  g_live_contexts.erase(c);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (auto &kv : c->keys) (void)hipFree(kv.second.data);
   for (auto &kv : c->bc_up) {
@@ -701,6 +711,7 @@ static ckks_ct *new_ct(ckks_context *c, int polys, int limbs, int is_ext, int sl
                        double scale, int scale_degree) {
   ckks_ct *ct = new ckks_ct();
   ct->ctx = c;
+  ct->serial = c->serial;
   ct->polys = polys;
   ct->limbs = limbs;
   ct->is_ext = is_ext;
@@ -716,7 +727,7 @@ static ckks_ct *new_ct(ckks_context *c, int polys, int limbs, int is_ext, int sl
 
 static void free_ct(ckks_ct *ct) {
   if (!ct) return;
-  if (g_live_contexts.count(ct->ctx)) ct->ctx->pool.release(ct->d, ct->bytes);
+  if (ct->serial && owner_alive(ct->ctx, ct->serial)) ct->ctx->pool.release(ct->d, ct->bytes);
   delete ct;
 }
 
@@ -1035,7 +1046,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     free_context(c);
     throw;
   }
-  g_live_contexts[c] = 1;
+  c->serial = g_next_serial++;
+  g_live_contexts[c] = c->serial;
   *out = c;
   API_END
 }
@@ -1938,7 +1950,7 @@ int ckks_tensor_upload(ckks_context *c, const void *data, size_t bytes, ckks_ten
   API_BEGIN
   require(c && data && out, "null argument");
   require(bytes > 0, "empty tensor");
-  ckks_tensor *t = new ckks_tensor{c, nullptr, bytes};
+  ckks_tensor *t = new ckks_tensor{c, nullptr, bytes, c->serial};
   if (hipMalloc(&t->d, bytes) != hipSuccess) {
     delete t;
     throw std::runtime_error("device allocation failed");
@@ -1961,7 +1973,7 @@ int ckks_tensor_download(ckks_context *c, const ckks_tensor *t, void *out, size_
 
 void ckks_tensor_free(ckks_tensor *t) {
   if (!t) return;
-  if (g_live_contexts.count(t->ctx)) {
+  if (owner_alive(t->ctx, t->serial)) {
     (void)hipStreamSynchronize(t->ctx->stream);
     (void)hipFree(t->d);
   }

@@ -167,6 +167,7 @@ struct FFTTable {  // encoder tables for one slot count n
 }  // namespace ckks
 
 struct ckks_context {
+  u64 serial = 0;  // unique per created context (never reused)
   ckks_params params;
   int N, logN, L, alpha, ds, K;
   hipStream_t stream;
@@ -199,6 +200,7 @@ struct ckks_ct {
   size_t bytes;
   int polys, limbs, is_ext, slots, scale_degree;
   double scale;
+  u64 serial;  // the owning context's serial (0: a view that owns no memory)
 };
 
 struct ckks_event {
@@ -210,6 +212,7 @@ struct ckks_tensor {  // raw device bytes (weights for the diagonal packers)
   ckks_context *ctx;
   void *d;
   size_t bytes;
+  u64 serial;  // the owning context's serial
 };
 
 // ---------------------------------------------------------------------------

@@ -460,3 +460,20 @@ def test_linear_combination_matches_composed_ops():
         acc = fhe.homo_add_scalar(acc, fhe.encode_scalar(const, limbs, scaling_factor=1.0,
                                                          context=ctx), ctx)
         assert np.array_equal(fused[i].download(), acc.download()), i
+
+
+def test_objects_outliving_their_context():
+    """Ciphertexts and tensors freed after their context was destroyed only
+    drop their host record, also when a new context takes the old address."""
+    _fhe()
+    from easyfhe.tensor import DeviceTensor
+
+    client, ctx = device_context("small", relin=False)
+    ct = client.encrypt(np.ones(ctx.max_slots), enc_id=1)
+    t = DeviceTensor(np.ones(16, dtype=np.float32), context=ctx)
+    ctx.close()
+    client2, ctx2 = device_context("small", relin=False)
+    ct.release()
+    t.release()
+    ct2 = client2.encrypt(np.full(ctx2.max_slots, 0.5), enc_id=2)
+    assert np.abs(client2.decrypt(ct2) - 0.5).max() < 1e-6
