@@ -294,9 +294,8 @@ static void parallel_for(int n, F f) {
 
 static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::vector<u64> &dst) {
   const int ns = (int)src.size(), nd = (int)dst.size();
-  // the kernel stages the table in a fixed LDS array
-  require(ns <= kMaxDigitSize && 2 * ns + ns * nd + nd <= 2 * kMaxDigitSize + kMaxDigitSize * 48 + 48,
-          "basis conversion table exceeds the kernel's staging area (16 sources x 48 targets)");
+  // the conversion kernels hold one value per source in registers
+  require(ns <= kMaxDigitSize, "basis conversion from more than 16 primes");
   std::vector<u64> h(2 * ns + (size_t)ns * nd + nd);
   for (int t = 0; t < nd; t++) {
     u64 m = 1;
@@ -322,8 +321,8 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
   BCTable t{ns, nd, nullptr, sizeof(u64) * h.size(), nullptr, 0};
   HIPCHECK(hipMalloc(&t.d, t.bytes));
   HIPCHECK(hipMemcpy(t.d, h.data(), t.bytes, hipMemcpyHostToDevice));
-  // the fp64 kernel stages (ns + ns*nd) double pairs in a fixed LDS array
-  bool fp = ns + ns * nd <= kMaxDigitSize + kMaxDigitSize * 48;
+  // the fp64 kernel needs every source prime below 2^45
+  bool fp = true;
   for (u64 q : src) fp = fp && q < (1ull << 45);
   if (fp) {
     // (w, w / q) pairs for the fp64 modular product; hmod in plain form
@@ -448,7 +447,7 @@ static const u64 *relin_rs_table(ckks_context *c, int limbs) {
 // The one-ModDown relinearise-rescale needs the Montgomery sums of its
 // conversion (alpha sources and the lift) below q_t 2^64.
 static bool relin_rs_fits(const ckks_context *c, int limbs) {
-  if (limbs < 2 || limbs > 48 || c->alpha > kMaxDigitSize) return false;
+  if (limbs < 2 || c->alpha > kMaxDigitSize) return false;
   u128 s = c->primes[limbs - 1];
   for (int j = 0; j < c->alpha; j++) s += c->primes[c->L + j];
   return s < ((u128)1 << 64);
