@@ -773,8 +773,10 @@ static Batch strided(u64 *base, size_t stride) {
 
 // ModUp of n polynomials d[i] (NTT domain, `limbs` limbs) into
 // ext = [n][digits][E][N].
+// own_copy false: the digits' own limbs are not copied into ext; the key
+// inner product then reads them from d (ks_inner's `own`).
 static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
-                     Scratch &s) {
+                     Scratch &s, bool own_copy = true) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   u64 *coeff = s.get((size_t)n * limbs * N);
@@ -787,7 +789,7 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
     for (int i = 0; i < n; i++) dsrc.p[i] = (u64 *)d[i] + (size_t)lo * N;
     u64 *ej = ext + (size_t)j * E * N;
     const size_t est = (size_t)digits * E * N;
-    launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
+    if (own_copy) launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
     launch_basis_convert(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N), strided(ej, est), n,
                          bc_up(c, limbs, j), lo, lo, ns, limbs, false);
     launch_ntt(c, strided(ej, est), strided(ej, est), n, 0, lo, limbs, false);
@@ -853,9 +855,10 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
   }
 }
 
-// Key inner product of every job into [n][2][E][N] accumulators.
+// Key inner product of every job into [n][2][E][N] accumulators.  With own
+// given, ext item i lacks its digits' own limbs, which are read from own[i].
 static u64 *ks_inner(ckks_context *c, int limbs, const u64 *ext, const std::vector<KsJob> &jobs,
-                     Scratch &s) {
+                     Scratch &s, const u64 *const *own = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   const int n = (int)jobs.size();
@@ -866,22 +869,29 @@ static u64 *ks_inner(ckks_context *c, int limbs, const u64 *ext, const std::vect
     shared = shared && jobs[i].ext_item == i && jobs[i].key == jobs[0].key &&
              jobs[i].galois == jobs[0].galois;
   if (shared) {
+    Batch ob{};
+    if (own)
+      for (int i = 0; i < n; i++) ob.p[i] = (u64 *)own[i];
     launch_key_inner(c, strided((u64 *)ext, est), strided(acc, 2 * E * N), n, *jobs[0].key,
-                     digits, E, limbs, jobs[0].galois);
+                     digits, E, limbs, jobs[0].galois, own ? &ob : nullptr);
   } else {
-    for (int i = 0; i < n; i++)
+    for (int i = 0; i < n; i++) {
+      Batch ob{};
+      if (own) ob.p[0] = (u64 *)own[jobs[i].ext_item];
       launch_key_inner(c, strided((u64 *)ext + (size_t)jobs[i].ext_item * est, 0),
                        strided(acc + (size_t)i * 2 * E * N, 0), 1, *jobs[i].key, digits, E,
-                       limbs, jobs[i].galois);
+                       limbs, jobs[i].galois, own ? &ob : nullptr);
+    }
   }
   return acc;
 }
 
 // Key inner product for every job, ModDown, and the combine with addends.
 static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
-                      const std::vector<KsJob> &jobs, Scratch &s) {
+                      const std::vector<KsJob> &jobs, Scratch &s,
+                      const u64 *const *own = nullptr) {
   (void)n_ext;
-  u64 *acc = ks_inner(c, limbs, ext, jobs, s);
+  u64 *acc = ks_inner(c, limbs, ext, jobs, s, own);
   ks_moddown(c, limbs, acc, jobs, s);
 }
 
@@ -917,12 +927,12 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + P;
     const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
     u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s);
+    ks_modup(c, limbs, nb, d.data(), ext, s, false);
     const DeviceKey &key = get_key(c, g);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, g, in[b0 + i]->d, nullptr, out[b0 + i]->d, out[b0 + i]->d + P};
-    ks_finish(c, limbs, ext, nb, jobs, s);
+    ks_finish(c, limbs, ext, nb, jobs, s, d.data());
   }
 }
 
@@ -938,12 +948,12 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
     u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s);
+    ks_modup(c, limbs, nb, d.data(), ext, s, false);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, 1, in[b0 + i]->d, in[b0 + i]->d + P, out[b0 + i]->d,
                       out[b0 + i]->d + P};
-    ks_finish(c, limbs, ext, nb, jobs, s);
+    ks_finish(c, limbs, ext, nb, jobs, s, d.data());
   }
 }
 
@@ -965,10 +975,10 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + A;
     u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s);
+    ks_modup(c, limbs, nb, d.data(), ext, s, false);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
-    u64 *acc = ks_inner(c, limbs, ext, jobs, s);
+    u64 *acc = ks_inner(c, limbs, ext, jobs, s, d.data());
     // per item: [A] P limbs of X, then its q_l limb, as coefficients
     const size_t xs = (size_t)(A + 1) * N;
     u64 *x = s.get((size_t)nb * 2 * xs);

@@ -239,7 +239,8 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
 void launch_copy_limbs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                        int limb_count);
 void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
-                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois);
+                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois,
+                      const Batch *own = nullptr);
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,

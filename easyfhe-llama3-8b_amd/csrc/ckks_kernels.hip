@@ -1052,6 +1052,7 @@ void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch 
 // Table: [ns] hinv, [ns] hinv shoup, [ns][nd] hmod (Montgomery), [nd] Q mod t.
 // ===========================================================================
 
+template <int MS>
 __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int logN, int ns,
                                                        int nd, const u64 *__restrict__ tab,
                                                        int src_prime0, int t_split, int t_skip,
@@ -1062,10 +1063,10 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
   const u64 *in = batch_ptr(src, blockIdx.y);
   u64 *out = batch_ptr(dst, blockIdx.y);
   const int k = blockIdx.x * TPB + threadIdx.x;
-  u64 v[kMaxDigitSize];
+  u64 v[MS];
   u64 cnt = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxDigitSize; i++) {
+  for (int i = 0; i < MS; i++) {
     if (i < ns) {
       const u64 qi = mods[src_prime0 + i].q;
       v[i] = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
@@ -1082,7 +1083,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
     const ModQ M1 = mods[prime_of(tl1, q_limbs, L)];
     u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i++) {
+    for (int i = 0; i < MS; i++) {
       if (i < ns) {
         mac_wide(h0, l0, v[i], hm[i * nd + t]);
         mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
@@ -1102,7 +1103,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
     const ModQ M = mods[prime_of(tl, q_limbs, L)];
     u64 hi = 0, lo = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i++)
+    for (int i = 0; i < MS; i++)
       if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + t]);
     u64 y = redc(hi, lo, M.q, M.qinv);
     if (cnt) y = sub_mod(y, mul_mod(cnt, qm[t], M), M.q);
@@ -1116,6 +1117,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert(Batch src, Batch dst, int
 // final reduction.  The exact integer sum is the same as the 64-bit kernel's,
 // so the output words are identical; a wider target (q_0) keeps the 128-bit
 // Montgomery accumulation of k_basis_convert.
+template <int MS>
 __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
     const double2 *__restrict__ ftab, int src_prime0, int t_split, int t_skip, int q_limbs,
@@ -1131,9 +1133,9 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
   // v_i as exact doubles: canonical, or centered when asked (only these stay
   // live across the target loop, to keep the register count and so the
   // occupancy of this latency-bound kernel up)
-  double vd[kMaxDigitSize];
+  double vd[MS];
 #pragma unroll
-  for (int i = 0; i < kMaxDigitSize; i++) {
+  for (int i = 0; i < MS; i++) {
     if (i < ns) {
       const double q = (double)mods[src_prime0 + i].q;
       double v = fp_mulmod((double)in[((size_t)i << logN) + k], sf[i].x, sf[i].y, q);
@@ -1153,7 +1155,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     const ModQ M = mods[prime_of(tl, q_limbs, L)];
     u64 hi = 0, lo = 0, cnt = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i++) {
+    for (int i = 0; i < MS; i++) {
       if (i < ns) {
         const double v = vd[i];
         const u64 vu = v < 0.0 ? (u64)__dadd_rn(v, (double)mods[src_prime0 + i].q) : (u64)v;
@@ -1170,7 +1172,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     const double q = (double)mods[prime_of(tl, q_limbs, L)].q;
     double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i += 2) {
+    for (int i = 0; i < MS; i += 2) {
       if (i < ns) {
         const double2 h = hf[i * nd + t];
         a0 = __dadd_rn(a0, fp_mulmod(vd[i], h.x, h.y, q));
@@ -1196,7 +1198,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     const double q0 = (double)q0u, q1 = (double)q1u;
     double a0 = 0.0, a1 = 0.0, b0 = 0.0, b1 = 0.0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i += 2) {
+    for (int i = 0; i < MS; i += 2) {
       if (i < ns) {
         const double2 h0 = hf[i * nd + t], h1 = hf[i * nd + t + 1];
         a0 = __dadd_rn(a0, fp_mulmod(vd[i], h0.x, h0.y, q0));
@@ -1221,14 +1223,18 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered) {
   dim3 grid(c->N / TPB, n_items);
+  // one register per source: a 12-source instance for digits (and P) of at
+  // most 12 primes keeps the register count down
+  const bool s12 = t.ns <= 12;
   if (t.fd) {
-    hipLaunchKernelGGL(k_basis_convert_fp, grid, dim3(TPB), 0, c->stream, src, dst, c->logN,
-                       t.ns, t.nd, t.d, (const double2 *)t.fd, src_prime0, t_split, t_skip,
-                       q_limbs, c->L, centered ? 1 : 0, c->d_mods);
+    hipLaunchKernelGGL(s12 ? k_basis_convert_fp<12> : k_basis_convert_fp<kMaxDigitSize>, grid,
+                       dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d,
+                       (const double2 *)t.fd, src_prime0, t_split, t_skip, q_limbs, c->L,
+                       centered ? 1 : 0, c->d_mods);
   } else {
-    hipLaunchKernelGGL(k_basis_convert, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
-                       t.nd, t.d, src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0,
-                       c->d_mods);
+    hipLaunchKernelGGL(s12 ? k_basis_convert<12> : k_basis_convert<kMaxDigitSize>, grid,
+                       dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, src_prime0,
+                       t_split, t_skip, q_limbs, c->L, centered ? 1 : 0, c->d_mods);
   }
   LAUNCH_CHECK();
 }
@@ -1245,6 +1251,7 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
 // tab: the ModDown conversion table to the nd = limbs Q primes; rtab:
 // [nd-1] [P]_t (Montgomery), [nd-1] [q_last P]_t, P^-1 mod q_last, shoup.
 // The Montgomery sums stay below q_t 2^64 when sum(p_j) + q_last < 2^64.
+template <int MS>
 __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, int logN, int ns,
                                                          int nd, const u64 *__restrict__ tab,
                                                          const u64 *__restrict__ rtab, int L,
@@ -1254,10 +1261,10 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   const u64 *in = batch_ptr(src, blockIdx.y);
   u64 *out = batch_ptr(dst, blockIdx.y);
   const int k = blockIdx.x * TPB + threadIdx.x;
-  u64 v[kMaxDigitSize];
+  u64 v[MS];
   u64 cnt = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxDigitSize; i++) {
+  for (int i = 0; i < MS; i++) {
     if (i < ns) {
       const u64 qi = mods[L + i].q;
       v[i] = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
@@ -1270,7 +1277,7 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   const ModQ Mq = mods[n1];
   u64 hi = 0, lo = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxDigitSize; i++)
+  for (int i = 0; i < MS; i++)
     if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + n1]);
   u64 y = redc(hi, lo, Mq.q, Mq.qinv);
   if (cnt) y = sub_mod(y, mul_mod(cnt, qm[n1], Mq), Mq.q);
@@ -1282,7 +1289,7 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
     const ModQ M0 = mods[t], M1 = mods[t + 1];
     u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i++) {
+    for (int i = 0; i < MS; i++) {
       if (i < ns) {
         mac_wide(h0, l0, v[i], hm[i * nd + t]);
         mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
@@ -1307,7 +1314,7 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
     const ModQ M = mods[t];
     u64 h0 = 0, l0 = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxDigitSize; i++)
+    for (int i = 0; i < MS; i++)
       if (i < ns) mac_wide(h0, l0, v[i], hm[i * nd + t]);
     mac_wide(h0, l0, rv, sr[t]);
     u64 y0 = redc(h0, l0, M.q, M.qinv);
@@ -1322,8 +1329,9 @@ void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst,
   if (t.nd < 2 || t.ns > kMaxDigitSize)
     throw std::invalid_argument("relinearise-rescale conversion: at least 2 limbs");
   dim3 grid(c->N / TPB, n_items);
-  hipLaunchKernelGGL(k_bc_down_rescale, grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns,
-                     t.nd, t.d, rtab, c->L, c->d_mods);
+  hipLaunchKernelGGL(t.ns <= 12 ? k_bc_down_rescale<12> : k_bc_down_rescale<kMaxDigitSize>, grid,
+                     dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, rtab, c->L,
+                     c->d_mods);
   LAUNCH_CHECK();
 }
 
@@ -1373,46 +1381,62 @@ void launch_copy_limbs(ckks_context *c, const Batch &src, const Batch &dst, int 
 // once per call.  grid (N / 256, E)
 // ===========================================================================
 
+template <int MD>
 __global__ __launch_bounds__(TPB) void k_key_inner(Batch ext, Batch acc, int n_items,
                                                    const u64 *__restrict__ key, int digits,
                                                    int E, int q_limbs, int L, int K, u64 galois,
-                                                   int logN, const ModQ *__restrict__ mods) {
+                                                   int logN, const ModQ *__restrict__ mods,
+                                                   Batch own, int has_own, int ds) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = blockIdx.y;
   const int p = prime_of(l, q_limbs, L);
   const ModQ M = mods[p];
   const size_t N = (size_t)1 << logN;
-  u64 kb[kMaxDigits], ka[kMaxDigits];
+  u64 kb[MD], ka[MD];
 #pragma unroll
-  for (int j = 0; j < kMaxDigits; j++) {
+  for (int j = 0; j < MD; j++) {
     if (j < digits) {
       kb[j] = key[((size_t)(2 * j) * K + p) * N + k];
       ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + k];
     }
   }
   const u32 kk = galois == 1 ? (u32)k : autom_index((u32)k, galois, logN);
+  // the digit holding limb l (its own limb: read from the source if given)
+  const int jo = (has_own && l < q_limbs) ? l / ds : -1;
   for (int it = 0; it < n_items; it++) {
     const u64 *e = batch_ptr(ext, it);
+    const u64 *o = jo >= 0 ? batch_ptr(own, it) : nullptr;
     u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxDigits; j++) {
+    for (int j = 0; j < MD; j++) {
       if (j < digits) {
-        const u64 x = e[((size_t)j * E + l) * N + kk];
+        const u64 x = j == jo ? o[(size_t)l * N + kk] : e[((size_t)j * E + l) * N + kk];
         mac_wide(h0, l0, x, kb[j]);
         mac_wide(h1, l1, x, ka[j]);
       }
     }
-    u64 *o = batch_ptr(acc, it);
-    o[(size_t)l * N + k] = redc(h0, l0, M.q, M.qinv);
-    o[((size_t)E + l) * N + k] = redc(h1, l1, M.q, M.qinv);
+    u64 *a = batch_ptr(acc, it);
+    a[(size_t)l * N + k] = redc(h0, l0, M.q, M.qinv);
+    a[((size_t)E + l) * N + k] = redc(h1, l1, M.q, M.qinv);
   }
 }
 
 void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
-                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois) {
+                      const DeviceKey &key, int digits, int E, int q_limbs, u64 galois,
+                      const Batch *own) {
   dim3 grid(c->N / TPB, E);
-  hipLaunchKernelGGL(k_key_inner, grid, dim3(TPB), 0, c->stream, ext, acc, n_items, key.data,
-                     digits, E, q_limbs, c->L, c->K, galois, c->logN, c->d_mods);
+  Batch ob{};
+  if (own) ob = *own;
+  // the keys of every digit are held in registers: a 4-digit instance keeps
+  // the register count (and so the occupancy) of the common dnum <= 4 down
+  if (digits <= 4)
+    hipLaunchKernelGGL(k_key_inner<4>, grid, dim3(TPB), 0, c->stream, ext, acc, n_items,
+                       key.data, digits, E, q_limbs, c->L, c->K, galois, c->logN, c->d_mods, ob,
+                       own ? 1 : 0, c->ds);
+  else
+    hipLaunchKernelGGL(k_key_inner<kMaxDigits>, grid, dim3(TPB), 0, c->stream, ext, acc,
+                       n_items, key.data, digits, E, q_limbs, c->L, c->K, galois, c->logN,
+                       c->d_mods, ob, own ? 1 : 0, c->ds);
   LAUNCH_CHECK();
 }
 
