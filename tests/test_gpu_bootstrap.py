@@ -167,3 +167,35 @@ def test_bootstrap_sparse_slots(boot_ctx):
     assert out.slots == slots and out.state.cur_limbs == 4
     err = np.abs(client.decrypt_complex(out) - z).max()
     assert -math.log2(err) > 14, err
+
+
+def test_refresh_point_pairs_and_clamped_drop(boot_ctx):
+    """A residual refresh point: 4 real streams refreshed by 2 paired
+    bootstraps, then the modulus drop clamped to the consumer budget
+    (reference operators/norm/refresh.py:70-93, 207-242)."""
+    from easyfhe.bs import openfhe as bs
+    from easyfhe.bs import placement as pl
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3),
+                                             output_levels=3))
+    rng = np.random.default_rng(12)
+    zs = [rng.uniform(-1, 1, n) for _ in range(4)]
+    cts = [client.encrypt(z, cur_limbs=1, enc_id=110 + i) for i, z in enumerate(zs)]
+    sched = pl.RefreshSchedule(residual_bootstrap_level_drop=3)
+    res = pl.refresh_and_drop(cts, ctx, prog, schedule=sched, rmsnorm_depth=1,
+                              minimum_output_limbs=2)
+    top = prog.output_limbs
+    want_drop = pl.adaptive_bootstrap_output_level_drop(
+        current_limbs=top, requested_level_drop=3, rmsnorm_depth=1, minimum_output_limbs=2)
+    assert want_drop == min(3, top - 3) and res.level_drops == [want_drop] * 4
+    assert res.output_limbs == (top - want_drop,)
+    for got, z in zip(res.ciphers, zs):
+        err = np.abs(client.decrypt(got) - z).max()
+        assert -math.log2(err) > 14, err
+    # the reference's explicit halving spends one more limb, same values
+    halved = pl.refresh_ciphers(cts[:2], ctx, prog, halve=True)
+    for got, z in zip(halved, zs[:2]):
+        assert int(got.state.cur_limbs) == top - 1
+        assert -math.log2(np.abs(client.decrypt(got) - z).max()) > 14
