@@ -391,25 +391,6 @@ static const u64 *pinv_table(ckks_context *c, int limbs) {
   return c->pinv[limbs] = d;
 }
 
-static const u64 *rescale_table(ckks_context *c, int limbs) {
-  auto it = c->rescale_c.find(limbs);
-  if (it != c->rescale_c.end()) return it->second;
-  const u64 ql = c->primes[limbs - 1];
-  std::vector<u64> h(4 * (size_t)(limbs - 1), 0);
-  for (int i = 0; i < limbs - 1; i++) {
-    const u64 q = c->primes[i];
-    const u64 m = ql % q, inv = invmod_h(m, q);
-    h[4 * i] = m;
-    h[4 * i + 1] = inv;
-    h[4 * i + 2] = shoup_h(inv, q);
-  }
-  u64 *d = nullptr;
-  HIPCHECK(hipMalloc(&d, sizeof(u64) * std::max<size_t>(4, h.size())));
-  if (!h.empty())
-    HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
-  return c->rescale_c[limbs] = d;
-}
-
 // Relinearise-rescale constants for a ciphertext of `limbs` limbs (q_l is
 // its last prime, l1 = limbs - 1): [l1][2] (P q_l)^-1 mod q_i + shoup,
 // [l1][2] q_l^-1 mod q_i + shoup, then the conversion's [l1] [P]_t
@@ -679,8 +660,8 @@ static void free_context(ckks_context *c) {
     if (kv.second.fd) (void)hipFree(kv.second.fd);
   }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
-  for (auto &kv : c->rescale_c) (void)hipFree(kv.second);
   for (auto &kv : c->relin_rs) (void)hipFree(kv.second);
+  for (auto &kv : c->rescale_d) (void)hipFree(kv.second);
   for (auto &kv : c->garner) (void)hipFree(kv.second);
   for (auto &kv : c->fft) {
     (void)hipFree(kv.second.tw_fwd);
@@ -820,19 +801,25 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
   launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
                        2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
   const u64 *pinv = pinv_table(c, limbs);
-  if (c->logN == 16 && n <= kMaxBatch) {
+  // the fused path addresses component 1 of the addend and of the output at
+  // a fixed offset from component 0 (as every caller lays them out)
+  bool uniform = n <= kMaxBatch;
+  const u64 add1_off = jobs[0].add1 ? (u64)(jobs[0].add1 - jobs[0].add0) : 0;
+  const u64 out1_off = (u64)(jobs[0].out1 - jobs[0].out0);
+  for (int i = 0; i < n && uniform; i++)
+    uniform = (jobs[i].add1 ? (u64)(jobs[i].add1 - jobs[i].add0) : 0) == add1_off &&
+              (!jobs[i].add1 || jobs[i].add0) && (u64)(jobs[i].out1 - jobs[i].out0) == out1_off;
+  if (c->logN == 16 && uniform) {
     // NTT of the conversion with the combine fused into its last pass
-    Batch a0{}, a1{}, o0{}, o1{};
+    Batch a0{}, o0{};
     std::vector<u64> gal(n);
     for (int i = 0; i < n; i++) {
       a0.p[i] = (u64 *)jobs[i].add0;
-      a1.p[i] = (u64 *)jobs[i].add1;
       o0.p[i] = jobs[i].out0;
-      o1.p[i] = jobs[i].out1;
       gal[i] = jobs[i].galois;
     }
-    launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, Strided{acc, 2 * E * N}, E,
-                       pinv, a0, a1, gal.data(), o0, o1);
+    launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
+                       pinv, a0, add1_off, gal.data(), o0, out1_off);
     return;
   }
   launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2 * n, 0,
@@ -991,6 +978,8 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
       o0.p[i] = out[b0 + i]->d;
       o1.p[i] = out[b0 + i]->d + (size_t)l1 * N;
     }
+    (void)a1;
+    (void)o1;
     launch_rs_prep(c, Strided{acc, (size_t)E * N}, E, limbs, d3, nb,
                    Strided{x + (size_t)A * N, xs});
     launch_ntt(c, strided(x + (size_t)A * N - (size_t)l1 * N, xs),
@@ -1001,8 +990,8 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     std::vector<u64> gal(nb, 1);
     const u64 *amul = rt + 2 * (size_t)l1;
     if (c->logN == 16) {
-      launch_ntt_moddown(c, strided(conv, (size_t)l1 * N), nb, l1, Strided{acc, 2 * E * N}, E, rt,
-                         a0, a1, gal.data(), o0, o1, amul);
+      launch_ntt_moddown(c, strided(conv, (size_t)l1 * N), nb, l1, strided(acc, 2 * E * N), E, rt,
+                         a0, P, gal.data(), o0, (u64)l1 * N, amul);
     } else {
       launch_ntt(c, strided(conv, (size_t)l1 * N), strided(conv, (size_t)l1 * N), 2 * nb, 0, l1,
                  l1, false);
@@ -1012,29 +1001,84 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
   }
 }
 
-// Rescale n ciphertexts of `polys` polynomials each.
-static void rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out) {
-  const int limbs = in[0]->limbs, polys = in[0]->polys;
+// Constants of a rescale by the last D primes p_1 = q_{limbs-1}, p_2, ... of
+// a `limbs`-limb ciphertext, T = limbs - D remaining limbs (k_rescale_lift):
+// [T][2] (p_1..p_D)^-1 mod q_i + shoup; [T][D][3] p_1..p_j mod q_i (j < D
+// factors), its shoup, p_{j+1} mod q_i; [D][D][3] p_m mod p_j, p_m^-1 mod
+// p_j, shoup (m < j).
+static const u64 *rescale_d_table(ckks_context *c, int limbs, int D) {
+  auto key = std::make_pair(limbs, D);
+  auto it = c->rescale_d.find(key);
+  if (it != c->rescale_d.end()) return it->second;
+  const int T = limbs - D;
+  auto p = [&](int j) { return c->primes[limbs - 1 - j]; };  // p_{j+1}
+  std::vector<u64> h(2 * (size_t)T + 3 * (size_t)T * D + 3 * (size_t)D * D, 0);
+  for (int i = 0; i < T; i++) {
+    const u64 q = c->primes[i];
+    u64 prod = 1;
+    for (int j = 0; j < D; j++) {
+      u64 *e = &h[2 * (size_t)T + 3 * ((size_t)i * D + j)];
+      e[0] = prod;
+      e[1] = shoup_h(prod, q);
+      e[2] = p(j) % q;
+      prod = mulmod_h(prod, p(j) % q, q);
+    }
+    const u64 inv = invmod_h(prod, q);
+    h[2 * i] = inv;
+    h[2 * i + 1] = shoup_h(inv, q);
+  }
+  for (int j = 0; j < D; j++)
+    for (int m = 0; m < j; m++) {
+      u64 *e = &h[2 * (size_t)T + 3 * (size_t)T * D + 3 * ((size_t)j * D + m)];
+      const u64 pj = p(j), pm = p(m) % pj, inv = invmod_h(pm, pj);
+      e[0] = pm;
+      e[1] = inv;
+      e[2] = shoup_h(inv, pj);
+    }
+  u64 *d = nullptr;
+  HIPCHECK(hipMalloc(&d, sizeof(u64) * h.size()));
+  HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
+  return c->rescale_d[key] = d;
+}
+
+// Rescale n ciphertexts of `polys` polynomials each by their last D primes:
+// the inverse NTT of those limbs, the combined lift (k_rescale_lift), its
+// forward NTT and the combine, which at N = 2^16 runs in the NTT's last pass.
+// The words equal those of D rescales in a row.
+static void rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out,
+                          int D = 1) {
+  const int limbs = in[0]->limbs, polys = in[0]->polys, T = limbs - D;
   const size_t N = c->N;
-  const u64 *consts = rescale_table(c, limbs);
+  const u64 *tab = rescale_d_table(c, limbs, D);
+  const bool fused = c->logN == 16 && polys == 2;
   const int per = kMaxBatch / polys;
   for (int b0 = 0; b0 < n; b0 += per) {
     const int nb = std::min(per, n - b0), items = nb * polys;
     Scratch s(c);
-    u64 *last = s.get((size_t)items * N);
-    u64 *r = s.get((size_t)items * (limbs - 1) * N);
+    u64 *last = s.get((size_t)items * D * N);
+    u64 *w = s.get((size_t)items * T * N);
     Batch src{}, dst{};
     for (int i = 0; i < nb; i++)
       for (int p = 0; p < polys; p++) {
         src.p[i * polys + p] = in[b0 + i]->d + (size_t)p * limbs * N;
-        dst.p[i * polys + p] = out[b0 + i]->d + (size_t)p * (limbs - 1) * N;
+        dst.p[i * polys + p] = out[b0 + i]->d + (size_t)p * T * N;
       }
-    launch_ntt(c, src, strided(last - (size_t)(limbs - 1) * N, N), items, limbs - 1, 1, limbs,
-               true);
-    launch_rescale_expand(c, strided(last, N), strided(r, (size_t)(limbs - 1) * N), items, limbs);
-    launch_ntt(c, strided(r, (size_t)(limbs - 1) * N), strided(r, (size_t)(limbs - 1) * N), items,
-               0, limbs - 1, limbs - 1, false);
-    launch_rescale_combine(c, src, strided(r, (size_t)(limbs - 1) * N), dst, items, limbs, consts);
+    launch_ntt(c, src, strided(last - (size_t)T * N, (size_t)D * N), items, T, D, limbs, true);
+    launch_rescale_lift(c, strided(last, (size_t)D * N), strided(w, (size_t)T * N), items, limbs,
+                        D, tab);
+    if (fused) {
+      Batch acc{}, o{};
+      for (int i = 0; i < nb; i++) {
+        acc.p[i] = in[b0 + i]->d;
+        o.p[i] = out[b0 + i]->d;
+      }
+      std::vector<u64> gal(nb, 1);
+      launch_ntt_moddown(c, strided(w, (size_t)T * N), nb, T, acc, limbs, tab, Batch{}, 0,
+                         gal.data(), o, (u64)T * N);
+    } else {
+      launch_ntt(c, strided(w, (size_t)T * N), strided(w, (size_t)T * N), items, 0, T, T, false);
+      launch_rescale_finish(c, src, strided(w, (size_t)T * N), dst, items, T, tab);
+    }
   }
 }
 
@@ -1903,24 +1947,35 @@ int ckks_linear_combination(ckks_context *c, const ckks_ct *const *terms, int T,
   API_END
 }
 
-int ckks_rescale_many(ckks_context *c, const ckks_ct *const *a, int n, ckks_ct **out) {
+int ckks_rescale_many_by(ckks_context *c, const ckks_ct *const *a, int n, int primes,
+                         ckks_ct **out) {
   API_BEGIN
   require(c && a && out, "null argument");
   require(n >= 1, "need at least one ciphertext");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
   for (int i = 0; i < n; i++) {
     check_ct(c, a[i], "rescale_many");
     require(!a[i]->is_ext && a[i]->polys >= 1 && a[i]->limbs == a[0]->limbs &&
                 a[i]->polys == a[0]->polys,
             "rescale_many expects Q-basis ciphertexts of one shape");
   }
-  require(a[0]->limbs >= 2, "rescale needs at least two limbs");
+  require(primes >= 1 && primes <= kMaxRescaleDrop, "a rescale divides by 1 to 4 primes");
+  require(a[0]->limbs > primes, "rescale needs more limbs than the primes it divides by");
   for (int i = 0; i < n; i++) {
-    const double q = (double)c->primes[a[i]->limbs - 1];
-    out[i] = new_ct(c, a[i]->polys, a[i]->limbs - 1, 0, a[i]->slots, a[i]->scale / q,
-                    a[i]->scale_degree > 1 ? a[i]->scale_degree - 1 : 1);
+    double scale = a[i]->scale;
+    int degree = a[i]->scale_degree;
+    for (int j = 0; j < primes; j++) {
+      scale /= (double)c->primes[a[i]->limbs - 1 - j];
+      degree = degree > 1 ? degree - 1 : 1;
+    }
+    out[i] = new_ct(c, a[i]->polys, a[i]->limbs - primes, 0, a[i]->slots, scale, degree);
   }
-  rescale_batch(c, a, n, out);
+  rescale_batch(c, a, n, out, primes);
   API_END
+}
+
+int ckks_rescale_many(ckks_context *c, const ckks_ct *const *a, int n, ckks_ct **out) {
+  return ckks_rescale_many_by(c, a, n, 1, out);
 }
 
 int ckks_hoisted_rotate_ext(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,

@@ -25,6 +25,7 @@ namespace ckks {
 constexpr int kMaxBatch = 64;    // explicit pointers per kernel argument block
 constexpr int kMaxDigitSize = 16;  // Montgomery fold bound: 16 * 2^60 <= 2^64
 constexpr int kMaxDigits = 8;
+constexpr int kMaxRescaleDrop = 4;  // primes one rescale call may divide by
 constexpr int kMultiItems = 4;    // items per multi-rotation key inner product launch
 
 // Per-prime constants, resident in device memory.
@@ -188,8 +189,8 @@ struct ckks_context {
   std::map<int, ckks::BCTable> bc_down;                // limbs
   std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
   u64 *d_pmod = nullptr;         // [L][2] P mod q_i, shoup (extended-basis lifts)
-  std::map<int, u64 *> rescale_c;  // limbs -> [limbs-1][4] ql mod qi, ql^-1, shoup
   std::map<int, u64 *> relin_rs;   // limbs -> relinearise-rescale constants
+  std::map<std::pair<int, int>, u64 *> rescale_d;  // (limbs, primes) -> rescale constants
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
 };
@@ -245,14 +246,14 @@ void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
                             int E, const u64 *pinv, const u64 *amul = nullptr);
-void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, int n_items,
-                           int limbs);
-void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
-                            const Batch &out, int n_items, int limbs, const u64 *consts);
-void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
-                        int E, const u64 *pinv, const Batch &add0, const Batch &add1,
-                        const u64 *galois, const Batch &out0, const Batch &out1,
+void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
+                        int E, const u64 *pinv, const Batch &add, u64 add1_off,
+                        const u64 *galois, const Batch &out, u64 out1_off,
                         const u64 *amul = nullptr);
+void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
+                         int limbs, int D, const u64 *tab);
+void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,
+                           int n_items, int T, const u64 *inv);
 void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                             const BCTable &t, const u64 *rtab);
 void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, const Batch &d, int n,

@@ -256,11 +256,14 @@ struct Galois64 {
 };
 
 struct MDCombine {
-  Strided acc;  // item layout [2][E][N]
+  Batch acc;        // per item: [2][E][N] (component c, limb l at (c E + l) N)
   int E;
   const u64 *pinv;  // per Q limb: P^-1, shoup
   const u64 *amul;  // per Q limb: multiplier of the addend, shoup (null: 1)
-  Batch add0, add1, out0, out1;
+  Batch add;        // per item: component-0 addend (or null)
+  u64 add1_off;     // component-1 addend at add + add1_off (0: none)
+  Batch out;        // per item: component-0 output
+  u64 out1_off;     // component-1 output at out + out1_off
   Galois64 gal;
 };
 
@@ -275,8 +278,9 @@ __device__ __forceinline__ void md_load(const MDCombine &md, int item2, int limb
                                         MDPrefetch &pf) {
   const int item = item2 >> 1, comp = item2 & 1;
   const size_t N = 65536;
-  const u64 *acc = md.acc.base + item * md.acc.stride + ((size_t)comp * md.E + limb) * N;
-  const u64 *ad = comp ? batch_ptr(md.add1, item) : batch_ptr(md.add0, item);
+  const u64 *acc = batch_ptr(md.acc, item) + ((size_t)comp * md.E + limb) * N;
+  const u64 *ad = batch_ptr(md.add, item);
+  if (comp) ad = (ad && md.add1_off) ? ad + md.add1_off : nullptr;
   const u64 g = md.gal.g[item];
 #pragma unroll
   for (int k = 0; k < 16; k++) pf.a[k] = acc[e0 + 16 * k];
@@ -294,7 +298,7 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
   u64 r = shoup_mul(sub_mod(a, y, q), md.pinv[2 * limb], md.pinv[2 * limb + 1], q);
   if (md.amul) d = shoup_mul(d, md.amul[2 * limb], md.amul[2 * limb + 1], q);
   r = add_mod(r, d, q);
-  u64 *o = comp ? batch_ptr(md.out1, item) : batch_ptr(md.out0, item);
+  u64 *o = batch_ptr(md.out, item) + (comp ? md.out1_off : 0);
   o[(size_t)limb * N + e] = r;
 }
 
@@ -881,20 +885,19 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
 // Forward NTT of the ModDown conversion conv (2 n items, Q limbs) with the
 // combine of k_moddown_combine fused into the low pass: the converted P part
 // is never written back.  N = 2^16 only.
-void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Strided &acc,
-                        int E, const u64 *pinv, const Batch &add0, const Batch &add1,
-                        const u64 *galois, const Batch &out0, const Batch &out1,
-                        const u64 *amul) {
+void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
+                        int E, const u64 *pinv, const Batch &add, u64 add1_off,
+                        const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul) {
   if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
   MDCombine md{};
   md.acc = acc;
   md.E = E;
   md.pinv = pinv;
   md.amul = amul;
-  md.add0 = add0;
-  md.add1 = add1;
-  md.out0 = out0;
-  md.out1 = out1;
+  md.add = add;
+  md.add1_off = add1_off;
+  md.out = out;
+  md.out1_off = out1_off;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
   int start = 0;
   while (start < limbs) {
@@ -1576,50 +1579,95 @@ void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &
 }
 
 // ===========================================================================
-// rescale by the last prime q_l (rounded): r = centered(c_last) mod q_i,
-// out_i = (c_i - NTT(r)) q_l^-1.  consts per i: [ql mod qi, ql^-1, shoup, -].
+// rescale (rounded division by the last primes)
 // ===========================================================================
 
-__global__ void k_rescale_expand(Batch last, Batch r, int logN, int limbs,
-                                 const u64 *__restrict__ consts,
-                                 const ModQ *__restrict__ mods) {
+// Rescale by the product of the last D primes p_1 = q_l, p_2 = q_{l-1}, ...
+// in one pass, giving the words of D rescales in a row.  With v_j the
+// coefficients of limb l - j + 1 (canonical mod p_j), rescale j subtracts the
+// centered lift r_j of
+//   u_j = (((v_j - r_1) p_1^-1 - r_2) p_2^-1 - ... - r_{j-1}) p_{j-1}^-1 mod p_j,
+// so the result is (c - NTT(W)) (p_1 ... p_D)^-1 with W = sum_j r_j p_1..p_{j-1}.
+// This kernel writes W mod q_i for every remaining limb i < T = limbs - D.
+// last: per item [D][N], limbs l - D + 1 .. l in order (v_1 last); w: per
+// item [T][N]; grid (N / 256, items).
+// tab (see rescale_d_table): [T][2] (prod p)^-1 + shoup, [T][D][3] (p_1..p_{j-1}
+// mod q_i, its shoup, p_j mod q_i), [D][D][3] (p_m mod p_j, p_m^-1 mod p_j, shoup).
+__global__ __launch_bounds__(TPB) void k_rescale_lift(Batch last, Batch w, int logN, int limbs,
+                                                      int D, const u64 *__restrict__ tab,
+                                                      const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
-  const int i = blockIdx.y;  // target limb < limbs - 1
   const size_t N = (size_t)1 << logN;
-  const ModQ M = mods[i];
-  const u64 ql = mods[limbs - 1].q;
-  const u64 v = batch_ptr(last, blockIdx.z)[k];
-  u64 red = barrett(0, v, M);
-  if (v > (ql - 1) / 2) red = sub_mod(red, consts[4 * i], M.q);
-  batch_ptr(r, blockIdx.z)[(size_t)i * N + k] = red;
+  const int T = limbs - D;
+  const u64 *in = batch_ptr(last, blockIdx.y);
+  u64 *out = batch_ptr(w, blockIdx.y);
+  const u64 *tq = tab + 2 * (size_t)T;          // per target
+  const u64 *tc = tq + 3 * (size_t)T * D;       // lift chain
+  // r_j as canonical residues rv[j] in [0, p_j) with the sign of the lift
+  u64 rv[kMaxRescaleDrop];
+  bool neg[kMaxRescaleDrop];
+#pragma unroll
+  for (int j = 0; j < kMaxRescaleDrop; j++) {
+    if (j < D) {
+      const ModQ Mj = mods[limbs - 1 - j];
+      u64 u = in[((size_t)(D - 1 - j) << logN) + k];  // limb l - j sits at slot D - 1 - j
+#pragma unroll
+      for (int m = 0; m < kMaxRescaleDrop; m++) {
+        if (m < j) {
+          const u64 *cm = tc + 3 * ((size_t)j * D + m);
+          u64 rm = barrett(0, rv[m], Mj);
+          if (neg[m]) rm = sub_mod(rm, cm[0], Mj.q);
+          u = shoup_mul(sub_mod(u, rm, Mj.q), cm[1], cm[2], Mj.q);
+        }
+      }
+      rv[j] = u;
+      neg[j] = u > (Mj.q - 1) / 2;
+    }
+  }
+  for (int i = 0; i < T; i++) {
+    const ModQ M = mods[i];
+    const u64 *ti = tq + 3 * (size_t)i * D;
+    u64 acc = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++) {
+      if (j < D) {
+        u64 r = barrett(0, rv[j], M);
+        if (neg[j]) r = sub_mod(r, ti[3 * j + 2], M.q);
+        acc = add_mod(acc, j ? shoup_mul(r, ti[3 * j], ti[3 * j + 1], M.q) : r, M.q);
+      }
+    }
+    out[((size_t)i << logN) + k] = acc;
+  }
 }
 
-void launch_rescale_expand(ckks_context *c, const Batch &last, const Batch &r, int n_items,
-                           int limbs) {
-  dim3 grid(c->N / TPB, limbs - 1, n_items);
-  hipLaunchKernelGGL(k_rescale_expand, grid, dim3(TPB), 0, c->stream, last, r, c->logN, limbs,
-                     c->rescale_c.at(limbs), c->d_mods);
+void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
+                         int limbs, int D, const u64 *tab) {
+  if (D < 1 || D > kMaxRescaleDrop || D >= limbs)
+    throw std::invalid_argument("rescale: 1 <= primes dropped <= 4 and below the limb count");
+  dim3 grid(c->N / TPB, n_items);
+  hipLaunchKernelGGL(k_rescale_lift, grid, dim3(TPB), 0, c->stream, last, w, c->logN, limbs, D,
+                     tab, c->d_mods);
   LAUNCH_CHECK();
 }
 
-__global__ void k_rescale_combine(Batch src, Batch r, Batch out, int logN, int limbs,
-                                  const u64 *__restrict__ consts,
-                                  const ModQ *__restrict__ mods) {
+// out_i = (src_i - w_i) inv_i for the T remaining limbs; grid (N / 256, T, items)
+__global__ void k_rescale_finish(Batch src, Batch w, Batch out, int logN,
+                                 const u64 *__restrict__ inv, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int i = blockIdx.y;
   const size_t N = (size_t)1 << logN;
   const u64 q = mods[i].q;
   const u64 a = batch_ptr(src, blockIdx.z)[(size_t)i * N + k];
-  const u64 b = batch_ptr(r, blockIdx.z)[(size_t)i * N + k];
+  const u64 b = batch_ptr(w, blockIdx.z)[(size_t)i * N + k];
   batch_ptr(out, blockIdx.z)[(size_t)i * N + k] =
-      shoup_mul(sub_mod(a, b, q), consts[4 * i + 1], consts[4 * i + 2], q);
+      shoup_mul(sub_mod(a, b, q), inv[2 * i], inv[2 * i + 1], q);
 }
 
-void launch_rescale_combine(ckks_context *c, const Batch &src, const Batch &r,
-                            const Batch &out, int n_items, int limbs, const u64 *consts) {
-  dim3 grid(c->N / TPB, limbs - 1, n_items);
-  hipLaunchKernelGGL(k_rescale_combine, grid, dim3(TPB), 0, c->stream, src, r, out, c->logN,
-                     limbs, consts, c->d_mods);
+void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,
+                           int n_items, int T, const u64 *inv) {
+  dim3 grid(c->N / TPB, T, n_items);
+  hipLaunchKernelGGL(k_rescale_finish, grid, dim3(TPB), 0, c->stream, src, w, out, c->logN, inv,
+                     c->d_mods);
   LAUNCH_CHECK();
 }
 

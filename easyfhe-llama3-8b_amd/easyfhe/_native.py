@@ -114,6 +114,7 @@ SIGNATURES = {
     "ckks_hoisted_rotate_ext": (I, [VP, VP, I64P, I, VPP]),
     "ckks_hoisted_mac_sum_ext_many": (I, [VP, VPP, I, I64P, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_rescale_many": (I, [VP, VPP, I, VPP]),
+    "ckks_rescale_many_by": (I, [VP, VPP, I, I, VPP]),
     "ckks_linear_combination": (I, [VP, VPP, I, I, DP, ctypes.c_double, I, ctypes.c_double, I,
                                     VPP]),
     "ckks_moddown_ext": (I, [VP, VP, VPP]),

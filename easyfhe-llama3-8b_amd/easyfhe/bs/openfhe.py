@@ -338,8 +338,8 @@ def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
     pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=ext)
     acc = fhe.hoisted_mac_sum(x, _baby_offsets(plan, n), pts, _giant_offset(plan, n),
                               plan.giant, ctx, strategy=prog.evalmod.strategy)
-    for _ in range(lv.primes):
-        acc = fhe.rescale(acc, ctx)
+    if lv.primes:
+        acc = fhe.rescale_many([acc], ctx, primes=lv.primes)[0]
     acc.set_scale(lv.out_scale, 1)
     return acc
 
@@ -392,8 +392,8 @@ def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> lis
     pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=True)
     accs = fhe.hoisted_mac_sum_ext_many(xs, _baby_offsets(plan, n), pts,
                                         _giant_offset(plan, n), plan.giant, ctx)
-    for _ in range(lv.primes):
-        accs = fhe.rescale_many(accs, ctx)
+    if lv.primes:
+        accs = fhe.rescale_many(accs, ctx, primes=lv.primes)
     for a in accs:
         a.set_scale(lv.out_scale, 1)
     return accs

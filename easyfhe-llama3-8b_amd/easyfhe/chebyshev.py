@@ -148,9 +148,8 @@ class LadderOps:
         return fhe.align_to(ct, ct.state.replace(cur_limbs=limbs, scaling_factor=None), self.ctx)
 
     def _rescale_steps(self, ct):
-        for _ in range(self.lad.step):
-            ct = fhe.rescale(ct, self.ctx)
-        return ct
+        # the level's primes in one pass (same words as one rescale per prime)
+        return fhe.rescale_many([ct], self.ctx, primes=self.lad.step)[0]
 
     def _settle(self, ct, level: int):
         ct.set_scale(self.lad.scale[level], 1)
@@ -215,8 +214,8 @@ class LadderOps:
         # relinearise and the first rescale as one ModDown (same words as
         # homo_mul_relin then rescale)
         prod = fhe.homo_mul_relin_rescale_many([a.ct], [b.ct], self.ctx)[0]
-        for _ in range(self.lad.step - 1):
-            prod = fhe.rescale(prod, self.ctx)
+        if self.lad.step > 1:
+            prod = fhe.rescale_many([prod], self.ctx, primes=self.lad.step - 1)[0]
         return self._settle(prod, lev + 1)
 
 
@@ -227,9 +226,7 @@ class BatchLadderOps(LadderOps):
     and shared."""
 
     def _rescale_steps(self, cts):
-        for _ in range(self.lad.step):
-            cts = fhe.rescale_many(cts, self.ctx)
-        return cts
+        return fhe.rescale_many(cts, self.ctx, primes=self.lad.step)
 
     def _settle(self, cts, level: int):
         for ct in cts:
@@ -280,8 +277,8 @@ class BatchLadderOps(LadderOps):
         a, b = self.lower(a, lev), self.lower(b, lev)
         self.mults += len(a.ct)
         prods = fhe.homo_mul_relin_rescale_many(a.ct, b.ct, self.ctx)
-        for _ in range(self.lad.step - 1):
-            prods = fhe.rescale_many(prods, self.ctx)
+        if self.lad.step > 1:
+            prods = fhe.rescale_many(prods, self.ctx, primes=self.lad.step - 1)
         return self._settle(prods, lev + 1)
 
 

@@ -702,14 +702,24 @@ def linear_combination(terms, weights, constant: float, limbs: int, scale: float
     return [Ciphertext(ctx, outs[i]) for i in range(n)]
 
 
-def rescale_many(cts: Sequence[Ciphertext], context=None) -> list:
-    """fhe.rescale of several ciphertexts of one shape in batched launches."""
+def rescale_many(cts: Sequence[Ciphertext], context=None, primes: int = 1) -> list:
+    """fhe.rescale of several ciphertexts of one shape in batched launches;
+    ``primes`` > 1 divides by that many last primes in one pass, with the
+    words of as many rescales in a row."""
     if not cts:
         return []
     ctx = _ctx(cts[0], context)
-    outs = (ctypes.c_void_p * len(cts))()
-    check(lib.ckks_rescale_many(ctx.handle, ptr_array([c.handle for c in cts]), len(cts), outs))
-    return [Ciphertext(ctx, outs[i]) for i in range(len(cts))]
+    cts, left = list(cts), int(primes)
+    if left < 1:
+        raise ValueError("rescale divides by at least one prime")
+    while left:
+        step = min(left, 4)  # primes per launch sequence
+        outs = (ctypes.c_void_p * len(cts))()
+        check(lib.ckks_rescale_many_by(ctx.handle, ptr_array([c.handle for c in cts]), len(cts),
+                                       step, outs))
+        cts = [Ciphertext(ctx, outs[i]) for i in range(len(cts))]
+        left -= step
+    return cts
 
 
 def hoisted_mac_sum_ext_many(cts: Sequence[Ciphertext], baby_offsets, plaintexts,

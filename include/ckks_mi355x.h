@@ -199,6 +199,13 @@ int ckks_linear_combination(ckks_context *ctx, const ckks_ct *const *terms, int 
                             int scale_degree, ckks_ct **out);
 /* fhe.rescale for n ciphertexts of one shape in batched launches. */
 int ckks_rescale_many(ckks_context *ctx, const ckks_ct *const *a, int n, ckks_ct **out);
+/* `primes` rescales in a row (1..4) of each of n ciphertexts of one shape, as
+ * one inverse NTT of the dropped limbs, one combined lift and one forward NTT
+ * (reference: the repeated fhe.rescale of a multi-prime level step,
+ * operators/nonlinear/polynomial.py:182, operators/linear/operator.py:386);
+ * the words equal those of `primes` calls of ckks_rescale. */
+int ckks_rescale_many_by(ckks_context *ctx, const ckks_ct *const *a, int n, int primes,
+                         ckks_ct **out);
 /* fhe.fast_rotate(..., output_ext=True) (reference attention/input.py:792-826):
  * hoisted rotations left in the Q u P basis, i.e. P rot_k(a) before ModDown;
  * the outputs are extended ciphertexts at a's scale. */

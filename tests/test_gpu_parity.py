@@ -233,6 +233,14 @@ def test_mul_relin_rescale_parity(name):
         assert np.array_equal(m.download(), rrs)
     # rescale of a degree-2 ciphertext (tensor) as well
     assert np.array_equal(fhe.rescale(t, ctx).download(), orc.rescale(rt))
+    # several primes in one pass = that many rescales in a row
+    for k in range(2, ctx.L):
+        want = rrl
+        for _ in range(k):
+            want = orc.rescale(want)
+        for m in fhe.rescale_many([rl, rl], ctx, primes=k):
+            assert np.array_equal(m.download(), want), k
+            assert m.state.cur_limbs == ctx.L - k
     # one level down (an even number of limbs left after the rescale)
     lim = ctx.L - 1
     a2 = client.encrypt(x, slots=slots, cur_limbs=lim, enc_id=23)
@@ -434,6 +442,17 @@ def test_keyswitch_size_parity():
         exp = orc.rescale(orc.relinearize(orc.tensor(refs[i], refs[i])))
         assert np.array_equal(prods[i].download(), exp)
         assert np.abs(client.decrypt(prods[i]) - zs[i] ** 2).max() < 1e-6
+    # rescales at this size (the combine runs in the NTT's last pass), by 1..3
+    # primes at once, and of a degree-2 ciphertext
+    want = refs[0]
+    for k in (1, 2, 3):
+        want = orc.rescale(want)
+        got = fhe.rescale_many(cts[:1], ctx, primes=k)[0]
+        assert np.array_equal(got.download(), want), k
+    t3 = fhe.homo_mul_no_relin(cts[0], cts[1], ctx)
+    r3 = orc.tensor(refs[0], refs[1])
+    assert np.array_equal(fhe.rescale_many([t3], ctx, primes=2)[0].download(),
+                          orc.rescale(orc.rescale(r3)))
 
 
 def test_linear_combination_matches_composed_ops():
