@@ -1844,13 +1844,22 @@ static void mac_sum_ext(ckks_context *c, const ckks_ct *const *a, int n,
   std::vector<u64 *> bp((size_t)B * n);
   for (size_t k = 0; k < bp.size(); k++) bp[k] = bab + k * EP;
   ext_babies(c, a, n, baby_rotations, B, bp.data(), s);
-  u64 *inner_ext = s.get((size_t)n * EP);
+  // the MAC of several giant groups runs as one pass over the babies
+  const int GC = std::max(1, std::min(kMacGroups, kMaxBatch / B));
+  u64 *inner_all = s.get((size_t)std::min(GC, giant_count) * n * EP);
   u64 *inner = s.get((size_t)n * 2 * P);
   for (int i = 0; i < n; i++) out[i] = nullptr;
+  int g_lo = giant_count;  // groups [g_lo, g_lo + GC) are in inner_all
   for (int g = giant_count - 1; g >= 0; g--) {
-    Batch ptb{};
-    for (int b = 0; b < B; b++) ptb.p[b] = pts[g * B + b]->d;
-    launch_mac_many(c, bab, n, ptb, B, inner_ext, E, limbs);
+    if (g < g_lo) {
+      g_lo = std::max(0, g - GC + 1);
+      const int gn = g - g_lo + 1;
+      Batch ptb{};
+      for (int gi = 0; gi < gn; gi++)
+        for (int b = 0; b < B; b++) ptb.p[gi * B + b] = pts[(g_lo + gi) * B + b]->d;
+      launch_mac_many(c, bab, n, ptb, B, gn, inner_all, E, limbs);
+    }
+    u64 *inner_ext = inner_all + (size_t)(g - g_lo) * n * EP;
     const bool first = out[0] == nullptr;
     std::vector<KsJob> jobs(n);
     for (int i = 0; i < n; i++) {

@@ -1725,36 +1725,67 @@ void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u
   LAUNCH_CHECK();
 }
 
-// Extended-basis MAC of n ciphertexts sharing the plaintexts: babies at
-// bab[(b n + i)][2][E][N], out[i][2][E][N]; the loop over ciphertexts is inside
-// each thread, so every plaintext word is fetched from HBM once (its repeats
-// hit L2).  grid (N / 256, E, 2)
-__global__ void k_mac_many(const u64 *__restrict__ bab, int n, Batch pts, int B,
-                           u64 *__restrict__ out, int E, int q_limbs, int L, int logN,
-                           const ModQ *__restrict__ mods) {
+// Extended-basis MAC of n ciphertexts sharing the plaintexts, for G giant
+// groups at once: babies at bab[(b n + i)][2][E][N], plaintext of group g and
+// baby b at pts[g B + b], out[(g n + i)][2][E][N].  Each thread walks the
+// babies for kMacCts ciphertexts at a time with the plaintext words of every
+// group in registers: every baby word is read from HBM once for all groups,
+// and a plaintext word is re-read (from L2) once per kMacCts ciphertexts.
+// grid (N / 256, E, 2)
+__global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, int n, Batch pts,
+                                                  int B, int G, u64 *__restrict__ out, int E,
+                                                  int q_limbs, int L, int logN,
+                                                  const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = blockIdx.y, comp = blockIdx.z;
   const size_t N = (size_t)1 << logN, EP = 2 * (size_t)E * N;
   const ModQ M = mods[prime_of(l, q_limbs, L)];
   const size_t off = ((size_t)comp * E + l) * N + k;
-  for (int i = 0; i < n; i++) {
-    u64 acc = 0, hi = 0, lo = 0;
+  for (int i0 = 0; i0 < n; i0 += kMacCts) {
+    u64 acc[kMacGroups][kMacCts], hi[kMacGroups][kMacCts], lo[kMacGroups][kMacCts];
+#pragma unroll
+    for (int g = 0; g < kMacGroups; g++)
+#pragma unroll
+      for (int c = 0; c < kMacCts; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
     for (int b = 0; b < B; b++) {
-      mac_wide(hi, lo, bab[((size_t)b * n + i) * EP + off], batch_ptr(pts, b)[(size_t)l * N + k]);
+      u64 pt[kMacGroups];
+#pragma unroll
+      for (int g = 0; g < kMacGroups; g++)
+        pt[g] = g < G ? batch_ptr(pts, g * B + b)[(size_t)l * N + k] : 0;
+#pragma unroll
+      for (int c = 0; c < kMacCts; c++) {
+        if (i0 + c < n) {
+          const u64 x = bab[((size_t)b * n + i0 + c) * EP + off];
+#pragma unroll
+          for (int g = 0; g < kMacGroups; g++)
+            if (g < G) mac_wide(hi[g][c], lo[g][c], x, pt[g]);
+        }
+      }
       if ((b & 15) == 15 || b == B - 1) {
-        acc = add_mod(acc, redc(hi, lo, M.q, M.qinv), M.q);
-        hi = lo = 0;
+#pragma unroll
+        for (int g = 0; g < kMacGroups; g++)
+#pragma unroll
+          for (int c = 0; c < kMacCts; c++) {
+            acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
+            hi[g][c] = lo[g][c] = 0;
+          }
       }
     }
-    out[(size_t)i * EP + off] = to_mont(acc, M);
+#pragma unroll
+    for (int g = 0; g < kMacGroups; g++)
+#pragma unroll
+      for (int c = 0; c < kMacCts; c++)
+        if (g < G && i0 + c < n) out[((size_t)g * n + i0 + c) * EP + off] = to_mont(acc[g][c], M);
   }
 }
 
-void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, u64 *out,
-                     int E, int q_limbs) {
+void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, int G,
+                     u64 *out, int E, int q_limbs) {
+  if (G < 1 || G > kMacGroups || G * B > kMaxBatch)
+    throw std::invalid_argument("mac_many: 1 <= groups <= 2 and groups x babies <= 64");
   dim3 grid(c->N / TPB, E, 2);
-  hipLaunchKernelGGL(k_mac_many, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, out, E, q_limbs,
-                     c->L, c->logN, c->d_mods);
+  hipLaunchKernelGGL(k_mac_many, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, E,
+                     q_limbs, c->L, c->logN, c->d_mods);
   LAUNCH_CHECK();
 }
 
