@@ -391,45 +391,65 @@ static const u64 *pinv_table(ckks_context *c, int limbs) {
   return c->pinv[limbs] = d;
 }
 
-// Relinearise-rescale constants for a ciphertext of `limbs` limbs (q_l is
-// its last prime, l1 = limbs - 1): [l1][2] (P q_l)^-1 mod q_i + shoup,
-// [l1][2] q_l^-1 mod q_i + shoup, then the conversion's [l1] [P]_t
-// (Montgomery), [l1] [q_l P]_t, P^-1 mod q_l + shoup.
-static const u64 *relin_rs_table(ckks_context *c, int limbs) {
-  auto it = c->relin_rs.find(limbs);
+// Relinearise-rescale constants for a ciphertext of `limbs` limbs dropping
+// its last D primes p_1 = q_{limbs-1}, p_2, ... (T = limbs - D): [T][2]
+// (P p_1..p_D)^-1 mod q_t + shoup, [T][2] (p_1..p_D)^-1 mod q_t + shoup, then
+// the conversion's part (k_bc_down_rescale): [T][D] P p_1..p_{j-1} mod q_t
+// (Montgomery), [T][D] P p_1..p_j mod q_t, [D][2] P^-1 mod p_j + shoup,
+// [D][D][3] p_m mod p_j, p_m^-1 mod p_j, shoup (m < j).
+static const u64 *relin_rs_table(ckks_context *c, int limbs, int D) {
+  auto key = std::make_pair(limbs, D);
+  auto it = c->relin_rs.find(key);
   if (it != c->relin_rs.end()) return it->second;
-  const int l1 = limbs - 1;
-  const u64 ql = c->primes[l1];
-  std::vector<u64> h(6 * (size_t)l1 + 2);
+  const int T = limbs - D;
+  auto p = [&](int j) { return c->primes[limbs - 1 - j]; };  // p_{j+1}
   auto pmod = [&](u64 q) {
     u64 P = 1;
     for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
     return P;
   };
-  for (int i = 0; i < l1; i++) {
-    const u64 q = c->primes[i], P = pmod(q);
-    const u64 inv2 = invmod_h(mulmod_h(P, ql % q, q), q), invq = invmod_h(ql % q, q);
-    h[2 * i] = inv2;
-    h[2 * i + 1] = shoup_h(inv2, q);
-    h[2 * (size_t)l1 + 2 * i] = invq;
-    h[2 * (size_t)l1 + 2 * i + 1] = shoup_h(invq, q);
-    h[4 * (size_t)l1 + i] = (u64)(((u128)P << 64) % q);
-    h[5 * (size_t)l1 + i] = mulmod_h(P, ql % q, q);
+  std::vector<u64> h(4 * (size_t)T + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D, 0);
+  u64 *pm = h.data() + 4 * (size_t)T, *pp = pm + (size_t)T * D, *pi = pp + (size_t)T * D;
+  u64 *chain = pi + 2 * (size_t)D;
+  for (int t = 0; t < T; t++) {
+    const u64 q = c->primes[t], P = pmod(q);
+    u64 prod = 1;  // p_1..p_j mod q
+    for (int j = 0; j < D; j++) {
+      const u64 f = mulmod_h(P, prod, q);
+      pm[(size_t)t * D + j] = (u64)(((u128)f << 64) % q);
+      prod = mulmod_h(prod, p(j) % q, q);
+      pp[(size_t)t * D + j] = mulmod_h(P, prod, q);
+    }
+    const u64 inv2 = invmod_h(mulmod_h(P, prod, q), q), invq = invmod_h(prod, q);
+    h[2 * t] = inv2;
+    h[2 * t + 1] = shoup_h(inv2, q);
+    h[2 * (size_t)T + 2 * t] = invq;
+    h[2 * (size_t)T + 2 * t + 1] = shoup_h(invq, q);
   }
-  const u64 pinv = invmod_h(pmod(ql), ql);
-  h[6 * (size_t)l1] = pinv;
-  h[6 * (size_t)l1 + 1] = shoup_h(pinv, ql);
+  for (int j = 0; j < D; j++) {
+    const u64 pj = p(j), inv = invmod_h(pmod(pj), pj);
+    pi[2 * j] = inv;
+    pi[2 * j + 1] = shoup_h(inv, pj);
+    for (int m = 0; m < j; m++) {
+      u64 *e = chain + 3 * ((size_t)j * D + m);
+      const u64 r = p(m) % pj, ri = invmod_h(r, pj);
+      e[0] = r;
+      e[1] = ri;
+      e[2] = shoup_h(ri, pj);
+    }
+  }
   u64 *d = nullptr;
   HIPCHECK(hipMalloc(&d, sizeof(u64) * h.size()));
   HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
-  return c->relin_rs[limbs] = d;
+  return c->relin_rs[key] = d;
 }
 
 // The one-ModDown relinearise-rescale needs the Montgomery sums of its
-// conversion (alpha sources and the lift) below q_t 2^64.
-static bool relin_rs_fits(const ckks_context *c, int limbs) {
-  if (limbs < 2 || c->alpha > kMaxDigitSize) return false;
-  u128 s = c->primes[limbs - 1];
+// conversion (alpha sources and D lifts) below q_t 2^64.
+static bool relin_rs_fits(const ckks_context *c, int limbs, int D) {
+  if (D < 1 || D > kMaxRescaleDrop || limbs <= D || c->alpha > kMaxDigitSize) return false;
+  u128 s = 0;
+  for (int j = 0; j < D; j++) s += c->primes[limbs - 1 - j];
   for (int j = 0; j < c->alpha; j++) s += c->primes[c->L + j];
   return s < ((u128)1 << 64);
 }
@@ -944,17 +964,18 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
   }
 }
 
-// Relinearisation of n degree-2 ciphertexts followed by the rescale, as one
-// ModDown by P q_l (see k_bc_down_rescale): the same words as relin_batch
-// then rescale_batch, without the relinearised ciphertext's forward NTT, its
-// last-limb inverse NTT and the rescale's lift NTT and combine.
-static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n,
-                                ckks_ct **out) {
-  const int limbs = in[0]->limbs, l1 = limbs - 1, A = c->alpha;
+// Relinearisation of n degree-2 ciphertexts followed by D rescales, as one
+// ModDown by P p_1..p_D (see k_bc_down_rescale): the same words as
+// relin_batch then D rescales, without the relinearised ciphertext's forward
+// NTT, the inverse NTTs of the dropped limbs and the rescales' lift NTTs and
+// combines.
+static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out,
+                                int D = 1) {
+  const int limbs = in[0]->limbs, T = limbs - D, A = c->alpha;
   const size_t N = c->N, P = (size_t)limbs * N;
   const DeviceKey &key = get_key(c, 0);
   const BCTable &bt = bc_down(c, limbs);
-  const u64 *rt = relin_rs_table(c, limbs);
+  const u64 *rt = relin_rs_table(c, limbs, D);
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
     Scratch s(c);
@@ -966,37 +987,38 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
     u64 *acc = ks_inner(c, limbs, ext, jobs, s, d.data());
-    // per item: [A] P limbs of X, then its q_l limb, as coefficients
-    const size_t xs = (size_t)(A + 1) * N;
+    // per item: [A] P limbs of X, then its limbs limbs-D .. limbs-1, as
+    // coefficients
+    const size_t xs = (size_t)(A + D) * N;
     u64 *x = s.get((size_t)nb * 2 * xs);
     launch_ntt(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A, limbs, true);
-    Batch d3{}, a0{}, a1{}, o0{}, o1{};
+    Batch d3{}, o0{};
     for (int i = 0; i < nb; i++) {
       d3.p[i] = in[b0 + i]->d;
-      a0.p[i] = in[b0 + i]->d;
-      a1.p[i] = in[b0 + i]->d + P;
       o0.p[i] = out[b0 + i]->d;
-      o1.p[i] = out[b0 + i]->d + (size_t)l1 * N;
     }
-    (void)a1;
-    (void)o1;
-    launch_rs_prep(c, Strided{acc, (size_t)E * N}, E, limbs, d3, nb,
-                   Strided{x + (size_t)A * N, xs});
-    launch_ntt(c, strided(x + (size_t)A * N - (size_t)l1 * N, xs),
-               strided(x + (size_t)A * N - (size_t)l1 * N, xs), 2 * nb, l1, 1, limbs, true);
-    u64 *conv = s.get((size_t)nb * 2 * l1 * N);
-    launch_bc_down_rescale(c, strided(x, xs), strided(conv, (size_t)l1 * N), 2 * nb, bt,
-                           rt + 4 * (size_t)l1);
+    u64 *xq = x + (size_t)A * N;  // slot A holds limb T
+    launch_rs_prep(c, Strided{acc, (size_t)E * N}, E, limbs, D, d3, nb, Strided{xq, xs});
+    launch_ntt(c, strided(xq - (size_t)T * N, xs), strided(xq - (size_t)T * N, xs), 2 * nb, T, D,
+               limbs, true);
+    u64 *conv = s.get((size_t)nb * 2 * T * N);
+    launch_bc_down_rescale(c, strided(x, xs), strided(conv, (size_t)T * N), 2 * nb, bt, D,
+                           rt + 4 * (size_t)T);
     std::vector<u64> gal(nb, 1);
-    const u64 *amul = rt + 2 * (size_t)l1;
+    const u64 *amul = rt + 2 * (size_t)T;
     if (c->logN == 16) {
-      launch_ntt_moddown(c, strided(conv, (size_t)l1 * N), nb, l1, strided(acc, 2 * E * N), E, rt,
-                         a0, P, gal.data(), o0, (u64)l1 * N, amul);
+      launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
+                         d3, P, gal.data(), o0, (u64)T * N, amul);
     } else {
-      launch_ntt(c, strided(conv, (size_t)l1 * N), strided(conv, (size_t)l1 * N), 2 * nb, 0, l1,
-                 l1, false);
-      launch_moddown_combine(c, Strided{acc, 2 * E * N}, Strided{conv, 2 * l1 * N}, a0, a1,
-                             gal.data(), o0, o1, nb, l1, E, rt, amul);
+      Batch a1{}, o1{};
+      for (int i = 0; i < nb; i++) {
+        a1.p[i] = in[b0 + i]->d + P;
+        o1.p[i] = out[b0 + i]->d + (size_t)T * N;
+      }
+      launch_ntt(c, strided(conv, (size_t)T * N), strided(conv, (size_t)T * N), 2 * nb, 0, T, T,
+                 false);
+      launch_moddown_combine(c, Strided{acc, 2 * E * N}, Strided{conv, 2 * T * N}, d3, a1,
+                             gal.data(), o0, o1, nb, T, E, rt, amul);
     }
   }
 }
@@ -1617,12 +1639,14 @@ int ckks_rotate(ckks_context *c, const ckks_ct *a, int64_t rotation, ckks_ct **o
   API_END
 }
 
-int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
-                                const ckks_ct *const *b, int n, ckks_ct **out) {
+int ckks_mul_relin_rescale_many_by(ckks_context *c, const ckks_ct *const *a,
+                                   const ckks_ct *const *b, int n, int primes, ckks_ct **out) {
   API_BEGIN
   require(c && a && b && out && n >= 1, "null argument");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
   const int limbs = a[0]->limbs;
-  require(limbs >= 2, "rescale needs at least two limbs");
+  require(primes >= 1 && primes <= kMaxRescaleDrop, "a rescale divides by 1 to 4 primes");
+  require(limbs > primes, "rescale needs more limbs than the primes it divides by");
   for (int i = 0; i < n; i++) {
     check_ct(c, a[i], "mul");
     check_ct(c, b[i], "mul");
@@ -1631,11 +1655,12 @@ int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
   }
   get_key(c, 0);
   const size_t N = c->N;
+  const bool merged = relin_rs_fits(c, limbs, primes);
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
     Scratch s(c);
     u64 *t3 = s.get((size_t)nb * 3 * limbs * N);
-    u64 *t2 = s.get((size_t)nb * 2 * limbs * N);
+    u64 *t2 = merged ? nullptr : s.get((size_t)nb * 2 * limbs * N);
     Batch ba{}, bb{};
     for (int i = 0; i < nb; i++) {
       ba.p[i] = a[b0 + i]->d;
@@ -1647,25 +1672,36 @@ int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
     std::vector<ckks_ct *> p2(nb);
     for (int i = 0; i < nb; i++) {
       v3[i] = ckks_ct{c, t3 + (size_t)i * 3 * limbs * N, 0, 3, limbs, 0, a[b0 + i]->slots, 2, 0};
-      v2[i] = ckks_ct{c, t2 + (size_t)i * 2 * limbs * N, 0, 2, limbs, 0, a[b0 + i]->slots, 2, 0};
       p3[i] = &v3[i];
-      p2[i] = &v2[i];
+      if (!merged) {
+        v2[i] = ckks_ct{c, t2 + (size_t)i * 2 * limbs * N, 0, 2, limbs, 0, a[b0 + i]->slots, 2, 0};
+        p2[i] = &v2[i];
+      }
     }
-    const double div = (double)c->primes[limbs - 1];
     std::vector<ckks_ct *> o(nb);
-    for (int i = 0; i < nb; i++)
-      o[i] = out[b0 + i] = new_ct(c, 2, limbs - 1, 0, a[b0 + i]->slots,
-                                  a[b0 + i]->scale * b[b0 + i]->scale / div,
-                                  std::max(1, a[b0 + i]->scale_degree + b[b0 + i]->scale_degree - 1));
-    if (relin_rs_fits(c, limbs)) {
-      relin_rescale_batch(c, p3.data(), nb, o.data());
+    for (int i = 0; i < nb; i++) {
+      double scale = a[b0 + i]->scale * b[b0 + i]->scale;
+      int degree = a[b0 + i]->scale_degree + b[b0 + i]->scale_degree;
+      for (int j = 0; j < primes; j++) {
+        scale /= (double)c->primes[limbs - 1 - j];
+        degree = std::max(1, degree - 1);
+      }
+      o[i] = out[b0 + i] = new_ct(c, 2, limbs - primes, 0, a[b0 + i]->slots, scale, degree);
+    }
+    if (merged) {
+      relin_rescale_batch(c, p3.data(), nb, o.data(), primes);
       continue;
     }
     relin_batch(c, p3.data(), nb, p2.data());
     std::vector<const ckks_ct *> cp2(p2.begin(), p2.end());
-    rescale_batch(c, cp2.data(), nb, o.data());
+    rescale_batch(c, cp2.data(), nb, o.data(), primes);
   }
   API_END
+}
+
+int ckks_mul_relin_rescale_many(ckks_context *c, const ckks_ct *const *a,
+                                const ckks_ct *const *b, int n, ckks_ct **out) {
+  return ckks_mul_relin_rescale_many_by(c, a, b, n, 1, out);
 }
 
 int ckks_hoisted_rotate(ckks_context *c, const ckks_ct *a, const int64_t *rotations, int n,

@@ -191,7 +191,7 @@ struct ckks_context {
   std::map<int, ckks::BCTable> bc_down;                // limbs
   std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
   u64 *d_pmod = nullptr;         // [L][2] P mod q_i, shoup (extended-basis lifts)
-  std::map<int, u64 *> relin_rs;   // limbs -> relinearise-rescale constants
+  std::map<std::pair<int, int>, u64 *> relin_rs;  // (limbs, primes) -> relin-rescale constants
   std::map<std::pair<int, int>, u64 *> rescale_d;  // (limbs, primes) -> rescale constants
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
@@ -257,9 +257,9 @@ void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int
 void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,
                            int n_items, int T, const u64 *inv);
 void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
-                            const BCTable &t, const u64 *rtab);
-void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, const Batch &d, int n,
-                    const Strided &x);
+                            const BCTable &t, int D, const u64 *rtab);
+void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, int D, const Batch &d,
+                    int n, const Strided &x);
 // Feature-major BSGS diagonal geometry (token-lane packing)
 struct DiagGeom {
   int D, lanes, baby, giant_base;

@@ -1242,28 +1242,34 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
   LAUNCH_CHECK();
 }
 
-// ModDown conversion of a relinearisation fused with the rescale that
-// follows it (division by P q_last in one ModDown, bit-identical to the two
-// steps).  Per item (the 2 polynomials of each ciphertext) the source holds
-// the ns = alpha P limbs of X = acc + P d and, at slot ns, its q_last limb,
-// all as coefficients.  y = conv(X_P) in q_last gives the last coefficient of
-// the relinearised ciphertext, rv = [(X_q - y) P^-1]_{q_last}; its centered
-// lift r is what the rescale subtracts.  Written for t < nd - 1:
-//   out_t = conv(X_P)_t + [P]_t r   (mod q_t)
-// so that (acc - NTT(out)) (P q_last)^-1 + d q_last^-1 is the rescaled limb.
+// ModDown conversion of a relinearisation fused with the D rescales that
+// follow it (division by P p_1 .. p_D in one ModDown, bit-identical to the
+// separate steps; p_1 = q_{l-1} is the last prime, p_2 the one before, ...).
+// Per item (the 2 polynomials of each ciphertext) the source holds the
+// ns = alpha P limbs of X = acc + P d and, at slots ns .. ns + D - 1, its
+// limbs l - D .. l - 1, all as coefficients.  For each dropped prime p_j,
+// y_j = conv(X_P)_{p_j} gives the relinearised coefficient
+// [(X_{p_j} - y_j) P^-1]_{p_j}; the rescale chain turns these into the
+// centered lifts r_j that the rescales subtract (as in k_rescale_lift).
+// Written for the T = nd - D remaining limbs:
+//   out_t = conv(X_P)_t + P sum_j r_j p_1 .. p_{j-1}   (mod q_t)
+// so that (acc - NTT(out)) (P p_1..p_D)^-1 + d (p_1..p_D)^-1 is the result.
 // tab: the ModDown conversion table to the nd = limbs Q primes; rtab:
-// [nd-1] [P]_t (Montgomery), [nd-1] [q_last P]_t, P^-1 mod q_last, shoup.
-// The Montgomery sums stay below q_t 2^64 when sum(p_j) + q_last < 2^64.
+// [T][D] P p_1..p_{j-1} mod q_t (Montgomery), [T][D] P p_1..p_j mod q_t,
+// [D][2] P^-1 mod p_j + shoup, [D][D][3] p_m mod p_j, p_m^-1 mod p_j, shoup.
+// The Montgomery sums stay below q_t 2^64 when sum(P primes) + sum(p_j) < 2^64.
 template <int MS>
 __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, int logN, int ns,
-                                                         int nd, const u64 *__restrict__ tab,
+                                                         int nd, int D,
+                                                         const u64 *__restrict__ tab,
                                                          const u64 *__restrict__ rtab, int L,
                                                          const ModQ *__restrict__ mods) {
   // constants at wave-uniform addresses (scalar loads)
-  const u64 *st = tab, *sr = rtab;
+  const u64 *st = tab;
   const u64 *in = batch_ptr(src, blockIdx.y);
   u64 *out = batch_ptr(dst, blockIdx.y);
   const int k = blockIdx.x * TPB + threadIdx.x;
+  const int T = nd - D;
   u64 v[MS];
   u64 cnt = 0;
 #pragma unroll
@@ -1276,19 +1282,38 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   }
   const u64 *hm = st + 2 * ns;
   const u64 *qm = hm + (size_t)ns * nd;
-  const int n1 = nd - 1;
-  const ModQ Mq = mods[n1];
-  u64 hi = 0, lo = 0;
+  const u64 *pm = rtab, *pp = rtab + (size_t)T * D, *pinv = pp + (size_t)T * D;
+  const u64 *chain = pinv + 2 * (size_t)D;
+  u64 rv[kMaxRescaleDrop];
+  bool neg[kMaxRescaleDrop];
 #pragma unroll
-  for (int i = 0; i < MS; i++)
-    if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + n1]);
-  u64 y = redc(hi, lo, Mq.q, Mq.qinv);
-  if (cnt) y = sub_mod(y, mul_mod(cnt, qm[n1], Mq), Mq.q);
-  const u64 xq = in[((size_t)ns << logN) + k];
-  const u64 rv = shoup_mul(sub_mod(xq, y, Mq.q), sr[2 * n1], sr[2 * n1 + 1], Mq.q);
-  const bool neg = rv > (Mq.q - 1) / 2;
+  for (int j = 0; j < kMaxRescaleDrop; j++) {
+    if (j < D) {
+      const int tj = nd - 1 - j;
+      const ModQ Mj = mods[tj];
+      u64 hi = 0, lo = 0;
+#pragma unroll
+      for (int i = 0; i < MS; i++)
+        if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + tj]);
+      u64 y = redc(hi, lo, Mj.q, Mj.qinv);
+      if (cnt) y = sub_mod(y, mul_mod(cnt, qm[tj], Mj), Mj.q);
+      const u64 xq = in[((size_t)(ns + D - 1 - j) << logN) + k];
+      u64 u = shoup_mul(sub_mod(xq, y, Mj.q), pinv[2 * j], pinv[2 * j + 1], Mj.q);
+#pragma unroll
+      for (int m = 0; m < kMaxRescaleDrop; m++) {
+        if (m < j) {
+          const u64 *cm = chain + 3 * ((size_t)j * D + m);
+          u64 rm = barrett(0, rv[m], Mj);
+          if (neg[m]) rm = sub_mod(rm, cm[0], Mj.q);
+          u = shoup_mul(sub_mod(u, rm, Mj.q), cm[1], cm[2], Mj.q);
+        }
+      }
+      rv[j] = u;
+      neg[j] = u > (Mj.q - 1) / 2;
+    }
+  }
   int t = 0;
-  for (; t + 1 < n1; t += 2) {
+  for (; t + 1 < T; t += 2) {
     const ModQ M0 = mods[t], M1 = mods[t + 1];
     u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
 #pragma unroll
@@ -1298,67 +1323,80 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
         mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
       }
     }
-    mac_wide(h0, l0, rv, sr[t]);
-    mac_wide(h1, l1, rv, sr[t + 1]);
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++) {
+      if (j < D) {
+        mac_wide(h0, l0, rv[j], pm[(size_t)t * D + j]);
+        mac_wide(h1, l1, rv[j], pm[(size_t)(t + 1) * D + j]);
+      }
+    }
     u64 y0 = redc(h0, l0, M0.q, M0.qinv);
     u64 y1 = redc(h1, l1, M1.q, M1.qinv);
     if (cnt) {
       y0 = sub_mod(y0, mul_mod(cnt, qm[t], M0), M0.q);
       y1 = sub_mod(y1, mul_mod(cnt, qm[t + 1], M1), M1.q);
     }
-    if (neg) {
-      y0 = sub_mod(y0, sr[n1 + t], M0.q);
-      y1 = sub_mod(y1, sr[n1 + t + 1], M1.q);
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++) {
+      if (j < D && neg[j]) {
+        y0 = sub_mod(y0, pp[(size_t)t * D + j], M0.q);
+        y1 = sub_mod(y1, pp[(size_t)(t + 1) * D + j], M1.q);
+      }
     }
     out[((size_t)t << logN) + k] = y0;
     out[((size_t)(t + 1) << logN) + k] = y1;
   }
-  if (t < n1) {
+  if (t < T) {
     const ModQ M = mods[t];
     u64 h0 = 0, l0 = 0;
 #pragma unroll
     for (int i = 0; i < MS; i++)
       if (i < ns) mac_wide(h0, l0, v[i], hm[i * nd + t]);
-    mac_wide(h0, l0, rv, sr[t]);
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++)
+      if (j < D) mac_wide(h0, l0, rv[j], pm[(size_t)t * D + j]);
     u64 y0 = redc(h0, l0, M.q, M.qinv);
     if (cnt) y0 = sub_mod(y0, mul_mod(cnt, qm[t], M), M.q);
-    if (neg) y0 = sub_mod(y0, sr[n1 + t], M.q);
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++)
+      if (j < D && neg[j]) y0 = sub_mod(y0, pp[(size_t)t * D + j], M.q);
     out[((size_t)t << logN) + k] = y0;
   }
 }
 
 void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
-                            const BCTable &t, const u64 *rtab) {
-  if (t.nd < 2 || t.ns > kMaxDigitSize)
-    throw std::invalid_argument("relinearise-rescale conversion: at least 2 limbs");
+                            const BCTable &t, int D, const u64 *rtab) {
+  if (D < 1 || D > kMaxRescaleDrop || t.nd <= D || t.ns > kMaxDigitSize)
+    throw std::invalid_argument("relinearise-rescale conversion: 1 <= primes < limbs");
   dim3 grid(c->N / TPB, n_items);
   hipLaunchKernelGGL(t.ns <= 12 ? k_bc_down_rescale<12> : k_bc_down_rescale<kMaxDigitSize>, grid,
-                     dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, rtab, c->L,
+                     dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, D, t.d, rtab, c->L,
                      c->d_mods);
   LAUNCH_CHECK();
 }
 
-// X_q = acc_q + [P]_q d_q for the q_last limb (limb l1) of every item:
-// acc items [2 n][E][N], d: ciphertext c of item i is batch_ptr(d, i) with
-// polynomials [3][limbs][N]; written to x (strided per item2).
-// grid (N / 256, 2 n)
-__global__ void k_rs_prep(Strided acc, int E, int limbs, Batch d, Strided x, int logN,
-                          const u64 *__restrict__ pm, const ModQ *__restrict__ mods) {
+// X_l = acc_l + [P]_l d_l for the last D limbs l = limbs - D .. limbs - 1 of
+// every item: acc items [2 n][E][N]; ciphertext i of d is batch_ptr(d, i)
+// with polynomials [3][limbs][N]; written to x (strided per item2, the D
+// limbs in order).  grid (N / 256, 2 n, D)
+__global__ void k_rs_prep(Strided acc, int E, int limbs, int D, Batch d, Strided x, int logN,
+                          const u64 *__restrict__ pmod, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int item = blockIdx.y >> 1, comp = blockIdx.y & 1;
   const size_t N = (size_t)1 << logN;
-  const int l1 = limbs - 1;
-  const u64 q = mods[l1].q;
-  const u64 a = acc.base[blockIdx.y * acc.stride + (size_t)l1 * N + k];
-  const u64 dv = batch_ptr(d, item)[((size_t)comp * limbs + l1) * N + k];
-  x.base[blockIdx.y * x.stride + k] = add_mod(a, shoup_mul(dv, pm[0], pm[1], q), q);
+  const int l = limbs - D + blockIdx.z;
+  const u64 q = mods[l].q;
+  const u64 a = acc.base[blockIdx.y * acc.stride + (size_t)l * N + k];
+  const u64 dv = batch_ptr(d, item)[((size_t)comp * limbs + l) * N + k];
+  x.base[blockIdx.y * x.stride + (size_t)blockIdx.z * N + k] =
+      add_mod(a, shoup_mul(dv, pmod[2 * l], pmod[2 * l + 1], q), q);
 }
 
-void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, const Batch &d, int n,
-                    const Strided &x) {
-  dim3 grid(c->N / TPB, 2 * n);
-  hipLaunchKernelGGL(k_rs_prep, grid, dim3(TPB), 0, c->stream, acc, E, limbs, d, x, c->logN,
-                     c->d_pmod + 2 * (limbs - 1), c->d_mods);
+void launch_rs_prep(ckks_context *c, const Strided &acc, int E, int limbs, int D, const Batch &d,
+                    int n, const Strided &x) {
+  dim3 grid(c->N / TPB, 2 * n, D);
+  hipLaunchKernelGGL(k_rs_prep, grid, dim3(TPB), 0, c->stream, acc, E, limbs, D, d, x, c->logN,
+                     c->d_pmod, c->d_mods);
   LAUNCH_CHECK();
 }
 

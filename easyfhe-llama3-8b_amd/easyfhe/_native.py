@@ -108,6 +108,7 @@ SIGNATURES = {
     "ckks_mod_raise": (I, [VP, VP, I, VPP]),
     "ckks_rotate_many": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
     "ckks_mul_relin_rescale_many": (I, [VP, VPP, VPP, I, VPP]),
+    "ckks_mul_relin_rescale_many_by": (I, [VP, VPP, VPP, I, I, VPP]),
     "ckks_hoisted_rotate": (I, [VP, VP, I64P, I, VPP]),
     "ckks_hoisted_mac_sum": (I, [VP, VPP, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_hoisted_mac_sum_ext": (I, [VP, VP, I64P, I, VPP, ctypes.c_int64, I, VPP]),

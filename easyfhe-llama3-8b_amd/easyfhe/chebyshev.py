@@ -211,11 +211,10 @@ class LadderOps:
             raise ValueError("ladder depth exhausted")
         a, b = self.lower(a, lev), self.lower(b, lev)
         self.mults += 1
-        # relinearise and the first rescale as one ModDown (same words as
-        # homo_mul_relin then rescale)
-        prod = fhe.homo_mul_relin_rescale_many([a.ct], [b.ct], self.ctx)[0]
-        if self.lad.step > 1:
-            prod = fhe.rescale_many([prod], self.ctx, primes=self.lad.step - 1)[0]
+        # relinearise and the level's rescales as one ModDown (same words as
+        # homo_mul_relin then the rescales)
+        prod = fhe.homo_mul_relin_rescale_many([a.ct], [b.ct], self.ctx,
+                                               primes=self.lad.step)[0]
         return self._settle(prod, lev + 1)
 
 
@@ -276,9 +275,7 @@ class BatchLadderOps(LadderOps):
             raise ValueError("ladder depth exhausted")
         a, b = self.lower(a, lev), self.lower(b, lev)
         self.mults += len(a.ct)
-        prods = fhe.homo_mul_relin_rescale_many(a.ct, b.ct, self.ctx)
-        if self.lad.step > 1:
-            prods = fhe.rescale_many(prods, self.ctx, primes=self.lad.step - 1)
+        prods = fhe.homo_mul_relin_rescale_many(a.ct, b.ct, self.ctx, primes=self.lad.step)
         return self._settle(prods, lev + 1)
 
 

@@ -760,18 +760,25 @@ def homo_rotate_many(cts: Sequence[Ciphertext], rotation: int, context=None) -> 
 
 
 def homo_mul_relin_rescale_many(left: Sequence[Ciphertext], right: Sequence[Ciphertext],
-                                context=None) -> list:
+                                context=None, primes: int = 1) -> list:
+    """Products, relinearised and rescaled by ``primes`` (1..4) last primes,
+    batched: one key switch per product whose ModDown also does the rescales
+    (the same words as homo_mul_relin and ``primes`` rescales)."""
     left, right = list(left), list(right)
     if len(left) != len(right):
         raise ValueError("operand lists differ in length")
     if not left:
         return []
     ctx = _ctx(left[0], context)
+    if int(primes) < 1:
+        raise ValueError("rescale divides by at least one prime")
+    first = min(int(primes), 4)  # primes one merged ModDown takes
     outs = (ctypes.c_void_p * len(left))()
-    check(lib.ckks_mul_relin_rescale_many(ctx.handle, ptr_array([c.handle for c in left]),
-                                          ptr_array([c.handle for c in right]), len(left),
-                                          outs))
-    return [Ciphertext(ctx, outs[i]) for i in range(len(left))]
+    check(lib.ckks_mul_relin_rescale_many_by(ctx.handle, ptr_array([c.handle for c in left]),
+                                             ptr_array([c.handle for c in right]), len(left),
+                                             first, outs))
+    res = [Ciphertext(ctx, outs[i]) for i in range(len(left))]
+    return rescale_many(res, ctx, primes=int(primes) - first) if int(primes) > first else res
 
 
 def _hoisted(ct: Ciphertext, offsets: Sequence[int], ctx: NativeContext) -> list:

@@ -160,6 +160,13 @@ int ckks_rotate_many(ckks_context *ctx, const ckks_ct *const *in, int n,
 /* homo_mul_relin + rescale for n pairs (config: HMult+relin+rescale). */
 int ckks_mul_relin_rescale_many(ckks_context *ctx, const ckks_ct *const *a,
                                 const ckks_ct *const *b, int n, ckks_ct **out);
+/* ckks_mul_relin_rescale_many followed by `primes` - 1 more rescales (1..4
+ * primes in all; the step of a multi-prime level, reference
+ * operators/nonlinear/polynomial.py:115-203): one key switch whose ModDown
+ * divides by P and the dropped primes at once, with the words of the
+ * separate steps. */
+int ckks_mul_relin_rescale_many_by(ckks_context *ctx, const ckks_ct *const *a,
+                                   const ckks_ct *const *b, int n, int primes, ckks_ct **out);
 /* fhe.prepare_hoisted_baby_rotations (reference operators/linear/operator.py:105):
  * one ModUp of c1 shared by all rotations. */
 int ckks_hoisted_rotate(ckks_context *ctx, const ckks_ct *a,

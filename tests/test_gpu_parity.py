@@ -233,7 +233,8 @@ def test_mul_relin_rescale_parity(name):
         assert np.array_equal(m.download(), rrs)
     # rescale of a degree-2 ciphertext (tensor) as well
     assert np.array_equal(fhe.rescale(t, ctx).download(), orc.rescale(rt))
-    # several primes in one pass = that many rescales in a row
+    # several primes in one pass = that many rescales in a row, after a
+    # relinearisation as well as merged into its ModDown
     for k in range(2, ctx.L):
         want = rrl
         for _ in range(k):
@@ -241,6 +242,9 @@ def test_mul_relin_rescale_parity(name):
         for m in fhe.rescale_many([rl, rl], ctx, primes=k):
             assert np.array_equal(m.download(), want), k
             assert m.state.cur_limbs == ctx.L - k
+        if k <= 4:
+            for m in fhe.homo_mul_relin_rescale_many([a, a], [b, b], ctx, primes=k):
+                assert np.array_equal(m.download(), want), k
     # one level down (an even number of limbs left after the rescale)
     lim = ctx.L - 1
     a2 = client.encrypt(x, slots=slots, cur_limbs=lim, enc_id=23)
@@ -453,6 +457,9 @@ def test_keyswitch_size_parity():
     r3 = orc.tensor(refs[0], refs[1])
     assert np.array_equal(fhe.rescale_many([t3], ctx, primes=2)[0].download(),
                           orc.rescale(orc.rescale(r3)))
+    # relinearise + two rescales as one ModDown
+    got = fhe.homo_mul_relin_rescale_many(cts[:1], cts[1:], ctx, primes=2)[0]
+    assert np.array_equal(got.download(), orc.rescale(orc.rescale(orc.relinearize(r3))))
 
 
 def test_linear_combination_matches_composed_ops():
