@@ -1635,7 +1635,6 @@ __global__ __launch_bounds__(TPB) void k_rescale_lift(Batch last, Batch w, int l
                                                       int D, const u64 *__restrict__ tab,
                                                       const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
-  const size_t N = (size_t)1 << logN;
   const int T = limbs - D;
   const u64 *in = batch_ptr(last, blockIdx.y);
   u64 *out = batch_ptr(w, blockIdx.y);
