@@ -1795,6 +1795,78 @@ int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
   API_END
 }
 
+int ckks_hoisted_mac_sum_many(ckks_context *c, const ckks_ct *const *babies, int n, int B,
+                              const ckks_ct *const *pts, int64_t giant_rotation,
+                              int giant_count, ckks_ct **out) {
+  API_BEGIN
+  require(c && babies && pts && out, "null argument");
+  require(n >= 1 && n <= 4096 && B >= 1 && B <= 4096, "ciphertext and baby counts in [1, 4096]");
+  require(giant_count >= 1, "giant_count must be positive");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  const int limbs = babies[0]->limbs;
+  for (int j = 0; j < n * B; j++) {
+    check_ct(c, babies[j], "hoisted_mac_sum_many");
+    require(babies[j]->limbs == limbs && babies[j]->polys == 2 && !babies[j]->is_ext,
+            "babies must be degree-1 Q-basis ciphertexts at one level");
+  }
+  for (int j = 0; j < B * giant_count; j++) {
+    check_ct(c, pts[j], "hoisted_mac_sum_many");
+    // an extended plaintext stores its Q limbs first
+    require(pts[j]->polys == 1 && pts[j]->limbs >= limbs,
+            "plaintexts must be at or above the babies' level");
+  }
+  const u64 gg = galois_of(c, giant_rotation);
+  if (giant_count > 1 && gg != 1) get_key(c, gg);
+  const size_t N = c->N, CP = 2 * (size_t)limbs * N;
+  std::vector<u64> btab((size_t)n * B), ptab((size_t)B * giant_count);
+  for (size_t j = 0; j < btab.size(); j++) btab[j] = (u64)babies[j]->d;
+  for (size_t j = 0; j < ptab.size(); j++) ptab[j] = (u64)pts[j]->d;
+  Scratch s(c);
+  u64 *dbt = s.get(btab.size()), *dpt = s.get(ptab.size());
+  HIPCHECK(hipMemcpyAsync(dbt, btab.data(), sizeof(u64) * btab.size(), hipMemcpyHostToDevice,
+                          c->stream));
+  HIPCHECK(hipMemcpyAsync(dpt, ptab.data(), sizeof(u64) * ptab.size(), hipMemcpyHostToDevice,
+                          c->stream));
+  const int GC = std::min(kTabGroups, giant_count);
+  u64 *inner = s.get((size_t)GC * n * CP);
+  const double scale = babies[0]->scale * pts[0]->scale;
+  const int sdeg = babies[0]->scale_degree + pts[0]->scale_degree;
+  int g_lo = giant_count;  // groups [g_lo, g_lo + GC) are in inner
+  for (int g = giant_count - 1; g >= 0; g--) {
+    if (g < g_lo) {
+      g_lo = std::max(0, g - GC + 1);
+      launch_mac_table(c, (const u64 *const *)dbt, n, (const u64 *const *)(dpt + (size_t)g_lo * B),
+                       B, g - g_lo + 1, inner, limbs);
+    }
+    const u64 *ig = inner + (size_t)(g - g_lo) * n * CP;
+    if (!out[0]) {
+      for (int i = 0; i < n; i++) {
+        out[i] = new_ct(c, 2, limbs, 0, babies[(size_t)i * B]->slots, scale, sdeg);
+        HIPCHECK(hipMemcpyAsync(out[i]->d, ig + (size_t)i * CP, sizeof(u64) * CP,
+                                hipMemcpyDeviceToDevice, c->stream));
+      }
+      continue;
+    }
+    // Horner: out = rot(out) + inner_g, the rotations batched over the n
+    std::vector<ckks_ct *> rot(n);
+    for (int i = 0; i < n; i++)
+      rot[i] = new_ct(c, 2, limbs, 0, out[i]->slots, scale, sdeg);
+    if (gg == 1) {
+      for (int i = 0; i < n; i++)
+        HIPCHECK(hipMemcpyAsync(rot[i]->d, out[i]->d, out[i]->bytes, hipMemcpyDeviceToDevice,
+                                c->stream));
+    } else {
+      std::vector<const ckks_ct *> cur(out, out + n);
+      rotate_batch(c, cur.data(), n, gg, rot.data());
+    }
+    for (int i = 0; i < n; i++) {
+      launch_addsub(c, rot[i]->d, ig + (size_t)i * CP, out[i]->d, 2, limbs, limbs, 0);
+      free_ct(rot[i]);
+    }
+  }
+  API_END
+}
+
 // Extended-basis babies of n ciphertexts for the given rotations, each
 // [2][E][N] before its ModDown: (P c0, P c1) for offset 0,
 // (P sigma(c0) + acc_0, acc_1) otherwise.  One ModUp per ciphertext (batched)

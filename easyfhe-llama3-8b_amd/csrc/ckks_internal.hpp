@@ -28,6 +28,8 @@ constexpr int kMaxDigits = 8;
 constexpr int kMaxRescaleDrop = 4;  // primes one rescale call may divide by
 constexpr int kMacGroups = 2;       // giant groups of one extended MAC pass
 constexpr int kMacCts = 4;          // ciphertexts per plaintext read in that pass
+constexpr int kTabGroups = 8;       // giant groups of one Q-basis MAC pass (k_mac_table)
+constexpr int kTabCts = 2;          // ciphertexts per plaintext read in that pass
 constexpr int kMultiItems = 4;    // items per multi-rotation key inner product launch
 
 // Per-prime constants, resident in device memory.
@@ -283,6 +285,8 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             const u64 *const *d_outp, int digits, int E, int q_limbs);
 void launch_lincomb(ckks_context *c, const u64 *d_table, int T, int n, const double *d_w,
                     double cst, u64 *const *d_outp, int limbs, u64 *wtab, u64 *ctab);
+void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *const *pts, int B,
+                      int G, u64 *out, int limbs);
 void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, int G,
                      u64 *out, int E, int q_limbs);
 void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);

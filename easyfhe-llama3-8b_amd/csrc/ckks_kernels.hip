@@ -1826,6 +1826,69 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
   LAUNCH_CHECK();
 }
 
+// BSGS MAC of n Q-basis ciphertexts sharing G x B plaintexts, up to
+// kTabGroups giant groups per pass: baby b of ciphertext i at bab[i B + b]
+// ([2][limbs][N]), plaintext of group g and baby b at pts[g B + b] (limb l at
+// l N), inner sum of group g for ciphertext i to out + (g n + i) 2 limbs N.
+// Each thread walks the babies of kTabCts ciphertexts at a time with the
+// groups' plaintext words in registers: a baby word is read once per pass, a
+// plaintext word (from L2) once per kTabCts ciphertexts.
+// grid (N / 256, limbs, 2)
+__global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict__ bab, int n,
+                                                   const u64 *const *__restrict__ pts, int B,
+                                                   int G, u64 *__restrict__ out, int limbs,
+                                                   int logN, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, comp = blockIdx.z;
+  const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
+  const ModQ M = mods[l];
+  const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
+  for (int i0 = 0; i0 < n; i0 += kTabCts) {
+    u64 acc[kTabGroups][kTabCts], hi[kTabGroups][kTabCts], lo[kTabGroups][kTabCts];
+#pragma unroll
+    for (int g = 0; g < kTabGroups; g++)
+#pragma unroll
+      for (int c = 0; c < kTabCts; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+    for (int b = 0; b < B; b++) {
+      u64 x[kTabCts];
+#pragma unroll
+      for (int c = 0; c < kTabCts; c++) x[c] = i0 + c < n ? bab[(size_t)(i0 + c) * B + b][off] : 0;
+#pragma unroll
+      for (int g = 0; g < kTabGroups; g++) {
+        if (g < G) {
+          const u64 w = pts[(size_t)g * B + b][poff];
+#pragma unroll
+          for (int c = 0; c < kTabCts; c++) mac_wide(hi[g][c], lo[g][c], x[c], w);
+        }
+      }
+      if ((b & 15) == 15 || b == B - 1) {
+#pragma unroll
+        for (int g = 0; g < kTabGroups; g++)
+#pragma unroll
+          for (int c = 0; c < kTabCts; c++) {
+            acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
+            hi[g][c] = lo[g][c] = 0;
+          }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < kTabGroups; g++)
+#pragma unroll
+      for (int c = 0; c < kTabCts; c++)
+        if (g < G && i0 + c < n) out[((size_t)g * n + i0 + c) * CP + off] = to_mont(acc[g][c], M);
+  }
+}
+
+void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *const *pts, int B,
+                      int G, u64 *out, int limbs) {
+  if (G < 1 || G > kTabGroups || B < 1 || n < 1)
+    throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
+  dim3 grid(c->N / TPB, limbs, 2);
+  hipLaunchKernelGGL(k_mac_table, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs,
+                     c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
 // Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0
 // on the special limbs (layout [2][limbs + alpha][N]); grid (N / 256, E, 2)
 __global__ void k_ext_identity(const u64 *__restrict__ ct, u64 *__restrict__ out, int limbs,

@@ -865,6 +865,31 @@ def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count
                 b.release()
 
 
+def hoisted_mac_sum_many(baby_rotations: Sequence[Sequence[Ciphertext]], plaintexts,
+                         giant_offset: int, giant_count: int, context=None) -> list:
+    """hoisted_mac_sum with precomputed babies for several ciphertexts that
+    share the plaintexts (every input of one linear chunk): ``baby_rotations[i]``
+    holds the B babies of ciphertext i.  The plaintexts are read once for the
+    batch and the babies once per pass of up to 8 giant groups; results are
+    unrescaled and the same words as one hoisted_mac_sum per ciphertext."""
+    sets = [list(b) for b in baby_rotations]
+    if not sets:
+        return []
+    B = len(sets[0])
+    if B == 0 or any(len(b) != B for b in sets):
+        raise ValueError("every ciphertext needs the same number of babies")
+    ctx = _ctx(sets[0][0], context)
+    pts = plaintexts if isinstance(plaintexts, (list, tuple)) else [plaintexts]
+    if len(pts) < B * int(giant_count):
+        raise ValueError(f"need {B * int(giant_count)} plaintexts, got {len(pts)}")
+    flat = [b.handle for bs in sets for b in bs]
+    outs = (ctypes.c_void_p * len(sets))()
+    check(lib.ckks_hoisted_mac_sum_many(ctx.handle, ptr_array(flat), len(sets), B,
+                                        ptr_array([p.handle for p in pts[: B * int(giant_count)]]),
+                                        int(giant_offset), int(giant_count), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(sets))]
+
+
 # ---------------------------------------------------------------------------
 # batches (reference operators/attention/kernel_helpers.py:83-85,
 # attention/input.py:792-826)

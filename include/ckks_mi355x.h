@@ -179,6 +179,15 @@ int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
                          const ckks_ct *const *pts, int64_t giant_rotation,
                          int giant_count, ckks_ct **out);
 
+/* fhe.hoisted_mac_sum with precomputed babies for n ciphertexts sharing the
+ * plaintexts (reference operators/linear/operator.py:320-330 for every input
+ * of one chunk): baby b of ciphertext i at babies[i * B + b], plaintexts
+ * pts[g * B + b]; out[i] = Horner over the giant key of sum_b pt (.) baby,
+ * unrescaled.  Each baby word is read once per pass of up to 8 giant groups
+ * and each plaintext word once per pass for all n (L2 re-reads aside). */
+int ckks_hoisted_mac_sum_many(ckks_context *ctx, const ckks_ct *const *babies, int n, int B,
+                              const ckks_ct *const *pts, int64_t giant_rotation,
+                              int giant_count, ckks_ct **out);
 /* fhe.hoisted_mac_sum, strategies "ext_normal" / "ext_double_hoist" (reference
  * operators/linear/operator.py:320-330, linear/config.py:296-305): the babies
  * of `a` for baby_rotations stay in the Q u P basis (no ModDown), the
