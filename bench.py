@@ -80,12 +80,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bootstrap", action="store_true",
                     help="skip the bootstrap measurement of the default run")
+    ap.add_argument("--no-linear", action="store_true",
+                    help="skip the feature-major linear measurement of the default run")
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
-    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap"],
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
-                         "bootstrap: the full-slot bootstrap workload on the same chain")
+                         "bootstrap: the full-slot bootstrap workload on the same chain; "
+                         "linear: one 4096x4096 feature-major linear over 128 tokens")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -105,6 +108,12 @@ def main() -> int:
         return ntt_profile(spec, args.cts)
     if args.mode == "bootstrap":
         return bootstrap_bench(spec, args)
+    if args.mode == "linear":
+        spec.rotations = ()
+        client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+        print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
+              flush=True)
+        return 0
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
     ctx.synchronize()
@@ -217,12 +226,16 @@ def main() -> int:
             "limb_polys_per_launch": limb_polys,
         },
     }
-    if not args.no_bootstrap:
-        # the bootstrap workload on the same chain (32 ciphertexts at one limb)
+    if not args.no_bootstrap or not args.no_linear:
         for c in cts:
             c.release()
+    if not args.no_bootstrap:
+        # the bootstrap workload on the same chain (32 ciphertexts at one limb)
         result["bootstrap"] = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group,
                                                 args.budget, 1)
+    if not args.no_linear:
+        # the square linear of a decoder layer on the same chain
+        result["fm_linear"] = measure_fm_linear(client, ctx)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -287,6 +300,66 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int) 
         "precision_bits_mean": round(float(np.mean(bits)), 2),
         "setup_s": round(setup_s, 2),
         "first_group_s": round(first_s, 3),
+    }
+
+
+def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1) -> dict:
+    """One 4096 x 4096 feature-major linear (the square projection of a
+    Llama-3-8B decoder layer) over 128 tokens = 16 ciphertexts of 8 token
+    lanes, entering at `limbs` limbs (the 13-limb QKV budget): the
+    reference's production schedule (B = 64, 8 chunks of 8 giants), weights
+    N(0, 0.02), activations N(0, 1), seed 0.  Timed from the inputs to the
+    rescaled outputs, baby rotations included."""
+    from feature_major import (FeatureMajorPrefillLayout, LinearOperator, LinearWeight,
+                               linear_rotations)
+
+    D, lanes = 4096, ctx.max_slots // 4096
+    t0 = time.perf_counter()
+    ctx.generate_rotation_keys(linear_rotations(dimension=D, token_lanes=lanes))
+    ctx.synchronize()
+    keygen_s = time.perf_counter() - t0
+    lay = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=D, slots=ctx.max_slots)
+    rng = np.random.default_rng(0)
+    W = rng.normal(0.0, 0.02, (D, D))
+    X = rng.normal(0.0, 1.0, (lay.seq_len, D))
+    packed = lay.pack(X)
+    cts = [client.encrypt(packed[i], cur_limbs=limbs, enc_id=200000 + i)
+           for i in range(lay.cipher_count)]
+    weight = LinearWeight(W, context=ctx)
+    op = LinearOperator(context=ctx, token_lanes=lanes)
+    for _ in range(max(1, warmup)):
+        outs, _ = op.apply(cts, weight)
+        for o in outs:
+            o.release()
+        op.clear_baby_cache()
+    ctx.synchronize()
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    outs, profile = op.apply(cts, weight)
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    plan = op.plan(D)
+    per_ct = (len(plan.baby_offsets) - 1 + sum(c.giant_count - 1 for c in plan.chunks)
+              + sum(1 for c in plan.chunks if c.giant_base))
+    got = lay.unpack(np.stack([client.decrypt(o) for o in outs]))
+    err = float(np.abs(got - X @ W.T).max())
+    for o in outs:
+        o.release()
+    op.close()
+    weight.close()
+    return {
+        "seconds": round(wall, 4),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 4),
+        "workload": f"4096x4096 feature-major linear, 128 tokens in {len(cts)} ciphertexts of "
+                    f"{lanes} lanes at {limbs} limbs; B={plan.baby_steps}, "
+                    f"{len(plan.chunks)} chunks of {plan.chunk_giants} giants",
+        "keyswitches": per_ct * len(cts),
+        "pt_ct_products": D * len(cts),
+        "max_abs_err_vs_fp64": err,
+        "stages_s": {k: round(v, 4) for k, v in profile.items()},
+        "rotation_keygen_s": round(keygen_s, 2),
     }
 
 

@@ -1800,8 +1800,10 @@ int ckks_hoisted_mac_sum_many(ckks_context *c, const ckks_ct *const *babies, int
                               int giant_count, ckks_ct **out) {
   API_BEGIN
   require(c && babies && pts && out, "null argument");
-  require(n >= 1 && n <= 4096 && B >= 1 && B <= 4096, "ciphertext and baby counts in [1, 4096]");
+  require(n >= 1 && B >= 1, "ciphertext and baby counts must be positive");
   require(giant_count >= 1, "giant_count must be positive");
+  require(((size_t)n + std::min(kTabGroups, giant_count)) * B <= 8192,
+          "(ciphertexts + min(giants, 8)) x babies must be at most 8192 (split the batch)");
   for (int i = 0; i < n; i++) out[i] = nullptr;
   const int limbs = babies[0]->limbs;
   for (int j = 0; j < n * B; j++) {

@@ -1833,16 +1833,55 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // Each thread walks the babies of kTabCts ciphertexts at a time with the
 // groups' plaintext words in registers: a baby word is read once per pass, a
 // plaintext word (from L2) once per kTabCts ciphertexts.
-// grid (N / 256, limbs, 2)
+// FP (limbs whose prime is below 2^45): each product is the exact fp64
+// residue of fp_mulmod (|r| < 1.5 q) and the B-term sums stay exact integers
+// below 2^53, reduced once at the end, so the words equal the 64-bit path's.
+// grid (N / 256, limb_count, 2), limbs from l_begin
+template <bool FP>
 __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict__ bab, int n,
                                                    const u64 *const *__restrict__ pts, int B,
                                                    int G, u64 *__restrict__ out, int limbs,
-                                                   int logN, const ModQ *__restrict__ mods) {
+                                                   int l_begin, int logN,
+                                                   const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = blockIdx.y, comp = blockIdx.z;
+  const int l = l_begin + blockIdx.y, comp = blockIdx.z;
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
+  if constexpr (FP) {
+    constexpr int IC = kTabCtsFp;
+    const double q = (double)M.q, qinv = 1.0 / q;
+    for (int i0 = 0; i0 < n; i0 += IC) {
+      double acc[kTabGroups][IC];
+#pragma unroll
+      for (int g = 0; g < kTabGroups; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++) acc[g][c] = 0.0;
+      for (int b = 0; b < B; b++) {
+        double x[IC];
+#pragma unroll
+        for (int c = 0; c < IC; c++)
+          x[c] = i0 + c < n ? (double)bab[(size_t)(i0 + c) * B + b][off] : 0.0;
+#pragma unroll
+        for (int g = 0; g < kTabGroups; g++) {
+          if (g < G) {
+            const double w = (double)pts[(size_t)g * B + b][poff];
+            const double wq = __dmul_rn(w, qinv);
+#pragma unroll
+            for (int c = 0; c < IC; c++)
+              acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < kTabGroups; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++)
+          if (g < G && i0 + c < n)
+            out[((size_t)g * n + i0 + c) * CP + off] = fp_canon(acc[g][c], qinv, q);
+    }
+    return;
+  }
   for (int i0 = 0; i0 < n; i0 += kTabCts) {
     u64 acc[kTabGroups][kTabCts], hi[kTabGroups][kTabCts], lo[kTabGroups][kTabCts];
 #pragma unroll
@@ -1883,10 +1922,22 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
                       int G, u64 *out, int limbs) {
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
-  dim3 grid(c->N / TPB, limbs, 2);
-  hipLaunchKernelGGL(k_mac_table, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs,
-                     c->logN, c->d_mods);
-  LAUNCH_CHECK();
+  // fp64 sums stay exact for up to 2^52 / (1.5 q) terms: B <= 64 at q < 2^45
+  int start = 0;
+  while (start < limbs) {
+    const bool fp = c->prime_fp[start] != 0 && B <= 64;
+    int stop = start + 1;
+    while (stop < limbs && (c->prime_fp[stop] != 0 && B <= 64) == fp) stop++;
+    dim3 grid(c->N / TPB, stop - start, 2);
+    if (fp)
+      hipLaunchKernelGGL(k_mac_table<true>, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out,
+                         limbs, start, c->logN, c->d_mods);
+    else
+      hipLaunchKernelGGL(k_mac_table<false>, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G,
+                         out, limbs, start, c->logN, c->d_mods);
+    LAUNCH_CHECK();
+    start = stop;
+  }
 }
 
 // Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0

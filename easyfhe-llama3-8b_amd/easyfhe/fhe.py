@@ -882,12 +882,18 @@ def hoisted_mac_sum_many(baby_rotations: Sequence[Sequence[Ciphertext]], plainte
     pts = plaintexts if isinstance(plaintexts, (list, tuple)) else [plaintexts]
     if len(pts) < B * int(giant_count):
         raise ValueError(f"need {B * int(giant_count)} plaintexts, got {len(pts)}")
-    flat = [b.handle for bs in sets for b in bs]
-    outs = (ctypes.c_void_p * len(sets))()
-    check(lib.ckks_hoisted_mac_sum_many(ctx.handle, ptr_array(flat), len(sets), B,
-                                        ptr_array([p.handle for p in pts[: B * int(giant_count)]]),
-                                        int(giant_offset), int(giant_count), outs))
-    return [Ciphertext(ctx, outs[i]) for i in range(len(sets))]
+    used = ptr_array([p.handle for p in pts[: B * int(giant_count)]])
+    per = max(1, 8192 // B - min(8, int(giant_count)))  # the kernel's pointer-table bound
+    results: list = []
+    for i0 in range(0, len(sets), per):
+        part = sets[i0: i0 + per]
+        outs = (ctypes.c_void_p * len(part))()
+        check(lib.ckks_hoisted_mac_sum_many(ctx.handle, ptr_array([b.handle for bs in part
+                                                                   for b in bs]),
+                                            len(part), B, used, int(giant_offset),
+                                            int(giant_count), outs))
+        results.extend(Ciphertext(ctx, outs[i]) for i in range(len(part)))
+    return results
 
 
 # ---------------------------------------------------------------------------

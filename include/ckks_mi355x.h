@@ -184,7 +184,8 @@ int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
  * of one chunk): baby b of ciphertext i at babies[i * B + b], plaintexts
  * pts[g * B + b]; out[i] = Horner over the giant key of sum_b pt (.) baby,
  * unrescaled.  Each baby word is read once per pass of up to 8 giant groups
- * and each plaintext word once per pass for all n (L2 re-reads aside). */
+ * and each plaintext word once per pass for all n (L2 re-reads aside).
+ * Requires (n + min(giant_count, 8)) * B <= 8192. */
 int ckks_hoisted_mac_sum_many(ckks_context *ctx, const ckks_ct *const *babies, int n, int B,
                               const ckks_ct *const *pts, int64_t giant_rotation,
                               int giant_count, ckks_ct **out);
