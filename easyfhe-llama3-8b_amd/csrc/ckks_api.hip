@@ -1742,6 +1742,61 @@ int ckks_hoisted_rotate(ckks_context *c, const ckks_ct *a, const int64_t *rotati
   API_END
 }
 
+int ckks_hoisted_rotate_many(ckks_context *c, const ckks_ct *const *a, int m,
+                             const int64_t *rotations, int n, ckks_ct **out) {
+  API_BEGIN
+  require(a && out && rotations && m >= 1 && n >= 1, "null argument");
+  for (int j = 0; j < m * n; j++) out[j] = nullptr;
+  const int limbs = a[0]->limbs;
+  for (int i = 0; i < m; i++) {
+    check_ct(c, a[i], "hoisted_rotate_many");
+    require(a[i]->polys == 2 && !a[i]->is_ext && a[i]->limbs == limbs,
+            "hoisted rotation expects degree-1 Q-basis ciphertexts at one level");
+  }
+  const size_t N = c->N, P = (size_t)limbs * N;
+  std::vector<u64> gs(n);
+  for (int r = 0; r < n; r++) {
+    gs[r] = galois_of(c, rotations[r]);
+    if (gs[r] != 1) get_key(c, gs[r]);
+  }
+  std::vector<ckks_ct *> o((size_t)m * n);
+  for (int i = 0; i < m; i++)
+    for (int r = 0; r < n; r++)
+      o[(size_t)i * n + r] = new_ct(c, 2, limbs, 0, a[i]->slots, a[i]->scale, a[i]->scale_degree);
+  const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+  for (int i0 = 0; i0 < m; i0 += kMaxBatch) {
+    const int mb = std::min(kMaxBatch, m - i0);
+    Scratch s(c);
+    u64 *ext = nullptr;
+    for (int r = 0; r < n; r++) {
+      if (gs[r] == 1) {
+        for (int i = i0; i < i0 + mb; i++)
+          HIPCHECK(hipMemcpyAsync(o[(size_t)i * n + r]->d, a[i]->d, a[i]->bytes,
+                                  hipMemcpyDeviceToDevice, c->stream));
+        continue;
+      }
+      if (!ext) {
+        // one ModUp per ciphertext, shared by every rotation
+        ext = s.get((size_t)mb * digits * E * N);
+        std::vector<const u64 *> d(mb);
+        for (int i = 0; i < mb; i++) d[i] = a[i0 + i]->d + P;
+        ks_modup(c, limbs, mb, d.data(), ext, s);
+      }
+      // one rotation for the whole batch: its key is read once
+      const DeviceKey &key = get_key(c, gs[r]);
+      std::vector<KsJob> jobs(mb);
+      for (int i = 0; i < mb; i++) {
+        ckks_ct *d = o[(size_t)(i0 + i) * n + r];
+        jobs[i] = KsJob{i, &key, gs[r], a[i0 + i]->d, nullptr, d->d, d->d + P};
+      }
+      Scratch s2(c);
+      ks_finish(c, limbs, ext, mb, jobs, s2);
+    }
+  }
+  for (size_t j = 0; j < o.size(); j++) out[j] = o[j];
+  API_END
+}
+
 int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
                          const ckks_ct *const *pts, int64_t giant_rotation, int giant_count,
                          ckks_ct **out) {

@@ -113,6 +113,7 @@ SIGNATURES = {
     "ckks_hoisted_mac_sum": (I, [VP, VPP, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_hoisted_mac_sum_ext": (I, [VP, VP, I64P, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_hoisted_mac_sum_many": (I, [VP, VPP, I, I, VPP, ctypes.c_int64, I, VPP]),
+    "ckks_hoisted_rotate_many": (I, [VP, VPP, I, I64P, I, VPP]),
     "ckks_hoisted_rotate_ext": (I, [VP, VP, I64P, I, VPP]),
     "ckks_hoisted_mac_sum_ext_many": (I, [VP, VPP, I, I64P, I, VPP, ctypes.c_int64, I, VPP]),
     "ckks_rescale_many": (I, [VP, VPP, I, VPP]),

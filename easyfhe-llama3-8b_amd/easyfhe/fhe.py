@@ -819,6 +819,48 @@ def prepare_hoisted_baby_rotations(ct, baby_offsets, context=None, strategy: str
     return tuple(result)
 
 
+def prepare_hoisted_baby_rotations_many(cts: Sequence[Ciphertext], baby_offsets, context=None,
+                                        baby_anchor_step: int = -1) -> list:
+    """prepare_hoisted_baby_rotations for several same-level ciphertexts: one
+    batched ModUp, each baby key read once for the batch; returns one tuple of
+    babies per ciphertext (same words as the single-ciphertext form)."""
+    cts = list(cts)
+    if not cts:
+        return []
+    ctx = _ctx(cts[0], context)
+    offsets = [int(o) for o in baby_offsets]
+    B = len(offsets)
+
+    def hoisted(bases, offs):
+        arr = np.asarray(offs, dtype=np.int64)
+        outs = (ctypes.c_void_p * (len(bases) * len(offs)))()
+        check(lib.ckks_hoisted_rotate_many(ctx.handle, ptr_array([c.handle for c in bases]),
+                                           len(bases), arr.ctypes.data_as(_native.I64P),
+                                           len(offs), outs))
+        return [[Ciphertext(ctx, outs[i * len(offs) + r]) for r in range(len(offs))]
+                for i in range(len(bases))]
+
+    anchor = int(baby_anchor_step)
+    if anchor < 2 or anchor >= B:
+        return [tuple(x) for x in hoisted(cts, offsets)]
+    result: list = [[] for _ in cts]
+    bases = cts
+    for start in range(0, B, anchor):
+        block = offsets[start: start + anchor]
+        if start:
+            nxt = homo_rotate_many(bases, offsets[start] - offsets[start - anchor], ctx)
+            if bases is not cts:
+                for b in bases:
+                    b.release()
+            bases = nxt
+        for i, part in enumerate(hoisted(bases, [o - offsets[start] for o in block])):
+            result[i].extend(part)
+    if bases is not cts:
+        for b in bases:
+            b.release()
+    return [tuple(r) for r in result]
+
+
 def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count: int,
                     context=None, strategy: str = "normal", baby_anchor_step: int = -1,
                     baby_rotations=None):

@@ -10,9 +10,9 @@ is aligned by one rotation of ``giant_base * B * lanes``, and the chunk sums
 are added before one rescale.
 
 Execution on this backend:
-* the baby rotations of every input come from one hoisted ModUp per input
-  and are cached by the operator across chunks (and across weights applied
-  to the same input);
+* the baby rotations of all inputs come from one batched hoisted call (one
+  ModUp per input, each baby key read once for the batch) and are cached by
+  the operator across chunks (and across weights applied to the same input);
 * a chunk's plaintexts are packed and encoded on the device straight from
   the resident weight (``easyfhe.packing``), once for all inputs;
 * the chunk's MAC and its giant Horner chain run for all inputs at once
@@ -239,22 +239,37 @@ class LinearOperator:
     def _key(self, ct, plan: LinearPlan):
         return (id(ct), plan.cache_key + (int(plan.baby_anchor_step),))
 
-    def _babies_for(self, ct, plan: LinearPlan):
-        key = self._key(ct, plan)
-        limbs = int(ct.state.cur_limbs)
-        entry = self._babies.get(key)
-        if entry is not None and entry[0] is ct and entry[1] == limbs:
-            self._hits += 1
-            return entry[2]
-        if entry is not None:
-            _release(entry[2])
-        self._misses += 1
-        babies = fhe.prepare_hoisted_baby_rotations(
-            ct, plan.baby_offsets, self.context, strategy="normal",
-            baby_anchor_step=int(plan.baby_anchor_step))
-        if self.config.reuse_baby_rotations:
-            self._babies[key] = (ct, limbs, babies)
-        return babies
+    def _ensure_babies(self, inputs, plan: LinearPlan) -> list:
+        """The babies of every input: cached ones reused, the missing ones
+        computed in one batched call (one key read per baby rotation for the
+        batch) and cached when the config reuses them."""
+        found, missing = [], []
+        for ct in inputs:
+            entry = self._babies.get(self._key(ct, plan))
+            if entry is not None and entry[0] is ct and entry[1] == int(ct.state.cur_limbs):
+                self._hits += 1
+                found.append(entry[2])
+            else:
+                found.append(None)
+                missing.append(ct)
+        if missing:
+            self._misses += len(missing)
+            made = fhe.prepare_hoisted_baby_rotations_many(
+                missing, plan.baby_offsets, self.context,
+                baby_anchor_step=int(plan.baby_anchor_step))
+            it = iter(made)
+            for n, ct in enumerate(inputs):
+                if found[n] is not None:
+                    continue
+                babies = next(it)
+                found[n] = babies
+                if self.config.reuse_baby_rotations:
+                    key = self._key(ct, plan)
+                    old = self._babies.get(key)
+                    if old is not None:
+                        _release(old[2])
+                    self._babies[key] = (ct, int(ct.state.cur_limbs), babies)
+        return found
 
     def clear_baby_cache(self) -> None:
         for entry in self._babies.values():
@@ -274,8 +289,7 @@ class LinearOperator:
         if len({int(c.state.cur_limbs) for c in inputs}) > 1:
             raise ValueError("linear inputs must enter at one common level.")
         start = time.perf_counter()
-        for ct in inputs:
-            self._babies_for(ct, plan)
+        self._ensure_babies(inputs, plan)
         self.context.synchronize()
         return {"baby_precompute": time.perf_counter() - start}
 
@@ -300,7 +314,7 @@ class LinearOperator:
         ext = str(self.config.hoist_strategy).lower() != "normal"
         sync = ctx.synchronize
         t0 = time.perf_counter()
-        babies = None if ext else [self._babies_for(ct, plan) for ct in inputs]
+        babies = None if ext else self._ensure_babies(inputs, plan)
         sync()
         stage["baby_precompute"] = time.perf_counter() - t0
         acc: list = []

@@ -179,6 +179,12 @@ int ckks_hoisted_mac_sum(ckks_context *ctx, const ckks_ct *const *babies, int B,
                          const ckks_ct *const *pts, int64_t giant_rotation,
                          int giant_count, ckks_ct **out);
 
+/* fhe.prepare_hoisted_baby_rotations for m ciphertexts at one level (every
+ * input of a linear, reference operators/linear/operator.py:100-117): one
+ * batched ModUp, then each rotation's key is read once for all m;
+ * out[i * n + r] = rot_{rotations[r]}(a[i]). */
+int ckks_hoisted_rotate_many(ckks_context *ctx, const ckks_ct *const *a, int m,
+                             const int64_t *rotations, int n, ckks_ct **out);
 /* fhe.hoisted_mac_sum with precomputed babies for n ciphertexts sharing the
  * plaintexts (reference operators/linear/operator.py:320-330 for every input
  * of one chunk): baby b of ciphertext i at babies[i * B + b], plaintexts

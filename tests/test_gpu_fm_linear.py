@@ -19,11 +19,11 @@ pytestmark = pytest.mark.gpu
 D, LANES = 128, 32
 
 
-def _setup(cfg):
+def _setup(cfg, extra=()):
     from feature_major import FeatureMajorPrefillLayout, linear_rotations
 
     rots = linear_rotations(dimension=D, token_lanes=LANES, operator_config=cfg)
-    client, ctx = device_context("matvec", rotations=rots)
+    client, ctx = device_context("matvec", rotations=tuple(sorted(set(rots) | set(extra))))
     lay = FeatureMajorPrefillLayout(seq_len=3 * LANES, hidden_dim=D, slots=ctx.max_slots)
     rng = np.random.default_rng(0)
     W = rng.uniform(-1, 1, (D, D))
@@ -81,3 +81,22 @@ def test_fm_linear_extended_schedule():
         outs, _ = op.project(cts, W)
     got = lay.unpack(np.stack([client.decrypt(o) for o in outs]))
     assert np.abs(got - X @ W.T).max() < 1e-5
+
+
+def test_batched_babies_match_single():
+    """prepare_hoisted_baby_rotations_many (one ModUp per input, one key read
+    per rotation for the batch) = the single-ciphertext form, with and
+    without anchored blocks."""
+    from easyfhe import fhe
+    from feature_major import LinearOperatorConfig
+
+    cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=4, max_plaintext_rows=32)
+    offs = [LANES * b for b in range(16)]
+    client, ctx, lay, W, X, cts = _setup(cfg, extra=offs[1:])
+    for anchor in (-1, 4):
+        many = fhe.prepare_hoisted_baby_rotations_many(cts, offs, ctx, baby_anchor_step=anchor)
+        for ct, got in zip(cts, many):
+            want = fhe.prepare_hoisted_baby_rotations(ct, offs, ctx, baby_anchor_step=anchor)
+            assert len(got) == len(want) == 16
+            for g, w in zip(got, want):
+                assert np.array_equal(g.download(), w.download())
