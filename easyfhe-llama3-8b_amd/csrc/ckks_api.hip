@@ -698,6 +698,9 @@ static void free_context(ckks_context *c) {
   (void)hipFree(c->d_ninv);
   (void)hipFree(c->d_pmod);
   (void)hipFree(c->d_secret);
+  (void)hipFree(c->d_tw_fp);
+  (void)hipFree(c->d_itw_fp);
+  (void)hipFree(c->d_ninv_fp);
   c->pool.trim();
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
