@@ -443,8 +443,48 @@ def eval_chebyshev_series_cipher(input_cipher, coefficients, *, lower_bound: flo
     return evaluate(ops, y, coeffs).ct
 
 
+def eval_chebyshev_series_many(input_ciphers, coefficients, *, lower_bound: float,
+                               upper_bound: float, crypto_context,
+                               input_is_chebyshev_mapped: bool = False) -> list:
+    """eval_chebyshev_series_cipher over a group of ciphertexts that share
+    their limb count and scale: every product of the evaluation is one batched
+    relinearise + rescale for the group (BatchLadderOps), so the relinearisation
+    key is read once per product level.  Same words as evaluating each
+    ciphertext alone."""
+    ctx = _native_context(crypto_context)
+    cts = list(input_ciphers)
+    if not cts:
+        return []
+    coeffs = np.asarray(coefficients, dtype=np.float64)
+    if chebyshev_degree(coeffs) < 1:
+        raise ValueError("degree must be >= 1")
+    limbs = int(cts[0].state.cur_limbs)
+    scale = float(cts[0].state.scaling_factor)
+    for ct in cts:
+        if int(ct.state.cur_limbs) != limbs:
+            raise ValueError("a polynomial group must share its limb count")
+        if abs(float(ct.state.scaling_factor) / scale - 1.0) > 2.0 ** -30:
+            raise ValueError("a polynomial group must share its scale")
+    primes = [int(q) for q in ctx.primes()[: ctx.L]]
+    depth = chebyshev_depth(coeffs)
+    a, b = float(lower_bound), float(upper_bound)
+    if input_is_chebyshev_mapped:
+        lad = Ladder(primes, limbs, scale, 1, depth)
+        ops = BatchLadderOps(ctx, lad)
+        y = LCt(cts, 0)
+    else:
+        if limbs < depth + 2:
+            raise ValueError(f"need {depth + 2} limbs, ciphertexts have {limbs}")
+        top = limbs - 1
+        lad = Ladder(primes, top, float(primes[top - 1]), 1, depth)
+        ops = BatchLadderOps(ctx, lad)
+        y = ops.combine([(cts, 2.0 / (b - a))], -(a + b) / (b - a), 0)
+    return list(evaluate(ops, y, coeffs).ct)
+
+
 __all__ = [
     "BatchLadderOps", "Ladder", "LadderOps", "LCt", "chebyshev_coefficients", "chebyshev_degree",
-    "chebyshev_depth", "divide_by_t", "eval_chebyshev_series_cipher", "evaluate",
+    "chebyshev_depth", "divide_by_t", "eval_chebyshev_series_cipher", "eval_chebyshev_series_many",
+    "evaluate",
     "evaluate_direct", "plan_baby", "series_depth",
 ]

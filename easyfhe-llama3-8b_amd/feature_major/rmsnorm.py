@@ -1,0 +1,249 @@
+"""Feature-major RMSNorm and residual additions on ciphertexts (reference
+llama3fhe/operators/norm/rmsnorm.py:120-704).
+
+RMSNorm of 128 tokens held as 16 feature-major ciphertexts (slot
+``f * lanes + t``) evaluates ``x * p(mean_f x^2)`` with a fitted inverse
+square root series p, evaluated once for all tokens:
+
+1. ``x_c^2`` (one batched multiply-relinearise-rescale for the 16 inputs);
+2. a rotate-and-add tree over the feature orbit (strides ``lanes * 2^b``,
+   b < log2 D): every slot then holds its token's sum of squares;
+3. "slim pack": ciphertext c keeps only feature row c (a mask that also
+   carries the map onto [-1, 1] and 1/D), and the 16 rows are summed into one
+   ciphertext holding all 128 token values;
+4. the series on that single ciphertext (plus the map's offset, level-free);
+5. each row c is masked out again and broadcast back over the feature orbit
+   by the same tree with negative strides;
+6. one product with the input (which, if a gamma vector is given, was first
+   multiplied by it on its own spare levels).
+
+Depth: square, pack mask, the series, extract mask, product.  An input that
+arrives as ``s * x`` (the doubled values of a complex-paired refresh) is
+normalised to ``x`` through the masks at no level (``input_value_scale``).
+
+Every step over the 16 ciphertexts is batched: a tree step is one key switch
+call whose key is read once for the batch.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from easyfhe import fhe
+from easyfhe.chebyshev import chebyshev_depth, eval_chebyshev_series_cipher
+
+from .approx import chebyshev_map
+from .layout import FeatureMajorPrefillLayout
+
+
+def _ctx(context):
+    return getattr(context, "context", context)
+
+
+def _release(values) -> None:
+    for v in values or ():
+        if v is not None:
+            v.release()
+
+
+def is_rmsn_weight(weight, *, atol: float = 0.0) -> bool:
+    """True when the gamma vector is absent (QuaRot folds it into the next
+    linear and stores zeros or one scalar, approx/rmsnorm.py:85-97)."""
+    w = np.asarray(weight, dtype=np.float64).reshape(-1)
+    if w.size <= 1:
+        return w.size == 0 or abs(float(w[0])) <= atol
+    return float(np.max(np.abs(w))) <= atol
+
+
+def rmsnorm_rotations(layout: FeatureMajorPrefillLayout) -> tuple[int, ...]:
+    """Keys of the reduction and broadcast trees (rmsnorm.py:120-131)."""
+    stride = int(layout.tokens_per_cipher)
+    offs = {stride * (1 << b) for b in range(int(math.log2(int(layout.hidden_dim))))}
+    return tuple(sorted(offs | {-o for o in offs}))
+
+
+def rmsnorm_depth(coeffs: dict, *, apply_gamma: bool = False) -> int:
+    """Levels from the input to the output (gamma rides on the input's spare
+    levels, so it does not add to this count)."""
+    _ = apply_gamma
+    return 4 + int(chebyshev_depth(coeffs["coefficients"]))
+
+
+@dataclass
+class RMSNormResult:
+    ciphers: tuple
+    wall_seconds: float
+    stage_seconds: dict = field(default_factory=dict)
+    output_limbs: int = 0
+
+    def release(self) -> None:
+        _release(self.ciphers)
+        self.ciphers = ()
+
+
+def _fold(cts, stride: int, steps: int, sign: int, ctx) -> list:
+    """Rotate-and-add over the feature orbit, all inputs per batched call."""
+    cur = list(cts)
+    owned = False
+    for b in range(steps):
+        rot = fhe.homo_rotate_many(cur, sign * stride * (1 << b), ctx)
+        nxt = [fhe.homo_add(c, r, ctx) for c, r in zip(cur, rot)]
+        _release(rot)
+        if owned:
+            _release(cur)
+        cur, owned = nxt, True
+    return cur
+
+
+def _row_masks(layout: FeatureMajorPrefillLayout, value: float) -> np.ndarray:
+    """[cipher_count, slots]: ``value`` on feature row c's active token slots."""
+    n, slots, lanes = int(layout.cipher_count), int(layout.slots), int(layout.tokens_per_cipher)
+    rows = np.zeros((n, slots), dtype=np.float64)
+    for c in range(n):
+        act = layout.active_tokens(c)
+        rows[c, c * lanes: c * lanes + act] = value
+    return rows
+
+
+def _mul_rows_rescale(cts, rows: np.ndarray, ctx) -> list:
+    """ct_i * encode(rows[i]) rescaled, every plaintext at the ciphertexts'
+    level and the level's scale."""
+    limbs = int(cts[0].state.cur_limbs)
+    pts = fhe.encode_rows(ctx, rows, limbs=limbs, scale=ctx.scale_at(limbs), slots=ctx.max_slots)
+    try:
+        prods = [fhe.homo_mul_pt(c, p, ctx) for c, p in zip(cts, pts)]
+    finally:
+        _release(pts)
+    try:
+        return fhe.rescale_many(prods, ctx)
+    finally:
+        _release(prods)
+
+
+def _align_all(cts, limbs: int, ctx) -> list:
+    out = []
+    for c in cts:
+        if int(c.state.cur_limbs) == limbs:
+            out.append(c.deep_copy())
+        else:
+            out.append(fhe.align_to(c, c.state.replace(cur_limbs=limbs, scaling_factor=None), ctx))
+    return out
+
+
+def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPrefillLayout,
+                crypto_context, input_value_scale: float = 1.0,
+                defer_output_scale: bool = False) -> RMSNormResult:
+    """``x * p(mean(x^2)) [* gamma]`` per token on feature-major ciphertexts
+    (rmsnorm.py:353-704).  Inputs are not consumed."""
+    ctx = _ctx(crypto_context)
+    xs = tuple(input_ciphers)
+    if len(xs) != int(layout.cipher_count):
+        raise ValueError(f"feature-major RMSNorm expects {layout.cipher_count} input ciphers, "
+                         f"got {len(xs)}.")
+    if int(layout.cipher_count) > int(layout.hidden_dim):
+        raise ValueError("slim feature-major RMSNorm requires cipher_count <= hidden_dim.")
+    if int(layout.slots) != int(ctx.max_slots):
+        raise ValueError("feature-major RMSNorm requires layout.slots == context.max_slots.")
+    if len({int(c.state.cur_limbs) for c in xs}) != 1:
+        raise ValueError("RMSNorm inputs must share one level.")
+    s_in = float(input_value_scale)
+    if not math.isfinite(s_in) or s_in <= 0.0:
+        raise ValueError(f"input_value_scale must be finite and positive, got {s_in}.")
+    w = np.asarray(weight, dtype=np.float64).reshape(-1)
+    apply_gamma = not is_rmsn_weight(w) and not defer_output_scale
+    if apply_gamma and w.shape != (int(layout.hidden_dim),):
+        raise ValueError(f"RMSNorm gamma must have width {layout.hidden_dim}, got {w.shape}.")
+    coefficients = np.asarray(coeffs["coefficients"], dtype=np.float64)
+    alpha, beta = chebyshev_map(coeffs["fit_interval"])
+    depth = rmsnorm_depth(coeffs)
+    limbs_in = int(xs[0].state.cur_limbs)
+    if limbs_in < depth + 2:
+        raise ValueError(f"RMSNorm needs {depth + 2} limbs, inputs have {limbs_in}.")
+    D = int(layout.hidden_dim)
+    lanes = int(layout.tokens_per_cipher)
+    steps = int(math.log2(D))
+    sync = ctx.synchronize
+    stage: dict[str, float] = {}
+    t_start = time.perf_counter()
+    tmp: list = []
+    try:
+        t0 = time.perf_counter()
+        sq = fhe.homo_mul_relin_rescale_many(xs, xs, ctx)
+        red = _fold(sq, lanes, steps, +1, ctx)
+        _release(sq)
+        terms = _mul_rows_rescale(red, _row_masks(layout, alpha / (D * s_in * s_in)), ctx)
+        _release(red)
+        slim = terms[0]
+        for t in terms[1:]:
+            nxt = fhe.homo_add(slim, t, ctx)
+            slim.release()
+            slim = nxt
+        _release(terms[1:])
+        sync()
+        stage["mean_square_and_slim_pack"] = time.perf_counter() - t0
+
+        t0 = time.perf_counter()
+        limbs = int(slim.state.cur_limbs)
+        off = fhe.encode_scalar(beta, limbs, scaling_factor=float(slim.state.scaling_factor),
+                                context=ctx)
+        mapped = fhe.homo_add_scalar(slim, off, ctx)
+        slim.release()
+        poly = eval_chebyshev_series_cipher(mapped, coefficients, lower_bound=-1.0,
+                                            upper_bound=1.0, crypto_context=ctx,
+                                            input_is_chebyshev_mapped=True)
+        mapped.release()
+        sync()
+        stage["rsqrt_polynomial"] = time.perf_counter() - t0
+
+        t0 = time.perf_counter()
+        n = len(xs)
+        sel = _mul_rows_rescale([poly] * n, _row_masks(layout, 1.0 / s_in), ctx)
+        poly.release()
+        bcast = _fold(sel, lanes, steps, -1, ctx)
+        _release(sel)
+        tmp = bcast
+        if apply_gamma:
+            gamma_rows = np.repeat(w, lanes)[None, :].repeat(n, axis=0)
+            lifted = _mul_rows_rescale(list(xs), gamma_rows, ctx)
+            tmp = bcast + lifted
+            xa = _align_all(lifted, int(bcast[0].state.cur_limbs), ctx)
+        else:
+            xa = _align_all(xs, int(bcast[0].state.cur_limbs), ctx)
+        tmp = tmp + xa
+        out = fhe.homo_mul_relin_rescale_many(xa, bcast, ctx)
+        sync()
+        stage["scale_broadcast_and_output"] = time.perf_counter() - t0
+        return RMSNormResult(tuple(out), time.perf_counter() - t_start, stage,
+                             int(out[0].state.cur_limbs))
+    finally:
+        _release(tmp)
+
+
+def residual_add(left, right, *, crypto_context) -> tuple:
+    """Limb-wise sums of two feature-major streams at their common level
+    (rmsnorm.py:244-351); inputs are not consumed."""
+    ctx = _ctx(crypto_context)
+    a, b = tuple(left), tuple(right)
+    if len(a) != len(b):
+        raise ValueError("residual streams differ in length.")
+    out = []
+    for x, y in zip(a, b):
+        limbs = min(int(x.state.cur_limbs), int(y.state.cur_limbs))
+        xa = x if int(x.state.cur_limbs) == limbs else fhe.align_to(
+            x, x.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+        ya = y if int(y.state.cur_limbs) == limbs else fhe.align_to(
+            y, y.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+        out.append(fhe.homo_add(xa, ya, ctx))
+        if xa is not x:
+            xa.release()
+        if ya is not y:
+            ya.release()
+    return tuple(out)
+
+
+__all__ = ["RMSNormResult", "is_rmsn_weight", "residual_add", "rmsnorm_depth", "rmsnorm_fhe",
+           "rmsnorm_rotations"]

@@ -1,0 +1,79 @@
+"""fp64 plaintext model of the encrypted decoder-layer operators.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of decrypted
+values.  The product path never imports this module.
+
+Each function restates the mathematics of a reference numpy model that the
+reference compares its encrypted layer against:
+* ``eval_chebyshev_series_direct``: approx/chebyshev.py:136-163 (the series
+  ``c_0/2 + sum_i c_i T_i`` on [a, b], mapped affinely onto [-1, 1]);
+* ``rmsnorm_poly_numpy``: approx/rmsnorm.py:24-51 (``x * p(mean(x^2))`` with
+  the fitted inverse-square-root series p, no clamping in FHE mode);
+* ``silu_poly_mlp_numpy``: the MLP half of approx/layer.py:121-140
+  (``down @ (p_silu(gate @ x) * (up @ x))``);
+* ``fm_pack`` / ``fm_unpack``: the feature-major token-lane layout of
+  layouts/feature_major.py:74-92 (slot = feature * lanes + token % lanes,
+  ciphertext = token // lanes).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def eval_chebyshev_series_direct(x, coefficients, a: float, b: float) -> np.ndarray:
+    """Three-term recurrence T_{n+1} = 2 y T_n - T_{n-1} at y = (2x - a - b)/(b - a)."""
+    c = np.asarray(coefficients, dtype=np.float64)
+    y = (2.0 * np.asarray(x, dtype=np.float64) - (a + b)) / (b - a)
+    if c.size == 0:
+        return np.zeros_like(y)
+    acc = np.full_like(y, c[0] / 2.0)
+    if c.size == 1:
+        return acc
+    t_prev, t_cur = np.ones_like(y), y
+    acc = acc + c[1] * t_cur
+    for i in range(2, c.size):
+        t_prev, t_cur = t_cur, 2.0 * y * t_cur - t_prev
+        acc = acc + c[i] * t_cur
+    return acc
+
+
+def rmsnorm_poly_numpy(x, coefficients, fit_interval) -> np.ndarray:
+    """[tokens, hidden] -> x * p(mean(x^2)) per token."""
+    x = np.asarray(x, dtype=np.float64)
+    lo, hi = (float(v) for v in fit_interval)
+    var = np.mean(x * x, axis=-1, keepdims=True)
+    return x * eval_chebyshev_series_direct(var, coefficients, lo, hi)
+
+
+def silu_poly_mlp_numpy(x, gate_weight, up_weight, down_weight, coefficients,
+                        fit_interval) -> np.ndarray:
+    """[tokens, hidden] -> [tokens, hidden] SwiGLU with the fitted SiLU series."""
+    x = np.asarray(x, dtype=np.float64)
+    lo, hi = (float(v) for v in fit_interval)
+    gate = x @ np.asarray(gate_weight, dtype=np.float64).T
+    up = x @ np.asarray(up_weight, dtype=np.float64).T
+    act = eval_chebyshev_series_direct(gate, coefficients, lo, hi) * up
+    return act @ np.asarray(down_weight, dtype=np.float64).T
+
+
+def fm_pack(rows, slots: int) -> np.ndarray:
+    """[tokens, dim] -> [ceil(tokens / lanes), slots], lanes = slots // dim."""
+    rows = np.asarray(rows)
+    tokens, dim = rows.shape
+    lanes = slots // dim
+    count = -(-tokens // lanes)
+    out = np.zeros((count, slots), dtype=rows.dtype)
+    for t in range(tokens):
+        out[t // lanes, np.arange(dim) * lanes + t % lanes] = rows[t]
+    return out
+
+
+def fm_unpack(packed, tokens: int, dim: int) -> np.ndarray:
+    packed = np.asarray(packed)
+    slots = packed.shape[1]
+    lanes = slots // dim
+    out = np.zeros((tokens, dim), dtype=packed.dtype)
+    for t in range(tokens):
+        out[t] = packed[t // lanes, np.arange(dim) * lanes + t % lanes]
+    return out

@@ -1,0 +1,112 @@
+"""Feature-major decoder-layer operators on the GPU, decrypted and compared
+with the fp64 layer model (oracle/layer_numpy.py):
+
+* complex pairing and the conjugation split (operators/linear/complex.py);
+* RMSNorm with the slim-packed single series evaluation
+  (operators/norm/rmsnorm.py), with and without gamma, with a doubled input
+  (the complex-paired refresh contract), and at the full Llama shape
+  (128 tokens x 4096 features at N = 2^16).
+
+Tolerances are stated per test: they bound the CKKS error (scale 2^40) and
+the drift of the fixed-scale residual bookkeeping, not the series fits,
+which the model evaluates identically.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import layer_numpy as LN
+from conftest import PARAMS, device_context
+
+pytestmark = pytest.mark.gpu
+
+FM_SMALL = dict(log_n=13, depth=13, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+def _stream(client, ctx, x, enc0=700):
+    from feature_major import FeatureMajorPrefillLayout
+
+    lay = FeatureMajorPrefillLayout(seq_len=x.shape[0], hidden_dim=x.shape[1],
+                                    slots=ctx.max_slots)
+    packed = lay.pack(x)
+    cts = [client.encrypt(packed[i], enc_id=enc0 + i) for i in range(lay.cipher_count)]
+    return lay, cts
+
+
+def _decrypt_stream(client, lay, cts):
+    return lay.unpack(np.stack([client.decrypt(c) for c in cts]))
+
+
+def test_complex_pair_and_split_roundtrip():
+    from feature_major.complex import pair_real_ciphers, split_complex_ciphers_twice
+
+    client, ctx = device_context(FM_SMALL, rotations=(2 * 8192 - 1,), relin=False)
+    rng = np.random.default_rng(0)
+    slots = ctx.max_slots
+    xs = [rng.uniform(-1, 1, slots) for _ in range(4)]
+    cts = [client.encrypt(x, enc_id=10 + i) for i, x in enumerate(xs)]
+    pairs = pair_real_ciphers(cts, crypto_context=ctx)
+    assert len(pairs) == 2
+    z = client.decrypt_complex(pairs[1])
+    assert np.max(np.abs(z - (xs[2] + 1j * xs[3]))) < 1e-7
+    split = split_complex_ciphers_twice(pairs, crypto_context=ctx)
+    for x, s in zip(xs, split):
+        assert np.max(np.abs(client.decrypt(s) - 2 * x)) < 1e-6
+    halved = split_complex_ciphers_twice(pairs, crypto_context=ctx, halve=True)
+    for x, s in zip(xs, halved):
+        assert int(s.state.cur_limbs) == int(cts[0].state.cur_limbs)
+        assert np.max(np.abs(client.decrypt(s) - x)) < 1e-6
+    with pytest.raises(ValueError):
+        pair_real_ciphers(cts[:3], crypto_context=ctx)
+
+
+@pytest.mark.parametrize("gamma,scale_in", [(False, 1.0), (True, 1.0), (True, 2.0)])
+def test_rmsnorm_matches_poly_model(gamma, scale_in):
+    from feature_major.approx import rsqrt_entry
+    from feature_major.rmsnorm import rmsnorm_depth, rmsnorm_fhe, rmsnorm_rotations
+    from feature_major import FeatureMajorPrefillLayout
+
+    tokens, dim = 64, 512
+    lay0 = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=4096)
+    client, ctx = device_context(FM_SMALL, rotations=rmsnorm_rotations(lay0))
+    rng = np.random.default_rng(1)
+    x = rng.normal(size=(tokens, dim))
+    w = rng.normal(1.0, 0.1, dim) if gamma else np.zeros(1)
+    entry = rsqrt_entry(0.25, 4.0, 31)
+    lay, cts = _stream(client, ctx, scale_in * x)
+    res = rmsnorm_fhe(cts, w, coeffs=entry, layout=lay, crypto_context=ctx,
+                      input_value_scale=scale_in)
+    assert res.output_limbs == int(cts[0].state.cur_limbs) - rmsnorm_depth(entry)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    want = LN.rmsnorm_poly_numpy(x, entry["coefficients"], entry["fit_interval"])
+    if gamma:
+        want = want * w[None, :]
+    err = float(np.max(np.abs(got - want)))
+    assert err < 2e-4, err
+    assert set(res.stage_seconds) == {"mean_square_and_slim_pack", "rsqrt_polynomial",
+                                      "scale_broadcast_and_output"}
+
+
+def test_rmsnorm_full_llama_shape():
+    """128 tokens x 4096 features in 16 ciphertexts at N = 2^16 on the bench
+    chain (60-bit + 35 x 40-bit, dnum 3)."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry
+    from feature_major.rmsnorm import rmsnorm_fhe, rmsnorm_rotations
+
+    lay0 = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=4096, slots=32768)
+    client, ctx = device_context(PARAMS["keyswitch"], rotations=rmsnorm_rotations(lay0))
+    rng = np.random.default_rng(2)
+    x = rng.normal(size=(128, 4096))
+    entry = rsqrt_entry(0.25, 4.0, 31)
+    lay, cts = _stream(client, ctx, x)
+    cts = [c.deep_copy() for c in cts]
+    res = rmsnorm_fhe(cts, np.zeros(1), coeffs=entry, layout=lay, crypto_context=ctx)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    want = LN.rmsnorm_poly_numpy(x, entry["coefficients"], entry["fit_interval"])
+    err = float(np.max(np.abs(got - want)))
+    print(f"rmsnorm 128x4096: max err {err:.3g}, {res.wall_seconds:.3f} s, "
+          f"stages {res.stage_seconds}", flush=True)
+    assert err < 2e-4, err
