@@ -2,7 +2,7 @@
 
 Workload (one GPU): 64 ciphertexts at N = 2^16 (2^15 slots, values
 uniform[-1, 1] from seed 0), Q = one 60-bit + 35 40-bit primes, dnum 3 hybrid
-key switching with 12 60-bit special primes.  One step = rotations by
+key switching with 12 44-bit special primes.  One step = rotations by
 2^0 .. 2^14 of all 64 ciphertexts (chained, 15 x 64 key switches at 36 limbs),
 then HMult + relinearise + rescale at every level 36 -> 2 (34 x 64 key
 switches).  Inputs are resident in HBM before the timed region.
@@ -83,12 +83,15 @@ def main() -> int:
     ap.add_argument("--no-linear", action="store_true",
                     help="skip the feature-major linear measurement of the default run")
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
-    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear"],
+    ap.add_argument("--no-mlp", action="store_true",
+                    help="skip the RMSNorm + MLP block measurement of the default run")
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
                          "bootstrap: the full-slot bootstrap workload on the same chain; "
-                         "linear: one 4096x4096 feature-major linear over 128 tokens")
+                         "linear: one 4096x4096 feature-major linear over 128 tokens; "
+                         "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -112,6 +115,13 @@ def main() -> int:
         spec.rotations = ()
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
+              flush=True)
+        return 0
+    if args.mode == "mlp":
+        spec.rotations = ()
+        client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+        print(json.dumps({"fm_mlp_block": measure_fm_mlp_block(client, ctx,
+                                                               warmup=args.warmup)}),
               flush=True)
         return 0
     t0 = time.perf_counter()
@@ -226,7 +236,7 @@ def main() -> int:
             "limb_polys_per_launch": limb_polys,
         },
     }
-    if not args.no_bootstrap or not args.no_linear:
+    if not args.no_bootstrap or not args.no_linear or not args.no_mlp:
         for c in cts:
             c.release()
     if not args.no_bootstrap:
@@ -236,6 +246,9 @@ def main() -> int:
     if not args.no_linear:
         # the square linear of a decoder layer on the same chain
         result["fm_linear"] = measure_fm_linear(client, ctx)
+    if not args.no_mlp:
+        # the RMSNorm + MLP + residual half of a decoder layer on the same chain
+        result["fm_mlp_block"] = measure_fm_mlp_block(client, ctx)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -360,6 +373,94 @@ def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1) -> dict:
         "max_abs_err_vs_fp64": err,
         "stages_s": {k: round(v, 4) for k, v in profile.items()},
         "rotation_keygen_s": round(keygen_s, 2),
+    }
+
+
+def measure_fm_mlp_block(client, ctx, limbs: int = 20, warmup: int = 1) -> dict:
+    """The post-attention half of a Llama-3-8B decoder layer over 128 tokens
+    (16 feature-major ciphertexts of 8 lanes): RMSNorm (rsqrt series of
+    degree 31 on [0.25, 4]), the SwiGLU MLP (gate/up 14336 x 4096, down
+    4096 x 14336, four pages, SiLU series of degree 63 on [-12, 12]) and the
+    residual addition, entering at `limbs` limbs.  Weights N(0, 0.02),
+    residual stream N(0, 1), seed 0.  The error is against the same
+    composition evaluated in fp64 on the plaintexts."""
+    from easyfhe.chebyshev import evaluate_direct
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.mlp import FeatureMajorMLPLayout, MLPWeights, mlp_fhe, mlp_rotations
+    from feature_major.rmsnorm import residual_add, rmsnorm_fhe, rmsnorm_rotations
+
+    D, I = 4096, 14336
+    lay = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=D, slots=ctx.max_slots)
+    t0 = time.perf_counter()
+    ctx.generate_rotation_keys(sorted(set(rmsnorm_rotations(lay)) | set(mlp_rotations(lay))))
+    ctx.synchronize()
+    keygen_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    G = rng.normal(0.0, 0.02, (I, D))
+    U = rng.normal(0.0, 0.02, (I, D))
+    Dn = rng.normal(0.0, 0.02, (D, I))
+    X = rng.normal(0.0, 1.0, (lay.seq_len, D))
+    rs, silu = rsqrt_entry(0.25, 4.0, 31), silu_entry(-12.0, 12.0, 63)
+    packed = lay.pack(X)
+    cts = [client.encrypt(packed[i], cur_limbs=limbs, enc_id=300000 + i)
+           for i in range(lay.cipher_count)]
+    mlay = FeatureMajorMLPLayout(lay, I)
+    t0 = time.perf_counter()
+    weights = MLPWeights(G, U, Dn, silu=silu, layout=mlay, context=ctx)
+    ctx.synchronize()
+    upload_s = time.perf_counter() - t0
+
+    def run():
+        t = {}
+        s0 = time.perf_counter()
+        norm = rmsnorm_fhe(cts, np.zeros(1), coeffs=rs, layout=lay, crypto_context=ctx)
+        t["rmsnorm"] = time.perf_counter() - s0
+        s0 = time.perf_counter()
+        mlp = mlp_fhe(norm.ciphers, weights, silu=silu, crypto_context=ctx)
+        norm.release()
+        t["mlp"] = time.perf_counter() - s0
+        s0 = time.perf_counter()
+        out = residual_add(cts, mlp.ciphers, crypto_context=ctx)
+        ctx.synchronize()
+        t["residual"] = time.perf_counter() - s0
+        stages = dict(mlp.stage_seconds)
+        mlp.release()
+        return out, t, stages
+
+    for _ in range(max(1, warmup)):
+        out, _, _ = run()
+        for o in out:
+            o.release()
+    ctx.synchronize()
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    out, parts, stages = run()
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    got = lay.unpack(np.stack([client.decrypt(o) for o in out]))
+    limbs_out = int(out[0].state.cur_limbs)
+    for o in out:
+        o.release()
+    weights.close()
+    var = np.mean(X * X, axis=-1, keepdims=True)
+    xn = X * evaluate_direct(var, rs["coefficients"], *rs["fit_interval"])
+    g = xn @ G.T
+    want = X + (evaluate_direct(g, silu["coefficients"], *silu["fit_interval"])
+                * (xn @ U.T)) @ Dn.T
+    return {
+        "seconds": round(wall, 4),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 4),
+        "workload": "RMSNorm + SwiGLU MLP (4096 -> 14336 -> 4096, 4 pages) + residual, "
+                    f"128 tokens in {lay.cipher_count} ciphertexts of {lay.tokens_per_cipher} "
+                    f"lanes, {limbs} -> {limbs_out} limbs",
+        "parts_s": {k: round(v, 4) for k, v in parts.items()},
+        "mlp_stages_s": {k: round(v, 4) for k, v in stages.items()},
+        "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
+        "rotation_keygen_s": round(keygen_s, 2),
+        "weight_upload_s": round(upload_s, 2),
     }
 
 

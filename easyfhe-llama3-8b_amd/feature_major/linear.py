@@ -186,7 +186,8 @@ class LinearWeight:
         self.closed = False
 
     def plaintext(self, plan: LinearPlan, chunk: LinearChunk, *, limbs: int,
-                  operator_config: LinearOperatorConfig | None = None) -> list:
+                  operator_config: LinearOperatorConfig | None = None,
+                  scale: float | None = None) -> list:
         if self.closed:
             raise RuntimeError("linear weight is closed.")
         if int(plan.dimension) != self.dimension:
@@ -197,7 +198,8 @@ class LinearWeight:
         diag = packing.pack_token_lane_bsgs_weight_chunk(
             self._w, slots=ctx.max_slots, dimension=plan.dimension, token_lanes=plan.token_lanes,
             baby_steps=plan.baby_steps, giant_base=chunk.giant_base, giant_count=chunk.giant_count)
-        return diag.encode(ctx, limbs=int(limbs), scale=ctx.scale_at(int(limbs)),
+        return diag.encode(ctx, limbs=int(limbs),
+                           scale=float(scale) if scale else ctx.scale_at(int(limbs)),
                            is_ext=str(cfg.hoist_strategy).lower() != "normal")
 
     def close(self) -> None:
@@ -271,6 +273,12 @@ class LinearOperator:
                     self._babies[key] = (ct, int(ct.state.cur_limbs), babies)
         return found
 
+    def release_babies(self, inputs) -> None:
+        """Drop the cached babies of these inputs (every plan)."""
+        ids = {id(ct) for ct in inputs}
+        for key in [k for k, e in self._babies.items() if k[0] in ids and e[0] in inputs]:
+            _release(self._babies.pop(key)[2])
+
     def clear_baby_cache(self) -> None:
         for entry in self._babies.values():
             _release(entry[2])
@@ -294,9 +302,12 @@ class LinearOperator:
         return {"baby_precompute": time.perf_counter() - start}
 
     # -- application ---------------------------------------------------------
-    def apply(self, inputs, weight: LinearWeight):
+    def apply(self, inputs, weight: LinearWeight, *, output_scale: float | None = None):
         """``W x`` for every input ciphertext, rescaled once; returns the
-        outputs and a profile of seconds per stage."""
+        outputs and a profile of seconds per stage.  With ``output_scale`` the
+        plaintexts are encoded at ``output_scale * q / s_in`` (q the prime the
+        rescale drops), so the outputs land exactly on that scale: a
+        polynomial ladder that starts there keeps its scales at the primes."""
         if self.closed:
             raise RuntimeError("linear operator is closed.")
         inputs = tuple(inputs)
@@ -311,6 +322,12 @@ class LinearOperator:
             raise ValueError("linear inputs must enter at one common level.")
         limbs = levels.pop()
         ctx = self.context
+        pt_scale = None
+        if output_scale is not None:
+            s_in = float(inputs[0].state.scaling_factor)
+            if any(abs(float(c.state.scaling_factor) / s_in - 1.0) > 2.0 ** -30 for c in inputs):
+                raise ValueError("an exact output scale needs inputs of one scale.")
+            pt_scale = float(output_scale) * float(int(ctx.primes()[limbs - 1])) / s_in
         ext = str(self.config.hoist_strategy).lower() != "normal"
         sync = ctx.synchronize
         t0 = time.perf_counter()
@@ -321,7 +338,8 @@ class LinearOperator:
         try:
             for chunk in plan.chunks:
                 t0 = time.perf_counter()
-                pts = weight.plaintext(plan, chunk, limbs=limbs, operator_config=self.config)
+                pts = weight.plaintext(plan, chunk, limbs=limbs, operator_config=self.config,
+                                       scale=pt_scale)
                 sync()
                 stage["pack_encode"] += time.perf_counter() - t0
                 t0 = time.perf_counter()

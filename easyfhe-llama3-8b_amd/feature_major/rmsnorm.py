@@ -109,11 +109,16 @@ def _row_masks(layout: FeatureMajorPrefillLayout, value: float) -> np.ndarray:
     return rows
 
 
-def _mul_rows_rescale(cts, rows: np.ndarray, ctx) -> list:
+def _mul_rows_rescale(cts, rows: np.ndarray, ctx, out_scale: float | None = None) -> list:
     """ct_i * encode(rows[i]) rescaled, every plaintext at the ciphertexts'
-    level and the level's scale."""
+    level and the level's scale, or at the scale that lands the products
+    exactly on ``out_scale`` (inputs of one scale)."""
     limbs = int(cts[0].state.cur_limbs)
-    pts = fhe.encode_rows(ctx, rows, limbs=limbs, scale=ctx.scale_at(limbs), slots=ctx.max_slots)
+    scale = ctx.scale_at(limbs)
+    if out_scale is not None:
+        scale = float(out_scale) * float(int(ctx.primes()[limbs - 1])) / float(
+            cts[0].state.scaling_factor)
+    pts = fhe.encode_rows(ctx, rows, limbs=limbs, scale=scale, slots=ctx.max_slots)
     try:
         prods = [fhe.homo_mul_pt(c, p, ctx) for c, p in zip(cts, pts)]
     finally:
@@ -175,7 +180,11 @@ def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPref
         sq = fhe.homo_mul_relin_rescale_many(xs, xs, ctx)
         red = _fold(sq, lanes, steps, +1, ctx)
         _release(sq)
-        terms = _mul_rows_rescale(red, _row_masks(layout, alpha / (D * s_in * s_in)), ctx)
+        # the slim ciphertext lands on the scale of the prime its series drops
+        # first, the fixed point of the series' scale ladder
+        rl = int(red[0].state.cur_limbs)
+        terms = _mul_rows_rescale(red, _row_masks(layout, alpha / (D * s_in * s_in)), ctx,
+                                  out_scale=float(int(ctx.primes()[rl - 2])))
         _release(red)
         slim = terms[0]
         for t in terms[1:]:
@@ -223,27 +232,69 @@ def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPref
         _release(tmp)
 
 
+def match_scale(ct, limbs: int, scale: float, crypto_context):
+    """``ct`` re-expressed at ``limbs`` limbs with recorded scale ``scale``:
+    one integer multiple ``K = rint(scale q / s)`` on its first limbs + 1 limbs
+    and a rescale by q (the prime that rescale drops), so the value changes by
+    a relative ``K / (scale q / s) - 1`` (below 2^-40 for 40-bit primes).
+    Costs one of ``ct``'s levels; ``ct`` is not consumed."""
+    ctx = _ctx(crypto_context)
+    limbs = int(limbs)
+    if int(ct.state.cur_limbs) < limbs + 1:
+        raise ValueError(f"matching a scale at {limbs} limbs needs {limbs + 1} limbs, "
+                         f"the ciphertext has {ct.state.cur_limbs}.")
+    q = float(int(ctx.primes()[limbs]))
+    target = float(scale) * q
+    acc = fhe.linear_combination([[ct]], [target / float(ct.state.scaling_factor)], 0.0,
+                                 limbs + 1, target, 2, ctx)[0]
+    try:
+        out = fhe.rescale_many([acc], ctx)[0]
+    finally:
+        acc.release()
+    out.set_scale(float(scale), 1)
+    return out
+
+
+def _same_scale(a: float, b: float) -> bool:
+    return abs(a / b - 1.0) <= 2.0 ** -30
+
+
 def residual_add(left, right, *, crypto_context) -> tuple:
-    """Limb-wise sums of two feature-major streams at their common level
-    (rmsnorm.py:244-351); inputs are not consumed."""
+    """Limb-wise sums of two feature-major streams (rmsnorm.py:244-351);
+    inputs are not consumed.  Operands meet at the lower level; when their
+    exact scales differ (the ladders of the polynomial steps move a stream's
+    scale away from the fixed one), the higher operand is brought to the
+    other's scale by match_scale on its spare level (both drop one level when
+    they sit at the same level)."""
     ctx = _ctx(crypto_context)
     a, b = tuple(left), tuple(right)
     if len(a) != len(b):
         raise ValueError("residual streams differ in length.")
     out = []
     for x, y in zip(a, b):
-        limbs = min(int(x.state.cur_limbs), int(y.state.cur_limbs))
-        xa = x if int(x.state.cur_limbs) == limbs else fhe.align_to(
-            x, x.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
-        ya = y if int(y.state.cur_limbs) == limbs else fhe.align_to(
-            y, y.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+        lx, ly = int(x.state.cur_limbs), int(y.state.cur_limbs)
+        sx, sy = float(x.state.scaling_factor), float(y.state.scaling_factor)
+        made = []
+        if _same_scale(sx, sy):
+            limbs = min(lx, ly)
+            xa = x if lx == limbs else fhe.align_to(
+                x, x.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+            ya = y if ly == limbs else fhe.align_to(
+                y, y.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+        else:
+            if lx < ly:
+                x, y, lx, ly, sx, sy = y, x, ly, lx, sy, sx
+            limbs = ly if lx > ly else ly - 1
+            if limbs < 1:
+                raise ValueError("no level left to match the residual scales.")
+            ya = y if ly == limbs else fhe.align_to(
+                y, y.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+            xa = match_scale(x, limbs, float(ya.state.scaling_factor), ctx)
+        made = [c for c, src in ((xa, x), (ya, y)) if c is not src]
         out.append(fhe.homo_add(xa, ya, ctx))
-        if xa is not x:
-            xa.release()
-        if ya is not y:
-            ya.release()
+        _release(made)
     return tuple(out)
 
 
-__all__ = ["RMSNormResult", "is_rmsn_weight", "residual_add", "rmsnorm_depth", "rmsnorm_fhe",
-           "rmsnorm_rotations"]
+__all__ = ["RMSNormResult", "is_rmsn_weight", "match_scale", "residual_add", "rmsnorm_depth",
+           "rmsnorm_fhe", "rmsnorm_rotations"]

@@ -62,8 +62,14 @@ def test_complex_pair_and_split_roundtrip():
         pair_real_ciphers(cts[:3], crypto_context=ctx)
 
 
-@pytest.mark.parametrize("gamma,scale_in", [(False, 1.0), (True, 1.0), (True, 2.0)])
-def test_rmsnorm_matches_poly_model(gamma, scale_in):
+@pytest.mark.parametrize("gamma,scale_in,enc_scale", [(False, 1.0, 2.0 ** 40),
+                                                     (True, 1.0, 2.0 ** 40),
+                                                     (True, 2.0, 2.0 ** 40),
+                                                     (False, 1.0, 2.0 ** 41)])
+def test_rmsnorm_matches_poly_model(gamma, scale_in, enc_scale):
+    """Inputs at the fixed scale, doubled values (input_value_scale 2), and a
+    doubled recorded scale (what the complex-paired refresh returns): the
+    series' ladder starts at a prime in every case."""
     from feature_major.approx import rsqrt_entry
     from feature_major.rmsnorm import rmsnorm_depth, rmsnorm_fhe, rmsnorm_rotations
     from feature_major import FeatureMajorPrefillLayout
@@ -75,7 +81,10 @@ def test_rmsnorm_matches_poly_model(gamma, scale_in):
     x = rng.normal(size=(tokens, dim))
     w = rng.normal(1.0, 0.1, dim) if gamma else np.zeros(1)
     entry = rsqrt_entry(0.25, 4.0, 31)
-    lay, cts = _stream(client, ctx, scale_in * x)
+    lay = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=ctx.max_slots)
+    packed = lay.pack(scale_in * x)
+    cts = [client.encrypt(packed[i], scaling_factor=enc_scale, enc_id=800 + i)
+           for i in range(lay.cipher_count)]
     res = rmsnorm_fhe(cts, w, coeffs=entry, layout=lay, crypto_context=ctx,
                       input_value_scale=scale_in)
     assert res.output_limbs == int(cts[0].state.cur_limbs) - rmsnorm_depth(entry)
@@ -110,3 +119,73 @@ def test_rmsnorm_full_llama_shape():
     print(f"rmsnorm 128x4096: max err {err:.3g}, {res.wall_seconds:.3f} s, "
           f"stages {res.stage_seconds}", flush=True)
     assert err < 2e-4, err
+
+
+@pytest.mark.parametrize("limbs", [14, 10])
+def test_mlp_matches_poly_model(limbs):
+    """SwiGLU with the fitted SiLU series: 64 tokens x 512 features, intermediate
+    1408 (three pages, the last one partly active), at N = 2^13; entering with
+    spare limbs, or with exactly the MLP's depth + 1 (the output on q_0 alone:
+    any growth of the exact scales along the series' ladder would overflow)."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import silu_entry
+    from feature_major.mlp import FeatureMajorMLPLayout, MLPWeights, mlp_depth, mlp_fhe, \
+        mlp_rotations
+
+    from easyfhe import fhe
+
+    tokens, dim, inter = 64, 512, 1408
+    lay0 = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=4096)
+    client, ctx = device_context(FM_SMALL, rotations=mlp_rotations(lay0))
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(tokens, dim))
+    G = rng.normal(0, 0.05, (inter, dim))
+    U = rng.normal(0, 0.05, (inter, dim))
+    Dn = rng.normal(0, 0.05, (dim, inter))
+    silu = silu_entry()
+    lay, cts = _stream(client, ctx, x)
+    cts = [fhe.align_to(c, c.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
+           for c in cts]
+    mlay = FeatureMajorMLPLayout(lay, inter)
+    assert mlay.feature_page_count == 3 and mlay.active_width(2) == 384
+    with MLPWeights(G, U, Dn, silu=silu, layout=mlay, context=ctx) as w:
+        res = mlp_fhe(cts, w, silu=silu, crypto_context=ctx)
+    assert res.output_limbs == int(cts[0].state.cur_limbs) - mlp_depth(silu)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    want = LN.silu_poly_mlp_numpy(x, G, U, Dn, silu["coefficients"], silu["fit_interval"])
+    err = float(np.max(np.abs(got - want)))
+    print(f"mlp 64x512 (I=1408) from {limbs} limbs: max err {err:.3g}, "
+          f"|y| max {np.max(np.abs(want)):.3g}, "
+          f"{res.wall_seconds:.3f} s", flush=True)
+    assert err < 1e-5, err
+
+
+def test_residual_add_matches_exact_scales():
+    """A stream at a scale away from the fixed one (as a polynomial ladder's
+    output is) plus a fixed-scale stream: the higher operand is re-expressed
+    at the other's scale on its spare level; at equal levels both drop one."""
+    from easyfhe import fhe
+    from feature_major.rmsnorm import match_scale, residual_add
+
+    client, ctx = device_context(FM_SMALL)
+    rng = np.random.default_rng(5)
+    slots = ctx.max_slots
+    a, b = rng.uniform(-1, 1, slots), rng.uniform(-1, 1, slots)
+    ca = client.encrypt(a, enc_id=900)
+    cb = client.encrypt(b, cur_limbs=8, scaling_factor=2.0 ** 40 * 1.003, enc_id=901)
+    low = fhe.align_to(ca, ca.state.replace(cur_limbs=8, scaling_factor=None), ctx)
+    with pytest.raises(ValueError):
+        fhe.homo_add(low, cb, ctx)
+    (out,) = residual_add([ca], [cb], crypto_context=ctx)
+    assert int(out.state.cur_limbs) == 8
+    assert np.max(np.abs(client.decrypt(out) - (a + b))) < 1e-6
+    (out2,) = residual_add([cb], [ca], crypto_context=ctx)
+    assert np.max(np.abs(client.decrypt(out2) - (a + b))) < 1e-6
+    # equal levels, different scales: both operands drop one level
+    (out3,) = residual_add([low], [cb], crypto_context=ctx)
+    assert int(out3.state.cur_limbs) == 7
+    assert np.max(np.abs(client.decrypt(out3) - (a + b))) < 1e-6
+    m = match_scale(ca, 8, float(cb.state.scaling_factor), ctx)
+    assert np.max(np.abs(client.decrypt(m) - a)) < 1e-7
+    with pytest.raises(ValueError):
+        match_scale(cb, 8, 2.0 ** 40, ctx)
