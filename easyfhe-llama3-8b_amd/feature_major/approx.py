@@ -56,6 +56,20 @@ def silu_entry(lo: float = -12.0, hi: float = 12.0, degree: int = 63) -> dict:
     return fit_entry(lambda g: g / (1.0 + np.exp(-g)), lo, hi, degree)
 
 
+def exp_entry(lo: float, hi: float = 0.0, degree: int = 15) -> dict:
+    """Series of ``exp(x)`` on [lo, hi] (the shifted, 2^-k scaled scores of
+    the softmax)."""
+    return fit_entry(np.exp, lo, hi, degree)
+
+
+def inverse_entry(lo: float, hi: float = 1.0, degree: int = 63) -> dict:
+    """Series of ``1/v`` on [lo, hi] (the softmax rounds' normalised row
+    sums of squares)."""
+    if lo <= 0.0:
+        raise ValueError("the inverse needs an interval above zero.")
+    return fit_entry(lambda v: 1.0 / v, lo, hi, degree)
+
+
 def chebyshev_map(fit_interval) -> tuple[float, float]:
     """(alpha, beta) of the affine map v -> alpha v + beta onto [-1, 1]
     (operators/norm/rmsnorm.py:401-402)."""
@@ -71,5 +85,5 @@ def entry_depth(entry: dict) -> int:
     return int(chebyshev_depth(entry["coefficients"]))
 
 
-__all__ = ["RMSNORM_EPS", "chebyshev_map", "entry_depth", "fit_entry", "rsqrt_entry",
-           "silu_entry"]
+__all__ = ["RMSNORM_EPS", "chebyshev_map", "entry_depth", "exp_entry", "fit_entry",
+           "inverse_entry", "rsqrt_entry", "silu_entry"]

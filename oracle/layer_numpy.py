@@ -11,6 +11,11 @@ reference compares its encrypted layer against:
   the fitted inverse-square-root series p, no clamping in FHE mode);
 * ``silu_poly_mlp_numpy``: the MLP half of approx/layer.py:121-140
   (``down @ (p_silu(gate @ x) * (up @ x))``);
+* ``softmax_alg2_numpy``: the "Algorithm 2" softmax of
+  operators/attention/softmax.py:648-1262 (exp of the shifted, 2^-k scaled
+  scores, then k rounds of squaring and row normalisation), with the given
+  series;
+* ``attention_numpy``: causal grouped attention, approx/attention.py:134-173;
 * ``fm_pack`` / ``fm_unpack``: the feature-major token-lane layout of
   layouts/feature_major.py:74-92 (slot = feature * lanes + token % lanes,
   ciphertext = token // lanes).
@@ -55,6 +60,52 @@ def silu_poly_mlp_numpy(x, gate_weight, up_weight, down_weight, coefficients,
     up = x @ np.asarray(up_weight, dtype=np.float64).T
     act = eval_chebyshev_series_direct(gate, coefficients, lo, hi) * up
     return act @ np.asarray(down_weight, dtype=np.float64).T
+
+
+def softmax_alg2_numpy(scores, exp_entry, first_inverse, inverse, *, rounds: int,
+                       shift: float) -> np.ndarray:
+    """Causal softmax of [H, T, T] scores by "Algorithm 2" (the reference's
+    encrypted softmax, operators/attention/softmax.py:648-1262): y =
+    exp_series((s - shift) / 2^k) on valid keys, then k rounds of
+    y <- y^2 * inv(sum_row y^2); the first round's sums are taken as means over
+    the valid keys.  With exact series the result is exp(s) / sum exp(s)."""
+    s = np.asarray(scores, dtype=np.float64)
+    T = s.shape[-1]
+    valid = np.tril(np.ones((T, T), dtype=bool))[None]
+    count = valid.sum(-1, keepdims=True).astype(np.float64)
+    lo, hi = exp_entry["fit_interval"]
+    y = np.where(valid, eval_chebyshev_series_direct((s - shift) / 2.0 ** rounds,
+                                                     exp_entry["coefficients"], lo, hi), 0.0)
+    for r in range(int(rounds)):
+        sq = y * y
+        tot = sq.sum(-1, keepdims=True)
+        e = first_inverse if r == 0 else inverse
+        lo, hi = e["fit_interval"]
+        if r == 0:
+            inv = eval_chebyshev_series_direct(tot / count, e["coefficients"], lo, hi) / count
+        else:
+            inv = eval_chebyshev_series_direct(tot, e["coefficients"], lo, hi)
+        y = sq * inv
+    return y
+
+
+def attention_numpy(q, k, v, heads: int, probs_fn=None) -> np.ndarray:
+    """Causal multi-head attention of [T, H hd] streams (heads already
+    repeated for grouped queries), scores scaled by 1/sqrt(hd)
+    (approx/attention.py:134-173); ``probs_fn`` replaces the exact softmax."""
+    q, k, v = (np.asarray(a, dtype=np.float64) for a in (q, k, v))
+    T, D = q.shape
+    hd = D // int(heads)
+    qh, kh, vh = (a.reshape(T, heads, hd).transpose(1, 0, 2) for a in (q, k, v))
+    s = qh @ kh.transpose(0, 2, 1) / np.sqrt(hd)
+    if probs_fn is None:
+        valid = np.tril(np.ones((T, T), dtype=bool))[None]
+        m = np.where(valid, s, -np.inf)
+        e = np.where(valid, np.exp(m - m.max(-1, keepdims=True)), 0.0)
+        p = e / e.sum(-1, keepdims=True)
+    else:
+        p = probs_fn(s)
+    return (p @ vh).transpose(1, 0, 2).reshape(T, D)
 
 
 def fm_pack(rows, slots: int) -> np.ndarray:

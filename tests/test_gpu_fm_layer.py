@@ -189,3 +189,93 @@ def test_residual_add_matches_exact_scales():
     assert np.max(np.abs(client.decrypt(m) - a)) < 1e-7
     with pytest.raises(ValueError):
         match_scale(cb, 8, 2.0 ** 40, ctx)
+
+
+FM_DEEP = dict(log_n=13, depth=39, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+def _attention_setup(seed=6, rotations=None):
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.attention import AttentionGeometry, attention_rotations
+
+    tokens, dim, heads, hd = 64, 512, 4, 128
+    lay0 = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=4096)
+    geo0 = AttentionGeometry(lay0, heads, hd)
+    client, ctx = device_context(FM_DEEP, rotations=rotations or attention_rotations(geo0))
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 0.5, (tokens, dim))
+    k = rng.normal(0, 0.5, (tokens, dim))
+    v = rng.normal(0, 1.0, (tokens, dim))
+    return client, ctx, geo0, q, k, v
+
+
+def test_qk_scores_layout():
+    """Score layout of Q K^T / sqrt(hd) for 64 tokens, 4 heads of 128 at
+    N = 2^13 (8 ciphertexts of 8 lanes): every head, query and key offset."""
+    from feature_major.attention import qk_scores
+
+    client, ctx, geo, q, k, _ = _attention_setup()
+    lay, qc = _stream(client, ctx, q, enc0=1000)
+    _, kc = _stream(client, ctx, k, enc0=1100)
+    res = qk_scores(qc, kc, geo, crypto_context=ctx, output_scale=1 / np.sqrt(128))
+    got = geo.unpack_scores(np.stack([client.decrypt(c) for c in res.ciphers]))
+    qh = q.reshape(64, 4, 128).transpose(1, 0, 2)
+    kh = k.reshape(64, 4, 128).transpose(1, 0, 2)
+    want = qh @ kh.transpose(0, 2, 1) / np.sqrt(128)
+    err = float(np.max(np.abs(got - want)))
+    print(f"qk 64 tokens x 4 heads: max err {err:.3g} (|s| max {np.abs(want).max():.3g}), "
+          f"limbs {int(qc[0].state.cur_limbs)} -> {int(res.ciphers[0].state.cur_limbs)}, "
+          f"stages {res.stage_seconds}", flush=True)
+    assert int(qc[0].state.cur_limbs) - int(res.ciphers[0].state.cur_limbs) == 4
+    assert err < 1e-5, err
+
+
+def test_pv_output_from_probabilities():
+    """Feature-major P V from score-layout probabilities (causal, rows summing
+    to one) and a value stream: 64 tokens, 4 heads of 128 at N = 2^13."""
+    from feature_major.attention import pv_output
+
+    client, ctx, geo, _, _, v = _attention_setup(seed=7)
+    rng = np.random.default_rng(8)
+    T = 64
+    logits = rng.normal(0, 1, (4, T, T))
+    causal = np.tril(np.ones((T, T), dtype=bool))
+    e = np.where(causal[None], np.exp(logits), 0.0)
+    P = e / e.sum(-1, keepdims=True)
+    packed = geo.pack_scores(P)
+    pc = [client.encrypt(packed[c], enc_id=1200 + c) for c in range(geo.ciphers)]
+    lay, vc = _stream(client, ctx, v, enc0=1300)
+    res = pv_output(pc, vc, geo, crypto_context=ctx)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    vh = v.reshape(T, 4, 128).transpose(1, 0, 2)
+    want = (P @ vh).transpose(1, 0, 2).reshape(T, 512)
+    err = float(np.max(np.abs(got - want)))
+    print(f"pv 64 tokens x 4 heads: max err {err:.3g}, limbs -> "
+          f"{int(res.ciphers[0].state.cur_limbs)}, stages {res.stage_seconds}", flush=True)
+    assert err < 1e-6, err
+
+
+def test_attention_matches_alg2_model():
+    """Causal attention of 64 tokens, 4 heads of 128 at N = 2^13 (QK, the
+    Alg2 softmax with two rounds, PV), against the fp64 model of the same
+    algorithm (its series included) and, more loosely, exact attention."""
+    from feature_major.attention import SoftmaxConfig, attention_fhe, softmax_depth
+
+    client, ctx, geo, q, k, v = _attention_setup(seed=10)
+    cfg = SoftmaxConfig(rounds=2, shift=2.0, bound=2.0)
+    lay, qc = _stream(client, ctx, q, enc0=1400)
+    _, kc = _stream(client, ctx, k, enc0=1500)
+    _, vc = _stream(client, ctx, v, enc0=1600)
+    res = attention_fhe(qc, kc, vc, geo, cfg, crypto_context=ctx)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    model = LN.attention_numpy(q, k, v, 4, probs_fn=lambda s: LN.softmax_alg2_numpy(
+        s, cfg.exp(), cfg.first_inverse(), cfg.inverse(64), rounds=2, shift=2.0))
+    exact = LN.attention_numpy(q, k, v, 4)
+    err = float(np.max(np.abs(got - model)))
+    used = int(qc[0].state.cur_limbs) - int(res.ciphers[0].state.cur_limbs)
+    print(f"attention 64 tokens x 4 heads: max err {err:.3g} vs model, "
+          f"{np.max(np.abs(got - exact)):.3g} vs exact, levels {used} "
+          f"(softmax depth {softmax_depth(cfg, 64)}), stages "
+          f"{ {k: round(t, 3) for k, t in res.stage_seconds.items()} }", flush=True)
+    assert err < 1e-4, err
+    assert np.max(np.abs(got - exact)) < 1e-3

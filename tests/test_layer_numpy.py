@@ -83,3 +83,37 @@ def test_fm_pack_matches_product_layout(tokens, dim, slots):
     # token t, feature f at slot f * lanes + t % lanes of ciphertext t // lanes
     lanes = slots // dim
     assert packed[5 // lanes, 7 * lanes + 5 % lanes] == x[5, 7]
+
+
+def test_alg2_softmax_model_converges_to_softmax():
+    """The Alg2 model with the fitted series equals the exact causal softmax
+    (with exact exp and inverse the rounds turn exp(s / 2^k) into
+    exp(s) / sum exp(s) for any k); a round too few for its 2^-k scaling
+    would give the softmax at twice the temperature instead."""
+    from feature_major.attention import SoftmaxConfig
+
+    rng = np.random.default_rng(9)
+    T, H = 32, 3
+    s = rng.uniform(-3.5, 3.5, (H, T, T))
+    cfg = SoftmaxConfig(rounds=2, shift=4.0, bound=4.0)
+    got = LN.softmax_alg2_numpy(s, cfg.exp(), cfg.first_inverse(), cfg.inverse(T),
+                                rounds=2, shift=4.0)
+    valid = np.tril(np.ones((T, T), dtype=bool))[None]
+    e = np.where(valid, np.exp(s), 0.0)
+    want = e / e.sum(-1, keepdims=True)
+    assert np.max(np.abs(got - want)) < 1e-4
+    # one round on half the score range (the first inverse's interval is
+    # set by exp(2 (s - shift) / 2^k), so it is the same here)
+    one = SoftmaxConfig(rounds=1, shift=2.0, bound=2.0)
+    half = s / 2
+    e1 = np.where(valid, np.exp(half), 0.0)
+    assert np.max(np.abs(LN.softmax_alg2_numpy(half, one.exp(), one.first_inverse(),
+                                               one.inverse(T), rounds=1, shift=2.0)
+                         - e1 / e1.sum(-1, keepdims=True))) < 1e-4
+    e2 = np.where(valid, np.exp(s / 2), 0.0)
+    assert np.max(np.abs(got - e2 / e2.sum(-1, keepdims=True))) > 1e-2
+    q = rng.normal(size=(T, H * 16))
+    out = LN.attention_numpy(q, q, q, H)
+    assert out.shape == (T, H * 16)
+    # token 0 attends to itself only
+    assert np.allclose(out[0], q[0])
