@@ -85,13 +85,17 @@ def main() -> int:
     ap.add_argument("--levels", type=int, default=34, help="HMult levels per step")
     ap.add_argument("--no-mlp", action="store_true",
                     help="skip the RMSNorm + MLP block measurement of the default run")
-    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp"],
+    ap.add_argument("--no-attention", action="store_true",
+                    help="skip the attention measurement of the default run")
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp",
+                                       "attention"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
                          "bootstrap: the full-slot bootstrap workload on the same chain; "
                          "linear: one 4096x4096 feature-major linear over 128 tokens; "
-                         "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer")
+                         "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer; "
+                         "attention: the causal attention of a layer")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -115,6 +119,13 @@ def main() -> int:
         spec.rotations = ()
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
+              flush=True)
+        return 0
+    if args.mode == "attention":
+        spec.rotations = ()
+        client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+        print(json.dumps({"fm_attention": measure_fm_attention(client, ctx,
+                                                               warmup=args.warmup)}),
               flush=True)
         return 0
     if args.mode == "mlp":
@@ -236,7 +247,7 @@ def main() -> int:
             "limb_polys_per_launch": limb_polys,
         },
     }
-    if not args.no_bootstrap or not args.no_linear or not args.no_mlp:
+    if not (args.no_bootstrap and args.no_linear and args.no_mlp and args.no_attention):
         for c in cts:
             c.release()
     if not args.no_bootstrap:
@@ -249,6 +260,9 @@ def main() -> int:
     if not args.no_mlp:
         # the RMSNorm + MLP + residual half of a decoder layer on the same chain
         result["fm_mlp_block"] = measure_fm_mlp_block(client, ctx)
+    if not args.no_attention:
+        # the causal attention of a decoder layer on the same chain
+        result["fm_attention"] = measure_fm_attention(client, ctx)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -461,6 +475,70 @@ def measure_fm_mlp_block(client, ctx, limbs: int = 20, warmup: int = 1) -> dict:
         "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
         "rotation_keygen_s": round(keygen_s, 2),
         "weight_upload_s": round(upload_s, 2),
+    }
+
+
+def measure_fm_attention(client, ctx, limbs: int = 34, warmup: int = 1) -> dict:
+    """Causal attention of a Llama-3-8B decoder layer over 128 tokens: 32 query
+    heads of 128 (key/value heads already repeated for the query groups), in
+    16 feature-major ciphertexts of 8 lanes entering at `limbs` limbs;
+    QK, the Algorithm-2 softmax (2 rounds, scores assumed in [-4, 4]) and PV.
+    Q, K, V entries N(0, 0.5^2) / N(0, 1), seed 0; the error is against exact
+    causal softmax attention in fp64."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.attention import (AttentionGeometry, SoftmaxConfig, attention_fhe,
+                                         attention_rotations)
+
+    T, D, H, hd = 128, 4096, 32, 128
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=ctx.max_slots)
+    geo = AttentionGeometry(lay, H, hd)
+    t0 = time.perf_counter()
+    ctx.generate_rotation_keys(attention_rotations(geo))
+    ctx.synchronize()
+    keygen_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    q = rng.normal(0, 0.5, (T, D))
+    k = rng.normal(0, 0.5, (T, D))
+    v = rng.normal(0, 1.0, (T, D))
+    cfg = SoftmaxConfig(rounds=2, shift=4.0, bound=4.0)
+
+    def enc(x, base):
+        p = lay.pack(x)
+        return [client.encrypt(p[i], cur_limbs=limbs, enc_id=base + i)
+                for i in range(lay.cipher_count)]
+
+    qc, kc, vc = enc(q, 400000), enc(k, 400100), enc(v, 400200)
+    for _ in range(max(1, warmup)):
+        res = attention_fhe(qc, kc, vc, geo, cfg, crypto_context=ctx)
+        res.release()
+    ctx.synchronize()
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    res = attention_fhe(qc, kc, vc, geo, cfg, crypto_context=ctx)
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    got = lay.unpack(np.stack([client.decrypt(o) for o in res.ciphers]))
+    limbs_out = int(res.ciphers[0].state.cur_limbs)
+    res_stages = dict(res.stage_seconds)
+    res.release()
+    qh, kh, vh = (a.reshape(T, H, hd).transpose(1, 0, 2) for a in (q, k, v))
+    s = qh @ kh.transpose(0, 2, 1) / np.sqrt(hd)
+    valid = np.tril(np.ones((T, T), dtype=bool))[None]
+    e = np.where(valid, np.exp(np.where(valid, s, 0) - 4.0), 0.0)
+    want = ((e / e.sum(-1, keepdims=True)) @ vh).transpose(1, 0, 2).reshape(T, D)
+    return {
+        "seconds": round(wall, 4),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 4),
+        "workload": f"causal attention, 128 tokens x 32 heads x 128 in {lay.cipher_count} "
+                    f"ciphertexts of {lay.tokens_per_cipher} lanes, {limbs} -> {limbs_out} limbs; "
+                    "Algorithm-2 softmax, 2 rounds",
+        "stages_s": {k2: round(v2, 4) for k2, v2 in res_stages.items()},
+        "max_abs_err_vs_exact_fp64": float(np.abs(got - want).max()),
+        "score_abs_max": float(np.abs(np.where(valid, s, 0)).max()),
+        "rotation_keygen_s": round(keygen_s, 2),
+        "rotation_keys": len(attention_rotations(geo)),
     }
 
 

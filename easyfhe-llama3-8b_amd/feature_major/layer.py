@@ -1,0 +1,223 @@
+"""One encrypted Llama decoder layer on feature-major ciphertexts (the
+reference's per-layer graph, llama3fhe/graph.py:545-1584, whose plaintext
+counterpart is approx/layer.py:64-149):
+
+    h   = x + W_o attention(rope(W_q n1), rope(W_k n1), W_v n1),  n1 = rmsnorm(x)
+    out = h + mlp(rmsnorm(h))
+
+* RMSNorm: the slim-packed single-series form (``rmsnorm.rmsnorm_fhe``);
+* projections: the BSGS linear engine on complex-paired token ciphertexts
+  (``x_2r + i x_(2r+1)``: one real projection serves two token groups), each
+  weight halved so that the conjugation split after it returns the real
+  streams at their own scale; key/value weights with their rows repeated for
+  the grouped query heads (``attention.kv_repeat_rows``);
+* RoPE on queries and keys (``rope.rope_fhe``);
+* causal attention with the Algorithm-2 softmax (``attention.attention_fhe``);
+* the SwiGLU MLP (``mlp.mlp_fhe``);
+* residual additions with exact-scale matching (``rmsnorm.residual_add``).
+
+The layer runs without refreshes here: it needs a chain that holds its depth
+(``decoder_layer_depth``).  Bootstrap placement for a chain that does not is
+``easyfhe.bs.placement``'s.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .attention import (AttentionGeometry, SoftmaxConfig, attention_fhe, attention_rotations,
+                        kv_repeat_rows, softmax_depth)
+from .complex import pair_real_ciphers, split_complex_ciphers_twice
+from .layout import FeatureMajorPrefillLayout
+from .linear import LinearOperator, LinearWeight, linear_rotations
+from .mlp import FeatureMajorMLPLayout, MLPWeights, mlp_depth, mlp_fhe
+from .rmsnorm import residual_add, rmsnorm_depth, rmsnorm_fhe, rmsnorm_rotations
+from .rope import rope_fhe, rope_rotations
+
+
+def _ctx(context):
+    return getattr(context, "context", context)
+
+
+def _release(values) -> None:
+    for v in values or ():
+        if v is not None:
+            v.release()
+
+
+@dataclass(frozen=True)
+class LayerApproximations:
+    """The layer's polynomial entries (the reference's per-layer JSON
+    artifacts, application/approx_config.py)."""
+
+    input_norm: dict
+    post_attention_norm: dict
+    silu: dict
+    softmax: SoftmaxConfig
+
+
+def decoder_layer_depth(approx: LayerApproximations, seq_len: int) -> int:
+    return (rmsnorm_depth(approx.input_norm) + 1 + 1 + 4 + softmax_depth(approx.softmax, seq_len)
+            + 2 + 1 + 1 + rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu))
+
+
+def decoder_layer_rotations(layout: FeatureMajorPrefillLayout, heads: int,
+                            head_dim: int) -> tuple[int, ...]:
+    geo = AttentionGeometry(layout, heads, head_dim)
+    keys = set(linear_rotations(dimension=int(layout.hidden_dim),
+                                token_lanes=int(layout.tokens_per_cipher),
+                                slots=int(layout.slots), include_conjugation=True))
+    keys |= set(rmsnorm_rotations(layout)) | set(attention_rotations(geo))
+    keys |= set(rope_rotations(layout, head_dim))
+    return tuple(sorted(k for k in keys if k))
+
+
+class DecoderLayerWeights:
+    """A layer's projections resident on the device: W_q, W_k, W_v (rows of
+    the key/value heads repeated for the query groups), W_o, each halved for
+    the complex-paired projection, and the paged MLP."""
+
+    def __init__(self, q, k, v, o, gate, up, down, *, heads: int, kv_heads: int,
+                 head_dim: int, intermediate: int, approx: LayerApproximations,
+                 layout: FeatureMajorPrefillLayout, context):
+        ctx = _ctx(context)
+        D = int(layout.hidden_dim)
+        q, o = np.asarray(q, dtype=np.float64), np.asarray(o, dtype=np.float64)
+        if q.shape != (D, D) or o.shape != (D, D):
+            raise ValueError(f"q and o must be {(D, D)}.")
+        kr = kv_repeat_rows(k, query_heads=heads, kv_heads=kv_heads, head_dim=head_dim)
+        vr = kv_repeat_rows(v, query_heads=heads, kv_heads=kv_heads, head_dim=head_dim)
+        self.layout = layout
+        self.geometry = AttentionGeometry(layout, heads, head_dim)
+        self.approx = approx
+        self._w = []
+        try:
+            self.q = self._keep(LinearWeight(0.5 * q, context=ctx))
+            self.k = self._keep(LinearWeight(0.5 * kr, context=ctx))
+            self.v = self._keep(LinearWeight(0.5 * vr, context=ctx))
+            self.o = self._keep(LinearWeight(0.5 * o, context=ctx))
+            self.mlp = MLPWeights(gate, up, down, silu=approx.silu,
+                                  layout=FeatureMajorMLPLayout(layout, intermediate), context=ctx)
+        except Exception:
+            self.close()
+            raise
+
+    def _keep(self, w):
+        self._w.append(w)
+        return w
+
+    def close(self) -> None:
+        for w in self._w:
+            w.close()
+        self._w = []
+        if getattr(self, "mlp", None) is not None:
+            self.mlp.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+@dataclass
+class LayerResult:
+    ciphers: tuple
+    wall_seconds: float
+    stage_seconds: dict = field(default_factory=dict)
+    output_limbs: int = 0
+
+    def release(self) -> None:
+        _release(self.ciphers)
+        self.ciphers = ()
+
+
+def _paired_projection(op: LinearOperator, paired, weight, ctx) -> tuple:
+    out, _ = op.apply(paired, weight)
+    try:
+        return split_complex_ciphers_twice(out, crypto_context=ctx)
+    finally:
+        _release(out)
+
+
+def decoder_layer_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
+                      rope_theta: float = 500000.0) -> LayerResult:
+    """One decoder layer of a feature-major residual stream; the input is not
+    consumed."""
+    ctx = _ctx(crypto_context)
+    lay, geo, ap = weights.layout, weights.geometry, weights.approx
+    xs = tuple(input_ciphers)
+    need = decoder_layer_depth(ap, geo.seq_len) + 1
+    if int(xs[0].state.cur_limbs) < need:
+        raise ValueError(f"the layer needs {need} limbs, the input has "
+                         f"{int(xs[0].state.cur_limbs)}.")
+    sync = ctx.synchronize
+    stage: dict[str, float] = {}
+    t_start = time.perf_counter()
+    op = LinearOperator(context=ctx, token_lanes=geo.lanes)
+    keep: list = []
+    try:
+        t0 = time.perf_counter()
+        n1 = rmsnorm_fhe(xs, np.zeros(1), coeffs=ap.input_norm, layout=lay, crypto_context=ctx)
+        sync()
+        stage["input_rmsnorm"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        z = pair_real_ciphers(n1.ciphers, crypto_context=ctx)
+        n1.release()
+        q = _paired_projection(op, z, weights.q, ctx)
+        k = _paired_projection(op, z, weights.k, ctx)
+        v = _paired_projection(op, z, weights.v, ctx)
+        op.release_babies(z)
+        _release(z)
+        sync()
+        stage["qkv_projection"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        qr = rope_fhe(q, lay, head_dim=geo.head_dim, crypto_context=ctx, theta=rope_theta)
+        kr = rope_fhe(k, lay, head_dim=geo.head_dim, crypto_context=ctx, theta=rope_theta)
+        _release(q)
+        _release(k)
+        sync()
+        stage["rope"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        att = attention_fhe(qr, kr, v, geo, ap.softmax, crypto_context=ctx)
+        _release(qr)
+        _release(kr)
+        _release(v)
+        sync()
+        stage["attention"] = time.perf_counter() - t0
+        stage.update({f"attention.{k2}": v2 for k2, v2 in att.stage_seconds.items()})
+        t0 = time.perf_counter()
+        za = pair_real_ciphers(att.ciphers, crypto_context=ctx)
+        att.release()
+        o = _paired_projection(op, za, weights.o, ctx)
+        op.release_babies(za)
+        _release(za)
+        h = residual_add(xs, o, crypto_context=ctx)
+        _release(o)
+        keep = list(h)
+        sync()
+        stage["output_projection_and_residual"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n2 = rmsnorm_fhe(h, np.zeros(1), coeffs=ap.post_attention_norm, layout=lay,
+                         crypto_context=ctx)
+        sync()
+        stage["post_attention_rmsnorm"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        m = mlp_fhe(n2.ciphers, weights.mlp, silu=ap.silu, crypto_context=ctx, operator=op)
+        n2.release()
+        out = residual_add(h, m.ciphers, crypto_context=ctx)
+        m.release()
+        sync()
+        stage["mlp_and_residual"] = time.perf_counter() - t0
+        return LayerResult(tuple(out), time.perf_counter() - t_start, stage,
+                           int(out[0].state.cur_limbs))
+    finally:
+        _release(keep)
+        op.close()
+
+
+__all__ = ["DecoderLayerWeights", "LayerApproximations", "LayerResult", "decoder_layer_depth",
+           "decoder_layer_fhe", "decoder_layer_rotations"]

@@ -16,6 +16,8 @@ reference compares its encrypted layer against:
   scores, then k rounds of squaring and row normalisation), with the given
   series;
 * ``attention_numpy``: causal grouped attention, approx/attention.py:134-173;
+* ``apply_rope_numpy``: rotary embedding, approx/attention.py:22-70;
+* ``decoder_layer_numpy``: the whole layer, approx/layer.py:64-149;
 * ``fm_pack`` / ``fm_unpack``: the feature-major token-lane layout of
   layouts/feature_major.py:74-92 (slot = feature * lanes + token % lanes,
   ciphertext = token // lanes).
@@ -106,6 +108,44 @@ def attention_numpy(q, k, v, heads: int, probs_fn=None) -> np.ndarray:
     else:
         p = probs_fn(s)
     return (p @ vh).transpose(1, 0, 2).reshape(T, D)
+
+
+def apply_rope_numpy(x, heads: int, head_dim: int, theta: float = 500000.0,
+                     start_pos: int = 0) -> np.ndarray:
+    """RoPE of [T, heads * hd] rows (approx/attention.py:22-70): pairs (d,
+    d + hd/2) rotated by ``p * theta^(-2j / hd)`` at position p."""
+    x = np.asarray(x, dtype=np.float64)
+    T = x.shape[0]
+    hd, half = int(head_dim), int(head_dim) // 2
+    inv = 1.0 / (float(theta) ** (np.arange(0, hd, 2, dtype=np.float64) / hd))
+    ang = np.outer(np.arange(start_pos, start_pos + T, dtype=np.float64), inv)
+    cos, sin = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    h = x.reshape(T, int(heads), hd)
+    a, b = h[..., :half], h[..., half:]
+    out = np.concatenate([a * cos - b * sin, b * cos + a * sin], axis=-1)
+    return out.reshape(T, -1)
+
+
+def decoder_layer_numpy(x, wq, wk, wv, wo, gate, up, down, *, heads: int, kv_heads: int,
+                        head_dim: int, input_norm, post_attention_norm, silu,
+                        probs_fn=None, theta: float = 500000.0) -> np.ndarray:
+    """One decoder layer with polynomial RMSNorm and SiLU (approx/layer.py:64-149);
+    ``probs_fn`` replaces the exact causal softmax (e.g. the Alg2 model)."""
+    x = np.asarray(x, dtype=np.float64)
+    g = int(heads) // int(kv_heads)
+
+    def rep(w):
+        w = np.asarray(w, dtype=np.float64).reshape(int(kv_heads), int(head_dim), -1)
+        return np.repeat(w, g, axis=0).reshape(int(heads) * int(head_dim), -1)
+
+    n1 = rmsnorm_poly_numpy(x, input_norm["coefficients"], input_norm["fit_interval"])
+    q = apply_rope_numpy(n1 @ np.asarray(wq).T, heads, head_dim, theta)
+    k = apply_rope_numpy(n1 @ rep(wk).T, heads, head_dim, theta)
+    v = n1 @ rep(wv).T
+    h = x + attention_numpy(q, k, v, heads, probs_fn) @ np.asarray(wo).T
+    n2 = rmsnorm_poly_numpy(h, post_attention_norm["coefficients"],
+                            post_attention_norm["fit_interval"])
+    return h + silu_poly_mlp_numpy(n2, gate, up, down, silu["coefficients"], silu["fit_interval"])
 
 
 def fm_pack(rows, slots: int) -> np.ndarray:

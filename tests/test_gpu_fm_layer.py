@@ -279,3 +279,52 @@ def test_attention_matches_alg2_model():
           f"{ {k: round(t, 3) for k, t in res.stage_seconds.items()} }", flush=True)
     assert err < 1e-4, err
     assert np.max(np.abs(got - exact)) < 1e-3
+
+
+FM_LAYER = dict(log_n=13, depth=63, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+def test_decoder_layer_matches_poly_model():
+    """One decoder layer end to end (RMSNorm, Q/K/V with grouped heads, RoPE,
+    attention with the Alg2 softmax, W_o, residual, RMSNorm, SwiGLU MLP,
+    residual) for 64 tokens x 512 features, 4 query / 2 key-value heads of
+    128, intermediate 1408, at N = 2^13 on a 64-limb chain (no refresh);
+    against the fp64 model of the same layer."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_depth, decoder_layer_fhe,
+                                     decoder_layer_rotations)
+
+    T, D, H, KV, hd, I = 64, 512, 4, 2, 128, 1408
+    lay0 = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=4096)
+    client, ctx = device_context(FM_LAYER, rotations=decoder_layer_rotations(lay0, H, hd))
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 1, (T, D))
+    sd = 1.0 / np.sqrt(D)
+    wq, wo = rng.normal(0, sd, (D, D)), rng.normal(0, sd, (D, D))
+    wk, wv = rng.normal(0, sd, (KV * hd, D)), rng.normal(0, sd, (KV * hd, D))
+    G, U = rng.normal(0, sd, (I, D)), rng.normal(0, sd, (I, D))
+    Dn = rng.normal(0, 1.0 / np.sqrt(I), (D, I))
+    ap = LayerApproximations(rsqrt_entry(0.25, 4.0, 31), rsqrt_entry(0.25, 4.0, 31),
+                             silu_entry(), SoftmaxConfig(rounds=2, shift=4.0, bound=4.0))
+    assert decoder_layer_depth(ap, T) < 63
+    lay, xc = _stream(client, ctx, x, enc0=1700)
+    with DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+                             intermediate=I, approx=ap, layout=lay, context=ctx) as w:
+        res = decoder_layer_fhe(xc, w, crypto_context=ctx)
+    got = _decrypt_stream(client, lay, res.ciphers)
+    sm = ap.softmax
+    kw = dict(heads=H, kv_heads=KV, head_dim=hd, input_norm=ap.input_norm,
+              post_attention_norm=ap.post_attention_norm, silu=ap.silu)
+    model = LN.decoder_layer_numpy(x, wq, wk, wv, wo, G, U, Dn, probs_fn=lambda s: (
+        LN.softmax_alg2_numpy(s, sm.exp(), sm.first_inverse(), sm.inverse(T),
+                              rounds=sm.rounds, shift=sm.shift)), **kw)
+    exact_softmax = LN.decoder_layer_numpy(x, wq, wk, wv, wo, G, U, Dn, **kw)
+    err = float(np.max(np.abs(got - model)))
+    print(f"layer 64x512: max err {err:.3g} vs model, "
+          f"{np.max(np.abs(got - exact_softmax)):.3g} vs exact softmax, "
+          f"|out| {np.abs(model).max():.3g}, limbs 64 -> {res.output_limbs}, "
+          f"{res.wall_seconds:.2f} s", flush=True)
+    assert err < 1e-4, err

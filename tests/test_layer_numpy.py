@@ -117,3 +117,28 @@ def test_alg2_softmax_model_converges_to_softmax():
     assert out.shape == (T, H * 16)
     # token 0 attends to itself only
     assert np.allclose(out[0], q[0])
+
+
+def test_rope_model_matches_product_plaintexts_and_is_a_rotation():
+    """RoPE keeps each (d, d + hd/2) pair's norm and is the identity at
+    position 0; the product's per-slot plaintexts (C, S1, S2 with the two
+    half-head rotations) reproduce the model on packed rows."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.rope import rope_plaintext_rows
+
+    rng = np.random.default_rng(11)
+    T, H, hd = 16, 2, 128
+    x = rng.normal(size=(T, H * hd))
+    y = LN.apply_rope_numpy(x, H, hd)
+    assert np.allclose(y[0], x[0])
+    xa, xb = x.reshape(T, H, hd)[..., :64], x.reshape(T, H, hd)[..., 64:]
+    ya, yb = y.reshape(T, H, hd)[..., :64], y.reshape(T, H, hd)[..., 64:]
+    assert np.allclose(xa ** 2 + xb ** 2, ya ** 2 + yb ** 2)
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=H * hd, slots=4096)
+    L = lay.tokens_per_cipher
+    packed = lay.pack(x)
+    out = np.zeros_like(packed)
+    for c in range(lay.cipher_count):
+        C, S1, S2 = rope_plaintext_rows(lay, hd, c)
+        out[c] = packed[c] * C + np.roll(packed[c], -64 * L) * S1 + np.roll(packed[c], 64 * L) * S2
+    assert np.allclose(lay.unpack(out), y)
