@@ -87,15 +87,18 @@ def main() -> int:
                     help="skip the RMSNorm + MLP block measurement of the default run")
     ap.add_argument("--no-attention", action="store_true",
                     help="skip the attention measurement of the default run")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="skip the whole-layer measurement of the default run")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp",
-                                       "attention"],
+                                       "attention", "layer"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
                          "bootstrap: the full-slot bootstrap workload on the same chain; "
                          "linear: one 4096x4096 feature-major linear over 128 tokens; "
                          "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer; "
-                         "attention: the causal attention of a layer")
+                         "attention: the causal attention of a layer; "
+                         "layer: one whole encrypted decoder layer on a deeper chain")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -120,6 +123,9 @@ def main() -> int:
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
               flush=True)
+        return 0
+    if args.mode == "layer":
+        print(json.dumps({"fm_layer": measure_fm_layer(warmup=args.warmup)}), flush=True)
         return 0
     if args.mode == "attention":
         spec.rotations = ()
@@ -263,6 +269,10 @@ def main() -> int:
     if not args.no_attention:
         # the causal attention of a decoder layer on the same chain
         result["fm_attention"] = measure_fm_attention(client, ctx)
+    if not args.no_layer:
+        # one whole layer on a deeper chain; this chain's keys are freed first
+        ctx.close()
+        result["fm_layer"] = measure_fm_layer()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -539,6 +549,131 @@ def measure_fm_attention(client, ctx, limbs: int = 34, warmup: int = 1) -> dict:
         "score_abs_max": float(np.abs(np.where(valid, s, 0)).max()),
         "rotation_keygen_s": round(keygen_s, 2),
         "rotation_keys": len(attention_rotations(geo)),
+    }
+
+
+# A chain that holds one whole decoder layer without a refresh: 60-bit q_0 +
+# 71 x 40-bit primes, dnum 5 (digits of 15 primes), 15 special primes of 44 bits
+LAYER_PARAMS = dict(log_n=16, depth=71, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+
+
+def randomized_hadamard(dim: int, seed: int) -> np.ndarray:
+    """Orthogonal ``H diag(s) / sqrt(dim)`` (Sylvester Hadamard, seeded random
+    signs): the QuaRot-style rotation of the residual basis."""
+    h = np.ones((1, 1))
+    while h.shape[0] < dim:
+        h = np.block([[h, h], [h, -h]])
+    s = np.random.default_rng(seed).choice([-1.0, 1.0], dim)
+    return h * s[None, :] / np.sqrt(dim)
+
+
+def measure_fm_layer(warmup: int = 0) -> dict:
+    """One Llama-3-8B decoder layer over 128 tokens, end to end and encrypted
+    (d=4096, 32 query / 8 key-value heads of 128, SwiGLU 14336, RMSNorm),
+    on a chain deep enough for the whole layer (LAYER_PARAMS, no refresh).
+    Weights N(0, 0.02) in a residual basis rotated by a seeded randomized
+    Hadamard, inputs N(0, 1), seed 0; Alg2 softmax with 3 rounds on scores
+    in [-8, 8].  The error is against the same layer in fp64 with exact
+    softmax.  The refreshes a shallower chain would add are measured
+    separately (`bootstrap`)."""
+    from easyfhe import fhe
+    from easyfhe.chebyshev import evaluate_direct
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_depth, decoder_layer_fhe,
+                                     decoder_layer_rotations)
+    from feature_major.rope import rope_angles
+
+    T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
+    ap = LayerApproximations(rsqrt_entry(0.25, 4.0, 31), rsqrt_entry(0.25, 4.0, 31),
+                             silu_entry(-12.0, 12.0, 63),
+                             SoftmaxConfig(rounds=3, shift=8.0, bound=8.0, exp_degree=9,
+                                           first_inverse_degree=31, inverse_degree=47))
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
+    spec = fhe.CKKSContextSpec(**LAYER_PARAMS, seed=0,
+                               rotations=decoder_layer_rotations(lay, H, hd))
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    ctx.synchronize()
+    keygen_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    R = randomized_hadamard(D, 1)
+    wq = rng.normal(0, 0.02, (D, D)) @ R
+    wk = rng.normal(0, 0.02, (KV * hd, D)) @ R
+    wv = rng.normal(0, 0.02, (KV * hd, D)) @ R
+    wo = R.T @ rng.normal(0, 0.02, (D, D))
+    G = rng.normal(0, 0.02, (I, D)) @ R
+    U = rng.normal(0, 0.02, (I, D)) @ R
+    Dn = R.T @ rng.normal(0, 0.02, (D, I))
+    x = rng.normal(0, 1, (T, D))
+    packed = lay.pack(x)
+    xc = [client.encrypt(packed[i], enc_id=500000 + i) for i in range(lay.cipher_count)]
+    t0 = time.perf_counter()
+    w = DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+                            intermediate=I, approx=ap, layout=lay, context=ctx)
+    ctx.synchronize()
+    upload_s = time.perf_counter() - t0
+    for _ in range(max(0, warmup)):
+        decoder_layer_fhe(xc, w, crypto_context=ctx).release()
+    ctx.synchronize()
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    res = decoder_layer_fhe(xc, w, crypto_context=ctx)
+    ev1.record()
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    got = lay.unpack(np.stack([client.decrypt(o) for o in res.ciphers]))
+    limbs_out = res.output_limbs
+    stages = dict(res.stage_seconds)
+    res.release()
+    w.close()
+    mem = ctx.memory_info()
+    ctx.close()
+
+    # fp64 reference: the same layer with the fitted series and exact softmax
+    def rms(a, e):
+        var = np.mean(a * a, axis=-1, keepdims=True)
+        return a * evaluate_direct(var, e["coefficients"], *e["fit_interval"])
+
+    def rope(a, heads):
+        ang = rope_angles(np.arange(T), hd)
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        h = a.reshape(T, heads, hd)
+        lo, hi = h[..., :hd // 2], h[..., hd // 2:]
+        return np.concatenate([lo * c - hi * s, hi * c + lo * s], -1).reshape(T, -1)
+
+    rep = lambda m: np.repeat(m.reshape(KV, hd, -1), H // KV, axis=0).reshape(H * hd, -1)  # noqa: E731
+    n1 = rms(x, ap.input_norm)
+    q, k, v = rope(n1 @ wq.T, H), rope(n1 @ rep(wk).T, H), n1 @ rep(wv).T
+    qh, kh, vh = (a.reshape(T, H, hd).transpose(1, 0, 2) for a in (q, k, v))
+    sc = qh @ kh.transpose(0, 2, 1) / np.sqrt(hd)
+    valid = np.tril(np.ones((T, T), dtype=bool))[None]
+    m = np.where(valid, sc, -np.inf)
+    e = np.where(valid, np.exp(m - m.max(-1, keepdims=True)), 0.0)
+    att = ((e / e.sum(-1, keepdims=True)) @ vh).transpose(1, 0, 2).reshape(T, D)
+    h1 = x + att @ wo.T
+    n2 = rms(h1, ap.post_attention_norm)
+    g = n2 @ G.T
+    want = h1 + (evaluate_direct(g, ap.silu["coefficients"], *ap.silu["fit_interval"])
+                 * (n2 @ U.T)) @ Dn.T
+    return {
+        "seconds": round(wall, 3),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 3),
+        "workload": "one Llama-3-8B decoder layer (d=4096, 32/8 heads x 128, SwiGLU 14336), "
+                    "128 tokens in 16 ciphertexts of 8 lanes, N=2^16, Q=1x60b+71x40b, dnum=5, "
+                    f"P=15x44b; {ctx.L} -> {limbs_out} limbs, no refresh "
+                    f"(depth {decoder_layer_depth(ap, T)})",
+        "stages_s": {k2: round(v2, 3) for k2, v2 in stages.items()},
+        "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
+        "output_abs_max": float(np.abs(want).max()),
+        "score_abs_max": float(np.abs(np.where(valid, sc, 0)).max()),
+        "rotation_keys": len(spec.rotations),
+        "keygen_s": round(keygen_s, 2),
+        "weight_upload_s": round(upload_s, 2),
+        "device_memory_gib": {k2: round(v2 / 2 ** 30, 1) for k2, v2 in mem.items()},
     }
 
 
