@@ -58,8 +58,21 @@ static void require(bool cond, const std::string &msg) {
 // next kernel on that stream without a synchronisation.
 // ===========================================================================
 
-void *Pool::alloc(size_t bytes) {
+// Size classes: 256-byte granularity up to 1 MiB, then eight classes per
+// octave (at most 1/8 over the request), so that the blocks of neighbouring
+// modulus levels share classes and a computation walking down the chain
+// reuses its cache instead of accumulating one class per limb count.
+static size_t pool_class(size_t bytes) {
   bytes = (bytes + 255) & ~(size_t)255;
+  if (bytes <= ((size_t)1 << 20)) return bytes;
+  int e = 63 - __builtin_clzll((unsigned long long)bytes);
+  const size_t step = (size_t)1 << (e - 3);
+  return (bytes + step - 1) / step * step;
+}
+
+void *Pool::alloc(size_t bytes) {
+  bytes = pool_class(bytes);
+  last_use_[bytes] = ++clock_;
   auto it = free_.find(bytes);
   void *p = nullptr;
   if (it != free_.end() && !it->second.empty()) {
@@ -68,8 +81,7 @@ void *Pool::alloc(size_t bytes) {
     cached -= bytes;
   } else if (hipMalloc(&p, bytes) != hipSuccess) {
     (void)hipGetLastError();
-    trim();
-    HIPCHECK(hipMalloc(&p, bytes));
+    if (!evict_for(bytes, &p)) HIPCHECK(hipMalloc(&p, bytes));
   }
   live += bytes;
   live_[p] = bytes;
@@ -78,7 +90,7 @@ void *Pool::alloc(size_t bytes) {
 
 void Pool::release(void *p, size_t bytes) {
   if (!p) return;
-  bytes = (bytes + 255) & ~(size_t)255;
+  bytes = pool_class(bytes);
   live_.erase(p);
   free_[bytes].push_back(p);
   live -= bytes;
@@ -104,6 +116,26 @@ static u64 g_next_serial = 1;
 static bool owner_alive(const ckks_context *c, u64 serial) {
   auto it = g_live_contexts.find(const_cast<ckks_context *>(c));
   return it != g_live_contexts.end() && it->second == serial;
+}
+
+// Out of device memory: free the cached size classes least recently used
+// first, retrying after each, so that the classes the running computation
+// cycles through stay cached.
+bool Pool::evict_for(size_t bytes, void **p) {
+  std::vector<std::pair<u64, size_t>> order;  // (last use, class)
+  for (auto &kv : free_)
+    if (!kv.second.empty()) order.push_back({last_use_[kv.first], kv.first});
+  std::sort(order.begin(), order.end());
+  (void)hipDeviceSynchronize();
+  for (auto &e : order) {
+    auto &v = free_[e.second];
+    for (void *q : v) (void)hipFree(q);
+    cached -= e.second * v.size();
+    v.clear();
+    if (hipMalloc(p, bytes) == hipSuccess) return true;
+    (void)hipGetLastError();
+  }
+  return false;
 }
 
 void Pool::trim() {

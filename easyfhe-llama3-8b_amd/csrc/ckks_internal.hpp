@@ -137,9 +137,12 @@ __device__ __forceinline__ int prime_of(int limb, int q_limbs, int L) {
 struct Pool {
   std::unordered_map<size_t, std::vector<void *>> free_;
   std::unordered_map<void *, size_t> live_;
+  std::unordered_map<size_t, u64> last_use_;  // size class -> allocation clock
+  u64 clock_ = 0;
   size_t live = 0, cached = 0;
   void *alloc(size_t bytes);
   void release(void *p, size_t bytes);
+  bool evict_for(size_t bytes, void **p);
   void trim();
   void release_all();
 };

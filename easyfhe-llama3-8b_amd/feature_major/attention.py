@@ -16,10 +16,12 @@ for ``delta = a L + r``; ``K^(r)`` is a lane shift with carry into the next
 ciphertext (two rotations and two masks).  For each query ciphertext and
 delta, ``Q_c * K^(delta)_c`` holds the per-feature products; their sums over
 each head's hd features come from a rotate-and-add tree, run in groups of L
-offsets: log2(L) steps of partial sums, a mask keeping every L-th feature,
-the L products of a group interleaved into one ciphertext, the remaining
-log2(hd / L) steps, and a final mask-and-shift that places group a at feature
-offsets ``a L .. a L + L - 1``.  Depth: lane-shift mask, product, two masks.
+offsets: for offset r of a group, the sum of L consecutive features of its
+product lands on the features ``= r mod L`` (one extended-basis hoisted MAC
+over the L rotations ``(e - r) L``, the mask in its plaintexts, batched over
+the groups), the remaining log2(hd / L) tree steps, and a final mask-and-shift
+that places group a at feature offsets ``a L .. a L + L - 1``.  Depth:
+lane-shift mask, product, MAC mask, merge mask.
 
 Softmax ("Algorithm 2", softmax.py:648-1262).  ``y = exp((s - U) / 2^k)`` by a
 Chebyshev series (its domain map folded into the last QK mask), causal mask,
@@ -120,6 +122,11 @@ class AttentionGeometry:
         f = np.arange(self.slots) // self.lanes
         return np.where((f % int(modulus)) < int(below), float(value), 0.0)
 
+    def residue_mask(self, modulus: int, residue: int) -> np.ndarray:
+        """1 on features f with ``f mod modulus == residue``."""
+        f = np.arange(self.slots) // self.lanes
+        return ((f % int(modulus)) == int(residue)).astype(np.float64)
+
     def causal_mask(self, c: int) -> np.ndarray:
         """Score-layout validity of query ciphertext c: key (i + delta) mod T
         is at most i (delta = 0, or the offset wraps past T)."""
@@ -182,7 +189,7 @@ def qk_rotations(geo: AttentionGeometry) -> set[int]:
     L, hd = geo.lanes, int(geo.head_dim)
     keys = set()
     for r in range(1, L):
-        keys.update((r, r - L, -r * L))
+        keys.update((r, r - L, r * L, -r * L))
     keys.update(L << b for b in range(_log2(hd, "head_dim")))
     keys.update(-a * L * L for a in range(1, geo.ciphers))
     return {k for k in keys if k}
@@ -219,6 +226,12 @@ def _encode(ctx, rows, limbs: int, scale: float | None = None) -> list:
     return fhe.encode_rows(ctx, rows, limbs=int(limbs),
                            scale=float(scale) if scale else ctx.scale_at(int(limbs)),
                            slots=ctx.max_slots)
+
+
+def _encode_ext(ctx, rows, limbs: int) -> list:
+    rows = np.atleast_2d(np.asarray(rows, dtype=np.float64))
+    return fhe.encode_rows(ctx, rows, limbs=int(limbs), scale=ctx.scale_at(int(limbs)),
+                           slots=ctx.max_slots, is_ext=True)
 
 
 def _mul_pt_rescale(cts, pts, ctx) -> list:
@@ -336,27 +349,31 @@ def qk_scores(query, key, geo: AttentionGeometry, *, crypto_context,
             prods = _mul_relin_rescale([qa[c]] * (groups * L),
                                        [_shifted(shifts, geo, c, d) for d in range(groups * L)],
                                        ctx)
-            part = _rotate_add_tree(prods, [L << b for b in range(sb)], ctx)
+            lp = int(prods[0].state.cur_limbs)
+            # group a interleaves its L offsets r at features = r mod L, each
+            # holding the sum of L consecutive features of its product:
+            #   Y_a = sum_r mask_r * sum_e rot(P_(a L + r), (e - r) L)
+            # one extended-basis hoisted MAC per r over all groups (one ModUp,
+            # L key inner products and one ModDown per product; the mask rides
+            # in the MAC's plaintexts)
+            acc = None
+            for r in range(L):
+                pt = _encode_ext(ctx, geo.residue_mask(L, r), lp)
+                try:
+                    m = fhe.hoisted_mac_sum_ext_many(
+                        [prods[a * L + r] for a in range(groups)],
+                        [(e - r) * L for e in range(L)], pt * L, 0, 1, ctx)
+                finally:
+                    _release(pt)
+                if acc is None:
+                    acc = m
+                else:
+                    nxt = [fhe.homo_add(x, y, ctx) for x, y in zip(acc, m)]
+                    _release(acc + m)
+                    acc = nxt
             _release(prods)
-            lp = int(part[0].state.cur_limbs)
-            m8 = _encode(ctx, geo.feature_mask(L, 1), lp)
-            masked = _mul_pt_rescale(part, m8, ctx)
-            _release(part + m8)
-            packed = []
-            for a in range(groups):
-                acc = None
-                for r in range(L):
-                    x = masked[a * L + r]
-                    y = x.deep_copy() if r == 0 else fhe.homo_rotate(x, -r * L, ctx)
-                    if acc is None:
-                        acc = y
-                    else:
-                        nxt = fhe.homo_add(acc, y, ctx)
-                        acc.release()
-                        y.release()
-                        acc = nxt
-                packed.append(acc)
-            _release(masked)
+            packed = fhe.rescale_many(acc, ctx)
+            _release(acc)
             zs.append(_rotate_add_tree(packed, [L << b for b in range(sb, hb)], ctx))
             _release(packed)
         sync()
