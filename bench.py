@@ -553,8 +553,8 @@ def measure_fm_attention(client, ctx, limbs: int = 34, warmup: int = 1) -> dict:
 
 
 # A chain that holds one whole decoder layer without a refresh: 60-bit q_0 +
-# 71 x 40-bit primes, dnum 5 (digits of 15 primes), 15 special primes of 44 bits
-LAYER_PARAMS = dict(log_n=16, depth=71, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+# 72 x 40-bit primes, dnum 5 (digits of 15 primes), 15 special primes of 44 bits
+LAYER_PARAMS = dict(log_n=16, depth=72, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
 
 
 def randomized_hadamard(dim: int, seed: int) -> np.ndarray:
@@ -663,7 +663,7 @@ def measure_fm_layer(warmup: int = 0) -> dict:
         "seconds": round(wall, 3),
         "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 3),
         "workload": "one Llama-3-8B decoder layer (d=4096, 32/8 heads x 128, SwiGLU 14336), "
-                    "128 tokens in 16 ciphertexts of 8 lanes, N=2^16, Q=1x60b+71x40b, dnum=5, "
+                    "128 tokens in 16 ciphertexts of 8 lanes, N=2^16, Q=1x60b+72x40b, dnum=5, "
                     f"P=15x44b; {ctx.L} -> {limbs_out} limbs, no refresh "
                     f"(depth {decoder_layer_depth(ap, T)})",
         "stages_s": {k2: round(v2, 3) for k2, v2 in stages.items()},

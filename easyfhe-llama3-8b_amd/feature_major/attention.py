@@ -33,12 +33,13 @@ rows (``1/x`` on a narrow interval), optionally refreshed by a bootstrap, and
 broadcast back over the head blocks.  The main stream loses two levels per
 round.
 
-PV.  ``O_c = sum_delta B_delta(P_c) * V^(delta)_c`` where ``B_delta`` moves
-the probabilities of offset delta to the head's first feature (one hoisted
-rotation per offset), masks it and spreads it over the head's hd features;
+PV.  ``O_c = sum_delta B_delta(P_c) * V^(delta)_c`` where ``B_delta`` spreads
+the probabilities of offset delta over the head's hd features;
 ``V^(delta)`` is the shifted value stream built like ``K^(delta)``.  The
-products are summed as degree-2 ciphertexts and relinearised once per query
-ciphertext.  Depth: mask, product.
+spread runs in groups of L offsets (one hoisted rotation per group, a tree
+over strides of L features, and extended-basis MACs whose masks fill the
+rest; see pv_output).  The products are summed as degree-2 ciphertexts and
+relinearised once per query ciphertext.  Depth: mask, MAC, product.
 
 Grouped-query attention uses key/value projections whose rows are repeated
 for the query heads of each group (``kv_repeat_rows``): the streams then
@@ -205,10 +206,10 @@ def softmax_rotations(geo: AttentionGeometry) -> set[int]:
 
 def pv_rotations(geo: AttentionGeometry) -> set[int]:
     L, hd = geo.lanes, int(geo.head_dim)
-    keys = {d * L for d in range(1, geo.seq_len)}
-    keys.update(-(L << b) for b in range(_log2(hd, "head_dim")))
+    keys = {a * L * L for a in range(1, -(-geo.seq_len // L))}
+    keys.update(-(L * L << b) for b in range(_log2(hd // L, "head_dim / lanes")))
     for r in range(1, L):
-        keys.update((r, r - L))
+        keys.update((r, r - L, -r * L))
     return keys
 
 
@@ -577,13 +578,23 @@ def _to_limbs(cts, limbs: int, ctx) -> list:
 def pv_output(probs, value, geo: AttentionGeometry, *, crypto_context) -> StageResult:
     """Feature-major ``O[i, h hd + d] = sum_j P[h, i, j] V[j, h hd + d]`` from
     score-layout probabilities (zero at invalid offsets) and a feature-major
-    value stream; inputs are not consumed."""
+    value stream; inputs are not consumed.
+
+    The probabilities of offset ``delta = a L + m`` are spread over their
+    head in groups of L offsets: ``G_a = rot(P_c, a L)`` (in features, one
+    hoisted rotation per group) masked to each head's first L features, spread
+    by the tree over strides ``L 2^b`` (copies at every feature ``= m mod L``),
+    then one extended-basis hoisted MAC per m over all groups,
+    ``B_(a L + m) = sum_k mask_k * rot(W_a, m - k)`` (features ``= k mod L``
+    read the copy at residue m of their own L-block), which fills the
+    remaining L - 1 features of each block.  Depth: mask, MAC, product."""
     ctx = _ctx(crypto_context)
     ps, vs = list(probs), list(value)
     n, L, hd, T = geo.ciphers, geo.lanes, int(geo.head_dim), geo.seq_len
     if len(ps) != n or len(vs) != n:
         raise ValueError(f"PV expects {n} probability and value ciphertexts.")
-    hb = _log2(hd, "head_dim")
+    sb, hb = _log2(L, "lanes"), _log2(hd, "head_dim")
+    groups = -(-T // L)
     stage = {}
     sync = ctx.synchronize
     t0 = time.perf_counter()
@@ -594,15 +605,30 @@ def pv_output(probs, value, geo: AttentionGeometry, *, crypto_context) -> StageR
     t_spread = t_prod = 0.0
     try:
         lp = int(ps[0].state.cur_limbs)
-        first = _encode(ctx, geo.feature_mask(hd, 1), lp)
+        first = _encode(ctx, geo.feature_mask(hd, L), lp)
+        lw = lp - 1
+        fill = [_encode_ext(ctx, geo.residue_mask(L, r), lw) for r in range(L)]
         for c in range(n):
             t0 = time.perf_counter()
-            offs = [d * L for d in range(T)]
-            rots = fhe.prepare_hoisted_baby_rotations(ps[c], offs, ctx)
+            rots = fhe.prepare_hoisted_baby_rotations(ps[c], [a * L * L for a in range(groups)],
+                                                      ctx)
             masked = _mul_pt_rescale(list(rots), first, ctx)
             _release(rots)
-            spread = _rotate_add_tree(masked, [-(L << b) for b in range(hb)], ctx)
+            ws = _rotate_add_tree(masked, [-(L * L << b) for b in range(hb - sb)], ctx)
             _release(masked)
+            spread = [None] * (groups * L)
+            for m in range(L):
+                # features = k mod L take the copy at residue m of their own
+                # block, (m - k) features away (up or down, inside the head)
+                pts = [fill[k][0] for k in range(L)]
+                acc = fhe.hoisted_mac_sum_ext_many(ws, [(m - k) * L for k in range(L)], pts, 0, 1,
+                                                   ctx)
+                res = fhe.rescale_many(acc, ctx)
+                _release(acc)
+                for a in range(groups):
+                    spread[a * L + m] = res[a]
+            _release(ws)
+            spread = spread[:T]
             sync()
             t_spread += time.perf_counter() - t0
             t0 = time.perf_counter()
@@ -630,12 +656,14 @@ def pv_output(probs, value, geo: AttentionGeometry, *, crypto_context) -> StageR
             sync()
             t_prod += time.perf_counter() - t0
         _release(first)
+        for f in fill:
+            _release(f)
         stage["probability_spread"] = t_spread
         stage["products"] = t_prod
         return StageResult(tuple(out), stage)
     finally:
-        for s in shifts:
-            _release(s)
+        for s_ in shifts:
+            _release(s_)
 
 
 def attention_fhe(query, key, value, geo: AttentionGeometry, cfg: SoftmaxConfig, *,

@@ -17,7 +17,7 @@ counterpart is approx/layer.py:64-149):
 * residual additions with exact-scale matching (``rmsnorm.residual_add``).
 
 The layer runs without refreshes here: it needs a chain that holds its depth
-(``decoder_layer_depth``).  Bootstrap placement for a chain that does not is
+(``decoder_layer_depth``: 72 levels with a 3-round softmax).  Bootstrap placement for a chain that does not is
 ``easyfhe.bs.placement``'s.
 """
 
@@ -61,7 +61,7 @@ class LayerApproximations:
 
 def decoder_layer_depth(approx: LayerApproximations, seq_len: int) -> int:
     return (rmsnorm_depth(approx.input_norm) + 1 + 1 + 4 + softmax_depth(approx.softmax, seq_len)
-            + 2 + 1 + 1 + rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu))
+            + 3 + 1 + 1 + rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu))
 
 
 def decoder_layer_rotations(layout: FeatureMajorPrefillLayout, heads: int,
