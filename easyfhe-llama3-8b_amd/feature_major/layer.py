@@ -219,5 +219,162 @@ def decoder_layer_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_con
         op.close()
 
 
+# ---------------------------------------------------------------------------
+# the layer with refreshes (bootstraps included)
+# ---------------------------------------------------------------------------
+
+
+def refresh_stream(ciphers, *, crypto_context, program, value_bound: float = 1.0,
+                   group: int = 8) -> list:
+    """Refresh a real feature-major stream (reference operators/norm/refresh.py:96-150):
+    values divided by a power of two S >= value_bound through the recorded
+    scale (no level), adjacent ciphertexts paired as ``a + i b``, the pairs
+    bootstrapped in batched groups (keys and diagonals read once per group),
+    the conjugation split's factor 2 and S returned to the recorded scale.
+    Inputs are not consumed."""
+    from easyfhe.bs import openfhe as bs
+
+    ctx = _ctx(crypto_context)
+    S = 2.0 ** max(0, int(np.ceil(np.log2(max(float(value_bound), 1.0)))))
+    views = []
+    for c in ciphers:
+        v = c.deep_copy()
+        v.set_scale(float(c.state.scaling_factor) * S, 1)
+        views.append(v)
+    try:
+        pairs = pair_real_ciphers(views, crypto_context=ctx)
+    finally:
+        _release(views)
+    try:
+        boots = bs.bootstrap_many(list(pairs), ctx, program, group=int(group))
+    finally:
+        _release(pairs)
+    try:
+        out = list(split_complex_ciphers_twice(boots, crypto_context=ctx, halve=True))
+    finally:
+        _release(boots)
+    for o in out:
+        o.set_scale(float(o.state.scaling_factor) / S, 1)
+    return out
+
+
+def _land_on_ladder(cts, ctx) -> list:
+    """One level down, at exactly the scale of the next prime a series drops
+    first (the fixed point of its scale ladder)."""
+    from .rmsnorm import match_scale
+
+    out = []
+    for c in cts:
+        limbs = int(c.state.cur_limbs) - 1
+        out.append(match_scale(c, limbs, float(int(ctx.primes()[limbs - 1])), ctx))
+    return out
+
+
+def refreshed_layer_depths(approx: LayerApproximations, seq_len: int) -> tuple[int, int, int]:
+    """Levels of the three blocks between refreshes: RMSNorm + Q/K/V + RoPE +
+    QK; the scores' landing + softmax + PV + W_o; RMSNorm + MLP."""
+    a = rmsnorm_depth(approx.input_norm) + 1 + 1 + 4
+    b = 1 + softmax_depth(approx.softmax, seq_len) + 3 + 1
+    c = rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu)
+    return a, b, c
+
+
+def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
+                                program, residual_bound: float = 32.0, group: int = 8,
+                                rope_theta: float = 500000.0) -> LayerResult:
+    """One decoder layer with its refreshes (three paired refresh points: the
+    residual stream before each RMSNorm, and the softmax's mapped scores;
+    the reference refreshes at the same places, graph.py:780-990,
+    operators/norm/refresh.py:153-344, the pre-exp checkpoint of
+    operators/attention/softmax.py).  ``program`` is a bootstrap program whose
+    outputs hold the deepest block plus one limb.  The input may sit at any
+    level; it is not consumed."""
+    ctx = _ctx(crypto_context)
+    lay, geo, ap = weights.layout, weights.geometry, weights.approx
+    a_depth, b_depth, c_depth = refreshed_layer_depths(ap, geo.seq_len)
+    sync = ctx.synchronize
+    stage: dict[str, float] = {}
+    t_start = time.perf_counter()
+    op = LinearOperator(context=ctx, token_lanes=geo.lanes)
+    keep: list = []
+    try:
+        t0 = time.perf_counter()
+        x = refresh_stream(input_ciphers, crypto_context=ctx, program=program,
+                           value_bound=residual_bound, group=group)
+        keep = x
+        sync()
+        stage["refresh_residual_1"] = time.perf_counter() - t0
+        if int(x[0].state.cur_limbs) < max(a_depth, b_depth, c_depth) + 1:
+            raise ValueError("the bootstrap program's outputs are too shallow for the layer.")
+        t0 = time.perf_counter()
+        n1 = rmsnorm_fhe(x, np.zeros(1), coeffs=ap.input_norm, layout=lay, crypto_context=ctx)
+        z = pair_real_ciphers(n1.ciphers, crypto_context=ctx)
+        n1.release()
+        q = _paired_projection(op, z, weights.q, ctx)
+        k = _paired_projection(op, z, weights.k, ctx)
+        v = _paired_projection(op, z, weights.v, ctx)
+        op.release_babies(z)
+        _release(z)
+        qr = rope_fhe(q, lay, head_dim=geo.head_dim, crypto_context=ctx, theta=rope_theta)
+        kr = rope_fhe(k, lay, head_dim=geo.head_dim, crypto_context=ctx, theta=rope_theta)
+        _release(q)
+        _release(k)
+        from .attention import pv_output, qk_scores, softmax_alg2
+
+        sa, sb_ = ap.softmax.score_map(1.0 / float(np.sqrt(geo.head_dim)))
+        scores = qk_scores(qr, kr, geo, crypto_context=ctx, output_scale=sa, output_offset=sb_)
+        _release(qr)
+        _release(kr)
+        sync()
+        stage["rmsnorm_qkv_rope_qk"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        sr = refresh_stream(scores.ciphers, crypto_context=ctx, program=program, value_bound=1.0,
+                            group=group)
+        scores.release()
+        sync()
+        stage["refresh_scores"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        landed = _land_on_ladder(sr, ctx)
+        _release(sr)
+        probs = softmax_alg2(landed, geo, ap.softmax, crypto_context=ctx)
+        _release(landed)
+        att = pv_output(probs.ciphers, v, geo, crypto_context=ctx)
+        probs.release()
+        _release(v)
+        za = pair_real_ciphers(att.ciphers, crypto_context=ctx)
+        att.release()
+        o = _paired_projection(op, za, weights.o, ctx)
+        op.release_babies(za)
+        _release(za)
+        h = residual_add(x, o, crypto_context=ctx)
+        _release(o)
+        _release(x)
+        keep = list(h)
+        sync()
+        stage["softmax_pv_output_residual"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        hr = refresh_stream(h, crypto_context=ctx, program=program, value_bound=residual_bound,
+                            group=group)
+        _release(h)
+        keep = hr
+        sync()
+        stage["refresh_residual_2"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n2 = rmsnorm_fhe(hr, np.zeros(1), coeffs=ap.post_attention_norm, layout=lay,
+                         crypto_context=ctx)
+        m = mlp_fhe(n2.ciphers, weights.mlp, silu=ap.silu, crypto_context=ctx, operator=op)
+        n2.release()
+        out = residual_add(hr, m.ciphers, crypto_context=ctx)
+        m.release()
+        sync()
+        stage["rmsnorm_mlp_residual"] = time.perf_counter() - t0
+        return LayerResult(tuple(out), time.perf_counter() - t_start, stage,
+                           int(out[0].state.cur_limbs))
+    finally:
+        _release(keep)
+        op.close()
+
+
 __all__ = ["DecoderLayerWeights", "LayerApproximations", "LayerResult", "decoder_layer_depth",
-           "decoder_layer_fhe", "decoder_layer_rotations"]
+           "decoder_layer_fhe", "decoder_layer_refreshed_fhe", "decoder_layer_rotations",
+           "refresh_stream", "refreshed_layer_depths"]

@@ -328,3 +328,64 @@ def test_decoder_layer_matches_poly_model():
           f"|out| {np.abs(model).max():.3g}, limbs 64 -> {res.output_limbs}, "
           f"{res.wall_seconds:.2f} s", flush=True)
     assert err < 1e-4, err
+
+
+FM_REFRESH = dict(log_n=13, depth=57, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+def test_refreshed_decoder_layer_matches_poly_model():
+    """The layer with its three paired refresh points (bootstraps of the
+    residual stream before each RMSNorm and of the softmax's mapped scores),
+    two layers in a row from a one-limb input, 64 tokens x 512 features at
+    N = 2^13: against the fp64 model of the same two layers.  The tolerance
+    covers six bootstraps at ~20 bits on values up to 32."""
+    from easyfhe.bs import openfhe as bs
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_refreshed_fhe, decoder_layer_rotations,
+                                     refreshed_layer_depths)
+
+    T, D, H, KV, hd, I = 64, 512, 4, 2, 128, 1408
+    lay0 = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=4096)
+    client, ctx = device_context(FM_REFRESH, rotations=decoder_layer_rotations(lay0, H, hd))
+    # the residual stream's variance grows past 4 by the second layer
+    norm = rsqrt_entry(0.5, 16.0, 63)
+    ap = LayerApproximations(norm, norm, silu_entry(), SoftmaxConfig(rounds=2, shift=4.0,
+                                                                     bound=4.0))
+    need = max(refreshed_layer_depths(ap, T)) + 1
+    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3), output_levels=0))
+    out_levels = ctx.L - probe.depth_limbs - 1
+    assert out_levels + 1 >= need, (out_levels, need)
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3),
+                                             output_levels=out_levels))
+    rng = np.random.default_rng(13)
+    x = rng.normal(0, 1, (T, D))
+    sd = 1.0 / np.sqrt(D)
+    wq, wo = rng.normal(0, sd, (D, D)), rng.normal(0, sd, (D, D))
+    wk, wv = rng.normal(0, sd, (KV * hd, D)), rng.normal(0, sd, (KV * hd, D))
+    G, U = rng.normal(0, sd, (I, D)), rng.normal(0, sd, (I, D))
+    Dn = rng.normal(0, 1.0 / np.sqrt(I), (D, I))
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=ctx.max_slots)
+    packed = lay.pack(x)
+    xc = [client.encrypt(packed[i], cur_limbs=1, enc_id=1800 + i) for i in range(lay.cipher_count)]
+    sm = ap.softmax
+    kw = dict(heads=H, kv_heads=KV, head_dim=hd, input_norm=ap.input_norm,
+              post_attention_norm=ap.post_attention_norm, silu=ap.silu,
+              probs_fn=lambda s: LN.softmax_alg2_numpy(s, sm.exp(), sm.first_inverse(),
+                                                       sm.inverse(T), rounds=sm.rounds,
+                                                       shift=sm.shift))
+    with DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+                             intermediate=I, approx=ap, layout=lay, context=ctx) as w:
+        r1 = decoder_layer_refreshed_fhe(xc, w, crypto_context=ctx, program=prog)
+        r2 = decoder_layer_refreshed_fhe(r1.ciphers, w, crypto_context=ctx, program=prog)
+    want1 = LN.decoder_layer_numpy(x, wq, wk, wv, wo, G, U, Dn, **kw)
+    want2 = LN.decoder_layer_numpy(want1, wq, wk, wv, wo, G, U, Dn, **kw)
+    got1 = _decrypt_stream(client, lay, r1.ciphers)
+    got2 = _decrypt_stream(client, lay, r2.ciphers)
+    e1, e2 = float(np.max(np.abs(got1 - want1))), float(np.max(np.abs(got2 - want2)))
+    print(f"refreshed layers 64x512: max err {e1:.3g} / {e2:.3g} vs model, |out| "
+          f"{np.abs(want2).max():.3g}, limbs out {r1.output_limbs}, {r2.wall_seconds:.2f} s, "
+          f"stages {r2.stage_seconds}", flush=True)
+    assert e1 < 1e-3 and e2 < 2e-3, (e1, e2)
