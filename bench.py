@@ -89,8 +89,10 @@ def main() -> int:
                     help="skip the attention measurement of the default run")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the whole-layer measurement of the default run")
+    ap.add_argument("--layers", type=int, default=2,
+                    help="layers of the refreshed-layer measurement (layers mode)")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp",
-                                       "attention", "layer"],
+                                       "attention", "layer", "layers"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
@@ -98,7 +100,8 @@ def main() -> int:
                          "linear: one 4096x4096 feature-major linear over 128 tokens; "
                          "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer; "
                          "attention: the causal attention of a layer; "
-                         "layer: one whole encrypted decoder layer on a deeper chain")
+                         "layer: one whole encrypted decoder layer on a deeper chain; "
+                         "layers: consecutive layers with their bootstraps (--layers)")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -123,6 +126,9 @@ def main() -> int:
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
               flush=True)
+        return 0
+    if args.mode == "layers":
+        print(json.dumps({"fm_layers": measure_fm_layers(args.layers)}), flush=True)
         return 0
     if args.mode == "layer":
         print(json.dumps({"fm_layer": measure_fm_layer(warmup=args.warmup)}), flush=True)
@@ -567,6 +573,55 @@ def randomized_hadamard(dim: int, seed: int) -> np.ndarray:
     return h * s[None, :] / np.sqrt(dim)
 
 
+def _memory_summary(mem: dict) -> dict:
+    """Pool figures in GiB (byte counts) beside the allocation count."""
+    return {(k[:-6] + "_gib" if k.endswith("_bytes") else k):
+            (round(v / 2 ** 30, 1) if k.endswith("_bytes") else v) for k, v in mem.items()}
+
+
+def _layer_weights(rng, D, KV, hd, I, R):
+    """Weights N(0, 0.02) in a residual basis rotated by R (QuaRot-style)."""
+    return dict(q=rng.normal(0, 0.02, (D, D)) @ R, k=rng.normal(0, 0.02, (KV * hd, D)) @ R,
+                v=rng.normal(0, 0.02, (KV * hd, D)) @ R, o=R.T @ rng.normal(0, 0.02, (D, D)),
+                gate=rng.normal(0, 0.02, (I, D)) @ R, up=rng.normal(0, 0.02, (I, D)) @ R,
+                down=R.T @ rng.normal(0, 0.02, (D, I)))
+
+
+def _layer_fp64(x, w, ap, H, KV, hd):
+    """The layer in fp64 with the fitted RMSNorm / SiLU series and exact
+    causal softmax (the plaintext layer the encrypted one approximates)."""
+    from easyfhe.chebyshev import evaluate_direct
+    from feature_major.rope import rope_angles
+
+    T, D = x.shape
+
+    def rms(a, e):
+        var = np.mean(a * a, axis=-1, keepdims=True)
+        return a * evaluate_direct(var, e["coefficients"], *e["fit_interval"])
+
+    def rope(a):
+        ang = rope_angles(np.arange(T), hd)
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        h = a.reshape(T, H, hd)
+        lo, hi = h[..., :hd // 2], h[..., hd // 2:]
+        return np.concatenate([lo * c - hi * s, hi * c + lo * s], -1).reshape(T, -1)
+
+    rep = lambda m: np.repeat(m.reshape(KV, hd, -1), H // KV, axis=0).reshape(H * hd, -1)  # noqa: E731
+    n1 = rms(x, ap.input_norm)
+    q, k, v = rope(n1 @ w["q"].T), rope(n1 @ rep(w["k"]).T), n1 @ rep(w["v"]).T
+    qh, kh, vh = (a.reshape(T, H, hd).transpose(1, 0, 2) for a in (q, k, v))
+    sc = qh @ kh.transpose(0, 2, 1) / np.sqrt(hd)
+    valid = np.tril(np.ones((T, T), dtype=bool))[None]
+    m = np.where(valid, sc, -np.inf)
+    e = np.where(valid, np.exp(m - m.max(-1, keepdims=True)), 0.0)
+    att = ((e / e.sum(-1, keepdims=True)) @ vh).transpose(1, 0, 2).reshape(T, D)
+    h1 = x + att @ w["o"].T
+    n2 = rms(h1, ap.post_attention_norm)
+    g = n2 @ w["gate"].T
+    act = evaluate_direct(g, ap.silu["coefficients"], *ap.silu["fit_interval"]) * (n2 @ w["up"].T)
+    return h1 + act @ w["down"].T, float(np.abs(np.where(valid, sc, 0)).max())
+
+
 def measure_fm_layer(warmup: int = 0) -> dict:
     """One Llama-3-8B decoder layer over 128 tokens, end to end and encrypted
     (d=4096, 32 query / 8 key-value heads of 128, SwiGLU 14336, RMSNorm),
@@ -577,14 +632,12 @@ def measure_fm_layer(warmup: int = 0) -> dict:
     softmax.  The refreshes a shallower chain would add are measured
     separately (`bootstrap`)."""
     from easyfhe import fhe
-    from easyfhe.chebyshev import evaluate_direct
     from feature_major import FeatureMajorPrefillLayout
     from feature_major.approx import rsqrt_entry, silu_entry
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_depth, decoder_layer_fhe,
                                      decoder_layer_rotations)
-    from feature_major.rope import rope_angles
 
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     ap = LayerApproximations(rsqrt_entry(0.25, 4.0, 31), rsqrt_entry(0.25, 4.0, 31),
@@ -599,19 +652,13 @@ def measure_fm_layer(warmup: int = 0) -> dict:
     ctx.synchronize()
     keygen_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
-    R = randomized_hadamard(D, 1)
-    wq = rng.normal(0, 0.02, (D, D)) @ R
-    wk = rng.normal(0, 0.02, (KV * hd, D)) @ R
-    wv = rng.normal(0, 0.02, (KV * hd, D)) @ R
-    wo = R.T @ rng.normal(0, 0.02, (D, D))
-    G = rng.normal(0, 0.02, (I, D)) @ R
-    U = rng.normal(0, 0.02, (I, D)) @ R
-    Dn = R.T @ rng.normal(0, 0.02, (D, I))
+    wm = _layer_weights(rng, D, KV, hd, I, randomized_hadamard(D, 1))
     x = rng.normal(0, 1, (T, D))
     packed = lay.pack(x)
     xc = [client.encrypt(packed[i], enc_id=500000 + i) for i in range(lay.cipher_count)]
     t0 = time.perf_counter()
-    w = DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+    w = DecoderLayerWeights(wm["q"], wm["k"], wm["v"], wm["o"], wm["gate"], wm["up"], wm["down"],
+                            heads=H, kv_heads=KV, head_dim=hd,
                             intermediate=I, approx=ap, layout=lay, context=ctx)
     ctx.synchronize()
     upload_s = time.perf_counter() - t0
@@ -633,32 +680,7 @@ def measure_fm_layer(warmup: int = 0) -> dict:
     mem = ctx.memory_info()
     ctx.close()
 
-    # fp64 reference: the same layer with the fitted series and exact softmax
-    def rms(a, e):
-        var = np.mean(a * a, axis=-1, keepdims=True)
-        return a * evaluate_direct(var, e["coefficients"], *e["fit_interval"])
-
-    def rope(a, heads):
-        ang = rope_angles(np.arange(T), hd)
-        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
-        h = a.reshape(T, heads, hd)
-        lo, hi = h[..., :hd // 2], h[..., hd // 2:]
-        return np.concatenate([lo * c - hi * s, hi * c + lo * s], -1).reshape(T, -1)
-
-    rep = lambda m: np.repeat(m.reshape(KV, hd, -1), H // KV, axis=0).reshape(H * hd, -1)  # noqa: E731
-    n1 = rms(x, ap.input_norm)
-    q, k, v = rope(n1 @ wq.T, H), rope(n1 @ rep(wk).T, H), n1 @ rep(wv).T
-    qh, kh, vh = (a.reshape(T, H, hd).transpose(1, 0, 2) for a in (q, k, v))
-    sc = qh @ kh.transpose(0, 2, 1) / np.sqrt(hd)
-    valid = np.tril(np.ones((T, T), dtype=bool))[None]
-    m = np.where(valid, sc, -np.inf)
-    e = np.where(valid, np.exp(m - m.max(-1, keepdims=True)), 0.0)
-    att = ((e / e.sum(-1, keepdims=True)) @ vh).transpose(1, 0, 2).reshape(T, D)
-    h1 = x + att @ wo.T
-    n2 = rms(h1, ap.post_attention_norm)
-    g = n2 @ G.T
-    want = h1 + (evaluate_direct(g, ap.silu["coefficients"], *ap.silu["fit_interval"])
-                 * (n2 @ U.T)) @ Dn.T
+    want, score_max = _layer_fp64(x, wm, ap, H, KV, hd)
     return {
         "seconds": round(wall, 3),
         "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 3),
@@ -669,11 +691,119 @@ def measure_fm_layer(warmup: int = 0) -> dict:
         "stages_s": {k2: round(v2, 3) for k2, v2 in stages.items()},
         "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
         "output_abs_max": float(np.abs(want).max()),
-        "score_abs_max": float(np.abs(np.where(valid, sc, 0)).max()),
+        "score_abs_max": score_max,
         "rotation_keys": len(spec.rotations),
         "keygen_s": round(keygen_s, 2),
         "weight_upload_s": round(upload_s, 2),
-        "device_memory_gib": {k2: round(v2 / 2 ** 30, 1) for k2, v2 in mem.items()},
+        "device_memory": _memory_summary(mem),
+    }
+
+
+# A chain for refreshed layers: bootstraps (budget (3,3), 26 limbs) return the
+# 40 limbs of a layer's deepest block (scores -> softmax -> PV -> W_o)
+REFRESH_PARAMS = dict(log_n=16, depth=65, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+
+
+def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
+    """Consecutive Llama-3-8B decoder layers over 128 tokens with their
+    refreshes (bootstraps included): per layer, paired batched refreshes of
+    the residual stream before each RMSNorm and of the softmax's mapped
+    scores (24 ciphertext bootstraps), on REFRESH_PARAMS.  The first layer
+    starts from a one-limb input; from the second on a layer runs in steady
+    state.  Weights N(0, 0.02) in a Hadamard-rotated residual basis,
+    `weight_sets` distinct sets cycled over the layers; inputs N(0, 1); seed
+    0.  The error is against the same layers in fp64 with exact softmax."""
+    from easyfhe import fhe
+    from easyfhe.bs import openfhe as bs
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_refreshed_fhe, decoder_layer_rotations,
+                                     refreshed_layer_depths)
+
+    T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
+    norm = rsqrt_entry(0.5, 16.0, 63)
+    ap = LayerApproximations(norm, norm, silu_entry(-12.0, 12.0, 63),
+                             SoftmaxConfig(rounds=3, shift=8.0, bound=8.0, exp_degree=9,
+                                           first_inverse_degree=31, inverse_degree=47))
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
+    spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=0,
+                               rotations=decoder_layer_rotations(lay, H, hd))
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3), output_levels=0))
+    out_levels = ctx.L - probe.depth_limbs - 1
+    probe.release()
+    need = max(refreshed_layer_depths(ap, T)) + 1
+    if out_levels + 1 < need:
+        raise ValueError(f"bootstrap outputs {out_levels + 1} limbs, the layer needs {need}")
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3),
+                                             output_levels=out_levels))
+    ctx.synchronize()
+    setup_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    R = randomized_hadamard(D, 1)
+    wsets = [_layer_weights(rng, D, KV, hd, I, R) for _ in range(max(1, weight_sets))]
+    x = rng.normal(0, 1, (T, D))
+    t0 = time.perf_counter()
+    dev = [DecoderLayerWeights(w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"],
+                               heads=H, kv_heads=KV, head_dim=hd, intermediate=I, approx=ap,
+                               layout=lay, context=ctx) for w in wsets]
+    ctx.synchronize()
+    upload_s = time.perf_counter() - t0
+    packed = lay.pack(x)
+    cur = [client.encrypt(packed[i], cur_limbs=1, enc_id=600000 + i)
+           for i in range(lay.cipher_count)]
+    per_layer, stages = [], {}
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t_all = time.perf_counter()
+    for layer in range(int(n_layers)):
+        res = decoder_layer_refreshed_fhe(cur, dev[layer % len(dev)], crypto_context=ctx,
+                                          program=prog)
+        for c in cur:
+            c.release()
+        cur = list(res.ciphers)
+        per_layer.append(res.wall_seconds)
+        stages = res.stage_seconds
+        print(f"layer {layer}: {res.wall_seconds:.2f} s, {cur[0].state.cur_limbs} limbs out",
+              file=sys.stderr, flush=True)
+    ev1.record()
+    ctx.synchronize()
+    total = time.perf_counter() - t_all
+    got = lay.unpack(np.stack([client.decrypt(o) for o in cur]))
+    out_limbs = int(cur[0].state.cur_limbs)
+    for c in cur:
+        c.release()
+    for d in dev:
+        d.close()
+    mem = ctx.memory_info()
+    ctx.close()
+    want, smax = x, 0.0
+    for layer in range(int(n_layers)):
+        want, s_ = _layer_fp64(want, wsets[layer % len(wsets)], ap, H, KV, hd)
+        smax = max(smax, s_)
+    steady = per_layer[1:] or per_layer
+    return {
+        "seconds_per_layer": round(float(np.mean(steady)), 3),
+        "layers": int(n_layers),
+        "total_seconds": round(total, 3),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 3),
+        "per_layer_s": [round(v, 3) for v in per_layer],
+        "workload": f"{n_layers} Llama-3-8B decoder layers (d=4096, 32/8 heads x 128, SwiGLU 14336) "
+                    "over 128 tokens in 16 ciphertexts of 8 lanes, bootstraps included "
+                    "(3 paired refreshes = 24 bootstraps per layer), N=2^16, Q=1x60b+65x40b, "
+                    f"dnum=5, P=14x44b; bootstrap outputs {out_levels + 1} limbs; "
+                    f"{len(wsets)} weight sets cycled",
+        "last_layer_stages_s": {k: round(v, 3) for k, v in stages.items()},
+        "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
+        "output_abs_max": float(np.abs(want).max()),
+        "score_abs_max": smax,
+        "output_limbs": out_limbs,
+        "setup_s": round(setup_s, 2),
+        "weight_upload_s": round(upload_s, 2),
+        "device_memory": _memory_summary(mem),
     }
 
 

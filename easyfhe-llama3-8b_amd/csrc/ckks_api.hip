@@ -53,55 +53,208 @@ static void require(bool cond, const std::string &msg) {
 }
 
 // ===========================================================================
-// device memory pool: exact-size free lists, all use is ordered on the
-// context's single stream, so a buffer released here can be handed to the
-// next kernel on that stream without a synchronisation.
+// device memory pool: all use is ordered on the context's single stream, so
+// a buffer released here can be handed to the next kernel on that stream
+// without a synchronisation.
 // ===========================================================================
 
-// Size classes: 256-byte granularity up to 1 MiB, then eight classes per
-// octave (at most 1/8 over the request), so that the blocks of neighbouring
-// modulus levels share classes and a computation walking down the chain
-// reuses its cache instead of accumulating one class per limb count.
-static size_t pool_class(size_t bytes) {
-  bytes = (bytes + 255) & ~(size_t)255;
-  if (bytes <= ((size_t)1 << 20)) return bytes;
-  int e = 63 - __builtin_clzll((unsigned long long)bytes);
-  const size_t step = (size_t)1 << (e - 3);
-  return (bytes + step - 1) / step * step;
+static constexpr size_t kSmallMax = (size_t)1 << 20;     // exact classes up to here
+static constexpr size_t kLargeGrain = (size_t)64 << 10;  // large blocks: 64 KiB units
+static constexpr size_t kSegment = (size_t)1 << 30;      // large blocks come from 1 GiB
+// Device memory the pool leaves free for the runtime: hardware queues and
+// the private segment it sizes for a kernel when that kernel is dispatched.
+static constexpr size_t kRuntimeReserve = (size_t)2 << 30;
+
+static size_t round_up(size_t v, size_t g) { return (v + g - 1) / g * g; }
+
+static size_t device_free_bytes() {
+  size_t fr = 0, tot = 0;
+  if (hipMemGetInfo(&fr, &tot) != hipSuccess) {
+    (void)hipGetLastError();
+    return (size_t)-1;
+  }
+  return fr;
 }
 
 void *Pool::alloc(size_t bytes) {
-  bytes = pool_class(bytes);
-  last_use_[bytes] = ++clock_;
-  auto it = free_.find(bytes);
   void *p = nullptr;
-  if (it != free_.end() && !it->second.empty()) {
-    p = it->second.back();
-    it->second.pop_back();
-    cached -= bytes;
-  } else if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    if (!evict_for(bytes, &p)) HIPCHECK(hipMalloc(&p, bytes));
+  if (bytes > kSmallMax) {
+    p = alloc_large(bytes);
+  } else {
+    bytes = round_up(bytes, 256);
+    auto it = free_.find(bytes);
+    if (it != free_.end() && !it->second.empty()) {
+      p = it->second.back();
+      it->second.pop_back();
+      cached -= bytes;
+    } else {
+      p = raw_alloc(bytes);
+    }
+    live_[p] = bytes;
+    live += bytes;
   }
-  live += bytes;
-  live_[p] = bytes;
+  if (live > peak) peak = live;
   return p;
 }
 
 void Pool::release(void *p, size_t bytes) {
   if (!p) return;
-  bytes = pool_class(bytes);
+  if (bytes > kSmallMax) {
+    release_large(p);
+    return;
+  }
+  bytes = round_up(bytes, 256);
   live_.erase(p);
   free_[bytes].push_back(p);
   live -= bytes;
   cached += bytes;
 }
 
+void *Pool::alloc_large(size_t bytes) {
+  bytes = round_up(bytes, kLargeGrain);
+  auto it = bins_.lower_bound(bytes);
+  if (it == bins_.end()) {
+    if (!grow(bytes)) throw std::runtime_error("device memory exhausted");
+    it = bins_.lower_bound(bytes);
+  }
+  Block *b = it->second;
+  bins_.erase(it);
+  b->free = false;
+  if (b->size > bytes) {  // split: the tail stays free
+    Block *t = new Block{b->base + bytes, b->size - bytes, true, b, b->next, {}};
+    if (b->next) b->next->prev = t;
+    b->next = t;
+    b->size = bytes;
+    t->slot = bins_.emplace(t->size, t);
+    blocks_[t->base] = t;
+  }
+  cached -= bytes;
+  live += bytes;
+  return b->base;
+}
+
+void Pool::release_large(void *p) {
+  auto it = blocks_.find(p);
+  if (it == blocks_.end() || it->second->free)
+    throw std::runtime_error("release of a block the pool did not hand out");
+  Block *b = it->second;
+  live -= b->size;
+  cached += b->size;
+  b->free = true;
+  if (b->next && b->next->free) {  // merge the following free block
+    Block *n = b->next;
+    bins_.erase(n->slot);
+    blocks_.erase(n->base);
+    b->size += n->size;
+    b->next = n->next;
+    if (n->next) n->next->prev = b;
+    delete n;
+  }
+  if (b->prev && b->prev->free) {  // merge into the preceding free block
+    Block *q = b->prev;
+    bins_.erase(q->slot);
+    blocks_.erase(b->base);
+    q->size += b->size;
+    q->next = b->next;
+    if (b->next) b->next->prev = q;
+    delete b;
+    b = q;
+  }
+  b->slot = bins_.emplace(b->size, b);
+}
+
+// A new segment of at least `bytes`: 1 GiB where the device has room for it
+// beside the runtime reserve, else exactly `bytes` after handing back what
+// the cache holds.
+bool Pool::grow(size_t bytes) {
+  size_t want = bytes > kSegment ? bytes : kSegment;
+  if (device_free_bytes() < want + kRuntimeReserve) {
+    want = bytes;
+    if (!make_room(bytes)) return false;
+  }
+  char *d = nullptr;
+  if (hipMalloc((void **)&d, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  device_allocs++;
+  segments_.push_back({d, want});
+  segment_bytes += want;
+  Block *b = new Block{d, want, true, nullptr, nullptr, {}};
+  b->slot = bins_.emplace(want, b);
+  blocks_[d] = b;
+  cached += want;
+  return true;
+}
+
+// Segments with nothing live in them go back to the device.
+size_t Pool::free_segments() {
+  size_t freed = 0;
+  for (size_t i = 0; i < segments_.size();) {
+    Block *b = blocks_.at(segments_[i].first);
+    if (b->free && b->size == segments_[i].second) {
+      bins_.erase(b->slot);
+      blocks_.erase(b->base);
+      (void)hipFree(b->base);
+      cached -= b->size;
+      segment_bytes -= b->size;
+      freed += b->size;
+      delete b;
+      segments_[i] = segments_.back();
+      segments_.pop_back();
+    } else {
+      i++;
+    }
+  }
+  return freed;
+}
+
+// Make `bytes` (plus the runtime reserve) free on the device: first the small
+// classes and the empty segments, then give up the reserve.
+bool Pool::make_room(size_t bytes) {
+  if (device_free_bytes() >= bytes + kRuntimeReserve) return true;
+  (void)hipDeviceSynchronize();
+  for (auto &kv : free_) {
+    for (void *q : kv.second) (void)hipFree(q);
+    cached -= kv.first * kv.second.size();
+    kv.second.clear();
+  }
+  free_segments();
+  return device_free_bytes() >= bytes;
+}
+
+void *Pool::raw_alloc(size_t bytes) {
+  void *p = nullptr;
+  if (device_free_bytes() < bytes + kRuntimeReserve) make_room(bytes);
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    make_room(bytes);
+    HIPCHECK(hipMalloc(&p, bytes));
+  }
+  device_allocs++;
+  return p;
+}
+
+void Pool::trim() {
+  (void)hipDeviceSynchronize();
+  for (auto &kv : free_)
+    for (void *p : kv.second) (void)hipFree(p);
+  free_.clear();
+  free_segments();
+  cached = 0;
+  for (auto &kv : bins_) cached += kv.first;
+}
+
 void Pool::release_all() {
   trim();
   for (auto &kv : live_) (void)hipFree(kv.first);
   live_.clear();
-  live = 0;
+  for (auto &s : segments_) (void)hipFree(s.first);
+  segments_.clear();
+  for (auto &kv : blocks_) delete kv.second;
+  blocks_.clear();
+  bins_.clear();
+  live = cached = segment_bytes = 0;
 }
 
 // Contexts that are alive; a ciphertext released after its context was
@@ -116,34 +269,6 @@ static u64 g_next_serial = 1;
 static bool owner_alive(const ckks_context *c, u64 serial) {
   auto it = g_live_contexts.find(const_cast<ckks_context *>(c));
   return it != g_live_contexts.end() && it->second == serial;
-}
-
-// Out of device memory: free the cached size classes least recently used
-// first, retrying after each, so that the classes the running computation
-// cycles through stay cached.
-bool Pool::evict_for(size_t bytes, void **p) {
-  std::vector<std::pair<u64, size_t>> order;  // (last use, class)
-  for (auto &kv : free_)
-    if (!kv.second.empty()) order.push_back({last_use_[kv.first], kv.first});
-  std::sort(order.begin(), order.end());
-  (void)hipDeviceSynchronize();
-  for (auto &e : order) {
-    auto &v = free_[e.second];
-    for (void *q : v) (void)hipFree(q);
-    cached -= e.second * v.size();
-    v.clear();
-    if (hipMalloc(p, bytes) == hipSuccess) return true;
-    (void)hipGetLastError();
-  }
-  return false;
-}
-
-void Pool::trim() {
-  (void)hipDeviceSynchronize();
-  for (auto &kv : free_)
-    for (void *p : kv.second) (void)hipFree(p);
-  free_.clear();
-  cached = 0;
 }
 
 // ===========================================================================
@@ -953,7 +1078,7 @@ static void gen_key(ckks_context *c, u64 id, int relin, u64 galois) {
   k.galois = id;
   k.digits = (c->L + c->ds - 1) / c->ds;
   k.bytes = sizeof(u64) * (size_t)k.digits * 2 * c->K * c->N;
-  HIPCHECK(hipMalloc(&k.data, k.bytes));
+  k.data = (u64 *)c->pool.raw_alloc(k.bytes);
   launch_keygen(c, k, id, relin, galois);
   c->keys[id] = k;
 }
@@ -1286,6 +1411,16 @@ int ckks_memory_info(ckks_context *c, size_t *live, size_t *cached) {
   require(c, "null argument");
   if (live) *live = c->pool.live;
   if (cached) *cached = c->pool.cached;
+  API_END
+}
+
+int ckks_memory_stats(ckks_context *c, size_t *peak_live, size_t *segment_bytes,
+                      uint64_t *device_allocs) {
+  API_BEGIN
+  require(c, "null argument");
+  if (peak_live) *peak_live = c->pool.peak;
+  if (segment_bytes) *segment_bytes = c->pool.segment_bytes;
+  if (device_allocs) *device_allocs = c->pool.device_allocs;
   API_END
 }
 
@@ -2224,9 +2359,11 @@ int ckks_tensor_upload(ckks_context *c, const void *data, size_t bytes, ckks_ten
   require(c && data && out, "null argument");
   require(bytes > 0, "empty tensor");
   ckks_tensor *t = new ckks_tensor{c, nullptr, bytes, c->serial};
-  if (hipMalloc(&t->d, bytes) != hipSuccess) {
+  try {
+    t->d = c->pool.raw_alloc(bytes);
+  } catch (...) {
     delete t;
-    throw std::runtime_error("device allocation failed");
+    throw;
   }
   HIPCHECK(hipMemcpyAsync(t->d, data, bytes, hipMemcpyHostToDevice, c->stream));
   HIPCHECK(hipStreamSynchronize(c->stream));

@@ -2462,6 +2462,10 @@ __global__ void k_dec_poly(const u64 *__restrict__ ct, int polys, int limbs,
 // Balanced Garner reconstruction of coefficient (idx gap) over K limbs, then
 // x[br(k)] = (v_k + i v_{k+n}) * untwist_k for the decoding FFT.
 // grid (n / 256 rounded up)
+// Decryption reconstructs at most this many limbs (40-bit primes: ~320 bits,
+// far above any scale times the 2^40 headroom it keeps).
+constexpr int GARNER_MAX_LIMBS = 8;
+
 __global__ void k_dec_garner(const u64 *__restrict__ m, int K, const u64 *__restrict__ inv,
                              const cplx *__restrict__ untwist, cplx *__restrict__ x, int n,
                              int logn, int logN, const ModQ *__restrict__ mods) {
@@ -2472,18 +2476,23 @@ __global__ void k_dec_garner(const u64 *__restrict__ m, int K, const u64 *__rest
   double vv[2];
   for (int h = 0; h < 2; h++) {
     const size_t ci = (size_t)(k + h * n) * gap;
-    long long d[64];
-    for (int kk = 0; kk < K; kk++) {
-      const ModQ M = mods[kk];
-      u64 t = m[kk * N + ci];
-      for (int j = 0; j < kk; j++) {
-        t = mul_mod(sub_mod(t, signed_residue(d[j], M), M.q), inv[j * K + kk], M);
+    // fully unrolled over the bound so that the digits stay in registers
+    long long d[GARNER_MAX_LIMBS];
+#pragma unroll
+    for (int kk = 0; kk < GARNER_MAX_LIMBS; kk++) {
+      if (kk < K) {
+        const ModQ M = mods[kk];
+        u64 t = m[kk * N + ci];
+#pragma unroll
+        for (int j = 0; j < kk; j++)
+          t = mul_mod(sub_mod(t, signed_residue(d[j], M), M.q), inv[j * K + kk], M);
+        d[kk] = t > (M.q - 1) / 2 ? (long long)t - (long long)M.q : (long long)t;
       }
-      d[kk] = t > (M.q - 1) / 2 ? (long long)t - (long long)M.q : (long long)t;
     }
-    double v = (double)d[K - 1];
-    for (int kk = K - 2; kk >= 0; kk--)
-      v = __dadd_rn(__dmul_rn(v, (double)mods[kk].q), (double)d[kk]);
+    double v = 0.0;
+#pragma unroll
+    for (int kk = GARNER_MAX_LIMBS - 1; kk >= 0; kk--)
+      if (kk < K) v = __dadd_rn(__dmul_rn(v, (double)mods[kk].q), (double)d[kk]);
     vv[h] = v;
   }
   const u32 r = __brev((u32)k) >> (32 - logn);
@@ -2506,7 +2515,8 @@ void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, dou
   // limbs needed: smallest K with sum log2 q >= log2(scale) + 40
   double need = log2(ct->scale) + 40.0, have = 0.0;
   int K = 0;
-  while (K < ct->limbs && K < 64 && have < need) have += log2((double)c->primes[K++]);
+  while (K < ct->limbs && K < GARNER_MAX_LIMBS && have < need)
+    have += log2((double)c->primes[K++]);
   if (K < 1) K = 1;
   u64 *m = (u64 *)c->pool.alloc(sizeof(u64) * (size_t)K * N);
   const bool is_pt = ct->polys == 1;

@@ -80,6 +80,8 @@ SIGNATURES = {
     "ckks_clear_rotation_keys": (I, [VP, I64P, I]),
     "ckks_synchronize": (I, [VP]),
     "ckks_memory_info": (I, [VP, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+    "ckks_memory_stats": (I, [VP, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t),
+                              ctypes.POINTER(ctypes.c_uint64)]),
     "ckks_empty_cache": (I, [VP]),
     "ckks_encrypt": (I, [VP, DP, DP, I, I, ctypes.c_double, ctypes.c_uint32, VPP]),
     "ckks_decrypt": (I, [VP, VP, DP, DP]),

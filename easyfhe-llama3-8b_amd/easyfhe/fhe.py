@@ -175,7 +175,12 @@ class NativeContext:
     def memory_info(self) -> dict[str, int]:
         live, cached = ctypes.c_size_t(), ctypes.c_size_t()
         check(lib.ckks_memory_info(self._h, ctypes.byref(live), ctypes.byref(cached)))
-        return {"live_bytes": int(live.value), "cached_bytes": int(cached.value)}
+        peak, seg, allocs = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_uint64()
+        check(lib.ckks_memory_stats(self._h, ctypes.byref(peak), ctypes.byref(seg),
+                                    ctypes.byref(allocs)))
+        return {"live_bytes": int(live.value), "cached_bytes": int(cached.value),
+                "peak_live_bytes": int(peak.value), "segment_bytes": int(seg.value),
+                "device_allocations": int(allocs.value)}
 
     def empty_cache(self) -> None:
         check(lib.ckks_empty_cache(self._h))

@@ -28,6 +28,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+from easyfhe import fhe
+
 from .attention import (AttentionGeometry, SoftmaxConfig, attention_fhe, attention_rotations,
                         kv_repeat_rows, softmax_depth)
 from .complex import pair_real_ciphers, split_complex_ciphers_twice
@@ -270,6 +272,22 @@ def _land_on_ladder(cts, ctx) -> list:
     return out
 
 
+def _drop_owned(cts, limbs: int, ctx) -> list:
+    """Modulus drop of refreshed ciphertexts to the ``limbs`` the next block
+    uses (every later operation then runs on that many limbs); the inputs
+    are consumed.  A block's result is bootstrapped next, and the bootstrap
+    may spend one limb bringing the input's scale down to its own, so the
+    blocks keep one limb above their depth."""
+    out = []
+    for c in cts:
+        d = fhe.align_to(c, c.state.replace(cur_limbs=min(int(limbs), int(c.state.cur_limbs)),
+                                            scaling_factor=None), ctx)
+        if d is not c:
+            c.release()
+        out.append(d)
+    return out
+
+
 def refreshed_layer_depths(approx: LayerApproximations, seq_len: int) -> tuple[int, int, int]:
     """Levels of the three blocks between refreshes: RMSNorm + Q/K/V + RoPE +
     QK; the scores' landing + softmax + PV + W_o; RMSNorm + MLP."""
@@ -306,6 +324,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         stage["refresh_residual_1"] = time.perf_counter() - t0
         if int(x[0].state.cur_limbs) < max(a_depth, b_depth, c_depth) + 1:
             raise ValueError("the bootstrap program's outputs are too shallow for the layer.")
+        x = keep = _drop_owned(x, a_depth + 2, ctx)
         t0 = time.perf_counter()
         n1 = rmsnorm_fhe(x, np.zeros(1), coeffs=ap.input_norm, layout=lay, crypto_context=ctx)
         z = pair_real_ciphers(n1.ciphers, crypto_context=ctx)
@@ -356,7 +375,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         hr = refresh_stream(h, crypto_context=ctx, program=program, value_bound=residual_bound,
                             group=group)
         _release(h)
-        keep = hr
+        hr = keep = _drop_owned(hr, c_depth + 2, ctx)
         sync()
         stage["refresh_residual_2"] = time.perf_counter() - t0
         t0 = time.perf_counter()

@@ -724,11 +724,11 @@ static void crt_to_double(const orc_ctx *c, const u64 *coeff, int K, double *out
 }
 
 /* Number of leading limbs used to reconstruct a coefficient: the smallest K
- * with sum(log2 q_k) >= log2(scale) + 40, capped at `limbs` and 64. */
+ * with sum(log2 q_k) >= log2(scale) + 40, capped at `limbs` and 8. */
 static int decode_limbs(const orc_ctx *c, int limbs, double scale) {
   double need = log2(scale) + 40.0, have = 0.0;
   int K = 0;
-  while (K < limbs && K < 64 && have < need) have += log2((double)c->primes[K++]);
+  while (K < limbs && K < 8 && have < need) have += log2((double)c->primes[K++]);
   return K < 1 ? 1 : K;
 }
 
