@@ -89,10 +89,11 @@ def main() -> int:
                     help="skip the attention measurement of the default run")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the whole-layer measurement of the default run")
-    ap.add_argument("--layers", type=int, default=2,
-                    help="layers of the refreshed-layer measurement (layers mode)")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="layers of the layers mode (default 2) and of the prefill mode "
+                         "(default 32)")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp",
-                                       "attention", "layer", "layers"],
+                                       "attention", "layer", "layers", "prefill"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
@@ -101,7 +102,9 @@ def main() -> int:
                          "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer; "
                          "attention: the causal attention of a layer; "
                          "layer: one whole encrypted decoder layer on a deeper chain; "
-                         "layers: consecutive layers with their bootstraps (--layers)")
+                         "layers: consecutive layers with their bootstraps (--layers); "
+                         "prefill: the encrypted prefill from token ids to logits (--layers, "
+                         "default 32)")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -111,6 +114,11 @@ def main() -> int:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the key-switch "
               "path shards by ciphertext, see DESIGN.md)", file=sys.stderr)
         return 2
+    if args.mode == "prefill":
+        # The plaintext passes run on torch; its bundled HIP runtime must be
+        # the process's only one, which holds when torch loads before the
+        # backend library (the backend then binds to the runtime by soname).
+        import torch  # noqa: F401
 
     from easyfhe import _native, fhe
 
@@ -127,8 +135,13 @@ def main() -> int:
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
               flush=True)
         return 0
+    if args.mode == "prefill":
+        n = 32 if args.layers is None else args.layers
+        print(json.dumps({"fm_prefill": measure_fm_prefill(n)}), flush=True)
+        return 0
     if args.mode == "layers":
-        print(json.dumps({"fm_layers": measure_fm_layers(args.layers)}), flush=True)
+        print(json.dumps({"fm_layers": measure_fm_layers(2 if args.layers is None
+                                                         else args.layers)}), flush=True)
         return 0
     if args.mode == "layer":
         print(json.dumps({"fm_layer": measure_fm_layer(warmup=args.warmup)}), flush=True)
@@ -803,6 +816,209 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
         "output_limbs": out_limbs,
         "setup_s": round(setup_s, 2),
         "weight_upload_s": round(upload_s, 2),
+        "device_memory": _memory_summary(mem),
+    }
+
+
+def _cheb_torch(x, entry):
+    """Chebyshev series of a fitted entry (first coefficient halved) by
+    Clenshaw's recurrence, elementwise on a torch tensor."""
+    lo, hi = (float(v) for v in entry["fit_interval"])
+    c = [float(v) for v in entry["coefficients"]]
+    y = (2.0 * x - (lo + hi)) / (hi - lo)
+    b1, b2 = x.new_zeros(()), x.new_zeros(())
+    for ck in reversed(c[1:]):
+        b1, b2 = ck + 2.0 * y * b1 - b2, b1
+    return 0.5 * c[0] + y * b1 - b2
+
+
+class _TorchLayer:
+    """A decoder layer in fp64 on the GPU for the prefill's plaintext passes:
+    exact (rsqrt, SiLU, softmax) or with the layer's fitted RMSNorm and SiLU
+    series (softmax exact)."""
+
+    def __init__(self, w, *, H, KV, hd, T, eps=1e-5, device="cuda"):
+        import torch
+
+        from feature_major.rope import rope_angles
+
+        self.w, self.H, self.KV, self.hd, self.eps = w, H, KV, hd, eps
+        ang = torch.tensor(rope_angles(np.arange(T), hd), dtype=torch.float64, device=device)
+        self.cos, self.sin = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+        self.mask = torch.tril(torch.ones(T, T, dtype=torch.bool, device=device))
+
+    def _rope(self, a):
+        import torch
+
+        T = a.shape[0]
+        h = a.reshape(T, -1, self.hd)
+        lo, hi = h[..., :self.hd // 2], h[..., self.hd // 2:]
+        return torch.cat([lo * self.cos - hi * self.sin, hi * self.cos + lo * self.sin],
+                         -1).reshape(T, -1)
+
+    def __call__(self, x, ap=None):
+        """(output, h1, gate, scores) for input ``x`` [T, D]."""
+        import torch
+
+        w, H, KV, hd = self.w, self.H, self.KV, self.hd
+        T = x.shape[0]
+
+        def norm(a, entry):
+            ms = (a * a).mean(-1, keepdim=True)
+            return a * (torch.rsqrt(ms + self.eps) if entry is None else _cheb_torch(ms, entry))
+
+        n1 = norm(x, None if ap is None else ap.input_norm)
+        q = self._rope(n1 @ w["q"].T)
+        k = self._rope(n1 @ w["k"].T).reshape(T, KV, hd).repeat_interleave(H // KV, 1)
+        v = (n1 @ w["v"].T).reshape(T, KV, hd).repeat_interleave(H // KV, 1)
+        qh = q.reshape(T, H, hd).transpose(0, 1).contiguous()
+        kt = k.permute(1, 2, 0).contiguous()
+        vh = v.transpose(0, 1).contiguous()
+        sc = torch.matmul(qh, kt) / float(np.sqrt(hd))
+        p = torch.softmax(sc.masked_fill(~self.mask, float("-inf")), -1)
+        att = torch.matmul(p, vh).transpose(0, 1).reshape(T, -1)
+        h1 = x + att @ w["o"].T
+        n2 = norm(h1, None if ap is None else ap.post_attention_norm)
+        g = n2 @ w["gate"].T
+        act = torch.nn.functional.silu(g) if ap is None else _cheb_torch(g, ap.silu)
+        return h1 + (act * (n2 @ w["up"].T)) @ w["down"].T, h1, g, sc
+
+
+def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -> dict:
+    """The full encrypted Llama-3-8B prefill over 128 tokens: random token
+    ids (seed) embedded by the client, ``n_layers`` encrypted decoder layers
+    with their refreshes (bootstraps included) on REFRESH_PARAMS, every key
+    and every layer's weights resident on the device, the final hidden state
+    decrypted and the final token's logits computed in the clear (exact final
+    RMSNorm and LM head).  Weights N(0, 0.02) (embedding, projections, LM
+    head) in a Hadamard-rotated residual basis, drawn on the GPU from seeded
+    generators.  Each layer's series intervals are calibrated on a second
+    random token sequence in plaintext.  Logits are compared with the fp64
+    forward (exact RMSNorm, SiLU and softmax) and with the fp64 forward that
+    uses the fitted series."""
+    import torch
+
+    from easyfhe import fhe
+    from easyfhe.bs import openfhe as bs
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.layer import DecoderLayerWeights, decoder_layer_rotations
+    from feature_major.model import (approximations_for, embed_tokens, final_logits,
+                                     layer_ranges, prefill_fhe)
+
+    T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
+    spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=seed,
+                               rotations=decoder_layer_rotations(lay, H, hd))
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3), output_levels=0))
+    out_levels = ctx.L - probe.depth_limbs - 1
+    probe.release()
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3),
+                                             output_levels=out_levels))
+    ctx.synchronize()
+    setup_s = time.perf_counter() - t0
+
+    t0 = time.perf_counter()
+    dev = torch.device("cuda")
+    R = torch.tensor(randomized_hadamard(D, seed + 1), dtype=torch.float64, device=dev)
+
+    def draw(gen, *shape):
+        return torch.randn(*shape, generator=gen, dtype=torch.float64, device=dev) * 0.02
+
+    g0 = torch.Generator(device=dev).manual_seed(seed)
+    embed = (draw(g0, vocab, D) @ R).cpu().numpy()
+    lm_head = (draw(g0, vocab, D) @ R).cpu().numpy()
+    rng = np.random.default_rng(seed)
+    test_ids, cal_ids = rng.integers(0, vocab, T), rng.integers(0, vocab, T)
+    x_test = embed_tokens(test_ids, embed)
+    x_cal = torch.tensor(embed_tokens(cal_ids, embed), device=dev)
+    x_ex = torch.tensor(x_test, device=dev)
+    x_po = x_ex.clone()
+    layers, bounds, ranges = [], [], []
+    try:
+        for li in range(int(n_layers)):
+            g = torch.Generator(device=dev).manual_seed(seed * 1000 + 7 + li)
+            w = dict(q=draw(g, D, D) @ R, k=draw(g, KV * hd, D) @ R, v=draw(g, KV * hd, D) @ R,
+                     o=R.T @ draw(g, D, D), gate=draw(g, I, D) @ R, up=draw(g, I, D) @ R,
+                     down=R.T @ draw(g, D, I))
+            f = _TorchLayer(w, H=H, KV=KV, hd=hd, T=T)
+            x_next, h1, gate, sc = f(x_cal)
+            r = layer_ranges(x_cal.cpu().numpy(), h1.cpu().numpy(), gate.cpu().numpy(),
+                             sc.cpu().numpy())
+            ap, bound = approximations_for(r)
+            x_cal = x_next
+            x_ex = f(x_ex)[0]
+            x_po = f(x_po, ap)[0]
+            host = {k: v.cpu().numpy() for k, v in w.items()}
+            del w, f, h1, gate, sc
+            layers.append(DecoderLayerWeights(host["q"], host["k"], host["v"], host["o"],
+                                              host["gate"], host["up"], host["down"], heads=H,
+                                              kv_heads=KV, head_dim=hd, intermediate=I,
+                                              approx=ap, layout=lay, context=ctx))
+            bounds.append(bound)
+            ranges.append(r)
+            print(f"prepared layer {li}: residual bound {bound:.3g}, mean square "
+                  f"{r.input_mean_square[0]:.3g}..{r.post_attention_mean_square[1]:.3g}, "
+                  f"scores {r.score_min:.2f}..{r.score_max:.2f}", file=sys.stderr, flush=True)
+        want_exact = x_ex.cpu().numpy()
+        want_poly = x_po.cpu().numpy()
+        del x_cal, x_ex, x_po, R
+        torch.cuda.empty_cache()
+        ctx.synchronize()
+        prep_s = time.perf_counter() - t0
+
+        packed = lay.pack(x_test)
+        cts = [client.encrypt(packed[i], cur_limbs=1, enc_id=700000 + i)
+               for i in range(lay.cipher_count)]
+        ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+        ev0.record()
+        t0 = time.perf_counter()
+        res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog, residual_bounds=bounds,
+                          on_layer=lambda i, s: print(f"layer {i}: {s:.2f} s", file=sys.stderr,
+                                                      flush=True))
+        ev1.record()
+        ctx.synchronize()
+        wall = time.perf_counter() - t0
+        for c in cts:
+            c.release()
+        got = lay.unpack(np.stack([client.decrypt(o) for o in res.ciphers]))
+        out_limbs = int(res.ciphers[0].state.cur_limbs)
+        res.release()
+    finally:
+        for w_ in layers:
+            w_.close()
+    mem = ctx.memory_info()
+    ctx.close()
+    ones = np.ones(D)
+    lg = final_logits(got, norm_weight=ones, lm_head=lm_head)
+    lg_exact = final_logits(want_exact, norm_weight=ones, lm_head=lm_head)
+    lg_poly = final_logits(want_poly, norm_weight=ones, lm_head=lm_head)
+    top5 = lambda v: set(np.argsort(v)[-5:].tolist())  # noqa: E731
+    return {
+        "seconds": round(wall, 2),
+        "seconds_per_layer": round(wall / max(1, int(n_layers)), 3),
+        "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 2),
+        "layers": int(n_layers),
+        "layer_s": [round(v, 2) for v in res.layer_seconds],
+        "workload": f"{n_layers}-layer Llama-3-8B prefill (d=4096, 32/8 heads x 128, SwiGLU "
+                    f"14336, vocab {vocab}) over 128 random tokens in 16 ciphertexts of 8 lanes, "
+                    "every layer boundary encrypted, bootstraps included (24 per layer), "
+                    "N=2^16, Q=1x60b+65x40b, dnum=5, P=14x44b; final token's logits in the "
+                    "clear",
+        "logits_max_abs_err_vs_fp64_exact": float(np.abs(lg - lg_exact).max()),
+        "logits_max_abs_err_vs_fp64_series": float(np.abs(lg - lg_poly).max()),
+        "logits_abs_max": float(np.abs(lg_exact).max()),
+        "top1_match_exact": bool(int(np.argmax(lg)) == int(np.argmax(lg_exact))),
+        "top5_overlap_exact": len(top5(lg) & top5(lg_exact)),
+        "hidden_max_abs_err_vs_fp64_series": float(np.abs(got - want_poly).max()),
+        "hidden_max_abs_err_vs_fp64_exact": float(np.abs(got - want_exact).max()),
+        "hidden_abs_max": float(np.abs(want_exact).max()),
+        "output_limbs": out_limbs,
+        "setup_s": round(setup_s, 2),
+        "weights_and_calibration_s": round(prep_s, 2),
+        "residual_bounds": [round(b, 2) for b in bounds],
+        "score_max": round(max(r.score_max for r in ranges), 2),
         "device_memory": _memory_summary(mem),
     }
 

@@ -2,6 +2,11 @@
 
 The library is the only compute path: if it is missing this module raises at
 import, so nothing can silently fall back to host arithmetic.
+
+A process that also runs torch on the GPU imports torch first: torch ships
+its own HIP runtime under unversioned file names, so loaded after this
+library it comes up as a second runtime that finds no device; loaded before,
+this library binds to that runtime by soname and the two share it.
 """
 
 from __future__ import annotations

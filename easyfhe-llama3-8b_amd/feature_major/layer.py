@@ -229,15 +229,18 @@ def decoder_layer_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_con
 def refresh_stream(ciphers, *, crypto_context, program, value_bound: float = 1.0,
                    group: int = 8) -> list:
     """Refresh a real feature-major stream (reference operators/norm/refresh.py:96-150):
-    values divided by a power of two S >= value_bound through the recorded
-    scale (no level), adjacent ciphertexts paired as ``a + i b``, the pairs
+    values divided by the power of two S >= value_bound through the recorded
+    scale (no level; S < 1 spreads a small stream over the bootstrap's input
+    range), adjacent ciphertexts paired as ``a + i b``, the pairs
     bootstrapped in batched groups (keys and diagonals read once per group),
     the conjugation split's factor 2 and S returned to the recorded scale.
     Inputs are not consumed."""
     from easyfhe.bs import openfhe as bs
 
     ctx = _ctx(crypto_context)
-    S = 2.0 ** max(0, int(np.ceil(np.log2(max(float(value_bound), 1.0)))))
+    if not float(value_bound) > 0.0:
+        raise ValueError("the value bound must be positive.")
+    S = 2.0 ** int(np.ceil(np.log2(float(value_bound))))
     views = []
     for c in ciphers:
         v = c.deep_copy()

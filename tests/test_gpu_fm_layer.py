@@ -389,3 +389,92 @@ def test_refreshed_decoder_layer_matches_poly_model():
           f"{np.abs(want2).max():.3g}, limbs out {r1.output_limbs}, {r2.wall_seconds:.2f} s, "
           f"stages {r2.stage_seconds}", flush=True)
     assert e1 < 1e-3 and e2 < 2e-3, (e1, e2)
+
+
+def _exact_layer_and_ranges(x, wq, wk, wv, wo, G, U, Dn, *, heads, kv_heads, head_dim):
+    """The layer with exact RMSNorm, SiLU and softmax, and the ranges its
+    nonlinearities saw (the calibration pass)."""
+    from feature_major.model import layer_ranges
+
+    T = x.shape[0]
+    g = heads // kv_heads
+    rep = lambda w: np.repeat(w.reshape(kv_heads, head_dim, -1), g, axis=0).reshape(  # noqa: E731
+        heads * head_dim, -1)
+    norm = lambda a: a / np.sqrt(np.mean(a * a, axis=-1, keepdims=True) + 1e-5)  # noqa: E731
+    n1 = norm(x)
+    q = LN.apply_rope_numpy(n1 @ wq.T, heads, head_dim)
+    k = LN.apply_rope_numpy(n1 @ rep(wk).T, heads, head_dim)
+    v = n1 @ rep(wv).T
+    qh, kh = (a.reshape(T, heads, head_dim).transpose(1, 0, 2) for a in (q, k))
+    scores = qh @ kh.transpose(0, 2, 1) / np.sqrt(head_dim)
+    h1 = x + LN.attention_numpy(q, k, v, heads) @ wo.T
+    n2 = norm(h1)
+    gate = n2 @ G.T
+    out = h1 + ((gate / (1.0 + np.exp(-gate))) * (n2 @ U.T)) @ Dn.T
+    return out, layer_ranges(x, h1, gate, scores)
+
+
+def test_prefill_from_token_ids_to_logits():
+    """Three encrypted layers from embedded token ids to the final token's
+    logits, 64 tokens x 512 features at N = 2^13, each layer's series fitted
+    on ranges calibrated with another token sequence; embedding and LM head
+    N(0, 0.02), so the first refresh carries a stream far below one.  Against
+    the fp64 model of the same layers (fitted series, Algorithm-2 softmax)."""
+    from easyfhe.bs import openfhe as bs
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.layer import DecoderLayerWeights, decoder_layer_rotations
+    from feature_major.model import (RangeMargins, approximations_for, embed_tokens,
+                                     final_logits, prefill_fhe)
+
+    T, D, H, KV, hd, I, V, n_layers = 64, 512, 4, 2, 128, 1408, 1000, 3
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=4096)
+    client, ctx = device_context(FM_REFRESH, rotations=decoder_layer_rotations(lay, H, hd))
+    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3), output_levels=0))
+    out_levels = ctx.L - probe.depth_limbs - 1
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3),
+                                             output_levels=out_levels))
+    rng = np.random.default_rng(21)
+    embed, head = rng.normal(0, 0.02, (V, D)), rng.normal(0, 0.02, (V, D))
+    x = embed_tokens(rng.integers(0, V, T), embed)
+    x_cal = embed_tokens(rng.integers(0, V, T), embed)
+    margins = RangeMargins(softmax_rounds=2, score_span=10.0)
+    sd = 1.0 / np.sqrt(D)
+    layers, bounds, want = [], [], x
+    try:
+        for _ in range(n_layers):
+            wq, wo = rng.normal(0, sd, (D, D)), rng.normal(0, sd, (D, D))
+            wk, wv = rng.normal(0, sd, (KV * hd, D)), rng.normal(0, sd, (KV * hd, D))
+            G, U = rng.normal(0, sd, (I, D)), rng.normal(0, sd, (I, D))
+            Dn = rng.normal(0, 1.0 / np.sqrt(I), (D, I))
+            x_cal, ranges = _exact_layer_and_ranges(x_cal, wq, wk, wv, wo, G, U, Dn, heads=H,
+                                                    kv_heads=KV, head_dim=hd)
+            ap, bound = approximations_for(ranges, margins)
+            sm = ap.softmax
+            want = LN.decoder_layer_numpy(
+                want, wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+                input_norm=ap.input_norm, post_attention_norm=ap.post_attention_norm,
+                silu=ap.silu,
+                probs_fn=lambda s, sm=sm: LN.softmax_alg2_numpy(
+                    s, sm.exp(), sm.first_inverse(), sm.inverse(T), rounds=sm.rounds,
+                    shift=sm.shift))
+            layers.append(DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV,
+                                              head_dim=hd, intermediate=I, approx=ap,
+                                              layout=lay, context=ctx))
+            bounds.append(bound)
+        packed = lay.pack(x)
+        xc = [client.encrypt(packed[i], cur_limbs=1, enc_id=1900 + i)
+              for i in range(lay.cipher_count)]
+        res = prefill_fhe(xc, layers, crypto_context=ctx, program=prog, residual_bounds=bounds)
+        got = _decrypt_stream(client, lay, res.ciphers)
+        res.release()
+    finally:
+        for w in layers:
+            w.close()
+    ones = np.ones(D)
+    lg, lw = (final_logits(h, norm_weight=ones, lm_head=head) for h in (got, want))
+    e_h, e_l = float(np.max(np.abs(got - want))), float(np.max(np.abs(lg - lw)))
+    print(f"prefill 3 layers 64x512: hidden err {e_h:.3g} (|h| {np.abs(want).max():.3g}), "
+          f"logits err {e_l:.3g} (|logit| {np.abs(lw).max():.3g}), bounds {bounds}, "
+          f"{res.wall_seconds:.2f} s", flush=True)
+    assert int(np.argmax(lg)) == int(np.argmax(lw))
+    assert e_h < 2e-3 and e_l < 1e-4, (e_h, e_l)

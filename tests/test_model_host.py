@@ -1,0 +1,69 @@
+"""Host side of the encrypted prefill: the client's embedding lookup and
+final logits, and the per-layer series selection from calibrated ranges."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from feature_major.model import (LayerRanges, RangeMargins, approximations_for, embed_tokens,
+                                 final_logits, layer_ranges)
+
+
+def test_embed_tokens_rows_and_bounds():
+    table = np.arange(20.0).reshape(5, 4)
+    assert np.array_equal(embed_tokens([4, 0, 4], table), table[[4, 0, 4]])
+    with pytest.raises(IndexError):
+        embed_tokens([5], table)
+    with pytest.raises(ValueError):
+        embed_tokens([], table)
+
+
+def test_final_logits_is_scale_free_and_picks_the_token():
+    rng = np.random.default_rng(0)
+    h, head = rng.normal(0, 3, (6, 16)), rng.normal(0, 1, (11, 16))
+    gamma = rng.uniform(0.5, 2.0, 16)
+    base = final_logits(h, norm_weight=gamma, lm_head=head, eps=0.0)
+    # RMSNorm removes any positive scale of the token's row
+    assert np.allclose(final_logits(7.5 * h, norm_weight=gamma, lm_head=head, eps=0.0), base)
+    # only the chosen token's row matters
+    h2 = h.copy()
+    h2[:-1] = 0.0
+    assert np.allclose(final_logits(h2, norm_weight=gamma, lm_head=head, eps=0.0), base)
+    # a unit-RMS row with unit gamma and an identity head returns the row
+    row = np.array([1.0, -1.0, 1.0, -1.0])
+    assert np.allclose(final_logits(row[None], norm_weight=np.ones(4), lm_head=np.eye(4),
+                                    eps=0.0), row)
+    assert np.allclose(final_logits(h, norm_weight=gamma, lm_head=head, token_index=2, eps=0.0),
+                       final_logits(h[:3], norm_weight=gamma, lm_head=head, eps=0.0))
+    with pytest.raises(IndexError):
+        final_logits(h, norm_weight=gamma, lm_head=head, token_index=6)
+    with pytest.raises(ValueError):
+        final_logits(h, norm_weight=gamma, lm_head=head[:, :8])
+
+
+def test_layer_ranges_reads_the_causal_scores_only():
+    x = np.array([[1.0, -1.0], [2.0, 2.0]])
+    h1 = np.array([[3.0, 0.0], [0.0, -5.0]])
+    scores = np.array([[[0.5, 99.0], [-2.0, 1.5]]])
+    r = layer_ranges(x, h1, np.array([[-7.0, 2.0]]), scores)
+    assert r.input_mean_square == (1.0, 4.0)
+    assert r.post_attention_mean_square == (4.5, 12.5)
+    assert r.residual_abs_max == 5.0 and r.gate_abs_max == 7.0
+    assert r.score_max == 1.5 and r.score_min == -2.0
+
+
+def test_approximations_cover_the_ranges():
+    r = LayerRanges((0.9, 1.2), (3.0, 5.0), 40.0, 6.5, 9.03, -8.0)
+    ap, bound = approximations_for(r)
+    lo, hi = ap.input_norm["fit_interval"]
+    assert lo <= 0.9 / 4 + 1e-12 and hi >= 1.2 * 4 - 1e-12
+    lo, hi = ap.post_attention_norm["fit_interval"]
+    assert lo <= 3.0 / 4 + 1e-12 and hi >= 5.0 * 4 - 1e-12
+    lo, hi = ap.silu["fit_interval"]
+    assert lo <= -6.5 and hi >= 6.5
+    assert ap.softmax.shift >= 9.03 + 1.0 and ap.softmax.shift == int(ap.softmax.shift)
+    assert ap.softmax.shift + ap.softmax.bound == RangeMargins().score_span
+    assert bound == 80.0
+    with pytest.raises(ValueError):
+        approximations_for(LayerRanges((1, 2), (1, 2), 1.0, 1.0, 19.0, -1.0))
