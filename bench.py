@@ -88,7 +88,7 @@ def main() -> int:
     ap.add_argument("--no-attention", action="store_true",
                     help="skip the attention measurement of the default run")
     ap.add_argument("--no-layer", action="store_true",
-                    help="skip the whole-layer measurement of the default run")
+                    help="skip the refreshed-layer measurement of the default run")
     ap.add_argument("--layers", type=int, default=None,
                     help="layers of the layers mode (default 2) and of the prefill mode "
                          "(default 32)")
@@ -289,9 +289,10 @@ def main() -> int:
         # the causal attention of a decoder layer on the same chain
         result["fm_attention"] = measure_fm_attention(client, ctx)
     if not args.no_layer:
-        # one whole layer on a deeper chain; this chain's keys are freed first
+        # two whole layers with their bootstraps on the refresh chain (the
+        # second in steady state); this chain's keys are freed first
         ctx.close()
-        result["fm_layer"] = measure_fm_layer()
+        result["fm_layers"] = measure_fm_layers(2)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

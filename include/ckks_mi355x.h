@@ -94,8 +94,8 @@ int ckks_synchronize(ckks_context *ctx);
 /* Bytes currently held by the context's device pool (live + cached). */
 int ckks_memory_info(ckks_context *ctx, size_t *live, size_t *cached);
 /* Pool counters: the most bytes live at once, device memory held by the
- * pool's segments, and the device allocations made so far (torch's
- * memory_stats, which the reference's memory reports read). */
+ * pool's segments, and the device allocations made so far (the peak the
+ * reference samples from torch's allocator, application/client.py:177-200). */
 int ckks_memory_stats(ckks_context *ctx, size_t *peak_live, size_t *segment_bytes,
                       uint64_t *device_allocs);
 int ckks_empty_cache(ckks_context *ctx);
