@@ -52,217 +52,10 @@ static void require(bool cond, const std::string &msg) {
   if (!cond) throw std::invalid_argument(msg);
 }
 
-// ===========================================================================
-// device memory pool: all use is ordered on the context's single stream, so
-// a buffer released here can be handed to the next kernel on that stream
-// without a synchronisation.
-// ===========================================================================
-
-static constexpr size_t kSmallMax = (size_t)1 << 20;     // exact classes up to here
-static constexpr size_t kLargeGrain = (size_t)64 << 10;  // large blocks: 64 KiB units
-static constexpr size_t kSegment = (size_t)1 << 30;      // large blocks come from 1 GiB
-// Device memory the pool leaves free for the runtime: hardware queues and
-// the private segment it sizes for a kernel when that kernel is dispatched.
-static constexpr size_t kRuntimeReserve = (size_t)2 << 30;
-
-static size_t round_up(size_t v, size_t g) { return (v + g - 1) / g * g; }
-
-static size_t device_free_bytes() {
-  size_t fr = 0, tot = 0;
-  if (hipMemGetInfo(&fr, &tot) != hipSuccess) {
-    (void)hipGetLastError();
-    return (size_t)-1;
-  }
-  return fr;
-}
-
-void *Pool::alloc(size_t bytes) {
-  void *p = nullptr;
-  if (bytes > kSmallMax) {
-    p = alloc_large(bytes);
-  } else {
-    bytes = round_up(bytes, 256);
-    auto it = free_.find(bytes);
-    if (it != free_.end() && !it->second.empty()) {
-      p = it->second.back();
-      it->second.pop_back();
-      cached -= bytes;
-    } else {
-      p = raw_alloc(bytes);
-    }
-    live_[p] = bytes;
-    live += bytes;
-  }
-  if (live > peak) peak = live;
-  return p;
-}
-
-void Pool::release(void *p, size_t bytes) {
-  if (!p) return;
-  if (bytes > kSmallMax) {
-    release_large(p);
-    return;
-  }
-  bytes = round_up(bytes, 256);
-  live_.erase(p);
-  free_[bytes].push_back(p);
-  live -= bytes;
-  cached += bytes;
-}
-
-void *Pool::alloc_large(size_t bytes) {
-  bytes = round_up(bytes, kLargeGrain);
-  auto it = bins_.lower_bound(bytes);
-  if (it == bins_.end()) {
-    if (!grow(bytes)) throw std::runtime_error("device memory exhausted");
-    it = bins_.lower_bound(bytes);
-  }
-  Block *b = it->second;
-  bins_.erase(it);
-  b->free = false;
-  if (b->size > bytes) {  // split: the tail stays free
-    Block *t = new Block{b->base + bytes, b->size - bytes, true, b, b->next, {}};
-    if (b->next) b->next->prev = t;
-    b->next = t;
-    b->size = bytes;
-    t->slot = bins_.emplace(t->size, t);
-    blocks_[t->base] = t;
-  }
-  cached -= bytes;
-  live += bytes;
-  return b->base;
-}
-
-void Pool::release_large(void *p) {
-  auto it = blocks_.find(p);
-  if (it == blocks_.end() || it->second->free)
-    throw std::runtime_error("release of a block the pool did not hand out");
-  Block *b = it->second;
-  live -= b->size;
-  cached += b->size;
-  b->free = true;
-  if (b->next && b->next->free) {  // merge the following free block
-    Block *n = b->next;
-    bins_.erase(n->slot);
-    blocks_.erase(n->base);
-    b->size += n->size;
-    b->next = n->next;
-    if (n->next) n->next->prev = b;
-    delete n;
-  }
-  if (b->prev && b->prev->free) {  // merge into the preceding free block
-    Block *q = b->prev;
-    bins_.erase(q->slot);
-    blocks_.erase(b->base);
-    q->size += b->size;
-    q->next = b->next;
-    if (b->next) b->next->prev = q;
-    delete b;
-    b = q;
-  }
-  b->slot = bins_.emplace(b->size, b);
-}
-
-// A new segment of at least `bytes`: 1 GiB where the device has room for it
-// beside the runtime reserve, else exactly `bytes` after handing back what
-// the cache holds.
-bool Pool::grow(size_t bytes) {
-  size_t want = bytes > kSegment ? bytes : kSegment;
-  if (device_free_bytes() < want + kRuntimeReserve) {
-    want = bytes;
-    if (!make_room(bytes)) return false;
-  }
-  char *d = nullptr;
-  if (hipMalloc((void **)&d, want) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  device_allocs++;
-  segments_.push_back({d, want});
-  segment_bytes += want;
-  Block *b = new Block{d, want, true, nullptr, nullptr, {}};
-  b->slot = bins_.emplace(want, b);
-  blocks_[d] = b;
-  cached += want;
-  return true;
-}
-
-// Segments with nothing live in them go back to the device.
-size_t Pool::free_segments() {
-  size_t freed = 0;
-  for (size_t i = 0; i < segments_.size();) {
-    Block *b = blocks_.at(segments_[i].first);
-    if (b->free && b->size == segments_[i].second) {
-      bins_.erase(b->slot);
-      blocks_.erase(b->base);
-      (void)hipFree(b->base);
-      cached -= b->size;
-      segment_bytes -= b->size;
-      freed += b->size;
-      delete b;
-      segments_[i] = segments_.back();
-      segments_.pop_back();
-    } else {
-      i++;
-    }
-  }
-  return freed;
-}
-
-// Make `bytes` (plus the runtime reserve) free on the device: first the small
-// classes and the empty segments, then give up the reserve.
-bool Pool::make_room(size_t bytes) {
-  if (device_free_bytes() >= bytes + kRuntimeReserve) return true;
-  (void)hipDeviceSynchronize();
-  for (auto &kv : free_) {
-    for (void *q : kv.second) (void)hipFree(q);
-    cached -= kv.first * kv.second.size();
-    kv.second.clear();
-  }
-  free_segments();
-  return device_free_bytes() >= bytes;
-}
-
-void *Pool::raw_alloc(size_t bytes) {
-  void *p = nullptr;
-  if (device_free_bytes() < bytes + kRuntimeReserve) make_room(bytes);
-  if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    make_room(bytes);
-    HIPCHECK(hipMalloc(&p, bytes));
-  }
-  device_allocs++;
-  return p;
-}
-
-void Pool::trim() {
-  (void)hipDeviceSynchronize();
-  for (auto &kv : free_)
-    for (void *p : kv.second) (void)hipFree(p);
-  free_.clear();
-  free_segments();
-  cached = 0;
-  for (auto &kv : bins_) cached += kv.first;
-}
-
-void Pool::release_all() {
-  trim();
-  for (auto &kv : live_) (void)hipFree(kv.first);
-  live_.clear();
-  for (auto &s : segments_) (void)hipFree(s.first);
-  segments_.clear();
-  for (auto &kv : blocks_) delete kv.second;
-  blocks_.clear();
-  bins_.clear();
-  live = cached = segment_bytes = 0;
-}
-
-// Contexts that are alive; a ciphertext released after its context was
+// Live contexts and their serials: an object released after its context was
 // destroyed only drops its host record (the device memory went with the
-// context).
-// live contexts and their serials: objects freed after their context was
-// destroyed only drop their host record (a later context may reuse the
-// address, the serial tells them apart)
+// context; a later context may reuse the address, the serial tells them
+// apart).
 static std::unordered_map<ckks_context *, u64> g_live_contexts;
 static u64 g_next_serial = 1;
 

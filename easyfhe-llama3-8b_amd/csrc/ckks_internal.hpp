@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/ckks_mi355x.h"
+#include "device_pool.hpp"
 
 typedef uint64_t u64;
 typedef uint32_t u32;
@@ -134,40 +135,26 @@ __device__ __forceinline__ int prime_of(int limb, int q_limbs, int L) {
 
 // Device memory of one context: exact-size free lists plus the set of live
 // blocks, so that destroying the context returns everything it allocated.
-// Device memory of one context.  Blocks up to 1 MiB come from exact-size
-// free lists; larger ones are carved best-fit out of big segments, split on
-// allocation and merged with free neighbours on release, so that buffers of
-// every modulus level share one cache instead of one cache per size.
-struct Pool {
-  struct Block {
-    char *base;
-    size_t size;
-    bool free;
-    Block *prev, *next;  // address neighbours inside the segment
-    std::multimap<size_t, Block *>::iterator slot;  // entry in `bins_` while free
-  };
-  std::unordered_map<size_t, std::vector<void *>> free_;  // small classes
-  std::unordered_map<void *, size_t> live_;               // small blocks handed out
-  std::multimap<size_t, Block *> bins_;                   // free large blocks by size
-  std::unordered_map<void *, Block *> blocks_;            // every large block by base
-  std::vector<std::pair<char *, size_t>> segments_;
-  size_t live = 0, cached = 0, peak = 0, segment_bytes = 0;
-  u64 device_allocs = 0;
-  void *alloc(size_t bytes);
-  void release(void *p, size_t bytes);
-  // device memory for long-lived objects (keys, tensors), after giving back
-  // what the cache holds when the device is short of it
-  void *raw_alloc(size_t bytes);
-  void trim();
-  void release_all();
-
- private:
-  void *alloc_large(size_t bytes);
-  void release_large(void *p);
-  bool grow(size_t bytes);
-  bool make_room(size_t bytes);
-  size_t free_segments();
+// The HIP device behind the context's pool (device_pool.hpp).
+struct HipDevice {
+  static bool alloc(void **p, size_t bytes) {
+    if (hipMalloc(p, bytes) == hipSuccess) return true;
+    (void)hipGetLastError();
+    return false;
+  }
+  static void release(void *p) { (void)hipFree(p); }
+  static size_t free_bytes() {
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) != hipSuccess) {
+      (void)hipGetLastError();
+      return (size_t)-1;
+    }
+    return fr;
+  }
+  static void synchronize() { (void)hipDeviceSynchronize(); }
 };
+using Pool = BasicPool<HipDevice>;
+
 
 struct DeviceKey {
   u64 galois;
