@@ -2266,17 +2266,85 @@ __global__ void k_fft_place(const double *__restrict__ re, const double *__restr
   x[row * n + r] = cplx{re[row * n + j], im ? im[row * n + j] : 0.0};
 }
 
-// One radix-2 DIT stage of length `len`; grid (n / 2 / 256, rows)
-__global__ void k_fft_stage(cplx *__restrict__ x, int n, int len, const cplx *__restrict__ tw) {
-  const int bidx = blockIdx.x * TPB + threadIdx.x;
-  if (bidx >= n / 2) return;
-  const int half = len >> 1, step = n / len;
-  const int st = (bidx / half) * len, k = bidx % half;
+// Radix-2 DIT FFT of rows of n points (bit-reversed input).  Stage len
+// (2, 4, .., n) takes, for every st multiple of len and k < len / 2,
+//   u = x[st + k], v = x[st + k + len/2] * tw[k n / len],
+//   x[st + k] = u + v, x[st + k + len/2] = u - v
+// (complex product as cmul, each sum rounded once).  The stages run in two
+// launches per batch of rows: len = 2 .. min(n, kFftTile) inside tiles of
+// kFftTile contiguous points staged in LDS (k_fft_tile), then len =
+// 2 kFftTile .. n in registers over the points r + kFftTile m of a row
+// (k_fft_cols, M = n / kFftTile per thread).  The order of the stages, and
+// so every rounding, is that of the stage-by-stage definition above.
+constexpr int kFftTile = 2048;
+
+// grid (n / tile, rows), tile = min(n, kFftTile)
+__global__ __launch_bounds__(TPB) void k_fft_tile(cplx *__restrict__ x, int n, int tile,
+                                                  const cplx *__restrict__ tw) {
+  __shared__ cplx sm[kFftTile];
+  cplx *row = x + (size_t)blockIdx.y * n + (size_t)blockIdx.x * tile;
+  for (int i = threadIdx.x; i < tile; i += TPB) sm[i] = row[i];
+  __syncthreads();
+  for (int len = 2; len <= tile; len <<= 1) {
+    const int half = len >> 1, step = n / len;
+    for (int b = threadIdx.x; b < (tile >> 1); b += TPB) {
+      const int k = b & (half - 1);
+      const int i0 = 2 * (b - k) + k;
+      const cplx u = sm[i0];
+      const cplx v = cmul(sm[i0 + half], tw[k * step]);
+      sm[i0] = cplx{__dadd_rn(u.re, v.re), __dadd_rn(u.im, v.im)};
+      sm[i0 + half] = cplx{__dsub_rn(u.re, v.re), __dsub_rn(u.im, v.im)};
+    }
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < tile; i += TPB) row[i] = sm[i];
+}
+
+// grid (kFftTile / 256, rows); n = M kFftTile
+template <int M>
+__global__ __launch_bounds__(TPB) void k_fft_cols(cplx *__restrict__ x, int n,
+                                                  const cplx *__restrict__ tw) {
+  const int r = blockIdx.x * TPB + threadIdx.x;
   cplx *row = x + (size_t)blockIdx.y * n;
-  const cplx u = row[st + k];
-  const cplx v = cmul(row[st + k + half], tw[k * step]);
-  row[st + k] = cplx{__dadd_rn(u.re, v.re), __dadd_rn(u.im, v.im)};
-  row[st + k + half] = cplx{__dsub_rn(u.re, v.re), __dsub_rn(u.im, v.im)};
+  cplx v[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) v[m] = row[r + kFftTile * m];
+#pragma unroll
+  for (int hm = 1; hm < M; hm <<= 1) {
+    const int step = n / (2 * kFftTile * hm);
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      if (m & hm) continue;
+      const int k = r + kFftTile * (m & (hm - 1));
+      const cplx u = v[m];
+      const cplx w = cmul(v[m + hm], tw[k * step]);
+      v[m] = cplx{__dadd_rn(u.re, w.re), __dadd_rn(u.im, w.im)};
+      v[m + hm] = cplx{__dsub_rn(u.re, w.re), __dsub_rn(u.im, w.im)};
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) row[r + kFftTile * m] = v[m];
+}
+
+// In-place FFT of `rows` rows of n points (n a power of two, bit-reversed
+// input) with the stage twiddles `tw` (tw[k n / len] for stage len).
+static void launch_fft(ckks_context *c, cplx *x, int rows, int n, const cplx *tw) {
+  if (n < 2 || rows < 1) return;
+  if (rows > 65535) throw std::invalid_argument("fft: at most 65535 rows per launch");
+  const int tile = n < kFftTile ? n : kFftTile;
+  hipLaunchKernelGGL(k_fft_tile, dim3(n / tile, rows), dim3(TPB), 0, c->stream, x, n, tile, tw);
+  LAUNCH_CHECK();
+  const dim3 g(kFftTile / TPB, rows);
+  switch (n / tile) {
+    case 1: break;
+    case 2: hipLaunchKernelGGL(k_fft_cols<2>, g, dim3(TPB), 0, c->stream, x, n, tw); break;
+    case 4: hipLaunchKernelGGL(k_fft_cols<4>, g, dim3(TPB), 0, c->stream, x, n, tw); break;
+    case 8: hipLaunchKernelGGL(k_fft_cols<8>, g, dim3(TPB), 0, c->stream, x, n, tw); break;
+    case 16: hipLaunchKernelGGL(k_fft_cols<16>, g, dim3(TPB), 0, c->stream, x, n, tw); break;
+    case 32: hipLaunchKernelGGL(k_fft_cols<32>, g, dim3(TPB), 0, c->stream, x, n, tw); break;
+    default: throw std::invalid_argument("fft: at most 2^16 points");
+  }
+  LAUNCH_CHECK();
 }
 
 // Residue of an integer-valued double of any magnitude (exact).
@@ -2319,11 +2387,7 @@ static void encode_placed(ckks_context *c, cplx *x, int rows, int slots, double 
                           int limbs, int is_ext, const Batch &out) {
   const FFTTable &t = c->fft.at(slots);
   const int n = slots;
-  for (int len = 2; len <= n; len <<= 1) {
-    hipLaunchKernelGGL(k_fft_stage, dim3((n / 2 + TPB - 1) / TPB, rows), dim3(TPB), 0,
-                       c->stream, x, n, len, (const cplx *)t.tw_inv);
-    LAUNCH_CHECK();
-  }
+  launch_fft(c, x, rows, n, (const cplx *)t.tw_inv);
   const int total = limbs + (is_ext ? c->alpha : 0);
   hipLaunchKernelGGL(k_encode_finish, dim3(c->N / TPB, total, rows), dim3(TPB), 0, c->stream,
                      x, (const cplx *)t.twist, out, n, c->logN, scale, limbs, c->L, c->d_mods);
@@ -2558,11 +2622,7 @@ void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, dou
   hipLaunchKernelGGL(k_dec_garner, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, c->stream, m, K,
                      c->garner[K], (const cplx *)t.untwist, x, n, logn, c->logN, c->d_mods);
   LAUNCH_CHECK();
-  for (int len = 2; len <= n; len <<= 1) {
-    hipLaunchKernelGGL(k_fft_stage, dim3((n / 2 + TPB - 1) / TPB, 1), dim3(TPB), 0, c->stream,
-                       x, n, len, (const cplx *)t.tw_fwd);
-    LAUNCH_CHECK();
-  }
+  launch_fft(c, x, 1, n, (const cplx *)t.tw_fwd);
   hipLaunchKernelGGL(k_dec_gather, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, c->stream, x,
                      t.perm, n, ct->scale, d_re, d_im);
   LAUNCH_CHECK();
