@@ -31,7 +31,7 @@ constexpr int kMacGroups = 2;       // giant groups of one extended MAC pass
 constexpr int kMacCts = 4;          // ciphertexts per plaintext read in that pass
 constexpr int kTabGroups = 8;       // giant groups of one Q-basis MAC pass (k_mac_table)
 constexpr int kTabCts = 2;          // ciphertexts per plaintext read in that pass
-constexpr int kTabCtsFp = 4;        // the same for its fp64 path
+constexpr int kTabCtsFp = 8;        // the same for its fp64 path
 constexpr int kMultiItems = 4;    // items per multi-rotation key inner product launch
 
 // Per-prime constants, resident in device memory.
