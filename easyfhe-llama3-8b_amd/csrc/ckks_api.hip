@@ -616,10 +616,64 @@ static void build_context(ckks_context *c, const ckks_params &p) {
   HIPCHECK(hipFree(d_sv));
 }
 
+// Pinned staging: buffers in 1 MiB units, up to 1 GiB in all; past that the
+// stream is drained and the buffers too small for the request are dropped.
+static constexpr size_t kStageUnit = (size_t)1 << 20, kStageCap = (size_t)1 << 30;
+
+namespace ckks {
+void upload_async(ckks_context *c, void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return;
+  ckks_context::StageBuf *pick = nullptr;
+  for (auto &b : c->stage)
+    if (b.bytes >= bytes && hipEventQuery(b.ev) == hipSuccess) {
+      pick = &b;
+      break;
+    }
+  if (!pick) {
+    const size_t want = (bytes + kStageUnit - 1) / kStageUnit * kStageUnit;
+    size_t total = 0;
+    for (auto &b : c->stage) total += b.bytes;
+    if (total + want > kStageCap) {
+      HIPCHECK(hipStreamSynchronize(c->stream));
+      for (auto &b : c->stage)
+        if (b.bytes >= bytes) {
+          pick = &b;
+          break;
+        }
+      if (!pick) {
+        for (auto &b : c->stage) {
+          (void)hipHostFree(b.p);
+          (void)hipEventDestroy(b.ev);
+        }
+        c->stage.clear();
+      }
+    }
+    if (!pick) {
+      ckks_context::StageBuf nb{nullptr, want, nullptr};
+      HIPCHECK(hipHostMalloc(&nb.p, want, hipHostMallocDefault));
+      if (hipEventCreateWithFlags(&nb.ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipHostFree(nb.p);
+        throw std::runtime_error("hipEventCreateWithFlags failed");
+      }
+      c->stage.push_back(nb);
+      pick = &c->stage.back();
+    }
+  }
+  memcpy(pick->p, src, bytes);
+  HIPCHECK(hipMemcpyAsync(dst, pick->p, bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHECK(hipEventRecord(pick->ev, c->stream));
+}
+}  // namespace ckks
+
 static void free_context(ckks_context *c) {
   if (!c) return;
   g_live_contexts.erase(c);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto &b : c->stage) {
+    (void)hipHostFree(b.p);
+    (void)hipEventDestroy(b.ev);
+  }
+  c->stage.clear();
   for (auto &kv : c->keys) (void)hipFree(kv.second.data);
   for (auto &kv : c->bc_up) {
     (void)hipFree(kv.second.d);
@@ -1292,15 +1346,11 @@ int ckks_encode_rows(ckks_context *c, const double *re, const double *im, int ro
     Scratch s(c);
     double *dre = (double *)s.get((size_t)nr * slots);
     double *dim = im ? (double *)s.get((size_t)nr * slots) : nullptr;
-    HIPCHECK(hipMemcpyAsync(dre, re + (size_t)r0 * slots, sizeof(double) * nr * slots,
-                            hipMemcpyHostToDevice, c->stream));
-    if (im)
-      HIPCHECK(hipMemcpyAsync(dim, im + (size_t)r0 * slots, sizeof(double) * nr * slots,
-                              hipMemcpyHostToDevice, c->stream));
+    upload_async(c, dre, re + (size_t)r0 * slots, sizeof(double) * nr * slots);
+    if (im) upload_async(c, dim, im + (size_t)r0 * slots, sizeof(double) * nr * slots);
     Batch o{};
     for (int r = 0; r < nr; r++) o.p[r] = out[r0 + r]->d;
     launch_encode(c, dre, dim, nr, slots, scale, limbs, is_ext, o);
-    HIPCHECK(hipStreamSynchronize(c->stream));
   }
   API_END
 }
@@ -1843,10 +1893,8 @@ int ckks_hoisted_mac_sum_many(ckks_context *c, const ckks_ct *const *babies, int
   for (size_t j = 0; j < ptab.size(); j++) ptab[j] = (u64)pts[j]->d;
   Scratch s(c);
   u64 *dbt = s.get(btab.size()), *dpt = s.get(ptab.size());
-  HIPCHECK(hipMemcpyAsync(dbt, btab.data(), sizeof(u64) * btab.size(), hipMemcpyHostToDevice,
-                          c->stream));
-  HIPCHECK(hipMemcpyAsync(dpt, ptab.data(), sizeof(u64) * ptab.size(), hipMemcpyHostToDevice,
-                          c->stream));
+  upload_async(c, dbt, btab.data(), sizeof(u64) * btab.size());
+  upload_async(c, dpt, ptab.data(), sizeof(u64) * ptab.size());
   const int GC = std::min(kTabGroups, giant_count);
   u64 *inner = s.get((size_t)GC * n * CP);
   const double scale = babies[0]->scale * pts[0]->scale;
@@ -1937,8 +1985,7 @@ static void ext_babies(ckks_context *c, const ckks_ct *const *a, int n, const in
     for (size_t r = 0; r < rb.size(); r++)
       for (int it = 0; it < ni; it++) table[r * ni + it] = dst[(size_t)rb[r] * n + i0 + it];
     u64 *dtab = s.get(table.size());
-    HIPCHECK(hipMemcpyAsync(dtab, table.data(), sizeof(u64) * table.size(),
-                            hipMemcpyHostToDevice, c->stream));
+    upload_async(c, dtab, table.data(), sizeof(u64) * table.size());
     Batch c0{};
     for (int it = 0; it < ni; it++) c0.p[it] = a[i0 + it]->d;
     launch_key_inner_multi(c, ext + (size_t)i0 * est, est, ni, keys, ginv, c0,
@@ -2076,10 +2123,9 @@ int ckks_linear_combination(ckks_context *c, const ckks_ct *const *terms, int T,
   u64 *dout = s.get(n);
   u64 *wtab = s.get((size_t)T * limbs);
   u64 *ctab = s.get(limbs);
-  HIPCHECK(hipMemcpyAsync(dtab, table.data(), sizeof(u64) * table.size(), hipMemcpyHostToDevice,
-                          c->stream));
-  HIPCHECK(hipMemcpyAsync(dw, w.data(), sizeof(double) * T, hipMemcpyHostToDevice, c->stream));
-  HIPCHECK(hipMemcpyAsync(dout, outp.data(), sizeof(u64) * n, hipMemcpyHostToDevice, c->stream));
+  upload_async(c, dtab, table.data(), sizeof(u64) * table.size());
+  upload_async(c, dw, w.data(), sizeof(double) * T);
+  upload_async(c, dout, outp.data(), sizeof(u64) * n);
   launch_lincomb(c, dtab, T, n, dw, rint(constant), (u64 *const *)dout, limbs, wtab, ctab);
   API_END
 }
@@ -2259,11 +2305,9 @@ int ckks_encode_structured(ckks_context *c, const ckks_tensor *const *sources, i
   for (int r = 0; r < rows; r++) out[r] = new_ct(c, 1, limbs, is_ext, slots, scale, 1);
   Scratch s(c);
   u64 *dmaps = s.get(maps.size());
-  HIPCHECK(hipMemcpyAsync(dmaps, maps.data(), sizeof(u64) * maps.size(), hipMemcpyHostToDevice,
-                          c->stream));
+  upload_async(c, dmaps, maps.data(), sizeof(u64) * maps.size());
   DiagGeom gm{D, lanes, baby, giant_base};
   launch_encode_diagonals(c, nullptr, 0, &src, dmaps, gm, rows, slots, scale, limbs, is_ext, out);
-  HIPCHECK(hipStreamSynchronize(c->stream));
   API_END
 }
 

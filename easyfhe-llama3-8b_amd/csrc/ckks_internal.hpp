@@ -190,6 +190,14 @@ struct ckks_context {
   int N, logN, L, alpha, ds, K;
   hipStream_t stream;
   ckks::Pool pool;
+  // pinned staging of host-to-device uploads made mid-computation: a buffer
+  // is reused once the event recorded after its copy has completed
+  struct StageBuf {
+    void *p;
+    size_t bytes;
+    hipEvent_t ev;
+  };
+  std::vector<StageBuf> stage;
   std::vector<u64> primes;
   std::vector<int8_t> secret;
   ckks::ModQ *d_mods;  // [K]
@@ -300,6 +308,10 @@ void launch_lincomb(ckks_context *c, const u64 *d_table, int T, int n, const dou
                     double cst, u64 *const *d_outp, int limbs, u64 *wtab, u64 *ctab);
 void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *const *pts, int B,
                       int G, u64 *out, int limbs);
+// Queue a copy of `bytes` host bytes to device memory `dst` on the context
+// stream without waiting for it (the bytes go through pinned staging first,
+// so `src` may be freed on return).
+void upload_async(ckks_context *c, void *dst, const void *src, size_t bytes);
 void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, int G,
                      u64 *out, int E, int q_limbs);
 void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);
