@@ -34,7 +34,7 @@ from .attention import (AttentionGeometry, SoftmaxConfig, attention_fhe, attenti
                         kv_repeat_rows, softmax_depth)
 from .complex import pair_real_ciphers, split_complex_ciphers_twice
 from .layout import FeatureMajorPrefillLayout
-from .linear import LinearOperator, LinearWeight, linear_rotations
+from .linear import LinearOperator, LinearOperatorConfig, LinearWeight, linear_rotations
 from .mlp import FeatureMajorMLPLayout, MLPWeights, mlp_depth, mlp_fhe
 from .rmsnorm import residual_add, rmsnorm_depth, rmsnorm_fhe, rmsnorm_rotations
 from .rope import rope_fhe, rope_rotations
@@ -159,7 +159,8 @@ def decoder_layer_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_con
     sync = ctx.synchronize
     stage: dict[str, float] = {}
     t_start = time.perf_counter()
-    op = LinearOperator(context=ctx, token_lanes=geo.lanes)
+    op = LinearOperator(context=ctx, token_lanes=geo.lanes,
+                        config=LinearOperatorConfig(timed_stages=False))
     keep: list = []
     try:
         t0 = time.perf_counter()
@@ -316,7 +317,8 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
     sync = ctx.synchronize
     stage: dict[str, float] = {}
     t_start = time.perf_counter()
-    op = LinearOperator(context=ctx, token_lanes=geo.lanes)
+    op = LinearOperator(context=ctx, token_lanes=geo.lanes,
+                        config=LinearOperatorConfig(timed_stages=False))
     keep: list = []
     try:
         t0 = time.perf_counter()

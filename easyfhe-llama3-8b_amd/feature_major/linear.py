@@ -122,6 +122,10 @@ class LinearOperatorConfig:
     hoist_strategy: str = "normal"
     constant_cache_mode: str = "none"
     raw_weight_policy: str = "device"
+    # synchronise after each stage so that apply()'s profile holds device
+    # time; False keeps the stream busy across stages and chunks (the
+    # profile then holds host time)
+    timed_stages: bool = True
 
     def __post_init__(self) -> None:
         if int(self.baby_steps) <= 0:
@@ -329,7 +333,7 @@ class LinearOperator:
                 raise ValueError("an exact output scale needs inputs of one scale.")
             pt_scale = float(output_scale) * float(int(ctx.primes()[limbs - 1])) / s_in
         ext = str(self.config.hoist_strategy).lower() != "normal"
-        sync = ctx.synchronize
+        sync = ctx.synchronize if self.config.timed_stages else (lambda: None)
         t0 = time.perf_counter()
         babies = None if ext else self._ensure_babies(inputs, plan)
         sync()

@@ -186,7 +186,8 @@ def mlp_fhe(input_ciphers, weights: MLPWeights, *, silu: dict, crypto_context,
     if int(xs[0].state.cur_limbs) < depth + 1:
         raise ValueError(f"MLP needs {depth + 1} limbs, inputs have {xs[0].state.cur_limbs}.")
     own_op = operator is None
-    op = operator or LinearOperator(context=ctx, token_lanes=int(lay.canonical.tokens_per_cipher))
+    op = operator or LinearOperator(context=ctx, token_lanes=int(lay.canonical.tokens_per_cipher),
+                                    config=LinearOperatorConfig(timed_stages=False))
     coeffs = np.asarray(silu["coefficients"], dtype=np.float64)
     stage = {"pair": 0.0, "gate_up": 0.0, "split": 0.0, "silu": 0.0, "product": 0.0,
              "down": 0.0, "output_split": 0.0}
