@@ -728,32 +728,24 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     `weight_sets` distinct sets cycled over the layers; inputs N(0, 1); seed
     0.  The error is against the same layers in fp64 with exact softmax."""
     from easyfhe import fhe
-    from easyfhe.bs import openfhe as bs
     from feature_major import FeatureMajorPrefillLayout
     from feature_major.approx import rsqrt_entry, silu_entry
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     refreshed_layer_depths)
+                                     refreshed_layer_programs)
 
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     norm = rsqrt_entry(0.5, 16.0, 63)
     ap = LayerApproximations(norm, norm, silu_entry(-12.0, 12.0, 63),
-                             SoftmaxConfig(rounds=3, shift=8.0, bound=8.0, exp_degree=9,
+                             SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=9,
                                            first_inverse_degree=31, inverse_degree=47))
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
     spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=0,
                                rotations=decoder_layer_rotations(lay, H, hd))
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
-    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3), output_levels=0))
-    out_levels = ctx.L - probe.depth_limbs - 1
-    probe.release()
-    need = max(refreshed_layer_depths(ap, T)) + 1
-    if out_levels + 1 < need:
-        raise ValueError(f"bootstrap outputs {out_levels + 1} limbs, the layer needs {need}")
-    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3),
-                                             output_levels=out_levels))
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15)
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
@@ -775,7 +767,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     t_all = time.perf_counter()
     for layer in range(int(n_layers)):
         res = decoder_layer_refreshed_fhe(cur, dev[layer % len(dev)], crypto_context=ctx,
-                                          program=prog)
+                                          program=prog, residual_program=res_prog)
         for c in cur:
             c.release()
         cur = list(res.ciphers)
@@ -808,7 +800,8 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
         "workload": f"{n_layers} Llama-3-8B decoder layers (d=4096, 32/8 heads x 128, SwiGLU 14336) "
                     "over 128 tokens in 16 ciphertexts of 8 lanes, bootstraps included "
                     "(3 paired refreshes = 24 bootstraps per layer), N=2^16, Q=1x60b+65x40b, "
-                    f"dnum=5, P=14x44b; bootstrap outputs {out_levels + 1} limbs; "
+                    f"dnum=5, P=14x44b; bootstraps return {prog.output_limbs} limbs (scores) "
+                    f"and {res_prog.output_limbs} (residual stream); "
                     f"{len(wsets)} weight sets cycled",
         "last_layer_stages_s": {k: round(v, 3) for k, v in stages.items()},
         "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
@@ -900,9 +893,9 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
     import torch
 
     from easyfhe import fhe
-    from easyfhe.bs import openfhe as bs
     from feature_major import FeatureMajorPrefillLayout
-    from feature_major.layer import DecoderLayerWeights, decoder_layer_rotations
+    from feature_major.layer import (DecoderLayerWeights, decoder_layer_rotations,
+                                     refreshed_layer_depths, refreshed_layer_programs)
     from feature_major.model import (approximations_for, embed_tokens, final_logits,
                                      layer_ranges, prefill_fhe)
 
@@ -912,11 +905,6 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
                                rotations=decoder_layer_rotations(lay, H, hd))
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
-    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3), output_levels=0))
-    out_levels = ctx.L - probe.depth_limbs - 1
-    probe.release()
-    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=15, level_budget=(3, 3),
-                                             output_levels=out_levels))
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
 
@@ -968,6 +956,13 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         torch.cuda.empty_cache()
         ctx.synchronize()
         prep_s = time.perf_counter() - t0
+        # every layer's series have the same degrees, hence the same depths
+        if len({refreshed_layer_depths(w_.approx, T) for w_ in layers}) != 1:
+            raise ValueError("layers with different depths need programs of their own")
+        t0 = time.perf_counter()
+        prog, res_prog = refreshed_layer_programs(ctx, layers[0].approx, T, log_slots=15)
+        ctx.synchronize()
+        setup_s += time.perf_counter() - t0
 
         packed = lay.pack(x_test)
         cts = [client.encrypt(packed[i], cur_limbs=1, enc_id=700000 + i)
@@ -975,7 +970,8 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
         ev0.record()
         t0 = time.perf_counter()
-        res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog, residual_bounds=bounds,
+        res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog,
+                          residual_program=res_prog, residual_bounds=bounds,
                           on_layer=lambda i, s: print(f"layer {i}: {s:.2f} s", file=sys.stderr,
                                                       flush=True))
         ev1.record()

@@ -301,19 +301,45 @@ def refreshed_layer_depths(approx: LayerApproximations, seq_len: int) -> tuple[i
     return a, b, c
 
 
+def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_len: int, *,
+                             log_slots: int, level_budget=(3, 3)):
+    """(score program, residual program): bootstrap programs whose outputs
+    hold the score block plus one limb, and the deeper of the two residual
+    blocks plus two (``refreshed_layer_depths``).  A bootstrap raises its
+    input only to its outputs plus its own depth, so the residual program,
+    with fewer output levels, runs every stage on fewer limbs."""
+    from easyfhe.bs import openfhe as bs
+
+    ctx = _ctx(crypto_context)
+    a, b, c = refreshed_layer_depths(approx, seq_len)
+    spec = lambda levels: bs.BootstrapSpec(log_slots=int(log_slots),  # noqa: E731
+                                           level_budget=tuple(level_budget),
+                                           output_levels=int(levels))
+    probe = bs.generate(ctx, spec(0))
+    top = ctx.L - probe.depth_limbs - 1
+    probe.release()
+    if top < b or top < max(a, c) + 1:
+        raise ValueError(f"the chain's bootstraps return at most {top + 1} limbs; the layer "
+                         f"needs {max(b + 1, max(a, c) + 2)}.")
+    return bs.generate(ctx, spec(b)), bs.generate(ctx, spec(max(a, c) + 1))
+
+
 def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
-                                program, residual_bound: float = 32.0, group: int = 8,
-                                rope_theta: float = 500000.0) -> LayerResult:
+                                program, residual_program=None, residual_bound: float = 32.0,
+                                group: int = 8, rope_theta: float = 500000.0) -> LayerResult:
     """One decoder layer with its refreshes (three paired refresh points: the
     residual stream before each RMSNorm, and the softmax's mapped scores;
     the reference refreshes at the same places, graph.py:780-990,
     operators/norm/refresh.py:153-344, the pre-exp checkpoint of
-    operators/attention/softmax.py).  ``program`` is a bootstrap program whose
-    outputs hold the deepest block plus one limb.  The input may sit at any
-    level; it is not consumed."""
+    operators/attention/softmax.py).  ``program`` refreshes the scores and
+    must return the score block's depth plus one limb; ``residual_program``
+    (default ``program``) refreshes the residual stream and must return the
+    deeper residual block plus two (``refreshed_layer_programs`` makes
+    both).  The input may sit at any level; it is not consumed."""
     ctx = _ctx(crypto_context)
     lay, geo, ap = weights.layout, weights.geometry, weights.approx
     a_depth, b_depth, c_depth = refreshed_layer_depths(ap, geo.seq_len)
+    res_prog = program if residual_program is None else residual_program
     sync = ctx.synchronize
     stage: dict[str, float] = {}
     t_start = time.perf_counter()
@@ -322,13 +348,14 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
     keep: list = []
     try:
         t0 = time.perf_counter()
-        x = refresh_stream(input_ciphers, crypto_context=ctx, program=program,
+        x = refresh_stream(input_ciphers, crypto_context=ctx, program=res_prog,
                            value_bound=residual_bound, group=group)
         keep = x
         sync()
         stage["refresh_residual_1"] = time.perf_counter() - t0
-        if int(x[0].state.cur_limbs) < max(a_depth, b_depth, c_depth) + 1:
-            raise ValueError("the bootstrap program's outputs are too shallow for the layer.")
+        if int(x[0].state.cur_limbs) < max(a_depth, c_depth) + 2:
+            raise ValueError("the residual bootstrap program's outputs are too shallow for the "
+                             "layer.")
         x = keep = _drop_owned(x, a_depth + 2, ctx)
         t0 = time.perf_counter()
         n1 = rmsnorm_fhe(x, np.zeros(1), coeffs=ap.input_norm, layout=lay, crypto_context=ctx)
@@ -355,6 +382,10 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         sr = refresh_stream(scores.ciphers, crypto_context=ctx, program=program, value_bound=1.0,
                             group=group)
         scores.release()
+        if int(sr[0].state.cur_limbs) < b_depth + 1:
+            _release(sr)
+            raise ValueError("the score bootstrap program's outputs are too shallow for the "
+                             "layer.")
         sync()
         stage["refresh_scores"] = time.perf_counter() - t0
         t0 = time.perf_counter()
@@ -377,7 +408,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         sync()
         stage["softmax_pv_output_residual"] = time.perf_counter() - t0
         t0 = time.perf_counter()
-        hr = refresh_stream(h, crypto_context=ctx, program=program, value_bound=residual_bound,
+        hr = refresh_stream(h, crypto_context=ctx, program=res_prog, value_bound=residual_bound,
                             group=group)
         _release(h)
         hr = keep = _drop_owned(hr, c_depth + 2, ctx)
@@ -401,4 +432,4 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
 
 __all__ = ["DecoderLayerWeights", "LayerApproximations", "LayerResult", "decoder_layer_depth",
            "decoder_layer_fhe", "decoder_layer_refreshed_fhe", "decoder_layer_rotations",
-           "refresh_stream", "refreshed_layer_depths"]
+           "refresh_stream", "refreshed_layer_depths", "refreshed_layer_programs"]

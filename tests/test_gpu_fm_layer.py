@@ -339,13 +339,12 @@ def test_refreshed_decoder_layer_matches_poly_model():
     two layers in a row from a one-limb input, 64 tokens x 512 features at
     N = 2^13: against the fp64 model of the same two layers.  The tolerance
     covers six bootstraps at ~20 bits on values up to 32."""
-    from easyfhe.bs import openfhe as bs
     from feature_major import FeatureMajorPrefillLayout
     from feature_major.approx import rsqrt_entry, silu_entry
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     refreshed_layer_depths)
+                                     refreshed_layer_depths, refreshed_layer_programs)
 
     T, D, H, KV, hd, I = 64, 512, 4, 2, 128, 1408
     lay0 = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=4096)
@@ -354,12 +353,11 @@ def test_refreshed_decoder_layer_matches_poly_model():
     norm = rsqrt_entry(0.5, 16.0, 63)
     ap = LayerApproximations(norm, norm, silu_entry(), SoftmaxConfig(rounds=2, shift=4.0,
                                                                      bound=4.0))
-    need = max(refreshed_layer_depths(ap, T)) + 1
-    probe = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3), output_levels=0))
-    out_levels = ctx.L - probe.depth_limbs - 1
-    assert out_levels + 1 >= need, (out_levels, need)
-    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3),
-                                             output_levels=out_levels))
+    # a score program at the score block's depth, a shallower one for the
+    # residual stream
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=12)
+    a, b, c = refreshed_layer_depths(ap, T)
+    assert prog.output_limbs == b + 1 and res_prog.output_limbs == max(a, c) + 2
     rng = np.random.default_rng(13)
     x = rng.normal(0, 1, (T, D))
     sd = 1.0 / np.sqrt(D)
@@ -378,8 +376,10 @@ def test_refreshed_decoder_layer_matches_poly_model():
                                                        shift=sm.shift))
     with DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
                              intermediate=I, approx=ap, layout=lay, context=ctx) as w:
-        r1 = decoder_layer_refreshed_fhe(xc, w, crypto_context=ctx, program=prog)
-        r2 = decoder_layer_refreshed_fhe(r1.ciphers, w, crypto_context=ctx, program=prog)
+        r1 = decoder_layer_refreshed_fhe(xc, w, crypto_context=ctx, program=prog,
+                                         residual_program=res_prog)
+        r2 = decoder_layer_refreshed_fhe(r1.ciphers, w, crypto_context=ctx, program=prog,
+                                         residual_program=res_prog)
     want1 = LN.decoder_layer_numpy(x, wq, wk, wv, wo, G, U, Dn, **kw)
     want2 = LN.decoder_layer_numpy(want1, wq, wk, wv, wo, G, U, Dn, **kw)
     got1 = _decrypt_stream(client, lay, r1.ciphers)
