@@ -303,12 +303,12 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
 }
 
 // forward, bit positions 15..8: tile = 256 rows (stride 256) x 16 columns
-__global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, int l_begin,
+__device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
                                                         const ModQ *__restrict__ mods,
                                                         const u64 *__restrict__ psi,
                                                         const u64 *__restrict__ psi_sh) {
-  __shared__ u64 sm[16 * 272];
+  u64 *sm = lds;
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
@@ -356,12 +356,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_high(Batch src, Batch dst, in
 // forward, bit positions 7..0: tile = 16 contiguous rows of 256; output in [0, q)
 // (COMBINE: the ModDown epilogue instead of the store)
 template <bool COMBINE>
-__global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, int q_limbs,
+__device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                        int L, const ModQ *__restrict__ mods,
                                                        const u64 *__restrict__ psi,
                                                        const u64 *__restrict__ psi_sh,
                                                        MDCombine md) {
-  __shared__ u64 sm[16 * 272];
+  u64 *sm = lds;
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
@@ -422,12 +422,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16_fwd_low(Batch dst, int l_begin, i
 }
 
 // inverse, bit positions 0..7 (first pass): input in [0, 2q), output lazy
-__global__ __launch_bounds__(TPB) void k_ntt16_inv_low(Batch src, Batch dst, int l_begin,
+__device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                        int q_limbs, int L,
                                                        const ModQ *__restrict__ mods,
                                                        const u64 *__restrict__ ipsi,
                                                        const u64 *__restrict__ ipsi_sh) {
-  __shared__ u64 sm[16 * 272];
+  u64 *sm = lds;
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
@@ -477,12 +477,12 @@ __global__ __launch_bounds__(TPB) void k_ntt16_inv_low(Batch src, Batch dst, int
 }
 
 // inverse, bit positions 8..15 (second pass), then x N^-1, output in [0, q)
-__global__ __launch_bounds__(TPB) void k_ntt16_inv_high(Batch dst, int l_begin, int q_limbs,
+__device__ __forceinline__ void k_ntt16_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                         int L, const ModQ *__restrict__ mods,
                                                         const u64 *__restrict__ ipsi,
                                                         const u64 *__restrict__ ipsi_sh,
                                                         const u64 *__restrict__ ninv) {
-  __shared__ u64 sm[16 * 272];
+  u64 *sm = lds;
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const u64 q = mods[p].q, q2 = 2 * q;
@@ -580,11 +580,11 @@ __device__ __forceinline__ double as_dbl(u64 v) { return __longlong_as_double((l
 __device__ __forceinline__ u64 dbl_bits(double v) { return (u64)__double_as_longlong(v); }
 
 // Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
-__global__ __launch_bounds__(TPB) void k_ntt16f_fwd_high(Batch src, Batch dst, int l_begin,
+__device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                          int q_limbs, int L,
                                                          const ModQ *__restrict__ mods,
                                                          const double2 *__restrict__ tw) {
-  __shared__ double sm[16 * 272];
+  double *sm = reinterpret_cast<double *>(lds);
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q;
@@ -626,11 +626,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_high(Batch src, Batch dst, i
 }
 
 template <bool COMBINE>
-__global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, int q_limbs,
+__device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                         int L, const ModQ *__restrict__ mods,
                                                         const double2 *__restrict__ tw,
                                                         MDCombine md) {
-  __shared__ double sm[16 * 272];
+  double *sm = reinterpret_cast<double *>(lds);
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
@@ -685,11 +685,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_fwd_low(Batch dst, int l_begin, 
   }
 }
 
-__global__ __launch_bounds__(TPB) void k_ntt16f_inv_low(Batch src, Batch dst, int l_begin,
+__device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
                                                         const ModQ *__restrict__ mods,
                                                         const double2 *__restrict__ itw) {
-  __shared__ double sm[16 * 272];
+  double *sm = reinterpret_cast<double *>(lds);
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
@@ -734,11 +734,11 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_inv_low(Batch src, Batch dst, in
   for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = dbl_bits(x[k]);
 }
 
-__global__ __launch_bounds__(TPB) void k_ntt16f_inv_high(Batch dst, int l_begin, int q_limbs,
+__device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                          int L, const ModQ *__restrict__ mods,
                                                          const double2 *__restrict__ itw,
                                                          const double2 *__restrict__ ninv) {
-  __shared__ double sm[16 * 272];
+  double *sm = reinterpret_cast<double *>(lds);
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
   const double q = (double)mods[p].q, qinv = 1.0 / q;
@@ -780,62 +780,87 @@ __global__ __launch_bounds__(TPB) void k_ntt16f_inv_high(Batch dst, int l_begin,
     io[(g + 16 * k) * 256 + col] = fp_canon(fp_mulmod(x[k], ni.x, ni.y, q), qinv, q);
 }
 
-static void ntt16_launch(ckks_context *c, bool fp, const Batch &src, const Batch &dst,
-                         int n_items, int l_begin, int l_count, int q_limbs, bool inverse) {
-  // grid (tiles, items, limbs): blocks of one prime run back to back and
-  // share its twiddle table in L2
-  dim3 block(TPB), grid(16, n_items, l_count);
-  if (fp) {
-    const double2 *tw = (const double2 *)(inverse ? c->d_itw_fp : c->d_tw_fp);
-    if (!inverse) {
-      hipLaunchKernelGGL(k_ntt16f_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                         c->L, c->d_mods, tw);
-      LAUNCH_CHECK();
-      hipLaunchKernelGGL(k_ntt16f_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin,
-                         q_limbs, c->L, c->d_mods, tw, MDCombine{});
-      LAUNCH_CHECK();
-    } else {
-      hipLaunchKernelGGL(k_ntt16f_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                         c->L, c->d_mods, tw);
-      LAUNCH_CHECK();
-      hipLaunchKernelGGL(k_ntt16f_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs,
-                         c->L, c->d_mods, tw, (const double2 *)c->d_ninv_fp);
-      LAUNCH_CHECK();
-    }
-    return;
-  }
-  if (!inverse) {
-    hipLaunchKernelGGL(k_ntt16_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                       c->L, c->d_mods, c->d_psi, c->d_psi_sh);
-    LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_ntt16_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin,
-                       q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh, MDCombine{});
-    LAUNCH_CHECK();
-  } else {
-    hipLaunchKernelGGL(k_ntt16_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                       c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh);
-    LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_ntt16_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
-                       c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv);
-    LAUNCH_CHECK();
-  }
+// One launch per pass over every limb of a batch: a block takes the fp64
+// body when its prime is below 2^45 and the 64-bit body otherwise (q_0), so
+// the few 64-bit limbs run beside the others instead of in launches of their
+// own.  Both bodies share one LDS tile.
+constexpr u64 kFpPrimeBound = (u64)1 << 45;
+
+__global__ __launch_bounds__(TPB) void k_ntt16m_fwd_high(Batch src, Batch dst, int l_begin,
+                                                         int q_limbs, int L,
+                                                         const ModQ *__restrict__ mods,
+                                                         const u64 *__restrict__ psi,
+                                                         const u64 *__restrict__ psi_sh,
+                                                         const double2 *__restrict__ tw) {
+  __shared__ u64 lds[16 * 272];
+  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
+    k_ntt16f_fwd_high_body(lds, src, dst, l_begin, q_limbs, L, mods, tw);
+  else
+    k_ntt16_fwd_high_body(lds, src, dst, l_begin, q_limbs, L, mods, psi, psi_sh);
 }
 
-// Launch over maximal runs of limbs whose primes share one arithmetic path.
+template <bool COMBINE>
+__global__ __launch_bounds__(TPB) void k_ntt16m_fwd_low(Batch dst, int l_begin, int q_limbs,
+                                                        int L, const ModQ *__restrict__ mods,
+                                                        const u64 *__restrict__ psi,
+                                                        const u64 *__restrict__ psi_sh,
+                                                        const double2 *__restrict__ tw,
+                                                        MDCombine md) {
+  __shared__ u64 lds[16 * 272];
+  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
+    k_ntt16f_fwd_low_body<COMBINE>(lds, dst, l_begin, q_limbs, L, mods, tw, md);
+  else
+    k_ntt16_fwd_low_body<COMBINE>(lds, dst, l_begin, q_limbs, L, mods, psi, psi_sh, md);
+}
+
+__global__ __launch_bounds__(TPB) void k_ntt16m_inv_low(Batch src, Batch dst, int l_begin,
+                                                        int q_limbs, int L,
+                                                        const ModQ *__restrict__ mods,
+                                                        const u64 *__restrict__ ipsi,
+                                                        const u64 *__restrict__ ipsi_sh,
+                                                        const double2 *__restrict__ itw) {
+  __shared__ u64 lds[16 * 272];
+  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
+    k_ntt16f_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, itw);
+  else
+    k_ntt16_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh);
+}
+
+__global__ __launch_bounds__(TPB) void k_ntt16m_inv_high(Batch dst, int l_begin, int q_limbs,
+                                                         int L, const ModQ *__restrict__ mods,
+                                                         const u64 *__restrict__ ipsi,
+                                                         const u64 *__restrict__ ipsi_sh,
+                                                         const u64 *__restrict__ ninv,
+                                                         const double2 *__restrict__ itw,
+                                                         const double2 *__restrict__ ninv_fp) {
+  __shared__ u64 lds[16 * 272];
+  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
+    k_ntt16f_inv_high_body(lds, dst, l_begin, q_limbs, L, mods, itw, ninv_fp);
+  else
+    k_ntt16_inv_high_body(lds, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh, ninv);
+}
+
+// grid (tiles, items, limbs): blocks of one prime run back to back and share
+// its twiddle table in L2
 static void ntt16_dispatch(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                            int l_begin, int l_count, int q_limbs, bool inverse) {
-  int start = l_begin;
-  const int end = l_begin + l_count;
-  while (start < end) {
-    auto is_fp = [&](int limb) {
-      const int p = limb < q_limbs ? limb : c->L + (limb - q_limbs);
-      return c->prime_fp[p] != 0;
-    };
-    const bool fp = is_fp(start);
-    int stop = start + 1;
-    while (stop < end && is_fp(stop) == fp) stop++;
-    ntt16_launch(c, fp, src, dst, n_items, start, stop - start, q_limbs, inverse);
-    start = stop;
+  dim3 block(TPB), grid(16, n_items, l_count);
+  if (!inverse) {
+    hipLaunchKernelGGL(k_ntt16m_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                       c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_ntt16m_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin, q_limbs,
+                       c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp,
+                       MDCombine{});
+    LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL(k_ntt16m_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
+                       c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh, (const double2 *)c->d_itw_fp);
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_ntt16m_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
+                       c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
+                       (const double2 *)c->d_itw_fp, (const double2 *)c->d_ninv_fp);
+    LAUNCH_CHECK();
   }
 }
 
@@ -899,30 +924,13 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   md.out = out;
   md.out1_off = out1_off;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
-  int start = 0;
-  while (start < limbs) {
-    const bool fp = c->prime_fp[start] != 0;
-    int stop = start + 1;
-    while (stop < limbs && (c->prime_fp[stop] != 0) == fp) stop++;
-    dim3 block(TPB), grid(16, 2 * n, stop - start);
-    if (fp) {
-      const double2 *tw = (const double2 *)c->d_tw_fp;
-      hipLaunchKernelGGL(k_ntt16f_fwd_high, grid, block, 0, c->stream, conv, conv, start, limbs,
-                         c->L, c->d_mods, tw);
-      LAUNCH_CHECK();
-      hipLaunchKernelGGL(k_ntt16f_fwd_low<true>, grid, block, 0, c->stream, conv, start, limbs,
-                         c->L, c->d_mods, tw, md);
-      LAUNCH_CHECK();
-    } else {
-      hipLaunchKernelGGL(k_ntt16_fwd_high, grid, block, 0, c->stream, conv, conv, start, limbs,
-                         c->L, c->d_mods, c->d_psi, c->d_psi_sh);
-      LAUNCH_CHECK();
-      hipLaunchKernelGGL(k_ntt16_fwd_low<true>, grid, block, 0, c->stream, conv, start, limbs,
-                         c->L, c->d_mods, c->d_psi, c->d_psi_sh, md);
-      LAUNCH_CHECK();
-    }
-    start = stop;
-  }
+  dim3 block(TPB), grid(16, 2 * n, limbs);
+  hipLaunchKernelGGL(k_ntt16m_fwd_high, grid, block, 0, c->stream, conv, conv, 0, limbs, c->L,
+                     c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
+  LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, grid, block, 0, c->stream, conv, 0, limbs, c->L,
+                     c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp, md);
+  LAUNCH_CHECK();
 }
 
 // ===========================================================================
@@ -1833,11 +1841,12 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // Each thread walks the babies of kTabCts ciphertexts at a time with the
 // groups' plaintext words in registers: a baby word is read once per pass, a
 // plaintext word (from L2) once per kTabCts ciphertexts.
-// FP (limbs whose prime is below 2^45): each product is the exact fp64
-// residue of fp_mulmod (|r| < 1.5 q) and the B-term sums stay exact integers
-// below 2^53, reduced once at the end, so the words equal the 64-bit path's.
+// Limbs whose prime is below 2^45 (with B <= 64) take the fp64 path: each
+// product is the exact fp64 residue of fp_mulmod (|r| < 1.5 q) and the
+// B-term sums stay exact integers below 2^53, reduced once at the end, so the
+// words equal the 64-bit path's.  Both paths run in one launch, so the slower
+// 64-bit blocks of q_0 overlap the others.
 // grid (N / 256, limb_count, 2), limbs from l_begin
-template <bool FP>
 __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict__ bab, int n,
                                                    const u64 *const *__restrict__ pts, int B,
                                                    int G, u64 *__restrict__ out, int limbs,
@@ -1848,7 +1857,7 @@ __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict_
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
-  if constexpr (FP) {
+  if (M.q < ((u64)1 << 45) && B <= 64) {
     constexpr int IC = kTabCtsFp;
     const double q = (double)M.q, qinv = 1.0 / q;
     for (int i0 = 0; i0 < n; i0 += IC) {
@@ -1922,22 +1931,10 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
                       int G, u64 *out, int limbs) {
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
-  // fp64 sums stay exact for up to 2^52 / (1.5 q) terms: B <= 64 at q < 2^45
-  int start = 0;
-  while (start < limbs) {
-    const bool fp = c->prime_fp[start] != 0 && B <= 64;
-    int stop = start + 1;
-    while (stop < limbs && (c->prime_fp[stop] != 0 && B <= 64) == fp) stop++;
-    dim3 grid(c->N / TPB, stop - start, 2);
-    if (fp)
-      hipLaunchKernelGGL(k_mac_table<true>, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out,
-                         limbs, start, c->logN, c->d_mods);
-    else
-      hipLaunchKernelGGL(k_mac_table<false>, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G,
-                         out, limbs, start, c->logN, c->d_mods);
-    LAUNCH_CHECK();
-    start = stop;
-  }
+  dim3 grid(c->N / TPB, limbs, 2);
+  hipLaunchKernelGGL(k_mac_table, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs, 0,
+                     c->logN, c->d_mods);
+  LAUNCH_CHECK();
 }
 
 // Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0
