@@ -577,6 +577,32 @@ static void build_context(ckks_context *c, const ckks_params &p) {
       nv[2 * pi] = (double)ninv[2 * pi];
       nv[2 * pi + 1] = (double)ninv[2 * pi] / q;
     }
+    if (N == 65536) {
+      // The low NTT passes read the twiddles of bit positions 2..0 of a row
+      // as runs of M = 2, 4, 8 per thread: store each run's m-th entries of
+      // the 16 threads of a row side by side, so that one load of the 64
+      // lanes touches contiguous memory ([row][m][c0] instead of
+      // [row][c0][m]; entries below 8192 keep their places).
+      std::vector<double> tmp(2 * (size_t)N);
+      for (int pi = 0; pi < K; pi++) {
+        if (!c->prime_fp[pi]) continue;
+        for (std::vector<double> *t : {&tw, &itw}) {
+          double *row0 = t->data() + 2 * (size_t)pi * N;
+          std::copy(row0, row0 + 2 * (size_t)N, tmp.begin());
+          for (int b = 0; b < 3; b++) {
+            const int M = 8 >> b, base = 65536 >> (b + 1);
+            for (int r = 0; r < 256; r++)
+              for (int c0 = 0; c0 < 16; c0++)
+                for (int m = 0; m < M; m++) {
+                  const size_t to = (size_t)base + (size_t)r * 16 * M + (size_t)m * 16 + c0;
+                  const size_t from = (size_t)base + (size_t)r * 16 * M + (size_t)c0 * M + m;
+                  row0[2 * to] = tmp[2 * from];
+                  row0[2 * to + 1] = tmp[2 * from + 1];
+                }
+          }
+        }
+      }
+    }
     auto upd = [&](double **dst, const std::vector<double> &v) {
       HIPCHECK(hipMalloc(dst, sizeof(double) * v.size()));
       HIPCHECK(hipMemcpy(*dst, v.data(), sizeof(double) * v.size(), hipMemcpyHostToDevice));

@@ -664,7 +664,9 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       if (j & half) continue;
-      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1))];
+      // entry (row 256 + 16 c0 + j) >> (b + 1) of the stage, in the table's
+      // [row][m][c0] order for these stages
+      const double2 w = T[(65536 >> (b + 1)) + row * (128 >> b) + ((j >> (b + 1)) << 4) + c0];
       ct_fp(x[j], x[j + half], w.x, w.y, q);
     }
   }
@@ -710,7 +712,8 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
 #pragma unroll
     for (int j = 0; j < 16; j++) {
       if (j & half) continue;
-      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1))];
+      // entry (row 256 + 16 c0 + j) >> (b + 1), table in [row][m][c0] order
+      const double2 w = T[(65536 >> (b + 1)) + row * (128 >> b) + ((j >> (b + 1)) << 4) + c0];
       gs_fp(x[j], x[j + half], w.x, w.y, q);
     }
   }
