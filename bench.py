@@ -260,8 +260,9 @@ def main() -> int:
         "gpu_event_ms_per_step": round(gpu_ms / args.steps, 3),
         "keygen_s": round(keygen_s, 2),
         "roofline": {
-            "kernel": "batch NTT (k_ntt16f_* fp64 passes for 40-bit limbs, k_ntt16_* for the "
-                      "60-bit limb); mean of forward and inverse transform",
+            "kernel": "batch NTT (k_ntt16m_* passes, one launch per pass over all limbs: fp64 "
+                      "bodies for the 40-bit limbs, the 64-bit body for the 60-bit limb); mean "
+                      "of forward and inverse transform",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
