@@ -268,15 +268,20 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
       h[2 * ns + (size_t)i * nd + t] = (u64)(((u128)pt << 64) % qt);  // Montgomery form
     }
   }
-  BCTable t{ns, nd, nullptr, sizeof(u64) * h.size(), nullptr, 0};
+  BCTable t{ns, nd, nullptr, sizeof(u64) * h.size(), nullptr, 0, 0};
   HIPCHECK(hipMalloc(&t.d, t.bytes));
   HIPCHECK(hipMemcpy(t.d, h.data(), t.bytes, hipMemcpyHostToDevice));
-  // the fp64 kernel needs every source prime below 2^45
-  bool fp = true;
-  for (u64 q : src) fp = fp && q < (1ull << 45);
-  if (fp) {
+  // the fp64 kernel needs every source prime below 2^45, or every one but
+  // the first when no target is wide (the first source's value then enters
+  // as two 32-bit halves)
+  bool narrow_rest = true, narrow_dst = true;
+  for (int i = 1; i < ns; i++) narrow_rest = narrow_rest && src[i] < (1ull << 45);
+  for (u64 q : dst) narrow_dst = narrow_dst && q < (1ull << 45);
+  const bool narrow0 = src[0] < (1ull << 45);
+  t.wide0 = (!narrow0 && narrow_rest && narrow_dst) ? 1 : 0;
+  if ((narrow0 && narrow_rest) || t.wide0) {
     // (w, w / q) pairs for the fp64 modular product; hmod in plain form
-    std::vector<double> f(2 * ((size_t)ns + (size_t)ns * nd));
+    std::vector<double> f(2 * ((size_t)ns + (size_t)ns * nd + (t.wide0 ? nd : 0)));
     for (int i = 0; i < ns; i++) {
       f[2 * i] = (double)h[i];
       f[2 * i + 1] = (double)h[i] / (double)src[i];
@@ -290,6 +295,12 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
         const size_t o = 2 * ((size_t)ns + (size_t)i * nd + t2);
         f[o] = (double)pt;
         f[o + 1] = (double)pt / (double)qt;
+        if (i == 0 && t.wide0) {
+          const u64 p32 = (u64)(((u128)pt << 32) % qt);
+          const size_t o2 = 2 * ((size_t)ns + (size_t)ns * nd + t2);
+          f[o2] = (double)p32;
+          f[o2 + 1] = (double)p32 / (double)qt;
+        }
       }
     }
     t.fbytes = sizeof(double) * f.size();

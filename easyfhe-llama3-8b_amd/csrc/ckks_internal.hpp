@@ -167,10 +167,13 @@ struct BCTable {  // fast basis conversion constants, device resident
   int ns, nd;
   u64 *d;  // [ns] hinv, [ns] hinv_shoup, [ns*nd] hmod (Montgomery form), [nd] Q mod t
   size_t bytes;
-  // every source prime below 2^45: fp64 table [ns] (hinv, hinv / q_i),
-  // [ns*nd] (hmod, hmod / t) with hmod in [0, t); null otherwise
+  // every source prime below 2^45, or all but the first: fp64 table [ns]
+  // (hinv, hinv / q_i), [ns*nd] (hmod, hmod / t) with hmod in [0, t), and,
+  // when the first source is wide (wide0), [nd] (2^32 hmod_0 mod t, / t);
+  // null otherwise
   double *fd;
   size_t fbytes;
+  int wide0;
 };
 
 struct FFTTable {  // encoder tables for one slot count n

@@ -1135,7 +1135,7 @@ template <int MS>
 __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
     const double2 *__restrict__ ftab, int src_prime0, int t_split, int t_skip, int q_limbs,
-    int L, int centered, const ModQ *__restrict__ mods) {
+    int L, int centered, int wide0, const ModQ *__restrict__ mods) {
   // the constants are read at wave-uniform addresses straight from global
   // memory (scalar loads into SGPRs) rather than staged in LDS, which cost one
   // broadcast LDS read per product (7 % slower)
@@ -1148,9 +1148,22 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
   // live across the target loop, to keep the register count and so the
   // occupancy of this latency-bound kernel up)
   double vd[MS];
+  // wide first source (q_0 >= 2^45, every target narrow): its value, found
+  // with the 64-bit Shoup product, enters as v_0 = va 2^32 + vd[0] with
+  // vd[0] in [0, 2^32) and |va| < 2^28, both exact doubles; the products
+  // with 2^32 hmod and hmod then stay within fp_mulmod's range
+  double va = 0.0;
+  if (wide0) {
+    const u64 q0 = mods[src_prime0].q;
+    const u64 v0 = shoup_mul(in[k], st[0], st[ns], q0);
+    const long long sv = (centered && v0 > (q0 - 1) / 2) ? (long long)v0 - (long long)q0
+                                                          : (long long)v0;
+    va = (double)(sv >> 32);
+    vd[0] = (double)(sv & 0xffffffffLL);
+  }
 #pragma unroll
   for (int i = 0; i < MS; i++) {
-    if (i < ns) {
+    if (i < ns && !(wide0 && i == 0)) {
       const double q = (double)mods[src_prime0 + i].q;
       double v = fp_mulmod((double)in[((size_t)i << logN) + k], sf[i].x, sf[i].y, q);
       v = v < 0.0 ? __dadd_rn(v, q) : v;
@@ -1160,6 +1173,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     }
   }
   const double2 *hf = sf + ns;
+  const double2 *hw = hf + (size_t)ns * nd;  // wide0: (2^32 hmod_0 mod t, / t)
   const u64 *hm = st + 2 * ns;
   const u64 *qm = hm + (size_t)ns * nd;
   // wide target (q_0): 128-bit Montgomery accumulation of the canonical v,
@@ -1185,6 +1199,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     const int tl = t < t_split ? t : t + t_skip;
     const double q = (double)mods[prime_of(tl, q_limbs, L)].q;
     double a0 = 0.0, a1 = 0.0;
+    if (wide0) a1 = fp_mulmod(va, hw[t].x, hw[t].y, q);
 #pragma unroll
     for (int i = 0; i < MS; i += 2) {
       if (i < ns) {
@@ -1211,6 +1226,10 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     // two fp64 targets: four independent accumulation chains
     const double q0 = (double)q0u, q1 = (double)q1u;
     double a0 = 0.0, a1 = 0.0, b0 = 0.0, b1 = 0.0;
+    if (wide0) {
+      a1 = fp_mulmod(va, hw[t].x, hw[t].y, q0);
+      b1 = fp_mulmod(va, hw[t + 1].x, hw[t + 1].y, q1);
+    }
 #pragma unroll
     for (int i = 0; i < MS; i += 2) {
       if (i < ns) {
@@ -1244,7 +1263,7 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
     hipLaunchKernelGGL(s12 ? k_basis_convert_fp<12> : k_basis_convert_fp<kMaxDigitSize>, grid,
                        dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d,
                        (const double2 *)t.fd, src_prime0, t_split, t_skip, q_limbs, c->L,
-                       centered ? 1 : 0, c->d_mods);
+                       centered ? 1 : 0, t.wide0, c->d_mods);
   } else {
     hipLaunchKernelGGL(s12 ? k_basis_convert<12> : k_basis_convert<kMaxDigitSize>, grid,
                        dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, src_prime0,
