@@ -739,7 +739,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     norm = rsqrt_entry(0.5, 16.0, 63)
     ap = LayerApproximations(norm, norm, silu_entry(-12.0, 12.0, 63),
-                             SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=9,
+                             SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=7,
                                            first_inverse_degree=31, inverse_degree=47))
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
     spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=0,

@@ -106,7 +106,7 @@ class RangeMargins:
     rmsnorm_degree: int = 63
     silu_degree: int = 63
     softmax_rounds: int = 3
-    exp_degree: int = 9
+    exp_degree: int = 7
     first_inverse_degree: int = 31
     inverse_degree: int = 47
 
