@@ -187,6 +187,7 @@ class NativeContext:
 
     def close(self) -> None:
         if getattr(self, "_h", None):
+            clear_plaintext_cache(self)
             lib.ckks_context_destroy(self._h)
             self._h = None
 
@@ -224,11 +225,12 @@ class Ciphertext:
     the reference's usage (operators/primitives.py:115-150,
     backend.py:336-351)."""
 
-    __slots__ = ("context", "_h", "__weakref__")
+    __slots__ = ("context", "_h", "_pinned", "__weakref__")
 
     def __init__(self, context: NativeContext, handle: int):
         self.context = context
         self._h = handle
+        self._pinned = False  # held by the context's plaintext cache
 
     @property
     def handle(self) -> int:
@@ -285,12 +287,13 @@ class Ciphertext:
         return out
 
     def release(self) -> None:
-        if self._h:
+        if self._h and not self._pinned:
             lib.ckks_ct_free(self._h)
             self._h = None
 
     def __del__(self):
         try:
+            self._pinned = False
             self.release()
         except Exception:
             pass
@@ -399,6 +402,65 @@ def encode_rows(context: NativeContext, rows, *, limbs: int, scale: float, slots
                                im.ctypes.data_as(_native.DP), n, int(slots), int(limbs),
                                float(scale), int(is_ext), handles))
     return [Ciphertext(context, handles[i]) for i in range(n)]
+
+
+# Plaintexts of constant rows (masks, rotation tables, row selectors) that an
+# operator encodes on every call: kept per context, keyed by the rows'
+# content (xxh3-128 of their bytes), shape, limbs, scale and basis, least
+# recently used dropped beyond a byte cap.  The cached objects are pinned:
+# release() leaves them alone until the cache drops them.
+PLAINTEXT_CACHE_BYTES = 8 << 30
+
+
+def _rows_digest(z: np.ndarray) -> str:
+    try:
+        import xxhash
+
+        return xxhash.xxh3_128_hexdigest(z.tobytes())
+    except ImportError:  # pragma: no cover - xxhash ships with the image
+        import hashlib
+
+        return hashlib.blake2b(z.tobytes(), digest_size=16).hexdigest()
+
+
+def encode_rows_cached(context: NativeContext, rows, *, limbs: int, scale: float, slots: int,
+                       is_ext: bool = False) -> list[Ciphertext]:
+    """encode_rows through the context's plaintext cache; the returned
+    plaintexts may be released by the caller (a no-op while cached) and must
+    not be modified."""
+    z = np.ascontiguousarray(np.asarray(rows))
+    if z.ndim == 1:
+        z = z[None, :]
+    key = (_rows_digest(z), z.shape, str(z.dtype), int(limbs), float(scale), int(slots),
+           bool(is_ext))
+    cache = context.__dict__.setdefault("_pt_cache", {})
+    hit = cache.pop(key, None)
+    if hit is None:
+        pts = encode_rows(context, z, limbs=limbs, scale=scale, slots=slots, is_ext=is_ext)
+        width = int(limbs) + (context.alpha if is_ext else 0)
+        hit = (pts, 8 * context.N * width * len(pts))
+        for p in pts:
+            p._pinned = True
+        used = context.__dict__.get("_pt_cache_bytes", 0) + hit[1]
+        while cache and used > PLAINTEXT_CACHE_BYTES:
+            old_key = next(iter(cache))
+            old, nbytes = cache.pop(old_key)
+            for p in old:
+                p._pinned = False
+                p.release()
+            used -= nbytes
+        context.__dict__["_pt_cache_bytes"] = used
+    cache[key] = hit  # most recently used last
+    return list(hit[0])
+
+
+def clear_plaintext_cache(context: NativeContext) -> None:
+    cache = context.__dict__.pop("_pt_cache", {})
+    context.__dict__["_pt_cache_bytes"] = 0
+    for pts, _ in cache.values():
+        for p in pts:
+            p._pinned = False
+            p.release()
 
 
 def decode(pt: Ciphertext) -> np.ndarray:

@@ -224,15 +224,15 @@ def attention_rotations(geo: AttentionGeometry) -> tuple[int, ...]:
 
 def _encode(ctx, rows, limbs: int, scale: float | None = None) -> list:
     rows = np.atleast_2d(np.asarray(rows, dtype=np.float64))
-    return fhe.encode_rows(ctx, rows, limbs=int(limbs),
-                           scale=float(scale) if scale else ctx.scale_at(int(limbs)),
-                           slots=ctx.max_slots)
+    return fhe.encode_rows_cached(ctx, rows, limbs=int(limbs),
+                                  scale=float(scale) if scale else ctx.scale_at(int(limbs)),
+                                  slots=ctx.max_slots)
 
 
 def _encode_ext(ctx, rows, limbs: int) -> list:
     rows = np.atleast_2d(np.asarray(rows, dtype=np.float64))
-    return fhe.encode_rows(ctx, rows, limbs=int(limbs), scale=ctx.scale_at(int(limbs)),
-                           slots=ctx.max_slots, is_ext=True)
+    return fhe.encode_rows_cached(ctx, rows, limbs=int(limbs), scale=ctx.scale_at(int(limbs)),
+                                  slots=ctx.max_slots, is_ext=True)
 
 
 def _mul_pt_rescale(cts, pts, ctx) -> list:

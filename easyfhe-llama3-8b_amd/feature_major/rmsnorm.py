@@ -118,7 +118,7 @@ def _mul_rows_rescale(cts, rows: np.ndarray, ctx, out_scale: float | None = None
     if out_scale is not None:
         scale = float(out_scale) * float(int(ctx.primes()[limbs - 1])) / float(
             cts[0].state.scaling_factor)
-    pts = fhe.encode_rows(ctx, rows, limbs=limbs, scale=scale, slots=ctx.max_slots)
+    pts = fhe.encode_rows_cached(ctx, rows, limbs=limbs, scale=scale, slots=ctx.max_slots)
     try:
         prods = [fhe.homo_mul_pt(c, p, ctx) for c, p in zip(cts, pts)]
     finally:

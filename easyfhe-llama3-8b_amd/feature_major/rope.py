@@ -77,8 +77,8 @@ def rope_fhe(stream, layout: FeatureMajorPrefillLayout, *, head_dim: int, crypto
     try:
         for c, (x, a, b) in enumerate(zip(xs, ra, rb)):
             rows = rope_plaintext_rows(layout, head_dim, c, theta, start_pos)
-            pts = fhe.encode_rows(ctx, rows, limbs=limbs, scale=ctx.scale_at(limbs),
-                                  slots=ctx.max_slots)
+            pts = fhe.encode_rows_cached(ctx, rows, limbs=limbs, scale=ctx.scale_at(limbs),
+                                         slots=ctx.max_slots)
             t = [fhe.homo_mul_pt(x, pts[0], ctx), fhe.homo_mul_pt(a, pts[1], ctx),
                  fhe.homo_mul_pt(b, pts[2], ctx)]
             _release(pts)
