@@ -111,8 +111,9 @@ def main() -> int:
     ap.add_argument("--budget", type=int, nargs=2, default=(3, 3))
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the key-switch "
-              "path shards by ciphertext, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (across GPUs "
+              "the key-switch batches and the feature-major ciphertexts would be split by "
+              "ciphertext, each GPU holding its own copy of the keys)", file=sys.stderr)
         return 2
     if args.mode == "prefill":
         # The plaintext passes run on torch; its bundled HIP runtime must be
