@@ -661,11 +661,14 @@ namespace ckks {
 void upload_async(ckks_context *c, void *dst, const void *src, size_t bytes) {
   if (bytes == 0) return;
   ckks_context::StageBuf *pick = nullptr;
-  for (auto &b : c->stage)
-    if (b.bytes >= bytes && hipEventQuery(b.ev) == hipSuccess) {
+  for (auto &b : c->stage) {
+    if (b.bytes < bytes) continue;
+    if (hipEventQuery(b.ev) == hipSuccess) {
       pick = &b;
       break;
     }
+    (void)hipGetLastError();  // a copy still pending is not an error for later checks
+  }
   if (!pick) {
     const size_t want = (bytes + kStageUnit - 1) / kStageUnit * kStageUnit;
     size_t total = 0;
