@@ -1483,6 +1483,40 @@ int ckks_sub(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out)
   return binary_limbwise(c, a, b, out, 1);
 }
 
+int ckks_add_many(ckks_context *c, const ckks_ct *const *a, const ckks_ct *const *b, int n,
+                  int op, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && b && out && n >= 1, "null argument");
+  require(op == 0 || op == 1, "op must be 0 (add) or 1 (sub)");
+  // every pair is checked before any output exists
+  for (int i = 0; i < n; i++) {
+    check_ct(c, a[i], "add_many");
+    check_ct(c, b[i], "add_many");
+    require(a[i]->limbs == b[i]->limbs && a[i]->limbs == a[0]->limbs,
+            "add_many operands must share one limb count");
+    require(a[i]->is_ext == b[i]->is_ext && a[i]->is_ext == a[0]->is_ext,
+            "add_many operands must share the basis");
+    require(a[i]->polys == b[i]->polys && a[i]->polys == a[0]->polys,
+            "add_many operands must share the degree");
+    check_scales(a[i], b[i]);
+  }
+  const int limbs = a[0]->limbs, polys = a[0]->polys;
+  const int total = limbs + (a[0]->is_ext ? c->alpha : 0);
+  for (int i = 0; i < n; i++)
+    out[i] = new_ct(c, polys, limbs, a[i]->is_ext, a[i]->slots, a[i]->scale, a[i]->scale_degree);
+  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - i0);
+    Batch ba{}, bb{}, bo{};
+    for (int i = 0; i < nb; i++) {
+      ba.p[i] = a[i0 + i]->d;
+      bb.p[i] = b[i0 + i]->d;
+      bo.p[i] = out[i0 + i]->d;
+    }
+    launch_addsub_many(c, ba, bb, bo, nb, polys, total, limbs, op);
+  }
+  API_END
+}
+
 int ckks_add_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out) {
   API_BEGIN
   check_ct(c, a, "add_pt");

@@ -252,6 +252,8 @@ namespace ckks {
 void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                 int l_begin, int l_count, int q_limbs, bool inverse);
 // out = a op b over `limbs` limbs of `polys` polynomials (op: 0 add, 1 sub)
+void launch_addsub_many(ckks_context *c, const Batch &a, const Batch &b, const Batch &out, int n,
+                        int polys, int limbs, int q_limbs, int op);
 void launch_addsub(ckks_context *c, const u64 *a, const u64 *b, u64 *out, int polys,
                    int limbs, int q_limbs, int op);
 void launch_mul_pt(ckks_context *c, const u64 *ct, const u64 *pt, u64 *out, int polys,

@@ -950,6 +950,27 @@ __global__ void k_addsub(const u64 *__restrict__ a, const u64 *__restrict__ b,
   out[off] = op == 0 ? add_mod(a[off], b[off], q) : sub_mod(a[off], b[off], q);
 }
 
+// n pairs at once: grid (N / 256, limbs, polys n), z = item polys + poly
+__global__ void k_addsub_many(Batch a, Batch b, Batch out, int logN, int polys, int limbs,
+                              int q_limbs, int L, const ModQ *__restrict__ mods, int op) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y;
+  const int item = blockIdx.z / polys, poly = blockIdx.z - item * polys;
+  const size_t off = (((size_t)poly * limbs + l) << logN) + k;
+  const u64 q = mods[prime_of(l, q_limbs, L)].q;
+  const u64 x = batch_ptr(a, item)[off], y = batch_ptr(b, item)[off];
+  batch_ptr(out, item)[off] = op == 0 ? add_mod(x, y, q) : sub_mod(x, y, q);
+}
+
+void launch_addsub_many(ckks_context *c, const Batch &a, const Batch &b, const Batch &out, int n,
+                        int polys, int limbs, int q_limbs, int op) {
+  if (n < 1 || n > kMaxBatch) throw std::invalid_argument("addsub_many: 1..64 pairs per launch");
+  dim3 grid(c->N / TPB, limbs, polys * n);
+  hipLaunchKernelGGL(k_addsub_many, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, polys,
+                     limbs, q_limbs, c->L, c->d_mods, op);
+  LAUNCH_CHECK();
+}
+
 void launch_addsub(ckks_context *c, const u64 *a, const u64 *b, u64 *out, int polys,
                    int limbs, int q_limbs, int op) {
   dim3 grid(c->N / TPB, limbs, polys);

@@ -101,6 +101,7 @@ SIGNATURES = {
     "ckks_ct_free": (None, [VP]),
     "ckks_add": (I, [VP, VP, VP, VPP]),
     "ckks_sub": (I, [VP, VP, VP, VPP]),
+    "ckks_add_many": (I, [VP, VPP, VPP, I, I, VPP]),
     "ckks_add_pt": (I, [VP, VP, VP, VPP]),
     "ckks_mul_pt": (I, [VP, VP, VP, VPP]),
     "ckks_mul_i": (I, [VP, VP, I, VPP]),

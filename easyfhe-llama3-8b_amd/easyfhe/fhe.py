@@ -616,6 +616,29 @@ def homo_sub(a, b, context=None):
     return _binary(lib.ckks_sub, a, b, context)
 
 
+def _binary_many(op: int, a: Sequence[Ciphertext], b: Sequence[Ciphertext], context) -> list:
+    a, b = list(a), list(b)
+    if len(a) != len(b):
+        raise ValueError("operand lists differ in length")
+    if not a:
+        return []
+    ctx = _ctx(a[0], context)
+    outs = (ctypes.c_void_p * len(a))()
+    check(lib.ckks_add_many(ctx.handle, ptr_array([x.handle for x in a]),
+                            ptr_array([y.handle for y in b]), len(a), int(op), outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(a))]
+
+
+def homo_add_many(a: Sequence[Ciphertext], b: Sequence[Ciphertext], context=None) -> list:
+    """[homo_add(x, y) for x, y in zip(a, b)] for pairs of one shape in
+    batched launches."""
+    return _binary_many(0, a, b, context)
+
+
+def homo_sub_many(a: Sequence[Ciphertext], b: Sequence[Ciphertext], context=None) -> list:
+    return _binary_many(1, a, b, context)
+
+
 def homo_add_pt(a, pt, context=None):
     return _binary(lib.ckks_add_pt, a, pt, context)
 

@@ -253,7 +253,7 @@ def _rotate_add_tree(cts, strides, ctx) -> list:
         rot = []
         for i in range(0, len(cur), 64):
             rot.extend(fhe.homo_rotate_many(cur[i: i + 64], int(s), ctx))
-        nxt = [fhe.homo_add(a, b, ctx) for a, b in zip(cur, rot)]
+        nxt = fhe.homo_add_many(cur, rot, ctx)
         _release(rot)
         if owned:
             _release(cur)
@@ -300,7 +300,7 @@ def lane_shifts(stream, geo: AttentionGeometry, *, crypto_context) -> list:
         a = _mul_pt_rescale(keep, pk, ctx)
         b = _mul_pt_rescale(carry, pc, ctx)
         _release(keep + carry + pk + pc)
-        out.append([fhe.homo_add(x, y, ctx) for x, y in zip(a, b)])
+        out.append(fhe.homo_add_many(a, b, ctx))
         _release(a + b)
     return out
 
@@ -369,7 +369,7 @@ def qk_scores(query, key, geo: AttentionGeometry, *, crypto_context,
                 if acc is None:
                     acc = m
                 else:
-                    nxt = [fhe.homo_add(x, y, ctx) for x, y in zip(acc, m)]
+                    nxt = fhe.homo_add_many(acc, m, ctx)
                     _release(acc + m)
                     acc = nxt
             _release(prods)

@@ -364,7 +364,7 @@ class LinearOperator:
                 if not acc:
                     acc = outs
                 else:
-                    summed = [fhe.homo_add(a, o, ctx) for a, o in zip(acc, outs)]
+                    summed = fhe.homo_add_many(acc, outs, ctx)
                     _release(acc)
                     _release(outs)
                     acc = summed

@@ -242,7 +242,7 @@ def mlp_fhe(input_ciphers, weights: MLPWeights, *, silu: dict, crypto_context,
             if not acc:
                 acc = list(y)
             else:
-                summed = [fhe.homo_add(a, b, ctx) for a, b in zip(acc, y)]
+                summed = fhe.homo_add_many(acc, y, ctx)
                 _release(acc)
                 _release(y)
                 acc = summed

@@ -91,7 +91,7 @@ def _fold(cts, stride: int, steps: int, sign: int, ctx) -> list:
     owned = False
     for b in range(steps):
         rot = fhe.homo_rotate_many(cur, sign * stride * (1 << b), ctx)
-        nxt = [fhe.homo_add(c, r, ctx) for c, r in zip(cur, rot)]
+        nxt = fhe.homo_add_many(cur, rot, ctx)
         _release(rot)
         if owned:
             _release(cur)

@@ -135,6 +135,11 @@ void ckks_ct_free(ckks_ct *ct);
  * operators/nonlinear/polynomial.py:73,82). */
 int ckks_add(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
 int ckks_sub(ckks_context *ctx, const ckks_ct *a, const ckks_ct *b, ckks_ct **out);
+/* out[i] = a[i] + b[i] (op 0) or a[i] - b[i] (op 1) for n pairs of one shape in
+ * batched launches (the reference's list comprehensions over homo_add /
+ * homo_sub, e.g. operators/linear/operator.py's per-chunk accumulation). */
+int ckks_add_many(ckks_context *ctx, const ckks_ct *const *a, const ckks_ct *const *b, int n,
+                  int op, ckks_ct **out);
 int ckks_add_pt(ckks_context *ctx, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out);
 int ckks_mul_pt(ckks_context *ctx, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out);
 int ckks_mul_i(ckks_context *ctx, const ckks_ct *a, int negative, ckks_ct **out);
