@@ -67,3 +67,17 @@ def test_approximations_cover_the_ranges():
     assert bound == 80.0
     with pytest.raises(ValueError):
         approximations_for(LayerRanges((1, 2), (1, 2), 1.0, 1.0, 19.0, -1.0))
+
+
+def test_refreshed_blocks_partition_the_layer_depth():
+    """The three blocks between refreshes use, together, exactly the levels
+    of the refresh-free layer, for the prefill's default series."""
+    from feature_major.layer import decoder_layer_depth, refreshed_layer_depths
+
+    for r in (LayerRanges((0.9, 1.2), (3.0, 5.0), 40.0, 6.5, 9.03, -8.0),
+              LayerRanges((1e-4, 5e-4), (1.0, 4.0), 8.0, 6.0, 4.0, -4.0)):
+        ap, _ = approximations_for(r)
+        a, b, c = refreshed_layer_depths(ap, 128)
+        assert a + b + c == decoder_layer_depth(ap, 128)
+        # the score block is the deepest: its bootstrap returns the most limbs
+        assert b > max(a, c)
