@@ -783,6 +783,14 @@ static void check_ct(const ckks_context *c, const ckks_ct *ct, const char *what)
   require(ct->ctx == c, std::string(what) + ": ciphertext belongs to another context");
 }
 
+// A ciphertext or plaintext polynomial set (polys >= 1); the per-limb
+// constants of encode_scalar (polys 0) hold one word per limb and are only
+// accepted where an entry point says so.
+static void check_poly(const ckks_context *c, const ckks_ct *ct, const char *what) {
+  check_ct(c, ct, what);
+  require(ct->polys >= 1, std::string(what) + ": expects a ciphertext or plaintext, not a scalar");
+}
+
 static int poly_words(const ckks_context *c, const ckks_ct *ct) {
   return (ct->limbs + (ct->is_ext ? c->alpha : 0)) * c->N;
 }
@@ -1410,7 +1418,10 @@ int ckks_ct_upload(ckks_context *c, const uint64_t *data, int polys, int limbs, 
   API_BEGIN
   require(c && data && out, "null argument");
   require(polys >= 1 && polys <= 3, "polys must be 1, 2 or 3");
+  require(is_ext == 0 || is_ext == 1, "is_ext must be 0 or 1");
   check_limbs(c, limbs);
+  check_slots(c, slots);
+  require(scale > 0 && scale_degree >= 1, "scale must be positive and scale_degree at least 1");
   ckks_ct *ct = new_ct(c, polys, limbs, is_ext, slots, scale, scale_degree);
   HIPCHECK(hipMemcpyAsync(ct->d, data, ct->bytes, hipMemcpyHostToDevice, c->stream));
   HIPCHECK(hipStreamSynchronize(c->stream));
@@ -1461,8 +1472,8 @@ void ckks_ct_free(ckks_ct *ct) { free_ct(ct); }
 static int binary_limbwise(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct **out,
                            int op) {
   API_BEGIN
-  check_ct(c, a, "add/sub");
-  check_ct(c, b, "add/sub");
+  check_poly(c, a, "add/sub");
+  check_poly(c, b, "add/sub");
   require(out, "null argument");
   require(a->limbs == b->limbs, "operands must have the same limb count");
   require(a->is_ext == b->is_ext, "operands must share the basis");
@@ -1490,8 +1501,8 @@ int ckks_add_many(ckks_context *c, const ckks_ct *const *a, const ckks_ct *const
   require(op == 0 || op == 1, "op must be 0 (add) or 1 (sub)");
   // every pair is checked before any output exists
   for (int i = 0; i < n; i++) {
-    check_ct(c, a[i], "add_many");
-    check_ct(c, b[i], "add_many");
+    check_poly(c, a[i], "add_many");
+    check_poly(c, b[i], "add_many");
     require(a[i]->limbs == b[i]->limbs && a[i]->limbs == a[0]->limbs,
             "add_many operands must share one limb count");
     require(a[i]->is_ext == b[i]->is_ext && a[i]->is_ext == a[0]->is_ext,
@@ -1519,7 +1530,7 @@ int ckks_add_many(ckks_context *c, const ckks_ct *const *a, const ckks_ct *const
 
 int ckks_add_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "add_pt");
+  check_poly(c, a, "add_pt");
   check_ct(c, pt, "add_pt");
   require(out, "null argument");
   require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
@@ -1537,7 +1548,7 @@ int ckks_add_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **
 
 int ckks_mul_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "mul_pt");
+  check_poly(c, a, "mul_pt");
   check_ct(c, pt, "mul_pt");
   require(out, "null argument");
   require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
@@ -1555,7 +1566,7 @@ int ckks_mul_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **
 
 int ckks_mul_i(ckks_context *c, const ckks_ct *a, int negative, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "mul_i");
+  check_poly(c, a, "mul_i");
   require(out, "null argument");
   ckks_ct *o = new_ct(c, a->polys, a->limbs, a->is_ext, a->slots, a->scale, a->scale_degree);
   const int total = a->limbs + (a->is_ext ? c->alpha : 0);
@@ -1566,7 +1577,7 @@ int ckks_mul_i(ckks_context *c, const ckks_ct *a, int negative, ckks_ct **out) {
 
 int ckks_add_scalar(ckks_context *c, const ckks_ct *a, const ckks_ct *s, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "add_scalar");
+  check_poly(c, a, "add_scalar");
   check_ct(c, s, "add_scalar");
   require(out, "null argument");
   require(s->polys == 0 && s->limbs >= a->limbs, "scalar limbs below ciphertext limbs");
@@ -1579,7 +1590,7 @@ int ckks_add_scalar(ckks_context *c, const ckks_ct *a, const ckks_ct *s, ckks_ct
 
 int ckks_mul_scalar(ckks_context *c, const ckks_ct *a, const ckks_ct *s, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "mul_scalar");
+  check_poly(c, a, "mul_scalar");
   check_ct(c, s, "mul_scalar");
   require(out, "null argument");
   require(s->polys == 0 && s->limbs >= a->limbs, "scalar limbs below ciphertext limbs");
@@ -1637,7 +1648,7 @@ int ckks_mul_relin(ckks_context *c, const ckks_ct *a, const ckks_ct *b, ckks_ct 
 
 int ckks_rescale(ckks_context *c, const ckks_ct *a, ckks_ct **out) {
   API_BEGIN
-  check_ct(c, a, "rescale");
+  check_poly(c, a, "rescale");
   require(out, "null argument");
   require(a->limbs >= 2, "rescale needs at least two limbs");
   require(!a->is_ext, "rescale expects a Q-basis ciphertext");
@@ -1656,8 +1667,14 @@ int ckks_drop_limbs(ckks_context *c, const ckks_ct *a, int target, ckks_ct **out
   require(!a->is_ext, "drop_limbs expects a Q-basis ciphertext");
   require(target >= 1 && target <= a->limbs, "target limbs out of range");
   ckks_ct *o = new_ct(c, a->polys, target, 0, a->slots, a->scale, a->scale_degree);
+  if (a->polys == 0) {
+    // a scalar constant: one word per limb, the leading `target` of them
+    HIPCHECK(hipMemcpyAsync(o->d, a->d, sizeof(u64) * target, hipMemcpyDeviceToDevice, c->stream));
+    *out = o;
+    return CKKS_OK;
+  }
   const size_t N = c->N;
-  for (int p = 0; p < std::max(1, a->polys); p++)
+  for (int p = 0; p < a->polys; p++)
     HIPCHECK(hipMemcpyAsync(o->d + (size_t)p * target * N, a->d + (size_t)p * a->limbs * N,
                             sizeof(u64) * target * N, hipMemcpyDeviceToDevice, c->stream));
   *out = o;
@@ -2460,7 +2477,7 @@ int ckks_ntt_many(ckks_context *c, ckks_ct *const *cts, int n, int inverse) {
     const int limbs = cts[b0]->limbs, polys = cts[b0]->polys;
     Batch b{};
     for (int i = 0; i < nb; i++) {
-      check_ct(c, cts[b0 + i], "ntt_many");
+      check_poly(c, cts[b0 + i], "ntt_many");
       require(cts[b0 + i]->limbs == limbs && cts[b0 + i]->polys == polys && !cts[b0 + i]->is_ext,
               "ntt_many needs one shape");
       b.p[i] = cts[b0 + i]->d;

@@ -316,6 +316,8 @@ def upload(context: NativeContext, data: np.ndarray, *, slots: int, scale: float
            scale_degree: int = 1, is_ext: bool = False) -> Ciphertext:
     """Raw limbs [polys, limbs(+alpha), N] to a device object (tests, batching)."""
     data = np.ascontiguousarray(data, dtype=np.uint64)
+    if data.ndim != 3 or data.shape[2] != context.N:
+        raise ValueError(f"raw limbs must have shape [polys, limbs, {context.N}], got {data.shape}")
     polys, per = int(data.shape[0]), int(data.shape[1])
     limbs = per - (context.alpha if is_ext else 0)
     out = ctypes.c_void_p()

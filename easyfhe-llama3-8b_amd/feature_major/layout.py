@@ -1,102 +1,151 @@
-"""Feature-major slot layouts (reference llama3fhe/layouts/feature_major.py:10-110,
-layouts/linear.py:15-116).
+"""Token-lane slot maps of the feature-major stream (interface of reference
+llama3fhe/layouts/feature_major.py and layouts/linear.py).
 
-A ciphertext carries ``lanes = slots / dimension`` tokens; feature ``d`` of
-local token ``t`` sits at slot ``d * lanes + t``, so a rotation by
-``k * lanes`` moves every token's feature ``d + k`` onto ``d`` at once.
+One ciphertext holds ``lanes = slots // width`` consecutive tokens.  Token ``k``
+of the sequence lives in ciphertext ``k // lanes`` on lane ``k % lanes``, and
+its feature ``d`` occupies slot ``d * lanes + k % lanes``.  Rotating a
+ciphertext by ``j * lanes`` therefore moves feature ``d + j`` of every token
+onto feature ``d`` at once, which is what the diagonal method needs.
+
+``pack`` and ``unpack`` are the scatter and gather of that map, computed from
+index arrays; tokens past ``seq_len`` in the last ciphertext are zero.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-
 import numpy as np
 
 
-def _power_of_two(value: int, name: str) -> int:
-    value = int(value)
-    if value <= 0 or value & (value - 1):
-        raise ValueError(f"{name} must be a positive power of two, got {value}.")
-    return value
+def _require(ok: bool, what: str) -> None:
+    if not ok:
+        raise ValueError(f"feature-major layout: {what}")
 
 
-@dataclass(frozen=True)
-class _TokenLaneLayout:
-    seq_len: int
-    dimension: int
-    slots: int = 32768
+class _TokenLanes:
+    """The slot map for ``seq_len`` tokens of ``width`` features each."""
 
-    def __post_init__(self) -> None:
-        _power_of_two(self.dimension, "dimension")
-        if int(self.seq_len) <= 0:
-            raise ValueError(f"seq_len must be positive, got {self.seq_len}.")
-        if int(self.slots) % int(self.dimension):
-            raise ValueError(f"slots={self.slots} must be divisible by dimension={self.dimension}.")
+    __slots__ = ("_seq", "_width", "_slots", "_lanes")
+
+    def __init__(self, seq_len: int, width: int, slots: int):
+        seq, width, slots = int(seq_len), int(width), int(slots)
+        _require(width >= 1 and (width & (width - 1)) == 0,
+                 f"the feature width {width} is not a power of two")
+        _require(seq >= 1, f"a sequence needs at least one token (seq_len={seq})")
+        _require(slots >= width and slots % width == 0,
+                 f"{slots} slots do not hold a whole number of {width}-feature rows")
+        self._seq, self._width, self._slots = seq, width, slots
+        self._lanes = slots // width
+
+    # -- geometry -------------------------------------------------------------
+    @property
+    def seq_len(self) -> int:
+        return self._seq
+
+    @property
+    def slots(self) -> int:
+        return self._slots
 
     @property
     def token_lanes(self) -> int:
-        return int(self.slots) // int(self.dimension)
+        return self._lanes
 
     @property
     def cipher_count(self) -> int:
-        return -(-int(self.seq_len) // self.token_lanes)
+        return (self._seq + self._lanes - 1) // self._lanes
 
     def active_tokens(self, cipher_index: int) -> int:
-        i = int(cipher_index)
-        if not 0 <= i < self.cipher_count:
-            raise IndexError(f"cipher_index={i} is outside [0, {self.cipher_count}).")
-        return max(0, min(self.token_lanes, int(self.seq_len) - i * self.token_lanes))
+        """Tokens of the sequence carried by ciphertext ``cipher_index``."""
+        c = int(cipher_index)
+        if c < 0 or c >= self.cipher_count:
+            raise IndexError(f"ciphertext {c} does not exist (the layout has "
+                             f"{self.cipher_count})")
+        first = c * self._lanes
+        return min(self._lanes, self._seq - first)
 
     def slot(self, dim: int, token: int) -> int:
-        dim, token = int(dim), int(token)
-        if not 0 <= dim < int(self.dimension):
-            raise IndexError(f"dim={dim} is outside [0, {self.dimension}).")
-        if not 0 <= token < self.token_lanes:
-            raise IndexError(f"token={token} is outside [0, {self.token_lanes}).")
-        return dim * self.token_lanes + token
+        """Slot of feature ``dim`` for lane ``token`` of any ciphertext."""
+        d, t = int(dim), int(token)
+        if d < 0 or d >= self._width:
+            raise IndexError(f"feature {d} is not below the width {self._width}")
+        if t < 0 or t >= self._lanes:
+            raise IndexError(f"lane {t} is not below the lane count {self._lanes}")
+        return d * self._lanes + t
+
+    # -- scatter / gather -----------------------------------------------------
+    def _index(self):
+        """(ciphertext of each token [seq, 1], slot of each (token, feature))."""
+        cipher, lane = np.divmod(np.arange(self._seq), self._lanes)
+        cols = np.arange(self._width)[None, :] * self._lanes + lane[:, None]
+        return cipher[:, None], cols
 
     def pack(self, rows: np.ndarray, *, dtype=np.float64) -> np.ndarray:
-        """[seq_len, dimension] -> [cipher_count, slots] (zero padded tokens)."""
+        """``[seq_len, width]`` token rows -> ``[cipher_count, slots]`` payloads."""
         rows = np.asarray(rows, dtype=dtype)
-        want = (int(self.seq_len), int(self.dimension))
-        if rows.shape != want:
-            raise ValueError(f"rows must have shape {want}, got {rows.shape}.")
-        lanes, n = self.token_lanes, self.cipher_count
-        out = np.zeros((n * lanes, int(self.dimension)), dtype=dtype)
-        out[: int(self.seq_len)] = rows
-        # token t of cipher c, feature d -> cipher c, slot d * lanes + t
-        return out.reshape(n, lanes, int(self.dimension)).swapaxes(1, 2).reshape(n, int(self.slots))
+        _require(rows.shape == (self._seq, self._width),
+                 f"expected token rows of shape {(self._seq, self._width)}, got {rows.shape}")
+        out = np.zeros((self.cipher_count, self._slots), dtype=dtype)
+        cipher, cols = self._index()
+        out[cipher, cols] = rows
+        return out
 
     def unpack(self, packed: np.ndarray, *, output_dim: int | None = None) -> np.ndarray:
+        """``[cipher_count, slots]`` payloads -> the first ``output_dim`` features of
+        every token as float32 (the reference's client-side dtype)."""
         packed = np.asarray(packed)
-        want = (self.cipher_count, int(self.slots))
-        if packed.shape != want:
-            raise ValueError(f"payload must have shape {want}, got {packed.shape}.")
-        d = int(self.dimension if output_dim is None else output_dim)
-        if not 0 < d <= int(self.dimension):
-            raise ValueError(f"output_dim must be in [1, {self.dimension}], got {d}.")
-        rows = packed.reshape(self.cipher_count, int(self.dimension), self.token_lanes)
-        rows = rows.swapaxes(1, 2).reshape(-1, int(self.dimension))
-        return np.asarray(rows[: int(self.seq_len), :d], dtype=np.float32)
+        _require(packed.shape == (self.cipher_count, self._slots),
+                 f"expected payloads of shape {(self.cipher_count, self._slots)}, "
+                 f"got {packed.shape}")
+        keep = self._width if output_dim is None else int(output_dim)
+        _require(1 <= keep <= self._width,
+                 f"cannot keep {keep} features of a {self._width}-feature row")
+        cipher, cols = self._index()
+        return packed[cipher, cols[:, :keep]].astype(np.float32)
+
+    # -- value semantics (layouts are compared and used as cache keys) ----------
+    def _key(self):
+        return (type(self), self._seq, self._width, self._slots)
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, _TokenLanes) and self._key() == other._key()
+
+    def __hash__(self) -> int:
+        return hash(self._key())
+
+    def __repr__(self) -> str:
+        return (f"{type(self).__name__}(seq_len={self._seq}, width={self._width}, "
+                f"slots={self._slots})")
 
 
-class FeatureMajorPrefillLayout(_TokenLaneLayout):
-    """The persistent layout of the model's hidden states: hidden_dim features
-    per token (production S = 128, D = 4096, slots = 32768: 8 tokens per
-    ciphertext, 16 ciphertexts)."""
+class FeatureMajorPrefillLayout(_TokenLanes):
+    """The hidden-state layout between layers: ``hidden_dim`` features per token
+    (at S = 128, D = 4096 and 2^15 slots: 8 tokens in each of 16 ciphertexts)."""
+
+    __slots__ = ()
 
     def __init__(self, seq_len: int = 128, hidden_dim: int = 4096, slots: int = 32768):
-        super().__init__(seq_len=seq_len, dimension=hidden_dim, slots=slots)
+        super().__init__(seq_len, hidden_dim, slots)
 
     @property
     def hidden_dim(self) -> int:
-        return int(self.dimension)
+        return self._width
 
     @property
     def tokens_per_cipher(self) -> int:
-        return self.token_lanes
+        return self._lanes
 
 
-class LinearCarrierLayout(_TokenLaneLayout):
-    """The private carrier of a linear's output: ``dimension`` is the
-    power-of-two physical row width; an operator may use a prefix of it."""
+class LinearCarrierLayout(_TokenLanes):
+    """A linear's output carrier: ``dimension`` is the power-of-two row width
+    of the physical matrix; an operator may use only a prefix of it."""
+
+    __slots__ = ()
+
+    def __init__(self, seq_len: int, dimension: int, slots: int = 32768):
+        super().__init__(seq_len, dimension, slots)
+
+    @property
+    def dimension(self) -> int:
+        return self._width
+
+
+__all__ = ["FeatureMajorPrefillLayout", "LinearCarrierLayout"]

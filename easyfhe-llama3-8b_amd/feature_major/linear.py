@@ -47,6 +47,18 @@ class LinearChunk:
         return f"chunk.{int(self.index)}"
 
 
+def _check_schedule(baby_steps: int, anchor: int, rows: int) -> None:
+    """One check of the BSGS schedule fields shared by the plan and the config."""
+    if int(baby_steps) < 1:
+        raise ValueError(f"a BSGS schedule needs at least one baby step (got {baby_steps})")
+    if not (int(anchor) == -1 or int(anchor) >= 2):
+        raise ValueError(f"the baby anchor is -1 (off) or a block of two or more steps "
+                         f"(got {anchor})")
+    if int(rows) < int(baby_steps):
+        raise ValueError(f"a chunk of {rows} plaintext rows cannot hold the {baby_steps} "
+                         "diagonals of one giant group")
+
+
 @dataclass(frozen=True)
 class LinearPlan:
     """The physical BSGS schedule of one D-wide linear (config.py:158-273)."""
@@ -58,14 +70,13 @@ class LinearPlan:
     max_plaintext_rows: int
 
     def __post_init__(self) -> None:
-        if int(self.dimension) <= 0 or int(self.token_lanes) <= 0 or int(self.baby_steps) <= 0:
-            raise ValueError("dimension, token_lanes and baby_steps must be positive.")
+        if int(self.dimension) < 1 or int(self.token_lanes) < 1:
+            raise ValueError(f"a linear plan needs a positive width and lane count "
+                             f"(got {self.dimension}, {self.token_lanes})")
+        _check_schedule(self.baby_steps, self.baby_anchor_step, self.max_plaintext_rows)
         if int(self.dimension) % int(self.baby_steps):
-            raise ValueError(f"baby_steps={self.baby_steps} must divide dimension={self.dimension}.")
-        if int(self.baby_anchor_step) in (0, 1) or int(self.baby_anchor_step) < -1:
-            raise ValueError("baby_anchor_step must be at least two or -1.")
-        if int(self.max_plaintext_rows) < int(self.baby_steps):
-            raise ValueError("max_plaintext_rows must hold one baby-step group.")
+            raise ValueError(f"{self.baby_steps} baby steps do not split a {self.dimension}-wide "
+                             "matrix into whole giant groups")
 
     @property
     def giant_steps(self) -> int:
@@ -128,18 +139,16 @@ class LinearOperatorConfig:
     timed_stages: bool = True
 
     def __post_init__(self) -> None:
-        if int(self.baby_steps) <= 0:
-            raise ValueError("baby_steps must be positive.")
-        if int(self.baby_anchor_step) in (0, 1) or int(self.baby_anchor_step) < -1:
-            raise ValueError("baby_anchor_step must be at least two or -1.")
-        if int(self.max_plaintext_rows) < int(self.baby_steps):
-            raise ValueError("max_plaintext_rows must hold one baby-step group.")
+        _check_schedule(self.baby_steps, self.baby_anchor_step, self.max_plaintext_rows)
         if str(self.hoist_strategy).lower() not in _HOIST_STRATEGIES:
-            raise ValueError("hoist_strategy must be 'normal', 'ext_normal', or 'ext_double_hoist'.")
+            raise ValueError(f"unknown hoist strategy {self.hoist_strategy!r} "
+                             f"(known: {sorted(_HOIST_STRATEGIES)})")
         if str(self.constant_cache_mode) not in _CACHE_MODES:
-            raise ValueError(f"constant_cache_mode must be one of {sorted(_CACHE_MODES)}.")
+            raise ValueError(f"unknown constant cache mode {self.constant_cache_mode!r} "
+                             f"(known: {sorted(_CACHE_MODES)})")
         if str(self.raw_weight_policy) not in _RAW_WEIGHT_POLICIES:
-            raise ValueError("raw_weight_policy must be 'device' or 'host'.")
+            raise ValueError(f"unknown raw weight policy {self.raw_weight_policy!r} "
+                             f"(known: {sorted(_RAW_WEIGHT_POLICIES)})")
 
     def plan(self, *, dimension: int, token_lanes: int) -> LinearPlan:
         return LinearPlan(int(dimension), int(token_lanes), int(self.baby_steps),
@@ -163,7 +172,7 @@ def linear_rotations(*, dimension: int, token_lanes: int, slots: int | None = No
     keys.update(c.giant_base * plan.giant_offset for c in plan.chunks if c.giant_base)
     if include_conjugation:
         if slots is None:
-            raise ValueError("slots are required when conjugation is requested.")
+            raise ValueError("the conjugation key index 4 * slots - 1 needs the slot count")
         keys.add(4 * int(slots) - 1)
     return tuple(sorted(int(k) for k in keys if int(k)))
 
@@ -232,7 +241,8 @@ class LinearOperator:
         self.context = _ctx(context)
         self.token_lanes = int(token_lanes)
         if self.token_lanes <= 0:
-            raise ValueError("token_lanes must be positive.")
+            raise ValueError(f"a linear operator needs at least one token lane "
+                             f"(got {self.token_lanes})")
         self.config = config or LinearOperatorConfig()
         self._babies: dict = {}
         self._hits = self._misses = 0

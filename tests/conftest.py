@@ -23,6 +23,16 @@ for p in (ROOT / "easyfhe-llama3-8b_amd", ROOT / "oracle", ROOT):
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library)")
     config.addinivalue_line("markers", "slow: full-size (N = 2^16) case")
+    # A session that may run GPU tests loads torch before any test module
+    # loads the backend library: torch bundles its own HIP runtime, and the
+    # library binds to a runtime already in the process (the full-size
+    # prefill test draws its weights with torch on the device).
+    expr = str(config.getoption("markexpr", "") or "")
+    if "not gpu" not in expr:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
 
 
 # Parameter sets shared by the oracle and the device context.

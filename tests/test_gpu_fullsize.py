@@ -1,0 +1,131 @@
+"""The benchmark's workloads at their full sizes, each with a stated tolerance.
+
+* Bootstrap: 32 ciphertexts at one limb on the key-switch chain (N = 2^16,
+  1 x 60-bit + 35 x 40-bit primes, dnum 3, 12 special primes), full 2^15
+  slots uniform[-1, 1] from seed 0, budget (3, 3), groups of 16.  Every
+  ciphertext must come back within 2^-20 of its message (precision of at
+  least 20 bits; bootstrapping has no bit-level oracle).
+* One Llama-3-8B decoder layer (d = 4096, 32 / 8 heads of 128, SwiGLU 14336)
+  over 128 tokens with its refreshes, from a one-limb input, weights
+  N(0, 0.02) in a residual basis rotated by a seeded randomized Hadamard,
+  inputs N(0, 1).  It is compared with the fp64 model of the same layer with
+  the same series and the same Algorithm-2 softmax (oracle/layer_numpy.py),
+  so the difference is the CKKS error alone.
+* The 32-layer prefill from 128 random token ids to the final token's
+  logits (vocabulary 128256), every layer boundary encrypted.
+
+Each case prints its figures so that a run's log records them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import device_context
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+
+@pytest.mark.timeout(300)
+def test_bootstrap_32_ciphertexts_full_size(capsys):
+    import bench
+
+    client, ctx = device_context(bench.PARAMS, relin=True)
+    b = bench.measure_bootstrap(client, ctx, n_cts=32, group=16, budget=(3, 3), warmup=0)
+    with capsys.disabled():
+        print(f"\nbootstrap N=2^16, 32 ciphertexts: precision min {b['precision_bits_min']} "
+              f"mean {b['precision_bits_mean']} bits, {b['ms_per_bootstrap']} ms each, "
+              f"{b['raise_limbs']} -> {b['output_limbs']} limbs", flush=True)
+    ctx.close()
+    assert b["ciphertexts"] == 32
+    assert b["precision_bits_min"] >= 20.0, b
+
+
+# CKKS error of one refreshed full-size layer against its own fp64 model
+# (same series, same Algorithm-2 softmax): the refreshes work at ~23 bits on
+# a stream bounded by 16, and the three softmax rounds square the
+# probabilities' error.  Measured 6.0e-5 on outputs up to 14.6; the bound is
+# 3e-4 absolute.
+LAYER_TOL = 3e-4
+
+
+@pytest.mark.timeout(400)
+def test_refreshed_layer_full_size(capsys):
+    import bench
+    import layer_numpy as LN
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_refreshed_fhe, decoder_layer_rotations,
+                                     refreshed_layer_programs)
+
+    T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
+    norm = rsqrt_entry(0.5, 16.0, 63)
+    ap = LayerApproximations(norm, norm, silu_entry(-12.0, 12.0, 63),
+                             SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=7,
+                                           first_inverse_degree=31, inverse_degree=47))
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
+    client, ctx = device_context(bench.REFRESH_PARAMS,
+                                 rotations=decoder_layer_rotations(lay, H, hd))
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15)
+    rng = np.random.default_rng(0)
+    w = bench._layer_weights(rng, D, KV, hd, I, bench.randomized_hadamard(D, 1))
+    x = rng.normal(0, 1, (T, D))
+    packed = lay.pack(x)
+    xc = [client.encrypt(packed[i], cur_limbs=1, enc_id=600000 + i)
+          for i in range(lay.cipher_count)]
+    with DecoderLayerWeights(w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"],
+                             heads=H, kv_heads=KV, head_dim=hd, intermediate=I, approx=ap,
+                             layout=lay, context=ctx) as dw:
+        res = decoder_layer_refreshed_fhe(xc, dw, crypto_context=ctx, program=prog,
+                                          residual_program=res_prog)
+    got = LN.fm_unpack(np.stack([client.decrypt(o) for o in res.ciphers]), T, D)
+    wall, limbs_out = res.wall_seconds, res.output_limbs
+    res.release()
+    prog.release()
+    res_prog.release()
+    ctx.close()
+    sm = ap.softmax
+    kw = dict(heads=H, kv_heads=KV, head_dim=hd, input_norm=ap.input_norm,
+              post_attention_norm=ap.post_attention_norm, silu=ap.silu)
+    model = LN.decoder_layer_numpy(x, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"],
+                                   w["down"], probs_fn=lambda s: LN.softmax_alg2_numpy(
+                                       s, sm.exp(), sm.first_inverse(), sm.inverse(T),
+                                       rounds=sm.rounds, shift=sm.shift), **kw)
+    exact = LN.decoder_layer_numpy(x, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"],
+                                   w["down"], **kw)
+    err = float(np.abs(got - model).max())
+    with capsys.disabled():
+        print(f"\nrefreshed layer 128x4096: max err {err:.3g} vs the model with the same "
+              f"series and softmax, {np.abs(got - exact).max():.3g} vs exact softmax, |out| "
+              f"{np.abs(model).max():.3g}, {wall:.2f} s, {limbs_out} limbs out", flush=True)
+    assert err < LAYER_TOL, err
+
+
+# The prefill's final-token logits (|logits| up to ~6) against the fp64
+# forward with exact RMSNorm, SiLU and softmax, and against the one with the
+# fitted series: measured 0.023 for both; the bound is 0.1 absolute, and the
+# arg-max token must agree.
+PREFILL_LOGITS_TOL = 0.1
+
+
+@pytest.mark.timeout(600)
+def test_prefill_32_layers_full_size(capsys):
+    pytest.importorskip("torch")
+    import bench
+
+    with capsys.disabled():
+        print("", flush=True)
+        r = bench.measure_fm_prefill(32)
+        print(f"prefill 32 layers: {r['seconds']} s, logits err {r['logits_max_abs_err_vs_fp64_exact']:.3g} "
+              f"(exact) / {r['logits_max_abs_err_vs_fp64_series']:.3g} (series), |logits| "
+              f"{r['logits_abs_max']:.3g}, top-1 {r['top1_match_exact']}, top-5 "
+              f"{r['top5_overlap_exact']}/5", flush=True)
+    assert math.isfinite(r["logits_max_abs_err_vs_fp64_exact"])
+    assert r["top1_match_exact"], r
+    assert r["logits_max_abs_err_vs_fp64_exact"] < PREFILL_LOGITS_TOL, r
+    assert r["logits_max_abs_err_vs_fp64_series"] < PREFILL_LOGITS_TOL, r

@@ -503,3 +503,32 @@ def test_objects_outliving_their_context():
     t.release()
     ct2 = client2.encrypt(np.full(ctx2.max_slots, 0.5), enc_id=2)
     assert np.abs(client2.decrypt(ct2) - 0.5).max() < 1e-6
+
+
+def test_scalar_constants_and_invalid_objects():
+    """A scalar constant (one word per limb) drops limbs without writing past
+    its own words; entry points that need a ciphertext reject it with
+    ValueError instead of reading N words per limb; uploads check the slot
+    count and the array shape."""
+    fhe = _fhe()
+    client, ctx = device_context("small", relin=False)
+    primes = [int(q) for q in ctx.primes()[: ctx.L]]
+    sc = 2.0**40
+    s = fhe.encode_scalar(-1.5, cur_limbs=ctx.L, scaling_factor=sc, context=ctx)
+    want = np.array([(-int(1.5 * sc)) % q for q in primes], dtype=np.uint64)
+    assert np.array_equal(s.download(), want)
+    guard = client.encrypt(np.linspace(-1, 1, ctx.max_slots), enc_id=9)
+    before = guard.download()
+    dropped = fhe.align_to(s, s.state.replace(cur_limbs=2), ctx)
+    assert np.array_equal(dropped.download(), want[:2])
+    ctx.synchronize()
+    assert np.array_equal(guard.download(), before)
+    for op in (lambda: fhe.rescale(s, ctx), lambda: fhe.homo_mul_i(s, ctx),
+               lambda: fhe.homo_add(s, s, ctx), lambda: fhe.homo_mul_scalar(s, s, ctx)):
+        with pytest.raises(ValueError):
+            op()
+    for bad in (0, 3, 2 * ctx.max_slots):
+        with pytest.raises(ValueError):
+            fhe.upload(ctx, before, slots=bad, scale=sc)
+    with pytest.raises(ValueError):
+        fhe.upload(ctx, before[:, :, :-1], slots=ctx.max_slots, scale=sc)
