@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <stdexcept>
 #include <thread>
 
@@ -751,6 +752,32 @@ static void free_context(ckks_context *c) {
 }
 
 // ===========================================================================
+// fixed key-switch scratch of ckks_rotate_many_noalloc
+// ===========================================================================
+
+// 256 MiB per device, held from the library's first context on that device
+// until the process ends; every context on one device shares it.
+static constexpr size_t kNoAllocWords = (size_t)1 << 25;
+static __device__ __align__(256) u64 scratch[kNoAllocWords];
+
+static constexpr int kMaxDevices = 64;
+static u64 *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device (each device holds
+// its own copy of the array at its own address); resolved once per device.
+static u64 *device_scratch(int dev) {
+  require(dev >= 0 && dev < kMaxDevices, "device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = (u64 *)p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// ===========================================================================
 // ciphertext objects
 // ===========================================================================
 
@@ -806,11 +833,29 @@ static void check_scales(const ckks_ct *a, const ckks_ct *b) {
 // key switching pipeline
 // ===========================================================================
 
+// Key-switch intermediates: blocks from the context pool, released when the
+// Scratch goes out of scope, or (arena mode) consecutive ranges of a fixed
+// device buffer that is never allocated or freed here.
 struct Scratch {
   ckks_context *c;
   std::vector<std::pair<void *, size_t>> bufs;
+  u64 *arena = nullptr;
+  size_t arena_words = 0, used = 0;
   explicit Scratch(ckks_context *cc) : c(cc) {}
+  Scratch(ckks_context *cc, u64 *base, size_t words) : c(cc), arena(base), arena_words(words) {}
+  Scratch(const Scratch &) = delete;
+  Scratch &operator=(const Scratch &) = delete;
   u64 *get(size_t words) {
+    if (arena) {
+      // 256-byte aligned ranges, as the pool's blocks
+      const size_t w = (words + 31) & ~(size_t)31;
+      if (used + w > arena_words)
+        throw std::invalid_argument("fixed scratch exhausted: " + std::to_string(used + w) +
+                                    " words needed, " + std::to_string(arena_words) + " held");
+      u64 *p = arena + used;
+      used += w;
+      return p;
+    }
     void *p = c->pool.alloc(sizeof(u64) * words);
     bufs.emplace_back(p, sizeof(u64) * words);
     return (u64 *)p;
@@ -978,13 +1023,26 @@ static void gen_key(ckks_context *c, u64 id, int relin, u64 galois) {
   c->keys[id] = k;
 }
 
-// Rotations of n ciphertexts at one level by the same Galois element.
-static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g, ckks_ct **out) {
+// Words of key-switch scratch that rotate_batch takes for nb ciphertexts at
+// `limbs` limbs (each range rounded up to 256 bytes, as Scratch hands them out).
+static size_t rotate_scratch_words(const ckks_context *c, int limbs, int nb) {
+  const size_t N = c->N;
+  const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
+  auto r = [](size_t w) { return (w + 31) & ~(size_t)31; };
+  return r((size_t)nb * digits * E * N) + r((size_t)nb * limbs * N) + r((size_t)nb * 2 * E * N) +
+         r((size_t)nb * 2 * c->alpha * N) + r((size_t)nb * 2 * limbs * N);
+}
+
+// Rotations of n ciphertexts at one level by the same Galois element.  With
+// `arena` given, every intermediate lives in that fixed buffer of
+// `arena_words` words (n <= 64) and nothing is allocated.
+static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g, ckks_ct **out,
+                         u64 *arena = nullptr, size_t arena_words = 0) {
   const int limbs = in[0]->limbs;
   const size_t N = c->N, P = (size_t)limbs * N;
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
-    Scratch s(c);
+    Scratch s = arena ? Scratch(c, arena, arena_words) : Scratch(c);
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + P;
     const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
@@ -1172,6 +1230,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
   c->stream = nullptr;
   try {
     build_context(c, *params);
+    HIPCHECK(hipGetDevice(&c->device));
+    c->noalloc_scratch = device_scratch(c->device);
   } catch (...) {
     free_context(c);
     throw;
@@ -1234,6 +1294,16 @@ int ckks_keygen_rotations(ckks_context *c, const int64_t *rot, int n) {
   for (int i = 0; i < n; i++) {
     const u64 g = galois_of(c, rot[i]);
     if (g != 1) gen_key(c, g, 0, g);
+  }
+  // the conversion constants of every level, so that a rotation at any
+  // level needs no further device allocation (ckks_rotate_many_noalloc)
+  if (n > 0 && !c->rotation_tables) {
+    for (int limbs = 1; limbs <= c->L; limbs++) {
+      for (int j = 0; j * c->ds < limbs; j++) bc_up(c, limbs, j);
+      bc_down(c, limbs);
+      pinv_table(c, limbs);
+    }
+    c->rotation_tables = true;
   }
   API_END
 }
@@ -1740,6 +1810,51 @@ int ckks_rotate(ckks_context *c, const ckks_ct *a, int64_t rotation, ckks_ct **o
   ckks_ct *o = new_ct(c, 2, a->limbs, 0, a->slots, a->scale, a->scale_degree);
   rotate_batch(c, &a, 1, g, &o);
   *out = o;
+  API_END
+}
+
+int ckks_rotate_many_noalloc(ckks_context *c, const ckks_ct *const *in, int n, int64_t rotation,
+                             ckks_ct *const *out) {
+  API_BEGIN
+  require(c && in && out, "null argument");
+  require(n >= 1 && n <= kMaxBatch, "noalloc rotation takes 1 to 64 ciphertexts");
+  const int limbs = in[0] ? in[0]->limbs : 0;
+  for (int i = 0; i < n; i++) {
+    check_ct(c, in[i], "rotate_noalloc");
+    check_ct(c, out[i], "rotate_noalloc output");
+    require(in[i]->polys == 2 && !in[i]->is_ext && in[i]->limbs == limbs,
+            "noalloc rotation expects degree-1 Q-basis ciphertexts at one level");
+    require(out[i]->polys == 2 && !out[i]->is_ext && out[i]->limbs == limbs,
+            "each output must be a degree-1 Q-basis ciphertext at the input's level");
+    for (int j = 0; j < n; j++)
+      require(out[i]->d != in[j]->d, "an output may not be one of the inputs");
+    for (int j = 0; j < i; j++) require(out[i]->d != out[j]->d, "outputs must be distinct");
+  }
+  const u64 g = galois_of(c, rotation);
+  if (g != 1) {
+    get_key(c, g);
+    require(c->rotation_tables,
+            "the key-switch constants are built with the rotation keys (ckks_keygen_rotations)");
+    const size_t need = rotate_scratch_words(c, limbs, n);
+    require(need <= kNoAllocWords,
+            "noalloc rotation needs " + std::to_string(need * 8 >> 20) +
+                " MiB of scratch, above its fixed 256 MiB: rotate fewer ciphertexts per call");
+    require(c->noalloc_scratch != nullptr, "fixed scratch not resolved for this device");
+  }
+  for (int i = 0; i < n; i++) {
+    out[i]->slots = in[i]->slots;
+    out[i]->scale = in[i]->scale;
+    out[i]->scale_degree = in[i]->scale_degree;
+  }
+  if (g == 1) {
+    for (int i = 0; i < n; i++)
+      HIPCHECK(hipMemcpyAsync(out[i]->d, in[i]->d, in[i]->bytes, hipMemcpyDeviceToDevice,
+                              c->stream));
+  } else {
+    ckks_ct *o[kMaxBatch];
+    for (int i = 0; i < n; i++) o[i] = out[i];
+    rotate_batch(c, in, n, g, o, c->noalloc_scratch, kNoAllocWords);
+  }
   API_END
 }
 

@@ -221,6 +221,9 @@ struct ckks_context {
   std::map<std::pair<int, int>, u64 *> rescale_d;  // (limbs, primes) -> rescale constants
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
+  int device = 0;                  // HIP device current at creation
+  u64 *noalloc_scratch = nullptr;  // that device's fixed scratch (ckks_rotate_many_noalloc)
+  bool rotation_tables = false;    // every level's key-switch constants built
 };
 
 struct ckks_ct {

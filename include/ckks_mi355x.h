@@ -167,6 +167,19 @@ int ckks_rotate(ckks_context *ctx, const ckks_ct *a, int64_t rotation, ckks_ct *
  * hot path under homo_rotate). */
 int ckks_rotate_many(ckks_context *ctx, const ckks_ct *const *in, int n,
                      int64_t rotation, ckks_ct **out);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * ckks_rotate_many into caller-provided outputs: out[i] must be an existing
+ * degree-1 Q-basis ciphertext at the inputs' level, distinct from every
+ * input; its limbs, scale and slot count are overwritten.  Every
+ * intermediate lives in one fixed 256 MiB device buffer per GPU; nothing is
+ * allocated or freed.  CKKS_EINVAL when the call needs more scratch than
+ * that (at N = 2^16 with 36 + 12 limbs and dnum 3 one ciphertext takes
+ * 186 MiB) or when the rotation keys (whose generation also builds every
+ * level's constants) are missing.  Calls that overlap on one GPU (contexts
+ * on other streams or threads) share the buffer and race. */
+int ckks_rotate_many_noalloc(ckks_context *ctx, const ckks_ct *const *in, int n,
+                             int64_t rotation, ckks_ct *const *out);
 /* homo_mul_relin + rescale for n pairs (config: HMult+relin+rescale). */
 int ckks_mul_relin_rescale_many(ckks_context *ctx, const ckks_ct *const *a,
                                 const ckks_ct *const *b, int n, ckks_ct **out);
