@@ -1082,8 +1082,28 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
 // relin_batch then D rescales, without the relinearised ciphertext's forward
 // NTT, the inverse NTTs of the dropped limbs and the rescales' lift NTTs and
 // combines.
+// The postop of homo_mul_relin_rescale_postop on the host side: doubling,
+// the ciphertexts subtracted (per pair, or null) and the scalar's words.
+struct PostSpec {
+  int dbl;
+  const ckks_ct *const *sub;
+  const u64 *scal;
+};
+
+static PostOp post_chunk(const ckks_context *c, const PostSpec *ps, int b0, int nb) {
+  PostOp po{};
+  if (!ps) return po;
+  po.dbl = ps->dbl;
+  po.scal = ps->scal;
+  if (ps->sub) {
+    for (int i = 0; i < nb; i++) po.sub.p[i] = ps->sub[b0 + i]->d;
+    po.sub1_off = (u64)ps->sub[b0]->limbs * c->N;
+  }
+  return po;
+}
+
 static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out,
-                                int D = 1) {
+                                int D = 1, const PostSpec *ps = nullptr) {
   const int limbs = in[0]->limbs, T = limbs - D, A = c->alpha;
   const size_t N = c->N, P = (size_t)limbs * N;
   const DeviceKey &key = get_key(c, 0);
@@ -1119,9 +1139,10 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
                            rt + 4 * (size_t)T);
     std::vector<u64> gal(nb, 1);
     const u64 *amul = rt + 2 * (size_t)T;
+    const PostOp po = post_chunk(c, ps, b0, nb);
     if (c->logN == 16) {
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
-                         d3, P, gal.data(), o0, (u64)T * N, amul);
+                         d3, P, gal.data(), o0, (u64)T * N, amul, &po);
     } else {
       Batch a1{}, o1{};
       for (int i = 0; i < nb; i++) {
@@ -1131,7 +1152,7 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
       launch_ntt(c, strided(conv, (size_t)T * N), strided(conv, (size_t)T * N), 2 * nb, 0, T, T,
                  false);
       launch_moddown_combine(c, Strided{acc, 2 * E * N}, Strided{conv, 2 * T * N}, d3, a1,
-                             gal.data(), o0, o1, nb, T, E, rt, amul);
+                             gal.data(), o0, o1, nb, T, E, rt, amul, &po);
     }
   }
 }
@@ -1858,11 +1879,13 @@ int ckks_rotate_many_noalloc(ckks_context *c, const ckks_ct *const *in, int n, i
   API_END
 }
 
-int ckks_mul_relin_rescale_many_by(ckks_context *c, const ckks_ct *const *a,
-                                   const ckks_ct *const *b, int n, int primes, ckks_ct **out) {
-  API_BEGIN
-  require(c && a && b && out && n >= 1, "null argument");
+// HMult + relinearise + `primes` rescales of n pairs, with the postop of
+// ps (primes == 1) folded into the ModDown epilogue when the merged path
+// applies and applied by limb-wise launches otherwise.
+static void mul_relin_rescale(ckks_context *c, const ckks_ct *const *a, const ckks_ct *const *b,
+                              int n, int primes, const PostSpec *ps, ckks_ct **out) {
   for (int i = 0; i < n; i++) out[i] = nullptr;
+  check_ct(c, a[0], "mul");
   const int limbs = a[0]->limbs;
   require(primes >= 1 && primes <= kMaxRescaleDrop, "a rescale divides by 1 to 4 primes");
   require(limbs > primes, "rescale needs more limbs than the primes it divides by");
@@ -1908,13 +1931,63 @@ int ckks_mul_relin_rescale_many_by(ckks_context *c, const ckks_ct *const *a,
       o[i] = out[b0 + i] = new_ct(c, 2, limbs - primes, 0, a[b0 + i]->slots, scale, degree);
     }
     if (merged) {
-      relin_rescale_batch(c, p3.data(), nb, o.data(), primes);
+      relin_rescale_batch(c, p3.data(), nb, o.data(), primes, ps);
       continue;
     }
     relin_batch(c, p3.data(), nb, p2.data());
     std::vector<const ckks_ct *> cp2(p2.begin(), p2.end());
     rescale_batch(c, cp2.data(), nb, o.data(), primes);
+    if (!ps) continue;
+    const int T = limbs - primes;
+    for (int i = 0; i < nb; i++) {
+      u64 *od = o[i]->d;
+      if (ps->dbl) launch_addsub(c, od, od, od, 2, T, T, 0);
+      if (ps->sub) {
+        const ckks_ct *sb = ps->sub[b0 + i];
+        for (int comp = 0; comp < 2; comp++)
+          launch_addsub(c, od + (size_t)comp * T * N, sb->d + (size_t)comp * sb->limbs * N,
+                        od + (size_t)comp * T * N, 1, T, T, 1);
+      }
+      if (ps->scal) launch_scalar(c, od, ps->scal, od, 2, T, T, 0);
+    }
   }
+}
+
+int ckks_mul_relin_rescale_many_by(ckks_context *c, const ckks_ct *const *a,
+                                   const ckks_ct *const *b, int n, int primes, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && b && out && n >= 1, "null argument");
+  mul_relin_rescale(c, a, b, n, primes, nullptr, out);
+  API_END
+}
+
+int ckks_mul_relin_rescale_postop_many(ckks_context *c, const ckks_ct *const *a,
+                                       const ckks_ct *const *b, int n, int apply_double,
+                                       const ckks_ct *const *sub, const ckks_ct *scalar,
+                                       ckks_ct **out) {
+  API_BEGIN
+  require(c && a && b && out && n >= 1, "null argument");
+  check_ct(c, a[0], "postop");
+  require(a[0]->limbs >= 2, "the product needs at least two limbs");
+  const int T = a[0]->limbs - 1;
+  if (sub) {
+    for (int i = 0; i < n; i++) {
+      check_ct(c, sub[i], "postop sub");
+      require(sub[i]->polys == 2 && !sub[i]->is_ext && sub[i]->limbs >= T,
+              "sub must be a degree-1 Q-basis ciphertext at or above the output level");
+      require(sub[i]->limbs == sub[0]->limbs, "every sub must have one limb count");
+      require(a[i] && b[i], "null argument");
+      const double s = a[i]->scale * b[i]->scale / (double)c->primes[T];
+      const double r = fabs(s - sub[i]->scale) / std::max(s, sub[i]->scale);
+      require(r < 1.0 / 1024.0, "sub's scale differs from the product's");
+    }
+  }
+  if (scalar) {
+    check_ct(c, scalar, "postop scalar");
+    require(scalar->polys == 0 && scalar->limbs >= T, "scalar limbs below the output level");
+  }
+  PostSpec ps{apply_double ? 1 : 0, sub, scalar ? scalar->d : nullptr};
+  mul_relin_rescale(c, a, b, n, 1, &ps, out);
   API_END
 }
 

@@ -58,6 +58,18 @@ struct Strided {
   u64 stride;
 };
 
+// Epilogue of a relinearise-rescale ModDown (the fused Chebyshev step of
+// homo_mul_relin_rescale_postop): the result r becomes
+//   (dbl ? 2 r : r) - sub + scal   (scal on component 0 only)
+// with sub per item at component 0 (null: none), its component 1 at
+// sub + sub1_off, and scal one word per output limb (null: none).
+struct PostOp {
+  int dbl;
+  Batch sub;
+  u64 sub1_off;
+  const u64 *scal;
+};
+
 __device__ __forceinline__ u64 *batch_ptr(const Batch &b, int i) {
   return b.base ? b.base + (u64)i * b.stride : b.p[i];
 }
@@ -278,11 +290,12 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
-                            int E, const u64 *pinv, const u64 *amul = nullptr);
+                            int E, const u64 *pinv, const u64 *amul = nullptr,
+                            const PostOp *post = nullptr);
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off,
-                        const u64 *amul = nullptr);
+                        const u64 *amul = nullptr, const PostOp *post = nullptr);
 void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
                          int limbs, int D, const u64 *tab);
 void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,

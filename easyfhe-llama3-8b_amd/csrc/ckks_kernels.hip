@@ -265,7 +265,19 @@ struct MDCombine {
   Batch out;        // per item: component-0 output
   u64 out1_off;     // component-1 output at out + out1_off
   Galois64 gal;
+  PostOp post;      // postop of the relinearise-rescale step (zero: none)
 };
+
+// (dbl ? 2 r : r) - sub + scal of the postop, at word (limb, e) of an output
+// component (PostOp)
+__device__ __forceinline__ u64 apply_post(const PostOp &po, int item, int comp, int limb, u32 e,
+                                          size_t N, u64 r, u64 q) {
+  if (po.dbl) r = add_mod(r, r, q);
+  const u64 *sb = batch_ptr(po.sub, item);
+  if (sb) r = sub_mod(r, sb[(comp ? po.sub1_off : 0) + (size_t)limb * N + e], q);
+  if (po.scal && !comp) r = add_mod(r, po.scal[limb], q);
+  return r;
+}
 
 // Operands of the epilogue for the 16 outputs e(k) = tile + rl 256 + c0 + 16 k
 // of one thread, loaded at kernel entry so that their latency overlaps the
@@ -298,6 +310,7 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
   u64 r = shoup_mul(sub_mod(a, y, q), md.pinv[2 * limb], md.pinv[2 * limb + 1], q);
   if (md.amul) d = shoup_mul(d, md.amul[2 * limb], md.amul[2 * limb + 1], q);
   r = add_mod(r, d, q);
+  r = apply_post(md.post, item, comp, limb, e, N, r, q);
   u64 *o = batch_ptr(md.out, item) + (comp ? md.out1_off : 0);
   o[(size_t)limb * N + e] = r;
 }
@@ -915,7 +928,8 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
 // is never written back.  N = 2^16 only.
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
-                        const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul) {
+                        const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul,
+                        const PostOp *post) {
   if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
   MDCombine md{};
   md.acc = acc;
@@ -926,6 +940,7 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   md.add1_off = add1_off;
   md.out = out;
   md.out1_off = out1_off;
+  if (post) md.post = *post;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
   dim3 block(TPB), grid(16, 2 * n, limbs);
   hipLaunchKernelGGL(k_ntt16m_fwd_high, grid, block, 0, c->stream, conv, conv, 0, limbs, c->L,
@@ -1631,7 +1646,8 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
 __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch add1,
                                   Galois64 gal, Batch out0, Batch out1, int logN, int limbs,
                                   int E, const u64 *__restrict__ pinv,
-                                  const u64 *__restrict__ amul, const ModQ *__restrict__ mods) {
+                                  const u64 *__restrict__ amul, const ModQ *__restrict__ mods,
+                                  PostOp post) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = blockIdx.y;
   const int item = blockIdx.z >> 1, comp = blockIdx.z & 1;
@@ -1650,6 +1666,7 @@ __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch a
     if (amul) d = shoup_mul(d, amul[2 * l], amul[2 * l + 1], q);
     r = add_mod(r, d, q);
   }
+  r = apply_post(post, item, comp, l, (u32)k, N, r, q);
   u64 *o = comp ? batch_ptr(out1, item) : batch_ptr(out0, item);
   o[(size_t)l * N + k] = r;
 }
@@ -1657,13 +1674,15 @@ __global__ void k_moddown_combine(Strided acc, Strided conv, Batch add0, Batch a
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
-                            int E, const u64 *pinv, const u64 *amul) {
+                            int E, const u64 *pinv, const u64 *amul, const PostOp *post) {
   if (n_items > kMaxBatch) throw std::invalid_argument("moddown combine: too many items");
   Galois64 g{};
   for (int i = 0; i < n_items; i++) g.g[i] = galois[i];
+  PostOp po{};
+  if (post) po = *post;
   dim3 grid(c->N / TPB, limbs, 2 * n_items);
   hipLaunchKernelGGL(k_moddown_combine, grid, dim3(TPB), 0, c->stream, acc, conv, add0, add1,
-                     g, out0, out1, c->logN, limbs, E, pinv, amul, c->d_mods);
+                     g, out0, out1, c->logN, limbs, E, pinv, amul, c->d_mods, po);
   LAUNCH_CHECK();
 }
 

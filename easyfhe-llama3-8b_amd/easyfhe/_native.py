@@ -116,6 +116,7 @@ SIGNATURES = {
     "ckks_mod_raise": (I, [VP, VP, I, VPP]),
     "ckks_rotate_many": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
     "ckks_rotate_many_noalloc": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
+    "ckks_mul_relin_rescale_postop_many": (I, [VP, VPP, VPP, I, I, VPP, VP, VPP]),
     "ckks_mul_relin_rescale_many": (I, [VP, VPP, VPP, I, VPP]),
     "ckks_mul_relin_rescale_many_by": (I, [VP, VPP, VPP, I, I, VPP]),
     "ckks_hoisted_rotate": (I, [VP, VP, I64P, I, VPP]),

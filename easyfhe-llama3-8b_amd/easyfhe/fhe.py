@@ -698,64 +698,116 @@ def rescale(a, context=None):
     return _wrap(ctx, out)
 
 
+# relative scale differences below this are one scale (float rounding of the
+# exact bookkeeping); above it align_to adjusts the scale when it has a level
+_SAME_SCALE = 2.0 ** -32
+# fixed-scale tolerance of limb-wise sums (the library's check_scales)
+_FIXED_SCALE_TOL = 1.0 / 1024.0
+
+
 def align_to(a, target_state: CipherState, context=None):
-    """Modulus drop to ``target_state.cur_limbs``; returns ``a`` itself when
-    nothing changes (reference operators/primitives.py:145-150).  A target
-    scaling factor must agree with ``a``'s to 2^-10 relative (fixed-scale
-    bookkeeping: primes are within 2^-17 of the nominal scale)."""
+    """Bring ``a`` to ``target_state``: its limb count and, when the state
+    names one, its scaling factor (reference operators/primitives.py:140-150,
+    the Meta-BTS alignments of operators/nonlinear/bootstrap.py:386-424).
+    Returns ``a`` itself when nothing changes.
+
+    A limb drop keeps the scale.  A different target scale ``w`` is reached
+    exactly up to integer rounding: ``a`` is cut to ``t + D`` limbs, multiplied
+    by the integer ``round(w p / s)`` with ``p`` the product of the D primes
+    above the target level (D the fewest that make the integer at least
+    2^30), and rescaled by those primes; the result's scale is ``w`` to
+    within 2^-31 relative, and only levels that the drop would shed are used.
+    Without such a level, a scale within the fixed-scale tolerance (2^-10
+    relative) is kept and a larger difference raises ``ValueError``."""
     ctx = _ctx(a, context)
     target = int(target_state.cur_limbs)
     info = a._info()
-    if target > int(info.limbs):
-        raise ValueError(
-            f"cannot align {int(info.limbs)} limbs up to {target} limbs")
+    cur, scale = int(info.limbs), float(info.scale)
+    if target > cur:
+        raise ValueError(f"cannot align {cur} limbs up to {target} limbs")
+    if target < 1:
+        raise ValueError("cannot align below one limb")
     want = target_state.scaling_factor
-    if want is not None and abs(float(want) - info.scale) > float(info.scale) / 1024.0:
-        raise ValueError("align_to cannot change the scaling factor")
-    if target == int(info.limbs):
-        return a
+    if want is not None and float(want) <= 0.0:
+        raise ValueError("the target scaling factor must be positive")
+    if want is None or abs(float(want) - scale) <= scale * _SAME_SCALE:
+        return a if target == cur else _drop_limbs(a, target, ctx)
+    want = float(want)
+    primes = [int(q) for q in ctx.primes()[: ctx.L]]
+    prod, D = 1.0, 0
+    while target + D < cur and want * prod / scale < 2.0 ** 30:
+        prod *= float(primes[target + D])
+        D += 1
+    k = want * prod / scale
+    if D == 0 or k < 2.0 ** 30:
+        if abs(want - scale) <= scale * _FIXED_SCALE_TOL:
+            return a if target == cur else _drop_limbs(a, target, ctx)
+        raise ValueError(
+            f"align_to needs a spare level to change the scale by {want / scale:.6g} "
+            f"({cur} limbs -> {target})")
+    if k >= 2.0 ** 62:
+        raise ValueError(f"scale ratio {want / scale:.6g} is too large to adjust in one step")
+    work = a if target + D == cur else _drop_limbs(a, target + D, ctx)
+    try:
+        factor = encode_scalar(1.0, target + D, scaling_factor=float(np.rint(k)), context=ctx)
+        try:
+            prod_ct = homo_mul_scalar(work, factor, ctx)
+        finally:
+            factor.release()
+        try:
+            return rescale_many([prod_ct], ctx, primes=D)[0]
+        finally:
+            prod_ct.release()
+    finally:
+        if work is not a:
+            work.release()
+
+
+def _drop_limbs(a, target: int, ctx) -> "Ciphertext":
     out = ctypes.c_void_p()
-    check(lib.ckks_drop_limbs(ctx.handle, a.handle, target, ctypes.byref(out)))
+    check(lib.ckks_drop_limbs(ctx.handle, a.handle, int(target), ctypes.byref(out)))
     return _wrap(ctx, out)
 
 
 def homo_mul_relin_rescale_postop(left, right, context=None, *, apply_double: bool = False,
                                   sub=None, scalar=None):
-    """rescale(relin(l r)), then x2 when ``apply_double``, then ``- sub`` or
-    ``+ scalar`` at the output state (reference
-    operators/nonlinear/polynomial.py:115-203)."""
+    """rescale(relin(l r)), then x2 when ``apply_double``, then ``- sub`` and
+    ``+ scalar`` at the output level, as one key switch whose ModDown applies
+    the postop (reference operators/nonlinear/polynomial.py:115-203).  The
+    operands meet at the lower of their levels first."""
     ctx = _ctx(left, context)
     limbs = min(left.state.cur_limbs, right.state.cur_limbs)
     l2 = align_to(left, left.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
     r2 = align_to(right, right.state.replace(cur_limbs=limbs, scaling_factor=None), ctx)
-    owned = [x for x, y in ((l2, left), (r2, right)) if x is not y]
     try:
-        prod = homo_mul_relin(l2, r2, ctx)
-        try:
-            value = rescale(prod, ctx)
-        finally:
-            prod.release()
+        return homo_mul_relin_rescale_postop_many(
+            [l2], [r2], ctx, apply_double=apply_double,
+            sub=None if sub is None else [sub], scalar=scalar)[0]
     finally:
-        for x in owned:
-            x.release()
-    if apply_double:
-        doubled = homo_add(value, value, ctx)
-        value.release()
-        value = doubled
-    if sub is not None:
-        aligned = align_to(sub, value.state.replace(scaling_factor=None), ctx)
-        try:
-            diff = homo_sub(value, aligned, ctx)
-        finally:
-            if aligned is not sub:
-                aligned.release()
-        value.release()
-        value = diff
-    if scalar is not None:
-        added = homo_add_scalar(value, scalar, ctx)
-        value.release()
-        value = added
-    return value
+        for x, y in ((l2, left), (r2, right)):
+            if x is not y:
+                x.release()
+
+
+def homo_mul_relin_rescale_postop_many(left: Sequence[Ciphertext], right: Sequence[Ciphertext],
+                                       context=None, *, apply_double: bool = False,
+                                       sub: Sequence[Ciphertext] | None = None,
+                                       scalar=None) -> list:
+    """``homo_mul_relin_rescale_postop`` of n pairs at one level in batched
+    launches; ``sub`` holds one ciphertext per pair (or None), ``scalar`` is
+    shared by all pairs."""
+    left, right = list(left), list(right)
+    if len(left) != len(right) or (sub is not None and len(list(sub)) != len(left)):
+        raise ValueError("operand lists differ in length")
+    if not left:
+        return []
+    ctx = _ctx(left[0], context)
+    outs = (ctypes.c_void_p * len(left))()
+    subs = None if sub is None else ptr_array([c.handle for c in sub])
+    check(lib.ckks_mul_relin_rescale_postop_many(
+        ctx.handle, ptr_array([c.handle for c in left]), ptr_array([c.handle for c in right]),
+        len(left), int(bool(apply_double)), subs, None if scalar is None else scalar.handle, outs))
+    return [Ciphertext(ctx, outs[i]) for i in range(len(left))]
 
 
 def homo_rotate(a, rotation: int, context=None):

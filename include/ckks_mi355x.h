@@ -190,6 +190,19 @@ int ckks_mul_relin_rescale_many(ckks_context *ctx, const ckks_ct *const *a,
  * separate steps. */
 int ckks_mul_relin_rescale_many_by(ckks_context *ctx, const ckks_ct *const *a,
                                    const ckks_ct *const *b, int n, int primes, ckks_ct **out);
+/* homo_mul_relin_rescale_postop for n pairs (reference
+ * operators/nonlinear/polynomial.py:115-203, the Chebyshev basis steps
+ * 2 T_i T_j - T_1 and 2 T_i T_j - 1):
+ *   out_i = (apply_double ? 2 : 1) rescale(relin(a_i b_i)) - sub_i + scalar
+ * with sub (n degree-1 ciphertexts of one limb count at or above the output
+ * level, their leading limbs used) and scalar (encode_scalar at or above the
+ * output level, added to component 0) each optional (NULL).  The ModDown by
+ * P q_l of the relinearise-rescale applies the postop in its epilogue, so
+ * the words equal those of the separate calls. */
+int ckks_mul_relin_rescale_postop_many(ckks_context *ctx, const ckks_ct *const *a,
+                                       const ckks_ct *const *b, int n, int apply_double,
+                                       const ckks_ct *const *sub, const ckks_ct *scalar,
+                                       ckks_ct **out);
 /* fhe.prepare_hoisted_baby_rotations (reference operators/linear/operator.py:105):
  * one ModUp of c1 shared by all rotations. */
 int ckks_hoisted_rotate(ckks_context *ctx, const ckks_ct *a,

@@ -116,6 +116,49 @@ def test_bootstrap_two_pass_gains_precision(boot_ctx):
     assert e2 < e1 / 16
 
 
+def test_reference_meta_bts_sequence_gains_precision(boot_ctx):
+    """The reference's two-pass refresh (operators/nonlinear/bootstrap.py:404-433)
+    restated with the fhe calls it makes, on an input whose scale (1.37 x 2^40)
+    differs from the bootstrap output's: its first align_to must change the
+    scale (a ValueError there makes the reference fall back to one pass), and
+    the second pass must gain at least 4 bits over a coarse first pass."""
+    from easyfhe import fhe
+    from easyfhe.bs import openfhe as bs
+
+    client, ctx = boot_ctx
+    n = ctx.max_slots
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3),
+                                             output_levels=3), bs.BootstrapParams(cts_pt_bits=45))
+    rng = np.random.default_rng(18)
+    z = rng.uniform(-1, 1, n)
+    original = client.encrypt(z, cur_limbs=2, scaling_factor=1.37 * 2.0**40, enc_id=76)
+    factor = 1 << 8
+
+    def times_int(ct, v):
+        enc = fhe.encode_scalar(int(v), cur_limbs=int(ct.state.cur_limbs), scale_degree=0,
+                                mode="integer", context=ctx)
+        return fhe.homo_mul_scalar(ct, enc, ctx)
+
+    first = bs.bootstrap(original, ctx, prog)
+    first_scaled = times_int(first, factor)
+    first_down = fhe.align_to(first_scaled, original.state, ctx)
+    assert first_down.state.cur_limbs == 2
+    original_scaled = fhe.align_to(times_int(original, factor), first_down.state, ctx)
+    error = bs.bootstrap(fhe.homo_sub(first_down, original_scaled, ctx), ctx, prog)
+    first_aligned = fhe.align_to(first_scaled, error.state, ctx)
+    error_aligned = fhe.align_to(error, first_aligned.state, ctx)
+    corrected = fhe.homo_sub(first_aligned, error_aligned, ctx)
+    enc = fhe.encode_scalar(1.0 / factor, cur_limbs=int(corrected.state.cur_limbs),
+                            scale_degree=1, scaling_factor=corrected.state.scaling_factor,
+                            context=ctx)
+    two = fhe.homo_mul_scalar_rescale(corrected, enc, ctx)
+    e1 = np.abs(client.decrypt(first) - z).max()
+    e2 = np.abs(client.decrypt(two) - z).max()
+    print(f"reference Meta-BTS: one pass {-math.log2(e1):.1f} bits, two {-math.log2(e2):.1f}")
+    assert e2 < e1 / 16
+    prog.release()
+
+
 def test_bootstrap_many_matches_single(boot_ctx):
     """Batched groups run the same arithmetic per ciphertext: identical limbs."""
     from easyfhe.bs import openfhe as bs

@@ -532,3 +532,89 @@ def test_scalar_constants_and_invalid_objects():
             fhe.upload(ctx, before, slots=bad, scale=sc)
     with pytest.raises(ValueError):
         fhe.upload(ctx, before[:, :, :-1], slots=ctx.max_slots, scale=sc)
+
+
+# a chain whose special primes are too wide for the merged relinearise-rescale
+# ModDown (12 x 60-bit P: the postop then runs as separate launches)
+WIDE_P = dict(log_n=12, depth=35, dnum=3, dcrt_bits=40, first_mod=60, special_bits=60)
+
+
+@pytest.mark.parametrize("name", ["small", "matvec", "keyswitch", "wide_p"])
+def test_mul_relin_rescale_postop_matches_composed(name):
+    """homo_mul_relin_rescale_postop (x2, - sub, + scalar folded into the
+    ModDown epilogue) equals the oracle's relinearise, rescale, add, sub and
+    scalar add on the same words (reference operators/nonlinear/
+    polynomial.py:115-203: 2 T_i T_j - T_1 and 2 T_i T_j - 1)."""
+    fhe = _fhe()
+    p = WIDE_P if name == "wide_p" else name
+    client, ctx = device_context(p)
+    orc = oracle_context(p)
+    orc.gen_relin_key()
+    slots, L = ctx.max_slots, ctx.L
+    n = 2 if name == "keyswitch" else 3
+    rng = np.random.default_rng(31)
+    sc = ctx.scale_at(L)
+    xs = [rng.uniform(-1, 1, slots) for _ in range(n)]
+    ys = [rng.uniform(-1, 1, slots) for _ in range(n)]
+    zs = [rng.uniform(-1, 1, slots) for _ in range(n)]
+    a = [client.encrypt(x, enc_id=500 + i) for i, x in enumerate(xs)]
+    b = [client.encrypt(y, enc_id=520 + i) for i, y in enumerate(ys)]
+    subs = [client.encrypt(z, enc_id=540 + i) for i, z in enumerate(zs)]
+    ra = [orc.encrypt(x, slots=slots, scale=sc, limbs=L, enc_id=500 + i) for i, x in enumerate(xs)]
+    rb = [orc.encrypt(y, slots=slots, scale=sc, limbs=L, enc_id=520 + i) for i, y in enumerate(ys)]
+    rs = [orc.encrypt(z, slots=slots, scale=sc, limbs=L, enc_id=540 + i) for i, z in enumerate(zs)]
+    base = [orc.rescale(orc.relinearize(orc.tensor(ra[i], rb[i]))) for i in range(n)]
+    out_scale = sc * sc / ctx.rescale_divisor_at(L - 1)
+    scal = fhe.encode_scalar(-1.0, cur_limbs=L, scaling_factor=out_scale, context=ctx)
+    words = scal.download()[: L - 1].astype(np.uint64)
+    primes = ctx.primes()[: L - 1].astype(np.uint64)
+    cases = [(True, True, False), (True, False, True), (False, True, True), (False, False, False)]
+    for dbl, use_sub, use_scal in cases[: 2 if name == "keyswitch" else 4]:
+        outs = fhe.homo_mul_relin_rescale_postop_many(
+            a, b, ctx, apply_double=dbl, sub=subs if use_sub else None,
+            scalar=scal if use_scal else None)
+        for i in range(n):
+            want = base[i]
+            if dbl:
+                want = orc.add(want, want)
+            if use_sub:
+                want = orc.sub(want, orc.drop_limbs(rs[i], L - 1))
+            if use_scal:
+                want = want.copy()
+                want[0] = (want[0] + words[:, None]) % primes[:, None]
+            assert np.array_equal(outs[i].download(), want), (dbl, use_sub, use_scal, i)
+        # the subtrahend enters at its own scale (fixed-scale bookkeeping): on a
+        # 40-bit chain the product's scale 2^80 / q differs from it by ~2^-15
+        got = client.decrypt(outs[0])
+        exp = ((2 if dbl else 1) * xs[0] * ys[0] - (zs[0] * sc / out_scale if use_sub else 0)
+               - (1 if use_scal else 0))
+        assert np.abs(got - exp).max() < 1e-5
+    # the single-pair form aligns operands at different levels first
+    low = fhe.align_to(b[0], b[0].state.replace(cur_limbs=L - 1, scaling_factor=None), ctx)
+    one = fhe.homo_mul_relin_rescale_postop(a[0], low, ctx, apply_double=True, sub=subs[0])
+    assert one.state.cur_limbs == L - 2
+    ratio = subs[0].state.scaling_factor / one.state.scaling_factor
+    assert np.abs(client.decrypt(one) - (2 * xs[0] * ys[0] - zs[0] * ratio)).max() < 1e-5
+
+
+def test_align_to_changes_the_scale():
+    """A target scaling factor different from the source's is reached by an
+    integer multiply and a rescale on the levels the drop sheds; without a
+    spare level only the fixed-scale tolerance is accepted."""
+    fhe = _fhe()
+    client, ctx = device_context("small", relin=False)
+    L = ctx.L
+    rng = np.random.default_rng(41)
+    z = rng.uniform(-1, 1, ctx.max_slots)
+    ct = client.encrypt(z, enc_id=600)
+    for target, ratio in ((2, 1.37), (3, 0.61), (L - 1, 1.0 + 2.0**-20)):
+        want = ct.state.scaling_factor * ratio
+        out = fhe.align_to(ct, ct.state.replace(cur_limbs=target, scaling_factor=want), ctx)
+        assert out.state.cur_limbs == target
+        assert abs(out.state.scaling_factor / want - 1.0) < 2.0**-30
+        assert np.abs(client.decrypt(out) - z).max() < 1e-6
+    # same limbs: within 2^-10 kept as is, beyond it refused
+    near = ct.state.replace(scaling_factor=ct.state.scaling_factor * (1 + 2.0**-12))
+    assert fhe.align_to(ct, near, ctx) is ct
+    with pytest.raises(ValueError):
+        fhe.align_to(ct, ct.state.replace(scaling_factor=ct.state.scaling_factor * 1.5), ctx)
