@@ -44,31 +44,118 @@ def keyswitch_bytes(N: int, limbs: int, alpha: int, digits: int, batch: int, rel
     return 8.0 * N * (polys + 2.0 * digits * (limbs + alpha) / batch)
 
 
-def cpu_baseline(seconds_budget: float = 20.0):
-    """Oracle rotations at the full workload size on the host cores."""
+def _oracle_timing_library():
+    """The oracle's ORC_FAST build (Shoup reductions, the same words as the
+    pinned build) compiled for this host with -O3 -march=native when gcc is
+    here, else the prebuilt generic x86-64 one."""
     sys.path.insert(0, str(ROOT / "oracle"))
+    import tempfile
+
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
-    O.set_threads(threads)
+    src = ROOT / "oracle" / "ckks_oracle.c"
+    out = Path(tempfile.mkdtemp(prefix="ckks_oracle_")) / "libckks_oracle_native.so"
+    cmd = ["gcc", "-O3", "-march=native", "-std=gnu11", "-fPIC", "-fopenmp", "-ffp-contract=off",
+           "-DORC_FAST", "-shared", "-o", str(out), str(src), "-lm"]
+    try:
+        import subprocess
+
+        subprocess.run(cmd, check=True, capture_output=True, timeout=180)
+        return O.load(out), "gcc -O3 -march=native -DORC_FAST (built on this host)"
+    except Exception:
+        return O.load(O.fast_library_path()), "gcc -O3 -DORC_FAST, generic x86-64 (prebuilt)"
+
+
+def _cpu_threads() -> tuple[int, int, int]:
+    """(threads used for the all-core figure, nproc, CPUs in this process's
+    affinity mask); a GPU host's share is 16 cores per GPU."""
+    nproc = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = nproc
+    return max(1, min(16, aff)), nproc, aff
+
+
+def _cpu_rotations(O, lib, threads: int, budget_s: float, cap: int) -> tuple[int, float]:
+    """Chained rotations of one full-size ciphertext (36 limbs, N = 2^16,
+    dnum 3, 12 special primes) on `threads` threads within about budget_s."""
+    lib.orc_set_threads(int(threads))
     L = PARAMS["depth"] + 1
     ctx = O.OracleContext(log_n=16, limbs=L, alpha=12, dnum=3, first_bits=60, dcrt_bits=40,
-                          special_bits=PARAMS["special_bits"], seed=0)
+                          special_bits=PARAMS["special_bits"], seed=0, library=lib)
     g = ctx.galois_elt(1)
     ctx.gen_rotation_key(g)
     z = np.random.default_rng(0).uniform(-1, 1, 1 << 15)
     ct = ctx.encrypt(z, slots=1 << 15, scale=2.0**40, limbs=L, enc_id=1)
-    n = 0
-    t0 = time.perf_counter()
+    n, t0 = 0, time.perf_counter()
     while True:
         ct = ctx.rotate_g(ct, g)
         n += 1
-        if time.perf_counter() - t0 > seconds_budget or n >= 64:
+        if time.perf_counter() - t0 > budget_s or n >= cap:
             break
     dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
-            "sample": f"{n} chained rotations of one ciphertext at 36 limbs, N=2^16 "
-                      f"(oracle/ckks_oracle.c, OpenMP over limbs)"}
+    ctx.close()
+    return n, dt
+
+
+def _cpu_matvec(O, lib, threads: int) -> dict:
+    """The CPU matvec workload end to end on the oracle: N = 2^13, 4 x 40-bit
+    limbs + one 60-bit special prime, W and x uniform[-1, 1] from seed 0, BSGS
+    B = 16, G = 8, 32 token lanes; keys, encode and encrypt timed as set-up,
+    then the hoisted MAC + rescale + decrypt, checked against fp64 W x."""
+    lib.orc_set_threads(int(threads))
+    D, lanes, B, G = 128, 32, 16, 8
+    t0 = time.perf_counter()
+    ctx = O.OracleContext(log_n=13, limbs=4, alpha=1, dnum=4, first_bits=40, dcrt_bits=40,
+                          special_bits=60, seed=0, library=lib)
+    for o in list(range(lanes, B * lanes, lanes)) + [B * lanes]:
+        ctx.gen_rotation_key(ctx.galois_elt(o))
+    slots = ctx.N // 2
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    feat = np.arange(slots) // lanes
+    rows = [W[(feat - g * B) % D, (feat + b) % D] for g in range(G) for b in range(B)]
+    pts = np.stack([ctx.encode(r, slots=slots, scale=2.0**40, limbs=4) for r in rows])
+    ct = ctx.encrypt(packed, slots=slots, scale=2.0**40, limbs=4, enc_id=41)
+    setup = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    acc = ctx.hoisted_mac_sum(ct, [ctx.galois_elt(lanes * b) for b in range(B)], pts,
+                              ctx.galois_elt(B * lanes), G)
+    out = ctx.rescale(acc)
+    sc = 2.0**80 / float(ctx.primes[3])
+    dec = ctx.decrypt(out, slots=slots, scale=sc).real[np.arange(D) * lanes]
+    run = time.perf_counter() - t0
+    ctx.close()
+    return {"setup_s": round(setup, 4), "matvec_s": round(run, 4),
+            "max_abs_err_vs_fp64": float(np.abs(dec - W @ x).max())}
+
+
+def cpu_baseline(seconds_budget: float = 20.0) -> dict:
+    """The oracle (the same algorithms as the kernels) on the host cores: the
+    full-size key switch on one thread and on all of this GPU's cores, and the
+    N = 2^13 matvec workload end to end."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    lib, build = _oracle_timing_library()
+    threads, nproc, aff = _cpu_threads()
+    n1, t1 = _cpu_rotations(O, lib, 1, 0.3 * seconds_budget, 8)
+    n, t = _cpu_rotations(O, lib, threads, 0.5 * seconds_budget, 64)
+    mv1 = _cpu_matvec(O, lib, 1)
+    mv = _cpu_matvec(O, lib, threads)
+    return {"value": n / t, "unit": "keyswitch/s", "cores": threads, "kind": "port",
+            "sample": f"{n} chained rotations of one ciphertext at 36 limbs, N=2^16, dnum 3, "
+                      f"12 special primes, on {threads} threads (oracle/ckks_oracle.c, OpenMP "
+                      f"over limbs and coefficients); {n1} on one thread",
+            "single_thread_value": n1 / t1,
+            "build": build, "nproc": nproc, "affinity_cpus": aff,
+            "matvec_config": {"workload": "BSGS matvec, N=2^13, 4x40b limbs + 1x60b special, "
+                                          "128x128 W, B=16, G=8, seed 0",
+                              "one_thread": mv1, f"{threads}_threads": mv}}
 
 
 def main() -> int:
@@ -92,11 +179,15 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=None,
                     help="layers of the layers mode (default 2) and of the prefill mode "
                          "(default 32)")
-    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "bootstrap", "linear", "mlp",
-                                       "attention", "layer", "layers", "prefill"],
+    ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "ks-profile", "int-peak",
+                                       "bootstrap", "linear", "mlp", "attention", "layer",
+                                       "layers", "prefill"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
+                         "ks-profile: one key-switch step and a 36 MiB device copy, for "
+                         "rocprofv3 counter runs; "
+                         "int-peak: the register-only integer-throughput probes; "
                          "bootstrap: the full-slot bootstrap workload on the same chain; "
                          "linear: one 4096x4096 feature-major linear over 128 tokens; "
                          "mlp: the RMSNorm + SwiGLU MLP + residual half of a layer; "
@@ -128,6 +219,14 @@ def main() -> int:
                                special_bits=PARAMS["special_bits"], seed=0, rotations=ROTATIONS)
     if args.mode == "ntt-profile":
         return ntt_profile(spec, args.cts)
+    if args.mode == "ks-profile":
+        return ks_profile(spec, args.cts, args.levels)
+    if args.mode == "int-peak":
+        spec.rotations = ()
+        spec.relin_key = False
+        client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+        print(json.dumps({"int_peak": int_peaks(ctx)}), flush=True)
+        return 0
     if args.mode == "bootstrap":
         return bootstrap_bench(spec, args)
     if args.mode == "linear":
@@ -174,20 +273,7 @@ def main() -> int:
     levels = min(args.levels, L - 2)
 
     def step():
-        cur = cts
-        for r in ROTATIONS:
-            nxt = fhe.homo_rotate_many(cur, r, ctx)
-            if cur is not cts:
-                for c in cur:
-                    c.release()
-            cur = nxt
-        for _ in range(levels):
-            nxt = fhe.homo_mul_relin_rescale_many(cur, cur, ctx)
-            for c in cur:
-                if c not in cts:
-                    c.release()
-            cur = nxt
-        return cur
+        return keyswitch_step(ctx, cts, levels)
 
     for _ in range(args.warmup):
         out = step()
@@ -274,6 +360,27 @@ def main() -> int:
             "limb_polys_per_launch": limb_polys,
         },
     }
+    # one more step with per-kernel timing (events on the library stream,
+    # outside the timed region): each kernel group's share of the step, its
+    # algorithmic HBM rate and its modular-operation rate against the probes
+    peaks = int_peaks(ctx)
+    ctx.profile(True)
+    out = step()
+    for c in out:
+        c.release()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    result["int_peak"] = peaks
+    result["kernels"] = kernel_table(prof, peaks)
+    kernel_bytes = sum(v["bytes"] for v in prof.values())
+    result["keyswitch_roofline"] = {
+        "bound": "hbm", "achieved": round(ks_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(ks_gbs / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes_per_step": round(step_bytes),
+        "kernel_bytes_per_step": round(kernel_bytes),
+        "kernel_over_algorithmic": round(kernel_bytes / step_bytes, 2),
+    }
+    result["matvec_config"] = measure_matvec_config()
     if not (args.no_bootstrap and args.no_linear and args.no_mlp and args.no_attention):
         for c in cts:
             c.release()
@@ -1020,6 +1127,144 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         "score_max": round(max(r.score_max for r in ranges), 2),
         "device_memory": _memory_summary(mem),
     }
+
+
+def keyswitch_step(ctx, cts, levels: int) -> list:
+    """One step of the key-switch workload: rotations by 2^0 .. 2^14 of every
+    ciphertext (chained), then `levels` levels of HMult + relinearise +
+    rescale; intermediates are released as they are consumed."""
+    from easyfhe import fhe
+
+    cur = cts
+    for r in ROTATIONS:
+        nxt = fhe.homo_rotate_many(cur, r, ctx)
+        if cur is not cts:
+            for c in cur:
+                c.release()
+        cur = nxt
+    for _ in range(levels):
+        nxt = fhe.homo_mul_relin_rescale_many(cur, cur, ctx)
+        for c in cur:
+            if c not in cts:
+                c.release()
+        cur = nxt
+    return cur
+
+
+def ks_profile(spec, n_cts: int, levels: int) -> int:
+    """Exactly one key-switch step over n_cts ciphertexts (after set-up), then
+    three device copies of one 36 MiB ciphertext (the counters' calibration
+    kernel): the program rocprofv3 counter runs of the step use."""
+    from easyfhe import fhe
+
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    cts = [client.encrypt(rng.uniform(-1, 1, slots), slots=slots, enc_id=i + 1)
+           for i in range(n_cts)]
+    ctx.synchronize()
+    for c in keyswitch_step(ctx, cts, min(levels, ctx.L - 2)):
+        c.release()
+    copies = [cts[0].deep_copy() for _ in range(3)]
+    ctx.synchronize()
+    print(json.dumps({"keyswitch_steps": 1, "ciphertexts": n_cts,
+                      "copy_bytes": 2 * ctx.L * ctx.N * 8, "copies": len(copies)}), flush=True)
+    return 0
+
+
+def int_peaks(ctx) -> dict:
+    """Device-wide rates of the register-only probes (ops/s): the fp64-path
+    modular product (limbs below 2^45), the 64-bit Shoup product, fp64 FMA."""
+    import ctypes
+
+    from easyfhe import _native
+
+    out = {}
+    for kind, name in ((0, "fp64_modmul"), (1, "shoup64_modmul"), (2, "fp64_fma")):
+        v = ctypes.c_double()
+        _native.check(_native.lib.ckks_int_peak(ctx.handle, kind, ctypes.byref(v)))
+        out[name] = v.value
+    return out
+
+
+# kernel groups whose modular operations run on the fp64 path (40-bit limbs)
+_INT_GROUPS = ("basis_convert", "basis_convert_rescale", "key_inner", "key_inner_multi",
+               "mac", "mac_many", "mac_table", "tensor", "lincomb")
+
+
+def kernel_table(prof: dict, peaks: dict) -> dict:
+    """Per kernel group of one profiled step: launches, device ms, share of the
+    summed kernel time, algorithmic bytes / time against the 8 TB/s peak and,
+    for the modular-arithmetic groups, operations / time against the fp64-path
+    probe."""
+    total = sum(v["ms"] for v in prof.values()) or 1.0
+    out = {}
+    for name, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        t = max(v["ms"], 1e-9) * 1e-3
+        row = {"launches": v["launches"], "ms": round(v["ms"], 3),
+               "share": round(v["ms"] / total, 4),
+               "gbs": round(v["bytes"] / t / 1e9, 1),
+               "hbm_frac": round(v["bytes"] / t / 1e9 / HBM_PEAK_GBS, 4)}
+        if name in _INT_GROUPS:
+            rate = v["ops"] / t
+            row["gmodops"] = round(rate / 1e9, 1)
+            row["int_frac"] = round(rate / peaks["fp64_modmul"], 4)
+        out[name] = row
+    return out
+
+
+def measure_matvec_config(iters: int = 20) -> dict:
+    """The CPU matvec workload on the device: N = 2^13, 4096 slots, 4 x 40-bit
+    limbs + one 60-bit special prime, scale 2^40, 128 x 128 W and x
+    uniform[-1, 1] from seed 0, BSGS B = 16, G = 8, 32 token lanes; one
+    matvec = hoisted babies + MAC + giant Horner + rescale, averaged over
+    `iters` after a warm-up; decrypted against fp64 W x."""
+    from easyfhe import fhe
+
+    D, lanes, B, G = 128, 32, 16, 8
+    rots = tuple(lanes * b for b in range(1, B)) + (B * lanes,)
+    spec = fhe.CKKSContextSpec(depth=3, log_n=13, dnum=4, dcrt_bits=40, first_mod=40,
+                               special_bits=60, seed=0, rotations=rots)
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec, device="cuda:0")
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    feat = np.arange(slots) // lanes
+    rows = np.stack([W[(feat - g * B) % D, (feat + b) % D] for g in range(G) for b in range(B)])
+    pts = fhe.encode_rows(ctx, rows, limbs=ctx.L, scale=ctx.scale_at(ctx.L), slots=slots)
+    ct = client.encrypt(packed, slots=slots, enc_id=41)
+    ctx.synchronize()
+    setup = time.perf_counter() - t0
+    offsets = [lanes * b for b in range(B)]
+
+    def one():
+        acc = fhe.hoisted_mac_sum(ct, offsets, pts, B * lanes, G, ctx)
+        out = fhe.rescale(acc, ctx)
+        acc.release()
+        return out
+
+    one().release()
+    ctx.synchronize()
+    ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ev0.record()
+    t0 = time.perf_counter()
+    for _ in range(iters - 1):
+        one().release()
+    out = one()
+    ev1.record()
+    ctx.synchronize()
+    wall = (time.perf_counter() - t0) / iters
+    err = float(np.abs(client.decrypt(out)[np.arange(D) * lanes] - W @ x).max())
+    res = {"workload": "BSGS matvec, N=2^13, 4x40b limbs + 1x60b special, 128x128 W, B=16, G=8, "
+                       "seed 0", "ms_per_matvec": round(wall * 1e3, 3),
+           "gpu_event_ms_per_matvec": round(ev0.elapsed_time(ev1) / iters, 3),
+           "setup_s": round(setup, 3), "max_abs_err_vs_fp64": err}
+    ctx.close()
+    return res
 
 
 def bootstrap_bench(spec, args) -> int:

@@ -715,6 +715,11 @@ static void free_context(ckks_context *c) {
     (void)hipEventDestroy(b.ev);
   }
   c->stage.clear();
+  for (auto &r : c->prof_recs) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (auto e : c->prof_pool) (void)hipEventDestroy(e);
   for (auto &kv : c->keys) (void)hipFree(kv.second.data);
   for (auto &kv : c->bc_up) {
     (void)hipFree(kv.second.d);
@@ -750,6 +755,36 @@ static void free_context(ckks_context *c) {
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
+
+// ===========================================================================
+// per-kernel timing
+// ===========================================================================
+
+namespace ckks {
+static hipEvent_t prof_event(ckks_context *c) {
+  if (!c->prof_pool.empty()) {
+    hipEvent_t e = c->prof_pool.back();
+    c->prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  HIPCHECK(hipEventCreate(&e));
+  return e;
+}
+
+KTimer::KTimer(ckks_context *cc, const char *name, double bytes, double ops)
+    : c(cc), on(cc->prof) {
+  if (!on) return;
+  r = ProfRec{name, prof_event(c), prof_event(c), bytes, ops};
+  (void)hipEventRecord(r.a, c->stream);
+}
+
+KTimer::~KTimer() {
+  if (!on) return;
+  (void)hipEventRecord(r.b, c->stream);
+  c->prof_recs.push_back(r);
+}
+}  // namespace ckks
 
 // ===========================================================================
 // fixed key-switch scratch of ckks_rotate_many_noalloc
@@ -2678,6 +2713,59 @@ int ckks_ntt_many(ckks_context *c, ckks_ct *const *cts, int n, int inverse) {
       launch_ntt(c, bp, bp, nb, 0, limbs, limbs, inverse != 0);
     }
   }
+  API_END
+}
+
+int ckks_int_peak(ckks_context *c, int kind, double *ops_per_second) {
+  API_BEGIN
+  require(c && ops_per_second, "null argument");
+  require(kind >= 0 && kind <= 2, "kind must be 0 (fp64 modular product), 1 (64-bit Shoup) or 2 (fp64 FMA)");
+  const int blocks = 4096, iters = 2048;
+  Scratch s(c);
+  double *out = (double *)s.get((size_t)blocks * 256);
+  launch_int_peak(c, kind, out, blocks, iters / 8);  // warm-up
+  *ops_per_second = launch_int_peak(c, kind, out, blocks, iters);
+  API_END
+}
+
+int ckks_profile_enable(ckks_context *c, int enable) {
+  API_BEGIN
+  require(c, "null argument");
+  c->prof = enable != 0;
+  API_END
+}
+
+int ckks_profile_read(ckks_context *c, char *buf, size_t len) {
+  API_BEGIN
+  require(c && buf && len > 0, "null argument");
+  HIPCHECK(hipStreamSynchronize(c->stream));
+  struct Sum {
+    long calls = 0;
+    double ms = 0, bytes = 0, ops = 0;
+  };
+  std::map<std::string, Sum> sums;
+  for (auto &r : c->prof_recs) {
+    float ms = 0;
+    HIPCHECK(hipEventElapsedTime(&ms, r.a, r.b));
+    Sum &s = sums[r.name];
+    s.calls++;
+    s.ms += ms;
+    s.bytes += r.bytes;
+    s.ops += r.ops;
+    c->prof_pool.push_back(r.a);
+    c->prof_pool.push_back(r.b);
+  }
+  c->prof_recs.clear();
+  std::string text;
+  for (auto &kv : sums) {
+    char line[256];
+    snprintf(line, sizeof line, "%s %ld %.6f %.6e %.6e\n", kv.first.c_str(), kv.second.calls,
+             kv.second.ms, kv.second.bytes, kv.second.ops);
+    text += line;
+  }
+  const size_t n = std::min(len - 1, text.size());
+  memcpy(buf, text.data(), n);
+  buf[n] = 0;
   API_END
 }
 

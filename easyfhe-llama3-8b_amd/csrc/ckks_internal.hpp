@@ -197,6 +197,15 @@ struct FFTTable {  // encoder tables for one slot count n
   u32 *perm;       // [n] r_j = (5^j mod 4n - 1) / 4
 };
 
+// Per-kernel timing (ckks_profile_enable / ckks_profile_read): HIP events on
+// the context stream around a launch, with its algorithmic bytes (each input
+// word read once, each output word written once) and modular operations.
+struct ProfRec {
+  const char *name;
+  hipEvent_t a, b;
+  double bytes, ops;
+};
+
 }  // namespace ckks
 
 struct ckks_context {
@@ -233,6 +242,9 @@ struct ckks_context {
   std::map<std::pair<int, int>, u64 *> rescale_d;  // (limbs, primes) -> rescale constants
   std::map<int, ckks::FFTTable> fft;
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
+  bool prof = false;                     // per-kernel timing on
+  std::vector<ckks::ProfRec> prof_recs;  // timed launches since the last read
+  std::vector<hipEvent_t> prof_pool;     // events for reuse
   int device = 0;                  // HIP device current at creation
   u64 *noalloc_scratch = nullptr;  // that device's fixed scratch (ckks_rotate_many_noalloc)
   bool rotation_tables = false;    // every level's key-switch constants built
@@ -263,6 +275,17 @@ struct ckks_tensor {  // raw device bytes (weights for the diagonal packers)
 // kernel launchers (ckks_kernels.hip)
 // ---------------------------------------------------------------------------
 namespace ckks {
+
+// Records one timed launch when the context profiles (scope = the launches).
+struct KTimer {
+  ckks_context *c;
+  ProfRec r{};
+  bool on;
+  KTimer(ckks_context *c, const char *name, double bytes, double ops);
+  ~KTimer();
+  KTimer(const KTimer &) = delete;
+  KTimer &operator=(const KTimer &) = delete;
+};
 
 void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                 int l_begin, int l_count, int q_limbs, bool inverse);
@@ -349,5 +372,8 @@ void launch_encode(ckks_context *c, const double *d_re, const double *d_im, int 
 void launch_encrypt_finish(ckks_context *c, u64 *ct, int limbs, u32 enc_id);
 void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, double *d_im);
 void launch_scalar_encode(ckks_context *c, double v, int limbs, u64 *out);
+// operations per second of the register-only probe (blocks x 256 threads,
+// scratch holds one double per thread)
+double launch_int_peak(ckks_context *c, int kind, double *scratch, int blocks, int iters);
 
 }  // namespace ckks

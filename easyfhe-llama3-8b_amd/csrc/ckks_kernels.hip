@@ -255,6 +255,11 @@ struct Galois64 {
   u64 g[kMaxBatch];
 };
 
+// item 0 of a batch on the host (null when the batch is empty)
+static inline const u64 *batch_ptr_host(const Batch &b, int i) {
+  return b.base ? b.base + (u64)i * b.stride : b.p[i];
+}
+
 struct MDCombine {
   Batch acc;        // per item: [2][E][N] (component c, limb l at (c E + l) N)
   int E;
@@ -909,6 +914,8 @@ static void ntt_dispatch(ckks_context *c, const Batch &src, const Batch &dst, in
 
 void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                 int l_begin, int l_count, int q_limbs, bool inverse) {
+  KTimer kt(c, inverse ? "ntt_inv" : "ntt_fwd", 16.0 * c->N * n_items * l_count,
+            0.5 * c->N * c->logN * n_items * l_count);
   if (n_items <= 0 || l_count <= 0) return;
   switch (c->logN) {
     case 10: ntt_dispatch<5, 5, 1024>(c, src, dst, n_items, l_begin, l_count, q_limbs, inverse); break;
@@ -930,6 +937,9 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul,
                         const PostOp *post) {
+  KTimer kt(c, "ntt_fwd_moddown",
+            8.0 * c->N * limbs * (6.0 * n + (batch_ptr_host(add, 0) ? (add1_off ? 2.0 : 1.0) * n : 0.0)),
+            0.5 * c->N * c->logN * 2.0 * n * limbs);
   if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
   MDCombine md{};
   md.acc = acc;
@@ -979,6 +989,7 @@ __global__ void k_addsub_many(Batch a, Batch b, Batch out, int logN, int polys, 
 
 void launch_addsub_many(ckks_context *c, const Batch &a, const Batch &b, const Batch &out, int n,
                         int polys, int limbs, int q_limbs, int op) {
+  KTimer kt(c, "limbwise", 8.0 * c->N * 3.0 * n * polys * limbs, (double)c->N * n * polys * limbs);
   if (n < 1 || n > kMaxBatch) throw std::invalid_argument("addsub_many: 1..64 pairs per launch");
   dim3 grid(c->N / TPB, limbs, polys * n);
   hipLaunchKernelGGL(k_addsub_many, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, polys,
@@ -988,6 +999,7 @@ void launch_addsub_many(ckks_context *c, const Batch &a, const Batch &b, const B
 
 void launch_addsub(ckks_context *c, const u64 *a, const u64 *b, u64 *out, int polys,
                    int limbs, int q_limbs, int op) {
+  KTimer kt(c, "limbwise", 8.0 * c->N * 3.0 * polys * limbs, (double)c->N * polys * limbs);
   dim3 grid(c->N / TPB, limbs, polys);
   hipLaunchKernelGGL(k_addsub, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
                      q_limbs, c->L, c->d_mods, op);
@@ -1084,6 +1096,7 @@ __global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs,
 
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
                    int n_items, int limbs) {
+  KTimer kt(c, "tensor", 8.0 * c->N * 7.0 * n_items * limbs, 4.0 * c->N * n_items * limbs);
   dim3 grid(c->N / TPB, limbs, n_items);
   hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
                      c->d_mods);
@@ -1291,6 +1304,8 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
 void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered) {
+  KTimer kt(c, "basis_convert", 8.0 * c->N * n_items * (t.ns + t.nd),
+            (double)c->N * n_items * t.ns * t.nd);
   dim3 grid(c->N / TPB, n_items);
   // one register per source: a 12-source instance for digits (and P) of at
   // most 12 primes keeps the register count down
@@ -1432,6 +1447,8 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
 
 void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                             const BCTable &t, int D, const u64 *rtab) {
+  KTimer kt(c, "basis_convert_rescale", 8.0 * c->N * n_items * (t.ns + t.nd),
+            (double)c->N * n_items * t.ns * t.nd);
   if (D < 1 || D > kMaxRescaleDrop || t.nd <= D || t.ns > kMaxDigitSize)
     throw std::invalid_argument("relinearise-rescale conversion: 1 <= primes < limbs");
   dim3 grid(c->N / TPB, n_items);
@@ -1531,6 +1548,8 @@ __global__ __launch_bounds__(TPB) void k_key_inner(Batch ext, Batch acc, int n_i
 void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
                       const DeviceKey &key, int digits, int E, int q_limbs, u64 galois,
                       const Batch *own) {
+  KTimer kt(c, "key_inner", 8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
+            2.0 * c->N * E * digits * n_items);
   dim3 grid(c->N / TPB, E);
   Batch ob{};
   if (own) ob = *own;
@@ -1616,6 +1635,10 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             const std::vector<const DeviceKey *> &keys,
                             const std::vector<u64> &galois_inv, const Batch &c0,
                             const u64 *const *d_outp, int digits, int E, int q_limbs) {
+  KTimer kt(c, "key_inner_multi",
+            8.0 * c->N * E * ((double)n_items * digits + 2.0 * digits * keys.size() +
+                              2.0 * n_items * keys.size()),
+            2.0 * c->N * E * digits * (double)keys.size() * n_items);
   if (n_items < 1 || n_items > kMultiItems) throw std::invalid_argument("key_inner_multi: items");
   const int nb = (int)keys.size();
   if (nb < 1 || nb > kMaxBatch) throw std::invalid_argument("key_inner_multi: babies");
@@ -1675,6 +1698,8 @@ void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
                             int E, const u64 *pinv, const u64 *amul, const PostOp *post) {
+  KTimer kt(c, "moddown_combine", 8.0 * c->N * 2.0 * n_items * limbs * 4.0,
+            2.0 * c->N * n_items * limbs);
   if (n_items > kMaxBatch) throw std::invalid_argument("moddown combine: too many items");
   Galois64 g{};
   for (int i = 0; i < n_items; i++) g.g[i] = galois[i];
@@ -1749,6 +1774,7 @@ __global__ __launch_bounds__(TPB) void k_rescale_lift(Batch last, Batch w, int l
 
 void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
                          int limbs, int D, const u64 *tab) {
+  KTimer kt(c, "rescale", 8.0 * c->N * n_items * limbs, (double)c->N * n_items * limbs * D);
   if (D < 1 || D > kMaxRescaleDrop || D >= limbs)
     throw std::invalid_argument("rescale: 1 <= primes dropped <= 4 and below the limb count");
   dim3 grid(c->N / TPB, n_items);
@@ -1772,6 +1798,7 @@ __global__ void k_rescale_finish(Batch src, Batch w, Batch out, int logN,
 
 void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,
                            int n_items, int T, const u64 *inv) {
+  KTimer kt(c, "rescale", 8.0 * c->N * 3.0 * n_items * T, (double)c->N * n_items * T);
   dim3 grid(c->N / TPB, T, n_items);
   hipLaunchKernelGGL(k_rescale_finish, grid, dim3(TPB), 0, c->stream, src, w, out, c->logN, inv,
                      c->d_mods);
@@ -1826,6 +1853,7 @@ __global__ void k_mac(Batch babies, Batch pts, int B, u64 *__restrict__ out, int
 
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
                 int limbs_total, int q_limbs) {
+  KTimer kt(c, "mac", 8.0 * c->N * limbs_total * (3.0 * B + 2.0), 2.0 * c->N * limbs_total * B);
   dim3 grid(c->N / TPB, limbs_total, 2);
   hipLaunchKernelGGL(k_mac, grid, dim3(TPB), 0, c->stream, babies, pts, B, out, c->logN,
                      limbs_total, q_limbs, c->L, c->d_mods);
@@ -1888,6 +1916,8 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
 
 void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, int B, int G,
                      u64 *out, int E, int q_limbs) {
+  KTimer kt(c, "mac_many", 8.0 * c->N * E * (2.0 * n * B + (double)G * B + 2.0 * G * n),
+            2.0 * c->N * E * (double)n * B * G);
   if (G < 1 || G > kMacGroups || G * B > kMaxBatch)
     throw std::invalid_argument("mac_many: 1 <= groups <= 2 and groups x babies <= 64");
   dim3 grid(c->N / TPB, E, 2);
@@ -1991,6 +2021,8 @@ __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict_
 
 void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *const *pts, int B,
                       int G, u64 *out, int limbs) {
+  KTimer kt(c, "mac_table", 8.0 * c->N * limbs * (2.0 * n * B + (double)G * B + 2.0 * G * n),
+            2.0 * c->N * limbs * (double)n * B * G);
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
   dim3 grid(c->N / TPB, limbs, 2);
@@ -2086,6 +2118,7 @@ __global__ void k_lincomb(const u64 *__restrict__ table, int T, int n,
 
 void launch_lincomb(ckks_context *c, const u64 *d_table, int T, int n, const double *d_w,
                     double cst, u64 *const *d_outp, int limbs, u64 *wtab, u64 *ctab) {
+  KTimer kt(c, "lincomb", 8.0 * c->N * 2.0 * n * limbs * (T + 1.0), 2.0 * c->N * n * limbs * T);
   hipLaunchKernelGGL(k_lincomb_prep, dim3(limbs), dim3(TPB), 0, c->stream, d_w, T, rint(cst),
                      limbs, wtab, ctab, c->d_mods);
   LAUNCH_CHECK();
@@ -2687,6 +2720,60 @@ void launch_decrypt_decode(ckks_context *c, const ckks_ct *ct, double *d_re, dou
   LAUNCH_CHECK();
   c->pool.release(x, sizeof(cplx) * n);
   c->pool.release(m, sizeof(u64) * (size_t)K * N);
+}
+
+// ===========================================================================
+// integer-throughput probe: eight independent chains per thread of the
+// modular product the kernels use, in registers only (kind 0: the fp64-path
+// product of 40-bit limbs, 1: the 64-bit Shoup product, 2: a plain fp64 FMA)
+// ===========================================================================
+
+__global__ __launch_bounds__(TPB) void k_int_peak(int kind, int iters, double *out) {
+  const int t = blockIdx.x * TPB + threadIdx.x;
+  const double q = 1099511480321.0, w = 774036213477.0, wq = w / q;  // q < 2^40 prime
+  const u64 qi = 1152921504606830593ull, wi = 1015234567890123ull;    // q < 2^60
+  const u64 ws = (u64)(((unsigned __int128)wi << 64) / qi);
+  double a[8];
+  u64 b[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    a[j] = (double)(t * 8 + j + 1);
+    b[j] = (u64)(t * 8 + j + 1);
+  }
+  if (kind == 0) {
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] = fp_mulmod(a[j], w, wq, q);
+  } else if (kind == 1) {
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) b[j] = shoup_mul(b[j], wi, ws, qi);
+  } else {
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] = __fma_rn(a[j], 0.999999, 1e-3);
+  }
+  double acc = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) acc += a[j] + (double)(b[j] & 1023);
+  out[t] = acc;
+}
+
+double launch_int_peak(ckks_context *c, int kind, double *scratch, int blocks, int iters) {
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    throw std::runtime_error("int peak: event creation failed");
+  (void)hipEventRecord(e0, c->stream);
+  hipLaunchKernelGGL(k_int_peak, dim3(blocks), dim3(TPB), 0, c->stream, kind, iters, scratch);
+  (void)hipEventRecord(e1, c->stream);
+  hipError_t err = hipGetLastError();
+  float ms = 0;
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (err != hipSuccess) throw std::runtime_error(std::string("int peak: ") + hipGetErrorString(err));
+  return 8.0 * TPB * (double)blocks * iters / (ms * 1e-3);
 }
 
 }  // namespace ckks

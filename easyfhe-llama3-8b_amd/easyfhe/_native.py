@@ -117,6 +117,9 @@ SIGNATURES = {
     "ckks_rotate_many": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
     "ckks_rotate_many_noalloc": (I, [VP, VPP, I, ctypes.c_int64, VPP]),
     "ckks_mul_relin_rescale_postop_many": (I, [VP, VPP, VPP, I, I, VPP, VP, VPP]),
+    "ckks_profile_enable": (I, [VP, I]),
+    "ckks_int_peak": (I, [VP, I, ctypes.POINTER(ctypes.c_double)]),
+    "ckks_profile_read": (I, [VP, ctypes.c_char_p, ctypes.c_size_t]),
     "ckks_mul_relin_rescale_many": (I, [VP, VPP, VPP, I, VPP]),
     "ckks_mul_relin_rescale_many_by": (I, [VP, VPP, VPP, I, I, VPP]),
     "ckks_hoisted_rotate": (I, [VP, VP, I64P, I, VPP]),

@@ -185,6 +185,22 @@ class NativeContext:
     def empty_cache(self) -> None:
         check(lib.ckks_empty_cache(self._h))
 
+    def profile(self, enable: bool = True) -> None:
+        """Start (or stop) recording device time per kernel group."""
+        check(lib.ckks_profile_enable(self._h, int(bool(enable))))
+
+    def profile_read(self) -> dict[str, dict[str, float]]:
+        """Kernel groups recorded since the last read: launches, device
+        milliseconds, algorithmic bytes and modular operations."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        check(lib.ckks_profile_read(self._h, buf, len(buf)))
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, calls, ms, nbytes, ops = line.split()
+            out[name] = {"launches": int(calls), "ms": float(ms), "bytes": float(nbytes),
+                         "ops": float(ops)}
+        return out
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             clear_plaintext_cache(self)

@@ -315,6 +315,26 @@ int ckks_poly_moddown(ckks_context *ctx, const uint64_t *acc, int limbs, uint64_
  * resident ciphertexts: the kernel pair that bench.py times. */
 int ckks_ntt_many(ckks_context *ctx, ckks_ct *const *cts, int n, int inverse);
 
+/* No counterpart in the reference: the register-only throughput probe that
+ * the measurements divide kernel operation rates by.  kind 0: the fp64-path
+ * modular product of limbs below 2^45 (the basis conversions' and MACs'
+ * inner operation), 1: the 64-bit Shoup modular product, 2: fp64 FMA;
+ * *ops_per_second receives the device-wide rate. */
+int ckks_int_peak(ckks_context *ctx, int kind, double *ops_per_second);
+
+/* Per-kernel timing, the kernel-level counterpart of the reference's device-
+ * event stage timing (operators/linear/operator.py:272-291): with enable 1
+ * the library records HIP events on the context stream around each launch of
+ * its key kernels (NTT passes, basis conversions, key inner products, MACs,
+ * tensor, rescale, limb-wise sums); ckks_profile_read synchronises the
+ * stream and writes one line per kernel group recorded since the last read,
+ *   "<name> <launches> <milliseconds> <algorithmic bytes> <modular ops>\n",
+ * into buf (NUL-terminated, truncated to len), then clears the records.
+ * Algorithmic bytes count each input word read once and each output word
+ * written once. */
+int ckks_profile_enable(ckks_context *ctx, int enable);
+int ckks_profile_read(ckks_context *ctx, char *buf, size_t len);
+
 /* Device events on the context stream (reference easyfhe.cuda.Event,
  * operators/linear/operator.py:273-291). */
 int ckks_event_create(ckks_context *ctx, ckks_event **out);

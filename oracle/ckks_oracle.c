@@ -31,9 +31,62 @@ typedef uint64_t u64;
 /* modular arithmetic                                                        */
 /* ------------------------------------------------------------------------ */
 
-uint64_t orc_mulmod(uint64_t a, uint64_t b, uint64_t q) {
-  return (u64)(((u128)a * b) % q);
+/* Reduction of a 128-bit value modulo a 64-bit prime.  The plain build uses
+ * `%` (obviously correct; the pinned checker).  ORC_FAST builds, made for
+ * timing the CPU baseline, reduce the two 64-bit halves with Shoup's
+ * precomputed-quotient product, x = hi 2^64 + lo == hi (2^64 mod q) + lo,
+ * with the per-prime constants in a table filled at context creation; the
+ * two builds give the same words (tests/test_oracle_pins.py compares them). */
+#ifdef ORC_FAST
+typedef struct {
+  u64 q, r64, r64s, one_s;
+} fastmod_t;
+/* Open-addressing table of every context's primes; written only while a
+ * context is created (orc_ctx_create), read by the computing threads. */
+#define FM_SLOTS 1024
+static fastmod_t fm_table[FM_SLOTS];
+
+static inline unsigned fm_slot(u64 q) {
+  return (unsigned)(((q >> 17) * 0x9E3779B97F4A7C15ull) >> 54);
 }
+
+static void fm_register(u64 q) {
+  unsigned i = fm_slot(q);
+  for (int n = 0; n < FM_SLOTS; n++, i = (i + 1) & (FM_SLOTS - 1)) {
+    if (fm_table[i].q == q) return;
+    if (fm_table[i].q == 0) {
+      fm_table[i].r64 = (u64)((((u128)1) << 64) % q);
+      fm_table[i].r64s = (u64)(((u128)fm_table[i].r64 << 64) / q);
+      fm_table[i].one_s = (u64)((((u128)1) << 64) / q);
+      fm_table[i].q = q;
+      return;
+    }
+  }
+}
+
+static inline u64 fm_shoup(u64 a, u64 w, u64 ws, u64 q) {
+  u64 hi = (u64)(((u128)a * ws) >> 64);
+  u64 r = a * w - hi * q;
+  return r >= q ? r - q : r;
+}
+
+static inline u64 mod128(u128 x, u64 q) {
+  unsigned i = fm_slot(q);
+  while (fm_table[i].q != q) {
+    if (fm_table[i].q == 0) return (u64)(x % q); /* not a registered prime */
+    i = (i + 1) & (FM_SLOTS - 1);
+  }
+  const fastmod_t *m = &fm_table[i];
+  const u64 h = fm_shoup((u64)(x >> 64), m->r64, m->r64s, q);
+  const u64 l = fm_shoup((u64)x, 1, m->one_s, q);
+  const u64 s = h + l;
+  return s >= q ? s - q : s;
+}
+#else
+static inline u64 mod128(u128 x, u64 q) { return (u64)(x % q); }
+#endif
+
+uint64_t orc_mulmod(uint64_t a, uint64_t b, uint64_t q) { return mod128((u128)a * b, q); }
 
 static inline u64 addmod(u64 a, u64 b, u64 q) {
   u64 s = a + b;
@@ -220,7 +273,7 @@ static void sample_uniform(u64 seed, uint32_t dom, uint32_t id, uint32_t sub,
     for (int r = 0; r < 4; r++) {
       u64 lo = (u64)blk[4 * r] | ((u64)blk[4 * r + 1] << 32);
       u64 hi = (u64)blk[4 * r + 2] | ((u64)blk[4 * r + 3] << 32);
-      out[k + r] = (u64)((((u128)hi << 64) | lo) % q);
+      out[k + r] = mod128(((u128)hi << 64) | lo, q);
     }
   }
 }
@@ -355,6 +408,9 @@ orc_ctx *orc_ctx_create(int logN, int L, int alpha, int dnum, int first_bits,
   if (orc_gen_primes(logN, special_bits, alpha, c->primes, L, c->primes + L) !=
       alpha)
     goto fail;
+#ifdef ORC_FAST
+  for (int p = 0; p < K; p++) fm_register(c->primes[p]);
+#endif
   c->psi = (u64 **)calloc(K, sizeof(u64 *));
   c->psi_sh = (u64 **)calloc(K, sizeof(u64 *));
   c->ipsi = (u64 **)calloc(K, sizeof(u64 *));
@@ -429,6 +485,64 @@ void orc_ctx_free(orc_ctx *c) {
 /* NTT: a_hat[i] = sum_k a_k psi^((2 br(i) + 1) k)  (bit-reversed output)     */
 /* ------------------------------------------------------------------------ */
 
+#ifdef ORC_FAST
+/* Timed build: Harvey's lazy butterflies (values kept in [0, 4q), Shoup
+ * products left in [0, 2q)), canonical words at the end, so the outputs are
+ * those of the plain transforms below (D. Harvey, "Faster arithmetic for
+ * number-theoretic transforms", J. Symb. Comput. 60, 2014). */
+static inline u64 shoup_lazy(u64 a, u64 w, u64 ws, u64 q) {
+  u64 hi = (u64)(((u128)a * ws) >> 64);
+  return a * w - hi * q;
+}
+
+void orc_ntt_fwd(const orc_ctx *c, int p, uint64_t *a) {
+  const u64 q = c->primes[p], q2 = 2 * q;
+  const u64 *W = c->psi[p], *Ws = c->psi_sh[p];
+  const int N = c->N;
+  int t = N;
+  for (int m = 1; m < N; m <<= 1) {
+    t >>= 1;
+    for (int i = 0; i < m; i++) {
+      const u64 w = W[m + i], ws = Ws[m + i];
+      const int j1 = 2 * i * t;
+      for (int j = j1; j < j1 + t; j++) {
+        u64 u = a[j];
+        u = u >= q2 ? u - q2 : u;
+        const u64 v = shoup_lazy(a[j + t], w, ws, q);
+        a[j] = u + v;
+        a[j + t] = u - v + q2;
+      }
+    }
+  }
+  for (int j = 0; j < N; j++) {
+    u64 x = a[j];
+    x = x >= q2 ? x - q2 : x;
+    a[j] = x >= q ? x - q : x;
+  }
+}
+
+void orc_ntt_inv(const orc_ctx *c, int p, uint64_t *a) {
+  const u64 q = c->primes[p], q2 = 2 * q;
+  const u64 *W = c->ipsi[p], *Ws = c->ipsi_sh[p];
+  const int N = c->N;
+  int t = 1;
+  for (int m = N >> 1; m >= 1; m >>= 1) {
+    for (int i = 0; i < m; i++) {
+      const u64 w = W[m + i], ws = Ws[m + i];
+      const int j1 = 2 * i * t;
+      for (int j = j1; j < j1 + t; j++) {
+        const u64 x = a[j], y = a[j + t];
+        const u64 s = x + y;
+        a[j] = s >= q2 ? s - q2 : s;
+        a[j + t] = shoup_lazy(x - y + q2, w, ws, q);
+      }
+    }
+    t <<= 1;
+  }
+  const u64 ni = c->ninv[p], nis = shoup_pre(ni, q);
+  for (int j = 0; j < N; j++) a[j] = shoup_mul(a[j], ni, nis, q);
+}
+#else
 void orc_ntt_fwd(const orc_ctx *c, int p, uint64_t *a) {
   const u64 q = c->primes[p];
   const u64 *W = c->psi[p], *Ws = c->psi_sh[p];
@@ -469,6 +583,7 @@ void orc_ntt_inv(const orc_ctx *c, int p, uint64_t *a) {
   const u64 ni = c->ninv[p];
   for (int j = 0; j < N; j++) a[j] = orc_mulmod(a[j], ni, q);
 }
+#endif
 
 void orc_ntt_fwd_limbs(const orc_ctx *c, uint64_t *a, int limbs, int q_limbs) {
 #pragma omp parallel for
@@ -491,7 +606,7 @@ void orc_automorphism_coeff(const orc_ctx *c, int p, uint64_t g,
   const u64 q = c->primes[p];
   const u64 N = (u64)c->N, M = 2 * N;
   for (u64 k = 0; k < N; k++) {
-    u64 e = (u64)(((u128)k * g) % M);
+    u64 e = (u64)((u128)k * g) & (M - 1); /* M = 2N, a power of two */
     if (e < N)
       out[e] = in[k];
     else
@@ -506,7 +621,7 @@ void orc_automorphism_ntt(const orc_ctx *c, uint64_t g, const uint64_t *in,
   const u64 M = 2 * (u64)N;
   uint32_t *idx = (uint32_t *)malloc(sizeof(uint32_t) * N);
   for (int i = 0; i < N; i++) {
-    u64 e = (u64)(((u128)(2 * (u64)bitrev((uint32_t)i, logN) + 1) * g) % M);
+    u64 e = (u64)((u128)(2 * (u64)bitrev((uint32_t)i, logN) + 1) * g) & (M - 1);
     idx[i] = bitrev((uint32_t)((e - 1) >> 1), logN);
   }
   for (int l = 0; l < limbs; l++) {
@@ -1023,9 +1138,9 @@ static void basis_convert(const orc_ctx *c, const u64 *const *x, const int *src,
         u128 acc = 0;
         for (int i = 0; i < ns; i++) {
           acc += (u128)v[i] * hmod[i * nd + t];
-          if ((i & 15) == 15) acc %= qt;
+          if ((i & 15) == 15) acc = mod128(acc, qt);
         }
-        y[t][k] = submod((u64)(acc % qt), orc_mulmod(cnt, qmod[t], qt), qt);
+        y[t][k] = submod(mod128(acc, qt), orc_mulmod(cnt, qmod[t], qt), qt);
       }
     }
   }
@@ -1123,8 +1238,8 @@ static void key_inner(const orc_ctx *c, const orc_key *k, const u64 *ext,
         s0 += (u128)x * k->data[((size_t)(j * 2 + 0) * K + p) * N + i];
         s1 += (u128)x * k->data[((size_t)(j * 2 + 1) * K + p) * N + i];
       }
-      acc0[(size_t)l * N + i] = (u64)(s0 % q);
-      acc1[(size_t)l * N + i] = (u64)(s1 % q);
+      acc0[(size_t)l * N + i] = mod128(s0, q);
+      acc1[(size_t)l * N + i] = mod128(s1, q);
     }
   }
 }
@@ -1226,7 +1341,7 @@ void orc_rescale(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,
       u64 *r = (u64 *)malloc(sizeof(u64) * N);
       for (int k = 0; k < N; k++) {
         u64 v = last[k];
-        r[k] = v > (ql - 1) / 2 ? submod(v % q, qlm, q) : v % q;
+        r[k] = v > (ql - 1) / 2 ? submod(mod128(v, q), qlm, q) : mod128(v, q);
       }
       orc_ntt_fwd(c, i, r);
       const u64 *src = ct + ((size_t)d * limbs + i) * N;
@@ -1254,7 +1369,7 @@ void orc_mod_raise(const orc_ctx *c, const uint64_t *ct, int polys, int target,
       u64 *dst = out + ((size_t)d * target + i) * N;
       for (int k = 0; k < N; k++) {
         u64 v = coef[k];
-        dst[k] = v > (q0 - 1) / 2 ? submod(v % q, q0 % q, q) : v % q;
+        dst[k] = v > (q0 - 1) / 2 ? submod(mod128(v, q), q0 % q, q) : mod128(v, q);
       }
       orc_ntt_fwd(c, i, dst);
     }
@@ -1302,9 +1417,9 @@ int orc_hoisted_mac_sum(const orc_ctx *c, const uint64_t *ct, int limbs,
           for (int b = 0; b < B; b++) {
             s += (u128)babies[(size_t)b * 2 * P + ((size_t)d * limbs + p) * N + i] *
                  pts[((size_t)(g * B + b) * limbs + p) * N + i];
-            if ((b & 15) == 15) s %= q;
+            if ((b & 15) == 15) s = mod128(s, q);
           }
-          dst[i] = (u64)(s % q);
+          dst[i] = mod128(s, q);
         }
       }
     }
@@ -1380,9 +1495,9 @@ int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
           for (int b = 0; b < B; b++) {
             s += (u128)bab[(size_t)b * 2 * EP + (size_t)d * EP + (size_t)l * N + i] *
                  pts[((size_t)(g * B + b) * E + l) * N + i];
-            if ((b & 15) == 15) s %= q;
+            if ((b & 15) == 15) s = mod128(s, q);
           }
-          dst[i] = (u64)(s % q);
+          dst[i] = mod128(s, q);
         }
       }
     }

@@ -516,3 +516,44 @@ def test_bsgs_matvec_ext_schedule_decrypts_to_wx():
                                  ctx.galois_elt(B * lanes), G)
     assert not np.array_equal(acc, normal)
 
+
+
+@pytest.mark.parametrize("special,first", [(60, 60), (44, 40)])
+def test_fast_build_gives_the_same_words(special, first):
+    """The ORC_FAST build (Shoup reductions of 128-bit sums, the build the CPU
+    baseline times) equals the pinned `%` build word for word: encryption,
+    rotation, relinearisation, rescale, ModUp / ModDown and the BSGS MAC, on
+    60-bit and on 40/44-bit primes at N = 2^12."""
+    fast = O.load(O.fast_library_path())
+    kw = dict(log_n=12, limbs=6, alpha=2, dnum=3, first_bits=first, dcrt_bits=40,
+              special_bits=special, seed=3)
+    a, b = O.OracleContext(**kw), O.OracleContext(**kw, library=fast)
+    assert np.array_equal(a.primes, b.primes)
+    g = a.galois_elt(5)
+    for ctx in (a, b):
+        ctx.gen_rotation_key(g)
+        ctx.gen_relin_key()
+    rng = np.random.default_rng(special)
+    z = rng.uniform(-1, 1, 2048) + 1j * rng.uniform(-1, 1, 2048)
+    ca = a.encrypt(z, slots=2048, scale=2.0**40, limbs=6, enc_id=7)
+    cb = b.encrypt(z, slots=2048, scale=2.0**40, limbs=6, enc_id=7)
+    assert np.array_equal(ca, cb)
+    # the timed build's lazy (Harvey) butterflies end on the same words,
+    # including the edge values 0 and q - 1
+    for pi in (0, 3, 7):
+        q = int(a.primes[pi])
+        poly = rng.integers(0, q, 4096, dtype=np.uint64)
+        poly[:3] = [0, q - 1, 1]
+        assert np.array_equal(a.ntt(poly, pi), b.ntt(poly, pi))
+        assert np.array_equal(a.intt(poly, pi), b.intt(poly, pi))
+    assert np.array_equal(a.rotate_g(ca, g), b.rotate_g(cb, g))
+    assert np.array_equal(a.relinearize(a.tensor(ca, ca)), b.relinearize(b.tensor(cb, cb)))
+    assert np.array_equal(a.rescale(ca), b.rescale(cb))
+    ext = a.modup(ca[1])
+    assert np.array_equal(ext, b.modup(cb[1]))
+    acc = ext[0]
+    assert np.array_equal(a.moddown(acc), b.moddown(acc))
+    pts = [a.encode(rng.uniform(-1, 1, 2048), slots=2048, scale=2.0**40, limbs=6)
+           for _ in range(4)]
+    assert np.array_equal(a.hoisted_mac_sum(ca, [1, g], pts, g, 2),
+                          b.hoisted_mac_sum(cb, [1, g], pts, g, 2))
