@@ -31,6 +31,10 @@ FLAGS = [
     "-Wno-unused-function",
 ]
 SOURCES = ["ckks_kernels.hip", "ckks_api.hip"]
+# per-source flags: the int8 matrix-core conversion keeps its accumulators in
+# ordinary VGPRs (the AGPR form moves every accumulator through v_accvgpr
+# reads and writes, which the VALU pays for)
+EXTRA = {"ckks_kernels.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def build(verbose: bool = False) -> Path:
@@ -39,7 +43,7 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(name: str) -> Path:
         obj = BUILD / (Path(name).stem + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", str(SRC / name), "-o", str(obj)]
+        cmd = [HIPCC, *FLAGS, *EXTRA.get(name, []), "-c", str(SRC / name), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)

@@ -308,6 +308,36 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
     HIPCHECK(hipMalloc(&t.fd, t.fbytes));
     HIPCHECK(hipMemcpy(t.fd, f.data(), t.fbytes, hipMemcpyHostToDevice));
   }
+  // the MFMA B operand: for source quad i, target group tg, digit b, lane
+  // l = col + 16 g (source s = 4 i + g, target t = 16 tg + col), byte a of
+  // the lane's word is the balanced digit b of M'[(s, a)][t]; the balanced
+  // digits of x < 2^63 are the bytes of x + 0x80..80, each xor 0x80 (as int8:
+  // byte - 128, and sum (byte_b - 128) 256^b = x)
+  t.n_k = (ns + 3) / 4;
+  t.n_tg = (nd + 15) / 16;
+  for (int t2 = 0; t2 < nd; t2++)
+    if (dst[t2] >= (1ull << 45)) t.wide_mask |= 1 << (t2 / 16);
+  std::vector<u64> m((size_t)t.n_k * t.n_tg * 8 * 64, 0);
+  for (int s = 0; s < ns; s++) {
+    for (int t2 = 0; t2 < nd; t2++) {
+      const u64 qt = dst[t2];
+      u64 hm = 1;
+      for (int j = 0; j < ns; j++)
+        if (j != s) hm = mulmod_h(hm, src[j] % qt, qt);
+      const int lane = (t2 % 16) + 16 * (s % 4);
+      for (int a = 0; a < 8; a++) {
+        const u64 mp = mulmod_h(hm, (1ull << (8 * a)) % qt, qt);
+        const u64 mb = mp + 0x8080808080808080ull;
+        for (int b = 0; b < 8; b++) {
+          const u64 digit = ((mb >> (8 * b)) & 0xff) ^ 0x80;
+          m[(((size_t)(s / 4) * t.n_tg + t2 / 16) * 8 + b) * 64 + lane] |= digit << (8 * a);
+        }
+      }
+    }
+  }
+  t.mbytes = sizeof(u64) * m.size();
+  HIPCHECK(hipMalloc(&t.mf, t.mbytes));
+  HIPCHECK(hipMemcpy(t.mf, m.data(), t.mbytes, hipMemcpyHostToDevice));
   return t;
 }
 
@@ -724,10 +754,12 @@ static void free_context(ckks_context *c) {
   for (auto &kv : c->bc_up) {
     (void)hipFree(kv.second.d);
     if (kv.second.fd) (void)hipFree(kv.second.fd);
+    if (kv.second.mf) (void)hipFree(kv.second.mf);
   }
   for (auto &kv : c->bc_down) {
     (void)hipFree(kv.second.d);
     if (kv.second.fd) (void)hipFree(kv.second.fd);
+    if (kv.second.mf) (void)hipFree(kv.second.mf);
   }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
   for (auto &kv : c->relin_rs) (void)hipFree(kv.second);
@@ -1286,6 +1318,10 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
   c->stream = nullptr;
   try {
     build_context(c, *params);
+    // basis conversions run on the int8 matrix cores unless
+    // CKKS_BASIS_CONVERT=valu selects the fp64/integer VALU kernels (same words)
+    const char *bc = getenv("CKKS_BASIS_CONVERT");
+    c->bc_mfma = !(bc && strcmp(bc, "valu") == 0);
     HIPCHECK(hipGetDevice(&c->device));
     c->noalloc_scratch = device_scratch(c->device);
   } catch (...) {

@@ -186,6 +186,14 @@ struct BCTable {  // fast basis conversion constants, device resident
   double *fd;
   size_t fbytes;
   int wide0;
+  // int8-MFMA conversion (k_basis_convert_mfma): the balanced base-256
+  // digits of M'[(s, a)][t] = [2^(8a) hmod_s]_t laid out as the MFMA B
+  // operand, [n_k][n_tg][8][64] words (n_k = ceil(ns / 4) source quads,
+  // n_tg = ceil(nd / 16) target groups); bit g of wide_mask: group g holds a
+  // target of 2^45 or more (its digits 6 and 7 are not zero)
+  u64 *mf = nullptr;
+  size_t mbytes = 0;
+  int n_k = 0, n_tg = 0, wide_mask = 0;
 };
 
 struct FFTTable {  // encoder tables for one slot count n
@@ -248,6 +256,10 @@ struct ckks_context {
   int device = 0;                  // HIP device current at creation
   u64 *noalloc_scratch = nullptr;  // that device's fixed scratch (ckks_rotate_many_noalloc)
   bool rotation_tables = false;    // every level's key-switch constants built
+  // basis conversions on the int8 matrix cores (k_basis_convert_mfma, the
+  // default) or the VALU kernels (environment CKKS_BASIS_CONVERT=valu when
+  // the context is created); both give the same words
+  bool bc_mfma = true;
 };
 
 struct ckks_ct {

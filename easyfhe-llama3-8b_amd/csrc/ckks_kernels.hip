@@ -1301,11 +1301,167 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
   }
 }
 
+// int8-MFMA variant (the tensor-core formulation of fast basis conversion:
+// residues split into bytes, exact int32 sums on the matrix cores, one
+// modular reduction per output).  For coefficients k:
+//   A[k][(s, a)] = digit a of v_s(k)   (8 balanced base-256 digits)
+//   B[(s, a)][(t, b)] = digit b of M'[(s, a)][t] = [2^(8a) hmod_s]_t
+//   C_b[k][t] = sum_(s, a) A B,  |C_b| <= 8 ns 2^14 < 2^21
+// so that sum_b C_b 256^b = sum_(s, a) d_a(v_s) 2^(8a) hmod_s = sum_s v_s
+// hmod_s (mod t), the exact integer sum of the VALU kernels: the words are
+// the same.  One 16x16x32 MFMA covers a quad of sources (lane group g = lane
+// / 16 holds source 4 i + g of coefficient lane % 16) for one target group of
+// 16 and one digit b; it computes C^T (table operand first), so lane l holds
+// targets 16 tg + 4 (l / 16) .. + 3 of coefficient lane % 16 and a store
+// writes 16 consecutive coefficients of each of 4 targets.
+// Centered (ModDown) v_s are taken in (-q_s/2, q_s/2] as signed values.
+// grid (N / (64 R chunks), items): a block stages the table in LDS once and
+// converts `chunks` chunks of 4 waves x R x 16 coefficients, loading the next
+// chunk's residues while it converts the current one.
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaRows = 2;    // 16-coefficient column tiles per wave and chunk
+constexpr int kMfmaChunks = 4;  // chunks of 4 waves x R tiles per block
+
+template <int R, int NK, int CH>
+__global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
+    Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
+    const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
+    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods) {
+  // the block's table, staged once: [NK][n_tg][8][64] words
+  extern __shared__ u64 tb[];
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
+  const u64 *in = batch_ptr(src, blockIdx.y);
+  u64 *out = batch_ptr(dst, blockIdx.y);
+  const int kblk = blockIdx.x * CH * 64 * R;
+  // per source quad i: source s = 4 i + g, its prime and Shoup constants
+  u64 sq[NK], sw[NK], sws[NK];
+#pragma unroll
+  for (int i = 0; i < NK; i++) {
+    const int s = 4 * i + g;
+    const bool live = s < ns;
+    sq[i] = live ? mods[src_prime0 + s].q : 1;
+    sw[i] = live ? tab[s] : 0;
+    sws[i] = live ? tab[ns + s] : 0;
+  }
+  // raw residues of the chunk being loaded (coefficient k + 16 r + col)
+  u64 x[R][NK];
+  auto load = [&](int ch) {
+    const int k0 = kblk + ch * 64 * R + wave * 16 * R;
+#pragma unroll
+    for (int i = 0; i < NK; i++)
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        x[r][i] = 4 * i + g < ns ? in[((size_t)(4 * i + g) << logN) + k0 + 16 * r + col] : 0;
+  };
+  load(0);
+  const int words = NK * n_tg * 512;
+  for (int idx = threadIdx.x; idx < words; idx += TPB) tb[idx] = mtab[idx];
+  __syncthreads();
+  const int quad = n_tg * 512;
+  for (int ch = 0; ch < CH; ch++) {
+    const int k0 = kblk + ch * 64 * R + wave * 16 * R;
+    // the data operand: digits of v_s at coefficient k0 + 16 r + col
+    long a[R][NK];
+#pragma unroll
+    for (int i = 0; i < NK; i++)
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        u64 v = shoup_mul(x[r][i], sw[i], sws[i], sq[i]);
+        if (centered && v > (sq[i] - 1) / 2) v -= sq[i];  // two's complement of v - q
+        a[r][i] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
+      }
+    if (ch + 1 < CH) load(ch + 1);  // in flight during this chunk
+    for (int tg = 0; tg < n_tg; tg++) {
+      const bool wide = (wide_mask >> tg) & 1;
+      const u64 *mt = tb + tg * 512 + lane;
+      // C_b (rows: targets 16 tg + 4 g + e, columns: coefficients) and
+      // sum_b C_b 256^b = lo + hi 2^32 with lo = sum_(b<4) C_b 256^b, hi =
+      // sum_(b>=4) C_b 256^(b-4).  Digits go in pairs (b, b + 1): two
+      // independent MFMA chains per tile, then D = C_b + 256 C_(b+1) in
+      // int32 (|D| < 2^29.1), folded into lo / hi as exact fp64 sums (|lo|,
+      // |hi| < 2^45.01); only one pair's accumulators are live at a time
+      double lo[R][4], hi[R][4];
+#pragma unroll
+      for (int pr = 0; pr < 4; pr++) {
+        if (pr >= 3 && !wide) continue;  // digits 6, 7 of a narrow table are 0
+        v4i c0[R], c1[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) c0[r] = c1[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+          const long b0 = (long)mt[i * quad + (2 * pr) * 64];
+          const long b1 = (long)mt[i * quad + (2 * pr + 1) * 64];
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            c0[r] = __builtin_amdgcn_mfma_i32_16x16x32_i8(b0, a[r][i], c0[r], 0, 0, 0);
+            c1[r] = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, a[r][i], c1[r], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const double d = (double)(c0[r][e] + 256 * c1[r][e]);
+            if (pr == 0) lo[r][e] = d;
+            else if (pr == 1) lo[r][e] = __fma_rn(d, 65536.0, lo[r][e]);
+            else if (pr == 2) hi[r][e] = d;
+            else hi[r][e] = __fma_rn(d, 65536.0, hi[r][e]);
+          }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = 16 * tg + 4 * g + e;
+        if (t >= nd) continue;
+        const int tl = t < t_split ? t : t + t_skip;
+        const ModQ M = mods[prime_of(tl, q_limbs, L)];
+        u64 *o = out + ((size_t)tl << logN) + k0 + col;
+        if (M.q < kFpPrimeBound) {
+          // y = hi 2^32 + lo: hi 2^32 is an exact double, the quotient by
+          // round(hi 2^32 / q) leaves an exact residue, one reduction after
+          const double q = (double)M.q, qinv = 1.0 / q, w32q = 4294967296.0 * qinv;
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const double tq = fp_rint(__dmul_rn(hi[r][e], w32q));
+            const double y =
+                __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e], 4294967296.0)), lo[r][e]);
+            o[16 * r] = fp_canon(y, qinv, q);
+          }
+        } else {
+          // q > 2^45 > |hi|, |lo|: one correction each, then the 64-bit product
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const long long hv = (long long)hi[r][e], lv = (long long)lo[r][e];
+            const u64 h = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
+            const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
+            o[16 * r] = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
+          }
+        }
+      }
+    }
+  }
+}
+
 void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered) {
   KTimer kt(c, "basis_convert", 8.0 * c->N * n_items * (t.ns + t.nd),
             (double)c->N * n_items * t.ns * t.nd);
+  // the table is staged in LDS: tables above 64 KiB (digits of more than
+  // 12 primes into more than 48 targets) take the VALU kernels
+  if (c->bc_mfma && t.mf && (size_t)t.n_k * t.n_tg * 512 * sizeof(u64) <= 65536) {
+    auto kern = t.n_k == 1   ? k_basis_convert_mfma<kMfmaRows, 1, kMfmaChunks>
+                : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks>
+                : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks>
+                             : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks>;
+    const size_t lds = sizeof(u64) * (size_t)t.n_k * t.n_tg * 512;
+    hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
+                       lds, c->stream,
+                       src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg, t.wide_mask,
+                       src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0, c->d_mods);
+    LAUNCH_CHECK();
+    return;
+  }
   dim3 grid(c->N / TPB, n_items);
   // one register per source: a 12-source instance for digits (and P) of at
   // most 12 primes keeps the register count down
