@@ -605,7 +605,8 @@ static void build_context(ckks_context *c, const ckks_params &p) {
   c->prime_fp.assign(K, 0);
   for (int pi = 0; pi < K; pi++) c->prime_fp[pi] = c->primes[pi] < ((u64)1 << 45) ? 1 : 0;
   {
-    std::vector<double> tw(2 * (size_t)K * N, 0.0), itw(2 * (size_t)K * N, 0.0), nv(2 * (size_t)K, 0.0);
+    std::vector<double> tw(2 * (size_t)K * N, 0.0), itw(2 * (size_t)K * N, 0.0), nv(2 * (size_t)K, 0.0),
+        rv(2 * (size_t)K, 0.0);
     for (int pi = 0; pi < K; pi++) {
       if (!c->prime_fp[pi]) continue;
       const double q = (double)c->primes[pi];
@@ -618,6 +619,10 @@ static void build_context(ckks_context *c, const ckks_params &p) {
       }
       nv[2 * pi] = (double)ninv[2 * pi];
       nv[2 * pi + 1] = (double)ninv[2 * pi] / q;
+      // 2^-64 mod q: the Montgomery factor of the key words
+      const u64 r = invmod_h((u64)(((u128)1 << 64) % c->primes[pi]), c->primes[pi]);
+      rv[2 * pi] = (double)r;
+      rv[2 * pi + 1] = (double)r / q;
     }
     if (N == 65536) {
       // The low NTT passes read the twiddles of bit positions 2..0 of a row
@@ -652,6 +657,7 @@ static void build_context(ckks_context *c, const ckks_params &p) {
     upd(&c->d_tw_fp, tw);
     upd(&c->d_itw_fp, itw);
     upd(&c->d_ninv_fp, nv);
+    upd(&c->d_rinv_fp, rv);
   }
   up(&c->d_psi, psi);
   up(&c->d_psi_sh, psi_sh);
@@ -783,6 +789,7 @@ static void free_context(ckks_context *c) {
   (void)hipFree(c->d_tw_fp);
   (void)hipFree(c->d_itw_fp);
   (void)hipFree(c->d_ninv_fp);
+  (void)hipFree(c->d_rinv_fp);
   c->pool.trim();
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -943,8 +950,10 @@ static Batch strided(u64 *base, size_t stride) {
 // ext = [n][digits][E][N].
 // own_copy false: the digits' own limbs are not copied into ext; the key
 // inner product then reads them from d (ks_inner's `own`).
+// high_only (N = 2^16, own_copy false): the converted limbs get only the
+// high pass of the forward NTT; launch_ntt_low_key runs the low pass.
 static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
-                     Scratch &s, bool own_copy = true) {
+                     Scratch &s, bool own_copy = true, bool high_only = false) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   u64 *coeff = s.get((size_t)n * limbs * N);
@@ -960,8 +969,13 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
     if (own_copy) launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
     launch_basis_convert(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N), strided(ej, est), n,
                          bc_up(c, limbs, j), lo, lo, ns, limbs, false);
-    launch_ntt(c, strided(ej, est), strided(ej, est), n, 0, lo, limbs, false);
-    launch_ntt(c, strided(ej, est), strided(ej, est), n, hi, E - hi, limbs, false);
+    if (high_only) {
+      launch_ntt_fwd_high(c, strided(ej, est), strided(ej, est), n, 0, lo, limbs);
+      launch_ntt_fwd_high(c, strided(ej, est), strided(ej, est), n, hi, E - hi, limbs);
+    } else {
+      launch_ntt(c, strided(ej, est), strided(ej, est), n, 0, lo, limbs, false);
+      launch_ntt(c, strided(ej, est), strided(ej, est), n, hi, E - hi, limbs, false);
+    }
   }
 }
 
@@ -1060,6 +1074,36 @@ static u64 *ks_inner(ckks_context *c, int limbs, const u64 *ext, const std::vect
   return acc;
 }
 
+// g^-1 mod 2N: the units mod 2N have order N / 2, so g^-1 = g^(N - 1)
+static u64 galois_inverse(const ckks_context *c, u64 g) {
+  const u64 two_n = 2 * (u64)c->N;
+  u64 inv = 1, base = g % two_n;
+  for (u64 e = c->N - 1; e; e >>= 1, base = base * base % two_n)
+    if (e & 1) inv = inv * base % two_n;
+  return inv;
+}
+
+// ModUp of n polynomials d[i] (NTT domain) and the key inner product of
+// every job (job i takes ext item i; all share one key and Galois element)
+// into [n][2][E][N] accumulators.  At N = 2^16 the extended digits get only
+// the NTT's high pass and their low pass runs with the key product.
+static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *d,
+                           const std::vector<KsJob> &jobs, Scratch &s) {
+  const size_t N = c->N;
+  const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  const size_t est = (size_t)digits * E * N;
+  u64 *ext = s.get((size_t)n * est);
+  const bool fused = c->ks_fused && c->logN == 16 && n <= kMaxBatch;
+  ks_modup(c, limbs, n, d, ext, s, false, fused);
+  if (!fused) return ks_inner(c, limbs, ext, jobs, s, d);
+  u64 *acc = s.get((size_t)n * 2 * E * N);
+  Batch ob{};
+  for (int i = 0; i < n; i++) ob.p[i] = (u64 *)d[i];
+  launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
+                     galois_inverse(c, jobs[0].galois));
+  return acc;
+}
+
 // Key inner product for every job, ModDown, and the combine with addends.
 static void ks_finish(ckks_context *c, int limbs, const u64 *ext, int n_ext,
                       const std::vector<KsJob> &jobs, Scratch &s,
@@ -1112,14 +1156,12 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
     Scratch s = arena ? Scratch(c, arena, arena_words) : Scratch(c);
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + P;
-    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
-    u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s, false);
     const DeviceKey &key = get_key(c, g);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, g, in[b0 + i]->d, nullptr, out[b0 + i]->d, out[b0 + i]->d + P};
-    ks_finish(c, limbs, ext, nb, jobs, s, d.data());
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
+    ks_moddown(c, limbs, acc, jobs, s);
   }
 }
 
@@ -1133,14 +1175,12 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
     Scratch s(c);
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
-    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + c->alpha;
-    u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s, false);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, 1, in[b0 + i]->d, in[b0 + i]->d + P, out[b0 + i]->d,
                       out[b0 + i]->d + P};
-    ks_finish(c, limbs, ext, nb, jobs, s, d.data());
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
+    ks_moddown(c, limbs, acc, jobs, s);
   }
 }
 
@@ -1181,12 +1221,10 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     Scratch s(c);
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
-    const int digits = (limbs + c->ds - 1) / c->ds, E = limbs + A;
-    u64 *ext = s.get((size_t)nb * digits * E * N);
-    ks_modup(c, limbs, nb, d.data(), ext, s, false);
+    const int E = limbs + A;
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
-    u64 *acc = ks_inner(c, limbs, ext, jobs, s, d.data());
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
     // per item: [A] P limbs of X, then its limbs limbs-D .. limbs-1, as
     // coefficients
     const size_t xs = (size_t)(A + D) * N;
@@ -1322,6 +1360,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     // CKKS_BASIS_CONVERT=valu selects the fp64/integer VALU kernels (same words)
     const char *bc = getenv("CKKS_BASIS_CONVERT");
     c->bc_mfma = !(bc && strcmp(bc, "valu") == 0);
+    const char *kf = getenv("CKKS_KEYSWITCH_FUSED");
+    c->ks_fused = !(kf && strcmp(kf, "0") == 0);
     HIPCHECK(hipGetDevice(&c->device));
     c->noalloc_scratch = device_scratch(c->device);
   } catch (...) {
@@ -1412,12 +1452,17 @@ int ckks_has_rotation_key(const ckks_context *c, int64_t rotation) {
   return g == 1 || c->keys.count(g) ? 1 : 0;
 }
 
-__global__ void k_from_mont(u64 *d, size_t words, int K, int logN, const ModQ *mods) {
+// key words in NTT position order and out of Montgomery form: word k of each
+// row from autom_index(k, g) of the stored key (g = 1: in place)
+__global__ void k_key_export(const u64 *__restrict__ key, u64 *__restrict__ out, size_t words,
+                             int K, int logN, u64 g, const ModQ *__restrict__ mods) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= words) return;
-  const int p = (int)((i >> logN) % K);
-  const ModQ M = mods[p];
-  d[i] = redc(0, d[i], M.q, M.qinv);
+  const size_t row = i >> logN;
+  const u32 k = (u32)(i & (((size_t)1 << logN) - 1));
+  const u32 s = g <= 1 ? k : autom_index(k, g, logN);
+  const ModQ M = mods[(int)(row % K)];
+  out[i] = redc(0, key[(row << logN) + s], M.q, M.qinv);
 }
 
 int ckks_key_download(ckks_context *c, uint64_t galois, uint64_t *out, int *digits) {
@@ -1428,9 +1473,8 @@ int ckks_key_download(ckks_context *c, uint64_t galois, uint64_t *out, int *digi
   if (out) {
     const size_t words = k.bytes / sizeof(u64);
     u64 *tmp = (u64 *)c->pool.alloc(k.bytes);
-    HIPCHECK(hipMemcpyAsync(tmp, k.data, k.bytes, hipMemcpyDeviceToDevice, c->stream));
-    hipLaunchKernelGGL(k_from_mont, dim3((words + 255) / 256), dim3(256), 0, c->stream, tmp,
-                       words, c->K, c->logN, c->d_mods);
+    hipLaunchKernelGGL(k_key_export, dim3((words + 255) / 256), dim3(256), 0, c->stream, k.data,
+                       tmp, words, c->K, c->logN, k.galois, c->d_mods);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipMemcpyAsync(out, tmp, k.bytes, hipMemcpyDeviceToHost, c->stream));
     HIPCHECK(hipStreamSynchronize(c->stream));

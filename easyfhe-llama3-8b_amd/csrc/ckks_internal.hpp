@@ -171,7 +171,9 @@ using Pool = BasicPool<HipDevice>;
 struct DeviceKey {
   u64 galois;
   int digits;
-  u64 *data;  // [digits][2][K][N], Montgomery form
+  // [digits][2][K][N], Montgomery form; a rotation key by g holds the word
+  // of NTT position k at autom_index(k, g) (source order)
+  u64 *data;
   size_t bytes;
 };
 
@@ -240,6 +242,8 @@ struct ckks_context {
   // doubles (w, w / q) of psi_br and psi_br^-1, and [K][2] (N^-1, N^-1 / q)
   std::vector<int> prime_fp;
   double *d_tw_fp = nullptr, *d_itw_fp = nullptr, *d_ninv_fp = nullptr;
+  // per prime below 2^45: 2^-64 mod q and its quotient by q (Montgomery factor)
+  double *d_rinv_fp = nullptr;
   u64 *d_secret;                               // [K][N] NTT domain
   std::map<u64, ckks::DeviceKey> keys;          // galois -> key (0 = relin)
   std::map<std::pair<int, int>, ckks::BCTable> bc_up;  // (limbs, digit)
@@ -260,6 +264,10 @@ struct ckks_context {
   // default) or the VALU kernels (environment CKKS_BASIS_CONVERT=valu when
   // the context is created); both give the same words
   bool bc_mfma = true;
+  // N = 2^16 key switches run the extended digits' low NTT pass with the key
+  // inner product fused (launch_ntt_low_key); environment
+  // CKKS_KEYSWITCH_FUSED=0 at creation selects the separate kernels
+  bool ks_fused = true;
 };
 
 struct ckks_ct {
@@ -322,6 +330,18 @@ void launch_copy_limbs(ckks_context *c, const Batch &src, const Batch &dst, int 
 void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n_items,
                       const DeviceKey &key, int digits, int E, int q_limbs, u64 galois,
                       const Batch *own = nullptr);
+// N = 2^16: the high pass of the forward NTT alone (the low pass then runs in
+// launch_ntt_low_key)
+void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                         int l_begin, int l_count, int q_limbs);
+// N = 2^16: the forward low pass of the extended digits ext (item it at
+// ext + it ext_stride, [digits][E][N], high pass done; a digit's own limbs
+// are read from own) fused with the key inner product into acc (item it at
+// acc + it acc_stride, [2][E][N]); ginv = g^-1 mod 2N (1 for
+// relinearisation).  The words of launch_ntt's low pass then launch_key_inner.
+void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
+                        u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
+                        int digits, int E, int q_limbs, u64 ginv);
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,

@@ -371,6 +371,39 @@ __device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Bat
   for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = x[j];
 }
 
+// Rounds of the forward low pass on one thread's 16 words of global row
+// `row`: A on columns c0 + 16 k (bits 7..4), B on columns 16 c0 + j (bits
+// 3..0); values in [0, 4q)
+__device__ __forceinline__ void u64_low_round_a(u64 (&x)[16], const u64 *__restrict__ W,
+                                                const u64 *__restrict__ Ws, int row, u64 q,
+                                                u64 q2) {
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 7 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1));
+      ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+}
+
+__device__ __forceinline__ void u64_low_round_b(u64 (&x)[16], const u64 *__restrict__ W,
+                                                const u64 *__restrict__ Ws, int row, int c0, u64 q,
+                                                u64 q2) {
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int b = 7 - st, half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1));
+      ct_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+}
+
 // forward, bit positions 7..0: tile = 16 contiguous rows of 256; output in [0, q)
 // (COMBINE: the ModDown epilogue instead of the store)
 template <bool COMBINE>
@@ -394,32 +427,14 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = base[rl * 256 + c0 + 16 * k];
   if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
-#pragma unroll
-  for (int st = 0; st < 4; st++) {
-    const int b = 7 - st, half = 8 >> st;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (k & half) continue;
-      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1));
-      ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
-    }
-  }
+  u64_low_round_a(x, W, Ws, row, q, q2);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
   __syncthreads();
   // round B: column = 16 c0 + j, stages on column bits 3..0
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
-#pragma unroll
-  for (int st = 4; st < 8; st++) {
-    const int b = 7 - st, half = 1 << b;
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      const int ti = (65536 >> (b + 1)) + ((row * 256 + 16 * c0 + j) >> (b + 1));
-      ct_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
-    }
-  }
+  u64_low_round_b(x, W, Ws, row, c0, q, q2);
   // store through LDS so that adjacent lanes write adjacent words
   __syncthreads();
 #pragma unroll
@@ -597,6 +612,16 @@ __device__ __forceinline__ void gs_fp(double &X, double &Y, double w, double wq,
 __device__ __forceinline__ double as_dbl(u64 v) { return __longlong_as_double((long long)v); }
 __device__ __forceinline__ u64 dbl_bits(double v) { return (u64)__double_as_longlong(v); }
 
+// exact conversions of integers in [0, 2^52): the word is the mantissa of
+// 2^52 + x
+constexpr u64 kTwo52Bits = 0x4330000000000000ull;
+__device__ __forceinline__ double u52_to_dbl(u64 x) {
+  return __dsub_rn(as_dbl(x | kTwo52Bits), 4503599627370496.0);
+}
+__device__ __forceinline__ u64 dbl_to_u52(double r) {
+  return dbl_bits(__dadd_rn(r, 4503599627370496.0)) - kTwo52Bits;
+}
+
 // Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
 __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                          int q_limbs, int L,
@@ -643,6 +668,38 @@ __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Ba
   for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = dbl_bits(x[j]);
 }
 
+// Rounds of the fp64 forward low pass (as u64_low_round_a/b); the table
+// holds bit positions 2..0 in [row][m][c0] order
+__device__ __forceinline__ void fp_low_round_a(double (&x)[16], const double2 *__restrict__ T,
+                                               int row, double q) {
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 7 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1))];
+      ct_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+}
+
+__device__ __forceinline__ void fp_low_round_b(double (&x)[16], const double2 *__restrict__ T,
+                                               int row, int c0, double q) {
+#pragma unroll
+  for (int st = 4; st < 8; st++) {
+    const int b = 7 - st, half = 1 << b;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j & half) continue;
+      // entry (row 256 + 16 c0 + j) >> (b + 1) of the stage, in the table's
+      // [row][m][c0] order for these stages
+      const double2 w = T[(65536 >> (b + 1)) + row * (128 >> b) + ((j >> (b + 1)) << 4) + c0];
+      ct_fp(x[j], x[j + half], w.x, w.y, q);
+    }
+  }
+}
+
 template <bool COMBINE>
 __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                         int L, const ModQ *__restrict__ mods,
@@ -661,33 +718,13 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = as_dbl(base[rl * 256 + c0 + 16 * k]);
   if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
-#pragma unroll
-  for (int st = 0; st < 4; st++) {
-    const int b = 7 - st, half = 8 >> st;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (k & half) continue;
-      const double2 w = T[(65536 >> (b + 1)) + ((row * 256 + 16 * k) >> (b + 1))];
-      ct_fp(x[k], x[k + half], w.x, w.y, q);
-    }
-  }
+  fp_low_round_a(x, T, row, q);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
-#pragma unroll
-  for (int st = 4; st < 8; st++) {
-    const int b = 7 - st, half = 1 << b;
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      // entry (row 256 + 16 c0 + j) >> (b + 1) of the stage, in the table's
-      // [row][m][c0] order for these stages
-      const double2 w = T[(65536 >> (b + 1)) + row * (128 >> b) + ((j >> (b + 1)) << 4) + c0];
-      ct_fp(x[j], x[j + half], w.x, w.y, q);
-    }
-  }
+  fp_low_round_b(x, T, row, c0, q);
   __syncthreads();
   u64 *smu = reinterpret_cast<u64 *>(sm);
 #pragma unroll
@@ -959,6 +996,265 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, grid, block, 0, c->stream, conv, 0, limbs, c->L,
                      c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp, md);
   LAUNCH_CHECK();
+}
+
+// Only the high pass of the forward NTT (bit positions 15..8), for limbs
+// whose low pass runs inside launch_ntt_low_key.  N = 2^16 only.
+void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                         int l_begin, int l_count, int q_limbs) {
+  KTimer kt(c, "ntt_fwd_high", 16.0 * c->N * n_items * l_count,
+            0.25 * c->N * c->logN * n_items * l_count);
+  if (n_items <= 0 || l_count <= 0) return;
+  if (c->logN != 16) throw std::invalid_argument("high pass alone: N = 2^16 only");
+  hipLaunchKernelGGL(k_ntt16m_fwd_high, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream,
+                     src, dst, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh,
+                     (const double2 *)c->d_tw_fp);
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// N = 2^16: the forward NTT's low pass of every digit's extended limb with
+// the key inner product as its epilogue, so that the ModUp output is never
+// stored in NTT form.  Block (item, tile, limb) holds the 4096 words
+// tile 4096 + [0, 4096) of limb l: for each digit j it runs the low pass on
+// what the high pass left in ext (or reads the digit's own limb, already in
+// NTT form, from the source), then accumulates
+//   acc_c[l][t] = sum_j ext_j[l][s] key_j[c][l][s],  t = autom_index(s, g^-1)
+// with the key in source order (the words of k_key_inner, which reads both
+// at s = autom_index(t, g)).  The automorphism maps each aligned group of 16
+// words onto an aligned group of 16, so the 16 lanes holding one group of s
+// (the coalesced layout s = tile 4096 + rl 256 + c0 + 16 k) write the
+// accumulator at one 128-byte group of t.
+// fp64 primes multiply by the Montgomery-form key words in fp64 and take
+// the factor 2^-64 out once at the end; the 64-bit body reduces each digit's
+// product by redc, as k_key_inner reduces their sum: the same words.
+// grid (items, 16, E): the blocks of one tile and limb run back to back and
+// read its key words from L2.
+// ===========================================================================
+
+struct LowKeyArgs {
+  const u64 *ext;     // item it, digit j, limb l: ext + it ext_stride + ((j E + l) << 16)
+  size_t ext_stride;
+  Batch own;          // per item: the source polynomial, limb l at l << 16 (NTT form)
+  u64 *acc;           // per item [2][E][N] at acc + it acc_stride
+  size_t acc_stride;
+  const u64 *key;     // [digits][2][K][N], Montgomery form, source order
+  u64 ginv;           // inverse of the Galois element mod 2N (1: none)
+  int digits, E, q_limbs, L, K, ds;
+};
+
+// 16 consecutive words from a 128-byte aligned address, as 8 loads of 16 bytes
+__device__ __forceinline__ void load16(const u64 *__restrict__ p, u64 (&v)[16]) {
+  const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(p);
+#pragma unroll
+  for (int m = 0; m < 8; m++) {
+    const ulonglong2 t = q[m];
+    v[2 * m] = t.x;
+    v[2 * m + 1] = t.y;
+  }
+}
+
+// The permuted store of one accumulator component: word(i), the thread's
+// word for position s = sb + i, goes to t = autom_index(s, g^-1), inside the
+// tile tb + [0, 4096); it passes through the LDS tile so that the store is
+// coalesced.
+template <typename F>
+__device__ __forceinline__ void low_key_store(u64 *__restrict__ sm, F word, u32 sb, u64 ginv,
+                                              u64 *__restrict__ out, u32 tb) {
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  __syncthreads();  // earlier reads of the tile are done
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const u32 t = ginv == 1 ? sb + i : autom_index(sb + i, ginv, 16);
+    sm[lds16((t >> 8) & 15, t & 255)] = word(i);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; k++) out[tb + rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
+}
+
+// Per digit: the low pass leaves each thread the 16 consecutive positions
+// s = sb + i of round B, where the key product runs; the own limb and the
+// key words are read at those positions.
+__device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKeyArgs &a, int it,
+                                           int tile, int l, int p, const ModQ *__restrict__ mods,
+                                           const double2 *__restrict__ tw,
+                                           const double2 *__restrict__ rinv) {
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const double2 *T = tw + ((size_t)p << 16);
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = tile * 16 + rl;
+  const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  const int jo = l < a.q_limbs ? l / a.ds : -1;
+  double acc0[16], acc1[16];
+  for (int j = 0; j < a.digits; j++) {
+    double y[16];
+    if (j == jo) {
+      u64 w[16];
+      load16(batch_ptr(a.own, it) + ((size_t)l << 16) + sb, w);
+#pragma unroll
+      for (int i = 0; i < 16; i++) y[i] = u52_to_dbl(w[i]);
+    } else {
+      const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
+                       (size_t)tile * 4096;
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = as_dbl(src[rl * 256 + c0 + 16 * k]);
+      fp_low_round_a(y, T, row, q);
+      __syncthreads();  // the previous digit's reads of the tile are done
+#pragma unroll
+      for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 16; i++) y[i] = sm[lds16(rl, 16 * c0 + i)];
+      fp_low_round_b(y, T, row, c0, q);
+    }
+    // |y| <= 17 q < 2^50: the products need no reduction first
+    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + sb;
+    const u64 *ka = kb + (size_t)a.K * 65536;
+#pragma unroll
+    for (int i0 = 0; i0 < 16; i0 += 4) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = i0; i < i0 + 4; i++) {
+        const double wb = u52_to_dbl(kb[i]), wa = u52_to_dbl(ka[i]);
+        const double pb = fp_mulmod(y[i], wb, __dmul_rn(wb, qinv), q);
+        const double pa = fp_mulmod(y[i], wa, __dmul_rn(wa, qinv), q);
+        acc0[i] = j == 0 ? pb : __dadd_rn(acc0[i], pb);
+        acc1[i] = j == 0 ? pa : __dadd_rn(acc1[i], pa);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // x 2^-64 (the keys' Montgomery factor), then canonical
+  const double2 ri = rinv[p];
+  auto canon = [&](double x) {
+    double r = fp_reduce(fp_mulmod(x, ri.x, ri.y, q), qinv, q);
+    r = r < 0.0 ? __dadd_rn(r, q) : r;
+    return dbl_to_u52(r);
+  };
+  u64 *o = a.acc + it * a.acc_stride + ((size_t)l << 16);
+  const u32 tb = a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u;
+  u64 *smu = reinterpret_cast<u64 *>(sm);
+  low_key_store(smu, [&](int i) { return canon(acc0[i]); }, sb, a.ginv, o, tb);
+  low_key_store(smu, [&](int i) { return canon(acc1[i]); }, sb, a.ginv, o + ((size_t)a.E << 16),
+                tb);
+}
+
+__device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArgs &a, int it,
+                                           int tile, int l, int p, const ModQ *__restrict__ mods,
+                                           const u64 *__restrict__ psi,
+                                           const u64 *__restrict__ psi_sh) {
+  const ModQ M = mods[p];
+  const u64 q = M.q, q2 = 2 * q;
+  const u64 *W = psi + ((size_t)p << 16);
+  const u64 *Ws = psi_sh + ((size_t)p << 16);
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int row = tile * 16 + rl;
+  const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  const int jo = l < a.q_limbs ? l / a.ds : -1;
+  u64 acc0[16], acc1[16];
+  for (int j = 0; j < a.digits; j++) {
+    u64 y[16];
+    if (j == jo) {
+      load16(batch_ptr(a.own, it) + ((size_t)l << 16) + sb, y);
+    } else {
+      const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
+                       (size_t)tile * 4096;
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = src[rl * 256 + c0 + 16 * k];
+      u64_low_round_a(y, W, Ws, row, q, q2);
+      __syncthreads();  // the previous digit's reads of the tile are done
+#pragma unroll
+      for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 16; i++) y[i] = sm[lds16(rl, 16 * c0 + i)];
+      u64_low_round_b(y, W, Ws, row, c0, q, q2);
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const u64 v = y[i] >= q2 ? y[i] - q2 : y[i];
+        y[i] = v >= q ? v - q : v;
+      }
+    }
+    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + sb;
+    const u64 *ka = kb + (size_t)a.K * 65536;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const u64 b = kb[i], c = ka[i];
+      const u64 pb = redc(__umul64hi(y[i], b), y[i] * b, q, M.qinv);
+      const u64 pa = redc(__umul64hi(y[i], c), y[i] * c, q, M.qinv);
+      acc0[i] = j == 0 ? pb : add_mod(acc0[i], pb, q);
+      acc1[i] = j == 0 ? pa : add_mod(acc1[i], pa, q);
+    }
+  }
+  u64 *o = a.acc + it * a.acc_stride + ((size_t)l << 16);
+  const u32 tb = a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u;
+  low_key_store(sm, [&](int i) { return acc0[i]; }, sb, a.ginv, o, tb);
+  low_key_store(sm, [&](int i) { return acc1[i]; }, sb, a.ginv, o + ((size_t)a.E << 16), tb);
+}
+
+// One kernel per body, each over a run of nl limbs of its kind starting at
+// l_begin, so that each gets its own register allocation.  1-D grid of
+// n_items x 16 x nl blocks, decoded so that the n_items blocks of one
+// (tile, limb) share b % 8, i.e. run on one XCD (blocks go to the 8 XCDs
+// round robin) and read the tile's key words into one L2.
+template <bool FP>
+__global__ __launch_bounds__(TPB, FP ? 3 : 2) void k_ntt16_low_key(LowKeyArgs a, int l_begin,
+                                                                   int n_items,
+                                                                   const ModQ *__restrict__ mods,
+                                                                   const u64 *__restrict__ psi,
+                                                                   const u64 *__restrict__ psi_sh,
+                                                                   const double2 *__restrict__ tw,
+                                                                   const double2 *__restrict__ rinv) {
+  __shared__ u64 lds[16 * 272];
+  const int b = blockIdx.x, r = b >> 3;
+  const int it = r % n_items, tl = (r / n_items) * 8 + (b & 7);
+  const int tile = tl & 15, l = l_begin + (tl >> 4);
+  const int p = prime_of(l, a.q_limbs, a.L);
+  if constexpr (FP)
+    low_key_fp(reinterpret_cast<double *>(lds), a, it, tile, l, p, mods, tw, rinv);
+  else
+    low_key_64(lds, a, it, tile, l, p, mods, psi, psi_sh);
+}
+
+void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
+                        u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
+                        int digits, int E, int q_limbs, u64 ginv) {
+  KTimer kt(c, "ntt_low_key",
+            8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
+            2.0 * c->N * E * digits * n_items);
+  if (n_items <= 0) return;
+  if (c->logN != 16) throw std::invalid_argument("fused low pass and key product: N = 2^16 only");
+  if (digits < 1 || digits > key.digits || q_limbs > c->L || E != q_limbs + c->alpha)
+    throw std::invalid_argument("fused low pass and key product: shape");
+  LowKeyArgs a{};
+  a.ext = ext;
+  a.ext_stride = ext_stride;
+  a.own = own;
+  a.acc = acc;
+  a.acc_stride = acc_stride;
+  a.key = key.data;
+  a.ginv = ginv;
+  a.digits = digits;
+  a.E = E;
+  a.q_limbs = q_limbs;
+  a.L = c->L;
+  a.K = c->K;
+  a.ds = c->ds;
+  // runs of limbs whose primes take the same body (q_0 and wide special
+  // primes the 64-bit one)
+  auto fp_limb = [&](int l) { return c->prime_fp[l < q_limbs ? l : c->L + (l - q_limbs)] != 0; };
+  for (int l0 = 0; l0 < E;) {
+    const bool fp = fp_limb(l0);
+    int l1 = l0 + 1;
+    while (l1 < E && fp_limb(l1) == fp) l1++;
+    hipLaunchKernelGGL(fp ? k_ntt16_low_key<true> : k_ntt16_low_key<false>,
+                       dim3(n_items * 16 * (l1 - l0)), dim3(TPB), 0, c->stream, a, l0, n_items,
+                       c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp,
+                       (const double2 *)c->d_rinv_fp);
+    LAUNCH_CHECK();
+    l0 = l1;
+  }
 }
 
 // ===========================================================================
@@ -1672,15 +1968,16 @@ __global__ __launch_bounds__(TPB) void k_key_inner(Batch ext, Batch acc, int n_i
   const int p = prime_of(l, q_limbs, L);
   const ModQ M = mods[p];
   const size_t N = (size_t)1 << logN;
+  const u32 kk = galois == 1 ? (u32)k : autom_index((u32)k, galois, logN);
+  // rotation keys are stored in source order: the word for output k at kk
   u64 kb[MD], ka[MD];
 #pragma unroll
   for (int j = 0; j < MD; j++) {
     if (j < digits) {
-      kb[j] = key[((size_t)(2 * j) * K + p) * N + k];
-      ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + k];
+      kb[j] = key[((size_t)(2 * j) * K + p) * N + kk];
+      ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + kk];
     }
   }
-  const u32 kk = galois == 1 ? (u32)k : autom_index((u32)k, galois, logN);
   // the digit holding limb l (its own limb: read from the source if given)
   const int jo = (has_own && l < q_limbs) ? l / ds : -1;
   for (int it = 0; it < n_items; it++) {
@@ -1760,12 +2057,13 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
   for (int b = 0; b < n_babies; b++) {
     const u32 t = autom_index((u32)s, mk.ginv[b], logN);
     const u64 *key = mk.key[b];
+    // keys in source order: the word for output t sits at s
     u64 kb[MD], ka[MD];
 #pragma unroll
     for (int j = 0; j < MD; j++) {
       if (j < digits) {
-        kb[j] = key[((size_t)(2 * j) * K + p) * N + t];
-        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + t];
+        kb[j] = key[((size_t)(2 * j) * K + p) * N + s];
+        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + s];
       }
     }
 #pragma unroll
@@ -2401,8 +2699,12 @@ __global__ void k_keygen_digit(u64 seed, u32 id, int j, const u64 *__restrict__ 
         sp = s_ntt[p * N + autom_index(k, galois, logN)];
       b = add_mod(b, mul_mod(pmod[p], sp, M), M.q);
     }
-    out_b[p * N + k] = to_mont(b, M);
-    out_a[p * N + k] = to_mont(a, M);
+    // rotation keys in source order: the word of position k at
+    // autom_index(k, g), so that a key switch reads it where it reads the
+    // extended digit it multiplies
+    const u32 so = relin ? k : autom_index(k, galois, logN);
+    out_b[p * N + so] = to_mont(b, M);
+    out_a[p * N + so] = to_mont(a, M);
   }
 }
 

@@ -2,7 +2,8 @@
 basis conversion: ModUp of every digit and the centered ModDown at several
 levels, on chains with a 60-bit q_0 among 40-bit primes (a wide source digit
 and a wide target) and with 60-bit special primes, then rotations and
-products through them at the key-switch workload's size.
+products through them at the key-switch workload's size, with the key
+product fused into the forward NTT's low pass and without.
 
 The kernel is chosen when a context is created: the int8-MFMA kernel
 (k_basis_convert_mfma) by default, the VALU kernels (k_basis_convert_fp and
@@ -64,11 +65,15 @@ def test_mfma_modup_moddown_parity(name):
 
 
 @pytest.mark.slow
-def test_mfma_keyswitch_full_size():
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_mfma_keyswitch_full_size(fused, monkeypatch):
     """Rotation, multiply-relinearise-rescale and a hoisted rotation at
-    N = 2^16 on the key-switch chain, limbs equal to the oracle's."""
+    N = 2^16 on the key-switch chain, limbs equal to the oracle's; with the
+    extended digits' low NTT pass fused with the key product (the default)
+    and with the separate kernels (CKKS_KEYSWITCH_FUSED=0)."""
     from easyfhe import fhe
 
+    monkeypatch.setenv("CKKS_KEYSWITCH_FUSED", fused)
     rot = 1 << 7
     client, ctx = device_context("keyswitch", rotations=(rot, 3))
     orc = oracle_context("keyswitch")
