@@ -31,6 +31,12 @@ HBM_PEAK_GBS = 8000.0
 # of each limb-polynomial once): two passes, FETCH_SIZE/WRITE_SIZE counter
 # runs calibrated against a device copy (profiles/ntt_batch_pmc_traffic.md)
 NTT_TRAFFIC_RATIO = 2.02
+# HBM bytes of one key-switch step (64 ciphertexts, 15 rotations + 34 HMult
+# levels): FETCH_SIZE x 1.999 + WRITE_SIZE x 1.000 summed over the step's
+# kernels in rocprofv3 counter runs of bench.py --mode ks-profile
+# (profiles/keyswitch_step_traffic.md); "fused" is the default path,
+# "separate" the one with CKKS_KEYSWITCH_FUSED=0
+KS_STEP_TRAFFIC = {"fused": 1737.4e9, "separate": 1942.6e9}
 # 12 special primes of 44 bits: P = 2^528 exceeds the largest digit (2^500) and
 # every limb but q_0 takes the fp64 modular-arithmetic path of the NTT
 PARAMS = dict(log_n=16, depth=35, dnum=3, dcrt_bits=40, first_mod=60, special_bits=44)
@@ -373,12 +379,17 @@ def main() -> int:
     result["int_peak"] = peaks
     result["kernels"] = kernel_table(prof, peaks)
     kernel_bytes = sum(v["bytes"] for v in prof.values())
+    path = "separate" if os.environ.get("CKKS_KEYSWITCH_FUSED") == "0" else "fused"
+    traffic = KS_STEP_TRAFFIC[path] if args.cts == 64 and levels == 34 else None
     result["keyswitch_roofline"] = {
         "bound": "hbm", "achieved": round(ks_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(ks_gbs / HBM_PEAK_GBS, 4),
         "algorithmic_bytes_per_step": round(step_bytes),
         "kernel_bytes_per_step": round(kernel_bytes),
         "kernel_over_algorithmic": round(kernel_bytes / step_bytes, 2),
+        "path": path,
+        "traffic": round(traffic) if traffic else None,
+        "traffic_over_algorithmic": round(traffic / step_bytes, 2) if traffic else None,
     }
     result["matvec_config"] = measure_matvec_config()
     if not (args.no_bootstrap and args.no_linear and args.no_mlp and args.no_attention):
