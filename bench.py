@@ -399,6 +399,11 @@ def main() -> int:
         # the bootstrap workload on the same chain (32 ciphertexts at one limb)
         result["bootstrap"] = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group,
                                                 args.budget, 1)
+        # the slim refreshes' shape: 128-slot ciphertexts through the sparse
+        # program (sub-sum, then 128-slot transforms)
+        result["bootstrap_sparse_128"] = measure_bootstrap(client, ctx, args.boot_cts,
+                                                           args.boot_group, args.budget, 1,
+                                                           log_slots=7)
     if not args.no_linear:
         # the square linear of a decoder layer on the same chain
         result["fm_linear"] = measure_fm_linear(client, ctx)
@@ -419,28 +424,32 @@ def main() -> int:
     return 0
 
 
-def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int) -> dict:
-    """Full-slot bootstrap of n_cts ciphertexts at the bottom level (one limb,
-    values uniform[-1, 1] from seed 0) in batched groups: CoeffToSlot /
-    SlotToCoeff with the given level budget, EvalMod at a 2^80 working scale,
-    output_levels the most the chain allows.  Returns rate, precision and the
-    program's shape."""
+def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
+                      log_slots: int | None = None) -> dict:
+    """Bootstrap of n_cts ciphertexts at the bottom level (one limb, values
+    uniform[-1, 1] from seed 0) in batched groups: CoeffToSlot / SlotToCoeff
+    with the given level budget, EvalMod at a 2^80 working scale,
+    output_levels the most the chain allows.  Full-slot by default; with
+    log_slots below log N - 1 the sparse program (sub-sum, then the
+    2^log_slots-slot transforms) on ciphertexts of that many slots.  Returns
+    rate, precision and the program's shape."""
     import math
 
     from easyfhe.bs import openfhe as bs
 
     budget = tuple(int(v) for v in budget)
-    probe = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget, output_levels=0)
+    ls = ctx.logN - 1 if log_slots is None else int(log_slots)
+    probe = bs.BootstrapSpec(log_slots=ls, level_budget=budget, output_levels=0)
     depth = bs.generate(ctx, probe).depth_limbs
-    bspec = bs.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=budget,
-                             output_levels=ctx.L - depth - 1)
+    bspec = bs.BootstrapSpec(log_slots=ls, level_budget=budget, output_levels=ctx.L - depth - 1)
     t0 = time.perf_counter()
     prog = bs.generate(ctx, bspec)
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
-    zs = [rng.uniform(-1, 1, ctx.max_slots) for _ in range(n_cts)]
-    cts = [client.encrypt(z, cur_limbs=1, enc_id=100000 + i) for i, z in enumerate(zs)]
+    zs = [rng.uniform(-1, 1, 1 << ls) for _ in range(n_cts)]
+    cts = [client.encrypt(z, slots=1 << ls, cur_limbs=1, enc_id=100000 + i)
+           for i, z in enumerate(zs)]
     group = max(1, min(group, len(cts)))
     t0 = time.perf_counter()
     for _ in range(max(1, warmup)):
@@ -465,6 +474,8 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int) 
         "ms_per_bootstrap": round(wall * 1000.0 / len(cts), 3),
         "gpu_event_ms_per_bootstrap": round(ev0.elapsed_time(ev1) / len(cts), 3),
         "ciphertexts": len(cts),
+        "slots": 1 << ls,
+        "subsum_rotations": len(prog.subsum),
         "group": group,
         "budget": list(budget),
         "linear_levels": prog.evalmod.strategy,
@@ -1285,6 +1296,8 @@ def bootstrap_bench(spec, args) -> int:
     spec.rotations = ()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
     b = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group, args.budget, args.warmup)
+    sparse = measure_bootstrap(client, ctx, args.boot_cts, args.boot_group, args.budget,
+                               args.warmup, log_slots=7)
     result = {
         "metric": "bootstrap/s @N=2^16",
         "value": b["value"],
@@ -1304,6 +1317,7 @@ def bootstrap_bench(spec, args) -> int:
                         f"{tuple(b['budget'])}",
         },
         "bootstrap": b,
+        "bootstrap_sparse_128": sparse,
     }
     print(json.dumps(result), flush=True)
     return 0

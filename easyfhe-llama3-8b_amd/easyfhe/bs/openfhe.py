@@ -98,10 +98,29 @@ def _check_spec(spec: BootstrapSpec, log_n: int) -> None:
 
 
 def _transform_log_slots(spec: BootstrapSpec, log_n: int) -> int:
-    """The linear transforms always act on all N/2 slots: a sparse
-    ciphertext's plaintext is a full-slot plaintext whose slots repeat its
-    2^log_slots values, so the full-slot program refreshes it unchanged."""
-    return log_n - 1
+    """The linear transforms act on the program's 2^log_slots slots.  A
+    sparse ciphertext's plaintext (log_slots < log_n - 1) is a polynomial in
+    Y = X^gap, gap = N / 2^(log_slots + 1), whose full-slot view repeats its
+    2^log_slots values; after the sub-sum the raised ciphertext is such a
+    polynomial too, and the n-slot special FFT maps its 2n coefficients to
+    the n slots (the full-slot view of every rotation and diagonal repeats
+    with period n)."""
+    return int(spec.log_slots)
+
+
+def _subsum_rotations(spec: BootstrapSpec, log_n: int) -> list[int]:
+    """Rotations of the sub-sum: n, 2n, 4n, .. N/4 for n = 2^log_slots (none
+    for a full-slot program).  Adding each rotation sums the N / 2n copies of
+    the n-periodic slot vector, i.e. the trace to Z[Y]/(Y^2n + 1): it keeps
+    the raised polynomial's coefficients at multiples of gap (times gap) and
+    removes the others (reference bootstrap.py:34-45 selects such a program
+    for the slim refreshes)."""
+    n, half = 1 << int(spec.log_slots), 1 << (int(log_n) - 1)
+    out, r = [], n
+    while r < half:
+        out.append(r)
+        r *= 2
+    return out
 
 
 def _plans(spec: BootstrapSpec, params: "BootstrapParams | None" = None, log_n: int = 0):
@@ -140,6 +159,7 @@ def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> 
         cts, stc = _plans(spec, p, int(log_n))
         for plan in (*cts, *stc):
             rots |= _level_rotations(plan, n)
+        rots.update(_subsum_rotations(spec, int(log_n)))
         rots.add(2 * (1 << int(log_n)) - 1)
     return Requirements(rotations=tuple(sorted(rots)))
 
@@ -172,6 +192,8 @@ class BootstrapProgram:
     ladder: cheb.Ladder | None = None
     constants: fhe.ConstantBundle | None = None
     output_limbs: int = 0
+    subsum: list = field(default_factory=list)  # sub-sum rotations (sparse programs)
+    read_scale: float = 0.0                     # scale the CoeffToSlot input is read at
 
     @property
     def depth_limbs(self) -> int:
@@ -240,6 +262,10 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     ladder_levels = depth + p.double_angles
     q0 = float(primes[0])
     s0 = 2.0 * p.K * q0  # scale the raised ciphertext is read at
+    # the sub-sum multiplies the kept coefficients by gap = N / 2n: the first
+    # CoeffToSlot level's diagonals carry 1 / gap, so the scale plan and the
+    # level count are those of the full-slot program
+    gap = (ctx.N // 2) // n
     drops = _plan_cts_drops(n_cts, math.log2(s0), bits, step * bits, p.cts_pt_bits)
     cost = sum(drops) + step * ladder_levels + step + (n_stc - 1)
     T = int(spec.output_levels) + 1 + cost
@@ -250,7 +276,8 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
 
     prog = BootstrapProgram(spec=spec, context=ctx, evalmod=p, coefficients=coeffs,
                             cheb_depth=depth, step=step, raise_limbs=T,
-                            target_ratio=2.0 ** -p.ratio_bits)
+                            target_ratio=2.0 ** -p.ratio_bits,
+                            subsum=_subsum_rotations(spec, ctx.logN), read_scale=s0)
     vectors = {}
 
     # CoeffToSlot: the last level lands on the ladder top
@@ -268,7 +295,7 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
             w = 2.0 ** p.cts_pt_bits
             want = scale * w / div
         name = f"cts{i}"
-        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n))
+        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, 1.0 / gap if i == 0 else 1.0))
         prog.cts.append(_Level(name, plan, limbs, d, w, want))
         scale, limbs = want, limbs - d
     prog.ladder = ladder
@@ -330,8 +357,12 @@ def _prescale(ct, prog: BootstrapProgram, ctx):
     return x, s * c / q1 / want
 
 
+def _program_slots(prog: BootstrapProgram) -> int:
+    return 1 << int(prog.spec.log_slots)
+
+
 def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
-    n = ctx.N // 2
+    n = _program_slots(prog)
     plan = lv.plan
     ext = prog.evalmod.strategy != "normal"
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
@@ -342,6 +373,19 @@ def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
         acc = fhe.rescale_many([acc], ctx, primes=lv.primes)[0]
     acc.set_scale(lv.out_scale, 1)
     return acc
+
+
+def _subsum_many(xs: list, prog: BootstrapProgram, ctx) -> list:
+    """x <- x + rot(x, r) for the program's sub-sum rotations, on every
+    ciphertext of the batch (one batched key switch per rotation)."""
+    for r in prog.subsum:
+        rot = fhe.homo_rotate_many(xs, int(r), ctx)
+        nxt = [fhe.homo_add(a, b, ctx) for a, b in zip(xs, rot)]
+        for a, b in zip(xs, rot):
+            a.release()
+            b.release()
+        xs = nxt
+    return xs
 
 
 def _evalmod(ops: cheb.LadderOps, y: cheb.LCt, prog: BootstrapProgram) -> cheb.LCt:
@@ -360,10 +404,10 @@ def bootstrap(ct, context, program: BootstrapProgram):
         raise ValueError("bootstrap expects a degree-1 Q-basis ciphertext")
     if int(ct.slots) != prog.spec.slots:
         raise ValueError(f"bootstrap input slots={ct.slots} != program slots={prog.spec.slots}")
-    q0 = float(ctx.primes()[0])
     x, ratio = _prescale(ct, prog, ctx)
     x = fhe.mod_raise(x, prog.raise_limbs, ctx)
-    x.set_scale(2.0 * prog.evalmod.K * q0, 1)
+    x = _subsum_many([x], prog, ctx)[0]
+    x.set_scale(prog.read_scale, 1)
     for lv in prog.cts:
         x = _linear_level(x, lv, prog, ctx)
 
@@ -384,7 +428,7 @@ def bootstrap(ct, context, program: BootstrapProgram):
 
 
 def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> list:
-    n = ctx.N // 2
+    n = _program_slots(prog)
     plan = lv.plan
     if prog.evalmod.strategy == "normal":
         return [_linear_level(x, lv, prog, ctx) for x in xs]
@@ -400,7 +444,6 @@ def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> lis
 
 
 def _bootstrap_group(cts: list, ctx, prog: BootstrapProgram) -> list:
-    q0 = float(ctx.primes()[0])
     xs, ratios = [], []
     for ct in cts:
         if ct.degree != 1 or ct.is_ext:
@@ -408,10 +451,11 @@ def _bootstrap_group(cts: list, ctx, prog: BootstrapProgram) -> list:
         if int(ct.slots) != prog.spec.slots:
             raise ValueError(f"bootstrap input slots={ct.slots} != program slots={prog.spec.slots}")
         x, ratio = _prescale(ct, prog, ctx)
-        x = fhe.mod_raise(x, prog.raise_limbs, ctx)
-        x.set_scale(2.0 * prog.evalmod.K * q0, 1)
-        xs.append(x)
+        xs.append(fhe.mod_raise(x, prog.raise_limbs, ctx))
         ratios.append(ratio)
+    xs = _subsum_many(xs, prog, ctx)
+    for x in xs:
+        x.set_scale(prog.read_scale, 1)
     for lv in prog.cts:
         xs = _linear_level_many(xs, lv, prog, ctx)
     ops = cheb.BatchLadderOps(ctx, prog.ladder)

@@ -207,8 +207,91 @@ def test_requirements_and_limb_plan():
     assert all(0 < r < 2 * 65536 for r in req.rotations)
     # extended-basis levels (at most 2 giants): up to 32 babies per level
     assert len(req.rotations) <= 96
-    # a sparse program runs the full-slot transforms (its slots repeat)
+    # a sparse program: the sub-sum's rotations n, 2n, .., N/4 plus its
+    # n-slot transforms' (all below n), and the conjugation
     sparse = bs.requirements([bs.BootstrapSpec(log_slots=7, level_budget=(3, 3))], log_n=16)
-    assert sparse.rotations == req.rotations
+    subsum = {128 << k for k in range(8)}
+    assert subsum <= set(sparse.rotations)
+    assert all(r < 128 for r in set(sparse.rotations) - subsum - {2 * 65536 - 1})
+    assert len(sparse.rotations) < len(req.rotations)
     with pytest.raises(ValueError):
         bs.requirements([bs.BootstrapSpec(log_slots=16)], log_n=16)
+
+
+def _slots_of(coeffs: np.ndarray) -> np.ndarray:
+    """Full-slot view (N/2 slots) of a real coefficient vector of length N:
+    the special FFT of u_k = m_k + i m_(k + N/2)."""
+    half = len(coeffs) // 2
+    return _special_fft(coeffs[:half] + 1j * coeffs[half:])
+
+
+@pytest.mark.parametrize("log_n,log_slots,budget", [(10, 4, (2, 2)), (9, 3, (3, 3))])
+def test_sparse_bootstrap_model(log_n, log_slots, budget):
+    """The sparse program on values: after ModRaise the raised polynomial has
+    all N coefficients (the overflow I); the sub-sum (rotations n, 2n, ..)
+    is the trace, which keeps gap times the coefficients at multiples of
+    gap = N / 2n; the n-slot CoeffToSlot (first level scaled by 1 / gap)
+    applied to the full-length, n-periodic vector, EvalMod and SlotToCoeff
+    return the message in every copy."""
+    N, half = 1 << log_n, 1 << (log_n - 1)
+    n = 1 << log_slots
+    gap = half // n
+    rng = np.random.default_rng(log_n + log_slots)
+    p = bs.BootstrapParams()
+    spec = bs.BootstrapSpec(log_slots=log_slots, level_budget=budget)
+    cts_plans, stc_plans = bs._plans(spec, p, log_n)
+    rots = bs._subsum_rotations(spec, log_n)
+    assert rots == [n << k for k in range(int(math.log2(gap)))]
+    # the message's Y-polynomial (Y = X^gap, 2n real coefficients)
+    z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    Pn = np.array([int(format(i, f"0{log_slots}b")[::-1], 2) for i in range(n)])
+    u = z.copy()
+    for s_ in reversed(range(1, log_slots + 1)):
+        u = lintrans.apply_diagonals(lintrans.stage_diagonals(n, s_, True), u)
+    u_nat = np.empty_like(u)
+    u_nat[Pn] = u
+    t = np.concatenate([u_nat.real, u_nat.imag]) * 2.0 ** -p.ratio_bits
+    m = np.zeros(N)
+    m[::gap] = t
+    # its full-slot view repeats z
+    assert np.abs(_slots_of(m) - np.tile(z, gap) * 2.0 ** -p.ratio_bits).max() < 1e-9
+    # ModRaise: an integer overflow on every coefficient
+    I = rng.integers(-12, 13, N).astype(float)
+    x = _slots_of(m + I) / (2 * p.K)
+    # the sub-sum, as slot rotations
+    for r in rots:
+        x = x + np.roll(x, -r)
+    keep = np.zeros(N)
+    keep[::gap] = gap * (m + I)[::gap]
+    assert np.abs(x - _slots_of(keep) / (2 * p.K)).max() < 1e-8
+    assert np.abs(x - np.tile(x[:n], gap)).max() < 1e-8
+    for i, plan in enumerate(cts_plans):
+        rows = plan.plaintext_rows(n, 1.0 / gap if i == 0 else 1.0)
+        offs = bs._baby_offsets(plan, n)
+        giant = bs._giant_offset(plan, n)
+        full = np.zeros(half, dtype=np.complex128)
+        for g in range(plan.giant):
+            inner = sum(np.tile(rows[g * plan.baby + b], gap) * np.roll(x, -offs[b])
+                        for b in range(plan.baby))
+            full = full + np.roll(inner, -g * giant)
+        x_n = _bsgs(x[:n], plan, rows)
+        assert np.abs(full - np.tile(x_n, gap)).max() < 1e-8
+        x = full
+    # bit-reversed t_k + i t_(k+n) (with the kept overflow) / 2K
+    tk = (m + I)[::gap]
+    want = (tk[:n] + 1j * tk[n:])[Pn] / (2 * p.K)
+    assert np.abs(x[:n] - want).max() < 1e-8
+    coeffs = bs._evalmod_coefficients(p)
+    outs = []
+    for v in (x[:n] + np.conj(x[:n]), -1j * (x[:n] - np.conj(x[:n]))):
+        ops = ValueOps()
+        c = cheb.evaluate(ops, cheb.LCt(v.real, 0), coeffs)
+        for _ in range(p.double_angles):
+            c = ops.add_const(ops.double(ops.mul(c, c)), -1.0)
+        outs.append(c.ct)
+    u2 = outs[0] + 1j * outs[1]
+    fold = 1.0 / (2 * math.pi * 2.0 ** -p.ratio_bits)
+    for i, plan in enumerate(stc_plans):
+        u2 = _bsgs(u2, plan, plan.plaintext_rows(n, fold if i == 0 else 1.0))
+    err = np.abs(u2 - z).max()
+    assert err < 2.0 ** -18, err

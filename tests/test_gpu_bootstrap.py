@@ -194,22 +194,33 @@ def test_bootstrap_pair_refreshes_two_real_streams(boot_ctx):
         assert -math.log2(err) > 14, err
 
 
-def test_bootstrap_sparse_slots(boot_ctx):
-    """A 128-slot ciphertext (the reference's slim RMSNorm program shape) is
-    refreshed by the full-slot transform: its plaintext repeats the 128 values."""
+@pytest.mark.parametrize("log_slots,budget", [(7, (3, 3)), (4, (2, 2)), (10, (3, 3))])
+def test_bootstrap_sparse_slots(boot_ctx, log_slots, budget):
+    """A sparse ciphertext (128 slots: the reference's slim RMSNorm program
+    shape) through the sparse program: the sub-sum (rotations by n, 2n, ..
+    N/4) leaves the raised polynomial's coefficients at multiples of
+    N / 2n, then the n-slot CoeffToSlot, EvalMod and SlotToCoeff.  One
+    bootstrap and a batched group of three agree with each other and with
+    the message."""
     from easyfhe.bs import openfhe as bs
 
     client, ctx = boot_ctx
-    slots = 128
-    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=7, level_budget=(3, 3), output_levels=3))
+    slots = 1 << log_slots
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=log_slots, level_budget=budget,
+                                             output_levels=3))
     assert prog.spec.slots == slots
+    assert prog.subsum == [slots << k for k in range(ctx.logN - 1 - log_slots)]
     rng = np.random.default_rng(11)
-    z = rng.uniform(-1, 1, slots)
-    ct = client.encrypt(z, slots=slots, cur_limbs=1, enc_id=95)
-    out = bs.bootstrap(ct, ctx, prog)
+    zs = [rng.uniform(-1, 1, slots) for _ in range(3)]
+    cts = [client.encrypt(z, slots=slots, cur_limbs=1, enc_id=95 + i) for i, z in enumerate(zs)]
+    out = bs.bootstrap(cts[0], ctx, prog)
     assert out.slots == slots and out.state.cur_limbs == 4
-    err = np.abs(client.decrypt_complex(out) - z).max()
+    err = np.abs(client.decrypt_complex(out) - zs[0]).max()
     assert -math.log2(err) > 14, err
+    many = bs.bootstrap_many(cts, ctx, prog, group=3)
+    assert np.array_equal(many[0].download(), out.download())
+    for o, z in zip(many, zs):
+        assert -math.log2(np.abs(client.decrypt_complex(o) - z).max()) > 14
 
 
 def test_refresh_point_pairs_and_clamped_drop(boot_ctx):

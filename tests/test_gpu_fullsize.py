@@ -44,6 +44,31 @@ def test_bootstrap_32_ciphertexts_full_size(capsys):
     assert b["precision_bits_min"] >= 20.0, b
 
 
+@pytest.mark.timeout(300)
+def test_sparse_bootstrap_128_slots_full_size(capsys):
+    """The sparse program on 128-slot ciphertexts at N = 2^16 (the slim
+    refreshes' shape): 32 ciphertexts, groups of 16, budget (3, 3): at least
+    20 bits, as the full-slot program, and at least its output limbs (the
+    level plan is the same; the sub-sum's factor rides on the first
+    CoeffToSlot level)."""
+    import bench
+
+    client, ctx = device_context(bench.PARAMS, relin=True)
+    full = bench.measure_bootstrap(client, ctx, n_cts=16, group=16, budget=(3, 3), warmup=0)
+    b = bench.measure_bootstrap(client, ctx, n_cts=32, group=16, budget=(3, 3), warmup=0,
+                                log_slots=7)
+    with capsys.disabled():
+        print(f"\nsparse bootstrap N=2^16, 128 slots: precision min {b['precision_bits_min']} "
+              f"mean {b['precision_bits_mean']} bits, {b['ms_per_bootstrap']} ms each, "
+              f"{b['raise_limbs']} -> {b['output_limbs']} limbs; full-slot: "
+              f"{full['precision_bits_min']} bits, {full['ms_per_bootstrap']} ms, "
+              f"{full['raise_limbs']} -> {full['output_limbs']} limbs", flush=True)
+    ctx.close()
+    assert b["slots"] == 128 and b["subsum_rotations"] == 8
+    assert b["precision_bits_min"] >= 20.0, b
+    assert b["output_limbs"] >= full["output_limbs"]
+
+
 # CKKS error of one refreshed full-size layer against its own fp64 model
 # (same series, same Algorithm-2 softmax): the refreshes work at ~23 bits on
 # a stream bounded by 16, and the three softmax rounds square the
