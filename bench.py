@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -187,7 +188,7 @@ def main() -> int:
                          "(default 32)")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "ks-profile", "int-peak",
                                        "bootstrap", "linear", "mlp", "attention", "layer",
-                                       "layers", "prefill"],
+                                       "layers", "layers-reference-chain", "prefill"],
                     default="keyswitch",
                     help="ntt-profile: only the batch NTT and a 36 MiB device copy "
                          "(the calibration kernel), for rocprofv3 counter runs; "
@@ -200,6 +201,9 @@ def main() -> int:
                          "attention: the causal attention of a layer; "
                          "layer: one whole encrypted decoder layer on a deeper chain; "
                          "layers: consecutive layers with their bootstraps (--layers); "
+                         "layers-reference-chain: the same on the reference's chain "
+                         "(60 + 37 x 59-bit primes, dnum 5) with the softmax normalisers "
+                         "refreshed; "
                          "prefill: the encrypted prefill from token ids to logits (--layers, "
                          "default 32)")
     ap.add_argument("--boot-cts", type=int, default=32)
@@ -248,6 +252,11 @@ def main() -> int:
     if args.mode == "layers":
         print(json.dumps({"fm_layers": measure_fm_layers(2 if args.layers is None
                                                          else args.layers)}), flush=True)
+        return 0
+    if args.mode == "layers-reference-chain":
+        print(json.dumps({"fm_layers_reference_chain": measure_fm_layers(
+            2 if args.layers is None else args.layers, params=REFERENCE_CHAIN_PARAMS,
+            refresh_normalisers=True)}), flush=True)
         return 0
     if args.mode == "layer":
         print(json.dumps({"fm_layer": measure_fm_layer(warmup=args.warmup)}), flush=True)
@@ -418,6 +427,11 @@ def main() -> int:
         # second in steady state); this chain's keys are freed first
         ctx.close()
         result["fm_layers"] = measure_fm_layers(2)
+        # the same layers on the reference's chain (60 + 37 x 59-bit primes,
+        # dnum 5), whose bootstraps return fewer levels: every softmax
+        # round's normaliser is refreshed as well
+        result["fm_layers_reference_chain"] = measure_fm_layers(
+            2, params=REFERENCE_CHAIN_PARAMS, refresh_normalisers=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -847,13 +861,23 @@ def measure_fm_layer(warmup: int = 0) -> dict:
 # A chain for refreshed layers: bootstraps (budget (3,3), 26 limbs) return the
 # 40 limbs of a layer's deepest block (scores -> softmax -> PV -> W_o)
 REFRESH_PARAMS = dict(log_n=16, depth=65, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+# the reference's layer chain (assets/feature_major.json:3-16): 60 + 37 x 59-bit
+# primes, dnum 5; 8 special primes of 60 bits (P = 2^480 exceeds the largest
+# digit, 60 + 7 x 59 = 473 bits)
+REFERENCE_CHAIN_PARAMS = dict(log_n=16, depth=37, dnum=5, dcrt_bits=59, first_mod=60,
+                              special_bits=60)
 
 
-def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
+def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
+                      budget=(3, 3), refresh_normalisers: bool = False) -> dict:
     """Consecutive Llama-3-8B decoder layers over 128 tokens with their
     refreshes (bootstraps included): per layer, paired batched refreshes of
     the residual stream before each RMSNorm and of the softmax's mapped
-    scores (24 ciphertext bootstraps), on REFRESH_PARAMS.  The first layer
+    scores (24 ciphertext bootstraps), on REFRESH_PARAMS (or `params`) with
+    CoeffToSlot / SlotToCoeff budget `budget`.  With `refresh_normalisers`
+    every softmax round's slim normaliser is bootstrapped too (3 more
+    bootstraps per layer), which lets the layer run on a chain whose
+    bootstraps return fewer levels (the reference's).  The first layer
     starts from a one-limb input; from the second on a layer runs in steady
     state.  Weights N(0, 0.02) in a Hadamard-rotated residual basis,
     `weight_sets` distinct sets cycled over the layers; inputs N(0, 1); seed
@@ -864,19 +888,22 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     refreshed_layer_programs)
+                                     normaliser_program, refreshed_layer_programs)
 
+    params = REFRESH_PARAMS if params is None else params
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     norm = rsqrt_entry(0.5, 16.0, 63)
     ap = LayerApproximations(norm, norm, silu_entry(-12.0, 12.0, 63),
                              SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=7,
                                            first_inverse_degree=31, inverse_degree=47))
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
-    spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=0,
-                               rotations=decoder_layer_rotations(lay, H, hd))
+    spec = fhe.CKKSContextSpec(**params, seed=0, rotations=decoder_layer_rotations(lay, H, hd))
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
-    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15)
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15, level_budget=budget,
+                                              refresh_normalisers=refresh_normalisers)
+    lam_prog = (normaliser_program(ctx, ap, T, log_slots=15, level_budget=budget)
+                if refresh_normalisers else None)
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
@@ -890,7 +917,12 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     ctx.synchronize()
     upload_s = time.perf_counter() - t0
     packed = lay.pack(x)
-    cur = [client.encrypt(packed[i], cur_limbs=1, enc_id=600000 + i)
+    from easyfhe.bs import openfhe as bs
+
+    # the lowest level a refresh takes on this chain (two limbs when the
+    # primes are about as wide as q_0)
+    start = bs.input_limbs(ctx)
+    cur = [client.encrypt(packed[i], cur_limbs=start, enc_id=600000 + i)
            for i in range(lay.cipher_count)]
     per_layer, stages = [], {}
     ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
@@ -898,7 +930,8 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     t_all = time.perf_counter()
     for layer in range(int(n_layers)):
         res = decoder_layer_refreshed_fhe(cur, dev[layer % len(dev)], crypto_context=ctx,
-                                          program=prog, residual_program=res_prog)
+                                          program=prog, residual_program=res_prog,
+                                          normaliser_program=lam_prog)
         for c in cur:
             c.release()
         cur = list(res.ciphers)
@@ -916,6 +949,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
     for d in dev:
         d.close()
     mem = ctx.memory_info()
+    L, alpha, primes = ctx.L, ctx.alpha, [int(q) for q in ctx.primes()]
     ctx.close()
     want, smax = x, 0.0
     for layer in range(int(n_layers)):
@@ -930,10 +964,14 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2) -> dict:
         "per_layer_s": [round(v, 3) for v in per_layer],
         "workload": f"{n_layers} Llama-3-8B decoder layers (d=4096, 32/8 heads x 128, SwiGLU 14336) "
                     "over 128 tokens in 16 ciphertexts of 8 lanes, bootstraps included "
-                    "(3 paired refreshes = 24 bootstraps per layer), N=2^16, Q=1x60b+65x40b, "
-                    f"dnum=5, P=14x44b; bootstraps return {prog.output_limbs} limbs (scores) "
+                    "(3 paired refreshes = 24 bootstraps per layer"
+                    + (", plus 3 softmax normaliser refreshes" if refresh_normalisers else "")
+                    + f"), N=2^16, Q=1x{params['first_mod']}b+{L - 1}x{params['dcrt_bits']}b, "
+                    f"dnum={params['dnum']}, P={alpha}x{params['special_bits']}b, CtS/StC budget "
+                    f"{tuple(budget)}; bootstraps return {prog.output_limbs} limbs (scores) "
                     f"and {res_prog.output_limbs} (residual stream); "
                     f"{len(wsets)} weight sets cycled",
+        "log_qp_bits": round(sum(math.log2(q) for q in primes), 1),
         "last_layer_stages_s": {k: round(v, 3) for k, v in stages.items()},
         "max_abs_err_vs_fp64": float(np.abs(got - want).max()),
         "output_abs_max": float(np.abs(want).max()),

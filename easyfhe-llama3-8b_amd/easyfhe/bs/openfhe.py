@@ -361,6 +361,17 @@ def _program_slots(prog: BootstrapProgram) -> int:
     return 1 << int(prog.spec.log_slots)
 
 
+def input_limbs(context, params: "BootstrapParams | None" = None) -> int:
+    """Limbs a bootstrap input needs at the chain's one-limb scale: one when
+    that scale is at most 2^-ratio_bits q_0 (an integer multiply then brings
+    the message to it), two when it is larger (the prescale rescales by q_1:
+    chains whose primes are about as wide as q_0)."""
+    ctx = getattr(context, "context", context)
+    p = params or BootstrapParams()
+    want = 2.0 ** -p.ratio_bits * float(ctx.primes()[0])
+    return 1 if round(want / float(ctx.scale_at(1))) >= 1 else 2
+
+
 def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
     n = _program_slots(prog)
     plan = lv.plan

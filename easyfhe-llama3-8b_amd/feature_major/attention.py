@@ -477,6 +477,36 @@ def softmax_depth(cfg: SoftmaxConfig, seq_len: int) -> int:
     return exp_d + 1 + (first + 4) + (int(cfg.rounds) - 1) * (later + 4)
 
 
+def softmax_depth_refreshed(cfg: SoftmaxConfig, seq_len: int,
+                            input_limbs: int = 1) -> tuple[int, int]:
+    """With every round's normaliser refreshed: (levels the main stream
+    consumes, limbs the softmax input needs so that round r's slim
+    normaliser keeps ``input_limbs`` limbs after its series, what its
+    bootstrap takes).  The main stream
+    then loses two levels per round (square, product with the normaliser):
+    the inverse series runs on the slim ciphertext, which the refresh lifts
+    back above the squares."""
+    from easyfhe.chebyshev import chebyshev_depth
+
+    exp_d = chebyshev_depth(cfg.exp()["coefficients"])
+    first = chebyshev_depth(cfg.first_inverse()["coefficients"])
+    later = chebyshev_depth(cfg.inverse(seq_len)["coefficients"])
+    rounds = int(cfg.rounds)
+    main = exp_d + 1 + 2 * rounds
+    # round r starts exp_d + 1 + 2 r levels down; its slim normaliser is two
+    # levels below that and needs the series' depth plus one limb
+    need = max(exp_d + 1 + 2 * r + 2 + (first if r == 0 else later) + int(input_limbs)
+               for r in range(rounds))
+    return main, need
+
+
+def _slim_active(geo: AttentionGeometry) -> np.ndarray:
+    """Slots of the slim normaliser that hold a row sum: ciphertext c's lanes
+    at feature offset c of every head block, i.e. slot mod (hd L) < n L."""
+    s = np.arange(geo.slots)
+    return (s % (int(geo.head_dim) * geo.lanes)) < geo.ciphers * geo.lanes
+
+
 def _lane_rows(geo: AttentionGeometry, c: int, lane_values, *, modulus: int, below: int):
     """Values per lane on features f with f mod modulus < below."""
     s = np.arange(geo.slots)
@@ -537,10 +567,16 @@ def softmax_alg2(mapped_scores, geo: AttentionGeometry, cfg: SoftmaxConfig, *, c
                 t.release()
                 slim = nxt
             _release(terms[1:])
-            off = fhe.encode_scalar(beta, int(slim.state.cur_limbs),
-                                    scaling_factor=float(slim.state.scaling_factor), context=ctx)
-            mapped = fhe.homo_add_scalar(slim, off, ctx)
-            _release([slim, off])
+            # the map's offset on the slots that hold a row sum only: the
+            # others stay at 0, the middle of the series' interval, so the
+            # series stays bounded there (beta alone maps them just outside
+            # [-1, 1], where a degree-47 series reaches hundreds) and a
+            # refresh sees only values in its range (the reference fills
+            # them too, softmax.py:1020-1031)
+            off = _encode(ctx, np.where(_slim_active(geo), beta, 0.0),
+                          int(slim.state.cur_limbs), float(slim.state.scaling_factor))
+            mapped = fhe.homo_add_pt(slim, off[0], ctx)
+            _release([slim] + off)
             inv = eval_chebyshev_series_cipher(mapped, entry["coefficients"], lower_bound=-1.0,
                                                upper_bound=1.0, crypto_context=ctx,
                                                input_is_chebyshev_mapped=True)
@@ -558,9 +594,14 @@ def softmax_alg2(mapped_scores, geo: AttentionGeometry, cfg: SoftmaxConfig, *, c
             _release(parts + ext)
             lam = _rotate_add_tree(sel, [-(L << b) for b in range(hb)], ctx)
             _release(sel)
-            sqa = _to_limbs(sq, int(lam[0].state.cur_limbs), ctx)
-            y = _mul_relin_rescale(sqa, lam, ctx)
+            # a refreshed normaliser may sit above the squares: both go to the
+            # lower of the two levels
+            tl = min(int(lam[0].state.cur_limbs), int(sq[0].state.cur_limbs))
+            sqa = _to_limbs(sq, tl, ctx)
+            lama = _to_limbs(lam, tl, ctx)
+            y = _mul_relin_rescale(sqa, lama, ctx)
             _release([a for a, b in zip(sqa, sq) if a is not b])
+            _release([a for a, b in zip(lama, lam) if a is not b])
             _release(sq + lam)
             sync()
             stage[f"round_{r + 1}"] = time.perf_counter() - t0

@@ -292,17 +292,81 @@ def _drop_owned(cts, limbs: int, ctx) -> list:
     return out
 
 
-def refreshed_layer_depths(approx: LayerApproximations, seq_len: int) -> tuple[int, int, int]:
+def refreshed_layer_depths(approx: LayerApproximations, seq_len: int, *,
+                           refresh_normalisers: bool = False,
+                           input_limbs: int = 1) -> tuple[int, int, int]:
     """Levels of the three blocks between refreshes: RMSNorm + Q/K/V + RoPE +
-    QK; the scores' landing + softmax + PV + W_o; RMSNorm + MLP."""
+    QK; the scores' landing + softmax + PV + W_o; RMSNorm + MLP.  With
+    ``refresh_normalisers`` every softmax round's slim normaliser is
+    bootstrapped (the reference's per-round lambda refresh,
+    operators/attention/softmax.py:1044-1095), so the score block needs the
+    main stream's levels or the slim normalisers' need, whichever is larger.
+    ``input_limbs`` is what a bootstrap input needs (``bs.input_limbs``)."""
+    from .attention import softmax_depth_refreshed
+
     a = rmsnorm_depth(approx.input_norm) + 1 + 1 + 4
-    b = 1 + softmax_depth(approx.softmax, seq_len) + 3 + 1
+    if refresh_normalisers:
+        # the softmax input (after the landing) holds b limbs
+        main, need = softmax_depth_refreshed(approx.softmax, seq_len, input_limbs)
+        b = max(1 + main + 3 + 1, need)
+    else:
+        b = 1 + softmax_depth(approx.softmax, seq_len) + 3 + 1
     c = rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu)
     return a, b, c
 
 
+def normaliser_program(crypto_context, approx: LayerApproximations, seq_len: int, *,
+                       log_slots: int, level_budget=(3, 3)):
+    """Bootstrap program for the per-round softmax normalisers: it returns
+    the softmax input's level (the highest the squares of any round sit
+    at), so that the refreshed normaliser never pulls the main stream down."""
+    from easyfhe.bs import openfhe as bs
+    from easyfhe.chebyshev import chebyshev_depth
+
+    ctx = _ctx(crypto_context)
+    lim = bs.input_limbs(ctx)
+    _, b, _ = refreshed_layer_depths(approx, seq_len, refresh_normalisers=True, input_limbs=lim)
+    exp_d = chebyshev_depth(approx.softmax.exp()["coefficients"])
+    # the score block enters with b + lim limbs; the softmax starts after the
+    # landing, the series and the mask
+    levels = b + lim - 2 - exp_d - 1
+    return bs.generate(ctx, bs.BootstrapSpec(log_slots=int(log_slots),
+                                             level_budget=tuple(level_budget),
+                                             output_levels=int(levels)))
+
+
+# |1 / x| on the normalisers' intervals stays below 2^8 (the first round's
+# inverse starts at 0.006)
+_NORMALISER_BOUND = 256.0
+
+
+def _refresh_normaliser(ct, ctx, program):
+    """One slim normaliser refreshed: scaled into the bootstrap's input range
+    through the recorded scale (no level), bootstrapped, then multiplied by
+    the bound as an integer (no level).  The result keeps the program's
+    output scale: dividing the recorded scale instead would leave the
+    normaliser 2^8 below it, and every round's product with it would carry
+    that loss into the next round's squares."""
+    from easyfhe.bs import openfhe as bs
+
+    v = ct.deep_copy()
+    v.set_scale(float(ct.state.scaling_factor) * _NORMALISER_BOUND, 1)
+    try:
+        out = bs.bootstrap(v, ctx, program)
+    finally:
+        v.release()
+    k = fhe.encode_scalar(int(_NORMALISER_BOUND), int(out.state.cur_limbs), scale_degree=0,
+                          mode="integer", context=ctx)
+    try:
+        return fhe.homo_mul_scalar(out, k, ctx)
+    finally:
+        out.release()
+        k.release()
+
+
 def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_len: int, *,
-                             log_slots: int, level_budget=(3, 3)):
+                             log_slots: int, level_budget=(3, 3),
+                             refresh_normalisers: bool = False):
     """(score program, residual program): bootstrap programs whose outputs
     hold the score block plus one limb, and the deeper of the two residual
     blocks plus two (``refreshed_layer_depths``).  A bootstrap raises its
@@ -311,22 +375,27 @@ def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_le
     from easyfhe.bs import openfhe as bs
 
     ctx = _ctx(crypto_context)
-    a, b, c = refreshed_layer_depths(approx, seq_len)
+    # the score block ends where the next refresh takes its input: one limb,
+    # or two on chains whose one-limb scale is near q_0 (bs.input_limbs)
+    lim = bs.input_limbs(ctx)
+    a, b, c = refreshed_layer_depths(approx, seq_len, refresh_normalisers=refresh_normalisers,
+                                     input_limbs=lim)
     spec = lambda levels: bs.BootstrapSpec(log_slots=int(log_slots),  # noqa: E731
                                            level_budget=tuple(level_budget),
                                            output_levels=int(levels))
     probe = bs.generate(ctx, spec(0))
     top = ctx.L - probe.depth_limbs - 1
     probe.release()
-    if top < b or top < max(a, c) + 1:
+    if top < b + lim - 1 or top < max(a, c) + 1:
         raise ValueError(f"the chain's bootstraps return at most {top + 1} limbs; the layer "
-                         f"needs {max(b + 1, max(a, c) + 2)}.")
-    return bs.generate(ctx, spec(b)), bs.generate(ctx, spec(max(a, c) + 1))
+                         f"needs {max(b + lim, max(a, c) + 2)}.")
+    return bs.generate(ctx, spec(b + lim - 1)), bs.generate(ctx, spec(max(a, c) + 1))
 
 
 def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
                                 program, residual_program=None, residual_bound: float = 32.0,
-                                group: int = 8, rope_theta: float = 500000.0) -> LayerResult:
+                                group: int = 8, rope_theta: float = 500000.0,
+                                normaliser_program=None) -> LayerResult:
     """One decoder layer with its refreshes (three paired refresh points: the
     residual stream before each RMSNorm, and the softmax's mapped scores;
     the reference refreshes at the same places, graph.py:780-990,
@@ -335,10 +404,20 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
     must return the score block's depth plus one limb; ``residual_program``
     (default ``program``) refreshes the residual stream and must return the
     deeper residual block plus two (``refreshed_layer_programs`` makes
-    both).  The input may sit at any level; it is not consumed."""
+    both).  With ``normaliser_program`` (``normaliser_program()``) every
+    softmax round's slim normaliser is refreshed as well, which shortens
+    the score block (``refreshed_layer_programs(refresh_normalisers=True)``
+    sizes the programs for it).  The input may sit at any level; it is not
+    consumed."""
+    from easyfhe.bs import openfhe as bs
+
     ctx = _ctx(crypto_context)
     lay, geo, ap = weights.layout, weights.geometry, weights.approx
-    a_depth, b_depth, c_depth = refreshed_layer_depths(ap, geo.seq_len)
+    a_depth, b_depth, c_depth = refreshed_layer_depths(
+        ap, geo.seq_len, refresh_normalisers=normaliser_program is not None,
+        input_limbs=bs.input_limbs(ctx))
+    refresh_lam = (None if normaliser_program is None
+                   else (lambda ct: _refresh_normaliser(ct, ctx, normaliser_program)))
     res_prog = program if residual_program is None else residual_program
     sync = ctx.synchronize
     stage: dict[str, float] = {}
@@ -382,7 +461,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         sr = refresh_stream(scores.ciphers, crypto_context=ctx, program=program, value_bound=1.0,
                             group=group)
         scores.release()
-        if int(sr[0].state.cur_limbs) < b_depth + 1:
+        if int(sr[0].state.cur_limbs) < b_depth + bs.input_limbs(ctx):
             _release(sr)
             raise ValueError("the score bootstrap program's outputs are too shallow for the "
                              "layer.")
@@ -391,7 +470,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         t0 = time.perf_counter()
         landed = _land_on_ladder(sr, ctx)
         _release(sr)
-        probs = softmax_alg2(landed, geo, ap.softmax, crypto_context=ctx)
+        probs = softmax_alg2(landed, geo, ap.softmax, crypto_context=ctx, refresh=refresh_lam)
         _release(landed)
         att = pv_output(probs.ciphers, v, geo, crypto_context=ctx)
         probs.release()
@@ -432,4 +511,5 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
 
 __all__ = ["DecoderLayerWeights", "LayerApproximations", "LayerResult", "decoder_layer_depth",
            "decoder_layer_fhe", "decoder_layer_refreshed_fhe", "decoder_layer_rotations",
-           "refresh_stream", "refreshed_layer_depths", "refreshed_layer_programs"]
+           "normaliser_program", "refresh_stream", "refreshed_layer_depths",
+           "refreshed_layer_programs"]

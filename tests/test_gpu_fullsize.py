@@ -11,6 +11,9 @@
   inputs N(0, 1).  It is compared with the fp64 model of the same layer with
   the same series and the same Algorithm-2 softmax (oracle/layer_numpy.py),
   so the difference is the CKKS error alone.
+* The same layer on the reference's chain (60 + 37 x 59-bit primes, dnum 5)
+  with every softmax round's normaliser refreshed as well.
+* The sparse program on 128-slot ciphertexts at N = 2^16.
 * The 32-layer prefill from 128 random token ids to the final token's
   logits (vocabulary 128256), every layer boundary encrypted.
 
@@ -77,16 +80,18 @@ def test_sparse_bootstrap_128_slots_full_size(capsys):
 LAYER_TOL = 3e-4
 
 
-@pytest.mark.timeout(400)
-def test_refreshed_layer_full_size(capsys):
+def _refreshed_layer(params, refresh_normalisers: bool):
+    """One refreshed full-size layer on the chain `params`; (decrypted output,
+    input, weights, approximations, wall seconds, output limbs)."""
     import bench
     import layer_numpy as LN
+    from easyfhe.bs import openfhe as bs
     from feature_major import FeatureMajorPrefillLayout
     from feature_major.approx import rsqrt_entry, silu_entry
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     refreshed_layer_programs)
+                                     normaliser_program, refreshed_layer_programs)
 
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     norm = rsqrt_entry(0.5, 16.0, 63)
@@ -94,26 +99,36 @@ def test_refreshed_layer_full_size(capsys):
                              SoftmaxConfig(rounds=3, shift=10.0, bound=10.0, exp_degree=7,
                                            first_inverse_degree=31, inverse_degree=47))
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
-    client, ctx = device_context(bench.REFRESH_PARAMS,
-                                 rotations=decoder_layer_rotations(lay, H, hd))
-    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15)
+    client, ctx = device_context(params, rotations=decoder_layer_rotations(lay, H, hd))
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15,
+                                              refresh_normalisers=refresh_normalisers)
+    lam = normaliser_program(ctx, ap, T, log_slots=15) if refresh_normalisers else None
     rng = np.random.default_rng(0)
     w = bench._layer_weights(rng, D, KV, hd, I, bench.randomized_hadamard(D, 1))
     x = rng.normal(0, 1, (T, D))
     packed = lay.pack(x)
-    xc = [client.encrypt(packed[i], cur_limbs=1, enc_id=600000 + i)
+    xc = [client.encrypt(packed[i], cur_limbs=bs.input_limbs(ctx), enc_id=600000 + i)
           for i in range(lay.cipher_count)]
     with DecoderLayerWeights(w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"],
                              heads=H, kv_heads=KV, head_dim=hd, intermediate=I, approx=ap,
                              layout=lay, context=ctx) as dw:
         res = decoder_layer_refreshed_fhe(xc, dw, crypto_context=ctx, program=prog,
-                                          residual_program=res_prog)
+                                          residual_program=res_prog, normaliser_program=lam)
     got = LN.fm_unpack(np.stack([client.decrypt(o) for o in res.ciphers]), T, D)
     wall, limbs_out = res.wall_seconds, res.output_limbs
     res.release()
-    prog.release()
-    res_prog.release()
+    for p_ in (prog, res_prog, lam):
+        if p_ is not None:
+            p_.release()
     ctx.close()
+    return got, x, w, ap, wall, limbs_out
+
+
+def _layer_models(x, w, ap):
+    """(fp64 model with the same series and Algorithm-2 softmax, exact fp64)."""
+    import layer_numpy as LN
+
+    H, KV, hd, T = 32, 8, 128, x.shape[0]
     sm = ap.softmax
     kw = dict(heads=H, kv_heads=KV, head_dim=hd, input_norm=ap.input_norm,
               post_attention_norm=ap.post_attention_norm, silu=ap.silu)
@@ -123,12 +138,48 @@ def test_refreshed_layer_full_size(capsys):
                                        rounds=sm.rounds, shift=sm.shift), **kw)
     exact = LN.decoder_layer_numpy(x, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"],
                                    w["down"], **kw)
+    return model, exact
+
+
+@pytest.mark.timeout(400)
+def test_refreshed_layer_full_size(capsys):
+    import bench
+
+    got, x, w, ap, wall, limbs_out = _refreshed_layer(bench.REFRESH_PARAMS, False)
+    model, exact = _layer_models(x, w, ap)
     err = float(np.abs(got - model).max())
     with capsys.disabled():
         print(f"\nrefreshed layer 128x4096: max err {err:.3g} vs the model with the same "
               f"series and softmax, {np.abs(got - exact).max():.3g} vs exact softmax, |out| "
               f"{np.abs(model).max():.3g}, {wall:.2f} s, {limbs_out} limbs out", flush=True)
     assert err < LAYER_TOL, err
+
+
+# The reference chain's bootstraps return about 20 bits (one 59-bit prime
+# per EvalMod level, against two 40-bit primes on the refresh chain: 23.6
+# bits), and the layer runs three more of them (the normalisers): measured
+# 8.3e-4 against the same-series model (0.0061 against exact softmax, as on
+# the refresh chain); the bound is 2e-3 absolute.
+LAYER_TOL_REFERENCE_CHAIN = 2e-3
+
+
+@pytest.mark.timeout(400)
+def test_refreshed_layer_reference_chain(capsys):
+    """The same layer on the reference's chain (60 + 37 x 59-bit primes,
+    dnum 5, 8 special primes of 60 bits), whose bootstraps return at most 21
+    levels: every softmax round's normaliser is refreshed too, and every
+    refresh takes its input at two limbs (the one-limb scale 2^59 is above
+    q_0 2^-10)."""
+    import bench
+
+    got, x, w, ap, wall, limbs_out = _refreshed_layer(bench.REFERENCE_CHAIN_PARAMS, True)
+    model, exact = _layer_models(x, w, ap)
+    err = float(np.abs(got - model).max())
+    with capsys.disabled():
+        print(f"\nrefreshed layer on the reference chain: max err {err:.3g} vs the model with "
+              f"the same series and softmax, {np.abs(got - exact).max():.3g} vs exact softmax, "
+              f"{wall:.2f} s, {limbs_out} limbs out", flush=True)
+    assert err < LAYER_TOL_REFERENCE_CHAIN, err
 
 
 # The prefill's final-token logits (|logits| up to ~6) against the fp64
