@@ -400,14 +400,20 @@ static const u64 *relin_rs_table(ckks_context *c, int limbs, int D) {
     for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
     return P;
   };
-  std::vector<u64> h(4 * (size_t)T + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D, 0);
+  // u64 part, then [T][D] (P p_1..p_{j-1} mod q_t, / q_t) as doubles for the
+  // fp64 kernel (targets below 2^45)
+  const size_t words = 4 * (size_t)T + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D;
+  std::vector<u64> h(words + 2 * (size_t)T * D, 0);
   u64 *pm = h.data() + 4 * (size_t)T, *pp = pm + (size_t)T * D, *pi = pp + (size_t)T * D;
   u64 *chain = pi + 2 * (size_t)D;
+  double *pmf = reinterpret_cast<double *>(h.data() + words);
   for (int t = 0; t < T; t++) {
     const u64 q = c->primes[t], P = pmod(q);
     u64 prod = 1;  // p_1..p_j mod q
     for (int j = 0; j < D; j++) {
       const u64 f = mulmod_h(P, prod, q);
+      pmf[2 * ((size_t)t * D + j)] = (double)f;
+      pmf[2 * ((size_t)t * D + j) + 1] = (double)f / (double)q;
       pm[(size_t)t * D + j] = (u64)(((u128)f << 64) % q);
       prod = mulmod_h(prod, p(j) % q, q);
       pp[(size_t)t * D + j] = mulmod_h(P, prod, q);
@@ -1362,6 +1368,15 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     c->bc_mfma = !(bc && strcmp(bc, "valu") == 0);
     const char *kf = getenv("CKKS_KEYSWITCH_FUSED");
     c->ks_fused = !(kf && strcmp(kf, "0") == 0);
+    for (auto [var, dst] : {std::pair<const char *, int *>{"CKKS_NTT_COLS_FWD", &c->ntt_cols_fwd},
+                            {"CKKS_NTT_COLS_INV", &c->ntt_cols_inv}}) {
+      const char *v = getenv(var);
+      if (v) {
+        const int n = atoi(v);
+        require(n == 16 || n == 32 || n == 64, std::string(var) + " must be 16, 32 or 64");
+        *dst = n;
+      }
+    }
     HIPCHECK(hipGetDevice(&c->device));
     c->noalloc_scratch = device_scratch(c->device);
   } catch (...) {

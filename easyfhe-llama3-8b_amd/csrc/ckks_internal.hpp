@@ -268,6 +268,9 @@ struct ckks_context {
   // inner product fused (launch_ntt_low_key); environment
   // CKKS_KEYSWITCH_FUSED=0 at creation selects the separate kernels
   bool ks_fused = true;
+  // columns per block of the N = 2^16 column passes (16, 32 or 64), forward
+  // and inverse; environment CKKS_NTT_COLS_FWD / CKKS_NTT_COLS_INV at creation
+  int ntt_cols_fwd = 64, ntt_cols_inv = 32;
 };
 
 struct ckks_ct {

@@ -249,6 +249,24 @@ __device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u6
 
 __device__ __forceinline__ int lds16(int r, int c) { return r * 272 + c + (c >> 4); }
 
+// Column passes (bit positions 15..8): a block holds all 256 rows of C
+// columns, 16 C threads (column tid mod C, row group tid / C).  C = 16: the
+// padded 16 x 272 tile above.  C = 32 or 64: every global access of a wave
+// is 8 C contiguous bytes of one row (256 or 512, against 128), and element
+// (row 16 a + b, column c) sits at b 16 C + a C + c, where both exchanges
+// are consecutive per wave without padding (64 or 128 KiB per block).
+template <int COLS>
+struct ColTile {
+  static constexpr int C = COLS;
+  static constexpr int THREADS = 16 * C;
+  static constexpr int LDS_WORDS = C == 16 ? 16 * 272 : 16 * 16 * C;
+  __device__ static int col() { return threadIdx.x & (C - 1); }
+  __device__ static int grp() { return threadIdx.x / C; }
+  __device__ static int at(int a, int b, int c) {
+    return C == 16 ? lds16(b, 16 * a + c) : b * 16 * C + a * C + c;
+  }
+};
+
 // ModDown epilogue of the forward low pass (conv items 2 i + c):
 // out_c[l][k] = (acc_c[l][k] - NTT(conv_c)[l][k]) P^-1 + add_c[l][sigma(k)]
 struct Galois64 {
@@ -321,6 +339,7 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
 }
 
 // forward, bit positions 15..8: tile = 256 rows (stride 256) x 16 columns
+template <int COLS>
 __device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
                                                         const ModQ *__restrict__ mods,
@@ -334,8 +353,9 @@ __device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Bat
   const u64 *Ws = psi_sh + ((size_t)p << 16);
   const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
   u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
-  const int col = blockIdx.x * 16 + c;
+  using CT = ColTile<COLS>;
+  const int c = CT::col(), g = CT::grp();
+  const int col = blockIdx.x * CT::C + c;
   u64 x[16];
   // round A: row = g + 16 k, stages on row bits 7..4 (k bits 3..0)
 #pragma unroll
@@ -352,11 +372,11 @@ __device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Bat
   }
   // row = g + 16 k lives at LDS tile row g, "column" 16 k + c
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(g, 16 * k + c)] = x[k];
+  for (int k = 0; k < 16; k++) sm[CT::at(k, g, c)] = x[k];
   __syncthreads();
   // round B: row = 16 g + j, stages on row bits 3..0
 #pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = sm[lds16(j, 16 * g + c)];
+  for (int j = 0; j < 16; j++) x[j] = sm[CT::at(g, j, c)];
 #pragma unroll
   for (int st = 4; st < 8; st++) {
     const int half = 8 >> (st - 4);
@@ -510,6 +530,7 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
 }
 
 // inverse, bit positions 8..15 (second pass), then x N^-1, output in [0, q)
+template <int COLS>
 __device__ __forceinline__ void k_ntt16_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                         int L, const ModQ *__restrict__ mods,
                                                         const u64 *__restrict__ ipsi,
@@ -522,8 +543,9 @@ __device__ __forceinline__ void k_ntt16_inv_high_body(u64 *__restrict__ lds, Bat
   const u64 *W = ipsi + ((size_t)p << 16);
   const u64 *Ws = ipsi_sh + ((size_t)p << 16);
   u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
-  const int col = blockIdx.x * 16 + c;
+  using CT = ColTile<COLS>;
+  const int c = CT::col(), g = CT::grp();
+  const int col = blockIdx.x * CT::C + c;
   u64 x[16];
   // round A: row = 16 g + j, stages on row bits 0..3 (st = 7..4)
 #pragma unroll
@@ -539,11 +561,11 @@ __device__ __forceinline__ void k_ntt16_inv_high_body(u64 *__restrict__ lds, Bat
     }
   }
 #pragma unroll
-  for (int j = 0; j < 16; j++) sm[lds16(j, 16 * g + c)] = x[j];
+  for (int j = 0; j < 16; j++) sm[CT::at(g, j, c)] = x[j];
   __syncthreads();
   // round B: row = g + 16 k, stages on row bits 4..7 (st = 3..0)
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = sm[lds16(g, 16 * k + c)];
+  for (int k = 0; k < 16; k++) x[k] = sm[CT::at(k, g, c)];
 #pragma unroll
   for (int st = 3; st >= 0; st--) {
     const int half = 8 >> st;
@@ -590,6 +612,12 @@ __device__ __forceinline__ double fp_reduce(double x, double qinv, double q) {
   return __fma_rn(-fp_rint(__dmul_rn(x, qinv)), q, x);
 }
 
+// x reduced to [0, q) as an exact double
+__device__ __forceinline__ double fp_canon_d(double x, double qinv, double q) {
+  const double r = fp_reduce(x, qinv, q);
+  return r < 0.0 ? __dadd_rn(r, q) : r;
+}
+
 __device__ __forceinline__ u64 fp_canon(double x, double qinv, double q) {
   double r = fp_reduce(x, qinv, q);
   r = r < 0.0 ? __dadd_rn(r, q) : r;
@@ -623,6 +651,7 @@ __device__ __forceinline__ u64 dbl_to_u52(double r) {
 }
 
 // Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
+template <int COLS>
 __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                          int q_limbs, int L,
                                                          const ModQ *__restrict__ mods,
@@ -634,8 +663,9 @@ __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Ba
   const double2 *T = tw + ((size_t)p << 16);
   const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
   u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
-  const int col = blockIdx.x * 16 + c;
+  using CT = ColTile<COLS>;
+  const int c = CT::col(), g = CT::grp();
+  const int col = blockIdx.x * CT::C + c;
   double x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = (double)in[(g + 16 * k) * 256 + col];
@@ -650,10 +680,10 @@ __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Ba
     }
   }
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(g, 16 * k + c)] = x[k];
+  for (int k = 0; k < 16; k++) sm[CT::at(k, g, c)] = x[k];
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = sm[lds16(j, 16 * g + c)];
+  for (int j = 0; j < 16; j++) x[j] = sm[CT::at(g, j, c)];
 #pragma unroll
   for (int st = 4; st < 8; st++) {
     const int half = 8 >> (st - 4);
@@ -792,6 +822,7 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = dbl_bits(x[k]);
 }
 
+template <int COLS>
 __device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                          int L, const ModQ *__restrict__ mods,
                                                          const double2 *__restrict__ itw,
@@ -802,8 +833,9 @@ __device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Ba
   const double q = (double)mods[p].q, qinv = 1.0 / q;
   const double2 *T = itw + ((size_t)p << 16);
   u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  const int c = threadIdx.x & 15, g = threadIdx.x >> 4;
-  const int col = blockIdx.x * 16 + c;
+  using CT = ColTile<COLS>;
+  const int c = CT::col(), g = CT::grp();
+  const int col = blockIdx.x * CT::C + c;
   double x[16];
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = fp_reduce(as_dbl(io[(16 * g + j) * 256 + col]), qinv, q);
@@ -818,10 +850,10 @@ __device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Ba
     }
   }
 #pragma unroll
-  for (int j = 0; j < 16; j++) sm[lds16(j, 16 * g + c)] = x[j];
+  for (int j = 0; j < 16; j++) sm[CT::at(g, j, c)] = x[j];
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[lds16(g, 16 * k + c)], qinv, q);
+  for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[CT::at(k, g, c)], qinv, q);
 #pragma unroll
   for (int st = 3; st >= 0; st--) {
     const int half = 8 >> st;
@@ -844,17 +876,16 @@ __device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Ba
 // own.  Both bodies share one LDS tile.
 constexpr u64 kFpPrimeBound = (u64)1 << 45;
 
-__global__ __launch_bounds__(TPB) void k_ntt16m_fwd_high(Batch src, Batch dst, int l_begin,
-                                                         int q_limbs, int L,
-                                                         const ModQ *__restrict__ mods,
-                                                         const u64 *__restrict__ psi,
-                                                         const u64 *__restrict__ psi_sh,
-                                                         const double2 *__restrict__ tw) {
-  __shared__ u64 lds[16 * 272];
+template <int COLS>
+__global__ __launch_bounds__(ColTile<COLS>::THREADS) void k_ntt16m_fwd_high(
+    Batch src, Batch dst, int l_begin, int q_limbs, int L, const ModQ *__restrict__ mods,
+    const u64 *__restrict__ psi, const u64 *__restrict__ psi_sh,
+    const double2 *__restrict__ tw) {
+  __shared__ u64 lds[ColTile<COLS>::LDS_WORDS];
   if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
-    k_ntt16f_fwd_high_body(lds, src, dst, l_begin, q_limbs, L, mods, tw);
+    k_ntt16f_fwd_high_body<COLS>(lds, src, dst, l_begin, q_limbs, L, mods, tw);
   else
-    k_ntt16_fwd_high_body(lds, src, dst, l_begin, q_limbs, L, mods, psi, psi_sh);
+    k_ntt16_fwd_high_body<COLS>(lds, src, dst, l_begin, q_limbs, L, mods, psi, psi_sh);
 }
 
 template <bool COMBINE>
@@ -884,18 +915,54 @@ __global__ __launch_bounds__(TPB) void k_ntt16m_inv_low(Batch src, Batch dst, in
     k_ntt16_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh);
 }
 
-__global__ __launch_bounds__(TPB) void k_ntt16m_inv_high(Batch dst, int l_begin, int q_limbs,
-                                                         int L, const ModQ *__restrict__ mods,
-                                                         const u64 *__restrict__ ipsi,
-                                                         const u64 *__restrict__ ipsi_sh,
-                                                         const u64 *__restrict__ ninv,
-                                                         const double2 *__restrict__ itw,
-                                                         const double2 *__restrict__ ninv_fp) {
-  __shared__ u64 lds[16 * 272];
+template <int COLS>
+__global__ __launch_bounds__(ColTile<COLS>::THREADS) void k_ntt16m_inv_high(
+    Batch dst, int l_begin, int q_limbs, int L, const ModQ *__restrict__ mods,
+    const u64 *__restrict__ ipsi, const u64 *__restrict__ ipsi_sh, const u64 *__restrict__ ninv,
+    const double2 *__restrict__ itw, const double2 *__restrict__ ninv_fp) {
+  __shared__ u64 lds[ColTile<COLS>::LDS_WORDS];
   if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
-    k_ntt16f_inv_high_body(lds, dst, l_begin, q_limbs, L, mods, itw, ninv_fp);
+    k_ntt16f_inv_high_body<COLS>(lds, dst, l_begin, q_limbs, L, mods, itw, ninv_fp);
   else
-    k_ntt16_inv_high_body(lds, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh, ninv);
+    k_ntt16_inv_high_body<COLS>(lds, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh, ninv);
+}
+
+// the column passes of a batch: grid (256 / C, items, limbs)
+template <int COLS>
+static void fwd_high16(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                       int l_begin, int l_count, int q_limbs) {
+  hipLaunchKernelGGL(k_ntt16m_fwd_high<COLS>, dim3(256 / COLS, n_items, l_count),
+                     dim3(ColTile<COLS>::THREADS), 0, c->stream, src, dst, l_begin, q_limbs,
+                     c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
+  LAUNCH_CHECK();
+}
+
+template <int COLS>
+static void inv_high16(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
+                       int q_limbs) {
+  hipLaunchKernelGGL(k_ntt16m_inv_high<COLS>, dim3(256 / COLS, n_items, l_count),
+                     dim3(ColTile<COLS>::THREADS), 0, c->stream, dst, l_begin, q_limbs, c->L,
+                     c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
+                     (const double2 *)c->d_itw_fp, (const double2 *)c->d_ninv_fp);
+  LAUNCH_CHECK();
+}
+
+static void launch_fwd_high16(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                              int l_begin, int l_count, int q_limbs) {
+  switch (c->ntt_cols_fwd) {
+    case 64: fwd_high16<64>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
+    case 32: fwd_high16<32>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
+    default: fwd_high16<16>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
+  }
+}
+
+static void launch_inv_high16(ckks_context *c, const Batch &dst, int n_items, int l_begin,
+                              int l_count, int q_limbs) {
+  switch (c->ntt_cols_inv) {
+    case 64: inv_high16<64>(c, dst, n_items, l_begin, l_count, q_limbs); break;
+    case 32: inv_high16<32>(c, dst, n_items, l_begin, l_count, q_limbs); break;
+    default: inv_high16<16>(c, dst, n_items, l_begin, l_count, q_limbs); break;
+  }
 }
 
 // grid (tiles, items, limbs): blocks of one prime run back to back and share
@@ -904,9 +971,7 @@ static void ntt16_dispatch(ckks_context *c, const Batch &src, const Batch &dst, 
                            int l_begin, int l_count, int q_limbs, bool inverse) {
   dim3 block(TPB), grid(16, n_items, l_count);
   if (!inverse) {
-    hipLaunchKernelGGL(k_ntt16m_fwd_high, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                       c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
-    LAUNCH_CHECK();
+    launch_fwd_high16(c, src, dst, n_items, l_begin, l_count, q_limbs);
     hipLaunchKernelGGL(k_ntt16m_fwd_low<false>, grid, block, 0, c->stream, dst, l_begin, q_limbs,
                        c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp,
                        MDCombine{});
@@ -915,10 +980,7 @@ static void ntt16_dispatch(ckks_context *c, const Batch &src, const Batch &dst, 
     hipLaunchKernelGGL(k_ntt16m_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
                        c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh, (const double2 *)c->d_itw_fp);
     LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_ntt16m_inv_high, grid, block, 0, c->stream, dst, l_begin, q_limbs, c->L,
-                       c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
-                       (const double2 *)c->d_itw_fp, (const double2 *)c->d_ninv_fp);
-    LAUNCH_CHECK();
+    launch_inv_high16(c, dst, n_items, l_begin, l_count, q_limbs);
   }
 }
 
@@ -990,9 +1052,7 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   if (post) md.post = *post;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
   dim3 block(TPB), grid(16, 2 * n, limbs);
-  hipLaunchKernelGGL(k_ntt16m_fwd_high, grid, block, 0, c->stream, conv, conv, 0, limbs, c->L,
-                     c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
-  LAUNCH_CHECK();
+  launch_fwd_high16(c, conv, conv, 2 * n, 0, limbs, limbs);
   hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, grid, block, 0, c->stream, conv, 0, limbs, c->L,
                      c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp, md);
   LAUNCH_CHECK();
@@ -1006,10 +1066,7 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
             0.25 * c->N * c->logN * n_items * l_count);
   if (n_items <= 0 || l_count <= 0) return;
   if (c->logN != 16) throw std::invalid_argument("high pass alone: N = 2^16 only");
-  hipLaunchKernelGGL(k_ntt16m_fwd_high, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream,
-                     src, dst, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh,
-                     (const double2 *)c->d_tw_fp);
-  LAUNCH_CHECK();
+  launch_fwd_high16(c, src, dst, n_items, l_begin, l_count, q_limbs);
 }
 
 // ===========================================================================
@@ -1897,6 +1954,116 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   }
 }
 
+// fp64 variant for P primes and dropped primes below 2^45 (the ModDown table
+// has its fp64 part): the v_i as centered exact doubles, every narrow
+// target's sum sum_i v_i hmod_i + sum_j r_j P p_1..p_{j-1} of exact fp64
+// residues reduced once, minus P p_1..p_j for the negative lifts; the
+// dropped primes' values and the lift chain in 64-bit arithmetic; a wide
+// target (q_0) as the 64-bit kernel.  The same words.
+template <int MS>
+__global__ __launch_bounds__(TPB, MS <= 12 ? 5 : 4) void k_bc_down_rescale_fp(
+    Batch src, Batch dst, int logN, int ns, int nd, int D, const u64 *__restrict__ tab,
+    const double2 *__restrict__ ftab, const u64 *__restrict__ rtab,
+    const double2 *__restrict__ frtab, int L, const ModQ *__restrict__ mods) {
+  const u64 *in = batch_ptr(src, blockIdx.y);
+  u64 *out = batch_ptr(dst, blockIdx.y);
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int T = nd - D;
+  const double2 *sf = ftab, *hf = ftab + ns;
+  double vd[MS];
+#pragma unroll
+  for (int i = 0; i < MS; i++) {
+    if (i < ns) {
+      const double q = (double)mods[L + i].q;
+      double v = fp_mulmod(u52_to_dbl(in[((size_t)i << logN) + k]), sf[i].x, sf[i].y, q);
+      v = v < 0.0 ? __dadd_rn(v, q) : v;
+      v = v >= q ? __dsub_rn(v, q) : v;
+      vd[i] = v > __dmul_rn(__dsub_rn(q, 1.0), 0.5) ? __dsub_rn(v, q) : v;
+    }
+  }
+  const u64 *hm = tab + 2 * ns;
+  const u64 *qm = hm + (size_t)ns * nd;
+  const u64 *pm = rtab, *pp = rtab + (size_t)T * D, *pinv = pp + (size_t)T * D;
+  const u64 *chain = pinv + 2 * (size_t)D;
+  // sum_i v_i hmod_i (centered) mod the narrow prime of target t
+  auto conv = [&](int t, double q) {
+    double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+    for (int i = 0; i < MS; i += 2) {
+      if (i < ns) {
+        const double2 h = hf[i * nd + t];
+        a0 = __dadd_rn(a0, fp_mulmod(vd[i], h.x, h.y, q));
+      }
+      if (i + 1 < ns) {
+        const double2 h = hf[(i + 1) * nd + t];
+        a1 = __dadd_rn(a1, fp_mulmod(vd[i + 1], h.x, h.y, q));
+      }
+    }
+    return __dadd_rn(a0, a1);
+  };
+  u64 rv[kMaxRescaleDrop];
+  bool neg[kMaxRescaleDrop];
+#pragma unroll
+  for (int j = 0; j < kMaxRescaleDrop; j++) {
+    if (j < D) {
+      const int tj = nd - 1 - j;
+      const ModQ Mj = mods[tj];
+      const double qj = (double)Mj.q;
+      const u64 y = dbl_to_u52(fp_canon_d(conv(tj, qj), 1.0 / qj, qj));
+      const u64 xq = in[((size_t)(ns + D - 1 - j) << logN) + k];
+      u64 u = shoup_mul(sub_mod(xq, y, Mj.q), pinv[2 * j], pinv[2 * j + 1], Mj.q);
+#pragma unroll
+      for (int m = 0; m < kMaxRescaleDrop; m++) {
+        if (m < j) {
+          const u64 *cm = chain + 3 * ((size_t)j * D + m);
+          u64 rm = barrett(0, rv[m], Mj);
+          if (neg[m]) rm = sub_mod(rm, cm[0], Mj.q);
+          u = shoup_mul(sub_mod(u, rm, Mj.q), cm[1], cm[2], Mj.q);
+        }
+      }
+      rv[j] = u;
+      neg[j] = u > (Mj.q - 1) / 2;
+    }
+  }
+  for (int t = 0; t < T; t++) {
+    const ModQ M = mods[t];
+    if (M.q >= (1ull << 45)) {
+      // wide target: 128-bit Montgomery accumulation of the canonical v
+      u64 hi = 0, lo = 0, cnt = 0;
+#pragma unroll
+      for (int i = 0; i < MS; i++) {
+        if (i < ns) {
+          const double v = vd[i];
+          const u64 vu = v < 0.0 ? dbl_to_u52(__dadd_rn(v, (double)mods[L + i].q)) : dbl_to_u52(v);
+          cnt += v < 0.0 ? 1 : 0;
+          mac_wide(hi, lo, vu, hm[i * nd + t]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxRescaleDrop; j++)
+        if (j < D) mac_wide(hi, lo, rv[j], pm[(size_t)t * D + j]);
+      u64 y = redc(hi, lo, M.q, M.qinv);
+      if (cnt) y = sub_mod(y, mul_mod(cnt, qm[t], M), M.q);
+#pragma unroll
+      for (int j = 0; j < kMaxRescaleDrop; j++)
+        if (j < D && neg[j]) y = sub_mod(y, pp[(size_t)t * D + j], M.q);
+      out[((size_t)t << logN) + k] = y;
+      continue;
+    }
+    const double q = (double)M.q;
+    double a = conv(t, q);
+#pragma unroll
+    for (int j = 0; j < kMaxRescaleDrop; j++) {
+      if (j < D) {
+        const double2 w = frtab[(size_t)t * D + j];
+        a = __dadd_rn(a, fp_mulmod(u52_to_dbl(rv[j]), w.x, w.y, q));
+        if (neg[j]) a = __dsub_rn(a, u52_to_dbl(pp[(size_t)t * D + j]));
+      }
+    }
+    out[((size_t)t << logN) + k] = dbl_to_u52(fp_canon_d(a, 1.0 / q, q));
+  }
+}
+
 void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                             const BCTable &t, int D, const u64 *rtab) {
   KTimer kt(c, "basis_convert_rescale", 8.0 * c->N * n_items * (t.ns + t.nd),
@@ -1904,9 +2071,22 @@ void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst,
   if (D < 1 || D > kMaxRescaleDrop || t.nd <= D || t.ns > kMaxDigitSize)
     throw std::invalid_argument("relinearise-rescale conversion: 1 <= primes < limbs");
   dim3 grid(c->N / TPB, n_items);
-  hipLaunchKernelGGL(t.ns <= 12 ? k_bc_down_rescale<12> : k_bc_down_rescale<kMaxDigitSize>, grid,
-                     dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, D, t.d, rtab, c->L,
-                     c->d_mods);
+  // the fp64 kernel needs the table's fp64 part and the dropped primes below
+  // 2^45 (their values come from the fp64 sums)
+  bool fp = t.fd != nullptr && !t.wide0;
+  for (int j = 0; j < D && fp; j++) fp = c->primes[t.nd - 1 - j] < (1ull << 45);
+  if (fp) {
+    const int T = t.nd - D;
+    const double2 *frtab =
+        (const double2 *)(rtab + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D);
+    hipLaunchKernelGGL(t.ns <= 12 ? k_bc_down_rescale_fp<12> : k_bc_down_rescale_fp<kMaxDigitSize>,
+                       grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, D, t.d,
+                       (const double2 *)t.fd, rtab, frtab, c->L, c->d_mods);
+  } else {
+    hipLaunchKernelGGL(t.ns <= 12 ? k_bc_down_rescale<12> : k_bc_down_rescale<kMaxDigitSize>,
+                       grid, dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, D, t.d, rtab,
+                       c->L, c->d_mods);
+  }
   LAUNCH_CHECK();
 }
 
