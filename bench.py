@@ -256,7 +256,7 @@ def main() -> int:
     if args.mode == "layers-reference-chain":
         print(json.dumps({"fm_layers_reference_chain": measure_fm_layers(
             2 if args.layers is None else args.layers, params=REFERENCE_CHAIN_PARAMS,
-            refresh_normalisers=True)}), flush=True)
+            budget=REFERENCE_BUDGET, refresh_normalisers=True, slim_rmsnorm=True)}), flush=True)
         return 0
     if args.mode == "layer":
         print(json.dumps({"fm_layer": measure_fm_layer(warmup=args.warmup)}), flush=True)
@@ -431,7 +431,8 @@ def main() -> int:
         # dnum 5), whose bootstraps return fewer levels: every softmax
         # round's normaliser is refreshed as well
         result["fm_layers_reference_chain"] = measure_fm_layers(
-            2, params=REFERENCE_CHAIN_PARAMS, refresh_normalisers=True)
+            2, params=REFERENCE_CHAIN_PARAMS, budget=REFERENCE_BUDGET, refresh_normalisers=True,
+            slim_rmsnorm=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
@@ -868,8 +869,14 @@ REFERENCE_CHAIN_PARAMS = dict(log_n=16, depth=37, dnum=5, dcrt_bits=59, first_mo
                               special_bits=60)
 
 
+# the reference's CoeffToSlot / SlotToCoeff level budget (schedule.py
+# bootstrap_level_budget, assets/feature_major.json)
+REFERENCE_BUDGET = (4, 4)
+
+
 def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
-                      budget=(3, 3), refresh_normalisers: bool = False) -> dict:
+                      budget=(3, 3), refresh_normalisers: bool = False,
+                      slim_rmsnorm: bool = False) -> dict:
     """Consecutive Llama-3-8B decoder layers over 128 tokens with their
     refreshes (bootstraps included): per layer, paired batched refreshes of
     the residual stream before each RMSNorm and of the softmax's mapped
@@ -877,7 +884,10 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     CoeffToSlot / SlotToCoeff budget `budget`.  With `refresh_normalisers`
     every softmax round's slim normaliser is bootstrapped too (3 more
     bootstraps per layer), which lets the layer run on a chain whose
-    bootstraps return fewer levels (the reference's).  The first layer
+    bootstraps return fewer levels (the reference's); with `slim_rmsnorm` the
+    post-attention RMSNorm refreshes its slim series (one more bootstrap per
+    layer), which lets the residual refreshes return fewer levels (the
+    reference's budget (4, 4) on its chain).  The first layer
     starts from a one-limb input; from the second on a layer runs in steady
     state.  Weights N(0, 0.02) in a Hadamard-rotated residual basis,
     `weight_sets` distinct sets cycled over the layers; inputs N(0, 1); seed
@@ -888,7 +898,8 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     normaliser_program, refreshed_layer_programs)
+                                     normaliser_program, refreshed_layer_programs,
+                                     rmsnorm_slim_program)
 
     params = REFRESH_PARAMS if params is None else params
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
@@ -901,9 +912,13 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
     prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15, level_budget=budget,
-                                              refresh_normalisers=refresh_normalisers)
+                                              refresh_normalisers=refresh_normalisers,
+                                              slim_rmsnorm=slim_rmsnorm)
     lam_prog = (normaliser_program(ctx, ap, T, log_slots=15, level_budget=budget)
                 if refresh_normalisers else None)
+    rms_prog = (rmsnorm_slim_program(ctx, ap, T, log_slots=15, level_budget=budget,
+                                     refresh_normalisers=refresh_normalisers)
+                if slim_rmsnorm else None)
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
@@ -931,7 +946,8 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     for layer in range(int(n_layers)):
         res = decoder_layer_refreshed_fhe(cur, dev[layer % len(dev)], crypto_context=ctx,
                                           program=prog, residual_program=res_prog,
-                                          normaliser_program=lam_prog)
+                                          normaliser_program=lam_prog,
+                                          rmsnorm_program=rms_prog)
         for c in cur:
             c.release()
         cur = list(res.ciphers)
@@ -966,6 +982,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
                     "over 128 tokens in 16 ciphertexts of 8 lanes, bootstraps included "
                     "(3 paired refreshes = 24 bootstraps per layer"
                     + (", plus 3 softmax normaliser refreshes" if refresh_normalisers else "")
+                    + (", plus 1 slim RMSNorm refresh" if slim_rmsnorm else "")
                     + f"), N=2^16, Q=1x{params['first_mod']}b+{L - 1}x{params['dcrt_bits']}b, "
                     f"dnum={params['dnum']}, P={alpha}x{params['special_bits']}b, CtS/StC budget "
                     f"{tuple(budget)}; bootstraps return {prog.output_limbs} limbs (scores) "

@@ -607,6 +607,26 @@ __device__ __forceinline__ double fp_mulmod(double a, double w, double wq, doubl
   return __dadd_rn(__fma_rn(-t, q, hi), lo);
 }
 
+__device__ __forceinline__ double as_dbl(u64 v) { return __longlong_as_double((long long)v); }
+__device__ __forceinline__ u64 dbl_bits(double v) { return (u64)__double_as_longlong(v); }
+
+// exact conversions of integers in [0, 2^52): the word is the mantissa of
+// 2^52 + x
+constexpr u64 kTwo52Bits = 0x4330000000000000ull;
+__device__ __forceinline__ double u52_to_dbl(u64 x) {
+  return __dsub_rn(as_dbl(x | kTwo52Bits), 4503599627370496.0);
+}
+__device__ __forceinline__ u64 dbl_to_u52(double r) {
+  return dbl_bits(__dadd_rn(r, 4503599627370496.0)) - kTwo52Bits;
+}
+
+// exact conversion of an integer |x| < 2^51 to a signed word: 1.5 2^52 + x
+// keeps the exponent of 1.5 2^52, so its word differs from that of 1.5 2^52
+// by x
+__device__ __forceinline__ long long dbl_to_i51(double x) {
+  return (long long)(dbl_bits(__dadd_rn(x, FP_ROUND_C)) - 0x4338000000000000ull);
+}
+
 // x -> x - round(x / q) q in [-q/2 - 1, q/2 + 1]
 __device__ __forceinline__ double fp_reduce(double x, double qinv, double q) {
   return __fma_rn(-fp_rint(__dmul_rn(x, qinv)), q, x);
@@ -621,7 +641,7 @@ __device__ __forceinline__ double fp_canon_d(double x, double qinv, double q) {
 __device__ __forceinline__ u64 fp_canon(double x, double qinv, double q) {
   double r = fp_reduce(x, qinv, q);
   r = r < 0.0 ? __dadd_rn(r, q) : r;
-  return (u64)r;
+  return dbl_to_u52(r);
 }
 
 __device__ __forceinline__ void ct_fp(double &X, double &Y, double w, double wq, double q) {
@@ -637,18 +657,6 @@ __device__ __forceinline__ void gs_fp(double &X, double &Y, double w, double wq,
   Y = fp_mulmod(__dsub_rn(x, y), w, wq, q);
 }
 
-__device__ __forceinline__ double as_dbl(u64 v) { return __longlong_as_double((long long)v); }
-__device__ __forceinline__ u64 dbl_bits(double v) { return (u64)__double_as_longlong(v); }
-
-// exact conversions of integers in [0, 2^52): the word is the mantissa of
-// 2^52 + x
-constexpr u64 kTwo52Bits = 0x4330000000000000ull;
-__device__ __forceinline__ double u52_to_dbl(u64 x) {
-  return __dsub_rn(as_dbl(x | kTwo52Bits), 4503599627370496.0);
-}
-__device__ __forceinline__ u64 dbl_to_u52(double r) {
-  return dbl_bits(__dadd_rn(r, 4503599627370496.0)) - kTwo52Bits;
-}
 
 // Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
 template <int COLS>
@@ -668,7 +676,7 @@ __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Ba
   const int col = blockIdx.x * CT::C + c;
   double x[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = (double)in[(g + 16 * k) * 256 + col];
+  for (int k = 0; k < 16; k++) x[k] = u52_to_dbl(in[(g + 16 * k) * 256 + col]);
 #pragma unroll
   for (int st = 0; st < 4; st++) {
     const int half = 8 >> st;
@@ -787,7 +795,7 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   const int row = blockIdx.x * 16 + rl;
   double x[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = (double)in[rl * 256 + c0 + 16 * k];
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
@@ -1256,7 +1264,7 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
 // (tile, limb) share b % 8, i.e. run on one XCD (blocks go to the 8 XCDs
 // round robin) and read the tile's key words into one L2.
 template <bool FP>
-__global__ __launch_bounds__(TPB, FP ? 3 : 2) void k_ntt16_low_key(LowKeyArgs a, int l_begin,
+__global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_begin,
                                                                    int n_items,
                                                                    const ModQ *__restrict__ mods,
                                                                    const u64 *__restrict__ psi,
@@ -1567,7 +1575,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
   for (int i = 0; i < MS; i++) {
     if (i < ns && !(wide0 && i == 0)) {
       const double q = (double)mods[src_prime0 + i].q;
-      double v = fp_mulmod((double)in[((size_t)i << logN) + k], sf[i].x, sf[i].y, q);
+      double v = fp_mulmod(u52_to_dbl(in[((size_t)i << logN) + k]), sf[i].x, sf[i].y, q);
       v = v < 0.0 ? __dadd_rn(v, q) : v;
       v = v >= q ? __dsub_rn(v, q) : v;
       if (centered && v > __dmul_rn(__dsub_rn(q, 1.0), 0.5)) v = __dsub_rn(v, q);
@@ -1588,7 +1596,7 @@ __global__ __launch_bounds__(TPB, 5) void k_basis_convert_fp(
     for (int i = 0; i < MS; i++) {
       if (i < ns) {
         const double v = vd[i];
-        const u64 vu = v < 0.0 ? (u64)__dadd_rn(v, (double)mods[src_prime0 + i].q) : (u64)v;
+        const u64 vu = dbl_to_u52(v < 0.0 ? __dadd_rn(v, (double)mods[src_prime0 + i].q) : v);
         cnt += v < 0.0 ? 1 : 0;
         mac_wide(hi, lo, vu, hm[i * nd + t]);
       }
@@ -1784,7 +1792,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
           // q > 2^45 > |hi|, |lo|: one correction each, then the 64-bit product
 #pragma unroll
           for (int r = 0; r < R; r++) {
-            const long long hv = (long long)hi[r][e], lv = (long long)lo[r][e];
+            const long long hv = dbl_to_i51(hi[r][e]), lv = dbl_to_i51(lo[r][e]);
             const u64 h = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
             const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
             o[16 * r] = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
@@ -2596,11 +2604,11 @@ __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict_
         double x[IC];
 #pragma unroll
         for (int c = 0; c < IC; c++)
-          x[c] = i0 + c < n ? (double)bab[(size_t)(i0 + c) * B + b][off] : 0.0;
+          x[c] = i0 + c < n ? u52_to_dbl(bab[(size_t)(i0 + c) * B + b][off]) : 0.0;
 #pragma unroll
         for (int g = 0; g < kTabGroups; g++) {
           if (g < G) {
-            const double w = (double)pts[(size_t)g * B + b][poff];
+            const double w = u52_to_dbl(pts[(size_t)g * B + b][poff]);
             const double wq = __dmul_rn(w, qinv);
 #pragma unroll
             for (int c = 0; c < IC; c++)

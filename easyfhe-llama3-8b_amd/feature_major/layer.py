@@ -36,7 +36,8 @@ from .complex import pair_real_ciphers, split_complex_ciphers_twice
 from .layout import FeatureMajorPrefillLayout
 from .linear import LinearOperator, LinearOperatorConfig, LinearWeight, linear_rotations
 from .mlp import FeatureMajorMLPLayout, MLPWeights, mlp_depth, mlp_fhe
-from .rmsnorm import residual_add, rmsnorm_depth, rmsnorm_fhe, rmsnorm_rotations
+from .rmsnorm import (SlimRefresh, refresh_slim, residual_add, rmsnorm_depth, rmsnorm_fhe,
+                      rmsnorm_rotations, rmsnorm_slim_refresh_depths)
 from .rope import rope_fhe, rope_rotations
 
 
@@ -294,14 +295,21 @@ def _drop_owned(cts, limbs: int, ctx) -> list:
 
 def refreshed_layer_depths(approx: LayerApproximations, seq_len: int, *,
                            refresh_normalisers: bool = False,
-                           input_limbs: int = 1) -> tuple[int, int, int]:
+                           input_limbs: int = 1,
+                           slim_rmsnorm: bool = False) -> tuple[int, int, int]:
     """Levels of the three blocks between refreshes: RMSNorm + Q/K/V + RoPE +
     QK; the scores' landing + softmax + PV + W_o; RMSNorm + MLP.  With
     ``refresh_normalisers`` every softmax round's slim normaliser is
     bootstrapped (the reference's per-round lambda refresh,
     operators/attention/softmax.py:1044-1095), so the score block needs the
     main stream's levels or the slim normalisers' need, whichever is larger.
-    ``input_limbs`` is what a bootstrap input needs (``bs.input_limbs``)."""
+    With ``slim_rmsnorm`` the post-attention RMSNorm's slim series is
+    refreshed (operators/norm/rmsnorm.py:517-566, schedule.py
+    ``adaptive_rmsnorm_slim_refresh``; the input RMSNorm keeps its depth, as
+    in the reference), so the last block needs the MLP's levels plus the
+    product's, or the slim path's, whichever is larger.  ``input_limbs`` is
+    what a bootstrap input needs (``bs.input_limbs``).  A block's input holds
+    its levels plus two limbs."""
     from .attention import softmax_depth_refreshed
 
     a = rmsnorm_depth(approx.input_norm) + 1 + 1 + 4
@@ -311,7 +319,11 @@ def refreshed_layer_depths(approx: LayerApproximations, seq_len: int, *,
         b = max(1 + main + 3 + 1, need)
     else:
         b = 1 + softmax_depth(approx.softmax, seq_len) + 3 + 1
-    c = rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu)
+    if slim_rmsnorm:
+        lost, need = rmsnorm_slim_refresh_depths(approx.post_attention_norm, input_limbs)
+        c = max(lost + mlp_depth(approx.silu), need - 2)
+    else:
+        c = rmsnorm_depth(approx.post_attention_norm) + mlp_depth(approx.silu)
     return a, b, c
 
 
@@ -341,32 +353,33 @@ _NORMALISER_BOUND = 256.0
 
 
 def _refresh_normaliser(ct, ctx, program):
-    """One slim normaliser refreshed: scaled into the bootstrap's input range
-    through the recorded scale (no level), bootstrapped, then multiplied by
-    the bound as an integer (no level).  The result keeps the program's
-    output scale: dividing the recorded scale instead would leave the
-    normaliser 2^8 below it, and every round's product with it would carry
-    that loss into the next round's squares."""
+    """One slim normaliser refreshed (``rmsnorm.refresh_slim``): the result
+    keeps the program's output scale, because dividing the recorded scale
+    instead would leave the normaliser 2^8 below it, and every round's
+    product with it would carry that loss into the next round's squares."""
+    return refresh_slim(ct, ctx, program, _NORMALISER_BOUND)
+
+
+def rmsnorm_slim_program(crypto_context, approx: LayerApproximations, seq_len: int, *,
+                         log_slots: int, level_budget=(3, 3), refresh_normalisers: bool = False):
+    """Bootstrap program for the post-attention RMSNorm's slim refresh: its
+    output sits one level above the block's input (``refreshed_layer_depths``
+    with ``slim_rmsnorm``: c + 2 limbs), where the extraction lands the
+    broadcast on the stream's level."""
     from easyfhe.bs import openfhe as bs
 
-    v = ct.deep_copy()
-    v.set_scale(float(ct.state.scaling_factor) * _NORMALISER_BOUND, 1)
-    try:
-        out = bs.bootstrap(v, ctx, program)
-    finally:
-        v.release()
-    k = fhe.encode_scalar(int(_NORMALISER_BOUND), int(out.state.cur_limbs), scale_degree=0,
-                          mode="integer", context=ctx)
-    try:
-        return fhe.homo_mul_scalar(out, k, ctx)
-    finally:
-        out.release()
-        k.release()
+    ctx = _ctx(crypto_context)
+    lim = bs.input_limbs(ctx)
+    _, _, c = refreshed_layer_depths(approx, seq_len, refresh_normalisers=refresh_normalisers,
+                                     input_limbs=lim, slim_rmsnorm=True)
+    return bs.generate(ctx, bs.BootstrapSpec(log_slots=int(log_slots),
+                                             level_budget=tuple(level_budget),
+                                             output_levels=int(c + 2)))
 
 
 def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_len: int, *,
                              log_slots: int, level_budget=(3, 3),
-                             refresh_normalisers: bool = False):
+                             refresh_normalisers: bool = False, slim_rmsnorm: bool = False):
     """(score program, residual program): bootstrap programs whose outputs
     hold the score block plus one limb, and the deeper of the two residual
     blocks plus two (``refreshed_layer_depths``).  A bootstrap raises its
@@ -379,7 +392,7 @@ def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_le
     # or two on chains whose one-limb scale is near q_0 (bs.input_limbs)
     lim = bs.input_limbs(ctx)
     a, b, c = refreshed_layer_depths(approx, seq_len, refresh_normalisers=refresh_normalisers,
-                                     input_limbs=lim)
+                                     input_limbs=lim, slim_rmsnorm=slim_rmsnorm)
     spec = lambda levels: bs.BootstrapSpec(log_slots=int(log_slots),  # noqa: E731
                                            level_budget=tuple(level_budget),
                                            output_levels=int(levels))
@@ -395,7 +408,7 @@ def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_le
 def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
                                 program, residual_program=None, residual_bound: float = 32.0,
                                 group: int = 8, rope_theta: float = 500000.0,
-                                normaliser_program=None) -> LayerResult:
+                                normaliser_program=None, rmsnorm_program=None) -> LayerResult:
     """One decoder layer with its refreshes (three paired refresh points: the
     residual stream before each RMSNorm, and the softmax's mapped scores;
     the reference refreshes at the same places, graph.py:780-990,
@@ -407,15 +420,19 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
     both).  With ``normaliser_program`` (``normaliser_program()``) every
     softmax round's slim normaliser is refreshed as well, which shortens
     the score block (``refreshed_layer_programs(refresh_normalisers=True)``
-    sizes the programs for it).  The input may sit at any level; it is not
-    consumed."""
+    sizes the programs for it).  With ``rmsnorm_program``
+    (``rmsnorm_slim_program()``) the post-attention RMSNorm refreshes its
+    slim series instead of spending the stream's levels on it, which
+    shortens the last block (``refreshed_layer_programs(slim_rmsnorm=True)``).
+    The input may sit at any level; it is not consumed."""
     from easyfhe.bs import openfhe as bs
 
     ctx = _ctx(crypto_context)
     lay, geo, ap = weights.layout, weights.geometry, weights.approx
     a_depth, b_depth, c_depth = refreshed_layer_depths(
         ap, geo.seq_len, refresh_normalisers=normaliser_program is not None,
-        input_limbs=bs.input_limbs(ctx))
+        input_limbs=bs.input_limbs(ctx), slim_rmsnorm=rmsnorm_program is not None)
+    slim = None if rmsnorm_program is None else SlimRefresh(rmsnorm_program)
     refresh_lam = (None if normaliser_program is None
                    else (lambda ct: _refresh_normaliser(ct, ctx, normaliser_program)))
     res_prog = program if residual_program is None else residual_program
@@ -495,7 +512,7 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         stage["refresh_residual_2"] = time.perf_counter() - t0
         t0 = time.perf_counter()
         n2 = rmsnorm_fhe(hr, np.zeros(1), coeffs=ap.post_attention_norm, layout=lay,
-                         crypto_context=ctx)
+                         crypto_context=ctx, slim_refresh=slim)
         m = mlp_fhe(n2.ciphers, weights.mlp, silu=ap.silu, crypto_context=ctx, operator=op)
         n2.release()
         out = residual_add(hr, m.ciphers, crypto_context=ctx)
@@ -512,4 +529,4 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
 __all__ = ["DecoderLayerWeights", "LayerApproximations", "LayerResult", "decoder_layer_depth",
            "decoder_layer_fhe", "decoder_layer_refreshed_fhe", "decoder_layer_rotations",
            "normaliser_program", "refresh_stream", "refreshed_layer_depths",
-           "refreshed_layer_programs"]
+           "refreshed_layer_programs", "rmsnorm_slim_program"]

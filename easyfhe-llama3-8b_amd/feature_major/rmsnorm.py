@@ -21,6 +21,13 @@ Depth: square, pack mask, the series, extract mask, product.  An input that
 arrives as ``s * x`` (the doubled values of a complex-paired refresh) is
 normalised to ``x`` through the masks at no level (``input_value_scale``).
 
+With a ``SlimRefresh`` (the reference's adaptive slim refresh,
+operators/norm/rmsnorm.py:517-566) the series' output is bootstrapped when it
+sits too low for the product to keep the input's level: one bootstrap of one
+ciphertext for all 128 tokens, after which the norm costs the stream only the
+product's level, and the slim path needs its own levels (square, pack, series
+and a bootstrap input) instead of the stream's.
+
 Every step over the 16 ciphertexts is batched: a tree step is one key switch
 call whose key is read once for the batch.
 """
@@ -71,6 +78,58 @@ def rmsnorm_depth(coeffs: dict, *, apply_gamma: bool = False) -> int:
     levels, so it does not add to this count)."""
     _ = apply_gamma
     return 4 + int(chebyshev_depth(coeffs["coefficients"]))
+
+
+def rmsnorm_slim_refresh_depths(coeffs: dict, input_limbs: int) -> tuple[int, int]:
+    """(levels the stream loses, limbs the input needs) of RMSNorm with its
+    slim refresh: the stream loses the product's level only; the slim path
+    spends the square, the pack mask and the series below the input and must
+    still hold a bootstrap input (``input_limbs``)."""
+    return 1, 2 + int(chebyshev_depth(coeffs["coefficients"])) + int(input_limbs)
+
+
+@dataclass(frozen=True)
+class SlimRefresh:
+    """Refresh of RMSNorm's slim inverse-square-root ciphertext (reference
+    operators/norm/rmsnorm.py:517-566, ``adaptive_rmsnorm_slim_refresh`` of
+    schedule.py): when the series leaves it below the level at which the
+    extraction lands on the stream's level, ``program`` (a full-slot
+    bootstrap program returning at least that level) refreshes it, and the
+    result is dropped to exactly that level.  ``value_bound`` bounds the
+    series' values on [-1, 1] (the refresh divides by the power of two above
+    it)."""
+
+    program: object
+    value_bound: float = 2.0
+
+
+def refresh_slim(ct, crypto_context, program, bound: float):
+    """One slim ciphertext refreshed: divided by the power of two S >= bound
+    through the recorded scale (no level) so that its values fit the
+    bootstrap's input range, bootstrapped, then multiplied by S as an integer
+    (no level), so the result keeps the program's output scale.  ``ct`` is
+    not consumed."""
+    from easyfhe.bs import openfhe as bs
+
+    ctx = _ctx(crypto_context)
+    if not float(bound) > 0.0:
+        raise ValueError("the value bound must be positive.")
+    S = int(2 ** max(0, int(math.ceil(math.log2(float(bound))))))
+    v = ct.deep_copy()
+    v.set_scale(float(ct.state.scaling_factor) * S, 1)
+    try:
+        out = bs.bootstrap(v, ctx, program)
+    finally:
+        v.release()
+    if S == 1:
+        return out
+    k = fhe.encode_scalar(S, int(out.state.cur_limbs), scale_degree=0, mode="integer",
+                          context=ctx)
+    try:
+        return fhe.homo_mul_scalar(out, k, ctx)
+    finally:
+        out.release()
+        k.release()
 
 
 @dataclass
@@ -141,9 +200,12 @@ def _align_all(cts, limbs: int, ctx) -> list:
 
 def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPrefillLayout,
                 crypto_context, input_value_scale: float = 1.0,
-                defer_output_scale: bool = False) -> RMSNormResult:
+                defer_output_scale: bool = False,
+                slim_refresh: SlimRefresh | None = None) -> RMSNormResult:
     """``x * p(mean(x^2)) [* gamma]`` per token on feature-major ciphertexts
-    (rmsnorm.py:353-704).  Inputs are not consumed."""
+    (rmsnorm.py:353-704).  With ``slim_refresh`` the series' output is
+    refreshed when it would pull the stream down (rmsnorm.py:517-566).
+    Inputs are not consumed."""
     ctx = _ctx(crypto_context)
     xs = tuple(input_ciphers)
     if len(xs) != int(layout.cipher_count):
@@ -166,8 +228,16 @@ def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPref
     alpha, beta = chebyshev_map(coeffs["fit_interval"])
     depth = rmsnorm_depth(coeffs)
     limbs_in = int(xs[0].state.cur_limbs)
-    if limbs_in < depth + 2:
-        raise ValueError(f"RMSNorm needs {depth + 2} limbs, inputs have {limbs_in}.")
+    if slim_refresh is None:
+        if limbs_in < depth + 2:
+            raise ValueError(f"RMSNorm needs {depth + 2} limbs, inputs have {limbs_in}.")
+    else:
+        from easyfhe.bs import openfhe as bs
+
+        _, need = rmsnorm_slim_refresh_depths(coeffs, bs.input_limbs(ctx))
+        if limbs_in < need:
+            raise ValueError(f"RMSNorm with its slim refresh needs {need} limbs, inputs have "
+                             f"{limbs_in}.")
     D = int(layout.hidden_dim)
     lanes = int(layout.tokens_per_cipher)
     steps = int(math.log2(D))
@@ -197,9 +267,22 @@ def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPref
 
         t0 = time.perf_counter()
         limbs = int(slim.state.cur_limbs)
-        off = fhe.encode_scalar(beta, limbs, scaling_factor=float(slim.state.scaling_factor),
-                                context=ctx)
-        mapped = fhe.homo_add_scalar(slim, off, ctx)
+        if slim_refresh is None:
+            off = fhe.encode_scalar(beta, limbs, scaling_factor=float(slim.state.scaling_factor),
+                                    context=ctx)
+            mapped = fhe.homo_add_scalar(slim, off, ctx)
+        else:
+            # the map's offset on the token slots only: the others stay at 0,
+            # inside the series' interval, so the refresh sees only values in
+            # its range (beta alone maps them just outside [-1, 1], where the
+            # series grows fast; the reference adds it on the active slots,
+            # rmsnorm.py:493-507)
+            active = _row_masks(layout, 1.0).sum(axis=0) > 0.0
+            off = fhe.encode_rows_cached(ctx, np.where(active, beta, 0.0)[None, :], limbs=limbs,
+                                         scale=float(slim.state.scaling_factor),
+                                         slots=ctx.max_slots)[0]
+            mapped = fhe.homo_add_pt(slim, off, ctx)
+        off.release()
         slim.release()
         poly = eval_chebyshev_series_cipher(mapped, coefficients, lower_bound=-1.0,
                                             upper_bound=1.0, crypto_context=ctx,
@@ -207,6 +290,27 @@ def rmsnorm_fhe(input_ciphers, weight, *, coeffs: dict, layout: FeatureMajorPref
         mapped.release()
         sync()
         stage["rsqrt_polynomial"] = time.perf_counter() - t0
+        if slim_refresh is not None:
+            # the extraction lands one level below the series' output: that
+            # must be the level of the stream the product takes (the input,
+            # or one below once gamma is applied)
+            want = limbs_in - (1 if apply_gamma else 0) + 1
+            if int(poly.state.cur_limbs) < want:
+                t0 = time.perf_counter()
+                fresh = refresh_slim(poly, ctx, slim_refresh.program, slim_refresh.value_bound)
+                poly.release()
+                poly = fresh
+                if int(poly.state.cur_limbs) < want:
+                    raise ValueError(f"the slim refresh program returns "
+                                     f"{int(poly.state.cur_limbs)} limbs; RMSNorm needs {want}.")
+                if int(poly.state.cur_limbs) > want:
+                    dropped = fhe.align_to(poly, poly.state.replace(cur_limbs=want,
+                                                                    scaling_factor=None), ctx)
+                    if dropped is not poly:
+                        poly.release()
+                    poly = dropped
+                sync()
+                stage["rsqrt_slim_bootstrap"] = time.perf_counter() - t0
 
         t0 = time.perf_counter()
         n = len(xs)
@@ -296,5 +400,6 @@ def residual_add(left, right, *, crypto_context) -> tuple:
     return tuple(out)
 
 
-__all__ = ["RMSNormResult", "is_rmsn_weight", "match_scale", "residual_add", "rmsnorm_depth",
-           "rmsnorm_fhe", "rmsnorm_rotations"]
+__all__ = ["RMSNormResult", "SlimRefresh", "is_rmsn_weight", "match_scale", "refresh_slim",
+           "residual_add", "rmsnorm_depth", "rmsnorm_fhe", "rmsnorm_rotations",
+           "rmsnorm_slim_refresh_depths"]

@@ -4,8 +4,8 @@ with the fp64 layer model (oracle/layer_numpy.py):
 * complex pairing and the conjugation split (operators/linear/complex.py);
 * RMSNorm with the slim-packed single series evaluation
   (operators/norm/rmsnorm.py), with and without gamma, with a doubled input
-  (the complex-paired refresh contract), and at the full Llama shape
-  (128 tokens x 4096 features at N = 2^16).
+  (the complex-paired refresh contract), with its slim refresh, and at the
+  full Llama shape (128 tokens x 4096 features at N = 2^16).
 
 Tolerances are stated per test: they bound the CKKS error (scale 2^40) and
 the drift of the fixed-scale residual bookkeeping, not the series fits,
@@ -23,6 +23,8 @@ from conftest import PARAMS, device_context
 pytestmark = pytest.mark.gpu
 
 FM_SMALL = dict(log_n=13, depth=13, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
+# deep enough for a bootstrap beside a layer's blocks
+FM_REFRESH = dict(log_n=13, depth=57, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
 
 
 def _stream(client, ctx, x, enc0=700):
@@ -118,6 +120,56 @@ def test_rmsnorm_full_llama_shape():
     err = float(np.max(np.abs(got - want)))
     print(f"rmsnorm 128x4096: max err {err:.3g}, {res.wall_seconds:.3f} s, "
           f"stages {res.stage_seconds}", flush=True)
+    assert err < 2e-4, err
+
+
+@pytest.mark.parametrize("gamma", [False, True])
+def test_rmsnorm_slim_refresh_keeps_the_stream_level(gamma):
+    """RMSNorm whose slim series is bootstrapped (the reference's adaptive
+    slim refresh, operators/norm/rmsnorm.py:517-566): from the fewest limbs
+    the slim path allows, the output loses only the product's level (two with
+    gamma), against the fp64 model of the same series; without the refresh
+    the same input is too shallow.  64 tokens x 512 features at N = 2^13;
+    the tolerance covers one bootstrap (~20 bits) of values below 2."""
+    from easyfhe.bs import openfhe as bs
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry
+    from feature_major.rmsnorm import (SlimRefresh, rmsnorm_depth, rmsnorm_fhe,
+                                       rmsnorm_rotations, rmsnorm_slim_refresh_depths)
+
+    tokens, dim = 64, 512
+    lay0 = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=4096)
+    client, ctx = device_context(FM_REFRESH, rotations=rmsnorm_rotations(lay0))
+    rng = np.random.default_rng(21)
+    x = rng.normal(size=(tokens, dim))
+    w = rng.normal(1.0, 0.1, dim) if gamma else np.zeros(1)
+    entry = rsqrt_entry(0.25, 4.0, 31)
+    lost, need = rmsnorm_slim_refresh_depths(entry, bs.input_limbs(ctx))
+    assert lost == 1 and need < rmsnorm_depth(entry) + 2
+    lay = FeatureMajorPrefillLayout(seq_len=tokens, hidden_dim=dim, slots=ctx.max_slots)
+    packed = lay.pack(x)
+    cts = [client.encrypt(packed[i], cur_limbs=need, enc_id=900 + i)
+           for i in range(lay.cipher_count)]
+    # the series' output is refreshed to one limb above the stream the
+    # product takes (the input, or one below it with gamma)
+    out_levels = need - (1 if gamma else 0)
+    prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=12, level_budget=(3, 3),
+                                             output_levels=out_levels))
+    with pytest.raises(ValueError):
+        rmsnorm_fhe(cts, w, coeffs=entry, layout=lay, crypto_context=ctx)
+    res = rmsnorm_fhe(cts, w, coeffs=entry, layout=lay, crypto_context=ctx,
+                      slim_refresh=SlimRefresh(prog))
+    assert res.output_limbs == need - 1 - (1 if gamma else 0)
+    assert "rsqrt_slim_bootstrap" in res.stage_seconds
+    got = _decrypt_stream(client, lay, res.ciphers)
+    want = LN.rmsnorm_poly_numpy(x, entry["coefficients"], entry["fit_interval"])
+    if gamma:
+        want = want * w[None, :]
+    err = float(np.max(np.abs(got - want)))
+    print(f"rmsnorm with slim refresh: {need} -> {res.output_limbs} limbs, max err {err:.3g}",
+          flush=True)
+    res.release()
+    prog.release()
     assert err < 2e-4, err
 
 
@@ -328,9 +380,6 @@ def test_decoder_layer_matches_poly_model():
           f"|out| {np.abs(model).max():.3g}, limbs 64 -> {res.output_limbs}, "
           f"{res.wall_seconds:.2f} s", flush=True)
     assert err < 1e-4, err
-
-
-FM_REFRESH = dict(log_n=13, depth=57, dnum=4, dcrt_bits=40, first_mod=60, special_bits=60)
 
 
 def test_refreshed_decoder_layer_matches_poly_model():

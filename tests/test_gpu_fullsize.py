@@ -80,7 +80,7 @@ def test_sparse_bootstrap_128_slots_full_size(capsys):
 LAYER_TOL = 3e-4
 
 
-def _refreshed_layer(params, refresh_normalisers: bool):
+def _refreshed_layer(params, refresh_normalisers: bool, budget=(3, 3), slim_rmsnorm=False):
     """One refreshed full-size layer on the chain `params`; (decrypted output,
     input, weights, approximations, wall seconds, output limbs)."""
     import bench
@@ -91,7 +91,8 @@ def _refreshed_layer(params, refresh_normalisers: bool):
     from feature_major.attention import SoftmaxConfig
     from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
                                      decoder_layer_refreshed_fhe, decoder_layer_rotations,
-                                     normaliser_program, refreshed_layer_programs)
+                                     normaliser_program, refreshed_layer_programs,
+                                     rmsnorm_slim_program)
 
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     norm = rsqrt_entry(0.5, 16.0, 63)
@@ -100,9 +101,14 @@ def _refreshed_layer(params, refresh_normalisers: bool):
                                            first_inverse_degree=31, inverse_degree=47))
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
     client, ctx = device_context(params, rotations=decoder_layer_rotations(lay, H, hd))
-    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15,
-                                              refresh_normalisers=refresh_normalisers)
-    lam = normaliser_program(ctx, ap, T, log_slots=15) if refresh_normalisers else None
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=15, level_budget=budget,
+                                              refresh_normalisers=refresh_normalisers,
+                                              slim_rmsnorm=slim_rmsnorm)
+    lam = (normaliser_program(ctx, ap, T, log_slots=15, level_budget=budget)
+           if refresh_normalisers else None)
+    rms = (rmsnorm_slim_program(ctx, ap, T, log_slots=15, level_budget=budget,
+                                refresh_normalisers=refresh_normalisers)
+           if slim_rmsnorm else None)
     rng = np.random.default_rng(0)
     w = bench._layer_weights(rng, D, KV, hd, I, bench.randomized_hadamard(D, 1))
     x = rng.normal(0, 1, (T, D))
@@ -113,11 +119,12 @@ def _refreshed_layer(params, refresh_normalisers: bool):
                              heads=H, kv_heads=KV, head_dim=hd, intermediate=I, approx=ap,
                              layout=lay, context=ctx) as dw:
         res = decoder_layer_refreshed_fhe(xc, dw, crypto_context=ctx, program=prog,
-                                          residual_program=res_prog, normaliser_program=lam)
+                                          residual_program=res_prog, normaliser_program=lam,
+                                          rmsnorm_program=rms)
     got = LN.fm_unpack(np.stack([client.decrypt(o) for o in res.ciphers]), T, D)
     wall, limbs_out = res.wall_seconds, res.output_limbs
     res.release()
-    for p_ in (prog, res_prog, lam):
+    for p_ in (prog, res_prog, lam, rms):
         if p_ is not None:
             p_.release()
     ctx.close()
@@ -166,13 +173,15 @@ LAYER_TOL_REFERENCE_CHAIN = 2e-3
 @pytest.mark.timeout(400)
 def test_refreshed_layer_reference_chain(capsys):
     """The same layer on the reference's chain (60 + 37 x 59-bit primes,
-    dnum 5, 8 special primes of 60 bits), whose bootstraps return at most 21
-    levels: every softmax round's normaliser is refreshed too, and every
-    refresh takes its input at two limbs (the one-limb scale 2^59 is above
-    q_0 2^-10)."""
+    dnum 5, 8 special primes of 60 bits) at the reference's level budget
+    (4, 4), whose bootstraps return at most 19 levels: every softmax round's
+    normaliser is refreshed too, the post-attention RMSNorm refreshes its
+    slim series, and every refresh takes its input at two limbs (the one-limb
+    scale 2^59 is above q_0 2^-10)."""
     import bench
 
-    got, x, w, ap, wall, limbs_out = _refreshed_layer(bench.REFERENCE_CHAIN_PARAMS, True)
+    got, x, w, ap, wall, limbs_out = _refreshed_layer(
+        bench.REFERENCE_CHAIN_PARAMS, True, budget=bench.REFERENCE_BUDGET, slim_rmsnorm=True)
     model, exact = _layer_models(x, w, ap)
     err = float(np.abs(got - model).max())
     with capsys.disabled():

@@ -69,6 +69,37 @@ def test_approximations_cover_the_ranges():
         approximations_for(LayerRanges((1, 2), (1, 2), 1.0, 1.0, 19.0, -1.0))
 
 
+def test_slim_rmsnorm_refresh_shortens_the_last_block():
+    """With the post-attention RMSNorm's slim refresh, the last block is the
+    smallest depth at which both paths fit: the stream (one level for the
+    norm's product, then the MLP, leaving the two limbs the next refresh
+    takes) and the slim path (square, pack mask and series below the
+    block's input, then a bootstrap input).  The other blocks are unchanged."""
+    from easyfhe.chebyshev import chebyshev_depth
+    from feature_major.layer import refreshed_layer_depths
+    from feature_major.mlp import mlp_depth
+
+    for r in (LayerRanges((0.9, 1.2), (3.0, 5.0), 40.0, 6.5, 9.03, -8.0),
+              LayerRanges((1e-4, 5e-4), (1.0, 4.0), 8.0, 6.0, 4.0, -4.0)):
+        ap, _ = approximations_for(r)
+        d = chebyshev_depth(ap.post_attention_norm["coefficients"])
+        for lim in (1, 2):
+            for rn in (False, True):
+                a0, b0, c0 = refreshed_layer_depths(ap, 128, refresh_normalisers=rn,
+                                                    input_limbs=lim)
+                a, b, c = refreshed_layer_depths(ap, 128, refresh_normalisers=rn,
+                                                 input_limbs=lim, slim_rmsnorm=True)
+                assert (a, b) == (a0, b0) and c < c0
+
+                def fits(depth):
+                    block_in = depth + 2
+                    stream_ok = block_in - 1 - mlp_depth(ap.silu) >= 2
+                    slim_ok = block_in - 2 - d >= lim
+                    return stream_ok and slim_ok
+
+                assert fits(c) and not fits(c - 1)
+
+
 def test_refreshed_blocks_partition_the_layer_depth():
     """The three blocks between refreshes use, together, exactly the levels
     of the refresh-free layer, for the prefill's default series."""
