@@ -797,6 +797,11 @@ static void free_context(ckks_context *c) {
   (void)hipFree(c->d_ninv_fp);
   (void)hipFree(c->d_rinv_fp);
   c->pool.trim();
+  if (c->fork_ev) (void)hipEventDestroy(c->fork_ev);
+  for (int i = 0; i < ckks_context::kMaxSplit - 1; i++) {
+    if (c->join_ev[i]) (void)hipEventDestroy(c->join_ev[i]);
+    if (c->aux[i]) (void)hipStreamDestroy(c->aux[i]);
+  }
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -1140,6 +1145,49 @@ static void gen_key(ckks_context *c, u64 id, int relin, u64 galois) {
   c->keys[id] = k;
 }
 
+// Parts of a batched key switch on several streams.  run(b0, nb, s) issues
+// the work of items b0 .. b0 + nb - 1 on c->stream with intermediates from
+// s.  The first part goes on the context stream and part i on c->aux[i - 1],
+// which waits for everything issued before it (its inputs) and is joined
+// back before the function returns; every part's intermediates stay
+// allocated until then, so that no block of one part is handed to another
+// while still in use.  Parts keep at least kSplitMin items.
+constexpr int kSplitMin = 16;
+
+struct StreamSwap {
+  ckks_context *c;
+  hipStream_t saved;
+  StreamSwap(ckks_context *cc, hipStream_t s) : c(cc), saved(cc->stream) { cc->stream = s; }
+  ~StreamSwap() { c->stream = saved; }
+};
+
+template <typename F>
+static void run_parts(ckks_context *c, int b0, int nb, F run) {
+  const int parts = std::min(c->split_parts, std::max(1, nb / kSplitMin));
+  if (parts <= 1) {
+    Scratch s(c);
+    run(b0, nb, s);
+    return;
+  }
+  std::vector<std::unique_ptr<Scratch>> sc;
+  for (int i = 0; i < parts; i++) sc.emplace_back(new Scratch(c));
+  HIPCHECK(hipEventRecord(c->fork_ev, c->stream));
+  for (int i = 1; i < parts; i++) HIPCHECK(hipStreamWaitEvent(c->aux[i - 1], c->fork_ev, 0));
+  for (int i = 0; i < parts; i++) {
+    const int lo = b0 + nb * i / parts, hi = b0 + nb * (i + 1) / parts;
+    if (i == 0) {
+      run(lo, hi - lo, *sc[i]);
+    } else {
+      StreamSwap sw(c, c->aux[i - 1]);
+      run(lo, hi - lo, *sc[i]);
+    }
+  }
+  for (int i = 1; i < parts; i++) {
+    HIPCHECK(hipEventRecord(c->join_ev[i - 1], c->aux[i - 1]));
+    HIPCHECK(hipStreamWaitEvent(c->stream, c->join_ev[i - 1], 0));
+  }
+}
+
 // Words of key-switch scratch that rotate_batch takes for nb ciphertexts at
 // `limbs` limbs (each range rounded up to 256 bytes, as Scratch hands them out).
 static size_t rotate_scratch_words(const ckks_context *c, int limbs, int nb) {
@@ -1157,17 +1205,25 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
                          u64 *arena = nullptr, size_t arena_words = 0) {
   const int limbs = in[0]->limbs;
   const size_t N = c->N, P = (size_t)limbs * N;
-  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
-    const int nb = std::min(kMaxBatch, n - b0);
-    Scratch s = arena ? Scratch(c, arena, arena_words) : Scratch(c);
+  const DeviceKey &key = get_key(c, g);
+  auto run = [&](int b0, int nb, Scratch &s) {
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + P;
-    const DeviceKey &key = get_key(c, g);
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, g, in[b0 + i]->d, nullptr, out[b0 + i]->d, out[b0 + i]->d + P};
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
     ks_moddown(c, limbs, acc, jobs, s);
+  };
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    if (arena) {
+      // the fixed scratch holds one batch's intermediates: one stream
+      Scratch s(c, arena, arena_words);
+      run(b0, nb, s);
+    } else {
+      run_parts(c, b0, nb, run);
+    }
   }
 }
 
@@ -1176,9 +1232,7 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
   const int limbs = in[0]->limbs;
   const size_t N = c->N, P = (size_t)limbs * N;
   const DeviceKey &key = get_key(c, 0);
-  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
-    const int nb = std::min(kMaxBatch, n - b0);
-    Scratch s(c);
+  auto run = [&](int b0, int nb, Scratch &s) {
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     std::vector<KsJob> jobs(nb);
@@ -1187,7 +1241,8 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
                       out[b0 + i]->d + P};
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
     ks_moddown(c, limbs, acc, jobs, s);
-  }
+  };
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) run_parts(c, b0, std::min(kMaxBatch, n - b0), run);
 }
 
 // Relinearisation of n degree-2 ciphertexts followed by D rescales, as one
@@ -1222,9 +1277,7 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
   const DeviceKey &key = get_key(c, 0);
   const BCTable &bt = bc_down(c, limbs);
   const u64 *rt = relin_rs_table(c, limbs, D);
-  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
-    const int nb = std::min(kMaxBatch, n - b0);
-    Scratch s(c);
+  auto run = [&](int b0, int nb, Scratch &s) {
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     const int E = limbs + A;
@@ -1265,7 +1318,8 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
       launch_moddown_combine(c, Strided{acc, 2 * E * N}, Strided{conv, 2 * T * N}, d3, a1,
                              gal.data(), o0, o1, nb, T, E, rt, amul, &po);
     }
-  }
+  };
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) run_parts(c, b0, std::min(kMaxBatch, n - b0), run);
 }
 
 // Constants of a rescale by the last D primes p_1 = q_{limbs-1}, p_2, ... of
@@ -1368,6 +1422,18 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     c->bc_mfma = !(bc && strcmp(bc, "valu") == 0);
     const char *kf = getenv("CKKS_KEYSWITCH_FUSED");
     c->ks_fused = !(kf && strcmp(kf, "0") == 0);
+    const char *ss = getenv("CKKS_SPLIT_STREAMS");
+    if (ss) {
+      c->split_parts = atoi(ss);
+      require(c->split_parts >= 1 && c->split_parts <= ckks_context::kMaxSplit,
+              "CKKS_SPLIT_STREAMS must be 1 .. 4");
+    }
+    HIPCHECK(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming));
+    for (int i = 0; i + 1 < c->split_parts; i++) {
+      // default priority, as the context stream
+      HIPCHECK(hipStreamCreateWithFlags(&c->aux[i], hipStreamNonBlocking));
+      HIPCHECK(hipEventCreateWithFlags(&c->join_ev[i], hipEventDisableTiming));
+    }
     for (auto [var, dst] : {std::pair<const char *, int *>{"CKKS_NTT_COLS_FWD", &c->ntt_cols_fwd},
                             {"CKKS_NTT_COLS_INV", &c->ntt_cols_inv}}) {
       const char *v = getenv(var);

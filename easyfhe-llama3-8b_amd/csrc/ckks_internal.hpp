@@ -271,6 +271,16 @@ struct ckks_context {
   // columns per block of the N = 2^16 column passes (16, 32 or 64), forward
   // and inverse; environment CKKS_NTT_COLS_FWD / CKKS_NTT_COLS_INV at creation
   int ntt_cols_fwd = 64, ntt_cols_inv = 32;
+  // batched key switches of at least kSplitMin ciphertexts per part run as
+  // `split_parts` parts, the first on the context stream and the others on
+  // `aux` streams (forked from and joined back into the context stream), so
+  // that a latency-bound kernel of one part shares the CUs with a streaming
+  // kernel of another; environment CKKS_SPLIT_STREAMS=<parts> at creation
+  // (1 keeps one stream)
+  static constexpr int kMaxSplit = 4;
+  int split_parts = 2;
+  hipStream_t aux[kMaxSplit - 1] = {};
+  hipEvent_t fork_ev = nullptr, join_ev[kMaxSplit - 1] = {};
 };
 
 struct ckks_ct {
