@@ -210,6 +210,9 @@ def main() -> int:
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
     ap.add_argument("--budget", type=int, nargs=2, default=(3, 3))
+    ap.add_argument("--linear-strategy", default="normal",
+                    choices=["normal", "ext_normal", "ext_double_hoist"],
+                    help="hoist strategy of the linear mode")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (across GPUs "
@@ -242,7 +245,8 @@ def main() -> int:
     if args.mode == "linear":
         spec.rotations = ()
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
-        print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup)}),
+        print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup,
+                                                         strategy=args.linear_strategy)}),
               flush=True)
         return 0
     if args.mode == "prefill":
@@ -440,14 +444,15 @@ def main() -> int:
 
 
 def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
-                      log_slots: int | None = None) -> dict:
+                      log_slots: int | None = None, evalmod=None) -> dict:
     """Bootstrap of n_cts ciphertexts at the bottom level (one limb, values
     uniform[-1, 1] from seed 0) in batched groups: CoeffToSlot / SlotToCoeff
     with the given level budget, EvalMod at a 2^80 working scale,
     output_levels the most the chain allows.  Full-slot by default; with
     log_slots below log N - 1 the sparse program (sub-sum, then the
     2^log_slots-slot transforms) on ciphertexts of that many slots.  Returns
-    rate, precision and the program's shape."""
+    rate, precision and the program's shape.  `evalmod` (bs.BootstrapParams)
+    overrides the program's parameters (linear-level strategy, giants)."""
     import math
 
     from easyfhe.bs import openfhe as bs
@@ -455,10 +460,10 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
     budget = tuple(int(v) for v in budget)
     ls = ctx.logN - 1 if log_slots is None else int(log_slots)
     probe = bs.BootstrapSpec(log_slots=ls, level_budget=budget, output_levels=0)
-    depth = bs.generate(ctx, probe).depth_limbs
+    depth = bs.generate(ctx, probe, evalmod).depth_limbs
     bspec = bs.BootstrapSpec(log_slots=ls, level_budget=budget, output_levels=ctx.L - depth - 1)
     t0 = time.perf_counter()
-    prog = bs.generate(ctx, bspec)
+    prog = bs.generate(ctx, bspec, evalmod)
     ctx.synchronize()
     setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(0)
@@ -506,19 +511,23 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
     }
 
 
-def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1) -> dict:
+def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1,
+                      strategy: str = "normal") -> dict:
     """One 4096 x 4096 feature-major linear (the square projection of a
     Llama-3-8B decoder layer) over 128 tokens = 16 ciphertexts of 8 token
     lanes, entering at `limbs` limbs (the 13-limb QKV budget): the
-    reference's production schedule (B = 64, 8 chunks of 8 giants), weights
+    reference's production schedule (B = 64, 8 chunks of 8 giants; hoist
+    strategy `strategy`, the reference's production one is "normal"), weights
     N(0, 0.02), activations N(0, 1), seed 0.  Timed from the inputs to the
     rescaled outputs, baby rotations included."""
-    from feature_major import (FeatureMajorPrefillLayout, LinearOperator, LinearWeight,
-                               linear_rotations)
+    from feature_major import (FeatureMajorPrefillLayout, LinearOperator, LinearOperatorConfig,
+                               LinearWeight, linear_rotations)
 
     D, lanes = 4096, ctx.max_slots // 4096
+    cfg = LinearOperatorConfig(hoist_strategy=strategy)
     t0 = time.perf_counter()
-    ctx.generate_rotation_keys(linear_rotations(dimension=D, token_lanes=lanes))
+    ctx.generate_rotation_keys(linear_rotations(dimension=D, token_lanes=lanes,
+                                                operator_config=cfg))
     ctx.synchronize()
     keygen_s = time.perf_counter() - t0
     lay = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=D, slots=ctx.max_slots)
@@ -529,7 +538,7 @@ def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1) -> dict:
     cts = [client.encrypt(packed[i], cur_limbs=limbs, enc_id=200000 + i)
            for i in range(lay.cipher_count)]
     weight = LinearWeight(W, context=ctx)
-    op = LinearOperator(context=ctx, token_lanes=lanes)
+    op = LinearOperator(context=ctx, token_lanes=lanes, config=cfg)
     for _ in range(max(1, warmup)):
         outs, _ = op.apply(cts, weight)
         for o in outs:
@@ -557,7 +566,8 @@ def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1) -> dict:
         "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 4),
         "workload": f"4096x4096 feature-major linear, 128 tokens in {len(cts)} ciphertexts of "
                     f"{lanes} lanes at {limbs} limbs; B={plan.baby_steps}, "
-                    f"{len(plan.chunks)} chunks of {plan.chunk_giants} giants",
+                    f"{len(plan.chunks)} chunks of {plan.chunk_giants} giants, hoist strategy "
+                    f"{strategy}",
         "keyswitches": per_ct * len(cts),
         "pt_ct_products": D * len(cts),
         "max_abs_err_vs_fp64": err,

@@ -2542,6 +2542,144 @@ static void mac_sum_ext(ckks_context *c, const ckks_ct *const *a, int n,
   }
 }
 
+// ModDown of m single polynomials src[i] ([E][N], NTT form, Q limbs then P
+// limbs) into dst[i] ([limbs][N]): the P limbs' inverse NTT, their centred
+// conversion to the Q primes, its forward NTT, then (x - conv) P^-1.
+static void moddown_polys(ckks_context *c, int limbs, const std::vector<const u64 *> &src,
+                          const std::vector<u64 *> &dst, Scratch &s) {
+  const size_t N = c->N;
+  const int m = (int)src.size();
+  const u64 *pinv = pinv_table(c, limbs);
+  for (int b0 = 0; b0 < m; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, m - b0);
+    Batch sb{}, ob{};
+    for (int i = 0; i < nb; i++) {
+      sb.p[i] = (u64 *)src[b0 + i];
+      ob.p[i] = dst[b0 + i];
+    }
+    u64 *ptmp = s.get((size_t)nb * c->alpha * N);
+    launch_ntt(c, sb, strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N), nb, limbs,
+               c->alpha, limbs, true);
+    u64 *conv = s.get((size_t)nb * limbs * N);
+    launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
+                         nb, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+    launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), nb, 0,
+               limbs, limbs, false);
+    launch_moddown_one(c, sb, Strided{conv, (size_t)limbs * N}, ob, nb, limbs, pinv);
+  }
+}
+
+// hoisted_mac_sum with doubly hoisted giant steps (the reference's
+// "ext_double_hoist" strategy, operators/linear/config.py:296-305) for n
+// ciphertexts at one level sharing the plaintexts.  The babies and every
+// giant group's inner sum u_g = (u0, u1) stay in Q u P; group g >= 1 is
+// rotated there by its own key (the rotation by g giant steps): v =
+// ModDown(u1) (one polynomial), then (sigma(u0) + KS_0(sigma v), KS_1(sigma v))
+// with KS the key product of ModUp(sigma v), before any ModDown; the groups
+// are summed in Q u P and one ModDown of the sum ends it.  Against the Horner
+// chain of the extended schedule this saves, per giant group, the ModDown of
+// u0 and the ModDown of the rotated accumulator.
+static void mac_sum_double(ckks_context *c, const ckks_ct *const *a, int n,
+                           const int64_t *baby_rotations, int B, const ckks_ct *const *pts,
+                           int64_t giant_rotation, int giant_count, ckks_ct **out) {
+  require(n >= 1 && n <= kMaxBatch, "ciphertext count must be in [1, 64]");
+  require(B >= 1 && B <= kMaxBatch, "baby count must be in [1, 64]");
+  require(giant_count >= 1, "giant_count must be positive");
+  const int limbs = a[0]->limbs, E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
+  for (int i = 0; i < n; i++) {
+    check_ct(c, a[i], "hoisted_mac_sum_double");
+    require(a[i]->polys == 2 && !a[i]->is_ext && a[i]->limbs == limbs,
+            "hoisted_mac_sum_double expects degree-1 Q-basis ciphertexts at one level");
+  }
+  for (int i = 0; i < B * giant_count; i++) {
+    check_ct(c, pts[i], "hoisted_mac_sum_double");
+    require(pts[i]->polys == 1 && pts[i]->is_ext && pts[i]->limbs == limbs,
+            "plaintexts must be extended (Q u P) at the ciphertexts' level");
+  }
+  // every giant group's own rotation key (the keys must exist before any launch)
+  std::vector<u64> gal(giant_count, 1);
+  for (int g = 1; g < giant_count; g++) {
+    gal[g] = galois_of(c, (int64_t)g * giant_rotation);
+    if (gal[g] != 1) get_key(c, gal[g]);
+  }
+  const size_t N = c->N, P = (size_t)limbs * N, EP = 2 * (size_t)E * N;
+  const size_t est = (size_t)digits * E * N;
+  Scratch s(c);
+  u64 *bab = s.get((size_t)B * n * EP);
+  std::vector<u64 *> bp((size_t)B * n);
+  for (size_t k = 0; k < bp.size(); k++) bp[k] = bab + k * EP;
+  ext_babies(c, a, n, baby_rotations, B, bp.data(), s);
+  // inner sums of every group: [g][n][2][E][N]; group 0's are the running sum
+  u64 *inner = s.get((size_t)giant_count * n * EP);
+  const int GC = std::max(1, std::min(kMacGroups, kMaxBatch / B));
+  for (int g0 = 0; g0 < giant_count; g0 += GC) {
+    const int gn = std::min(GC, giant_count - g0);
+    Batch ptb{};
+    for (int gi = 0; gi < gn; gi++)
+      for (int b = 0; b < B; b++) ptb.p[gi * B + b] = pts[(g0 + gi) * B + b]->d;
+    launch_mac_many(c, bab, n, ptb, B, gn, inner + (size_t)g0 * n * EP, E, limbs);
+  }
+  u64 *total = inner;
+  Batch tb{};
+  for (int i = 0; i < n; i++) tb.p[i] = total + (size_t)i * EP;
+  for (int g = 1; g < giant_count; g++) {
+    u64 *ug = inner + (size_t)g * n * EP;
+    Batch ub{};
+    for (int i = 0; i < n; i++) ub.p[i] = ug + (size_t)i * EP;
+    if (gal[g] == 1) {
+      launch_ext_rot_accum(c, ub, Batch{}, tb, 1, n, E, limbs);
+      continue;
+    }
+    Scratch s2(c);
+    u64 *v = s2.get((size_t)n * P);
+    std::vector<const u64 *> src(n), vp(n);
+    std::vector<u64 *> dst(n);
+    for (int i = 0; i < n; i++) {
+      src[i] = ug + (size_t)i * EP + (size_t)E * N;  // component 1
+      dst[i] = v + (size_t)i * P;
+      vp[i] = dst[i];
+    }
+    moddown_polys(c, limbs, src, dst, s2);
+    u64 *ext = s2.get((size_t)n * est);
+    ks_modup(c, limbs, n, vp.data(), ext, s2);
+    u64 *acc = s2.get((size_t)n * EP);
+    launch_key_inner(c, strided(ext, est), strided(acc, EP), n, get_key(c, gal[g]), digits, E,
+                     limbs, gal[g], nullptr);
+    Batch ab{};
+    for (int i = 0; i < n; i++) ab.p[i] = acc + (size_t)i * EP;
+    launch_ext_rot_accum(c, ub, ab, tb, gal[g], n, E, limbs);
+  }
+  std::vector<KsJob> jobs(n);
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  for (int i = 0; i < n; i++) {
+    out[i] = new_ct(c, 2, limbs, 0, a[i]->slots, a[i]->scale * pts[0]->scale,
+                    a[i]->scale_degree + pts[0]->scale_degree);
+    jobs[i] = KsJob{0, nullptr, 1, nullptr, nullptr, out[i]->d, out[i]->d + P};
+  }
+  Scratch s3(c);
+  ks_moddown(c, limbs, total, jobs, s3);
+}
+
+int ckks_hoisted_mac_sum_double(ckks_context *c, const ckks_ct *a,
+                                const int64_t *baby_rotations, int B, const ckks_ct *const *pts,
+                                int64_t giant_rotation, int giant_count, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && baby_rotations && pts && out, "null argument");
+  *out = nullptr;
+  mac_sum_double(c, &a, 1, baby_rotations, B, pts, giant_rotation, giant_count, out);
+  API_END
+}
+
+int ckks_hoisted_mac_sum_double_many(ckks_context *c, const ckks_ct *const *a, int n,
+                                     const int64_t *baby_rotations, int B,
+                                     const ckks_ct *const *pts, int64_t giant_rotation,
+                                     int giant_count, ckks_ct **out) {
+  API_BEGIN
+  require(c && a && baby_rotations && pts && out, "null argument");
+  mac_sum_double(c, a, n, baby_rotations, B, pts, giant_rotation, giant_count, out);
+  API_END
+}
+
 int ckks_hoisted_mac_sum_ext(ckks_context *c, const ckks_ct *a, const int64_t *baby_rotations,
                              int B, const ckks_ct *const *pts, int64_t giant_rotation,
                              int giant_count, ckks_ct **out) {

@@ -405,6 +405,10 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
                      u64 *out, int E, int q_limbs);
 void launch_ext_identity(ckks_context *c, const u64 *ct, u64 *out, int limbs);
 void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64 galois);
+void launch_moddown_one(ckks_context *c, const Batch &src, Strided conv, const Batch &out,
+                        int n_items, int limbs, const u64 *pinv);
+void launch_ext_rot_accum(ckks_context *c, const Batch &u, const Batch &acc, const Batch &total,
+                          u64 galois, int n_items, int E, int q_limbs);
 // MAC over limbs_total limbs per component; limbs >= q_limbs are special
 // limbs (an extended object: Q limbs then alpha P limbs)
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,

@@ -2717,6 +2717,62 @@ void launch_ext_add_pc0(ckks_context *c, const u64 *ct, u64 *out, int limbs, u64
   LAUNCH_CHECK();
 }
 
+// The Q limbs of a one-polynomial ModDown: out[l] = (src[l] - conv[l]) P^-1
+// mod q_l, conv = the forward NTT of the centred conversion of src's P limbs
+// (the first `limbs` limbs of src are the Q ones).  grid (N / 256, limbs, items)
+__global__ void k_moddown_one(Batch src, Strided conv, Batch out, int logN,
+                              const u64 *__restrict__ pinv, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, it = blockIdx.z;
+  const size_t N = (size_t)1 << logN, o = (size_t)l * N + k;
+  const u64 q = mods[l].q;
+  const u64 d = sub_mod(batch_ptr(src, it)[o], conv.base[(size_t)it * conv.stride + o], q);
+  batch_ptr(out, it)[o] = shoup_mul(d, pinv[2 * l], pinv[2 * l + 1], q);
+}
+
+void launch_moddown_one(ckks_context *c, const Batch &src, Strided conv, const Batch &out,
+                        int n_items, int limbs, const u64 *pinv) {
+  if (n_items <= 0) return;
+  dim3 grid(c->N / TPB, limbs, n_items);
+  hipLaunchKernelGGL(k_moddown_one, grid, dim3(TPB), 0, c->stream, src, conv, out, c->logN,
+                     pinv, c->d_mods);
+  LAUNCH_CHECK();
+}
+
+// One giant group of the double-hoisted BSGS added to the running sum, all
+// in Q u P (item layout [2][E][N], Q limbs then P limbs):
+//   total_0[l][k] += u_0[l][autom(k, g)] + acc_0[l][k],  total_1 += acc_1,
+// i.e. sigma_g of the group's first component plus the key product of its
+// second; for g = 1 the group is added as it is (acc unused).
+// grid (N / 256, E, items)
+__global__ void k_ext_rot_accum(Batch u, Batch acc, Batch total, u64 galois, int E, int q_limbs,
+                                int L, int logN, const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = blockIdx.y, it = blockIdx.z;
+  const size_t N = (size_t)1 << logN, o = (size_t)l * N + k, EN = (size_t)E * N;
+  const u64 q = mods[prime_of(l, q_limbs, L)].q;
+  const u64 *ui = batch_ptr(u, it);
+  u64 *ti = batch_ptr(total, it);
+  if (galois == 1) {
+    ti[o] = add_mod(ti[o], ui[o], q);
+    ti[EN + o] = add_mod(ti[EN + o], ui[EN + o], q);
+    return;
+  }
+  const u64 *ai = batch_ptr(acc, it);
+  const u32 kk = autom_index((u32)k, galois, logN);
+  ti[o] = add_mod(ti[o], add_mod(ui[(size_t)l * N + kk], ai[o], q), q);
+  ti[EN + o] = add_mod(ti[EN + o], ai[EN + o], q);
+}
+
+void launch_ext_rot_accum(ckks_context *c, const Batch &u, const Batch &acc, const Batch &total,
+                          u64 galois, int n_items, int E, int q_limbs) {
+  if (n_items <= 0) return;
+  dim3 grid(c->N / TPB, E, n_items);
+  hipLaunchKernelGGL(k_ext_rot_accum, grid, dim3(TPB), 0, c->stream, u, acc, total, galois, E,
+                     q_limbs, c->L, c->logN, c->d_mods);
+  LAUNCH_CHECK();
+}
+
 // ===========================================================================
 // Linear combination of n ciphertexts' terms in one launch:
 //   out_i = sum_t W_t x_(t,i) + C   (C on c0 only), on the first `limbs` limbs

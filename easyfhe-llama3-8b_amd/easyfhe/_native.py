@@ -129,6 +129,9 @@ SIGNATURES = {
     "ckks_hoisted_rotate_many": (I, [VP, VPP, I, I64P, I, VPP]),
     "ckks_hoisted_rotate_ext": (I, [VP, VP, I64P, I, VPP]),
     "ckks_hoisted_mac_sum_ext_many": (I, [VP, VPP, I, I64P, I, VPP, ctypes.c_int64, I, VPP]),
+    "ckks_hoisted_mac_sum_double": (I, [VP, VP, I64P, I, VPP, ctypes.c_int64, I, VPP]),
+    "ckks_hoisted_mac_sum_double_many": (I, [VP, VPP, I, I64P, I, VPP, ctypes.c_int64, I,
+                                             VPP]),
     "ckks_rescale_many": (I, [VP, VPP, I, VPP]),
     "ckks_rescale_many_by": (I, [VP, VPP, I, I, VPP]),
     "ckks_linear_combination": (I, [VP, VPP, I, I, DP, ctypes.c_double, I, ctypes.c_double, I,

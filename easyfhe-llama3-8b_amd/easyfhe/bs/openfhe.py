@@ -76,8 +76,11 @@ class BootstrapParams:
     ratio_bits: int = 10
     cts_pt_bits: int = 58
     # linear levels: "ext_normal" keeps the babies in Q u P (one ModDown per
-    # giant group, at most `giants` giants); "normal" ModDowns every baby
-    strategy: str = "ext_normal"
+    # giant group, at most `giants` giants); "ext_double_hoist" (the default)
+    # also rotates the giant groups in Q u P (one key per giant step, one
+    # ModDown per level: 2.5-3.5 % faster bootstraps at 2 giants, the same
+    # precision; more giants are slower); "normal" ModDowns every baby
+    strategy: str = "ext_double_hoist"
     giants: int = 2
 
 
@@ -139,10 +142,15 @@ def _giant_offset(plan: LevelPlan, n: int) -> int:
     return (plan.baby * plan.stride) % n
 
 
-def _level_rotations(plan: LevelPlan, n: int) -> set[int]:
+def _level_rotations(plan: LevelPlan, n: int, strategy: str = "ext_normal") -> set[int]:
     rots = {o for o in _baby_offsets(plan, n) if o}
     if plan.giant > 1 and _giant_offset(plan, n):
-        rots.add(_giant_offset(plan, n))
+        if strategy == "ext_double_hoist":
+            # every giant group rotates by its own multiple of the giant step
+            rots.update(g * _giant_offset(plan, n) % n for g in range(1, plan.giant))
+            rots.discard(0)
+        else:
+            rots.add(_giant_offset(plan, n))
     return rots
 
 
@@ -158,7 +166,7 @@ def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> 
         n = 1 << _transform_log_slots(spec, int(log_n))
         cts, stc = _plans(spec, p, int(log_n))
         for plan in (*cts, *stc):
-            rots |= _level_rotations(plan, n)
+            rots |= _level_rotations(plan, n, p.strategy)
         rots.update(_subsum_rotations(spec, int(log_n)))
         rots.add(2 * (1 << int(log_n)) - 1)
     return Requirements(rotations=tuple(sorted(rots)))
@@ -255,7 +263,7 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     step = max(1, math.ceil(_EVALMOD_BITS / bits))
     coeffs = _evalmod_coefficients(p)
     depth = cheb.chebyshev_depth(coeffs)
-    if p.strategy not in ("normal", "ext_normal"):
+    if p.strategy not in ("normal", "ext_normal", "ext_double_hoist"):
         raise ValueError(f"unknown linear-level strategy {p.strategy!r}")
     cts_plans, stc_plans = _plans(spec, p, ctx.logN)
     n_cts, n_stc = len(cts_plans), len(stc_plans)
@@ -446,7 +454,8 @@ def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> lis
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
     pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=True)
     accs = fhe.hoisted_mac_sum_ext_many(xs, _baby_offsets(plan, n), pts,
-                                        _giant_offset(plan, n), plan.giant, ctx)
+                                        _giant_offset(plan, n), plan.giant, ctx,
+                                        strategy=prog.evalmod.strategy)
     if lv.primes:
         accs = fhe.rescale_many(accs, ctx, primes=lv.primes)
     for a in accs:

@@ -883,10 +883,14 @@ def rescale_many(cts: Sequence[Ciphertext], context=None, primes: int = 1) -> li
 
 
 def hoisted_mac_sum_ext_many(cts: Sequence[Ciphertext], baby_offsets, plaintexts,
-                             giant_offset: int, giant_count: int, context=None) -> list:
+                             giant_offset: int, giant_count: int, context=None,
+                             strategy: str = "ext_normal") -> list:
     """The extended-basis hoisted_mac_sum of several ciphertexts at one level
     with shared (extended) plaintexts; keys and plaintexts are read once per
-    batch of up to 64."""
+    batch of up to 64.  ``strategy`` "ext_double_hoist" rotates the giant
+    groups in Q u P (see hoisted_mac_sum)."""
+    if strategy not in ("ext_normal", "ext_double_hoist"):
+        raise ValueError(f"unknown extended strategy {strategy!r}")
     if not cts:
         return []
     ctx = _ctx(cts[0], context)
@@ -899,10 +903,11 @@ def hoisted_mac_sum_ext_many(cts: Sequence[Ciphertext], baby_offsets, plaintexts
     for i0 in range(0, len(cts), 64):
         chunk = cts[i0: i0 + 64]
         outs = (ctypes.c_void_p * len(chunk))()
-        check(lib.ckks_hoisted_mac_sum_ext_many(
-            ctx.handle, ptr_array([c.handle for c in chunk]), len(chunk),
-            offs.ctypes.data_as(_native.I64P), B, ptr_array([p.handle for p in pts]),
-            int(giant_offset), int(giant_count), outs))
+        fn = (lib.ckks_hoisted_mac_sum_double_many if strategy == "ext_double_hoist"
+              else lib.ckks_hoisted_mac_sum_ext_many)
+        check(fn(ctx.handle, ptr_array([c.handle for c in chunk]), len(chunk),
+                 offs.ctypes.data_as(_native.I64P), B, ptr_array([p.handle for p in pts]),
+                 int(giant_offset), int(giant_count), outs))
         results.extend(Ciphertext(ctx, outs[i]) for i in range(len(chunk)))
     return results
 
@@ -1029,9 +1034,12 @@ def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count
     with a Horner chain over one giant key; unrescaled
     (reference operators/linear/operator.py:320-330, operators/transform.py:108).
     Strategies "ext_normal" and "ext_double_hoist" with extended plaintexts
-    keep the babies in the Q u P basis and take one ModDown per giant group
-    instead of one per baby; with Q-basis plaintexts (or precomputed babies
-    or an anchor step) they run the normal schedule."""
+    keep the babies in the Q u P basis: "ext_normal" takes one ModDown per
+    giant group before the Horner chain, "ext_double_hoist" rotates every
+    giant group in Q u P with its own key (g * giant_offset) and takes one
+    ModDown of the sum (reference operators/linear/config.py:296-305).  With
+    Q-basis plaintexts (or precomputed babies or an anchor step) both run
+    the normal schedule."""
     ctx = _ctx(ct, context)
     pts = plaintexts if isinstance(plaintexts, (list, tuple)) else [plaintexts]
     B = len(list(baby_offsets))
@@ -1040,14 +1048,15 @@ def hoisted_mac_sum(ct, baby_offsets, plaintexts, giant_offset: int, giant_count
     used = pts[: B * int(giant_count)]
     if (strategy in ("ext_normal", "ext_double_hoist") and baby_rotations is None
             and int(baby_anchor_step) < 2 and all(p.is_ext for p in used)):
-        # babies kept in Q u P, one ModDown per giant group
+        # babies kept in Q u P: one ModDown per giant group, or (double
+        # hoisting) giant groups rotated in Q u P and one ModDown of the sum
         offs = np.asarray([int(o) for o in baby_offsets], dtype=np.int64)
         out = ctypes.c_void_p()
-        check(lib.ckks_hoisted_mac_sum_ext(ctx.handle, ct.handle,
-                                           offs.ctypes.data_as(_native.I64P), B,
-                                           ptr_array([p.handle for p in used]),
-                                           int(giant_offset), int(giant_count),
-                                           ctypes.byref(out)))
+        fn = (lib.ckks_hoisted_mac_sum_double if strategy == "ext_double_hoist"
+              else lib.ckks_hoisted_mac_sum_ext)
+        check(fn(ctx.handle, ct.handle, offs.ctypes.data_as(_native.I64P), B,
+                 ptr_array([p.handle for p in used]), int(giant_offset), int(giant_count),
+                 ctypes.byref(out)))
         return _wrap(ctx, out)
     babies = baby_rotations
     owned = False

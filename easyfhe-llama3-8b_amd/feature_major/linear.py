@@ -359,9 +359,10 @@ class LinearOperator:
                 t0 = time.perf_counter()
                 try:
                     if ext:
-                        outs = fhe.hoisted_mac_sum_ext_many(list(inputs), plan.baby_offsets, pts,
-                                                            plan.giant_offset, chunk.giant_count,
-                                                            ctx)
+                        outs = fhe.hoisted_mac_sum_ext_many(
+                            list(inputs), plan.baby_offsets, pts, plan.giant_offset,
+                            chunk.giant_count, ctx,
+                            strategy=str(self.config.hoist_strategy).lower())
                     else:
                         outs = fhe.hoisted_mac_sum_many(babies, pts, plan.giant_offset,
                                                         chunk.giant_count, ctx)

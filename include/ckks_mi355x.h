@@ -231,7 +231,7 @@ int ckks_hoisted_rotate_many(ckks_context *ctx, const ckks_ct *const *a, int m,
 int ckks_hoisted_mac_sum_many(ckks_context *ctx, const ckks_ct *const *babies, int n, int B,
                               const ckks_ct *const *pts, int64_t giant_rotation,
                               int giant_count, ckks_ct **out);
-/* fhe.hoisted_mac_sum, strategies "ext_normal" / "ext_double_hoist" (reference
+/* fhe.hoisted_mac_sum, strategy "ext_normal" (reference
  * operators/linear/operator.py:320-330, linear/config.py:296-305): the babies
  * of `a` for baby_rotations stay in the Q u P basis (no ModDown), the
  * plaintexts are extended (is_ext, at a's level), and each giant group is
@@ -247,6 +247,25 @@ int ckks_hoisted_mac_sum_ext_many(ckks_context *ctx, const ckks_ct *const *a, in
                                   const int64_t *baby_rotations, int B,
                                   const ckks_ct *const *pts, int64_t giant_rotation,
                                   int giant_count, ckks_ct **out);
+/* fhe.hoisted_mac_sum, strategy "ext_double_hoist" (reference
+ * operators/linear/config.py:296-305, operators/linear/operator.py:320-330):
+ * babies and plaintexts as in ckks_hoisted_mac_sum_ext; every giant group
+ * g >= 1 is rotated by g * giant_rotation in the Q u P basis with its own key
+ * (ModDown of its second component only, ModUp, key product, sigma of its
+ * first component added), the groups are summed there and one ModDown ends
+ * it; result unrescaled.  Needs the keys of g * giant_rotation, g = 1 ..
+ * giant_count - 1 (the reference's key set for this strategy,
+ * linear/config.py:296-305). */
+int ckks_hoisted_mac_sum_double(ckks_context *ctx, const ckks_ct *a,
+                                const int64_t *baby_rotations, int B, const ckks_ct *const *pts,
+                                int64_t giant_rotation, int giant_count, ckks_ct **out);
+/* ckks_hoisted_mac_sum_double for n <= 64 ciphertexts at one level sharing
+ * the plaintexts: one batched ModUp for the babies, each key read once for
+ * all n. */
+int ckks_hoisted_mac_sum_double_many(ckks_context *ctx, const ckks_ct *const *a, int n,
+                                     const int64_t *baby_rotations, int B,
+                                     const ckks_ct *const *pts, int64_t giant_rotation,
+                                     int giant_count, ckks_ct **out);
 /* Linear combination in one launch for n ciphertexts (the many small
  * homo_mul_scalar / homo_add launches of a polynomial's leaf sums, reference
  * operators/nonlinear/polynomial.py:182-199):

@@ -1442,18 +1442,16 @@ int orc_hoisted_mac_sum(const orc_ctx *c, const uint64_t *ct, int limbs,
  * without its ModDown; the plaintexts carry P limbs ([G*B][limbs+alpha][N]);
  * each giant group sum_b pt_b babies_b is brought back to Q by one ModDown,
  * then the Horner chain over the giant key runs as in orc_hoisted_mac_sum. */
-int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
-                            const uint64_t *baby_gs, int B, const uint64_t *pts,
-                            uint64_t giant_g, int G, uint64_t *out) {
+/* Extended-basis babies of ct for the Galois elements baby_gs (keys present):
+ * bab[b] = [2][E][N] holding (P c0, P c1) for g = 1, (P sigma(c0) + acc_0, acc_1)
+ * otherwise, from one ModUp of c1. */
+static void ext_babies(const orc_ctx *c, const uint64_t *ct, int limbs, const uint64_t *baby_gs,
+                       int B, u64 *bab) {
   const int N = c->N, A = c->alpha, L = c->L, E = limbs + A;
   const int digits = (limbs + c->ds - 1) / c->ds;
   const size_t P = (size_t)limbs * N, EP = (size_t)E * N;
-  for (int b = 0; b < B; b++)
-    if (baby_gs[b] != 1 && !find_key(c, baby_gs[b])) return -1;
-  if (G > 1 && giant_g != 1 && !find_key(c, giant_g)) return -1;
   u64 *ext = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
   u64 *extg = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
-  u64 *bab = (u64 *)malloc(sizeof(u64) * (size_t)B * 2 * EP);
   u64 *sc0 = (u64 *)malloc(sizeof(u64) * P);
   u64 Pm[64];
   for (int i = 0; i < limbs; i++) {
@@ -1481,26 +1479,49 @@ int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
         *x = addmod(*x, orc_mulmod(sc0[(size_t)i * N + k], Pm[i], c->primes[i]), c->primes[i]);
       }
   }
+  free(ext);
+  free(extg);
+  free(sc0);
+}
+
+/* inner = sum_b pts[g B + b] * bab[b] over Q_limbs u P, both components */
+static void ext_inner(const orc_ctx *c, const u64 *bab, int B, const uint64_t *pts, int g,
+                      int limbs, u64 *inner_ext) {
+  const int N = c->N, E = limbs + c->alpha;
+  const size_t EP = (size_t)E * N;
+#pragma omp parallel for
+  for (int l = 0; l < E; l++) {
+    const u64 q = c->primes[prime_of(c, l, limbs)];
+    for (int d = 0; d < 2; d++) {
+      u64 *dst = inner_ext + (size_t)d * EP + (size_t)l * N;
+      for (int i = 0; i < N; i++) {
+        u128 s = 0;
+        for (int b = 0; b < B; b++) {
+          s += (u128)bab[(size_t)b * 2 * EP + (size_t)d * EP + (size_t)l * N + i] *
+               pts[((size_t)(g * B + b) * E + l) * N + i];
+          if ((b & 15) == 15) s = mod128(s, q);
+        }
+        dst[i] = mod128(s, q);
+      }
+    }
+  }
+}
+
+int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
+                            const uint64_t *baby_gs, int B, const uint64_t *pts,
+                            uint64_t giant_g, int G, uint64_t *out) {
+  const int N = c->N, A = c->alpha, E = limbs + A;
+  const size_t P = (size_t)limbs * N, EP = (size_t)E * N;
+  for (int b = 0; b < B; b++)
+    if (baby_gs[b] != 1 && !find_key(c, baby_gs[b])) return -1;
+  if (G > 1 && giant_g != 1 && !find_key(c, giant_g)) return -1;
+  u64 *bab = (u64 *)malloc(sizeof(u64) * (size_t)B * 2 * EP);
+  ext_babies(c, ct, limbs, baby_gs, B, bab);
   u64 *inner_ext = (u64 *)malloc(sizeof(u64) * 2 * EP);
   u64 *inner = (u64 *)malloc(sizeof(u64) * 2 * P);
   u64 *tmp = (u64 *)malloc(sizeof(u64) * 2 * P);
   for (int g = G - 1; g >= 0; g--) {
-#pragma omp parallel for
-    for (int l = 0; l < E; l++) {
-      const u64 q = c->primes[prime_of(c, l, limbs)];
-      for (int d = 0; d < 2; d++) {
-        u64 *dst = inner_ext + (size_t)d * EP + (size_t)l * N;
-        for (int i = 0; i < N; i++) {
-          u128 s = 0;
-          for (int b = 0; b < B; b++) {
-            s += (u128)bab[(size_t)b * 2 * EP + (size_t)d * EP + (size_t)l * N + i] *
-                 pts[((size_t)(g * B + b) * E + l) * N + i];
-            if ((b & 15) == 15) s = mod128(s, q);
-          }
-          dst[i] = mod128(s, q);
-        }
-      }
-    }
+    ext_inner(c, bab, B, pts, g, limbs, inner_ext);
     orc_moddown(c, inner_ext, limbs, inner);
     orc_moddown(c, inner_ext + EP, limbs, inner + P);
     if (g == G - 1) {
@@ -1510,12 +1531,80 @@ int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
       orc_add(c, tmp, inner, out, 2, limbs);
     }
   }
-  free(ext);
-  free(extg);
   free(bab);
-  free(sc0);
   free(inner_ext);
   free(inner);
   free(tmp);
+  return 0;
+}
+
+/* Double-hoisted schedule (ext_double_hoist): the babies and every giant
+ * group's inner sum u_g = (u0, u1) stay in Q_limbs u P; each giant group g >= 1
+ * is rotated there by its own Galois element G_g (the rotation by g giant
+ * steps): v = ModDown(u1) (one polynomial), then
+ *   (sigma(u0) + KS_0(sigma(v)), KS_1(sigma(v)))  before its ModDown,
+ * KS = the key product of ModUp(sigma(v)); the groups are summed in Q u P and
+ * one ModDown of the sum ends it.  Using sigma(u0) for P sigma(ModDown(u0))
+ * and the ModDown of u1 only leaves a rounding error of a key switch's
+ * ModDown size (the message is P times the decrypted value). */
+int orc_hoisted_mac_sum_double(const orc_ctx *c, const uint64_t *ct, int limbs,
+                               const uint64_t *baby_gs, int B, const uint64_t *pts,
+                               const uint64_t *giant_gs, int G, uint64_t *out) {
+  const int N = c->N, A = c->alpha, E = limbs + A;
+  const int digits = (limbs + c->ds - 1) / c->ds;
+  const size_t P = (size_t)limbs * N, EP = (size_t)E * N;
+  for (int b = 0; b < B; b++)
+    if (baby_gs[b] != 1 && !find_key(c, baby_gs[b])) return -1;
+  for (int g = 1; g < G; g++)
+    if (giant_gs[g] != 1 && !find_key(c, giant_gs[g])) return -1;
+  u64 *bab = (u64 *)malloc(sizeof(u64) * (size_t)B * 2 * EP);
+  ext_babies(c, ct, limbs, baby_gs, B, bab);
+  u64 *total = (u64 *)malloc(sizeof(u64) * 2 * EP);
+  u64 *inner = (u64 *)malloc(sizeof(u64) * 2 * EP);
+  u64 *v = (u64 *)malloc(sizeof(u64) * P);
+  u64 *ext = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
+  u64 *extg = (u64 *)malloc(sizeof(u64) * (size_t)digits * EP);
+  u64 *k0 = (u64 *)malloc(sizeof(u64) * EP);
+  u64 *k1 = (u64 *)malloc(sizeof(u64) * EP);
+  u64 *su0 = (u64 *)malloc(sizeof(u64) * EP);
+  ext_inner(c, bab, B, pts, 0, limbs, total);
+  for (int g = 1; g < G; g++) {
+    ext_inner(c, bab, B, pts, g, limbs, inner);
+    if (giant_gs[g] == 1) {
+      for (int d = 0; d < 2; d++)
+        for (int l = 0; l < E; l++) {
+          const u64 q = c->primes[prime_of(c, l, limbs)];
+          for (int i = 0; i < N; i++) {
+            const size_t o = (size_t)d * EP + (size_t)l * N + i;
+            total[o] = addmod(total[o], inner[o], q);
+          }
+        }
+      continue;
+    }
+    orc_moddown(c, inner + EP, limbs, v);
+    orc_modup(c, v, limbs, ext);
+    orc_automorphism_ntt(c, giant_gs[g], ext, extg, digits * E);
+    key_inner(c, find_key(c, giant_gs[g]), extg, limbs, k0, k1);
+    orc_automorphism_ntt(c, giant_gs[g], inner, su0, E);
+    for (int l = 0; l < E; l++) {
+      const u64 q = c->primes[prime_of(c, l, limbs)];
+      for (int i = 0; i < N; i++) {
+        const size_t o = (size_t)l * N + i;
+        total[o] = addmod(total[o], addmod(su0[o], k0[o], q), q);
+        total[EP + o] = addmod(total[EP + o], k1[o], q);
+      }
+    }
+  }
+  orc_moddown(c, total, limbs, out);
+  orc_moddown(c, total + EP, limbs, out + P);
+  free(bab);
+  free(total);
+  free(inner);
+  free(v);
+  free(ext);
+  free(extg);
+  free(k0);
+  free(k1);
+  free(su0);
   return 0;
 }

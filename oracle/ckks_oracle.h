@@ -140,6 +140,9 @@ void orc_rescale(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,
 int orc_hoisted_mac_sum_ext(const orc_ctx *c, const uint64_t *ct, int limbs,
                             const uint64_t *baby_gs, int B, const uint64_t *pts,
                             uint64_t giant_g, int G, uint64_t *out);
+int orc_hoisted_mac_sum_double(const orc_ctx *c, const uint64_t *ct, int limbs,
+                               const uint64_t *baby_gs, int B, const uint64_t *pts,
+                               const uint64_t *giant_gs, int G, uint64_t *out);
 void orc_mod_raise(const orc_ctx *c, const uint64_t *ct, int polys, int target,
                    uint64_t *out);
 void orc_drop_limbs(const orc_ctx *c, const uint64_t *ct, int polys, int limbs,

@@ -82,6 +82,7 @@ def SIGNATURES(vp, i, u64) -> dict:
         "orc_drop_limbs": (None, [vp, _u64p, i, i, i, _u64p]),
         "orc_mod_raise": (None, [vp, _u64p, i, i, _u64p]),
         "orc_hoisted_mac_sum_ext": (i, [vp, _u64p, i, _u64p, i, _u64p, u64, i, _u64p]),
+        "orc_hoisted_mac_sum_double": (i, [vp, _u64p, i, _u64p, i, _u64p, _u64p, i, _u64p]),
         "orc_hoisted_mac_sum": (i, [vp, _u64p, i, _u64p, i, _u64p, u64, i, _u64p]),
     }
 
@@ -398,6 +399,21 @@ class OracleContext:
         out = np.zeros_like(ct)
         if self._lib.orc_hoisted_mac_sum_ext(self._c, _p(ct), ct.shape[1], _p(gs), len(gs), _p(pts),
                                          giant_g, giant_count, _p(out)):
+            raise KeyError("missing rotation key")
+        return out
+
+    def hoisted_mac_sum_double(self, ct, baby_gs, pts_ext, giant_gs):
+        """Double-hoisted schedule: giant group g >= 1 rotated in Q u P by its
+        own Galois element giant_gs[g] (giant_gs[0] unused), one ModDown of the
+        sum; pts_ext are [G*B][limbs + alpha][N] with G = len(giant_gs)."""
+        gs = np.asarray(baby_gs, dtype=np.uint64)
+        ggs = np.asarray(giant_gs, dtype=np.uint64)
+        pts = np.ascontiguousarray(pts_ext, dtype=np.uint64)
+        assert pts.shape[1] == ct.shape[1] + self.alpha
+        assert pts.shape[0] >= len(gs) * len(ggs)
+        out = np.zeros_like(ct)
+        if self._lib.orc_hoisted_mac_sum_double(self._c, _p(ct), ct.shape[1], _p(gs), len(gs),
+                                            _p(pts), _p(ggs), len(ggs), _p(out)):
             raise KeyError("missing rotation key")
         return out
 

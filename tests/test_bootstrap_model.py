@@ -145,7 +145,8 @@ def _horner_check(x, plan, rows):
 
 @pytest.mark.parametrize("log_n,budget,strategy",
                          [(6, (2, 2), "normal"), (10, (3, 3), "normal"), (10, (3, 3), "ext_normal"),
-                          (10, (4, 4), "ext_normal"), (11, (3, 2), "normal")])
+                          (10, (4, 4), "ext_normal"), (10, (3, 3), "ext_double_hoist"),
+                          (11, (3, 2), "normal")])
 def test_bootstrap_model_recovers_message(log_n, budget, strategy):
     n = 1 << log_n
     rng = np.random.default_rng(log_n)

@@ -71,11 +71,12 @@ def test_fm_linear_matches_per_input_bsgs_and_wx():
     op.close()
 
 
-def test_fm_linear_extended_schedule():
+@pytest.mark.parametrize("strategy", ["ext_normal", "ext_double_hoist"])
+def test_fm_linear_extended_schedule(strategy):
     from feature_major import LinearOperator, LinearOperatorConfig
 
     cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=32,
-                               hoist_strategy="ext_normal")
+                               hoist_strategy=strategy)
     client, ctx, lay, W, X, cts = _setup(cfg)
     with LinearOperator(context=ctx, token_lanes=LANES, config=cfg) as op:
         outs, _ = op.project(cts, W)

@@ -390,6 +390,47 @@ def test_bsgs_matvec_ext_parity():
     assert np.abs(dec - W @ x).max() < 1e-5
 
 
+@pytest.mark.parametrize("n_cts", [1, 3])
+def test_bsgs_matvec_double_hoist_parity(n_cts):
+    """The matvec workload with strategy "ext_double_hoist": babies and
+    giant groups in Q u P, every giant group rotated by its own key, one
+    ModDown of the sum; bit-exact with the oracle's double-hoisted schedule
+    for one ciphertext and for a batch of three (each equal to its own
+    single-ciphertext result), decrypting to W x."""
+    fhe = _fhe()
+    D, lanes, B, G = 128, 32, 16, 8
+    rots = tuple(lanes * b for b in range(1, B)) + tuple(g * B * lanes for g in range(1, G))
+    client, ctx, orc = _pair("matvec", rotations=rots)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    xs = [rng.uniform(-1, 1, D) for _ in range(n_cts)]
+    sc = ctx.scale_at(ctx.L)
+    rows = _diagonals(W, slots=slots, lanes=lanes, baby=B, giant_base=0, giant_count=G)
+    pts = fhe.encode_rows(ctx, rows, limbs=ctx.L, scale=sc, slots=slots, is_ext=True)
+    rpts = np.stack([orc.encode(r, slots=slots, scale=sc, limbs=ctx.L, is_ext=True)
+                     for r in rows])
+    offsets = [lanes * b for b in range(B)]
+    cts, refs = [], []
+    for i, x in enumerate(xs):
+        packed = np.zeros(slots)
+        packed[np.arange(D) * lanes] = x
+        cts.append(client.encrypt(packed, slots=slots, enc_id=41 + i))
+        refs.append(orc.encrypt(packed, slots=slots, scale=sc, limbs=ctx.L, enc_id=41 + i))
+    if n_cts == 1:
+        accs = [fhe.hoisted_mac_sum(cts[0], offsets, pts, B * lanes, G, ctx,
+                                    strategy="ext_double_hoist")]
+    else:
+        accs = fhe.hoisted_mac_sum_ext_many(cts, offsets, pts, B * lanes, G, ctx,
+                                            strategy="ext_double_hoist")
+    ggs = [orc.galois_elt(g * B * lanes) for g in range(G)]
+    for acc, ref, x in zip(accs, refs, xs):
+        racc = orc.hoisted_mac_sum_double(ref, [orc.galois_elt(o) for o in offsets], rpts, ggs)
+        assert np.array_equal(acc.download(), racc)
+        dec = client.decrypt(fhe.rescale(acc, ctx))[np.arange(D) * lanes]
+        assert np.abs(dec - W @ x).max() < 1e-5
+
+
 @pytest.mark.parametrize("name", ["small", "matvec"])
 def test_fast_rotate_ext_moddown_is_rotation(name):
     """ModDown(P sigma(c0) + acc_0, acc_1) is the rotation bit for bit (P

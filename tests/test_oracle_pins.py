@@ -518,6 +518,50 @@ def test_bsgs_matvec_ext_schedule_decrypts_to_wx():
 
 
 
+def test_bsgs_matvec_double_hoist_decrypts_to_wx():
+    """The double-hoisted schedule (every giant group rotated in Q u P by its
+    own key, one ModDown of the sum) on the oracle: decrypt(rescale(MAC)) =
+    W x; its decrypted value agrees with the extended schedule's to the
+    rounding of a key switch, and its limbs differ (another rounding).  A
+    giant Galois element of 1 adds the group unrotated: the matvec with its
+    diagonals' giant offsets all 0 (G copies of one group) decrypts to G W x
+    restricted to the first group."""
+    ctx = oracle_context("matvec")
+    D, lanes, B, G = 128, 32, 16, 8
+    for o in list(range(lanes, B * lanes, lanes)) + [g * B * lanes for g in range(1, G)]:
+        ctx.gen_rotation_key(ctx.galois_elt(o))
+    slots = ctx.N // 2
+    rng = np.random.default_rng(0)
+    W = rng.uniform(-1, 1, (D, D))
+    x = rng.uniform(-1, 1, D)
+    packed = np.zeros(slots)
+    packed[np.arange(D) * lanes] = x
+    ct = ctx.encrypt(packed, slots=slots, scale=2.0**40, limbs=ctx.L, enc_id=41)
+    feat = np.arange(slots) // lanes
+    rows = [W[(feat - g * B) % D, (feat + b) % D] for g in range(G) for b in range(B)]
+    pts = np.stack([ctx.encode(r, slots=slots, scale=2.0**40, limbs=ctx.L, is_ext=True)
+                    for r in rows])
+    gs = [ctx.galois_elt(lanes * b) for b in range(B)]
+    ggs = [ctx.galois_elt(g * B * lanes) for g in range(G)]
+    acc = ctx.hoisted_mac_sum_double(ct, gs, pts, ggs)
+    sc = 2.0**80 / float(ctx.primes[ctx.L - 1])
+    dec = ctx.decrypt(ctx.rescale(acc), slots=slots, scale=sc).real[np.arange(D) * lanes]
+    assert np.abs(dec - W @ x).max() < 1e-5
+    ext = ctx.hoisted_mac_sum_ext(ct, gs, pts, ctx.galois_elt(B * lanes), G)
+    dext = ctx.decrypt(ctx.rescale(ext), slots=slots, scale=sc).real[np.arange(D) * lanes]
+    assert np.abs(dec - dext).max() < 1e-7
+    assert not np.array_equal(acc, ext)
+    # identity giants: the group-0 diagonals G times
+    same = np.concatenate([pts[:B]] * G)
+    acc1 = ctx.hoisted_mac_sum_double(ct, gs, same, [1] * G)
+    d1 = ctx.decrypt(ctx.rescale(acc1), slots=slots, scale=sc).real[np.arange(D) * lanes]
+    Wb = np.zeros((D, D))
+    f = np.arange(D)
+    for b in range(B):
+        Wb[f, (f + b) % D] = W[f, (f + b) % D]
+    assert np.abs(d1 - G * (Wb @ x)).max() < 1e-5
+
+
 @pytest.mark.parametrize("special,first", [(60, 60), (44, 40)])
 def test_fast_build_gives_the_same_words(special, first):
     """The ORC_FAST build (Shoup reductions of 128-bit sums, the build the CPU
