@@ -1684,11 +1684,22 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kMfmaRows = 2;    // 16-coefficient column tiles per wave and chunk
 constexpr int kMfmaChunks = 4;  // chunks of 4 waves x R tiles per block
 
-template <int R, int NK, int CH>
+// RS: the relinearise-rescale ModDown by P p (one dropped prime p = the
+// last target, td = nd - 1; k_bc_down_rescale states the algebra): the
+// dropped target's group runs first, its value y_td gives the centred lift
+// r = [(x_td - y_td) P^-1]_p, where x_td is source slot ns (the dropped limb
+// of X as coefficients), broadcast from the lanes that hold it; every other
+// target t < td is written as y_t + r [P]_t - (r > p / 2 ? [P p]_t : 0).
+// rs: the rescale table of one dropped prime, the conversion part of the
+// relinearise-rescale constants ([td] Montgomery [P]_t, [td] [P p]_t, then
+// P^-1 mod p and its Shoup constant); rsf: ([P]_t, [P]_t / q_t) for the
+// fp64 targets.
+template <int R, int NK, int CH, bool RS = false>
 __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
     Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
     const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
-    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods) {
+    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods,
+    const u64 *__restrict__ rs = nullptr, const double2 *__restrict__ rsf = nullptr) {
   // the block's table, staged once: [NK][n_tg][8][64] words
   extern __shared__ u64 tb[];
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
@@ -1707,6 +1718,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
   }
   // raw residues of the chunk being loaded (coefficient k + 16 r + col)
   u64 x[R][NK];
+  u64 xd[R];  // RS: the dropped limb of X at the same coefficients
   auto load = [&](int ch) {
     const int k0 = kblk + ch * 64 * R + wave * 16 * R;
 #pragma unroll
@@ -1714,7 +1726,13 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
 #pragma unroll
       for (int r = 0; r < R; r++)
         x[r][i] = 4 * i + g < ns ? in[((size_t)(4 * i + g) << logN) + k0 + 16 * r + col] : 0;
+    if constexpr (RS) {
+#pragma unroll
+      for (int r = 0; r < R; r++) xd[r] = in[((size_t)ns << logN) + k0 + 16 * r + col];
+    }
   };
+  // RS: the dropped target, its group, lane group and accumulator slot
+  const int td = nd - 1, tg_d = td >> 4, g_d = (td & 15) >> 2, e_d = td & 3;
   load(0);
   const int words = NK * n_tg * 512;
   for (int idx = threadIdx.x; idx < words; idx += TPB) tb[idx] = mtab[idx];
@@ -1732,8 +1750,17 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
         if (centered && v > (sq[i] - 1) / 2) v -= sq[i];  // two's complement of v - q
         a[r][i] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
       }
+    u64 xdc[R];  // RS: this chunk's dropped-limb words
+    if constexpr (RS) {
+#pragma unroll
+      for (int r = 0; r < R; r++) xdc[r] = xd[r];
+    }
     if (ch + 1 < CH) load(ch + 1);  // in flight during this chunk
-    for (int tg = 0; tg < n_tg; tg++) {
+    u64 rv[R];
+    bool rneg[R];
+    for (int tt = 0; tt < n_tg; tt++) {
+      // RS: the dropped target's group first
+      const int tg = RS ? (tt == 0 ? tg_d : (tt <= tg_d ? tt - 1 : tt)) : tt;
       const bool wide = (wide_mask >> tg) & 1;
       const u64 *mt = tb + tg * 512 + lane;
       // C_b (rows: targets 16 tg + 4 g + e, columns: coefficients) and
@@ -1770,10 +1797,29 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
             else hi[r][e] = __fma_rn(d, 65536.0, hi[r][e]);
           }
       }
+      if constexpr (RS) {
+        if (tt == 0) {
+          // the dropped target's value in its lanes, the lift r from it,
+          // then r to every lane of the same coefficient column
+          const u64 qd = mods[td].q;
+          const double q = (double)qd, qinv = 1.0 / q, w32q = 4294967296.0 * qinv;
+          const u64 pinv = rs[2 * (size_t)td], pinvs = rs[2 * (size_t)td + 1];
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const double tq = fp_rint(__dmul_rn(hi[r][e_d], w32q));
+            const double y =
+                __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e_d], 4294967296.0)), lo[r][e_d]);
+            const u64 u = shoup_mul(sub_mod(xdc[r], fp_canon(y, qinv, q), qd), pinv, pinvs, qd);
+            const u64 ub = (u64)__shfl((long long)u, 16 * g_d + col);
+            rv[r] = ub;
+            rneg[r] = ub > (qd - 1) / 2;
+          }
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int t = 16 * tg + 4 * g + e;
-        if (t >= nd) continue;
+        if (t >= (RS ? td : nd)) continue;
         const int tl = t < t_split ? t : t + t_skip;
         const ModQ M = mods[prime_of(tl, q_limbs, L)];
         u64 *o = out + ((size_t)tl << logN) + k0 + col;
@@ -1781,11 +1827,22 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
           // y = hi 2^32 + lo: hi 2^32 is an exact double, the quotient by
           // round(hi 2^32 / q) leaves an exact residue, one reduction after
           const double q = (double)M.q, qinv = 1.0 / q, w32q = 4294967296.0 * qinv;
+          double2 pf{0.0, 0.0};
+          double ppd = 0.0;
+          if constexpr (RS) {
+            pf = rsf[t];
+            ppd = u52_to_dbl(rs[(size_t)td + t]);
+          }
 #pragma unroll
           for (int r = 0; r < R; r++) {
             const double tq = fp_rint(__dmul_rn(hi[r][e], w32q));
-            const double y =
+            double y =
                 __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e], 4294967296.0)), lo[r][e]);
+            if constexpr (RS) {
+              // |y| < 2q; the lift's product and [P p]_t keep it below 2^50
+              y = __dadd_rn(y, fp_mulmod(u52_to_dbl(rv[r]), pf.x, pf.y, q));
+              if (rneg[r]) y = __dsub_rn(y, ppd);
+            }
             o[16 * r] = fp_canon(y, qinv, q);
           }
         } else {
@@ -1795,7 +1852,13 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
             const long long hv = dbl_to_i51(hi[r][e]), lv = dbl_to_i51(lo[r][e]);
             const u64 h = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
             const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
-            o[16 * r] = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
+            u64 y = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
+            if constexpr (RS) {
+              const u64 pmM = rs[t];  // Montgomery form: the REDC of the product is r [P]_t
+              y = add_mod(y, redc(__umul64hi(rv[r], pmM), rv[r] * pmM, M.q, M.qinv), M.q);
+              if (rneg[r]) y = sub_mod(y, rs[(size_t)td + t], M.q);
+            }
+            o[16 * r] = y;
           }
         }
       }
@@ -1819,7 +1882,8 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
     hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
                        lds, c->stream,
                        src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg, t.wide_mask,
-                       src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0, c->d_mods);
+                       src_prime0, t_split, t_skip, q_limbs, c->L, centered ? 1 : 0, c->d_mods,
+                       (const u64 *)nullptr, (const double2 *)nullptr);
     LAUNCH_CHECK();
     return;
   }
@@ -2078,6 +2142,23 @@ void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst,
             (double)c->N * n_items * t.ns * t.nd);
   if (D < 1 || D > kMaxRescaleDrop || t.nd <= D || t.ns > kMaxDigitSize)
     throw std::invalid_argument("relinearise-rescale conversion: 1 <= primes < limbs");
+  // one dropped prime below 2^45: the int8 matrix-core conversion with the
+  // lift in its epilogue (the same words as the VALU kernels)
+  const int T1 = t.nd - 1;
+  if (D == 1 && c->bc_mfma && t.mf && c->primes[T1] < kFpPrimeBound &&
+      (size_t)t.n_k * t.n_tg * 512 * sizeof(u64) <= 65536) {
+    const double2 *rsf = (const double2 *)(rtab + 2 * (size_t)T1 + 2 + 3);
+    auto kern = t.n_k == 1   ? k_basis_convert_mfma<kMfmaRows, 1, kMfmaChunks, true>
+                : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks, true>
+                : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks, true>
+                             : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks, true>;
+    const size_t lds = sizeof(u64) * (size_t)t.n_k * t.n_tg * 512;
+    hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
+                       lds, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg,
+                       t.wide_mask, c->L, t.nd, 0, t.nd, c->L, 1, c->d_mods, rtab, rsf);
+    LAUNCH_CHECK();
+    return;
+  }
   dim3 grid(c->N / TPB, n_items);
   // the fp64 kernel needs the table's fp64 part and the dropped primes below
   // 2^45 (their values come from the fp64 sums)
