@@ -2127,7 +2127,10 @@ static void mul_relin_rescale(ckks_context *c, const ckks_ct *const *a, const ck
       o[i] = out[b0 + i] = new_ct(c, 2, limbs - primes, 0, a[b0 + i]->slots, scale, degree);
     }
     if (merged) {
-      relin_rescale_batch(c, p3.data(), nb, o.data(), primes, ps);
+      // relin_rescale_batch indexes the subtrahends from its own first item
+      PostSpec pss{};
+      if (ps) pss = PostSpec{ps->dbl, ps->sub ? ps->sub + b0 : nullptr, ps->scal};
+      relin_rescale_batch(c, p3.data(), nb, o.data(), primes, ps ? &pss : nullptr);
       continue;
     }
     relin_batch(c, p3.data(), nb, p2.data());

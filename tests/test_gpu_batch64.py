@@ -75,3 +75,29 @@ def test_keyswitch_batches_every_item(n):
     many = fhe.rescale_many(prods, ctx, primes=1)
     for i in (0, 31, 32, n - 1):
         assert np.array_equal(many[i].download(), orc.rescale(prods[i].download())), i
+
+
+@pytest.mark.parametrize("name", ["small", "keyswitch"])
+def test_postop_batches_past_64_match_single(name):
+    """The fused product's post-operation (x2, - sub) indexes each launch of
+    64 ciphertexts' subtrahends from that launch's first item: items 0, 63,
+    64 and 65 of a batch of 66 equal the same pair multiplied alone (each
+    single-pair form is held to the oracle by the parity tests)."""
+    from easyfhe import fhe
+
+    client, ctx = device_context(name)
+    slots = ctx.max_slots
+    rng = np.random.default_rng(66)
+    n = 66
+    zs = [rng.uniform(-1, 1, slots) for _ in range(n)]
+    cts = [client.encrypt(z, slots=slots, enc_id=5000 + i) for i, z in enumerate(zs)]
+    b = cts[::-1]
+    subs = cts[1:] + cts[:1]
+    outs = fhe.homo_mul_relin_rescale_postop_many(cts, b, ctx, apply_double=True, sub=subs)
+    for i in (0, 63, 64, 65):
+        one = fhe.homo_mul_relin_rescale_postop_many([cts[i]], [b[i]], ctx, apply_double=True,
+                                                    sub=[subs[i]])[0]
+        assert np.array_equal(outs[i].download(), one.download()), i
+    ratio = subs[65].state.scaling_factor / outs[65].state.scaling_factor
+    want = 2 * zs[65] * zs[0] - zs[0] * ratio
+    assert np.abs(client.decrypt(outs[65]) - want).max() < 1e-5
