@@ -1001,14 +1001,20 @@ struct KsJob {
 // ModDown of n accumulators acc = [n][2][E][N] (Q limbs then P limbs) into
 // the jobs' outputs, adding each job's addends (sigma-permuted): the P-part
 // iNTT, the centered conversion, then the forward NTT with the combine.
+// With ptmp given ([2 n][alpha][N]) and sp_done, ks_modup_inner's key
+// product left the P part there after the inverse NTT's low pass.
 static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<KsJob> &jobs,
-                       Scratch &s) {
+                       Scratch &s, u64 *ptmp = nullptr, bool sp_done = false) {
   const size_t N = c->N;
   const int E = limbs + c->alpha;
   const int n = (int)jobs.size();
-  u64 *ptmp = s.get((size_t)n * 2 * c->alpha * N);
-  launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N),
-             2 * n, limbs, c->alpha, limbs, true);
+  if (!ptmp) ptmp = s.get((size_t)n * 2 * c->alpha * N);
+  if (sp_done)
+    launch_ntt_inv_high(c, strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N), 2 * n, limbs,
+                        c->alpha, limbs);
+  else
+    launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N),
+               2 * n, limbs, c->alpha, limbs, true);
   u64 *conv = s.get((size_t)n * 2 * limbs * N);
   launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
                        2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
@@ -1097,21 +1103,26 @@ static u64 galois_inverse(const ckks_context *c, u64 g) {
 // ModUp of n polynomials d[i] (NTT domain) and the key inner product of
 // every job (job i takes ext item i; all share one key and Galois element)
 // into [n][2][E][N] accumulators.  At N = 2^16 the extended digits get only
-// the NTT's high pass and their low pass runs with the key product.
+// the NTT's high pass and their low pass runs with the key product.  With sp
+// given, *sp_done tells whether the P part went through the inverse NTT's
+// low pass into sp (launch_ntt_low_key) instead of into the accumulators.
 static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *d,
-                           const std::vector<KsJob> &jobs, Scratch &s) {
+                           const std::vector<KsJob> &jobs, Scratch &s,
+                           const Strided *sp = nullptr, bool *sp_done = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   const size_t est = (size_t)digits * E * N;
   u64 *ext = s.get((size_t)n * est);
   const bool fused = c->ks_fused && c->logN == 16 && n <= kMaxBatch;
+  const bool spf = fused && sp && c->ks_sp_inv && low_key_special_fp(c);
+  if (sp_done) *sp_done = spf;
   ks_modup(c, limbs, n, d, ext, s, false, fused);
   if (!fused) return ks_inner(c, limbs, ext, jobs, s, d);
   u64 *acc = s.get((size_t)n * 2 * E * N);
   Batch ob{};
   for (int i = 0; i < n; i++) ob.p[i] = (u64 *)d[i];
   launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
-                     galois_inverse(c, jobs[0].galois));
+                     galois_inverse(c, jobs[0].galois), spf ? sp : nullptr);
   return acc;
 }
 
@@ -1212,8 +1223,11 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, g, in[b0 + i]->d, nullptr, out[b0 + i]->d, out[b0 + i]->d + P};
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
-    ks_moddown(c, limbs, acc, jobs, s);
+    u64 *ptmp = s.get((size_t)nb * 2 * c->alpha * N);
+    const Strided sp{ptmp, (u64)c->alpha * N};
+    bool sp_done = false;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
+    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done);
   };
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
@@ -1239,8 +1253,11 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
     for (int i = 0; i < nb; i++)
       jobs[i] = KsJob{i, &key, 1, in[b0 + i]->d, in[b0 + i]->d + P, out[b0 + i]->d,
                       out[b0 + i]->d + P};
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
-    ks_moddown(c, limbs, acc, jobs, s);
+    u64 *ptmp = s.get((size_t)nb * 2 * c->alpha * N);
+    const Strided sp{ptmp, (u64)c->alpha * N};
+    bool sp_done = false;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
+    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done);
   };
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) run_parts(c, b0, std::min(kMaxBatch, n - b0), run);
 }
@@ -1283,12 +1300,18 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     const int E = limbs + A;
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s);
     // per item: [A] P limbs of X, then its limbs limbs-D .. limbs-1, as
     // coefficients
     const size_t xs = (size_t)(A + D) * N;
     u64 *x = s.get((size_t)nb * 2 * xs);
-    launch_ntt(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A, limbs, true);
+    const Strided sp{x, (u64)xs};
+    bool sp_done = false;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
+    if (sp_done)
+      launch_ntt_inv_high(c, strided(x - P, xs), 2 * nb, limbs, A, limbs);
+    else
+      launch_ntt(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A, limbs,
+                 true);
     Batch d3{}, o0{};
     for (int i = 0; i < nb; i++) {
       d3.p[i] = in[b0 + i]->d;
@@ -1422,6 +1445,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     c->bc_mfma = !(bc && strcmp(bc, "valu") == 0);
     const char *kf = getenv("CKKS_KEYSWITCH_FUSED");
     c->ks_fused = !(kf && strcmp(kf, "0") == 0);
+    const char *si = getenv("CKKS_KS_SPECIAL_INV");
+    c->ks_sp_inv = !(si && strcmp(si, "0") == 0);
     const char *ss = getenv("CKKS_SPLIT_STREAMS");
     if (ss) {
       c->split_parts = atoi(ss);

@@ -268,6 +268,10 @@ struct ckks_context {
   // inner product fused (launch_ntt_low_key); environment
   // CKKS_KEYSWITCH_FUSED=0 at creation selects the separate kernels
   bool ks_fused = true;
+  // with ks_fused and fp64 special primes, the special limbs of the key
+  // product also take the ModDown's inverse low pass in the same kernel;
+  // environment CKKS_KS_SPECIAL_INV=0 at creation keeps it separate
+  bool ks_sp_inv = true;
   // columns per block of the N = 2^16 column passes (16, 32 or 64), forward
   // and inverse; environment CKKS_NTT_COLS_FWD / CKKS_NTT_COLS_INV at creation
   int ntt_cols_fwd = 64, ntt_cols_inv = 32;
@@ -352,9 +356,18 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
 // are read from own) fused with the key inner product into acc (item it at
 // acc + it acc_stride, [2][E][N]); ginv = g^-1 mod 2N (1 for
 // relinearisation).  The words of launch_ntt's low pass then launch_key_inner.
+// With sp (only where low_key_special_fp holds), the special limbs' two
+// components also take the inverse NTT's low pass, into sp.base + (2 it + c)
+// sp.stride + (l - q_limbs) N, and are not written to acc: the ModDown then
+// runs launch_ntt_inv_high on them.
+bool low_key_special_fp(const ckks_context *c);
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
-                        int digits, int E, int q_limbs, u64 ginv);
+                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr);
+// N = 2^16: the high pass of the inverse NTT alone, in place (after the low
+// pass of launch_ntt_low_key's sp output)
+void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
+                         int q_limbs);
 void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &conv,
                             const Batch &add0, const Batch &add1, const u64 *galois,
                             const Batch &out0, const Batch &out1, int n_items, int limbs,

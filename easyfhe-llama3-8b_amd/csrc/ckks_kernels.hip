@@ -780,23 +780,18 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
   }
 }
 
-__device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
-                                                        int q_limbs, int L,
-                                                        const ModQ *__restrict__ mods,
-                                                        const double2 *__restrict__ itw) {
-  double *sm = reinterpret_cast<double *>(lds);
-  const int limb = l_begin + blockIdx.z;
-  const int p = prime_of(limb, q_limbs, L);
-  const double q = (double)mods[p].q, qinv = 1.0 / q;
-  const double2 *T = itw + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
-  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+// The fp64 inverse low pass of one tile of 16 rows held in the LDS tile sm
+// (position rl 256 + c of the tile at lds16(rl, c), values in [0, q)),
+// rows 16 tile .. 16 tile + 15 of the limb: round A on bit positions 3..0
+// from the 16 consecutive positions 16 c0 + j of row rl, round B on 7..4
+// from positions c0 + 16 k; the result (fp64 words of the pass) goes to
+// out[rl 256 + c0 + 16 k].  The caller has synchronised after filling sm.
+__device__ __forceinline__ void fp_inv_low_tile(double *__restrict__ sm, int tile,
+                                                const double2 *__restrict__ T, double q,
+                                                double qinv, u64 *__restrict__ out) {
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
-  const int row = blockIdx.x * 16 + rl;
+  const int row = tile * 16 + rl;
   double x[16];
-#pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
-  __syncthreads();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
 #pragma unroll
@@ -828,6 +823,24 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   }
 #pragma unroll
   for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = dbl_bits(x[k]);
+}
+
+__device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
+                                                        int q_limbs, int L,
+                                                        const ModQ *__restrict__ mods,
+                                                        const double2 *__restrict__ itw) {
+  double *sm = reinterpret_cast<double *>(lds);
+  const int limb = l_begin + blockIdx.z;
+  const int p = prime_of(limb, q_limbs, L);
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const double2 *T = itw + ((size_t)p << 16);
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
+  __syncthreads();
+  fp_inv_low_tile(sm, blockIdx.x, T, q, qinv, out);
 }
 
 template <int COLS>
@@ -1037,6 +1050,15 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
   }
 }
 
+void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
+                         int q_limbs) {
+  KTimer kt(c, "ntt_inv", 16.0 * c->N * n_items * l_count,
+            0.25 * c->N * c->logN * n_items * l_count);
+  if (n_items <= 0 || l_count <= 0) return;
+  if (c->logN != 16) throw std::invalid_argument("inverse high pass alone: N = 2^16 only");
+  launch_inv_high16(c, dst, n_items, l_begin, l_count, q_limbs);
+}
+
 // Forward NTT of the ModDown conversion conv (2 n items, Q limbs) with the
 // combine of k_moddown_combine fused into the low pass: the converted P part
 // is never written back.  N = 2^16 only.
@@ -1106,6 +1128,13 @@ struct LowKeyArgs {
   const u64 *key;     // [digits][2][K][N], Montgomery form, source order
   u64 ginv;           // inverse of the Galois element mod 2N (1: none)
   int digits, E, q_limbs, L, K, ds;
+  // with sp (fp64 special primes only): component c of special limb
+  // l >= q_limbs leaves through the inverse NTT's low pass, to
+  // sp + (2 it + c) sp_stride + ((l - q_limbs) << 16), and acc's special
+  // limbs are not written
+  u64 *sp;
+  size_t sp_stride;
+  const double2 *itw;
 };
 
 // 16 consecutive words from a 128-byte aligned address, as 8 loads of 16 bytes
@@ -1136,6 +1165,23 @@ __device__ __forceinline__ void low_key_store(u64 *__restrict__ sm, F word, u32 
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < 16; k++) out[tb + rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
+}
+
+// As low_key_store, then the inverse NTT's low pass of the permuted tile
+// (fp64 words in [0, q)) from the LDS tile into out + tb (fp_inv_low_tile).
+template <typename F>
+__device__ __forceinline__ void low_key_store_inv(double *__restrict__ sm, F word, u32 sb,
+                                                  u64 ginv, const double2 *__restrict__ T,
+                                                  double q, double qinv, u64 *__restrict__ out,
+                                                  u32 tb) {
+  __syncthreads();  // earlier reads of the tile are done
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const u32 t = ginv == 1 ? sb + i : autom_index(sb + i, ginv, 16);
+    sm[lds16((t >> 8) & 15, t & 255)] = word(i);
+  }
+  __syncthreads();
+  fp_inv_low_tile(sm, (int)(tb >> 12), T, q, qinv, out + tb);
 }
 
 // Per digit: the low pass leaves each thread the 16 consecutive positions
@@ -1192,13 +1238,21 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
   }
   // x 2^-64 (the keys' Montgomery factor), then canonical
   const double2 ri = rinv[p];
-  auto canon = [&](double x) {
-    double r = fp_reduce(fp_mulmod(x, ri.x, ri.y, q), qinv, q);
-    r = r < 0.0 ? __dadd_rn(r, q) : r;
-    return dbl_to_u52(r);
+  auto canon_d = [&](double x) {
+    const double r = fp_reduce(fp_mulmod(x, ri.x, ri.y, q), qinv, q);
+    return r < 0.0 ? __dadd_rn(r, q) : r;
   };
-  u64 *o = a.acc + it * a.acc_stride + ((size_t)l << 16);
+  auto canon = [&](double x) { return dbl_to_u52(canon_d(x)); };
   const u32 tb = a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u;
+  if (a.sp && l >= a.q_limbs) {
+    const double2 *Ti = a.itw + ((size_t)p << 16);
+    u64 *o = a.sp + 2 * (size_t)it * a.sp_stride + ((size_t)(l - a.q_limbs) << 16);
+    low_key_store_inv(sm, [&](int i) { return canon_d(acc0[i]); }, sb, a.ginv, Ti, q, qinv, o, tb);
+    low_key_store_inv(sm, [&](int i) { return canon_d(acc1[i]); }, sb, a.ginv, Ti, q, qinv,
+                      o + a.sp_stride, tb);
+    return;
+  }
+  u64 *o = a.acc + it * a.acc_stride + ((size_t)l << 16);
   u64 *smu = reinterpret_cast<u64 *>(sm);
   low_key_store(smu, [&](int i) { return canon(acc0[i]); }, sb, a.ginv, o, tb);
   low_key_store(smu, [&](int i) { return canon(acc1[i]); }, sb, a.ginv, o + ((size_t)a.E << 16),
@@ -1282,9 +1336,15 @@ __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_be
     low_key_64(lds, a, it, tile, l, p, mods, psi, psi_sh);
 }
 
+bool low_key_special_fp(const ckks_context *c) {
+  for (int j = 0; j < c->alpha; j++)
+    if (!c->prime_fp[c->L + j]) return false;
+  return true;
+}
+
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
-                        int digits, int E, int q_limbs, u64 ginv) {
+                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp) {
   KTimer kt(c, "ntt_low_key",
             8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
@@ -1306,6 +1366,12 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
   a.L = c->L;
   a.K = c->K;
   a.ds = c->ds;
+  if (sp) {
+    if (!low_key_special_fp(c)) throw std::invalid_argument("fused special inverse: fp64 special primes only");
+    a.sp = sp->base;
+    a.sp_stride = sp->stride;
+    a.itw = (const double2 *)c->d_itw_fp;
+  }
   // runs of limbs whose primes take the same body (q_0 and wide special
   // primes the 64-bit one)
   auto fp_limb = [&](int l) { return c->prime_fp[l < q_limbs ? l : c->L + (l - q_limbs)] != 0; };
