@@ -1750,6 +1750,12 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kMfmaRows = 2;    // 16-coefficient column tiles per wave and chunk
 constexpr int kMfmaChunks = 4;  // chunks of 4 waves x R tiles per block
 
+// Per-target constants staged in LDS after the digit table (words per
+// target): the ModQ of the target's prime (0..4), 1/q (5), the output limb
+// (6), 2^32/q (7), q as a double (8); with RS also [P]_t, [P]_t / q_t
+// (10, 11: the fp64 form), Montgomery [P]_t (12) and [P p]_t (13).
+constexpr int kBcTgtWords = 10, kBcTgtWordsRS = 14;
+
 // RS: the relinearise-rescale ModDown by P p (one dropped prime p = the
 // last target, td = nd - 1; k_bc_down_rescale states the algebra): the
 // dropped target's group runs first, its value y_td gives the centred lift
@@ -1802,6 +1808,37 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
   load(0);
   const int words = NK * n_tg * 512;
   for (int idx = threadIdx.x; idx < words; idx += TPB) tb[idx] = mtab[idx];
+  constexpr int TW = RS ? kBcTgtWordsRS : kBcTgtWords;
+  u64 *tgt = tb + words;
+  for (int t = threadIdx.x; t < nd; t += TPB) {
+    const int tl = t < t_split ? t : t + t_skip;
+    const ModQ M = mods[prime_of(tl, q_limbs, L)];
+    u64 *w = tgt + (size_t)t * TW;
+    w[0] = M.q;
+    w[1] = M.qinv;
+    w[2] = M.r2;
+    w[3] = M.mu;
+    w[4] = (u64)M.k | ((u64)M.pad << 32);
+    const double q = (double)M.q, qinv = 1.0 / q;
+    w[5] = dbl_bits(qinv);
+    w[6] = (u64)tl;
+    w[7] = dbl_bits(4294967296.0 * qinv);
+    w[8] = dbl_bits(q);
+    if constexpr (RS) {
+      if (t < td) {
+        w[10] = dbl_bits(rsf[t].x);
+        w[11] = dbl_bits(rsf[t].y);
+        w[12] = rs[t];
+        w[13] = rs[(size_t)td + t];
+      }
+    }
+  }
+  // RS: the dropped target's lift constants (uniform)
+  u64 pinv_d = 0, pinvs_d = 0;
+  if constexpr (RS) {
+    pinv_d = rs[2 * (size_t)td];
+    pinvs_d = rs[2 * (size_t)td + 1];
+  }
   __syncthreads();
   const int quad = n_tg * 512;
   for (int ch = 0; ch < CH; ch++) {
@@ -1867,9 +1904,10 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
         if (tt == 0) {
           // the dropped target's value in its lanes, the lift r from it,
           // then r to every lane of the same coefficient column
-          const u64 qd = mods[td].q;
-          const double q = (double)qd, qinv = 1.0 / q, w32q = 4294967296.0 * qinv;
-          const u64 pinv = rs[2 * (size_t)td], pinvs = rs[2 * (size_t)td + 1];
+          const u64 *wd = tgt + (size_t)td * TW;
+          const u64 qd = wd[0];
+          const double q = as_dbl(wd[8]), qinv = as_dbl(wd[5]), w32q = as_dbl(wd[7]);
+          const u64 pinv = pinv_d, pinvs = pinvs_d;
 #pragma unroll
           for (int r = 0; r < R; r++) {
             const double tq = fp_rint(__dmul_rn(hi[r][e_d], w32q));
@@ -1886,18 +1924,17 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
       for (int e = 0; e < 4; e++) {
         const int t = 16 * tg + 4 * g + e;
         if (t >= (RS ? td : nd)) continue;
-        const int tl = t < t_split ? t : t + t_skip;
-        const ModQ M = mods[prime_of(tl, q_limbs, L)];
-        u64 *o = out + ((size_t)tl << logN) + k0 + col;
-        if (M.q < kFpPrimeBound) {
+        const u64 *w = tgt + (size_t)t * TW;
+        u64 *o = out + ((size_t)w[6] << logN) + k0 + col;
+        if (w[0] < kFpPrimeBound) {
           // y = hi 2^32 + lo: hi 2^32 is an exact double, the quotient by
           // round(hi 2^32 / q) leaves an exact residue, one reduction after
-          const double q = (double)M.q, qinv = 1.0 / q, w32q = 4294967296.0 * qinv;
+          const double q = as_dbl(w[8]), qinv = as_dbl(w[5]), w32q = as_dbl(w[7]);
           double2 pf{0.0, 0.0};
           double ppd = 0.0;
           if constexpr (RS) {
-            pf = rsf[t];
-            ppd = u52_to_dbl(rs[(size_t)td + t]);
+            pf = double2{as_dbl(w[10]), as_dbl(w[11])};
+            ppd = u52_to_dbl(w[13]);
           }
 #pragma unroll
           for (int r = 0; r < R; r++) {
@@ -1913,6 +1950,13 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
           }
         } else {
           // q > 2^45 > |hi|, |lo|: one correction each, then the 64-bit product
+          ModQ M;
+          M.q = w[0];
+          M.qinv = w[1];
+          M.r2 = w[2];
+          M.mu = w[3];
+          M.k = (u32)w[4];
+          M.pad = (u32)(w[4] >> 32);
 #pragma unroll
           for (int r = 0; r < R; r++) {
             const long long hv = dbl_to_i51(hi[r][e]), lv = dbl_to_i51(lo[r][e]);
@@ -1920,9 +1964,9 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
             const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
             u64 y = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
             if constexpr (RS) {
-              const u64 pmM = rs[t];  // Montgomery form: the REDC of the product is r [P]_t
+              const u64 pmM = w[12];  // Montgomery form: the REDC of the product is r [P]_t
               y = add_mod(y, redc(__umul64hi(rv[r], pmM), rv[r] * pmM, M.q, M.qinv), M.q);
-              if (rneg[r]) y = sub_mod(y, rs[(size_t)td + t], M.q);
+              if (rneg[r]) y = sub_mod(y, w[13], M.q);
             }
             o[16 * r] = y;
           }
@@ -1944,7 +1988,8 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
                 : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks>
                 : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks>
                              : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks>;
-    const size_t lds = sizeof(u64) * (size_t)t.n_k * t.n_tg * 512;
+    const size_t lds =
+        sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWords);
     hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
                        lds, c->stream,
                        src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg, t.wide_mask,
@@ -2218,7 +2263,8 @@ void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst,
                 : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks, true>
                 : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks, true>
                              : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks, true>;
-    const size_t lds = sizeof(u64) * (size_t)t.n_k * t.n_tg * 512;
+    const size_t lds =
+        sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWordsRS);
     hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
                        lds, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg,
                        t.wide_mask, c->L, t.nd, 0, t.nd, c->L, 1, c->d_mods, rtab, rsf);
