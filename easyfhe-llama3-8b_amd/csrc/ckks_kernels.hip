@@ -304,9 +304,12 @@ __device__ __forceinline__ u64 apply_post(const PostOp &po, int item, int comp, 
 
 // Operands of the epilogue for the 16 outputs e(k) = tile + rl 256 + c0 + 16 k
 // of one thread, loaded at kernel entry so that their latency overlaps the
-// butterflies: acc - is kept, add (or 0) is summed in.
+// butterflies: acc - is kept, add (or 0) is summed in; the limb's constants
+// (P^-1, the addend's multiplier, the postop's scalar) are read here too, so
+// that the stores issue no loads but the postop's subtrahends (md_sub_load).
 struct MDPrefetch {
   u64 a[16], d[16];
+  u64 pinv, pinvs, am, ams, sc;
 };
 
 __device__ __forceinline__ void md_load(const MDCombine &md, int item2, int limb, u32 e0,
@@ -317,6 +320,11 @@ __device__ __forceinline__ void md_load(const MDCombine &md, int item2, int limb
   const u64 *ad = batch_ptr(md.add, item);
   if (comp) ad = (ad && md.add1_off) ? ad + md.add1_off : nullptr;
   const u64 g = md.gal.g[item];
+  pf.pinv = md.pinv[2 * limb];
+  pf.pinvs = md.pinv[2 * limb + 1];
+  pf.am = md.amul ? md.amul[2 * limb] : 0;
+  pf.ams = md.amul ? md.amul[2 * limb + 1] : 0;
+  pf.sc = md.post.scal && !comp ? md.post.scal[limb] : 0;
 #pragma unroll
   for (int k = 0; k < 16; k++) pf.a[k] = acc[e0 + 16 * k];
 #pragma unroll
@@ -326,14 +334,33 @@ __device__ __forceinline__ void md_load(const MDCombine &md, int item2, int limb
   }
 }
 
+// The postop's subtrahend words of the 16 outputs (all 0 without one), read
+// together before the stores.
+__device__ __forceinline__ void md_sub_load(const MDCombine &md, int item2, int limb, u32 e0,
+                                            u64 (&sv)[16]) {
+  const int item = item2 >> 1, comp = item2 & 1;
+  const u64 *sb = batch_ptr(md.post.sub, item);
+  if (sb) {
+    sb += (comp ? md.post.sub1_off : 0) + ((size_t)limb << 16);
+#pragma unroll
+    for (int k = 0; k < 16; k++) sv[k] = sb[e0 + 16 * k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) sv[k] = 0;
+  }
+}
+
+// (dbl ? 2 r : r) - s + sc with r = (a - y) P^-1 + d amul (apply_post's terms)
 __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int limb, u32 e, u64 y,
-                                         u64 a, u64 d, u64 q) {
+                                         const MDPrefetch &pf, u64 a, u64 d, u64 s, u64 q) {
   const int item = item2 >> 1, comp = item2 & 1;
   const size_t N = 65536;
-  u64 r = shoup_mul(sub_mod(a, y, q), md.pinv[2 * limb], md.pinv[2 * limb + 1], q);
-  if (md.amul) d = shoup_mul(d, md.amul[2 * limb], md.amul[2 * limb + 1], q);
+  u64 r = shoup_mul(sub_mod(a, y, q), pf.pinv, pf.pinvs, q);
+  if (md.amul) d = shoup_mul(d, pf.am, pf.ams, q);
   r = add_mod(r, d, q);
-  r = apply_post(md.post, item, comp, limb, e, N, r, q);
+  if (md.post.dbl) r = add_mod(r, r, q);
+  r = sub_mod(r, s, q);
+  if (pf.sc) r = add_mod(r, pf.sc, q);
   u64 *o = batch_ptr(md.out, item) + (comp ? md.out1_off : 0);
   o[(size_t)limb * N + e] = r;
 }
@@ -464,10 +491,13 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
   }
   __syncthreads();
   if constexpr (COMBINE) {
+    const u32 e0 = blockIdx.x * 4096 + rl * 256 + c0;
+    u64 sv[16];
+    md_sub_load(md, blockIdx.y, limb, e0, sv);
 #pragma unroll
     for (int k = 0; k < 16; k++)
-      md_store(md, blockIdx.y, limb, (u32)(blockIdx.x * 4096 + rl * 256 + c0 + 16 * k),
-               sm[lds16(rl, c0 + 16 * k)], pf.a[k], pf.d[k], q);
+      md_store(md, blockIdx.y, limb, e0 + 16 * k, sm[lds16(rl, c0 + 16 * k)], pf, pf.a[k],
+               pf.d[k], sv[k], q);
   } else {
 #pragma unroll
     for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = sm[lds16(rl, c0 + 16 * k)];
@@ -770,10 +800,13 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
   __syncthreads();
   if constexpr (COMBINE) {
     const u64 qu = mods[p].q;
+    const u32 e0 = blockIdx.x * 4096 + rl * 256 + c0;
+    u64 sv[16];
+    md_sub_load(md, blockIdx.y, limb, e0, sv);
 #pragma unroll
     for (int k = 0; k < 16; k++)
-      md_store(md, blockIdx.y, limb, (u32)(blockIdx.x * 4096 + rl * 256 + c0 + 16 * k),
-               smu[lds16(rl, c0 + 16 * k)], pf.a[k], pf.d[k], qu);
+      md_store(md, blockIdx.y, limb, e0 + 16 * k, smu[lds16(rl, c0 + 16 * k)], pf, pf.a[k],
+               pf.d[k], sv[k], qu);
   } else {
 #pragma unroll
     for (int k = 0; k < 16; k++) base[rl * 256 + c0 + 16 * k] = smu[lds16(rl, c0 + 16 * k)];
