@@ -2805,8 +2805,14 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // product is the exact fp64 residue of fp_mulmod (|r| < 1.5 q) and the
 // B-term sums stay exact integers below 2^53, reduced once at the end, so the
 // words equal the 64-bit path's.  Both paths run in one launch, so the slower
-// 64-bit blocks of q_0 overlap the others.
+// 64-bit blocks of q_0 overlap the others.  GT >= G groups are compiled: the
+// loads of a baby step's IC baby words and GT plaintext words issue together
+// (groups beyond G re-read group G - 1 and are not stored), one step ahead of
+// the products that use them.
 // grid (N / 256, limb_count, 2), limbs from l_begin
+typedef __attribute__((address_space(1))) u64 GlobalU64;
+
+template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict__ bab, int n,
                                                    const u64 *const *__restrict__ pts, int B,
                                                    int G, u64 *__restrict__ out, int limbs,
@@ -2821,29 +2827,43 @@ __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict_
     constexpr int IC = kTabCtsFp;
     const double q = (double)M.q, qinv = 1.0 / q;
     for (int i0 = 0; i0 < n; i0 += IC) {
-      double acc[kTabGroups][IC];
+      double acc[GT][IC];
 #pragma unroll
-      for (int g = 0; g < kTabGroups; g++)
+      for (int g = 0; g < GT; g++)
 #pragma unroll
         for (int c = 0; c < IC; c++) acc[g][c] = 0.0;
-      for (int b = 0; b < B; b++) {
-        double x[IC];
+      // the tables hold device pointers: global loads, not flat ones
+      u64 xw[IC], ww[GT];
+      auto issue = [&](int b) {
 #pragma unroll
         for (int c = 0; c < IC; c++)
-          x[c] = i0 + c < n ? u52_to_dbl(bab[(size_t)(i0 + c) * B + b][off]) : 0.0;
+          xw[c] = ((const GlobalU64 *)bab[(size_t)min(i0 + c, n - 1) * B + b])[off];
 #pragma unroll
-        for (int g = 0; g < kTabGroups; g++) {
-          if (g < G) {
-            const double w = u52_to_dbl(pts[(size_t)g * B + b][poff]);
-            const double wq = __dmul_rn(w, qinv);
+        for (int g = 0; g < GT; g++)
+          ww[g] = ((const GlobalU64 *)pts[(size_t)min(g, G - 1) * B + b])[poff];
+      };
+      issue(0);
+      for (int b = 0; b < B; b++) {
+        u64 xc[IC], wc[GT];
 #pragma unroll
-            for (int c = 0; c < IC; c++)
-              acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
-          }
+        for (int c = 0; c < IC; c++) xc[c] = xw[c];
+#pragma unroll
+        for (int g = 0; g < GT; g++) wc[g] = ww[g];
+        if (b + 1 < B) issue(b + 1);  // the next step's words in flight
+        __builtin_amdgcn_sched_barrier(0);
+        double x[IC];
+#pragma unroll
+        for (int c = 0; c < IC; c++) x[c] = u52_to_dbl(xc[c]);
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+          const double w = u52_to_dbl(wc[g]);
+          const double wq = __dmul_rn(w, qinv);
+#pragma unroll
+          for (int c = 0; c < IC; c++) acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
         }
       }
 #pragma unroll
-      for (int g = 0; g < kTabGroups; g++)
+      for (int g = 0; g < GT; g++)
 #pragma unroll
         for (int c = 0; c < IC; c++)
           if (g < G && i0 + c < n)
@@ -2894,7 +2914,9 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
   dim3 grid(c->N / TPB, limbs, 2);
-  hipLaunchKernelGGL(k_mac_table, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs, 0,
+  auto kern = G <= 1 ? k_mac_table<1> : G <= 2 ? k_mac_table<2> : G <= 4 ? k_mac_table<4>
+                                                                           : k_mac_table<kTabGroups>;
+  hipLaunchKernelGGL(kern, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs, 0,
                      c->logN, c->d_mods);
   LAUNCH_CHECK();
 }
