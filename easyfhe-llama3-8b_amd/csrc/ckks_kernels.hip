@@ -2440,15 +2440,25 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
 // i.e. the automorphism is applied on the output side, so each thread reads
 // the extended digits (and c0) at its own index s once for all babies.  With
 // c0 given, acc_b,0[t] += P c0[s] on the Q limbs (the extended lift).
-// grid (N / 256, E); up to kMultiItems items per launch.
+// grid (N / 256, E); up to kMultiItems items per launch.  At N = 2^16 the
+// 16 blocks of a tile of 16 rows (4096 positions, which the automorphisms
+// map onto one tile) share blockIdx.x % 8, so they run on one XCD and the
+// permuted stores of the tile fill whole lines in one L2.  Limbs whose prime
+// is below 2^45 take fp64 products (exact residues, as the fused low pass +
+// key product: the sum times 2^-64, the keys' Montgomery factor, then
+// canonical; the same words).
 // ===========================================================================
 
 template <int MD>
 __global__ __launch_bounds__(TPB) void k_key_inner_multi(
     Strided ext, int n_items, MultiKeys mk, int n_babies, Batch c0, const u64 *__restrict__ pmod,
     const u64 *const *__restrict__ outp, int digits, int E, int q_limbs, int L, int K, int logN,
-    const ModQ *__restrict__ mods) {
-  const int s = blockIdx.x * TPB + threadIdx.x;
+    const ModQ *__restrict__ mods, const double2 *__restrict__ rinv) {
+  int s = blockIdx.x * TPB + threadIdx.x;
+  if (logN == 16) {
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    s = ((((j >> 4) << 3) | xcd) << 12) + ((j & 15) << 8) + threadIdx.x;
+  }
   const int l = blockIdx.y;
   const int p = prime_of(l, q_limbs, L);
   const ModQ M = mods[p];
@@ -2467,6 +2477,50 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
       pc[it] = (lift && c) ? shoup_mul(c[(size_t)l * N + s], pmod[2 * l], pmod[2 * l + 1], M.q)
                            : 0;
     }
+  }
+  if (M.q < kFpPrimeBound) {
+    const double q = (double)M.q, qinv = 1.0 / q;
+    const double2 ri = rinv[p];
+    double xd[kMultiItems][MD];
+#pragma unroll
+    for (int it = 0; it < kMultiItems; it++)
+#pragma unroll
+      for (int j = 0; j < MD; j++)
+        xd[it][j] = it < n_items && j < digits ? u52_to_dbl(x[it][j]) : 0.0;
+    for (int b = 0; b < n_babies; b++) {
+      const u32 t = autom_index((u32)s, mk.ginv[b], logN);
+      const u64 *key = mk.key[b];
+      double kb[MD], kbq[MD], ka[MD], kaq[MD];
+#pragma unroll
+      for (int j = 0; j < MD; j++) {
+        if (j < digits) {
+          kb[j] = u52_to_dbl(key[((size_t)(2 * j) * K + p) * N + s]);
+          ka[j] = u52_to_dbl(key[((size_t)(2 * j + 1) * K + p) * N + s]);
+          kbq[j] = __dmul_rn(kb[j], qinv);
+          kaq[j] = __dmul_rn(ka[j], qinv);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < kMultiItems; it++) {
+        if (it < n_items) {
+          // |sum| < 1.5 q digits < 2^49
+          double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+          for (int j = 0; j < MD; j++) {
+            if (j < digits) {
+              a0 = __dadd_rn(a0, fp_mulmod(xd[it][j], kb[j], kbq[j], q));
+              a1 = __dadd_rn(a1, fp_mulmod(xd[it][j], ka[j], kaq[j], q));
+            }
+          }
+          const u64 r0 = fp_canon(fp_mulmod(a0, ri.x, ri.y, q), qinv, q);
+          const u64 r1 = fp_canon(fp_mulmod(a1, ri.x, ri.y, q), qinv, q);
+          u64 *o = (u64 *)outp[(size_t)b * n_items + it];
+          o[(size_t)l * N + t] = add_mod(r0, pc[it], M.q);
+          o[((size_t)E + l) * N + t] = r1;
+        }
+      }
+    }
+    return;
   }
   for (int b = 0; b < n_babies; b++) {
     const u32 t = autom_index((u32)s, mk.ginv[b], logN);
@@ -2519,11 +2573,13 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
   if (digits <= 4)
     hipLaunchKernelGGL(k_key_inner_multi<4>, grid, dim3(TPB), 0, c->stream,
                        Strided{(u64 *)ext, ext_stride}, n_items, mk, nb, c0, c->d_pmod, d_outp,
-                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods);
+                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods,
+                       (const double2 *)c->d_rinv_fp);
   else
     hipLaunchKernelGGL(k_key_inner_multi<kMaxDigits>, grid, dim3(TPB), 0, c->stream,
                        Strided{(u64 *)ext, ext_stride}, n_items, mk, nb, c0, c->d_pmod, d_outp,
-                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods);
+                       digits, E, q_limbs, c->L, c->K, c->logN, c->d_mods,
+                       (const double2 *)c->d_rinv_fp);
   LAUNCH_CHECK();
 }
 
@@ -2734,7 +2790,12 @@ void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u
 // babies for kMacCts ciphertexts at a time with the plaintext words of every
 // group in registers: every baby word is read from HBM once for all groups,
 // and a plaintext word is re-read (from L2) once per kMacCts ciphertexts.
+// Limbs whose prime is below 2^45 (with B <= 64) take the fp64 path of
+// k_mac_table (exact residues, sums below 2^53, one reduction; the same
+// words), kMacCtsFp ciphertexts per plaintext read, with GT >= G groups
+// compiled and a baby step's loads issued one step ahead of its products.
 // grid (N / 256, E, 2)
+template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, int n, Batch pts,
                                                   int B, int G, u64 *__restrict__ out, int E,
                                                   int q_limbs, int L, int logN,
@@ -2744,6 +2805,52 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
   const size_t N = (size_t)1 << logN, EP = 2 * (size_t)E * N;
   const ModQ M = mods[prime_of(l, q_limbs, L)];
   const size_t off = ((size_t)comp * E + l) * N + k;
+  if (M.q < ((u64)1 << 45) && B <= 64) {
+    constexpr int IC = kMacCtsFp;
+    const double q = (double)M.q, qinv = 1.0 / q;
+    const size_t poff = (size_t)l * N + k;
+    for (int i0 = 0; i0 < n; i0 += IC) {
+      double acc[GT][IC];
+#pragma unroll
+      for (int g = 0; g < GT; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++) acc[g][c] = 0.0;
+      u64 xw[IC], ww[GT];
+      auto issue = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < IC; c++) xw[c] = bab[((size_t)b * n + min(i0 + c, n - 1)) * EP + off];
+#pragma unroll
+        for (int g = 0; g < GT; g++) ww[g] = batch_ptr(pts, min(g, G - 1) * B + b)[poff];
+      };
+      issue(0);
+      for (int b = 0; b < B; b++) {
+        u64 xc[IC], wc[GT];
+#pragma unroll
+        for (int c = 0; c < IC; c++) xc[c] = xw[c];
+#pragma unroll
+        for (int g = 0; g < GT; g++) wc[g] = ww[g];
+        if (b + 1 < B) issue(b + 1);  // the next step's words in flight
+        __builtin_amdgcn_sched_barrier(0);
+        double x[IC];
+#pragma unroll
+        for (int c = 0; c < IC; c++) x[c] = u52_to_dbl(xc[c]);
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+          const double w = u52_to_dbl(wc[g]);
+          const double wq = __dmul_rn(w, qinv);
+#pragma unroll
+          for (int c = 0; c < IC; c++) acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GT; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++)
+          if (g < G && i0 + c < n)
+            out[((size_t)g * n + i0 + c) * EP + off] = fp_canon(acc[g][c], qinv, q);
+    }
+    return;
+  }
   for (int i0 = 0; i0 < n; i0 += kMacCts) {
     u64 acc[kMacGroups][kMacCts], hi[kMacGroups][kMacCts], lo[kMacGroups][kMacCts];
 #pragma unroll
@@ -2789,8 +2896,8 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
   if (G < 1 || G > kMacGroups || G * B > kMaxBatch)
     throw std::invalid_argument("mac_many: 1 <= groups <= 2 and groups x babies <= 64");
   dim3 grid(c->N / TPB, E, 2);
-  hipLaunchKernelGGL(k_mac_many, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, E,
-                     q_limbs, c->L, c->logN, c->d_mods);
+  hipLaunchKernelGGL(G <= 1 ? k_mac_many<1> : k_mac_many<kMacGroups>, grid, dim3(TPB), 0,
+                     c->stream, bab, n, pts, B, G, out, E, q_limbs, c->L, c->logN, c->d_mods);
   LAUNCH_CHECK();
 }
 
