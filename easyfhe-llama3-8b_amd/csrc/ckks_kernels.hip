@@ -2908,29 +2908,29 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // Each thread walks the babies of kTabCts ciphertexts at a time with the
 // groups' plaintext words in registers: a baby word is read once per pass, a
 // plaintext word (from L2) once per kTabCts ciphertexts.
-// Limbs whose prime is below 2^45 (with B <= 64) take the fp64 path: each
+// Limbs whose prime is below 2^45 (with B <= 64) take the fp64 kernel: each
 // product is the exact fp64 residue of fp_mulmod (|r| < 1.5 q) and the
 // B-term sums stay exact integers below 2^53, reduced once at the end, so the
-// words equal the 64-bit path's.  Both paths run in one launch, so the slower
-// 64-bit blocks of q_0 overlap the others.  GT >= G groups are compiled: the
-// loads of a baby step's IC baby words and GT plaintext words issue together
-// (groups beyond G re-read group G - 1 and are not stored), one step ahead of
-// the products that use them.
+// words equal the 64-bit kernel's.  The two are separate kernels, each with
+// its own register allocation.  GT >= G groups are compiled: the loads of a
+// baby step's IC baby words and GT plaintext words issue together (groups
+// beyond G re-read group G - 1 and are not stored), one step ahead of the
+// products that use them.
 // grid (N / 256, limb_count, 2), limbs from l_begin
 typedef __attribute__((address_space(1))) u64 GlobalU64;
 
 template <int GT>
-__global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict__ bab, int n,
-                                                   const u64 *const *__restrict__ pts, int B,
-                                                   int G, u64 *__restrict__ out, int limbs,
-                                                   int l_begin, int logN,
-                                                   const ModQ *__restrict__ mods) {
+__global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restrict__ bab, int n,
+                                                      const u64 *const *__restrict__ pts, int B,
+                                                      int G, u64 *__restrict__ out, int limbs,
+                                                      int l_begin, int logN,
+                                                      const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int l = l_begin + blockIdx.y, comp = blockIdx.z;
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
-  if (M.q < ((u64)1 << 45) && B <= 64) {
+  {
     constexpr int IC = kTabCtsFp;
     const double q = (double)M.q, qinv = 1.0 / q;
     for (int i0 = 0; i0 < n; i0 += IC) {
@@ -2976,8 +2976,19 @@ __global__ __launch_bounds__(TPB) void k_mac_table(const u64 *const *__restrict_
           if (g < G && i0 + c < n)
             out[((size_t)g * n + i0 + c) * CP + off] = fp_canon(acc[g][c], qinv, q);
     }
-    return;
   }
+}
+
+__global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restrict__ bab, int n,
+                                                      const u64 *const *__restrict__ pts, int B,
+                                                      int G, u64 *__restrict__ out, int limbs,
+                                                      int l_begin, int logN,
+                                                      const ModQ *__restrict__ mods) {
+  const int k = blockIdx.x * TPB + threadIdx.x;
+  const int l = l_begin + blockIdx.y, comp = blockIdx.z;
+  const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
+  const ModQ M = mods[l];
+  const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
   for (int i0 = 0; i0 < n; i0 += kTabCts) {
     u64 acc[kTabGroups][kTabCts], hi[kTabGroups][kTabCts], lo[kTabGroups][kTabCts];
 #pragma unroll
@@ -3020,12 +3031,35 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
             2.0 * c->N * limbs * (double)n * B * G);
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
-  dim3 grid(c->N / TPB, limbs, 2);
-  auto kern = G <= 1 ? k_mac_table<1> : G <= 2 ? k_mac_table<2> : G <= 4 ? k_mac_table<4>
-                                                                           : k_mac_table<kTabGroups>;
-  hipLaunchKernelGGL(kern, grid, dim3(TPB), 0, c->stream, bab, n, pts, B, G, out, limbs, 0,
-                     c->logN, c->d_mods);
-  LAUNCH_CHECK();
+  auto fp_kern = G <= 1   ? k_mac_table_fp<1>
+                 : G <= 2 ? k_mac_table_fp<2>
+                 : G <= 4 ? k_mac_table_fp<4>
+                          : k_mac_table_fp<kTabGroups>;
+  auto fp_limb = [&](int l) { return B <= 64 && c->prime_fp[l] != 0; };
+  auto launch_run = [&](int l0, int l1, hipStream_t st) {
+    hipLaunchKernelGGL(fp_limb(l0) ? fp_kern : k_mac_table_64, dim3(c->N / TPB, l1 - l0, 2),
+                       dim3(TPB), 0, st, bab, n, pts, B, G, out, limbs, l0, c->logN, c->d_mods);
+    LAUNCH_CHECK();
+  };
+  // runs of limbs of one kind; with both kinds and a second stream, the
+  // 64-bit runs (q_0) run beside the fp64 ones
+  std::vector<std::pair<int, int>> runs;
+  for (int l0 = 0; l0 < limbs;) {
+    int l1 = l0 + 1;
+    while (l1 < limbs && fp_limb(l1) == fp_limb(l0)) l1++;
+    runs.emplace_back(l0, l1);
+    l0 = l1;
+  }
+  const bool fork = runs.size() > 1 && c->aux[0] && c->stream != c->aux[0];
+  if (fork) {
+    HIP_OK(hipEventRecord(c->fork_ev, c->stream));
+    HIP_OK(hipStreamWaitEvent(c->aux[0], c->fork_ev, 0));
+  }
+  for (auto [l0, l1] : runs) launch_run(l0, l1, fork && !fp_limb(l0) ? c->aux[0] : c->stream);
+  if (fork) {
+    HIP_OK(hipEventRecord(c->join_ev[0], c->aux[0]));
+    HIP_OK(hipStreamWaitEvent(c->stream, c->join_ev[0], 0));
+  }
 }
 
 // Extended-basis babies.  Offset 0: out = (P c0, P c1) on the Q limbs and 0
