@@ -2979,50 +2979,65 @@ __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restri
   }
 }
 
+// The 64-bit kernel: 128-bit sums of 64-bit products, reduced every 16 babies
+// (below q 2^64 for q < 2^60); GT >= G groups compiled, a baby step's loads
+// issued together one step ahead, and each block takes kTabCts ciphertexts
+// (blockIdx.z = component + 2 x ciphertext group), so that a single limb (q_0)
+// still fills the chip.
+template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restrict__ bab, int n,
                                                       const u64 *const *__restrict__ pts, int B,
                                                       int G, u64 *__restrict__ out, int limbs,
                                                       int l_begin, int logN,
                                                       const ModQ *__restrict__ mods) {
+  constexpr int IC = kTabCts;
   const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = l_begin + blockIdx.y, comp = blockIdx.z;
+  const int l = l_begin + blockIdx.y, comp = blockIdx.z & 1, i0 = (blockIdx.z >> 1) * IC;
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
-  for (int i0 = 0; i0 < n; i0 += kTabCts) {
-    u64 acc[kTabGroups][kTabCts], hi[kTabGroups][kTabCts], lo[kTabGroups][kTabCts];
+  u64 acc[GT][IC], hi[GT][IC], lo[GT][IC];
 #pragma unroll
-    for (int g = 0; g < kTabGroups; g++)
+  for (int g = 0; g < GT; g++)
 #pragma unroll
-      for (int c = 0; c < kTabCts; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
-    for (int b = 0; b < B; b++) {
-      u64 x[kTabCts];
+    for (int c = 0; c < IC; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+  u64 xw[IC], ww[GT];
+  auto issue = [&](int b) {
 #pragma unroll
-      for (int c = 0; c < kTabCts; c++) x[c] = i0 + c < n ? bab[(size_t)(i0 + c) * B + b][off] : 0;
+    for (int c = 0; c < IC; c++)
+      xw[c] = ((const GlobalU64 *)bab[(size_t)min(i0 + c, n - 1) * B + b])[off];
 #pragma unroll
-      for (int g = 0; g < kTabGroups; g++) {
-        if (g < G) {
-          const u64 w = pts[(size_t)g * B + b][poff];
+    for (int g = 0; g < GT; g++)
+      ww[g] = ((const GlobalU64 *)pts[(size_t)min(g, G - 1) * B + b])[poff];
+  };
+  issue(0);
+  for (int b = 0; b < B; b++) {
+    u64 xc[IC], wc[GT];
 #pragma unroll
-          for (int c = 0; c < kTabCts; c++) mac_wide(hi[g][c], lo[g][c], x[c], w);
+    for (int c = 0; c < IC; c++) xc[c] = xw[c];
+#pragma unroll
+    for (int g = 0; g < GT; g++) wc[g] = ww[g];
+    if (b + 1 < B) issue(b + 1);  // the next step's words in flight
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < GT; g++)
+#pragma unroll
+      for (int c = 0; c < IC; c++) mac_wide(hi[g][c], lo[g][c], xc[c], wc[g]);
+    if ((b & 15) == 15 || b == B - 1) {
+#pragma unroll
+      for (int g = 0; g < GT; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++) {
+          acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
+          hi[g][c] = lo[g][c] = 0;
         }
-      }
-      if ((b & 15) == 15 || b == B - 1) {
-#pragma unroll
-        for (int g = 0; g < kTabGroups; g++)
-#pragma unroll
-          for (int c = 0; c < kTabCts; c++) {
-            acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
-            hi[g][c] = lo[g][c] = 0;
-          }
-      }
     }
-#pragma unroll
-    for (int g = 0; g < kTabGroups; g++)
-#pragma unroll
-      for (int c = 0; c < kTabCts; c++)
-        if (g < G && i0 + c < n) out[((size_t)g * n + i0 + c) * CP + off] = to_mont(acc[g][c], M);
   }
+#pragma unroll
+  for (int g = 0; g < GT; g++)
+#pragma unroll
+    for (int c = 0; c < IC; c++)
+      if (g < G && i0 + c < n) out[((size_t)g * n + i0 + c) * CP + off] = to_mont(acc[g][c], M);
 }
 
 void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *const *pts, int B,
@@ -3035,10 +3050,19 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
                  : G <= 2 ? k_mac_table_fp<2>
                  : G <= 4 ? k_mac_table_fp<4>
                           : k_mac_table_fp<kTabGroups>;
+  auto w_kern = G <= 1   ? k_mac_table_64<1>
+                : G <= 2 ? k_mac_table_64<2>
+                : G <= 4 ? k_mac_table_64<4>
+                         : k_mac_table_64<kTabGroups>;
   auto fp_limb = [&](int l) { return B <= 64 && c->prime_fp[l] != 0; };
   auto launch_run = [&](int l0, int l1, hipStream_t st) {
-    hipLaunchKernelGGL(fp_limb(l0) ? fp_kern : k_mac_table_64, dim3(c->N / TPB, l1 - l0, 2),
-                       dim3(TPB), 0, st, bab, n, pts, B, G, out, limbs, l0, c->logN, c->d_mods);
+    if (fp_limb(l0))
+      hipLaunchKernelGGL(fp_kern, dim3(c->N / TPB, l1 - l0, 2), dim3(TPB), 0, st, bab, n, pts, B,
+                         G, out, limbs, l0, c->logN, c->d_mods);
+    else
+      hipLaunchKernelGGL(w_kern, dim3(c->N / TPB, l1 - l0, 2 * ((n + kTabCts - 1) / kTabCts)),
+                         dim3(TPB), 0, st, bab, n, pts, B, G, out, limbs, l0, c->logN,
+                         c->d_mods);
     LAUNCH_CHECK();
   };
   // runs of limbs of one kind; with both kinds and a second stream, the
