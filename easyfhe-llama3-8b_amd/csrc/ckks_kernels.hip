@@ -2852,39 +2852,47 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
     return;
   }
   for (int i0 = 0; i0 < n; i0 += kMacCts) {
-    u64 acc[kMacGroups][kMacCts], hi[kMacGroups][kMacCts], lo[kMacGroups][kMacCts];
+    constexpr int IC = kMacCts;
+    u64 acc[GT][IC], hi[GT][IC], lo[GT][IC];
 #pragma unroll
-    for (int g = 0; g < kMacGroups; g++)
+    for (int g = 0; g < GT; g++)
 #pragma unroll
-      for (int c = 0; c < kMacCts; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+      for (int c = 0; c < IC; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+    // a baby step's words issued together, one step ahead of their products
+    u64 xw[IC], ww[GT];
+    auto issue = [&](int b) {
+#pragma unroll
+      for (int c = 0; c < IC; c++) xw[c] = bab[((size_t)b * n + min(i0 + c, n - 1)) * EP + off];
+#pragma unroll
+      for (int g = 0; g < GT; g++) ww[g] = batch_ptr(pts, min(g, G - 1) * B + b)[(size_t)l * N + k];
+    };
+    issue(0);
     for (int b = 0; b < B; b++) {
-      u64 pt[kMacGroups];
+      u64 xc[IC], wc[GT];
 #pragma unroll
-      for (int g = 0; g < kMacGroups; g++)
-        pt[g] = g < G ? batch_ptr(pts, g * B + b)[(size_t)l * N + k] : 0;
+      for (int c = 0; c < IC; c++) xc[c] = xw[c];
 #pragma unroll
-      for (int c = 0; c < kMacCts; c++) {
-        if (i0 + c < n) {
-          const u64 x = bab[((size_t)b * n + i0 + c) * EP + off];
+      for (int g = 0; g < GT; g++) wc[g] = ww[g];
+      if (b + 1 < B) issue(b + 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int g = 0; g < kMacGroups; g++)
-            if (g < G) mac_wide(hi[g][c], lo[g][c], x, pt[g]);
-        }
-      }
+      for (int g = 0; g < GT; g++)
+#pragma unroll
+        for (int c = 0; c < IC; c++) mac_wide(hi[g][c], lo[g][c], xc[c], wc[g]);
       if ((b & 15) == 15 || b == B - 1) {
 #pragma unroll
-        for (int g = 0; g < kMacGroups; g++)
+        for (int g = 0; g < GT; g++)
 #pragma unroll
-          for (int c = 0; c < kMacCts; c++) {
+          for (int c = 0; c < IC; c++) {
             acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
             hi[g][c] = lo[g][c] = 0;
           }
       }
     }
 #pragma unroll
-    for (int g = 0; g < kMacGroups; g++)
+    for (int g = 0; g < GT; g++)
 #pragma unroll
-      for (int c = 0; c < kMacCts; c++)
+      for (int c = 0; c < IC; c++)
         if (g < G && i0 + c < n) out[((size_t)g * n + i0 + c) * EP + off] = to_mont(acc[g][c], M);
   }
 }
