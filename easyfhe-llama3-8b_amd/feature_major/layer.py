@@ -408,7 +408,9 @@ def refreshed_layer_programs(crypto_context, approx: LayerApproximations, seq_le
 def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, crypto_context,
                                 program, residual_program=None, residual_bound: float = 32.0,
                                 group: int = 8, rope_theta: float = 500000.0,
-                                normaliser_program=None, rmsnorm_program=None) -> LayerResult:
+                                normaliser_program=None, rmsnorm_program=None,
+                                pairfm_refresh_min_limbs: int | None = None,
+                                pv_value_bound: float = 8.0) -> LayerResult:
     """One decoder layer with its refreshes (three paired refresh points: the
     residual stream before each RMSNorm, and the softmax's mapped scores;
     the reference refreshes at the same places, graph.py:780-990,
@@ -424,6 +426,14 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
     (``rmsnorm_slim_program()``) the post-attention RMSNorm refreshes its
     slim series instead of spending the stream's levels on it, which
     shortens the last block (``refreshed_layer_programs(slim_rmsnorm=True)``).
+    With ``pairfm_refresh_min_limbs`` the attention output is refreshed
+    with the residual program (values through ``pv_value_bound``) when it
+    reaches the pairing for W_o below that many limbs: the reference's
+    PairFM threshold refresh (operators/attention/config.py:44-56,
+    ``pairfm_post_refresh_input_limbs`` of schedule.py), which its release
+    schedule fires only where the PV output runs short.  The depth plan
+    here keeps the output above the W_o block's need, so the refresh fires
+    only for thresholds above that (stage ``refresh_pv_output``).
     The input may sit at any level; it is not consumed."""
     from easyfhe.bs import openfhe as bs
 
@@ -492,8 +502,21 @@ def decoder_layer_refreshed_fhe(input_ciphers, weights: DecoderLayerWeights, *, 
         att = pv_output(probs.ciphers, v, geo, crypto_context=ctx)
         probs.release()
         _release(v)
-        za = pair_real_ciphers(att.ciphers, crypto_context=ctx)
-        att.release()
+        att_c = list(att.ciphers)
+        if (pairfm_refresh_min_limbs is not None
+                and int(att_c[0].state.cur_limbs) < int(pairfm_refresh_min_limbs)):
+            sync()
+            t1 = time.perf_counter()
+            att_c = refresh_stream(att_c, crypto_context=ctx, program=res_prog,
+                                   value_bound=pv_value_bound, group=group)
+            att.release()
+            sync()
+            stage["refresh_pv_output"] = time.perf_counter() - t1
+        za = pair_real_ciphers(att_c, crypto_context=ctx)
+        if att.ciphers:
+            att.release()
+        else:
+            _release(att_c)
         o = _paired_projection(op, za, weights.o, ctx)
         op.release_babies(za)
         _release(za)

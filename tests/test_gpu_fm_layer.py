@@ -440,6 +440,59 @@ def test_refreshed_decoder_layer_matches_poly_model():
     assert e1 < 1e-3 and e2 < 2e-3, (e1, e2)
 
 
+def test_pv_output_threshold_refresh():
+    """The PairFM threshold refresh (reference operators/attention/config.py:
+    44-56): with a threshold above the attention output's limbs, the output
+    is refreshed before the pairing for W_o (stage ``refresh_pv_output``) and
+    the layer still matches the fp64 model; with the default (no threshold)
+    the stage does not run.  64 tokens x 512 features at N = 2^13."""
+    from feature_major import FeatureMajorPrefillLayout
+    from feature_major.approx import rsqrt_entry, silu_entry
+    from feature_major.attention import SoftmaxConfig
+    from feature_major.layer import (DecoderLayerWeights, LayerApproximations,
+                                     decoder_layer_refreshed_fhe, decoder_layer_rotations,
+                                     refreshed_layer_programs)
+
+    T, D, H, KV, hd, I = 64, 512, 4, 2, 128, 1408
+    lay0 = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=4096)
+    client, ctx = device_context(FM_REFRESH, rotations=decoder_layer_rotations(lay0, H, hd))
+    norm = rsqrt_entry(0.5, 16.0, 63)
+    ap = LayerApproximations(norm, norm, silu_entry(), SoftmaxConfig(rounds=2, shift=4.0,
+                                                                     bound=4.0))
+    prog, res_prog = refreshed_layer_programs(ctx, ap, T, log_slots=12)
+    rng = np.random.default_rng(17)
+    x = rng.normal(0, 1, (T, D))
+    sd = 1.0 / np.sqrt(D)
+    wq, wo = rng.normal(0, sd, (D, D)), rng.normal(0, sd, (D, D))
+    wk, wv = rng.normal(0, sd, (KV * hd, D)), rng.normal(0, sd, (KV * hd, D))
+    G, U = rng.normal(0, sd, (I, D)), rng.normal(0, sd, (I, D))
+    Dn = rng.normal(0, 1.0 / np.sqrt(I), (D, I))
+    lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=ctx.max_slots)
+    packed = lay.pack(x)
+    xc = [client.encrypt(packed[i], cur_limbs=1, enc_id=1900 + i) for i in range(lay.cipher_count)]
+    sm = ap.softmax
+    kw = dict(heads=H, kv_heads=KV, head_dim=hd, input_norm=ap.input_norm,
+              post_attention_norm=ap.post_attention_norm, silu=ap.silu,
+              probs_fn=lambda s: LN.softmax_alg2_numpy(s, sm.exp(), sm.first_inverse(),
+                                                       sm.inverse(T), rounds=sm.rounds,
+                                                       shift=sm.shift))
+    want = LN.decoder_layer_numpy(x, wq, wk, wv, wo, G, U, Dn, **kw)
+    with DecoderLayerWeights(wq, wk, wv, wo, G, U, Dn, heads=H, kv_heads=KV, head_dim=hd,
+                             intermediate=I, approx=ap, layout=lay, context=ctx) as w:
+        plain = decoder_layer_refreshed_fhe(xc, w, crypto_context=ctx, program=prog,
+                                            residual_program=res_prog)
+        forced = decoder_layer_refreshed_fhe(xc, w, crypto_context=ctx, program=prog,
+                                             residual_program=res_prog,
+                                             pairfm_refresh_min_limbs=64)
+    assert "refresh_pv_output" not in plain.stage_seconds
+    assert "refresh_pv_output" in forced.stage_seconds
+    e0 = float(np.max(np.abs(_decrypt_stream(client, lay, plain.ciphers) - want)))
+    e1 = float(np.max(np.abs(_decrypt_stream(client, lay, forced.ciphers) - want)))
+    print(f"PV threshold refresh: max err {e0:.3g} without, {e1:.3g} with, "
+          f"{forced.stage_seconds['refresh_pv_output']:.3f} s", flush=True)
+    assert e0 < 1e-3 and e1 < 1e-3, (e0, e1)
+
+
 def _exact_layer_and_ranges(x, wq, wk, wv, wo, G, U, Dn, *, heads, kv_heads, head_dim):
     """The layer with exact RMSNorm, SiLU and softmax, and the ranges its
     nonlinearities saw (the calibration pass)."""
