@@ -2913,9 +2913,11 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // kTabGroups giant groups per pass: baby b of ciphertext i at bab[i B + b]
 // ([2][limbs][N]), plaintext of group g and baby b at pts[g B + b] (limb l at
 // l N), inner sum of group g for ciphertext i to out + (g n + i) 2 limbs N.
-// Each thread walks the babies of kTabCts ciphertexts at a time with the
-// groups' plaintext words in registers: a baby word is read once per pass, a
-// plaintext word (from L2) once per kTabCts ciphertexts.
+// A block takes one component of IC ciphertexts (kTabCtsFp on the fp64
+// kernel, kTabCts on the 64-bit one) for 256 coefficients, each thread the
+// babies of its coefficient with the groups' plaintext words in registers: a
+// baby word is read once per pass, a plaintext word once per block, which
+// the block decode below turns into one HBM read per 256 coefficients.
 // Limbs whose prime is below 2^45 (with B <= 64) take the fp64 kernel: each
 // product is the exact fp64 residue of fp_mulmod (|r| < 1.5 q) and the
 // B-term sums stay exact integers below 2^53, reduced once at the end, so the
@@ -2924,8 +2926,24 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // baby step's IC baby words and GT plaintext words issue together (groups
 // beyond G re-read group G - 1 and are not stored), one step ahead of the
 // products that use them.
-// grid (N / 256, limb_count, 2), limbs from l_begin
+// grid (N / 256 x 2 x input groups, limb_count), limbs from l_begin
 typedef __attribute__((address_space(1))) u64 GlobalU64;
+
+// 1-D block decode of the table MACs: kb, the block of 256 coefficients, and
+// z, the component and input group (nz of them).  The nz blocks of one kb
+// read the same plaintext words; with N / 256 a multiple of 8 they get ids 8
+// apart, so they run on one XCD close in time and the words come from its L2.
+__device__ __forceinline__ void mac_table_block(int nz, int logN, int &kb, int &z) {
+  const int b = blockIdx.x, nkb = (1 << logN) / TPB;
+  if (nkb & 7) {
+    kb = b % nkb;
+    z = b / nkb;
+  } else {
+    const int r = b >> 3;
+    z = r % nz;
+    kb = (r / nz) * 8 + (b & 7);
+  }
+}
 
 template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restrict__ bab, int n,
@@ -2933,58 +2951,56 @@ __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restri
                                                       int G, u64 *__restrict__ out, int limbs,
                                                       int l_begin, int logN,
                                                       const ModQ *__restrict__ mods) {
-  const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = l_begin + blockIdx.y, comp = blockIdx.z;
+  constexpr int IC = kTabCtsFp;
+  int kb, z;
+  mac_table_block(2 * ((n + IC - 1) / IC), logN, kb, z);
+  const int k = kb * TPB + threadIdx.x;
+  const int l = l_begin + blockIdx.y, comp = z & 1, i0 = (z >> 1) * IC;
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
-  {
-    constexpr int IC = kTabCtsFp;
-    const double q = (double)M.q, qinv = 1.0 / q;
-    for (int i0 = 0; i0 < n; i0 += IC) {
-      double acc[GT][IC];
+  const double q = (double)M.q, qinv = 1.0 / q;
+  double acc[GT][IC];
 #pragma unroll
-      for (int g = 0; g < GT; g++)
+  for (int g = 0; g < GT; g++)
 #pragma unroll
-        for (int c = 0; c < IC; c++) acc[g][c] = 0.0;
-      // the tables hold device pointers: global loads, not flat ones
-      u64 xw[IC], ww[GT];
-      auto issue = [&](int b) {
+    for (int c = 0; c < IC; c++) acc[g][c] = 0.0;
+  // the tables hold device pointers: global loads, not flat ones
+  u64 xw[IC], ww[GT];
+  auto issue = [&](int b) {
 #pragma unroll
-        for (int c = 0; c < IC; c++)
-          xw[c] = ((const GlobalU64 *)bab[(size_t)min(i0 + c, n - 1) * B + b])[off];
+    for (int c = 0; c < IC; c++)
+      xw[c] = ((const GlobalU64 *)bab[(size_t)min(i0 + c, n - 1) * B + b])[off];
 #pragma unroll
-        for (int g = 0; g < GT; g++)
-          ww[g] = ((const GlobalU64 *)pts[(size_t)min(g, G - 1) * B + b])[poff];
-      };
-      issue(0);
-      for (int b = 0; b < B; b++) {
-        u64 xc[IC], wc[GT];
+    for (int g = 0; g < GT; g++)
+      ww[g] = ((const GlobalU64 *)pts[(size_t)min(g, G - 1) * B + b])[poff];
+  };
+  issue(0);
+  for (int b = 0; b < B; b++) {
+    u64 xc[IC], wc[GT];
 #pragma unroll
-        for (int c = 0; c < IC; c++) xc[c] = xw[c];
+    for (int c = 0; c < IC; c++) xc[c] = xw[c];
 #pragma unroll
-        for (int g = 0; g < GT; g++) wc[g] = ww[g];
-        if (b + 1 < B) issue(b + 1);  // the next step's words in flight
-        __builtin_amdgcn_sched_barrier(0);
-        double x[IC];
+    for (int g = 0; g < GT; g++) wc[g] = ww[g];
+    if (b + 1 < B) issue(b + 1);  // the next step's words in flight
+    __builtin_amdgcn_sched_barrier(0);
+    double x[IC];
 #pragma unroll
-        for (int c = 0; c < IC; c++) x[c] = u52_to_dbl(xc[c]);
+    for (int c = 0; c < IC; c++) x[c] = u52_to_dbl(xc[c]);
 #pragma unroll
-        for (int g = 0; g < GT; g++) {
-          const double w = u52_to_dbl(wc[g]);
-          const double wq = __dmul_rn(w, qinv);
+    for (int g = 0; g < GT; g++) {
+      const double w = u52_to_dbl(wc[g]);
+      const double wq = __dmul_rn(w, qinv);
 #pragma unroll
-          for (int c = 0; c < IC; c++) acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < GT; g++)
-#pragma unroll
-        for (int c = 0; c < IC; c++)
-          if (g < G && i0 + c < n)
-            out[((size_t)g * n + i0 + c) * CP + off] = fp_canon(acc[g][c], qinv, q);
+      for (int c = 0; c < IC; c++) acc[g][c] = __dadd_rn(acc[g][c], fp_mulmod(x[c], w, wq, q));
     }
   }
+#pragma unroll
+  for (int g = 0; g < GT; g++)
+#pragma unroll
+    for (int c = 0; c < IC; c++)
+      if (g < G && i0 + c < n)
+        out[((size_t)g * n + i0 + c) * CP + off] = fp_canon(acc[g][c], qinv, q);
 }
 
 // The 64-bit kernel: 128-bit sums of 64-bit products, reduced every 16 babies
@@ -2999,8 +3015,10 @@ __global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restri
                                                       int l_begin, int logN,
                                                       const ModQ *__restrict__ mods) {
   constexpr int IC = kTabCts;
-  const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = l_begin + blockIdx.y, comp = blockIdx.z & 1, i0 = (blockIdx.z >> 1) * IC;
+  int kb, z;
+  mac_table_block(2 * ((n + IC - 1) / IC), logN, kb, z);
+  const int k = kb * TPB + threadIdx.x;
+  const int l = l_begin + blockIdx.y, comp = z & 1, i0 = (z >> 1) * IC;
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
@@ -3064,13 +3082,10 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
                          : k_mac_table_64<kTabGroups>;
   auto fp_limb = [&](int l) { return B <= 64 && c->prime_fp[l] != 0; };
   auto launch_run = [&](int l0, int l1, hipStream_t st) {
-    if (fp_limb(l0))
-      hipLaunchKernelGGL(fp_kern, dim3(c->N / TPB, l1 - l0, 2), dim3(TPB), 0, st, bab, n, pts, B,
-                         G, out, limbs, l0, c->logN, c->d_mods);
-    else
-      hipLaunchKernelGGL(w_kern, dim3(c->N / TPB, l1 - l0, 2 * ((n + kTabCts - 1) / kTabCts)),
-                         dim3(TPB), 0, st, bab, n, pts, B, G, out, limbs, l0, c->logN,
-                         c->d_mods);
+    const int ic = fp_limb(l0) ? kTabCtsFp : kTabCts;
+    const dim3 grid(c->N / TPB * 2 * ((n + ic - 1) / ic), l1 - l0);
+    hipLaunchKernelGGL(fp_limb(l0) ? fp_kern : w_kern, grid, dim3(TPB), 0, st, bab, n, pts, B, G,
+                       out, limbs, l0, c->logN, c->d_mods);
     LAUNCH_CHECK();
   };
   // runs of limbs of one kind; with both kinds and a second stream, the
