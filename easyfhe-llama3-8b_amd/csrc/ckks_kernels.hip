@@ -2784,24 +2784,43 @@ void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u
   LAUNCH_CHECK();
 }
 
+// 1-D block decode of the table and extended MACs: kb, the block of 256 coefficients, and
+// z, the component and input group (nz of them).  The nz blocks of one kb
+// read the same plaintext words; with N / 256 a multiple of 8 they get ids 8
+// apart, so they run on one XCD close in time and the words come from its L2.
+__device__ __forceinline__ void mac_table_block(int nz, int logN, int &kb, int &z) {
+  const int b = blockIdx.x, nkb = (1 << logN) / TPB;
+  if (nkb & 7) {
+    kb = b % nkb;
+    z = b / nkb;
+  } else {
+    const int r = b >> 3;
+    z = r % nz;
+    kb = (r / nz) * 8 + (b & 7);
+  }
+}
+
 // Extended-basis MAC of n ciphertexts sharing the plaintexts, for G giant
 // groups at once: babies at bab[(b n + i)][2][E][N], plaintext of group g and
-// baby b at pts[g B + b], out[(g n + i)][2][E][N].  Each thread walks the
-// babies for kMacCts ciphertexts at a time with the plaintext words of every
-// group in registers: every baby word is read from HBM once for all groups,
-// and a plaintext word is re-read (from L2) once per kMacCts ciphertexts.
-// Limbs whose prime is below 2^45 (with B <= 64) take the fp64 path of
-// k_mac_table (exact residues, sums below 2^53, one reduction; the same
-// words), kMacCtsFp ciphertexts per plaintext read, with GT >= G groups
-// compiled and a baby step's loads issued one step ahead of its products.
-// grid (N / 256, E, 2)
+// baby b at pts[g B + b], out[(g n + i)][2][E][N].  A block takes one
+// component of kMacCtsFp ciphertexts for 256 coefficients (mac_table_block:
+// the blocks sharing a plaintext tile run on one XCD back to back); each
+// thread walks the babies with the plaintext words of every group in
+// registers: every baby word is read from HBM once for all groups.  Limbs
+// whose prime is below 2^45 (with B <= 64) take the fp64 path of k_mac_table
+// (exact residues, sums below 2^53, one reduction; the same words) over the
+// block's ciphertexts at once, the 64-bit path kMacCts at a time; GT >= G
+// groups compiled and a baby step's loads issued one step ahead of its
+// products.  grid (N / 256 x 2 x input groups, E)
 template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, int n, Batch pts,
                                                   int B, int G, u64 *__restrict__ out, int E,
                                                   int q_limbs, int L, int logN,
                                                   const ModQ *__restrict__ mods) {
-  const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = blockIdx.y, comp = blockIdx.z;
+  int kb, z;
+  mac_table_block(2 * ((n + kMacCtsFp - 1) / kMacCtsFp), logN, kb, z);
+  const int k = kb * TPB + threadIdx.x;
+  const int l = blockIdx.y, comp = z & 1, ib = (z >> 1) * kMacCtsFp;
   const size_t N = (size_t)1 << logN, EP = 2 * (size_t)E * N;
   const ModQ M = mods[prime_of(l, q_limbs, L)];
   const size_t off = ((size_t)comp * E + l) * N + k;
@@ -2809,7 +2828,7 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
     constexpr int IC = kMacCtsFp;
     const double q = (double)M.q, qinv = 1.0 / q;
     const size_t poff = (size_t)l * N + k;
-    for (int i0 = 0; i0 < n; i0 += IC) {
+    for (int i0 = ib; i0 < ib + IC; i0 += IC) {
       double acc[GT][IC];
 #pragma unroll
       for (int g = 0; g < GT; g++)
@@ -2851,7 +2870,8 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
     }
     return;
   }
-  for (int i0 = 0; i0 < n; i0 += kMacCts) {
+  static_assert(kMacCtsFp % kMacCts == 0, "a block's inputs split into 64-bit passes");
+  for (int i0 = ib; i0 < ib + kMacCtsFp && i0 < n; i0 += kMacCts) {
     constexpr int IC = kMacCts;
     u64 acc[GT][IC], hi[GT][IC], lo[GT][IC];
 #pragma unroll
@@ -2903,7 +2923,7 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
             2.0 * c->N * E * (double)n * B * G);
   if (G < 1 || G > kMacGroups || G * B > kMaxBatch)
     throw std::invalid_argument("mac_many: 1 <= groups <= 2 and groups x babies <= 64");
-  dim3 grid(c->N / TPB, E, 2);
+  dim3 grid(c->N / TPB * 2 * ((n + kMacCtsFp - 1) / kMacCtsFp), E);
   hipLaunchKernelGGL(G <= 1 ? k_mac_many<1> : k_mac_many<kMacGroups>, grid, dim3(TPB), 0,
                      c->stream, bab, n, pts, B, G, out, E, q_limbs, c->L, c->logN, c->d_mods);
   LAUNCH_CHECK();
@@ -2928,22 +2948,6 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // products that use them.
 // grid (N / 256 x 2 x input groups, limb_count), limbs from l_begin
 typedef __attribute__((address_space(1))) u64 GlobalU64;
-
-// 1-D block decode of the table MACs: kb, the block of 256 coefficients, and
-// z, the component and input group (nz of them).  The nz blocks of one kb
-// read the same plaintext words; with N / 256 a multiple of 8 they get ids 8
-// apart, so they run on one XCD close in time and the words come from its L2.
-__device__ __forceinline__ void mac_table_block(int nz, int logN, int &kb, int &z) {
-  const int b = blockIdx.x, nkb = (1 << logN) / TPB;
-  if (nkb & 7) {
-    kb = b % nkb;
-    z = b / nkb;
-  } else {
-    const int r = b >> 3;
-    z = r % nz;
-    kb = (r / nz) * 8 + (b & 7);
-  }
-}
 
 template <int GT>
 __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restrict__ bab, int n,
