@@ -3593,26 +3593,26 @@ __device__ u64 dbl_residue(double v, const ModQ &M) {
 }
 
 // Encoder tail: u = (x_k / n) * twist_k, coefficient k gap and (k + n) gap
-// get rint(scale u.re), rint(scale u.im); then residues for every limb.
-// grid (N / 256, total_limbs, rows)
+// get rint(scale u.re), rint(scale u.im); then residues for every limb, the
+// rounded value formed once per coefficient.  grid (N / 256, rows)
 __global__ void k_encode_finish(const cplx *__restrict__ x, const cplx *__restrict__ twist,
-                                Batch out, int n, int logN, double scale, int q_limbs, int L,
-                                const ModQ *__restrict__ mods) {
+                                Batch out, int n, int logN, double scale, int total, int q_limbs,
+                                int L, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;  // coefficient index
-  const int l = blockIdx.y;
   const int N = 1 << logN, gap = N / (2 * n);
-  const ModQ M = mods[prime_of(l, q_limbs, L)];
   double v = 0.0;
   if (k % gap == 0) {
     const int idx = k / gap;
     const int kk = idx < n ? idx : idx - n;
-    const cplx w = x[(size_t)blockIdx.z * n + kk];
+    const cplx w = x[(size_t)blockIdx.y * n + kk];
     const double inv_n = 1.0 / (double)n;
     cplx u = cplx{__dmul_rn(w.re, inv_n), __dmul_rn(w.im, inv_n)};
     u = cmul(u, twist[kk]);
     v = rint(__dmul_rn(scale, idx < n ? u.re : u.im));
   }
-  batch_ptr(out, blockIdx.z)[((size_t)l << logN) + k] = dbl_residue(v, M);
+  u64 *o = batch_ptr(out, blockIdx.y) + k;
+  for (int l = 0; l < total; l++)
+    o[(size_t)l << logN] = dbl_residue(v, mods[prime_of(l, q_limbs, L)]);
 }
 
 // Encoder tail over rows already placed in x ([rows][n], slot j at
@@ -3623,8 +3623,9 @@ static void encode_placed(ckks_context *c, cplx *x, int rows, int slots, double 
   const int n = slots;
   launch_fft(c, x, rows, n, (const cplx *)t.tw_inv);
   const int total = limbs + (is_ext ? c->alpha : 0);
-  hipLaunchKernelGGL(k_encode_finish, dim3(c->N / TPB, total, rows), dim3(TPB), 0, c->stream,
-                     x, (const cplx *)t.twist, out, n, c->logN, scale, limbs, c->L, c->d_mods);
+  hipLaunchKernelGGL(k_encode_finish, dim3(c->N / TPB, rows), dim3(TPB), 0, c->stream, x,
+                     (const cplx *)t.twist, out, n, c->logN, scale, total, limbs, c->L,
+                     c->d_mods);
   LAUNCH_CHECK();
   launch_ntt(c, out, out, rows, 0, total, limbs, false);
 }
