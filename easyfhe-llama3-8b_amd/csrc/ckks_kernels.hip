@@ -1787,24 +1787,31 @@ constexpr int kMfmaChunks = 4;  // chunks of 4 waves x R tiles per block
 // target): the ModQ of the target's prime (0..4), 1/q (5), the output limb
 // (6), 2^32/q (7), q as a double (8); with RS also [P]_t, [P]_t / q_t
 // (10, 11: the fp64 form), Montgomery [P]_t (12) and [P p]_t (13).
-constexpr int kBcTgtWords = 10, kBcTgtWordsRS = 14;
+constexpr int kBcTgtWords = 10;
+// with RSD dropped primes: per dropped prime j, ([P p_1..p_(j-1)]_t, its
+// fp64 quotient), Montgomery [P p_1..p_(j-1)]_t and [P p_1..p_j]_t
+__host__ __device__ constexpr int bc_tgt_words(int rsd) { return kBcTgtWords + 4 * rsd; }
 
-// RS: the relinearise-rescale ModDown by P p (one dropped prime p = the
-// last target, td = nd - 1; k_bc_down_rescale states the algebra): the
-// dropped target's group runs first, its value y_td gives the centred lift
-// r = [(x_td - y_td) P^-1]_p, where x_td is source slot ns (the dropped limb
-// of X as coefficients), broadcast from the lanes that hold it; every other
-// target t < td is written as y_t + r [P]_t - (r > p / 2 ? [P p]_t : 0).
-// rs: the rescale table of one dropped prime, the conversion part of the
-// relinearise-rescale constants ([td] Montgomery [P]_t, [td] [P p]_t, then
-// P^-1 mod p and its Shoup constant); rsf: ([P]_t, [P]_t / q_t) for the
-// fp64 targets.
-template <int R, int NK, int CH, bool RS = false>
+// RSD > 0: the relinearise-rescale ModDown by P p_1 .. p_RSD (the dropped
+// primes are the last targets, p_(j+1) at target td_j = nd - 1 - j, all in
+// one target group; k_bc_down_rescale states the algebra): the dropped
+// targets' group runs first; p_1's value y gives the centred lift r_0 =
+// [(x - y) P^-1]_(p_1), where x is the dropped limb of X as coefficients
+// (source slot ns + RSD - 1 - j for p_(j+1)), broadcast from the lanes that
+// hold it; p_2's lift r_1 follows from its own value and r_0 (the rescale
+// chain of k_rescale_lift); every target t < T = nd - RSD is written as
+// y_t + sum_j r_j [P p_1..p_j]_t - (r_j > p_(j+1) / 2 ? [P p_1..p_(j+1)]_t : 0).
+// rs: the relinearise-rescale table of k_bc_down_rescale ([T][RSD]
+// Montgomery [P p_1..p_j]_t, [T][RSD] [P p_1..p_(j+1)]_t, [RSD][2] P^-1 mod
+// p_(j+1) + Shoup, [RSD][RSD][3] chain constants); rsf: its fp64 part.
+template <int R, int NK, int CH, int RSD = 0>
 __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
     Batch src, Batch dst, int logN, int ns, int nd, const u64 *__restrict__ tab,
     const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
     int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods,
     const u64 *__restrict__ rs = nullptr, const double2 *__restrict__ rsf = nullptr) {
+  constexpr bool RS = RSD > 0;
+  constexpr int RJ = RS ? RSD : 1;
   // the block's table, staged once: [NK][n_tg][8][64] words
   extern __shared__ u64 tb[];
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
@@ -1823,7 +1830,7 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
   }
   // raw residues of the chunk being loaded (coefficient k + 16 r + col)
   u64 x[R][NK];
-  u64 xd[R];  // RS: the dropped limb of X at the same coefficients
+  u64 xd[RJ][R];  // RS: the dropped limbs of X at the same coefficients
   auto load = [&](int ch) {
     const int k0 = kblk + ch * 64 * R + wave * 16 * R;
 #pragma unroll
@@ -1833,15 +1840,18 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
         x[r][i] = 4 * i + g < ns ? in[((size_t)(4 * i + g) << logN) + k0 + 16 * r + col] : 0;
     if constexpr (RS) {
 #pragma unroll
-      for (int r = 0; r < R; r++) xd[r] = in[((size_t)ns << logN) + k0 + 16 * r + col];
+      for (int j = 0; j < RSD; j++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          xd[j][r] = in[((size_t)(ns + RSD - 1 - j) << logN) + k0 + 16 * r + col];
     }
   };
-  // RS: the dropped target, its group, lane group and accumulator slot
-  const int td = nd - 1, tg_d = td >> 4, g_d = (td & 15) >> 2, e_d = td & 3;
+  // RS: the remaining targets, the dropped targets' group
+  const int T = nd - (RS ? RSD : 0), tg_d = (nd - 1) >> 4;
   load(0);
   const int words = NK * n_tg * 512;
   for (int idx = threadIdx.x; idx < words; idx += TPB) tb[idx] = mtab[idx];
-  constexpr int TW = RS ? kBcTgtWordsRS : kBcTgtWords;
+  constexpr int TW = bc_tgt_words(RS ? RSD : 0);
   u64 *tgt = tb + words;
   for (int t = threadIdx.x; t < nd; t += TPB) {
     const int tl = t < t_split ? t : t + t_skip;
@@ -1858,20 +1868,22 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
     w[7] = dbl_bits(4294967296.0 * qinv);
     w[8] = dbl_bits(q);
     if constexpr (RS) {
-      if (t < td) {
-        w[10] = dbl_bits(rsf[t].x);
-        w[11] = dbl_bits(rsf[t].y);
-        w[12] = rs[t];
-        w[13] = rs[(size_t)td + t];
+      if (t < T) {
+#pragma unroll
+        for (int j = 0; j < RSD; j++) {
+          const size_t tj = (size_t)t * RSD + j;
+          w[10 + 4 * j] = dbl_bits(rsf[tj].x);
+          w[11 + 4 * j] = dbl_bits(rsf[tj].y);
+          w[12 + 4 * j] = rs[tj];
+          w[13 + 4 * j] = rs[(size_t)T * RSD + tj];
+        }
       }
     }
   }
-  // RS: the dropped target's lift constants (uniform)
-  u64 pinv_d = 0, pinvs_d = 0;
-  if constexpr (RS) {
-    pinv_d = rs[2 * (size_t)td];
-    pinvs_d = rs[2 * (size_t)td + 1];
-  }
+  // RS: the dropped primes' lift constants (uniform): P^-1 mod p_(j+1) and
+  // its Shoup constant, then the chain's [p_2] mod p_1... (k_bc_down_rescale)
+  const u64 *rpinv = RS ? rs + 2 * (size_t)T * RSD : nullptr;
+  const u64 *rchain = RS ? rpinv + 2 * RSD : nullptr;
   __syncthreads();
   const int quad = n_tg * 512;
   for (int ch = 0; ch < CH; ch++) {
@@ -1886,14 +1898,16 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
         if (centered && v > (sq[i] - 1) / 2) v -= sq[i];  // two's complement of v - q
         a[r][i] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
       }
-    u64 xdc[R];  // RS: this chunk's dropped-limb words
+    u64 xdc[RJ][R];  // RS: this chunk's dropped-limb words
     if constexpr (RS) {
 #pragma unroll
-      for (int r = 0; r < R; r++) xdc[r] = xd[r];
+      for (int j = 0; j < RSD; j++)
+#pragma unroll
+        for (int r = 0; r < R; r++) xdc[j][r] = xd[j][r];
     }
     if (ch + 1 < CH) load(ch + 1);  // in flight during this chunk
-    u64 rv[R];
-    bool rneg[R];
+    u64 rv[RJ][R];
+    bool rneg[RJ][R];
     for (int tt = 0; tt < n_tg; tt++) {
       // RS: the dropped target's group first
       const int tg = RS ? (tt == 0 ? tg_d : (tt <= tg_d ? tt - 1 : tt)) : tt;
@@ -1935,49 +1949,67 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
       }
       if constexpr (RS) {
         if (tt == 0) {
-          // the dropped target's value in its lanes, the lift r from it,
-          // then r to every lane of the same coefficient column
-          const u64 *wd = tgt + (size_t)td * TW;
-          const u64 qd = wd[0];
-          const double q = as_dbl(wd[8]), qinv = as_dbl(wd[5]), w32q = as_dbl(wd[7]);
-          const u64 pinv = pinv_d, pinvs = pinvs_d;
+          // each dropped target's value in its lanes, the lift from it (and
+          // the earlier lifts), then the lift to every lane of the same
+          // coefficient column
 #pragma unroll
-          for (int r = 0; r < R; r++) {
-            const double tq = fp_rint(__dmul_rn(hi[r][e_d], w32q));
-            const double y =
-                __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e_d], 4294967296.0)), lo[r][e_d]);
-            const u64 u = shoup_mul(sub_mod(xdc[r], fp_canon(y, qinv, q), qd), pinv, pinvs, qd);
-            const u64 ub = (u64)__shfl((long long)u, 16 * g_d + col);
-            rv[r] = ub;
-            rneg[r] = ub > (qd - 1) / 2;
+          for (int j = 0; j < RSD; j++) {
+            const int td = nd - 1 - j, g_d = (td & 15) >> 2, e_d = td & 3;
+            const u64 *wd = tgt + (size_t)td * TW;
+            ModQ Mj;
+            Mj.q = wd[0];
+            Mj.qinv = wd[1];
+            Mj.r2 = wd[2];
+            Mj.mu = wd[3];
+            Mj.k = (u32)wd[4];
+            Mj.pad = (u32)(wd[4] >> 32);
+            const u64 qd = Mj.q;
+            const double q = as_dbl(wd[8]), qinv = as_dbl(wd[5]), w32q = as_dbl(wd[7]);
+            const u64 pinv = rpinv[2 * j], pinvs = rpinv[2 * j + 1];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+              const double tq = fp_rint(__dmul_rn(hi[r][e_d], w32q));
+              const double y =
+                  __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e_d], 4294967296.0)), lo[r][e_d]);
+              u64 u = shoup_mul(sub_mod(xdc[j][r], fp_canon(y, qinv, q), qd), pinv, pinvs, qd);
+#pragma unroll
+              for (int m = 0; m < j; m++) {
+                const u64 *cm = rchain + 3 * ((size_t)j * RSD + m);
+                u64 rm = barrett(0, rv[m][r], Mj);
+                if (rneg[m][r]) rm = sub_mod(rm, cm[0], qd);
+                u = shoup_mul(sub_mod(u, rm, qd), cm[1], cm[2], qd);
+              }
+              const u64 ub = (u64)__shfl((long long)u, 16 * g_d + col);
+              rv[j][r] = ub;
+              rneg[j][r] = ub > (qd - 1) / 2;
+            }
           }
         }
       }
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int t = 16 * tg + 4 * g + e;
-        if (t >= (RS ? td : nd)) continue;
+        if (t >= T) continue;
         const u64 *w = tgt + (size_t)t * TW;
         u64 *o = out + ((size_t)w[6] << logN) + k0 + col;
         if (w[0] < kFpPrimeBound) {
           // y = hi 2^32 + lo: hi 2^32 is an exact double, the quotient by
           // round(hi 2^32 / q) leaves an exact residue, one reduction after
           const double q = as_dbl(w[8]), qinv = as_dbl(w[5]), w32q = as_dbl(w[7]);
-          double2 pf{0.0, 0.0};
-          double ppd = 0.0;
-          if constexpr (RS) {
-            pf = double2{as_dbl(w[10]), as_dbl(w[11])};
-            ppd = u52_to_dbl(w[13]);
-          }
 #pragma unroll
           for (int r = 0; r < R; r++) {
             const double tq = fp_rint(__dmul_rn(hi[r][e], w32q));
             double y =
                 __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[r][e], 4294967296.0)), lo[r][e]);
             if constexpr (RS) {
-              // |y| < 2q; the lift's product and [P p]_t keep it below 2^50
-              y = __dadd_rn(y, fp_mulmod(u52_to_dbl(rv[r]), pf.x, pf.y, q));
-              if (rneg[r]) y = __dsub_rn(y, ppd);
+              // |y| < 2q; each lift's product (< 1.5 q) and [P p..]_t (< q)
+              // keep it below 2^50
+#pragma unroll
+              for (int j = 0; j < RSD; j++) {
+                y = __dadd_rn(y, fp_mulmod(u52_to_dbl(rv[j][r]), as_dbl(w[10 + 4 * j]),
+                                           as_dbl(w[11 + 4 * j]), q));
+                if (rneg[j][r]) y = __dsub_rn(y, u52_to_dbl(w[13 + 4 * j]));
+              }
             }
             o[16 * r] = fp_canon(y, qinv, q);
           }
@@ -1997,9 +2029,13 @@ __global__ __launch_bounds__(TPB) void k_basis_convert_mfma(
             const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
             u64 y = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
             if constexpr (RS) {
-              const u64 pmM = w[12];  // Montgomery form: the REDC of the product is r [P]_t
-              y = add_mod(y, redc(__umul64hi(rv[r], pmM), rv[r] * pmM, M.q, M.qinv), M.q);
-              if (rneg[r]) y = sub_mod(y, w[13], M.q);
+#pragma unroll
+              for (int j = 0; j < RSD; j++) {
+                // Montgomery form: the REDC of the product is r_j [P p..]_t
+                const u64 pmM = w[12 + 4 * j], rj = rv[j][r];
+                y = add_mod(y, redc(__umul64hi(rj, pmM), rj * pmM, M.q, M.qinv), M.q);
+                if (rneg[j][r]) y = sub_mod(y, w[13 + 4 * j], M.q);
+              }
             }
             o[16 * r] = y;
           }
@@ -2286,21 +2322,31 @@ void launch_bc_down_rescale(ckks_context *c, const Batch &src, const Batch &dst,
             (double)c->N * n_items * t.ns * t.nd);
   if (D < 1 || D > kMaxRescaleDrop || t.nd <= D || t.ns > kMaxDigitSize)
     throw std::invalid_argument("relinearise-rescale conversion: 1 <= primes < limbs");
-  // one dropped prime below 2^45: the int8 matrix-core conversion with the
-  // lift in its epilogue (the same words as the VALU kernels)
-  const int T1 = t.nd - 1;
-  if (D == 1 && c->bc_mfma && t.mf && c->primes[T1] < kFpPrimeBound &&
-      (size_t)t.n_k * t.n_tg * 512 * sizeof(u64) <= 65536) {
-    const double2 *rsf = (const double2 *)(rtab + 2 * (size_t)T1 + 2 + 3);
-    auto kern = t.n_k == 1   ? k_basis_convert_mfma<kMfmaRows, 1, kMfmaChunks, true>
-                : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks, true>
-                : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks, true>
-                             : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks, true>;
+  // one or two dropped primes below 2^45, in one target group: the int8
+  // matrix-core conversion with the lifts in its epilogue (the same words as
+  // the VALU kernels)
+  bool mfma = D <= 2 && c->bc_mfma && t.mf &&
+              (size_t)t.n_k * t.n_tg * 512 * sizeof(u64) <= 65536 &&
+              ((t.nd - 1) >> 4) == ((t.nd - D) >> 4);
+  for (int j = 0; j < D && mfma; j++) mfma = c->primes[t.nd - 1 - j] < kFpPrimeBound;
+  if (mfma) {
+    const int T = t.nd - D;
+    const double2 *rsf =
+        (const double2 *)(rtab + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D);
+    auto pick1 = t.n_k == 1   ? k_basis_convert_mfma<kMfmaRows, 1, kMfmaChunks, 1>
+                 : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks, 1>
+                 : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks, 1>
+                              : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks, 1>;
+    auto pick2 = t.n_k == 1   ? k_basis_convert_mfma<kMfmaRows, 1, kMfmaChunks, 2>
+                 : t.n_k == 2 ? k_basis_convert_mfma<kMfmaRows, 2, kMfmaChunks, 2>
+                 : t.n_k == 3 ? k_basis_convert_mfma<kMfmaRows, 3, kMfmaChunks, 2>
+                              : k_basis_convert_mfma<kMfmaRows, 4, kMfmaChunks, 2>;
     const size_t lds =
-        sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWordsRS);
-    hipLaunchKernelGGL(kern, dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB),
-                       lds, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, t.mf, t.n_tg,
-                       t.wide_mask, c->L, t.nd, 0, t.nd, c->L, 1, c->d_mods, rtab, rsf);
+        sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * bc_tgt_words(D));
+    hipLaunchKernelGGL(D == 1 ? pick1 : pick2,
+                       dim3(c->N / (64 * kMfmaRows * kMfmaChunks), n_items), dim3(TPB), lds,
+                       c->stream, src, dst, c->logN, t.ns, t.nd, t.d, t.mf,
+                       t.n_tg, t.wide_mask, c->L, t.nd, 0, t.nd, c->L, 1, c->d_mods, rtab, rsf);
     LAUNCH_CHECK();
     return;
   }

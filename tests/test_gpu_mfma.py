@@ -98,3 +98,32 @@ def test_mfma_keyswitch_full_size(fused, monkeypatch):
         assert np.array_equal(h.download(), w)
     assert np.abs(client.decrypt(rots[0]) - np.roll(zs[0], -rot)).max() < 1e-6
     ctx.close()
+
+
+@pytest.mark.slow
+def test_mfma_relin_rescale_two_primes_full_size():
+    """Relinearise + two rescales as one ModDown at N = 2^16 on the key-switch
+    chain: at 36 limbs the two dropped primes' targets share a target group
+    (the int8-MFMA conversion with both lifts in its epilogue), at 33 limbs
+    they do not (the fp64 VALU kernel); limbs equal to the oracle's
+    relinearise then two rescales."""
+    from easyfhe import fhe
+
+    client, ctx = device_context("keyswitch")
+    orc = oracle_context("keyswitch")
+    orc.gen_relin_key()
+    slots = ctx.max_slots
+    rng = np.random.default_rng(5)
+    zs = [rng.uniform(-1, 1, slots) for _ in range(2)]
+    for limbs in (36, 33):
+        # two rescales by ~2^40 primes: inputs at 2^60 leave the product near 2^40
+        sc = 2.0**60
+        cts = [client.encrypt(z, cur_limbs=limbs, scaling_factor=sc, enc_id=720 + i)
+               for i, z in enumerate(zs)]
+        refs = [orc.encrypt(z, slots=slots, scale=sc, limbs=limbs, enc_id=720 + i)
+                for i, z in enumerate(zs)]
+        prod = fhe.homo_mul_relin_rescale_many(cts[:1], cts[1:], ctx, primes=2)[0]
+        want = orc.rescale(orc.rescale(orc.relinearize(orc.tensor(refs[0], refs[1]))))
+        assert np.array_equal(prod.download(), want), limbs
+        assert np.abs(client.decrypt(prod) - zs[0] * zs[1]).max() < 1e-4, limbs
+    ctx.close()
