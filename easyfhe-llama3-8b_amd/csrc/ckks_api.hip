@@ -1559,7 +1559,8 @@ int ckks_has_rotation_key(const ckks_context *c, int64_t rotation) {
 }
 
 // key words in NTT position order and out of Montgomery form: word k of each
-// row from autom_index(k, g) of the stored key (g = 1: in place)
+// row from position autom_index(k, g) of the stored key (g = 1: in place),
+// stored at key_slot of it
 __global__ void k_key_export(const u64 *__restrict__ key, u64 *__restrict__ out, size_t words,
                              int K, int logN, u64 g, const ModQ *__restrict__ mods) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -1568,7 +1569,7 @@ __global__ void k_key_export(const u64 *__restrict__ key, u64 *__restrict__ out,
   const u32 k = (u32)(i & (((size_t)1 << logN) - 1));
   const u32 s = g <= 1 ? k : autom_index(k, g, logN);
   const ModQ M = mods[(int)(row % K)];
-  out[i] = redc(0, key[(row << logN) + s], M.q, M.qinv);
+  out[i] = redc(0, key[(row << logN) + key_slot(s)], M.q, M.qinv);
 }
 
 int ckks_key_download(ckks_context *c, uint64_t galois, uint64_t *out, int *digits) {

@@ -138,6 +138,15 @@ __device__ __forceinline__ u32 autom_index(u32 i, u64 g, int logN) {
   return __brev((u32)((e - 1) >> 1)) >> (32 - logN);
 }
 
+// Storage slot of key position s (N >= 1024): within each group of 1024
+// positions, bits 1-3 and 4-9 of s trade places (bit 0 stays), so that the
+// 16 consecutive positions a thread of the fused low pass + key product reads
+// (positions 16 c0 .. 16 c0 + 15 of row r, lane (r mod 4) 16 + c0) become 8
+// pairs 128 words apart, and each pair's load is contiguous across the wave.
+__host__ __device__ __forceinline__ u32 key_slot(u32 s) {
+  return (s & ~1023u) | (s & 1u) | (((s >> 4) & 63u) << 1) | (((s >> 1) & 7u) << 7);
+}
+
 __device__ __forceinline__ int prime_of(int limb, int q_limbs, int L) {
   return limb < q_limbs ? limb : L + (limb - q_limbs);
 }
@@ -173,7 +182,8 @@ struct DeviceKey {
   u64 galois;
   int digits;
   // [digits][2][K][N], Montgomery form; a rotation key by g holds the word
-  // of NTT position k at autom_index(k, g) (source order)
+  // of NTT position k at position autom_index(k, g) (source order), and the
+  // word of position s sits at slot key_slot(s) of its row
   u64 *data;
   size_t bytes;
 };

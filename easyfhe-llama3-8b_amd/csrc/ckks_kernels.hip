@@ -1170,6 +1170,9 @@ struct LowKeyArgs {
   const double2 *itw;
 };
 
+// Offset of position sb + i's key word from key_slot(sb) (sb 16-aligned)
+__device__ __forceinline__ constexpr int kword(int i) { return ((i >> 1) << 7) | (i & 1); }
+
 // 16 consecutive words from a 128-byte aligned address, as 8 loads of 16 bytes
 __device__ __forceinline__ void load16(const u64 *__restrict__ p, u64 (&v)[16]) {
   const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(p);
@@ -1229,6 +1232,7 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = tile * 16 + rl;
   const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  const u32 kslot = key_slot(sb);
   const int jo = l < a.q_limbs ? l / a.ds : -1;
   double acc0[16], acc1[16];
   for (int j = 0; j < a.digits; j++) {
@@ -1252,15 +1256,16 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
       for (int i = 0; i < 16; i++) y[i] = sm[lds16(rl, 16 * c0 + i)];
       fp_low_round_b(y, T, row, c0, q);
     }
-    // |y| <= 17 q < 2^50: the products need no reduction first
-    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + sb;
+    // |y| <= 17 q < 2^50: the products need no reduction first.  The key
+    // words of positions sb + i sit at key_slot(sb + i) = kslot + kword(i)
+    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + kslot;
     const u64 *ka = kb + (size_t)a.K * 65536;
 #pragma unroll
     for (int i0 = 0; i0 < 16; i0 += 4) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = i0; i < i0 + 4; i++) {
-        const double wb = u52_to_dbl(kb[i]), wa = u52_to_dbl(ka[i]);
+        const double wb = u52_to_dbl(kb[kword(i)]), wa = u52_to_dbl(ka[kword(i)]);
         const double pb = fp_mulmod(y[i], wb, __dmul_rn(wb, qinv), q);
         const double pa = fp_mulmod(y[i], wa, __dmul_rn(wa, qinv), q);
         acc0[i] = j == 0 ? pb : __dadd_rn(acc0[i], pb);
@@ -1303,6 +1308,7 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = tile * 16 + rl;
   const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  const u32 kslot = key_slot(sb);
   const int jo = l < a.q_limbs ? l / a.ds : -1;
   u64 acc0[16], acc1[16];
   for (int j = 0; j < a.digits; j++) {
@@ -1328,11 +1334,11 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
         y[i] = v >= q ? v - q : v;
       }
     }
-    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + sb;
+    const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + kslot;
     const u64 *ka = kb + (size_t)a.K * 65536;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const u64 b = kb[i], c = ka[i];
+      const u64 b = kb[kword(i)], c = ka[kword(i)];
       const u64 pb = redc(__umul64hi(y[i], b), y[i] * b, q, M.qinv);
       const u64 pa = redc(__umul64hi(y[i], c), y[i] * c, q, M.qinv);
       acc0[i] = j == 0 ? pb : add_mod(acc0[i], pb, q);
@@ -2434,8 +2440,8 @@ __global__ __launch_bounds__(TPB) void k_key_inner(Batch ext, Batch acc, int n_i
 #pragma unroll
   for (int j = 0; j < MD; j++) {
     if (j < digits) {
-      kb[j] = key[((size_t)(2 * j) * K + p) * N + kk];
-      ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + kk];
+      kb[j] = key[((size_t)(2 * j) * K + p) * N + key_slot(kk)];
+      ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + key_slot(kk)];
     }
   }
   // the digit holding limb l (its own limb: read from the source if given)
@@ -2540,8 +2546,8 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
 #pragma unroll
       for (int j = 0; j < MD; j++) {
         if (j < digits) {
-          kb[j] = u52_to_dbl(key[((size_t)(2 * j) * K + p) * N + s]);
-          ka[j] = u52_to_dbl(key[((size_t)(2 * j + 1) * K + p) * N + s]);
+          kb[j] = u52_to_dbl(key[((size_t)(2 * j) * K + p) * N + key_slot(s)]);
+          ka[j] = u52_to_dbl(key[((size_t)(2 * j + 1) * K + p) * N + key_slot(s)]);
           kbq[j] = __dmul_rn(kb[j], qinv);
           kaq[j] = __dmul_rn(ka[j], qinv);
         }
@@ -2576,8 +2582,8 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
 #pragma unroll
     for (int j = 0; j < MD; j++) {
       if (j < digits) {
-        kb[j] = key[((size_t)(2 * j) * K + p) * N + s];
-        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + s];
+        kb[j] = key[((size_t)(2 * j) * K + p) * N + key_slot(s)];
+        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + key_slot(s)];
       }
     }
 #pragma unroll
@@ -3432,7 +3438,7 @@ __global__ void k_keygen_digit(u64 seed, u32 id, int j, const u64 *__restrict__ 
     // rotation keys in source order: the word of position k at
     // autom_index(k, g), so that a key switch reads it where it reads the
     // extended digit it multiplies
-    const u32 so = relin ? k : autom_index(k, galois, logN);
+    const u32 so = key_slot(relin ? k : autom_index(k, galois, logN));
     out_b[p * N + so] = to_mont(b, M);
     out_a[p * N + so] = to_mont(a, M);
   }
