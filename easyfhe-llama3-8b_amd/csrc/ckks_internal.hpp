@@ -293,7 +293,7 @@ struct ckks_context {
   // kernel of another; environment CKKS_SPLIT_STREAMS=<parts> at creation
   // (1 keeps one stream)
   static constexpr int kMaxSplit = 4;
-  int split_parts = 2;
+  int split_parts = 3;
   hipStream_t aux[kMaxSplit - 1] = {};
   hipEvent_t fork_ev = nullptr, join_ev[kMaxSplit - 1] = {};
 };
