@@ -1163,7 +1163,7 @@ static void gen_key(ckks_context *c, u64 id, int relin, u64 galois) {
 // back before the function returns; every part's intermediates stay
 // allocated until then, so that no block of one part is handed to another
 // while still in use.  Parts keep at least kSplitMin items.
-constexpr int kSplitMin = 16;
+constexpr int kSplitMin = 8;
 
 struct StreamSwap {
   ckks_context *c;
