@@ -496,6 +496,7 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
         "ciphertexts": len(cts),
         "slots": 1 << ls,
         "subsum_rotations": len(prog.subsum),
+        "evalmods_per_ciphertext": 1 if prog.packed else 2,
         "group": group,
         "budget": list(budget),
         "linear_levels": prog.evalmod.strategy,

@@ -82,6 +82,9 @@ class BootstrapParams:
     # precision; more giants are slower); "normal" ModDowns every baby
     strategy: str = "ext_double_hoist"
     giants: int = 2
+    # sparse programs (n <= N/4 slots): real and imaginary parts share one
+    # 2n-periodic vector, so EvalMod runs once per ciphertext, not twice
+    packed_evalmod: bool = True
 
 
 
@@ -134,16 +137,20 @@ def _plans(spec: BootstrapSpec, params: "BootstrapParams | None" = None, log_n: 
             plan_levels(ls, b1, inverse=False, giants=giants))
 
 
-def _baby_offsets(plan: LevelPlan, n: int) -> list[int]:
-    return [(b * plan.stride - plan.center) % n for b in range(plan.baby)]
+def _baby_offsets(plan: LevelPlan, n: int, shift: int = 0) -> list[int]:
+    """Baby rotations of a level whose slot vectors repeat with period n;
+    with ``shift`` the list is followed by the same rotations plus shift."""
+    offs = [(b * plan.stride - plan.center) % n for b in range(plan.baby)]
+    return offs + [(o + shift) % n for o in offs] if shift else offs
 
 
 def _giant_offset(plan: LevelPlan, n: int) -> int:
     return (plan.baby * plan.stride) % n
 
 
-def _level_rotations(plan: LevelPlan, n: int, strategy: str = "ext_normal") -> set[int]:
-    rots = {o for o in _baby_offsets(plan, n) if o}
+def _level_rotations(plan: LevelPlan, n: int, strategy: str = "ext_normal",
+                     shift: int = 0) -> set[int]:
+    rots = {o for o in _baby_offsets(plan, n, shift) if o}
     if plan.giant > 1 and _giant_offset(plan, n):
         if strategy == "ext_double_hoist":
             # every giant group rotates by its own multiple of the giant step
@@ -152,6 +159,53 @@ def _level_rotations(plan: LevelPlan, n: int, strategy: str = "ext_normal") -> s
         else:
             rots.add(_giant_offset(plan, n))
     return rots
+
+
+def _packed(spec: BootstrapSpec, log_n: int, p: BootstrapParams) -> bool:
+    """Whether the program runs one EvalMod on a 2n-periodic vector that
+    holds the real parts in its first n slots and the imaginary parts in the
+    next n (possible when 2n slots fit: n <= N/4)."""
+    return bool(p.packed_evalmod) and int(spec.log_slots) <= int(log_n) - 2
+
+
+def _packing_masks(n: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Slot masks of period 2n (lo = the first n slots of each period):
+    a = lo - i hi, so that w' + conj(w') for w' = a w is 2 Re w on lo and
+    2 Im w on hi (w n-periodic); then u = d1 s + d2 rot_n(s) with
+    d1 = lo + i hi, d2 = i lo + hi rebuilds the n-periodic s_lo + i s_hi."""
+    lo = np.arange(2 * n) < n
+    a = np.where(lo, 1.0 + 0j, -1j)
+    d1 = np.where(lo, 1.0 + 0j, 1j)
+    d2 = np.where(lo, 1j, 1.0 + 0j)
+    return a, d1, d2
+
+
+def _period_rows(plan: LevelPlan, n: int, m: int, out_mask=None, in_masks=None,
+                 scale_factor: float = 1.0) -> np.ndarray:
+    """Diagonal rows of a level applied to slot vectors of period m (a
+    multiple of n), in the order of hoisted_mac_sum: row g B' + k B + b for
+    giant g, input mask k and baby b (B' = B times the number of masks).
+    out_mask multiplies the level's output slot-wise; with in_masks
+    [d_0, d_1, ..] the level reads u = sum_k d_k rot_(k n)(x), which puts the
+    term of offset o on the baby rot_(o + k n)(x) with the diagonal
+    d_o(i) d_k(i + o)."""
+    masks = list(in_masks) if in_masks is not None else [None]
+    B, reps = plan.baby, m // n
+    rows = np.zeros((plan.giant * B * len(masks), m), dtype=np.complex128)
+    for g in range(plan.giant):
+        for k, d_in in enumerate(masks):
+            for b in range(B):
+                t = g * B + b
+                o = t * plan.stride - plan.center
+                if t >= plan.width or o % n not in plan.diagonals:
+                    continue
+                d = np.tile(plan.diagonals[o % n], reps)
+                if out_mask is not None:
+                    d = d * out_mask
+                if d_in is not None:
+                    d = d * np.roll(d_in, -o)
+                rows[(g * len(masks) + k) * B + b] = np.roll(d, g * B * plan.stride)
+    return rows * scale_factor
 
 
 def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> Requirements:
@@ -165,8 +219,15 @@ def requirements(specs, log_n: int, params: "BootstrapParams | None" = None) -> 
         _check_spec(spec, int(log_n))
         n = 1 << _transform_log_slots(spec, int(log_n))
         cts, stc = _plans(spec, p, int(log_n))
-        for plan in (*cts, *stc):
-            rots |= _level_rotations(plan, n, p.strategy)
+        packed = _packed(spec, int(log_n), p)
+        for i, plan in enumerate(cts):
+            m = 2 * n if packed and i == len(cts) - 1 else n
+            rots |= _level_rotations(plan, m, p.strategy)
+        for i, plan in enumerate(stc):
+            if packed and i == 0:
+                rots |= _level_rotations(plan, 2 * n, p.strategy, shift=n)
+            else:
+                rots |= _level_rotations(plan, n, p.strategy)
         rots.update(_subsum_rotations(spec, int(log_n)))
         rots.add(2 * (1 << int(log_n)) - 1)
     return Requirements(rotations=tuple(sorted(rots)))
@@ -180,6 +241,8 @@ class _Level:
     primes: int         # primes dropped after the MAC
     pt_scale: float     # encoding scale of the diagonals
     out_scale: float    # exact scale after the rescales
+    period: int = 0     # slot period of the diagonals (0: the program's slots)
+    shift: int = 0      # second baby set rot_(o + shift) (packed SlotToCoeff input)
 
 
 @dataclass
@@ -202,6 +265,7 @@ class BootstrapProgram:
     output_limbs: int = 0
     subsum: list = field(default_factory=list)  # sub-sum rotations (sparse programs)
     read_scale: float = 0.0                     # scale the CoeffToSlot input is read at
+    packed: bool = False                        # one EvalMod on the 2n-periodic vector
 
     @property
     def depth_limbs(self) -> int:
@@ -285,8 +349,10 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
     prog = BootstrapProgram(spec=spec, context=ctx, evalmod=p, coefficients=coeffs,
                             cheb_depth=depth, step=step, raise_limbs=T,
                             target_ratio=2.0 ** -p.ratio_bits,
-                            subsum=_subsum_rotations(spec, ctx.logN), read_scale=s0)
+                            subsum=_subsum_rotations(spec, ctx.logN), read_scale=s0,
+                            packed=_packed(spec, ctx.logN, p))
     vectors = {}
+    mask_a, mask_d1, mask_d2 = _packing_masks(n)
 
     # CoeffToSlot: the last level lands on the ladder top
     top = T - sum(drops)
@@ -303,8 +369,15 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
             w = 2.0 ** p.cts_pt_bits
             want = scale * w / div
         name = f"cts{i}"
-        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, 1.0 / gap if i == 0 else 1.0))
-        prog.cts.append(_Level(name, plan, limbs, d, w, want))
+        factor = 1.0 / gap if i == 0 else 1.0
+        if prog.packed and i == n_cts - 1:
+            # the last level also multiplies its output by the packing mask a
+            vectors[name] = fhe.PackedRaw(_period_rows(plan, n, 2 * n, out_mask=mask_a,
+                                                       scale_factor=factor))
+            prog.cts.append(_Level(name, plan, limbs, d, w, want, period=2 * n))
+        else:
+            vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, factor))
+            prog.cts.append(_Level(name, plan, limbs, d, w, want))
         scale, limbs = want, limbs - d
     prog.ladder = ladder
 
@@ -319,8 +392,16 @@ def generate(context, spec: BootstrapSpec, evalmod: BootstrapParams | None = Non
         want = ctx.scale_at(limbs - drop) if i == n_stc - 1 else _STC_SCALE
         w = want * div / scale
         name = f"stc{i}"
-        vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, fold if i == 0 else 1.0))
-        prog.stc.append(_Level(name, plan, limbs, drop, w, want))
+        if prog.packed and i == 0:
+            # the first level reads u = d1 s + d2 rot_n(s) from EvalMod's
+            # 2n-periodic output s: two baby sets, rot_o(s) and rot_(o+n)(s)
+            vectors[name] = fhe.PackedRaw(_period_rows(plan, n, 2 * n,
+                                                       in_masks=(mask_d1, mask_d2),
+                                                       scale_factor=fold))
+            prog.stc.append(_Level(name, plan, limbs, drop, w, want, period=2 * n, shift=n))
+        else:
+            vectors[name] = fhe.PackedRaw(plan.plaintext_rows(n, fold if i == 0 else 1.0))
+            prog.stc.append(_Level(name, plan, limbs, drop, w, want))
         scale, limbs = want, limbs - drop
     prog.output_limbs = limbs
     assert limbs == int(spec.output_levels) + 1, (limbs, spec.output_levels)
@@ -380,14 +461,19 @@ def input_limbs(context, params: "BootstrapParams | None" = None) -> int:
     return 1 if round(want / float(ctx.scale_at(1))) >= 1 else 2
 
 
+def _level_layout(lv: _Level, prog: BootstrapProgram) -> tuple[int, list[int], int]:
+    """(slot period, baby rotations, giant rotation) of a linear level."""
+    m = lv.period or _program_slots(prog)
+    return m, _baby_offsets(lv.plan, m, lv.shift), _giant_offset(lv.plan, m)
+
+
 def _linear_level(x, lv: _Level, prog: BootstrapProgram, ctx):
-    n = _program_slots(prog)
-    plan = lv.plan
+    m, babies, giant = _level_layout(lv, prog)
     ext = prog.evalmod.strategy != "normal"
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
-    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=ext)
-    acc = fhe.hoisted_mac_sum(x, _baby_offsets(plan, n), pts, _giant_offset(plan, n),
-                              plan.giant, ctx, strategy=prog.evalmod.strategy)
+    pts = prog.constants.plaintext(lv.name, state=state, slots=m, context=ctx, is_ext=ext)
+    acc = fhe.hoisted_mac_sum(x, babies, pts, giant, lv.plan.giant, ctx,
+                              strategy=prog.evalmod.strategy)
     if lv.primes:
         acc = fhe.rescale_many([acc], ctx, primes=lv.primes)[0]
     acc.set_scale(lv.out_scale, 1)
@@ -434,12 +520,17 @@ def bootstrap(ct, context, program: BootstrapProgram):
     y = cheb.LCt(x, 0)
     yc = cheb.LCt(fhe.homo_rotate(x, 2 * ctx.N - 1, ctx), 0)
     re = ops.add(y, yc)
-    im = cheb.LCt(fhe.homo_mul_i(ops.add(y, yc, sign=-1.0).ct, ctx, negative=True), 0)
-    del y, yc, x
-    s_re = _evalmod(ops, re, prog)
-    s_im = _evalmod(ops, im, prog)
-    u = fhe.homo_add(s_re.ct, fhe.homo_mul_i(s_im.ct, ctx), ctx)
-    del s_re, s_im
+    if prog.packed:
+        # 2 Re on the first n slots of each 2n, 2 Im on the next n
+        del y, yc, x
+        u = _evalmod(ops, re, prog).ct
+    else:
+        im = cheb.LCt(fhe.homo_mul_i(ops.add(y, yc, sign=-1.0).ct, ctx, negative=True), 0)
+        del y, yc, x
+        s_re = _evalmod(ops, re, prog)
+        s_im = _evalmod(ops, im, prog)
+        u = fhe.homo_add(s_re.ct, fhe.homo_mul_i(s_im.ct, ctx), ctx)
+        del s_re, s_im
     for lv in prog.stc:
         u = _linear_level(u, lv, prog, ctx)
     u.set_scale(prog.stc[-1].out_scale * ratio, 1)
@@ -447,14 +538,12 @@ def bootstrap(ct, context, program: BootstrapProgram):
 
 
 def _linear_level_many(xs: list, lv: _Level, prog: BootstrapProgram, ctx) -> list:
-    n = _program_slots(prog)
-    plan = lv.plan
     if prog.evalmod.strategy == "normal":
         return [_linear_level(x, lv, prog, ctx) for x in xs]
+    m, babies, giant = _level_layout(lv, prog)
     state = fhe.CipherState(cur_limbs=lv.limbs, scale_degree=1, scaling_factor=lv.pt_scale)
-    pts = prog.constants.plaintext(lv.name, state=state, slots=n, context=ctx, is_ext=True)
-    accs = fhe.hoisted_mac_sum_ext_many(xs, _baby_offsets(plan, n), pts,
-                                        _giant_offset(plan, n), plan.giant, ctx,
+    pts = prog.constants.plaintext(lv.name, state=state, slots=m, context=ctx, is_ext=True)
+    accs = fhe.hoisted_mac_sum_ext_many(xs, babies, pts, giant, lv.plan.giant, ctx,
                                         strategy=prog.evalmod.strategy)
     if lv.primes:
         accs = fhe.rescale_many(accs, ctx, primes=lv.primes)
@@ -482,13 +571,18 @@ def _bootstrap_group(cts: list, ctx, prog: BootstrapProgram) -> list:
     conj = fhe.homo_rotate_many(xs, 2 * ctx.N - 1, ctx)
     y, yc = cheb.LCt(xs, 0), cheb.LCt(conj, 0)
     re = ops.add(y, yc)
-    im = [fhe.homo_mul_i(d, ctx, negative=True) for d in ops.add(y, yc, sign=-1.0).ct]
-    del xs, conj, y, yc
-    k = len(cts)
-    # real and imaginary parts of the whole group run through EvalMod together
-    s = _evalmod(ops, cheb.LCt(re.ct + im, 0), prog).ct
-    u = [fhe.homo_add(s[i], fhe.homo_mul_i(s[k + i], ctx), ctx) for i in range(k)]
-    del s
+    if prog.packed:
+        # real and imaginary parts share each ciphertext's 2n-periodic vector
+        del xs, conj, y, yc
+        u = _evalmod(ops, re, prog).ct
+    else:
+        im = [fhe.homo_mul_i(d, ctx, negative=True) for d in ops.add(y, yc, sign=-1.0).ct]
+        del xs, conj, y, yc
+        k = len(cts)
+        # real and imaginary parts of the whole group run through EvalMod together
+        s = _evalmod(ops, cheb.LCt(re.ct + im, 0), prog).ct
+        u = [fhe.homo_add(s[i], fhe.homo_mul_i(s[k + i], ctx), ctx) for i in range(k)]
+        del s
     for lv in prog.stc:
         u = _linear_level_many(u, lv, prog, ctx)
     for x, r in zip(u, ratios):

@@ -209,11 +209,15 @@ def test_requirements_and_limb_plan():
     # extended-basis levels (at most 2 giants): up to 32 babies per level
     assert len(req.rotations) <= 96
     # a sparse program: the sub-sum's rotations n, 2n, .., N/4 plus its
-    # n-slot transforms' (all below n), and the conjugation
+    # n-slot transforms' (all below n; below 2n for the two levels next to
+    # the packed EvalMod), and the conjugation
     sparse = bs.requirements([bs.BootstrapSpec(log_slots=7, level_budget=(3, 3))], log_n=16)
     subsum = {128 << k for k in range(8)}
     assert subsum <= set(sparse.rotations)
-    assert all(r < 128 for r in set(sparse.rotations) - subsum - {2 * 65536 - 1})
+    assert all(r < 256 for r in set(sparse.rotations) - subsum - {2 * 65536 - 1})
+    unpacked = bs.requirements([bs.BootstrapSpec(log_slots=7, level_budget=(3, 3))], log_n=16,
+                               params=bs.BootstrapParams(packed_evalmod=False))
+    assert all(r < 128 for r in set(unpacked.rotations) - subsum - {2 * 65536 - 1})
     assert len(sparse.rotations) < len(req.rotations)
     with pytest.raises(ValueError):
         bs.requirements([bs.BootstrapSpec(log_slots=16)], log_n=16)
@@ -296,3 +300,98 @@ def test_sparse_bootstrap_model(log_n, log_slots, budget):
         u2 = _bsgs(u2, plan, plan.plaintext_rows(n, fold if i == 0 else 1.0))
     err = np.abs(u2 - z).max()
     assert err < 2.0 ** -18, err
+
+
+def _mac_period(x: np.ndarray, rows: np.ndarray, babies, giant_off: int, giants: int):
+    """hoisted_mac_sum on a full-length slot vector with rows of a shorter
+    period: sum_g rot_(g giant)(sum_b tile(p[g B + b]) rot_(baby_b) x)."""
+    reps, B = len(x) // rows.shape[1], len(babies)
+    acc = np.zeros(len(x), dtype=np.complex128)
+    for g in range(giants):
+        inner = sum(np.tile(rows[g * B + b], reps) * np.roll(x, -babies[b]) for b in range(B))
+        acc = acc + np.roll(inner, -g * giant_off)
+    return acc
+
+
+@pytest.mark.parametrize("log_n,log_slots,budget", [(10, 4, (2, 2)), (9, 3, (3, 3)),
+                                                     (10, 6, (1, 3))])
+def test_sparse_packed_evalmod_model(log_n, log_slots, budget):
+    """Sparse program with one EvalMod per ciphertext (n <= N/4): the last
+    CoeffToSlot level multiplies its output by the 2n-periodic mask
+    a = lo - i hi, so w' + conj(w') holds 2 Re w on the first n slots of
+    each 2n and 2 Im w on the next n; the first SlotToCoeff level reads
+    d1 s + d2 rot_n(s) through a second baby set.  Checked on values: the
+    packed vector, the first SlotToCoeff level against the unpacked level on
+    2 w (EvalMod replaced by the identity), and the whole pipeline against
+    the message."""
+    N, half = 1 << log_n, 1 << (log_n - 1)
+    n = 1 << log_slots
+    gap = half // n
+    rng = np.random.default_rng(3 * log_n + log_slots)
+    p = bs.BootstrapParams()
+    spec = bs.BootstrapSpec(log_slots=log_slots, level_budget=budget)
+    assert bs._packed(spec, log_n, p)
+    assert not bs._packed(bs.BootstrapSpec(log_slots=log_n - 1), log_n, p)
+    assert not bs._packed(spec, log_n, bs.BootstrapParams(packed_evalmod=False))
+    cts_plans, stc_plans = bs._plans(spec, p, log_n)
+    a, d1, d2 = bs._packing_masks(n)
+    z = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    Pn = np.array([int(format(i, f"0{log_slots}b")[::-1], 2) for i in range(n)])
+    u = z.copy()
+    for s_ in reversed(range(1, log_slots + 1)):
+        u = lintrans.apply_diagonals(lintrans.stage_diagonals(n, s_, True), u)
+    u_nat = np.empty_like(u)
+    u_nat[Pn] = u
+    t = np.concatenate([u_nat.real, u_nat.imag]) * 2.0 ** -p.ratio_bits
+    m = np.zeros(N)
+    m[::gap] = t
+    I = rng.integers(-12, 13, N).astype(float)
+    x = _slots_of(m + I) / (2 * p.K)
+    for r in bs._subsum_rotations(spec, log_n):
+        x = x + np.roll(x, -r)
+    for i, plan in enumerate(cts_plans):
+        factor = 1.0 / gap if i == 0 else 1.0
+        if i == len(cts_plans) - 1:
+            rows = bs._period_rows(plan, n, 2 * n, out_mask=a, scale_factor=factor)
+            x_n = x  # the level's n-periodic input, kept for the unpacked check
+            x = _mac_period(x, rows, bs._baby_offsets(plan, 2 * n), bs._giant_offset(plan, 2 * n),
+                            plan.giant)
+            w = _mac_period(x_n, plan.plaintext_rows(n, factor), bs._baby_offsets(plan, n),
+                            bs._giant_offset(plan, n), plan.giant)
+        else:
+            x = _mac_period(x, plan.plaintext_rows(n, factor), bs._baby_offsets(plan, n),
+                            bs._giant_offset(plan, n), plan.giant)
+    tk = (m + I)[::gap]
+    want = (tk[:n] + 1j * tk[n:])[Pn] / (2 * p.K)
+    assert np.abs(w[:n] - want).max() < 1e-8
+    assert np.abs(x - np.tile(a, gap // 2) * w).max() < 1e-8
+    v = x + np.conj(x)
+    packed = np.concatenate([2 * want.real, 2 * want.imag])
+    assert np.abs(v - np.tile(packed, gap // 2)).max() < 1e-8
+    fold = 1.0 / (2 * math.pi * 2.0 ** -p.ratio_bits)
+    plan0 = stc_plans[0]
+    rows0 = bs._period_rows(plan0, n, 2 * n, in_masks=(d1, d2), scale_factor=fold)
+    babies0 = bs._baby_offsets(plan0, 2 * n, n)
+    assert len(babies0) == 2 * plan0.baby and len(set(babies0)) == len(babies0)
+    giant0 = bs._giant_offset(plan0, 2 * n)
+    # EvalMod as the identity: the first level equals the unpacked one on 2 w
+    lin = _mac_period(v, rows0, babies0, giant0, plan0.giant)
+    ref = _mac_period(np.tile(2 * want, gap), plan0.plaintext_rows(n, fold),
+                      bs._baby_offsets(plan0, n), bs._giant_offset(plan0, n), plan0.giant)
+    assert np.abs(lin - ref).max() < 1e-6 * np.abs(ref).max()
+    # the pipeline with EvalMod
+    coeffs = bs._evalmod_coefficients(p)
+    ops = ValueOps()
+    c = cheb.evaluate(ops, cheb.LCt(v.real, 0), coeffs)
+    for _ in range(p.double_angles):
+        c = ops.add_const(ops.double(ops.mul(c, c)), -1.0)
+    y = _mac_period(c.ct.astype(np.complex128), rows0, babies0, giant0, plan0.giant)
+    for plan in stc_plans[1:]:
+        y = _mac_period(y, plan.plaintext_rows(n), bs._baby_offsets(plan, n),
+                        bs._giant_offset(plan, n), plan.giant)
+    err = np.abs(y - np.tile(z, gap)).max()
+    assert err < 2.0 ** -18, err
+    # the program's rotation keys cover both masked levels
+    rots = set(bs.requirements([spec], log_n=log_n, params=p).rotations)
+    assert {r for r in babies0 if r} <= rots
+    assert {r for r in bs._baby_offsets(cts_plans[-1], 2 * n) if r} <= rots

@@ -194,12 +194,16 @@ def test_bootstrap_pair_refreshes_two_real_streams(boot_ctx):
         assert -math.log2(err) > 14, err
 
 
-@pytest.mark.parametrize("log_slots,budget", [(7, (3, 3)), (4, (2, 2)), (10, (3, 3))])
-def test_bootstrap_sparse_slots(boot_ctx, log_slots, budget):
+@pytest.mark.parametrize("log_slots,budget,packed", [(7, (3, 3), True), (7, (3, 3), False),
+                                                     (4, (2, 2), True), (10, (3, 3), True),
+                                                     (10, (3, 3), False)])
+def test_bootstrap_sparse_slots(boot_ctx, log_slots, budget, packed):
     """A sparse ciphertext (128 slots: the reference's slim RMSNorm program
     shape) through the sparse program: the sub-sum (rotations by n, 2n, ..
     N/4) leaves the raised polynomial's coefficients at multiples of
-    N / 2n, then the n-slot CoeffToSlot, EvalMod and SlotToCoeff.  One
+    N / 2n, then the n-slot CoeffToSlot, EvalMod and SlotToCoeff.  With
+    ``packed`` the real and imaginary parts share one 2n-periodic vector
+    (one EvalMod per ciphertext), else they run through two.  One
     bootstrap and a batched group of three agree with each other and with
     the message."""
     from easyfhe.bs import openfhe as bs
@@ -207,8 +211,9 @@ def test_bootstrap_sparse_slots(boot_ctx, log_slots, budget):
     client, ctx = boot_ctx
     slots = 1 << log_slots
     prog = bs.generate(ctx, bs.BootstrapSpec(log_slots=log_slots, level_budget=budget,
-                                             output_levels=3))
-    assert prog.spec.slots == slots
+                                             output_levels=3),
+                       bs.BootstrapParams(packed_evalmod=packed))
+    assert prog.spec.slots == slots and prog.packed == packed
     assert prog.subsum == [slots << k for k in range(ctx.logN - 1 - log_slots)]
     rng = np.random.default_rng(11)
     zs = [rng.uniform(-1, 1, slots) for _ in range(3)]
