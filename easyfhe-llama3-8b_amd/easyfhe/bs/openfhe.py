@@ -17,7 +17,9 @@ Pipeline ("modraise_first", reference bootstrap.py:29):
    a Chebyshev interpolant of cos(2 pi (K y - 1/4) / 2^r) on [-1, 1] and r
    double-angle steps give sin(2 pi t), evaluated on an exact-scale ladder
    (``easyfhe.chebyshev``) at a working scale of at least 2^55 (two primes
-   per level on a 40-bit chain).
+   per level on a 40-bit chain).  A sparse program of at most N/4 slots
+   packs both parts into one 2n-periodic vector (``_packing_masks``) and
+   runs EvalMod once.
 5. **SlotToCoeff**: the special FFT, with q_0 / (2 pi Delta') folded into
    its first level; the last level lands on the nominal scale 2^dcrt_bits.
 
