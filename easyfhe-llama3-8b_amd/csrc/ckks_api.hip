@@ -3097,6 +3097,13 @@ int ckks_profile_read(ckks_context *c, char *buf, size_t len) {
   API_END
 }
 
+int ckks_context_stream(ckks_context *c, void **stream) {
+  API_BEGIN
+  require(c && stream, "null argument");
+  *stream = (void *)c->stream;
+  API_END
+}
+
 int ckks_event_create(ckks_context *c, ckks_event **out) {
   API_BEGIN
   require(c && out, "null argument");

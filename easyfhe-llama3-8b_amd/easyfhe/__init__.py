@@ -10,11 +10,16 @@ bridge of reference backend.py:274-284 uses ``from_numpy`` and an optional
 
 from __future__ import annotations
 
+import types
+
 import numpy as np
 
 from . import _native  # noqa: F401  (loads the library; raises if it is missing)
 from . import bs, cuda, fhe, packing
 from .tensor import DeviceTensor, HostTensor
+
+# the reference's Triton bridge reads torch.version.hip (gpu_packer.py:16-19)
+version = types.SimpleNamespace(hip="7.2", cuda=None)
 
 complex128 = np.complex128
 float64 = np.float64
@@ -41,4 +46,4 @@ def get_device_module(device: str):
 
 
 __all__ = ["bs", "complex128", "cuda", "empty", "fhe", "float32", "float64", "from_numpy",
-           "get_device_module", "is_tensor"]
+           "get_device_module", "is_tensor", "version"]

@@ -151,6 +151,7 @@ SIGNATURES = {
     "ckks_event_record": (I, [VP]),
     "ckks_event_elapsed_ms": (I, [VP, VP, ctypes.POINTER(ctypes.c_float)]),
     "ckks_event_destroy": (None, [VP]),
+    "ckks_context_stream": (I, [VP, VPP]),
 }
 
 

@@ -361,6 +361,12 @@ int ckks_event_record(ckks_event *ev);
 int ckks_event_elapsed_ms(ckks_event *start, ckks_event *end, float *ms);
 void ckks_event_destroy(ckks_event *ev);
 
+/* The context's HIP stream as an opaque handle (hipStream_t), for callers
+ * that order their own launches with the library's work (the reference's
+ * Triton bridge reads torch.cuda.current_stream(idx).cuda_stream,
+ * operators/linear/gpu_packer.py:35-45). */
+int ckks_context_stream(ckks_context *ctx, void **stream);
+
 #ifdef __cplusplus
 }
 #endif

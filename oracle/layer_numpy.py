@@ -21,6 +21,13 @@ reference compares its encrypted layer against:
 * ``fm_pack`` / ``fm_unpack``: the feature-major token-lane layout of
   layouts/feature_major.py:74-92 (slot = feature * lanes + token % lanes,
   ciphertext = token // lanes).
+
+Pins: ``apply_rope_numpy``, ``attention_numpy`` and ``decoder_layer_numpy``
+match golden vectors of the reference's own ``apply_rope_heads``,
+``attention_gqa_numpy`` and ``poly_transformer_layer_numpy``
+(tests/test_layer_golden.py); the series evaluator, RMSNorm, MLP, Alg2
+softmax and packing are pinned by library routines and closed forms
+(tests/test_layer_numpy.py).
 """
 
 from __future__ import annotations
