@@ -846,20 +846,39 @@ static constexpr size_t kNoAllocWords = (size_t)1 << 25;
 static __device__ __align__(256) u64 scratch[kNoAllocWords];
 
 static constexpr int kMaxDevices = 64;
-static u64 *g_scratch_ptr[kMaxDevices];
+
+// Per device: the array's device address, and the ordering of its users.
+// Calls from different contexts run on different streams; each call holds
+// `mu` while it enqueues, makes its stream wait on `done` (the previous
+// call's completion on whatever stream it ran) and records `done` after its
+// last launch, so the calls use the buffer one after another on the device
+// without the host waiting.
+struct NoAllocDevice {
+  u64 *ptr = nullptr;
+  hipEvent_t done = nullptr;
+  std::mutex mu;
+};
+static NoAllocDevice g_noalloc[kMaxDevices];
 static std::mutex g_scratch_mu;
 
-// The device address of `scratch` on the current device (each device holds
-// its own copy of the array at its own address); resolved once per device.
-static u64 *device_scratch(int dev) {
+// Resolves the device address of `scratch` on the current device (each
+// device holds its own copy of the array at its own address) and creates its
+// ordering event, recorded once on `stream` so that it is always in a
+// recorded state; done once per device.
+static u64 *device_scratch(int dev, hipStream_t stream) {
   require(dev >= 0 && dev < kMaxDevices, "device index out of range");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  NoAllocDevice &nd = g_noalloc[dev];
+  if (!nd.ptr) {
     void *p = nullptr;
     HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    g_scratch_ptr[dev] = (u64 *)p;
+    hipEvent_t ev = nullptr;
+    HIPCHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    HIPCHECK(hipEventRecord(ev, stream));
+    nd.done = ev;
+    nd.ptr = (u64 *)p;
   }
-  return g_scratch_ptr[dev];
+  return nd.ptr;
 }
 
 // ===========================================================================
@@ -1213,7 +1232,8 @@ static size_t rotate_scratch_words(const ckks_context *c, int limbs, int nb) {
 // `arena` given, every intermediate lives in that fixed buffer of
 // `arena_words` words (n <= 64) and nothing is allocated.
 static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g, ckks_ct **out,
-                         u64 *arena = nullptr, size_t arena_words = 0) {
+                         u64 *arena = nullptr, size_t arena_words = 0,
+                         size_t *arena_used = nullptr) {
   const int limbs = in[0]->limbs;
   const size_t N = c->N, P = (size_t)limbs * N;
   const DeviceKey &key = get_key(c, g);
@@ -1235,6 +1255,7 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
       // the fixed scratch holds one batch's intermediates: one stream
       Scratch s(c, arena, arena_words);
       run(b0, nb, s);
+      if (arena_used) *arena_used = std::max(*arena_used, s.used);
     } else {
       run_parts(c, b0, nb, run);
     }
@@ -1469,7 +1490,7 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
       }
     }
     HIPCHECK(hipGetDevice(&c->device));
-    c->noalloc_scratch = device_scratch(c->device);
+    c->noalloc_scratch = device_scratch(c->device, c->stream);
   } catch (...) {
     free_context(c);
     throw;
@@ -2061,7 +2082,8 @@ int ckks_rotate_many_noalloc(ckks_context *c, const ckks_ct *const *in, int n, i
   API_BEGIN
   require(c && in && out, "null argument");
   require(n >= 1 && n <= kMaxBatch, "noalloc rotation takes 1 to 64 ciphertexts");
-  const int limbs = in[0] ? in[0]->limbs : 0;
+  check_ct(c, in[0], "rotate_noalloc");
+  const int limbs = in[0]->limbs;
   for (int i = 0; i < n; i++) {
     check_ct(c, in[i], "rotate_noalloc");
     check_ct(c, out[i], "rotate_noalloc output");
@@ -2074,29 +2096,43 @@ int ckks_rotate_many_noalloc(ckks_context *c, const ckks_ct *const *in, int n, i
     for (int j = 0; j < i; j++) require(out[i]->d != out[j]->d, "outputs must be distinct");
   }
   const u64 g = galois_of(c, rotation);
+  size_t need = 0;
   if (g != 1) {
     get_key(c, g);
     require(c->rotation_tables,
             "the key-switch constants are built with the rotation keys (ckks_keygen_rotations)");
-    const size_t need = rotate_scratch_words(c, limbs, n);
+    need = rotate_scratch_words(c, limbs, n);
     require(need <= kNoAllocWords,
             "noalloc rotation needs " + std::to_string(need * 8 >> 20) +
                 " MiB of scratch, above its fixed 256 MiB: rotate fewer ciphertexts per call");
     require(c->noalloc_scratch != nullptr, "fixed scratch not resolved for this device");
-  }
-  for (int i = 0; i < n; i++) {
-    out[i]->slots = in[i]->slots;
-    out[i]->scale = in[i]->scale;
-    out[i]->scale_degree = in[i]->scale_degree;
   }
   if (g == 1) {
     for (int i = 0; i < n; i++)
       HIPCHECK(hipMemcpyAsync(out[i]->d, in[i]->d, in[i]->bytes, hipMemcpyDeviceToDevice,
                               c->stream));
   } else {
+    NoAllocDevice &nd = g_noalloc[c->device];
+    std::lock_guard<std::mutex> lk(nd.mu);
+    HIPCHECK(hipStreamWaitEvent(c->stream, nd.done, 0));
+    // whatever was enqueued (also if a launch below fails) uses the buffer:
+    // the next call waits for it
+    struct Release {
+      NoAllocDevice &nd;
+      hipStream_t st;
+      ~Release() { (void)hipEventRecord(nd.done, st); }
+    } release{nd, c->stream};
     ckks_ct *o[kMaxBatch];
     for (int i = 0; i < n; i++) o[i] = out[i];
-    rotate_batch(c, in, n, g, o, c->noalloc_scratch, kNoAllocWords);
+    size_t used = 0;
+    rotate_batch(c, in, n, g, o, c->noalloc_scratch, kNoAllocWords, &used);
+    require(used <= need, "noalloc rotation used " + std::to_string(used) +
+                              " scratch words, above the " + std::to_string(need) + " it sized");
+  }
+  for (int i = 0; i < n; i++) {
+    out[i]->slots = in[i]->slots;
+    out[i]->scale = in[i]->scale;
+    out[i]->scale_degree = in[i]->scale_degree;
   }
   API_END
 }
@@ -2638,45 +2674,50 @@ static void mac_sum_double(ckks_context *c, const ckks_ct *const *a, int n,
   std::vector<u64 *> bp((size_t)B * n);
   for (size_t k = 0; k < bp.size(); k++) bp[k] = bab + k * EP;
   ext_babies(c, a, n, baby_rotations, B, bp.data(), s);
-  // inner sums of every group: [g][n][2][E][N]; group 0's are the running sum
-  u64 *inner = s.get((size_t)giant_count * n * EP);
+  // inner sums, GC groups per MAC launch, [slot][n][2][E][N]: slot 0 holds
+  // group 0's, the running sum; the other groups of a launch go to slots
+  // 1..gn (the first launch's to 1..gn-1) and are folded into the sum before
+  // the next launch reuses them, so at most GC + 1 groups are held at once
   const int GC = std::max(1, std::min(kMacGroups, kMaxBatch / B));
-  for (int g0 = 0; g0 < giant_count; g0 += GC) {
-    const int gn = std::min(GC, giant_count - g0);
-    Batch ptb{};
-    for (int gi = 0; gi < gn; gi++)
-      for (int b = 0; b < B; b++) ptb.p[gi * B + b] = pts[(g0 + gi) * B + b]->d;
-    launch_mac_many(c, bab, n, ptb, B, gn, inner + (size_t)g0 * n * EP, E, limbs);
-  }
+  u64 *inner = s.get((size_t)std::min(giant_count, GC + 1) * n * EP);
   u64 *total = inner;
   Batch tb{};
   for (int i = 0; i < n; i++) tb.p[i] = total + (size_t)i * EP;
-  for (int g = 1; g < giant_count; g++) {
-    u64 *ug = inner + (size_t)g * n * EP;
-    Batch ub{};
-    for (int i = 0; i < n; i++) ub.p[i] = ug + (size_t)i * EP;
-    if (gal[g] == 1) {
-      launch_ext_rot_accum(c, ub, Batch{}, tb, 1, n, E, limbs);
-      continue;
+  for (int g0 = 0; g0 < giant_count; g0 += GC) {
+    const int gn = std::min(GC, giant_count - g0);
+    u64 *dst = g0 == 0 ? inner : inner + (size_t)n * EP;
+    Batch ptb{};
+    for (int gi = 0; gi < gn; gi++)
+      for (int b = 0; b < B; b++) ptb.p[gi * B + b] = pts[(g0 + gi) * B + b]->d;
+    launch_mac_many(c, bab, n, ptb, B, gn, dst, E, limbs);
+    for (int gi = g0 == 0 ? 1 : 0; gi < gn; gi++) {
+      const int g = g0 + gi;
+      u64 *ug = dst + (size_t)gi * n * EP;
+      Batch ub{};
+      for (int i = 0; i < n; i++) ub.p[i] = ug + (size_t)i * EP;
+      if (gal[g] == 1) {
+        launch_ext_rot_accum(c, ub, Batch{}, tb, 1, n, E, limbs);
+        continue;
+      }
+      Scratch s2(c);
+      u64 *v = s2.get((size_t)n * P);
+      std::vector<const u64 *> src(n), vp(n);
+      std::vector<u64 *> dstp(n);
+      for (int i = 0; i < n; i++) {
+        src[i] = ug + (size_t)i * EP + (size_t)E * N;  // component 1
+        dstp[i] = v + (size_t)i * P;
+        vp[i] = dstp[i];
+      }
+      moddown_polys(c, limbs, src, dstp, s2);
+      u64 *ext = s2.get((size_t)n * est);
+      ks_modup(c, limbs, n, vp.data(), ext, s2);
+      u64 *acc = s2.get((size_t)n * EP);
+      launch_key_inner(c, strided(ext, est), strided(acc, EP), n, get_key(c, gal[g]), digits,
+                       E, limbs, gal[g], nullptr);
+      Batch ab{};
+      for (int i = 0; i < n; i++) ab.p[i] = acc + (size_t)i * EP;
+      launch_ext_rot_accum(c, ub, ab, tb, gal[g], n, E, limbs);
     }
-    Scratch s2(c);
-    u64 *v = s2.get((size_t)n * P);
-    std::vector<const u64 *> src(n), vp(n);
-    std::vector<u64 *> dst(n);
-    for (int i = 0; i < n; i++) {
-      src[i] = ug + (size_t)i * EP + (size_t)E * N;  // component 1
-      dst[i] = v + (size_t)i * P;
-      vp[i] = dst[i];
-    }
-    moddown_polys(c, limbs, src, dst, s2);
-    u64 *ext = s2.get((size_t)n * est);
-    ks_modup(c, limbs, n, vp.data(), ext, s2);
-    u64 *acc = s2.get((size_t)n * EP);
-    launch_key_inner(c, strided(ext, est), strided(acc, EP), n, get_key(c, gal[g]), digits, E,
-                     limbs, gal[g], nullptr);
-    Batch ab{};
-    for (int i = 0; i < n; i++) ab.p[i] = acc + (size_t)i * EP;
-    launch_ext_rot_accum(c, ub, ab, tb, gal[g], n, E, limbs);
   }
   std::vector<KsJob> jobs(n);
   for (int i = 0; i < n; i++) out[i] = nullptr;

@@ -176,8 +176,11 @@ int ckks_rotate_many(ckks_context *ctx, const ckks_ct *const *in, int n,
  * allocated or freed.  CKKS_EINVAL when the call needs more scratch than
  * that (at N = 2^16 with 36 + 12 limbs and dnum 3 one ciphertext takes
  * 186 MiB) or when the rotation keys (whose generation also builds every
- * level's constants) are missing.  Calls that overlap on one GPU (contexts
- * on other streams or threads) share the buffer and race. */
+ * level's constants) are missing.  Calls on one GPU (contexts on other
+ * streams or threads) are ordered on the device: each call's stream waits
+ * for the previous call's work (an event, no host wait), so they use the
+ * buffer one after another.  Outputs' scale and slot count are written after
+ * the rotation is enqueued. */
 int ckks_rotate_many_noalloc(ckks_context *ctx, const ckks_ct *const *in, int n,
                              int64_t rotation, ckks_ct *const *out);
 /* homo_mul_relin + rescale for n pairs (config: HMult+relin+rescale). */

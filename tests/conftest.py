@@ -41,6 +41,10 @@ PARAMS = {
     "small": dict(log_n=12, depth=5, dnum=3, dcrt_bits=40, first_mod=60, special_bits=60),
     # CPU matvec workload: N = 2^13, 4 x 40-bit limbs, one 60-bit special prime
     "matvec": dict(log_n=13, depth=3, dnum=4, dcrt_bits=40, first_mod=40, special_bits=60),
+    # the matvec ring with 44-bit special primes (the fp64 arithmetic path on
+    # the P limbs, as on the keyswitch chain): 6 x 40-bit limbs, three digits
+    # of two, P = two 44-bit primes above each 80-bit digit
+    "ext44": dict(log_n=13, depth=5, dnum=3, dcrt_bits=40, first_mod=40, special_bits=44),
     # keyswitch workload: N = 2^16, 60-bit + 35 x 40-bit, dnum 3, 12 44-bit special
     # primes (P = 2^528 above the largest digit, 2^500)
     "keyswitch": dict(log_n=16, depth=35, dnum=3, dcrt_bits=40, first_mod=60, special_bits=44),

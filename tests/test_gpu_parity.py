@@ -361,13 +361,16 @@ def test_bsgs_matvec_parity():
     assert np.abs(dec - W @ x).max() < 1e-5
 
 
-def test_bsgs_matvec_ext_parity():
+@pytest.mark.parametrize("name", ["matvec", "ext44"])
+def test_bsgs_matvec_ext_parity(name):
     """The matvec workload with strategy "ext_normal": babies in Q u P, one
-    ModDown per giant group; bit-exact with the oracle's extended schedule."""
+    ModDown per giant group; bit-exact with the oracle's extended schedule,
+    on a 60-bit special prime (64-bit arithmetic on P) and on 44-bit ones
+    (the fp64 path of the extended MAC and the babies' key products)."""
     fhe = _fhe()
     D, lanes, B, G = 128, 32, 16, 8
     rots = tuple(lanes * b for b in range(1, B)) + (B * lanes,)
-    client, ctx, orc = _pair("matvec", rotations=rots)
+    client, ctx, orc = _pair(name, rotations=rots)
     slots = ctx.max_slots
     rng = np.random.default_rng(0)
     W = rng.uniform(-1, 1, (D, D))
@@ -390,17 +393,20 @@ def test_bsgs_matvec_ext_parity():
     assert np.abs(dec - W @ x).max() < 1e-5
 
 
+@pytest.mark.parametrize("name", ["matvec", "ext44"])
 @pytest.mark.parametrize("n_cts", [1, 3])
-def test_bsgs_matvec_double_hoist_parity(n_cts):
+def test_bsgs_matvec_double_hoist_parity(n_cts, name):
     """The matvec workload with strategy "ext_double_hoist": babies and
     giant groups in Q u P, every giant group rotated by its own key, one
     ModDown of the sum; bit-exact with the oracle's double-hoisted schedule
     for one ciphertext and for a batch of three (each equal to its own
-    single-ciphertext result), decrypting to W x."""
+    single-ciphertext result), decrypting to W x; on 60-bit and on 44-bit
+    special primes (the fp64 paths of the extended MAC, the multi-key
+    product and the giant groups' ModDown and re-ModUp)."""
     fhe = _fhe()
     D, lanes, B, G = 128, 32, 16, 8
     rots = tuple(lanes * b for b in range(1, B)) + tuple(g * B * lanes for g in range(1, G))
-    client, ctx, orc = _pair("matvec", rotations=rots)
+    client, ctx, orc = _pair(name, rotations=rots)
     slots = ctx.max_slots
     rng = np.random.default_rng(0)
     W = rng.uniform(-1, 1, (D, D))

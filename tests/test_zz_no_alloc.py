@@ -4,7 +4,10 @@ outputs with every intermediate in the library's fixed device buffer.
 Its outputs must equal ckks_rotate_many's word for word (the same kernels,
 the same order of operations), on two calls in a row with the second one
 smaller, at N = 2^16 on the key-switch chain and at N = 2^12 with a full
-batch of 64; the context's pool must see no allocation during the calls.
+batch of 64, on the default kernels and on the separate key product and
+special-limb inverse pass; the context's pool must see no allocation during
+the calls.  Two contexts (two streams) that call it alternately without any
+host synchronisation share the buffer one call after another.
 """
 
 from __future__ import annotations
@@ -70,9 +73,43 @@ def test_noalloc_rotation_full_size_two_calls():
     ctx.close()
 
 
-def test_noalloc_rotation_batches_two_calls():
+@pytest.mark.parametrize("env", [{}, {"CKKS_KEYSWITCH_FUSED": "0"},
+                                 {"CKKS_KS_SPECIAL_INV": "0"}])
+def test_noalloc_rotation_batches_two_calls(env, monkeypatch):
     """64 ciphertexts at N = 2^12, then 3 at a lower level; the identity
-    rotation copies."""
+    rotation copies.  The key-switch kernel choices are read at context
+    creation."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
     client, ctx = device_context("small", rotations=(1, -3))
     _check_calls(client, ctx, [(ctx.L, 64, 1), (ctx.L - 2, 3, -3), (ctx.L, 2, 0)])
     ctx.close()
+
+
+def test_noalloc_two_contexts_alternate_without_sync():
+    """Contexts A and B (own streams, own keys) call the entry point in turn,
+    four calls each, with no synchronisation between the calls; every output
+    equals that context's ckks_rotate_many afterwards."""
+    from easyfhe import fhe
+
+    rng = np.random.default_rng(11)
+    pairs = [device_context("small", seed=s, rotations=(1, 7)) for s in (3, 4)]
+    calls = []
+    for step in range(8):
+        client, ctx = pairs[step % 2]
+        rot = (1, 7)[(step // 2) % 2]
+        count = 64 if step < 2 else 8
+        ins = [client.encrypt(rng.uniform(-1, 1, ctx.max_slots), enc_id=7000 + 100 * step + i)
+               for i in range(count)]
+        outs = [client.encrypt(np.zeros(ctx.max_slots), enc_id=7900 + i) for i in range(count)]
+        calls.append((ctx, ins, rot, outs))
+    for client, ctx in pairs:
+        ctx.synchronize()
+    for ctx, ins, rot, outs in calls:
+        _noalloc(ctx, ins, rot, outs)  # no host wait between the calls
+    for ctx, ins, rot, outs in calls:
+        want = fhe.homo_rotate_many(ins, rot, ctx)
+        for i in range(len(ins)):
+            assert np.array_equal(outs[i].download(), want[i].download()), (rot, i)
+    for client, ctx in pairs:
+        ctx.close()
