@@ -989,6 +989,21 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
   u64 *coeff = s.get((size_t)n * limbs * N);
   Batch src{};
   for (int i = 0; i < n; i++) src.p[i] = (u64 *)d[i];
+  // N = 2^16 with the high-pass-only output: the inverse NTT's high pass, the
+  // conversion and the targets' forward high pass run as one kernel per digit
+  bool tile = high_only && !own_copy && c->ks_tile;
+  for (int j = 0; j < digits && tile; j++) tile = convert_h4_ok(c, bc_up(c, limbs, j));
+  if (tile) {
+    const size_t est = (size_t)digits * E * N;
+    launch_ntt_inv_low(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs);
+    for (int j = 0; j < digits; j++) {
+      const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
+      launch_convert_h4(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N),
+                        strided(ext + (size_t)j * E * N, est), n, bc_up(c, limbs, j), lo, lo, ns,
+                        limbs, false);
+    }
+    return;
+  }
   launch_ntt(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs, true);
   for (int j = 0; j < digits; j++) {
     const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
@@ -1028,15 +1043,6 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
   const int E = limbs + c->alpha;
   const int n = (int)jobs.size();
   if (!ptmp) ptmp = s.get((size_t)n * 2 * c->alpha * N);
-  if (sp_done)
-    launch_ntt_inv_high(c, strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N), 2 * n, limbs,
-                        c->alpha, limbs);
-  else
-    launch_ntt(c, strided(acc, E * N), strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N),
-               2 * n, limbs, c->alpha, limbs, true);
-  u64 *conv = s.get((size_t)n * 2 * limbs * N);
-  launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
-                       2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
   const u64 *pinv = pinv_table(c, limbs);
   // the fused path addresses component 1 of the addend and of the output at
   // a fixed offset from component 0 (as every caller lays them out)
@@ -1046,6 +1052,25 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
   for (int i = 0; i < n && uniform; i++)
     uniform = (jobs[i].add1 ? (u64)(jobs[i].add1 - jobs[i].add0) : 0) == add1_off &&
               (!jobs[i].add1 || jobs[i].add0) && (u64)(jobs[i].out1 - jobs[i].out0) == out1_off;
+  const Batch spb = strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N);  // limb l at l N
+  u64 *conv = s.get((size_t)n * 2 * limbs * N);
+  // N = 2^16: the special limbs' inverse high pass, the conversion and the
+  // forward high pass of the Q limbs in one kernel, then the low pass with
+  // the combine
+  const bool tile = c->logN == 16 && uniform && c->ks_tile && convert_h4_ok(c, bc_down(c, limbs));
+  if (tile) {
+    if (!sp_done) launch_ntt_inv_low(c, strided(acc, E * N), spb, 2 * n, limbs, c->alpha, limbs);
+    launch_convert_h4(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
+                      2 * n, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+  } else {
+    if (sp_done)
+      launch_ntt_inv_high(c, spb, 2 * n, limbs, c->alpha, limbs);
+    else
+      launch_ntt(c, strided(acc, E * N), spb, 2 * n, limbs, c->alpha, limbs, true);
+    launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N),
+                         strided(conv, (size_t)limbs * N), 2 * n, bc_down(c, limbs), c->L, limbs,
+                         0, limbs, true);
+  }
   if (c->logN == 16 && uniform) {
     // NTT of the conversion with the combine fused into its last pass
     Batch a0{}, o0{};
@@ -1056,7 +1081,7 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
       gal[i] = jobs[i].galois;
     }
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
-                       pinv, a0, add1_off, gal.data(), o0, out1_off);
+                       pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile);
     return;
   }
   launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2 * n, 0,
@@ -1468,6 +1493,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     c->ks_fused = !(kf && strcmp(kf, "0") == 0);
     const char *si = getenv("CKKS_KS_SPECIAL_INV");
     c->ks_sp_inv = !(si && strcmp(si, "0") == 0);
+    const char *kt = getenv("CKKS_KS_TILE");
+    c->ks_tile = !(kt && strcmp(kt, "0") == 0);
     const char *ss = getenv("CKKS_SPLIT_STREAMS");
     if (ss) {
       c->split_parts = atoi(ss);
@@ -1479,15 +1506,6 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
       // default priority, as the context stream
       HIPCHECK(hipStreamCreateWithFlags(&c->aux[i], hipStreamNonBlocking));
       HIPCHECK(hipEventCreateWithFlags(&c->join_ev[i], hipEventDisableTiming));
-    }
-    for (auto [var, dst] : {std::pair<const char *, int *>{"CKKS_NTT_COLS_FWD", &c->ntt_cols_fwd},
-                            {"CKKS_NTT_COLS_INV", &c->ntt_cols_inv}}) {
-      const char *v = getenv(var);
-      if (v) {
-        const int n = atoi(v);
-        require(n == 16 || n == 32 || n == 64, std::string(var) + " must be 16, 32 or 64");
-        *dst = n;
-      }
     }
     HIPCHECK(hipGetDevice(&c->device));
     c->noalloc_scratch = device_scratch(c->device, c->stream);

@@ -283,9 +283,11 @@ struct ckks_context {
   // product also take the ModDown's inverse low pass in the same kernel;
   // environment CKKS_KS_SPECIAL_INV=0 at creation keeps it separate
   bool ks_sp_inv = true;
-  // columns per block of the N = 2^16 column passes (16, 32 or 64), forward
-  // and inverse; environment CKKS_NTT_COLS_FWD / CKKS_NTT_COLS_INV at creation
-  int ntt_cols_fwd = 64, ntt_cols_inv = 32;
+  // N = 2^16: the ModUp's and ModDown's conversions run between the NTT
+  // halves in one register-resident kernel (launch_convert_h4) where the
+  // int8-MFMA table allows; environment CKKS_KS_TILE=0 at creation keeps the
+  // separate high passes and conversion
+  bool ks_tile = true;
   // batched key switches of at least kSplitMin ciphertexts per part run as
   // `split_parts` parts, the first on the context stream and the others on
   // `aux` streams (forked from and joined back into the context stream), so
@@ -384,10 +386,27 @@ void launch_moddown_combine(ckks_context *c, const Strided &acc, const Strided &
                             const Batch &out0, const Batch &out1, int n_items, int limbs,
                             int E, const u64 *pinv, const u64 *amul = nullptr,
                             const PostOp *post = nullptr);
+// high_done: conv already went through the forward high pass
+// (launch_convert_h4), only the low pass with the combine runs
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off,
-                        const u64 *amul = nullptr, const PostOp *post = nullptr);
+                        const u64 *amul = nullptr, const PostOp *post = nullptr,
+                        bool high_done = false);
+// N = 2^16: the inverse NTT's low pass alone (its high pass then runs in
+// launch_convert_h4 or launch_ntt_inv_high)
+void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                        int l_begin, int l_count, int q_limbs);
+// N = 2^16: launch_basis_convert of inverse-low-passed sources (src item at
+// the first source limb, as launch_basis_convert's) with the inverse high
+// pass before and the forward high pass of every target after, in one
+// register-resident kernel; targets leave ready for the forward low pass.
+// convert_h4_ok tells whether table t takes it (int8-MFMA table, at most 12
+// sources and 64 targets).
+bool convert_h4_ok(const ckks_context *c, const BCTable &t);
+void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                       const BCTable &t, int src_prime0, int t_split, int t_skip, int q_limbs,
+                       bool centered);
 void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
                          int limbs, int D, const u64 *tab);
 void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,

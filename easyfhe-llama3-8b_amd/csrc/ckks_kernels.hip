@@ -217,11 +217,21 @@ __global__ __launch_bounds__(TPB) void k_ntt_inv_high(Batch dst, int logN, int l
 }
 
 // ===========================================================================
-// N = 2^16: register-resident radix-16 passes.  Each pass covers 8 bit
-// positions as two rounds of 4 stages held in 16 registers per thread, with
-// one LDS exchange between the rounds.  Butterflies are Harvey's lazy ones
-// (forward values in [0, 4q), inverse values in [0, 2q)); only the last pass
-// reduces to [0, q), so pass-to-pass data in HBM may be lazy.
+// N = 2^16 as a 16 x 4096 array (position j = 4096 r + c): two passes of
+// register-resident radix-16 rounds (4 stages each in 16 registers per
+// thread).
+//   high pass, bit positions 15..12: one 16-point transform per column c,
+//     held by one thread (words c + 4096 k), no exchange; every stage's
+//     twiddle is the same for all columns;
+//   low pass, bit positions 11..0: one 4096-word row (tile) per block: round
+//     Z on bits 11..8 (thread t holds words t + 256 k, read and written
+//     coalesced), then rounds A (7..4) and B (3..0) on the tile as 16 rows
+//     of 256 through the padded LDS tile.
+// Forward: high then low (Cooley-Tukey, twiddle psi_br[(N + j) >> (b + 1)]
+// for bit b and position j); inverse: low then high (Gentleman-Sande with
+// psi_br^-1), then x N^-1.  Butterflies are Harvey's lazy ones (forward
+// values in [0, 4q), inverse values in [0, 2q)); only the last pass reduces
+// to [0, q), so pass-to-pass data in HBM may be lazy.
 // LDS layout: element (r, c) of a 16 x 256 tile at r * 272 + c + (c >> 4):
 // the +1 per 16 keeps 16-apart columns in distinct banks.
 // ===========================================================================
@@ -248,24 +258,6 @@ __device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u6
 }
 
 __device__ __forceinline__ int lds16(int r, int c) { return r * 272 + c + (c >> 4); }
-
-// Column passes (bit positions 15..8): a block holds all 256 rows of C
-// columns, 16 C threads (column tid mod C, row group tid / C).  C = 16: the
-// padded 16 x 272 tile above.  C = 32 or 64: every global access of a wave
-// is 8 C contiguous bytes of one row (256 or 512, against 128), and element
-// (row 16 a + b, column c) sits at b 16 C + a C + c, where both exchanges
-// are consecutive per wave without padding (64 or 128 KiB per block).
-template <int COLS>
-struct ColTile {
-  static constexpr int C = COLS;
-  static constexpr int THREADS = 16 * C;
-  static constexpr int LDS_WORDS = C == 16 ? 16 * 272 : 16 * 16 * C;
-  __device__ static int col() { return threadIdx.x & (C - 1); }
-  __device__ static int grp() { return threadIdx.x / C; }
-  __device__ static int at(int a, int b, int c) {
-    return C == 16 ? lds16(b, 16 * a + c) : b * 16 * C + a * C + c;
-  }
-};
 
 // ModDown epilogue of the forward low pass (conv items 2 i + c):
 // out_c[l][k] = (acc_c[l][k] - NTT(conv_c)[l][k]) P^-1 + add_c[l][sigma(k)]
@@ -365,28 +357,11 @@ __device__ __forceinline__ void md_store(const MDCombine &md, int item2, int lim
   o[(size_t)limb * N + e] = r;
 }
 
-// forward, bit positions 15..8: tile = 256 rows (stride 256) x 16 columns
-template <int COLS>
-__device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
-                                                        int q_limbs, int L,
-                                                        const ModQ *__restrict__ mods,
-                                                        const u64 *__restrict__ psi,
-                                                        const u64 *__restrict__ psi_sh) {
-  u64 *sm = lds;
-  const int limb = l_begin + blockIdx.z;
-  const int p = prime_of(limb, q_limbs, L);
-  const u64 q = mods[p].q, q2 = 2 * q;
-  const u64 *W = psi + ((size_t)p << 16);
-  const u64 *Ws = psi_sh + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
-  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  using CT = ColTile<COLS>;
-  const int c = CT::col(), g = CT::grp();
-  const int col = blockIdx.x * CT::C + c;
-  u64 x[16];
-  // round A: row = g + 16 k, stages on row bits 7..4 (k bits 3..0)
-#pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = in[(g + 16 * k) * 256 + col];
+// High pass, 64-bit body: x[k] = word c + 4096 k of one column, stages on
+// bits 15..12 (k bits 3..0); the twiddle of stage st and pair k is
+// psi_br[2^st + (k >> (4 - st))], the same for every column.
+__device__ __forceinline__ void u64_high_fwd(u64 (&x)[16], const u64 *__restrict__ W,
+                                             const u64 *__restrict__ Ws, u64 q, u64 q2) {
 #pragma unroll
   for (int st = 0; st < 4; st++) {
     const int half = 8 >> st;
@@ -397,30 +372,66 @@ __device__ __forceinline__ void k_ntt16_fwd_high_body(u64 *__restrict__ lds, Bat
       ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
     }
   }
-  // row = g + 16 k lives at LDS tile row g, "column" 16 k + c
+}
+
+// inverse high pass on one column (lazy input), then x N^-1 to [0, q)
+__device__ __forceinline__ void u64_high_inv(u64 (&x)[16], const u64 *__restrict__ W,
+                                             const u64 *__restrict__ Ws, u64 ni, u64 nis,
+                                             u64 q, u64 q2) {
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[CT::at(k, g, c)] = x[k];
-  __syncthreads();
-  // round B: row = 16 g + j, stages on row bits 3..0
+  for (int st = 3; st >= 0; st--) {
+    const int half = 8 >> st;
 #pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = sm[CT::at(g, j, c)];
-#pragma unroll
-  for (int st = 4; st < 8; st++) {
-    const int half = 8 >> (st - 4);
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      const int ti = (1 << st) + ((16 * g + j) >> (8 - st));
-      ct_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (1 << st) + (k >> (4 - st));
+      gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
     }
   }
 #pragma unroll
-  for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = x[j];
+  for (int k = 0; k < 16; k++) {
+    const u64 v = shoup_lazy(x[k], ni, nis, q);
+    x[k] = v >= q ? v - q : v;
+  }
+}
+
+// Round Z of the forward low pass: x[k] = word t + 256 k of tile `tile`
+// (position j = 4096 tile + 256 k + t), stages on bits 11..8 (k bits 3..0);
+// twiddle index (N >> (b + 1)) + (j >> (b + 1)) does not depend on t.
+__device__ __forceinline__ void u64_low_round_z(u64 (&x)[16], const u64 *__restrict__ W,
+                                                const u64 *__restrict__ Ws, int tile, u64 q,
+                                                u64 q2) {
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 11 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((tile * 4096 + 256 * k) >> (b + 1));
+      ct_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
+}
+
+// inverse round Z: stages on bits 8..11, same positions as round Z
+__device__ __forceinline__ void u64_inv_round_z(u64 (&x)[16], const u64 *__restrict__ W,
+                                                const u64 *__restrict__ Ws, int tile, u64 q,
+                                                u64 q2) {
+#pragma unroll
+  for (int b = 8; b < 12; b++) {
+    const int half = 1 << (b - 8);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const int ti = (65536 >> (b + 1)) + ((tile * 4096 + 256 * k) >> (b + 1));
+      gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
+    }
+  }
 }
 
 // Rounds of the forward low pass on one thread's 16 words of global row
-// `row`: A on columns c0 + 16 k (bits 7..4), B on columns 16 c0 + j (bits
-// 3..0); values in [0, 4q)
+// `row` (of 256): A on columns c0 + 16 k (bits 7..4), B on columns 16 c0 + j
+// (bits 3..0); values in [0, 4q)
 __device__ __forceinline__ void u64_low_round_a(u64 (&x)[16], const u64 *__restrict__ W,
                                                 const u64 *__restrict__ Ws, int row, u64 q,
                                                 u64 q2) {
@@ -451,8 +462,25 @@ __device__ __forceinline__ void u64_low_round_b(u64 (&x)[16], const u64 *__restr
   }
 }
 
-// forward, bit positions 7..0: tile = 16 contiguous rows of 256; output in [0, q)
-// (COMBINE: the ModDown epilogue instead of the store)
+// Round Z of tile `tile` from src (words t + 256 k), its result into the LDS
+// tile for round A (word 256 k + t at lds16(k, t)).  The caller synchronises
+// before (earlier reads of sm) and after.
+__device__ __forceinline__ void u64_round_z_to_lds(u64 *__restrict__ sm,
+                                                   const u64 *__restrict__ src,
+                                                   const u64 *__restrict__ W,
+                                                   const u64 *__restrict__ Ws, int tile, u64 q,
+                                                   u64 q2) {
+  const int t = threadIdx.x;
+  u64 x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = src[t + 256 * k];
+  u64_low_round_z(x, W, Ws, tile, q, q2);
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(k, t)] = x[k];
+}
+
+// forward, bit positions 11..0: one 4096-word tile per block; output in
+// [0, q) (COMBINE: the ModDown epilogue instead of the store)
 template <bool COMBINE>
 __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
                                                        int L, const ModQ *__restrict__ mods,
@@ -468,12 +496,15 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
   u64 *base = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;  // global row of 256
-  u64 x[16];
   MDPrefetch pf;
-  // round A: column = c0 + 16 k, stages on column bits 7..4
-#pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = base[rl * 256 + c0 + 16 * k];
   if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
+  u64_round_z_to_lds(sm, base, W, Ws, blockIdx.x, q, q2);
+  __syncthreads();
+  u64 x[16];
+  // round A: column = c0 + 16 k, stages on column bits 7..4; the thread
+  // writes back the slots it read, which no other thread reads
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
   u64_low_round_a(x, W, Ws, row, q, q2);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
@@ -504,7 +535,7 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
   }
 }
 
-// inverse, bit positions 0..7 (first pass): input in [0, 2q), output lazy
+// inverse, bit positions 0..11 (first pass): input in [0, 2q), output lazy
 __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                        int q_limbs, int L,
                                                        const ModQ *__restrict__ mods,
@@ -521,8 +552,8 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
   u64 x[16];
-  // round A: column = 16 c0 + j, stages on column bits 0..3; the load goes
-  // through LDS so that adjacent lanes read adjacent words
+  // round B^-1: column = 16 c0 + j, stages on column bits 0..3; the load
+  // goes through LDS so that adjacent lanes read adjacent words
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = in[rl * 256 + c0 + 16 * k];
   __syncthreads();
@@ -542,7 +573,7 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
 #pragma unroll
   for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
   __syncthreads();
-  // round B: column = c0 + 16 k, stages on column bits 4..7
+  // round A^-1: column = c0 + 16 k, stages on column bits 4..7
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
 #pragma unroll
@@ -555,63 +586,17 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
       gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
     }
   }
+  // round Z^-1 (bits 8..11) on words t + 256 k: the thread's slots go back
+  // (no other thread reads them), then each thread takes one tile column
 #pragma unroll
-  for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = x[k];
-}
-
-// inverse, bit positions 8..15 (second pass), then x N^-1, output in [0, q)
-template <int COLS>
-__device__ __forceinline__ void k_ntt16_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
-                                                        int L, const ModQ *__restrict__ mods,
-                                                        const u64 *__restrict__ ipsi,
-                                                        const u64 *__restrict__ ipsi_sh,
-                                                        const u64 *__restrict__ ninv) {
-  u64 *sm = lds;
-  const int limb = l_begin + blockIdx.z;
-  const int p = prime_of(limb, q_limbs, L);
-  const u64 q = mods[p].q, q2 = 2 * q;
-  const u64 *W = ipsi + ((size_t)p << 16);
-  const u64 *Ws = ipsi_sh + ((size_t)p << 16);
-  u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  using CT = ColTile<COLS>;
-  const int c = CT::col(), g = CT::grp();
-  const int col = blockIdx.x * CT::C + c;
-  u64 x[16];
-  // round A: row = 16 g + j, stages on row bits 0..3 (st = 7..4)
-#pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = io[(16 * g + j) * 256 + col];
-#pragma unroll
-  for (int st = 7; st >= 4; st--) {
-    const int half = 8 >> (st - 4);
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      const int ti = (1 << st) + ((16 * g + j) >> (8 - st));
-      gs_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 16; j++) sm[CT::at(g, j, c)] = x[j];
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
   __syncthreads();
-  // round B: row = g + 16 k, stages on row bits 4..7 (st = 3..0)
+  const int t = threadIdx.x;
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = sm[CT::at(k, g, c)];
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(k, t)];
+  u64_inv_round_z(x, W, Ws, blockIdx.x, q, q2);
 #pragma unroll
-  for (int st = 3; st >= 0; st--) {
-    const int half = 8 >> st;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (k & half) continue;
-      const int ti = (1 << st) + (k >> (4 - st));
-      gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
-    }
-  }
-  const u64 ni = ninv[2 * p], nis = ninv[2 * p + 1];
-#pragma unroll
-  for (int k = 0; k < 16; k++) {
-    u64 v = shoup_lazy(x[k], ni, nis, q);
-    io[(g + 16 * k) * 256 + col] = v >= q ? v - q : v;
-  }
+  for (int k = 0; k < 16; k++) out[t + 256 * k] = x[k];
 }
 
 // ---------------------------------------------------------------------------
@@ -689,24 +674,10 @@ __device__ __forceinline__ void gs_fp(double &X, double &Y, double w, double wq,
 
 
 // Twiddle table layout for the fp64 path, per prime: [N][2] doubles (w, w/q).
-template <int COLS>
-__device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
-                                                         int q_limbs, int L,
-                                                         const ModQ *__restrict__ mods,
-                                                         const double2 *__restrict__ tw) {
-  double *sm = reinterpret_cast<double *>(lds);
-  const int limb = l_begin + blockIdx.z;
-  const int p = prime_of(limb, q_limbs, L);
-  const double q = (double)mods[p].q;
-  const double2 *T = tw + ((size_t)p << 16);
-  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16);
-  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  using CT = ColTile<COLS>;
-  const int c = CT::col(), g = CT::grp();
-  const int col = blockIdx.x * CT::C + c;
-  double x[16];
-#pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = u52_to_dbl(in[(g + 16 * k) * 256 + col]);
+// High pass, fp64 body: x[k] = word c + 4096 k of one column, stages on bits
+// 15..12; |x| grows by at most q per stage.
+__device__ __forceinline__ void fp_high_fwd(double (&x)[16], const double2 *__restrict__ T,
+                                            double q) {
 #pragma unroll
   for (int st = 0; st < 4; st++) {
     const int half = 8 >> st;
@@ -717,23 +688,73 @@ __device__ __forceinline__ void k_ntt16f_fwd_high_body(u64 *__restrict__ lds, Ba
       ct_fp(x[k], x[k + half], w.x, w.y, q);
     }
   }
+}
+
+// inverse high pass on one column (|x| < 2^50 on entry: reduced first),
+// then x N^-1; result as exact doubles in [0, q)
+__device__ __forceinline__ void fp_high_inv(double (&x)[16], const double2 *__restrict__ T,
+                                            double2 ni, double q, double qinv) {
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[CT::at(k, g, c)] = x[k];
-  __syncthreads();
+  for (int k = 0; k < 16; k++) x[k] = fp_reduce(x[k], qinv, q);
 #pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = sm[CT::at(g, j, c)];
+  for (int st = 3; st >= 0; st--) {
+    const int half = 8 >> st;
 #pragma unroll
-  for (int st = 4; st < 8; st++) {
-    const int half = 8 >> (st - 4);
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      const double2 w = T[(1 << st) + ((16 * g + j) >> (8 - st))];
-      ct_fp(x[j], x[j + half], w.x, w.y, q);
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(1 << st) + (k >> (4 - st))];
+      gs_fp(x[k], x[k + half], w.x, w.y, q);
     }
   }
 #pragma unroll
-  for (int j = 0; j < 16; j++) out[(16 * g + j) * 256 + col] = dbl_bits(x[j]);
+  for (int k = 0; k < 16; k++) x[k] = fp_canon_d(fp_mulmod(x[k], ni.x, ni.y, q), qinv, q);
+}
+
+// Round Z of the fp64 forward low pass (as u64_low_round_z)
+__device__ __forceinline__ void fp_low_round_z(double (&x)[16], const double2 *__restrict__ T,
+                                               int tile, double q) {
+#pragma unroll
+  for (int st = 0; st < 4; st++) {
+    const int b = 11 - st, half = 8 >> st;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((tile * 4096 + 256 * k) >> (b + 1))];
+      ct_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+}
+
+// inverse round Z on bits 8..11 (entry values reduced first)
+__device__ __forceinline__ void fp_inv_round_z(double (&x)[16], const double2 *__restrict__ T,
+                                               int tile, double q, double qinv) {
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = fp_reduce(x[k], qinv, q);
+#pragma unroll
+  for (int b = 8; b < 12; b++) {
+    const int half = 1 << (b - 8);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k & half) continue;
+      const double2 w = T[(65536 >> (b + 1)) + ((tile * 4096 + 256 * k) >> (b + 1))];
+      gs_fp(x[k], x[k + half], w.x, w.y, q);
+    }
+  }
+}
+
+// Round Z of tile `tile` from src (raw double words t + 256 k) into the LDS
+// tile for round A (as u64_round_z_to_lds).
+__device__ __forceinline__ void fp_round_z_to_lds(double *__restrict__ sm,
+                                                  const u64 *__restrict__ src,
+                                                  const double2 *__restrict__ T, int tile,
+                                                  double q) {
+  const int t = threadIdx.x;
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = as_dbl(src[t + 256 * k]);
+  fp_low_round_z(x, T, tile, q);
+#pragma unroll
+  for (int k = 0; k < 16; k++) sm[lds16(k, t)] = x[k];
 }
 
 // Rounds of the fp64 forward low pass (as u64_low_round_a/b); the table
@@ -781,11 +802,15 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
   u64 *base = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const int row = blockIdx.x * 16 + rl;
-  double x[16];
   MDPrefetch pf;
-#pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = as_dbl(base[rl * 256 + c0 + 16 * k]);
   if constexpr (COMBINE) md_load(md, blockIdx.y, limb, blockIdx.x * 4096 + rl * 256 + c0, pf);
+  fp_round_z_to_lds(sm, base, T, blockIdx.x, q);
+  __syncthreads();
+  double x[16];
+  // round A on the thread's slots, written back in place (no other thread
+  // reads them)
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
   fp_low_round_a(x, T, row, q);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
@@ -813,12 +838,13 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
   }
 }
 
-// The fp64 inverse low pass of one tile of 16 rows held in the LDS tile sm
+// The fp64 inverse low pass of one 4096-word tile held in the LDS tile sm
 // (position rl 256 + c of the tile at lds16(rl, c), values in [0, q)),
-// rows 16 tile .. 16 tile + 15 of the limb: round A on bit positions 3..0
-// from the 16 consecutive positions 16 c0 + j of row rl, round B on 7..4
-// from positions c0 + 16 k; the result (fp64 words of the pass) goes to
-// out[rl 256 + c0 + 16 k].  The caller has synchronised after filling sm.
+// rows 16 tile .. 16 tile + 15 of 256: round A on bit positions 3..0 from
+// the 16 consecutive positions 16 c0 + j of row rl, round B on 7..4 from
+// positions c0 + 16 k, round Z on 11..8 from positions t + 256 k; the result
+// (fp64 words of the pass) goes to out[t + 256 k].  The caller has
+// synchronised after filling sm.
 __device__ __forceinline__ void fp_inv_low_tile(double *__restrict__ sm, int tile,
                                                 const double2 *__restrict__ T, double q,
                                                 double qinv, u64 *__restrict__ out) {
@@ -854,8 +880,16 @@ __device__ __forceinline__ void fp_inv_low_tile(double *__restrict__ sm, int til
       gs_fp(x[k], x[k + half], w.x, w.y, q);
     }
   }
+  // the thread's slots back in place, then one tile column per thread
 #pragma unroll
-  for (int k = 0; k < 16; k++) out[rl * 256 + c0 + 16 * k] = dbl_bits(x[k]);
+  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
+  __syncthreads();
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = sm[lds16(k, t)];
+  fp_inv_round_z(x, T, tile, q, qinv);
+#pragma unroll
+  for (int k = 0; k < 16; k++) out[t + 256 * k] = dbl_bits(x[k]);
 }
 
 __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
@@ -876,70 +910,43 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   fp_inv_low_tile(sm, blockIdx.x, T, q, qinv, out);
 }
 
-template <int COLS>
-__device__ __forceinline__ void k_ntt16f_inv_high_body(u64 *__restrict__ lds, Batch dst, int l_begin, int q_limbs,
-                                                         int L, const ModQ *__restrict__ mods,
-                                                         const double2 *__restrict__ itw,
-                                                         const double2 *__restrict__ ninv) {
-  double *sm = reinterpret_cast<double *>(lds);
-  const int limb = l_begin + blockIdx.z;
-  const int p = prime_of(limb, q_limbs, L);
-  const double q = (double)mods[p].q, qinv = 1.0 / q;
-  const double2 *T = itw + ((size_t)p << 16);
-  u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16);
-  using CT = ColTile<COLS>;
-  const int c = CT::col(), g = CT::grp();
-  const int col = blockIdx.x * CT::C + c;
-  double x[16];
-#pragma unroll
-  for (int j = 0; j < 16; j++) x[j] = fp_reduce(as_dbl(io[(16 * g + j) * 256 + col]), qinv, q);
-#pragma unroll
-  for (int st = 7; st >= 4; st--) {
-    const int half = 8 >> (st - 4);
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-      if (j & half) continue;
-      const double2 w = T[(1 << st) + ((16 * g + j) >> (8 - st))];
-      gs_fp(x[j], x[j + half], w.x, w.y, q);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 16; j++) sm[CT::at(g, j, c)] = x[j];
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[CT::at(k, g, c)], qinv, q);
-#pragma unroll
-  for (int st = 3; st >= 0; st--) {
-    const int half = 8 >> st;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      if (k & half) continue;
-      const double2 w = T[(1 << st) + (k >> (4 - st))];
-      gs_fp(x[k], x[k + half], w.x, w.y, q);
-    }
-  }
-  const double2 ni = ninv[p];
-#pragma unroll
-  for (int k = 0; k < 16; k++)
-    io[(g + 16 * k) * 256 + col] = fp_canon(fp_mulmod(x[k], ni.x, ni.y, q), qinv, q);
-}
-
 // One launch per pass over every limb of a batch: a block takes the fp64
 // body when its prime is below 2^45 and the 64-bit body otherwise (q_0), so
 // the few 64-bit limbs run beside the others instead of in launches of their
-// own.  Both bodies share one LDS tile.
+// own.  Both low-pass bodies share one LDS tile.
 constexpr u64 kFpPrimeBound = (u64)1 << 45;
 
-template <int COLS>
-__global__ __launch_bounds__(ColTile<COLS>::THREADS) void k_ntt16m_fwd_high(
-    Batch src, Batch dst, int l_begin, int q_limbs, int L, const ModQ *__restrict__ mods,
-    const u64 *__restrict__ psi, const u64 *__restrict__ psi_sh,
-    const double2 *__restrict__ tw) {
-  __shared__ u64 lds[ColTile<COLS>::LDS_WORDS];
-  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
-    k_ntt16f_fwd_high_body<COLS>(lds, src, dst, l_begin, q_limbs, L, mods, tw);
-  else
-    k_ntt16_fwd_high_body<COLS>(lds, src, dst, l_begin, q_limbs, L, mods, psi, psi_sh);
+// High passes: thread = one column c = 256 blockIdx.x + t of limb
+// l_begin + blockIdx.z of item blockIdx.y; words c + 4096 k, each load and
+// store of a wave 512 contiguous bytes.  Forward: canonical input, lazy
+// output (fp64: raw double bits); inverse: lazy input, canonical output.
+__global__ __launch_bounds__(TPB) void k_ntt16m_fwd_high(Batch src, Batch dst, int l_begin,
+                                                         int q_limbs, int L,
+                                                         const ModQ *__restrict__ mods,
+                                                         const u64 *__restrict__ psi,
+                                                         const u64 *__restrict__ psi_sh,
+                                                         const double2 *__restrict__ tw) {
+  const int limb = l_begin + blockIdx.z;
+  const int p = prime_of(limb, q_limbs, L);
+  const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + blockIdx.x * 256 + threadIdx.x;
+  u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + blockIdx.x * 256 + threadIdx.x;
+  const u64 qu = mods[p].q;
+  if (qu < kFpPrimeBound) {
+    const double q = (double)qu;
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = u52_to_dbl(in[4096 * k]);
+    fp_high_fwd(x, tw + ((size_t)p << 16), q);
+#pragma unroll
+    for (int k = 0; k < 16; k++) out[4096 * k] = dbl_bits(x[k]);
+  } else {
+    u64 x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = in[4096 * k];
+    u64_high_fwd(x, psi + ((size_t)p << 16), psi_sh + ((size_t)p << 16), qu, 2 * qu);
+#pragma unroll
+    for (int k = 0; k < 16; k++) out[4096 * k] = x[k];
+  }
 }
 
 template <bool COMBINE>
@@ -969,54 +976,48 @@ __global__ __launch_bounds__(TPB) void k_ntt16m_inv_low(Batch src, Batch dst, in
     k_ntt16_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh);
 }
 
-template <int COLS>
-__global__ __launch_bounds__(ColTile<COLS>::THREADS) void k_ntt16m_inv_high(
+__global__ __launch_bounds__(TPB) void k_ntt16m_inv_high(
     Batch dst, int l_begin, int q_limbs, int L, const ModQ *__restrict__ mods,
     const u64 *__restrict__ ipsi, const u64 *__restrict__ ipsi_sh, const u64 *__restrict__ ninv,
     const double2 *__restrict__ itw, const double2 *__restrict__ ninv_fp) {
-  __shared__ u64 lds[ColTile<COLS>::LDS_WORDS];
-  if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
-    k_ntt16f_inv_high_body<COLS>(lds, dst, l_begin, q_limbs, L, mods, itw, ninv_fp);
-  else
-    k_ntt16_inv_high_body<COLS>(lds, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh, ninv);
+  const int limb = l_begin + blockIdx.z;
+  const int p = prime_of(limb, q_limbs, L);
+  u64 *io = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + blockIdx.x * 256 + threadIdx.x;
+  const u64 qu = mods[p].q;
+  if (qu < kFpPrimeBound) {
+    const double q = (double)qu, qinv = 1.0 / q;
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = as_dbl(io[4096 * k]);
+    fp_high_inv(x, itw + ((size_t)p << 16), ninv_fp[p], q, qinv);
+#pragma unroll
+    for (int k = 0; k < 16; k++) io[4096 * k] = dbl_to_u52(x[k]);
+  } else {
+    u64 x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = io[4096 * k];
+    u64_high_inv(x, ipsi + ((size_t)p << 16), ipsi_sh + ((size_t)p << 16), ninv[2 * p],
+                 ninv[2 * p + 1], qu, 2 * qu);
+#pragma unroll
+    for (int k = 0; k < 16; k++) io[4096 * k] = x[k];
+  }
 }
 
-// the column passes of a batch: grid (256 / C, items, limbs)
-template <int COLS>
-static void fwd_high16(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
-                       int l_begin, int l_count, int q_limbs) {
-  hipLaunchKernelGGL(k_ntt16m_fwd_high<COLS>, dim3(256 / COLS, n_items, l_count),
-                     dim3(ColTile<COLS>::THREADS), 0, c->stream, src, dst, l_begin, q_limbs,
-                     c->L, c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp);
-  LAUNCH_CHECK();
-}
-
-template <int COLS>
-static void inv_high16(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
-                       int q_limbs) {
-  hipLaunchKernelGGL(k_ntt16m_inv_high<COLS>, dim3(256 / COLS, n_items, l_count),
-                     dim3(ColTile<COLS>::THREADS), 0, c->stream, dst, l_begin, q_limbs, c->L,
-                     c->d_mods, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
-                     (const double2 *)c->d_itw_fp, (const double2 *)c->d_ninv_fp);
-  LAUNCH_CHECK();
-}
-
+// the high passes of a batch: grid (16, items, limbs)
 static void launch_fwd_high16(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                               int l_begin, int l_count, int q_limbs) {
-  switch (c->ntt_cols_fwd) {
-    case 64: fwd_high16<64>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
-    case 32: fwd_high16<32>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
-    default: fwd_high16<16>(c, src, dst, n_items, l_begin, l_count, q_limbs); break;
-  }
+  hipLaunchKernelGGL(k_ntt16m_fwd_high, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream,
+                     src, dst, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh,
+                     (const double2 *)c->d_tw_fp);
+  LAUNCH_CHECK();
 }
 
 static void launch_inv_high16(ckks_context *c, const Batch &dst, int n_items, int l_begin,
                               int l_count, int q_limbs) {
-  switch (c->ntt_cols_inv) {
-    case 64: inv_high16<64>(c, dst, n_items, l_begin, l_count, q_limbs); break;
-    case 32: inv_high16<32>(c, dst, n_items, l_begin, l_count, q_limbs); break;
-    default: inv_high16<16>(c, dst, n_items, l_begin, l_count, q_limbs); break;
-  }
+  hipLaunchKernelGGL(k_ntt16m_inv_high, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream,
+                     dst, l_begin, q_limbs, c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh,
+                     c->d_ninv, (const double2 *)c->d_itw_fp, (const double2 *)c->d_ninv_fp);
+  LAUNCH_CHECK();
 }
 
 // grid (tiles, items, limbs): blocks of one prime run back to back and share
@@ -1085,8 +1086,7 @@ void launch_ntt(ckks_context *c, const Batch &src, const Batch &dst, int n_items
 
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
                          int q_limbs) {
-  KTimer kt(c, "ntt_inv", 16.0 * c->N * n_items * l_count,
-            0.25 * c->N * c->logN * n_items * l_count);
+  KTimer kt(c, "ntt_inv", 16.0 * c->N * n_items * l_count, 0.5 * c->N * 4 * n_items * l_count);
   if (n_items <= 0 || l_count <= 0) return;
   if (c->logN != 16) throw std::invalid_argument("inverse high pass alone: N = 2^16 only");
   launch_inv_high16(c, dst, n_items, l_begin, l_count, q_limbs);
@@ -1098,7 +1098,7 @@ void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_b
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul,
-                        const PostOp *post) {
+                        const PostOp *post, bool high_done) {
   KTimer kt(c, "ntt_fwd_moddown",
             8.0 * c->N * limbs * (6.0 * n + (batch_ptr_host(add, 0) ? (add1_off ? 2.0 : 1.0) * n : 0.0)),
             0.5 * c->N * c->logN * 2.0 * n * limbs);
@@ -1115,18 +1115,18 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   if (post) md.post = *post;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
   dim3 block(TPB), grid(16, 2 * n, limbs);
-  launch_fwd_high16(c, conv, conv, 2 * n, 0, limbs, limbs);
+  if (!high_done) launch_fwd_high16(c, conv, conv, 2 * n, 0, limbs, limbs);
   hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, grid, block, 0, c->stream, conv, 0, limbs, c->L,
                      c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp, md);
   LAUNCH_CHECK();
 }
 
-// Only the high pass of the forward NTT (bit positions 15..8), for limbs
+// Only the high pass of the forward NTT (bit positions 15..12), for limbs
 // whose low pass runs inside launch_ntt_low_key.  N = 2^16 only.
 void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                          int l_begin, int l_count, int q_limbs) {
   KTimer kt(c, "ntt_fwd_high", 16.0 * c->N * n_items * l_count,
-            0.25 * c->N * c->logN * n_items * l_count);
+            0.5 * c->N * 4 * n_items * l_count);
   if (n_items <= 0 || l_count <= 0) return;
   if (c->logN != 16) throw std::invalid_argument("high pass alone: N = 2^16 only");
   launch_fwd_high16(c, src, dst, n_items, l_begin, l_count, q_limbs);
@@ -1245,10 +1245,12 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
     } else {
       const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
                        (size_t)tile * 4096;
-#pragma unroll
-      for (int k = 0; k < 16; k++) y[k] = as_dbl(src[rl * 256 + c0 + 16 * k]);
-      fp_low_round_a(y, T, row, q);
       __syncthreads();  // the previous digit's reads of the tile are done
+      fp_round_z_to_lds(sm, src, T, tile, q);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = sm[lds16(rl, c0 + 16 * k)];
+      fp_low_round_a(y, T, row, q);
 #pragma unroll
       for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
       __syncthreads();
@@ -1318,10 +1320,12 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
     } else {
       const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
                        (size_t)tile * 4096;
-#pragma unroll
-      for (int k = 0; k < 16; k++) y[k] = src[rl * 256 + c0 + 16 * k];
-      u64_low_round_a(y, W, Ws, row, q, q2);
       __syncthreads();  // the previous digit's reads of the tile are done
+      u64_round_z_to_lds(sm, src, W, Ws, tile, q, q2);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = sm[lds16(rl, c0 + 16 * k)];
+      u64_low_round_a(y, W, Ws, row, q, q2);
 #pragma unroll
       for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
       __syncthreads();
@@ -2087,6 +2091,219 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
                        dim3(TPB), 0, c->stream, src, dst, c->logN, t.ns, t.nd, t.d, src_prime0,
                        t_split, t_skip, q_limbs, c->L, centered ? 1 : 0, c->d_mods);
   }
+  LAUNCH_CHECK();
+}
+
+// ===========================================================================
+// N = 2^16: fast base conversion between the two halves of the NTTs,
+// resident in registers (the ModUp of one digit, and the ModDown of the
+// special limbs).  Block (64 columns, item): wave w holds columns
+// 64 blockIdx.x + 16 w + col of the 16 x 4096 array; lane (g, col) takes,
+// for each source quad i, source s = 4 i + g:
+//   1. the inverse high pass (bits 12..15) of its 16-word column, read from
+//      what the inverse low pass left (raw double bits / lazy words), x N^-1;
+//   2. v_s = [x Qhat_s^-1]_(q_s) (centered for the ModDown) as 8 balanced
+//      bytes, the data operand of k_basis_convert_mfma for coefficient
+//      (row r, column col): the MFMA's 16 coefficients are the wave's 16
+//      columns of one row;
+//   3. per target group and row, the int8 MFMAs and the exact fp64 fold of
+//      k_basis_convert_mfma, so lane (g, col) holds targets 16 tg + 4 g + e
+//      of its column at all 16 rows: their canonical residues;
+//   4. the forward high pass (bits 15..12) of each of those columns, stored
+//      as the low pass expects it (raw double bits / lazy words).
+// The converted limbs never exist in coefficient form in HBM: the kernel
+// reads each source word and writes each target word once.  The same words
+// as the inverse high pass, k_basis_convert_mfma and the forward high pass
+// in a row (the same exact integers, canonical in between).
+// ===========================================================================
+struct H4Tabs {
+  const u64 *psi, *psi_sh, *ipsi, *ipsi_sh, *ninv;
+  const double2 *tw, *itw, *ninv_fp;
+};
+
+template <int NK>
+__global__ __launch_bounds__(TPB, 2) void k_convert_h4(
+    Batch src, Batch dst, int ns, int nd, const u64 *__restrict__ tab,
+    const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
+    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods, H4Tabs nt) {
+  extern __shared__ u64 tb[];
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
+  const int cc = blockIdx.x * 64 + wave * 16 + col;
+  const u64 *in = batch_ptr(src, blockIdx.y) + cc;
+  u64 *out = batch_ptr(dst, blockIdx.y) + cc;
+  // the table and per-target constants (k_basis_convert_mfma's words, and
+  // the target's prime index at word 9)
+  const int words = NK * n_tg * 512;
+  for (int idx = threadIdx.x; idx < words; idx += TPB) tb[idx] = mtab[idx];
+  u64 *tgt = tb + words;
+  for (int t = threadIdx.x; t < nd; t += TPB) {
+    const int tl = t < t_split ? t : t + t_skip;
+    const int pt = prime_of(tl, q_limbs, L);
+    const ModQ M = mods[pt];
+    u64 *w = tgt + (size_t)t * kBcTgtWords;
+    w[0] = M.q;
+    w[1] = M.qinv;
+    w[2] = M.r2;
+    w[3] = M.mu;
+    w[4] = (u64)M.k | ((u64)M.pad << 32);
+    const double q = (double)M.q, qinv = 1.0 / q;
+    w[5] = dbl_bits(qinv);
+    w[6] = (u64)tl;
+    w[7] = dbl_bits(4294967296.0 * qinv);
+    w[8] = dbl_bits(q);
+    w[9] = (u64)pt;
+  }
+  // 1-2: the sources of this lane group
+  long a[NK][16];
+#pragma unroll
+  for (int i = 0; i < NK; i++) {
+    const int s = 4 * i + g;
+    if (s < ns) {
+      const int p = src_prime0 + s;
+      const u64 qu = mods[p].q;
+      const u64 *ps = in + ((size_t)s << 16);
+      u64 x[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) x[r] = ps[4096 * r];
+      if (qu < kFpPrimeBound) {
+        const double q = (double)qu;
+        double xd[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) xd[r] = as_dbl(x[r]);
+        fp_high_inv(xd, nt.itw + ((size_t)p << 16), nt.ninv_fp[p], q, 1.0 / q);
+#pragma unroll
+        for (int r = 0; r < 16; r++) x[r] = dbl_to_u52(xd[r]);
+      } else {
+        u64_high_inv(x, nt.ipsi + ((size_t)p << 16), nt.ipsi_sh + ((size_t)p << 16),
+                     nt.ninv[2 * p], nt.ninv[2 * p + 1], qu, 2 * qu);
+      }
+      const u64 sw = tab[s], sws = tab[ns + s];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        u64 v = shoup_mul(x[r], sw, sws, qu);
+        if (centered && v > (qu - 1) / 2) v -= qu;  // two's complement of v - q
+        a[i][r] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) a[i][r] = 0;
+    }
+  }
+  __syncthreads();
+  const int quad = n_tg * 512;
+  for (int tg = 0; tg < n_tg; tg++) {
+    const bool wide = (wide_mask >> tg) & 1;
+    const u64 *mt = tb + tg * 512 + lane;
+    // 3: residues of targets 16 tg + 4 g + e at rows 0..15 (double bits for
+    // targets below 2^45, words otherwise)
+    u64 y[4][16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      double lo[4], hi[4];
+#pragma unroll
+      for (int pr = 0; pr < 4; pr++) {
+        if (pr >= 3 && !wide) continue;  // digits 6, 7 of a narrow table are 0
+        v4i c0 = v4i{0, 0, 0, 0}, c1 = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+          const long b0 = (long)mt[i * quad + (2 * pr) * 64];
+          const long b1 = (long)mt[i * quad + (2 * pr + 1) * 64];
+          c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b0, a[i][r], c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, a[i][r], c1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const double d = (double)(c0[e] + 256 * c1[e]);
+          if (pr == 0) lo[e] = d;
+          else if (pr == 1) lo[e] = __fma_rn(d, 65536.0, lo[e]);
+          else if (pr == 2) hi[e] = d;
+          else hi[e] = __fma_rn(d, 65536.0, hi[e]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = 16 * tg + 4 * g + e;
+        if (t >= nd) continue;
+        const u64 *w = tgt + (size_t)t * kBcTgtWords;
+        if (w[0] < kFpPrimeBound) {
+          const double q = as_dbl(w[8]), qinv = as_dbl(w[5]), w32q = as_dbl(w[7]);
+          const double tq = fp_rint(__dmul_rn(hi[e], w32q));
+          const double yv = __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[e], 4294967296.0)), lo[e]);
+          y[e][r] = dbl_bits(fp_canon_d(yv, qinv, q));
+        } else {
+          ModQ M;
+          M.q = w[0];
+          M.qinv = w[1];
+          M.r2 = w[2];
+          M.mu = w[3];
+          M.k = (u32)w[4];
+          M.pad = (u32)(w[4] >> 32);
+          const long long hv = dbl_to_i51(hi[e]), lv = dbl_to_i51(lo[e]);
+          const u64 h = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
+          const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
+          y[e][r] = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
+        }
+      }
+    }
+    // 4: forward high pass of each target column, stored for the low pass
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int t = 16 * tg + 4 * g + e;
+      if (t >= nd) continue;
+      const u64 *w = tgt + (size_t)t * kBcTgtWords;
+      const int pt = (int)w[9];
+      u64 *po = out + ((size_t)w[6] << 16);
+      if (w[0] < kFpPrimeBound) {
+        double xd[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) xd[r] = as_dbl(y[e][r]);
+        fp_high_fwd(xd, nt.tw + ((size_t)pt << 16), as_dbl(w[8]));
+#pragma unroll
+        for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
+      } else {
+        const u64 qu = w[0];
+        u64_high_fwd(y[e], nt.psi + ((size_t)pt << 16), nt.psi_sh + ((size_t)pt << 16), qu,
+                     2 * qu);
+#pragma unroll
+        for (int r = 0; r < 16; r++) po[4096 * r] = y[e][r];
+      }
+    }
+  }
+}
+
+bool convert_h4_ok(const ckks_context *c, const BCTable &t) {
+  return c->logN == 16 && c->bc_mfma && t.mf && t.n_k >= 1 && t.n_k <= 3 && t.n_tg <= 4 &&
+         t.nd <= 64;
+}
+
+void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                       const BCTable &t, int src_prime0, int t_split, int t_skip, int q_limbs,
+                       bool centered) {
+  KTimer kt(c, "convert_h4", 8.0 * c->N * n_items * (t.ns + t.nd),
+            (double)c->N * n_items * t.ns * t.nd);
+  if (!convert_h4_ok(c, t)) throw std::invalid_argument("tile-resident conversion: shape");
+  if (n_items <= 0) return;
+  auto kern = t.n_k == 1 ? k_convert_h4<1> : t.n_k == 2 ? k_convert_h4<2> : k_convert_h4<3>;
+  const size_t lds = sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWords);
+  H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
+            (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
+            (const double2 *)c->d_ninv_fp};
+  hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
+                     t.d, t.mf, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
+                     centered ? 1 : 0, c->d_mods, nt);
+  LAUNCH_CHECK();
+}
+
+// Only the low pass of the inverse NTT (bit positions 0..11), for limbs
+// whose high pass runs inside launch_convert_h4.  N = 2^16 only.
+void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                        int l_begin, int l_count, int q_limbs) {
+  KTimer kt(c, "ntt_inv", 16.0 * c->N * n_items * l_count, 0.5 * c->N * 12 * n_items * l_count);
+  if (n_items <= 0 || l_count <= 0) return;
+  if (c->logN != 16) throw std::invalid_argument("inverse low pass alone: N = 2^16 only");
+  hipLaunchKernelGGL(k_ntt16m_inv_low, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream, src,
+                     dst, l_begin, q_limbs, c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh,
+                     (const double2 *)c->d_itw_fp);
   LAUNCH_CHECK();
 }
 
