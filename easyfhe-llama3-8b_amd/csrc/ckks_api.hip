@@ -338,6 +338,32 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
   t.mbytes = sizeof(u64) * m.size();
   HIPCHECK(hipMalloc(&t.mf, t.mbytes));
   HIPCHECK(hipMemcpy(t.mf, m.data(), t.mbytes, hipMemcpyHostToDevice));
+  // k_convert_h4's table: lane m of a group's words moves to the row of its
+  // target in the transposed order (m = 4 (t % 4) + (t % 16) / 4 for t's
+  // place in the group)
+  std::vector<u64> mt(m.size(), 0);
+  for (size_t blk = 0; blk < m.size() / 64; blk++)
+    for (int gs = 0; gs < 4; gs++)
+      for (int tm = 0; tm < 16; tm++) {
+        const int row = 4 * (tm % 4) + tm / 4;
+        mt[blk * 64 + row + 16 * gs] = m[blk * 64 + tm + 16 * gs];
+      }
+  HIPCHECK(hipMalloc(&t.mt, t.mbytes));
+  HIPCHECK(hipMemcpy(t.mt, mt.data(), t.mbytes, hipMemcpyHostToDevice));
+  std::vector<u64> sn(4 * (size_t)ns);
+  const int N = c->N;
+  for (int i = 0; i < ns; i++) {
+    const u64 qi = src[i];
+    const u64 w = mulmod_h(h[i], invmod_h((u64)N % qi, qi), qi);
+    sn[i] = w;
+    sn[ns + i] = shoup_h(w, qi);
+    const double wf = (double)w, qf = (double)qi;
+    const double wq = wf / qf;
+    memcpy(&sn[2 * ns + 2 * i], &wf, 8);
+    memcpy(&sn[2 * ns + 2 * i + 1], &wq, 8);
+  }
+  HIPCHECK(hipMalloc(&t.sn, sizeof(u64) * sn.size()));
+  HIPCHECK(hipMemcpy(t.sn, sn.data(), sizeof(u64) * sn.size(), hipMemcpyHostToDevice));
   return t;
 }
 
@@ -767,11 +793,15 @@ static void free_context(ckks_context *c) {
     (void)hipFree(kv.second.d);
     if (kv.second.fd) (void)hipFree(kv.second.fd);
     if (kv.second.mf) (void)hipFree(kv.second.mf);
+    if (kv.second.mt) (void)hipFree(kv.second.mt);
+    if (kv.second.sn) (void)hipFree(kv.second.sn);
   }
   for (auto &kv : c->bc_down) {
     (void)hipFree(kv.second.d);
     if (kv.second.fd) (void)hipFree(kv.second.fd);
     if (kv.second.mf) (void)hipFree(kv.second.mf);
+    if (kv.second.mt) (void)hipFree(kv.second.mt);
+    if (kv.second.sn) (void)hipFree(kv.second.sn);
   }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
   for (auto &kv : c->relin_rs) (void)hipFree(kv.second);

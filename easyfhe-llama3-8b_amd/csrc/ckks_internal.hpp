@@ -207,6 +207,14 @@ struct BCTable {  // fast basis conversion constants, device resident
   u64 *mf = nullptr;
   size_t mbytes = 0;
   int n_k = 0, n_tg = 0, wide_mask = 0;
+  // k_convert_h4's operands: the MFMA table with the targets of each group
+  // in the order row m <- target 16 tg + 4 (m % 4) + m / 4 (so that lane
+  // group g holds targets 4 e + g: a group's first targets fill every lane
+  // group), [n_k][n_tg][8][64] words; and per source [N^-1 hinv]_(q_s) as
+  // [ns] words, [ns] Shoup constants, [ns] (w, w / q_s) doubles (the inverse
+  // high pass leaves its x N^-1 to this product)
+  u64 *mt = nullptr;
+  u64 *sn = nullptr;
 };
 
 struct FFTTable {  // encoder tables for one slot count n

@@ -374,10 +374,9 @@ __device__ __forceinline__ void u64_high_fwd(u64 (&x)[16], const u64 *__restrict
   }
 }
 
-// inverse high pass on one column (lazy input), then x N^-1 to [0, q)
-__device__ __forceinline__ void u64_high_inv(u64 (&x)[16], const u64 *__restrict__ W,
-                                             const u64 *__restrict__ Ws, u64 ni, u64 nis,
-                                             u64 q, u64 q2) {
+// inverse high pass on one column (lazy input, lazy output in [0, 2q))
+__device__ __forceinline__ void u64_high_inv_stages(u64 (&x)[16], const u64 *__restrict__ W,
+                                                    const u64 *__restrict__ Ws, u64 q, u64 q2) {
 #pragma unroll
   for (int st = 3; st >= 0; st--) {
     const int half = 8 >> st;
@@ -388,6 +387,13 @@ __device__ __forceinline__ void u64_high_inv(u64 (&x)[16], const u64 *__restrict
       gs_bfly(x[k], x[k + half], W[ti], Ws[ti], q, q2);
     }
   }
+}
+
+// the inverse high pass, then x N^-1 to [0, q)
+__device__ __forceinline__ void u64_high_inv(u64 (&x)[16], const u64 *__restrict__ W,
+                                             const u64 *__restrict__ Ws, u64 ni, u64 nis,
+                                             u64 q, u64 q2) {
+  u64_high_inv_stages(x, W, Ws, q, q2);
 #pragma unroll
   for (int k = 0; k < 16; k++) {
     const u64 v = shoup_lazy(x[k], ni, nis, q);
@@ -690,10 +696,10 @@ __device__ __forceinline__ void fp_high_fwd(double (&x)[16], const double2 *__re
   }
 }
 
-// inverse high pass on one column (|x| < 2^50 on entry: reduced first),
-// then x N^-1; result as exact doubles in [0, q)
-__device__ __forceinline__ void fp_high_inv(double (&x)[16], const double2 *__restrict__ T,
-                                            double2 ni, double q, double qinv) {
+// inverse high pass on one column (|x| < 2^50 on entry: reduced first);
+// |x| <= 8 q + 8 after
+__device__ __forceinline__ void fp_high_inv_stages(double (&x)[16], const double2 *__restrict__ T,
+                                                   double q, double qinv) {
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = fp_reduce(x[k], qinv, q);
 #pragma unroll
@@ -706,6 +712,12 @@ __device__ __forceinline__ void fp_high_inv(double (&x)[16], const double2 *__re
       gs_fp(x[k], x[k + half], w.x, w.y, q);
     }
   }
+}
+
+// the inverse high pass, then x N^-1; result as exact doubles in [0, q)
+__device__ __forceinline__ void fp_high_inv(double (&x)[16], const double2 *__restrict__ T,
+                                            double2 ni, double q, double qinv) {
+  fp_high_inv_stages(x, T, q, qinv);
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = fp_canon_d(fp_mulmod(x[k], ni.x, ni.y, q), qinv, q);
 }
@@ -1223,6 +1235,7 @@ __device__ __forceinline__ void low_key_store_inv(double *__restrict__ sm, F wor
 // Per digit: the low pass leaves each thread the 16 consecutive positions
 // s = sb + i of round B, where the key product runs; the own limb and the
 // key words are read at those positions.
+template <bool SPINV>
 __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKeyArgs &a, int it,
                                            int tile, int l, int p, const ModQ *__restrict__ mods,
                                            const double2 *__restrict__ tw,
@@ -1284,7 +1297,7 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
   };
   auto canon = [&](double x) { return dbl_to_u52(canon_d(x)); };
   const u32 tb = a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u;
-  if (a.sp && l >= a.q_limbs) {
+  if constexpr (SPINV) {
     const double2 *Ti = a.itw + ((size_t)p << 16);
     u64 *o = a.sp + 2 * (size_t)it * a.sp_stride + ((size_t)(l - a.q_limbs) << 16);
     low_key_store_inv(sm, [&](int i) { return canon_d(acc0[i]); }, sb, a.ginv, Ti, q, qinv, o, tb);
@@ -1360,7 +1373,11 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
 // n_items x 16 x nl blocks, decoded so that the n_items blocks of one
 // (tile, limb) share b % 8, i.e. run on one XCD (blocks go to the 8 XCDs
 // round robin) and read the tile's key words into one L2.
-template <bool FP>
+// SPINV (fp64 bodies of special limbs with a.sp): the inverse low pass of
+// the two accumulator components into a.sp instead of the stores to acc; a
+// kernel of its own, so that the Q limbs' blocks keep the smaller register
+// allocation of the plain body.
+template <bool FP, bool SPINV = false>
 __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_begin,
                                                                    int n_items,
                                                                    const ModQ *__restrict__ mods,
@@ -1374,7 +1391,7 @@ __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_be
   const int tile = tl & 15, l = l_begin + (tl >> 4);
   const int p = prime_of(l, a.q_limbs, a.L);
   if constexpr (FP)
-    low_key_fp(reinterpret_cast<double *>(lds), a, it, tile, l, p, mods, tw, rinv);
+    low_key_fp<SPINV>(reinterpret_cast<double *>(lds), a, it, tile, l, p, mods, tw, rinv);
   else
     low_key_64(lds, a, it, tile, l, p, mods, psi, psi_sh);
 }
@@ -1417,13 +1434,17 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
   }
   // runs of limbs whose primes take the same body (q_0 and wide special
   // primes the 64-bit one)
+  // (with sp, the special limbs (all fp64) form a run of their own)
   auto fp_limb = [&](int l) { return c->prime_fp[l < q_limbs ? l : c->L + (l - q_limbs)] != 0; };
+  auto kind = [&](int l) { return fp_limb(l) ? (sp && l >= q_limbs ? 2 : 1) : 0; };
   for (int l0 = 0; l0 < E;) {
-    const bool fp = fp_limb(l0);
+    const int k = kind(l0);
     int l1 = l0 + 1;
-    while (l1 < E && fp_limb(l1) == fp) l1++;
-    hipLaunchKernelGGL(fp ? k_ntt16_low_key<true> : k_ntt16_low_key<false>,
-                       dim3(n_items * 16 * (l1 - l0)), dim3(TPB), 0, c->stream, a, l0, n_items,
+    while (l1 < E && kind(l1) == k) l1++;
+    auto kern = k == 2 ? k_ntt16_low_key<true, true>
+                : k == 1 ? k_ntt16_low_key<true, false>
+                         : k_ntt16_low_key<false, false>;
+    hipLaunchKernelGGL(kern, dim3(n_items * 16 * (l1 - l0)), dim3(TPB), 0, c->stream, a, l0, n_items,
                        c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp,
                        (const double2 *)c->d_rinv_fp);
     LAUNCH_CHECK();
@@ -2101,14 +2122,16 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
 // 64 blockIdx.x + 16 w + col of the 16 x 4096 array; lane (g, col) takes,
 // for each source quad i, source s = 4 i + g:
 //   1. the inverse high pass (bits 12..15) of its 16-word column, read from
-//      what the inverse low pass left (raw double bits / lazy words), x N^-1;
-//   2. v_s = [x Qhat_s^-1]_(q_s) (centered for the ModDown) as 8 balanced
-//      bytes, the data operand of k_basis_convert_mfma for coefficient
-//      (row r, column col): the MFMA's 16 coefficients are the wave's 16
-//      columns of one row;
+//      what the inverse low pass left (raw double bits / lazy words);
+//   2. v_s = [x N^-1 Qhat_s^-1]_(q_s) (centered for the ModDown) as 8
+//      balanced bytes, the data operand of k_basis_convert_mfma for
+//      coefficient (row r, column col): the MFMA's 16 coefficients are the
+//      wave's 16 columns of one row;
 //   3. per target group and row, the int8 MFMAs and the exact fp64 fold of
-//      k_basis_convert_mfma, so lane (g, col) holds targets 16 tg + 4 g + e
-//      of its column at all 16 rows: their canonical residues;
+//      k_basis_convert_mfma; the table (BCTable::mt) orders each group's
+//      targets so that lane (g, col) holds targets 16 tg + 4 e + g of its
+//      column at all 16 rows, and a group's rows e past its last target are
+//      skipped by the whole wave;
 //   4. the forward high pass (bits 15..12) of each of those columns, stored
 //      as the low pass expects it (raw double bits / lazy words).
 // The converted limbs never exist in coefficient form in HBM: the kernel
@@ -2165,22 +2188,28 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
       u64 x[16];
 #pragma unroll
       for (int r = 0; r < 16; r++) x[r] = ps[4096 * r];
+      // v = x [N^-1 hinv]_q: the inverse pass's x N^-1 folded into the
+      // conversion's first product
       if (qu < kFpPrimeBound) {
-        const double q = (double)qu;
+        const double q = (double)qu, qinv = 1.0 / q;
+        const double2 wn = reinterpret_cast<const double2 *>(tab + 2 * ns)[s];
         double xd[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) xd[r] = as_dbl(x[r]);
-        fp_high_inv(xd, nt.itw + ((size_t)p << 16), nt.ninv_fp[p], q, 1.0 / q);
+        fp_high_inv_stages(xd, nt.itw + ((size_t)p << 16), q, qinv);
 #pragma unroll
-        for (int r = 0; r < 16; r++) x[r] = dbl_to_u52(xd[r]);
+        for (int r = 0; r < 16; r++)
+          x[r] = dbl_to_u52(fp_canon_d(fp_mulmod(xd[r], wn.x, wn.y, q), qinv, q));
       } else {
-        u64_high_inv(x, nt.ipsi + ((size_t)p << 16), nt.ipsi_sh + ((size_t)p << 16),
-                     nt.ninv[2 * p], nt.ninv[2 * p + 1], qu, 2 * qu);
+        u64_high_inv_stages(x, nt.ipsi + ((size_t)p << 16), nt.ipsi_sh + ((size_t)p << 16), qu,
+                            2 * qu);
+        const u64 sw = tab[s], sws = tab[ns + s];
+#pragma unroll
+        for (int r = 0; r < 16; r++) x[r] = shoup_mul(x[r], sw, sws, qu);
       }
-      const u64 sw = tab[s], sws = tab[ns + s];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        u64 v = shoup_mul(x[r], sw, sws, qu);
+        u64 v = x[r];
         if (centered && v > (qu - 1) / 2) v -= qu;  // two's complement of v - q
         a[i][r] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
       }
@@ -2194,8 +2223,8 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
   for (int tg = 0; tg < n_tg; tg++) {
     const bool wide = (wide_mask >> tg) & 1;
     const u64 *mt = tb + tg * 512 + lane;
-    // 3: residues of targets 16 tg + 4 g + e at rows 0..15 (double bits for
-    // targets below 2^45, words otherwise)
+    // 3: values of targets 16 tg + 4 e + g at rows 0..15 (for targets below
+    // 2^45 exact doubles congruent to the residue, as bits; words otherwise)
     u64 y[4][16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -2213,6 +2242,7 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
         }
 #pragma unroll
         for (int e = 0; e < 4; e++) {
+          if (16 * tg + 4 * e >= nd) continue;  // no lane group holds a target
           const double d = (double)(c0[e] + 256 * c1[e]);
           if (pr == 0) lo[e] = d;
           else if (pr == 1) lo[e] = __fma_rn(d, 65536.0, lo[e]);
@@ -2222,14 +2252,16 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
       }
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const int t = 16 * tg + 4 * g + e;
-        if (t >= nd) continue;
+        const int t = 16 * tg + 4 * e + g;
+        if (16 * tg + 4 * e >= nd || t >= nd) continue;
         const u64 *w = tgt + (size_t)t * kBcTgtWords;
         if (w[0] < kFpPrimeBound) {
-          const double q = as_dbl(w[8]), qinv = as_dbl(w[5]), w32q = as_dbl(w[7]);
+          // |y| < q / 2 + 2^45.1 < 2^46: the forward passes take it as it is
+          // (|x| grows by at most q per stage, 16 stages, below 2^50)
+          const double q = as_dbl(w[8]), w32q = as_dbl(w[7]);
           const double tq = fp_rint(__dmul_rn(hi[e], w32q));
           const double yv = __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[e], 4294967296.0)), lo[e]);
-          y[e][r] = dbl_bits(fp_canon_d(yv, qinv, q));
+          y[e][r] = dbl_bits(yv);
         } else {
           ModQ M;
           M.q = w[0];
@@ -2248,8 +2280,8 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     // 4: forward high pass of each target column, stored for the low pass
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int t = 16 * tg + 4 * g + e;
-      if (t >= nd) continue;
+      const int t = 16 * tg + 4 * e + g;
+      if (16 * tg + 4 * e >= nd || t >= nd) continue;
       const u64 *w = tgt + (size_t)t * kBcTgtWords;
       const int pt = (int)w[9];
       u64 *po = out + ((size_t)w[6] << 16);
@@ -2272,8 +2304,8 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 }
 
 bool convert_h4_ok(const ckks_context *c, const BCTable &t) {
-  return c->logN == 16 && c->bc_mfma && t.mf && t.n_k >= 1 && t.n_k <= 3 && t.n_tg <= 4 &&
-         t.nd <= 64;
+  return c->logN == 16 && c->bc_mfma && t.mt && t.sn && t.n_k >= 1 && t.n_k <= 3 &&
+         t.n_tg <= 4 && t.nd <= 64;
 }
 
 void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
@@ -2289,7 +2321,7 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
   hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
-                     t.d, t.mf, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
+                     t.sn, t.mt, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
                      centered ? 1 : 0, c->d_mods, nt);
   LAUNCH_CHECK();
 }
