@@ -391,6 +391,24 @@ static const BCTable &bc_down(ckks_context *c, int limbs) {
   return c->bc_down[limbs] = make_bc(c, src, dst);
 }
 
+// per Q limb i < limbs: P mod q_i and its Shoup constant
+static const u64 *pmod_table(ckks_context *c, int limbs) {
+  auto it = c->pmod.find(limbs);
+  if (it != c->pmod.end()) return it->second;
+  std::vector<u64> h(2 * (size_t)limbs);
+  for (int i = 0; i < limbs; i++) {
+    const u64 q = c->primes[i];
+    u64 P = 1;
+    for (int j = 0; j < c->alpha; j++) P = mulmod_h(P, c->primes[c->L + j] % q, q);
+    h[2 * i] = P;
+    h[2 * i + 1] = shoup_h(P, q);
+  }
+  u64 *d = nullptr;
+  HIPCHECK(hipMalloc(&d, sizeof(u64) * h.size()));
+  HIPCHECK(hipMemcpy(d, h.data(), sizeof(u64) * h.size(), hipMemcpyHostToDevice));
+  return c->pmod[limbs] = d;
+}
+
 static const u64 *pinv_table(ckks_context *c, int limbs) {
   auto it = c->pinv.find(limbs);
   if (it != c->pinv.end()) return it->second;
@@ -804,6 +822,7 @@ static void free_context(ckks_context *c) {
     if (kv.second.sn) (void)hipFree(kv.second.sn);
   }
   for (auto &kv : c->pinv) (void)hipFree(kv.second);
+  for (auto &kv : c->pmod) (void)hipFree(kv.second);
   for (auto &kv : c->relin_rs) (void)hipFree(kv.second);
   for (auto &kv : c->rescale_d) (void)hipFree(kv.second);
   for (auto &kv : c->garner) (void)hipFree(kv.second);
@@ -1062,13 +1081,26 @@ struct KsJob {
   u64 *out0, *out1;
 };
 
+// The key product of the fp64 Q limbs left by ks_modup_inner for ks_moddown
+// (launch_low_key_moddown): the extended digits and what it multiplies them by.
+struct KsDeferred {
+  bool on = false;
+  const u64 *ext = nullptr;
+  size_t est = 0;
+  Batch own{};
+  const DeviceKey *key = nullptr;
+  int digits = 0;
+  u64 ginv = 1;
+};
+
 // ModDown of n accumulators acc = [n][2][E][N] (Q limbs then P limbs) into
 // the jobs' outputs, adding each job's addends (sigma-permuted): the P-part
 // iNTT, the centered conversion, then the forward NTT with the combine.
 // With ptmp given ([2 n][alpha][N]) and sp_done, ks_modup_inner's key
 // product left the P part there after the inverse NTT's low pass.
 static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<KsJob> &jobs,
-                       Scratch &s, u64 *ptmp = nullptr, bool sp_done = false) {
+                       Scratch &s, u64 *ptmp = nullptr, bool sp_done = false,
+                       const KsDeferred *dk = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha;
   const int n = (int)jobs.size();
@@ -1088,6 +1120,8 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
   // forward high pass of the Q limbs in one kernel, then the low pass with
   // the combine
   const bool tile = c->logN == 16 && uniform && c->ks_tile && convert_h4_ok(c, bc_down(c, limbs));
+  const bool deferred = dk && dk->on;
+  if (deferred && !(tile && sp_done)) throw std::logic_error("deferred key product without the tile ModDown");
   if (tile) {
     if (!sp_done) launch_ntt_inv_low(c, strided(acc, E * N), spb, 2 * n, limbs, c->alpha, limbs);
     launch_convert_h4(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
@@ -1110,10 +1144,16 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
       o0.p[i] = jobs[i].out0;
       gal[i] = jobs[i].galois;
     }
+    if (deferred)
+      launch_low_key_moddown(c, dk->ext, dk->est, dk->own, n, *dk->key, dk->digits, E, limbs,
+                             dk->ginv, strided(conv, (size_t)limbs * N), pinv,
+                             pmod_table(c, limbs), a0, add1_off, gal.data(), o0, out1_off);
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
-                       pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile);
+                       pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile,
+                       deferred);
     return;
   }
+  if (deferred) throw std::logic_error("deferred key product without the fused combine");
   launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), 2 * n, 0,
              limbs, limbs, false);
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
@@ -1180,9 +1220,15 @@ static u64 galois_inverse(const ckks_context *c, u64 g) {
 // the NTT's high pass and their low pass runs with the key product.  With sp
 // given, *sp_done tells whether the P part went through the inverse NTT's
 // low pass into sp (launch_ntt_low_key) instead of into the accumulators.
+// With dk given (the caller's jobs meet ks_moddown's fused combine: one
+// addend per component at a fixed offset, outputs likewise), where the
+// special limbs take the inverse low pass here and the ModDown's conversion
+// runs tile-resident, the fp64 Q limbs' key product is left to ks_moddown
+// (dk->on), which runs it with the combine.
 static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *d,
                            const std::vector<KsJob> &jobs, Scratch &s,
-                           const Strided *sp = nullptr, bool *sp_done = nullptr) {
+                           const Strided *sp = nullptr, bool *sp_done = nullptr,
+                           KsDeferred *dk = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   const size_t est = (size_t)digits * E * N;
@@ -1195,8 +1241,21 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
   u64 *acc = s.get((size_t)n * 2 * E * N);
   Batch ob{};
   for (int i = 0; i < n; i++) ob.p[i] = (u64 *)d[i];
+  const u64 ginv = galois_inverse(c, jobs[0].galois);
+  const bool defer = dk && spf && c->ks_defer && c->ks_tile && convert_h4_ok(c, bc_down(c, limbs));
+  if (dk) {
+    dk->on = defer;
+    if (defer) {
+      dk->ext = ext;
+      dk->est = est;
+      dk->own = ob;
+      dk->key = jobs[0].key;
+      dk->digits = digits;
+      dk->ginv = ginv;
+    }
+  }
   launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
-                     galois_inverse(c, jobs[0].galois), spf ? sp : nullptr);
+                     ginv, spf ? sp : nullptr, defer);
   return acc;
 }
 
@@ -1301,8 +1360,9 @@ static void rotate_batch(ckks_context *c, const ckks_ct *const *in, int n, u64 g
     u64 *ptmp = s.get((size_t)nb * 2 * c->alpha * N);
     const Strided sp{ptmp, (u64)c->alpha * N};
     bool sp_done = false;
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
-    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done);
+    KsDeferred dk;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done, &dk);
+    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done, &dk);
   };
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
     const int nb = std::min(kMaxBatch, n - b0);
@@ -1332,8 +1392,9 @@ static void relin_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_c
     u64 *ptmp = s.get((size_t)nb * 2 * c->alpha * N);
     const Strided sp{ptmp, (u64)c->alpha * N};
     bool sp_done = false;
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
-    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done);
+    KsDeferred dk;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done, &dk);
+    ks_moddown(c, limbs, acc, jobs, s, ptmp, sp_done, &dk);
   };
   for (int b0 = 0; b0 < n; b0 += kMaxBatch) run_parts(c, b0, std::min(kMaxBatch, n - b0), run);
 }
@@ -1525,6 +1586,8 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
     c->ks_sp_inv = !(si && strcmp(si, "0") == 0);
     const char *kt = getenv("CKKS_KS_TILE");
     c->ks_tile = !(kt && strcmp(kt, "0") == 0);
+    const char *kd = getenv("CKKS_KS_DEFER");
+    c->ks_defer = !(kd && strcmp(kd, "0") == 0);
     const char *ss = getenv("CKKS_SPLIT_STREAMS");
     if (ss) {
       c->split_parts = atoi(ss);

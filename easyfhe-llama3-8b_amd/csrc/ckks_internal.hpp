@@ -268,6 +268,7 @@ struct ckks_context {
   std::map<std::pair<int, int>, ckks::BCTable> bc_up;  // (limbs, digit)
   std::map<int, ckks::BCTable> bc_down;                // limbs
   std::map<int, u64 *> pinv;     // limbs -> [limbs][2] P^-1 mod q_i, shoup
+  std::map<int, u64 *> pmod;     // limbs -> [limbs][2] P mod q_i, shoup
   u64 *d_pmod = nullptr;         // [L][2] P mod q_i, shoup (extended-basis lifts)
   std::map<std::pair<int, int>, u64 *> relin_rs;  // (limbs, primes) -> relin-rescale constants
   std::map<std::pair<int, int>, u64 *> rescale_d;  // (limbs, primes) -> rescale constants
@@ -296,6 +297,12 @@ struct ckks_context {
   // int8-MFMA table allows; environment CKKS_KS_TILE=0 at creation keeps the
   // separate high passes and conversion
   bool ks_tile = true;
+  // with ks_tile and the special limbs' inverse low pass in the key product,
+  // rotations and relinearisations run the fp64 Q limbs' key product with
+  // the ModDown's combine in one kernel (launch_low_key_moddown), after the
+  // special limbs' conversion; environment CKKS_KS_DEFER=0 at creation keeps
+  // the accumulators in HBM between the two
+  bool ks_defer = true;
   // batched key switches of at least kSplitMin ciphertexts per part run as
   // `split_parts` parts, the first on the context stream and the others on
   // `aux` streams (forked from and joined back into the context stream), so
@@ -382,9 +389,24 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
 // sp.stride + (l - q_limbs) N, and are not written to acc: the ModDown then
 // runs launch_ntt_inv_high on them.
 bool low_key_special_fp(const ckks_context *c);
+// defer_fp_q: the Q limbs of fp64 primes are skipped (launch_low_key_moddown
+// runs their key product with the ModDown's combine)
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
-                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr);
+                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr,
+                        bool defer_fp_q = false);
+// N = 2^16: for the Q limbs of fp64 primes, launch_ntt_low_key's key product
+// and launch_ntt_moddown's combine (addends, outputs and postop as there) in
+// one kernel, the accumulator kept in the block; conv holds the ModDown's
+// conversion after the forward high pass (launch_convert_h4), 2 n items of
+// q_limbs limbs; pmod per Q limb [P]_q and its Shoup constant.  The special
+// limbs' key product and the other Q limbs run through
+// launch_ntt_low_key(defer_fp_q) and launch_ntt_moddown(wide_only).
+void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
+                            int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
+                            u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
+                            const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
+                            u64 out1_off, const PostOp *post = nullptr);
 // N = 2^16: the high pass of the inverse NTT alone, in place (after the low
 // pass of launch_ntt_low_key's sp output)
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
@@ -400,7 +422,7 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off,
                         const u64 *amul = nullptr, const PostOp *post = nullptr,
-                        bool high_done = false);
+                        bool high_done = false, bool wide_only = false);
 // N = 2^16: the inverse NTT's low pass alone (its high pass then runs in
 // launch_convert_h4 or launch_ntt_inv_high)
 void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,

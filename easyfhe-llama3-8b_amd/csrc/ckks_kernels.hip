@@ -1110,7 +1110,7 @@ void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_b
 void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, const Batch &acc,
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul,
-                        const PostOp *post, bool high_done) {
+                        const PostOp *post, bool high_done, bool wide_only) {
   KTimer kt(c, "ntt_fwd_moddown",
             8.0 * c->N * limbs * (6.0 * n + (batch_ptr_host(add, 0) ? (add1_off ? 2.0 : 1.0) * n : 0.0)),
             0.5 * c->N * c->logN * 2.0 * n * limbs);
@@ -1126,11 +1126,22 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
   md.out1_off = out1_off;
   if (post) md.post = *post;
   for (int i = 0; i < n; i++) md.gal.g[i] = galois[i];
-  dim3 block(TPB), grid(16, 2 * n, limbs);
   if (!high_done) launch_fwd_high16(c, conv, conv, 2 * n, 0, limbs, limbs);
-  hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, grid, block, 0, c->stream, conv, 0, limbs, c->L,
-                     c->d_mods, c->d_psi, c->d_psi_sh, (const double2 *)c->d_tw_fp, md);
-  LAUNCH_CHECK();
+  // runs of limbs (wide_only: the limbs of primes at or above 2^45 alone,
+  // the others being combined by launch_low_key_moddown)
+  for (int l0 = 0; l0 < limbs;) {
+    if (wide_only && c->prime_fp[l0]) {
+      l0++;
+      continue;
+    }
+    int l1 = l0 + 1;
+    while (l1 < limbs && !(wide_only && c->prime_fp[l1])) l1++;
+    hipLaunchKernelGGL(k_ntt16m_fwd_low<true>, dim3(16, 2 * n, l1 - l0), dim3(TPB), 0, c->stream,
+                       conv, l0, limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh,
+                       (const double2 *)c->d_tw_fp, md);
+    LAUNCH_CHECK();
+    l0 = l1;
+  }
 }
 
 // Only the high pass of the forward NTT (bit positions 15..12), for limbs
@@ -1235,11 +1246,15 @@ __device__ __forceinline__ void low_key_store_inv(double *__restrict__ sm, F wor
 // Per digit: the low pass leaves each thread the 16 consecutive positions
 // s = sb + i of round B, where the key product runs; the own limb and the
 // key words are read at those positions.
-template <bool SPINV>
-__device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKeyArgs &a, int it,
-                                           int tile, int l, int p, const ModQ *__restrict__ mods,
-                                           const double2 *__restrict__ tw,
-                                           const double2 *__restrict__ rinv) {
+// The key product of one (item, tile, limb) on an fp64 prime: per digit the
+// low pass leaves each thread the 16 consecutive positions s = sb + i of
+// round B, where the key product runs; the own limb and the key words are
+// read at those positions.  acc0 / acc1 leave unreduced (|acc| <= digits q).
+__device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const LowKeyArgs &a,
+                                               int it, int tile, int l, int p,
+                                               const ModQ *__restrict__ mods,
+                                               const double2 *__restrict__ tw,
+                                               double (&acc0)[16], double (&acc1)[16]) {
   const double q = (double)mods[p].q, qinv = 1.0 / q;
   const double2 *T = tw + ((size_t)p << 16);
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
@@ -1247,7 +1262,6 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
   const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
   const u32 kslot = key_slot(sb);
   const int jo = l < a.q_limbs ? l / a.ds : -1;
-  double acc0[16], acc1[16];
   for (int j = 0; j < a.digits; j++) {
     double y[16];
     if (j == jo) {
@@ -1289,6 +1303,18 @@ __device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKey
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <bool SPINV>
+__device__ __forceinline__ void low_key_fp(double *__restrict__ sm, const LowKeyArgs &a, int it,
+                                           int tile, int l, int p, const ModQ *__restrict__ mods,
+                                           const double2 *__restrict__ tw,
+                                           const double2 *__restrict__ rinv) {
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  double acc0[16], acc1[16];
+  low_key_fp_acc(sm, a, it, tile, l, p, mods, tw, acc0, acc1);
   // x 2^-64 (the keys' Montgomery factor), then canonical
   const double2 ri = rinv[p];
   auto canon_d = [&](double x) {
@@ -1396,19 +1422,129 @@ __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_be
     low_key_64(lds, a, it, tile, l, p, mods, psi, psi_sh);
 }
 
+// ===========================================================================
+// N = 2^16, fp64 Q limbs: the key product of one (item, tile, limb) and the
+// ModDown's combine of the output tile it maps to, with the accumulator kept
+// in the block.  After the key product (low_key_fp_acc) each component's
+// words, x 2^-64 and canonical, go through the LDS tile to their output
+// positions t = autom_index(s, g^-1) (an aligned tile onto an aligned tile),
+// so that thread (rl, c0) holds output words tb + rl 256 + c0 + 16 k.  Then,
+// per component, the forward low pass of the converted special part (conv:
+// launch_convert_h4's output for this limb and output tile) and
+//   out = (acc - NTT(conv)) P^-1 + addend (+ postop),
+// the words of launch_ntt_low_key then launch_ntt_moddown.  The special
+// limbs' key product (and their inverse low pass) and the ModDown's
+// conversion run before it.
+// ===========================================================================
+__global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine md, Batch conv,
+                                                       const u64 *__restrict__ pmod,
+                                                       int l_begin, int n_items,
+                                                       const ModQ *__restrict__ mods,
+                                                       const double2 *__restrict__ tw,
+                                                       const double2 *__restrict__ rinv) {
+  // tile 0: the working tile; tile 1: component 1's accumulator words in
+  // their output order until its combine
+  __shared__ u64 lds[2 * 16 * 272];
+  double *sm = reinterpret_cast<double *>(lds);
+  u64 *smu = lds, *acc1t = lds + 16 * 272;
+  const int b = blockIdx.x, r0 = b >> 3;
+  const int it = r0 % n_items, tl = (r0 / n_items) * 8 + (b & 7);
+  const int tile = tl & 15, l = l_begin + (tl >> 4);
+  const int p = prime_of(l, a.q_limbs, a.L);
+  const u64 qu = mods[p].q;
+  const double q = (double)qu, qinv = 1.0 / q;
+  const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
+  double acc0[16], acc1[16];
+  low_key_fp_acc(sm, a, it, tile, l, p, mods, tw, acc0, acc1);
+  const double2 ri = rinv[p];
+  auto canon = [&](double x) {
+    const double rr = fp_reduce(fp_mulmod(x, ri.x, ri.y, q), qinv, q);
+    return dbl_to_u52(rr < 0.0 ? __dadd_rn(rr, q) : rr);
+  };
+  // The addend of output t is the word at sigma(t) = s: the thread holds it
+  // at its own positions, so (acc - conv) P^-1 + add is taken as
+  // (acc + [P] add - conv) P^-1, with add read here in source order.
+  const u64 Pm = pmod[2 * l], Pms = pmod[2 * l + 1];
+  const u64 *ad0 = batch_ptr(md.add, it);
+  const u64 *ad1 = (ad0 && md.add1_off) ? ad0 + md.add1_off : nullptr;
+  u64 w0[16], w1[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    w0[i] = canon(acc0[i]);
+    w1[i] = canon(acc1[i]);
+  }
+  if (ad0) {
+    u64 d[16];
+    load16(ad0 + ((size_t)l << 16) + sb, d);
+#pragma unroll
+    for (int i = 0; i < 16; i++) w0[i] = add_mod(w0[i], shoup_mul(d[i], Pm, Pms, qu), qu);
+  }
+  if (ad1) {
+    u64 d[16];
+    load16(ad1 + ((size_t)l << 16) + sb, d);
+#pragma unroll
+    for (int i = 0; i < 16; i++) w1[i] = add_mod(w1[i], shoup_mul(d[i], Pm, Pms, qu), qu);
+  }
+  // sigma maps the block's tile onto one output tile: the same base for
+  // every thread (uniform, so the low pass's twiddles stay scalar loads)
+  const u32 tb = (u32)__builtin_amdgcn_readfirstlane(
+      (int)(a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u));
+  const int ot = (int)(tb >> 12);
+  __syncthreads();  // the key product's reads of the working tile are done
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const u32 t = a.ginv == 1 ? sb + i : autom_index(sb + i, a.ginv, 16);
+    smu[lds16((t >> 8) & 15, t & 255)] = w0[i];
+    acc1t[lds16((t >> 8) & 15, t & 255)] = w1[i];
+  }
+  __syncthreads();
+  u64 av[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) av[k] = smu[lds16(rl, c0 + 16 * k)];
+  const double2 *T = tw + ((size_t)p << 16);
+  const int row = ot * 16 + rl;
+  const u32 e0 = tb + rl * 256 + c0;
+  const u64 pinv = md.pinv[2 * l], pinvs = md.pinv[2 * l + 1];
+#pragma unroll 1
+  for (int comp = 0; comp < 2; comp++) {
+    // forward low pass of conv's output tile
+    const u64 *src = batch_ptr(conv, 2 * it + comp) + ((size_t)l << 16) + tb;
+    __syncthreads();  // earlier reads of the working tile are done
+    fp_round_z_to_lds(sm, src, T, ot, q);
+    __syncthreads();
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
+    fp_low_round_a(x, T, row, q);
+#pragma unroll
+    for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
+    fp_low_round_b(x, T, row, c0, q);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; j++) smu[lds16(rl, 16 * c0 + j)] = fp_canon(x[j], qinv, q);
+    __syncthreads();
+    u64 *o = batch_ptr(md.out, it) + (comp ? md.out1_off : 0) + ((size_t)l << 16);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const u64 acc = comp ? acc1t[lds16(rl, c0 + 16 * k)] : av[k];
+      o[e0 + 16 * k] = shoup_mul(sub_mod(acc, smu[lds16(rl, c0 + 16 * k)], qu), pinv, pinvs, qu);
+    }
+  }
+}
+
 bool low_key_special_fp(const ckks_context *c) {
   for (int j = 0; j < c->alpha; j++)
     if (!c->prime_fp[c->L + j]) return false;
   return true;
 }
 
-void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
-                        u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
-                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp) {
-  KTimer kt(c, "ntt_low_key",
-            8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
-            2.0 * c->N * E * digits * n_items);
-  if (n_items <= 0) return;
+static LowKeyArgs low_key_args(ckks_context *c, const u64 *ext, size_t ext_stride,
+                               const Batch &own, u64 *acc, size_t acc_stride,
+                               const DeviceKey &key, int digits, int E, int q_limbs, u64 ginv) {
   if (c->logN != 16) throw std::invalid_argument("fused low pass and key product: N = 2^16 only");
   if (digits < 1 || digits > key.digits || q_limbs > c->L || E != q_limbs + c->alpha)
     throw std::invalid_argument("fused low pass and key product: shape");
@@ -1426,6 +1562,56 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
   a.L = c->L;
   a.K = c->K;
   a.ds = c->ds;
+  return a;
+}
+
+void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
+                            int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
+                            u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
+                            const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
+                            u64 out1_off, const PostOp *post) {
+  KTimer kt(c, "ntt_low_key_moddown",
+            8.0 * c->N * ((double)n_items * (digits * q_limbs + 7.0 * q_limbs) +
+                          2.0 * digits * q_limbs),
+            2.0 * c->N * q_limbs * digits * n_items + 0.5 * c->N * 12 * 2.0 * n_items * q_limbs);
+  if (n_items <= 0) return;
+  if (post && (post->dbl || post->scal || batch_ptr_host(post->sub, 0)))
+    throw std::invalid_argument("fused key product + ModDown: no postop");
+  if (n_items > kMaxBatch) throw std::invalid_argument("fused key product + ModDown: n <= 64");
+  LowKeyArgs a = low_key_args(c, ext, ext_stride, own, nullptr, 0, key, digits, E, q_limbs, ginv);
+  MDCombine md{};
+  md.pinv = pinv;
+  md.add = add;
+  md.add1_off = add1_off;
+  md.out = out;
+  md.out1_off = out1_off;
+  if (post) md.post = *post;
+  for (int i = 0; i < n_items; i++) md.gal.g[i] = galois[i];
+  for (int l0 = 0; l0 < q_limbs;) {
+    if (!c->prime_fp[l0]) {
+      l0++;
+      continue;
+    }
+    int l1 = l0 + 1;
+    while (l1 < q_limbs && c->prime_fp[l1]) l1++;
+    hipLaunchKernelGGL(k_low_key_md, dim3(n_items * 16 * (l1 - l0)), dim3(TPB), 0, c->stream, a,
+                       md, conv, pmod, l0, n_items, c->d_mods, (const double2 *)c->d_tw_fp,
+                       (const double2 *)c->d_rinv_fp);
+    LAUNCH_CHECK();
+    l0 = l1;
+  }
+}
+
+void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
+                        u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
+                        int digits, int E, int q_limbs, u64 ginv, const Strided *sp,
+                        bool defer_fp_q) {
+  KTimer kt(c, "ntt_low_key",
+            8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
+            2.0 * c->N * E * digits * n_items);
+  if (n_items <= 0) return;
+  LowKeyArgs a = low_key_args(c, ext, ext_stride, own, acc, acc_stride, key, digits, E, q_limbs,
+                              ginv);
   if (sp) {
     if (!low_key_special_fp(c)) throw std::invalid_argument("fused special inverse: fp64 special primes only");
     a.sp = sp->base;
@@ -1441,6 +1627,11 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
     const int k = kind(l0);
     int l1 = l0 + 1;
     while (l1 < E && kind(l1) == k) l1++;
+    if (defer_fp_q && k == 1 && l0 < q_limbs) {
+      // fp64 Q limbs left to launch_low_key_moddown
+      l0 = l1;
+      continue;
+    }
     auto kern = k == 2 ? k_ntt16_low_key<true, true>
                 : k == 1 ? k_ntt16_low_key<true, false>
                          : k_ntt16_low_key<false, false>;
