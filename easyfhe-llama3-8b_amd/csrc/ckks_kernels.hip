@@ -2367,14 +2367,47 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     w[8] = dbl_bits(q);
     w[9] = (u64)pt;
   }
+  // the high passes' 15 twiddles of every target's prime (forward) and every
+  // source's prime (inverse), 32 words each: fp64 primes as 16 (w, w / q)
+  // pairs, others as [16] psi_br and [16] Shoup constants; entry 0 is unused
+  // and word 0 holds q.  Each lane group works on its own primes, so these
+  // would otherwise be per-lane global loads.
+  u64 *ttw = tgt + (size_t)nd * kBcTgtWords, *stw = ttw + (size_t)nd * 32;
+  for (int idx = threadIdx.x; idx < (nd + ns) * 16; idx += TPB) {
+    const int t = idx >> 4, j = idx & 15;
+    const bool src_side = t >= nd;
+    int pt;
+    if (src_side) {
+      pt = src_prime0 + (t - nd);
+    } else {
+      const int tl = t < t_split ? t : t + t_skip;
+      pt = prime_of(tl, q_limbs, L);
+    }
+    u64 *w = src_side ? stw + (size_t)(t - nd) * 32 : ttw + (size_t)t * 32;
+    const u64 qu = mods[pt].q;
+    if (j == 0) {
+      w[0] = qu;
+      continue;
+    }
+    const size_t o = ((size_t)pt << 16) + j;
+    if (qu < kFpPrimeBound) {
+      const double2 v = src_side ? nt.itw[o] : nt.tw[o];
+      w[2 * j] = dbl_bits(v.x);
+      w[2 * j + 1] = dbl_bits(v.y);
+    } else {
+      w[j] = src_side ? nt.ipsi[o] : nt.psi[o];
+      w[16 + j] = src_side ? nt.ipsi_sh[o] : nt.psi_sh[o];
+    }
+  }
+  __syncthreads();
   // 1-2: the sources of this lane group
   long a[NK][16];
 #pragma unroll
   for (int i = 0; i < NK; i++) {
     const int s = 4 * i + g;
     if (s < ns) {
-      const int p = src_prime0 + s;
-      const u64 qu = mods[p].q;
+      const u64 *sw0 = stw + (size_t)s * 32;
+      const u64 qu = sw0[0];
       const u64 *ps = in + ((size_t)s << 16);
       u64 x[16];
 #pragma unroll
@@ -2387,13 +2420,12 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
         double xd[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) xd[r] = as_dbl(x[r]);
-        fp_high_inv_stages(xd, nt.itw + ((size_t)p << 16), q, qinv);
+        fp_high_inv_stages(xd, reinterpret_cast<const double2 *>(sw0), q, qinv);
 #pragma unroll
         for (int r = 0; r < 16; r++)
           x[r] = dbl_to_u52(fp_canon_d(fp_mulmod(xd[r], wn.x, wn.y, q), qinv, q));
       } else {
-        u64_high_inv_stages(x, nt.ipsi + ((size_t)p << 16), nt.ipsi_sh + ((size_t)p << 16), qu,
-                            2 * qu);
+        u64_high_inv_stages(x, sw0, sw0 + 16, qu, 2 * qu);
         const u64 sw = tab[s], sws = tab[ns + s];
 #pragma unroll
         for (int r = 0; r < 16; r++) x[r] = shoup_mul(x[r], sw, sws, qu);
@@ -2474,19 +2506,18 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
       const int t = 16 * tg + 4 * e + g;
       if (16 * tg + 4 * e >= nd || t >= nd) continue;
       const u64 *w = tgt + (size_t)t * kBcTgtWords;
-      const int pt = (int)w[9];
+      const u64 *tw0 = ttw + (size_t)t * 32;
       u64 *po = out + ((size_t)w[6] << 16);
       if (w[0] < kFpPrimeBound) {
         double xd[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) xd[r] = as_dbl(y[e][r]);
-        fp_high_fwd(xd, nt.tw + ((size_t)pt << 16), as_dbl(w[8]));
+        fp_high_fwd(xd, reinterpret_cast<const double2 *>(tw0), as_dbl(w[8]));
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
       } else {
         const u64 qu = w[0];
-        u64_high_fwd(y[e], nt.psi + ((size_t)pt << 16), nt.psi_sh + ((size_t)pt << 16), qu,
-                     2 * qu);
+        u64_high_fwd(y[e], tw0, tw0 + 16, qu, 2 * qu);
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = y[e][r];
       }
@@ -2494,9 +2525,14 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
   }
 }
 
+static size_t convert_h4_lds(const BCTable &t) {
+  return sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWords +
+                        32 * (size_t)(t.nd + t.ns));
+}
+
 bool convert_h4_ok(const ckks_context *c, const BCTable &t) {
   return c->logN == 16 && c->bc_mfma && t.mt && t.sn && t.n_k >= 1 && t.n_k <= 3 &&
-         t.n_tg <= 4 && t.nd <= 64;
+         t.n_tg <= 4 && t.nd <= 64 && convert_h4_lds(t) <= 65536;
 }
 
 void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
@@ -2507,7 +2543,7 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
   if (!convert_h4_ok(c, t)) throw std::invalid_argument("tile-resident conversion: shape");
   if (n_items <= 0) return;
   auto kern = t.n_k == 1 ? k_convert_h4<1> : t.n_k == 2 ? k_convert_h4<2> : k_convert_h4<3>;
-  const size_t lds = sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWords);
+  const size_t lds = convert_h4_lds(t);
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
