@@ -181,12 +181,15 @@ def main() -> int:
                     help="skip the RMSNorm + MLP block measurement of the default run")
     ap.add_argument("--no-attention", action="store_true",
                     help="skip the attention measurement of the default run")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the 32-layer prefill on the reference's chain")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip the refreshed-layer measurement of the default run")
     ap.add_argument("--layers", type=int, default=None,
                     help="layers of the layers mode (default 2) and of the prefill mode "
                          "(default 32)")
     ap.add_argument("--mode", choices=["keyswitch", "ntt-profile", "ks-profile", "int-peak",
+                                       "prefill-reference-chain",
                                        "bootstrap", "linear", "mlp", "attention", "layer",
                                        "layers", "layers-reference-chain", "prefill"],
                     default="keyswitch",
@@ -205,7 +208,9 @@ def main() -> int:
                          "(60 + 37 x 59-bit primes, dnum 5) with the softmax normalisers "
                          "refreshed; "
                          "prefill: the encrypted prefill from token ids to logits (--layers, "
-                         "default 32)")
+                         "default 32); prefill-reference-chain: the same on the reference's "
+                         "chain and budget (4, 4) with its normaliser and slim RMSNorm "
+                         "refreshes")
     ap.add_argument("--boot-cts", type=int, default=32)
     ap.add_argument("--boot-group", type=int, default=16,
                     help="ciphertexts per batched bootstrap group")
@@ -219,7 +224,8 @@ def main() -> int:
               "the key-switch batches and the feature-major ciphertexts would be split by "
               "ciphertext, each GPU holding its own copy of the keys)", file=sys.stderr)
         return 2
-    if args.mode == "prefill":
+    if args.mode in ("prefill", "prefill-reference-chain") or (args.mode == "keyswitch"
+                                                               and not args.no_prefill):
         # The plaintext passes run on torch; its bundled HIP runtime must be
         # the process's only one, which holds when torch loads before the
         # backend library (the backend then binds to the runtime by soname).
@@ -252,6 +258,12 @@ def main() -> int:
     if args.mode == "prefill":
         n = 32 if args.layers is None else args.layers
         print(json.dumps({"fm_prefill": measure_fm_prefill(n)}), flush=True)
+        return 0
+    if args.mode == "prefill-reference-chain":
+        n = 32 if args.layers is None else args.layers
+        print(json.dumps({"fm_prefill_reference_chain": measure_fm_prefill(
+            n, params=REFERENCE_CHAIN_PARAMS, budget=REFERENCE_BUDGET, refresh_normalisers=True,
+            slim_rmsnorm=True)}), flush=True)
         return 0
     if args.mode == "layers":
         print(json.dumps({"fm_layers": measure_fm_layers(2 if args.layers is None
@@ -436,6 +448,12 @@ def main() -> int:
         # round's normaliser is refreshed as well
         result["fm_layers_reference_chain"] = measure_fm_layers(
             2, params=REFERENCE_CHAIN_PARAMS, budget=REFERENCE_BUDGET, refresh_normalisers=True,
+            slim_rmsnorm=True)
+    if not args.no_prefill:
+        # the 32-layer prefill on the reference's chain and
+        # budget, against its ~511 s A100 figure (README.md:9)
+        result["fm_prefill_reference_chain"] = measure_fm_prefill(
+            32, params=REFERENCE_CHAIN_PARAMS, budget=REFERENCE_BUDGET, refresh_normalisers=True,
             slim_rmsnorm=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
@@ -1075,10 +1093,14 @@ class _TorchLayer:
         return h1 + (act * (n2 @ w["up"].T)) @ w["down"].T, h1, g, sc
 
 
-def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -> dict:
+def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *, params=None,
+                       budget=(3, 3), refresh_normalisers: bool = False,
+                       slim_rmsnorm: bool = False) -> dict:
     """The full encrypted Llama-3-8B prefill over 128 tokens: random token
     ids (seed) embedded by the client, ``n_layers`` encrypted decoder layers
-    with their refreshes (bootstraps included) on REFRESH_PARAMS, every key
+    with their refreshes (bootstraps included) on REFRESH_PARAMS (or
+    ``params``, CtS/StC budget ``budget``, with the softmax normalisers' and
+    the slim RMSNorm's refreshes as measure_fm_layers takes them), every key
     and every layer's weights resident on the device, the final hidden state
     decrypted and the final token's logits computed in the clear (exact final
     RMSNorm and LM head).  Weights N(0, 0.02) (embedding, projections, LM
@@ -1091,14 +1113,18 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
 
     from easyfhe import fhe
     from feature_major import FeatureMajorPrefillLayout
+    from easyfhe.bs import openfhe as bs
     from feature_major.layer import (DecoderLayerWeights, decoder_layer_rotations,
-                                     refreshed_layer_depths, refreshed_layer_programs)
+                                     normaliser_program, refreshed_layer_depths,
+                                     refreshed_layer_programs, rmsnorm_slim_program)
     from feature_major.model import (approximations_for, embed_tokens, final_logits,
                                      layer_ranges, prefill_fhe)
 
+    params = REFRESH_PARAMS if params is None else params
+    budget = tuple(int(v) for v in budget)
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
-    spec = fhe.CKKSContextSpec(**REFRESH_PARAMS, seed=seed,
+    spec = fhe.CKKSContextSpec(**params, seed=seed,
                                rotations=decoder_layer_rotations(lay, H, hd))
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec, device="cuda:0")
@@ -1154,23 +1180,43 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         ctx.synchronize()
         prep_s = time.perf_counter() - t0
         # every layer's series have the same degrees, hence the same depths
-        if len({refreshed_layer_depths(w_.approx, T) for w_ in layers}) != 1:
+        if len({refreshed_layer_depths(w_.approx, T, refresh_normalisers=refresh_normalisers,
+                                       slim_rmsnorm=slim_rmsnorm) for w_ in layers}) != 1:
             raise ValueError("layers with different depths need programs of their own")
         t0 = time.perf_counter()
-        prog, res_prog = refreshed_layer_programs(ctx, layers[0].approx, T, log_slots=15)
+        ap0 = layers[0].approx
+        prog, res_prog = refreshed_layer_programs(ctx, ap0, T, log_slots=15, level_budget=budget,
+                                                  refresh_normalisers=refresh_normalisers,
+                                                  slim_rmsnorm=slim_rmsnorm)
+        lam_prog = (normaliser_program(ctx, ap0, T, log_slots=15, level_budget=budget)
+                    if refresh_normalisers else None)
+        rms_prog = (rmsnorm_slim_program(ctx, ap0, T, log_slots=15, level_budget=budget,
+                                         refresh_normalisers=refresh_normalisers)
+                    if slim_rmsnorm else None)
         ctx.synchronize()
         setup_s += time.perf_counter() - t0
 
         packed = lay.pack(x_test)
-        cts = [client.encrypt(packed[i], cur_limbs=1, enc_id=700000 + i)
+        # the lowest level a refresh takes on this chain
+        start = bs.input_limbs(ctx)
+        cts = [client.encrypt(packed[i], cur_limbs=start, enc_id=700000 + i)
                for i in range(lay.cipher_count)]
         ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
         ev0.record()
         t0 = time.perf_counter()
+        allocs = []
+
+        def on_layer(i, s):
+            # the pool's device allocations so far: a layer that grows the
+            # pool pays its hipMalloc calls
+            allocs.append(int(ctx.memory_info()["device_allocations"]))
+            print(f"layer {i}: {s:.2f} s, {allocs[-1]} device allocations", file=sys.stderr,
+                  flush=True)
+
         res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog,
                           residual_program=res_prog, residual_bounds=bounds,
-                          on_layer=lambda i, s: print(f"layer {i}: {s:.2f} s", file=sys.stderr,
-                                                      flush=True))
+                          normaliser_program=lam_prog, rmsnorm_program=rms_prog,
+                          on_layer=on_layer)
         ev1.record()
         ctx.synchronize()
         wall = time.perf_counter() - t0
@@ -1183,6 +1229,8 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         for w_ in layers:
             w_.close()
     mem = ctx.memory_info()
+    L, alpha = ctx.L, ctx.alpha
+    log_qp = sum(int(q).bit_length() for q in ctx.primes())
     ctx.close()
     ones = np.ones(D)
     lg = final_logits(got, norm_weight=ones, lm_head=lm_head)
@@ -1195,11 +1243,19 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0) -
         "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 2),
         "layers": int(n_layers),
         "layer_s": [round(v, 2) for v in res.layer_seconds],
+        "device_allocations_after_layer": allocs,
         "workload": f"{n_layers}-layer Llama-3-8B prefill (d=4096, 32/8 heads x 128, SwiGLU "
                     f"14336, vocab {vocab}) over 128 random tokens in 16 ciphertexts of 8 lanes, "
-                    "every layer boundary encrypted, bootstraps included (24 per layer), "
-                    "N=2^16, Q=1x60b+65x40b, dnum=5, P=14x44b; final token's logits in the "
-                    "clear",
+                    "every layer boundary encrypted, bootstraps included (24 per layer"
+                    + (", plus 3 softmax normaliser refreshes" if refresh_normalisers else "")
+                    + (", plus 1 slim RMSNorm refresh" if slim_rmsnorm else "")
+                    + f"), N=2^16, Q=1x{params['first_mod']}b+{L - 1}x{params['dcrt_bits']}b, "
+                    f"dnum={params['dnum']}, P={alpha}x{params['special_bits']}b, CtS/StC budget "
+                    f"{budget}; final token's logits in the clear",
+        "log_qp_bits": log_qp,
+        # N / log QP scaled from the standard's 128-bit point (log QP <= 1747
+        # at N = 2^16, uniform ternary): an upper estimate for h = 192 secrets
+        "security_estimate_bits": round(128 * 1747 / log_qp),
         "logits_max_abs_err_vs_fp64_exact": float(np.abs(lg - lg_exact).max()),
         "logits_max_abs_err_vs_fp64_series": float(np.abs(lg - lg_poly).max()),
         "logits_abs_max": float(np.abs(lg_exact).max()),

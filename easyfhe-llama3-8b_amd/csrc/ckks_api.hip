@@ -2009,6 +2009,60 @@ int ckks_mul_pt(ckks_context *c, const ckks_ct *a, const ckks_ct *pt, ckks_ct **
   API_END
 }
 
+int ckks_grouped_mac(ckks_context *c, const ckks_ct *const *terms, const ckks_ct *const *pts,
+                     const int *group_sizes, int n_groups, ckks_ct **out) {
+  API_BEGIN
+  require(c && terms && pts && group_sizes && out, "null argument");
+  require(n_groups >= 1, "at least one group");
+  int n = 0;
+  for (int g = 0; g < n_groups; g++) {
+    require(group_sizes[g] >= 1 && group_sizes[g] <= kMaxBatch,
+            "a group takes 1 to 64 terms");
+    n += group_sizes[g];
+    out[g] = nullptr;
+  }
+  const ckks_ct *a0 = terms[0];
+  check_poly(c, a0, "grouped_pairwise_mac");
+  require(a0->polys == 2, "grouped_pairwise_mac: degree-1 ciphertexts");
+  const double sc = a0->scale * pts[0]->scale;
+  for (int t = 0; t < n; t++) {
+    const ckks_ct *a = terms[t], *pt = pts[t];
+    check_poly(c, a, "grouped_pairwise_mac");
+    check_ct(c, pt, "grouped_pairwise_mac plaintext");
+    require(a->polys == 2 && a->limbs == a0->limbs && a->is_ext == a0->is_ext,
+            "grouped_pairwise_mac: terms at one level and basis");
+    require(pt->polys == 1 && pt->limbs >= a->limbs, "plaintext limbs below ciphertext limbs");
+    if (a->is_ext)
+      require(pt->is_ext && pt->limbs == a->limbs,
+              "an extended ciphertext needs an extended plaintext at its level");
+    const double st = a->scale * pt->scale;
+    require(fabs(st - sc) / std::max(st, sc) < 1.0 / 1024.0,
+            "grouped_pairwise_mac: products at different scales");
+  }
+  const int total = a0->limbs + (a0->is_ext ? c->alpha : 0);
+  int t0 = 0;
+  try {
+    for (int g = 0; g < n_groups; g++) {
+      Batch bb{}, pb{};
+      for (int b = 0; b < group_sizes[g]; b++) {
+        bb.p[b] = terms[t0 + b]->d;
+        pb.p[b] = pts[t0 + b]->d;
+      }
+      out[g] = new_ct(c, 2, a0->limbs, a0->is_ext, a0->slots, sc,
+                      a0->scale_degree + pts[0]->scale_degree);
+      launch_mac(c, bb, pb, group_sizes[g], out[g]->d, total, a0->limbs);
+      t0 += group_sizes[g];
+    }
+  } catch (...) {
+    for (int g = 0; g < n_groups; g++) {
+      free_ct(out[g]);
+      out[g] = nullptr;
+    }
+    throw;
+  }
+  API_END
+}
+
 int ckks_mul_i(ckks_context *c, const ckks_ct *a, int negative, ckks_ct **out) {
   API_BEGIN
   check_poly(c, a, "mul_i");

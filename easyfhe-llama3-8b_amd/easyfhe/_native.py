@@ -104,6 +104,7 @@ SIGNATURES = {
     "ckks_add_many": (I, [VP, VPP, VPP, I, I, VPP]),
     "ckks_add_pt": (I, [VP, VP, VP, VPP]),
     "ckks_mul_pt": (I, [VP, VP, VP, VPP]),
+    "ckks_grouped_mac": (I, [VP, VPP, VPP, ctypes.POINTER(ctypes.c_int), I, VPP]),
     "ckks_mul_i": (I, [VP, VP, I, VPP]),
     "ckks_add_scalar": (I, [VP, VP, VP, VPP]),
     "ckks_mul_scalar": (I, [VP, VP, VP, VPP]),

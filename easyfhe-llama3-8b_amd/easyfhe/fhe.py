@@ -1176,26 +1176,50 @@ def moddown_from_ext(ct, context=None):
     return _wrap(ctx, out)
 
 
-def grouped_pairwise_mac(batch: CipherBatch, plaintexts, groups, context=None) -> list:
-    """``sum_{i in group} batch[i] * pt[i]`` per group (unrescaled)."""
-    cts = batch.cv if isinstance(batch, CipherBatch) else list(batch)
+def _batch_items(batch) -> list:
+    if isinstance(batch, CipherBatch):
+        return list(batch.cv)
+    if hasattr(batch, "cv") and not isinstance(batch, Ciphertext):
+        return list(batch.cv)
+    return list(batch)
+
+
+def grouped_pairwise_mac(batch, plaintexts, groups, context=None):
+    """``sum_i batch[i] * plaintexts[i]`` per group, unrescaled (reference
+    operators/attention/input.py:814-826, 1274-1286, 1322-1334).  ``groups``
+    is either a group count G (the batch split into G consecutive groups of
+    equal size; the reference passes 1 and gets one ciphertext back, a list
+    for G > 1) or a sequence of index groups (a list back).  One launch per
+    group reads each ciphertext and plaintext word once (ckks_grouped_mac);
+    extended (Q u P) terms take extended plaintexts and stay extended, for
+    ``moddown_from_ext``."""
+    cts = _batch_items(batch)
+    pts = _batch_items(plaintexts)
     if not cts:
         return []
     ctx = _ctx(cts[0], context)
-    results = []
-    for group in groups:
-        acc = None
-        for i in group:
-            term = homo_mul_pt(cts[int(i)], plaintexts[int(i)], ctx)
-            if acc is None:
-                acc = term
-            else:
-                new = homo_add(acc, term, ctx)
-                acc.release()
-                term.release()
-                acc = new
-        results.append(acc)
-    return results
+    if isinstance(groups, (int, np.integer)):
+        G = int(groups)
+        if G < 1 or len(cts) % G:
+            raise ValueError(f"{len(cts)} terms do not split into {G} equal groups.")
+        size = len(cts) // G
+        index_groups = [list(range(g * size, (g + 1) * size)) for g in range(G)]
+        single = G == 1
+    else:
+        index_groups = [[int(i) for i in grp] for grp in groups]
+        single = False
+    if not index_groups:
+        return []
+    order = [i for grp in index_groups for i in grp]
+    if any(i < 0 or i >= len(cts) or i >= len(pts) for i in order):
+        raise ValueError("grouped_pairwise_mac: term index out of range.")
+    sizes = (ctypes.c_int * len(index_groups))(*[len(grp) for grp in index_groups])
+    outs = (ctypes.c_void_p * len(index_groups))()
+    check(lib.ckks_grouped_mac(ctx.handle, _native.ptr_array([cts[i].handle for i in order]),
+                               _native.ptr_array([pts[i].handle for i in order]), sizes,
+                               len(index_groups), outs))
+    results = [_wrap(ctx, outs[g]) for g in range(len(index_groups))]
+    return results[0] if single else results
 
 
 __all__ = [name for name in dir() if not name.startswith("_")]

@@ -158,14 +158,18 @@ class PrefillResult:
 
 def prefill_fhe(input_ciphers, layers: Sequence[DecoderLayerWeights], *, crypto_context,
                 program, residual_bounds: Sequence[float], residual_program=None,
+                normaliser_program=None, rmsnorm_program=None,
                 group: int = 8, rope_theta: float = 500000.0,
                 on_layer: Callable[[int, float], None] | None = None) -> PrefillResult:
     """The encrypted layers in order, each refreshed as it begins (reference
     model.py:171 Llama3Model.forward).  ``program`` and ``residual_program``
     are the score and residual bootstrap programs of
-    ``decoder_layer_refreshed_fhe``; ``residual_bounds[i]`` bounds layer i's
-    residual stream; the inputs are not consumed.  ``on_layer(i, s)`` is
-    called after each layer with its wall time."""
+    ``decoder_layer_refreshed_fhe``, and ``normaliser_program`` /
+    ``rmsnorm_program`` its optional softmax-normaliser and slim RMSNorm
+    refreshes (the reference's lambda and slim refreshes, which its chain
+    needs); ``residual_bounds[i]`` bounds layer i's residual stream; the
+    inputs are not consumed.  ``on_layer(i, s)`` is called after each layer
+    with its wall time."""
     if len(residual_bounds) != len(layers):
         raise ValueError("one residual bound per layer.")
     if not layers:
@@ -178,7 +182,9 @@ def prefill_fhe(input_ciphers, layers: Sequence[DecoderLayerWeights], *, crypto_
             res = decoder_layer_refreshed_fhe(cur, w, crypto_context=crypto_context,
                                               program=program, residual_program=residual_program,
                                               residual_bound=float(residual_bounds[i]),
-                                              group=group, rope_theta=rope_theta)
+                                              group=group, rope_theta=rope_theta,
+                                              normaliser_program=normaliser_program,
+                                              rmsnorm_program=rmsnorm_program)
             if owned:
                 for c in cur:
                     c.release()

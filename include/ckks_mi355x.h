@@ -278,6 +278,16 @@ int ckks_hoisted_mac_sum_double_many(ckks_context *ctx, const ckks_ct *const *a,
 int ckks_linear_combination(ckks_context *ctx, const ckks_ct *const *terms, int T, int n,
                             const double *weights, double constant, int limbs, double scale,
                             int scale_degree, ckks_ct **out);
+/* fhe.grouped_pairwise_mac (reference operators/attention/input.py:814-826,
+ * 1274-1286, 1322-1334): terms[t] times plaintext pts[t], summed per group
+ * (group g takes the next group_sizes[g] terms, 1 to 64 of them), unrescaled,
+ * in one launch per group that reads each word once.  All terms share one
+ * level and basis (Q, or Q u P with extended plaintexts at that level; a
+ * Q-basis term takes a plaintext's leading limbs) and, with their
+ * plaintexts, one scale; out[g] at scale terms' x plaintexts'.  The words
+ * equal those of ckks_mul_pt then ckks_add over the group. */
+int ckks_grouped_mac(ckks_context *ctx, const ckks_ct *const *terms, const ckks_ct *const *pts,
+                     const int *group_sizes, int n_groups, ckks_ct **out);
 /* fhe.rescale for n ciphertexts of one shape in batched launches. */
 int ckks_rescale_many(ckks_context *ctx, const ckks_ct *const *a, int n, ckks_ct **out);
 /* `primes` rescales in a row (1..4) of each of n ciphertexts of one shape, as

@@ -465,6 +465,58 @@ def test_fast_rotate_ext_moddown_is_rotation(name):
     assert np.abs(client.decrypt(out) - want).max() < 1e-6
 
 
+def _composed_mac(fhe, ctx, cts, pts):
+    acc = None
+    for c, p in zip(cts, pts):
+        t = fhe.homo_mul_pt(c, p, ctx)
+        acc = t if acc is None else fhe.homo_add(acc, t, ctx)
+    return acc
+
+
+@pytest.mark.slow
+def test_grouped_pairwise_mac_matches_composed_full_size():
+    """N = 2^16 on the key-switch chain at 13 limbs: eight extended hoisted
+    rotations times extended plaintexts, as the reference calls it (the
+    rotations of one target packed into a batch of four, group count 1: one
+    ciphertext back; and the eight as two groups of four), and the same on
+    Q-basis rotations; every result equal word for word to homo_mul_pt then
+    homo_add, and its ModDown to the plain rotations' weighted sum."""
+    fhe = _fhe()
+    offs = list(range(8))
+    client, ctx = device_context("keyswitch", rotations=tuple(o for o in offs if o))
+    slots, limbs = ctx.max_slots, 13
+    rng = np.random.default_rng(23)
+    z = rng.uniform(-1, 1, slots)
+    ct = client.encrypt(z, cur_limbs=limbs, enc_id=31)
+    sc = ct.state.scaling_factor
+    w = [rng.uniform(-1, 1, slots) for _ in offs]
+    for ext in (True, False):
+        batch = fhe.fast_rotate(ct, offs, ctx, output_ext=ext)
+        assert all(b.is_ext == ext for b in batch.cv)
+        pts = [fhe.encode_rows(ctx, v, limbs=limbs, scale=sc, slots=slots, is_ext=ext)[0]
+               for v in w]
+        two = fhe.grouped_pairwise_mac(batch, pts, 2, ctx)
+        assert len(two) == 2
+        for g in range(2):
+            want = _composed_mac(fhe, ctx, batch.cv[4 * g:4 * g + 4], pts[4 * g:4 * g + 4])
+            assert two[g].is_ext == ext
+            assert np.array_equal(two[g].download(), want.download()), (ext, g)
+        one = fhe.grouped_pairwise_mac(fhe.pack_cipher_batch(batch.cv[4:]), pts[4:], 1, ctx)
+        assert not isinstance(one, list) and one.is_ext == ext
+        assert np.array_equal(one.download(), two[1].download())
+        picked = fhe.grouped_pairwise_mac(batch, pts, [[7, 0, 3]], ctx)[0]
+        want = _composed_mac(fhe, ctx, [batch.cv[i] for i in (7, 0, 3)],
+                             [pts[i] for i in (7, 0, 3)])
+        assert np.array_equal(picked.download(), want.download())
+        if ext:
+            out = fhe.rescale(fhe.moddown_from_ext(one, ctx), ctx)
+            want = sum(w[k] * np.roll(z, -k) for k in range(4, 8))
+            assert np.abs(client.decrypt(out) - want).max() < 1e-6
+    with pytest.raises(ValueError):
+        fhe.grouped_pairwise_mac(batch, pts, 3, ctx)  # 8 terms into 3 groups
+    ctx.close()
+
+
 # ---------------------------------------------------------------------------
 # keyswitch workload size (N = 2^16, 36 + 12 limbs, dnum 3)
 # ---------------------------------------------------------------------------
