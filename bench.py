@@ -416,6 +416,7 @@ def main() -> int:
         "traffic": round(traffic) if traffic else None,
         "traffic_over_algorithmic": round(traffic / step_bytes, 2) if traffic else None,
     }
+    result["grouped_mac"] = measure_grouped_mac(client, ctx)
     result["matvec_config"] = measure_matvec_config()
     if not (args.no_bootstrap and args.no_linear and args.no_mlp and args.no_attention):
         for c in cts:
@@ -459,6 +460,79 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measure_grouped_mac(client, ctx, limbs: int = 13, reps: int = 20) -> dict:
+    """The reference's Q/K gather step (operators/attention/input.py:792-826)
+    at N = 2^16: 16 hoisted rotations of one ciphertext kept in Q u P
+    (fast_rotate(output_ext=True)), then for each of 4 targets the grouped
+    pairwise MAC of its 4 rotations with 4 extended plaintexts (group count
+    1, as the reference calls it) and one ModDown.  Times the fused MAC
+    (ckks_grouped_mac) against homo_mul_pt + homo_add per term, and reports
+    its algorithmic rate (each term's c0, c1 and plaintext word read once,
+    each output word written once)."""
+    from easyfhe import fhe
+
+    slots = ctx.max_slots
+    rng = np.random.default_rng(7)
+    ct = client.encrypt(rng.uniform(-1, 1, slots), cur_limbs=limbs, enc_id=880001)
+    sc = ct.state.scaling_factor
+    offs = [0] + list(ROTATIONS)
+    batch = fhe.fast_rotate(ct, offs, ctx, output_ext=True)
+    pts = [fhe.encode_rows(ctx, rng.uniform(-1, 1, slots), limbs=limbs, scale=sc, slots=slots,
+                           is_ext=True)[0] for _ in offs]
+    targets = [(fhe.pack_cipher_batch(batch.cv[4 * t:4 * t + 4]), pts[4 * t:4 * t + 4])
+               for t in range(len(offs) // 4)]
+
+    def fused():
+        return [fhe.grouped_pairwise_mac(b, p, 1, ctx) for b, p in targets]
+
+    def composed():
+        outs = []
+        for b, p in targets:
+            acc = None
+            for c, q in zip(b.cv, p):
+                t = fhe.homo_mul_pt(c, q, ctx)
+                if acc is None:
+                    acc = t
+                else:
+                    nxt = fhe.homo_add(acc, t, ctx)
+                    acc.release()
+                    t.release()
+                    acc = nxt
+            outs.append(acc)
+        return outs
+
+    res = {}
+    for name, fn in (("fused", fused), ("composed", composed)):
+        for c in fn():
+            c.release()
+        ctx.synchronize()
+        ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+        ev0.record()
+        for _ in range(reps):
+            for c in fn():
+                c.release()
+        ev1.record()
+        ctx.synchronize()
+        res[name] = ev0.elapsed_time(ev1) / reps
+    E = limbs + ctx.alpha
+    terms, groups = len(offs), len(targets)
+    alg = 8.0 * ctx.N * E * (3 * terms + 2 * groups)
+    for c in batch.cv:
+        c.release()
+    for b, _ in targets:
+        b.release()
+    for q in pts:
+        q.release()
+    ct.release()
+    return {"workload": f"{terms} extended hoisted rotations at {limbs} + {ctx.alpha} limbs, "
+                        f"N=2^{ctx.logN}, {groups} targets x 4 terms (group count 1 per target)",
+            "ms_fused": round(res["fused"], 4), "ms_composed": round(res["composed"], 4),
+            "speedup": round(res["composed"] / res["fused"], 2),
+            "algorithmic_bytes": round(alg),
+            "fused_gbs": round(alg / (res["fused"] * 1e-3) / 1e9, 1),
+            "fused_hbm_frac": round(alg / (res["fused"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,

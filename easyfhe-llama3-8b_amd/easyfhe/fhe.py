@@ -1218,7 +1218,7 @@ def grouped_pairwise_mac(batch, plaintexts, groups, context=None):
     check(lib.ckks_grouped_mac(ctx.handle, _native.ptr_array([cts[i].handle for i in order]),
                                _native.ptr_array([pts[i].handle for i in order]), sizes,
                                len(index_groups), outs))
-    results = [_wrap(ctx, outs[g]) for g in range(len(index_groups))]
+    results = [Ciphertext(ctx, outs[g]) for g in range(len(index_groups))]
     return results[0] if single else results
 
 
