@@ -387,6 +387,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": round(ntt_bytes * NTT_TRAFFIC_RATIO),
+            "traffic_source": "NTT_TRAFFIC_RATIO from profiles/ntt_batch_pmc_traffic.md",
             "launch_ms": round(ntt_ms, 4),
             "limb_polys_per_launch": limb_polys,
         },
@@ -395,12 +396,15 @@ def main() -> int:
     # outside the timed region): each kernel group's share of the step, its
     # algorithmic HBM rate and its modular-operation rate against the probes
     peaks = int_peaks(ctx)
+    # on one stream, so that the kernels' event windows do not overlap
+    ctx.set_split_parts(1)
     ctx.profile(True)
     out = step()
     for c in out:
         c.release()
     prof = ctx.profile_read()
     ctx.profile(False)
+    ctx.set_split_parts(3)
     result["int_peak"] = peaks
     result["kernels"] = kernel_table(prof, peaks)
     kernel_bytes = sum(v["bytes"] for v in prof.values())
@@ -415,6 +419,10 @@ def main() -> int:
         "path": path,
         "traffic": round(traffic) if traffic else None,
         "traffic_over_algorithmic": round(traffic / step_bytes, 2) if traffic else None,
+        "traffic_source": "FETCH_SIZE/WRITE_SIZE counter runs of bench.py --mode ks-profile, "
+                          "profiles/keyswitch_step_traffic.md (copied, not measured in this run)",
+        "kernels_table": "one extra step on one stream (ckks_set_split_parts(1)), events per "
+                         "launch; algorithmic bytes count a squared operand once",
     }
     result["grouped_mac"] = measure_grouped_mac(client, ctx)
     result["matvec_config"] = measure_matvec_config()
@@ -535,6 +543,25 @@ def measure_grouped_mac(client, ctx, limbs: int = 13, reps: int = 20) -> dict:
             "fused_hbm_frac": round(alg / (res["fused"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def audit_roofline(audit: dict, seconds: float, units: int, unit: str) -> dict:
+    """HBM roofline of a whole program from the library's operation audit
+    (ckks_audit_read, the analogue of the reference's graph.py:348
+    operation_audit): algorithmic bytes = key switches' ciphertext bytes +
+    key bytes + plaintext (diagonal) bytes + rescale bytes, over the timed
+    wall time, against 8 TB/s."""
+    alg = (audit["keyswitch_ct_bytes"] + audit["key_bytes"] + audit["plaintext_bytes"]
+           + audit["rescale_bytes"])
+    gbs = alg / max(seconds, 1e-9) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": round(alg),
+            f"keyswitches_per_{unit}": round(audit["keyswitches"] / units, 1),
+            f"keyswitch_ct_bytes_per_{unit}": round(audit["keyswitch_ct_bytes"] / units),
+            f"key_bytes_per_{unit}": round(audit["key_bytes"] / units),
+            f"plaintext_bytes_per_{unit}": round(audit["plaintext_bytes"] / units),
+            f"rescale_bytes_per_{unit}": round(audit["rescale_bytes"] / units),
+            "source": "ckks_audit_read over the timed region"}
+
+
 def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
                       log_slots: int | None = None, evalmod=None) -> dict:
     """Bootstrap of n_cts ciphertexts at the bottom level (one limb, values
@@ -570,12 +597,14 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
     ctx.synchronize()
     first_s = time.perf_counter() - t0
     ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+    ctx.audit(reset=True)
     ev0.record()
     t0 = time.perf_counter()
     outs = bs.bootstrap_many(cts, ctx, prog, group=group)
     ev1.record()
     ctx.synchronize()
     wall = time.perf_counter() - t0
+    roof = audit_roofline(ctx.audit(reset=True), wall, len(cts), "bootstrap")
     bits = [-math.log2(np.abs(client.decrypt_complex(o) - z).max()) for o, z in zip(outs, zs)]
     for o in outs:
         o.release()
@@ -601,6 +630,7 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
         "precision_bits_mean": round(float(np.mean(bits)), 2),
         "setup_s": round(setup_s, 2),
         "first_group_s": round(first_s, 3),
+        "roofline": roof,
     }
 
 
@@ -1042,11 +1072,14 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     start = bs.input_limbs(ctx)
     cur = [client.encrypt(packed[i], cur_limbs=start, enc_id=600000 + i)
            for i in range(lay.cipher_count)]
-    per_layer, stages = [], {}
+    per_layer, stages, audit = [], {}, None
     ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
     ev0.record()
     t_all = time.perf_counter()
     for layer in range(int(n_layers)):
+        if layer == min(1, int(n_layers) - 1):
+            ctx.synchronize()
+            ctx.audit(reset=True)  # the audit covers the steady-state layers
         res = decoder_layer_refreshed_fhe(cur, dev[layer % len(dev)], crypto_context=ctx,
                                           program=prog, residual_program=res_prog,
                                           normaliser_program=lam_prog,
@@ -1060,6 +1093,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
               file=sys.stderr, flush=True)
     ev1.record()
     ctx.synchronize()
+    audit = ctx.audit(reset=True)
     total = time.perf_counter() - t_all
     got = lay.unpack(np.stack([client.decrypt(o) for o in cur]))
     out_limbs = int(cur[0].state.cur_limbs)
@@ -1077,6 +1111,7 @@ def measure_fm_layers(n_layers: int = 2, weight_sets: int = 2, *, params=None,
     steady = per_layer[1:] or per_layer
     return {
         "seconds_per_layer": round(float(np.mean(steady)), 3),
+        "roofline": audit_roofline(audit, float(np.sum(steady)), len(steady), "layer"),
         "layers": int(n_layers),
         "total_seconds": round(total, 3),
         "gpu_event_seconds": round(ev0.elapsed_time(ev1) / 1000.0, 3),
@@ -1276,6 +1311,8 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         cts = [client.encrypt(packed[i], cur_limbs=start, enc_id=700000 + i)
                for i in range(lay.cipher_count)]
         ev0, ev1 = fhe_event(ctx), fhe_event(ctx)
+        ctx.synchronize()
+        ctx.audit(reset=True)
         ev0.record()
         t0 = time.perf_counter()
         allocs = []
@@ -1294,6 +1331,7 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         ev1.record()
         ctx.synchronize()
         wall = time.perf_counter() - t0
+        audit = ctx.audit(reset=True)
         for c in cts:
             c.release()
         got = lay.unpack(np.stack([client.decrypt(o) for o in res.ciphers]))
@@ -1318,6 +1356,7 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         "layers": int(n_layers),
         "layer_s": [round(v, 2) for v in res.layer_seconds],
         "device_allocations_after_layer": allocs,
+        "roofline": audit_roofline(audit, wall, int(n_layers), "layer"),
         "workload": f"{n_layers}-layer Llama-3-8B prefill (d=4096, 32/8 heads x 128, SwiGLU "
                     f"14336, vocab {vocab}) over 128 random tokens in 16 ciphertexts of 8 lanes, "
                     "every layer boundary encrypted, bootstraps included (24 per layer"

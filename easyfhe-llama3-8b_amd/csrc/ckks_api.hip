@@ -1533,6 +1533,7 @@ static void rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks
   const u64 *tab = rescale_d_table(c, limbs, D);
   const bool fused = c->logN == 16 && polys == 2;
   const int per = kMaxBatch / polys;
+  audit_rescale(c, (double)n * polys * (limbs + T));
   for (int b0 = 0; b0 < n; b0 += per) {
     const int nb = std::min(per, n - b0), items = nb * polys;
     Scratch s(c);
@@ -1594,6 +1595,7 @@ int ckks_context_create(const ckks_params *params, ckks_context **out) {
       require(c->split_parts >= 1 && c->split_parts <= ckks_context::kMaxSplit,
               "CKKS_SPLIT_STREAMS must be 1 .. 4");
     }
+    c->split_streams = c->split_parts;
     HIPCHECK(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming));
     for (int i = 0; i + 1 < c->split_parts; i++) {
       // default priority, as the context stream
@@ -3300,6 +3302,24 @@ int ckks_profile_read(ckks_context *c, char *buf, size_t len) {
   const size_t n = std::min(len - 1, text.size());
   memcpy(buf, text.data(), n);
   buf[n] = 0;
+  API_END
+}
+
+int ckks_set_split_parts(ckks_context *c, int parts) {
+  API_BEGIN
+  require(c, "null argument");
+  require(parts >= 1 && parts <= c->split_streams,
+          "split parts must be 1 .. the count the context was created with");
+  c->split_parts = parts;
+  API_END
+}
+
+int ckks_audit_read(ckks_context *c, double *out, int reset) {
+  API_BEGIN
+  require(c && out, "null argument");
+  for (int i = 0; i < 5; i++) out[i] = c->audit[i];
+  if (reset)
+    for (int i = 0; i < 5; i++) c->audit[i] = 0.0;
   API_END
 }
 

@@ -276,6 +276,11 @@ struct ckks_context {
   std::map<int, u64 *> garner;   // K -> [K*K] q_j^-1 mod q_k
   bool prof = false;                     // per-kernel timing on
   std::vector<ckks::ProfRec> prof_recs;  // timed launches since the last read
+  // operation audit since the last ckks_audit_read with reset: key switches,
+  // their ciphertext bytes (input read once per ModUp, each output written
+  // once), their key bytes (each key read once per launch), the plaintext
+  // bytes of MACs and plaintext products, rescale bytes
+  double audit[5] = {0, 0, 0, 0, 0};
   std::vector<hipEvent_t> prof_pool;     // events for reuse
   int device = 0;                  // HIP device current at creation
   u64 *noalloc_scratch = nullptr;  // that device's fixed scratch (ckks_rotate_many_noalloc)
@@ -311,6 +316,7 @@ struct ckks_context {
   // (1 keeps one stream)
   static constexpr int kMaxSplit = 4;
   int split_parts = 3;
+  int split_streams = 3;  // parts whose streams exist (split_parts <= this)
   hipStream_t aux[kMaxSplit - 1] = {};
   hipEvent_t fork_ev = nullptr, join_ev[kMaxSplit - 1] = {};
 };
@@ -342,6 +348,19 @@ struct ckks_tensor {  // raw device bytes (weights for the diagonal packers)
 namespace ckks {
 
 // Records one timed launch when the context profiles (scope = the launches).
+// audit counters (ckks_context::audit)
+inline void audit_keyswitch(ckks_context *c, int n_items, int n_keys, int q_limbs, int digits,
+                            int E) {
+  const double lp = 8.0 * c->N;
+  c->audit[0] += (double)n_items * n_keys;
+  c->audit[1] += (double)n_items * (2.0 * q_limbs + 2.0 * q_limbs * n_keys) * lp;
+  c->audit[2] += (double)n_keys * digits * 2.0 * E * lp;
+}
+inline void audit_pt(ckks_context *c, double limb_polys) { c->audit[3] += limb_polys * 8.0 * c->N; }
+inline void audit_rescale(ckks_context *c, double limb_polys) {
+  c->audit[4] += limb_polys * 8.0 * c->N;
+}
+
 struct KTimer {
   ckks_context *c;
   ProfRec r{};

@@ -1609,6 +1609,7 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
   KTimer kt(c, "ntt_low_key",
             8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
+  audit_keyswitch(c, n_items, 1, q_limbs, digits, E);
   if (n_items <= 0) return;
   LowKeyArgs a = low_key_args(c, ext, ext_stride, own, acc, acc_stride, key, digits, E, q_limbs,
                               ginv);
@@ -1700,6 +1701,7 @@ __global__ void k_mul_pt(const u64 *__restrict__ ct, const u64 *__restrict__ pt,
 
 void launch_mul_pt(ckks_context *c, const u64 *ct, const u64 *pt, u64 *out, int polys,
                    int limbs, int q_limbs) {
+  audit_pt(c, (double)limbs);
   dim3 grid(c->N / TPB, limbs, polys);
   hipLaunchKernelGGL(k_mul_pt, grid, dim3(TPB), 0, c->stream, ct, pt, out, c->logN, limbs,
                      q_limbs, c->L, c->d_mods);
@@ -1778,7 +1780,11 @@ __global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs,
 
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
                    int n_items, int limbs) {
-  KTimer kt(c, "tensor", 8.0 * c->N * 7.0 * n_items * limbs, 4.0 * c->N * n_items * limbs);
+  // a squared operand (a = b) is read once
+  bool same = true;
+  for (int i = 0; i < n_items && same; i++) same = batch_ptr_host(a, i) == batch_ptr_host(b, i);
+  KTimer kt(c, "tensor", 8.0 * c->N * (same ? 5.0 : 7.0) * n_items * limbs,
+            4.0 * c->N * n_items * limbs);
   dim3 grid(c->N / TPB, limbs, n_items);
   hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
                      c->d_mods);
@@ -2945,6 +2951,7 @@ void launch_key_inner(ckks_context *c, const Batch &ext, const Batch &acc, int n
                       const Batch *own) {
   KTimer kt(c, "key_inner", 8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
+  audit_keyswitch(c, n_items, 1, q_limbs, digits, E);
   dim3 grid(c->N / TPB, E);
   Batch ob{};
   if (own) ob = *own;
@@ -3089,6 +3096,7 @@ void launch_key_inner_multi(ckks_context *c, const u64 *ext, size_t ext_stride, 
             8.0 * c->N * E * ((double)n_items * digits + 2.0 * digits * keys.size() +
                               2.0 * n_items * keys.size()),
             2.0 * c->N * E * digits * (double)keys.size() * n_items);
+  audit_keyswitch(c, n_items, (int)keys.size(), q_limbs, digits, E);
   if (n_items < 1 || n_items > kMultiItems) throw std::invalid_argument("key_inner_multi: items");
   const int nb = (int)keys.size();
   if (nb < 1 || nb > kMaxBatch) throw std::invalid_argument("key_inner_multi: babies");
@@ -3306,6 +3314,7 @@ __global__ void k_mac(Batch babies, Batch pts, int B, u64 *__restrict__ out, int
 void launch_mac(ckks_context *c, const Batch &babies, const Batch &pts, int B, u64 *out,
                 int limbs_total, int q_limbs) {
   KTimer kt(c, "mac", 8.0 * c->N * limbs_total * (3.0 * B + 2.0), 2.0 * c->N * limbs_total * B);
+  audit_pt(c, (double)B * limbs_total);
   dim3 grid(c->N / TPB, limbs_total, 2);
   hipLaunchKernelGGL(k_mac, grid, dim3(TPB), 0, c->stream, babies, pts, B, out, c->logN,
                      limbs_total, q_limbs, c->L, c->d_mods);
@@ -3449,6 +3458,7 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
                      u64 *out, int E, int q_limbs) {
   KTimer kt(c, "mac_many", 8.0 * c->N * E * (2.0 * n * B + (double)G * B + 2.0 * G * n),
             2.0 * c->N * E * (double)n * B * G);
+  audit_pt(c, (double)G * B * E);
   if (G < 1 || G > kMacGroups || G * B > kMaxBatch)
     throw std::invalid_argument("mac_many: 1 <= groups <= 2 and groups x babies <= 64");
   dim3 grid(c->N / TPB * 2 * ((n + kMacCtsFp - 1) / kMacCtsFp), E);
@@ -3602,6 +3612,7 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
                       int G, u64 *out, int limbs) {
   KTimer kt(c, "mac_table", 8.0 * c->N * limbs * (2.0 * n * B + (double)G * B + 2.0 * G * n),
             2.0 * c->N * limbs * (double)n * B * G);
+  audit_pt(c, (double)G * B * limbs);
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
     throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
   auto fp_kern = G <= 1   ? k_mac_table_fp<1>

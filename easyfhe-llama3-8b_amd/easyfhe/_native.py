@@ -153,6 +153,8 @@ SIGNATURES = {
     "ckks_event_elapsed_ms": (I, [VP, VP, ctypes.POINTER(ctypes.c_float)]),
     "ckks_event_destroy": (None, [VP]),
     "ckks_context_stream": (I, [VP, VPP]),
+    "ckks_audit_read": (I, [VP, ctypes.POINTER(ctypes.c_double), I]),
+    "ckks_set_split_parts": (I, [VP, I]),
 }
 
 

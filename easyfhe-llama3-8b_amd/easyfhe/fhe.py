@@ -172,6 +172,15 @@ class NativeContext:
     def synchronize(self) -> None:
         check(lib.ckks_synchronize(self._h))
 
+    def audit(self, reset: bool = False) -> dict[str, float]:
+        """Operation audit since the last reset (ckks_audit_read): key
+        switches and their ciphertext / key bytes, plaintext and rescale
+        bytes."""
+        v = (ctypes.c_double * 5)()
+        check(lib.ckks_audit_read(self._h, v, 1 if reset else 0))
+        return {"keyswitches": v[0], "keyswitch_ct_bytes": v[1], "key_bytes": v[2],
+                "plaintext_bytes": v[3], "rescale_bytes": v[4]}
+
     def memory_info(self) -> dict[str, int]:
         live, cached = ctypes.c_size_t(), ctypes.c_size_t()
         check(lib.ckks_memory_info(self._h, ctypes.byref(live), ctypes.byref(cached)))
@@ -184,6 +193,11 @@ class NativeContext:
 
     def empty_cache(self) -> None:
         check(lib.ckks_empty_cache(self._h))
+
+    def set_split_parts(self, parts: int) -> None:
+        """Streams a batched key switch is split over (1 to the count the
+        context was created with)."""
+        check(lib.ckks_set_split_parts(self._h, int(parts)))
 
     def profile(self, enable: bool = True) -> None:
         """Start (or stop) recording device time per kernel group."""

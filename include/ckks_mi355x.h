@@ -374,6 +374,22 @@ int ckks_event_record(ckks_event *ev);
 int ckks_event_elapsed_ms(ckks_event *start, ckks_event *end, float *ms);
 void ckks_event_destroy(ckks_event *ev);
 
+/* Streams a batched key switch of at least 16 ciphertexts is split over
+ * (1 .. the count set at creation by CKKS_SPLIT_STREAMS, default 3); no
+ * counterpart in the reference, whose library runs one stream.  1 gives the
+ * one-stream order per-kernel timings need. */
+int ckks_set_split_parts(ckks_context *ctx, int parts);
+
+/* The operation audit of the reference's graph audit (graph.py:348
+ * operation_audit), for the roofline of a whole program: out[0] key switches
+ * issued, out[1] their ciphertext bytes (a key switch's input read once per
+ * ModUp, each output written once: 4 l limb-polynomials for a plain one at l
+ * limbs), out[2] their key bytes (each key read once per batched launch),
+ * out[3] plaintext bytes of the MACs and plaintext products (each plaintext
+ * limb once per launch), out[4] rescale bytes (input and output once), all
+ * since the last call with reset != 0. */
+int ckks_audit_read(ckks_context *ctx, double *out, int reset);
+
 /* The context's HIP stream as an opaque handle (hipStream_t), for callers
  * that order their own launches with the library's work (the reference's
  * Triton bridge reads torch.cuda.current_stream(idx).cuda_stream,
