@@ -33,8 +33,12 @@ FLAGS = [
 SOURCES = ["ckks_kernels.hip", "ckks_api.hip"]
 # per-source flags: the int8 matrix-core conversion keeps its accumulators in
 # ordinary VGPRs (the AGPR form moves every accumulator through v_accvgpr
-# reads and writes, which the VALU pays for)
-EXTRA = {"ckks_kernels.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# reads and writes, which the VALU pays for); fully unrolled loops stay
+# unrolled up to a larger body (below it the tile-resident conversion's row
+# loop was left rolled, and its per-row register arrays went to scratch
+# memory)
+EXTRA = {"ckks_kernels.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form",
+                              "-mllvm", "-pragma-unroll-threshold=40000"]}
 
 
 def build(verbose: bool = False) -> Path:

@@ -1444,11 +1444,19 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     const Strided sp{x, (u64)xs};
     bool sp_done = false;
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
-    if (sp_done)
+    // N = 2^16: the special limbs' inverse high pass, the conversion with the
+    // lifts and the forward high pass of the kept limbs in one kernel
+    const bool tile = c->logN == 16 && c->ks_tile && convert_h4_rs_ok(c, bt, D);
+    if (tile) {
+      if (!sp_done)
+        launch_ntt_inv_low(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A,
+                           limbs);
+    } else if (sp_done) {
       launch_ntt_inv_high(c, strided(x - P, xs), 2 * nb, limbs, A, limbs);
-    else
+    } else {
       launch_ntt(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A, limbs,
                  true);
+    }
     Batch d3{}, o0{};
     for (int i = 0; i < nb; i++) {
       d3.p[i] = in[b0 + i]->d;
@@ -1459,14 +1467,18 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     launch_ntt(c, strided(xq - (size_t)T * N, xs), strided(xq - (size_t)T * N, xs), 2 * nb, T, D,
                limbs, true);
     u64 *conv = s.get((size_t)nb * 2 * T * N);
-    launch_bc_down_rescale(c, strided(x, xs), strided(conv, (size_t)T * N), 2 * nb, bt, D,
+    if (tile)
+      launch_convert_h4_rs(c, strided(x, xs), strided(conv, (size_t)T * N), 2 * nb, bt, D,
                            rt + 4 * (size_t)T);
+    else
+      launch_bc_down_rescale(c, strided(x, xs), strided(conv, (size_t)T * N), 2 * nb, bt, D,
+                             rt + 4 * (size_t)T);
     std::vector<u64> gal(nb, 1);
     const u64 *amul = rt + 2 * (size_t)T;
     const PostOp po = post_chunk(c, ps, b0, nb);
     if (c->logN == 16) {
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
-                         d3, P, gal.data(), o0, (u64)T * N, amul, &po);
+                         d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile);
     } else {
       Batch a1{}, o1{};
       for (int i = 0; i < nb; i++) {

@@ -453,6 +453,13 @@ void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int
 // convert_h4_ok tells whether table t takes it (int8-MFMA table, at most 12
 // sources and 64 targets).
 bool convert_h4_ok(const ckks_context *c, const BCTable &t);
+// The relinearise-rescale form (launch_bc_down_rescale's: D dropped primes,
+// rtab its table) of launch_convert_h4: src items hold the special limbs
+// after the inverse low pass, then the D dropped limbs of X as coefficients;
+// dst takes the T = nd - D kept targets after the forward high pass.
+bool convert_h4_rs_ok(const ckks_context *c, const BCTable &t, int D);
+void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                          const BCTable &t, int D, const u64 *rtab);
 void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                        const BCTable &t, int src_prime0, int t_split, int t_skip, int q_limbs,
                        bool centered);

@@ -1111,9 +1111,16 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         int E, const u64 *pinv, const Batch &add, u64 add1_off,
                         const u64 *galois, const Batch &out, u64 out1_off, const u64 *amul,
                         const PostOp *post, bool high_done, bool wide_only) {
+  // the limbs this call combines (wide_only: those of primes at or above 2^45)
+  int run_limbs = limbs;
+  if (wide_only) {
+    run_limbs = 0;
+    for (int l = 0; l < limbs; l++) run_limbs += c->prime_fp[l] ? 0 : 1;
+  }
   KTimer kt(c, "ntt_fwd_moddown",
-            8.0 * c->N * limbs * (6.0 * n + (batch_ptr_host(add, 0) ? (add1_off ? 2.0 : 1.0) * n : 0.0)),
-            0.5 * c->N * c->logN * 2.0 * n * limbs);
+            8.0 * c->N * run_limbs *
+                (6.0 * n + (batch_ptr_host(add, 0) ? (add1_off ? 2.0 : 1.0) * n : 0.0)),
+            0.5 * c->N * c->logN * 2.0 * n * run_limbs);
   if (c->logN != 16 || n > kMaxBatch) throw std::invalid_argument("fused ModDown: N = 2^16, n <= 64");
   MDCombine md{};
   md.acc = acc;
@@ -2341,11 +2348,23 @@ struct H4Tabs {
   const double2 *tw, *itw, *ninv_fp;
 };
 
-template <int NK>
+// RSD > 0: the relinearise-rescale ModDown by P p_1 .. p_RSD
+// (k_basis_convert_mfma's RS form): the dropped primes are the last targets,
+// p_(j+1) at target nd - 1 - j, all in one group, which runs first; its
+// lanes form each lift r_j from the dropped limb of X (source slot
+// ns + RSD - 1 - j, coefficient form) and leave it in LDS for every column
+// and row; each kept target t < nd - RSD then adds
+// r_j [P p_1..p_j]_t - (r_j > p_(j+1) / 2 ? [P p_1..p_(j+1)]_t : 0) before
+// its forward high pass.  rs / rsf: launch_bc_down_rescale's tables.
+template <int NK, int RSD = 0>
 __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     Batch src, Batch dst, int ns, int nd, const u64 *__restrict__ tab,
     const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
-    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods, H4Tabs nt) {
+    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods, H4Tabs nt,
+    const u64 *__restrict__ rs, const double2 *__restrict__ rsf) {
+  constexpr bool RS = RSD > 0;
+  constexpr int TW = bc_tgt_words(RSD);
+  const int T = nd - RSD;
   extern __shared__ u64 tb[];
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
   const int cc = blockIdx.x * 64 + wave * 16 + col;
@@ -2360,7 +2379,7 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     const int tl = t < t_split ? t : t + t_skip;
     const int pt = prime_of(tl, q_limbs, L);
     const ModQ M = mods[pt];
-    u64 *w = tgt + (size_t)t * kBcTgtWords;
+    u64 *w = tgt + (size_t)t * TW;
     w[0] = M.q;
     w[1] = M.qinv;
     w[2] = M.r2;
@@ -2372,13 +2391,27 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     w[7] = dbl_bits(4294967296.0 * qinv);
     w[8] = dbl_bits(q);
     w[9] = (u64)pt;
+    if constexpr (RS) {
+      if (t < T) {
+#pragma unroll
+        for (int j = 0; j < RSD; j++) {
+          const size_t tj = (size_t)t * RSD + j;
+          w[10 + 4 * j] = dbl_bits(rsf[tj].x);
+          w[11 + 4 * j] = dbl_bits(rsf[tj].y);
+          w[12 + 4 * j] = rs[tj];
+          w[13 + 4 * j] = rs[(size_t)T * RSD + tj];
+        }
+      }
+    }
   }
   // the high passes' 15 twiddles of every target's prime (forward) and every
   // source's prime (inverse), 32 words each: fp64 primes as 16 (w, w / q)
   // pairs, others as [16] psi_br and [16] Shoup constants; entry 0 is unused
   // and word 0 holds q.  Each lane group works on its own primes, so these
   // would otherwise be per-lane global loads.
-  u64 *ttw = tgt + (size_t)nd * kBcTgtWords, *stw = ttw + (size_t)nd * 32;
+  u64 *ttw = tgt + (size_t)nd * TW, *stw = ttw + (size_t)nd * 32;
+  // RS: the lifts, [RSD][16 rows][64 columns of the block]
+  u64 *lift = stw + (size_t)ns * 32;
   for (int idx = threadIdx.x; idx < (nd + ns) * 16; idx += TPB) {
     const int t = idx >> 4, j = idx & 15;
     const bool src_side = t >= nd;
@@ -2449,15 +2482,24 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
   }
   __syncthreads();
   const int quad = n_tg * 512;
-  for (int tg = 0; tg < n_tg; tg++) {
+  // 3-4 run in passes (tg, h): target group tg, rows e = 2 h, 2 h + 1 of its
+  // MFMA output (targets 16 tg + 4 e + g), so that a lane keeps two target
+  // columns (y) beside its sources (a) in registers; each pass recomputes
+  // the group's MFMAs.  RS: the pass of the dropped targets goes first.
+  const int first = RS ? ((nd - 1) >> 3) : 0;  // = 2 tg + h of the last target
+  for (int pp = 0; pp < 2 * n_tg; pp++) {
+    const int pq = RS ? (pp == 0 ? first : (pp <= first ? pp - 1 : pp)) : pp;
+    const int tg = pq >> 1, h = pq & 1;
+    if (16 * tg + 8 * h >= nd) continue;  // no target in this pass
     const bool wide = (wide_mask >> tg) & 1;
     const u64 *mt = tb + tg * 512 + lane;
-    // 3: values of targets 16 tg + 4 e + g at rows 0..15 (for targets below
-    // 2^45 exact doubles congruent to the residue, as bits; words otherwise)
-    u64 y[4][16];
+    // 3: values of targets 16 tg + 4 (2 h + ee) + g at rows 0..15 (for
+    // targets below 2^45 exact doubles congruent to the residue, as bits;
+    // words otherwise)
+    u64 y[2][16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      double lo[4], hi[4];
+      double lo[2], hi[2];
 #pragma unroll
       for (int pr = 0; pr < 4; pr++) {
         if (pr >= 3 && !wide) continue;  // digits 6, 7 of a narrow table are 0
@@ -2470,27 +2512,28 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
           c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, a[i][r], c1, 0, 0, 0);
         }
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          if (16 * tg + 4 * e >= nd) continue;  // no lane group holds a target
-          const double d = (double)(c0[e] + 256 * c1[e]);
-          if (pr == 0) lo[e] = d;
-          else if (pr == 1) lo[e] = __fma_rn(d, 65536.0, lo[e]);
-          else if (pr == 2) hi[e] = d;
-          else hi[e] = __fma_rn(d, 65536.0, hi[e]);
+        for (int ee = 0; ee < 2; ee++) {
+          if (16 * tg + 4 * (2 * h + ee) >= nd) continue;  // no lane group holds one
+          const int c0e = h ? c0[2 + ee] : c0[ee], c1e = h ? c1[2 + ee] : c1[ee];
+          const double d = (double)(c0e + 256 * c1e);
+          if (pr == 0) lo[ee] = d;
+          else if (pr == 1) lo[ee] = __fma_rn(d, 65536.0, lo[ee]);
+          else if (pr == 2) hi[ee] = d;
+          else hi[ee] = __fma_rn(d, 65536.0, hi[ee]);
         }
       }
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = 16 * tg + 4 * e + g;
-        if (16 * tg + 4 * e >= nd || t >= nd) continue;
-        const u64 *w = tgt + (size_t)t * kBcTgtWords;
+      for (int ee = 0; ee < 2; ee++) {
+        const int t = 16 * tg + 4 * (2 * h + ee) + g;
+        if (16 * tg + 4 * (2 * h + ee) >= nd || t >= nd) continue;
+        const u64 *w = tgt + (size_t)t * TW;
         if (w[0] < kFpPrimeBound) {
           // |y| < q / 2 + 2^45.1 < 2^46: the forward passes take it as it is
           // (|x| grows by at most q per stage, 16 stages, below 2^50)
           const double q = as_dbl(w[8]), w32q = as_dbl(w[7]);
-          const double tq = fp_rint(__dmul_rn(hi[e], w32q));
-          const double yv = __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[e], 4294967296.0)), lo[e]);
-          y[e][r] = dbl_bits(yv);
+          const double tq = fp_rint(__dmul_rn(hi[ee], w32q));
+          const double yv = __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[ee], 4294967296.0)), lo[ee]);
+          y[ee][r] = dbl_bits(yv);
         } else {
           ModQ M;
           M.q = w[0];
@@ -2499,41 +2542,116 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
           M.mu = w[3];
           M.k = (u32)w[4];
           M.pad = (u32)(w[4] >> 32);
-          const long long hv = dbl_to_i51(hi[e]), lv = dbl_to_i51(lo[e]);
-          const u64 h = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
-          const u64 l = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
-          y[e][r] = add_mod(mul_mod(h, 1ull << 32, M), l, M.q);
+          const long long hv = dbl_to_i51(hi[ee]), lv = dbl_to_i51(lo[ee]);
+          const u64 hh = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
+          const u64 ll = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
+          y[ee][r] = add_mod(mul_mod(hh, 1ull << 32, M), ll, M.q);
+        }
+      }
+    }
+    if constexpr (RS) {
+      if (pp == 0) {
+        // the lifts, in the lanes of each dropped target (fp64 primes; the
+        // transposed order puts target t in lane group t % 4, row t % 16 / 4)
+        const u64 *rpinv = rs + 2 * (size_t)T * RSD;
+        const u64 *rchain = rpinv + 2 * RSD;
+#pragma unroll
+        for (int j = 0; j < RSD; j++) {
+          const int td = nd - 1 - j, ee_d = ((td & 15) >> 2) & 1;
+          if (g == (td & 3)) {
+            const u64 *wd = tgt + (size_t)td * TW;
+            ModQ Mj;
+            Mj.q = wd[0];
+            Mj.qinv = wd[1];
+            Mj.r2 = wd[2];
+            Mj.mu = wd[3];
+            Mj.k = (u32)wd[4];
+            Mj.pad = (u32)(wd[4] >> 32);
+            const u64 qd = Mj.q;
+            const double q = as_dbl(wd[8]), qinv = as_dbl(wd[5]);
+            const u64 pinv = rpinv[2 * j], pinvs = rpinv[2 * j + 1];
+            const u64 *xs = in + ((size_t)(ns + RSD - 1 - j) << 16);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              // a mask select, so that y keeps static indices
+              const u64 msk = 0ull - (u64)ee_d;
+              const u64 yd = fp_canon(as_dbl((y[0][r] & ~msk) | (y[1][r] & msk)), qinv, q);
+              u64 u = shoup_mul(sub_mod(xs[4096 * r], yd, qd), pinv, pinvs, qd);
+#pragma unroll
+              for (int m = 0; m < j; m++) {
+                const u64 *cm = rchain + 3 * ((size_t)j * RSD + m);
+                const u64 rmv = lift[(m * 16 + r) * 64 + wave * 16 + col];
+                const u64 qm = tgt[(size_t)(nd - 1 - m) * TW];
+                u64 rm = barrett(0, rmv, Mj);
+                if (rmv > (qm - 1) / 2) rm = sub_mod(rm, cm[0], qd);
+                u = shoup_mul(sub_mod(u, rm, qd), cm[1], cm[2], qd);
+              }
+              lift[(j * 16 + r) * 64 + wave * 16 + col] = u;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      // every kept target adds its lifts
+#pragma unroll
+      for (int ee = 0; ee < 2; ee++) {
+        const int t = 16 * tg + 4 * (2 * h + ee) + g;
+        if (16 * tg + 4 * (2 * h + ee) >= nd || t >= T) continue;
+        const u64 *w = tgt + (size_t)t * TW;
+#pragma unroll
+        for (int j = 0; j < RSD; j++) {
+          const u64 qj = tgt[(size_t)(nd - 1 - j) * TW];
+          if (w[0] < kFpPrimeBound) {
+            const double q = as_dbl(w[8]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const u64 rj = lift[(j * 16 + r) * 64 + wave * 16 + col];
+              double yv = __dadd_rn(as_dbl(y[ee][r]), fp_mulmod(u52_to_dbl(rj), as_dbl(w[10 + 4 * j]),
+                                                                  as_dbl(w[11 + 4 * j]), q));
+              if (rj > (qj - 1) / 2) yv = __dsub_rn(yv, u52_to_dbl(w[13 + 4 * j]));
+              y[ee][r] = dbl_bits(yv);
+            }
+          } else {
+            const u64 qu = w[0], qinvm = w[1], pmM = w[12 + 4 * j];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const u64 rj = lift[(j * 16 + r) * 64 + wave * 16 + col];
+              u64 yw = add_mod(y[ee][r], redc(__umul64hi(rj, pmM), rj * pmM, qu, qinvm), qu);
+              if (rj > (qj - 1) / 2) yw = sub_mod(yw, w[13 + 4 * j], qu);
+              y[ee][r] = yw;
+            }
+          }
         }
       }
     }
     // 4: forward high pass of each target column, stored for the low pass
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int t = 16 * tg + 4 * e + g;
-      if (16 * tg + 4 * e >= nd || t >= nd) continue;
-      const u64 *w = tgt + (size_t)t * kBcTgtWords;
+    for (int ee = 0; ee < 2; ee++) {
+      const int t = 16 * tg + 4 * (2 * h + ee) + g;
+      if (16 * tg + 4 * (2 * h + ee) >= nd || t >= T) continue;
+      const u64 *w = tgt + (size_t)t * TW;
       const u64 *tw0 = ttw + (size_t)t * 32;
       u64 *po = out + ((size_t)w[6] << 16);
       if (w[0] < kFpPrimeBound) {
         double xd[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) xd[r] = as_dbl(y[e][r]);
+        for (int r = 0; r < 16; r++) xd[r] = as_dbl(y[ee][r]);
         fp_high_fwd(xd, reinterpret_cast<const double2 *>(tw0), as_dbl(w[8]));
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
       } else {
         const u64 qu = w[0];
-        u64_high_fwd(y[e], tw0, tw0 + 16, qu, 2 * qu);
+        u64_high_fwd(y[ee], tw0, tw0 + 16, qu, 2 * qu);
 #pragma unroll
-        for (int r = 0; r < 16; r++) po[4096 * r] = y[e][r];
+        for (int r = 0; r < 16; r++) po[4096 * r] = y[ee][r];
       }
     }
   }
 }
 
-static size_t convert_h4_lds(const BCTable &t) {
-  return sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * kBcTgtWords +
-                        32 * (size_t)(t.nd + t.ns));
+static size_t convert_h4_lds(const BCTable &t, int rsd = 0) {
+  return sizeof(u64) * ((size_t)t.n_k * t.n_tg * 512 + (size_t)t.nd * bc_tgt_words(rsd) +
+                        32 * (size_t)(t.nd + t.ns) + (size_t)rsd * 16 * 64);
 }
 
 bool convert_h4_ok(const ckks_context *c, const BCTable &t) {
@@ -2548,14 +2666,45 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
             (double)c->N * n_items * t.ns * t.nd);
   if (!convert_h4_ok(c, t)) throw std::invalid_argument("tile-resident conversion: shape");
   if (n_items <= 0) return;
-  auto kern = t.n_k == 1 ? k_convert_h4<1> : t.n_k == 2 ? k_convert_h4<2> : k_convert_h4<3>;
+  auto kern = t.n_k == 1 ? k_convert_h4<1, 0> : t.n_k == 2 ? k_convert_h4<2, 0> : k_convert_h4<3, 0>;
   const size_t lds = convert_h4_lds(t);
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
   hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
                      t.sn, t.mt, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
-                     centered ? 1 : 0, c->d_mods, nt);
+                     centered ? 1 : 0, c->d_mods, nt, (const u64 *)nullptr,
+                     (const double2 *)nullptr);
+  LAUNCH_CHECK();
+}
+
+bool convert_h4_rs_ok(const ckks_context *c, const BCTable &t, int D) {
+  // the dropped targets in one pass of the kernel (one group, one half)
+  if (!(D >= 1 && D <= 2 && t.nd > D && convert_h4_ok(c, t) && convert_h4_lds(t, D) <= 65536 &&
+        ((t.nd - 1) >> 3) == ((t.nd - D) >> 3)))
+    return false;
+  for (int j = 0; j < D; j++)
+    if (c->primes[t.nd - 1 - j] >= kFpPrimeBound) return false;
+  return true;
+}
+
+void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
+                          const BCTable &t, int D, const u64 *rtab) {
+  KTimer kt(c, "convert_h4_rescale", 8.0 * c->N * n_items * (t.ns + D + t.nd - D),
+            (double)c->N * n_items * t.ns * t.nd);
+  if (!convert_h4_rs_ok(c, t, D)) throw std::invalid_argument("tile-resident RS conversion: shape");
+  if (n_items <= 0) return;
+  const int T = t.nd - D;
+  const double2 *rsf =
+      (const double2 *)(rtab + 2 * (size_t)T * D + 2 * (size_t)D + 3 * (size_t)D * D);
+  auto k1 = t.n_k == 1 ? k_convert_h4<1, 1> : t.n_k == 2 ? k_convert_h4<2, 1> : k_convert_h4<3, 1>;
+  auto k2 = t.n_k == 1 ? k_convert_h4<1, 2> : t.n_k == 2 ? k_convert_h4<2, 2> : k_convert_h4<3, 2>;
+  H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
+            (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
+            (const double2 *)c->d_ninv_fp};
+  hipLaunchKernelGGL(D == 1 ? k1 : k2, dim3(64, n_items), dim3(TPB), convert_h4_lds(t, D),
+                     c->stream, src, dst, t.ns, t.nd, t.sn, t.mt, t.n_tg, t.wide_mask, c->L,
+                     t.nd, 0, t.nd, c->L, 1, c->d_mods, nt, rtab, rsf);
   LAUNCH_CHECK();
 }
 
