@@ -1084,6 +1084,9 @@ struct KsJob {
 // The key product of the fp64 Q limbs left by ks_modup_inner for ks_moddown
 // (launch_low_key_moddown): the extended digits and what it multiplies them by.
 struct KsDeferred {
+  // input: the Q limbs [0, below) whose key product may be deferred (-1: all,
+  // where ks_moddown's tile conversion applies)
+  int below = -1;
   bool on = false;
   const u64 *ext = nullptr;
   size_t est = 0;
@@ -1147,7 +1150,8 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
     if (deferred)
       launch_low_key_moddown(c, dk->ext, dk->est, dk->own, n, *dk->key, dk->digits, E, limbs,
                              dk->ginv, strided(conv, (size_t)limbs * N), pinv,
-                             pmod_table(c, limbs), a0, add1_off, gal.data(), o0, out1_off);
+                             pmod_table(c, limbs), a0, add1_off, gal.data(), o0, out1_off,
+                             limbs);
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
                        pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile,
                        deferred);
@@ -1224,7 +1228,8 @@ static u64 galois_inverse(const ckks_context *c, u64 g) {
 // addend per component at a fixed offset, outputs likewise), where the
 // special limbs take the inverse low pass here and the ModDown's conversion
 // runs tile-resident, the fp64 Q limbs' key product is left to ks_moddown
-// (dk->on), which runs it with the combine.
+// (dk->on), which runs it with the combine.  With dk->below >= 0 the caller
+// has checked its own conversion and only Q limbs below it are deferred.
 static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *d,
                            const std::vector<KsJob> &jobs, Scratch &s,
                            const Strided *sp = nullptr, bool *sp_done = nullptr,
@@ -1242,7 +1247,8 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
   Batch ob{};
   for (int i = 0; i < n; i++) ob.p[i] = (u64 *)d[i];
   const u64 ginv = galois_inverse(c, jobs[0].galois);
-  const bool defer = dk && spf && c->ks_defer && c->ks_tile && convert_h4_ok(c, bc_down(c, limbs));
+  const bool defer = dk && spf && c->ks_defer && c->ks_tile &&
+                     (dk->below >= 0 || convert_h4_ok(c, bc_down(c, limbs)));
   if (dk) {
     dk->on = defer;
     if (defer) {
@@ -1255,7 +1261,7 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
     }
   }
   launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
-                     ginv, spf ? sp : nullptr, defer);
+                     ginv, spf ? sp : nullptr, defer ? (dk->below >= 0 ? dk->below : limbs) : 0);
   return acc;
 }
 
@@ -1443,10 +1449,18 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     u64 *x = s.get((size_t)nb * 2 * xs);
     const Strided sp{x, (u64)xs};
     bool sp_done = false;
-    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done);
     // N = 2^16: the special limbs' inverse high pass, the conversion with the
-    // lifts and the forward high pass of the kept limbs in one kernel
+    // lifts and the forward high pass of the kept limbs in one kernel; then,
+    // without a postop, the kept fp64 limbs' key product runs with the
+    // combine (launch_low_key_moddown: (acc + [P] d - conv) (P p)^-1 is
+    // (acc - conv) (P p)^-1 + d p^-1), the dropped limbs' before the lift
     const bool tile = c->logN == 16 && c->ks_tile && convert_h4_rs_ok(c, bt, D);
+    const PostOp po = post_chunk(c, ps, b0, nb);
+    KsDeferred dk;
+    dk.below = T;
+    const bool may_defer = tile && !ps;
+    u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done,
+                              may_defer ? &dk : nullptr);
     if (tile) {
       if (!sp_done)
         launch_ntt_inv_low(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A,
@@ -1475,10 +1489,13 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
                              rt + 4 * (size_t)T);
     std::vector<u64> gal(nb, 1);
     const u64 *amul = rt + 2 * (size_t)T;
-    const PostOp po = post_chunk(c, ps, b0, nb);
     if (c->logN == 16) {
+      if (dk.on)
+        launch_low_key_moddown(c, dk.ext, dk.est, dk.own, nb, *dk.key, dk.digits, E, limbs,
+                               dk.ginv, strided(conv, (size_t)T * N), rt, pmod_table(c, limbs),
+                               d3, P, gal.data(), o0, (u64)T * N, T);
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
-                         d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile);
+                         d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile, dk.on);
     } else {
       Batch a1{}, o1{};
       for (int i = 0; i < nb; i++) {
@@ -1686,6 +1703,7 @@ int ckks_keygen_rotations(ckks_context *c, const int64_t *rot, int n) {
       for (int j = 0; j * c->ds < limbs; j++) bc_up(c, limbs, j);
       bc_down(c, limbs);
       pinv_table(c, limbs);
+      pmod_table(c, limbs);
     }
     c->rotation_tables = true;
   }

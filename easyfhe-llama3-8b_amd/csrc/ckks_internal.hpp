@@ -408,24 +408,25 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
 // sp.stride + (l - q_limbs) N, and are not written to acc: the ModDown then
 // runs launch_ntt_inv_high on them.
 bool low_key_special_fp(const ckks_context *c);
-// defer_fp_q: the Q limbs of fp64 primes are skipped (launch_low_key_moddown
-// runs their key product with the ModDown's combine)
+// The Q limbs of fp64 primes below defer_below are skipped
+// (launch_low_key_moddown runs their key product with the ModDown's combine)
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr,
-                        bool defer_fp_q = false);
+                        int defer_below = 0);
 // N = 2^16: for the Q limbs of fp64 primes, launch_ntt_low_key's key product
 // and launch_ntt_moddown's combine (addends, outputs and postop as there) in
-// one kernel, the accumulator kept in the block; conv holds the ModDown's
-// conversion after the forward high pass (launch_convert_h4), 2 n items of
-// q_limbs limbs; pmod per Q limb [P]_q and its Shoup constant.  The special
+// one kernel, the accumulator kept in the block, for output limbs
+// [0, out_limbs) (q_limbs, or the kept limbs of a relinearise-rescale, whose
+// pinv is (P p_1..p_D)^-1); conv holds the ModDown's conversion after the
+// forward high pass (launch_convert_h4), 2 n items of out_limbs limbs; pmod per Q limb [P]_q and its Shoup constant.  The special
 // limbs' key product and the other Q limbs run through
 // launch_ntt_low_key(defer_fp_q) and launch_ntt_moddown(wide_only).
 void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
-                            u64 out1_off, const PostOp *post = nullptr);
+                            u64 out1_off, int out_limbs, const PostOp *post = nullptr);
 // N = 2^16: the high pass of the inverse NTT alone, in place (after the low
 // pass of launch_ntt_low_key's sp output)
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,

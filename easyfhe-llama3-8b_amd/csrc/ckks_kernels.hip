@@ -1576,11 +1576,12 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
-                            u64 out1_off, const PostOp *post) {
+                            u64 out1_off, int out_limbs, const PostOp *post) {
   KTimer kt(c, "ntt_low_key_moddown",
-            8.0 * c->N * ((double)n_items * (digits * q_limbs + 7.0 * q_limbs) +
-                          2.0 * digits * q_limbs),
-            2.0 * c->N * q_limbs * digits * n_items + 0.5 * c->N * 12 * 2.0 * n_items * q_limbs);
+            8.0 * c->N * ((double)n_items * (digits * out_limbs + 7.0 * out_limbs) +
+                          2.0 * digits * out_limbs),
+            2.0 * c->N * out_limbs * digits * n_items +
+                0.5 * c->N * 12 * 2.0 * n_items * out_limbs);
   if (n_items <= 0) return;
   if (post && (post->dbl || post->scal || batch_ptr_host(post->sub, 0)))
     throw std::invalid_argument("fused key product + ModDown: no postop");
@@ -1594,13 +1595,15 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
   md.out1_off = out1_off;
   if (post) md.post = *post;
   for (int i = 0; i < n_items; i++) md.gal.g[i] = galois[i];
-  for (int l0 = 0; l0 < q_limbs;) {
+  if (out_limbs < 1 || out_limbs > q_limbs)
+    throw std::invalid_argument("fused key product + ModDown: output limbs");
+  for (int l0 = 0; l0 < out_limbs;) {
     if (!c->prime_fp[l0]) {
       l0++;
       continue;
     }
     int l1 = l0 + 1;
-    while (l1 < q_limbs && c->prime_fp[l1]) l1++;
+    while (l1 < out_limbs && c->prime_fp[l1]) l1++;
     hipLaunchKernelGGL(k_low_key_md, dim3(n_items * 16 * (l1 - l0)), dim3(TPB), 0, c->stream, a,
                        md, conv, pmod, l0, n_items, c->d_mods, (const double2 *)c->d_tw_fp,
                        (const double2 *)c->d_rinv_fp);
@@ -1612,7 +1615,7 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp,
-                        bool defer_fp_q) {
+                        int defer_below) {
   KTimer kt(c, "ntt_low_key",
             8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
@@ -1630,13 +1633,15 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
   // primes the 64-bit one)
   // (with sp, the special limbs (all fp64) form a run of their own)
   auto fp_limb = [&](int l) { return c->prime_fp[l < q_limbs ? l : c->L + (l - q_limbs)] != 0; };
-  auto kind = [&](int l) { return fp_limb(l) ? (sp && l >= q_limbs ? 2 : 1) : 0; };
+  // (kind 3: fp64 Q limbs below defer_below, left to launch_low_key_moddown)
+  auto kind = [&](int l) {
+    return fp_limb(l) ? (sp && l >= q_limbs ? 2 : (l < defer_below ? 3 : 1)) : 0;
+  };
   for (int l0 = 0; l0 < E;) {
     const int k = kind(l0);
     int l1 = l0 + 1;
     while (l1 < E && kind(l1) == k) l1++;
-    if (defer_fp_q && k == 1 && l0 < q_limbs) {
-      // fp64 Q limbs left to launch_low_key_moddown
+    if (k == 3) {
       l0 = l1;
       continue;
     }
