@@ -615,11 +615,10 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
 // Between the two passes the data is stored as raw double bits.
 // ---------------------------------------------------------------------------
 
-#define FP_ROUND_C 6755399441055744.0  // 1.5 * 2^52: (y + C) - C rounds |y| < 2^51
+#define FP_ROUND_C 6755399441055744.0  // 1.5 * 2^52: y + C keeps round(y) in its low bits
 
-__device__ __forceinline__ double fp_rint(double y) {
-  return __dsub_rn(__dadd_rn(y, FP_ROUND_C), FP_ROUND_C);
-}
+// round to nearest, ties to even (one v_rndne_f64)
+__device__ __forceinline__ double fp_rint(double y) { return __builtin_rint(y); }
 
 __device__ __forceinline__ double fp_mulmod(double a, double w, double wq, double q) {
   const double hi = __dmul_rn(a, w);
