@@ -404,7 +404,7 @@ def main() -> int:
         c.release()
     prof = ctx.profile_read()
     ctx.profile(False)
-    ctx.set_split_parts(3)
+    ctx.set_split_parts(0)
     result["int_peak"] = peaks
     result["kernels"] = kernel_table(prof, peaks)
     kernel_bytes = sum(v["bytes"] for v in prof.values())

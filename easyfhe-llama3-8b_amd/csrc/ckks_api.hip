@@ -3338,9 +3338,9 @@ int ckks_profile_read(ckks_context *c, char *buf, size_t len) {
 int ckks_set_split_parts(ckks_context *c, int parts) {
   API_BEGIN
   require(c, "null argument");
-  require(parts >= 1 && parts <= c->split_streams,
-          "split parts must be 1 .. the count the context was created with");
-  c->split_parts = parts;
+  require(parts >= 0 && parts <= c->split_streams,
+          "split parts must be 0 .. the count the context was created with");
+  c->split_parts = parts ? parts : c->split_streams;
   API_END
 }
 

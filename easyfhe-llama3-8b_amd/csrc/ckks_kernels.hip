@@ -1432,13 +1432,13 @@ __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_be
 // N = 2^16, fp64 Q limbs: the key product of one (item, tile, limb) and the
 // ModDown's combine of the output tile it maps to, with the accumulator kept
 // in the block.  After the key product (low_key_fp_acc) each component's
-// words, x 2^-64 and canonical, go through the LDS tile to their output
+// values, x 2^-64 plus [P] addend, go through the LDS tile to their output
 // positions t = autom_index(s, g^-1) (an aligned tile onto an aligned tile),
 // so that thread (rl, c0) holds output words tb + rl 256 + c0 + 16 k.  Then,
 // per component, the forward low pass of the converted special part (conv:
 // launch_convert_h4's output for this limb and output tile) and
-//   out = (acc - NTT(conv)) P^-1 + addend (+ postop),
-// the words of launch_ntt_low_key then launch_ntt_moddown.  The special
+//   out = (acc - NTT(conv)) P^-1 + addend,
+// the words of launch_ntt_low_key then launch_ntt_moddown (no postop).  The special
 // limbs' key product (and their inverse low pass) and the ModDown's
 // conversion run before it.
 // ===========================================================================
@@ -1448,49 +1448,47 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
                                                        const ModQ *__restrict__ mods,
                                                        const double2 *__restrict__ tw,
                                                        const double2 *__restrict__ rinv) {
-  // tile 0: the working tile; tile 1: component 1's accumulator words in
+  // tile 0: the working tile; tile 1: component 1's accumulator values in
   // their output order until its combine
   __shared__ u64 lds[2 * 16 * 272];
-  double *sm = reinterpret_cast<double *>(lds);
-  u64 *smu = lds, *acc1t = lds + 16 * 272;
+  double *sm = reinterpret_cast<double *>(lds), *acc1t = sm + 16 * 272;
   const int b = blockIdx.x, r0 = b >> 3;
   const int it = r0 % n_items, tl = (r0 / n_items) * 8 + (b & 7);
   const int tile = tl & 15, l = l_begin + (tl >> 4);
   const int p = prime_of(l, a.q_limbs, a.L);
-  const u64 qu = mods[p].q;
-  const double q = (double)qu, qinv = 1.0 / q;
+  const double q = (double)mods[p].q, qinv = 1.0 / q;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
   double acc0[16], acc1[16];
   low_key_fp_acc(sm, a, it, tile, l, p, mods, tw, acc0, acc1);
+  // Everything below stays in fp64: signed exact integers congruent to the
+  // words, reduced to [0, q) once at the store.  The addend of output t is
+  // the word at sigma(t) = s: the thread holds it at its own positions, so
+  // (acc - conv) P^-1 + add is taken as (acc + [P] add - conv) P^-1, with
+  // add read here in source order.  Bounds: acc 2^-64 and [P] add each in
+  // [-q, q]; the converted part after its 16 forward stages below 2^49.2
+  // (entry below 2^46, at most q more per stage), so the factor of P^-1
+  // sees less than 2^49.3 < 2^50, as fp_mulmod needs.
   const double2 ri = rinv[p];
-  auto canon = [&](double x) {
-    const double rr = fp_reduce(fp_mulmod(x, ri.x, ri.y, q), qinv, q);
-    return dbl_to_u52(rr < 0.0 ? __dadd_rn(rr, q) : rr);
-  };
-  // The addend of output t is the word at sigma(t) = s: the thread holds it
-  // at its own positions, so (acc - conv) P^-1 + add is taken as
-  // (acc + [P] add - conv) P^-1, with add read here in source order.
-  const u64 Pm = pmod[2 * l], Pms = pmod[2 * l + 1];
+  const double Pm = (double)pmod[2 * l], Pmq = __dmul_rn(Pm, qinv);
   const u64 *ad0 = batch_ptr(md.add, it);
   const u64 *ad1 = (ad0 && md.add1_off) ? ad0 + md.add1_off : nullptr;
-  u64 w0[16], w1[16];
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    w0[i] = canon(acc0[i]);
-    w1[i] = canon(acc1[i]);
+    acc0[i] = fp_mulmod(acc0[i], ri.x, ri.y, q);
+    acc1[i] = fp_mulmod(acc1[i], ri.x, ri.y, q);
   }
   if (ad0) {
     u64 d[16];
     load16(ad0 + ((size_t)l << 16) + sb, d);
 #pragma unroll
-    for (int i = 0; i < 16; i++) w0[i] = add_mod(w0[i], shoup_mul(d[i], Pm, Pms, qu), qu);
+    for (int i = 0; i < 16; i++) acc0[i] = __dadd_rn(acc0[i], fp_mulmod(u52_to_dbl(d[i]), Pm, Pmq, q));
   }
   if (ad1) {
     u64 d[16];
     load16(ad1 + ((size_t)l << 16) + sb, d);
 #pragma unroll
-    for (int i = 0; i < 16; i++) w1[i] = add_mod(w1[i], shoup_mul(d[i], Pm, Pms, qu), qu);
+    for (int i = 0; i < 16; i++) acc1[i] = __dadd_rn(acc1[i], fp_mulmod(u52_to_dbl(d[i]), Pm, Pmq, q));
   }
   // sigma maps the block's tile onto one output tile: the same base for
   // every thread (uniform, so the low pass's twiddles stay scalar loads)
@@ -1501,17 +1499,17 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const u32 t = a.ginv == 1 ? sb + i : autom_index(sb + i, a.ginv, 16);
-    smu[lds16((t >> 8) & 15, t & 255)] = w0[i];
-    acc1t[lds16((t >> 8) & 15, t & 255)] = w1[i];
+    sm[lds16((t >> 8) & 15, t & 255)] = acc0[i];
+    acc1t[lds16((t >> 8) & 15, t & 255)] = acc1[i];
   }
   __syncthreads();
-  u64 av[16];
+  double av[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++) av[k] = smu[lds16(rl, c0 + 16 * k)];
+  for (int k = 0; k < 16; k++) av[k] = sm[lds16(rl, c0 + 16 * k)];
   const double2 *T = tw + ((size_t)p << 16);
   const int row = ot * 16 + rl;
   const u32 e0 = tb + rl * 256 + c0;
-  const u64 pinv = md.pinv[2 * l], pinvs = md.pinv[2 * l + 1];
+  const double pinv = (double)md.pinv[2 * l], pinvq = __dmul_rn(pinv, qinv);
 #pragma unroll 1
   for (int comp = 0; comp < 2; comp++) {
     // forward low pass of conv's output tile
@@ -1531,13 +1529,14 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
     fp_low_round_b(x, T, row, c0, q);
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 16; j++) smu[lds16(rl, 16 * c0 + j)] = fp_canon(x[j], qinv, q);
+    for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
     __syncthreads();
     u64 *o = batch_ptr(md.out, it) + (comp ? md.out1_off : 0) + ((size_t)l << 16);
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const u64 acc = comp ? acc1t[lds16(rl, c0 + 16 * k)] : av[k];
-      o[e0 + 16 * k] = shoup_mul(sub_mod(acc, smu[lds16(rl, c0 + 16 * k)], qu), pinv, pinvs, qu);
+      const double acc = comp ? acc1t[lds16(rl, c0 + 16 * k)] : av[k];
+      const double v = __dsub_rn(acc, sm[lds16(rl, c0 + 16 * k)]);
+      o[e0 + 16 * k] = fp_canon(fp_mulmod(v, pinv, pinvq, q), qinv, q);
     }
   }
 }

@@ -196,7 +196,7 @@ class NativeContext:
 
     def set_split_parts(self, parts: int) -> None:
         """Streams a batched key switch is split over (1 to the count the
-        context was created with)."""
+        context was created with; 0 restores that count)."""
         check(lib.ckks_set_split_parts(self._h, int(parts)))
 
     def profile(self, enable: bool = True) -> None:

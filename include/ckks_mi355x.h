@@ -377,7 +377,7 @@ void ckks_event_destroy(ckks_event *ev);
 /* Streams a batched key switch of at least 16 ciphertexts is split over
  * (1 .. the count set at creation by CKKS_SPLIT_STREAMS, default 3); no
  * counterpart in the reference, whose library runs one stream.  1 gives the
- * one-stream order per-kernel timings need. */
+ * one-stream order per-kernel timings need; 0 restores the creation count. */
 int ckks_set_split_parts(ckks_context *ctx, int parts);
 
 /* The operation audit of the reference's graph audit (graph.py:348
