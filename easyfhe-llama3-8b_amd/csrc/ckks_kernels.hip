@@ -2495,7 +2495,10 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     const int tg = pq >> 1, h = pq & 1;
     if (16 * tg + 8 * h >= nd) continue;  // no target in this pass
     const bool wide = (wide_mask >> tg) & 1;
-    const u64 *mt = tb + tg * 512 + lane;
+    // lane m + 16 k supplies row m of the table operand; reading row
+    // (m & 12) | ((m + 2 h) & 3) instead puts targets 16 tg + 4 (2 h + ee) + g
+    // at accumulator entries ee = 0, 1 of lane group g (static indices)
+    const u64 *mt = tb + tg * 512 + ((lane & ~3) | ((lane + 2 * h) & 3));
     // 3: values of targets 16 tg + 4 (2 h + ee) + g at rows 0..15 (for
     // targets below 2^45 exact doubles congruent to the residue, as bits;
     // words otherwise)
@@ -2517,7 +2520,7 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 #pragma unroll
         for (int ee = 0; ee < 2; ee++) {
           if (16 * tg + 4 * (2 * h + ee) >= nd) continue;  // no lane group holds one
-          const int c0e = h ? c0[2 + ee] : c0[ee], c1e = h ? c1[2 + ee] : c1[ee];
+          const int c0e = c0[ee], c1e = c1[ee];
           const double d = (double)(c0e + 256 * c1e);
           if (pr == 0) lo[ee] = d;
           else if (pr == 1) lo[ee] = __fma_rn(d, 65536.0, lo[ee]);
