@@ -4,6 +4,7 @@
 // uint64 limb arrays of N residues; the NTT domain is the bit-reversed
 // evaluation order a_hat[i] = a(psi^(2 br(i) + 1)).
 #include <math.h>
+#include <type_traits>
 
 #include "ckks_internal.hpp"
 
@@ -2501,57 +2502,68 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     const u64 *mt = tb + tg * 512 + ((lane & ~3) | ((lane + 2 * h) & 3));
     // 3: values of targets 16 tg + 4 (2 h + ee) + g at rows 0..15 (for
     // targets below 2^45 exact doubles congruent to the residue, as bits;
-    // words otherwise)
+    // words otherwise).  The lane's two targets' constants are read once per
+    // pass; lanes without a target (past nd) compute unused values on the
+    // fp64 path.
+    bool fpt[2];
+    double tqd[2], tw32[2];
+#pragma unroll
+    for (int ee = 0; ee < 2; ee++) {
+      const int t = 16 * tg + 4 * (2 * h + ee) + g;
+      const bool tv = t < nd;
+      const u64 *w = tgt + (size_t)(tv ? t : 0) * TW;
+      fpt[ee] = !tv || w[0] < kFpPrimeBound;
+      tqd[ee] = as_dbl(w[8]);
+      tw32[ee] = as_dbl(w[7]);
+    }
     u64 y[2][16];
+    {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      double lo[2], hi[2];
+      for (int r = 0; r < 16; r++) {
+        double lo[2], hi[2];
 #pragma unroll
-      for (int pr = 0; pr < 4; pr++) {
-        if (pr >= 3 && !wide) continue;  // digits 6, 7 of a narrow table are 0
-        v4i c0 = v4i{0, 0, 0, 0}, c1 = v4i{0, 0, 0, 0};
+        for (int pr = 0; pr < 4; pr++) {
+          if (pr >= 3 && !wide) continue;  // digits 6, 7 of a narrow table are 0
+          v4i c0 = v4i{0, 0, 0, 0}, c1 = v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < NK; i++) {
-          const long b0 = (long)mt[i * quad + (2 * pr) * 64];
-          const long b1 = (long)mt[i * quad + (2 * pr + 1) * 64];
-          c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b0, a[i][r], c0, 0, 0, 0);
-          c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, a[i][r], c1, 0, 0, 0);
+          for (int i = 0; i < NK; i++) {
+            const long b0 = (long)mt[i * quad + (2 * pr) * 64];
+            const long b1 = (long)mt[i * quad + (2 * pr + 1) * 64];
+            c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b0, a[i][r], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b1, a[i][r], c1, 0, 0, 0);
+          }
+#pragma unroll
+          for (int ee = 0; ee < 2; ee++) {
+            const double d = (double)(c0[ee] + 256 * c1[ee]);
+            if (pr == 0) lo[ee] = d;
+            else if (pr == 1) lo[ee] = __fma_rn(d, 65536.0, lo[ee]);
+            else if (pr == 2) hi[ee] = d;
+            else hi[ee] = __fma_rn(d, 65536.0, hi[ee]);
+          }
         }
 #pragma unroll
         for (int ee = 0; ee < 2; ee++) {
-          if (16 * tg + 4 * (2 * h + ee) >= nd) continue;  // no lane group holds one
-          const int c0e = c0[ee], c1e = c1[ee];
-          const double d = (double)(c0e + 256 * c1e);
-          if (pr == 0) lo[ee] = d;
-          else if (pr == 1) lo[ee] = __fma_rn(d, 65536.0, lo[ee]);
-          else if (pr == 2) hi[ee] = d;
-          else hi[ee] = __fma_rn(d, 65536.0, hi[ee]);
-        }
-      }
-#pragma unroll
-      for (int ee = 0; ee < 2; ee++) {
-        const int t = 16 * tg + 4 * (2 * h + ee) + g;
-        if (16 * tg + 4 * (2 * h + ee) >= nd || t >= nd) continue;
-        const u64 *w = tgt + (size_t)t * TW;
-        if (w[0] < kFpPrimeBound) {
-          // |y| < q / 2 + 2^45.1 < 2^46: the forward passes take it as it is
-          // (|x| grows by at most q per stage, 16 stages, below 2^50)
-          const double q = as_dbl(w[8]), w32q = as_dbl(w[7]);
-          const double tq = fp_rint(__dmul_rn(hi[ee], w32q));
-          const double yv = __dadd_rn(__fma_rn(-tq, q, __dmul_rn(hi[ee], 4294967296.0)), lo[ee]);
-          y[ee][r] = dbl_bits(yv);
-        } else {
-          ModQ M;
-          M.q = w[0];
-          M.qinv = w[1];
-          M.r2 = w[2];
-          M.mu = w[3];
-          M.k = (u32)w[4];
-          M.pad = (u32)(w[4] >> 32);
-          const long long hv = dbl_to_i51(hi[ee]), lv = dbl_to_i51(lo[ee]);
-          const u64 hh = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
-          const u64 ll = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
-          y[ee][r] = add_mod(mul_mod(hh, 1ull << 32, M), ll, M.q);
+          // fp64 targets: |y| < q / 2 + 2^45.1 < 2^46, which the forward
+          // passes take as it is (|x| grows by at most q per stage, 16
+          // stages, below 2^50)
+          const double tq = fp_rint(__dmul_rn(hi[ee], tw32[ee]));
+          u64 yv = dbl_bits(
+              __dadd_rn(__fma_rn(-tq, tqd[ee], __dmul_rn(hi[ee], 4294967296.0)), lo[ee]));
+          if (!fpt[ee]) {
+            const u64 *w = tgt + (size_t)(16 * tg + 4 * (2 * h + ee) + g) * TW;
+            ModQ M;
+            M.q = w[0];
+            M.qinv = w[1];
+            M.r2 = w[2];
+            M.mu = w[3];
+            M.k = (u32)w[4];
+            M.pad = (u32)(w[4] >> 32);
+            const long long hv = dbl_to_i51(hi[ee]), lv = dbl_to_i51(lo[ee]);
+            const u64 hh = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
+            const u64 ll = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
+            yv = add_mod(mul_mod(hh, 1ull << 32, M), ll, M.q);
+          }
+          y[ee][r] = yv;
         }
       }
     }
