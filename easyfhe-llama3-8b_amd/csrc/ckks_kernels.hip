@@ -2464,20 +2464,27 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 #pragma unroll
         for (int r = 0; r < 16; r++) xd[r] = as_dbl(x[r]);
         fp_high_inv_stages(xd, reinterpret_cast<const double2 *>(sw0), q, qinv);
+        // fp_reduce of the product (in [-q, q]) leaves [-(q+1)/2, (q+1)/2]; a
+        // second one gives the centered representative, |v| <= (q-1)/2, and
+        // v < 0 ? v + q : v the canonical one.  The word of 1.5 2^52 + v is
+        // that of 1.5 2^52 plus v, so one 64-bit add gives the bytes' offset
+        // form of v's two's complement.
+        constexpr u64 kBal = 0x8080808080808080ull - 0x4338000000000000ull;
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          x[r] = dbl_to_u52(fp_canon_d(fp_mulmod(xd[r], wn.x, wn.y, q), qinv, q));
+        for (int r = 0; r < 16; r++) {
+          double v = fp_reduce(fp_mulmod(xd[r], wn.x, wn.y, q), qinv, q);
+          v = centered ? fp_reduce(v, qinv, q) : (v < 0.0 ? __dadd_rn(v, q) : v);
+          a[i][r] = (long)((dbl_bits(__dadd_rn(v, FP_ROUND_C)) + kBal) ^ 0x8080808080808080ull);
+        }
       } else {
         u64_high_inv_stages(x, sw0, sw0 + 16, qu, 2 * qu);
         const u64 sw = tab[s], sws = tab[ns + s];
 #pragma unroll
-        for (int r = 0; r < 16; r++) x[r] = shoup_mul(x[r], sw, sws, qu);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        u64 v = x[r];
-        if (centered && v > (qu - 1) / 2) v -= qu;  // two's complement of v - q
-        a[i][r] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
+        for (int r = 0; r < 16; r++) {
+          u64 v = shoup_mul(x[r], sw, sws, qu);
+          if (centered && v > (qu - 1) / 2) v -= qu;  // two's complement of v - q
+          a[i][r] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
+        }
       }
     } else {
 #pragma unroll
