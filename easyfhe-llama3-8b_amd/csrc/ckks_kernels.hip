@@ -260,6 +260,23 @@ __device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u6
 
 __device__ __forceinline__ int lds16(int r, int c) { return r * 272 + c + (c >> 4); }
 
+// The 16 threads of tile row rl (threads 16 rl .. 16 rl + 15) belong to one
+// wave, and the LDS serves one wave's instructions in order: an exchange
+// within rows needs only that the compiler keeps the wave's LDS accesses on
+// their side of this point, not a workgroup barrier.
+__device__ __forceinline__ void row_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// row_sync when every thread's accesses on both sides stay in its row, a
+// workgroup barrier otherwise (rows: wave-uniform)
+__device__ __forceinline__ void tile_sync(bool rows) {
+  if (rows) row_sync();
+  else __syncthreads();
+}
+
 // ModDown epilogue of the forward low pass (conv items 2 i + c):
 // out_c[l][k] = (acc_c[l][k] - NTT(conv_c)[l][k]) P^-1 + add_c[l][sigma(k)]
 struct Galois64 {
@@ -515,19 +532,19 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
   u64_low_round_a(x, W, Ws, row, q, q2);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
-  __syncthreads();
+  row_sync();
   // round B: column = 16 c0 + j, stages on column bits 3..0
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
   u64_low_round_b(x, W, Ws, row, c0, q, q2);
   // store through LDS so that adjacent lanes write adjacent words
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     u64 a = x[j] >= q2 ? x[j] - q2 : x[j];
     sm[lds16(rl, 16 * c0 + j)] = a >= q ? a - q : a;
   }
-  __syncthreads();
+  row_sync();
   if constexpr (COMBINE) {
     const u32 e0 = blockIdx.x * 4096 + rl * 256 + c0;
     u64 sv[16];
@@ -563,7 +580,7 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
   // goes through LDS so that adjacent lanes read adjacent words
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = in[rl * 256 + c0 + 16 * k];
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
 #pragma unroll
@@ -576,10 +593,10 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
       gs_bfly(x[j], x[j + half], W[ti], Ws[ti], q, q2);
     }
   }
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
-  __syncthreads();
+  row_sync();
   // round A^-1: column = c0 + 16 k, stages on column bits 4..7
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
@@ -826,15 +843,15 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
   fp_low_round_a(x, T, row, q);
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
   fp_low_round_b(x, T, row, c0, q);
-  __syncthreads();
+  row_sync();
   u64 *smu = reinterpret_cast<u64 *>(sm);
 #pragma unroll
   for (int j = 0; j < 16; j++) smu[lds16(rl, 16 * c0 + j)] = fp_canon(x[j], qinv, q);
-  __syncthreads();
+  row_sync();
   if constexpr (COMBINE) {
     const u64 qu = mods[p].q;
     const u32 e0 = blockIdx.x * 4096 + rl * 256 + c0;
@@ -876,10 +893,10 @@ __device__ __forceinline__ void fp_inv_low_tile(double *__restrict__ sm, int til
       gs_fp(x[j], x[j + half], w.x, w.y, q);
     }
   }
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = fp_reduce(sm[lds16(rl, c0 + 16 * k)], qinv, q);
 #pragma unroll
@@ -918,7 +935,7 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
 #pragma unroll
   for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
-  __syncthreads();
+  row_sync();
   fp_inv_low_tile(sm, blockIdx.x, T, q, qinv, out);
 }
 
@@ -1287,7 +1304,7 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
       fp_low_round_a(y, T, row, q);
 #pragma unroll
       for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
-      __syncthreads();
+      row_sync();
 #pragma unroll
       for (int i = 0; i < 16; i++) y[i] = sm[lds16(rl, 16 * c0 + i)];
       fp_low_round_b(y, T, row, c0, q);
@@ -1374,7 +1391,7 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
       u64_low_round_a(y, W, Ws, row, q, q2);
 #pragma unroll
       for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = y[k];
-      __syncthreads();
+      row_sync();
 #pragma unroll
       for (int i = 0; i < 16; i++) y[i] = sm[lds16(rl, 16 * c0 + i)];
       u64_low_round_b(y, W, Ws, row, c0, q, q2);
@@ -1496,14 +1513,16 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
   const u32 tb = (u32)__builtin_amdgcn_readfirstlane(
       (int)(a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u));
   const int ot = (int)(tb >> 12);
-  __syncthreads();  // the key product's reads of the working tile are done
+  // the key product's reads of the working tile are done (they read the
+  // thread's row, as the identity permutation writes it)
+  tile_sync(a.ginv == 1);
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const u32 t = a.ginv == 1 ? sb + i : autom_index(sb + i, a.ginv, 16);
     sm[lds16((t >> 8) & 15, t & 255)] = acc0[i];
     acc1t[lds16((t >> 8) & 15, t & 255)] = acc1[i];
   }
-  __syncthreads();
+  tile_sync(a.ginv == 1);
   double av[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) av[k] = sm[lds16(rl, c0 + 16 * k)];
@@ -1524,14 +1543,14 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
     fp_low_round_a(x, T, row, q);
 #pragma unroll
     for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = x[k];
-    __syncthreads();
+    row_sync();
 #pragma unroll
     for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
     fp_low_round_b(x, T, row, c0, q);
-    __syncthreads();
+    row_sync();
 #pragma unroll
     for (int j = 0; j < 16; j++) sm[lds16(rl, 16 * c0 + j)] = x[j];
-    __syncthreads();
+    row_sync();
     u64 *o = batch_ptr(md.out, it) + (comp ? md.out1_off : 0) + ((size_t)l << 16);
 #pragma unroll
     for (int k = 0; k < 16; k++) {
