@@ -350,7 +350,7 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
       }
   HIPCHECK(hipMalloc(&t.mt, t.mbytes));
   HIPCHECK(hipMemcpy(t.mt, mt.data(), t.mbytes, hipMemcpyHostToDevice));
-  std::vector<u64> sn(4 * (size_t)ns);
+  std::vector<u64> sn(6 * (size_t)ns);
   const int N = c->N;
   for (int i = 0; i < ns; i++) {
     const u64 qi = src[i];
@@ -361,6 +361,8 @@ static BCTable make_bc(ckks_context *c, const std::vector<u64> &src, const std::
     const double wq = wf / qf;
     memcpy(&sn[2 * ns + 2 * i], &wf, 8);
     memcpy(&sn[2 * ns + 2 * i + 1], &wq, 8);
+    sn[4 * ns + i] = h[i];
+    sn[5 * ns + i] = shoup_h(h[i], qi);
   }
   HIPCHECK(hipMalloc(&t.sn, sizeof(u64) * sn.size()));
   HIPCHECK(hipMemcpy(t.sn, sn.data(), sizeof(u64) * sn.size(), hipMemcpyHostToDevice));

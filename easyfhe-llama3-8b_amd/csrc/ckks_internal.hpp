@@ -212,7 +212,9 @@ struct BCTable {  // fast basis conversion constants, device resident
   // group g holds targets 4 e + g: a group's first targets fill every lane
   // group), [n_k][n_tg][8][64] words; and per source [N^-1 hinv]_(q_s) as
   // [ns] words, [ns] Shoup constants, [ns] (w, w / q_s) doubles (the inverse
-  // high pass leaves its x N^-1 to this product)
+  // high pass leaves its x N^-1 to this product), then hinv as [ns] words
+  // and [ns] Shoup constants (sources of 2^45 or more, whose inverse high
+  // pass runs before the kernel)
   u64 *mt = nullptr;
   u64 *sn = nullptr;
 };

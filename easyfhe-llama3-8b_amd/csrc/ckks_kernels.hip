@@ -2496,11 +2496,12 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
           a[i][r] = (long)((dbl_bits(__dadd_rn(v, FP_ROUND_C)) + kBal) ^ 0x8080808080808080ull);
         }
       } else {
-        u64_high_inv_stages(x, sw0, sw0 + 16, qu, 2 * qu);
-        const u64 sw = tab[s], sws = tab[ns + s];
+        // a prime of 2^45 or more: its inverse high pass (with the x N^-1)
+        // ran before the kernel (launch_convert_h4), x is canonical
+        const u64 hw = tab[4 * ns + s], hws = tab[5 * ns + s];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          u64 v = shoup_mul(x[r], sw, sws, qu);
+          u64 v = shoup_mul(x[r], hw, hws, qu);
           if (centered && v > (qu - 1) / 2) v -= qu;  // two's complement of v - q
           a[i][r] = (long)((v + 0x8080808080808080ull) ^ 0x8080808080808080ull);
         }
@@ -2576,18 +2577,16 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
           u64 yv = dbl_bits(
               __dadd_rn(__fma_rn(-tq, tqd[ee], __dmul_rn(hi[ee], 4294967296.0)), lo[ee]));
           if (!fpt[ee]) {
+            // a prime q of 2^45 or more: V = hi 2^32 + lo (|hi|, |lo| <
+            // 2^45) less t q, t = round(V / q) from fp64 (|V / q| < 2^32, so
+            // the error is below 2^-19), is exact in 64-bit two's complement
+            // and lies in (-q, q); one conditional q makes it canonical
             const u64 *w = tgt + (size_t)(16 * tg + 4 * (2 * h + ee) + g) * TW;
-            ModQ M;
-            M.q = w[0];
-            M.qinv = w[1];
-            M.r2 = w[2];
-            M.mu = w[3];
-            M.k = (u32)w[4];
-            M.pad = (u32)(w[4] >> 32);
-            const long long hv = dbl_to_i51(hi[ee]), lv = dbl_to_i51(lo[ee]);
-            const u64 hh = hv < 0 ? (u64)(hv + (long long)M.q) : (u64)hv;
-            const u64 ll = lv < 0 ? (u64)(lv + (long long)M.q) : (u64)lv;
-            yv = add_mod(mul_mod(hh, 1ull << 32, M), ll, M.q);
+            const u64 qw = w[0];
+            const double tv = fp_rint(__fma_rn(hi[ee], as_dbl(w[7]), __dmul_rn(lo[ee], as_dbl(w[5]))));
+            const u64 v = ((u64)dbl_to_i51(hi[ee]) << 32) + (u64)dbl_to_i51(lo[ee]) -
+                          (u64)dbl_to_i51(tv) * qw;
+            yv = (long long)v < 0 ? v + qw : v;
           }
           y[ee][r] = yv;
         }
@@ -2684,12 +2683,58 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
       } else {
-        const u64 qu = w[0];
-        u64_high_fwd(y[ee], tw0, tw0 + 16, qu, 2 * qu);
+        // a prime of 2^45 or more: stored canonical, its forward high pass
+        // runs after the kernel (launch_convert_h4)
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = y[ee][r];
       }
     }
+  }
+}
+
+// k_convert_h4 leaves the high passes of primes of 2^45 or more (their
+// 64-bit butterflies would run beside the fp64 ones of the other lane
+// groups) to these launches: the inverse high pass of such sources before
+// the kernel, in place (source s of prime src_prime0 + s sits at item limb
+// s; the batch is shifted so that the pass's limb index names that prime),
+// and the forward high pass of such targets after it (target t at output
+// limb t < t_split ? t : t + t_skip).
+static void h4_wide_sources(ckks_context *c, const Batch &src, int n_items, int ns,
+                            int src_prime0, int q_limbs) {
+  const int off = src_prime0 < c->L ? src_prime0 : q_limbs + (src_prime0 - c->L);
+  for (int s0 = 0; s0 < ns;) {
+    if (c->prime_fp[src_prime0 + s0]) {
+      s0++;
+      continue;
+    }
+    int s1 = s0 + 1;
+    while (s1 < ns && !c->prime_fp[src_prime0 + s1]) s1++;
+    Batch b = src;
+    const size_t back = (size_t)off << 16;
+    if (b.base) b.base -= back;
+    else
+      for (int i = 0; i < n_items; i++) b.p[i] -= back;
+    launch_inv_high16(c, b, n_items, off + s0, s1 - s0, q_limbs);
+    s0 = s1;
+  }
+}
+
+static void h4_wide_targets(ckks_context *c, const Batch &dst, int n_items, int n_out,
+                            int t_split, int t_skip, int q_limbs) {
+  auto limb = [&](int t) { return t < t_split ? t : t + t_skip; };
+  auto wide = [&](int t) {
+    const int tl = limb(t);
+    return !c->prime_fp[tl < q_limbs ? tl : c->L + (tl - q_limbs)];
+  };
+  for (int t0 = 0; t0 < n_out;) {
+    if (!wide(t0)) {
+      t0++;
+      continue;
+    }
+    int t1 = t0 + 1;
+    while (t1 < n_out && wide(t1) && limb(t1) == limb(t1 - 1) + 1) t1++;
+    launch_fwd_high16(c, dst, dst, n_items, limb(t0), t1 - t0, q_limbs);
+    t0 = t1;
   }
 }
 
@@ -2715,11 +2760,13 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
+  h4_wide_sources(c, src, n_items, t.ns, src_prime0, q_limbs);
   hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
                      t.sn, t.mt, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
                      centered ? 1 : 0, c->d_mods, nt, (const u64 *)nullptr,
                      (const double2 *)nullptr);
   LAUNCH_CHECK();
+  h4_wide_targets(c, dst, n_items, t.nd, t_split, t_skip, q_limbs);
 }
 
 bool convert_h4_rs_ok(const ckks_context *c, const BCTable &t, int D) {
@@ -2746,10 +2793,12 @@ void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, i
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
+  h4_wide_sources(c, src, n_items, t.ns, c->L, t.nd);
   hipLaunchKernelGGL(D == 1 ? k1 : k2, dim3(64, n_items), dim3(TPB), convert_h4_lds(t, D),
                      c->stream, src, dst, t.ns, t.nd, t.sn, t.mt, t.n_tg, t.wide_mask, c->L,
                      t.nd, 0, t.nd, c->L, 1, c->d_mods, nt, rtab, rsf);
   LAUNCH_CHECK();
+  h4_wide_targets(c, dst, n_items, T, t.nd, 0, t.nd);
 }
 
 // Only the low pass of the inverse NTT (bit positions 0..11), for limbs
