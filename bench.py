@@ -218,6 +218,9 @@ def main() -> int:
     ap.add_argument("--linear-strategy", default="normal",
                     choices=["normal", "ext_normal", "ext_double_hoist"],
                     help="hoist strategy of the linear mode")
+    ap.add_argument("--linear-rows", type=int, default=512,
+                    help="plaintext rows per chunk of the linear mode (512: the reference's "
+                         "8 giants of 64 babies)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (across GPUs "
@@ -252,7 +255,8 @@ def main() -> int:
         spec.rotations = ()
         client, ctx = fhe.generate_client_context(spec, device="cuda:0")
         print(json.dumps({"fm_linear": measure_fm_linear(client, ctx, warmup=args.warmup,
-                                                         strategy=args.linear_strategy)}),
+                                                         strategy=args.linear_strategy,
+                                                         rows=args.linear_rows)}),
               flush=True)
         return 0
     if args.mode == "prefill":
@@ -635,7 +639,7 @@ def measure_bootstrap(client, ctx, n_cts: int, group: int, budget, warmup: int,
 
 
 def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1,
-                      strategy: str = "normal") -> dict:
+                      strategy: str = "normal", rows: int = 512) -> dict:
     """One 4096 x 4096 feature-major linear (the square projection of a
     Llama-3-8B decoder layer) over 128 tokens = 16 ciphertexts of 8 token
     lanes, entering at `limbs` limbs (the 13-limb QKV budget): the
@@ -647,7 +651,7 @@ def measure_fm_linear(client, ctx, limbs: int = 13, warmup: int = 1,
                                LinearWeight, linear_rotations)
 
     D, lanes = 4096, ctx.max_slots // 4096
-    cfg = LinearOperatorConfig(hoist_strategy=strategy)
+    cfg = LinearOperatorConfig(hoist_strategy=strategy, max_plaintext_rows=rows)
     t0 = time.perf_counter()
     ctx.generate_rotation_keys(linear_rotations(dimension=D, token_lanes=lanes,
                                                 operator_config=cfg))

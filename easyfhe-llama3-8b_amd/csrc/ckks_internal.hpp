@@ -30,7 +30,7 @@ constexpr int kMaxRescaleDrop = 4;  // primes one rescale call may divide by
 constexpr int kMacGroups = 2;       // giant groups of one extended MAC pass
 constexpr int kMacCts = 4;          // ciphertexts per plaintext read in that pass
 constexpr int kMacCtsFp = 8;        // the same for its fp64 path
-constexpr int kTabGroups = 8;       // giant groups of one Q-basis MAC pass (k_mac_table)
+constexpr int kTabGroups = 16;      // giant groups of one Q-basis MAC pass (k_mac_table)
 constexpr int kTabCts = 2;          // ciphertexts per plaintext read in that pass
 constexpr int kTabCtsFp = 8;        // the same for its fp64 path
 constexpr int kMultiItems = 4;    // items per multi-rotation key inner product launch

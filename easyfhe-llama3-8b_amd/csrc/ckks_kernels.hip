@@ -3714,10 +3714,15 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // ([2][limbs][N]), plaintext of group g and baby b at pts[g B + b] (limb l at
 // l N), inner sum of group g for ciphertext i to out + (g n + i) 2 limbs N.
 // A block takes one component of IC ciphertexts (kTabCtsFp on the fp64
-// kernel, kTabCts on the 64-bit one) for 256 coefficients, each thread the
-// babies of its coefficient with the groups' plaintext words in registers: a
-// baby word is read once per pass, a plaintext word once per block, which
-// the block decode below turns into one HBM read per 256 coefficients.
+// kernel, half as many with more than 8 groups, so that a thread's GT x IC
+// accumulators stay within its registers; kTabCts on the 64-bit one, which
+// takes more than 8 groups as passes of 8) for 256
+// coefficients, each thread the babies of its coefficient with the groups'
+// plaintext words in registers: a baby word is read once per pass, a
+// plaintext word once per block, which the block decode below turns into
+// one HBM read per 256 coefficients.  Passes of 16 groups read the babies
+// half as often as passes of 8; their plaintext words serve twice as many
+// blocks, from the same XCD's L2.
 // Limbs whose prime is below 2^45 (with B <= 64) take the fp64 kernel: each
 // product is the exact fp64 residue of fp_mulmod (|r| < 1.5 q) and the
 // B-term sums stay exact integers below 2^53, reduced once at the end, so the
@@ -3729,13 +3734,12 @@ void launch_mac_many(ckks_context *c, const u64 *bab, int n, const Batch &pts, i
 // grid (N / 256 x 2 x input groups, limb_count), limbs from l_begin
 typedef __attribute__((address_space(1))) u64 GlobalU64;
 
-template <int GT>
+template <int GT, int IC>
 __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restrict__ bab, int n,
                                                       const u64 *const *__restrict__ pts, int B,
                                                       int G, u64 *__restrict__ out, int limbs,
                                                       int l_begin, int logN,
                                                       const ModQ *__restrict__ mods) {
-  constexpr int IC = kTabCtsFp;
   int kb, z;
   mac_table_block(2 * ((n + IC - 1) / IC), logN, kb, z);
   const int k = kb * TPB + threadIdx.x;
@@ -3792,13 +3796,12 @@ __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restri
 // issued together one step ahead, and each block takes kTabCts ciphertexts
 // (blockIdx.z = component + 2 x ciphertext group), so that a single limb (q_0)
 // still fills the chip.
-template <int GT>
+template <int GT, int IC>
 __global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restrict__ bab, int n,
                                                       const u64 *const *__restrict__ pts, int B,
                                                       int G, u64 *__restrict__ out, int limbs,
                                                       int l_begin, int logN,
                                                       const ModQ *__restrict__ mods) {
-  constexpr int IC = kTabCts;
   int kb, z;
   mac_table_block(2 * ((n + IC - 1) / IC), logN, kb, z);
   const int k = kb * TPB + threadIdx.x;
@@ -3856,22 +3859,41 @@ void launch_mac_table(ckks_context *c, const u64 *const *bab, int n, const u64 *
             2.0 * c->N * limbs * (double)n * B * G);
   audit_pt(c, (double)G * B * limbs);
   if (G < 1 || G > kTabGroups || B < 1 || n < 1)
-    throw std::invalid_argument("mac_table: 1 <= groups <= 8, babies and ciphertexts >= 1");
-  auto fp_kern = G <= 1   ? k_mac_table_fp<1>
-                 : G <= 2 ? k_mac_table_fp<2>
-                 : G <= 4 ? k_mac_table_fp<4>
-                          : k_mac_table_fp<kTabGroups>;
-  auto w_kern = G <= 1   ? k_mac_table_64<1>
-                : G <= 2 ? k_mac_table_64<2>
-                : G <= 4 ? k_mac_table_64<4>
-                         : k_mac_table_64<kTabGroups>;
+    throw std::invalid_argument("mac_table: 1 <= groups <= 16, babies and ciphertexts >= 1");
+  // a thread of the fp64 kernel holds GT x IC accumulators: up to 8 groups
+  // of 8 ciphertexts, or 16 groups of 4
+  const bool wide = G > 8;
+  auto fp_kern = G <= 1   ? k_mac_table_fp<1, kTabCtsFp>
+                 : G <= 2 ? k_mac_table_fp<2, kTabCtsFp>
+                 : G <= 4 ? k_mac_table_fp<4, kTabCtsFp>
+                 : G <= 8 ? k_mac_table_fp<8, kTabCtsFp>
+                          : k_mac_table_fp<16, kTabCtsFp / 2>;
+  // the 64-bit kernel (q_0 alone, beside the others) takes more than 8
+  // groups as passes of 8: one ciphertext per block measured 4x slower
+  auto w_kern = [](int g) {
+    return g <= 1 ? k_mac_table_64<1, kTabCts>
+           : g <= 2 ? k_mac_table_64<2, kTabCts>
+           : g <= 4 ? k_mac_table_64<4, kTabCts>
+                    : k_mac_table_64<8, kTabCts>;
+  };
   auto fp_limb = [&](int l) { return B <= 64 && c->prime_fp[l] != 0; };
   auto launch_run = [&](int l0, int l1, hipStream_t st) {
-    const int ic = fp_limb(l0) ? kTabCtsFp : kTabCts;
-    const dim3 grid(c->N / TPB * 2 * ((n + ic - 1) / ic), l1 - l0);
-    hipLaunchKernelGGL(fp_limb(l0) ? fp_kern : w_kern, grid, dim3(TPB), 0, st, bab, n, pts, B, G,
-                       out, limbs, l0, c->logN, c->d_mods);
-    LAUNCH_CHECK();
+    if (fp_limb(l0)) {
+      const int ic = kTabCtsFp / (wide ? 2 : 1);
+      const dim3 grid(c->N / TPB * 2 * ((n + ic - 1) / ic), l1 - l0);
+      hipLaunchKernelGGL(fp_kern, grid, dim3(TPB), 0, st, bab, n, pts, B, G, out, limbs, l0,
+                         c->logN, c->d_mods);
+      LAUNCH_CHECK();
+      return;
+    }
+    const dim3 grid(c->N / TPB * 2 * ((n + kTabCts - 1) / kTabCts), l1 - l0);
+    const size_t CP = 2 * (size_t)limbs * c->N;
+    for (int g0 = 0; g0 < G; g0 += 8) {
+      const int gn = std::min(8, G - g0);
+      hipLaunchKernelGGL(w_kern(gn), grid, dim3(TPB), 0, st, bab, n, pts + (size_t)g0 * B, B,
+                         gn, out + (size_t)g0 * n * CP, limbs, l0, c->logN, c->d_mods);
+      LAUNCH_CHECK();
+    }
   };
   // runs of limbs of one kind; with both kinds and a second stream, the
   // 64-bit runs (q_0) run beside the fp64 ones

@@ -3,7 +3,8 @@ slots, 4 x 40-bit limbs): D = 128, 32 token lanes, B = 16 and 2-giant chunks
 (4 chunks), three input ciphertexts (96 tokens).
 
 * the batched chunk MAC (fhe.hoisted_mac_sum_many) gives the same words as one
-  hoisted_mac_sum per input with the same babies and plaintexts;
+  hoisted_mac_sum per input with the same babies and plaintexts, also for a
+  chunk of 16 giants (B = 8, one 128-row chunk: the 16-group pass);
 * the decrypted outputs are W x for every token (fp64 reference).
 """
 
@@ -19,12 +20,12 @@ pytestmark = pytest.mark.gpu
 D, LANES = 128, 32
 
 
-def _setup(cfg, extra=()):
+def _setup(cfg, extra=(), chain="matvec", lanes=LANES):
     from feature_major import FeatureMajorPrefillLayout, linear_rotations
 
-    rots = linear_rotations(dimension=D, token_lanes=LANES, operator_config=cfg)
-    client, ctx = device_context("matvec", rotations=tuple(sorted(set(rots) | set(extra))))
-    lay = FeatureMajorPrefillLayout(seq_len=3 * LANES, hidden_dim=D, slots=ctx.max_slots)
+    rots = linear_rotations(dimension=D, token_lanes=lanes, operator_config=cfg)
+    client, ctx = device_context(chain, rotations=tuple(sorted(set(rots) | set(extra))))
+    lay = FeatureMajorPrefillLayout(seq_len=3 * lanes, hidden_dim=D, slots=ctx.max_slots)
     rng = np.random.default_rng(0)
     W = rng.uniform(-1, 1, (D, D))
     X = rng.uniform(-1, 1, (lay.seq_len, D))
@@ -33,13 +34,20 @@ def _setup(cfg, extra=()):
     return client, ctx, lay, W, X, cts
 
 
-def test_fm_linear_matches_per_input_bsgs_and_wx():
+# (babies, anchor step, plaintext rows per chunk, chain, token lanes): chunks
+# of 2 giants, and one chunk of 16 giants (the batched MAC's 16-group pass) on
+# the matvec chain (every limb on the fp64 kernel) and on a chain whose 60-bit
+# q_0 takes the 64-bit kernel (N = 2^12: 16 lanes of 128 features)
+@pytest.mark.parametrize("schedule", [(16, 16, 32, "matvec", LANES), (8, 8, 128, "matvec", LANES),
+                                      (8, 8, 128, "small", 16)])
+def test_fm_linear_matches_per_input_bsgs_and_wx(schedule):
     from easyfhe import fhe
     from feature_major import LinearOperator, LinearOperatorConfig, LinearWeight
 
-    cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=16, max_plaintext_rows=32)
-    client, ctx, lay, W, X, cts = _setup(cfg)
-    op = LinearOperator(context=ctx, token_lanes=LANES, config=cfg)
+    b, anchor, rows, chain, lanes = schedule
+    cfg = LinearOperatorConfig(baby_steps=b, baby_anchor_step=anchor, max_plaintext_rows=rows)
+    client, ctx, lay, W, X, cts = _setup(cfg, chain=chain, lanes=lanes)
+    op = LinearOperator(context=ctx, token_lanes=lanes, config=cfg)
     with LinearWeight(W, context=ctx) as weight:
         outs, profile = op.apply(cts, weight)
         assert set(profile) >= {"baby_precompute", "pack_encode", "online", "rescale"}
