@@ -2383,11 +2383,15 @@ template <int NK, int RSD = 0>
 __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
     Batch src, Batch dst, int ns, int nd, const u64 *__restrict__ tab,
     const u64 *__restrict__ mtab, int n_tg, int wide_mask, int src_prime0, int t_split,
-    int t_skip, int q_limbs, int L, int centered, const ModQ *__restrict__ mods, H4Tabs nt,
+    int t_skip, int q_limbs, int L, int flags, const ModQ *__restrict__ mods, H4Tabs nt,
     const u64 *__restrict__ rs, const double2 *__restrict__ rsf) {
   constexpr bool RS = RSD > 0;
   constexpr int TW = bc_tgt_words(RSD);
   const int T = nd - RSD;
+  // flags: 1 centered (ModDown); 2 / 4: the high passes of sources / targets
+  // of 2^45 or more run outside the kernel (when such primes share a launch
+  // with fp64 ones, whose lanes would wait on their 64-bit butterflies)
+  const bool centered = flags & 1, wide_src_out = flags & 2, wide_tgt_out = flags & 4;
   extern __shared__ u64 tb[];
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
   const int cc = blockIdx.x * 64 + wave * 16 + col;
@@ -2496,9 +2500,14 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
           a[i][r] = (long)((dbl_bits(__dadd_rn(v, FP_ROUND_C)) + kBal) ^ 0x8080808080808080ull);
         }
       } else {
-        // a prime of 2^45 or more: its inverse high pass (with the x N^-1)
-        // ran before the kernel (launch_convert_h4), x is canonical
-        const u64 hw = tab[4 * ns + s], hws = tab[5 * ns + s];
+        // a prime of 2^45 or more: the inverse high pass here, or (flag 2)
+        // before the kernel (with the x N^-1, x canonical)
+        u64 hw = tab[4 * ns + s], hws = tab[5 * ns + s];
+        if (!wide_src_out) {
+          u64_high_inv_stages(x, sw0, sw0 + 16, qu, 2 * qu);
+          hw = tab[s];
+          hws = tab[ns + s];
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           u64 v = shoup_mul(x[r], hw, hws, qu);
@@ -2683,8 +2692,12 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
       } else {
-        // a prime of 2^45 or more: stored canonical, its forward high pass
-        // runs after the kernel (launch_convert_h4)
+        // a prime of 2^45 or more: the forward high pass here, or (flag 4)
+        // stored canonical for the launch after the kernel
+        if (!wide_tgt_out) {
+          const u64 qu = w[0];
+          u64_high_fwd(y[ee], tw0, tw0 + 16, qu, 2 * qu);
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++) po[4096 * r] = y[ee][r];
       }
@@ -2692,15 +2705,21 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
   }
 }
 
-// k_convert_h4 leaves the high passes of primes of 2^45 or more (their
-// 64-bit butterflies would run beside the fp64 ones of the other lane
-// groups) to these launches: the inverse high pass of such sources before
-// the kernel, in place (source s of prime src_prime0 + s sits at item limb
-// s; the batch is shifted so that the pass's limb index names that prime),
-// and the forward high pass of such targets after it (target t at output
-// limb t < t_split ? t : t + t_skip).
-static void h4_wide_sources(ckks_context *c, const Batch &src, int n_items, int ns,
-                            int src_prime0, int q_limbs) {
+// Where a launch mixes primes of 2^45 or more with fp64 ones, k_convert_h4
+// leaves the wide primes' high passes (whose 64-bit butterflies would run
+// beside the fp64 ones of the other lane groups of a wave) to these
+// launches: the inverse high pass of such sources before the kernel, in
+// place (source s of prime src_prime0 + s sits at item limb s; the batch is
+// shifted so that the pass's limb index names that prime), and the forward
+// high pass of such targets after it (target t at output limb
+// t < t_split ? t : t + t_skip).  Each returns the kernel's flag (2, 4) when
+// the launch is mixed, else 0 and runs nothing: a launch of wide primes only
+// keeps its high passes inside.
+static int h4_wide_sources(ckks_context *c, const Batch &src, int n_items, int ns,
+                           int src_prime0, int q_limbs) {
+  int wide = 0;
+  for (int s = 0; s < ns; s++) wide += c->prime_fp[src_prime0 + s] ? 0 : 1;
+  if (wide == 0 || wide == ns) return 0;
   const int off = src_prime0 < c->L ? src_prime0 : q_limbs + (src_prime0 - c->L);
   for (int s0 = 0; s0 < ns;) {
     if (c->prime_fp[src_prime0 + s0]) {
@@ -2717,15 +2736,22 @@ static void h4_wide_sources(ckks_context *c, const Batch &src, int n_items, int 
     launch_inv_high16(c, b, n_items, off + s0, s1 - s0, q_limbs);
     s0 = s1;
   }
+  return 2;
 }
 
-static void h4_wide_targets(ckks_context *c, const Batch &dst, int n_items, int n_out,
-                            int t_split, int t_skip, int q_limbs) {
+// run: false asks only whether the launch is mixed (the flag), true runs
+// the passes
+static int h4_wide_targets(ckks_context *c, const Batch &dst, int n_items, int n_out,
+                           int t_split, int t_skip, int q_limbs, bool run) {
   auto limb = [&](int t) { return t < t_split ? t : t + t_skip; };
   auto wide = [&](int t) {
     const int tl = limb(t);
     return !c->prime_fp[tl < q_limbs ? tl : c->L + (tl - q_limbs)];
   };
+  int n_wide = 0;
+  for (int t = 0; t < n_out; t++) n_wide += wide(t) ? 1 : 0;
+  if (n_wide == 0 || n_wide == n_out) return 0;
+  if (!run) return 4;
   for (int t0 = 0; t0 < n_out;) {
     if (!wide(t0)) {
       t0++;
@@ -2736,6 +2762,7 @@ static void h4_wide_targets(ckks_context *c, const Batch &dst, int n_items, int 
     launch_fwd_high16(c, dst, dst, n_items, limb(t0), t1 - t0, q_limbs);
     t0 = t1;
   }
+  return 4;
 }
 
 static size_t convert_h4_lds(const BCTable &t, int rsd = 0) {
@@ -2760,13 +2787,13 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
-  h4_wide_sources(c, src, n_items, t.ns, src_prime0, q_limbs);
+  const int flags = (centered ? 1 : 0) | h4_wide_sources(c, src, n_items, t.ns, src_prime0, q_limbs) |
+                    h4_wide_targets(c, dst, n_items, t.nd, t_split, t_skip, q_limbs, false);
   hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
                      t.sn, t.mt, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
-                     centered ? 1 : 0, c->d_mods, nt, (const u64 *)nullptr,
-                     (const double2 *)nullptr);
+                     flags, c->d_mods, nt, (const u64 *)nullptr, (const double2 *)nullptr);
   LAUNCH_CHECK();
-  h4_wide_targets(c, dst, n_items, t.nd, t_split, t_skip, q_limbs);
+  if (flags & 4) h4_wide_targets(c, dst, n_items, t.nd, t_split, t_skip, q_limbs, true);
 }
 
 bool convert_h4_rs_ok(const ckks_context *c, const BCTable &t, int D) {
@@ -2793,12 +2820,13 @@ void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, i
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
-  h4_wide_sources(c, src, n_items, t.ns, c->L, t.nd);
+  const int flags = 1 | h4_wide_sources(c, src, n_items, t.ns, c->L, t.nd) |
+                    h4_wide_targets(c, dst, n_items, T, t.nd, 0, t.nd, false);
   hipLaunchKernelGGL(D == 1 ? k1 : k2, dim3(64, n_items), dim3(TPB), convert_h4_lds(t, D),
                      c->stream, src, dst, t.ns, t.nd, t.sn, t.mt, t.n_tg, t.wide_mask, c->L,
-                     t.nd, 0, t.nd, c->L, 1, c->d_mods, nt, rtab, rsf);
+                     t.nd, 0, t.nd, c->L, flags, c->d_mods, nt, rtab, rsf);
   LAUNCH_CHECK();
-  h4_wide_targets(c, dst, n_items, T, t.nd, 0, t.nd);
+  if (flags & 4) h4_wide_targets(c, dst, n_items, T, t.nd, 0, t.nd, true);
 }
 
 // Only the low pass of the inverse NTT (bit positions 0..11), for limbs

@@ -100,6 +100,45 @@ def test_mfma_keyswitch_full_size(fused, monkeypatch):
     ctx.close()
 
 
+# N = 2^16 with every prime of 2^45 or more (as on the reference's 59-bit
+# chain): the tile-resident conversion keeps the 64-bit high passes inside
+# when a launch holds wide primes only
+ALL_WIDE = dict(log_n=16, depth=5, dnum=2, dcrt_bits=59, first_mod=60, special_bits=60)
+
+
+@pytest.mark.slow
+def test_keyswitch_all_wide_primes_full_size():
+    """Rotation, multiply-relinearise-rescale and hoisted rotations at
+    N = 2^16 on a chain of 59- and 60-bit primes, limbs equal to the
+    oracle's."""
+    from easyfhe import fhe
+
+    rot = 1 << 9
+    client, ctx = device_context(ALL_WIDE, rotations=(rot, 5))
+    orc = oracle_context(ALL_WIDE)
+    orc.gen_relin_key()
+    for r in (rot, 5):
+        orc.gen_rotation_key(orc.galois_elt(r))
+    slots, L = ctx.max_slots, ctx.L
+    rng = np.random.default_rng(11)
+    zs = [rng.uniform(-1, 1, slots) for _ in range(2)]
+    cts = [client.encrypt(z, enc_id=740 + i) for i, z in enumerate(zs)]
+    refs = [orc.encrypt(z, slots=slots, scale=ctx.scale_at(L), limbs=L, enc_id=740 + i)
+            for i, z in enumerate(zs)]
+    rots = fhe.homo_rotate_many(cts, rot, ctx)
+    for i in range(2):
+        assert np.array_equal(rots[i].download(), orc.rotate_g(refs[i], orc.galois_elt(rot)))
+    prod = fhe.homo_mul_relin_rescale_many(cts[:1], cts[1:], ctx)[0]
+    assert np.array_equal(prod.download(),
+                          orc.rescale(orc.relinearize(orc.tensor(refs[0], refs[1]))))
+    hs = fhe.prepare_hoisted_baby_rotations(cts[0], [0, 5, rot], ctx)
+    want = orc.hoisted_rotate(refs[0], [orc.galois_elt(r) for r in (0, 5, rot)])
+    for h, w in zip(hs, want):
+        assert np.array_equal(h.download(), w)
+    assert np.abs(client.decrypt(rots[0]) - np.roll(zs[0], -rot)).max() < 1e-6
+    ctx.close()
+
+
 @pytest.mark.slow
 def test_mfma_relin_rescale_two_primes_full_size():
     """Relinearise + two rescales as one ModDown at N = 2^16 on the key-switch
