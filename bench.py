@@ -856,8 +856,9 @@ def measure_fm_attention(client, ctx, limbs: int = 34, warmup: int = 1) -> dict:
 
 
 # A chain that holds one whole decoder layer without a refresh: 60-bit q_0 +
-# 72 x 40-bit primes, dnum 5 (digits of 15 primes), 15 special primes of 44 bits
-LAYER_PARAMS = dict(log_n=16, depth=72, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+# 72 x 40-bit primes, dnum 7 (digits of 11 primes, within the tile-resident
+# conversion's three source quads), 11 special primes of 44 bits
+LAYER_PARAMS = dict(log_n=16, depth=72, dnum=7, dcrt_bits=40, first_mod=60, special_bits=44)
 
 
 def randomized_hadamard(dim: int, seed: int) -> np.ndarray:
@@ -997,8 +998,11 @@ def measure_fm_layer(warmup: int = 0) -> dict:
 
 
 # A chain for refreshed layers: bootstraps (budget (3,3), 26 limbs) return the
-# 40 limbs of a layer's deepest block (scores -> softmax -> PV -> W_o)
-REFRESH_PARAMS = dict(log_n=16, depth=65, dnum=5, dcrt_bits=40, first_mod=60, special_bits=44)
+# 40 limbs of a layer's deepest block (scores -> softmax -> PV -> W_o).  dnum 6
+# keeps digits of 11 limbs and 11 special primes (P = 2^484 above the largest
+# digit, 60 + 10 x 40 bits), within the tile-resident conversion's three
+# source quads: 2.95 -> 2.69 s per layer against dnum 5, and a smaller P
+REFRESH_PARAMS = dict(log_n=16, depth=65, dnum=6, dcrt_bits=40, first_mod=60, special_bits=44)
 # the reference's layer chain (assets/feature_major.json:3-16): 60 + 37 x 59-bit
 # primes, dnum 5; 8 special primes of 60 bits (P = 2^480 exceeds the largest
 # digit, 60 + 7 x 59 = 473 bits)
@@ -1319,14 +1323,17 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         ctx.audit(reset=True)
         ev0.record()
         t0 = time.perf_counter()
-        allocs = []
+        allocs, mems = [], []
 
         def on_layer(i, s):
             # the pool's device allocations so far: a layer that grows the
-            # pool pays its hipMalloc calls
-            allocs.append(int(ctx.memory_info()["device_allocations"]))
-            print(f"layer {i}: {s:.2f} s, {allocs[-1]} device allocations", file=sys.stderr,
-                  flush=True)
+            # pool pays its hipMalloc calls; and its live / cached bytes
+            m = ctx.memory_info()
+            allocs.append(int(m["device_allocations"]))
+            mems.append([round(m["live_bytes"] / 2**30, 1), round(m["cached_bytes"] / 2**30, 1),
+                         round(m["segment_bytes"] / 2**30, 1)])
+            print(f"layer {i}: {s:.2f} s, {allocs[-1]} device allocations, live / cached / "
+                  f"segments {mems[-1]} GiB", file=sys.stderr, flush=True)
 
         res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog,
                           residual_program=res_prog, residual_bounds=bounds,
@@ -1360,6 +1367,7 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         "layers": int(n_layers),
         "layer_s": [round(v, 2) for v in res.layer_seconds],
         "device_allocations_after_layer": allocs,
+        "live_cached_segment_gib_after_layer": mems,
         "roofline": audit_roofline(audit, wall, int(n_layers), "layer"),
         "workload": f"{n_layers}-layer Llama-3-8B prefill (d=4096, 32/8 heads x 128, SwiGLU "
                     f"14336, vocab {vocab}) over 128 random tokens in 16 ciphertexts of 8 lanes, "

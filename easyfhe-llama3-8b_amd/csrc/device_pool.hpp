@@ -270,15 +270,21 @@ struct BasicPool {
 
   // Make `bytes` (plus the runtime reserve) free on the device: first the
   // small classes and the empty segments, then give up the reserve.
+  // Whole free segments go back first; the small cached blocks (at most
+  // 1 MiB each, each its own device allocation) only when that is not
+  // enough: they free little and cost one device allocation each when they
+  // are needed again (a layer of the prefill reallocated about 550 of them,
+  // over a second, each time they went).
   bool make_room(size_t bytes) {
     if (Dev::free_bytes() >= bytes + kRuntimeReserve) return true;
     Dev::synchronize();
+    free_segments();
+    if (Dev::free_bytes() >= bytes + kRuntimeReserve) return true;
     for (auto &kv : free_) {
       for (void *q : kv.second) Dev::release(q);
       cached -= kv.first * kv.second.size();
       kv.second.clear();
     }
-    free_segments();
     return Dev::free_bytes() >= bytes;
   }
 };
