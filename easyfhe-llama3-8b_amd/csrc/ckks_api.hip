@@ -1040,18 +1040,28 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
   u64 *coeff = s.get((size_t)n * limbs * N);
   Batch src{};
   for (int i = 0; i < n; i++) src.p[i] = (u64 *)d[i];
-  // N = 2^16 with the high-pass-only output: the inverse NTT's high pass, the
-  // conversion and the targets' forward high pass run as one kernel per digit
-  bool tile = high_only && !own_copy && c->ks_tile;
+  // N = 2^16: the inverse NTT's high pass, the conversion and the targets'
+  // forward high pass run as one kernel per digit; for the full NTT form
+  // (not high_only) the targets' low pass follows
+  bool tile = c->ks_tile;
   for (int j = 0; j < digits && tile; j++) tile = convert_h4_ok(c, bc_up(c, limbs, j));
   if (tile) {
     const size_t est = (size_t)digits * E * N;
     launch_ntt_inv_low(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs);
     for (int j = 0; j < digits; j++) {
       const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
-      launch_convert_h4(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N),
-                        strided(ext + (size_t)j * E * N, est), n, bc_up(c, limbs, j), lo, lo, ns,
-                        limbs, false);
+      u64 *ej = ext + (size_t)j * E * N;
+      if (own_copy) {
+        Batch dsrc{};
+        for (int i = 0; i < n; i++) dsrc.p[i] = (u64 *)d[i] + (size_t)lo * N;
+        launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
+      }
+      launch_convert_h4(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N), strided(ej, est),
+                        n, bc_up(c, limbs, j), lo, lo, ns, limbs, false);
+      if (!high_only) {
+        launch_ntt_fwd_low(c, strided(ej, est), n, 0, lo, limbs);
+        launch_ntt_fwd_low(c, strided(ej, est), n, hi, E - hi, limbs);
+      }
     }
     return;
   }

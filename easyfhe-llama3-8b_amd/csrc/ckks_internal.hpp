@@ -447,6 +447,10 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         bool high_done = false, bool wide_only = false);
 // N = 2^16: the inverse NTT's low pass alone (its high pass then runs in
 // launch_convert_h4 or launch_ntt_inv_high)
+// the forward NTT's low pass alone, in place (N = 2^16: after the high pass of
+// launch_convert_h4 or launch_ntt_fwd_high)
+void launch_ntt_fwd_low(ckks_context *c, const Batch &data, int n_items, int l_begin,
+                        int l_count, int q_limbs);
 void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                         int l_begin, int l_count, int q_limbs);
 // N = 2^16: launch_basis_convert of inverse-low-passed sources (src item at

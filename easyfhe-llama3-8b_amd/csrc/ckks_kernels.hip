@@ -2829,6 +2829,19 @@ void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, i
   if (flags & 4) h4_wide_targets(c, dst, n_items, T, t.nd, 0, t.nd, true);
 }
 
+// Only the low pass of the forward NTT (bit positions 11..0), in place, for
+// limbs whose high pass ran inside launch_convert_h4.  N = 2^16 only.
+void launch_ntt_fwd_low(ckks_context *c, const Batch &data, int n_items, int l_begin,
+                        int l_count, int q_limbs) {
+  KTimer kt(c, "ntt_fwd", 16.0 * c->N * n_items * l_count, 0.5 * c->N * 12 * n_items * l_count);
+  if (n_items <= 0 || l_count <= 0) return;
+  if (c->logN != 16) throw std::invalid_argument("low pass alone: N = 2^16 only");
+  hipLaunchKernelGGL(k_ntt16m_fwd_low<false>, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream,
+                     data, l_begin, q_limbs, c->L, c->d_mods, c->d_psi, c->d_psi_sh,
+                     (const double2 *)c->d_tw_fp, MDCombine{});
+  LAUNCH_CHECK();
+}
+
 // Only the low pass of the inverse NTT (bit positions 0..11), for limbs
 // whose high pass runs inside launch_convert_h4.  N = 2^16 only.
 void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
