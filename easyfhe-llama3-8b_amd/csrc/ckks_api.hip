@@ -2832,13 +2832,23 @@ static void moddown_polys(ckks_context *c, int limbs, const std::vector<const u6
       ob.p[i] = dst[b0 + i];
     }
     u64 *ptmp = s.get((size_t)nb * c->alpha * N);
-    launch_ntt(c, sb, strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N), nb, limbs,
-               c->alpha, limbs, true);
     u64 *conv = s.get((size_t)nb * limbs * N);
-    launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
-                         nb, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
-    launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), nb, 0,
-               limbs, limbs, false);
+    const Batch spb = strided(ptmp - (size_t)limbs * N, (size_t)c->alpha * N);
+    if (c->ks_tile && convert_h4_ok(c, bc_down(c, limbs))) {
+      // N = 2^16: the P limbs' inverse high pass, the conversion and the
+      // forward high pass in the tile-resident kernel, then the low pass
+      launch_ntt_inv_low(c, sb, spb, nb, limbs, c->alpha, limbs);
+      launch_convert_h4(c, strided(ptmp, (size_t)c->alpha * N), strided(conv, (size_t)limbs * N),
+                        nb, bc_down(c, limbs), c->L, limbs, 0, limbs, true);
+      launch_ntt_fwd_low(c, strided(conv, (size_t)limbs * N), nb, 0, limbs, limbs);
+    } else {
+      launch_ntt(c, sb, spb, nb, limbs, c->alpha, limbs, true);
+      launch_basis_convert(c, strided(ptmp, (size_t)c->alpha * N),
+                           strided(conv, (size_t)limbs * N), nb, bc_down(c, limbs), c->L, limbs, 0,
+                           limbs, true);
+      launch_ntt(c, strided(conv, (size_t)limbs * N), strided(conv, (size_t)limbs * N), nb, 0,
+                 limbs, limbs, false);
+    }
     launch_moddown_one(c, sb, Strided{conv, (size_t)limbs * N}, ob, nb, limbs, pinv);
   }
 }
