@@ -2612,6 +2612,23 @@ int ckks_hoisted_mac_sum(ckks_context *c, const ckks_ct *const *babies, int B,
   API_END
 }
 
+// out[i] = a[i] + b[i] for n degree-1 ciphertexts at `limbs` limbs, 64 pairs
+// per launch (the giant Horner chains' adds)
+// (item i's second operand at b + i b_stride)
+static void add_batched(ckks_context *c, const std::vector<ckks_ct *> &a, const u64 *b,
+                        size_t b_stride, ckks_ct *const *out, int n, int limbs) {
+  for (int b0 = 0; b0 < n; b0 += kMaxBatch) {
+    const int nb = std::min(kMaxBatch, n - b0);
+    Batch ba{}, bb{}, bo{};
+    for (int i = 0; i < nb; i++) {
+      ba.p[i] = a[b0 + i]->d;
+      bb.p[i] = (u64 *)(b + (size_t)(b0 + i) * b_stride);
+      bo.p[i] = out[b0 + i]->d;
+    }
+    launch_addsub_many(c, ba, bb, bo, nb, 2, limbs, limbs, 0);
+  }
+}
+
 int ckks_hoisted_mac_sum_many(ckks_context *c, const ckks_ct *const *babies, int n, int B,
                               const ckks_ct *const *pts, int64_t giant_rotation,
                               int giant_count, ckks_ct **out) {
@@ -2676,10 +2693,8 @@ int ckks_hoisted_mac_sum_many(ckks_context *c, const ckks_ct *const *babies, int
       std::vector<const ckks_ct *> cur(out, out + n);
       rotate_batch(c, cur.data(), n, gg, rot.data());
     }
-    for (int i = 0; i < n; i++) {
-      launch_addsub(c, rot[i]->d, ig + (size_t)i * CP, out[i]->d, 2, limbs, limbs, 0);
-      free_ct(rot[i]);
-    }
+    add_batched(c, rot, ig, CP, out, n, limbs);
+    for (int i = 0; i < n; i++) free_ct(rot[i]);
   }
   API_END
 }
@@ -2809,10 +2824,8 @@ static void mac_sum_ext(ckks_context *c, const ckks_ct *const *a, int n,
       std::vector<const ckks_ct *> cur(out, out + n);
       rotate_batch(c, cur.data(), n, gg, rot.data());
     }
-    for (int i = 0; i < n; i++) {
-      launch_addsub(c, rot[i]->d, inner + (size_t)i * 2 * P, out[i]->d, 2, limbs, limbs, 0);
-      free_ct(rot[i]);
-    }
+    add_batched(c, rot, inner, 2 * P, out, n, limbs);
+    for (int i = 0; i < n; i++) free_ct(rot[i]);
   }
 }
 
