@@ -15,6 +15,7 @@ keyswitch rate on the host cores.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -1240,6 +1241,11 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
 
     params = REFRESH_PARAMS if params is None else params
     budget = tuple(int(v) for v in budget)
+    # contexts dropped by earlier work in this process give their device
+    # memory back before this one sizes its pool against what is free
+    gc.collect()
+    torch.cuda.empty_cache()
+    free_at_start = torch.cuda.mem_get_info()[0]
     T, D, H, KV, hd, I = 128, 4096, 32, 8, 128, 14336
     lay = FeatureMajorPrefillLayout(seq_len=T, hidden_dim=D, slots=32768)
     spec = fhe.CKKSContextSpec(**params, seed=seed,
@@ -1324,17 +1330,20 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         ctx.audit(reset=True)
         ev0.record()
         t0 = time.perf_counter()
-        allocs, mems = [], []
+        allocs, mems, free = [], [], []
 
         def on_layer(i, s):
             # the pool's device allocations so far: a layer that grows the
-            # pool pays its hipMalloc calls; and its live / cached bytes
+            # pool pays its hipMalloc calls; its live / cached bytes; and the
+            # device memory nobody holds
             m = ctx.memory_info()
             allocs.append(int(m["device_allocations"]))
             mems.append([round(m["live_bytes"] / 2**30, 1), round(m["cached_bytes"] / 2**30, 1),
                          round(m["segment_bytes"] / 2**30, 1)])
+            free.append(round(torch.cuda.mem_get_info()[0] / 2**30, 1))
             print(f"layer {i}: {s:.2f} s, {allocs[-1]} device allocations, live / cached / "
-                  f"segments {mems[-1]} GiB", file=sys.stderr, flush=True)
+                  f"segments {mems[-1]} GiB, device free {free[-1]} GiB", file=sys.stderr,
+                  flush=True)
 
         res = prefill_fhe(cts, layers, crypto_context=ctx, program=prog,
                           residual_program=res_prog, residual_bounds=bounds,
@@ -1369,6 +1378,8 @@ def measure_fm_prefill(n_layers: int = 32, vocab: int = 128256, seed: int = 0, *
         "layer_s": [round(v, 2) for v in res.layer_seconds],
         "device_allocations_after_layer": allocs,
         "live_cached_segment_gib_after_layer": mems,
+        "device_free_gib_after_layer": free,
+        "device_free_gib_at_start": round(free_at_start / 2**30, 1),
         "roofline": audit_roofline(audit, wall, int(n_layers), "layer"),
         "workload": f"{n_layers}-layer Llama-3-8B prefill (d=4096, 32/8 heads x 128, SwiGLU "
                     f"14336, vocab {vocab}) over 128 random tokens in 16 ciphertexts of 8 lanes, "

@@ -34,6 +34,19 @@ from conftest import device_context
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
 
+@pytest.fixture(autouse=True)
+def _release_device_memory():
+    # each case holds tens of GiB: what a finished case dropped goes back to
+    # the device before the next one sizes its pool against what is free
+    yield
+    import gc
+
+    import torch
+
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.timeout(300)
 def test_bootstrap_32_ciphertexts_full_size(capsys):
     import bench
