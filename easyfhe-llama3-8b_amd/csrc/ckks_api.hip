@@ -1162,8 +1162,7 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
     if (deferred)
       launch_low_key_moddown(c, dk->ext, dk->est, dk->own, n, *dk->key, dk->digits, E, limbs,
                              dk->ginv, strided(conv, (size_t)limbs * N), pinv,
-                             pmod_table(c, limbs), a0, add1_off, gal.data(), o0, out1_off,
-                             limbs);
+                             pmod_table(c, limbs), a0, add1_off, o0, out1_off, limbs);
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
                        pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile,
                        deferred);
@@ -1442,14 +1441,29 @@ static PostOp post_chunk(const ckks_context *c, const PostSpec *ps, int b0, int 
   return po;
 }
 
+// With ta / tb given, in[i] is the degree-2 product of ta[i] and tb[i], not
+// yet formed (in[0 .. n - 1] spaced 3 limbs N words apart): each part forms
+// its items' d2 before the ModUp and, after it, the d0 / d1 limbs that the
+// ModDown reads from memory; the fused combine forms the other d0 / d1
+// words from the factors.
 static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n, ckks_ct **out,
-                                int D = 1, const PostSpec *ps = nullptr) {
+                                int D = 1, const PostSpec *ps = nullptr,
+                                const Batch *ta = nullptr, const Batch *tb = nullptr) {
   const int limbs = in[0]->limbs, T = limbs - D, A = c->alpha;
   const size_t N = c->N, P = (size_t)limbs * N;
   const DeviceKey &key = get_key(c, 0);
   const BCTable &bt = bc_down(c, limbs);
   const u64 *rt = relin_rs_table(c, limbs, D);
   auto run = [&](int b0, int nb, Scratch &s) {
+    Batch fa{}, fb{};
+    const Batch prod = strided(in[b0]->d, 3 * P);
+    if (ta) {
+      for (int i = 0; i < nb; i++) {
+        fa.p[i] = batch_ptr_host(*ta, b0 + i);
+        fb.p[i] = batch_ptr_host(*tb, b0 + i);
+      }
+      launch_tensor(c, fa, fb, prod, nb, limbs, 0, limbs, 2);
+    }
     std::vector<const u64 *> d(nb);
     for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     const int E = limbs + A;
@@ -1473,6 +1487,23 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     const bool may_defer = tile && !ps;
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done,
                               may_defer ? &dk : nullptr);
+    if (ta && dk.on) {
+      // d0 / d1 of the dropped limbs (the lift) and of the kept limbs of
+      // primes of 2^45 or more (launch_ntt_moddown's combine)
+      for (int l0 = 0; l0 < T;) {
+        if (c->prime_fp[l0]) {
+          l0++;
+          continue;
+        }
+        int l1 = l0 + 1;
+        while (l1 < T && !c->prime_fp[l1]) l1++;
+        launch_tensor(c, fa, fb, prod, nb, limbs, l0, l1 - l0, 1);
+        l0 = l1;
+      }
+      launch_tensor(c, fa, fb, prod, nb, limbs, T, D, 1);
+    } else if (ta) {
+      launch_tensor(c, fa, fb, prod, nb, limbs, 0, limbs, 1);
+    }
     if (tile) {
       if (!sp_done)
         launch_ntt_inv_low(c, strided(acc, (size_t)E * N), strided(x - P, xs), 2 * nb, limbs, A,
@@ -1505,7 +1536,7 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
       if (dk.on)
         launch_low_key_moddown(c, dk.ext, dk.est, dk.own, nb, *dk.key, dk.digits, E, limbs,
                                dk.ginv, strided(conv, (size_t)T * N), rt, pmod_table(c, limbs),
-                               d3, P, gal.data(), o0, (u64)T * N, T);
+                               ta ? fa : d3, P, o0, (u64)T * N, T, ta ? &fb : nullptr);
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
                          d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile, dk.on);
     } else {
@@ -2375,7 +2406,8 @@ static void mul_relin_rescale(ckks_context *c, const ckks_ct *const *a, const ck
       ba.p[i] = a[b0 + i]->d;
       bb.p[i] = b[b0 + i]->d;
     }
-    launch_tensor(c, ba, bb, strided(t3, (size_t)3 * limbs * N), nb, limbs);
+    // the merged path forms the products itself, part by part
+    if (!merged) launch_tensor(c, ba, bb, strided(t3, (size_t)3 * limbs * N), nb, limbs);
     std::vector<ckks_ct> v3(nb), v2(nb);
     std::vector<const ckks_ct *> p3(nb);
     std::vector<ckks_ct *> p2(nb);
@@ -2401,7 +2433,7 @@ static void mul_relin_rescale(ckks_context *c, const ckks_ct *const *a, const ck
       // relin_rescale_batch indexes the subtrahends from its own first item
       PostSpec pss{};
       if (ps) pss = PostSpec{ps->dbl, ps->sub ? ps->sub + b0 : nullptr, ps->scal};
-      relin_rescale_batch(c, p3.data(), nb, o.data(), primes, ps ? &pss : nullptr);
+      relin_rescale_batch(c, p3.data(), nb, o.data(), primes, ps ? &pss : nullptr, &ba, &bb);
       continue;
     }
     relin_batch(c, p3.data(), nb, p2.data());

@@ -75,6 +75,11 @@ __device__ __forceinline__ u64 *batch_ptr(const Batch &b, int i) {
   return b.base ? b.base + (u64)i * b.stride : b.p[i];
 }
 
+// item i of a batch on the host (null for an empty batch's item 0)
+inline u64 *batch_ptr_host(const Batch &b, int i) {
+  return b.base ? b.base + (u64)i * b.stride : b.p[i];
+}
+
 // ---------------------------------------------------------------------------
 // modular arithmetic (device)
 // ---------------------------------------------------------------------------
@@ -386,8 +391,11 @@ void launch_mul_i(ckks_context *c, const u64 *ct, u64 *out, int polys, int limbs
                   int q_limbs, int negative);
 void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int polys,
                    int limbs, int q_limbs, int op);  // op 0: add to poly 0, 1: mul all
+// out = a x b of degree-1 ciphertexts at `limbs` limbs: parts 1 writes d0 and
+// d1, 2 writes d2, 3 all three, for limbs [l_begin, l_begin + l_count)
+// (l_count -1: to the last limb)
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
-                   int n_items, int limbs);
+                   int n_items, int limbs, int l_begin = 0, int l_count = -1, int parts = 3);
 void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered);
@@ -417,18 +425,23 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr,
                         int defer_below = 0);
 // N = 2^16: for the Q limbs of fp64 primes, launch_ntt_low_key's key product
-// and launch_ntt_moddown's combine (addends, outputs and postop as there) in
-// one kernel, the accumulator kept in the block, for output limbs
+// and launch_ntt_moddown's combine (addends and outputs as there, no postop)
+// in one kernel, the accumulator kept in the block, for output limbs
 // [0, out_limbs) (q_limbs, or the kept limbs of a relinearise-rescale, whose
 // pinv is (P p_1..p_D)^-1); conv holds the ModDown's conversion after the
-// forward high pass (launch_convert_h4), 2 n items of out_limbs limbs; pmod per Q limb [P]_q and its Shoup constant.  The special
-// limbs' key product and the other Q limbs run through
-// launch_ntt_low_key(defer_fp_q) and launch_ntt_moddown(wide_only).
+// forward high pass (launch_convert_h4), 2 n items of out_limbs limbs; pmod
+// per Q limb [P]_q and its Shoup constant.  The special limbs' key product
+// and the other Q limbs run through launch_ntt_low_key(defer_below) and
+// launch_ntt_moddown(wide_only).
+// With mul_b, add and mul_b are the factors a and b of the degree-2
+// products whose d0 = a0 b0 and d1 = a0 b1 + a1 b0 (a1, b1 at add1_off)
+// are the addend, formed in the kernel (launch_tensor then writes d2 and the
+// d0 / d1 limbs other kernels read).
 void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
-                            const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
-                            u64 out1_off, int out_limbs, const PostOp *post = nullptr);
+                            const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
+                            int out_limbs, const Batch *mul_b = nullptr);
 // N = 2^16: the high pass of the inverse NTT alone, in place (after the low
 // pass of launch_ntt_low_key's sp output)
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,

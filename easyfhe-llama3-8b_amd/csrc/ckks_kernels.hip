@@ -283,11 +283,6 @@ struct Galois64 {
   u64 g[kMaxBatch];
 };
 
-// item 0 of a batch on the host (null when the batch is empty)
-static inline const u64 *batch_ptr_host(const Batch &b, int i) {
-  return b.base ? b.base + (u64)i * b.stride : b.p[i];
-}
-
 struct MDCombine {
   Batch acc;        // per item: [2][E][N] (component c, limb l at (c E + l) N)
   int E;
@@ -1460,7 +1455,33 @@ __global__ __launch_bounds__(TPB, 2) void k_ntt16_low_key(LowKeyArgs a, int l_be
 // limbs' key product (and their inverse low pass) and the ModDown's
 // conversion run before it.
 // ===========================================================================
-__global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine md, Batch conv,
+// The combine's side of k_low_key_md: P^-1 per Q limb (and its quotient
+// constant), the outputs, and per item either the addend (prod 0: d0 at add,
+// d1 at add + add1_off, add null for none) or the factors of the degree-2
+// product whose d0 = a0 b0 and d1 = a0 b1 + a1 b0 are the addend (prod 1: a0
+// at add, a1 at add + add1_off, b0 and b1 likewise from mulb; prod 2: the
+// square of a, mulb unused).
+struct LowMD {
+  const u64 *pinv;
+  Batch add;
+  u64 add1_off;
+  Batch mulb;
+  Batch out;
+  u64 out1_off;
+  int prod;
+};
+
+// 4 consecutive words from a 32-byte aligned address, as 2 loads of 16 bytes
+__device__ __forceinline__ void load4(const u64 *__restrict__ p, u64 (&v)[4]) {
+  const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(p);
+  const ulonglong2 x = q[0], y = q[1];
+  v[0] = x.x;
+  v[1] = x.y;
+  v[2] = y.x;
+  v[3] = y.y;
+}
+
+__global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, LowMD md, Batch conv,
                                                        const u64 *__restrict__ pmod,
                                                        int l_begin, int n_items,
                                                        const ModQ *__restrict__ mods,
@@ -1496,13 +1517,51 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, MDCombine m
     acc0[i] = fp_mulmod(acc0[i], ri.x, ri.y, q);
     acc1[i] = fp_mulmod(acc1[i], ri.x, ri.y, q);
   }
-  if (ad0) {
+  if (md.prod) {
+    // the addend formed here from the factors (words below q < 2^45): each
+    // product |a b| < 2^90 leaves fp_mulmod within (-q, q), so d0 lies in
+    // (-q, q), d1 in (-2 q, 2 q) and [P] d again in (-q, q)
+    const u64 *pa0 = ad0 + ((size_t)l << 16) + sb, *pa1 = pa0 + md.add1_off;
+    const u64 *pb0 = md.prod == 2 ? pa0 : batch_ptr(md.mulb, it) + ((size_t)l << 16) + sb;
+    const u64 *pb1 = pb0 + md.add1_off;
+#pragma unroll
+    for (int i0 = 0; i0 < 16; i0 += 4) {
+      u64 x0[4], x1[4];
+      load4(pa0 + i0, x0);
+      load4(pa1 + i0, x1);
+      if (md.prod == 2) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const double a0 = u52_to_dbl(x0[i]), a1 = u52_to_dbl(x1[i]);
+          const double d0 = fp_mulmod(a0, a0, __dmul_rn(a0, qinv), q);
+          const double h = fp_mulmod(a0, a1, __dmul_rn(a1, qinv), q);
+          acc0[i0 + i] = __dadd_rn(acc0[i0 + i], fp_mulmod(d0, Pm, Pmq, q));
+          acc1[i0 + i] = __dadd_rn(acc1[i0 + i], fp_mulmod(__dadd_rn(h, h), Pm, Pmq, q));
+        }
+      } else {
+        u64 y0[4], y1[4];
+        load4(pb0 + i0, y0);
+        load4(pb1 + i0, y1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const double a0 = u52_to_dbl(x0[i]), a1 = u52_to_dbl(x1[i]);
+          const double b0 = u52_to_dbl(y0[i]), b1 = u52_to_dbl(y1[i]);
+          const double b0q = __dmul_rn(b0, qinv);
+          const double d0 = fp_mulmod(a0, b0, b0q, q);
+          const double d1 = __dadd_rn(fp_mulmod(a0, b1, __dmul_rn(b1, qinv), q),
+                                      fp_mulmod(a1, b0, b0q, q));
+          acc0[i0 + i] = __dadd_rn(acc0[i0 + i], fp_mulmod(d0, Pm, Pmq, q));
+          acc1[i0 + i] = __dadd_rn(acc1[i0 + i], fp_mulmod(d1, Pm, Pmq, q));
+        }
+      }
+    }
+  } else if (ad0) {
     u64 d[16];
     load16(ad0 + ((size_t)l << 16) + sb, d);
 #pragma unroll
     for (int i = 0; i < 16; i++) acc0[i] = __dadd_rn(acc0[i], fp_mulmod(u52_to_dbl(d[i]), Pm, Pmq, q));
   }
-  if (ad1) {
+  if (ad1 && !md.prod) {
     u64 d[16];
     load16(ad1 + ((size_t)l << 16) + sb, d);
 #pragma unroll
@@ -1593,28 +1652,36 @@ static LowKeyArgs low_key_args(ckks_context *c, const u64 *ext, size_t ext_strid
 void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
-                            const Batch &add, u64 add1_off, const u64 *galois, const Batch &out,
-                            u64 out1_off, int out_limbs, const PostOp *post) {
-  KTimer kt(c, "ntt_low_key_moddown",
-            8.0 * c->N * ((double)n_items * (digits * out_limbs + 7.0 * out_limbs) +
-                          2.0 * digits * out_limbs),
-            2.0 * c->N * out_limbs * digits * n_items +
-                0.5 * c->N * 12 * 2.0 * n_items * out_limbs);
+                            const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
+                            int out_limbs, const Batch *mul_b) {
   if (n_items <= 0) return;
-  if (post && (post->dbl || post->scal || batch_ptr_host(post->sub, 0)))
-    throw std::invalid_argument("fused key product + ModDown: no postop");
   if (n_items > kMaxBatch) throw std::invalid_argument("fused key product + ModDown: n <= 64");
+  if (out_limbs < 1 || out_limbs > q_limbs)
+    throw std::invalid_argument("fused key product + ModDown: output limbs");
   LowKeyArgs a = low_key_args(c, ext, ext_stride, own, nullptr, 0, key, digits, E, q_limbs, ginv);
-  MDCombine md{};
+  LowMD md{};
   md.pinv = pinv;
   md.add = add;
   md.add1_off = add1_off;
   md.out = out;
   md.out1_off = out1_off;
-  if (post) md.post = *post;
-  for (int i = 0; i < n_items; i++) md.gal.g[i] = galois[i];
-  if (out_limbs < 1 || out_limbs > q_limbs)
-    throw std::invalid_argument("fused key product + ModDown: output limbs");
+  if (mul_b) {
+    if (!batch_ptr_host(add, 0) || !add1_off)
+      throw std::invalid_argument("fused key product + ModDown: product addend needs both factors");
+    bool same = true;
+    for (int i = 0; i < n_items && same; i++) same = batch_ptr_host(add, i) == batch_ptr_host(*mul_b, i);
+    md.prod = same ? 2 : 1;
+    md.mulb = *mul_b;
+  }
+  // words per output limb and item: the extended digits, the conversion (2),
+  // the addend (2, or the product's factors: 2 or 4) and the outputs (2)
+  const double addend = md.prod == 1 ? 4.0 : 2.0;
+  KTimer kt(c, "ntt_low_key_moddown",
+            8.0 * c->N * ((double)n_items * (digits + 4.0 + addend) * out_limbs +
+                          2.0 * digits * out_limbs),
+            2.0 * c->N * out_limbs * digits * n_items +
+                0.5 * c->N * 12 * 2.0 * n_items * out_limbs +
+                (md.prod ? 3.0 * c->N * n_items * out_limbs : 0.0));
   for (int l0 = 0; l0 < out_limbs;) {
     if (!c->prime_fp[l0]) {
       l0++;
@@ -1789,35 +1856,47 @@ void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int p
 
 // Tensor product of degree-1 ciphertexts: (a0 b0, a0 b1 + a1 b0, a1 b1).
 // grid (N / 256, limbs, items)
-__global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs,
-                         const ModQ *__restrict__ mods) {
+// parts: 1 writes d0 = a0 b0 and d1 = a0 b1 + a1 b0, 2 writes d2 = a1 b1 (3
+// both), for limbs l_begin + blockIdx.y; grid (N / 256, limb count, items)
+__global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs, int l_begin,
+                         int parts, const ModQ *__restrict__ mods) {
   const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = blockIdx.y;
+  const int l = l_begin + blockIdx.y;
   const ModQ M = mods[l];
   const size_t P = (size_t)limbs << logN;
   const size_t off = ((size_t)l << logN) + k;
   const u64 *pa = batch_ptr(a, blockIdx.z), *pb = batch_ptr(b, blockIdx.z);
   u64 *po = batch_ptr(out, blockIdx.z);
-  const u64 a0 = pa[off], a1 = pa[P + off], b0 = pb[off], b1 = pb[P + off];
-  po[off] = mul_mod(a0, b0, M);
-  // a0 b1 + a1 b0 < 2 q^2 < q 2^64: one Montgomery fold, then x R
-  u64 hi = 0, lo = 0;
-  mac_wide(hi, lo, a0, b1);
-  mac_wide(hi, lo, a1, b0);
-  po[P + off] = to_mont(redc(hi, lo, M.q, M.qinv), M);
-  po[2 * P + off] = mul_mod(a1, b1, M);
+  const u64 a1 = pa[P + off], b1 = pb[P + off];
+  if (parts & 1) {
+    const u64 a0 = pa[off], b0 = pb[off];
+    po[off] = mul_mod(a0, b0, M);
+    // a0 b1 + a1 b0 < 2 q^2 < q 2^64: one Montgomery fold, then x R
+    u64 hi = 0, lo = 0;
+    mac_wide(hi, lo, a0, b1);
+    mac_wide(hi, lo, a1, b0);
+    po[P + off] = to_mont(redc(hi, lo, M.q, M.qinv), M);
+  }
+  if (parts & 2) po[2 * P + off] = mul_mod(a1, b1, M);
 }
 
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
-                   int n_items, int limbs) {
+                   int n_items, int limbs, int l_begin, int l_count, int parts) {
+  if (l_count < 0) l_count = limbs - l_begin;
+  if (n_items <= 0 || l_count <= 0) return;
+  if (parts < 1 || parts > 3 || l_begin < 0 || l_begin + l_count > limbs)
+    throw std::invalid_argument("tensor: parts or limb range");
   // a squared operand (a = b) is read once
   bool same = true;
   for (int i = 0; i < n_items && same; i++) same = batch_ptr_host(a, i) == batch_ptr_host(b, i);
-  KTimer kt(c, "tensor", 8.0 * c->N * (same ? 5.0 : 7.0) * n_items * limbs,
-            4.0 * c->N * n_items * limbs);
-  dim3 grid(c->N / TPB, limbs, n_items);
-  hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs,
-                     c->d_mods);
+  // words per coefficient: the reads of a (and b) and the writes of the parts
+  const double reads = (parts & 1 ? 2.0 : 1.0) * (same ? 1.0 : 2.0);
+  const double writes = (parts & 1 ? 2.0 : 0.0) + (parts & 2 ? 1.0 : 0.0);
+  KTimer kt(c, "tensor", 8.0 * c->N * (reads + writes) * n_items * l_count,
+            ((parts & 1 ? 3.0 : 0.0) + (parts & 2 ? 1.0 : 0.0)) * c->N * n_items * l_count);
+  dim3 grid(c->N / TPB, l_count, n_items);
+  hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs, l_begin,
+                     parts, c->d_mods);
   LAUNCH_CHECK();
 }
 
