@@ -1488,19 +1488,23 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done,
                               may_defer ? &dk : nullptr);
     if (ta && dk.on) {
-      // d0 / d1 of the dropped limbs (the lift) and of the kept limbs of
-      // primes of 2^45 or more (launch_ntt_moddown's combine)
-      for (int l0 = 0; l0 < T;) {
-        if (c->prime_fp[l0]) {
-          l0++;
+      // d0 / d1 of the kept limbs of primes of 2^45 or more (launch_ntt_moddown's
+      // combine), run by run, the last run with the dropped limbs (the lift)
+      int l0 = 0;
+      for (;;) {
+        while (l0 < T && c->prime_fp[l0]) l0++;
+        int l1 = l0;
+        while (l1 < T && !c->prime_fp[l1]) l1++;
+        int r0 = l1;
+        while (r0 < T && c->prime_fp[r0]) r0++;
+        if (r0 < T) {  // another run follows: this one alone
+          launch_tensor(c, fa, fb, prod, nb, limbs, l0, l1 - l0, 1);
+          l0 = r0;
           continue;
         }
-        int l1 = l0 + 1;
-        while (l1 < T && !c->prime_fp[l1]) l1++;
-        launch_tensor(c, fa, fb, prod, nb, limbs, l0, l1 - l0, 1);
-        l0 = l1;
+        launch_tensor(c, fa, fb, prod, nb, limbs, l0, l1 - l0, 1, T, D);
+        break;
       }
-      launch_tensor(c, fa, fb, prod, nb, limbs, T, D, 1);
     } else if (ta) {
       launch_tensor(c, fa, fb, prod, nb, limbs, 0, limbs, 1);
     }

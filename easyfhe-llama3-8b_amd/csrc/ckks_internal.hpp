@@ -393,9 +393,10 @@ void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int p
                    int limbs, int q_limbs, int op);  // op 0: add to poly 0, 1: mul all
 // out = a x b of degree-1 ciphertexts at `limbs` limbs: parts 1 writes d0 and
 // d1, 2 writes d2, 3 all three, for limbs [l_begin, l_begin + l_count)
-// (l_count -1: to the last limb)
+// (l_count -1: to the last limb) and [l_begin2, l_begin2 + l_count2)
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
-                   int n_items, int limbs, int l_begin = 0, int l_count = -1, int parts = 3);
+                   int n_items, int limbs, int l_begin = 0, int l_count = -1, int parts = 3,
+                   int l_begin2 = 0, int l_count2 = 0);
 void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int src_prime0, int t_split, int t_skip,
                           int q_limbs, bool centered);

@@ -1857,46 +1857,69 @@ void launch_scalar(ckks_context *c, const u64 *ct, const u64 *s, u64 *out, int p
 // Tensor product of degree-1 ciphertexts: (a0 b0, a0 b1 + a1 b0, a1 b1).
 // grid (N / 256, limbs, items)
 // parts: 1 writes d0 = a0 b0 and d1 = a0 b1 + a1 b0, 2 writes d2 = a1 b1 (3
-// both), for limbs l_begin + blockIdx.y; grid (N / 256, limb count, items)
-__global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs, int l_begin,
-                         int parts, const ModQ *__restrict__ mods) {
-  const int k = blockIdx.x * TPB + threadIdx.x;
-  const int l = l_begin + blockIdx.y;
+// both), for limb la + blockIdx.y (blockIdx.y < na), else lb + blockIdx.y -
+// na; two coefficients per thread.  grid (N / 512, limb count, items)
+__device__ __forceinline__ void tensor_word(u64 a0, u64 a1, u64 b0, u64 b1, const ModQ &M,
+                                            int parts, u64 &d0, u64 &d1, u64 &d2) {
+  if (parts & 1) {
+    d0 = mul_mod(a0, b0, M);
+    // a0 b1 + a1 b0 < 2 q^2 < q 2^64: one Montgomery fold, then x R
+    u64 hi = 0, lo = 0;
+    mac_wide(hi, lo, a0, b1);
+    mac_wide(hi, lo, a1, b0);
+    d1 = to_mont(redc(hi, lo, M.q, M.qinv), M);
+  }
+  if (parts & 2) d2 = mul_mod(a1, b1, M);
+}
+
+__global__ void k_tensor(Batch a, Batch b, Batch out, int logN, int limbs, int la, int na,
+                         int lb, int parts, const ModQ *__restrict__ mods) {
+  const int k = 2 * (blockIdx.x * TPB + threadIdx.x);
+  const int y = blockIdx.y;
+  const int l = y < na ? la + y : lb + (y - na);
   const ModQ M = mods[l];
   const size_t P = (size_t)limbs << logN;
   const size_t off = ((size_t)l << logN) + k;
   const u64 *pa = batch_ptr(a, blockIdx.z), *pb = batch_ptr(b, blockIdx.z);
   u64 *po = batch_ptr(out, blockIdx.z);
-  const u64 a1 = pa[P + off], b1 = pb[P + off];
+  using V = ulonglong2;
+  const V a1 = *reinterpret_cast<const V *>(pa + P + off);
+  const V b1 = *reinterpret_cast<const V *>(pb + P + off);
+  V a0{}, b0{};
   if (parts & 1) {
-    const u64 a0 = pa[off], b0 = pb[off];
-    po[off] = mul_mod(a0, b0, M);
-    // a0 b1 + a1 b0 < 2 q^2 < q 2^64: one Montgomery fold, then x R
-    u64 hi = 0, lo = 0;
-    mac_wide(hi, lo, a0, b1);
-    mac_wide(hi, lo, a1, b0);
-    po[P + off] = to_mont(redc(hi, lo, M.q, M.qinv), M);
+    a0 = *reinterpret_cast<const V *>(pa + off);
+    b0 = *reinterpret_cast<const V *>(pb + off);
   }
-  if (parts & 2) po[2 * P + off] = mul_mod(a1, b1, M);
+  u64 d0[2], d1[2], d2[2];
+  tensor_word(a0.x, a1.x, b0.x, b1.x, M, parts, d0[0], d1[0], d2[0]);
+  tensor_word(a0.y, a1.y, b0.y, b1.y, M, parts, d0[1], d1[1], d2[1]);
+  if (parts & 1) {
+    *reinterpret_cast<V *>(po + off) = V{d0[0], d0[1]};
+    *reinterpret_cast<V *>(po + P + off) = V{d1[0], d1[1]};
+  }
+  if (parts & 2) *reinterpret_cast<V *>(po + 2 * P + off) = V{d2[0], d2[1]};
 }
 
 void launch_tensor(ckks_context *c, const Batch &a, const Batch &b, const Batch &out,
-                   int n_items, int limbs, int l_begin, int l_count, int parts) {
+                   int n_items, int limbs, int l_begin, int l_count, int parts, int l_begin2,
+                   int l_count2) {
   if (l_count < 0) l_count = limbs - l_begin;
-  if (n_items <= 0 || l_count <= 0) return;
-  if (parts < 1 || parts > 3 || l_begin < 0 || l_begin + l_count > limbs)
-    throw std::invalid_argument("tensor: parts or limb range");
+  if (n_items <= 0 || l_count + l_count2 <= 0) return;
+  if (parts < 1 || parts > 3 || l_begin < 0 || l_count < 0 || l_begin + l_count > limbs ||
+      l_count2 < 0 || (l_count2 > 0 && (l_begin2 < 0 || l_begin2 + l_count2 > limbs)))
+    throw std::invalid_argument("tensor: parts or limb ranges");
+  const int nl = l_count + l_count2;
   // a squared operand (a = b) is read once
   bool same = true;
   for (int i = 0; i < n_items && same; i++) same = batch_ptr_host(a, i) == batch_ptr_host(b, i);
   // words per coefficient: the reads of a (and b) and the writes of the parts
   const double reads = (parts & 1 ? 2.0 : 1.0) * (same ? 1.0 : 2.0);
   const double writes = (parts & 1 ? 2.0 : 0.0) + (parts & 2 ? 1.0 : 0.0);
-  KTimer kt(c, "tensor", 8.0 * c->N * (reads + writes) * n_items * l_count,
-            ((parts & 1 ? 3.0 : 0.0) + (parts & 2 ? 1.0 : 0.0)) * c->N * n_items * l_count);
-  dim3 grid(c->N / TPB, l_count, n_items);
+  KTimer kt(c, "tensor", 8.0 * c->N * (reads + writes) * n_items * nl,
+            ((parts & 1 ? 3.0 : 0.0) + (parts & 2 ? 1.0 : 0.0)) * c->N * n_items * nl);
+  dim3 grid(c->N / (2 * TPB), nl, n_items);
   hipLaunchKernelGGL(k_tensor, grid, dim3(TPB), 0, c->stream, a, b, out, c->logN, limbs, l_begin,
-                     parts, c->d_mods);
+                     l_count, l_begin2, parts, c->d_mods);
   LAUNCH_CHECK();
 }
 
