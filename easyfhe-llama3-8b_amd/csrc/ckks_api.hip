@@ -1033,8 +1033,11 @@ static Batch strided(u64 *base, size_t stride) {
 // inner product then reads them from d (ks_inner's `own`).
 // high_only (N = 2^16, own_copy false): the converted limbs get only the
 // high pass of the forward NTT; launch_ntt_low_key runs the low pass.
+// dmul (tile path, own_copy false): the polynomials are d[i] x dmul[i] word
+// by word, formed by the inverse low pass (modup_tile_ok tells when).
 static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
-                     Scratch &s, bool own_copy = true, bool high_only = false) {
+                     Scratch &s, bool own_copy = true, bool high_only = false,
+                     const Batch *dmul = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   u64 *coeff = s.get((size_t)n * limbs * N);
@@ -1045,9 +1048,10 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
   // (not high_only) the targets' low pass follows
   bool tile = c->ks_tile;
   for (int j = 0; j < digits && tile; j++) tile = convert_h4_ok(c, bc_up(c, limbs, j));
+  if (dmul && (!tile || own_copy)) throw std::logic_error("ModUp of a product: tile path only");
   if (tile) {
     const size_t est = (size_t)digits * E * N;
-    launch_ntt_inv_low(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs);
+    launch_ntt_inv_low(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs, dmul);
     for (int j = 0; j < digits; j++) {
       const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
       u64 *ej = ext + (size_t)j * E * N;
@@ -1103,6 +1107,7 @@ struct KsDeferred {
   const u64 *ext = nullptr;
   size_t est = 0;
   Batch own{};
+  const Batch *own_b = nullptr;  // own x own_b is the source (ks_modup_inner's dmul)
   const DeviceKey *key = nullptr;
   int digits = 0;
   u64 ginv = 1;
@@ -1162,7 +1167,8 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
     if (deferred)
       launch_low_key_moddown(c, dk->ext, dk->est, dk->own, n, *dk->key, dk->digits, E, limbs,
                              dk->ginv, strided(conv, (size_t)limbs * N), pinv,
-                             pmod_table(c, limbs), a0, add1_off, o0, out1_off, limbs);
+                             pmod_table(c, limbs), a0, add1_off, o0, out1_off, limbs,
+                             nullptr, dk->own_b);
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
                        pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile,
                        deferred);
@@ -1244,7 +1250,7 @@ static u64 galois_inverse(const ckks_context *c, u64 g) {
 static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *d,
                            const std::vector<KsJob> &jobs, Scratch &s,
                            const Strided *sp = nullptr, bool *sp_done = nullptr,
-                           KsDeferred *dk = nullptr) {
+                           KsDeferred *dk = nullptr, const Batch *dmul = nullptr) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   const size_t est = (size_t)digits * E * N;
@@ -1252,7 +1258,8 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
   const bool fused = c->ks_fused && c->logN == 16 && n <= kMaxBatch;
   const bool spf = fused && sp && c->ks_sp_inv && low_key_special_fp(c);
   if (sp_done) *sp_done = spf;
-  ks_modup(c, limbs, n, d, ext, s, false, fused);
+  if (dmul && !fused) throw std::logic_error("key switch of a product: fused path only");
+  ks_modup(c, limbs, n, d, ext, s, false, fused, dmul);
   if (!fused) return ks_inner(c, limbs, ext, jobs, s, d);
   u64 *acc = s.get((size_t)n * 2 * E * N);
   Batch ob{};
@@ -1266,14 +1273,26 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
       dk->ext = ext;
       dk->est = est;
       dk->own = ob;
+      dk->own_b = dmul;
       dk->key = jobs[0].key;
       dk->digits = digits;
       dk->ginv = ginv;
     }
   }
   launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
-                     ginv, spf ? sp : nullptr, defer ? (dk->below >= 0 ? dk->below : limbs) : 0);
+                     ginv, spf ? sp : nullptr, defer ? (dk->below >= 0 ? dk->below : limbs) : 0,
+                     dmul);
   return acc;
+}
+
+// Whether ks_modup_inner of n polynomials at `limbs` limbs takes the fused
+// tile path, on which the polynomials may be products formed on load (dmul)
+static bool modup_tile_ok(ckks_context *c, int limbs, int n) {
+  if (!(c->ks_fused && c->logN == 16 && n <= kMaxBatch && c->ks_tile)) return false;
+  const int digits = (limbs + c->ds - 1) / c->ds;
+  for (int j = 0; j < digits; j++)
+    if (!convert_h4_ok(c, bc_up(c, limbs, j))) return false;
+  return true;
 }
 
 // Key inner product for every job, ModDown, and the combine with addends.
@@ -1455,17 +1474,22 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
   const BCTable &bt = bc_down(c, limbs);
   const u64 *rt = relin_rs_table(c, limbs, D);
   auto run = [&](int b0, int nb, Scratch &s) {
-    Batch fa{}, fb{};
+    Batch fa{}, fb{}, fb1{};
     const Batch prod = strided(in[b0]->d, 3 * P);
+    std::vector<const u64 *> d(nb);
+    for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
+    // on the fused tile path d2 = a1 b1 is formed where the ModUp reads it
+    // (dmul: d[i] = a1 and fb1 the b1 polynomials), else written first
+    const bool d2_fused = ta && modup_tile_ok(c, limbs, nb);
     if (ta) {
       for (int i = 0; i < nb; i++) {
         fa.p[i] = batch_ptr_host(*ta, b0 + i);
         fb.p[i] = batch_ptr_host(*tb, b0 + i);
+        fb1.p[i] = fb.p[i] + P;
+        if (d2_fused) d[i] = fa.p[i] + P;
       }
-      launch_tensor(c, fa, fb, prod, nb, limbs, 0, limbs, 2);
+      if (!d2_fused) launch_tensor(c, fa, fb, prod, nb, limbs, 0, limbs, 2);
     }
-    std::vector<const u64 *> d(nb);
-    for (int i = 0; i < nb; i++) d[i] = in[b0 + i]->d + 2 * P;
     const int E = limbs + A;
     std::vector<KsJob> jobs(nb);
     for (int i = 0; i < nb; i++) jobs[i] = KsJob{i, &key, 1, nullptr, nullptr, nullptr, nullptr};
@@ -1486,7 +1510,7 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
     dk.below = T;
     const bool may_defer = tile && !ps;
     u64 *acc = ks_modup_inner(c, limbs, nb, d.data(), jobs, s, &sp, &sp_done,
-                              may_defer ? &dk : nullptr);
+                              may_defer ? &dk : nullptr, d2_fused ? &fb1 : nullptr);
     if (ta && dk.on) {
       // d0 / d1 of the kept limbs of primes of 2^45 or more (launch_ntt_moddown's
       // combine), run by run, the last run with the dropped limbs (the lift)
@@ -1540,7 +1564,8 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
       if (dk.on)
         launch_low_key_moddown(c, dk.ext, dk.est, dk.own, nb, *dk.key, dk.digits, E, limbs,
                                dk.ginv, strided(conv, (size_t)T * N), rt, pmod_table(c, limbs),
-                               ta ? fa : d3, P, o0, (u64)T * N, T, ta ? &fb : nullptr);
+                               ta ? fa : d3, P, o0, (u64)T * N, T, ta ? &fb : nullptr,
+                               dk.own_b);
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
                          d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile, dk.on);
     } else {

@@ -80,6 +80,14 @@ inline u64 *batch_ptr_host(const Batch &b, int i) {
   return b.base ? b.base + (u64)i * b.stride : b.p[i];
 }
 
+// Kernels that form a word-by-word product a x b on load: 2 when every item
+// of b is the item of a (a square, read once), else 1
+inline int product_mode(const Batch &a, const Batch &b, int n_items) {
+  for (int i = 0; i < n_items; i++)
+    if (batch_ptr_host(a, i) != batch_ptr_host(b, i)) return 1;
+  return 2;
+}
+
 // ---------------------------------------------------------------------------
 // modular arithmetic (device)
 // ---------------------------------------------------------------------------
@@ -421,10 +429,12 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
 bool low_key_special_fp(const ckks_context *c);
 // The Q limbs of fp64 primes below defer_below are skipped
 // (launch_low_key_moddown runs their key product with the ModDown's combine)
+// With own_b, the digits' own limbs are those of own x own_b (word by word),
+// formed where they are read.
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr,
-                        int defer_below = 0);
+                        int defer_below = 0, const Batch *own_b = nullptr);
 // N = 2^16: for the Q limbs of fp64 primes, launch_ntt_low_key's key product
 // and launch_ntt_moddown's combine (addends and outputs as there, no postop)
 // in one kernel, the accumulator kept in the block, for output limbs
@@ -436,13 +446,14 @@ void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, cons
 // launch_ntt_moddown(wide_only).
 // With mul_b, add and mul_b are the factors a and b of the degree-2
 // products whose d0 = a0 b0 and d1 = a0 b1 + a1 b0 (a1, b1 at add1_off)
-// are the addend, formed in the kernel (launch_tensor then writes d2 and the
-// d0 / d1 limbs other kernels read).
+// are the addend, formed in the kernel (launch_tensor then writes the d0 /
+// d1 limbs other kernels read).  own_b as for launch_ntt_low_key.
 void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
-                            int out_limbs, const Batch *mul_b = nullptr);
+                            int out_limbs, const Batch *mul_b = nullptr,
+                            const Batch *own_b = nullptr);
 // N = 2^16: the high pass of the inverse NTT alone, in place (after the low
 // pass of launch_ntt_low_key's sp output)
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
@@ -459,14 +470,15 @@ void launch_ntt_moddown(ckks_context *c, const Batch &conv, int n, int limbs, co
                         const u64 *galois, const Batch &out, u64 out1_off,
                         const u64 *amul = nullptr, const PostOp *post = nullptr,
                         bool high_done = false, bool wide_only = false);
-// N = 2^16: the inverse NTT's low pass alone (its high pass then runs in
-// launch_convert_h4 or launch_ntt_inv_high)
 // the forward NTT's low pass alone, in place (N = 2^16: after the high pass of
 // launch_convert_h4 or launch_ntt_fwd_high)
 void launch_ntt_fwd_low(ckks_context *c, const Batch &data, int n_items, int l_begin,
                         int l_count, int q_limbs);
+// N = 2^16: the inverse NTT's low pass alone (its high pass then runs in
+// launch_convert_h4 or launch_ntt_inv_high); with mul, of src x mul word by
+// word, formed on load
 void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
-                        int l_begin, int l_count, int q_limbs);
+                        int l_begin, int l_count, int q_limbs, const Batch *mul = nullptr);
 // N = 2^16: launch_basis_convert of inverse-low-passed sources (src item at
 // the first source limb, as launch_basis_convert's) with the inverse high
 // pass before and the forward high pass of every target after, in one

@@ -559,7 +559,8 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
                                                        int q_limbs, int L,
                                                        const ModQ *__restrict__ mods,
                                                        const u64 *__restrict__ ipsi,
-                                                       const u64 *__restrict__ ipsi_sh) {
+                                                       const u64 *__restrict__ ipsi_sh,
+                                                       const Batch &mul, int mm) {
   u64 *sm = lds;
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
@@ -572,9 +573,23 @@ __device__ __forceinline__ void k_ntt16_inv_low_body(u64 *__restrict__ lds, Batc
   const int row = blockIdx.x * 16 + rl;
   u64 x[16];
   // round B^-1: column = 16 c0 + j, stages on column bits 0..3; the load
-  // goes through LDS so that adjacent lanes read adjacent words
+  // goes through LDS so that adjacent lanes read adjacent words (with mm,
+  // of the product src x mul or src^2, formed here)
+  if (mm) {
+    const ModQ M = mods[p];
+    const u64 *mb = mm == 2 ? in
+                            : batch_ptr(mul, blockIdx.y) + ((size_t)limb << 16) +
+                                  (size_t)blockIdx.x * 4096;
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = in[rl * 256 + c0 + 16 * k];
+    for (int k = 0; k < 16; k++) {
+      const int e = rl * 256 + c0 + 16 * k;
+      const u64 v = in[e];
+      sm[lds16(rl, c0 + 16 * k)] = mul_mod(v, mm == 2 ? v : mb[e], M);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = in[rl * 256 + c0 + 16 * k];
+  }
   row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) x[j] = sm[lds16(rl, 16 * c0 + j)];
@@ -919,7 +934,8 @@ __device__ __forceinline__ void fp_inv_low_tile(double *__restrict__ sm, int til
 __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
                                                         const ModQ *__restrict__ mods,
-                                                        const double2 *__restrict__ itw) {
+                                                        const double2 *__restrict__ itw,
+                                                        const Batch &mul, int mm) {
   double *sm = reinterpret_cast<double *>(lds);
   const int limb = l_begin + blockIdx.z;
   const int p = prime_of(limb, q_limbs, L);
@@ -928,8 +944,23 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   const u64 *in = batch_ptr(src, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  if (mm) {
+    // the transform of src x mul (mm 1) or src^2 (mm 2), formed here:
+    // canonical products of words below q < 2^45
+    const u64 *mb = mm == 2 ? in
+                            : batch_ptr(mul, blockIdx.y) + ((size_t)limb << 16) +
+                                  (size_t)blockIdx.x * 4096;
 #pragma unroll
-  for (int k = 0; k < 16; k++) sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
+    for (int k = 0; k < 16; k++) {
+      const int e = rl * 256 + c0 + 16 * k;
+      const double x = u52_to_dbl(in[e]), w = mm == 2 ? x : u52_to_dbl(mb[e]);
+      sm[lds16(rl, c0 + 16 * k)] = fp_canon_d(fp_mulmod(x, w, __dmul_rn(w, qinv), q), qinv, q);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      sm[lds16(rl, c0 + 16 * k)] = u52_to_dbl(in[rl * 256 + c0 + 16 * k]);
+  }
   row_sync();
   fp_inv_low_tile(sm, blockIdx.x, T, q, qinv, out);
 }
@@ -987,17 +1018,19 @@ __global__ __launch_bounds__(TPB) void k_ntt16m_fwd_low(Batch dst, int l_begin, 
     k_ntt16_fwd_low_body<COMBINE>(lds, dst, l_begin, q_limbs, L, mods, psi, psi_sh, md);
 }
 
+// mm 1: the transform of src x mul (word by word), 2: of src^2, 0: of src
 __global__ __launch_bounds__(TPB) void k_ntt16m_inv_low(Batch src, Batch dst, int l_begin,
                                                         int q_limbs, int L,
                                                         const ModQ *__restrict__ mods,
                                                         const u64 *__restrict__ ipsi,
                                                         const u64 *__restrict__ ipsi_sh,
-                                                        const double2 *__restrict__ itw) {
+                                                        const double2 *__restrict__ itw,
+                                                        Batch mul, int mm) {
   __shared__ u64 lds[16 * 272];
   if (mods[prime_of(l_begin + blockIdx.z, q_limbs, L)].q < kFpPrimeBound)
-    k_ntt16f_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, itw);
+    k_ntt16f_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, itw, mul, mm);
   else
-    k_ntt16_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh);
+    k_ntt16_inv_low_body(lds, src, dst, l_begin, q_limbs, L, mods, ipsi, ipsi_sh, mul, mm);
 }
 
 __global__ __launch_bounds__(TPB) void k_ntt16m_inv_high(
@@ -1057,7 +1090,8 @@ static void ntt16_dispatch(ckks_context *c, const Batch &src, const Batch &dst, 
     LAUNCH_CHECK();
   } else {
     hipLaunchKernelGGL(k_ntt16m_inv_low, grid, block, 0, c->stream, src, dst, l_begin, q_limbs,
-                       c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh, (const double2 *)c->d_itw_fp);
+                       c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh, (const double2 *)c->d_itw_fp,
+                       Batch{}, 0);
     LAUNCH_CHECK();
     launch_inv_high16(c, dst, n_items, l_begin, l_count, q_limbs);
   }
@@ -1198,6 +1232,10 @@ struct LowKeyArgs {
   const u64 *ext;     // item it, digit j, limb l: ext + it ext_stride + ((j E + l) << 16)
   size_t ext_stride;
   Batch own;          // per item: the source polynomial, limb l at l << 16 (NTT form)
+  // own_mul 1: the source polynomial is own x own_b word by word, 2: own^2
+  // (formed where the digit's own limb is read), 0: own itself
+  Batch own_b;
+  int own_mul;
   u64 *acc;           // per item [2][E][N] at acc + it acc_stride
   size_t acc_stride;
   const u64 *key;     // [digits][2][K][N], Montgomery form, source order
@@ -1214,6 +1252,16 @@ struct LowKeyArgs {
 
 // Offset of position sb + i's key word from key_slot(sb) (sb 16-aligned)
 __device__ __forceinline__ constexpr int kword(int i) { return ((i >> 1) << 7) | (i & 1); }
+
+// 4 consecutive words from a 32-byte aligned address, as 2 loads of 16 bytes
+__device__ __forceinline__ void load4(const u64 *__restrict__ p, u64 (&v)[4]) {
+  const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(p);
+  const ulonglong2 x = q[0], y = q[1];
+  v[0] = x.x;
+  v[1] = x.y;
+  v[2] = y.x;
+  v[3] = y.y;
+}
 
 // 16 consecutive words from a 128-byte aligned address, as 8 loads of 16 bytes
 __device__ __forceinline__ void load16(const u64 *__restrict__ p, u64 (&v)[16]) {
@@ -1283,7 +1331,22 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
   const int jo = l < a.q_limbs ? l / a.ds : -1;
   for (int j = 0; j < a.digits; j++) {
     double y[16];
-    if (j == jo) {
+    if (j == jo && a.own_mul) {
+      // canonical products of words below q < 2^45, four at a time
+      const u64 *pa = batch_ptr(a.own, it) + ((size_t)l << 16) + sb;
+      const u64 *pb = a.own_mul == 2 ? pa : batch_ptr(a.own_b, it) + ((size_t)l << 16) + sb;
+#pragma unroll
+      for (int i0 = 0; i0 < 16; i0 += 4) {
+        u64 wa[4], wb[4];
+        load4(pa + i0, wa);
+        if (a.own_mul == 1) load4(pb + i0, wb);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const double x = u52_to_dbl(wa[i]), w = a.own_mul == 2 ? x : u52_to_dbl(wb[i]);
+          y[i0 + i] = fp_canon_d(fp_mulmod(x, w, __dmul_rn(w, qinv), q), qinv, q);
+        }
+      }
+    } else if (j == jo) {
       u64 w[16];
       load16(batch_ptr(a.own, it) + ((size_t)l << 16) + sb, w);
 #pragma unroll
@@ -1373,7 +1436,18 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
   u64 acc0[16], acc1[16];
   for (int j = 0; j < a.digits; j++) {
     u64 y[16];
-    if (j == jo) {
+    if (j == jo && a.own_mul) {
+      const u64 *pa = batch_ptr(a.own, it) + ((size_t)l << 16) + sb;
+      const u64 *pb = a.own_mul == 2 ? pa : batch_ptr(a.own_b, it) + ((size_t)l << 16) + sb;
+#pragma unroll
+      for (int i0 = 0; i0 < 16; i0 += 4) {
+        u64 wa[4], wb[4];
+        load4(pa + i0, wa);
+        if (a.own_mul == 1) load4(pb + i0, wb);
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[i0 + i] = mul_mod(wa[i], a.own_mul == 2 ? wa[i] : wb[i], M);
+      }
+    } else if (j == jo) {
       load16(batch_ptr(a.own, it) + ((size_t)l << 16) + sb, y);
     } else {
       const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
@@ -1471,15 +1545,6 @@ struct LowMD {
   int prod;
 };
 
-// 4 consecutive words from a 32-byte aligned address, as 2 loads of 16 bytes
-__device__ __forceinline__ void load4(const u64 *__restrict__ p, u64 (&v)[4]) {
-  const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(p);
-  const ulonglong2 x = q[0], y = q[1];
-  v[0] = x.x;
-  v[1] = x.y;
-  v[2] = y.x;
-  v[3] = y.y;
-}
 
 __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, LowMD md, Batch conv,
                                                        const u64 *__restrict__ pmod,
@@ -1628,7 +1693,8 @@ bool low_key_special_fp(const ckks_context *c) {
 
 static LowKeyArgs low_key_args(ckks_context *c, const u64 *ext, size_t ext_stride,
                                const Batch &own, u64 *acc, size_t acc_stride,
-                               const DeviceKey &key, int digits, int E, int q_limbs, u64 ginv) {
+                               const DeviceKey &key, int digits, int E, int q_limbs, u64 ginv,
+                               const Batch *own_b, int n_items) {
   if (c->logN != 16) throw std::invalid_argument("fused low pass and key product: N = 2^16 only");
   if (digits < 1 || digits > key.digits || q_limbs > c->L || E != q_limbs + c->alpha)
     throw std::invalid_argument("fused low pass and key product: shape");
@@ -1636,6 +1702,10 @@ static LowKeyArgs low_key_args(ckks_context *c, const u64 *ext, size_t ext_strid
   a.ext = ext;
   a.ext_stride = ext_stride;
   a.own = own;
+  if (own_b) {
+    a.own_b = *own_b;
+    a.own_mul = product_mode(own, *own_b, n_items);
+  }
   a.acc = acc;
   a.acc_stride = acc_stride;
   a.key = key.data;
@@ -1653,12 +1723,13 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
-                            int out_limbs, const Batch *mul_b) {
+                            int out_limbs, const Batch *mul_b, const Batch *own_b) {
   if (n_items <= 0) return;
   if (n_items > kMaxBatch) throw std::invalid_argument("fused key product + ModDown: n <= 64");
   if (out_limbs < 1 || out_limbs > q_limbs)
     throw std::invalid_argument("fused key product + ModDown: output limbs");
-  LowKeyArgs a = low_key_args(c, ext, ext_stride, own, nullptr, 0, key, digits, E, q_limbs, ginv);
+  LowKeyArgs a = low_key_args(c, ext, ext_stride, own, nullptr, 0, key, digits, E, q_limbs, ginv,
+                              own_b, n_items);
   LowMD md{};
   md.pinv = pinv;
   md.add = add;
@@ -1668,9 +1739,7 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
   if (mul_b) {
     if (!batch_ptr_host(add, 0) || !add1_off)
       throw std::invalid_argument("fused key product + ModDown: product addend needs both factors");
-    bool same = true;
-    for (int i = 0; i < n_items && same; i++) same = batch_ptr_host(add, i) == batch_ptr_host(*mul_b, i);
-    md.prod = same ? 2 : 1;
+    md.prod = product_mode(add, *mul_b, n_items);
     md.mulb = *mul_b;
   }
   // words per output limb and item: the extended digits, the conversion (2),
@@ -1700,14 +1769,14 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp,
-                        int defer_below) {
+                        int defer_below, const Batch *own_b) {
   KTimer kt(c, "ntt_low_key",
             8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
   audit_keyswitch(c, n_items, 1, q_limbs, digits, E);
   if (n_items <= 0) return;
   LowKeyArgs a = low_key_args(c, ext, ext_stride, own, acc, acc_stride, key, digits, E, q_limbs,
-                              ginv);
+                              ginv, own_b, n_items);
   if (sp) {
     if (!low_key_special_fp(c)) throw std::invalid_argument("fused special inverse: fp64 special primes only");
     a.sp = sp->base;
@@ -2947,13 +3016,15 @@ void launch_ntt_fwd_low(ckks_context *c, const Batch &data, int n_items, int l_b
 // Only the low pass of the inverse NTT (bit positions 0..11), for limbs
 // whose high pass runs inside launch_convert_h4.  N = 2^16 only.
 void launch_ntt_inv_low(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
-                        int l_begin, int l_count, int q_limbs) {
-  KTimer kt(c, "ntt_inv", 16.0 * c->N * n_items * l_count, 0.5 * c->N * 12 * n_items * l_count);
+                        int l_begin, int l_count, int q_limbs, const Batch *mul) {
+  const int mm = mul ? product_mode(src, *mul, n_items) : 0;
+  KTimer kt(c, "ntt_inv", (mm == 1 ? 24.0 : 16.0) * c->N * n_items * l_count,
+            (0.5 * 12 + (mm ? 1.0 : 0.0)) * c->N * n_items * l_count);
   if (n_items <= 0 || l_count <= 0) return;
   if (c->logN != 16) throw std::invalid_argument("inverse low pass alone: N = 2^16 only");
   hipLaunchKernelGGL(k_ntt16m_inv_low, dim3(16, n_items, l_count), dim3(TPB), 0, c->stream, src,
                      dst, l_begin, q_limbs, c->L, c->d_mods, c->d_ipsi, c->d_ipsi_sh,
-                     (const double2 *)c->d_itw_fp);
+                     (const double2 *)c->d_itw_fp, mul ? *mul : Batch{}, mm);
   LAUNCH_CHECK();
 }
 
