@@ -878,7 +878,8 @@ __device__ __forceinline__ void k_ntt16f_fwd_low_body(u64 *__restrict__ lds, Bat
 }
 
 // The fp64 inverse low pass of one 4096-word tile held in the LDS tile sm
-// (position rl 256 + c of the tile at lds16(rl, c), values in [0, q)),
+// (position rl 256 + c of the tile at lds16(rl, c), exact integers of
+// magnitude below q),
 // rows 16 tile .. 16 tile + 15 of 256: round A on bit positions 3..0 from
 // the 16 consecutive positions 16 c0 + j of row rl, round B on 7..4 from
 // positions c0 + 16 k, round Z on 11..8 from positions t + 256 k; the result
@@ -945,8 +946,9 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
   u64 *out = batch_ptr(dst, blockIdx.y) + ((size_t)limb << 16) + (size_t)blockIdx.x * 4096;
   const int c0 = threadIdx.x & 15, rl = threadIdx.x >> 4;
   if (mm) {
-    // the transform of src x mul (mm 1) or src^2 (mm 2), formed here:
-    // canonical products of words below q < 2^45
+    // the transform of src x mul (mm 1) or src^2 (mm 2), formed here: the
+    // product of two words below q < 2^45 leaves fp_mulmod in (-q, q), the
+    // magnitude fp_inv_low_tile takes
     const u64 *mb = mm == 2 ? in
                             : batch_ptr(mul, blockIdx.y) + ((size_t)limb << 16) +
                                   (size_t)blockIdx.x * 4096;
@@ -954,7 +956,7 @@ __device__ __forceinline__ void k_ntt16f_inv_low_body(u64 *__restrict__ lds, Bat
     for (int k = 0; k < 16; k++) {
       const int e = rl * 256 + c0 + 16 * k;
       const double x = u52_to_dbl(in[e]), w = mm == 2 ? x : u52_to_dbl(mb[e]);
-      sm[lds16(rl, c0 + 16 * k)] = fp_canon_d(fp_mulmod(x, w, __dmul_rn(w, qinv), q), qinv, q);
+      sm[lds16(rl, c0 + 16 * k)] = fp_mulmod(x, w, __dmul_rn(w, qinv), q);
     }
   } else {
 #pragma unroll
@@ -1332,7 +1334,7 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
   for (int j = 0; j < a.digits; j++) {
     double y[16];
     if (j == jo && a.own_mul) {
-      // canonical products of words below q < 2^45, four at a time
+      // products of words below q < 2^45, in (-q, q), four at a time
       const u64 *pa = batch_ptr(a.own, it) + ((size_t)l << 16) + sb;
       const u64 *pb = a.own_mul == 2 ? pa : batch_ptr(a.own_b, it) + ((size_t)l << 16) + sb;
 #pragma unroll
@@ -1343,7 +1345,7 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const double x = u52_to_dbl(wa[i]), w = a.own_mul == 2 ? x : u52_to_dbl(wb[i]);
-          y[i0 + i] = fp_canon_d(fp_mulmod(x, w, __dmul_rn(w, qinv), q), qinv, q);
+          y[i0 + i] = fp_mulmod(x, w, __dmul_rn(w, qinv), q);
         }
       }
     } else if (j == jo) {
