@@ -1373,16 +1373,32 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
     // words of positions sb + i sit at key_slot(sb + i) = kslot + kword(i)
     const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + kslot;
     const u64 *ka = kb + (size_t)a.K * 65536;
+    // groups of 4 positions; each group's 8 key words are loaded one group
+    // ahead of their products
+    u64 kw[2][8];
 #pragma unroll
-    for (int i0 = 0; i0 < 16; i0 += 4) {
+    for (int i = 0; i < 4; i++) {
+      kw[0][2 * i] = kb[kword(i)];
+      kw[0][2 * i + 1] = ka[kword(i)];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
       __builtin_amdgcn_sched_barrier(0);
+      if (g < 3) {
 #pragma unroll
-      for (int i = i0; i < i0 + 4; i++) {
-        const double wb = u52_to_dbl(kb[kword(i)]), wa = u52_to_dbl(ka[kword(i)]);
-        const double pb = fp_mulmod(y[i], wb, __dmul_rn(wb, qinv), q);
-        const double pa = fp_mulmod(y[i], wa, __dmul_rn(wa, qinv), q);
-        acc0[i] = j == 0 ? pb : __dadd_rn(acc0[i], pb);
-        acc1[i] = j == 0 ? pa : __dadd_rn(acc1[i], pa);
+        for (int i = 0; i < 4; i++) {
+          kw[(g + 1) & 1][2 * i] = kb[kword(4 * (g + 1) + i)];
+          kw[(g + 1) & 1][2 * i + 1] = ka[kword(4 * (g + 1) + i)];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int e = 4 * g + i;
+        const double wb = u52_to_dbl(kw[g & 1][2 * i]), wa = u52_to_dbl(kw[g & 1][2 * i + 1]);
+        const double pb = fp_mulmod(y[e], wb, __dmul_rn(wb, qinv), q);
+        const double pa = fp_mulmod(y[e], wa, __dmul_rn(wa, qinv), q);
+        acc0[e] = j == 0 ? pb : __dadd_rn(acc0[e], pb);
+        acc1[e] = j == 0 ? pa : __dadd_rn(acc1[e], pa);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
