@@ -487,7 +487,7 @@ def _subsum_many(xs: list, prog: BootstrapProgram, ctx) -> list:
     ciphertext of the batch (one batched key switch per rotation)."""
     for r in prog.subsum:
         rot = fhe.homo_rotate_many(xs, int(r), ctx)
-        nxt = [fhe.homo_add(a, b, ctx) for a, b in zip(xs, rot)]
+        nxt = fhe.homo_add_many(xs, rot, ctx)
         for a, b in zip(xs, rot):
             a.release()
             b.release()
@@ -583,8 +583,11 @@ def _bootstrap_group(cts: list, ctx, prog: BootstrapProgram) -> list:
         k = len(cts)
         # real and imaginary parts of the whole group run through EvalMod together
         s = _evalmod(ops, cheb.LCt(re.ct + im, 0), prog).ct
-        u = [fhe.homo_add(s[i], fhe.homo_mul_i(s[k + i], ctx), ctx) for i in range(k)]
-        del s
+        mi = [fhe.homo_mul_i(s[k + i], ctx) for i in range(k)]
+        u = fhe.homo_add_many(s[:k], mi, ctx)
+        for x in mi:
+            x.release()
+        del s, mi
     for lv in prog.stc:
         u = _linear_level_many(u, lv, prog, ctx)
     for x, r in zip(u, ratios):

@@ -255,8 +255,8 @@ class BatchLadderOps(LadderOps):
     def add(self, a: LCt, b: LCt, sign: float = 1.0) -> LCt:
         lev = max(a.level, b.level)
         a, b = self.lower(a, lev), self.lower(b, lev)
-        fn = fhe.homo_add if sign > 0 else fhe.homo_sub
-        return LCt([fn(x, y, self.ctx) for x, y in zip(a.ct, b.ct)], lev)
+        fn = fhe.homo_add_many if sign > 0 else fhe.homo_sub_many
+        return LCt(fn(a.ct, b.ct, self.ctx), lev)
 
     def add_const(self, a: LCt, c: float) -> LCt:
         if c == 0.0:
@@ -267,7 +267,7 @@ class BatchLadderOps(LadderOps):
         return LCt([fhe.homo_add_scalar(x, enc, self.ctx) for x in a.ct], a.level)
 
     def double(self, a: LCt) -> LCt:
-        return LCt([fhe.homo_add(x, x, self.ctx) for x in a.ct], a.level)
+        return LCt(fhe.homo_add_many(a.ct, a.ct, self.ctx), a.level)
 
     def mul(self, a: LCt, b: LCt) -> LCt:
         lev = max(a.level, b.level)
