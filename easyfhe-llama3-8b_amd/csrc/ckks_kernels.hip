@@ -1607,11 +1607,18 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, LowMD md, B
     const u64 *pa0 = ad0 + ((size_t)l << 16) + sb, *pa1 = pa0 + md.add1_off;
     const u64 *pb0 = md.prod == 2 ? pa0 : batch_ptr(md.mulb, it) + ((size_t)l << 16) + sb;
     const u64 *pb1 = pb0 + md.add1_off;
+    // each group of 4 positions' factor words loaded one group ahead
+    u64 fx[2][2][4];
+    load4(pa0, fx[0][0]);
+    load4(pa1, fx[0][1]);
 #pragma unroll
     for (int i0 = 0; i0 < 16; i0 += 4) {
-      u64 x0[4], x1[4];
-      load4(pa0 + i0, x0);
-      load4(pa1 + i0, x1);
+      const int cur = (i0 >> 2) & 1;
+      if (i0 + 4 < 16) {
+        load4(pa0 + i0 + 4, fx[cur ^ 1][0]);
+        load4(pa1 + i0 + 4, fx[cur ^ 1][1]);
+      }
+      const u64 *x0 = fx[cur][0], *x1 = fx[cur][1];
       if (md.prod == 2) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
