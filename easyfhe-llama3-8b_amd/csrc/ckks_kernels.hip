@@ -1356,8 +1356,15 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
     } else {
       const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
                        (size_t)tile * 4096;
-      __syncthreads();  // the previous digit's reads of the tile are done
-      fp_round_z_to_lds(sm, src, T, tile, q);
+      const int t = threadIdx.x;
+      // round Z on the thread's column; only its LDS writes wait for the
+      // previous digit's reads of the tile
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = as_dbl(src[t + 256 * k]);
+      fp_low_round_z(y, T, tile, q);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; k++) sm[lds16(k, t)] = y[k];
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < 16; k++) y[k] = sm[lds16(rl, c0 + 16 * k)];
@@ -1681,12 +1688,17 @@ __global__ __launch_bounds__(TPB, 2) void k_low_key_md(LowKeyArgs a, LowMD md, B
   const double pinv = (double)md.pinv[2 * l], pinvq = __dmul_rn(pinv, qinv);
 #pragma unroll 1
   for (int comp = 0; comp < 2; comp++) {
-    // forward low pass of conv's output tile
+    // forward low pass of conv's output tile: round Z on the thread's column,
+    // whose LDS writes wait for earlier reads of the working tile
     const u64 *src = batch_ptr(conv, 2 * it + comp) + ((size_t)l << 16) + tb;
-    __syncthreads();  // earlier reads of the working tile are done
-    fp_round_z_to_lds(sm, src, T, ot, q);
-    __syncthreads();
     double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = as_dbl(src[threadIdx.x + 256 * k]);
+    fp_low_round_z(x, T, ot, q);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) sm[lds16(k, threadIdx.x)] = x[k];
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = sm[lds16(rl, c0 + 16 * k)];
     fp_low_round_a(x, T, row, q);
