@@ -3515,17 +3515,36 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
 #pragma unroll
       for (int j = 0; j < MD; j++)
         xd[it][j] = it < n_items && j < digits ? u52_to_dbl(x[it][j]) : 0.0;
+    // each baby's key words are loaded one baby ahead of their products
+    const u32 ks = key_slot(s);
+    u64 kn[2 * MD];
+#pragma unroll
+    for (int j = 0; j < MD; j++) {
+      if (j < digits && n_babies > 0) {
+        kn[2 * j] = mk.key[0][((size_t)(2 * j) * K + p) * N + ks];
+        kn[2 * j + 1] = mk.key[0][((size_t)(2 * j + 1) * K + p) * N + ks];
+      }
+    }
     for (int b = 0; b < n_babies; b++) {
       const u32 t = autom_index((u32)s, mk.ginv[b], logN);
-      const u64 *key = mk.key[b];
       double kb[MD], kbq[MD], ka[MD], kaq[MD];
 #pragma unroll
       for (int j = 0; j < MD; j++) {
         if (j < digits) {
-          kb[j] = u52_to_dbl(key[((size_t)(2 * j) * K + p) * N + key_slot(s)]);
-          ka[j] = u52_to_dbl(key[((size_t)(2 * j + 1) * K + p) * N + key_slot(s)]);
+          kb[j] = u52_to_dbl(kn[2 * j]);
+          ka[j] = u52_to_dbl(kn[2 * j + 1]);
           kbq[j] = __dmul_rn(kb[j], qinv);
           kaq[j] = __dmul_rn(ka[j], qinv);
+        }
+      }
+      if (b + 1 < n_babies) {
+        const u64 *key = mk.key[b + 1];
+#pragma unroll
+        for (int j = 0; j < MD; j++) {
+          if (j < digits) {
+            kn[2 * j] = key[((size_t)(2 * j) * K + p) * N + ks];
+            kn[2 * j + 1] = key[((size_t)(2 * j + 1) * K + p) * N + ks];
+          }
         }
       }
 #pragma unroll
