@@ -4314,10 +4314,17 @@ __global__ void k_lincomb(const u64 *__restrict__ table, int T, int n,
   const size_t N = (size_t)1 << logN;
   const ModQ M = mods[l];
   u64 acc = 0, hi = 0, lo = 0;
-  for (int t = 0; t < T; t++) {
+  // each term's word loaded one term ahead of its product
+  auto word = [&](int t) {
     const u64 *x = (const u64 *)table[2 * ((size_t)t * n + i)];
     const u64 tl = table[2 * ((size_t)t * n + i) + 1];
-    mac_wide(hi, lo, x[((size_t)poly * tl + l) * N + k], wtab[(size_t)t * limbs + l]);
+    return x[((size_t)poly * tl + l) * N + k];
+  };
+  u64 xn = T > 0 ? word(0) : 0;
+  for (int t = 0; t < T; t++) {
+    const u64 xv = xn;
+    if (t + 1 < T) xn = word(t + 1);
+    mac_wide(hi, lo, xv, wtab[(size_t)t * limbs + l]);
     if ((t & 15) == 15 || t == T - 1) {
       acc = add_mod(acc, redc(hi, lo, M.q, M.qinv), M.q);
       hi = lo = 0;
