@@ -1458,7 +1458,10 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
   const u32 sb = (u32)(tile * 4096 + rl * 256 + 16 * c0);
   const u32 kslot = key_slot(sb);
   const int jo = l < a.q_limbs ? l / a.ds : -1;
+  // accumulators start at 0: add_mod(0, p) = p for the canonical products
   u64 acc0[16], acc1[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc0[i] = acc1[i] = 0;
   for (int j = 0; j < a.digits; j++) {
     u64 y[16];
     if (j == jo && a.own_mul) {
@@ -1497,14 +1500,35 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
     }
     const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + kslot;
     const u64 *ka = kb + (size_t)a.K * 65536;
+    // groups of 4 positions; each group's 8 key words are loaded one group
+    // ahead of their products
+    u64 kw[2][8];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const u64 b = kb[kword(i)], c = ka[kword(i)];
-      const u64 pb = redc(__umul64hi(y[i], b), y[i] * b, q, M.qinv);
-      const u64 pa = redc(__umul64hi(y[i], c), y[i] * c, q, M.qinv);
-      acc0[i] = j == 0 ? pb : add_mod(acc0[i], pb, q);
-      acc1[i] = j == 0 ? pa : add_mod(acc1[i], pa, q);
+    for (int i = 0; i < 4; i++) {
+      kw[0][2 * i] = kb[kword(i)];
+      kw[0][2 * i + 1] = ka[kword(i)];
     }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (g < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          kw[(g + 1) & 1][2 * i] = kb[kword(4 * (g + 1) + i)];
+          kw[(g + 1) & 1][2 * i + 1] = ka[kword(4 * (g + 1) + i)];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int e = 4 * g + i;
+        const u64 b = kw[g & 1][2 * i], c = kw[g & 1][2 * i + 1];
+        const u64 pb = redc(__umul64hi(y[e], b), y[e] * b, q, M.qinv);
+        const u64 pa = redc(__umul64hi(y[e], c), y[e] * c, q, M.qinv);
+        acc0[e] = add_mod(acc0[e], pb, q);
+        acc1[e] = add_mod(acc1[e], pa, q);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
   u64 *o = a.acc + it * a.acc_stride + ((size_t)l << 16);
   const u32 tb = a.ginv == 1 ? sb & ~4095u : autom_index(sb, a.ginv, 16) & ~4095u;
