@@ -1480,8 +1480,15 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
     } else {
       const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
                        (size_t)tile * 4096;
-      __syncthreads();  // the previous digit's reads of the tile are done
-      u64_round_z_to_lds(sm, src, W, Ws, tile, q, q2);
+      // round Z on the thread's column; only its LDS writes wait for the
+      // previous digit's reads of the tile
+      const int t = threadIdx.x;
+#pragma unroll
+      for (int k = 0; k < 16; k++) y[k] = src[t + 256 * k];
+      u64_low_round_z(y, W, Ws, tile, q, q2);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; k++) sm[lds16(k, t)] = y[k];
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < 16; k++) y[k] = sm[lds16(rl, c0 + 16 * k)];
