@@ -561,6 +561,51 @@ def test_keyswitch_size_parity():
     assert np.array_equal(got.download(), orc.rescale(orc.rescale(orc.relinearize(r3))))
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("env", [{"CKKS_KS_DEFER": "0"}, {"CKKS_KS_TILE": "0"},
+                                 {"CKKS_KS_SPECIAL_INV": "0"}, {"CKKS_SPLIT_STREAMS": "1"}])
+def test_keyswitch_kernel_choices_full_size(env, monkeypatch):
+    """The key-switch kernel choices read at context creation give the
+    oracle's words at N = 2^16 on the key-switch chain: without the deferred
+    combine (CKKS_KS_DEFER=0: the product's addend d0, d1 then written whole
+    before the ModDown), without the tile-resident conversion (CKKS_KS_TILE=0:
+    d2 = a1 b1 written before the ModUp instead of formed as it loads),
+    without the special limbs' inverse pass in the key product
+    (CKKS_KS_SPECIAL_INV=0) and with every batch on one stream
+    (CKKS_SPLIT_STREAMS=1).  Rotations, products of distinct factors and
+    squares (the addend formed from one factor), by one and by two primes, and
+    a relinearisation alone."""
+    fhe = _fhe()
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    r = 1 << 5
+    client, ctx, orc = _pair("keyswitch", rotations=(r,))
+    slots, L = ctx.max_slots, ctx.L
+    rng = np.random.default_rng(9)
+    zs = [rng.uniform(-1, 1, slots) for _ in range(3)]
+    cts = [client.encrypt(z, slots=slots, enc_id=300 + i) for i, z in enumerate(zs)]
+    refs = [orc.encrypt(z, slots=slots, scale=ctx.scale_at(L), limbs=L, enc_id=300 + i)
+            for i, z in enumerate(zs)]
+    for out, ref in zip(fhe.homo_rotate_many(cts, r, ctx), refs):
+        assert np.array_equal(out.download(), orc.rotate_g(ref, orc.galois_elt(r)))
+    pairs = [(0, 1), (2, 0)]
+    prods = fhe.homo_mul_relin_rescale_many([cts[i] for i, _ in pairs],
+                                            [cts[j] for _, j in pairs], ctx)
+    for (i, j), got in zip(pairs, prods):
+        want = orc.rescale(orc.relinearize(orc.tensor(refs[i], refs[j])))
+        assert np.array_equal(got.download(), want), (env, i, j)
+        # key switch + rescale rounding: 1e-6
+        assert np.abs(client.decrypt(got) - zs[i] * zs[j]).max() < 1e-6
+    sq = fhe.homo_mul_relin_rescale_many(cts[1:], cts[1:], ctx, primes=2)
+    for i, got in zip((1, 2), sq):
+        want = orc.rescale(orc.rescale(orc.relinearize(orc.tensor(refs[i], refs[i]))))
+        assert np.array_equal(got.download(), want), (env, i)
+    t = fhe.homo_mul_no_relin(cts[2], cts[1], ctx)
+    assert np.array_equal(fhe.homo_relinearize(t, ctx).download(),
+                          orc.relinearize(orc.tensor(refs[2], refs[1])))
+    ctx.close()
+
+
 def test_linear_combination_matches_composed_ops():
     """One fused launch = mul_scalar + add + add_scalar on the same words,
     with terms holding more limbs than the output."""
