@@ -116,6 +116,40 @@ __device__ __forceinline__ void mac_wide(u64 &hi, u64 &lo, u64 a, u64 b) {
   hi += h + (lo < l ? 1 : 0);
 }
 
+// Sums of products x w of words below 2^60 in 30-bit halves: x = x1 2^30 +
+// x0, w = w1 2^30 + w0 (every half below 2^30), so x w = x0 w0 + (x0 w1 +
+// x1 w0) 2^30 + x1 w1 2^60 and each partial product is below 2^60: four
+// 64-bit sums hold 16 products without a carry, each term one 32 x 32 + 64
+// multiply-add (v_mad_u64_u32).
+struct Half30 {
+  u32 lo, hi;
+};
+__device__ __forceinline__ Half30 half30(u64 x) {
+  return Half30{(u32)x & 0x3fffffffu, (u32)(x >> 30)};
+}
+struct Sum30 {
+  u64 s00, s01, s10, s11;
+};
+__device__ __forceinline__ void mac30(Sum30 &a, Half30 x, Half30 w) {
+  a.s00 += (u64)x.lo * w.lo;
+  a.s01 += (u64)x.lo * w.hi;
+  a.s10 += (u64)x.hi * w.lo;
+  a.s11 += (u64)x.hi * w.hi;
+}
+// the sum of the four partial sums as hi 2^64 + lo
+__device__ __forceinline__ void sum30_wide(const Sum30 &a, u64 &hi, u64 &lo) {
+  lo = a.s00;
+  hi = 0;
+  const u64 m = a.s01 + a.s10;  // may wrap: the carry is bit 64 of the middle sum
+  const u64 mc = m < a.s01 ? 1 : 0;
+  u64 t = m << 30;
+  lo += t;
+  hi += (m >> 34) + (mc << 30) + (lo < t ? 1 : 0);
+  t = a.s11 << 60;
+  lo += t;
+  hi += (a.s11 >> 4) + (lo < t ? 1 : 0);
+}
+
 // Montgomery reduction of x = hi 2^64 + lo < q 2^64: x 2^-64 mod q in [0, q).
 __device__ __forceinline__ u64 redc(u64 hi, u64 lo, u64 q, u64 qinv) {
   u64 m = lo * qinv;

@@ -3953,11 +3953,15 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
   static_assert(kMacCtsFp % kMacCts == 0, "a block's inputs split into 64-bit passes");
   for (int i0 = ib; i0 < ib + kMacCtsFp && i0 < n; i0 += kMacCts) {
     constexpr int IC = kMacCts;
-    u64 acc[GT][IC], hi[GT][IC], lo[GT][IC];
+    u64 acc[GT][IC];
+    Sum30 sum[GT][IC];
 #pragma unroll
     for (int g = 0; g < GT; g++)
 #pragma unroll
-      for (int c = 0; c < IC; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+      for (int c = 0; c < IC; c++) {
+        acc[g][c] = 0;
+        sum[g][c] = Sum30{0, 0, 0, 0};
+      }
     // a baby step's words issued together, one step ahead of their products
     u64 xw[IC], ww[GT];
     auto issue = [&](int b) {
@@ -3975,17 +3979,25 @@ __global__ __launch_bounds__(TPB) void k_mac_many(const u64 *__restrict__ bab, i
       for (int g = 0; g < GT; g++) wc[g] = ww[g];
       if (b + 1 < B) issue(b + 1);
       __builtin_amdgcn_sched_barrier(0);
+      // 16 babies' products as 30-bit half sums (mac30), then reduced
+      Half30 xh[IC];
 #pragma unroll
-      for (int g = 0; g < GT; g++)
+      for (int c = 0; c < IC; c++) xh[c] = half30(xc[c]);
 #pragma unroll
-        for (int c = 0; c < IC; c++) mac_wide(hi[g][c], lo[g][c], xc[c], wc[g]);
+      for (int g = 0; g < GT; g++) {
+        const Half30 wh = half30(wc[g]);
+#pragma unroll
+        for (int c = 0; c < IC; c++) mac30(sum[g][c], xh[c], wh);
+      }
       if ((b & 15) == 15 || b == B - 1) {
 #pragma unroll
         for (int g = 0; g < GT; g++)
 #pragma unroll
           for (int c = 0; c < IC; c++) {
-            acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
-            hi[g][c] = lo[g][c] = 0;
+            u64 hi, lo;
+            sum30_wide(sum[g][c], hi, lo);
+            acc[g][c] = add_mod(acc[g][c], redc(hi, lo, M.q, M.qinv), M.q);
+            sum[g][c] = Sum30{0, 0, 0, 0};
           }
       }
     }
@@ -4092,8 +4104,9 @@ __global__ __launch_bounds__(TPB) void k_mac_table_fp(const u64 *const *__restri
         out[((size_t)g * n + i0 + c) * CP + off] = fp_canon(acc[g][c], qinv, q);
 }
 
-// The 64-bit kernel: 128-bit sums of 64-bit products, reduced every 16 babies
-// (below q 2^64 for q < 2^60); GT >= G groups compiled, a baby step's loads
+// The 64-bit kernel: the sums of 16 babies' products (below q 2^64 for
+// q < 2^60) kept as four 64-bit sums of 30-bit half products (mac30), then
+// Montgomery-reduced; GT >= G groups compiled, a baby step's loads
 // issued together one step ahead, and each block takes kTabCts ciphertexts
 // (blockIdx.z = component + 2 x ciphertext group), so that a single limb (q_0)
 // still fills the chip.
@@ -4110,11 +4123,15 @@ __global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restri
   const size_t N = (size_t)1 << logN, CP = 2 * (size_t)limbs * N;
   const ModQ M = mods[l];
   const size_t off = ((size_t)comp * limbs + l) * N + k, poff = (size_t)l * N + k;
-  u64 acc[GT][IC], hi[GT][IC], lo[GT][IC];
+  u64 acc[GT][IC];
+  Sum30 sum[GT][IC];
 #pragma unroll
   for (int g = 0; g < GT; g++)
 #pragma unroll
-    for (int c = 0; c < IC; c++) acc[g][c] = hi[g][c] = lo[g][c] = 0;
+    for (int c = 0; c < IC; c++) {
+      acc[g][c] = 0;
+      sum[g][c] = Sum30{0, 0, 0, 0};
+    }
   u64 xw[IC], ww[GT];
   auto issue = [&](int b) {
 #pragma unroll
@@ -4133,17 +4150,24 @@ __global__ __launch_bounds__(TPB) void k_mac_table_64(const u64 *const *__restri
     for (int g = 0; g < GT; g++) wc[g] = ww[g];
     if (b + 1 < B) issue(b + 1);  // the next step's words in flight
     __builtin_amdgcn_sched_barrier(0);
+    Half30 xh[IC];
 #pragma unroll
-    for (int g = 0; g < GT; g++)
+    for (int c = 0; c < IC; c++) xh[c] = half30(xc[c]);
 #pragma unroll
-      for (int c = 0; c < IC; c++) mac_wide(hi[g][c], lo[g][c], xc[c], wc[g]);
+    for (int g = 0; g < GT; g++) {
+      const Half30 wh = half30(wc[g]);
+#pragma unroll
+      for (int c = 0; c < IC; c++) mac30(sum[g][c], xh[c], wh);
+    }
     if ((b & 15) == 15 || b == B - 1) {
 #pragma unroll
       for (int g = 0; g < GT; g++)
 #pragma unroll
         for (int c = 0; c < IC; c++) {
-          acc[g][c] = add_mod(acc[g][c], redc(hi[g][c], lo[g][c], M.q, M.qinv), M.q);
-          hi[g][c] = lo[g][c] = 0;
+          u64 hi, lo;
+          sum30_wide(sum[g][c], hi, lo);
+          acc[g][c] = add_mod(acc[g][c], redc(hi, lo, M.q, M.qinv), M.q);
+          sum[g][c] = Sum30{0, 0, 0, 0};
         }
     }
   }

@@ -393,6 +393,58 @@ def test_bsgs_matvec_ext_parity(name):
     assert np.abs(dec - W @ x).max() < 1e-5
 
 
+# every prime of 59 or 60 bits, as on the reference's chain: both MACs take
+# their 64-bit kernels on every limb
+WIDE59 = dict(log_n=13, depth=3, dnum=2, dcrt_bits=59, first_mod=60, special_bits=60)
+
+
+@pytest.mark.parametrize("strategy,B,G", [("normal", 40, 12), ("ext_normal", 40, 3),
+                                          ("ext_normal", 24, 5)])
+def test_bsgs_mac_wide_primes_parity(strategy, B, G):
+    """The BSGS MAC with every prime of 2^45 or more (the 64-bit MAC kernels,
+    which keep 16 babies' products as sums of 30-bit half products before a
+    reduction): 40 babies (reductions after babies 16, 32 and 40) or 24
+    (after 16 and 24); 12 giant groups on the Q basis (passes of 8 and 4),
+    with extended plaintexts one group per pass (40 babies) or two and one
+    (24 babies); three ciphertexts (a block's pair of inputs and a lone one).
+    Every result bit-exact with the oracle's schedule and decrypting to the
+    plaintext BSGS sum."""
+    fhe = _fhe()
+    lanes = 32
+    ext = strategy != "normal"
+    rots = tuple(lanes * b for b in range(1, B)) + (B * lanes,)
+    client, ctx, orc = _pair(WIDE59, rotations=rots)
+    assert all(int(p) >= 1 << 45 for p in orc.primes)
+    slots, sc = ctx.max_slots, 2.0**50
+    rng = np.random.default_rng(3)
+    xs = [rng.uniform(-1, 1, slots) for _ in range(3)]
+    rows = rng.uniform(-1, 1, (G * B, slots))
+    pts = fhe.encode_rows(ctx, rows, limbs=ctx.L, scale=sc, slots=slots, is_ext=ext)
+    rpts = np.stack([orc.encode(r, slots=slots, scale=sc, limbs=ctx.L, is_ext=ext)
+                     for r in rows])
+    cts = [client.encrypt(x, slots=slots, scaling_factor=sc, enc_id=60 + i)
+           for i, x in enumerate(xs)]
+    refs = [orc.encrypt(x, slots=slots, scale=sc, limbs=ctx.L, enc_id=60 + i)
+            for i, x in enumerate(xs)]
+    offsets = [lanes * b for b in range(B)]
+    bgs, gg = [orc.galois_elt(o) for o in offsets], orc.galois_elt(B * lanes)
+    if ext:
+        accs = fhe.hoisted_mac_sum_ext_many(cts, offsets, pts, B * lanes, G, ctx,
+                                            strategy="ext_normal")
+    else:
+        babies = [fhe.prepare_hoisted_baby_rotations(ct, offsets, ctx) for ct in cts]
+        accs = fhe.hoisted_mac_sum_many(babies, pts, B * lanes, G, ctx)
+        one = fhe.hoisted_mac_sum(cts[2], offsets, pts, B * lanes, G, ctx)
+        assert np.array_equal(one.download(), accs[2].download())
+    for acc, ref, x in zip(accs, refs, xs):
+        racc = (orc.hoisted_mac_sum_ext if ext else orc.hoisted_mac_sum)(ref, bgs, rpts, gg, G)
+        assert np.array_equal(acc.download(), racc)
+        want = sum(np.roll(sum(rows[g * B + b] * np.roll(x, -b * lanes) for b in range(B)),
+                           -g * B * lanes) for g in range(G))
+        # up to 480 products at scale 2^50, one rescale by a 59-bit prime: ~1e-8
+        assert np.abs(client.decrypt(fhe.rescale(acc, ctx)) - want).max() < 1e-6
+
+
 @pytest.mark.parametrize("name", ["matvec", "ext44"])
 @pytest.mark.parametrize("n_cts", [1, 3])
 def test_bsgs_matvec_double_hoist_parity(n_cts, name):
