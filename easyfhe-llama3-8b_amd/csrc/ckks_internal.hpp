@@ -149,6 +149,14 @@ __device__ __forceinline__ void sum30_wide(const Sum30 &a, u64 &hi, u64 &lo) {
   lo += t;
   hi += (a.s11 >> 4) + (lo < t ? 1 : 0);
 }
+// hi 2^64 + lo plus the sum of a's partial sums (a second set of sums, for
+// more than 16 products)
+__device__ __forceinline__ void sum30_add_wide(const Sum30 &a, u64 &hi, u64 &lo) {
+  u64 h, l;
+  sum30_wide(a, h, l);
+  lo += l;
+  hi += h + (lo < l ? 1 : 0);
+}
 
 // Montgomery reduction of x = hi 2^64 + lo < q 2^64: x 2^-64 mod q in [0, q).
 __device__ __forceinline__ u64 redc(u64 hi, u64 lo, u64 q, u64 qinv) {

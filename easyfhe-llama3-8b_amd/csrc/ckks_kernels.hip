@@ -3124,14 +3124,19 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   u64 *out = batch_ptr(dst, blockIdx.y);
   const int k = blockIdx.x * TPB + threadIdx.x;
   const int T = nd - D;
-  u64 v[MS];
+  // the sums of products (words below 2^60) as 30-bit half sums (mac30):
+  // the ns source terms in one set (ns <= MS <= 16), the D lift terms in the
+  // same set when MS + D <= 16, else in a second one
+  constexpr bool kOneSet = MS + kMaxRescaleDrop <= 16;
+  Half30 v[MS];
   u64 cnt = 0;
 #pragma unroll
   for (int i = 0; i < MS; i++) {
     if (i < ns) {
       const u64 qi = mods[L + i].q;
-      v[i] = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
-      cnt += v[i] > (qi - 1) / 2 ? 1 : 0;
+      const u64 vi = shoup_mul(in[((size_t)i << logN) + k], st[i], st[ns + i], qi);
+      v[i] = half30(vi);
+      cnt += vi > (qi - 1) / 2 ? 1 : 0;
     }
   }
   const u64 *hm = st + 2 * ns;
@@ -3139,16 +3144,19 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   const u64 *pm = rtab, *pp = rtab + (size_t)T * D, *pinv = pp + (size_t)T * D;
   const u64 *chain = pinv + 2 * (size_t)D;
   u64 rv[kMaxRescaleDrop];
+  Half30 rh[kMaxRescaleDrop];
   bool neg[kMaxRescaleDrop];
 #pragma unroll
   for (int j = 0; j < kMaxRescaleDrop; j++) {
     if (j < D) {
       const int tj = nd - 1 - j;
       const ModQ Mj = mods[tj];
-      u64 hi = 0, lo = 0;
+      Sum30 a{0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < MS; i++)
-        if (i < ns) mac_wide(hi, lo, v[i], hm[i * nd + tj]);
+        if (i < ns) mac30(a, v[i], half30(hm[i * nd + tj]));
+      u64 hi, lo;
+      sum30_wide(a, hi, lo);
       u64 y = redc(hi, lo, Mj.q, Mj.qinv);
       if (cnt) y = sub_mod(y, mul_mod(cnt, qm[tj], Mj), Mj.q);
       const u64 xq = in[((size_t)(ns + D - 1 - j) << logN) + k];
@@ -3163,26 +3171,34 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
         }
       }
       rv[j] = u;
+      rh[j] = half30(u);
       neg[j] = u > (Mj.q - 1) / 2;
     }
   }
   int t = 0;
   for (; t + 1 < T; t += 2) {
     const ModQ M0 = mods[t], M1 = mods[t + 1];
-    u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+    Sum30 a0{0, 0, 0, 0}, a1{0, 0, 0, 0}, b0{0, 0, 0, 0}, b1{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < MS; i++) {
       if (i < ns) {
-        mac_wide(h0, l0, v[i], hm[i * nd + t]);
-        mac_wide(h1, l1, v[i], hm[i * nd + t + 1]);
+        mac30(a0, v[i], half30(hm[i * nd + t]));
+        mac30(a1, v[i], half30(hm[i * nd + t + 1]));
       }
     }
 #pragma unroll
     for (int j = 0; j < kMaxRescaleDrop; j++) {
       if (j < D) {
-        mac_wide(h0, l0, rv[j], pm[(size_t)t * D + j]);
-        mac_wide(h1, l1, rv[j], pm[(size_t)(t + 1) * D + j]);
+        mac30(kOneSet ? a0 : b0, rh[j], half30(pm[(size_t)t * D + j]));
+        mac30(kOneSet ? a1 : b1, rh[j], half30(pm[(size_t)(t + 1) * D + j]));
       }
+    }
+    u64 h0, l0, h1, l1;
+    sum30_wide(a0, h0, l0);
+    sum30_wide(a1, h1, l1);
+    if constexpr (!kOneSet) {
+      sum30_add_wide(b0, h0, l0);
+      sum30_add_wide(b1, h1, l1);
     }
     u64 y0 = redc(h0, l0, M0.q, M0.qinv);
     u64 y1 = redc(h1, l1, M1.q, M1.qinv);
@@ -3202,13 +3218,16 @@ __global__ __launch_bounds__(TPB) void k_bc_down_rescale(Batch src, Batch dst, i
   }
   if (t < T) {
     const ModQ M = mods[t];
-    u64 h0 = 0, l0 = 0;
+    Sum30 a0{0, 0, 0, 0}, b0{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < MS; i++)
-      if (i < ns) mac_wide(h0, l0, v[i], hm[i * nd + t]);
+      if (i < ns) mac30(a0, v[i], half30(hm[i * nd + t]));
 #pragma unroll
     for (int j = 0; j < kMaxRescaleDrop; j++)
-      if (j < D) mac_wide(h0, l0, rv[j], pm[(size_t)t * D + j]);
+      if (j < D) mac30(kOneSet ? a0 : b0, rh[j], half30(pm[(size_t)t * D + j]));
+    u64 h0, l0;
+    sum30_wide(a0, h0, l0);
+    if constexpr (!kOneSet) sum30_add_wide(b0, h0, l0);
     u64 y0 = redc(h0, l0, M.q, M.qinv);
     if (cnt) y0 = sub_mod(y0, mul_mod(cnt, qm[t], M), M.q);
 #pragma unroll
@@ -3600,29 +3619,41 @@ __global__ __launch_bounds__(TPB) void k_key_inner_multi(
     }
     return;
   }
+  // primes of 2^45 or more: the extended words split once into 30-bit halves
+  // for every baby's products, each output's sum of at most MD <= 16
+  // products kept as 30-bit half sums (mac30) and reduced once
+  Half30 xh[kMultiItems][MD];
+#pragma unroll
+  for (int it = 0; it < kMultiItems; it++)
+#pragma unroll
+    for (int j = 0; j < MD; j++)
+      xh[it][j] = it < n_items && j < digits ? half30(x[it][j]) : Half30{0, 0};
   for (int b = 0; b < n_babies; b++) {
     const u32 t = autom_index((u32)s, mk.ginv[b], logN);
     const u64 *key = mk.key[b];
     // keys in source order: the word for output t sits at s
-    u64 kb[MD], ka[MD];
+    Half30 kb[MD], ka[MD];
 #pragma unroll
     for (int j = 0; j < MD; j++) {
       if (j < digits) {
-        kb[j] = key[((size_t)(2 * j) * K + p) * N + key_slot(s)];
-        ka[j] = key[((size_t)(2 * j + 1) * K + p) * N + key_slot(s)];
+        kb[j] = half30(key[((size_t)(2 * j) * K + p) * N + key_slot(s)]);
+        ka[j] = half30(key[((size_t)(2 * j + 1) * K + p) * N + key_slot(s)]);
       }
     }
 #pragma unroll
     for (int it = 0; it < kMultiItems; it++) {
       if (it < n_items) {
-        u64 h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+        Sum30 s0{0, 0, 0, 0}, s1{0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < MD; j++) {
           if (j < digits) {
-            mac_wide(h0, l0, x[it][j], kb[j]);
-            mac_wide(h1, l1, x[it][j], ka[j]);
+            mac30(s0, xh[it][j], kb[j]);
+            mac30(s1, xh[it][j], ka[j]);
           }
         }
+        u64 h0, l0, h1, l1;
+        sum30_wide(s0, h0, l0);
+        sum30_wide(s1, h1, l1);
         u64 *o = (u64 *)outp[(size_t)b * n_items + it];
         o[(size_t)l * N + t] = add_mod(redc(h0, l0, M.q, M.qinv), pc[it], M.q);
         o[((size_t)E + l) * N + t] = redc(h1, l1, M.q, M.qinv);

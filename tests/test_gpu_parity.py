@@ -445,6 +445,44 @@ def test_bsgs_mac_wide_primes_parity(strategy, B, G):
         assert np.abs(client.decrypt(fhe.rescale(acc, ctx)) - want).max() < 1e-6
 
 
+# 14 special primes of 60 bits (one digit of 14 limbs), and 59/60-bit primes
+# in 6 digits
+SP14 = dict(log_n=12, depth=13, dnum=1, dcrt_bits=40, first_mod=60, special_bits=60)
+DIG6 = dict(log_n=12, depth=11, dnum=6, dcrt_bits=59, first_mod=60, special_bits=60)
+
+
+@pytest.mark.parametrize("params", [SP14, DIG6, WIDE59], ids=["sp14", "dig6", "wide59"])
+def test_wide_prime_product_sums_parity(params):
+    """The 64-bit sums of products kept as 30-bit half sums outside the MACs:
+    the integer ModDown conversion fused with 1..4 rescales (its sums over
+    the special limbs and the lifts: 14 + 4 terms in two sets on SP14) and
+    the multi-key inner product of hoisted rotations (6 digits on DIG6);
+    limbs equal to the oracle's relinearise, rescales and rotations."""
+    fhe = _fhe()
+    rots = (1, 3, 7)
+    client, ctx, orc = _pair(params, rotations=rots)
+    slots, L = ctx.max_slots, ctx.L
+    rng = np.random.default_rng(12)
+    x, y = rng.uniform(-1, 1, slots), rng.uniform(-1, 1, slots)
+    a = client.encrypt(x, slots=slots, enc_id=81)
+    b = client.encrypt(y, slots=slots, enc_id=82)
+    ra = orc.encrypt(x, slots=slots, scale=ctx.scale_at(L), limbs=L, enc_id=81)
+    rb = orc.encrypt(y, slots=slots, scale=ctx.scale_at(L), limbs=L, enc_id=82)
+    want = [orc.relinearize(orc.tensor(ra, rb)), orc.relinearize(orc.tensor(rb, rb))]
+    for k in range(1, min(4, L - 1) + 1):
+        want = [orc.rescale(w) for w in want]
+        got = fhe.homo_mul_relin_rescale_many([a, b], [b, b], ctx, primes=k)
+        for i in range(2):
+            assert np.array_equal(got[i].download(), want[i]), (k, i)
+    sq = fhe.homo_mul_relin_rescale_many([b], [b], ctx)[0]
+    assert np.array_equal(sq.download(), orc.rescale(orc.relinearize(orc.tensor(rb, rb))))
+    hs = fhe.prepare_hoisted_baby_rotations(a, (0,) + rots, ctx)
+    hw = orc.hoisted_rotate(ra, [orc.galois_elt(r) for r in (0,) + rots])
+    for h, w in zip(hs, hw):
+        assert np.array_equal(h.download(), w)
+    assert np.abs(client.decrypt(hs[2]) - np.roll(x, -3)).max() < 1e-6
+
+
 @pytest.mark.parametrize("name", ["matvec", "ext44"])
 @pytest.mark.parametrize("n_cts", [1, 3])
 def test_bsgs_matvec_double_hoist_parity(n_cts, name):
