@@ -92,20 +92,25 @@ inline int product_mode(const Batch &a, const Batch &b, int n_items) {
 // modular arithmetic (device)
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ u64 add_mod(u64 a, u64 b, u64 q) {
-  u64 s = a + b;
-  return s >= q ? s - q : s;
+// v < m ? v : v - m, the choice taken from the subtraction's borrow (no
+// separate 64-bit compare)
+__device__ __forceinline__ u64 csub(u64 v, u64 m) {
+  u64 r;
+  return __builtin_sub_overflow(v, m, &r) ? v : r;
 }
 
+__device__ __forceinline__ u64 add_mod(u64 a, u64 b, u64 q) { return csub(a + b, q); }
+
 __device__ __forceinline__ u64 sub_mod(u64 a, u64 b, u64 q) {
-  return a >= b ? a - b : a + q - b;
+  u64 r;
+  return __builtin_sub_overflow(a, b, &r) ? r + q : r;
 }
 
 // Shoup: a * w mod q with ws = floor(w 2^64 / q); a < 2^64, result in [0, q).
 __device__ __forceinline__ u64 shoup_mul(u64 a, u64 w, u64 ws, u64 q) {
   u64 h = __umul64hi(a, ws);
   u64 r = a * w - h * q;
-  return r >= q ? r - q : r;
+  return csub(r, q);
 }
 
 // (hi, lo) += a * b
@@ -162,7 +167,7 @@ __device__ __forceinline__ void sum30_add_wide(const Sum30 &a, u64 &hi, u64 &lo)
 __device__ __forceinline__ u64 redc(u64 hi, u64 lo, u64 q, u64 qinv) {
   u64 m = lo * qinv;
   u64 t = hi + __umul64hi(m, q) + (lo != 0 ? 1 : 0);
-  return t >= q ? t - q : t;
+  return csub(t, q);
 }
 
 // Barrett reduction of x = hi 2^64 + lo < q^2 (HAC 14.42 with radix 2).
@@ -171,10 +176,7 @@ __device__ __forceinline__ u64 barrett(u64 hi, u64 lo, const ModQ &M) {
   u64 xs = (hi << (65 - k)) | (lo >> (k - 1));
   u64 ph = __umul64hi(xs, M.mu), pl = xs * M.mu;
   u64 qh = (ph << (63 - k)) | (pl >> (k + 1));
-  u64 r = lo - qh * M.q;
-  if (r >= M.q) r -= M.q;
-  if (r >= M.q) r -= M.q;
-  return r;
+  return csub(csub(lo - qh * M.q, M.q), M.q);
 }
 
 __device__ __forceinline__ u64 mul_mod(u64 a, u64 b, const ModQ &M) {

@@ -243,7 +243,7 @@ __device__ __forceinline__ u64 shoup_lazy(u64 a, u64 w, u64 ws, u64 q) {
 
 // Cooley-Tukey: X, Y in [0, 4q) -> X + wY, X - wY in [0, 4q)
 __device__ __forceinline__ void ct_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u64 q2) {
-  const u64 x = X >= q2 ? X - q2 : X;
+  const u64 x = csub(X, q2);
   const u64 t = shoup_lazy(Y, w, ws, q);
   X = x + t;
   Y = x - t + q2;
@@ -252,7 +252,7 @@ __device__ __forceinline__ void ct_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u6
 // Gentleman-Sande: X, Y in [0, 2q) -> X + Y, (X - Y) w in [0, 2q)
 __device__ __forceinline__ void gs_bfly(u64 &X, u64 &Y, u64 w, u64 ws, u64 q, u64 q2) {
   u64 sum = X + Y;
-  sum = sum >= q2 ? sum - q2 : sum;
+  sum = csub(sum, q2);
   const u64 d = X - Y + q2;
   X = sum;
   Y = shoup_lazy(d, w, ws, q);
@@ -410,7 +410,7 @@ __device__ __forceinline__ void u64_high_inv(u64 (&x)[16], const u64 *__restrict
 #pragma unroll
   for (int k = 0; k < 16; k++) {
     const u64 v = shoup_lazy(x[k], ni, nis, q);
-    x[k] = v >= q ? v - q : v;
+    x[k] = csub(v, q);
   }
 }
 
@@ -536,8 +536,7 @@ __device__ __forceinline__ void k_ntt16_fwd_low_body(u64 *__restrict__ lds, Batc
   row_sync();
 #pragma unroll
   for (int j = 0; j < 16; j++) {
-    u64 a = x[j] >= q2 ? x[j] - q2 : x[j];
-    sm[lds16(rl, 16 * c0 + j)] = a >= q ? a - q : a;
+    sm[lds16(rl, 16 * c0 + j)] = csub(csub(x[j], q2), q);
   }
   row_sync();
   if constexpr (COMBINE) {
@@ -1501,8 +1500,7 @@ __device__ __forceinline__ void low_key_64(u64 *__restrict__ sm, const LowKeyArg
       u64_low_round_b(y, W, Ws, row, c0, q, q2);
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const u64 v = y[i] >= q2 ? y[i] - q2 : y[i];
-        y[i] = v >= q ? v - q : v;
+        y[i] = csub(csub(y[i], q2), q);
       }
     }
     const u64 *kb = a.key + ((size_t)(2 * j) * a.K + p) * 65536 + kslot;
