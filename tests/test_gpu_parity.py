@@ -445,6 +445,41 @@ def test_bsgs_mac_wide_primes_parity(strategy, B, G):
         assert np.abs(client.decrypt(fhe.rescale(acc, ctx)) - want).max() < 1e-6
 
 
+@pytest.mark.parametrize("G", [1, 8])
+def test_mac_wide_sums_at_maximal_words(G):
+    """The 64-bit MAC's 30-bit half sums where their middle sum carries past
+    2^64: babies and plaintexts of q - 1 (both 30-bit halves near 2^30 on the
+    60-bit primes) with a few random ones, 40 babies, G giant groups with the
+    identity as giant rotation, three inputs; every word equal to
+    sum_g sum_b x_b w_(g B + b) mod q in exact integers."""
+    fhe = _fhe()
+    client, ctx = device_context(WIDE59, relin=False)
+    L, N = ctx.L, ctx.N
+    q = [int(p) for p in ctx.primes()[:L]]
+    # q - 1 of a prime above 1.5 2^59 has both halves above 2^29.5: the sums
+    # x0 w1 and x1 w0 of 16 such products each exceed 2^63
+    assert max(q) > 3 << 58
+    rng = np.random.default_rng(6)
+    B, n = 40, 3
+
+    def words(rand):
+        if rand:
+            return np.stack([rng.integers(0, q[l], N, dtype=np.uint64) for l in range(L)])
+        return np.repeat(np.array(q, dtype=np.uint64)[:, None] - np.uint64(1), N, axis=1)
+
+    xs = [[np.stack([words((b + i) % 7 == 3), words(False)]) for b in range(B)]
+          for i in range(n)]
+    ws = [words(k % 9 == 5)[None] for k in range(G * B)]
+    babies = [[fhe.upload(ctx, x, slots=ctx.max_slots, scale=2.0**50) for x in row] for row in xs]
+    pts = [fhe.upload(ctx, w, slots=ctx.max_slots, scale=2.0**50) for w in ws]
+    accs = fhe.hoisted_mac_sum_many(babies, pts, 0, G, ctx)
+    wsum = [sum(ws[g * B + b][0].astype(object) for g in range(G)) for b in range(B)]
+    qo = np.array(q, dtype=object)[None, :, None]
+    for i in range(n):
+        want = sum(xs[i][b].astype(object) * wsum[b][None] for b in range(B)) % qo
+        assert np.array_equal(accs[i].download(), want.astype(np.uint64)), i
+
+
 # 14 special primes of 60 bits (one digit of 14 limbs), and 59/60-bit primes
 # in 6 digits
 SP14 = dict(log_n=12, depth=13, dnum=1, dcrt_bits=40, first_mod=60, special_bits=60)
