@@ -1035,9 +1035,12 @@ static Batch strided(u64 *base, size_t stride) {
 // high pass of the forward NTT; launch_ntt_low_key runs the low pass.
 // dmul (tile path, own_copy false): the polynomials are d[i] x dmul[i] word
 // by word, formed by the inverse low pass (modup_tile_ok tells when).
-static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
+// pack (high_only, own_copy false): on the tile path the fp64 limbs are
+// written in the packed form of launch_convert_h4, which only the fused key
+// products read; returns whether they were.
+static bool ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64 *ext,
                      Scratch &s, bool own_copy = true, bool high_only = false,
-                     const Batch *dmul = nullptr) {
+                     const Batch *dmul = nullptr, bool pack = false) {
   const size_t N = c->N;
   const int E = limbs + c->alpha, digits = (limbs + c->ds - 1) / c->ds;
   u64 *coeff = s.get((size_t)n * limbs * N);
@@ -1051,6 +1054,7 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
   if (dmul && (!tile || own_copy)) throw std::logic_error("ModUp of a product: tile path only");
   if (tile) {
     const size_t est = (size_t)digits * E * N;
+    const bool packed = pack && high_only && !own_copy;
     launch_ntt_inv_low(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs, dmul);
     for (int j = 0; j < digits; j++) {
       const int lo = j * c->ds, hi = std::min((j + 1) * c->ds, limbs), ns = hi - lo;
@@ -1061,13 +1065,13 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
         launch_copy_limbs(c, dsrc, strided(ej + (size_t)lo * N, est), n, ns);
       }
       launch_convert_h4(c, strided(coeff + (size_t)lo * N, (size_t)limbs * N), strided(ej, est),
-                        n, bc_up(c, limbs, j), lo, lo, ns, limbs, false);
+                        n, bc_up(c, limbs, j), lo, lo, ns, limbs, false, packed);
       if (!high_only) {
         launch_ntt_fwd_low(c, strided(ej, est), n, 0, lo, limbs);
         launch_ntt_fwd_low(c, strided(ej, est), n, hi, E - hi, limbs);
       }
     }
-    return;
+    return packed;
   }
   launch_ntt(c, src, strided(coeff, (size_t)limbs * N), n, 0, limbs, limbs, true);
   for (int j = 0; j < digits; j++) {
@@ -1087,6 +1091,7 @@ static void ks_modup(ckks_context *c, int limbs, int n, const u64 *const *d, u64
       launch_ntt(c, strided(ej, est), strided(ej, est), n, hi, E - hi, limbs, false);
     }
   }
+  return false;
 }
 
 struct KsJob {
@@ -1108,6 +1113,7 @@ struct KsDeferred {
   size_t est = 0;
   Batch own{};
   const Batch *own_b = nullptr;  // own x own_b is the source (ks_modup_inner's dmul)
+  bool packed = false;           // ext's fp64 limbs in the packed form
   const DeviceKey *key = nullptr;
   int digits = 0;
   u64 ginv = 1;
@@ -1168,7 +1174,7 @@ static void ks_moddown(ckks_context *c, int limbs, u64 *acc, const std::vector<K
       launch_low_key_moddown(c, dk->ext, dk->est, dk->own, n, *dk->key, dk->digits, E, limbs,
                              dk->ginv, strided(conv, (size_t)limbs * N), pinv,
                              pmod_table(c, limbs), a0, add1_off, o0, out1_off, limbs,
-                             nullptr, dk->own_b);
+                             nullptr, dk->own_b, dk->packed);
     launch_ntt_moddown(c, strided(conv, (size_t)limbs * N), n, limbs, strided(acc, 2 * E * N), E,
                        pinv, a0, add1_off, gal.data(), o0, out1_off, nullptr, nullptr, tile,
                        deferred);
@@ -1259,7 +1265,9 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
   const bool spf = fused && sp && c->ks_sp_inv && low_key_special_fp(c);
   if (sp_done) *sp_done = spf;
   if (dmul && !fused) throw std::logic_error("key switch of a product: fused path only");
-  ks_modup(c, limbs, n, d, ext, s, false, fused, dmul);
+  // the fused key products are the only readers of ext: packed where the
+  // tile path writes it
+  const bool packed = ks_modup(c, limbs, n, d, ext, s, false, fused, dmul, fused);
   if (!fused) return ks_inner(c, limbs, ext, jobs, s, d);
   u64 *acc = s.get((size_t)n * 2 * E * N);
   Batch ob{};
@@ -1274,6 +1282,7 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
       dk->est = est;
       dk->own = ob;
       dk->own_b = dmul;
+      dk->packed = packed;
       dk->key = jobs[0].key;
       dk->digits = digits;
       dk->ginv = ginv;
@@ -1281,7 +1290,7 @@ static u64 *ks_modup_inner(ckks_context *c, int limbs, int n, const u64 *const *
   }
   launch_ntt_low_key(c, ext, est, ob, acc, 2 * (size_t)E * N, n, *jobs[0].key, digits, E, limbs,
                      ginv, spf ? sp : nullptr, defer ? (dk->below >= 0 ? dk->below : limbs) : 0,
-                     dmul);
+                     dmul, packed);
   return acc;
 }
 
@@ -1565,7 +1574,7 @@ static void relin_rescale_batch(ckks_context *c, const ckks_ct *const *in, int n
         launch_low_key_moddown(c, dk.ext, dk.est, dk.own, nb, *dk.key, dk.digits, E, limbs,
                                dk.ginv, strided(conv, (size_t)T * N), rt, pmod_table(c, limbs),
                                ta ? fa : d3, P, o0, (u64)T * N, T, ta ? &fb : nullptr,
-                               dk.own_b);
+                               dk.own_b, dk.packed);
       launch_ntt_moddown(c, strided(conv, (size_t)T * N), nb, T, strided(acc, 2 * E * N), E, rt,
                          d3, P, gal.data(), o0, (u64)T * N, amul, &po, tile, dk.on);
     } else {

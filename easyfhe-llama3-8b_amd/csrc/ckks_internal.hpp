@@ -478,7 +478,8 @@ bool low_key_special_fp(const ckks_context *c);
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp = nullptr,
-                        int defer_below = 0, const Batch *own_b = nullptr);
+                        int defer_below = 0, const Batch *own_b = nullptr,
+                        bool ext_packed = false);
 // N = 2^16: for the Q limbs of fp64 primes, launch_ntt_low_key's key product
 // and launch_ntt_moddown's combine (addends and outputs as there, no postop)
 // in one kernel, the accumulator kept in the block, for output limbs
@@ -497,7 +498,7 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
                             int out_limbs, const Batch *mul_b = nullptr,
-                            const Batch *own_b = nullptr);
+                            const Batch *own_b = nullptr, bool ext_packed = false);
 // N = 2^16: the high pass of the inverse NTT alone, in place (after the low
 // pass of launch_ntt_low_key's sp output)
 void launch_ntt_inv_high(ckks_context *c, const Batch &dst, int n_items, int l_begin, int l_count,
@@ -537,9 +538,11 @@ bool convert_h4_ok(const ckks_context *c, const BCTable &t);
 bool convert_h4_rs_ok(const ckks_context *c, const BCTable &t, int D);
 void launch_convert_h4_rs(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                           const BCTable &t, int D, const u64 *rtab);
+// packed: the fp64 targets' planes in the packed form the fused key products
+// read (ext_packed of launch_ntt_low_key / launch_low_key_moddown)
 void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                        const BCTable &t, int src_prime0, int t_split, int t_skip, int q_limbs,
-                       bool centered);
+                       bool centered, bool packed = false);
 void launch_rescale_lift(ckks_context *c, const Batch &last, const Batch &w, int n_items,
                          int limbs, int D, const u64 *tab);
 void launch_rescale_finish(ckks_context *c, const Batch &src, const Batch &w, const Batch &out,

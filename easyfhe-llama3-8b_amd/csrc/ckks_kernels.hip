@@ -1232,6 +1232,9 @@ void launch_ntt_fwd_high(ckks_context *c, const Batch &src, const Batch &dst, in
 struct LowKeyArgs {
   const u64 *ext;     // item it, digit j, limb l: ext + it ext_stride + ((j E + l) << 16)
   size_t ext_stride;
+  // 1: the planes of fp64 limbs hold k_convert_h4's packed form (the 32 low
+  // bits of a centered residue, then its 16 high bits), 0: raw double bits
+  int ext_packed;
   Batch own;          // per item: the source polynomial, limb l at l << 16 (NTT form)
   // own_mul 1: the source polynomial is own x own_b word by word, 2: own^2
   // (formed where the digit's own limb is read), 0: own itself
@@ -1353,13 +1356,23 @@ __device__ __forceinline__ void low_key_fp_acc(double *__restrict__ sm, const Lo
 #pragma unroll
       for (int i = 0; i < 16; i++) y[i] = u52_to_dbl(w[i]);
     } else {
-      const u64 *src = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16) +
-                       (size_t)tile * 4096;
+      const u64 *plane = a.ext + it * a.ext_stride + ((size_t)(j * a.E + l) << 16);
       const int t = threadIdx.x;
       // round Z on the thread's column; only its LDS writes wait for the
       // previous digit's reads of the tile
+      if (a.ext_packed) {
+        const u32 *lo = reinterpret_cast<const u32 *>(plane) + tile * 4096 + t;
+        const short *hi =
+            reinterpret_cast<const short *>(reinterpret_cast<const u32 *>(plane) + 65536) +
+            tile * 4096 + t;
 #pragma unroll
-      for (int k = 0; k < 16; k++) y[k] = as_dbl(src[t + 256 * k]);
+        for (int k = 0; k < 16; k++)
+          y[k] = __fma_rn((double)hi[256 * k], 4294967296.0, (double)lo[256 * k]);
+      } else {
+        const u64 *src = plane + (size_t)tile * 4096;
+#pragma unroll
+        for (int k = 0; k < 16; k++) y[k] = as_dbl(src[t + 256 * k]);
+      }
       fp_low_round_z(y, T, tile, q);
       __syncthreads();
 #pragma unroll
@@ -1760,13 +1773,14 @@ bool low_key_special_fp(const ckks_context *c) {
 static LowKeyArgs low_key_args(ckks_context *c, const u64 *ext, size_t ext_stride,
                                const Batch &own, u64 *acc, size_t acc_stride,
                                const DeviceKey &key, int digits, int E, int q_limbs, u64 ginv,
-                               const Batch *own_b, int n_items) {
+                               const Batch *own_b, int n_items, bool ext_packed) {
   if (c->logN != 16) throw std::invalid_argument("fused low pass and key product: N = 2^16 only");
   if (digits < 1 || digits > key.digits || q_limbs > c->L || E != q_limbs + c->alpha)
     throw std::invalid_argument("fused low pass and key product: shape");
   LowKeyArgs a{};
   a.ext = ext;
   a.ext_stride = ext_stride;
+  a.ext_packed = ext_packed ? 1 : 0;
   a.own = own;
   if (own_b) {
     a.own_b = *own_b;
@@ -1789,13 +1803,14 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
                             int n_items, const DeviceKey &key, int digits, int E, int q_limbs,
                             u64 ginv, const Batch &conv, const u64 *pinv, const u64 *pmod,
                             const Batch &add, u64 add1_off, const Batch &out, u64 out1_off,
-                            int out_limbs, const Batch *mul_b, const Batch *own_b) {
+                            int out_limbs, const Batch *mul_b, const Batch *own_b,
+                            bool ext_packed) {
   if (n_items <= 0) return;
   if (n_items > kMaxBatch) throw std::invalid_argument("fused key product + ModDown: n <= 64");
   if (out_limbs < 1 || out_limbs > q_limbs)
     throw std::invalid_argument("fused key product + ModDown: output limbs");
   LowKeyArgs a = low_key_args(c, ext, ext_stride, own, nullptr, 0, key, digits, E, q_limbs, ginv,
-                              own_b, n_items);
+                              own_b, n_items, ext_packed);
   LowMD md{};
   md.pinv = pinv;
   md.add = add;
@@ -1835,14 +1850,14 @@ void launch_low_key_moddown(ckks_context *c, const u64 *ext, size_t ext_stride, 
 void launch_ntt_low_key(ckks_context *c, const u64 *ext, size_t ext_stride, const Batch &own,
                         u64 *acc, size_t acc_stride, int n_items, const DeviceKey &key,
                         int digits, int E, int q_limbs, u64 ginv, const Strided *sp,
-                        int defer_below, const Batch *own_b) {
+                        int defer_below, const Batch *own_b, bool ext_packed) {
   KTimer kt(c, "ntt_low_key",
             8.0 * c->N * ((double)n_items * (digits * E + 2.0 * E) + 2.0 * digits * E),
             2.0 * c->N * E * digits * n_items);
   audit_keyswitch(c, n_items, 1, q_limbs, digits, E);
   if (n_items <= 0) return;
   LowKeyArgs a = low_key_args(c, ext, ext_stride, own, acc, acc_stride, key, digits, E, q_limbs,
-                              ginv, own_b, n_items);
+                              ginv, own_b, n_items, ext_packed);
   if (sp) {
     if (!low_key_special_fp(c)) throw std::invalid_argument("fused special inverse: fp64 special primes only");
     a.sp = sp->base;
@@ -2627,8 +2642,10 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
   const int T = nd - RSD;
   // flags: 1 centered (ModDown); 2 / 4: the high passes of sources / targets
   // of 2^45 or more run outside the kernel (when such primes share a launch
-  // with fp64 ones, whose lanes would wait on their 64-bit butterflies)
+  // with fp64 ones, whose lanes would wait on their 64-bit butterflies);
+  // 8: fp64 targets stored packed (LowKeyArgs::ext_packed), 3/4 of the bytes
   const bool centered = flags & 1, wide_src_out = flags & 2, wide_tgt_out = flags & 4;
+  const bool packed = !RS && (flags & 8);  // ModUp only (never with the lifts)
   extern __shared__ u64 tb[];
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, wave = threadIdx.x >> 6;
   const int cc = blockIdx.x * 64 + wave * 16 + col;
@@ -2926,8 +2943,23 @@ __global__ __launch_bounds__(TPB, 2) void k_convert_h4(
 #pragma unroll
         for (int r = 0; r < 16; r++) xd[r] = as_dbl(y[ee][r]);
         fp_high_fwd(xd, reinterpret_cast<const double2 *>(tw0), as_dbl(w[8]));
+        if (packed) {
+          // the centered residue v (|v| <= q / 2 + 1 < 2^44) as its 32 low
+          // bits (u32 plane) and 16 high bits (i16 plane after it)
+          u32 *plo = reinterpret_cast<u32 *>(po - cc);
+          short *phi = reinterpret_cast<short *>(plo + 65536) + cc;
+          plo += cc;
+          const double q = as_dbl(w[8]), qinv = as_dbl(w[5]);
 #pragma unroll
-        for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
+          for (int r = 0; r < 16; r++) {
+            const long long v = dbl_to_i51(fp_reduce(xd[r], qinv, q));
+            plo[4096 * r] = (u32)v;
+            phi[4096 * r] = (short)(v >> 32);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) po[4096 * r] = dbl_bits(xd[r]);
+        }
       } else {
         // a prime of 2^45 or more: the forward high pass here, or (flag 4)
         // stored canonical for the launch after the kernel
@@ -3014,7 +3046,7 @@ bool convert_h4_ok(const ckks_context *c, const BCTable &t) {
 
 void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int n_items,
                        const BCTable &t, int src_prime0, int t_split, int t_skip, int q_limbs,
-                       bool centered) {
+                       bool centered, bool packed) {
   KTimer kt(c, "convert_h4", 8.0 * c->N * n_items * (t.ns + t.nd),
             (double)c->N * n_items * t.ns * t.nd);
   if (!convert_h4_ok(c, t)) throw std::invalid_argument("tile-resident conversion: shape");
@@ -3024,7 +3056,8 @@ void launch_convert_h4(ckks_context *c, const Batch &src, const Batch &dst, int 
   H4Tabs nt{c->d_psi, c->d_psi_sh, c->d_ipsi, c->d_ipsi_sh, c->d_ninv,
             (const double2 *)c->d_tw_fp, (const double2 *)c->d_itw_fp,
             (const double2 *)c->d_ninv_fp};
-  const int flags = (centered ? 1 : 0) | h4_wide_sources(c, src, n_items, t.ns, src_prime0, q_limbs) |
+  const int flags = (centered ? 1 : 0) | (packed ? 8 : 0) |
+                    h4_wide_sources(c, src, n_items, t.ns, src_prime0, q_limbs) |
                     h4_wide_targets(c, dst, n_items, t.nd, t_split, t_skip, q_limbs, false);
   hipLaunchKernelGGL(kern, dim3(64, n_items), dim3(TPB), lds, c->stream, src, dst, t.ns, t.nd,
                      t.sn, t.mt, t.n_tg, t.wide_mask, src_prime0, t_split, t_skip, q_limbs, c->L,
