@@ -2612,7 +2612,9 @@ void launch_basis_convert(ckks_context *c, const Batch &src, const Batch &dst, i
 //      column at all 16 rows, and a group's rows e past its last target are
 //      skipped by the whole wave;
 //   4. the forward high pass (bits 15..12) of each of those columns, stored
-//      as the low pass expects it (raw double bits / lazy words).
+//      as the low pass expects it (raw double bits / lazy words), or for
+//      the fused key products (flag 8) fp64 targets in the packed form:
+//      the centered residue's 32 low bits, then its 16 high bits.
 // The converted limbs never exist in coefficient form in HBM: the kernel
 // reads each source word and writes each target word once.  The same words
 // as the inverse high pass, k_basis_convert_mfma and the forward high pass
